@@ -1,0 +1,23 @@
+"""ccq_amd -- the CCQ read-side cleaning operator and the chunked linear-attention
+path it feeds, written for AMD Instinct MI355X (gfx950).
+
+Public surface mirrors the reference ``ccq.ops`` packages (``ccq/ops/ccq_gdn``,
+``ccq/ops/common/fused_read.py``).  All compute runs in hand-written HIP
+kernels of ``libccq_hip.so`` (C ABI in ``include/ccq_hip.h``).
+"""
+
+from .ccq_gdn import (chunk_ccq_gdn, chunk_gated_delta_rule, fused_ccq_clean, fused_chunk_ccq_gdn,
+                      fused_recurrent_ccq_gdn)
+from .clean import FusedCCQCleanRead, fused_ccq_clean_read
+from .l2norm import l2norm
+
+__all__ = [
+    "chunk_ccq_gdn",
+    "fused_chunk_ccq_gdn",
+    "fused_recurrent_ccq_gdn",
+    "fused_ccq_clean",
+    "chunk_gated_delta_rule",
+    "fused_ccq_clean_read",
+    "FusedCCQCleanRead",
+    "l2norm",
+]

@@ -1,0 +1,75 @@
+"""ctypes binding of libccq_hip.so (the C ABI declared in include/ccq_hip.h).
+
+The shared library is built in-tree by ``ccq_amd/build.py``.  Loading fails
+loudly when it is missing: there is no CPU or PyTorch fallback for any op.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libccq_hip.so")
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); must match include/ccq_hip.h
+SIGNATURES = {
+    "ccq_abi_version": (_I, []),
+    "ccq_last_error": (ctypes.c_char_p, []),
+    "ccq_clean_fwd": (_I, [_P] * 13 + [_I] * 7 + [_P]),
+    "ccq_clean_bwd_workspace_bytes": (_SZ, [_I64, _I, _I, _I]),
+    "ccq_clean_bwd": (_I, [_P] * 24 + [_I] * 7 + [_P]),
+    "ccq_chunk_index": (_I, [_P, _I, _P, _P, _I, _P]),
+    "ccq_gdn_saved_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
+    "ccq_gdn_bwd_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
+    "ccq_gdn_fwd": (_I, [_P] * 10 + [_I] + [_P] * 3 + [_I] * 6 + [_F, _P]),
+    "ccq_gdn_bwd": (_I, [_P] * 9 + [_I] + [_P] * 10 + [_I] * 6 + [_F, _P]),
+    "ccq_l2norm_fwd": (_I, [_P, _P, _P, _I64, _I, _F, _P]),
+    "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m ccq_amd.build` "
+                "(or __graft_entry__.build()); the CCQ ops have no fallback")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def ptr(t: Optional[torch.Tensor]):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().ccq_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)

@@ -1,0 +1,193 @@
+"""CCQ cleaning operator on MI355X (mirror of the reference's
+``ccq/ops/common/fused_read.py`` public surface: ``fused_ccq_clean_read`` and
+``FusedCCQCleanRead``; the lambda coercion of ``clean.py:314-325``).
+
+Forward and backward each run hand-written gfx950 kernels through the C ABI
+of ``libccq_hip.so``; nothing here computes on the CPU or falls back to
+PyTorch math.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, stream_of
+
+__all__ = ["fused_ccq_clean_read", "FusedCCQCleanRead", "reshape_lambda_3d", "reduce_dlambda", "seq_count",
+           "l2norm_fwd", "l2norm_bwd"]
+
+
+def seq_count(B: int, cu_seqlens: Optional[torch.Tensor]) -> int:
+    return B if cu_seqlens is None else cu_seqlens.numel() - 1
+
+
+def reshape_lambda_3d(lam, q: torch.Tensor) -> torch.Tensor:
+    """lambda (python scalar, 0-d, ``(H,)``, ``(B,T,H,1)`` or ``(B,T,H)``) -> ``(B,T,H)`` in q's dtype,
+    as the reference's ``_reshape_lambda_3d`` (``clean.py:314-325``); returned as contiguous fp32
+    for the kernels (the q-dtype rounding is kept)."""
+    B, T, H = q.shape[:3]
+    if not isinstance(lam, torch.Tensor):
+        out = torch.full((B, T, H), float(lam), device=q.device, dtype=q.dtype)
+    elif lam.ndim == 0:
+        out = lam.expand(B, T, H).to(q.dtype)
+    elif lam.ndim == 1 and lam.shape[0] == H:
+        out = lam.view(1, 1, H).expand(B, T, H).to(q.dtype)
+    elif lam.ndim == 4 and lam.shape[-1] == 1:
+        out = lam.squeeze(-1).to(q.dtype)
+    else:
+        out = lam.to(q.dtype)
+    return out.float().contiguous()
+
+
+def reduce_dlambda(dlam3: torch.Tensor, lam) -> Optional[torch.Tensor]:
+    """Gradient for lambda in its original shape (``fused_read.py:502-513``)."""
+    if not isinstance(lam, torch.Tensor) or not lam.requires_grad:
+        return None
+    if lam.ndim == 0:
+        dl = dlam3.sum()
+    elif lam.ndim == 1:
+        dl = dlam3.sum(dim=(0, 1))
+    elif lam.ndim == 4 and lam.shape[-1] == 1:
+        dl = dlam3.unsqueeze(-1)
+    else:
+        dl = dlam3
+    return dl.to(lam.dtype)
+
+
+def _check_qk(q: torch.Tensor, k: torch.Tensor):
+    if not (q.is_cuda and k.is_cuda):
+        raise RuntimeError("ccq_amd ops run on the GPU only (inputs are on the CPU)")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise TypeError(f"ccq_amd kernels take bf16 q/k (got {q.dtype}, {k.dtype})")
+    if q.shape != k.shape or q.ndim != 4:
+        raise ValueError(f"q and k must both be [B, T, H, K] (got {tuple(q.shape)}, {tuple(k.shape)})")
+
+
+def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    return None if t is None else t.float().contiguous()
+
+
+def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6):
+    """Row L2 normalisation (fla ``l2norm``, called at ``ccq/ops/ccq_gdn/fused_chunk.py:43-44``)."""
+    x = x.contiguous()
+    D = x.shape[-1]
+    rows = x.numel() // D
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
+    call("ccq_l2norm_fwd", ptr(x), ptr(y), ptr(rstd), rows, D, float(eps), stream_of(x))
+    return y, rstd
+
+
+def l2norm_bwd(x: torch.Tensor, rstd: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
+    D = x.shape[-1]
+    rows = x.numel() // D
+    dy = dy.contiguous()
+    dx = torch.empty_like(x)
+    is32 = dy.dtype == torch.float32
+    if not is32:
+        dy = dy.to(torch.bfloat16)
+    call("ccq_l2norm_bwd", ptr(x), ptr(rstd), ptr(dy) if is32 else None, None if is32 else ptr(dy), ptr(dx), rows, D,
+         stream_of(x))
+    return dx
+
+
+def clean_forward(q, k, lam3, gate_w, gate_b, h0, m0, cu_seqlens, position_offset, subtract_mean, *,
+                  want_bf16=True, want_f32=False, want_hfin=False):
+    """Launch the cleaning forward.  Returns (q_clean bf16|None, q_clean fp32|None, h_final|None,
+    m_final (always, for the backward), lambda (gate output or lam3))."""
+    B, T, H, K = q.shape
+    N = seq_count(B, cu_seqlens)
+    dev = q.device
+    qc = torch.empty_like(q) if want_bf16 else None
+    qc32 = torch.empty(q.shape, device=dev, dtype=torch.float32) if want_f32 else None
+    hfin = torch.empty(N, H, K, K, device=dev, dtype=torch.float32) if want_hfin else None
+    mfin = torch.empty(N, H, K, device=dev, dtype=torch.float32) if subtract_mean else None
+    lam_out = torch.empty(B, T, H, device=dev, dtype=torch.float32) if gate_w is not None else None
+    call("ccq_clean_fwd", ptr(q), ptr(k), ptr(lam3), ptr(gate_w), ptr(gate_b), ptr(lam_out), ptr(h0), ptr(m0),
+         ptr(cu_seqlens), ptr(qc), ptr(qc32), ptr(hfin), ptr(mfin), B, T, H, K, N, int(position_offset),
+         int(bool(subtract_mean)), stream_of(q))
+    return qc, qc32, hfin, mfin, (lam_out if gate_w is not None else lam3)
+
+
+def clean_backward(q, k, lam_used, gate_w, gate_b, dqc, dk_extra, h0, m0, m_end, cu_seqlens, dh_fin, dm_fin,
+                   position_offset, subtract_mean, *, want_dlam=True, dq_f32=False, dk_f32=False):
+    """Launch the cleaning backward.  Returns (dq, dk, dlam3|None, dgate_w|None, dgate_b|None, dh0|None, dm0|None)."""
+    B, T, H, K = q.shape
+    N = seq_count(B, cu_seqlens)
+    dev = q.device
+    gate = gate_w is not None
+    ws = torch.empty(_lib.load().ccq_clean_bwd_workspace_bytes(B * T, H, K, int(gate)), device=dev,
+                     dtype=torch.uint8)
+    dqc = dqc.contiguous()
+    d32 = dqc if dqc.dtype == torch.float32 else None
+    d16 = None if d32 is not None else dqc.to(torch.bfloat16)
+    dq = torch.empty(q.shape, device=dev, dtype=torch.float32 if dq_f32 else q.dtype)
+    dk = torch.empty(k.shape, device=dev, dtype=torch.float32 if dk_f32 else k.dtype)
+    dlam = torch.empty(B, T, H, device=dev, dtype=torch.float32) if (want_dlam and not gate) else None
+    dgw = torch.empty_like(gate_w) if gate else None
+    dgb = torch.empty_like(gate_b) if gate else None
+    dh0 = torch.empty(N, H, K, K, device=dev, dtype=torch.float32) if h0 is not None else None
+    dm0 = torch.empty(N, H, K, device=dev, dtype=torch.float32) if (m0 is not None and subtract_mean) else None
+    call("ccq_clean_bwd", ptr(q), ptr(k), ptr(lam_used), ptr(gate_w), ptr(gate_b), ptr(d32), ptr(d16),
+         ptr(dk_extra), ptr(h0), ptr(m0), ptr(m_end), ptr(cu_seqlens), ptr(_f32(dh_fin)), ptr(_f32(dm_fin)),
+         None if dq_f32 else ptr(dq), ptr(dq) if dq_f32 else None, None if dk_f32 else ptr(dk),
+         ptr(dk) if dk_f32 else None, ptr(dlam), ptr(dgw), ptr(dgb), ptr(dh0), ptr(dm0), ptr(ws), B, T, H, K, N,
+         int(position_offset), int(bool(subtract_mean)), stream_of(q))
+    return dq, dk, dlam, dgw, dgb, dh0, dm0
+
+
+class FusedCCQCleanRead(torch.autograd.Function):
+    """q_clean, final covariance and final key-sum states from (q, k, lambda): one forward kernel
+    and one backward kernel pair (reference ``FusedCCQCleanRead``, ``fused_read.py:474-514``).
+
+    ``gate_w`` / ``gate_b`` (optional, fp32 ``[H, K]`` / ``[H]``) switch to the fused per-head gate
+    ``lambda = sigmoid(gate_w[h]·q + gate_b[h])``; ``lambda_h`` is then ignored."""
+
+    @staticmethod
+    def forward(ctx, q, k, lambda_h, position_offset, initial_cov_state, initial_mean_state, output_final_state,
+                subtract_mean, cu_seqlens, gate_w=None, gate_b=None):
+        _check_qk(q, k)
+        q, k = q.contiguous(), k.contiguous()
+        gw, gb = _f32(gate_w), _f32(gate_b)
+        lam3 = None if gw is not None else reshape_lambda_3d(lambda_h, q)
+        h0 = _f32(initial_cov_state)
+        m0 = _f32(initial_mean_state) if subtract_mean else None
+        qc, _, hfin, mfin, lam_used = clean_forward(q, k, lam3, gw, gb, h0, m0, cu_seqlens, position_offset,
+                                                    subtract_mean, want_hfin=bool(output_final_state))
+        ctx.save_for_backward(q, k, lam_used, h0, m0, mfin, cu_seqlens, gw, gb)
+        ctx.lambda_h = lambda_h if isinstance(lambda_h, torch.Tensor) else None
+        ctx.position_offset = int(position_offset)
+        ctx.subtract_mean = bool(subtract_mean)
+        ctx.has_h0 = initial_cov_state is not None
+        ctx.has_m0 = initial_mean_state is not None and subtract_mean
+        ctx.gate = gw is not None
+        mret = mfin if (output_final_state and subtract_mean) else None
+        if mret is not None:
+            mret = mret.clone()
+        return qc, hfin, mret
+
+    @staticmethod
+    def backward(ctx, dqc, dfinal_cov, dfinal_mean):
+        q, k, lam_used, h0, m0, mfin, cu_seqlens, gw, gb = ctx.saved_tensors
+        want_dlam = ctx.lambda_h is not None and ctx.lambda_h.requires_grad
+        dq, dk, dlam, dgw, dgb, dh0, dm0 = clean_backward(
+            q, k, lam_used, gw, gb, dqc, None, h0, m0, mfin, cu_seqlens, dfinal_cov, dfinal_mean,
+            ctx.position_offset, ctx.subtract_mean, want_dlam=want_dlam)
+        dl = reduce_dlambda(dlam, ctx.lambda_h) if (dlam is not None) else None
+        return dq, dk, dl, None, dh0, dm0, None, None, None, dgw, dgb
+
+
+def fused_ccq_clean_read(q, k, lambda_h, *, position_offset=0, initial_cov_state=None, initial_mean_state=None,
+                         output_final_state=False, subtract_mean=True, cu_seqlens=None, gate_w=None, gate_b=None):
+    """Fused covariance read + cleaning (reference ``fused_read.py:517-531``).
+
+    Returns ``(q_clean, final_cov_state, final_mean_state)``; the states are None unless requested.
+    """
+    qc, hf, mf = FusedCCQCleanRead.apply(q, k, lambda_h, int(position_offset), initial_cov_state, initial_mean_state,
+                                         bool(output_final_state), bool(subtract_mean), cu_seqlens, gate_w, gate_b)
+    if not output_final_state:
+        hf, mf = None, None
+    return qc, hf, mf

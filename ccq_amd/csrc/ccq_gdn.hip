@@ -1,0 +1,1133 @@
+// Gated delta rule, chunked (chunk size 64), forward and backward, on gfx950.
+//
+// Recurrence (arXiv:2412.06464; the backbone the reference calls through
+// fla's chunk_gated_delta_rule, ccq/ops/ccq_gdn/fused_chunk.py:54-58):
+//   S <- exp(g_t) S;  u_t = beta_t (v_t - S^T k_t);  S <- S + k_t u_t^T;  o_t = S^T (scale q_t)
+// Per chunk, with G the in-chunk cumulative sum of g, gamma = exp(G),
+// Gamma_ij = exp(G_i - G_j), L1 = last row:
+//   A = strict_lower(diag(beta) (K K^T o Gamma)),  T = (I + A)^-1
+//   w = T diag(beta gamma) K,  u = T diag(beta) V,  U = u - w S
+//   O = scale diag(gamma) Q S + P U,  P = scale (Q K^T o Gamma), causal incl. diagonal
+//   S <- gamma_L S + K^T diag(gamma_L / gamma) U
+//
+// Kernels:
+//   gdn_prep         chunk-parallel: G, T, w, u
+//   gdn_fwd_state    one workgroup per (sequence, head, 32 state columns), walks the chunks:
+//                    U, state snapshots hT
+//   gdn_fwd_o        chunk-parallel: P (kept for the backward as P^T) and O
+//   gdn_bwd_state    reverse walk per (sequence, head, 32 state columns): dU, dS snapshots dhT
+//   gdn_bwd_dqkw     chunk x 64-column tiles of K: dq, the state/output part of dk, dw, dG partials
+//   gdn_bwd_wy       chunk-parallel: backward through the WY representation -> dk, dv, dbeta, dg
+//
+// Precision: products whose operands are the bf16 inputs run as one bf16 MFMA; the
+// operands that carry the leading part of a result (U, P, the cleaned query, dU, ...)
+// are fed as hi/lo bf16 pairs so every result keeps ~16 significant bits.
+#include "ccq_tile.h"
+#include "ccq_params.h"
+
+namespace ccq {
+
+namespace {
+
+constexpr int BT = 64;
+
+struct Carver {
+  char* p;
+  template <typename T>
+  __device__ __forceinline__ T* take(int n) {
+    T* r = (T*)p;
+    p += ((long)n * sizeof(T) + 15) & ~15L;
+    return r;
+  }
+};
+
+// Returns false for the padding entries of a varlen launch (grid sized by an upper bound).
+__device__ __forceinline__ bool chunk_info(const GdnArgs& a, int gc, int& n, int& c0, long& bos, int& L) {
+  if (a.cu) {
+    n = a.chunk_idx[2 * gc];
+    if (n < 0) return false;
+    const int c = a.chunk_idx[2 * gc + 1];
+    bos = (long)a.cu[n];
+    const int len = (int)(a.cu[n + 1] - a.cu[n]);
+    c0 = c * BT;
+    L = min(BT, len - c0);
+  } else {
+    n = gc / a.NT;
+    const int c = gc % a.NT;
+    bos = (long)n * a.T;
+    c0 = c * BT;
+    L = min(BT, a.T - c0);
+  }
+  return true;
+}
+
+// Rows of fp32 or bf16 into fp32 LDS (row-major and/or transposed), zero-filled past nvalid.
+template <int D>
+__device__ __forceinline__ void stage_any_f32(float* dst, int ld, float* dst_t, int ldt, const float* g32,
+                                              const bf16* g16, long gstride, int rows, int nvalid) {
+  if (g32) {
+    stage_f32<D>(dst, ld, dst_t, ldt, g32, gstride, rows, nvalid);
+    return;
+  }
+  constexpr int VPR = D / 8;
+  for (int idx = threadIdx.x; idx < rows * VPR; idx += kThreads) {
+    const int r = idx / VPR, c = (idx % VPR) * 8;
+    bf16x8 v;
+    if (r < nvalid) {
+      v = *(const bf16x8*)(g16 + (long)r * gstride + c);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (bf16)0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (dst) dst[r * ld + c + i] = (float)v[i];
+      if (dst_t) dst_t[(c + i) * ldt + r] = (float)v[i];
+    }
+  }
+}
+
+// Copy `rows` rows of D bf16 from LDS (leading dim ld) to global (row stride gstride), 16-byte vectors.
+template <int D>
+__device__ __forceinline__ void lds_to_global_bf16(bf16* g, long gstride, const bf16* s, int ld, int rows) {
+  constexpr int VPR = D / 8;
+  for (int idx = threadIdx.x; idx < rows * VPR; idx += kThreads) {
+    const int r = idx / VPR, c = (idx % VPR) * 8;
+    *(bf16x8*)(g + (long)r * gstride + c) = *(const bf16x8*)(s + r * ld + c);
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+// gdn_prep: grid (NTG, H)
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, const int V) {
+  constexpr int LDK = K + 8, LDB = BT + 8, LDT = BT + 1;
+  constexpr long kBytes = (long)BT * LDK * 2 + (long)K * LDB * 2 + 2L * BT * LDT * 4 + 64L * LDB * 2 +
+                          4 * 256 * 4 + 3 * 256 * 4 + 4 * BT * 4 + 16 * 12;
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  Carver cv{smem};
+  bf16* sK = cv.take<bf16>(BT * LDK);
+  bf16* sKT = cv.take<bf16>(K * LDB);
+  float* sA = cv.take<float>(BT * LDT);   // A, later T
+  float* sTo = cv.take<float>(BT * LDT);  // off-diagonal blocks of T
+  bf16* sVT = cv.take<bf16>(64 * LDB);
+  float* sD = cv.take<float>(4 * 256);    // inverses of the 16x16 diagonal blocks
+  float* sScr = cv.take<float>(3 * 256);
+  float* sG = cv.take<float>(BT);
+  float* sBeta = cv.take<float>(BT);
+  float* sGam = cv.take<float>(BT);
+  float* sBG = cv.take<float>(BT);  // beta * gamma
+
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int gc = blockIdx.x, h = blockIdx.y;
+  int n, c0, L;
+  long bos;
+  if (!chunk_info(a, gc, n, c0, bos, L)) return;
+  const long tok0 = bos + c0;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+
+  stage_bf16<K>(sK, LDK, sKT, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
+  if (w == 0) {
+    float x = (l < L && a.g) ? a.g[(tok0 + l) * a.H + h] : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(x, off);
+      if (l >= off) x += y;
+    }
+    sG[l] = x;
+    sBeta[l] = (l < L) ? a.beta[(tok0 + l) * a.H + h] : 0.f;
+    sGam[l] = __expf(x);
+    sBG[l] = sBeta[l] * sGam[l];
+    if (l < L) a.gcum[(tok0 + l) * a.H + h] = x;
+  }
+  __syncthreads();
+
+  // A = strict_lower(beta_i Gamma_ij (K K^T)_ij)
+  if (w < 3) {
+    const int tr = (w == 0) ? 0 : 1, tc = (w == 2) ? 1 : 0;
+    f32x16 acc = zero16();
+    mma_rr(acc, sK + tr * 32 * LDK, LDK, sK + tc * 32 * LDK, LDK, K);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr * 32 + acc_row(i), c = tc * 32 + acc_col();
+      sA[r * LDT + c] = (r > c) ? sBeta[r] * __expf(sG[r] - sG[c]) * acc[i] : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sA[acc_row(i) * LDT + 32 + acc_col()] = 0.f;
+  }
+  __syncthreads();
+
+  // T = (I + A)^-1 by 16x16 blocks: diagonal blocks by forward substitution ...
+  if (tid < 64) {
+    const int b0 = (tid >> 4) * 16, col = tid & 15;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s = (i == col) ? 1.f : 0.f;
+#pragma unroll
+      for (int m = 0; m < i; ++m) s -= sA[(b0 + i) * LDT + b0 + m] * x[m];
+      x[i] = s;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sD[(tid >> 4) * 256 + i * 16 + col] = x[i];
+  }
+  __syncthreads();
+  // ... then off-diagonal blocks by distance d:  T_IJ = -T_II sum_{M=J}^{I-1} A_IM T_MJ
+  for (int d = 1; d < 4; ++d) {
+    const int np = 4 - d;
+    for (int e = tid; e < np * 256; e += kThreads) {
+      const int p = e >> 8, r = (e >> 4) & 15, c = e & 15;
+      const int I = p + d, J = p;
+      float s = 0.f;
+      for (int M = J; M < I; ++M) {
+        for (int m = 0; m < 16; ++m) {
+          const float tmj = (M == J) ? sD[J * 256 + m * 16 + c] : sTo[(M * 16 + m) * LDT + J * 16 + c];
+          s += sA[(I * 16 + r) * LDT + M * 16 + m] * tmj;
+        }
+      }
+      sScr[p * 256 + r * 16 + c] = s;
+    }
+    __syncthreads();
+    for (int e = tid; e < np * 256; e += kThreads) {
+      const int p = e >> 8, r = (e >> 4) & 15, c = e & 15;
+      const int I = p + d, J = p;
+      float s = 0.f;
+      for (int m = 0; m < 16; ++m) s += sD[I * 256 + r * 16 + m] * sScr[p * 256 + m * 16 + c];
+      sTo[(I * 16 + r) * LDT + J * 16 + c] = -s;
+    }
+    __syncthreads();
+  }
+  // assemble T into sA and the fp32 copy for the backward
+  float* tg = a.tmat + ((long)gc * a.H + h) * (BT * BT);
+  for (int e = tid; e < BT * BT; e += kThreads) {
+    const int r = e >> 6, c = e & 63;
+    const int I = r >> 4, J = c >> 4;
+    float t;
+    if (I == J) t = sD[I * 256 + (r & 15) * 16 + (c & 15)];
+    else if (I > J) t = sTo[r * LDT + c];
+    else t = 0.f;
+    sA[r * LDT + c] = t;
+    tg[e] = t;
+  }
+  __syncthreads();
+
+  // w = (T diag(beta gamma)) K  (64 x K); the column scaling is applied in fp32 and the
+  // scaled T enters as a hi/lo pair (beta itself is not a bf16 number in general)
+  {
+    bf16* wg = (bf16*)a.w + (tok0 * a.H + h) * K;
+    for (int tile = w; tile < 2 * (K / 32); tile += 4) {
+      const int tr = tile & 1, tc = tile >> 1;
+      f32x16 acc = zero16();
+      for (int k0 = 0; k0 < BT; k0 += 16) {
+        bf16x8 hi, lo;
+        frag_rm_f32_ks(sA + tr * 32 * LDT + k0, LDT, sBG + k0, hi, lo);
+        const bf16x8 b = frag_rm(sKT + tc * 32 * LDB + k0, LDB);
+        acc = mfma(hi, b, acc);
+        acc = mfma(lo, b, acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = tr * 32 + acc_row(i);
+        if (r < L) wg[(long)r * rsk + tc * 32 + acc_col()] = (bf16)acc[i];
+      }
+    }
+  }
+  // u = (T diag(beta)) V  (64 x V), 64 value columns at a time
+  float* ug = a.u + (tok0 * a.H + h) * (long)V;
+  const bf16* vg = (const bf16*)a.v + (tok0 * a.H + h) * (long)V;
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    stage_bf16<64>(nullptr, 0, sVT, LDB, vg + v0, rsv, BT, L);
+    __syncthreads();
+    {
+      const int tr = w & 1, tc = w >> 1;
+      f32x16 acc = zero16();
+      for (int k0 = 0; k0 < BT; k0 += 16) {
+        bf16x8 hi, lo;
+        frag_rm_f32_ks(sA + tr * 32 * LDT + k0, LDT, sBeta + k0, hi, lo);
+        const bf16x8 b = frag_rm(sVT + tc * 32 * LDB + k0, LDB);
+        acc = mfma(hi, b, acc);
+        acc = mfma(lo, b, acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = tr * 32 + acc_row(i);
+        if (r < L) ug[(long)r * rsv + v0 + tc * 32 + acc_col()] = acc[i];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
+// gdn_fwd_state: grid ((V/32) * N * H)
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a, const int V) {
+  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDU = BT + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
+  __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sKT[K * LDB];
+  __shared__ __attribute__((aligned(16))) bf16 sST[VB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sSTl[VB * LDK];
+  __shared__ float sUsT[VB * LDU];
+  __shared__ float sFac[BT];
+  __shared__ float sGL[1];
+
+  const int tid = threadIdx.x, w = wave_id();
+  const int nv = V / VB;
+  int unit, vt;
+  xcd_map(blockIdx.x, nv, a.N * a.H, unit, vt);
+  const int n = unit / a.H, h = unit % a.H;
+  long bos;
+  int len;
+  seq_bounds(a.cu, n, a.T, bos, len);
+  const int nc = (len + BT - 1) / BT;
+  const int gc0 = a.cu ? a.chunk_off[n] : n * a.NT;
+  const int v0 = vt * VB;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+
+  f32x16 S[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    S[j] = zero16();
+    const int rt = w + 4 * j;
+    if (rt < NRT && a.s0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S[j][i] = a.s0[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()];
+    }
+  }
+
+  for (int c = 0; c < nc; ++c) {
+    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
+    const long tok0 = bos + c0;
+    stage_bf16<K>(sW, LDK, nullptr, 0, (const bf16*)a.w + (tok0 * a.H + h) * K, rsk, BT, L);
+    stage_bf16<K>(nullptr, 0, sKT, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
+    if (tid < BT) {
+      const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
+      const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
+      sFac[tid] = __expf(gl - gt);
+      if (tid == 0) sGL[0] = __expf(gl);
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int e = acc_col() * LDK + rt * 32 + acc_row(i);
+          split2(S[j][i], sST[e], sSTl[e]);
+        }
+      }
+    }
+    __syncthreads();
+    lds_to_global_bf16<K>((bf16*)a.hT + (((long)gc * a.H + h) * V + v0) * K, K, sST, LDK, VB);
+    lds_to_global_bf16<K>((bf16*)a.hTl + (((long)gc * a.H + h) * V + v0) * K, K, sSTl, LDK, VB);
+    if (w < 2) {
+      f32x16 acc = zero16();
+      mma_rr(acc, sW + w * 32 * LDK, LDK, sST, LDK, K);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = w * 32 + acc_row(i), cc = acc_col();
+        float us = 0.f;
+        if (r < L) {
+          const long gi = (tok0 + r) * rsv + (long)h * V + v0 + cc;
+          const float uu = a.u[gi] - acc[i];
+          a.U[gi] = uu;
+          us = sFac[r] * uu;
+        }
+        sUsT[cc * LDU + r] = us;
+      }
+    }
+    __syncthreads();
+    const float gL = sGL[0];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[j][i] *= gL;
+        for (int k0 = 0; k0 < BT; k0 += 16) {
+          const bf16x8 ka = frag_rm(sKT + rt * 32 * LDB + k0, LDB);
+          bf16x8 hi, lo;
+          frag_rm_f32(sUsT + k0, LDU, hi, lo);
+          S[j] = mfma(ka, hi, S[j]);
+          S[j] = mfma(ka, lo, S[j]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (a.s_fin) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          a.s_fin[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()] = S[j][i];
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// gdn_fwd_o: grid (NTG, H)
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, const int V) {
+  constexpr int LDQ = K + 4, LDK = K + 8, LDP = BT + 1;
+  constexpr long kBytes = (long)BT * LDQ * 4 + (long)BT * LDK * 2 + 2L * BT * LDP * 4 + 2 * BT * 4 + 64;
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  Carver cv{smem};
+  float* sQc = cv.take<float>(BT * LDQ);
+  bf16* sK = cv.take<bf16>(BT * LDK);  // later: state tile [64 v][K]
+  float* sP = cv.take<float>(BT * LDP);
+  float* sUT = cv.take<float>(BT * LDP);
+  float* sG = cv.take<float>(BT);
+  float* sGam = cv.take<float>(BT);
+
+  const int tid = threadIdx.x, w = wave_id();
+  const int gc = blockIdx.x, h = blockIdx.y;
+  int n, c0, L;
+  long bos;
+  if (!chunk_info(a, gc, n, c0, bos, L)) return;
+  const long tok0 = bos + c0;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+
+  stage_any_f32<K>(sQc, LDQ, nullptr, 0, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K : nullptr,
+                   a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K : nullptr, rsk, BT, L);
+  stage_bf16<K>(sK, LDK, nullptr, 0, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
+  if (tid < BT) {
+    const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
+    const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
+    sG[tid] = gt;
+    sGam[tid] = __expf(gt);
+  }
+  __syncthreads();
+
+  float* ptg = a.PT + ((long)gc * a.H + h) * (BT * BT);
+  if (w < 3) {
+    const int tr = (w == 0) ? 0 : 1, tc = (w == 2) ? 1 : 0;
+    f32x16 acc = zero16();
+    for (int k0 = 0; k0 < K; k0 += 16) {
+      bf16x8 hi, lo;
+      frag_rm_f32(sQc + tr * 32 * LDQ + k0, LDQ, hi, lo);
+      const bf16x8 b = frag_rm(sK + tc * 32 * LDK + k0, LDK);
+      acc = mfma(hi, b, acc);
+      acc = mfma(lo, b, acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr * 32 + acc_row(i), c = tc * 32 + acc_col();
+      const float p = (r >= c && r < L) ? a.scale * __expf(sG[r] - sG[c]) * acc[i] : 0.f;
+      sP[r * LDP + c] = p;
+      ptg[c * BT + r] = p;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = acc_row(i), c = 32 + acc_col();
+      sP[r * LDP + c] = 0.f;
+      ptg[c * BT + r] = 0.f;
+    }
+  }
+  __syncthreads();
+
+  bf16* sHt = sK;
+  bf16* og = (bf16*)a.o + (tok0 * a.H + h) * (long)V;
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    stage_bf16<K>(sHt, LDK, nullptr, 0, (const bf16*)a.hT + (((long)gc * a.H + h) * V + v0) * K, K, 64, 64);
+    stage_f32<64>(nullptr, 0, sUT, LDP, a.U + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    __syncthreads();
+    const int tr = w >> 1, tc = w & 1;
+    f32x16 acc = zero16();
+    for (int k0 = 0; k0 < K; k0 += 16) {
+      bf16x8 hi, lo;
+      frag_rm_f32(sQc + tr * 32 * LDQ + k0, LDQ, hi, lo);
+      const bf16x8 b = frag_rm(sHt + tc * 32 * LDK + k0, LDK);
+      acc = mfma(hi, b, acc);
+      acc = mfma(lo, b, acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] *= a.scale * sGam[tr * 32 + acc_row(i)];
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      bf16x8 phi, plo, uhi, ulo;
+      frag_rm_f32(sP + tr * 32 * LDP + k0, LDP, phi, plo);
+      frag_rm_f32(sUT + tc * 32 * LDP + k0, LDP, uhi, ulo);
+      acc = mfma(phi, uhi, acc);
+      acc = mfma(phi, ulo, acc);
+      acc = mfma(plo, uhi, acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr * 32 + acc_row(i);
+      if (r < L) og[(long)r * rsv + v0 + tc * 32 + acc_col()] = (bf16)acc[i];
+    }
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
+// gdn_bwd_state: grid ((V/32) * N * H), reverse walk
+//   dU = P^T dO + diag(gamma_L/gamma) K dS'
+//   dS <- gamma_L dS' + Qc^T diag(scale gamma) dO - w^T dU
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a, const int V) {
+  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDP = BT + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
+  constexpr int KH = K > 128 ? 128 : K, NKH = K / KH;
+  constexpr long kBytes = (long)BT * LDP * 4 + (long)VB * LDB * 2 + (long)BT * LDK * 2 + (long)VB * LDK * 2 +
+                          2L * VB * LDP * 4 + (long)KH * LDP * 4 + (long)KH * LDB * 2 + 3L * BT * 4 +
+                          (long)VB * LDK * 2 + 16 * 11;
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  Carver cv{smem};
+  float* sPT = cv.take<float>(BT * LDP);
+  bf16* sdOT = cv.take<bf16>(VB * LDB);
+  bf16* sK = cv.take<bf16>(BT * LDK);
+  bf16* sdST = cv.take<bf16>(VB * LDK);
+  bf16* sdSTl = cv.take<bf16>(VB * LDK);
+  float* sdUT = cv.take<float>(VB * LDP);   // -dU, [v][t]
+  float* sgdOT = cv.take<float>(VB * LDP);  // scale gamma_t dO[t][v], [v][t]
+  float* sQcT = cv.take<float>(KH * LDP);
+  bf16* swT = cv.take<bf16>(KH * LDB);
+  float* sFac = cv.take<float>(BT);
+  float* sGam = cv.take<float>(BT);
+  float* sGL = cv.take<float>(4);
+
+  const int tid = threadIdx.x, w = wave_id();
+  const int nv = V / VB;
+  int unit, vt;
+  xcd_map(blockIdx.x, nv, a.N * a.H, unit, vt);
+  const int n = unit / a.H, h = unit % a.H;
+  long bos;
+  int len;
+  seq_bounds(a.cu, n, a.T, bos, len);
+  const int nc = (len + BT - 1) / BT;
+  const int gc0 = a.cu ? a.chunk_off[n] : n * a.NT;
+  const int v0 = vt * VB;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+
+  f32x16 dS[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    dS[j] = zero16();
+    const int rt = w + 4 * j;
+    if (rt < NRT && a.ds_fin) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        dS[j][i] = a.ds_fin[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()];
+    }
+  }
+
+  for (int c = nc - 1; c >= 0; --c) {
+    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
+    const long tok0 = bos + c0;
+    stage_f32<64>(sPT, LDP, nullptr, 0, a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT, BT);
+    stage_bf16<32>(nullptr, 0, sdOT, LDB, (const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    stage_bf16<K>(sK, LDK, nullptr, 0, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
+    if (tid < BT) {
+      const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
+      const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
+      sFac[tid] = __expf(gl - gt);
+      sGam[tid] = (tid < L) ? __expf(gt) : 0.f;
+      if (tid == 0) sGL[0] = __expf(gl);
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int e = acc_col() * LDK + rt * 32 + acc_row(i);
+          split2(dS[j][i], sdST[e], sdSTl[e]);
+        }
+      }
+    }
+    __syncthreads();
+    lds_to_global_bf16<K>((bf16*)a.dhT + (((long)gc * a.H + h) * V + v0) * K, K, sdST, LDK, VB);
+    lds_to_global_bf16<K>((bf16*)a.dhTl + (((long)gc * a.H + h) * V + v0) * K, K, sdSTl, LDK, VB);
+    if (w < 2) {
+      f32x16 acc = zero16(), acc2 = zero16();
+      for (int k0 = 0; k0 < BT; k0 += 16) {
+        bf16x8 hi, lo;
+        frag_rm_f32(sPT + w * 32 * LDP + k0, LDP, hi, lo);
+        const bf16x8 b = frag_rm(sdOT + k0, LDB);
+        acc = mfma(hi, b, acc);
+        acc = mfma(lo, b, acc);
+      }
+      mma_rr(acc2, sK + w * 32 * LDK, LDK, sdST, LDK, K);
+      mma_rr(acc2, sK + w * 32 * LDK, LDK, sdSTl, LDK, K);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = w * 32 + acc_row(i), cc = acc_col();
+        float du = 0.f;
+        if (r < L) {
+          du = acc[i] + sFac[r] * acc2[i];
+          a.dU[(tok0 + r) * rsv + (long)h * V + v0 + cc] = du;
+        }
+        sdUT[cc * LDP + r] = -du;
+      }
+    } else {
+      for (int e = tid - 128; e < VB * BT; e += 128) {
+        const int vv = e / BT, t = e % BT;
+        sgdOT[vv * LDP + t] = a.scale * sGam[t] * (float)sdOT[vv * LDB + t];
+      }
+    }
+    __syncthreads();
+    const float gL = sGL[0];
+    for (int hb = 0; hb < NKH; ++hb) {
+      stage_any_f32<KH>(nullptr, 0, sQcT, LDP, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + hb * KH : nullptr,
+                        a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + hb * KH : nullptr, rsk, BT, L);
+      stage_bf16<KH>(nullptr, 0, swT, LDB, (const bf16*)a.w + (tok0 * a.H + h) * K + hb * KH, rsk, BT, L);
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        const int rt = w + 4 * j;
+        if (rt < NRT && (rt * 32) / KH == hb) {
+          const int lr = rt * 32 - hb * KH;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) dS[j][i] *= gL;
+          for (int k0 = 0; k0 < BT; k0 += 16) {
+            bf16x8 qhi, qlo, ghi, glo;
+            frag_rm_f32(sQcT + lr * LDP + k0, LDP, qhi, qlo);
+            frag_rm_f32(sgdOT + k0, LDP, ghi, glo);
+            dS[j] = mfma(qhi, ghi, dS[j]);
+            dS[j] = mfma(qhi, glo, dS[j]);
+            dS[j] = mfma(qlo, ghi, dS[j]);
+            const bf16x8 wa = frag_rm(swT + lr * LDB + k0, LDB);
+            bf16x8 dhi, dlo;
+            frag_rm_f32(sdUT + k0, LDP, dhi, dlo);
+            dS[j] = mfma(wa, dhi, dS[j]);
+            dS[j] = mfma(wa, dlo, dS[j]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (a.ds0) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          a.ds0[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()] = dS[j][i];
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// gdn_bwd_dqkw: grid (K/64, NTG, H)
+//   dQi = dO h^T, dKs = U dS'^T, dw = -dU h^T, dP = dO U^T   (contractions over V)
+//   dq = scale gamma dQi + dPs K,  dk = fac dKs + dPs^T Qc,  dPs = dP o scale Gamma (causal)
+//   dG partials: decay terms of O, P and the state update
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_kernel(const GdnArgs a, const int V) {
+  constexpr int LDB = 64 + 8, LDF = 64 + 4, LDP = 64 + 1;
+  constexpr long kLoop = 5L * 64 * LDB * 2 + 2L * BT * LDF * 4;
+  constexpr long kPost = 4L * BT * LDP * 4 + 2L * 64 * LDB * 2;
+  constexpr long kBytes = (kLoop > kPost ? kLoop : kPost) + 6 * BT * 4 + 4 * 4 + 64;
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  Carver cv{smem};
+  char* region = cv.p;
+  // loop-phase views
+  bf16* sHt = (bf16*)region;        // [64 v][LDB]  h[k][v] stored [v][k] for k in the tile
+  bf16* sDSt = sHt + 64 * LDB;      // [64 v][LDB]
+  bf16* sHtl = sDSt + 64 * LDB;     // low parts
+  bf16* sDStl = sHtl + 64 * LDB;
+  bf16* sdO = sDStl + 64 * LDB;     // [64 t][LDB]
+  float* sU = (float*)(sdO + 64 * LDB);  // [64 t][LDF]
+  float* sdU = sU + BT * LDF;            // [64 t][LDF]
+  // post-phase views (same region)
+  float* sdP = (float*)region;     // [64][LDP]  dP, then dPs
+  float* sQcT = sdP + BT * LDP;    // [64 k][LDP]
+  float* sRed = sQcT + 64 * LDP;   // [64][LDP]
+  float* sPt = sRed + BT * LDP;    // [64][LDP]  P^T rows (kt == 0)
+  bf16* sKt = (bf16*)(sPt + BT * LDP);  // [64 k][LDB]  K transposed
+  bf16* sKr = sKt + 64 * LDB;           // [64 t][LDB]
+  cv.p = region + (kLoop > kPost ? kLoop : kPost);
+  float* sG = cv.take<float>(BT);
+  float* sGam = cv.take<float>(BT);
+  float* sFac = cv.take<float>(BT);
+  float* sDG = cv.take<float>(BT);
+  float* sTerm = cv.take<float>(BT);
+  float* sMisc = cv.take<float>(8);
+
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int kt = blockIdx.x, gc = blockIdx.y, h = blockIdx.z;
+  int n, c0, L;
+  long bos;
+  if (!chunk_info(a, gc, n, c0, bos, L)) return;
+  const long tok0 = bos + c0;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  const int k0c = kt * 64;
+
+  const int tr = (w >> 1) * 32, tc = (w & 1) * 32;
+  const int pr = (w == 0) ? 0 : 32, pc = (w == 2) ? 32 : 0;
+  f32x16 dQi = zero16(), dKs = zero16(), dW = zero16(), dP = zero16();
+  float hds = 0.f;
+
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    stage_bf16<64>(sHt, LDB, nullptr, 0, (const bf16*)a.hT + (((long)gc * a.H + h) * V + v0) * K + k0c, K, 64, 64);
+    stage_bf16<64>(sDSt, LDB, nullptr, 0, (const bf16*)a.dhT + (((long)gc * a.H + h) * V + v0) * K + k0c, K, 64,
+                   64);
+    stage_bf16<64>(sHtl, LDB, nullptr, 0, (const bf16*)a.hTl + (((long)gc * a.H + h) * V + v0) * K + k0c, K, 64,
+                   64);
+    stage_bf16<64>(sDStl, LDB, nullptr, 0, (const bf16*)a.dhTl + (((long)gc * a.H + h) * V + v0) * K + k0c, K,
+                   64, 64);
+    stage_bf16<64>(sdO, LDB, nullptr, 0, (const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    stage_f32<64>(sU, LDF, nullptr, 0, a.U + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    stage_f32<64>(sdU, LDF, nullptr, 0, a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    __syncthreads();
+    for (int e = tid; e < 64 * 64; e += kThreads) {
+      const int vv = e >> 6, kk = e & 63;
+      hds += ((float)sHt[vv * LDB + kk] + (float)sHtl[vv * LDB + kk]) *
+             ((float)sDSt[vv * LDB + kk] + (float)sDStl[vv * LDB + kk]);
+    }
+    for (int k0 = 0; k0 < 64; k0 += 16) {
+      const bf16x8 hb = frag_cm(sHt + k0 * LDB + tc, LDB);
+      const bf16x8 hbl = frag_cm(sHtl + k0 * LDB + tc, LDB);
+      const bf16x8 db = frag_cm(sDSt + k0 * LDB + tc, LDB);
+      const bf16x8 dbl = frag_cm(sDStl + k0 * LDB + tc, LDB);
+      const bf16x8 oa = frag_rm(sdO + tr * LDB + k0, LDB);
+      dQi = mfma(oa, hb, dQi);
+      dQi = mfma(oa, hbl, dQi);
+      bf16x8 uhi, ulo, dhi, dlo;
+      frag_rm_f32(sU + tr * LDF + k0, LDF, uhi, ulo);
+      dKs = mfma(uhi, db, dKs);
+      dKs = mfma(ulo, db, dKs);
+      dKs = mfma(uhi, dbl, dKs);
+      frag_rm_f32(sdU + tr * LDF + k0, LDF, dhi, dlo);
+      dW = mfma(dhi, hb, dW);
+      dW = mfma(dlo, hb, dW);
+      dW = mfma(dhi, hbl, dW);
+      if (w < 3) {
+        bf16x8 phi, plo;
+        frag_rm_f32(sU + pc * LDF + k0, LDF, phi, plo);
+        const bf16x8 pa = frag_rm(sdO + pr * LDB + k0, LDB);
+        dP = mfma(pa, phi, dP);
+        dP = mfma(pa, plo, dP);
+      }
+    }
+    __syncthreads();
+  }
+  // <dS', h> over this column tile
+  hds = group_sum(hds, 64);
+  if (l == 0) sMisc[w] = hds;
+
+  // post phase
+  stage_any_f32<64>(nullptr, 0, sQcT, LDP, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + k0c : nullptr,
+                    a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + k0c : nullptr, rsk, BT, L);
+  stage_bf16<64>(sKr, LDB, sKt, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K + k0c, rsk, BT, L);
+  if (kt == 0) stage_f32<64>(sPt, LDP, nullptr, 0, a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT, BT);
+  if (tid < BT) {
+    const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
+    const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
+    sG[tid] = gt;
+    sGam[tid] = __expf(gt);
+    sFac[tid] = __expf(gl - gt);
+    if (tid == 0) sMisc[4] = __expf(gl);
+  }
+  // dP -> LDS (masked, zero upper tile)
+  if (w < 3) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = pr + acc_row(i), c = pc + acc_col();
+      sdP[r * LDP + c] = (r >= c && r < L) ? dP[i] : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sdP[acc_row(i) * LDP + 32 + acc_col()] = 0.f;
+  }
+  __syncthreads();
+
+  // dG from P (once per chunk):  dG_i += sum_j dP_ij P_ij ;  dG_j -= sum_i dP_ij P_ij
+  if (tid < BT) {
+    float s = 0.f;
+    if (kt == 0) {
+      for (int j = 0; j < BT; ++j) s += sdP[tid * LDP + j] * sPt[j * LDP + tid];  // row tid
+      for (int i = 0; i < BT; ++i) s -= sdP[i * LDP + tid] * sPt[tid * LDP + i];  // column tid
+    }
+    sDG[tid] = s;
+  }
+  __syncthreads();
+  // dPs = dP o scale Gamma
+  for (int e = tid; e < BT * BT; e += kThreads) {
+    const int r = e >> 6, c = e & 63;
+    if (r >= c) sdP[r * LDP + c] *= a.scale * __expf(sG[r] - sG[c]);
+  }
+  __syncthreads();
+
+  // dq tile = scale gamma dQi + dPs K[:, tile]
+  {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dQi[i] *= a.scale * sGam[tr + acc_row(i)];
+    // decay term of O: dG_i += sum_k dQi_ik qc_ik
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr + acc_row(i), c = tc + acc_col();
+      sRed[r * LDP + c] = dQi[i] * sQcT[c * LDP + r];
+    }
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      bf16x8 hi, lo;
+      frag_rm_f32(sdP + tr * LDP + k0, LDP, hi, lo);
+      const bf16x8 b = frag_rm(sKt + tc * LDB + k0, LDB);
+      dQi = mfma(hi, b, dQi);
+      dQi = mfma(lo, b, dQi);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr + acc_row(i);
+      if (r < L) a.dq32[(tok0 + r) * rsk + (long)h * K + k0c + tc + acc_col()] = dQi[i];
+    }
+  }
+  __syncthreads();
+  if (tid < BT) {
+    float s = 0.f;
+    for (int c = 0; c < 64; ++c) s += sRed[tid * LDP + c];
+    sDG[tid] += s;
+  }
+  __syncthreads();
+  // dk tile = fac dKs + dPs^T Qc[:, tile];  state-update decay term
+  {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr + acc_row(i), c = tc + acc_col();
+      dKs[i] *= sFac[r];
+      sRed[r * LDP + c] = dKs[i] * (float)sKr[r * LDB + c];
+    }
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      bf16x8 ahi, alo, bhi, blo;
+      frag_cm_f32(sdP + k0 * LDP + tr, LDP, ahi, alo);
+      frag_rm_f32(sQcT + tc * LDP + k0, LDP, bhi, blo);
+      dKs = mfma(ahi, bhi, dKs);
+      dKs = mfma(ahi, blo, dKs);
+      dKs = mfma(alo, bhi, dKs);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr + acc_row(i);
+      if (r < L) {
+        const long gi = (tok0 + r) * rsk + (long)h * K + k0c + tc + acc_col();
+        a.dkp32[gi] = dKs[i];
+        a.dw32[gi] = -dW[i];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < BT) {
+    float s = 0.f;
+    for (int c = 0; c < 64; ++c) s += sRed[tid * LDP + c];
+    sTerm[tid] = s;  // term_j
+  }
+  __syncthreads();
+  if (tid < BT && tid < L) {
+    float d = sDG[tid] - sTerm[tid];
+    if (tid == L - 1) {
+      float tot = 0.f;
+      for (int j = 0; j < L; ++j) tot += sTerm[j];
+      d += tot + sMisc[4] * (sMisc[0] + sMisc[1] + sMisc[2] + sMisc[3]);
+    }
+    const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
+    a.dgp[(long)kt * ntok * a.H + (tok0 + tid) * a.H + h] = d;
+  }
+}
+
+// ===========================================================================
+// gdn_bwd_wy: grid (NTG, H)  -- backward through w = T diag(beta gamma) K, u = T diag(beta) V,
+// T = (I + A)^-1, A = strict_lower(diag(beta) (K K^T o Gamma)).
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, const int V) {
+  constexpr int LDB = 64 + 8, LDF = 64 + 4, LDP = 64 + 1, NK = K / 64;
+  constexpr long kBytes = 6L * BT * LDP * 4 + 2L * 64 * LDB * 2 + 2L * BT * LDF * 4 + 8 * BT * 4 + 64;
+  __shared__ __attribute__((aligned(16))) char smem[kBytes];
+  Carver cv{smem};
+  float* sT = cv.take<float>(BT * LDP);
+  float* sdT = cv.take<float>(BT * LDP);   // dT, then dA, then dAs
+  float* sM1T = cv.take<float>(BT * LDP);  // (dT T^T)^T
+  float* sKK = cv.take<float>(BT * LDP);
+  float* sRed = cv.take<float>(BT * LDP);
+  float* sXT = cv.take<float>(BT * LDP);   // a transposed fp32 operand tile [64 cols][64 rows]
+  bf16* sR = cv.take<bf16>(64 * LDB);      // bf16 rows tile [t][c]
+  bf16* sCT = cv.take<bf16>(64 * LDB);     // bf16 transposed tile [c][t]
+  float* sX = cv.take<float>(BT * LDF);    // fp32 rows tile [t][c]
+  float* sY = cv.take<float>(BT * LDF);
+  float* sG = cv.take<float>(BT);
+  float* sBeta = cv.take<float>(BT);
+  float* sGam = cv.take<float>(BT);
+  float* sDB = cv.take<float>(BT);
+  float* sDG = cv.take<float>(BT);
+  float* sTmp = cv.take<float>(BT);
+
+  const int tid = threadIdx.x, w = wave_id();
+  const int gc = blockIdx.x, h = blockIdx.y;
+  int n, c0, L;
+  long bos;
+  if (!chunk_info(a, gc, n, c0, bos, L)) return;
+  const long tok0 = bos + c0;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
+  const int nkt = K / 64;
+
+  stage_f32<64>(sT, LDP, nullptr, 0, a.tmat + ((long)gc * a.H + h) * (BT * BT), BT, BT, BT);
+  if (tid < BT) {
+    const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
+    const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
+    sG[tid] = gt;
+    sGam[tid] = __expf(gt);
+    sBeta[tid] = (tid < L) ? a.beta[(tok0 + tid) * a.H + h] : 0.f;
+    float dg = 0.f;
+    if (tid < L)
+      for (int kt = 0; kt < nkt; ++kt) dg += a.dgp[(long)kt * ntok * a.H + (tok0 + tid) * a.H + h];
+    sDG[tid] = dg;
+    sDB[tid] = 0.f;
+  }
+
+  // --- dT (lower incl. diagonal tiles) and K K^T -------------------------------------
+  const int lr = (w == 0) ? 0 : 32, lc = (w == 2) ? 32 : 0;
+  f32x16 dTk = zero16(), dTv = zero16(), kk = zero16();
+  for (int kt = 0; kt < nkt; ++kt) {
+    stage_f32<64>(sX, LDF, nullptr, 0, a.dw32 + (tok0 * a.H + h) * K + kt * 64, rsk, BT, L);
+    stage_bf16<64>(sR, LDB, nullptr, 0, (const bf16*)a.k + (tok0 * a.H + h) * K + kt * 64, rsk, BT, L);
+    __syncthreads();
+    if (w < 3) {
+      for (int k0 = 0; k0 < 64; k0 += 16) {
+        bf16x8 hi, lo;
+        frag_rm_f32(sX + lr * LDF + k0, LDF, hi, lo);
+        const bf16x8 b = frag_rm(sR + lc * LDB + k0, LDB);
+        dTk = mfma(hi, b, dTk);
+        dTk = mfma(lo, b, dTk);
+        kk = mfma(frag_rm(sR + lr * LDB + k0, LDB), b, kk);
+      }
+    }
+    __syncthreads();
+  }
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    stage_f32<64>(sX, LDF, nullptr, 0, a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    stage_bf16<64>(sR, LDB, nullptr, 0, (const bf16*)a.v + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    __syncthreads();
+    if (w < 3) {
+      for (int k0 = 0; k0 < 64; k0 += 16) {
+        bf16x8 hi, lo;
+        frag_rm_f32(sX + lr * LDF + k0, LDF, hi, lo);
+        const bf16x8 b = frag_rm(sR + lc * LDB + k0, LDB);
+        dTv = mfma(hi, b, dTv);
+        dTv = mfma(lo, b, dTv);
+      }
+    }
+    __syncthreads();
+  }
+  if (w < 3) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = lr + acc_row(i), c = lc + acc_col();
+      const float v = dTk[i] * sBeta[c] * sGam[c] + dTv[i] * sBeta[c];
+      sdT[r * LDP + c] = (r > c) ? v : 0.f;
+      sKK[r * LDP + c] = (r > c) ? kk[i] : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      sdT[acc_row(i) * LDP + 32 + acc_col()] = 0.f;
+      sKK[acc_row(i) * LDP + 32 + acc_col()] = 0.f;
+    }
+  }
+  __syncthreads();
+
+  // --- M1 = dT T^T (strictly-lower part), stored transposed ---------------------------------
+  if (w < 3) {
+    f32x16 acc = zero16();
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      bf16x8 ahi, alo, bhi, blo;
+      frag_rm_f32(sdT + lr * LDP + k0, LDP, ahi, alo);
+      frag_rm_f32(sT + lc * LDP + k0, LDP, bhi, blo);
+      acc = mfma(ahi, bhi, acc);
+      acc = mfma(ahi, blo, acc);
+      acc = mfma(alo, bhi, acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = lr + acc_row(i), c = lc + acc_col();
+      sM1T[c * LDP + r] = (r > c) ? acc[i] : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sM1T[(32 + acc_col()) * LDP + acc_row(i)] = 0.f;
+  }
+  __syncthreads();
+  // --- dA = -T^T M1 (strict lower) -----------------------------------------------------------
+  if (w < 3) {
+    f32x16 acc = zero16();
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      bf16x8 ahi, alo, bhi, blo;
+      frag_cm_f32(sT + k0 * LDP + lr, LDP, ahi, alo);
+      frag_rm_f32(sM1T + lc * LDP + k0, LDP, bhi, blo);
+      acc = mfma(ahi, bhi, acc);
+      acc = mfma(ahi, blo, acc);
+      acc = mfma(alo, bhi, acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = lr + acc_row(i), c = lc + acc_col();
+      sdT[r * LDP + c] = (r > c) ? -acc[i] : 0.f;  // dA
+    }
+  }
+  __syncthreads();
+  // dbeta_i += sum_j dA_ij Gamma_ij KK_ij ; dG_i += sum_j dA_ij A_ij ; dG_j -= sum_i dA_ij A_ij
+  if (tid < BT) {
+    const int r = tid;
+    float db = 0.f, dgr = 0.f, dgc = 0.f;
+    for (int j = 0; j < r; ++j) {
+      const float gkk = __expf(sG[r] - sG[j]) * sKK[r * LDP + j];
+      const float da = sdT[r * LDP + j];
+      db += da * gkk;
+      dgr += da * sBeta[r] * gkk;
+    }
+    for (int i = r + 1; i < BT; ++i) dgc += sdT[i * LDP + r] * sBeta[i] * __expf(sG[i] - sG[r]) * sKK[i * LDP + r];
+    sTmp[r] = dgr - dgc;
+    sDB[r] += db;
+  }
+  __syncthreads();
+  if (tid < BT) sDG[tid] += sTmp[tid];
+  // dAs = dA o beta_i Gamma_ij
+  for (int e = tid; e < BT * BT; e += kThreads) {
+    const int r = e >> 6, c = e & 63;
+    if (r > c) sdT[r * LDP + c] *= sBeta[r] * __expf(sG[r] - sG[c]);
+  }
+  __syncthreads();
+
+  // --- dk tiles: dk_part + dAs K + dAs^T K + diag(beta gamma) T^T dw -------------------------
+  const int tr = (w >> 1) * 32, tc = (w & 1) * 32;
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int kc = kt * 64;
+    stage_bf16<64>(sR, LDB, sCT, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K + kc, rsk, BT, L);
+    stage_f32<64>(nullptr, 0, sXT, LDP, a.dw32 + (tok0 * a.H + h) * K + kc, rsk, BT, L);
+    __syncthreads();
+    f32x16 acc = zero16(), acc2 = zero16();
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 kb = frag_rm(sCT + tc * LDB + k0, LDB);
+      bf16x8 hi, lo;
+      frag_rm_f32(sdT + tr * LDP + k0, LDP, hi, lo);
+      acc = mfma(hi, kb, acc);
+      acc = mfma(lo, kb, acc);
+      frag_cm_f32(sdT + k0 * LDP + tr, LDP, hi, lo);
+      acc = mfma(hi, kb, acc);
+      acc = mfma(lo, kb, acc);
+      bf16x8 thi, tlo, dhi, dlo;
+      frag_cm_f32(sT + k0 * LDP + tr, LDP, thi, tlo);
+      frag_rm_f32(sXT + tc * LDP + k0, LDP, dhi, dlo);
+      acc2 = mfma(thi, dhi, acc2);
+      acc2 = mfma(thi, dlo, acc2);
+      acc2 = mfma(tlo, dhi, acc2);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr + acc_row(i), c = tc + acc_col();
+      const float kv = (float)sR[r * LDB + c];
+      sRed[r * LDP + c] = acc2[i] * kv;
+      if (r < L) {
+        const long gi = (tok0 + r) * rsk + (long)h * K + kc + c;
+        a.dk32[gi] = a.dkp32[gi] + acc[i] + sBeta[r] * sGam[r] * acc2[i];
+      }
+    }
+    __syncthreads();
+    if (tid < BT) {
+      float s = 0.f;
+      for (int c = 0; c < 64; ++c) s += sRed[tid * LDP + c];
+      sDB[tid] += sGam[tid] * s;
+      sDG[tid] += sBeta[tid] * sGam[tid] * s;
+    }
+    __syncthreads();
+  }
+  // --- dv tiles: beta_j (T^T dU)_j ; dbeta_j += (T^T dU)_j . v_j ------------------------------
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    stage_bf16<64>(sR, LDB, nullptr, 0, (const bf16*)a.v + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    stage_f32<64>(nullptr, 0, sXT, LDP, a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    __syncthreads();
+    f32x16 acc = zero16();
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      bf16x8 thi, tlo, dhi, dlo;
+      frag_cm_f32(sT + k0 * LDP + tr, LDP, thi, tlo);
+      frag_rm_f32(sXT + tc * LDP + k0, LDP, dhi, dlo);
+      acc = mfma(thi, dhi, acc);
+      acc = mfma(thi, dlo, acc);
+      acc = mfma(tlo, dhi, acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = tr + acc_row(i), c = tc + acc_col();
+      sRed[r * LDP + c] = acc[i] * (float)sR[r * LDB + c];
+      if (r < L) ((bf16*)a.dv)[(tok0 + r) * rsv + (long)h * V + v0 + c] = (bf16)(sBeta[r] * acc[i]);
+    }
+    __syncthreads();
+    if (tid < BT) {
+      float s = 0.f;
+      for (int c = 0; c < 64; ++c) s += sRed[tid * LDP + c];
+      sDB[tid] += s;
+    }
+    __syncthreads();
+  }
+  // --- dg = reverse cumulative sum of dG within the chunk; dbeta ------------------------------
+  if (w == 0) {
+    const int ll = lane_id();
+    const int r = BT - 1 - ll;  // reverse order
+    float x = (r < L) ? sDG[r] : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(x, off);
+      if (ll >= off) x += y;
+    }
+    if (r < L) {
+      a.dg[(tok0 + r) * a.H + h] = x;
+      a.dbeta[(tok0 + r) * a.H + h] = sDB[r];
+    }
+  }
+}
+
+// ===========================================================================
+// launchers
+// ===========================================================================
+template <int K>
+static hipError_t gdn_fwd_k(const GdnArgs& a, int V, hipStream_t st) {
+  if (a.NTG == 0) return hipSuccess;
+  hipLaunchKernelGGL(gdn_prep_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+  hipLaunchKernelGGL(gdn_fwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+  hipLaunchKernelGGL(gdn_fwd_o_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+  return hipGetLastError();
+}
+
+template <int K>
+static hipError_t gdn_bwd_k(const GdnArgs& a, int V, hipStream_t st) {
+  if (a.NTG == 0) return hipSuccess;
+  hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+  hipLaunchKernelGGL(gdn_bwd_dqkw_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+  hipLaunchKernelGGL(gdn_bwd_wy_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_fwd(const GdnArgs& a, int K, int V, hipStream_t st) {
+  switch (K) {
+    case 64: return gdn_fwd_k<64>(a, V, st);
+    case 128: return gdn_fwd_k<128>(a, V, st);
+    case 256: return gdn_fwd_k<256>(a, V, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gdn_bwd(const GdnArgs& a, int K, int V, hipStream_t st) {
+  switch (K) {
+    case 64: return gdn_bwd_k<64>(a, V, st);
+    case 128: return gdn_bwd_k<128>(a, V, st);
+    case 256: return gdn_bwd_k<256>(a, V, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ccq

@@ -1,0 +1,97 @@
+// Small HBM-bound kernels: row L2 normalisation (forward/backward) and the varlen chunk index.
+#include "ccq_tile.h"
+#include "ccq_params.h"
+
+namespace ccq {
+
+// y = x / sqrt(sum x^2 + eps), one 64-lane wavefront per row (D <= 512, D % 8 == 0).
+__global__ __launch_bounds__(kThreads) void l2norm_fwd_kernel(const L2NormArgs a) {
+  const long row = (long)blockIdx.x * 4 + wave_id();
+  if (row >= a.rows) return;
+  const int l = lane_id();
+  const bf16* x = (const bf16*)a.x + row * a.D;
+  float s = 0.f;
+  for (int c = l; c < a.D; c += 64) {
+    const float v = (float)x[c];
+    s += v * v;
+  }
+  s = group_sum(s, 64);
+  const float r = rsqrtf(s + a.eps);
+  bf16* y = (bf16*)a.y + row * a.D;
+  for (int c = l; c < a.D; c += 64) y[c] = (bf16)((float)x[c] * r);
+  if (l == 0 && a.rstd) a.rstd[row] = r;
+}
+
+// dx = r (dy - y (y . dy)),  y = x r  (y recomputed in fp32 from x)
+__global__ __launch_bounds__(kThreads) void l2norm_bwd_kernel(const L2NormArgs a) {
+  const long row = (long)blockIdx.x * 4 + wave_id();
+  if (row >= a.rows) return;
+  const int l = lane_id();
+  const bf16* x = (const bf16*)a.x + row * a.D;
+  const float r = a.rstd[row];
+  float s = 0.f;
+  for (int c = l; c < a.D; c += 64) {
+    const float dy = a.dy32 ? a.dy32[row * a.D + c] : (float)((const bf16*)a.dy16)[row * a.D + c];
+    s += (float)x[c] * r * dy;
+  }
+  s = group_sum(s, 64);
+  bf16* dx = (bf16*)a.dx + row * a.D;
+  for (int c = l; c < a.D; c += 64) {
+    const float dy = a.dy32 ? a.dy32[row * a.D + c] : (float)((const bf16*)a.dy16)[row * a.D + c];
+    dx[c] = (bf16)(r * (dy - (float)x[c] * r * s));
+  }
+}
+
+// chunk_off[n] = first global 64-token chunk of sequence n (exclusive scan of ceil(len/64));
+// chunk_idx[2c], [2c+1] = (sequence, chunk within sequence) for c < total, -1 beyond it (up to cap).
+__global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int64_t* cu, int N, int* chunk_off, int* chunk_idx,
+                                                               int cap) {
+  __shared__ int sOff[1];
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int n = 0; n < N; ++n) {
+      chunk_off[n] = acc;
+      const int len = (int)(cu[n + 1] - cu[n]);
+      acc += (len + 63) / 64;
+    }
+    chunk_off[N] = acc;
+    sOff[0] = acc;
+  }
+  __syncthreads();
+  const int total = sOff[0];
+  for (int c = threadIdx.x; c < cap; c += kThreads) {
+    if (c >= total) {
+      chunk_idx[2 * c] = -1;
+      chunk_idx[2 * c + 1] = -1;
+    }
+  }
+  // each thread walks a range of sequences
+  for (int n = threadIdx.x; n < N; n += kThreads) {
+    const int len = (int)(cu[n + 1] - cu[n]);
+    const int nc = (len + 63) / 64;
+    const int o = chunk_off[n];
+    for (int c = 0; c < nc && o + c < cap; ++c) {
+      chunk_idx[2 * (o + c)] = n;
+      chunk_idx[2 * (o + c) + 1] = c;
+    }
+  }
+}
+
+hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st) {
+  if (a.rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(l2norm_fwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st) {
+  if (a.rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(l2norm_bwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_chunk_index(const int64_t* cu, int N, int* chunk_off, int* chunk_idx, int cap, hipStream_t st) {
+  hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, st, cu, N, chunk_off, chunk_idx, cap);
+  return hipGetLastError();
+}
+
+}  // namespace ccq

@@ -1,0 +1,137 @@
+// Argument blocks of the CCQ kernels (plain pointers and sizes; shared by the
+// kernels and the C-ABI entry points).
+//
+// Layouts (token-major, as in the reference): q, k [tokens, H, K]; v, o [tokens, H, V];
+// per-token scalars [tokens, H]; tokens = B*T for dense inputs, the packed length for
+// varlen inputs (B == 1 with cu_seqlens [N+1]).  States are per sequence:
+// covariance [N, H, K, K], key sum [N, H, K], backbone state S [N, H, K, V].
+#pragma once
+
+#include <stdint.h>
+
+namespace ccq {
+
+struct CleanFwdArgs {
+  const void* q;            // bf16 [tokens, H, K]
+  const void* k;            // bf16 [tokens, H, K]
+  const float* lam;         // fp32 [tokens, H], unused when gate_w != nullptr
+  const float* gate_w;      // fp32 [H, K]: fused gate lambda = sigmoid(W[h].q + b[h]) (nullable)
+  const float* gate_b;      // fp32 [H]
+  float* lam_out;           // fp32 [tokens, H]: gate output (nullable)
+  const float* h0;          // fp32 [N, H, K, K] (nullable)
+  const float* m0;          // fp32 [N, H, K]    (nullable)
+  const int64_t* cu;        // [N+1] (nullable)
+  void* qc;                 // bf16 [tokens, H, K] output (nullable)
+  float* qc32;              // fp32 [tokens, H, K] output (nullable)
+  float* h_fin;             // fp32 [N, H, K, K] output (nullable)
+  float* m_fin;             // fp32 [N, H, K] output (nullable)
+  int T, H, N, pos_off, subtract_mean;
+};
+
+struct CleanBwdArgs {
+  const void* q;            // bf16
+  const void* k;            // bf16
+  const float* lam;         // fp32 [tokens, H]
+  const float* dqc32;       // fp32 upstream gradient (or dqc16)
+  const void* dqc16;        // bf16 upstream gradient
+  const float* dk_extra;    // fp32 [tokens, H, K] added into dk (nullable)
+  const float* h0;          // fp32 [N, H, K, K] (nullable; must be symmetric)
+  const float* m0;          // fp32 [N, H, K] (nullable)
+  const float* m_end;       // fp32 [N, H, K]: key sum after the sequence (m0 + sum k); required if subtract_mean
+  const int64_t* cu;
+  const float* dh_fin;      // fp32 [N, H, K, K] gradient into the final covariance state (nullable)
+  const float* dm_fin;      // fp32 [N, H, K] gradient into the final key sum (nullable)
+  void* dq;                 // bf16 [tokens, H, K] (nullable)
+  float* dq32;              // fp32 [tokens, H, K] (nullable)
+  void* dk;                 // bf16 (nullable)
+  float* dk32;              // fp32 (nullable)
+  float* dlam_part;         // fp32 [K/32, tokens, H]
+  float* dh0;               // fp32 [N, H, K, K] (nullable)
+  float* dm0;               // fp32 [N, H, K] (nullable)
+  long ntok;
+  int T, H, N, pos_off, subtract_mean;
+};
+
+struct LamReduceArgs {
+  const float* dlam_part;   // [ncb, tokens, H]
+  const float* lam;         // [tokens, H] (gate output, for the sigmoid derivative)
+  const void* q;            // bf16 [tokens, H, K] (gate input)
+  const float* gate_w;      // [H, K] (nullable: plain dlambda reduction only)
+  const float* dq32;        // fp32 dq from the cleaning backward (gate mode)
+  float* dlam;              // [tokens, H] output (nullable)
+  void* dq;                 // bf16 dq output (gate mode, nullable)
+  float* dq_out32;          // fp32 dq output (gate mode, nullable)
+  float* dw_part;           // [nblk, H, K] (gate mode)
+  float* db_part;           // [nblk, H] (gate mode)
+  long ntok;
+  int H, K, ncb;
+};
+
+struct L2NormArgs {
+  const void* x;            // bf16 [rows, D]
+  void* y;                  // bf16 [rows, D]
+  float* rstd;              // fp32 [rows]
+  const float* dy32;        // bwd: fp32 upstream (or dy16)
+  const void* dy16;
+  void* dx;                 // bf16 [rows, D]
+  long rows;
+  int D;
+  float eps;
+};
+
+}  // namespace ccq
+
+namespace ccq {
+
+// Gated delta rule (chunk size 64).  Internal buffers (all caller-allocated):
+//   gcum [tokens, H] fp32         in-chunk cumulative log decay
+//   tmat [NTG, H, 64, 64] fp32    T = (I + A)^-1 of the WY representation
+//   w    [tokens, H, K] bf16      w = T diag(beta exp(G)) K
+//   u    [tokens, H, V] fp32      u = T diag(beta) V
+//   hT   [NTG, H, V, K] bf16      state at each chunk start (transposed); hTl its low part
+//   U    [tokens, H, V] fp32      U = u - w S (pseudo-values after the delta correction)
+//   PT   [NTG, H, 64, 64] fp32    P^T, P = scale (Qc K^T o Gamma), causal incl. diagonal
+//   dU   [tokens, H, V] fp32      gradient of U
+//   dhT  [NTG, H, V, K] bf16      gradient of the state after each chunk (transposed); dhTl low part
+//   dq32 / dkp32 / dw32 [tokens, H, K] fp32, dgp [K/64, tokens, H] fp32
+struct GdnArgs {
+  const void* qc16;         // bf16 cleaned query (or qc32)
+  const float* qc32;        // fp32 cleaned query
+  const void* k;            // bf16 [tokens, H, K]
+  const void* v;            // bf16 [tokens, H, V]
+  const float* g;           // fp32 [tokens, H] log decay (nullable: no decay)
+  const float* beta;        // fp32 [tokens, H]
+  const float* s0;          // fp32 [N, H, K, V] initial state (nullable)
+  const int64_t* cu;        // [N+1] (nullable)
+  const int* chunk_idx;     // [NTG, 2] (sequence, chunk) for varlen
+  const int* chunk_off;     // [N+1] first global chunk of each sequence (varlen)
+  float* gcum;
+  float* tmat;
+  void* w;
+  float* u;
+  void* hT;
+  void* hTl;                // bf16 low parts of hT (hT + hTl ~ fp32 state)
+  float* U;
+  float* PT;
+  void* o;                  // bf16 [tokens, H, V]
+  float* s_fin;             // fp32 [N, H, K, V] (nullable)
+  // backward
+  const void* dout;         // bf16 [tokens, H, V]
+  const float* ds_fin;      // fp32 [N, H, K, V] (nullable)
+  float* dU;
+  void* dhT;
+  void* dhTl;               // bf16 low parts of dhT
+  float* dq32;              // gradient of the cleaned query
+  float* dkp32;             // gradient of k (state/output part)
+  float* dw32;
+  float* dgp;
+  float* dk32;              // gradient of k (total GDN part)
+  void* dv;                 // bf16 [tokens, H, V]
+  float* dbeta;             // fp32 [tokens, H]
+  float* dg;                // fp32 [tokens, H]
+  float* ds0;               // fp32 [N, H, K, V] (nullable)
+  float scale;
+  int T, H, N, NT, NTG;     // NT: chunks per sequence (dense); NTG: total chunks
+};
+
+}  // namespace ccq

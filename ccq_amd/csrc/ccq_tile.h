@@ -1,0 +1,336 @@
+// Shared device-side building blocks for the CCQ HIP kernels (gfx950 / CDNA4).
+//
+// Every matrix product in this library is a 32x32 output tile computed by one
+// 64-lane wavefront with v_mfma_f32_32x32x16_bf16 (fp32 accumulate).  Operand
+// fragments come from LDS.  Lane layout of that instruction (checked on the
+// device by the GPU parity tests in tests/):
+//   A (32 x 16, rows x contraction):  lane l holds row l%32, k = 8*(l/32) .. +7
+//   B (16 x 32, contraction x cols):  lane l holds col l%32, k = 8*(l/32) .. +7
+//   C (32 x 32):                      lane l holds col l%32, rows
+//                                     8*(i/4) + 4*(l/32) + i%4 for i = 0..15
+//
+// fp32 operands that must keep more than bf16's 8 significant bits are fed as
+// a hi/lo pair (x = hi + lo, both bf16) and cost two or three MFMAs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ccq {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;  // 4 wavefronts per workgroup
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// Row / column inside a 32x32 accumulator tile of element i held by this lane.
+__device__ __forceinline__ int acc_row(int i) { return ((i >> 2) << 3) + ((lane_id() >> 5) << 2) + (i & 3); }
+__device__ __forceinline__ int acc_col() { return lane_id() & 31; }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+
+__device__ __forceinline__ void split2(float x, bf16& hi, bf16& lo) {
+  hi = (bf16)x;
+  lo = (bf16)(x - (float)hi);
+}
+
+// ---------------------------------------------------------------------------
+// fragment loaders.  `p` points at element (row 0, k 0) of the 32-row slab.
+// ---------------------------------------------------------------------------
+
+// Element (r, k) at p[r * ld + k]  (contraction index contiguous: one 16-byte read).
+__device__ __forceinline__ bf16x8 frag_rm(const bf16* p, int ld) {
+  const int l = lane_id();
+  return *(const bf16x8*)(p + (l & 31) * ld + ((l >> 5) << 3));
+}
+
+// Element (r, k) at p[k * ld + r]  (operand stored transposed: eight 2-byte reads).
+__device__ __forceinline__ bf16x8 frag_cm(const bf16* p, int ld) {
+  const int l = lane_id();
+  const bf16* q = p + ((l >> 5) << 3) * ld + (l & 31);
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = q[i * ld];
+  return v;
+}
+
+// fp32 operand, element (r, k) at p[r * ld + k], split into hi/lo on the fly.
+__device__ __forceinline__ void frag_rm_f32(const float* p, int ld, bf16x8& hi, bf16x8& lo) {
+  const int l = lane_id();
+  const float* q = p + (l & 31) * ld + ((l >> 5) << 3);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bf16 h, o;
+    split2(q[i], h, o);
+    hi[i] = h;
+    lo[i] = o;
+  }
+}
+
+// fp32 operand, element (r, k) at p[k * ld + r], split into hi/lo on the fly.
+__device__ __forceinline__ void frag_cm_f32(const float* p, int ld, bf16x8& hi, bf16x8& lo) {
+  const int l = lane_id();
+  const float* q = p + ((l >> 5) << 3) * ld + (l & 31);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bf16 h, o;
+    split2(q[i * ld], h, o);
+    hi[i] = h;
+    lo[i] = o;
+  }
+}
+
+// fp32 operand element (r, k) at p[r * ld + k] scaled by ks[k] (scale indexed by the contraction
+// index), split into hi/lo on the fly.
+__device__ __forceinline__ void frag_rm_f32_ks(const float* p, int ld, const float* ks, bf16x8& hi, bf16x8& lo) {
+  const int l = lane_id();
+  const int kb = (l >> 5) << 3;
+  const float* q = p + (l & 31) * ld + kb;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bf16 hh, oo;
+    split2(q[i] * ks[kb + i], hh, oo);
+    hi[i] = hh;
+    lo[i] = oo;
+  }
+}
+
+// 0/1 lower-triangular (inclusive) fragment: element (r, k) = (k <= r), rows offset r0, k offset k0.
+__device__ __forceinline__ bf16x8 frag_tril_ones(int r0, int k0) {
+  const int l = lane_id();
+  const int r = r0 + (l & 31);
+  const int kb = k0 + ((l >> 5) << 3);
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)((kb + i <= r) ? 1.f : 0.f);
+  return v;
+}
+
+// 0/1 upper-triangular (inclusive) fragment: element (r, k) = (k >= r).
+__device__ __forceinline__ bf16x8 frag_triu_ones(int r0, int k0) {
+  const int l = lane_id();
+  const int r = r0 + (l & 31);
+  const int kb = k0 + ((l >> 5) << 3);
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)((kb + i >= r) ? 1.f : 0.f);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// whole-contraction helpers: acc += A B over kdim (multiple of 16)
+// A: rows from p_a (layout rm or cm), B: columns from p_b (layout rm = [col][k], cm = [k][col])
+// ---------------------------------------------------------------------------
+
+// A row-major [r][k], B stored [n][k]
+__device__ __forceinline__ void mma_rr(f32x16& acc, const bf16* a, int lda, const bf16* b, int ldb, int kdim) {
+  for (int k0 = 0; k0 < kdim; k0 += 16) acc = mfma(frag_rm(a + k0, lda), frag_rm(b + k0, ldb), acc);
+}
+
+// A stored [k][r] (transposed), B stored [n][k]
+__device__ __forceinline__ void mma_cr(f32x16& acc, const bf16* a, int lda, const bf16* b, int ldb, int kdim) {
+  for (int k0 = 0; k0 < kdim; k0 += 16) acc = mfma(frag_cm(a + k0 * lda, lda), frag_rm(b + k0, ldb), acc);
+}
+
+// A stored [r][k], B stored [k][n] (transposed)
+__device__ __forceinline__ void mma_rc(f32x16& acc, const bf16* a, int lda, const bf16* b, int ldb, int kdim) {
+  for (int k0 = 0; k0 < kdim; k0 += 16) acc = mfma(frag_rm(a + k0, lda), frag_cm(b + k0 * ldb, ldb), acc);
+}
+
+// ---------------------------------------------------------------------------
+// global -> LDS tile staging (rows of a token-major tensor)
+// ---------------------------------------------------------------------------
+
+// Copy `rows` rows of D bf16 each (row r at g[r * gstride]) into LDS (row-major, leading dim ld)
+// and optionally a transposed copy (dst_t[c * ldt + r]).  Rows >= nvalid are zero-filled.
+template <int D>
+__device__ __forceinline__ void stage_bf16(bf16* dst, int ld, bf16* dst_t, int ldt, const bf16* g, long gstride,
+                                           int rows, int nvalid) {
+  constexpr int VPR = D / 8;
+  for (int idx = threadIdx.x; idx < rows * VPR; idx += kThreads) {
+    const int r = idx / VPR, c = (idx % VPR) * 8;
+    bf16x8 v;
+    if (r < nvalid) {
+      v = *(const bf16x8*)(g + (long)r * gstride + c);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (bf16)0.f;
+    }
+    if (dst) *(bf16x8*)(dst + r * ld + c) = v;
+    if (dst_t) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dst_t[(c + i) * ldt + r] = v[i];
+    }
+  }
+}
+
+// Same for fp32 rows into fp32 LDS (row-major and/or transposed).
+template <int D>
+__device__ __forceinline__ void stage_f32(float* dst, int ld, float* dst_t, int ldt, const float* g, long gstride,
+                                          int rows, int nvalid) {
+  constexpr int VPR = D / 4;
+  for (int idx = threadIdx.x; idx < rows * VPR; idx += kThreads) {
+    const int r = idx / VPR, c = (idx % VPR) * 4;
+    f32x4 v;
+    if (r < nvalid) {
+      v = *(const f32x4*)(g + (long)r * gstride + c);
+    } else {
+      v[0] = v[1] = v[2] = v[3] = 0.f;
+    }
+    if (dst) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[r * ld + c + i] = v[i];
+    }
+    if (dst_t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst_t[(c + i) * ldt + r] = v[i];
+    }
+  }
+}
+
+// Sequence bounds for dense ([B, T]) or varlen (B == 1 + cu_seqlens) inputs.
+__device__ __forceinline__ void seq_bounds(const int64_t* cu, int n, int T, long& bos, int& len) {
+  if (cu) {
+    bos = (long)cu[n];
+    len = (int)(cu[n + 1] - cu[n]);
+  } else {
+    bos = (long)n * T;
+    len = T;
+  }
+}
+
+// Workgroups are handed to the 8 XCDs round-robin by linear id.  Give the `nsplit`
+// workgroups that share one (sequence, head) the same XCD so they share its L2.
+__device__ __forceinline__ void xcd_map(int bid, int nsplit, int nunits, int& unit, int& split) {
+  if ((nunits & 7) == 0) {
+    const int xcd = bid & 7, slot = bid >> 3;
+    split = slot % nsplit;
+    unit = (slot / nsplit) * 8 + xcd;
+  } else {
+    split = bid % nsplit;
+    unit = bid / nsplit;
+  }
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+
+
+// ---------------------------------------------------------------------------
+// register prefetch of a ROWS x D tile (one step ahead of its use)
+// ---------------------------------------------------------------------------
+
+template <int D, int ROWS>
+struct PrefetchBf16 {
+  static constexpr int VPR = D / 8;
+  static constexpr int N = (ROWS * VPR + kThreads - 1) / kThreads;
+  bf16x8 v[N];
+  __device__ __forceinline__ void load(const bf16* g, long gstride, int nvalid) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int r = idx / VPR, c = (idx % VPR) * 8;
+      if (idx < ROWS * VPR && r < nvalid) {
+        v[j] = *(const bf16x8*)(g + (long)r * gstride + c);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[j][i] = (bf16)0.f;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(bf16* dst, int ld, bf16* dst_t, int ldt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      if (idx >= ROWS * VPR) continue;
+      const int r = idx / VPR, c = (idx % VPR) * 8;
+      if (dst) *(bf16x8*)(dst + r * ld + c) = v[j];
+      if (dst_t) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dst_t[(c + i) * ldt + r] = v[j][i];
+      }
+    }
+  }
+};
+
+template <int D, int ROWS>
+struct PrefetchF32 {
+  static constexpr int VPR = D / 4;
+  static constexpr int N = (ROWS * VPR + kThreads - 1) / kThreads;
+  f32x4 v[N];
+  __device__ __forceinline__ void load(const float* g, long gstride, int nvalid) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int r = idx / VPR, c = (idx % VPR) * 4;
+      if (idx < ROWS * VPR && r < nvalid) {
+        v[j] = *(const f32x4*)(g + (long)r * gstride + c);
+      } else {
+        v[j][0] = v[j][1] = v[j][2] = v[j][3] = 0.f;
+      }
+    }
+  }
+  // bf16 source promoted to fp32 (8 elements per vector -> two f32x4 per thread slot)
+  __device__ __forceinline__ void store(float* dst, int ld, float* dst_t, int ldt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      if (idx >= ROWS * VPR) continue;
+      const int r = idx / VPR, c = (idx % VPR) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (dst) dst[r * ld + c + i] = v[j][i];
+        if (dst_t) dst_t[(c + i) * ldt + r] = v[j][i];
+      }
+    }
+  }
+};
+
+// A gradient input that may arrive as fp32 or bf16 rows, staged into fp32 LDS.
+template <int D, int ROWS>
+struct PrefetchGrad {
+  PrefetchF32<D, ROWS> f;
+  PrefetchBf16<D, ROWS> b;
+  __device__ __forceinline__ void load(const float* g32, const bf16* g16, long gstride, int nvalid) {
+    if (g32) f.load(g32, gstride, nvalid);
+    else b.load(g16, gstride, nvalid);
+  }
+  __device__ __forceinline__ void store(bool is32, float* dst, int ld) const {
+    if (is32) {
+      f.store(dst, ld, nullptr, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < PrefetchBf16<D, ROWS>::N; ++j) {
+        const int idx = threadIdx.x + j * kThreads;
+        if (idx >= ROWS * (D / 8)) continue;
+        const int r = idx / (D / 8), c = (idx % (D / 8)) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dst[r * ld + c + i] = (float)b.v[j][i];
+      }
+    }
+  }
+};
+
+// Sum over the 2^log2n consecutive lanes that share a group (butterfly).
+__device__ __forceinline__ float group_sum(float x, int n) {
+  for (int m = 1; m < n; m <<= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+}  // namespace ccq

@@ -1,0 +1,140 @@
+/*
+ * ccq_hip.h -- C ABI of the MI355X (gfx950) CCQ library, libccq_hip.so.
+ *
+ * All pointers are device pointers allocated by the caller; every call is
+ * asynchronous on the given HIP stream (hipStream_t passed as void*, NULL =
+ * default stream) and returns 0 on success or a negative status
+ * (CCQ_ERR_*); ccq_last_error() describes the last failure of the calling
+ * host thread.  No entry point allocates device memory or keeps state between
+ * calls; buffers a backward pass needs from its forward ("saved") and scratch
+ * space ("workspace") are caller-provided, sized by the *_bytes() queries.
+ *
+ * Layouts follow the reference (token-major, head-interleaved):
+ *   q, k [tokens, H, K] bf16; v, o [tokens, H, V] bf16; per-token scalars
+ *   [tokens, H] fp32; tokens = B*T (dense) or the packed length (varlen:
+ *   B == 1 and cu_seqlens int64 [N+1]).  Per-sequence states are fp32:
+ *   covariance [N, H, K, K], key sum [N, H, K], backbone state [N, H, K, V].
+ */
+#ifndef CCQ_HIP_H
+#define CCQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CCQ_OK 0
+#define CCQ_ERR_SHAPE (-1)     /* unsupported or inconsistent sizes */
+#define CCQ_ERR_NULL (-2)      /* a required pointer is NULL */
+#define CCQ_ERR_ALIGN (-3)     /* a pointer is not 16-byte aligned */
+#define CCQ_ERR_HIP (-4)       /* a HIP runtime error (see ccq_last_error) */
+
+int ccq_abi_version(void);
+const char* ccq_last_error(void);
+
+/*
+ * Fused covariance read + cleaning, forward.
+ * Replaces the reference's FusedCCQCleanRead.forward -> _fused_read_fwd
+ * (ccq/ops/common/fused_read.py:480-491, :379-403), i.e. fla chunk_fwd_h(v=k)
+ * + _cumk_chunk_prefix + _ccq_fused_read_fwd_kernel, and the stock
+ * _ccq_compute_z_and_sum_kk + _CCQCleanQ forward (clean.py:751-771, :696-715).
+ *
+ *   q_clean_t = q_t - lambda_t (h_t^T q_t / pos_t - (m_t . q_t) m_t / pos_t^2)
+ *   h_t = h0 + sum_{j<=t} k_j k_j^T, m_t = m0 + sum_{j<=t} k_j, pos_t = max(t + 1 + position_offset, 1)
+ *
+ * lambda: fp32 [tokens, H] (the reference's lambda after _reshape_lambda_3d,
+ *   clean.py:314-325).  Alternatively gate_w [H, K] / gate_b [H] (fp32) compute
+ *   lambda_t = sigmoid(gate_w[h] . q_t + gate_b[h]) in the kernel (lambda is then
+ *   ignored and written to lambda_out if non-NULL) -- the per-head form of the
+ *   reference layer's erase_lambda_proj (ccq/gdn/layer.py:174, 292).
+ * h0, m0: initial states (nullable); m0 is ignored unless subtract_mean.
+ * Outputs: q_clean bf16 and/or q_clean_f32 (at least one), h_final, m_final (nullable).
+ * K in {32, 64, 128, 256}.
+ */
+int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
+                  float* lambda_out, const float* h0, const float* m0, const int64_t* cu_seqlens, void* q_clean,
+                  float* q_clean_f32, float* h_final, float* m_final, int B, int T, int H, int K, int N,
+                  int position_offset, int subtract_mean, void* stream);
+
+/* Workspace bytes for ccq_clean_bwd (gate != 0: the fused-gate form). */
+size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int H, int K, int gate);
+
+/*
+ * Cleaning backward.  Replaces FusedCCQCleanRead.backward -> _fused_read_bwd
+ * (fused_read.py:496-514, :406-460: chunk_bwd_dh, _ccq_fused_read_bwd_kernel,
+ * the dlambda tile sum :443, _chunk_carry + _ccq_add_carry_kernel) and
+ * _CCQCleanQ.backward (clean.py:720-748).
+ *
+ * dq_clean: upstream gradient, fp32 (dq_clean_f32) or bf16 (dq_clean).
+ * dk_extra: optional fp32 [tokens, H, K] added into dk (another use of k).
+ * m_end: key sum after each sequence (m_final of the forward); required if subtract_mean.
+ * dh_final / dm_final: gradients into the final states (nullable).
+ * Outputs: dq, dk (bf16 and/or fp32 variants, at least one of each),
+ *   dlambda fp32 [tokens, H] (per-token form) or, with gate_w/gate_b (and the
+ *   forward's lambda_out passed as lambda), dgate_w [H, K] and dgate_b [H] with
+ *   the gate's path folded into dq; dh0, dm0 (nullable; h0 must be symmetric).
+ */
+int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
+                  const float* dq_clean_f32, const void* dq_clean, const float* dk_extra, const float* h0,
+                  const float* m0, const float* m_end, const int64_t* cu_seqlens, const float* dh_final,
+                  const float* dm_final, void* dq, float* dq_f32, void* dk, float* dk_f32, float* dlambda,
+                  float* dgate_w, float* dgate_b, float* dh0, float* dm0, void* workspace, int B, int T, int H,
+                  int K, int N, int position_offset, int subtract_mean, void* stream);
+
+/*
+ * Varlen chunk index: chunk_offsets int32 [N+1] and chunk_index int32 [capacity, 2]
+ * ((sequence, chunk) per 64-token chunk, -1 past the end), capacity >= tokens/64 + N.
+ * Replaces fla prepare_chunk_indices / prepare_chunk_offsets (fused_read.py:36, :349-352).
+ */
+int ccq_chunk_index(const int64_t* cu_seqlens, int N, int* chunk_offsets, int* chunk_index, int capacity,
+                    void* stream);
+
+/* Bytes of the forward-to-backward buffer and of the backward workspace of the GDN chunk path. */
+size_t ccq_gdn_saved_bytes(int64_t tokens, int num_chunks, int H, int K, int V);
+size_t ccq_gdn_bwd_workspace_bytes(int64_t tokens, int num_chunks, int H, int K, int V);
+
+/*
+ * Gated delta rule, chunk form (64-token chunks), forward.
+ * Replaces fla chunk_gated_delta_rule as called by the reference
+ * (ccq/ops/ccq_gdn/fused_chunk.py:54-58, chunk.py:132-142):
+ *   S <- exp(g_t) S; u = beta_t (v_t - S^T k_t); S <- S + k_t u^T; o_t = S^T (scale q_t)
+ * q: bf16 (q) or fp32 (q_f32: the cleaned query kept in fp32); g fp32 [tokens, H]
+ * (log decay, nullable = 0); beta fp32 [tokens, H]; initial_state fp32 [N, H, K, V]
+ * (nullable).  num_chunks = B * ceil(T/64) (dense) or the capacity used for
+ * ccq_chunk_index (varlen, with chunk_index / chunk_offsets).
+ * Outputs: o bf16, final_state fp32 (nullable), saved (ccq_gdn_saved_bytes).
+ * K in {64, 128, 256}; V a multiple of 64.
+ */
+int ccq_gdn_fwd(const void* q, const float* q_f32, const void* k, const void* v, const float* g, const float* beta,
+                const float* initial_state, const int64_t* cu_seqlens, const int* chunk_index,
+                const int* chunk_offsets, int num_chunks, void* o, float* final_state, void* saved, int B, int T,
+                int H, int K, int V, int N, float scale, void* stream);
+
+/*
+ * Gated delta rule backward (same inputs and saved buffer as the forward).
+ * d_o bf16 [tokens, H, V], d_final_state fp32 (nullable).
+ * Outputs: dq_f32, dk_f32 fp32 [tokens, H, K]; dv bf16; dbeta, dg fp32 [tokens, H];
+ * d_initial_state fp32 [N, H, K, V] (nullable).
+ */
+int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v, const float* g, const float* beta,
+                const int64_t* cu_seqlens, const int* chunk_index, const int* chunk_offsets, int num_chunks,
+                const void* saved, const void* d_o, const float* d_final_state, void* workspace, float* dq_f32,
+                float* dk_f32, void* dv, float* dbeta, float* dg, float* d_initial_state, int B, int T, int H, int K,
+                int V, int N, float scale, void* stream);
+
+/*
+ * Row L2 normalisation y = x / sqrt(sum x^2 + eps) (bf16 rows of D <= 512) and its backward.
+ * Replaces fla l2norm as called by the reference (ccq/ops/ccq_gdn/fused_chunk.py:43-44).
+ * rstd fp32 [rows] is written by the forward and read by the backward.
+ */
+int ccq_l2norm_fwd(const void* x, void* y, float* rstd, int64_t rows, int D, float eps, void* stream);
+int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const void* dy, void* dx, int64_t rows,
+                   int D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CCQ_HIP_H */

@@ -1,0 +1,35 @@
+"""Shared helpers of the test-suite: seeded inputs (generated on the CPU) and error measures."""
+
+import math
+
+import torch
+
+
+def rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    """Relative L2 error ||a - b|| / ||b||, computed in float64 on the CPU."""
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    den = b.norm().item()
+    return (a - b).norm().item() / (den if den > 0 else 1.0)
+
+
+def bf(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16)
+
+
+def l2n(x: torch.Tensor) -> torch.Tensor:
+    return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+
+
+def gdn_inputs(B, T, H, K, V, seed=0, with_state=False, device="cuda"):
+    """q, k (L2-normalised, bf16), v (bf16), g (fp32 log decay), beta (fp32) and optional s0."""
+    gen = torch.Generator().manual_seed(seed)
+    q = bf(l2n(torch.randn(B, T, H, K, generator=gen)))
+    k = bf(l2n(torch.randn(B, T, H, K, generator=gen)))
+    v = bf(torch.randn(B, T, H, V, generator=gen))
+    a_log = torch.empty(H).uniform_(0.0, math.log(16.0), generator=gen)
+    g = (-torch.nn.functional.softplus(torch.randn(B, T, H, generator=gen)) * a_log.exp() * 0.1).float()
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen)).float()
+    s0 = torch.randn(B, H, K, V, generator=gen) * 0.1 if with_state else None
+    out = dict(q=q, k=k, v=v, g=g, beta=beta, s0=s0)
+    return {n: (t.to(device) if t is not None else None) for n, t in out.items()}, gen
