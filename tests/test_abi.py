@@ -1,0 +1,107 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point that
+include/ccq_hip.h declares, and rejects invalid arguments with the documented status codes
+before launching anything."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from ccq_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ccq_hip.h")
+
+CCQ_ERR_SHAPE, CCQ_ERR_NULL = -1, -2
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ccq_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+    assert lib.ccq_abi_version() == 1
+
+
+def _fake():
+    return ctypes.c_void_p(0x1000)  # never dereferenced: argument checks fail first
+
+
+def test_clean_fwd_rejects_bad_k():
+    lib = _lib.load()
+    p = _fake()
+    st = lib.ccq_clean_fwd(p, p, p, None, None, None, None, None, None, p, None, None, None, 1, 64, 2, 48, 1, 0, 1,
+                           None)
+    assert st == CCQ_ERR_SHAPE
+    assert b"K=48" in lib.ccq_last_error()
+
+
+def test_clean_fwd_rejects_missing_lambda_and_output():
+    lib = _lib.load()
+    p = _fake()
+    assert lib.ccq_clean_fwd(p, p, None, None, None, None, None, None, None, p, None, None, None, 1, 64, 2, 64, 1,
+                             0, 1, None) == CCQ_ERR_NULL
+    assert lib.ccq_clean_fwd(p, p, p, None, None, None, None, None, None, None, None, None, None, 1, 64, 2, 64, 1,
+                             0, 1, None) == CCQ_ERR_NULL
+
+
+def test_varlen_requires_batch_one():
+    lib = _lib.load()
+    p = _fake()
+    st = lib.ccq_clean_fwd(p, p, p, None, None, None, None, None, p, p, None, None, None, 2, 64, 2, 64, 3, 0, 1, None)
+    assert st == CCQ_ERR_SHAPE
+
+
+def test_clean_bwd_requires_m_end_with_mean():
+    lib = _lib.load()
+    p = _fake()
+    args = [p, p, p, None, None, p, None, None, None, None, None, None, None, None, p, None, p, None, None, None,
+            None, None, None, p, 1, 64, 2, 64, 1, 0, 1, None]
+    assert lib.ccq_clean_bwd(*args) == CCQ_ERR_NULL
+
+
+def test_gdn_rejects_bad_shapes():
+    lib = _lib.load()
+    p = _fake()
+    # V not a multiple of 64
+    st = lib.ccq_gdn_fwd(p, None, p, p, p, p, None, None, None, None, 1, p, None, p, 1, 64, 2, 64, 100, 1, 0.1, None)
+    assert st == CCQ_ERR_SHAPE
+    # K unsupported
+    st = lib.ccq_gdn_fwd(p, None, p, p, p, p, None, None, None, None, 1, p, None, p, 1, 64, 2, 96, 64, 1, 0.1, None)
+    assert st == CCQ_ERR_SHAPE
+    # wrong chunk count for dense inputs
+    st = lib.ccq_gdn_fwd(p, None, p, p, p, p, None, None, None, None, 3, p, None, p, 1, 64, 2, 64, 64, 1, 0.1, None)
+    assert st == CCQ_ERR_SHAPE
+    # varlen without the chunk index
+    st = lib.ccq_gdn_fwd(p, None, p, p, p, p, None, p, None, None, 3, p, None, p, 1, 64, 2, 64, 64, 2, 0.1, None)
+    assert st == CCQ_ERR_NULL
+
+
+def test_l2norm_rejects_wide_rows():
+    lib = _lib.load()
+    p = _fake()
+    assert lib.ccq_l2norm_fwd(p, p, p, 10, 1024, 1e-6, None) == CCQ_ERR_SHAPE
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (128, 128), (256, 512)])
+def test_workspace_sizes_are_consistent(K, V):
+    lib = _lib.load()
+    tokens, H = 4096, 4
+    nt = tokens // 64
+    saved = lib.ccq_gdn_saved_bytes(tokens, nt, H, K, V)
+    # gcum + T + w + u + hT (hi, lo) + U + P^T, each rounded up to 256 bytes
+    expect = tokens * H * 4 + nt * H * 4096 * 4 + tokens * H * K * 2 + tokens * H * V * 4 + 2 * nt * H * V * K * 2 \
+        + tokens * H * V * 4 + nt * H * 4096 * 4
+    assert expect <= saved <= expect + 7 * 256
+    ws = lib.ccq_clean_bwd_workspace_bytes(tokens, H, K, 0)
+    assert ws >= (K // 32) * tokens * H * 4
+    assert lib.ccq_clean_bwd_workspace_bytes(tokens, H, K, 1) > ws
