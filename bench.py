@@ -54,12 +54,49 @@ def make_inputs(device, seed=0, b=B, t=T):
     return {n: x.to(device) for n, x in xs.items()}
 
 
+LEAVES = ("q", "k", "v", "g", "beta", "w", "b")
+
+
 def gpu_step(x):
+    """One training step of the path: forward, then the gradients of every input."""
     from ccq_amd import fused_chunk_ccq_gdn
     o, _, _, _ = fused_chunk_ccq_gdn(x["q"], x["k"], x["v"], None, x["g"], x["beta"], gate_w=x["w"],
                                      gate_b=x["b"], use_qk_l2norm_in_kernel=False)
-    o.backward(x["do"])
-    return o
+    return torch.autograd.grad(o, [x[n] for n in LEAVES], x["do"])
+
+
+def kernel_work(k=K, v=V, bt=BT):
+    """Algorithmic FLOP and bytes per token x head of each kernel (its own inputs read once,
+    its own outputs written once; the decomposition and formulas are listed in DESIGN.md)."""
+    return {
+        "clean_fwd": (4 * k * k + 4 * bt * k, 4 * k + 4 * k + 4),
+        "clean_bwd": (8 * k * k + 8 * bt * k, 16 * k + 8),
+        "gdn_prep": (2 * bt * (2 * k + v) + (2 * bt * bt) // 3, 2 * k + 2 * v + 8 + 2 * k + 4 * v + 4 + 4 * bt),
+        "gdn_fwd_state": (4 * k * v, 4 * k + 4 * v + 4 * v + 4 * k * v // bt),
+        "gdn_fwd_o": (2 * bt * k + 2 * k * v + 2 * bt * v, 4 * k + 2 * k + 2 * k * v // bt + 4 * v + 2 * v + 4 * bt),
+        "gdn_bwd_state": (2 * bt * v + 6 * k * v, 4 * bt + 2 * v + 2 * k + 4 * k + 2 * k + 4 * v + 4 * k * v // bt),
+        "gdn_bwd_dqkw": (6 * k * v + 2 * bt * v + 4 * bt * k,
+                         8 * k * v // bt + 2 * v + 4 * v + 4 * v + 4 * k + 2 * k + 4 * bt + 12 * k + 4),
+        "gdn_bwd_wy": (10 * bt * k + 4 * bt * v + 4 * bt * bt,
+                       4 * bt + 4 * k + 4 * v + 2 * k + 2 * v + 4 * k + 4 * k + 2 * v + 8),
+    }
+
+
+def roofline(step_kernel_ms, launches_per_step):
+    """Roofline object for the kernel with the largest share of the step."""
+    work = kernel_work()
+    name = max((n for n in step_kernel_ms if n in work), key=lambda n: step_kernel_ms[n])
+    flop, byts = work[name]
+    units = B * T * H
+    avg_s = step_kernel_ms[name] / launches_per_step[name] * 1e-3
+    ai = flop / byts
+    if ai >= PEAK_BF16 / PEAK_HBM:
+        achieved, peak, unit, bound = flop * units / avg_s / 1e12, PEAK_BF16 / 1e12, "TFLOP/s", "mfma"
+    else:
+        achieved, peak, unit, bound = byts * units / avg_s / 1e9, PEAK_HBM / 1e9, "GB/s", "hbm"
+    return {"kernel": name, "bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+            "frac": achieved / peak, "traffic": None, "avg_launch_us": avg_s * 1e6,
+            "algorithmic_flop_per_launch": flop * units, "algorithmic_bytes_per_launch": byts * units}
 
 
 def cpu_baseline(seconds_budget=25.0):
@@ -70,7 +107,7 @@ def cpu_baseline(seconds_budget=25.0):
     torch.set_num_threads(os.cpu_count() or 1)
     t_s = 4096
     x = make_inputs("cpu", seed=0, b=1, t=t_s)
-    for n in ("q", "k", "v", "g", "beta", "w", "b"):
+    for n in LEAVES:
         x[n] = x[n].float().requires_grad_()
 
     def step():
@@ -105,17 +142,26 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     x = make_inputs(dev)
-    for n in ("q", "k", "v", "g", "beta", "w", "b"):
+    for n in LEAVES:
         x[n].requires_grad_()
+    from ccq_amd import _lib
 
     for _ in range(args.warmup):
         gpu_step(x)
     torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         gpu_step(x)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    _lib.timing_enable(False)
+    kms, klaunch = {}, {}
+    for name in _lib.KERNELS:
+        ms_tot, n = _lib.timing_read(name)
+        if n:
+            kms[name], klaunch[name] = ms_tot / args.steps, n / args.steps
     ms = elapsed / args.steps * 1e3
     tokens_per_s = B * T * args.steps / elapsed
     flops = FLOP_PER_TOKEN_HEAD * B * T * H
@@ -134,7 +180,9 @@ def main():
         "data": "synthetic (seeded, BASELINE.json configs[1] + configs[2] GDN conventions)",
         "config": {"workload": "fused CCQ cleaning (per-head gate) + GDN chunk fwd+bwd", "B": B, "T": T, "H": H,
                    "d_k": K, "d_v": V, "chunk": BT, "algorithmic_flop_per_step": flops,
-                   "mfma_peak_fraction": flops / (ms * 1e-3) / PEAK_BF16},
+                   "mfma_peak_fraction": flops / (ms * 1e-3) / PEAK_BF16,
+                   "kernel_ms_per_step": {n: round(v, 4) for n, v in kms.items()}},
+        "roofline": roofline(kms, klaunch),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()

@@ -34,6 +34,9 @@ SIGNATURES = {
     "ccq_gdn_bwd": (_I, [_P] * 9 + [_I] + [_P] * 10 + [_I] * 6 + [_F, _P]),
     "ccq_l2norm_fwd": (_I, [_P, _P, _P, _I64, _I, _F, _P]),
     "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
+    "ccq_timing_enable": (_I, [_I]),
+    "ccq_timing_reset": (_I, []),
+    "ccq_timing_read": (_I, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -73,3 +76,23 @@ def check(status: int, what: str) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args), name)
+
+
+KERNELS = ("clean_fwd", "clean_bwd", "lam_reduce", "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state",
+           "gdn_bwd_dqkw", "gdn_bwd_wy")
+
+
+def timing_enable(on: bool) -> None:
+    call("ccq_timing_enable", int(bool(on)))
+
+
+def timing_reset() -> None:
+    call("ccq_timing_reset")
+
+
+def timing_read(kernel: str):
+    """(total milliseconds, launches) recorded for `kernel` since the last reset."""
+    ms = ctypes.c_double(0.0)
+    n = ctypes.c_int64(0)
+    call("ccq_timing_read", kernel.encode(), ctypes.byref(ms), ctypes.byref(n))
+    return ms.value, n.value

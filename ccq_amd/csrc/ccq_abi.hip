@@ -4,6 +4,11 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/ccq_hip.h"
 #include "ccq_params.h"
@@ -13,8 +18,7 @@ hipError_t launch_clean_fwd(const CleanFwdArgs& a, int K, hipStream_t st);
 hipError_t launch_clean_bwd(const CleanBwdArgs& a, int K, hipStream_t st);
 hipError_t launch_lam_reduce(const LamReduceArgs& a, hipStream_t st);
 hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, hipStream_t st);
-hipError_t launch_gdn_fwd(const GdnArgs& a, int K, int V, hipStream_t st);
-hipError_t launch_gdn_bwd(const GdnArgs& a, int K, int V, hipStream_t st);
+hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st);
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_chunk_index(const int64_t* cu, int N, int* chunk_off, int* chunk_idx, int cap, hipStream_t st);
@@ -64,6 +68,57 @@ int check_common(int B, int T, int H, int N, const int64_t* cu) {
 
 int clean_k_ok(int K) { return K == 32 || K == 64 || K == 128 || K == 256; }
 
+// ---- optional kernel timing (measurement only; off unless ccq_timing_enable(1)) ----
+struct TimingState {
+  std::mutex mu;
+  bool on = false;
+  std::map<std::string, std::vector<std::pair<hipEvent_t, hipEvent_t>>> pending;
+  std::map<std::string, std::pair<double, int64_t>> done;
+};
+
+TimingState& timing() {
+  static TimingState t;
+  return t;
+}
+
+// Run `launch` between two events recorded on `st` when timing is enabled.
+template <typename F>
+hipError_t timed(const char* name, hipStream_t st, F&& launch) {
+  TimingState& t = timing();
+  {
+    std::lock_guard<std::mutex> g(t.mu);
+    if (!t.on) return launch();
+  }
+  hipEvent_t a, b;
+  if (hipEventCreate(&a) != hipSuccess) return launch();
+  if (hipEventCreate(&b) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    return launch();
+  }
+  (void)hipEventRecord(a, st);
+  const hipError_t e = launch();
+  (void)hipEventRecord(b, st);
+  std::lock_guard<std::mutex> g(t.mu);
+  t.pending[name].push_back({a, b});
+  return e;
+}
+
+void resolve_pending(TimingState& t) {
+  for (auto& kv : t.pending) {
+    auto& acc = t.done[kv.first];
+    for (auto& ev : kv.second) {
+      float ms = 0.f;
+      if (hipEventSynchronize(ev.second) == hipSuccess && hipEventElapsedTime(&ms, ev.first, ev.second) == hipSuccess) {
+        acc.first += ms;
+        acc.second += 1;
+      }
+      (void)hipEventDestroy(ev.first);
+      (void)hipEventDestroy(ev.second);
+    }
+  }
+  t.pending.clear();
+}
+
 }  // namespace
 
 extern "C" {
@@ -87,7 +142,8 @@ int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float
   a.q = q; a.k = k; a.lam = lambda; a.gate_w = gate_w; a.gate_b = gate_b; a.lam_out = lambda_out;
   a.h0 = h0; a.m0 = m0; a.cu = cu_seqlens; a.qc = q_clean; a.qc32 = q_clean_f32; a.h_fin = h_final;
   a.m_fin = m_final; a.T = T; a.H = H; a.N = N; a.pos_off = position_offset; a.subtract_mean = subtract_mean ? 1 : 0;
-  return hip_status(launch_clean_fwd(a, K, (hipStream_t)stream), "ccq_clean_fwd");
+  hipStream_t st = (hipStream_t)stream;
+  return hip_status(timed("clean_fwd", st, [&] { return launch_clean_fwd(a, K, st); }), "ccq_clean_fwd");
 }
 
 size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int H, int K, int gate) {
@@ -146,14 +202,16 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
     a.dq = dq;
     a.dq32 = dq_f32;
   }
-  if (int s = hip_status(launch_clean_bwd(a, K, st), "ccq_clean_bwd")) return s;
+  if (int s = hip_status(timed("clean_bwd", st, [&] { return launch_clean_bwd(a, K, st); }), "ccq_clean_bwd"))
+    return s;
   LamReduceArgs r{};
   r.dlam_part = dlam_part; r.lam = lambda; r.q = q; r.gate_w = gate_w; r.dq32 = dq32_ws;
   r.dlam = gate ? (dlambda ? dlambda : dlam_ws) : dlambda;
   r.dq = gate ? dq : nullptr; r.dq_out32 = gate ? dq_f32 : nullptr;
   r.dw_part = dw_part; r.db_part = db_part; r.ntok = tokens; r.H = H; r.K = K; r.ncb = ncb;
   if (r.dlam || gate) {
-    if (int s = hip_status(launch_lam_reduce(r, st), "ccq_clean_bwd(dlambda)")) return s;
+    if (int s = hip_status(timed("lam_reduce", st, [&] { return launch_lam_reduce(r, st); }), "ccq_clean_bwd(dlambda)"))
+      return s;
   }
   if (gate) {
     if (int s = hip_status(launch_sum_rows(dw_part, dgate_w, nblk, H * K, st), "ccq_clean_bwd(dW)")) return s;
@@ -263,7 +321,14 @@ int ccq_gdn_fwd(const void* q, const float* q_f32, const void* k, const void* v,
   a.gcum = sv.gcum; a.tmat = sv.tmat; a.w = sv.w; a.u = sv.u; a.hT = sv.hT; a.hTl = sv.hTl; a.U = sv.U; a.PT = sv.PT;
   a.o = o; a.s_fin = final_state; a.scale = scale;
   a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NTG = num_chunks;
-  return hip_status(launch_gdn_fwd(a, K, V, (hipStream_t)stream), "ccq_gdn_fwd");
+  hipStream_t st = (hipStream_t)stream;
+  static const char* names[] = {"gdn_prep", "gdn_fwd_state", "gdn_fwd_o"};
+  const int stages[] = {kGdnPrep, kGdnFwdState, kGdnFwdO};
+  for (int i = 0; i < 3; ++i) {
+    if (int s = hip_status(timed(names[i], st, [&] { return launch_gdn_stage(stages[i], a, K, V, st); }), names[i]))
+      return s;
+  }
+  return CCQ_OK;
 }
 
 int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v, const float* g, const float* beta,
@@ -287,7 +352,14 @@ int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v,
   a.dout = d_o; a.ds_fin = d_final_state; a.dU = wk.dU; a.dhT = wk.dhT; a.dhTl = wk.dhTl; a.dq32 = dq_f32; a.dkp32 = wk.dkp32;
   a.dw32 = wk.dw32; a.dgp = wk.dgp; a.dk32 = dk_f32; a.dv = dv; a.dbeta = dbeta; a.dg = dg; a.ds0 = d_initial_state;
   a.scale = scale; a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NTG = num_chunks;
-  return hip_status(launch_gdn_bwd(a, K, V, (hipStream_t)stream), "ccq_gdn_bwd");
+  hipStream_t st = (hipStream_t)stream;
+  static const char* names[] = {"gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy"};
+  const int stages[] = {kGdnBwdState, kGdnBwdDqkw, kGdnBwdWy};
+  for (int i = 0; i < 3; ++i) {
+    if (int s = hip_status(timed(names[i], st, [&] { return launch_gdn_stage(stages[i], a, K, V, st); }), names[i]))
+      return s;
+  }
+  return CCQ_OK;
 }
 
 int ccq_l2norm_fwd(const void* x, void* y, float* rstd, int64_t rows, int D, float eps, void* stream) {
@@ -305,6 +377,36 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
   L2NormArgs a{};
   a.x = x; a.rstd = const_cast<float*>(rstd); a.dy32 = dy_f32; a.dy16 = dy_f32 ? nullptr : dy; a.dx = dx; a.rows = rows; a.D = D;
   return hip_status(launch_l2norm_bwd(a, (hipStream_t)stream), "ccq_l2norm_bwd");
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int ccq_timing_enable(int on) {
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> g(t.mu);
+  t.on = on != 0;
+  return CCQ_OK;
+}
+
+int ccq_timing_reset(void) {
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> g(t.mu);
+  resolve_pending(t);
+  t.done.clear();
+  return CCQ_OK;
+}
+
+int ccq_timing_read(const char* kernel, double* total_ms, int64_t* launches) {
+  if (!kernel || !total_ms || !launches) return fail(CCQ_ERR_NULL, "ccq_timing_read: null pointer");
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> g(t.mu);
+  resolve_pending(t);
+  auto it = t.done.find(kernel);
+  *total_ms = it == t.done.end() ? 0.0 : it->second.first;
+  *launches = it == t.done.end() ? 0 : it->second.second;
+  return CCQ_OK;
 }
 
 }  // extern "C"

@@ -1092,40 +1092,41 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, c
 }
 
 // ===========================================================================
-// launchers
+// launchers (one per kernel so the C ABI can time each launch)
 // ===========================================================================
 template <int K>
-static hipError_t gdn_fwd_k(const GdnArgs& a, int V, hipStream_t st) {
+static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st) {
   if (a.NTG == 0) return hipSuccess;
-  hipLaunchKernelGGL(gdn_prep_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
-  hipLaunchKernelGGL(gdn_fwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
-  hipLaunchKernelGGL(gdn_fwd_o_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
-  return hipGetLastError();
-}
-
-template <int K>
-static hipError_t gdn_bwd_k(const GdnArgs& a, int V, hipStream_t st) {
-  if (a.NTG == 0) return hipSuccess;
-  hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
-  hipLaunchKernelGGL(gdn_bwd_dqkw_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
-  hipLaunchKernelGGL(gdn_bwd_wy_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
-  return hipGetLastError();
-}
-
-hipError_t launch_gdn_fwd(const GdnArgs& a, int K, int V, hipStream_t st) {
-  switch (K) {
-    case 64: return gdn_fwd_k<64>(a, V, st);
-    case 128: return gdn_fwd_k<128>(a, V, st);
-    case 256: return gdn_fwd_k<256>(a, V, st);
-    default: return hipErrorInvalidValue;
+  switch (stage) {
+    case kGdnPrep:
+      hipLaunchKernelGGL(gdn_prep_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      break;
+    case kGdnFwdState:
+      hipLaunchKernelGGL(gdn_fwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+      break;
+    case kGdnFwdO:
+      hipLaunchKernelGGL(gdn_fwd_o_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      break;
+    case kGdnBwdState:
+      hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+      break;
+    case kGdnBwdDqkw:
+      hipLaunchKernelGGL(gdn_bwd_dqkw_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      break;
+    case kGdnBwdWy:
+      hipLaunchKernelGGL(gdn_bwd_wy_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      break;
+    default:
+      return hipErrorInvalidValue;
   }
+  return hipGetLastError();
 }
 
-hipError_t launch_gdn_bwd(const GdnArgs& a, int K, int V, hipStream_t st) {
+hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st) {
   switch (K) {
-    case 64: return gdn_bwd_k<64>(a, V, st);
-    case 128: return gdn_bwd_k<128>(a, V, st);
-    case 256: return gdn_bwd_k<256>(a, V, st);
+    case 64: return gdn_stage_k<64>(stage, a, V, st);
+    case 128: return gdn_stage_k<128>(stage, a, V, st);
+    case 256: return gdn_stage_k<256>(stage, a, V, st);
     default: return hipErrorInvalidValue;
   }
 }

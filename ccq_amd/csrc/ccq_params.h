@@ -94,6 +94,8 @@ namespace ccq {
 //   dU   [tokens, H, V] fp32      gradient of U
 //   dhT  [NTG, H, V, K] bf16      gradient of the state after each chunk (transposed); dhTl low part
 //   dq32 / dkp32 / dw32 [tokens, H, K] fp32, dgp [K/64, tokens, H] fp32
+enum GdnStage { kGdnPrep = 0, kGdnFwdState, kGdnFwdO, kGdnBwdState, kGdnBwdDqkw, kGdnBwdWy };
+
 struct GdnArgs {
   const void* qc16;         // bf16 cleaned query (or qc32)
   const float* qc32;        // fp32 cleaned query

@@ -6,7 +6,8 @@
  * default stream) and returns 0 on success or a negative status
  * (CCQ_ERR_*); ccq_last_error() describes the last failure of the calling
  * host thread.  No entry point allocates device memory or keeps state between
- * calls; buffers a backward pass needs from its forward ("saved") and scratch
+ * calls (apart from the opt-in kernel timing at the end of this header); buffers a
+ * backward pass needs from its forward ("saved") and scratch
  * space ("workspace") are caller-provided, sized by the *_bytes() queries.
  *
  * Layouts follow the reference (token-major, head-interleaved):
@@ -132,6 +133,18 @@ int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v,
 int ccq_l2norm_fwd(const void* x, void* y, float* rstd, int64_t rows, int D, float eps, void* stream);
 int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const void* dy, void* dx, int64_t rows,
                    int D, void* stream);
+
+/*
+ * Kernel timing (measurement facility; no counterpart in the reference).  While enabled, each
+ * entry point records a HIP event pair around every launch of its kernels on the caller's
+ * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: clean_fwd,
+ * clean_bwd, lam_reduce, gdn_prep, gdn_fwd_state, gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw,
+ * gdn_bwd_wy) and returns the summed milliseconds and the number of launches since the last
+ * ccq_timing_reset.
+ */
+int ccq_timing_enable(int on);
+int ccq_timing_reset(void);
+int ccq_timing_read(const char* kernel, double* total_ms, int64_t* launches);
 
 #ifdef __cplusplus
 }
