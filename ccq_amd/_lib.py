@@ -24,8 +24,9 @@ _SZ = ctypes.c_size_t
 SIGNATURES = {
     "ccq_abi_version": (_I, []),
     "ccq_last_error": (ctypes.c_char_p, []),
-    "ccq_clean_fwd": (_I, [_P] * 13 + [_I] * 7 + [_P]),
-    "ccq_clean_bwd_workspace_bytes": (_SZ, [_I64, _I, _I, _I]),
+    "ccq_clean_saved_bytes": (_SZ, [_I64, _I, _I, _I, _I, _I, _I]),
+    "ccq_clean_fwd": (_I, [_P] * 14 + [_I] * 7 + [_P]),
+    "ccq_clean_bwd_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I, _I, _I, _I]),
     "ccq_clean_bwd": (_I, [_P] * 24 + [_I] * 7 + [_P]),
     "ccq_chunk_index": (_I, [_P, _I, _P, _P, _I, _P]),
     "ccq_gdn_saved_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
@@ -78,8 +79,8 @@ def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args), name)
 
 
-KERNELS = ("clean_fwd", "clean_bwd", "lam_reduce", "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state",
-           "gdn_bwd_dqkw", "gdn_bwd_wy")
+KERNELS = ("clean_segsum", "clean_fwd", "clean_bwd_dq", "clean_bwd_scan", "clean_bwd_dh0", "clean_bwd_dk",
+           "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy")
 
 
 def timing_enable(on: bool) -> None:

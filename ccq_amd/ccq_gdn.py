@@ -108,14 +108,15 @@ class ChunkCCQGDNFunction(torch.autograd.Function):
         lam_used = None
         if enable_ccq:
             lam3 = None if gw is not None else reshape_lambda_3d(lambda_h, q)
-            _, qc32, hfin, mfin, lam_used = clean_forward(qn, kn, lam3, gw, gb, h0, m0, cu_seqlens, position_offset,
-                                                          subtract_mean, want_bf16=False, want_f32=True,
-                                                          want_hfin=bool(output_final_state))
+            want = bool(output_final_state)
+            _, qc32, hfin, mfin, lam_used, csaved = clean_forward(qn, kn, lam3, gw, gb, h0, m0, cu_seqlens,
+                                                                  position_offset, subtract_mean, want_bf16=False,
+                                                                  want_f32=True, want_hfin=want, want_mfin=want)
             o, sfin, saved = _gdn_forward(None, qc32, kn, v, g32, beta32, s0, ch, scale, bool(output_final_state))
         else:
-            qc32 = None
+            qc32 = csaved = None
             o, sfin, saved = _gdn_forward(qn, None, kn, v, g32, beta32, s0, ch, scale, bool(output_final_state))
-        ctx.save_for_backward(q, k, qn, kn, v, g32, beta32, qc32, saved, rq, rk, lam_used, h0, m0, mfin, gw, gb,
+        ctx.save_for_backward(q, k, qn, kn, v, g32, beta32, qc32, saved, rq, rk, lam_used, h0, m0, csaved, gw, gb,
                               cu_seqlens, s0)
         ctx.ch = ch
         ctx.scale = scale
@@ -127,16 +128,11 @@ class ChunkCCQGDNFunction(torch.autograd.Function):
         ctx.g_dtype = g.dtype if g is not None else None
         ctx.beta_dtype = beta.dtype
         ctx.has_g = g is not None
-        mret = None
-        if output_final_state and enable_ccq and subtract_mean:
-            mret = mfin.clone()
-        if not output_final_state:
-            hfin = None
-        return o, sfin, hfin, mret
+        return o, sfin, hfin, mfin
 
     @staticmethod
     def backward(ctx, do, dsfin, dhfin, dmfin):
-        (q, k, qn, kn, v, g32, beta32, qc32, saved, rq, rk, lam_used, h0, m0, mfin, gw, gb, cu_seqlens,
+        (q, k, qn, kn, v, g32, beta32, qc32, saved, rq, rk, lam_used, h0, m0, csaved, gw, gb, cu_seqlens,
          s0) = ctx.saved_tensors
         ch = ctx.ch
         dq32g, dk32g, dv, dbeta, dg, ds0 = _gdn_backward(
@@ -146,7 +142,7 @@ class ChunkCCQGDNFunction(torch.autograd.Function):
         if ctx.enable_ccq:
             want_dlam = ctx.lambda_h is not None and ctx.lambda_h.requires_grad
             dqn, dkn, dlam3, dgw, dgb, dh0, dm0 = clean_backward(
-                qn, kn, lam_used, gw, gb, dq32g, dk32g, h0, m0, mfin, cu_seqlens, dhfin, dmfin, ctx.position_offset,
+                qn, kn, lam_used, gw, gb, dq32g, dk32g, h0, m0, cu_seqlens, csaved, dhfin, dmfin, ctx.position_offset,
                 ctx.subtract_mean, want_dlam=want_dlam, dq_f32=ctx.use_l2norm, dk_f32=ctx.use_l2norm)
             dlam = reduce_dlambda(dlam3, ctx.lambda_h) if dlam3 is not None else None
         else:

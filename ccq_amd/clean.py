@@ -95,32 +95,36 @@ def l2norm_bwd(x: torch.Tensor, rstd: torch.Tensor, dy: torch.Tensor) -> torch.T
 
 
 def clean_forward(q, k, lam3, gate_w, gate_b, h0, m0, cu_seqlens, position_offset, subtract_mean, *,
-                  want_bf16=True, want_f32=False, want_hfin=False):
+                  want_bf16=True, want_f32=False, want_hfin=False, want_mfin=False):
     """Launch the cleaning forward.  Returns (q_clean bf16|None, q_clean fp32|None, h_final|None,
-    m_final (always, for the backward), lambda (gate output or lam3))."""
+    m_final|None, lambda used (gate output or lam3), saved buffer for the backward)."""
     B, T, H, K = q.shape
     N = seq_count(B, cu_seqlens)
     dev = q.device
+    varlen = cu_seqlens is not None
+    saved = torch.empty(_lib.load().ccq_clean_saved_bytes(B * T, B, T, N, H, K, int(varlen)), device=dev,
+                        dtype=torch.uint8)
     qc = torch.empty_like(q) if want_bf16 else None
     qc32 = torch.empty(q.shape, device=dev, dtype=torch.float32) if want_f32 else None
     hfin = torch.empty(N, H, K, K, device=dev, dtype=torch.float32) if want_hfin else None
-    mfin = torch.empty(N, H, K, device=dev, dtype=torch.float32) if subtract_mean else None
+    mfin = torch.empty(N, H, K, device=dev, dtype=torch.float32) if (want_mfin and subtract_mean) else None
     lam_out = torch.empty(B, T, H, device=dev, dtype=torch.float32) if gate_w is not None else None
     call("ccq_clean_fwd", ptr(q), ptr(k), ptr(lam3), ptr(gate_w), ptr(gate_b), ptr(lam_out), ptr(h0), ptr(m0),
-         ptr(cu_seqlens), ptr(qc), ptr(qc32), ptr(hfin), ptr(mfin), B, T, H, K, N, int(position_offset),
+         ptr(cu_seqlens), ptr(saved), ptr(qc), ptr(qc32), ptr(hfin), ptr(mfin), B, T, H, K, N, int(position_offset),
          int(bool(subtract_mean)), stream_of(q))
-    return qc, qc32, hfin, mfin, (lam_out if gate_w is not None else lam3)
+    return qc, qc32, hfin, mfin, (lam_out if gate_w is not None else lam3), saved
 
 
-def clean_backward(q, k, lam_used, gate_w, gate_b, dqc, dk_extra, h0, m0, m_end, cu_seqlens, dh_fin, dm_fin,
+def clean_backward(q, k, lam_used, gate_w, gate_b, dqc, dk_extra, h0, m0, cu_seqlens, saved, dh_fin, dm_fin,
                    position_offset, subtract_mean, *, want_dlam=True, dq_f32=False, dk_f32=False):
     """Launch the cleaning backward.  Returns (dq, dk, dlam3|None, dgate_w|None, dgate_b|None, dh0|None, dm0|None)."""
     B, T, H, K = q.shape
     N = seq_count(B, cu_seqlens)
     dev = q.device
     gate = gate_w is not None
-    ws = torch.empty(_lib.load().ccq_clean_bwd_workspace_bytes(B * T, H, K, int(gate)), device=dev,
-                     dtype=torch.uint8)
+    varlen = cu_seqlens is not None
+    ws = torch.empty(_lib.load().ccq_clean_bwd_workspace_bytes(B * T, B, T, N, H, K, int(varlen), int(gate)),
+                     device=dev, dtype=torch.uint8)
     dqc = dqc.contiguous()
     d32 = dqc if dqc.dtype == torch.float32 else None
     d16 = None if d32 is not None else dqc.to(torch.bfloat16)
@@ -132,7 +136,7 @@ def clean_backward(q, k, lam_used, gate_w, gate_b, dqc, dk_extra, h0, m0, m_end,
     dh0 = torch.empty(N, H, K, K, device=dev, dtype=torch.float32) if h0 is not None else None
     dm0 = torch.empty(N, H, K, device=dev, dtype=torch.float32) if (m0 is not None and subtract_mean) else None
     call("ccq_clean_bwd", ptr(q), ptr(k), ptr(lam_used), ptr(gate_w), ptr(gate_b), ptr(d32), ptr(d16),
-         ptr(dk_extra), ptr(h0), ptr(m0), ptr(m_end), ptr(cu_seqlens), ptr(_f32(dh_fin)), ptr(_f32(dm_fin)),
+         ptr(dk_extra), ptr(h0), ptr(m0), ptr(cu_seqlens), ptr(saved), ptr(_f32(dh_fin)), ptr(_f32(dm_fin)),
          None if dq_f32 else ptr(dq), ptr(dq) if dq_f32 else None, None if dk_f32 else ptr(dk),
          ptr(dk) if dk_f32 else None, ptr(dlam), ptr(dgw), ptr(dgb), ptr(dh0), ptr(dm0), ptr(ws), B, T, H, K, N,
          int(position_offset), int(bool(subtract_mean)), stream_of(q))
@@ -155,26 +159,24 @@ class FusedCCQCleanRead(torch.autograd.Function):
         lam3 = None if gw is not None else reshape_lambda_3d(lambda_h, q)
         h0 = _f32(initial_cov_state)
         m0 = _f32(initial_mean_state) if subtract_mean else None
-        qc, _, hfin, mfin, lam_used = clean_forward(q, k, lam3, gw, gb, h0, m0, cu_seqlens, position_offset,
-                                                    subtract_mean, want_hfin=bool(output_final_state))
-        ctx.save_for_backward(q, k, lam_used, h0, m0, mfin, cu_seqlens, gw, gb)
+        want = bool(output_final_state)
+        qc, _, hfin, mfin, lam_used, saved = clean_forward(q, k, lam3, gw, gb, h0, m0, cu_seqlens, position_offset,
+                                                           subtract_mean, want_hfin=want, want_mfin=want)
+        ctx.save_for_backward(q, k, lam_used, h0, m0, saved, cu_seqlens, gw, gb)
         ctx.lambda_h = lambda_h if isinstance(lambda_h, torch.Tensor) else None
         ctx.position_offset = int(position_offset)
         ctx.subtract_mean = bool(subtract_mean)
         ctx.has_h0 = initial_cov_state is not None
         ctx.has_m0 = initial_mean_state is not None and subtract_mean
         ctx.gate = gw is not None
-        mret = mfin if (output_final_state and subtract_mean) else None
-        if mret is not None:
-            mret = mret.clone()
-        return qc, hfin, mret
+        return qc, hfin, mfin
 
     @staticmethod
     def backward(ctx, dqc, dfinal_cov, dfinal_mean):
-        q, k, lam_used, h0, m0, mfin, cu_seqlens, gw, gb = ctx.saved_tensors
+        q, k, lam_used, h0, m0, saved, cu_seqlens, gw, gb = ctx.saved_tensors
         want_dlam = ctx.lambda_h is not None and ctx.lambda_h.requires_grad
         dq, dk, dlam, dgw, dgb, dh0, dm0 = clean_backward(
-            q, k, lam_used, gw, gb, dqc, None, h0, m0, mfin, cu_seqlens, dfinal_cov, dfinal_mean,
+            q, k, lam_used, gw, gb, dqc, None, h0, m0, cu_seqlens, saved, dfinal_cov, dfinal_mean,
             ctx.position_offset, ctx.subtract_mean, want_dlam=want_dlam)
         dl = reduce_dlambda(dlam, ctx.lambda_h) if (dlam is not None) else None
         return dq, dk, dl, None, dh0, dm0, None, None, None, dgw, dgb

@@ -14,14 +14,13 @@
 #include "ccq_params.h"
 
 namespace ccq {
-hipError_t launch_clean_fwd(const CleanFwdArgs& a, int K, hipStream_t st);
-hipError_t launch_clean_bwd(const CleanBwdArgs& a, int K, hipStream_t st);
-hipError_t launch_lam_reduce(const LamReduceArgs& a, hipStream_t st);
+hipError_t launch_clean_stage(int stage, const CleanArgs& a, int K, int nseg, int nblk, hipStream_t st);
 hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, hipStream_t st);
 hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st);
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
-hipError_t launch_chunk_index(const int64_t* cu, int N, int* chunk_off, int* chunk_idx, int cap, hipStream_t st);
+hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
+                              hipStream_t st);
 }  // namespace ccq
 
 using namespace ccq;
@@ -127,95 +126,203 @@ int ccq_abi_version(void) { return 1; }
 
 const char* ccq_last_error(void) { return g_err; }
 
+}  // extern "C"
+
+// ---- cleaning: geometry and buffers ----
+namespace {
+
+constexpr int kCleanBlk = 32, kCleanSeg = 256;
+
+struct CleanGeom {
+  int nb, ns;        // blocks / segments per sequence (dense) or capacities (varlen)
+  int capb, caps;    // launched grid sizes
+};
+
+CleanGeom clean_geom(int64_t tokens, int B, int T, int N, bool varlen) {
+  CleanGeom g;
+  if (varlen) {
+    g.capb = (int)(tokens / kCleanBlk) + N + 1;
+    g.caps = (int)(tokens / kCleanSeg) + N + 1;
+    g.nb = g.capb;
+    g.ns = g.caps;
+  } else {
+    g.nb = (T + kCleanBlk - 1) / kCleanBlk;
+    g.ns = (T + kCleanSeg - 1) / kCleanSeg;
+    g.capb = B * g.nb;
+    g.caps = B * g.ns;
+  }
+  return g;
+}
+
+struct CleanSaved {
+  int* blk_idx;
+  int* blk_off;
+  int* seg_idx;
+  int* seg_off;
+  float* pseg;
+  float* mseg;
+  void* hs_hi;
+  void* hs_lo;
+  float* ms;
+};
+
+size_t carve_clean_saved(char* base, const CleanGeom& g, int N, int H, int K, bool varlen, CleanSaved* out) {
+  Slicer sl{base};
+  CleanSaved t{};
+  if (varlen) {
+    t.blk_idx = sl.take<int>((size_t)g.capb * 2);
+    t.blk_off = sl.take<int>((size_t)N + 1);
+    t.seg_idx = sl.take<int>((size_t)g.caps * 2);
+    t.seg_off = sl.take<int>((size_t)N + 1);
+  }
+  const size_t sk = (size_t)g.caps * H;
+  t.pseg = sl.take<float>(sk * K * K);
+  t.mseg = sl.take<float>(sk * K);
+  t.hs_hi = sl.take<uint16_t>(sk * K * K);
+  t.hs_lo = sl.take<uint16_t>(sk * K * K);
+  t.ms = sl.take<float>(sk * K);
+  if (out) *out = t;
+  return sl.off;
+}
+
+struct CleanWork {
+  float* pseg;
+  void* he_hi;
+  void* he_lo;
+  float* sc;
+  float* dmtot;
+  float* carry;
+  float* dw_part;
+  float* db_part;
+};
+
+size_t carve_clean_work(char* base, const CleanGeom& g, int64_t tokens, int H, int K, bool gate, CleanWork* out) {
+  Slicer sl{base};
+  CleanWork t{};
+  const size_t sk = (size_t)g.caps * H, bk = (size_t)g.capb * H;
+  t.pseg = sl.take<float>(sk * K * K);
+  t.he_hi = sl.take<uint16_t>(sk * K * K);
+  t.he_lo = sl.take<uint16_t>(sk * K * K);
+  t.sc = sl.take<float>((size_t)tokens * H * 2);
+  t.dmtot = sl.take<float>(bk * K);
+  t.carry = sl.take<float>(bk * K);
+  if (gate) {
+    t.dw_part = sl.take<float>(bk * K);
+    t.db_part = sl.take<float>(bk);
+  }
+  if (out) *out = t;
+  return sl.off;
+}
+
+void fill_clean_common(CleanArgs& a, const void* q, const void* k, const float* lambda, const float* gate_w,
+                       const float* gate_b, const float* h0, const float* m0, const int64_t* cu, const CleanSaved& sv,
+                       const CleanGeom& g, int T, int H, int N, int pos_off, int subtract_mean) {
+  a.q = q; a.k = k; a.lam = lambda; a.gate_w = gate_w; a.gate_b = gate_b; a.h0 = h0; a.m0 = m0; a.cu = cu;
+  a.blk_idx = sv.blk_idx; a.blk_off = sv.blk_off; a.seg_idx = sv.seg_idx; a.seg_off = sv.seg_off;
+  a.pseg = sv.pseg; a.mseg = sv.mseg; a.hs_hi = sv.hs_hi; a.hs_lo = sv.hs_lo; a.ms = sv.ms;
+  a.T = T; a.H = H; a.N = N; a.NB = g.nb; a.NS = g.ns; a.pos_off = pos_off; a.subtract_mean = subtract_mean ? 1 : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ccq_clean_saved_bytes(int64_t tokens, int B, int T, int N, int H, int K, int varlen) {
+  const CleanGeom g = clean_geom(tokens, B, T, N, varlen != 0);
+  return carve_clean_saved(nullptr, g, N, H, K, varlen != 0, nullptr);
+}
+
+size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int B, int T, int N, int H, int K, int varlen, int gate) {
+  const CleanGeom g = clean_geom(tokens, B, T, N, varlen != 0);
+  return carve_clean_work(nullptr, g, tokens, H, K, gate != 0, nullptr);
+}
+
 int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
-                  float* lambda_out, const float* h0, const float* m0, const int64_t* cu_seqlens, void* q_clean,
-                  float* q_clean_f32, float* h_final, float* m_final, int B, int T, int H, int K, int N,
-                  int position_offset, int subtract_mean, void* stream) {
+                  float* lambda_out, const float* h0, const float* m0, const int64_t* cu_seqlens, void* saved,
+                  void* q_clean, float* q_clean_f32, float* h_final, float* m_final, int B, int T, int H, int K,
+                  int N, int position_offset, int subtract_mean, void* stream) {
   if (int s = check_common(B, T, H, N, cu_seqlens)) return s;
   if (!clean_k_ok(K)) return fail(CCQ_ERR_SHAPE, "ccq_clean_fwd: K=%d not in {32, 64, 128, 256}", K);
-  if (!q || !k) return fail(CCQ_ERR_NULL, "ccq_clean_fwd: q and k are required");
+  if (!q || !k || !saved) return fail(CCQ_ERR_NULL, "ccq_clean_fwd: q, k and saved are required");
   if (!gate_w && !lambda) return fail(CCQ_ERR_NULL, "ccq_clean_fwd: lambda or gate_w is required");
   if (gate_w && !gate_b) return fail(CCQ_ERR_NULL, "ccq_clean_fwd: gate_w needs gate_b");
   if (!q_clean && !q_clean_f32) return fail(CCQ_ERR_NULL, "ccq_clean_fwd: no output (q_clean / q_clean_f32)");
-  if (!aligned16(q) || !aligned16(k)) return fail(CCQ_ERR_ALIGN, "ccq_clean_fwd: q/k must be 16-byte aligned");
-  CleanFwdArgs a{};
-  a.q = q; a.k = k; a.lam = lambda; a.gate_w = gate_w; a.gate_b = gate_b; a.lam_out = lambda_out;
-  a.h0 = h0; a.m0 = m0; a.cu = cu_seqlens; a.qc = q_clean; a.qc32 = q_clean_f32; a.h_fin = h_final;
-  a.m_fin = m_final; a.T = T; a.H = H; a.N = N; a.pos_off = position_offset; a.subtract_mean = subtract_mean ? 1 : 0;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(saved))
+    return fail(CCQ_ERR_ALIGN, "ccq_clean_fwd: q, k, saved must be 16-byte aligned");
+  const bool varlen = cu_seqlens != nullptr;
+  const int64_t tokens = (int64_t)B * T;
+  const CleanGeom g = clean_geom(tokens, B, T, N, varlen);
+  CleanSaved sv;
+  carve_clean_saved((char*)saved, g, N, H, K, varlen, &sv);
   hipStream_t st = (hipStream_t)stream;
-  return hip_status(timed("clean_fwd", st, [&] { return launch_clean_fwd(a, K, st); }), "ccq_clean_fwd");
-}
-
-size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int H, int K, int gate) {
-  const size_t ncb = (size_t)(K / 32);
-  size_t s = align256(ncb * (size_t)tokens * H * sizeof(float));
-  if (gate) {
-    const size_t nblk = (size_t)((tokens + 63) / 64);
-    s += align256((size_t)tokens * H * K * sizeof(float));    // dq of the cleaning path (fp32)
-    s += align256(nblk * H * K * sizeof(float));               // dW partials
-    s += align256(nblk * H * sizeof(float));                   // db partials
-    s += align256((size_t)tokens * H * sizeof(float));         // dlambda
+  if (varlen) {
+    if (int s = hip_status(launch_chunk_index(cu_seqlens, N, kCleanBlk, sv.blk_off, sv.blk_idx, g.capb, st),
+                           "ccq_clean_fwd(index)"))
+      return s;
+    if (int s = hip_status(launch_chunk_index(cu_seqlens, N, kCleanSeg, sv.seg_off, sv.seg_idx, g.caps, st),
+                           "ccq_clean_fwd(index)"))
+      return s;
   }
-  return s;
+  CleanArgs a{};
+  fill_clean_common(a, q, k, lambda, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, N, position_offset,
+                    subtract_mean);
+  a.lam_out = lambda_out; a.qc = q_clean; a.qc32 = q_clean_f32; a.h_fin = h_final; a.m_fin = m_final;
+  if (int s = hip_status(timed("clean_segsum", st, [&] { return launch_clean_stage(kCleanSegsum, a, K, g.caps, g.capb, st); }),
+                         "ccq_clean_fwd(segsum)"))
+    return s;
+  return hip_status(timed("clean_fwd", st, [&] { return launch_clean_stage(kCleanFwd, a, K, g.caps, g.capb, st); }),
+                    "ccq_clean_fwd");
 }
 
 int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
                   const float* dq_clean_f32, const void* dq_clean, const float* dk_extra, const float* h0,
-                  const float* m0, const float* m_end, const int64_t* cu_seqlens, const float* dh_final,
+                  const float* m0, const int64_t* cu_seqlens, const void* saved, const float* dh_final,
                   const float* dm_final, void* dq, float* dq_f32, void* dk, float* dk_f32, float* dlambda,
                   float* dgate_w, float* dgate_b, float* dh0, float* dm0, void* workspace, int B, int T, int H,
                   int K, int N, int position_offset, int subtract_mean, void* stream) {
   if (int s = check_common(B, T, H, N, cu_seqlens)) return s;
   if (!clean_k_ok(K)) return fail(CCQ_ERR_SHAPE, "ccq_clean_bwd: K=%d not in {32, 64, 128, 256}", K);
-  if (!q || !k || !lambda || !workspace) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: q, k, lambda, workspace are required");
+  if (!q || !k || !lambda || !saved || !workspace)
+    return fail(CCQ_ERR_NULL, "ccq_clean_bwd: q, k, lambda, saved, workspace are required");
   if (!dq_clean_f32 && !dq_clean) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: upstream gradient missing");
-  if (subtract_mean && !m_end) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: m_end is required when subtract_mean");
   if (!dq && !dq_f32) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: no dq output");
   if (!dk && !dk_f32) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: no dk output");
   const bool gate = gate_w != nullptr;
-  if (gate && (!gate_b || !dgate_w || !dgate_b)) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: gate needs gate_b, dgate_w, dgate_b");
-  const long tokens = (long)B * T;  // varlen: B == 1 and T is the packed length
-  const int ncb = K / 32;
-  Slicer sl{(char*)workspace};
-  float* dlam_part = sl.take<float>((size_t)ncb * tokens * H);
-  float* dq32_ws = nullptr;
-  float* dw_part = nullptr;
-  float* db_part = nullptr;
-  float* dlam_ws = nullptr;
-  const int nblk = (int)((tokens + 63) / 64);
-  if (gate) {
-    dq32_ws = sl.take<float>((size_t)tokens * H * K);
-    dw_part = sl.take<float>((size_t)nblk * H * K);
-    db_part = sl.take<float>((size_t)nblk * H);
-    dlam_ws = sl.take<float>((size_t)tokens * H);
-  }
+  if (gate && (!gate_b || !dgate_w || !dgate_b))
+    return fail(CCQ_ERR_NULL, "ccq_clean_bwd: gate needs gate_b, dgate_w, dgate_b");
+  const bool varlen = cu_seqlens != nullptr;
+  const int64_t tokens = (int64_t)B * T;
+  const CleanGeom g = clean_geom(tokens, B, T, N, varlen);
+  CleanSaved sv;
+  carve_clean_saved((char*)saved, g, N, H, K, varlen, &sv);
+  CleanWork wk;
+  carve_clean_work((char*)workspace, g, tokens, H, K, gate, &wk);
   hipStream_t st = (hipStream_t)stream;
-  CleanBwdArgs a{};
-  a.q = q; a.k = k; a.lam = lambda; a.dqc32 = dq_clean_f32; a.dqc16 = dq_clean_f32 ? nullptr : dq_clean;
-  a.dk_extra = dk_extra; a.h0 = h0; a.m0 = m0; a.m_end = m_end; a.cu = cu_seqlens; a.dh_fin = dh_final;
-  a.dm_fin = dm_final; a.dk = dk; a.dk32 = dk_f32; a.dlam_part = dlam_part; a.dh0 = dh0; a.dm0 = dm0;
-  a.ntok = tokens; a.T = T; a.H = H; a.N = N; a.pos_off = position_offset; a.subtract_mean = subtract_mean ? 1 : 0;
-  if (gate) {
-    a.dq = nullptr;
-    a.dq32 = dq32_ws;
-  } else {
-    a.dq = dq;
-    a.dq32 = dq_f32;
+  CleanArgs a{};
+  fill_clean_common(a, q, k, lambda, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, N, position_offset,
+                    subtract_mean);
+  a.pseg = wk.pseg; a.he_hi = wk.he_hi; a.he_lo = wk.he_lo; a.sc = wk.sc; a.dmtot = wk.dmtot; a.carry = wk.carry;
+  a.dw_part = wk.dw_part; a.db_part = wk.db_part;
+  a.dqc32 = dq_clean_f32; a.dqc16 = dq_clean_f32 ? nullptr : dq_clean; a.dk_extra = dk_extra;
+  a.dh_fin = dh_final; a.dm_fin = subtract_mean ? dm_final : nullptr;
+  a.dq = dq; a.dq32 = dq_f32; a.dk = dk; a.dk32 = dk_f32; a.dlam = dlambda; a.dh0 = dh0;
+  a.dm0 = subtract_mean ? dm0 : nullptr;
+  struct StageName { int stage; const char* name; };
+  const StageName stages[] = {{kCleanBwdDq, "clean_bwd_dq"}, {kCleanBwdScan, "clean_bwd_scan"},
+                              {kCleanBwdDh0, "clean_bwd_dh0"}, {kCleanBwdDk, "clean_bwd_dk"}};
+  for (const StageName& sn : stages) {
+    if (sn.stage == kCleanBwdDh0 && !dh0) continue;
+    if (int s = hip_status(timed(sn.name, st, [&] { return launch_clean_stage(sn.stage, a, K, g.caps, g.capb, st); }),
+                           sn.name))
+      return s;
   }
-  if (int s = hip_status(timed("clean_bwd", st, [&] { return launch_clean_bwd(a, K, st); }), "ccq_clean_bwd"))
-    return s;
-  LamReduceArgs r{};
-  r.dlam_part = dlam_part; r.lam = lambda; r.q = q; r.gate_w = gate_w; r.dq32 = dq32_ws;
-  r.dlam = gate ? (dlambda ? dlambda : dlam_ws) : dlambda;
-  r.dq = gate ? dq : nullptr; r.dq_out32 = gate ? dq_f32 : nullptr;
-  r.dw_part = dw_part; r.db_part = db_part; r.ntok = tokens; r.H = H; r.K = K; r.ncb = ncb;
-  if (r.dlam || gate) {
-    if (int s = hip_status(timed("lam_reduce", st, [&] { return launch_lam_reduce(r, st); }), "ccq_clean_bwd(dlambda)"))
+  if (dm0 && !subtract_mean) {
+    if (int s = hip_status(hipMemsetAsync(dm0, 0, (size_t)N * H * K * sizeof(float), st), "ccq_clean_bwd(dm0)"))
       return s;
   }
   if (gate) {
-    if (int s = hip_status(launch_sum_rows(dw_part, dgate_w, nblk, H * K, st), "ccq_clean_bwd(dW)")) return s;
-    if (int s = hip_status(launch_sum_rows(db_part, dgate_b, nblk, H, st), "ccq_clean_bwd(db)")) return s;
+    if (int s = hip_status(launch_sum_rows(wk.dw_part, dgate_w, g.capb, H * K, st), "ccq_clean_bwd(dW)")) return s;
+    if (int s = hip_status(launch_sum_rows(wk.db_part, dgate_b, g.capb, H, st), "ccq_clean_bwd(db)")) return s;
   }
   return CCQ_OK;
 }
@@ -224,7 +331,7 @@ int ccq_chunk_index(const int64_t* cu_seqlens, int N, int* chunk_offsets, int* c
                     void* stream) {
   if (!cu_seqlens || !chunk_offsets || !chunk_index) return fail(CCQ_ERR_NULL, "ccq_chunk_index: null pointer");
   if (N < 0 || capacity < 0) return fail(CCQ_ERR_SHAPE, "ccq_chunk_index: bad sizes");
-  return hip_status(launch_chunk_index(cu_seqlens, N, chunk_offsets, chunk_index, capacity, (hipStream_t)stream),
+  return hip_status(launch_chunk_index(cu_seqlens, N, 64, chunk_offsets, chunk_index, capacity, (hipStream_t)stream),
                     "ccq_chunk_index");
 }
 

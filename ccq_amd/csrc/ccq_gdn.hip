@@ -267,11 +267,12 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, con
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a, const int V) {
-  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDU = BT + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
+  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDU = BT + 1, LDV = VB + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
   __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sKT[K * LDB];
   __shared__ __attribute__((aligned(16))) bf16 sST[VB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sSTl[VB * LDK];
+  __shared__ float sU[BT * LDV];
   __shared__ float sUsT[VB * LDU];
   __shared__ float sFac[BT];
   __shared__ float sGL[1];
@@ -300,16 +301,32 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
     }
   }
 
+  // Everything a step reads except the state itself is loaded one step ahead into registers.
+  PrefetchBf16<K, BT> pw, pk;
+  PrefetchF32<VB, BT> pu;
+  float pg = 0.f, pgl = 0.f;
+  auto issue = [&](int c) {
+    const int c0 = c * BT, L = min(BT, len - c0);
+    const long tok0 = bos + c0;
+    pw.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L);
+    pk.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L);
+    pu.load(a.u + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+    if (tid < BT) {
+      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
+      pg = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
+    }
+  };
+  if (nc > 0) issue(0);
+
   for (int c = 0; c < nc; ++c) {
     const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
     const long tok0 = bos + c0;
-    stage_bf16<K>(sW, LDK, nullptr, 0, (const bf16*)a.w + (tok0 * a.H + h) * K, rsk, BT, L);
-    stage_bf16<K>(nullptr, 0, sKT, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
+    pw.store(sW, LDK, nullptr, 0);
+    pk.store(nullptr, 0, sKT, LDB);
+    pu.store(sU, LDV, nullptr, 0);
     if (tid < BT) {
-      const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
-      const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
-      sFac[tid] = __expf(gl - gt);
-      if (tid == 0) sGL[0] = __expf(gl);
+      sFac[tid] = __expf(pgl - pg);
+      if (tid == 0) sGL[0] = __expf(pgl);
     }
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
@@ -323,8 +340,7 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
       }
     }
     __syncthreads();
-    lds_to_global_bf16<K>((bf16*)a.hT + (((long)gc * a.H + h) * V + v0) * K, K, sST, LDK, VB);
-    lds_to_global_bf16<K>((bf16*)a.hTl + (((long)gc * a.H + h) * V + v0) * K, K, sSTl, LDK, VB);
+    if (c + 1 < nc) issue(c + 1);
     if (w < 2) {
       f32x16 acc = zero16();
       mma_rr(acc, sW + w * 32 * LDK, LDK, sST, LDK, K);
@@ -333,12 +349,21 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
         const int r = w * 32 + acc_row(i), cc = acc_col();
         float us = 0.f;
         if (r < L) {
-          const long gi = (tok0 + r) * rsv + (long)h * V + v0 + cc;
-          const float uu = a.u[gi] - acc[i];
-          a.U[gi] = uu;
+          const float uu = sU[r * LDV + cc] - acc[i];
+          a.U[(tok0 + r) * rsv + (long)h * V + v0 + cc] = uu;
           us = sFac[r] * uu;
         }
         sUsT[cc * LDU + r] = us;
+      }
+    } else {
+      // state snapshot (hi/lo) to HBM for the output kernel and the backward
+      constexpr int VPR = K / 8;
+      for (int idx = tid - 128; idx < 2 * VB * VPR; idx += 128) {
+        const int which = idx / (VB * VPR), e = idx % (VB * VPR);
+        const int r = e / VPR, cc = (e % VPR) * 8;
+        const bf16* src = which ? sSTl : sST;
+        bf16* dst = which ? (bf16*)a.hTl : (bf16*)a.hT;
+        *(bf16x8*)(dst + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
       }
     }
     __syncthreads();

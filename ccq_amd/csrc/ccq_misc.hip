@@ -42,17 +42,17 @@ __global__ __launch_bounds__(kThreads) void l2norm_bwd_kernel(const L2NormArgs a
   }
 }
 
-// chunk_off[n] = first global 64-token chunk of sequence n (exclusive scan of ceil(len/64));
+// chunk_off[n] = first global `size`-token chunk of sequence n (exclusive scan of ceil(len/size));
 // chunk_idx[2c], [2c+1] = (sequence, chunk within sequence) for c < total, -1 beyond it (up to cap).
-__global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int64_t* cu, int N, int* chunk_off, int* chunk_idx,
-                                                               int cap) {
+__global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int64_t* cu, int N, int size, int* chunk_off,
+                                                               int* chunk_idx, int cap) {
   __shared__ int sOff[1];
   if (threadIdx.x == 0) {
     int acc = 0;
     for (int n = 0; n < N; ++n) {
       chunk_off[n] = acc;
       const int len = (int)(cu[n + 1] - cu[n]);
-      acc += (len + 63) / 64;
+      acc += (len + size - 1) / size;
     }
     chunk_off[N] = acc;
     sOff[0] = acc;
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int64_t* cu
   // each thread walks a range of sequences
   for (int n = threadIdx.x; n < N; n += kThreads) {
     const int len = (int)(cu[n + 1] - cu[n]);
-    const int nc = (len + 63) / 64;
+    const int nc = (len + size - 1) / size;
     const int o = chunk_off[n];
     for (int c = 0; c < nc && o + c < cap; ++c) {
       chunk_idx[2 * (o + c)] = n;
@@ -89,8 +89,9 @@ hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_chunk_index(const int64_t* cu, int N, int* chunk_off, int* chunk_idx, int cap, hipStream_t st) {
-  hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, st, cu, N, chunk_off, chunk_idx, cap);
+hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
+                              hipStream_t st) {
+  hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, st, cu, N, size, chunk_off, chunk_idx, cap);
   return hipGetLastError();
 }
 

@@ -11,60 +11,63 @@
 
 namespace ccq {
 
-struct CleanFwdArgs {
+// Cleaning operator, chunk-parallel form.  Tokens are grouped in 32-token blocks and
+// 256-token segments (per sequence).  Buffers (caller-allocated):
+//   pseg [NSEG, H, K, K] fp32   per-segment sum of k k^T (forward) / q dz^T (backward)
+//   mseg [NSEG, H, K]    fp32   per-segment sum of k
+//   hs_hi/hs_lo [NSEG, H, K, K] bf16  state at each segment start, transposed, as a hi/lo pair
+//                                     (forward: h_seg; backward: E = G + G^T after the segment)
+//   ms   [NSEG, H, K]    fp32   key sum at each segment start
+//   sc   [tokens, H, 2]  fp32   (s_t, ds_t) of the backward
+//   dmtot/carry [NBLK, H, K] fp32  per-block sum of dm / sum of dm over later blocks (+ dm_final)
+enum CleanStage { kCleanSegsum = 0, kCleanFwd, kCleanBwdDq, kCleanBwdScan, kCleanBwdDh0, kCleanBwdDk };
+
+struct CleanArgs {
   const void* q;            // bf16 [tokens, H, K]
   const void* k;            // bf16 [tokens, H, K]
-  const float* lam;         // fp32 [tokens, H], unused when gate_w != nullptr
-  const float* gate_w;      // fp32 [H, K]: fused gate lambda = sigmoid(W[h].q + b[h]) (nullable)
+  const float* lam;         // fp32 [tokens, H] (forward: unused when gate_w != nullptr)
+  const float* gate_w;      // fp32 [H, K] (nullable)
   const float* gate_b;      // fp32 [H]
-  float* lam_out;           // fp32 [tokens, H]: gate output (nullable)
+  float* lam_out;           // fp32 [tokens, H] gate output (nullable)
   const float* h0;          // fp32 [N, H, K, K] (nullable)
-  const float* m0;          // fp32 [N, H, K]    (nullable)
-  const int64_t* cu;        // [N+1] (nullable)
-  void* qc;                 // bf16 [tokens, H, K] output (nullable)
-  float* qc32;              // fp32 [tokens, H, K] output (nullable)
-  float* h_fin;             // fp32 [N, H, K, K] output (nullable)
-  float* m_fin;             // fp32 [N, H, K] output (nullable)
-  int T, H, N, pos_off, subtract_mean;
-};
-
-struct CleanBwdArgs {
-  const void* q;            // bf16
-  const void* k;            // bf16
-  const float* lam;         // fp32 [tokens, H]
-  const float* dqc32;       // fp32 upstream gradient (or dqc16)
-  const void* dqc16;        // bf16 upstream gradient
-  const float* dk_extra;    // fp32 [tokens, H, K] added into dk (nullable)
-  const float* h0;          // fp32 [N, H, K, K] (nullable; must be symmetric)
   const float* m0;          // fp32 [N, H, K] (nullable)
-  const float* m_end;       // fp32 [N, H, K]: key sum after the sequence (m0 + sum k); required if subtract_mean
-  const int64_t* cu;
-  const float* dh_fin;      // fp32 [N, H, K, K] gradient into the final covariance state (nullable)
-  const float* dm_fin;      // fp32 [N, H, K] gradient into the final key sum (nullable)
-  void* dq;                 // bf16 [tokens, H, K] (nullable)
-  float* dq32;              // fp32 [tokens, H, K] (nullable)
-  void* dk;                 // bf16 (nullable)
-  float* dk32;              // fp32 (nullable)
-  float* dlam_part;         // fp32 [K/32, tokens, H]
+  const int64_t* cu;        // [N+1] (nullable)
+  const int* blk_idx;       // varlen: [cap, 2] (sequence, block) of 32-token blocks
+  const int* blk_off;       // varlen: [N+1]
+  const int* seg_idx;       // varlen: [cap, 2] (sequence, segment) of 256-token segments
+  const int* seg_off;       // varlen: [N+1]
+  float* pseg;
+  float* mseg;
+  void* hs_hi;
+  void* hs_lo;
+  float* ms;
+  void* he_hi;              // backward: E after each segment (hi/lo) [NSEG, H, K, K] bf16
+  void* he_lo;
+  // forward outputs
+  void* qc;                 // bf16 (nullable)
+  float* qc32;              // fp32 (nullable)
+  float* h_fin;             // fp32 [N, H, K, K] (nullable)
+  float* m_fin;             // fp32 [N, H, K] (nullable)
+  // backward
+  const float* dqc32;       // fp32 upstream gradient (or dqc16)
+  const void* dqc16;
+  const float* dk_extra;    // fp32 [tokens, H, K] (nullable)
+  const float* dh_fin;      // fp32 [N, H, K, K] (nullable)
+  const float* dm_fin;      // fp32 [N, H, K] (nullable)
+  float* sc;
+  float* dmtot;
+  float* carry;
+  void* dq;
+  float* dq32;
+  void* dk;
+  float* dk32;
+  float* dlam;              // fp32 [tokens, H] (nullable)
+  float* dw_part;           // fp32 [NBLK, H, K] gate partials
+  float* db_part;           // fp32 [NBLK, H]
   float* dh0;               // fp32 [N, H, K, K] (nullable)
   float* dm0;               // fp32 [N, H, K] (nullable)
-  long ntok;
-  int T, H, N, pos_off, subtract_mean;
-};
-
-struct LamReduceArgs {
-  const float* dlam_part;   // [ncb, tokens, H]
-  const float* lam;         // [tokens, H] (gate output, for the sigmoid derivative)
-  const void* q;            // bf16 [tokens, H, K] (gate input)
-  const float* gate_w;      // [H, K] (nullable: plain dlambda reduction only)
-  const float* dq32;        // fp32 dq from the cleaning backward (gate mode)
-  float* dlam;              // [tokens, H] output (nullable)
-  void* dq;                 // bf16 dq output (gate mode, nullable)
-  float* dq_out32;          // fp32 dq output (gate mode, nullable)
-  float* dw_part;           // [nblk, H, K] (gate mode)
-  float* db_part;           // [nblk, H] (gate mode)
-  long ntok;
-  int H, K, ncb;
+  int T, H, N, NB, NS;      // NB / NS: blocks / segments per sequence (dense) or capacities (varlen)
+  int pos_off, subtract_mean;
 };
 
 struct L2NormArgs {

@@ -205,6 +205,54 @@ __device__ __forceinline__ void stage_f32(float* dst, int ld, float* dst_t, int 
   }
 }
 
+
+// Stage ROWS x D bf16 rows into a transposed LDS tile dst_t[c * ldt + r] (ldt % 4 == 0).  Each
+// thread reads a 4-row x 8-column patch and writes eight 4-element (8-byte) column pieces; lanes
+// that share a column sit on consecutive rows, so the 8-byte writes hit consecutive banks.
+template <int D, int ROWS>
+__device__ __forceinline__ void stage_bf16_t4(bf16* dst_t, int ldt, const bf16* g, long gstride, int nvalid) {
+  constexpr int RG = ROWS / 4, CG = D / 8;
+  for (int idx = threadIdx.x; idx < RG * CG; idx += kThreads) {
+    const int rg = idx % RG, cg = idx / RG;
+    const int r0 = rg * 4, c0 = cg * 8;
+    bf16x8 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (r0 + j < nvalid) {
+        v[j] = *(const bf16x8*)(g + (long)(r0 + j) * gstride + c0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[j][i] = (bf16)0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+      bf16x4 col;
+      col[0] = v[0][i];
+      col[1] = v[1][i];
+      col[2] = v[2][i];
+      col[3] = v[3][i];
+      *(bf16x4*)(dst_t + (c0 + i) * ldt + r0) = col;
+    }
+  }
+}
+
+// fp32 operand stored row-major, read transposed: element (r, k) at p[k * ld + r] scaled by ks[k]
+// (scale indexed by the contraction index), split into hi/lo.
+__device__ __forceinline__ void frag_cm_f32_ks(const float* p, int ld, const float* ks, bf16x8& hi, bf16x8& lo) {
+  const int l = lane_id();
+  const int kb = (l >> 5) << 3;
+  const float* q = p + kb * ld + (l & 31);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bf16 hh, oo;
+    split2(q[i * ld] * ks[kb + i], hh, oo);
+    hi[i] = hh;
+    lo[i] = oo;
+  }
+}
+
 // Sequence bounds for dense ([B, T]) or varlen (B == 1 + cu_seqlens) inputs.
 __device__ __forceinline__ void seq_bounds(const int64_t* cu, int n, int T, long& bos, int& len) {
   if (cu) {

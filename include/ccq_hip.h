@@ -51,16 +51,16 @@ const char* ccq_last_error(void);
  *   ignored and written to lambda_out if non-NULL) -- the per-head form of the
  *   reference layer's erase_lambda_proj (ccq/gdn/layer.py:174, 292).
  * h0, m0: initial states (nullable); m0 is ignored unless subtract_mean.
+ * saved: ccq_clean_saved_bytes() bytes, written here and read by ccq_clean_bwd
+ *   (segment states; varlen block/segment indexes).  varlen = (cu_seqlens != NULL).
  * Outputs: q_clean bf16 and/or q_clean_f32 (at least one), h_final, m_final (nullable).
  * K in {32, 64, 128, 256}.
  */
+size_t ccq_clean_saved_bytes(int64_t tokens, int B, int T, int N, int H, int K, int varlen);
 int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
-                  float* lambda_out, const float* h0, const float* m0, const int64_t* cu_seqlens, void* q_clean,
-                  float* q_clean_f32, float* h_final, float* m_final, int B, int T, int H, int K, int N,
-                  int position_offset, int subtract_mean, void* stream);
-
-/* Workspace bytes for ccq_clean_bwd (gate != 0: the fused-gate form). */
-size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int H, int K, int gate);
+                  float* lambda_out, const float* h0, const float* m0, const int64_t* cu_seqlens, void* saved,
+                  void* q_clean, float* q_clean_f32, float* h_final, float* m_final, int B, int T, int H, int K,
+                  int N, int position_offset, int subtract_mean, void* stream);
 
 /*
  * Cleaning backward.  Replaces FusedCCQCleanRead.backward -> _fused_read_bwd
@@ -68,18 +68,19 @@ size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int H, int K, int gate);
  * the dlambda tile sum :443, _chunk_carry + _ccq_add_carry_kernel) and
  * _CCQCleanQ.backward (clean.py:720-748).
  *
- * dq_clean: upstream gradient, fp32 (dq_clean_f32) or bf16 (dq_clean).
- * dk_extra: optional fp32 [tokens, H, K] added into dk (another use of k).
- * m_end: key sum after each sequence (m_final of the forward); required if subtract_mean.
- * dh_final / dm_final: gradients into the final states (nullable).
- * Outputs: dq, dk (bf16 and/or fp32 variants, at least one of each),
- *   dlambda fp32 [tokens, H] (per-token form) or, with gate_w/gate_b (and the
- *   forward's lambda_out passed as lambda), dgate_w [H, K] and dgate_b [H] with
- *   the gate's path folded into dq; dh0, dm0 (nullable; h0 must be symmetric).
+ * Inputs as in the forward, plus `saved` from it.  lambda: the lambda the forward used
+ * (the gate's lambda_out in the fused-gate form).  dq_clean: upstream gradient, fp32
+ * (dq_clean_f32) or bf16 (dq_clean).  dk_extra: optional fp32 [tokens, H, K] added into dk
+ * (another use of k).  dh_final / dm_final: gradients into the final states (nullable).
+ * Outputs: dq, dk (bf16 and/or fp32 variants, at least one of each); dlambda fp32
+ *   [tokens, H] (nullable), or with gate_w/gate_b: dgate_w [H, K], dgate_b [H] and the
+ *   gate's path folded into dq; dh0, dm0 (nullable; h0 is treated as symmetric, as the
+ *   reference does).  workspace: ccq_clean_bwd_workspace_bytes() bytes.
  */
+size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int B, int T, int N, int H, int K, int varlen, int gate);
 int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
                   const float* dq_clean_f32, const void* dq_clean, const float* dk_extra, const float* h0,
-                  const float* m0, const float* m_end, const int64_t* cu_seqlens, const float* dh_final,
+                  const float* m0, const int64_t* cu_seqlens, const void* saved, const float* dh_final,
                   const float* dm_final, void* dq, float* dq_f32, void* dk, float* dk_f32, float* dlambda,
                   float* dgate_w, float* dgate_b, float* dh0, float* dm0, void* workspace, int B, int T, int H,
                   int K, int N, int position_offset, int subtract_mean, void* stream);
@@ -137,9 +138,9 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
 /*
  * Kernel timing (measurement facility; no counterpart in the reference).  While enabled, each
  * entry point records a HIP event pair around every launch of its kernels on the caller's
- * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: clean_fwd,
- * clean_bwd, lam_reduce, gdn_prep, gdn_fwd_state, gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw,
- * gdn_bwd_wy) and returns the summed milliseconds and the number of launches since the last
+ * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: clean_segsum,
+ * clean_fwd, clean_bwd_dq, clean_bwd_scan, clean_bwd_dh0, clean_bwd_dk, gdn_prep, gdn_fwd_state,
+ * gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw, gdn_bwd_wy) and returns the summed milliseconds and the number of launches since the last
  * ccq_timing_reset.
  */
 int ccq_timing_enable(int on);

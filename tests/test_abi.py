@@ -36,37 +36,43 @@ def _fake():
     return ctypes.c_void_p(0x1000)  # never dereferenced: argument checks fail first
 
 
+def _clean_fwd(lib, *, lam=True, saved=True, out=True, cu=False, B=1, K=64, N=1):
+    p = _fake()
+    return lib.ccq_clean_fwd(p, p, p if lam else None, None, None, None, None, None, p if cu else None,
+                             p if saved else None, p if out else None, None, None, None, B, 64, 2, K, N, 0, 1, None)
+
+
 def test_clean_fwd_rejects_bad_k():
     lib = _lib.load()
-    p = _fake()
-    st = lib.ccq_clean_fwd(p, p, p, None, None, None, None, None, None, p, None, None, None, 1, 64, 2, 48, 1, 0, 1,
-                           None)
-    assert st == CCQ_ERR_SHAPE
+    assert _clean_fwd(lib, K=48) == CCQ_ERR_SHAPE
     assert b"K=48" in lib.ccq_last_error()
 
 
-def test_clean_fwd_rejects_missing_lambda_and_output():
+def test_clean_fwd_rejects_missing_lambda_saved_and_output():
     lib = _lib.load()
-    p = _fake()
-    assert lib.ccq_clean_fwd(p, p, None, None, None, None, None, None, None, p, None, None, None, 1, 64, 2, 64, 1,
-                             0, 1, None) == CCQ_ERR_NULL
-    assert lib.ccq_clean_fwd(p, p, p, None, None, None, None, None, None, None, None, None, None, 1, 64, 2, 64, 1,
-                             0, 1, None) == CCQ_ERR_NULL
+    assert _clean_fwd(lib, lam=False) == CCQ_ERR_NULL
+    assert _clean_fwd(lib, saved=False) == CCQ_ERR_NULL
+    assert _clean_fwd(lib, out=False) == CCQ_ERR_NULL
 
 
 def test_varlen_requires_batch_one():
     lib = _lib.load()
-    p = _fake()
-    st = lib.ccq_clean_fwd(p, p, p, None, None, None, None, None, p, p, None, None, None, 2, 64, 2, 64, 3, 0, 1, None)
-    assert st == CCQ_ERR_SHAPE
+    assert _clean_fwd(lib, cu=True, B=2, N=3) == CCQ_ERR_SHAPE
 
 
-def test_clean_bwd_requires_m_end_with_mean():
+def test_clean_bwd_requires_saved_gradient_and_outputs():
     lib = _lib.load()
     p = _fake()
-    args = [p, p, p, None, None, p, None, None, None, None, None, None, None, None, p, None, p, None, None, None,
-            None, None, None, p, 1, 64, 2, 64, 1, 0, 1, None]
-    assert lib.ccq_clean_bwd(*args) == CCQ_ERR_NULL
+
+    def call(saved=p, dqc=p, dq=p, dk=p, ws=p):
+        return lib.ccq_clean_bwd(p, p, p, None, None, dqc, None, None, None, None, None, saved, None, None, dq, None,
+                                 dk, None, None, None, None, None, None, ws, 1, 64, 2, 64, 1, 0, 1, None)
+
+    assert call(saved=None) == CCQ_ERR_NULL
+    assert call(ws=None) == CCQ_ERR_NULL
+    assert call(dqc=None) == CCQ_ERR_NULL
+    assert call(dq=None) == CCQ_ERR_NULL
+    assert call(dk=None) == CCQ_ERR_NULL
 
 
 def test_gdn_rejects_bad_shapes():
@@ -102,6 +108,11 @@ def test_workspace_sizes_are_consistent(K, V):
     expect = tokens * H * 4 + nt * H * 4096 * 4 + tokens * H * K * 2 + tokens * H * V * 4 + 2 * nt * H * V * K * 2 \
         + tokens * H * V * 4 + nt * H * 4096 * 4
     assert expect <= saved <= expect + 7 * 256
-    ws = lib.ccq_clean_bwd_workspace_bytes(tokens, H, K, 0)
-    assert ws >= (K // 32) * tokens * H * 4
-    assert lib.ccq_clean_bwd_workspace_bytes(tokens, H, K, 1) > ws
+    # cleaning: one fp32 KxK state (hi/lo bf16 pair) per 256-token segment is the floor of both buffers
+    nseg = tokens // 256
+    csaved = lib.ccq_clean_saved_bytes(tokens, 1, tokens, 1, H, K, 0)
+    assert csaved >= nseg * H * K * K * 4
+    ws = lib.ccq_clean_bwd_workspace_bytes(tokens, 1, tokens, 1, H, K, 0, 0)
+    assert ws >= nseg * H * K * K * 4
+    assert lib.ccq_clean_bwd_workspace_bytes(tokens, 1, tokens, 1, H, K, 0, 1) > ws
+    assert lib.ccq_clean_saved_bytes(tokens, 1, tokens, 3, H, K, 1) > csaved  # varlen adds the indexes

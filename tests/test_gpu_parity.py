@@ -47,6 +47,9 @@ CLEAN_CASES = [
     (2, 70, 1, 32, False, False, 0, False, None),
     (1, 100, 2, 256, True, False, 3, True, None),
     (1, 200, 2, 64, True, True, 0, True, [0, 37, 100, 200]),
+    # several 256-token segments per sequence (segment prefix + cross-segment state)
+    (1, 1000, 2, 128, True, True, 0, True, None),
+    (1, 900, 2, 64, False, True, 2, True, [0, 300, 301, 301, 900]),
 ]
 
 
