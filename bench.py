@@ -65,7 +65,7 @@ def gpu_step(x):
     return torch.autograd.grad(o, [x[n] for n in LEAVES], x["do"])
 
 
-MULTI_KERNEL_STAGES = ("clean_segsum", "clean_bwd_scan", "clean_bwd_dh0")
+MULTI_KERNEL_STAGES = ("clean_segsum", "clean_bwd_scan", "clean_bwd_dh0", "clean_bwd_gate")
 
 
 def kernel_work(k=K, v=V, bt=BT, seg=256, blk=32):

@@ -79,7 +79,7 @@ def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args), name)
 
 
-KERNELS = ("clean_segsum", "clean_fwd", "clean_bwd_dq", "clean_bwd_scan", "clean_bwd_dh0", "clean_bwd_dk",
+KERNELS = ("clean_segsum", "clean_fwd", "clean_bwd_dq", "clean_bwd_scan", "clean_bwd_dh0", "clean_bwd_dk", "clean_bwd_gate",
            "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy")
 
 

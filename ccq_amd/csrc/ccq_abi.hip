@@ -15,7 +15,7 @@
 
 namespace ccq {
 hipError_t launch_clean_stage(int stage, const CleanArgs& a, int K, int nseg, int nblk, hipStream_t st);
-hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, hipStream_t st);
+hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, float* red, hipStream_t st);
 hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st);
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
@@ -194,6 +194,7 @@ struct CleanWork {
   float* carry;
   float* dw_part;
   float* db_part;
+  float* red;  // first-pass row sums of dw_part / db_part
 };
 
 size_t carve_clean_work(char* base, const CleanGeom& g, int64_t tokens, int H, int K, bool gate, CleanWork* out) {
@@ -209,6 +210,7 @@ size_t carve_clean_work(char* base, const CleanGeom& g, int64_t tokens, int H, i
   if (gate) {
     t.dw_part = sl.take<float>(bk * K);
     t.db_part = sl.take<float>(bk);
+    t.red = sl.take<float>((size_t)kSumSlices * H * (K + 1));
   }
   if (out) *out = t;
   return sl.off;
@@ -321,8 +323,13 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
       return s;
   }
   if (gate) {
-    if (int s = hip_status(launch_sum_rows(wk.dw_part, dgate_w, g.capb, H * K, st), "ccq_clean_bwd(dW)")) return s;
-    if (int s = hip_status(launch_sum_rows(wk.db_part, dgate_b, g.capb, H, st), "ccq_clean_bwd(db)")) return s;
+    float* red_b = wk.red + (size_t)kSumSlices * H * K;
+    if (int s = hip_status(timed("clean_bwd_gate", st, [&] {
+                             const hipError_t e = launch_sum_rows(wk.dw_part, dgate_w, g.capb, H * K, wk.red, st);
+                             return e != hipSuccess ? e : launch_sum_rows(wk.db_part, dgate_b, g.capb, H, red_b, st);
+                           }),
+                           "ccq_clean_bwd(dW, db)"))
+      return s;
   }
   return CCQ_OK;
 }

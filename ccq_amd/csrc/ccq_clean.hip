@@ -71,6 +71,18 @@ __device__ __forceinline__ int blk_global(const CleanArgs& a, int n, int c) {
   return a.cu ? a.blk_off[n] + c : n * a.NB + c;
 }
 
+// Workgroups go to the 8 XCDs round-robin by linear id.  The per-block kernels run on a 1-D grid
+// of nblk * H workgroups remapped so that each XCD gets a contiguous range of (head, block) pairs,
+// block fastest: the eight blocks of a segment then share one XCD's L2 copy of its state.
+__device__ __forceinline__ void xcd_blocks(const CleanArgs& a, int& gb, int& h) {
+  const int total = gridDim.x, nblk = total / a.H;
+  const int q = total >> 3, r = total & 7;
+  const int lin = blockIdx.x, xcd = lin & 7, idx = lin >> 3;
+  const int m = (xcd < r) ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+  h = m / nblk;
+  gb = m - h * nblk;
+}
+
 __device__ __forceinline__ float clamp_pos(int t_local, int off) {
   const float p = (float)(t_local + 1 + off);
   return p < 1.f ? 1.f : p;
@@ -324,17 +336,23 @@ __global__ __launch_bounds__(kThreads) void clean_vec_scan_kernel(const CleanArg
   } else {
     const int nb = (len + kBlk - 1) / kBlk;
     float run = a.dm_fin ? a.dm_fin[(long)unit * K + k] : 0.f;
-    for (int b = nb - 1; b >= 0; --b) {
-      const long gi = ((long)blk_global(a, n, b) * a.H + h) * K + k;
-      a.carry[gi] = run;
-      run += a.dmtot[gi];
+    // loads in batches of 8 so they are in flight together (the chain is only the running sum)
+    for (int b = nb - 1; b >= 0; b -= 8) {
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = (b - i >= 0) ? a.dmtot[((long)blk_global(a, n, b - i) * a.H + h) * K + k] : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (b - i >= 0) a.carry[((long)blk_global(a, n, b - i) * a.H + h) * K + k] = run;
+        run += x[i];
+      }
     }
     if (a.dm0) a.dm0[(long)unit * K + k] = run;
   }
 }
 
 // ===========================================================================
-// 3. forward main kernel, grid (NBLK, H)
+// 3. forward main kernel, grid NBLK * H (see xcd_blocks)
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void clean_fwd_main_kernel(const CleanArgs a) {
@@ -355,7 +373,8 @@ __global__ __launch_bounds__(kThreads) void clean_fwd_main_kernel(const CleanArg
   bf16* sKjT = sKj + kBlk * LDK;
 
   const int tid = threadIdx.x, w = wave_id();
-  const int gb = blockIdx.x, h = blockIdx.y;
+  int gb, h;
+  xcd_blocks(a, gb, h);
   int n, c;
   if (!blk_info(a, gb, n, c)) return;
   long bos;
@@ -485,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void clean_fwd_main_kernel(const CleanArg
 }
 
 // ===========================================================================
-// 4. backward dq kernel, grid (NBLK, H).  With dz_t = F_t dqc_t, F_t = -lambda_t / pos_t:
+// 4. backward dq kernel, grid NBLK * H.  With dz_t = F_t dqc_t, F_t = -lambda_t / pos_t:
 //   Z = Q H_s + sum_j (Q K_j^T o M) K_j       (z_t, for dlambda = -dqc . corr)
 //   Y = dZ H_s + sum_j (dZ K_j^T o M) K_j     (= h_t dz_t)
 //   ds_t = -(M_s . dz_t + rowsum(dZ K^T))/pos_t  (= lambda_t (cum_t . dqc_t)/pos_t^2)
@@ -514,7 +533,8 @@ __global__ __launch_bounds__(kThreads) void clean_bwd_dq_kernel(const CleanArgs 
   bf16* sKjT = sKj + kBlk * LDK;
 
   const int tid = threadIdx.x, w = wave_id();
-  const int gb = blockIdx.x, h = blockIdx.y;
+  int gb, h;
+  xcd_blocks(a, gb, h);
   const bool gate = a.gate_w != nullptr;
   int n, c;
   if (!blk_info(a, gb, n, c)) {
@@ -745,7 +765,7 @@ __global__ __launch_bounds__(kThreads) void clean_bwd_dq_kernel(const CleanArgs 
 }
 
 // ===========================================================================
-// 5. backward dk kernel, grid (NBLK, H).  For the key block j of this workgroup:
+// 5. backward dk kernel, grid NBLK * H.  For the key block j of this workgroup:
 //   dk_j = sum_{query blocks t >= j in the segment} [ (K_j dZ_t^T o M) Q_t + (K_j Q_t^T o M) dZ_t ]
 //          + K_j E_s + U1 dm_j + carry_j (+ dk_extra)
 //   (M keeps t >= j; U1 is the 0/1 upper-triangular matrix: the in-block suffix sum of dm).
@@ -767,7 +787,8 @@ __global__ __launch_bounds__(kThreads) void clean_bwd_dk_kernel(const CleanArgs 
   float* sGt = (float*)(sQt + kBlk * LDK);
 
   const int tid = threadIdx.x, w = wave_id();
-  const int gb = blockIdx.x, h = blockIdx.y;
+  int gb, h;
+  xcd_blocks(a, gb, h);
   int n, c;
   if (!blk_info(a, gb, n, c)) return;
   long bos;
@@ -909,17 +930,20 @@ __global__ __launch_bounds__(kThreads) void clean_bwd_dk_kernel(const CleanArgs 
   }
 }
 
-// Sum of partial rows: out[j] = sum_b part[b * cols + j].  grid ceil(cols / 64); 4 groups of 64 threads.
-__global__ __launch_bounds__(kThreads) void ccq_sum_rows_kernel(const float* part, float* out, int nblk, int cols) {
+// Sum of partial rows over a slice: out[y * cols + j] = sum_{b in slice y} part[b * cols + j],
+// slice y = rows [y * rps, min(nblk, (y + 1) * rps)).  grid (ceil(cols / 64), slices); 4 groups of 64 threads.
+__global__ __launch_bounds__(kThreads) void ccq_sum_rows_kernel(const float* part, float* out, int nblk, int cols,
+                                                                int rps) {
   __shared__ float sP[4][64];
   const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int j = blockIdx.x * 64 + cl;
+  const int b0 = blockIdx.y * rps, b1 = min(nblk, b0 + rps);
   float s = 0.f;
   if (j < cols)
-    for (int b = grp; b < nblk; b += 4) s += part[(long)b * cols + j];
+    for (int b = b0 + grp; b < b1; b += 4) s += part[(long)b * cols + j];
   sP[grp][cl] = s;
   __syncthreads();
-  if (grp == 0 && j < cols) out[j] = sP[0][cl] + sP[1][cl] + sP[2][cl] + sP[3][cl];
+  if (grp == 0 && j < cols) out[(long)blockIdx.y * cols + j] = sP[0][cl] + sP[1][cl] + sP[2][cl] + sP[3][cl];
 }
 
 // ===========================================================================
@@ -938,10 +962,10 @@ hipError_t clean_stage_k(int stage, const CleanArgs& a, int nseg, int nblk, hipS
       hipLaunchKernelGGL(clean_vec_scan_kernel<0>, dim3(a.N * a.H), dim3(kThreads), 0, st, a, K);
       break;
     case kCleanFwd:
-      hipLaunchKernelGGL(clean_fwd_main_kernel<K>, dim3(nblk, a.H), dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL(clean_fwd_main_kernel<K>, dim3(nblk * a.H), dim3(kThreads), 0, st, a);
       break;
     case kCleanBwdDq:
-      hipLaunchKernelGGL(clean_bwd_dq_kernel<K>, dim3(nblk, a.H), dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL(clean_bwd_dq_kernel<K>, dim3(nblk * a.H), dim3(kThreads), 0, st, a);
       break;
     case kCleanBwdScan:
       hipLaunchKernelGGL((clean_segsum_kernel<K, 1>), dim3(nseg, a.H, K / KC), dim3(kThreads), 0, st, a);
@@ -953,7 +977,7 @@ hipError_t clean_stage_k(int stage, const CleanArgs& a, int nseg, int nblk, hipS
       hipLaunchKernelGGL(clean_mat_scan_kernel<2>, scan_grid, dim3(kThreads), 0, st, a, K);
       break;
     case kCleanBwdDk:
-      hipLaunchKernelGGL(clean_bwd_dk_kernel<K>, dim3(nblk, a.H), dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL(clean_bwd_dk_kernel<K>, dim3(nblk * a.H), dim3(kThreads), 0, st, a);
       break;
     default:
       return hipErrorInvalidValue;
@@ -974,9 +998,18 @@ hipError_t launch_clean_stage(int stage, const CleanArgs& a, int K, int nseg, in
   }
 }
 
-hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, hipStream_t st) {
+// out[j] = sum_b part[b * cols + j]: kSumSlices partial sums into red[kSumSlices * cols], then one pass.
+hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, float* red, hipStream_t st) {
   if (cols == 0) return hipSuccess;
-  hipLaunchKernelGGL(ccq_sum_rows_kernel, dim3((cols + 63) / 64), dim3(kThreads), 0, st, part, out, nblk, cols);
+  const dim3 gx((cols + 63) / 64);
+  if (nblk <= 4 * kSumSlices || !red) {
+    hipLaunchKernelGGL(ccq_sum_rows_kernel, gx, dim3(kThreads), 0, st, part, out, nblk, cols, nblk);
+    return hipGetLastError();
+  }
+  const int rps = (nblk + kSumSlices - 1) / kSumSlices;
+  const int slices = (nblk + rps - 1) / rps;
+  hipLaunchKernelGGL(ccq_sum_rows_kernel, dim3(gx.x, slices), dim3(kThreads), 0, st, part, red, nblk, cols, rps);
+  hipLaunchKernelGGL(ccq_sum_rows_kernel, gx, dim3(kThreads), 0, st, (const float*)red, out, slices, cols, slices);
   return hipGetLastError();
 }
 

@@ -547,18 +547,47 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     }
   }
 
+  // Everything a step reads except dS itself is loaded one step ahead into registers
+  // (for K = 256 the query / w halves are staged inside the step instead).
+  constexpr bool kPreQW = (NKH == 1);
+  PrefetchF32<BT, BT> pP;
+  PrefetchBf16<VB, BT> pO;
+  PrefetchBf16<K, BT> pK;
+  PrefetchGrad<kPreQW ? KH : 8, BT> pQ;
+  PrefetchBf16<kPreQW ? KH : 8, BT> pW;
+  float pgl = 0.f, pgt = 0.f;
+  auto issue = [&](int c) {
+    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
+    const long tok0 = bos + c0;
+    pP.load(a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT);
+    pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+    pK.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L);
+    if (kPreQW) {
+      pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K : nullptr,
+              a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K : nullptr, rsk, L);
+      pW.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L);
+    }
+    if (tid < BT) {
+      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
+      pgt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
+    }
+  };
+  if (nc > 0) issue(nc - 1);
+
   for (int c = nc - 1; c >= 0; --c) {
     const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
     const long tok0 = bos + c0;
-    stage_f32<64>(sPT, LDP, nullptr, 0, a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT, BT);
-    stage_bf16<32>(nullptr, 0, sdOT, LDB, (const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
-    stage_bf16<K>(sK, LDK, nullptr, 0, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
+    pP.store(sPT, LDP, nullptr, 0);
+    pO.store(nullptr, 0, sdOT, LDB);
+    pK.store(sK, LDK, nullptr, 0);
+    if (kPreQW) {
+      pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
+      pW.store(nullptr, 0, swT, LDB);
+    }
     if (tid < BT) {
-      const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
-      const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
-      sFac[tid] = __expf(gl - gt);
-      sGam[tid] = (tid < L) ? __expf(gt) : 0.f;
-      if (tid == 0) sGL[0] = __expf(gl);
+      sFac[tid] = __expf(pgl - pgt);
+      sGam[tid] = (tid < L) ? __expf(pgt) : 0.f;
+      if (tid == 0) sGL[0] = __expf(pgl);
     }
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
@@ -572,6 +601,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
       }
     }
     __syncthreads();
+    if (c > 0) issue(c - 1);
     lds_to_global_bf16<K>((bf16*)a.dhT + (((long)gc * a.H + h) * V + v0) * K, K, sdST, LDK, VB);
     lds_to_global_bf16<K>((bf16*)a.dhTl + (((long)gc * a.H + h) * V + v0) * K, K, sdSTl, LDK, VB);
     if (w < 2) {
@@ -604,10 +634,12 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     __syncthreads();
     const float gL = sGL[0];
     for (int hb = 0; hb < NKH; ++hb) {
-      stage_any_f32<KH>(nullptr, 0, sQcT, LDP, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + hb * KH : nullptr,
-                        a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + hb * KH : nullptr, rsk, BT, L);
-      stage_bf16<KH>(nullptr, 0, swT, LDB, (const bf16*)a.w + (tok0 * a.H + h) * K + hb * KH, rsk, BT, L);
-      __syncthreads();
+      if (!kPreQW) {
+        stage_any_f32<KH>(nullptr, 0, sQcT, LDP, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + hb * KH : nullptr,
+                          a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + hb * KH : nullptr, rsk, BT, L);
+        stage_bf16<KH>(nullptr, 0, swT, LDB, (const bf16*)a.w + (tok0 * a.H + h) * K + hb * KH, rsk, BT, L);
+        __syncthreads();
+      }
 #pragma unroll
       for (int j = 0; j < TPW; ++j) {
         const int rt = w + 4 * j;
@@ -698,18 +730,47 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_kernel(const GdnArgs a,
   f32x16 dQi = zero16(), dKs = zero16(), dW = zero16(), dP = zero16();
   float hds = 0.f;
 
+  // Tiles of the next value block (or, in the last iteration, of the post phase) are loaded into
+  // registers while the current block is in the MFMA pipe.
+  PrefetchBf16<64, 64> pH, pHl, pD, pDl, pO;
+  PrefetchF32<64, BT> pU, pdU;
+  PrefetchGrad<64, BT> pQ;
+  PrefetchBf16<64, BT> pK;
+  PrefetchF32<BT, BT> pP;
+  float pgl = 0.f, pgt = 0.f;
+  auto issue_loop = [&](int v0) {
+    const long so = (((long)gc * a.H + h) * V + v0) * K + k0c;
+    pH.load((const bf16*)a.hT + so, K, 64);
+    pD.load((const bf16*)a.dhT + so, K, 64);
+    pHl.load((const bf16*)a.hTl + so, K, 64);
+    pDl.load((const bf16*)a.dhTl + so, K, 64);
+    pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+    pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+    pdU.load(a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+  };
+  auto issue_post = [&]() {
+    pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + k0c : nullptr,
+            a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + k0c : nullptr, rsk, L);
+    pK.load((const bf16*)a.k + (tok0 * a.H + h) * K + k0c, rsk, L);
+    if (kt == 0) pP.load(a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT);
+    if (tid < BT) {
+      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
+      pgt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
+    }
+  };
+  issue_loop(0);
+
   for (int v0 = 0; v0 < V; v0 += 64) {
-    stage_bf16<64>(sHt, LDB, nullptr, 0, (const bf16*)a.hT + (((long)gc * a.H + h) * V + v0) * K + k0c, K, 64, 64);
-    stage_bf16<64>(sDSt, LDB, nullptr, 0, (const bf16*)a.dhT + (((long)gc * a.H + h) * V + v0) * K + k0c, K, 64,
-                   64);
-    stage_bf16<64>(sHtl, LDB, nullptr, 0, (const bf16*)a.hTl + (((long)gc * a.H + h) * V + v0) * K + k0c, K, 64,
-                   64);
-    stage_bf16<64>(sDStl, LDB, nullptr, 0, (const bf16*)a.dhTl + (((long)gc * a.H + h) * V + v0) * K + k0c, K,
-                   64, 64);
-    stage_bf16<64>(sdO, LDB, nullptr, 0, (const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
-    stage_f32<64>(sU, LDF, nullptr, 0, a.U + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
-    stage_f32<64>(sdU, LDF, nullptr, 0, a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    pH.store(sHt, LDB, nullptr, 0);
+    pD.store(sDSt, LDB, nullptr, 0);
+    pHl.store(sHtl, LDB, nullptr, 0);
+    pDl.store(sDStl, LDB, nullptr, 0);
+    pO.store(sdO, LDB, nullptr, 0);
+    pU.store(sU, LDF, nullptr, 0);
+    pdU.store(sdU, LDF, nullptr, 0);
     __syncthreads();
+    if (v0 + 64 < V) issue_loop(v0 + 64);
+    else issue_post();
     for (int e = tid; e < 64 * 64; e += kThreads) {
       const int vv = e >> 6, kk = e & 63;
       hds += ((float)sHt[vv * LDB + kk] + (float)sHtl[vv * LDB + kk]) *
@@ -746,18 +807,15 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_kernel(const GdnArgs a,
   hds = group_sum(hds, 64);
   if (l == 0) sMisc[w] = hds;
 
-  // post phase
-  stage_any_f32<64>(nullptr, 0, sQcT, LDP, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + k0c : nullptr,
-                    a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + k0c : nullptr, rsk, BT, L);
-  stage_bf16<64>(sKr, LDB, sKt, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K + k0c, rsk, BT, L);
-  if (kt == 0) stage_f32<64>(sPt, LDP, nullptr, 0, a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT, BT);
+  // post phase (its tiles were loaded during the last value block)
+  pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
+  pK.store(sKr, LDB, sKt, LDB);
+  if (kt == 0) pP.store(sPt, LDP, nullptr, 0);
   if (tid < BT) {
-    const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
-    const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
-    sG[tid] = gt;
-    sGam[tid] = __expf(gt);
-    sFac[tid] = __expf(gl - gt);
-    if (tid == 0) sMisc[4] = __expf(gl);
+    sG[tid] = pgt;
+    sGam[tid] = __expf(pgt);
+    sFac[tid] = __expf(pgl - pgt);
+    if (tid == 0) sMisc[4] = __expf(pgl);
   }
   // dP -> LDS (masked, zero upper tile)
   if (w < 3) {
@@ -901,27 +959,53 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, c
   const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
   const int nkt = K / 64;
 
-  stage_f32<64>(sT, LDP, nullptr, 0, a.tmat + ((long)gc * a.H + h) * (BT * BT), BT, BT, BT);
-  if (tid < BT) {
-    const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
-    const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
-    sG[tid] = gt;
-    sGam[tid] = __expf(gt);
-    sBeta[tid] = (tid < L) ? a.beta[(tok0 + tid) * a.H + h] : 0.f;
-    float dg = 0.f;
-    if (tid < L)
-      for (int kt = 0; kt < nkt; ++kt) dg += a.dgp[(long)kt * ntok * a.H + (tok0 + tid) * a.H + h];
-    sDG[tid] = dg;
-    sDB[tid] = 0.f;
+  // Global tiles come in "jobs" of one fp32 and one bf16 64 x 64 tile, loaded one job ahead into
+  // registers: kinds A (dw, k) per key tile and B (dU, v) per value tile feed dT; kinds C (dw, k,
+  // dk_part) and D (dU, v) feed the dk / dv epilogues.  The M1 / dA phase between B and C runs
+  // while the first C job is in flight.
+  const int nv = V / 64, nA = nkt, nB = nkt + nv, nC = 2 * nkt + nv, njobs = 2 * (nkt + nv);
+  PrefetchF32<64, BT> pX, pY;
+  PrefetchBf16<64, BT> pR;
+  auto issue = [&](int j) {
+    const bool kside = j < nA || (j >= nB && j < nC);
+    const int col = 64 * (j < nA ? j : j < nB ? j - nA : j < nC ? j - nB : j - nC);
+    if (kside) {
+      pX.load(a.dw32 + (tok0 * a.H + h) * K + col, rsk, L);
+      pR.load((const bf16*)a.k + (tok0 * a.H + h) * K + col, rsk, L);
+      if (j >= nB) pY.load(a.dkp32 + (tok0 * a.H + h) * K + col, rsk, L);
+    } else {
+      pX.load(a.dU + (tok0 * a.H + h) * (long)V + col, rsv, L);
+      pR.load((const bf16*)a.v + (tok0 * a.H + h) * (long)V + col, rsv, L);
+    }
+  };
+  issue(0);
+  {
+    PrefetchF32<64, BT> pT;
+    pT.load(a.tmat + ((long)gc * a.H + h) * (BT * BT), BT, BT);
+    if (tid < BT) {
+      const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
+      const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
+      sG[tid] = gt;
+      sGam[tid] = __expf(gt);
+      sBeta[tid] = (tid < L) ? a.beta[(tok0 + tid) * a.H + h] : 0.f;
+      float dg = 0.f;
+      if (tid < L)
+        for (int kt = 0; kt < nkt; ++kt) dg += a.dgp[(long)kt * ntok * a.H + (tok0 + tid) * a.H + h];
+      sDG[tid] = dg;
+      sDB[tid] = 0.f;
+    }
+    pT.store(sT, LDP, nullptr, 0);
   }
+  int job = 0;
 
   // --- dT (lower incl. diagonal tiles) and K K^T -------------------------------------
   const int lr = (w == 0) ? 0 : 32, lc = (w == 2) ? 32 : 0;
   f32x16 dTk = zero16(), dTv = zero16(), kk = zero16();
-  for (int kt = 0; kt < nkt; ++kt) {
-    stage_f32<64>(sX, LDF, nullptr, 0, a.dw32 + (tok0 * a.H + h) * K + kt * 64, rsk, BT, L);
-    stage_bf16<64>(sR, LDB, nullptr, 0, (const bf16*)a.k + (tok0 * a.H + h) * K + kt * 64, rsk, BT, L);
+  for (int kt = 0; kt < nkt; ++kt, ++job) {
+    pX.store(sX, LDF, nullptr, 0);
+    pR.store(sR, LDB, nullptr, 0);
     __syncthreads();
+    if (job + 1 < njobs) issue(job + 1);
     if (w < 3) {
       for (int k0 = 0; k0 < 64; k0 += 16) {
         bf16x8 hi, lo;
@@ -934,10 +1018,11 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, c
     }
     __syncthreads();
   }
-  for (int v0 = 0; v0 < V; v0 += 64) {
-    stage_f32<64>(sX, LDF, nullptr, 0, a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
-    stage_bf16<64>(sR, LDB, nullptr, 0, (const bf16*)a.v + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+  for (int v0 = 0; v0 < V; v0 += 64, ++job) {
+    pX.store(sX, LDF, nullptr, 0);
+    pR.store(sR, LDB, nullptr, 0);
     __syncthreads();
+    if (job + 1 < njobs) issue(job + 1);
     if (w < 3) {
       for (int k0 = 0; k0 < 64; k0 += 16) {
         bf16x8 hi, lo;
@@ -1006,18 +1091,20 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, c
   }
   __syncthreads();
   // dbeta_i += sum_j dA_ij Gamma_ij KK_ij ; dG_i += sum_j dA_ij A_ij ; dG_j -= sum_i dA_ij A_ij
-  if (tid < BT) {
-    const int r = tid;
-    float db = 0.f, dgr = 0.f, dgc = 0.f;
-    for (int j = 0; j < r; ++j) {
-      const float gkk = __expf(sG[r] - sG[j]) * sKK[r * LDP + j];
-      const float da = sdT[r * LDP + j];
-      db += da * gkk;
-      dgr += da * sBeta[r] * gkk;
+  // (four threads per row, each over a quarter of the columns)
+  {
+    const int r = tid >> 2, part = tid & 3;
+    float db = 0.f, dgc = 0.f;
+    for (int j = part; j < BT; j += 4) {
+      if (j < r) db += sdT[r * LDP + j] * __expf(sG[r] - sG[j]) * sKK[r * LDP + j];
+      if (j > r) dgc += sdT[j * LDP + r] * sBeta[j] * __expf(sG[j] - sG[r]) * sKK[j * LDP + r];
     }
-    for (int i = r + 1; i < BT; ++i) dgc += sdT[i * LDP + r] * sBeta[i] * __expf(sG[i] - sG[r]) * sKK[i * LDP + r];
-    sTmp[r] = dgr - dgc;
-    sDB[r] += db;
+    db = group_sum(db, 4);
+    dgc = group_sum(dgc, 4);
+    if (part == 0) {
+      sTmp[r] = sBeta[r] * db - dgc;
+      sDB[r] += db;
+    }
   }
   __syncthreads();
   if (tid < BT) sDG[tid] += sTmp[tid];
@@ -1030,11 +1117,13 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, c
 
   // --- dk tiles: dk_part + dAs K + dAs^T K + diag(beta gamma) T^T dw -------------------------
   const int tr = (w >> 1) * 32, tc = (w & 1) * 32;
-  for (int kt = 0; kt < nkt; ++kt) {
+  for (int kt = 0; kt < nkt; ++kt, ++job) {
     const int kc = kt * 64;
-    stage_bf16<64>(sR, LDB, sCT, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K + kc, rsk, BT, L);
-    stage_f32<64>(nullptr, 0, sXT, LDP, a.dw32 + (tok0 * a.H + h) * K + kc, rsk, BT, L);
+    pR.store(sR, LDB, sCT, LDB);
+    pX.store(nullptr, 0, sXT, LDP);
+    pY.store(sY, LDF, nullptr, 0);
     __syncthreads();
+    if (job + 1 < njobs) issue(job + 1);
     f32x16 acc = zero16(), acc2 = zero16();
     for (int k0 = 0; k0 < BT; k0 += 16) {
       const bf16x8 kb = frag_rm(sCT + tc * LDB + k0, LDB);
@@ -1059,7 +1148,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, c
       sRed[r * LDP + c] = acc2[i] * kv;
       if (r < L) {
         const long gi = (tok0 + r) * rsk + (long)h * K + kc + c;
-        a.dk32[gi] = a.dkp32[gi] + acc[i] + sBeta[r] * sGam[r] * acc2[i];
+        a.dk32[gi] = sY[r * LDF + c] + acc[i] + sBeta[r] * sGam[r] * acc2[i];
       }
     }
     __syncthreads();
@@ -1072,10 +1161,11 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, c
     __syncthreads();
   }
   // --- dv tiles: beta_j (T^T dU)_j ; dbeta_j += (T^T dU)_j . v_j ------------------------------
-  for (int v0 = 0; v0 < V; v0 += 64) {
-    stage_bf16<64>(sR, LDB, nullptr, 0, (const bf16*)a.v + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
-    stage_f32<64>(nullptr, 0, sXT, LDP, a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+  for (int v0 = 0; v0 < V; v0 += 64, ++job) {
+    pR.store(sR, LDB, nullptr, 0);
+    pX.store(nullptr, 0, sXT, LDP);
     __syncthreads();
+    if (job + 1 < njobs) issue(job + 1);
     f32x16 acc = zero16();
     for (int k0 = 0; k0 < BT; k0 += 16) {
       bf16x8 thi, tlo, dhi, dlo;

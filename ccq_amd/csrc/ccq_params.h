@@ -22,6 +22,9 @@ namespace ccq {
 //   dmtot/carry [NBLK, H, K] fp32  per-block sum of dm / sum of dm over later blocks (+ dm_final)
 enum CleanStage { kCleanSegsum = 0, kCleanFwd, kCleanBwdDq, kCleanBwdScan, kCleanBwdDh0, kCleanBwdDk };
 
+// slices of the first pass of the gate-gradient row sums
+constexpr int kSumSlices = 32;
+
 struct CleanArgs {
   const void* q;            // bf16 [tokens, H, K]
   const void* k;            // bf16 [tokens, H, K]

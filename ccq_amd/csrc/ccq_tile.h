@@ -359,9 +359,10 @@ struct PrefetchGrad {
     if (g32) f.load(g32, gstride, nvalid);
     else b.load(g16, gstride, nvalid);
   }
-  __device__ __forceinline__ void store(bool is32, float* dst, int ld) const {
+  // row-major (dst[r * ld + c]) and/or transposed (dst_t[c * ldt + r]) fp32 copies
+  __device__ __forceinline__ void store(bool is32, float* dst, int ld, float* dst_t = nullptr, int ldt = 0) const {
     if (is32) {
-      f.store(dst, ld, nullptr, 0);
+      f.store(dst, ld, dst_t, ldt);
     } else {
 #pragma unroll
       for (int j = 0; j < PrefetchBf16<D, ROWS>::N; ++j) {
@@ -369,7 +370,10 @@ struct PrefetchGrad {
         if (idx >= ROWS * (D / 8)) continue;
         const int r = idx / (D / 8), c = (idx % (D / 8)) * 8;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dst[r * ld + c + i] = (float)b.v[j][i];
+        for (int i = 0; i < 8; ++i) {
+          if (dst) dst[r * ld + c + i] = (float)b.v[j][i];
+          if (dst_t) dst_t[(c + i) * ldt + r] = (float)b.v[j][i];
+        }
       }
     }
   }
