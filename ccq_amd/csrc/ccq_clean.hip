@@ -136,18 +136,36 @@ struct Pre4 {
   }
 };
 
-// Stage rows [r0, r0 + nr) of a K x K bf16 hi/lo state pair into LDS (leading dim K + 8).
-template <int K>
-__device__ __forceinline__ void stage_state(bf16* hi, bf16* lo, const bf16* ghi, const bf16* glo, int r0, int nr) {
-  constexpr int VPR = K / 8, LD = K + 8;
-  for (int idx = threadIdx.x; idx < 2 * nr * VPR; idx += kThreads) {
-    const int which = idx / (nr * VPR), e = idx % (nr * VPR);
-    const int r = e / VPR, cc = (e % VPR) * 8;
-    const bf16* src = which ? glo : ghi;
-    bf16* dst = which ? lo : hi;
-    *(bf16x8*)(dst + r * LD + cc) = *(const bf16x8*)(src + (long)(r0 + r) * K + cc);
+// Register prefetch of rows [r0, r0 + SR) of a K x K bf16 hi/lo state pair; stored into LDS
+// with leading dim K + 8.
+template <int K, int SR>
+struct PreState {
+  static constexpr int VPR = K / 8, NV = 2 * SR * VPR, N = (NV + kThreads - 1) / kThreads;
+  bf16x8 v[N];
+  __device__ __forceinline__ void load(const bf16* ghi, const bf16* glo, int r0) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      if (idx < NV) {
+        const int which = idx / (SR * VPR), e = idx % (SR * VPR);
+        const int r = e / VPR, cc = (e % VPR) * 8;
+        v[j] = *(const bf16x8*)((which ? glo : ghi) + (long)(r0 + r) * K + cc);
+      }
+    }
   }
-}
+  __device__ __forceinline__ void store(bf16* hi, bf16* lo) const {
+    constexpr int LD = K + 8;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      if (idx < NV) {
+        const int which = idx / (SR * VPR), e = idx % (SR * VPR);
+        const int r = e / VPR, cc = (e % VPR) * 8;
+        *(bf16x8*)((which ? lo : hi) + r * LD + cc) = v[j];
+      }
+    }
+  }
+};
 
 // fp32 (dqc32) or bf16 (dqc16) gradient rows into fp32 LDS rows.
 template <int K>
@@ -388,6 +406,10 @@ __global__ __launch_bounds__(kThreads) void clean_fwd_main_kernel(const CleanArg
   const bool mean = a.subtract_mean != 0;
   const bf16* kg = (const bf16*)a.k + base;
 
+  const bf16* ghi = (const bf16*)a.hs_hi + ((long)gs * a.H + h) * K * K;
+  const bf16* glo = (const bf16*)a.hs_lo + ((long)gs * a.H + h) * K * K;
+  PreState<K, SR> pst;  // state rows, one round ahead
+  pst.load(ghi, glo, 0);
   stage_bf16<K>(sQ, LDK, nullptr, 0, (const bf16*)a.q + base + (long)t0 * rs, rs, kBlk, L);
   for (int kk = tid; kk < K; kk += kThreads) {
     sM[kk] = mean ? a.ms[((long)gs * a.H + h) * K + kk] : 0.f;
@@ -416,11 +438,10 @@ __global__ __launch_bounds__(kThreads) void clean_fwd_main_kernel(const CleanArg
   f32x16 Z[TPW];
 #pragma unroll
   for (int j = 0; j < TPW; ++j) Z[j] = zero16();
-  const bf16* ghi = (const bf16*)a.hs_hi + ((long)gs * a.H + h) * K * K;
-  const bf16* glo = (const bf16*)a.hs_lo + ((long)gs * a.H + h) * K * K;
   for (int r0 = 0; r0 < K; r0 += SR) {
-    stage_state<K>(sHhi, sHlo, ghi, glo, r0, SR);
+    pst.store(sHhi, sHlo);
     __syncthreads();
+    if (r0 + SR < K) pst.load(ghi, glo, r0 + SR);
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
       const int ct = w + 4 * j;
@@ -555,6 +576,10 @@ __global__ __launch_bounds__(kThreads) void clean_bwd_dq_kernel(const CleanArgs 
   const bool mean = a.subtract_mean != 0;
   const bf16* kg = (const bf16*)a.k + base;
 
+  const bf16* ghi = (const bf16*)a.hs_hi + ((long)gs * a.H + h) * K * K;
+  const bf16* glo = (const bf16*)a.hs_lo + ((long)gs * a.H + h) * K * K;
+  PreState<K, SR> pst;  // state rows, one round ahead
+  pst.load(ghi, glo, 0);
   stage_bf16<K>(sQ, LDK, nullptr, 0, (const bf16*)a.q + base + (long)t0 * rs, rs, kBlk, L);
   stage_grad<K>(sG, LDG, a, base + (long)t0 * rs, rs, L);
   for (int kk = tid; kk < K; kk += kThreads) {
@@ -578,11 +603,10 @@ __global__ __launch_bounds__(kThreads) void clean_bwd_dq_kernel(const CleanArgs 
     Z[j] = zero16();
     Y[j] = zero16();
   }
-  const bf16* ghi = (const bf16*)a.hs_hi + ((long)gs * a.H + h) * K * K;
-  const bf16* glo = (const bf16*)a.hs_lo + ((long)gs * a.H + h) * K * K;
   for (int r0 = 0; r0 < K; r0 += SR) {
-    stage_state<K>(sHhi, sHlo, ghi, glo, r0, SR);
+    pst.store(sHhi, sHlo);
     __syncthreads();
+    if (r0 + SR < K) pst.load(ghi, glo, r0 + SR);
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
       const int ct = w + 4 * j;
@@ -803,15 +827,33 @@ __global__ __launch_bounds__(kThreads) void clean_bwd_dk_kernel(const CleanArgs 
   const int ce = min(nb - 1, (sidx + 1) * kBps - 1);  // last block of the segment
   const bool mean = a.subtract_mean != 0;
 
+  const bf16* ehi = (const bf16*)a.he_hi + ((long)gs * a.H + h) * K * K;
+  const bf16* elo = (const bf16*)a.he_lo + ((long)gs * a.H + h) * K * K;
+  PreState<K, SR> pst;  // E rows, one round ahead
+  pst.load(ehi, elo, 0);
+  // query block tb (q, dqc, F = -lambda / pos), one block ahead
+  PrefetchBf16<K, kBlk> pq;
+  PrefetchGrad<K, kBlk> pg;
+  float pf = 0.f;
+  auto issue_q = [&](int tb) {
+    const int tq = tb * kBlk, Lq = min(kBlk, len - tq);
+    pq.load((const bf16*)a.q + base + (long)tq * rs, rs, Lq);
+    pg.load(a.dqc32 ? a.dqc32 + base + (long)tq * rs : nullptr,
+            a.dqc32 ? nullptr : (const bf16*)a.dqc16 + base + (long)tq * rs, rs, Lq);
+    if (tid < kBlk) {
+      const float lm = (tid < Lq) ? a.lam[(bos + tq + tid) * a.H + h] : 0.f;
+      pf = -lm / clamp_pos(tq + tid, a.pos_off);
+    }
+  };
+  issue_q(c);
   stage_bf16<K>(sKj, LDK, nullptr, 0, (const bf16*)a.k + base + (long)t0 * rs, rs, kBlk, L);
   f32x16 D[TPW];
 #pragma unroll
   for (int j = 0; j < TPW; ++j) D[j] = zero16();
-  const bf16* ehi = (const bf16*)a.he_hi + ((long)gs * a.H + h) * K * K;
-  const bf16* elo = (const bf16*)a.he_lo + ((long)gs * a.H + h) * K * K;
   for (int r0 = 0; r0 < K; r0 += SR) {
-    stage_state<K>(sEhi, sElo, ehi, elo, r0, SR);
+    pst.store(sEhi, sElo);
     __syncthreads();
+    if (r0 + SR < K) pst.load(ehi, elo, r0 + SR);
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
       const int ct = w + 4 * j;
@@ -823,14 +865,11 @@ __global__ __launch_bounds__(kThreads) void clean_bwd_dk_kernel(const CleanArgs 
     __syncthreads();
   }
   for (int tb = c; tb <= ce; ++tb) {
-    const int tq = tb * kBlk, Lq = min(kBlk, len - tq);
-    stage_bf16<K>(sQt, LDK, nullptr, 0, (const bf16*)a.q + base + (long)tq * rs, rs, kBlk, Lq);
-    stage_grad<K>(sGt, LDG, a, base + (long)tq * rs, rs, Lq);
-    if (tid < kBlk) {
-      const float lm = (tid < Lq) ? a.lam[(bos + tq + tid) * a.H + h] : 0.f;
-      sF[tid] = -lm / clamp_pos(tq + tid, a.pos_off);
-    }
+    pq.store(sQt, LDK, nullptr, 0);
+    pg.store(a.dqc32 != nullptr, sGt, LDG);
+    if (tid < kBlk) sF[tid] = pf;
     __syncthreads();
+    if (tb < ce) issue_q(tb + 1);
     // S1[j][t] = k_j . q_t,  S2[j][t] = k_j . dz_t   (t >= j)
     if (w == 0) {
       f32x16 acc = zero16();

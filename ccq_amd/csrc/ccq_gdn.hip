@@ -105,15 +105,15 @@ __device__ __forceinline__ void lds_to_global_bf16(bf16* g, long gstride, const 
 template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, const int V) {
   constexpr int LDK = K + 8, LDB = BT + 8, LDT = BT + 1;
-  constexpr long kBytes = (long)BT * LDK * 2 + (long)K * LDB * 2 + 2L * BT * LDT * 4 + 64L * LDB * 2 +
-                          4 * 256 * 4 + 3 * 256 * 4 + 4 * BT * 4 + 16 * 12;
+  constexpr long kBytes = (long)BT * LDK * 2 + (long)K * LDB * 2 + 2L * BT * LDT * 4 + 4 * 256 * 4 + 3 * 256 * 4 +
+                          4 * BT * 4 + 16 * 12;
   __shared__ __attribute__((aligned(16))) char smem[kBytes];
   Carver cv{smem};
   bf16* sK = cv.take<bf16>(BT * LDK);
   bf16* sKT = cv.take<bf16>(K * LDB);
   float* sA = cv.take<float>(BT * LDT);   // A, later T
   float* sTo = cv.take<float>(BT * LDT);  // off-diagonal blocks of T
-  bf16* sVT = cv.take<bf16>(64 * LDB);
+  bf16* sVT = sK;                         // value tiles reuse the K rows once A is formed
   float* sD = cv.take<float>(4 * 256);    // inverses of the 16x16 diagonal blocks
   float* sScr = cv.take<float>(3 * 256);
   float* sG = cv.take<float>(BT);
@@ -129,6 +129,10 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, con
   const long tok0 = bos + c0;
   const long rsk = (long)a.H * K, rsv = (long)a.H * V;
 
+  // value tiles, one 64-column block ahead (the first one loads with K)
+  const bf16* vg = (const bf16*)a.v + (tok0 * a.H + h) * (long)V;
+  PrefetchBf16<64, BT> pV;
+  pV.load(vg, rsv, L);
   stage_bf16<K>(sK, LDK, sKT, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
   if (w == 0) {
     float x = (l < L && a.g) ? a.g[(tok0 + l) * a.H + h] : 0.f;
@@ -238,10 +242,10 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, con
   }
   // u = (T diag(beta)) V  (64 x V), 64 value columns at a time
   float* ug = a.u + (tok0 * a.H + h) * (long)V;
-  const bf16* vg = (const bf16*)a.v + (tok0 * a.H + h) * (long)V;
   for (int v0 = 0; v0 < V; v0 += 64) {
-    stage_bf16<64>(nullptr, 0, sVT, LDB, vg + v0, rsv, BT, L);
+    pV.store(nullptr, 0, sVT, LDB);
     __syncthreads();
+    if (v0 + 64 < V) pV.load(vg + v0 + 64, rsv, L);
     {
       const int tr = w & 1, tc = w >> 1;
       f32x16 acc = zero16();
@@ -422,6 +426,14 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
   const long tok0 = bos + c0;
   const long rsk = (long)a.H * K, rsv = (long)a.H * V;
 
+  // state tile and U of value block v0, one block ahead
+  PrefetchBf16<K, 64> pS;
+  PrefetchF32<64, BT> pU;
+  auto issue = [&](int v0) {
+    pS.load((const bf16*)a.hT + (((long)gc * a.H + h) * V + v0) * K, K, 64);
+    pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+  };
+  issue(0);
   stage_any_f32<K>(sQc, LDQ, nullptr, 0, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K : nullptr,
                    a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K : nullptr, rsk, BT, L);
   stage_bf16<K>(sK, LDK, nullptr, 0, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
@@ -464,9 +476,10 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
   bf16* sHt = sK;
   bf16* og = (bf16*)a.o + (tok0 * a.H + h) * (long)V;
   for (int v0 = 0; v0 < V; v0 += 64) {
-    stage_bf16<K>(sHt, LDK, nullptr, 0, (const bf16*)a.hT + (((long)gc * a.H + h) * V + v0) * K, K, 64, 64);
-    stage_f32<64>(nullptr, 0, sUT, LDP, a.U + (tok0 * a.H + h) * (long)V + v0, rsv, BT, L);
+    pS.store(sHt, LDK, nullptr, 0);
+    pU.store(nullptr, 0, sUT, LDP);
     __syncthreads();
+    if (v0 + 64 < V) issue(v0 + 64);
     const int tr = w >> 1, tc = w & 1;
     f32x16 acc = zero16();
     for (int k0 = 0; k0 < K; k0 += 16) {
