@@ -67,6 +67,22 @@ def gpu_step(x):
 
 MULTI_KERNEL_STAGES = ("clean_segsum", "clean_bwd_scan", "clean_bwd_dh0", "clean_bwd_gate")
 
+# HBM bytes per launch at the metric shape, measured with rocprofv3 --pmc FETCH_SIZE and
+# --pmc WRITE_SIZE on this workload (bench.py --copy-calibration), each scaled by the counter's
+# reading for a known-size elementwise copy (fetch x2.000, write x1.000).  Re-measured whenever a
+# kernel changes; a stage absent here reports traffic null.
+MEASURED_TRAFFIC_BYTES = {
+    "gdn_bwd_dqkw": (1493.9e6, 419.4e6),
+    "clean_bwd_dq": (344.9e6, 84.1e6),
+    "gdn_bwd_state": (411.4e6, 402.7e6),
+    "gdn_bwd_wy": (958.5e6, 218.1e6),
+    "clean_bwd_dk": (550.9e6, 67.1e6),
+    "gdn_fwd_state": (277.0e6, 402.7e6),
+    "clean_fwd": (202.1e6, 142.6e6),
+    "gdn_fwd_o": (478.4e6, 134.3e6),
+    "gdn_prep": (151.0e6, 276.8e6),
+}
+
 
 def kernel_work(k=K, v=V, bt=BT, seg=256, blk=32):
     """Algorithmic FLOP and bytes per token x head of each timed stage (its own inputs read once,
@@ -107,8 +123,9 @@ def roofline(step_kernel_ms, launches_per_step):
         achieved, peak, unit, bound = flop * units / avg_s / 1e12, PEAK_BF16 / 1e12, "TFLOP/s", "mfma"
     else:
         achieved, peak, unit, bound = byts * units / avg_s / 1e9, PEAK_HBM / 1e9, "GB/s", "hbm"
+    traffic = sum(MEASURED_TRAFFIC_BYTES[name]) if name in MEASURED_TRAFFIC_BYTES else None
     return {"kernel": name, "bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
-            "frac": achieved / peak, "traffic": None, "avg_launch_us": avg_s * 1e6,
+            "frac": achieved / peak, "traffic": traffic, "avg_launch_us": avg_s * 1e6,
             "algorithmic_flop_per_launch": flop * units, "algorithmic_bytes_per_launch": byts * units}
 
 
@@ -148,6 +165,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed steps, run one elementwise copy of 512 MiB (read) + 512 MiB (write), "
+                         "the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counts")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); this build has no multi-GPU path",
@@ -170,6 +190,12 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     _lib.timing_enable(False)
+    if args.copy_calibration:
+        src = torch.ones(256 << 20, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     kms, klaunch = {}, {}
     for name in _lib.KERNELS:
         ms_tot, n = _lib.timing_read(name)

@@ -18,6 +18,7 @@ hipError_t launch_clean_stage(int stage, const CleanArgs& a, int K, int nseg, in
 hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, float* red, hipStream_t st);
 hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st);
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
+hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
                               hipStream_t st);
@@ -319,7 +320,7 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
       return s;
   }
   if (dm0 && !subtract_mean) {
-    if (int s = hip_status(hipMemsetAsync(dm0, 0, (size_t)N * H * K * sizeof(float), st), "ccq_clean_bwd(dm0)"))
+    if (int s = hip_status(launch_fill_zero(dm0, (long)N * H * K, st), "ccq_clean_bwd(dm0)"))
       return s;
   }
   if (gate) {

@@ -77,6 +77,18 @@ __global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int64_t* cu
   }
 }
 
+// out[i] = 0 for i < n (a kernel rather than hipMemsetAsync, so the call can sit in a captured graph)
+__global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* out, long n) {
+  for (long i = (long)blockIdx.x * kThreads + threadIdx.x; i < n; i += (long)gridDim.x * kThreads) out[i] = 0.f;
+}
+
+hipError_t launch_fill_zero(float* out, long n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const long blocks = (n + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(kThreads), 0, st, out, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st) {
   if (a.rows == 0) return hipSuccess;
   hipLaunchKernelGGL(l2norm_fwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
