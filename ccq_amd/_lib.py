@@ -33,6 +33,10 @@ SIGNATURES = {
     "ccq_gdn_bwd_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
     "ccq_gdn_fwd": (_I, [_P] * 10 + [_I] + [_P] * 3 + [_I] * 6 + [_F, _P]),
     "ccq_gdn_bwd": (_I, [_P] * 9 + [_I] + [_P] * 10 + [_I] * 6 + [_F, _P]),
+    "ccq_gla_saved_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
+    "ccq_gla_bwd_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
+    "ccq_gla_fwd": (_I, [_P] * 9 + [_I] + [_P] * 3 + [_I] * 6 + [_F, _P]),
+    "ccq_gla_bwd": (_I, [_P] * 8 + [_I] + [_P] * 10 + [_I] * 6 + [_F, _P]),
     "ccq_l2norm_fwd": (_I, [_P, _P, _P, _I64, _I, _F, _P]),
     "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
     "ccq_timing_enable": (_I, [_I]),
@@ -80,7 +84,8 @@ def call(name: str, *args) -> None:
 
 
 KERNELS = ("clean_segsum", "clean_fwd", "clean_bwd_dq", "clean_bwd_scan", "clean_bwd_dh0", "clean_bwd_dk", "clean_bwd_gate",
-           "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy")
+           "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy",
+           "gla_intra", "gla_fwd_state", "gla_fwd_o", "gla_bwd_state", "gla_bwd_dv", "gla_bwd_dqk", "gla_bwd_gk")
 
 
 def timing_enable(on: bool) -> None:

@@ -19,6 +19,7 @@ hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, fl
 hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st);
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
+hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
                               hipStream_t st);
@@ -521,6 +522,139 @@ int ccq_timing_read(const char* kernel, double* total_ms, int64_t* launches) {
   auto it = t.done.find(kernel);
   *total_ms = it == t.done.end() ? 0.0 : it->second.first;
   *launches = it == t.done.end() ? 0 : it->second.second;
+  return CCQ_OK;
+}
+
+}  // extern "C"
+
+// ---- gated linear attention ----
+namespace {
+
+struct GlaSaved {
+  float* bcum;
+  float* A;
+  void* hT;
+  void* hTl;
+};
+
+size_t carve_gla_saved(char* base, int64_t tokens, int NTG, int H, int K, int V, GlaSaved* s) {
+  Slicer sl{base};
+  GlaSaved t;
+  t.bcum = sl.take<float>((size_t)tokens * H * K);
+  t.A = sl.take<float>((size_t)NTG * H * 64 * 64);
+  t.hT = sl.take<uint16_t>((size_t)NTG * H * V * K);
+  t.hTl = sl.take<uint16_t>((size_t)NTG * H * V * K);
+  if (s) *s = t;
+  return sl.off;
+}
+
+struct GlaWork {
+  void* dhT;
+  void* dhTl;
+  float* gk_tot;
+};
+
+size_t carve_gla_work(char* base, int NTG, int H, int K, int V, GlaWork* s) {
+  Slicer sl{base};
+  GlaWork t;
+  t.dhT = sl.take<uint16_t>((size_t)NTG * H * V * K);
+  t.dhTl = sl.take<uint16_t>((size_t)NTG * H * V * K);
+  t.gk_tot = sl.take<float>((size_t)NTG * H * K);
+  if (s) *s = t;
+  return sl.off;
+}
+
+int gla_check(const char* who, int B, int T, int H, int K, int V, int N, const int64_t* cu, const int* chunk_index,
+              const int* chunk_offsets, int num_chunks) {
+  if (int s = check_common(B, T, H, N, cu)) return s;
+  if (!(K == 64 || K == 128 || K == 256)) return fail(CCQ_ERR_SHAPE, "%s: K=%d not in {64, 128, 256}", who, K);
+  if (V <= 0 || V % 64 != 0 || V > 1024)
+    return fail(CCQ_ERR_SHAPE, "%s: V=%d must be a positive multiple of 64 (<= 1024)", who, V);
+  if (cu && (!chunk_index || !chunk_offsets))
+    return fail(CCQ_ERR_NULL, "%s: varlen needs chunk_index and chunk_offsets", who);
+  if (!cu && num_chunks != B * ((T + 63) / 64))
+    return fail(CCQ_ERR_SHAPE, "%s: num_chunks=%d, expected B*ceil(T/64)=%d", who, num_chunks, B * ((T + 63) / 64));
+  if (cu && num_chunks < 0) return fail(CCQ_ERR_SHAPE, "%s: negative num_chunks", who);
+  return CCQ_OK;
+}
+
+void fill_gla(GlaArgs& a, const void* q, const float* q_f32, const void* k, const void* v, const float* gk,
+              const int64_t* cu, const int* chunk_index, const int* chunk_offsets, int num_chunks, const GlaSaved& sv,
+              int B, int T, int H, int K, int V, int N, float scale) {
+  a.q16 = q_f32 ? nullptr : q; a.q32 = q_f32; a.k = k; a.v = v; a.gk = gk;
+  a.cu = cu; a.chunk_idx = chunk_index; a.chunk_off = chunk_offsets;
+  a.bcum = sv.bcum; a.A = sv.A; a.hT = sv.hT; a.hTl = sv.hTl;
+  a.scale = scale; a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NTG = num_chunks; a.K = K; a.V = V;
+  (void)B;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ccq_gla_saved_bytes(int64_t tokens, int num_chunks, int H, int K, int V) {
+  return carve_gla_saved(nullptr, tokens, num_chunks, H, K, V, nullptr);
+}
+
+size_t ccq_gla_bwd_workspace_bytes(int64_t tokens, int num_chunks, int H, int K, int V) {
+  (void)tokens;
+  return carve_gla_work(nullptr, num_chunks, H, K, V, nullptr);
+}
+
+int ccq_gla_fwd(const void* q, const float* q_f32, const void* k, const void* v, const float* gk,
+                const float* initial_state, const int64_t* cu_seqlens, const int* chunk_index,
+                const int* chunk_offsets, int num_chunks, void* o, float* final_state, void* saved, int B, int T,
+                int H, int K, int V, int N, float scale, void* stream) {
+  if (int s = gla_check("ccq_gla_fwd", B, T, H, K, V, N, cu_seqlens, chunk_index, chunk_offsets, num_chunks)) return s;
+  if ((!q && !q_f32) || !k || !v || !o || !saved) return fail(CCQ_ERR_NULL, "ccq_gla_fwd: null input/output");
+  if (!aligned16(q) || !aligned16(q_f32) || !aligned16(k) || !aligned16(v) || !aligned16(gk) || !aligned16(o) ||
+      !aligned16(saved))
+    return fail(CCQ_ERR_ALIGN, "ccq_gla_fwd: tensors must be 16-byte aligned");
+  const int64_t tokens = (int64_t)B * T;
+  GlaSaved sv;
+  carve_gla_saved((char*)saved, tokens, num_chunks, H, K, V, &sv);
+  GlaArgs a{};
+  fill_gla(a, q, q_f32, k, v, gk, cu_seqlens, chunk_index, chunk_offsets, num_chunks, sv, B, T, H, K, V, N, scale);
+  a.h0 = initial_state; a.o = o; a.s_fin = final_state;
+  hipStream_t st = (hipStream_t)stream;
+  static const char* names[] = {"gla_intra", "gla_fwd_state", "gla_fwd_o"};
+  const int stages[] = {kGlaIntra, kGlaFwdState, kGlaFwdO};
+  for (int i = 0; i < 3; ++i) {
+    if (int s = hip_status(timed(names[i], st, [&] { return launch_gla_stage(stages[i], a, st); }), names[i])) return s;
+  }
+  return CCQ_OK;
+}
+
+int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v, const float* gk,
+                const int64_t* cu_seqlens, const int* chunk_index, const int* chunk_offsets, int num_chunks,
+                const void* saved, const void* d_o, const float* d_final_state, const float* final_state,
+                void* workspace, float* dq_f32, float* dk_f32, void* dv, float* dgk, float* d_initial_state, int B,
+                int T, int H, int K, int V, int N, float scale, void* stream) {
+  if (int s = gla_check("ccq_gla_bwd", B, T, H, K, V, N, cu_seqlens, chunk_index, chunk_offsets, num_chunks)) return s;
+  if ((!q && !q_f32) || !k || !v || !saved || !d_o || !workspace || !dq_f32 || !dk_f32 || !dv)
+    return fail(CCQ_ERR_NULL, "ccq_gla_bwd: null input/output");
+  if (dgk && !gk) return fail(CCQ_ERR_NULL, "ccq_gla_bwd: dgk requested without gk");
+  if (d_final_state && dgk && !final_state)
+    return fail(CCQ_ERR_NULL, "ccq_gla_bwd: d_final_state with dgk needs the forward's final_state");
+  if (!aligned16(q) || !aligned16(q_f32) || !aligned16(k) || !aligned16(v) || !aligned16(d_o) || !aligned16(dv) ||
+      !aligned16(saved) || !aligned16(workspace))
+    return fail(CCQ_ERR_ALIGN, "ccq_gla_bwd: tensors must be 16-byte aligned");
+  const int64_t tokens = (int64_t)B * T;
+  GlaSaved sv;
+  carve_gla_saved((char*)saved, tokens, num_chunks, H, K, V, &sv);
+  GlaWork wk;
+  carve_gla_work((char*)workspace, num_chunks, H, K, V, &wk);
+  GlaArgs a{};
+  fill_gla(a, q, q_f32, k, v, gk, cu_seqlens, chunk_index, chunk_offsets, num_chunks, sv, B, T, H, K, V, N, scale);
+  a.dout = d_o; a.ds_fin = d_final_state; a.s_fin_in = final_state; a.dhT = wk.dhT; a.dhTl = wk.dhTl;
+  a.dq32 = dq_f32; a.dk32 = dk_f32; a.dv = dv; a.dgk = dgk; a.gk_tot = wk.gk_tot; a.dh0 = d_initial_state;
+  hipStream_t st = (hipStream_t)stream;
+  static const char* names[] = {"gla_bwd_state", "gla_bwd_dv", "gla_bwd_dqk", "gla_bwd_gk"};
+  const int stages[] = {kGlaBwdState, kGlaBwdDv, kGlaBwdDqk, kGlaBwdGk};
+  for (int i = 0; i < 4; ++i) {
+    if (stages[i] == kGlaBwdGk && !dgk) continue;
+    if (int s = hip_status(timed(names[i], st, [&] { return launch_gla_stage(stages[i], a, st); }), names[i])) return s;
+  }
   return CCQ_OK;
 }
 

@@ -143,3 +143,47 @@ struct GdnArgs {
 };
 
 }  // namespace ccq
+
+namespace ccq {
+
+// Gated linear attention (chunk size 64, per-channel log decay gk).  Buffers (caller-allocated):
+//   bcum [tokens, H, K] fp32      in-chunk cumulative log decay b_t = sum_{s<=t in chunk} gk_s
+//   A    [NTG, H, 64, 64] fp32    scale * sum_c q_tc k_sc exp(b_tc - b_sc), causal incl. diagonal
+//   hT   [NTG, H, V, K] bf16      state at each chunk start (transposed), hTl its low part
+//   dhT  [NTG, H, V, K] bf16      gradient of the state after each chunk (transposed), dhTl low part
+//   gk_tot [NTG, H, K] fp32       per-chunk totals of d(cumulative decay), then their suffix carry
+enum GlaStage { kGlaIntra = 0, kGlaFwdState, kGlaFwdO, kGlaBwdState, kGlaBwdDv, kGlaBwdDqk, kGlaBwdGk };
+
+struct GlaArgs {
+  const void* q16;          // bf16 query (or q32)
+  const float* q32;         // fp32 query (the cleaned query)
+  const void* k;            // bf16 [tokens, H, K]
+  const void* v;            // bf16 [tokens, H, V]
+  const float* gk;          // fp32 [tokens, H, K] per-channel log decay (nullable: no decay)
+  const float* h0;          // fp32 [N, H, K, V] (nullable)
+  const int64_t* cu;        // [N+1] (nullable)
+  const int* chunk_idx;     // varlen: [NTG, 2] (sequence, chunk)
+  const int* chunk_off;     // varlen: [N+1]
+  float* bcum;
+  float* A;
+  void* hT;
+  void* hTl;
+  void* o;                  // bf16 [tokens, H, V]
+  float* s_fin;             // fp32 [N, H, K, V] (nullable)
+  // backward
+  const void* dout;         // bf16 [tokens, H, V]
+  const float* ds_fin;      // fp32 [N, H, K, V] (nullable)
+  const float* s_fin_in;    // fp32 [N, H, K, V] forward final state (nullable; needed with ds_fin for dgk)
+  void* dhT;
+  void* dhTl;
+  float* dq32;              // fp32 [tokens, H, K]
+  float* dk32;              // fp32 [tokens, H, K]
+  void* dv;                 // bf16 [tokens, H, V]
+  float* dgk;               // fp32 [tokens, H, K] (nullable)
+  float* gk_tot;
+  float* dh0;               // fp32 [N, H, K, V] (nullable)
+  float scale;
+  int T, H, N, NT, NTG, K, V;
+};
+
+}  // namespace ccq

@@ -126,6 +126,38 @@ int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v,
                 float* dk_f32, void* dv, float* dbeta, float* dg, float* d_initial_state, int B, int T, int H, int K,
                 int V, int N, float scale, void* stream);
 
+/* Bytes of the forward-to-backward buffer and of the backward workspace of the GLA chunk path. */
+size_t ccq_gla_saved_bytes(int64_t tokens, int num_chunks, int H, int K, int V);
+size_t ccq_gla_bwd_workspace_bytes(int64_t tokens, int num_chunks, int H, int K, int V);
+
+/*
+ * Gated linear attention, chunk form (64-token chunks), forward.
+ * Replaces fla chunk_gla as called by the reference (ccq/ops/ccq_gla/fused_chunk.py:42-45,
+ * ccq/ops/ccq_gla/chunk.py:53-58):
+ *   S <- diag(exp(gk_t)) S + k_t v_t^T;  o_t = S^T (scale q_t)
+ * q: bf16 (q) or fp32 (q_f32: the cleaned query kept in fp32); gk fp32 [tokens, H, K] per-channel
+ * log decay (nullable = no decay); initial_state fp32 [N, H, K, V] (nullable).  num_chunks,
+ * chunk_index, chunk_offsets as for ccq_gdn_fwd.  Outputs: o bf16, final_state fp32 (nullable),
+ * saved (ccq_gla_saved_bytes).  K in {64, 128, 256}; V a multiple of 64 (<= 1024).  Exact while
+ * the log decay summed over any 16 consecutive tokens stays above -80.
+ */
+int ccq_gla_fwd(const void* q, const float* q_f32, const void* k, const void* v, const float* gk,
+                const float* initial_state, const int64_t* cu_seqlens, const int* chunk_index,
+                const int* chunk_offsets, int num_chunks, void* o, float* final_state, void* saved, int B, int T,
+                int H, int K, int V, int N, float scale, void* stream);
+
+/*
+ * GLA backward (same inputs and saved buffer as the forward).  d_o bf16 [tokens, H, V];
+ * d_final_state fp32 (nullable) -- with dgk it needs the forward's final_state.
+ * Outputs: dq_f32, dk_f32 fp32 [tokens, H, K]; dv bf16; dgk fp32 [tokens, H, K] (nullable);
+ * d_initial_state fp32 [N, H, K, V] (nullable).
+ */
+int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v, const float* gk,
+                const int64_t* cu_seqlens, const int* chunk_index, const int* chunk_offsets, int num_chunks,
+                const void* saved, const void* d_o, const float* d_final_state, const float* final_state,
+                void* workspace, float* dq_f32, float* dk_f32, void* dv, float* dgk, float* d_initial_state, int B,
+                int T, int H, int K, int V, int N, float scale, void* stream);
+
 /*
  * Row L2 normalisation y = x / sqrt(sum x^2 + eps) (bf16 rows of D <= 512) and its backward.
  * Replaces fla l2norm as called by the reference (ccq/ops/ccq_gdn/fused_chunk.py:43-44).
@@ -140,7 +172,8 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
  * entry point records a HIP event pair around every launch of its kernels on the caller's
  * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: clean_segsum,
  * clean_fwd, clean_bwd_dq, clean_bwd_scan, clean_bwd_dh0, clean_bwd_dk, clean_bwd_gate, gdn_prep, gdn_fwd_state,
- * gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw, gdn_bwd_wy) and returns the summed milliseconds and the number of launches since the last
+ * gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw, gdn_bwd_wy, gla_intra, gla_fwd_state, gla_fwd_o, gla_bwd_state,
+ * gla_bwd_dv, gla_bwd_dqk, gla_bwd_gk) and returns the summed milliseconds and the number of launches since the last
  * ccq_timing_reset.
  */
 int ccq_timing_enable(int on);

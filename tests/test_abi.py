@@ -116,3 +116,39 @@ def test_workspace_sizes_are_consistent(K, V):
     assert ws >= nseg * H * K * K * 4
     assert lib.ccq_clean_bwd_workspace_bytes(tokens, 1, tokens, 1, H, K, 0, 1) > ws
     assert lib.ccq_clean_saved_bytes(tokens, 1, tokens, 3, H, K, 1) > csaved  # varlen adds the indexes
+
+
+def test_gla_rejects_bad_shapes_and_missing_buffers():
+    lib = _lib.load()
+    p = _fake()
+
+    def fwd(K=64, V=64, nc=1, cu=None, ci=None, out=p):
+        return lib.ccq_gla_fwd(p, None, p, p, p, None, cu, ci, ci, nc, out, None, p, 1, 64, 2, K, V, 1 if cu is None
+                               else 2, 0.1, None)
+
+    assert fwd(V=96) == CCQ_ERR_SHAPE
+    assert fwd(K=32) == CCQ_ERR_SHAPE
+    assert fwd(nc=2) == CCQ_ERR_SHAPE
+    assert fwd(cu=p, nc=3) == CCQ_ERR_NULL
+    assert fwd(out=None) == CCQ_ERR_NULL
+
+    def bwd(dgk=p, gk=p, dsf=None, sf=None):
+        return lib.ccq_gla_bwd(p, None, p, p, gk, None, None, None, 1, p, p, dsf, sf, p, p, p, p, dgk, None, 1, 64,
+                               2, 64, 64, 1, 0.1, None)
+
+    assert bwd(gk=None) == CCQ_ERR_NULL          # dgk without gk
+    assert bwd(dsf=p, sf=None) == CCQ_ERR_NULL   # final-state gradient without the final state
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (128, 256), (256, 512)])
+def test_gla_buffer_sizes(K, V):
+    lib = _lib.load()
+    tokens, H = 4096, 4
+    nt = tokens // 64
+    saved = lib.ccq_gla_saved_bytes(tokens, nt, H, K, V)
+    # bcum + A + hT (hi, lo), each rounded up to 256 bytes
+    expect = tokens * H * K * 4 + nt * H * 4096 * 4 + 2 * nt * H * V * K * 2
+    assert expect <= saved <= expect + 4 * 256
+    ws = lib.ccq_gla_bwd_workspace_bytes(tokens, nt, H, K, V)
+    expect = 2 * nt * H * V * K * 2 + nt * H * K * 4
+    assert expect <= ws <= expect + 3 * 256
