@@ -37,6 +37,9 @@ SIGNATURES = {
     "ccq_gla_bwd_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
     "ccq_gla_fwd": (_I, [_P] * 9 + [_I] + [_P] * 3 + [_I] * 6 + [_F, _P]),
     "ccq_gla_bwd": (_I, [_P] * 8 + [_I] + [_P] * 10 + [_I] * 6 + [_F, _P]),
+    "ccq_decode_workspace_bytes": (_SZ, [_I64, _I, _I]),
+    "ccq_gdn_decode": (_I, [_P] * 17 + [_I] * 10 + [_F, _P]),
+    "ccq_gla_decode": (_I, [_P] * 16 + [_I] * 9 + [_F, _P]),
     "ccq_l2norm_fwd": (_I, [_P, _P, _P, _I64, _I, _F, _P]),
     "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
     "ccq_timing_enable": (_I, [_I]),

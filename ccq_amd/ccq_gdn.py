@@ -74,8 +74,9 @@ def _gdn_backward(q16, q32, k, v, g32, beta32, ch: _Chunks, saved, do, dsfin, sc
     dg = torch.empty(B, T, H, device=dev, dtype=torch.float32)
     ds0 = torch.empty(ch.N, H, K, V, device=dev, dtype=torch.float32) if want_ds0 else None
     do = do.contiguous().to(torch.bfloat16)
+    dsfin = _f32(dsfin)  # bound to a name: the buffer must outlive the launch
     call("ccq_gdn_bwd", ptr(q16), ptr(q32), ptr(k), ptr(v), ptr(g32), ptr(beta32), ptr(ch.cu), ptr(ch.index),
-         ptr(ch.offsets), ch.count, ptr(saved), ptr(do), ptr(_f32(dsfin)), ptr(ws), ptr(dq32), ptr(dk32), ptr(dv),
+         ptr(ch.offsets), ch.count, ptr(saved), ptr(do), ptr(dsfin), ptr(ws), ptr(dq32), ptr(dk32), ptr(dv),
          ptr(dbeta), ptr(dg), ptr(ds0), B, T, H, K, V, ch.N, float(scale), stream_of(k))
     return dq32, dk32, dv, dbeta, dg, ds0
 
@@ -213,12 +214,27 @@ def fused_recurrent_ccq_gdn(q, k, v, lambda_h, g=None, gk=None, gv=None, beta=No
                             position_offset=0, subtract_mean=True, enable_ccq=True):
     """CCQ-GDN, recurrent (decode) mode (reference ``ccq/ops/ccq_gdn/fused_recurrent.py:18-75``).
 
-    The recurrence is evaluated by the chunk kernels (a decode step is a one-token chunk).
+    Without autograd (decode, generation) this runs the decode kernels: rank-1 updates of the
+    cached S, C and m per token.  When a gradient is needed it runs the chunk kernels, which
+    compute the same recurrence and have a backward.
     """
+    from .decode import gdn_decode, needs_grad
     if gk is not None or gv is not None:
         raise NotImplementedError("fused_recurrent_ccq_gdn: per-key/per-value gates (gk, gv) are not supported")
     if beta is None:
         beta = torch.ones(q.shape[:3], device=q.device, dtype=torch.float32)
+    if not needs_grad(q, k, v, lambda_h, g, beta, initial_state, initial_cov_state, initial_mean_state):
+        s0 = initial_state
+        if transpose_state_layout and s0 is not None:
+            s0 = s0.transpose(-1, -2)
+        o, s, c, m = gdn_decode(q, k, v, lambda_h, g, beta, _default_scale(scale, q.shape[-1]), s0, initial_cov_state,
+                                initial_mean_state if subtract_mean else None, bool(output_final_state),
+                                bool(use_qk_l2norm_in_kernel), cu_seqlens, position_offset, subtract_mean, enable_ccq)
+        if not output_final_state:
+            return o, None, None, None
+        if transpose_state_layout:
+            s = s.transpose(-1, -2).contiguous()
+        return o, s, c, m
     return chunk_ccq_gdn(q, k, v, lambda_h, g, beta, scale, initial_state, initial_cov_state, initial_mean_state,
                          output_final_state, use_qk_l2norm_in_kernel, cu_seqlens, None, transpose_state_layout,
                          position_offset, subtract_mean, enable_ccq)

@@ -49,8 +49,9 @@ def _gla_backward(q16, q32, k, v, gk32, ch: _Chunks, saved, do, dsfin, sfin, sca
     dgk = torch.empty(B, T, H, K, device=dev, dtype=torch.float32) if want_dgk else None
     ds0 = torch.empty(ch.N, H, K, V, device=dev, dtype=torch.float32) if want_ds0 else None
     do = do.contiguous().to(torch.bfloat16)
+    dsfin = _f32(dsfin)  # bound to a name: the buffer must outlive the launch
     call("ccq_gla_bwd", ptr(q16), ptr(q32), ptr(k), ptr(v), ptr(gk32), ptr(ch.cu), ptr(ch.index), ptr(ch.offsets),
-         ch.count, ptr(saved), ptr(do), ptr(_f32(dsfin)), ptr(sfin), ptr(ws), ptr(dq32), ptr(dk32), ptr(dv), ptr(dgk),
+         ch.count, ptr(saved), ptr(do), ptr(dsfin), ptr(sfin), ptr(ws), ptr(dq32), ptr(dk32), ptr(dv), ptr(dgk),
          ptr(ds0), B, T, H, K, V, ch.N, float(scale), stream_of(k))
     return dq32, dk32, dv, dgk, ds0
 
@@ -163,12 +164,21 @@ def fused_recurrent_ccq_gla(q, k, v, lambda_h, gk=None, gv=None, scale=None, ini
                             initial_cov_state=None, initial_mean_state=None, output_final_state=False,
                             reverse=False, cu_seqlens=None, position_offset=0, subtract_mean=True):
     """CCQ-GLA, recurrent mode (reference ``ccq/ops/ccq_gla/fused_recurrent.py:9-51``), used for
-    decode and for sequences of at most 64 tokens.  Evaluated by the chunk kernels (a short
-    sequence is one partial chunk)."""
+    decode and (in the reference layer, also in training) for sequences of at most 64 tokens.
+    Without autograd it runs the decode kernels; when a gradient is needed it runs the chunk
+    kernels (same recurrence, with a backward)."""
+    from .decode import gla_decode, needs_grad
     if gv is not None:
         raise NotImplementedError("fused_recurrent_ccq_gla: per-value gates (gv) are not supported")
     if reverse:
         raise NotImplementedError("fused_recurrent_ccq_gla: reverse=True is not supported")
+    if not needs_grad(q, k, v, lambda_h, gk, initial_state, initial_cov_state, initial_mean_state):
+        o, s, c, m = gla_decode(q, k, v, lambda_h, gk, _default_scale(scale, q.shape[-1]), initial_state,
+                                initial_cov_state, initial_mean_state if subtract_mean else None,
+                                bool(output_final_state), cu_seqlens, position_offset, subtract_mean)
+        if not output_final_state:
+            return o, None, None, None
+        return o, s, c, m
     return fused_chunk_ccq_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state, initial_mean_state,
                                output_final_state, cu_seqlens, position_offset, subtract_mean)
 

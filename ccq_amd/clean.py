@@ -135,8 +135,11 @@ def clean_backward(q, k, lam_used, gate_w, gate_b, dqc, dk_extra, h0, m0, cu_seq
     dgb = torch.empty_like(gate_b) if gate else None
     dh0 = torch.empty(N, H, K, K, device=dev, dtype=torch.float32) if h0 is not None else None
     dm0 = torch.empty(N, H, K, device=dev, dtype=torch.float32) if (m0 is not None and subtract_mean) else None
+    # converted copies are bound to names so that each buffer outlives the launch (a temporary
+    # freed inside the argument list could be handed to the next conversion)
+    dh_fin, dm_fin = _f32(dh_fin), _f32(dm_fin)
     call("ccq_clean_bwd", ptr(q), ptr(k), ptr(lam_used), ptr(gate_w), ptr(gate_b), ptr(d32), ptr(d16),
-         ptr(dk_extra), ptr(h0), ptr(m0), ptr(cu_seqlens), ptr(saved), ptr(_f32(dh_fin)), ptr(_f32(dm_fin)),
+         ptr(dk_extra), ptr(h0), ptr(m0), ptr(cu_seqlens), ptr(saved), ptr(dh_fin), ptr(dm_fin),
          None if dq_f32 else ptr(dq), ptr(dq) if dq_f32 else None, None if dk_f32 else ptr(dk),
          ptr(dk) if dk_f32 else None, ptr(dlam), ptr(dgw), ptr(dgb), ptr(dh0), ptr(dm0), ptr(ws), B, T, H, K, N,
          int(position_offset), int(bool(subtract_mean)), stream_of(q))

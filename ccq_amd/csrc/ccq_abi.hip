@@ -12,6 +12,7 @@
 
 #include "../../include/ccq_hip.h"
 #include "ccq_params.h"
+#include "ccq_decode_args.h"
 
 namespace ccq {
 hipError_t launch_clean_stage(int stage, const CleanArgs& a, int K, int nseg, int nblk, hipStream_t st);
@@ -20,6 +21,7 @@ hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
                               hipStream_t st);
@@ -656,6 +658,87 @@ int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v,
     if (int s = hip_status(timed(names[i], st, [&] { return launch_gla_stage(stages[i], a, st); }), names[i])) return s;
   }
   return CCQ_OK;
+}
+
+}  // extern "C"
+
+// ---- recurrent (decode) step ----
+namespace {
+
+size_t carve_decode_work(char* base, int64_t tokens, int H, int K, float** qc, float** kn) {
+  Slicer sl{base};
+  float* a = sl.take<float>((size_t)tokens * H * K);
+  float* b = sl.take<float>((size_t)tokens * H * K);
+  if (qc) *qc = a;
+  if (kn) *kn = b;
+  return sl.off;
+}
+
+int decode_common(const char* who, DecodeArgs& a, const void* q, const void* k, const void* v, const float* lambda,
+                  const float* gate_w, const float* gate_b, const float* state, const float* cov_state,
+                  const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
+                  float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
+                  int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq, float scale) {
+  if (int s = check_common(B, T, H, N, cu_seqlens)) return s;
+  if (!clean_k_ok(K)) return fail(CCQ_ERR_SHAPE, "%s: K=%d not in {32, 64, 128, 256}", who, K);
+  if (V <= 0 || V % 64 != 0 || V > 1024)
+    return fail(CCQ_ERR_SHAPE, "%s: V=%d must be a positive multiple of 64 (<= 1024)", who, V);
+  if (!q || !k || !v || !o || !workspace) return fail(CCQ_ERR_NULL, "%s: q, k, v, o and workspace are required", who);
+  if (enable_ccq && !lambda && !gate_w) return fail(CCQ_ERR_NULL, "%s: lambda or gate_w is required", who);
+  if (gate_w && !gate_b) return fail(CCQ_ERR_NULL, "%s: gate_w needs gate_b", who);
+  if (mean_state_out && mean_state_out == mean_state)
+    return fail(CCQ_ERR_SHAPE, "%s: mean_state_out may not alias mean_state (every workgroup reads all of it)", who);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(workspace))
+    return fail(CCQ_ERR_ALIGN, "%s: tensors must be 16-byte aligned", who);
+  const int64_t tokens = (int64_t)B * T;
+  carve_decode_work((char*)workspace, tokens, H, K, &a.qc, &a.kn);
+  a.q = q; a.k = k; a.v = v; a.lam = lambda; a.gate_w = gate_w; a.gate_b = gate_b;
+  a.S_in = state; a.C_in = enable_ccq ? cov_state : nullptr; a.m_in = (enable_ccq && subtract_mean) ? mean_state : nullptr;
+  a.S_out = state_out; a.C_out = enable_ccq ? cov_state_out : nullptr;
+  a.m_out = enable_ccq ? mean_state_out : nullptr;
+  a.o = o; a.cu = cu_seqlens; a.scale = scale;
+  a.T = T; a.H = H; a.N = N; a.K = K; a.V = V; a.pos_off = position_offset; a.subtract_mean = subtract_mean ? 1 : 0;
+  a.l2norm = use_l2norm ? 1 : 0; a.ccq = enable_ccq ? 1 : 0;
+  return CCQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ccq_decode_workspace_bytes(int64_t tokens, int H, int K) {
+  return carve_decode_work(nullptr, tokens, H, K, nullptr, nullptr);
+}
+
+int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                   const float* gate_b, const float* g, const float* beta, const float* state, const float* cov_state,
+                   const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
+                   float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
+                   int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq, float scale,
+                   void* stream) {
+  DecodeArgs a{};
+  if (int s = decode_common("ccq_gdn_decode", a, q, k, v, lambda, gate_w, gate_b, state, cov_state, mean_state,
+                            cu_seqlens, o, state_out, cov_state_out, mean_state_out, workspace, B, T, H, K, V, N,
+                            position_offset, subtract_mean, use_l2norm, enable_ccq, scale))
+    return s;
+  if (!beta) return fail(CCQ_ERR_NULL, "ccq_gdn_decode: beta is required");
+  a.g = g; a.beta = beta; a.gla = 0;
+  return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gdn_decode");
+}
+
+int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                   const float* gate_b, const float* gk, const float* state, const float* cov_state,
+                   const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
+                   float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
+                   int N, int position_offset, int subtract_mean, int use_l2norm, float scale, void* stream) {
+  DecodeArgs a{};
+  if (int s = decode_common("ccq_gla_decode", a, q, k, v, lambda, gate_w, gate_b, state, cov_state, mean_state,
+                            cu_seqlens, o, state_out, cov_state_out, mean_state_out, workspace, B, T, H, K, V, N,
+                            position_offset, subtract_mean, use_l2norm, 1, scale))
+    return s;
+  if (K > 256) return fail(CCQ_ERR_SHAPE, "ccq_gla_decode: K=%d", K);
+  a.gk = gk; a.gla = 1;
+  return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gla_decode");
 }
 
 }  // extern "C"

@@ -1,0 +1,211 @@
+// Recurrent (decode) step of CCQ-GDN and CCQ-GLA on gfx950: a few tokens per sequence against the
+// cached states (S [K, V], C [K, K], m [K], fp32), as the reference's fused_recurrent_ccq_gdn /
+// fused_recurrent_ccq_gla compute it (ccq/ops/ccq_gdn/fused_recurrent.py:18-75 with
+// fused_clean.py:34-83; ccq/ops/ccq_gla/fused_recurrent.py:9-51).  Per token t of a sequence:
+//   q, k <- l2norm(q), l2norm(k)   (optional, outputs rounded to bf16 as fla's l2norm returns them)
+//   C <- C + k k^T;  m <- m + k;  z = C^T q;  s = m . q;  pos = max(t + 1 + position_offset, 1)
+//   q_clean = q - lambda (z / pos - s m / pos^2)          (mean term only with subtract_mean)
+//   GDN: S <- e^g S;  u = beta (v - S^T k);  S <- S + k u^T;  o = S^T (scale q_clean)
+//   GLA: S <- diag(e^gk) S + k v^T;  o = S^T (scale q_clean)
+//
+// The step is HBM-bound (each state element is read and written once per call).  Two launches:
+//   decode_clean   grid (N*H, K/64): each workgroup owns 64 columns of C (held in registers across
+//                  the call's tokens) and writes the fp32 cleaned query of those columns;
+//   decode_backbone grid (N*H, V/64): each workgroup owns 64 columns of S, reads the cleaned query.
+// Thread (column j = tid % 64, row group tid / 64) holds K/4 consecutive rows of its column, so
+// every state access is a coalesced 256-byte row segment.
+#include "ccq_tile.h"
+#include "ccq_decode_args.h"
+
+namespace ccq {
+
+namespace {
+
+__device__ __forceinline__ float block_sum256(float x, float* red) {
+  x = group_sum(x, 64);
+  if (lane_id() == 0) red[wave_id()] = x;
+  __syncthreads();
+  const float s = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return s;
+}
+
+// Normalised (optionally) q and k of one token into LDS as fp32 values of bf16 numbers.
+template <int K>
+__device__ __forceinline__ void load_qk(const DecodeArgs& a, long tok, int h, float* sq, float* sk, float* red) {
+  const int tid = threadIdx.x;
+  const bf16* qg = (const bf16*)a.q + (tok * a.H + h) * K;
+  const bf16* kg = (const bf16*)a.k + (tok * a.H + h) * K;
+  const float qv = tid < K ? (float)qg[tid] : 0.f;
+  const float kv = tid < K ? (float)kg[tid] : 0.f;
+  float rq = 1.f, rk = 1.f;
+  if (a.l2norm) {
+    rq = rsqrtf(block_sum256(qv * qv, red) + 1e-6f);
+    rk = rsqrtf(block_sum256(kv * kv, red) + 1e-6f);
+  }
+  if (tid < K) {
+    sq[tid] = a.l2norm ? (float)(bf16)(qv * rq) : qv;
+    sk[tid] = a.l2norm ? (float)(bf16)(kv * rk) : kv;
+  }
+  __syncthreads();
+}
+
+}  // namespace
+
+template <int K>
+__global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs a) {
+  constexpr int RPT = K / 4;  // rows per thread
+  __shared__ float sq[K], sk[K], sm[K];
+  __shared__ float sz[4][64];
+  __shared__ float red[4];
+  const int tid = threadIdx.x, jj = tid & 63, rg = tid >> 6;
+  const int unit = blockIdx.x, n = unit / a.H, h = unit % a.H;
+  const int j = blockIdx.y * 64 + jj;
+  long bos;
+  int len;
+  seq_bounds(a.cu, n, a.T, bos, len);
+  const bool own = j < K;  // K = 32 launches one 64-column slice with half of it idle
+
+  float creg[RPT];
+  const float* Cin = a.C_in ? a.C_in + (long)unit * K * K : nullptr;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) creg[r] = (Cin && own) ? Cin[(long)(rg * RPT + r) * K + j] : 0.f;
+  if (tid < K) sm[tid] = a.m_in ? a.m_in[(long)unit * K + tid] : 0.f;
+  __syncthreads();
+
+  for (int t = 0; t < len; ++t) {
+    const long tok = bos + t;
+    load_qk<K>(a, tok, h, sq, sk, red);
+    if (blockIdx.y == 0 && tid < K) a.kn[(tok * a.H + h) * K + tid] = sk[tid];
+    if (!a.ccq) {
+      if (blockIdx.y == 0 && tid < K) a.qc[(tok * a.H + h) * K + tid] = sq[tid];
+      __syncthreads();
+      continue;
+    }
+    // lambda
+    float lam;
+    if (a.gate_w) {
+      const float x = tid < K ? a.gate_w[(long)h * K + tid] * sq[tid] : 0.f;
+      lam = sigmoidf_(block_sum256(x, red) + a.gate_b[h]);
+    } else {
+      lam = a.lam[tok * a.H + h];
+    }
+    // running key sum and s = m . q
+    if (tid < K) sm[tid] += sk[tid];
+    __syncthreads();
+    const float s = block_sum256(tid < K ? sm[tid] * sq[tid] : 0.f, red);
+    // C column update and partial z over this thread's rows
+    const float kj = own ? sk[j] : 0.f;
+    float zp = 0.f;
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int i = rg * RPT + r;
+      creg[r] += sk[i] * kj;
+      zp += creg[r] * sq[i];
+    }
+    sz[rg][jj] = zp;
+    __syncthreads();
+    if (rg == 0 && own) {
+      const float z = sz[0][jj] + sz[1][jj] + sz[2][jj] + sz[3][jj];
+      float pos = (float)(t + 1 + a.pos_off);
+      pos = pos < 1.f ? 1.f : pos;
+      float corr = z / pos;
+      if (a.subtract_mean) corr -= s * sm[j] / (pos * pos);
+      a.qc[(tok * a.H + h) * K + j] = sq[j] - lam * corr;
+    }
+    __syncthreads();
+  }
+  if (a.C_out && own) {
+    float* Co = a.C_out + (long)unit * K * K;
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) Co[(long)(rg * RPT + r) * K + j] = creg[r];
+  }
+  if (a.m_out && rg == 0 && own) a.m_out[(long)unit * K + j] = sm[j];
+}
+
+template <int K>
+__global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeArgs a) {
+  constexpr int RPT = K / 4;
+  __shared__ float sq[K], sk[K], sgk[K];
+  __shared__ float sp[4][64];
+  const int tid = threadIdx.x, vv = tid & 63, rg = tid >> 6;
+  const int unit = blockIdx.x, n = unit / a.H, h = unit % a.H;
+  const int V = a.V, v = blockIdx.y * 64 + vv;
+  long bos;
+  int len;
+  seq_bounds(a.cu, n, a.T, bos, len);
+
+  float sreg[RPT];
+  const float* Sin = a.S_in ? a.S_in + (long)unit * K * V : nullptr;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) sreg[r] = Sin ? Sin[(long)(rg * RPT + r) * V + v] : 0.f;
+
+  for (int t = 0; t < len; ++t) {
+    const long tok = bos + t;
+    if (tid < K) {
+      sq[tid] = a.qc[(tok * a.H + h) * K + tid];
+      sk[tid] = a.kn[(tok * a.H + h) * K + tid];
+      if (a.gla) sgk[tid] = a.gk ? __expf(a.gk[(tok * a.H + h) * K + tid]) : 1.f;
+    }
+    __syncthreads();
+    const float vt = (float)((const bf16*)a.v)[(tok * a.H + h) * V + v];
+    if (a.gla) {
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const int i = rg * RPT + r;
+        sreg[r] = sgk[i] * sreg[r] + sk[i] * vt;
+      }
+    } else {
+      const float dec = a.g ? __expf(a.g[tok * a.H + h]) : 1.f;
+      float p = 0.f;
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        sreg[r] *= dec;
+        p += sreg[r] * sk[rg * RPT + r];
+      }
+      sp[rg][vv] = p;
+      __syncthreads();
+      const float ks = sp[0][vv] + sp[1][vv] + sp[2][vv] + sp[3][vv];
+      const float u = a.beta[tok * a.H + h] * (vt - ks);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) sreg[r] += sk[rg * RPT + r] * u;
+      __syncthreads();
+    }
+    float po = 0.f;
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) po += sreg[r] * sq[rg * RPT + r];
+    sp[rg][vv] = po;
+    __syncthreads();
+    if (rg == 0) {
+      const float o = a.scale * (sp[0][vv] + sp[1][vv] + sp[2][vv] + sp[3][vv]);
+      ((bf16*)a.o)[(tok * a.H + h) * V + v] = (bf16)o;
+    }
+    __syncthreads();
+  }
+  if (a.S_out) {
+    float* So = a.S_out + (long)unit * K * V;
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) So[(long)(rg * RPT + r) * V + v] = sreg[r];
+  }
+}
+
+template <int K>
+hipError_t launch_decode_k(const DecodeArgs& a, hipStream_t st) {
+  const int units = a.N * a.H;
+  hipLaunchKernelGGL(decode_clean_kernel<K>, dim3(units, (K + 63) / 64), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL(decode_backbone_kernel<K>, dim3(units, a.V / 64), dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t st) {
+  if (a.N <= 0 || a.H <= 0) return hipSuccess;
+  switch (a.K) {
+    case 32: return launch_decode_k<32>(a, st);
+    case 64: return launch_decode_k<64>(a, st);
+    case 128: return launch_decode_k<128>(a, st);
+    case 256: return launch_decode_k<256>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ccq

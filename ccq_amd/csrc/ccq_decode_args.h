@@ -1,0 +1,33 @@
+// Argument block of the recurrent (decode) step kernels (plain pointers and sizes; shared by the
+// kernels and the C-ABI entry points).
+#pragma once
+
+#include <stdint.h>
+
+namespace ccq {
+
+struct DecodeArgs {
+  const void* q;           // bf16 [tokens, H, K]
+  const void* k;           // bf16 [tokens, H, K]
+  const void* v;           // bf16 [tokens, H, V]
+  const float* lam;        // fp32 [tokens, H] (or gate_w / gate_b)
+  const float* gate_w;     // fp32 [H, K] (nullable)
+  const float* gate_b;     // fp32 [H]
+  const float* g;          // GDN: fp32 [tokens, H] log decay (nullable)
+  const float* beta;       // GDN: fp32 [tokens, H]
+  const float* gk;         // GLA: fp32 [tokens, H, K] log decay (nullable)
+  const float* S_in;       // [N, H, K, V] (nullable = 0)
+  const float* C_in;       // [N, H, K, K] (nullable = 0)
+  const float* m_in;       // [N, H, K] (nullable = 0)
+  float* S_out;            // nullable
+  float* C_out;            // nullable
+  float* m_out;            // nullable
+  void* o;                 // bf16 [tokens, H, V]
+  float* qc;               // workspace fp32 [tokens, H, K]: cleaned query
+  float* kn;               // workspace fp32 [tokens, H, K]: (normalised) key
+  const int64_t* cu;       // [N+1] (nullable)
+  float scale;
+  int T, H, N, K, V, pos_off, subtract_mean, l2norm, ccq, gla;
+};
+
+}  // namespace ccq

@@ -159,6 +159,36 @@ int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v,
                 int T, int H, int K, int V, int N, float scale, void* stream);
 
 /*
+ * Recurrent (decode) step: a few tokens per sequence against cached states, inference only.
+ * Replaces the reference's fused_recurrent_ccq_gdn (ccq/ops/ccq_gdn/fused_recurrent.py:18-75:
+ * fused_ccq_clean(use_chunk=False) = fla fused_recurrent_gla(v=k, h0=C) + _CCQCleanQ, then fla
+ * fused_recurrent_gated_delta_rule(h0=S)) and fused_recurrent_ccq_gla
+ * (ccq/ops/ccq_gla/fused_recurrent.py:9-51, backbone fla fused_recurrent_gla(gk)).  Per token:
+ *   q, k <- l2norm (if use_l2norm; results rounded to bf16); C += k k^T; m += k; z = C^T q;
+ *   q_clean = q - lambda (z/pos - (m.q) m/pos^2), pos = max(t + 1 + position_offset, 1);
+ *   GDN: S <- e^g S; u = beta (v - S^T k); S += k u^T.  GLA: S <- diag(e^gk) S + k v^T.
+ *   o = S^T (scale q_clean)  (bf16 [tokens, H, V]).
+ * state/cov_state/mean_state: cached fp32 S [N, H, K, V], C [N, H, K, K], m [N, H, K] (nullable =
+ * zero); the *_out buffers receive the updated states (nullable = not written).  state_out and
+ * cov_state_out may alias their inputs (in-place cache update); mean_state_out may not.
+ * lambda fp32 [tokens, H] or gate_w/gate_b as in ccq_clean_fwd.  enable_ccq = 0 (GDN only) skips
+ * the cleaning and the C/m states.  workspace: ccq_decode_workspace_bytes().
+ * K in {32, 64, 128, 256}; V a multiple of 64 (<= 1024).
+ */
+size_t ccq_decode_workspace_bytes(int64_t tokens, int H, int K);
+int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                   const float* gate_b, const float* g, const float* beta, const float* state, const float* cov_state,
+                   const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
+                   float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
+                   int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq, float scale,
+                   void* stream);
+int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                   const float* gate_b, const float* gk, const float* state, const float* cov_state,
+                   const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
+                   float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
+                   int N, int position_offset, int subtract_mean, int use_l2norm, float scale, void* stream);
+
+/*
  * Row L2 normalisation y = x / sqrt(sum x^2 + eps) (bf16 rows of D <= 512) and its backward.
  * Replaces fla l2norm as called by the reference (ccq/ops/ccq_gdn/fused_chunk.py:43-44).
  * rstd fp32 [rows] is written by the forward and read by the backward.
