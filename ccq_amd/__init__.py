@@ -9,7 +9,7 @@ kernels of ``libccq_hip.so`` (C ABI in ``include/ccq_hip.h``).
 from .ccq_gdn import (chunk_ccq_gdn, chunk_gated_delta_rule, fused_ccq_clean, fused_chunk_ccq_gdn,
                       fused_recurrent_ccq_gdn)
 from .ccq_gla import chunk_ccq_gla, chunk_gla, fused_chunk_ccq_gla, fused_recurrent_ccq_gla
-from .clean import FusedCCQCleanRead, fused_ccq_clean_read
+from .clean import FusedCCQCleanRead, _ccq_compute_z_and_sum_kk, _CCQCleanQ, fused_ccq_clean_read
 from .l2norm import l2norm
 
 __all__ = [
@@ -24,5 +24,7 @@ __all__ = [
     "chunk_gla",
     "fused_ccq_clean_read",
     "FusedCCQCleanRead",
+    "_CCQCleanQ",
+    "_ccq_compute_z_and_sum_kk",
     "l2norm",
 ]

@@ -36,10 +36,14 @@ SIGNATURES = {
     "ccq_gla_saved_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
     "ccq_gla_bwd_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
     "ccq_gla_fwd": (_I, [_P] * 9 + [_I] + [_P] * 3 + [_I] * 6 + [_F, _P]),
-    "ccq_gla_bwd": (_I, [_P] * 8 + [_I] + [_P] * 10 + [_I] * 6 + [_F, _P]),
+    "ccq_gla_bwd": (_I, [_P] * 8 + [_I] + [_P] * 11 + [_I] * 6 + [_F, _P]),
     "ccq_decode_workspace_bytes": (_SZ, [_I64, _I, _I]),
     "ccq_gdn_decode": (_I, [_P] * 17 + [_I] * 10 + [_F, _P]),
     "ccq_gla_decode": (_I, [_P] * 16 + [_I] * 9 + [_F, _P]),
+    "ccq_clean_z_saved_bytes": (_SZ, [_I, _I, _I]),
+    "ccq_clean_z_bwd_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "ccq_clean_z_fwd": (_I, [_P] * 8 + [_I] + [_P] * 3 + [_I] * 7 + [_P]),
+    "ccq_clean_z_bwd": (_I, [_P] * 7 + [_I] + [_P] * 10 + [_I] * 7 + [_P]),
     "ccq_l2norm_fwd": (_I, [_P, _P, _P, _I64, _I, _F, _P]),
     "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
     "ccq_timing_enable": (_I, [_I]),
@@ -88,7 +92,8 @@ def call(name: str, *args) -> None:
 
 KERNELS = ("clean_segsum", "clean_fwd", "clean_bwd_dq", "clean_bwd_scan", "clean_bwd_dh0", "clean_bwd_dk", "clean_bwd_gate",
            "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy",
-           "gla_intra", "gla_fwd_state", "gla_fwd_o", "gla_bwd_state", "gla_bwd_dv", "gla_bwd_dqk", "gla_bwd_gk")
+           "gla_intra", "gla_fwd_state", "gla_fwd_o", "gla_bwd_state", "gla_bwd_dv", "gla_bwd_dqk", "gla_bwd_gk",
+           "clean_z_fwd", "clean_z_bwd")
 
 
 def timing_enable(on: bool) -> None:

@@ -37,7 +37,8 @@ def _gla_forward(q16, q32, k, v, gk32, s0, ch: _Chunks, scale, want_final):
     return o, sfin, saved
 
 
-def _gla_backward(q16, q32, k, v, gk32, ch: _Chunks, saved, do, dsfin, sfin, scale, want_dgk, want_ds0):
+def _gla_backward(q16, q32, k, v, gk32, ch: _Chunks, saved, do, dsfin, sfin, scale, want_dgk, want_ds0,
+                  dv_f32=False):
     B, T, H, K = k.shape
     V = v.shape[-1]
     dev = k.device
@@ -45,14 +46,14 @@ def _gla_backward(q16, q32, k, v, gk32, ch: _Chunks, saved, do, dsfin, sfin, sca
                      dtype=torch.uint8)
     dq32 = torch.empty(B, T, H, K, device=dev, dtype=torch.float32)
     dk32 = torch.empty(B, T, H, K, device=dev, dtype=torch.float32)
-    dv = torch.empty_like(v)
+    dv = torch.empty(v.shape, device=dev, dtype=torch.float32 if dv_f32 else v.dtype)
     dgk = torch.empty(B, T, H, K, device=dev, dtype=torch.float32) if want_dgk else None
     ds0 = torch.empty(ch.N, H, K, V, device=dev, dtype=torch.float32) if want_ds0 else None
     do = do.contiguous().to(torch.bfloat16)
     dsfin = _f32(dsfin)  # bound to a name: the buffer must outlive the launch
     call("ccq_gla_bwd", ptr(q16), ptr(q32), ptr(k), ptr(v), ptr(gk32), ptr(ch.cu), ptr(ch.index), ptr(ch.offsets),
-         ch.count, ptr(saved), ptr(do), ptr(dsfin), ptr(sfin), ptr(ws), ptr(dq32), ptr(dk32), ptr(dv), ptr(dgk),
-         ptr(ds0), B, T, H, K, V, ch.N, float(scale), stream_of(k))
+         ch.count, ptr(saved), ptr(do), ptr(dsfin), ptr(sfin), ptr(ws), ptr(dq32), ptr(dk32), None if dv_f32 else ptr(dv),
+         ptr(dv) if dv_f32 else None, ptr(dgk), ptr(ds0), B, T, H, K, V, ch.N, float(scale), stream_of(k))
     return dq32, dk32, dv, dgk, ds0
 
 

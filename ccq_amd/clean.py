@@ -17,7 +17,7 @@ from . import _lib
 from ._lib import call, ptr, stream_of
 
 __all__ = ["fused_ccq_clean_read", "FusedCCQCleanRead", "reshape_lambda_3d", "reduce_dlambda", "seq_count",
-           "l2norm_fwd", "l2norm_bwd"]
+           "l2norm_fwd", "l2norm_bwd", "_CCQCleanQ", "_ccq_compute_z_and_sum_kk"]
 
 
 def seq_count(B: int, cu_seqlens: Optional[torch.Tensor]) -> int:
@@ -196,3 +196,107 @@ def fused_ccq_clean_read(q, k, lambda_h, *, position_offset=0, initial_cov_state
     if not output_final_state:
         hf, mf = None, None
     return qc, hf, mf
+
+
+# ---------------------------------------------------------------------------
+# the reference's stock `chunk` building blocks (ccq/ops/common/__init__.py):
+# the covariance read z and the cleaning given z
+# ---------------------------------------------------------------------------
+
+class _CCQCleanQ(torch.autograd.Function):
+    """Cleaning given a precomputed covariance read ``z`` (reference ``_CCQCleanQ``,
+    ``ccq/ops/common/clean.py:691-748``): ``q_clean = q - λ (z/pos - (m·q) m/pos²)`` with the running
+    key sum ``m`` (initial ``initial_state_K``).  Returns ``(q_clean, final_state_K | None)``.
+
+    The backward also returns the gradient of ``initial_state_K`` and folds the gradient of the
+    final key sum into ``dk`` (the reference drops both)."""
+
+    @staticmethod
+    def forward(ctx, q, k, z, lambda_h, position_offset, initial_state_K, output_final_state, subtract_mean,
+                cu_seqlens):
+        from .ccq_gdn import _Chunks
+        _check_qk(q, k)
+        if z.shape != q.shape:
+            raise ValueError(f"z must have q's shape {tuple(q.shape)} (got {tuple(z.shape)})")
+        q, k = q.contiguous(), k.contiguous()
+        z16 = z.contiguous().to(torch.bfloat16)
+        B, T, H, K = q.shape
+        ch = _Chunks(B, T, cu_seqlens, q.device)
+        lam3 = reshape_lambda_3d(lambda_h, q)
+        m0 = _f32(initial_state_K)
+        saved = torch.empty(_lib.load().ccq_clean_z_saved_bytes(ch.count, H, K), device=q.device, dtype=torch.uint8)
+        qc = torch.empty_like(q)
+        mfin = torch.empty(ch.N, H, K, device=q.device, dtype=torch.float32) if output_final_state else None
+        call("ccq_clean_z_fwd", ptr(q), ptr(k), ptr(z16), ptr(lam3), ptr(m0), ptr(cu_seqlens), ptr(ch.index),
+             ptr(ch.offsets), ch.count, ptr(saved), ptr(qc), ptr(mfin), B, T, H, K, ch.N, int(position_offset),
+             int(bool(subtract_mean)), stream_of(q))
+        ctx.save_for_backward(q, k, z16, lam3, saved, cu_seqlens)
+        ctx.ch = ch
+        ctx.lambda_h = lambda_h if isinstance(lambda_h, torch.Tensor) else None
+        ctx.z_dtype = z.dtype
+        ctx.has_m0 = initial_state_K is not None
+        ctx.position_offset = int(position_offset)
+        ctx.subtract_mean = bool(subtract_mean)
+        return qc, mfin
+
+    @staticmethod
+    def backward(ctx, dqc, dmfin):
+        q, k, z16, lam3, saved, cu_seqlens = ctx.saved_tensors
+        ch = ctx.ch
+        B, T, H, K = q.shape
+        ws = torch.empty(_lib.load().ccq_clean_z_bwd_workspace_bytes(ch.count, H, K), device=q.device,
+                         dtype=torch.uint8)
+        dqc = dqc.contiguous()
+        d32 = dqc if dqc.dtype == torch.float32 else None
+        d16 = None if d32 is not None else dqc.to(torch.bfloat16)
+        dmfin = _f32(dmfin)
+        dq, dk, dz = torch.empty_like(q), torch.empty_like(k), torch.empty_like(q)
+        want_dlam = ctx.lambda_h is not None and ctx.lambda_h.requires_grad
+        dlam = torch.empty(B, T, H, device=q.device, dtype=torch.float32) if want_dlam else None
+        dm0 = torch.empty(ch.N, H, K, device=q.device, dtype=torch.float32) if ctx.has_m0 else None
+        call("ccq_clean_z_bwd", ptr(q), ptr(k), ptr(z16), ptr(lam3), ptr(cu_seqlens), ptr(ch.index), ptr(ch.offsets),
+             ch.count, ptr(saved), ptr(d16), ptr(d32), ptr(dmfin), ptr(dq), ptr(dk), ptr(dz), ptr(dlam), ptr(dm0),
+             ptr(ws), B, T, H, K, ch.N, ctx.position_offset, int(ctx.subtract_mean), stream_of(q))
+        dl = reduce_dlambda(dlam, ctx.lambda_h) if dlam is not None else None
+        if dm0 is not None and not ctx.subtract_mean:
+            dm0.zero_()
+        return dq, dk, dz.to(ctx.z_dtype), dl, None, dm0, None, None, None
+
+
+class _CovarianceRead(torch.autograd.Function):
+    """``z = C_tᵀ q_t`` through the GLA chunk kernels with ``v = k`` (no decay, scale 1).  The two
+    roles of k (key and value) are summed in fp32 before the gradient is rounded to k's dtype."""
+
+    @staticmethod
+    def forward(ctx, q, k, initial_state, output_final_state, cu_seqlens):
+        from .ccq_gdn import _Chunks
+        from .ccq_gla import _gla_forward
+        _check_qk(q, k)
+        q, k = q.contiguous(), k.contiguous()
+        B, T, H, K = q.shape
+        ch = _Chunks(B, T, cu_seqlens, q.device)
+        h0 = _f32(initial_state)
+        want = bool(output_final_state)
+        z, hfin, saved = _gla_forward(q, None, k, k, None, h0, ch, 1.0, want)
+        ctx.save_for_backward(q, k, saved, h0, hfin)
+        ctx.ch = ch
+        return z, hfin
+
+    @staticmethod
+    def backward(ctx, dz, dhfin):
+        from .ccq_gla import _gla_backward
+        q, k, saved, h0, hfin = ctx.saved_tensors
+        dq32, dk32, dv32, _, dh0 = _gla_backward(q, None, k, k, None, ctx.ch, saved, dz, dhfin, hfin, 1.0, False,
+                                                 h0 is not None, dv_f32=True)
+        return dq32.to(q.dtype), (dk32 + dv32).to(k.dtype), dh0, None, None
+
+
+def _ccq_compute_z_and_sum_kk(q, k, output_final_state, cu_seqlens, initial_state=None, use_chunk=True,
+                              chunk_size=64):
+    """Covariance read ``z_t = C_tᵀ q_t`` with ``C_t = C_0 + Σ_{j≤t} k_j k_jᵀ`` and the final ``C``
+    (reference ``clean.py:751-771``: fla ``chunk_simple_gla(q, k, v=k, scale=1)``, or the recurrent
+    form for short inputs; both are the same recurrence).  Evaluated by the GLA chunk kernels with
+    ``v = k``, no decay and ``scale = 1``; differentiable in q, k and ``initial_state``.
+    Returns ``(z, final_state | None)`` with z in q's dtype."""
+    z, hfin = _CovarianceRead.apply(q, k, initial_state, bool(output_final_state), cu_seqlens)
+    return z, (hfin if output_final_state else None)

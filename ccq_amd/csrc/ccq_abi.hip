@@ -13,6 +13,7 @@
 #include "../../include/ccq_hip.h"
 #include "ccq_params.h"
 #include "ccq_decode_args.h"
+#include "ccq_zclean_args.h"
 
 namespace ccq {
 hipError_t launch_clean_stage(int stage, const CleanArgs& a, int K, int nseg, int nblk, hipStream_t st);
@@ -22,6 +23,7 @@ hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
+hipError_t launch_zclean(int stage, const ZCleanArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
                               hipStream_t st);
@@ -630,10 +632,10 @@ int ccq_gla_fwd(const void* q, const float* q_f32, const void* k, const void* v,
 int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v, const float* gk,
                 const int64_t* cu_seqlens, const int* chunk_index, const int* chunk_offsets, int num_chunks,
                 const void* saved, const void* d_o, const float* d_final_state, const float* final_state,
-                void* workspace, float* dq_f32, float* dk_f32, void* dv, float* dgk, float* d_initial_state, int B,
-                int T, int H, int K, int V, int N, float scale, void* stream) {
+                void* workspace, float* dq_f32, float* dk_f32, void* dv, float* dv_f32, float* dgk,
+                float* d_initial_state, int B, int T, int H, int K, int V, int N, float scale, void* stream) {
   if (int s = gla_check("ccq_gla_bwd", B, T, H, K, V, N, cu_seqlens, chunk_index, chunk_offsets, num_chunks)) return s;
-  if ((!q && !q_f32) || !k || !v || !saved || !d_o || !workspace || !dq_f32 || !dk_f32 || !dv)
+  if ((!q && !q_f32) || !k || !v || !saved || !d_o || !workspace || !dq_f32 || !dk_f32 || (!dv && !dv_f32))
     return fail(CCQ_ERR_NULL, "ccq_gla_bwd: null input/output");
   if (dgk && !gk) return fail(CCQ_ERR_NULL, "ccq_gla_bwd: dgk requested without gk");
   if (d_final_state && dgk && !final_state)
@@ -649,7 +651,7 @@ int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v,
   GlaArgs a{};
   fill_gla(a, q, q_f32, k, v, gk, cu_seqlens, chunk_index, chunk_offsets, num_chunks, sv, B, T, H, K, V, N, scale);
   a.dout = d_o; a.ds_fin = d_final_state; a.s_fin_in = final_state; a.dhT = wk.dhT; a.dhTl = wk.dhTl;
-  a.dq32 = dq_f32; a.dk32 = dk_f32; a.dv = dv; a.dgk = dgk; a.gk_tot = wk.gk_tot; a.dh0 = d_initial_state;
+  a.dq32 = dq_f32; a.dk32 = dk_f32; a.dv = dv; a.dv32 = dv_f32; a.dgk = dgk; a.gk_tot = wk.gk_tot; a.dh0 = d_initial_state;
   hipStream_t st = (hipStream_t)stream;
   static const char* names[] = {"gla_bwd_state", "gla_bwd_dv", "gla_bwd_dqk", "gla_bwd_gk"};
   const int stages[] = {kGlaBwdState, kGlaBwdDv, kGlaBwdDqk, kGlaBwdGk};
@@ -739,6 +741,87 @@ int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lam
   if (K > 256) return fail(CCQ_ERR_SHAPE, "ccq_gla_decode: K=%d", K);
   a.gk = gk; a.gla = 1;
   return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gla_decode");
+}
+
+}  // extern "C"
+
+// ---- cleaning given a precomputed covariance read z ----
+namespace {
+
+int zclean_check(const char* who, int B, int T, int H, int K, int N, const int64_t* cu, const int* chunk_index,
+                 const int* chunk_offsets, int num_blocks) {
+  if (int s = check_common(B, T, H, N, cu)) return s;
+  if (!clean_k_ok(K)) return fail(CCQ_ERR_SHAPE, "%s: K=%d not in {32, 64, 128, 256}", who, K);
+  if (cu && (!chunk_index || !chunk_offsets))
+    return fail(CCQ_ERR_NULL, "%s: varlen needs chunk_index and chunk_offsets", who);
+  if (!cu && num_blocks != B * ((T + 63) / 64))
+    return fail(CCQ_ERR_SHAPE, "%s: num_blocks=%d, expected B*ceil(T/64)=%d", who, num_blocks, B * ((T + 63) / 64));
+  if (cu && num_blocks < 0) return fail(CCQ_ERR_SHAPE, "%s: negative num_blocks", who);
+  return CCQ_OK;
+}
+
+void fill_zclean(ZCleanArgs& a, const void* q, const void* k, const void* z, const float* lambda,
+                 const int64_t* cu, const int* chunk_index, const int* chunk_offsets, int num_blocks, int T, int H,
+                 int K, int N, int position_offset, int subtract_mean) {
+  a.q = q; a.k = k; a.z = z; a.lam = lambda; a.cu = cu; a.chunk_idx = chunk_index; a.chunk_off = chunk_offsets;
+  a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NB = num_blocks; a.K = K; a.pos_off = position_offset;
+  a.subtract_mean = subtract_mean ? 1 : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ccq_clean_z_saved_bytes(int num_blocks, int H, int K) {
+  Slicer sl{nullptr};
+  sl.take<float>((size_t)num_blocks * H * K);
+  sl.take<float>((size_t)num_blocks * H * K);
+  return sl.off;
+}
+
+size_t ccq_clean_z_bwd_workspace_bytes(int num_blocks, int H, int K) { return ccq_clean_z_saved_bytes(num_blocks, H, K); }
+
+int ccq_clean_z_fwd(const void* q, const void* k, const void* z, const float* lambda, const float* m0,
+                    const int64_t* cu_seqlens, const int* chunk_index, const int* chunk_offsets, int num_blocks,
+                    void* saved, void* q_clean, float* m_final, int B, int T, int H, int K, int N, int position_offset,
+                    int subtract_mean, void* stream) {
+  if (int s = zclean_check("ccq_clean_z_fwd", B, T, H, K, N, cu_seqlens, chunk_index, chunk_offsets, num_blocks))
+    return s;
+  if (!q || !k || !z || !lambda || !saved || !q_clean)
+    return fail(CCQ_ERR_NULL, "ccq_clean_z_fwd: q, k, z, lambda, saved and q_clean are required");
+  ZCleanArgs a{};
+  fill_zclean(a, q, k, z, lambda, cu_seqlens, chunk_index, chunk_offsets, num_blocks, T, H, K, N, position_offset,
+              subtract_mean);
+  Slicer sl{(char*)saved};
+  a.prefix = sl.take<float>((size_t)num_blocks * H * K);
+  a.ksum = sl.take<float>((size_t)num_blocks * H * K);
+  a.m0 = m0; a.qc = q_clean; a.m_fin = m_final;
+  hipStream_t st = (hipStream_t)stream;
+  return hip_status(timed("clean_z_fwd", st, [&] { return launch_zclean(0, a, st); }), "ccq_clean_z_fwd");
+}
+
+int ccq_clean_z_bwd(const void* q, const void* k, const void* z, const float* lambda, const int64_t* cu_seqlens,
+                    const int* chunk_index, const int* chunk_offsets, int num_blocks, const void* saved,
+                    const void* dq_clean, const float* dq_clean_f32, const float* dm_final, void* dq, void* dk,
+                    void* dz, float* dlambda, float* dm0, void* workspace, int B, int T, int H, int K, int N,
+                    int position_offset, int subtract_mean, void* stream) {
+  if (int s = zclean_check("ccq_clean_z_bwd", B, T, H, K, N, cu_seqlens, chunk_index, chunk_offsets, num_blocks))
+    return s;
+  if (!q || !k || !z || !lambda || !saved || (!dq_clean && !dq_clean_f32) || !dq || !dk || !dz || !workspace)
+    return fail(CCQ_ERR_NULL, "ccq_clean_z_bwd: null input/output");
+  ZCleanArgs a{};
+  fill_zclean(a, q, k, z, lambda, cu_seqlens, chunk_index, chunk_offsets, num_blocks, T, H, K, N, position_offset,
+              subtract_mean);
+  Slicer sl{(char*)saved};
+  a.prefix = sl.take<float>((size_t)num_blocks * H * K);
+  Slicer wl{(char*)workspace};
+  a.ksum = wl.take<float>((size_t)num_blocks * H * K);
+  a.carry = wl.take<float>((size_t)num_blocks * H * K);
+  a.dqc16 = dq_clean_f32 ? nullptr : dq_clean; a.dqc32 = dq_clean_f32;
+  a.dm_fin = subtract_mean ? dm_final : nullptr; a.dq = dq; a.dk = dk; a.dz = dz; a.dlam = dlambda;
+  a.dm0 = dm0;
+  hipStream_t st = (hipStream_t)stream;
+  return hip_status(timed("clean_z_bwd", st, [&] { return launch_zclean(1, a, st); }), "ccq_clean_z_bwd");
 }
 
 }  // extern "C"

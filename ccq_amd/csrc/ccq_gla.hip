@@ -518,11 +518,15 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dv_kernel(const GlaArgs a) {
     }
     __syncthreads();
   }
-  bf16* dvg = (bf16*)a.dv + tok0 * rsv + (long)h * a.V + v0;
+  const long dvo = tok0 * rsv + (long)h * a.V + v0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = tr * 32 + acc_row(i);
-    if (r < L) dvg[(long)r * rsv + tc * 32 + acc_col()] = (bf16)acc[i];
+    if (r < L) {
+      const long e = dvo + (long)r * rsv + tc * 32 + acc_col();
+      if (a.dv32) a.dv32[e] = acc[i];
+      if (a.dv) ((bf16*)a.dv)[e] = (bf16)acc[i];
+    }
   }
 }
 

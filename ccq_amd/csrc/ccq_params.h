@@ -178,7 +178,8 @@ struct GlaArgs {
   void* dhTl;
   float* dq32;              // fp32 [tokens, H, K]
   float* dk32;              // fp32 [tokens, H, K]
-  void* dv;                 // bf16 [tokens, H, V]
+  void* dv;                 // bf16 [tokens, H, V] (nullable when dv32 is set)
+  float* dv32;              // fp32 [tokens, H, V] (nullable)
   float* dgk;               // fp32 [tokens, H, K] (nullable)
   float* gk_tot;
   float* dh0;               // fp32 [N, H, K, V] (nullable)

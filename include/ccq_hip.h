@@ -86,6 +86,30 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
                   int K, int N, int position_offset, int subtract_mean, void* stream);
 
 /*
+ * Cleaning given a precomputed covariance read z = C_t^T q_t (the reference's stock `chunk` path):
+ * replaces _CCQCleanQ (ccq/ops/common/clean.py:691-748; forward _ccq_clean_q_triton_fwd :341-384,
+ * backward _ccq_clean_q_bwd_triton :633-688 with _rev_cumsum_time :190-217).
+ *   q_clean_t = q_t - lambda_t (z_t/pos_t - (m_t . q_t) m_t/pos_t^2),  m_t = m0 + sum_{j<=t} k_j
+ * q, k, z, q_clean bf16 [tokens, H, K]; lambda fp32 [tokens, H]; m0, m_final fp32 [N, H, K]
+ * (nullable).  num_blocks / chunk_index / chunk_offsets: 64-token blocks, as for ccq_gdn_fwd.
+ * saved: ccq_clean_z_saved_bytes() bytes (key-sum prefix per block), read by the backward.
+ * Backward: dq_clean bf16 (or dq_clean_f32), dm_final (nullable; used with subtract_mean) ->
+ * dq, dk, dz bf16, dlambda fp32 [tokens, H] (nullable), dm0 fp32 [N, H, K] (nullable).
+ * K in {32, 64, 128, 256}.
+ */
+size_t ccq_clean_z_saved_bytes(int num_blocks, int H, int K);
+size_t ccq_clean_z_bwd_workspace_bytes(int num_blocks, int H, int K);
+int ccq_clean_z_fwd(const void* q, const void* k, const void* z, const float* lambda, const float* m0,
+                    const int64_t* cu_seqlens, const int* chunk_index, const int* chunk_offsets, int num_blocks,
+                    void* saved, void* q_clean, float* m_final, int B, int T, int H, int K, int N, int position_offset,
+                    int subtract_mean, void* stream);
+int ccq_clean_z_bwd(const void* q, const void* k, const void* z, const float* lambda, const int64_t* cu_seqlens,
+                    const int* chunk_index, const int* chunk_offsets, int num_blocks, const void* saved,
+                    const void* dq_clean, const float* dq_clean_f32, const float* dm_final, void* dq, void* dk,
+                    void* dz, float* dlambda, float* dm0, void* workspace, int B, int T, int H, int K, int N,
+                    int position_offset, int subtract_mean, void* stream);
+
+/*
  * Varlen chunk index: chunk_offsets int32 [N+1] and chunk_index int32 [capacity, 2]
  * ((sequence, chunk) per 64-token chunk, -1 past the end), capacity >= tokens/64 + N.
  * Replaces fla prepare_chunk_indices / prepare_chunk_offsets (fused_read.py:36, :349-352).
@@ -149,14 +173,14 @@ int ccq_gla_fwd(const void* q, const float* q_f32, const void* k, const void* v,
 /*
  * GLA backward (same inputs and saved buffer as the forward).  d_o bf16 [tokens, H, V];
  * d_final_state fp32 (nullable) -- with dgk it needs the forward's final_state.
- * Outputs: dq_f32, dk_f32 fp32 [tokens, H, K]; dv bf16; dgk fp32 [tokens, H, K] (nullable);
- * d_initial_state fp32 [N, H, K, V] (nullable).
+ * Outputs: dq_f32, dk_f32 fp32 [tokens, H, K]; dv bf16 and/or dv_f32 fp32 [tokens, H, V] (at least
+ * one); dgk fp32 [tokens, H, K] (nullable); d_initial_state fp32 [N, H, K, V] (nullable).
  */
 int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v, const float* gk,
                 const int64_t* cu_seqlens, const int* chunk_index, const int* chunk_offsets, int num_chunks,
                 const void* saved, const void* d_o, const float* d_final_state, const float* final_state,
-                void* workspace, float* dq_f32, float* dk_f32, void* dv, float* dgk, float* d_initial_state, int B,
-                int T, int H, int K, int V, int N, float scale, void* stream);
+                void* workspace, float* dq_f32, float* dk_f32, void* dv, float* dv_f32, float* dgk,
+                float* d_initial_state, int B, int T, int H, int K, int V, int N, float scale, void* stream);
 
 /*
  * Recurrent (decode) step: a few tokens per sequence against cached states, inference only.
@@ -203,7 +227,7 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
  * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: clean_segsum,
  * clean_fwd, clean_bwd_dq, clean_bwd_scan, clean_bwd_dh0, clean_bwd_dk, clean_bwd_gate, gdn_prep, gdn_fwd_state,
  * gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw, gdn_bwd_wy, gla_intra, gla_fwd_state, gla_fwd_o, gla_bwd_state,
- * gla_bwd_dv, gla_bwd_dqk, gla_bwd_gk) and returns the summed milliseconds and the number of launches since the last
+ * gla_bwd_dv, gla_bwd_dqk, gla_bwd_gk, clean_z_fwd, clean_z_bwd) and returns the summed milliseconds and the number of launches since the last
  * ccq_timing_reset.
  */
 int ccq_timing_enable(int on);

@@ -42,6 +42,8 @@ __all__ = [
     "clean_fwd_bruteforce",
     "clean_fwd_chunked",
     "clean_bwd_closed",
+    "covariance_read",
+    "clean_given_z",
     "gdn_recurrent",
     "gdn_chunked",
     "gla_recurrent",
@@ -291,6 +293,52 @@ def clean_bwd_closed(q, k, lam, dqc, *, position_offset=0, h0=None, m0=None,
     dh0 = torch.stack(dh0s, 0) if h0 is not None else None
     dm0 = torch.stack(dm0s, 0) if (m0 is not None and subtract_mean) else None
     return dq, dk, dlam, dh0, dm0
+
+
+def covariance_read(q, k, *, h0=None, cu_seqlens=None):
+    """``z_t = h_tᵀ q_t`` with ``h_t = h_0 + Σ_{j≤t} k_j k_jᵀ`` and the final ``h`` (the reference's
+    ``_ccq_compute_z_and_sum_kk``, ``clean.py:751-771``: ``chunk_simple_gla(q, k, v=k, scale=1)``).
+    Per-token loop; returns ``(z, h_final [N,H,K,K])``.  Differentiable."""
+    B, T, H, K = q.shape
+    rows = [[None] * T for _ in range(B)]
+    hf = []
+    for n, b, s0, s1 in _segments(B, T, cu_seqlens):
+        C = h0[n].to(q.dtype) if h0 is not None else torch.zeros(H, K, K, dtype=q.dtype)
+        for t in range(s0, s1):
+            kt = k[b, t]
+            C = C + kt[:, :, None] * kt[:, None, :]
+            rows[b][t] = torch.einsum("hab,ha->hb", C, q[b, t])
+        hf.append(C)
+    return torch.stack([torch.stack(r, 0) for r in rows], 0), torch.stack(hf, 0)
+
+
+def clean_given_z(q, k, z, lam, *, position_offset=0, m0=None, subtract_mean=True, cu_seqlens=None):
+    """Cleaning with a precomputed read ``z`` (the reference's ``_CCQCleanQ`` forward,
+    ``clean.py:286-311``)::
+
+        m_t = m_0 + Σ_{j≤t} k_j,   q_clean_t = q_t − λ_t (z_t/pos_t − (m_t·q_t) m_t/pos_t²)
+
+    Returns ``(q_clean, m_final or None)``.  Differentiable.  With ``z`` from
+    ``covariance_read`` it is ``clean_fwd_bruteforce`` (checked in tests).
+    """
+    B, T, H, K = q.shape
+    lam = reshape_lambda(lam, B, T, H, q.dtype)
+    pos = positions(T, cu_seqlens, position_offset, q.dtype)
+    rows = [[None] * T for _ in range(B)]
+    mf = []
+    for n, b, s0, s1 in _segments(B, T, cu_seqlens):
+        m = m0[n].to(q.dtype) if (m0 is not None and subtract_mean) else torch.zeros(H, K, dtype=q.dtype)
+        for t in range(s0, s1):
+            qt = q[b, t]
+            m = m + k[b, t]
+            p = pos[t]
+            corr = z[b, t] / p
+            if subtract_mean:
+                corr = corr - ((m * qt).sum(-1) / (p * p))[:, None] * m
+            rows[b][t] = qt - lam[b, t][:, None] * corr
+        mf.append(m)
+    out = torch.stack([torch.stack(r, 0) for r in rows], 0)
+    return out, (torch.stack(mf, 0) if subtract_mean else None)
 
 
 # ---------------------------------------------------------------------------

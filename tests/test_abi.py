@@ -133,8 +133,8 @@ def test_gla_rejects_bad_shapes_and_missing_buffers():
     assert fwd(out=None) == CCQ_ERR_NULL
 
     def bwd(dgk=p, gk=p, dsf=None, sf=None):
-        return lib.ccq_gla_bwd(p, None, p, p, gk, None, None, None, 1, p, p, dsf, sf, p, p, p, p, dgk, None, 1, 64,
-                               2, 64, 64, 1, 0.1, None)
+        return lib.ccq_gla_bwd(p, None, p, p, gk, None, None, None, 1, p, p, dsf, sf, p, p, p, p, None, dgk, None, 1,
+                               64, 2, 64, 64, 1, 0.1, None)
 
     assert bwd(gk=None) == CCQ_ERR_NULL          # dgk without gk
     assert bwd(dsf=p, sf=None) == CCQ_ERR_NULL   # final-state gradient without the final state

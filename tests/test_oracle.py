@@ -260,3 +260,45 @@ def test_round_through_keeps_gradient():
     assert torch.equal(y.detach(), x.detach().to(torch.bfloat16).to(D))
     y.sum().backward()
     assert torch.equal(x.grad, torch.ones(10, dtype=D))
+
+
+# ----------------------------------------------------------------------------- stock `chunk` blocks
+
+
+def test_covariance_read_closed_form_and_gla_identity():
+    # z_t = (h0 + sum_{j<=t} k_j k_j^T)^T q_t: with orthonormal keys e_1..e_T and no h0, z_t is the
+    # projection of q_t onto span(e_1..e_t); and the read is GLA with v = k, no decay, scale 1.
+    T, K = 5, 8
+    k = torch.eye(K, dtype=D)[:T].view(1, T, 1, K)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, T, 1, K, generator=g, dtype=D)
+    z, hf = O.covariance_read(q, k)
+    for t in range(T):
+        expect = torch.zeros(K, dtype=D)
+        expect[: t + 1] = q[0, t, 0, : t + 1]
+        assert torch.allclose(z[0, t, 0], expect)
+    assert torch.allclose(hf[0, 0], torch.diag(torch.tensor([1.0] * T + [0.0] * (K - T), dtype=D)))
+    q2, k2, _, g2 = _qk(2, 40, 2, 8, seed=4)
+    a = torch.randn(2, 2, 8, 8, generator=g2, dtype=D)
+    z2, h2 = O.covariance_read(q2, k2, h0=a)
+    zg, hg = O.gla_recurrent(q2, k2, k2, None, scale=1.0, h0=a)
+    assert torch.allclose(z2, zg) and torch.allclose(h2, hg)
+
+
+@pytest.mark.parametrize("sub", [True, False])
+def test_clean_given_z_composes_to_bruteforce(sub):
+    # the stock path (read, then clean given z) is the fused closed form, including m0, h0,
+    # position offsets and varlen segments
+    q, k, lam, g = _qk(1, 60, 2, 8, seed=5)
+    cu = torch.tensor([0, 17, 18, 60])
+    h0 = torch.randn(3, 2, 8, 8, generator=g, dtype=D)
+    m0 = torch.randn(3, 2, 8, generator=g, dtype=D)
+    z, hf = O.covariance_read(q, k, h0=h0, cu_seqlens=cu)
+    qc, mf = O.clean_given_z(q, k, z, lam, position_offset=3, m0=m0, subtract_mean=sub, cu_seqlens=cu)
+    ref, hr, mr = O.clean_fwd_bruteforce(q, k, lam, position_offset=3, h0=h0, m0=m0, subtract_mean=sub,
+                                         cu_seqlens=cu)
+    assert torch.allclose(qc, ref) and torch.allclose(hf, hr)
+    if sub:
+        assert torch.allclose(mf, mr)
+    else:
+        assert mf is None and mr is None
