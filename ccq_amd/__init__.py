@@ -11,6 +11,7 @@ from .ccq_gdn import (chunk_ccq_gdn, chunk_gated_delta_rule, fused_ccq_clean, fu
 from .ccq_gla import chunk_ccq_gla, chunk_gla, fused_chunk_ccq_gla, fused_recurrent_ccq_gla
 from .clean import FusedCCQCleanRead, _ccq_compute_z_and_sum_kk, _CCQCleanQ, fused_ccq_clean_read
 from .l2norm import l2norm
+from .layers import CCQGDN, CCQGLA, LayerCache
 
 __all__ = [
     "chunk_ccq_gdn",
@@ -27,4 +28,7 @@ __all__ = [
     "_CCQCleanQ",
     "_ccq_compute_z_and_sum_kk",
     "l2norm",
+    "CCQGDN",
+    "CCQGLA",
+    "LayerCache",
 ]

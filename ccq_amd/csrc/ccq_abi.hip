@@ -356,6 +356,7 @@ struct GdnSaved {
   float* gcum;
   float* tmat;
   void* w;
+  void* wl;
   float* u;
   void* hT;
   void* hTl;
@@ -369,6 +370,7 @@ size_t carve_saved(char* base, int64_t tokens, int NTG, int H, int K, int V, Gdn
   t.gcum = sl.take<float>((size_t)tokens * H);
   t.tmat = sl.take<float>((size_t)NTG * H * 64 * 64);
   t.w = sl.take<uint16_t>((size_t)tokens * H * K);
+  t.wl = sl.take<uint16_t>((size_t)tokens * H * K);
   t.u = sl.take<float>((size_t)tokens * H * V);
   t.hT = sl.take<uint16_t>((size_t)NTG * H * V * K);
   t.hTl = sl.take<uint16_t>((size_t)NTG * H * V * K);
@@ -438,7 +440,7 @@ int ccq_gdn_fwd(const void* q, const float* q_f32, const void* k, const void* v,
   GdnArgs a{};
   a.qc16 = q_f32 ? nullptr : q; a.qc32 = q_f32; a.k = k; a.v = v; a.g = g; a.beta = beta; a.s0 = initial_state;
   a.cu = cu_seqlens; a.chunk_idx = chunk_index; a.chunk_off = chunk_offsets;
-  a.gcum = sv.gcum; a.tmat = sv.tmat; a.w = sv.w; a.u = sv.u; a.hT = sv.hT; a.hTl = sv.hTl; a.U = sv.U; a.PT = sv.PT;
+  a.gcum = sv.gcum; a.tmat = sv.tmat; a.w = sv.w; a.wl = sv.wl; a.u = sv.u; a.hT = sv.hT; a.hTl = sv.hTl; a.U = sv.U; a.PT = sv.PT;
   a.o = o; a.s_fin = final_state; a.scale = scale;
   a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NTG = num_chunks;
   hipStream_t st = (hipStream_t)stream;
@@ -468,7 +470,7 @@ int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v,
   GdnArgs a{};
   a.qc16 = q_f32 ? nullptr : q; a.qc32 = q_f32; a.k = k; a.v = v; a.g = g; a.beta = beta;
   a.cu = cu_seqlens; a.chunk_idx = chunk_index; a.chunk_off = chunk_offsets;
-  a.gcum = sv.gcum; a.tmat = sv.tmat; a.w = sv.w; a.u = sv.u; a.hT = sv.hT; a.hTl = sv.hTl; a.U = sv.U; a.PT = sv.PT;
+  a.gcum = sv.gcum; a.tmat = sv.tmat; a.w = sv.w; a.wl = sv.wl; a.u = sv.u; a.hT = sv.hT; a.hTl = sv.hTl; a.U = sv.U; a.PT = sv.PT;
   a.dout = d_o; a.ds_fin = d_final_state; a.dU = wk.dU; a.dhT = wk.dhT; a.dhTl = wk.dhTl; a.dq32 = dq_f32; a.dkp32 = wk.dkp32;
   a.dw32 = wk.dw32; a.dgp = wk.dgp; a.dk32 = dk_f32; a.dv = dv; a.dbeta = dbeta; a.dg = dg; a.ds0 = d_initial_state;
   a.scale = scale; a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NTG = num_chunks;

@@ -223,6 +223,7 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, con
   // scaled T enters as a hi/lo pair (beta itself is not a bf16 number in general)
   {
     bf16* wg = (bf16*)a.w + (tok0 * a.H + h) * K;
+    bf16* wlg = (bf16*)a.wl + (tok0 * a.H + h) * K;
     for (int tile = w; tile < 2 * (K / 32); tile += 4) {
       const int tr = tile & 1, tc = tile >> 1;
       f32x16 acc = zero16();
@@ -236,7 +237,12 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, con
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = tr * 32 + acc_row(i);
-        if (r < L) wg[(long)r * rsk + tc * 32 + acc_col()] = (bf16)acc[i];
+        if (r < L) {
+          bf16 hi, lo;
+          split2(acc[i], hi, lo);
+          wg[(long)r * rsk + tc * 32 + acc_col()] = hi;
+          wlg[(long)r * rsk + tc * 32 + acc_col()] = lo;
+        }
       }
     }
   }
@@ -273,6 +279,7 @@ template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a, const int V) {
   constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDU = BT + 1, LDV = VB + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
   __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sWl[BT * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sKT[K * LDB];
   __shared__ __attribute__((aligned(16))) bf16 sST[VB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sSTl[VB * LDK];
@@ -306,13 +313,14 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
   }
 
   // Everything a step reads except the state itself is loaded one step ahead into registers.
-  PrefetchBf16<K, BT> pw, pk;
+  PrefetchBf16<K, BT> pw, pwl, pk;
   PrefetchF32<VB, BT> pu;
   float pg = 0.f, pgl = 0.f;
   auto issue = [&](int c) {
     const int c0 = c * BT, L = min(BT, len - c0);
     const long tok0 = bos + c0;
     pw.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L);
+    pwl.load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L);
     pk.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L);
     pu.load(a.u + (tok0 * a.H + h) * (long)V + v0, rsv, L);
     if (tid < BT) {
@@ -326,6 +334,7 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
     const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
     const long tok0 = bos + c0;
     pw.store(sW, LDK, nullptr, 0);
+    pwl.store(sWl, LDK, nullptr, 0);
     pk.store(nullptr, 0, sKT, LDB);
     pu.store(sU, LDV, nullptr, 0);
     if (tid < BT) {
@@ -347,7 +356,10 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
     if (c + 1 < nc) issue(c + 1);
     if (w < 2) {
       f32x16 acc = zero16();
+      // w S with both operands as hi/lo pairs (lo x lo dropped)
       mma_rr(acc, sW + w * 32 * LDK, LDK, sST, LDK, K);
+      mma_rr(acc, sW + w * 32 * LDK, LDK, sSTl, LDK, K);
+      mma_rr(acc, sWl + w * 32 * LDK, LDK, sST, LDK, K);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = w * 32 + acc_row(i), cc = acc_col();
@@ -408,11 +420,18 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
 template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, const int V) {
   constexpr int LDQ = K + 4, LDK = K + 8, LDP = BT + 1;
-  constexpr long kBytes = (long)BT * LDQ * 4 + (long)BT * LDK * 2 + 2L * BT * LDP * 4 + 2 * BT * 4 + 64;
+  // the state enters as a hi/lo pair, staged per 64 value columns x KS key rows
+  constexpr int KS = K > 128 ? 128 : K, NKS = K / KS, LDS_ = KS + 8;
+  constexpr long kRegion = (long)BT * LDK * 2 > 2L * 64 * LDS_ * 2 ? (long)BT * LDK * 2 : 2L * 64 * LDS_ * 2;
+  constexpr long kBytes = (long)BT * LDQ * 4 + kRegion + 2L * BT * LDP * 4 + 2 * BT * 4 + 64;
   __shared__ __attribute__((aligned(16))) char smem[kBytes];
   Carver cv{smem};
   float* sQc = cv.take<float>(BT * LDQ);
-  bf16* sK = cv.take<bf16>(BT * LDK);  // later: state tile [64 v][K]
+  char* region = cv.p;
+  cv.p += kRegion;
+  bf16* sK = (bf16*)region;                 // K rows first; then the state tiles
+  bf16* sHt = (bf16*)region;                // [64 v][KS] hi
+  bf16* sHtl = sHt + 64 * LDS_;             // [64 v][KS] lo
   float* sP = cv.take<float>(BT * LDP);
   float* sUT = cv.take<float>(BT * LDP);
   float* sG = cv.take<float>(BT);
@@ -426,12 +445,16 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
   const long tok0 = bos + c0;
   const long rsk = (long)a.H * K, rsv = (long)a.H * V;
 
-  // state tile and U of value block v0, one block ahead
-  PrefetchBf16<K, 64> pS;
+  // state slice (hi/lo) of step `it` = (value block it / NKS, key slice it % NKS) and, at a new value
+  // block, its U, one step ahead
+  PrefetchBf16<KS, 64> pS, pSl;
   PrefetchF32<64, BT> pU;
-  auto issue = [&](int v0) {
-    pS.load((const bf16*)a.hT + (((long)gc * a.H + h) * V + v0) * K, K, 64);
-    pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+  auto issue = [&](int it) {
+    const int v0 = (it / NKS) * 64, ks = (it % NKS) * KS;
+    const long so = (((long)gc * a.H + h) * V + v0) * K + ks;
+    pS.load((const bf16*)a.hT + so, K, 64);
+    pSl.load((const bf16*)a.hTl + so, K, 64);
+    if (ks == 0) pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, L);
   };
   issue(0);
   stage_any_f32<K>(sQc, LDQ, nullptr, 0, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K : nullptr,
@@ -473,21 +496,30 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
   }
   __syncthreads();
 
-  bf16* sHt = sK;
   bf16* og = (bf16*)a.o + (tok0 * a.H + h) * (long)V;
-  for (int v0 = 0; v0 < V; v0 += 64) {
-    pS.store(sHt, LDK, nullptr, 0);
-    pU.store(nullptr, 0, sUT, LDP);
+  const int nit = (V / 64) * NKS;
+  const int tr = w >> 1, tc = w & 1;
+  f32x16 acc = zero16();
+  for (int it = 0; it < nit; ++it) {
+    const int v0 = (it / NKS) * 64, ks = (it % NKS) * KS;
+    pS.store(sHt, LDS_, nullptr, 0);
+    pSl.store(sHtl, LDS_, nullptr, 0);
+    if (ks == 0) pU.store(nullptr, 0, sUT, LDP);
     __syncthreads();
-    if (v0 + 64 < V) issue(v0 + 64);
-    const int tr = w >> 1, tc = w & 1;
-    f32x16 acc = zero16();
-    for (int k0 = 0; k0 < K; k0 += 16) {
+    if (it + 1 < nit) issue(it + 1);
+    if (ks == 0) acc = zero16();
+    for (int k0 = 0; k0 < KS; k0 += 16) {
       bf16x8 hi, lo;
-      frag_rm_f32(sQc + tr * 32 * LDQ + k0, LDQ, hi, lo);
-      const bf16x8 b = frag_rm(sHt + tc * 32 * LDK + k0, LDK);
-      acc = mfma(hi, b, acc);
-      acc = mfma(lo, b, acc);
+      frag_rm_f32(sQc + tr * 32 * LDQ + ks + k0, LDQ, hi, lo);
+      const bf16x8 bh = frag_rm(sHt + tc * 32 * LDS_ + k0, LDS_);
+      const bf16x8 bl = frag_rm(sHtl + tc * 32 * LDS_ + k0, LDS_);
+      acc = mfma(hi, bh, acc);
+      acc = mfma(hi, bl, acc);
+      acc = mfma(lo, bh, acc);
+    }
+    if (ks + KS < K) {
+      __syncthreads();
+      continue;
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] *= a.scale * sGam[tr * 32 + acc_row(i)];
@@ -516,10 +548,10 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
 template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a, const int V) {
   constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDP = BT + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
-  constexpr int KH = K > 128 ? 128 : K, NKH = K / KH;
+  constexpr int KH = K > 128 ? 64 : K, NKH = K / KH;  // query / w rows staged per pass
   constexpr long kBytes = (long)BT * LDP * 4 + (long)VB * LDB * 2 + (long)BT * LDK * 2 + (long)VB * LDK * 2 +
-                          2L * VB * LDP * 4 + (long)KH * LDP * 4 + (long)KH * LDB * 2 + 3L * BT * 4 +
-                          (long)VB * LDK * 2 + 16 * 11;
+                          2L * VB * LDP * 4 + (long)KH * LDP * 4 + 2L * KH * LDB * 2 + 3L * BT * 4 +
+                          (long)VB * LDK * 2 + 16 * 12;
   __shared__ __attribute__((aligned(16))) char smem[kBytes];
   Carver cv{smem};
   float* sPT = cv.take<float>(BT * LDP);
@@ -531,6 +563,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
   float* sgdOT = cv.take<float>(VB * LDP);  // scale gamma_t dO[t][v], [v][t]
   float* sQcT = cv.take<float>(KH * LDP);
   bf16* swT = cv.take<bf16>(KH * LDB);
+  bf16* swTl = cv.take<bf16>(KH * LDB);
   float* sFac = cv.take<float>(BT);
   float* sGam = cv.take<float>(BT);
   float* sGL = cv.take<float>(4);
@@ -567,7 +600,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
   PrefetchBf16<VB, BT> pO;
   PrefetchBf16<K, BT> pK;
   PrefetchGrad<kPreQW ? KH : 8, BT> pQ;
-  PrefetchBf16<kPreQW ? KH : 8, BT> pW;
+  PrefetchBf16<kPreQW ? KH : 8, BT> pW, pWl;
   float pgl = 0.f, pgt = 0.f;
   auto issue = [&](int c) {
     const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
@@ -579,6 +612,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
       pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K : nullptr,
               a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K : nullptr, rsk, L);
       pW.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L);
+      pWl.load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L);
     }
     if (tid < BT) {
       pgl = a.gcum[(tok0 + L - 1) * a.H + h];
@@ -596,6 +630,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     if (kPreQW) {
       pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
       pW.store(nullptr, 0, swT, LDB);
+      pWl.store(nullptr, 0, swTl, LDB);
     }
     if (tid < BT) {
       sFac[tid] = __expf(pgl - pgt);
@@ -651,6 +686,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
         stage_any_f32<KH>(nullptr, 0, sQcT, LDP, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + hb * KH : nullptr,
                           a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + hb * KH : nullptr, rsk, BT, L);
         stage_bf16<KH>(nullptr, 0, swT, LDB, (const bf16*)a.w + (tok0 * a.H + h) * K + hb * KH, rsk, BT, L);
+        stage_bf16<KH>(nullptr, 0, swTl, LDB, (const bf16*)a.wl + (tok0 * a.H + h) * K + hb * KH, rsk, BT, L);
         __syncthreads();
       }
 #pragma unroll
@@ -668,10 +704,12 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
             dS[j] = mfma(qhi, glo, dS[j]);
             dS[j] = mfma(qlo, ghi, dS[j]);
             const bf16x8 wa = frag_rm(swT + lr * LDB + k0, LDB);
+            const bf16x8 wal = frag_rm(swTl + lr * LDB + k0, LDB);
             bf16x8 dhi, dlo;
             frag_rm_f32(sdUT + k0, LDP, dhi, dlo);
             dS[j] = mfma(wa, dhi, dS[j]);
             dS[j] = mfma(wa, dlo, dS[j]);
+            dS[j] = mfma(wal, dhi, dS[j]);
           }
         }
       }

@@ -92,7 +92,7 @@ namespace ccq {
 // Gated delta rule (chunk size 64).  Internal buffers (all caller-allocated):
 //   gcum [tokens, H] fp32         in-chunk cumulative log decay
 //   tmat [NTG, H, 64, 64] fp32    T = (I + A)^-1 of the WY representation
-//   w    [tokens, H, K] bf16      w = T diag(beta exp(G)) K
+//   w, wl [tokens, H, K] bf16     w = T diag(beta exp(G)) K as a hi/lo pair
 //   u    [tokens, H, V] fp32      u = T diag(beta) V
 //   hT   [NTG, H, V, K] bf16      state at each chunk start (transposed); hTl its low part
 //   U    [tokens, H, V] fp32      U = u - w S (pseudo-values after the delta correction)
@@ -116,6 +116,7 @@ struct GdnArgs {
   float* gcum;
   float* tmat;
   void* w;
+  void* wl;                 // bf16 low part of w (w + wl ~ fp32)
   float* u;
   void* hT;
   void* hTl;                // bf16 low parts of hT (hT + hTl ~ fp32 state)

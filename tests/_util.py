@@ -13,6 +13,12 @@ def rel(a: torch.Tensor, b: torch.Tensor) -> float:
     return (a - b).norm().item() / (den if den > 0 else 1.0)
 
 
+def kern(a: torch.Tensor, b: torch.Tensor) -> float:
+    """Error of a kernel output `a` against the oracle `b` rounded to `a`'s dtype: zero for an exact
+    kernel, apart from the rare element where the two roundings fall on different sides."""
+    return rel(a, b.detach().to(a.dtype))
+
+
 def bf(x: torch.Tensor) -> torch.Tensor:
     return x.to(torch.bfloat16)
 

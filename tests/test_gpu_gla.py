@@ -7,11 +7,12 @@ import torch
 import torch.nn.functional as F
 
 from oracle import ccq_oracle as O
-from tests._util import bf, l2n, rel
+from tests._util import bf, kern, l2n, rel
 
 pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-3
+TOL_KERNEL = 5e-4   # output vs the oracle rounded to bf16: the kernels' own error
 
 
 def _cuda():
@@ -64,12 +65,18 @@ def test_gla_backbone(case):
     ((o.float() * do.to(dev).float()).sum() + (s * dsf.to(dev)).sum()).backward()
     torch.cuda.synchronize()
     errs = {"o": rel(o, o_r), "S": rel(s, s_r)}
+    kerrs = {"o": kern(o, o_r)}
     for n in ("q", "k", "v", "gk", "s0"):
         if ref[n] is not None:
             errs["d" + n] = rel(g[n].grad, ref[n].grad)
-    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+            if g[n].grad.dtype == torch.bfloat16:
+                kerrs["d" + n] = kern(g[n].grad, ref[n].grad)
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
     for n, e in errs.items():
         assert e <= TOL_BF16, n
+    for n, e in kerrs.items():
+        assert e <= TOL_KERNEL, n
 
 
 FUSED_GLA_CASES = [
@@ -119,6 +126,11 @@ def test_fused_ccq_gla(case):
     # (fused_read.py:502-513): on a few hundred per-token values the bf16 rounding alone can pass
     # 2e-3, so it is held to the oracle gradient rounded the same way.
     errs["dlam"] = rel(g["lam"].grad, ref["lam"].grad.to(torch.bfloat16))
-    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    kerrs = {"o": kern(o, o_r), "dq": kern(g["q"].grad, ref["q"].grad), "dk": kern(g["k"].grad, ref["k"].grad),
+             "dv": kern(g["v"].grad, ref["v"].grad)}
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
     for n, e in errs.items():
         assert e <= TOL_BF16, n
+    for n, e in kerrs.items():
+        assert e <= TOL_KERNEL, n

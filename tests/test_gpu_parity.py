@@ -11,11 +11,14 @@ import pytest
 import torch
 
 from oracle import ccq_oracle as O
-from tests._util import bf, gdn_inputs, l2n, rel
+from tests._util import bf, gdn_inputs, kern, l2n, rel
 
 pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-3
+# The kernels keep every intermediate at ~16 significant bits, so their output differs from the
+# oracle's rounded to the same dtype only where a rounding flips: held to a quarter of the bar.
+TOL_KERNEL = 5e-4
 
 
 def _cuda():
@@ -106,9 +109,13 @@ def test_clean_fwd_bwd(case):
         errs["dh0"] = rel(h0g.grad, r_dh0)
     if m0 is not None and sub:
         errs["dm0"] = rel(m0g.grad, r_dm0)
-    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    kerrs = {"dq": kern(qg.grad, r_dq), "dk": kern(kg.grad, r_dk)}
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
     assert errs["q_clean"] <= TOL_BF16
-    assert errs["q_clean_vs_bf16_ref"] <= 5e-4
+    assert errs["q_clean_vs_bf16_ref"] <= TOL_KERNEL
+    for n, e in kerrs.items():
+        assert e <= TOL_KERNEL, n
     for n in ("dq", "dk"):
         assert errs[n] <= TOL_BF16, n
     for n in ("h_final", "m_final", "dh0", "dm0", "dlam"):  # fp32 outputs
@@ -150,12 +157,18 @@ def test_gdn_backbone(case):
     ((o.float() * do.to(dev).float()).sum() + (s * dsf.to(dev)).sum()).backward()
     torch.cuda.synchronize()
     errs = {"o": rel(o, o_r), "S": rel(s, s_r)}
+    kerrs = {"o": kern(o, o_r)}  # the kernels' own error, rounding of the outputs aside
     for n in ("q", "k", "v", "g", "beta", "s0"):
         if ref[n] is not None:
             errs["d" + n] = rel(g[n].grad, ref[n].grad)
-    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+            if g[n].grad.dtype == torch.bfloat16:
+                kerrs["d" + n] = kern(g[n].grad, ref[n].grad)
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
     for n, e in errs.items():
         assert e <= TOL_BF16, n
+    for n, e in kerrs.items():
+        assert e <= TOL_KERNEL, n
 
 
 FUSED_CASES = [
@@ -197,9 +210,15 @@ def test_fused_ccq_gdn(case):
     (o.float() * do.to(dev).float()).sum().backward()
     torch.cuda.synchronize()
     errs = {"o": rel(o, o_r), "S": rel(s, s_r), "C": rel(h, h_r), "m": rel(m, m_r)}
+    kerrs = {"o": kern(o, o_r)}
     for n in x:
         if ref[n] is not None and ref[n].grad is not None:
             errs["d" + n] = rel(g[n].grad, ref[n].grad)
-    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+            if g[n].grad.dtype == torch.bfloat16:
+                kerrs["d" + n] = kern(g[n].grad, ref[n].grad)
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
     for n, e in errs.items():
         assert e <= TOL_BF16, n
+    for n, e in kerrs.items():
+        assert e <= TOL_KERNEL, n

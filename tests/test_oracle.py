@@ -302,3 +302,4 @@ def test_clean_given_z_composes_to_bruteforce(sub):
         assert torch.allclose(mf, mr)
     else:
         assert mf is None and mr is None
+
