@@ -65,7 +65,7 @@ def gpu_step(x):
     return torch.autograd.grad(o, [x[n] for n in LEAVES], x["do"])
 
 
-MULTI_KERNEL_STAGES = ("clean_segsum", "clean_bwd_scan", "clean_bwd_dh0", "clean_bwd_gate")
+MULTI_KERNEL_STAGES = ("clean_bwd_gate",)
 
 # HBM bytes per launch at the metric shape, measured with rocprofv3 --pmc FETCH_SIZE and
 # --pmc WRITE_SIZE on this workload (bench.py --copy-calibration), each scaled by the counter's
@@ -73,30 +73,25 @@ MULTI_KERNEL_STAGES = ("clean_segsum", "clean_bwd_scan", "clean_bwd_dh0", "clean
 # kernel changes; a stage absent here reports traffic null.
 MEASURED_TRAFFIC_BYTES = {
     "gdn_bwd_dqkw": (1493.9e6, 419.4e6),
-    "clean_bwd_dq": (344.9e6, 84.1e6),
     "gdn_bwd_state": (411.4e6, 402.7e6),
     "gdn_bwd_wy": (958.5e6, 218.1e6),
-    "clean_bwd_dk": (550.9e6, 67.1e6),
     "gdn_fwd_state": (277.0e6, 402.7e6),
-    "clean_fwd": (202.1e6, 142.6e6),
     "gdn_fwd_o": (478.4e6, 134.3e6),
     "gdn_prep": (151.0e6, 276.8e6),
 }
 
 
-def kernel_work(k=K, v=V, bt=BT, seg=256, blk=32):
+def kernel_work(k=K, v=V, bt=BT, cb=64):
     """Algorithmic FLOP and bytes per token x head of each timed stage (its own inputs read once,
-    its own outputs written once).  Cleaning: 256-token segments of 32-token blocks, so a query
-    attends on average keys = blk * (seg / blk + 1) / 2 = 144 keys of its segment plus one state
-    read; segment states are counted once per segment (hi/lo bf16 = 4 bytes per element)."""
-    keys = blk * (seg // blk + 1) // 2
-    st = 4 * k * k // seg
+    its own outputs written once), for the metric's call (fp32 q_clean into the delta rule, fp32
+    upstream gradients, bf16 dq / dk).  Cleaning walks over cb-token chunks: per token a K x K state
+    read and update (2 K^2 each) plus causal scores over the chunk (K cb per product, two products
+    forward / dq, four in the dk walk with a second K x K update)."""
     return {
-        "clean_segsum": (2 * k * k, 2 * k + st + 4 * k // seg),
-        "clean_fwd": (2 * k * k + 4 * k * keys + 2 * k, 2 * k + 2 * k + 4 + st + 4 * k // seg + 4 * k),
-        "clean_bwd_dq": (4 * k * k + 8 * k * keys + 2 * k, 4 * k + 4 + 4 * k + st + 2 * k + 8 + 4 * k // blk),
-        "clean_bwd_scan": (4 * k * k, 2 * k + 4 * k + 4 + st),
-        "clean_bwd_dk": (2 * k * k + 8 * k * keys, 2 * k + 2 * k + 4 * k + 8 + 4 + st + 4 * k + 2 * k),
+        "clean_fwd": (4 * k * k + 2 * k * cb, 2 * k + 2 * k + 4 + 4 * k + 4 * k + 4 + 4 * k // cb),
+        "clean_bwd_rows": (6 * k, 4 * k + 4 * k + 2 * k + 2 * k + 4 + 4 + 4 * k // cb + 16 + 4 * k // cb),
+        "clean_bwd_dq": (4 * k * k + 2 * k * cb, 4 * k + 2 * k + 16 + 4 * k // cb + 2 * k),
+        "clean_bwd_dk": (6 * k * k + 4 * k * cb, 2 * k + 2 * k + 4 * k + 16 + 4 * k + 2 * k),
         "gdn_prep": (2 * bt * (2 * k + v) + (2 * bt * bt) // 3, 2 * k + 2 * v + 8 + 2 * k + 4 * v + 4 + 4 * bt),
         "gdn_fwd_state": (4 * k * v, 4 * k + 4 * v + 4 * v + 4 * k * v // bt),
         "gdn_fwd_o": (2 * bt * k + 2 * k * v + 2 * bt * v, 4 * k + 2 * k + 2 * k * v // bt + 4 * v + 2 * v + 4 * bt),
@@ -111,8 +106,8 @@ def kernel_work(k=K, v=V, bt=BT, seg=256, blk=32):
 def roofline(step_kernel_ms, launches_per_step):
     """Roofline object for the kernel with the largest share of the step."""
     work = kernel_work()
-    # stages that launch several kernels (segment sums + prefix scans) are left out so that the
-    # average launch time compares one-to-one with a kernel trace
+    # stages that launch several kernels (the gate's two row sums) are left out so that the average
+    # launch time compares one-to-one with a kernel trace
     single = [n for n in step_kernel_ms if n in work and n not in MULTI_KERNEL_STAGES]
     name = max(single, key=lambda n: step_kernel_ms[n])
     flop, byts = work[name]

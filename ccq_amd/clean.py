@@ -128,6 +128,11 @@ def clean_backward(q, k, lam_used, gate_w, gate_b, dqc, dk_extra, h0, m0, cu_seq
     dqc = dqc.contiguous()
     d32 = dqc if dqc.dtype == torch.float32 else None
     d16 = None if d32 is not None else dqc.to(torch.bfloat16)
+    # the kernels read the upstream gradient in 16-byte vectors
+    if d32 is not None and d32.data_ptr() % 16:
+        d32 = d32.clone()
+    if d16 is not None and d16.data_ptr() % 16:
+        d16 = d16.clone()
     dq = torch.empty(q.shape, device=dev, dtype=torch.float32 if dq_f32 else q.dtype)
     dk = torch.empty(k.shape, device=dev, dtype=torch.float32 if dk_f32 else k.dtype)
     dlam = torch.empty(B, T, H, device=dev, dtype=torch.float32) if (want_dlam and not gate) else None

@@ -14,9 +14,10 @@
 #include "ccq_params.h"
 #include "ccq_decode_args.h"
 #include "ccq_zclean_args.h"
+#include "ccq_walk_args.h"
 
 namespace ccq {
-hipError_t launch_clean_stage(int stage, const CleanArgs& a, int K, int nseg, int nblk, hipStream_t st);
+hipError_t launch_cwalk(int stage, const WalkArgs& a, hipStream_t st);
 hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, float* red, hipStream_t st);
 hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st);
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
@@ -137,98 +138,76 @@ const char* ccq_last_error(void) { return g_err; }
 // ---- cleaning: geometry and buffers ----
 namespace {
 
-constexpr int kCleanBlk = 32, kCleanSeg = 256;
-
-struct CleanGeom {
-  int nb, ns;        // blocks / segments per sequence (dense) or capacities (varlen)
-  int capb, caps;    // launched grid sizes
+struct WalkGeom {
+  int cb;   // tokens per chunk
+  int nt;   // chunks per sequence (dense)
+  int ntg;  // chunk slots (dense: B * nt; varlen: capacity of the chunk index)
 };
 
-CleanGeom clean_geom(int64_t tokens, int B, int T, int N, bool varlen) {
-  CleanGeom g;
+WalkGeom walk_geom(int64_t tokens, int B, int T, int N, int K, bool varlen) {
+  WalkGeom g;
+  g.cb = walk_chunk(K);
   if (varlen) {
-    g.capb = (int)(tokens / kCleanBlk) + N + 1;
-    g.caps = (int)(tokens / kCleanSeg) + N + 1;
-    g.nb = g.capb;
-    g.ns = g.caps;
+    g.nt = 0;
+    g.ntg = (int)(tokens / g.cb) + N + 1;
   } else {
-    g.nb = (T + kCleanBlk - 1) / kCleanBlk;
-    g.ns = (T + kCleanSeg - 1) / kCleanSeg;
-    g.capb = B * g.nb;
-    g.caps = B * g.ns;
+    g.nt = (T + g.cb - 1) / g.cb;
+    g.ntg = B * g.nt;
   }
   return g;
 }
 
-struct CleanSaved {
-  int* blk_idx;
-  int* blk_off;
-  int* seg_idx;
-  int* seg_off;
-  float* pseg;
-  float* mseg;
-  void* hs_hi;
-  void* hs_lo;
-  float* ms;
+struct WalkSaved {
+  int* chunk_idx;
+  int* chunk_off;
+  float* z;
+  float* srow;
+  float* mpre;
 };
 
-size_t carve_clean_saved(char* base, const CleanGeom& g, int N, int H, int K, bool varlen, CleanSaved* out) {
+size_t carve_walk_saved(char* base, const WalkGeom& g, int64_t tokens, int N, int H, int K, bool varlen,
+                        WalkSaved* out) {
   Slicer sl{base};
-  CleanSaved t{};
+  WalkSaved t{};
   if (varlen) {
-    t.blk_idx = sl.take<int>((size_t)g.capb * 2);
-    t.blk_off = sl.take<int>((size_t)N + 1);
-    t.seg_idx = sl.take<int>((size_t)g.caps * 2);
-    t.seg_off = sl.take<int>((size_t)N + 1);
+    t.chunk_idx = sl.take<int>((size_t)g.ntg * 2);
+    t.chunk_off = sl.take<int>((size_t)N + 1);
   }
-  const size_t sk = (size_t)g.caps * H;
-  t.pseg = sl.take<float>(sk * K * K);
-  t.mseg = sl.take<float>(sk * K);
-  t.hs_hi = sl.take<uint16_t>(sk * K * K);
-  t.hs_lo = sl.take<uint16_t>(sk * K * K);
-  t.ms = sl.take<float>(sk * K);
+  t.z = sl.take<float>((size_t)tokens * H * K);
+  t.srow = sl.take<float>((size_t)tokens * H);
+  t.mpre = sl.take<float>((size_t)g.ntg * H * K);
   if (out) *out = t;
   return sl.off;
 }
 
-struct CleanWork {
-  float* pseg;
-  void* he_hi;
-  void* he_lo;
+struct WalkWork {
   float* sc;
-  float* dmtot;
-  float* carry;
   float* dw_part;
   float* db_part;
   float* red;  // first-pass row sums of dw_part / db_part
 };
 
-size_t carve_clean_work(char* base, const CleanGeom& g, int64_t tokens, int H, int K, bool gate, CleanWork* out) {
+size_t carve_walk_work(char* base, const WalkGeom& g, int64_t tokens, int H, int K, bool gate, WalkWork* out) {
   Slicer sl{base};
-  CleanWork t{};
-  const size_t sk = (size_t)g.caps * H, bk = (size_t)g.capb * H;
-  t.pseg = sl.take<float>(sk * K * K);
-  t.he_hi = sl.take<uint16_t>(sk * K * K);
-  t.he_lo = sl.take<uint16_t>(sk * K * K);
-  t.sc = sl.take<float>((size_t)tokens * H * 2);
-  t.dmtot = sl.take<float>(bk * K);
-  t.carry = sl.take<float>(bk * K);
+  WalkWork t{};
+  t.sc = sl.take<float>((size_t)tokens * H * 4);
   if (gate) {
-    t.dw_part = sl.take<float>(bk * K);
-    t.db_part = sl.take<float>(bk);
+    t.dw_part = sl.take<float>((size_t)g.ntg * H * K);
+    t.db_part = sl.take<float>((size_t)g.ntg * H);
     t.red = sl.take<float>((size_t)kSumSlices * H * (K + 1));
   }
   if (out) *out = t;
   return sl.off;
 }
 
-void fill_clean_common(CleanArgs& a, const void* q, const void* k, const float* lambda, const float* gate_w,
-                       const float* gate_b, const float* h0, const float* m0, const int64_t* cu, const CleanSaved& sv,
-                       const CleanGeom& g, int T, int H, int N, int pos_off, int subtract_mean) {
-  a.q = q; a.k = k; a.lam = lambda; a.gate_w = gate_w; a.gate_b = gate_b; a.h0 = h0; a.m0 = m0; a.cu = cu;
-  a.blk_idx = sv.blk_idx; a.blk_off = sv.blk_off; a.seg_idx = sv.seg_idx; a.seg_off = sv.seg_off;
-  a.pseg = sv.pseg; a.mseg = sv.mseg; a.hs_hi = sv.hs_hi; a.hs_lo = sv.hs_lo; a.ms = sv.ms;
-  a.T = T; a.H = H; a.N = N; a.NB = g.nb; a.NS = g.ns; a.pos_off = pos_off; a.subtract_mean = subtract_mean ? 1 : 0;
+void fill_walk_common(WalkArgs& a, const void* q, const void* k, const float* gate_w, const float* gate_b,
+                      const float* h0, const float* m0, const int64_t* cu, const WalkSaved& sv, const WalkGeom& g,
+                      int T, int H, int K, int N, int pos_off, int subtract_mean) {
+  a.q = q; a.k = k; a.gate_w = gate_w; a.gate_b = gate_b; a.h0 = h0; a.m0 = subtract_mean ? m0 : nullptr;
+  a.cu = cu; a.chunk_idx = sv.chunk_idx; a.chunk_off = sv.chunk_off;
+  a.z = sv.z; a.srow = sv.srow; a.mpre = sv.mpre;
+  a.T = T; a.H = H; a.N = N; a.NT = g.nt; a.NTG = g.ntg; a.K = K; a.pos_off = pos_off;
+  a.subtract_mean = subtract_mean ? 1 : 0;
 }
 
 }  // namespace
@@ -236,13 +215,13 @@ void fill_clean_common(CleanArgs& a, const void* q, const void* k, const float* 
 extern "C" {
 
 size_t ccq_clean_saved_bytes(int64_t tokens, int B, int T, int N, int H, int K, int varlen) {
-  const CleanGeom g = clean_geom(tokens, B, T, N, varlen != 0);
-  return carve_clean_saved(nullptr, g, N, H, K, varlen != 0, nullptr);
+  const WalkGeom g = walk_geom(tokens, B, T, N, K, varlen != 0);
+  return carve_walk_saved(nullptr, g, tokens, N, H, K, varlen != 0, nullptr);
 }
 
 size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int B, int T, int N, int H, int K, int varlen, int gate) {
-  const CleanGeom g = clean_geom(tokens, B, T, N, varlen != 0);
-  return carve_clean_work(nullptr, g, tokens, H, K, gate != 0, nullptr);
+  const WalkGeom g = walk_geom(tokens, B, T, N, K, varlen != 0);
+  return carve_walk_work(nullptr, g, tokens, H, K, gate != 0, nullptr);
 }
 
 int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
@@ -259,27 +238,20 @@ int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float
     return fail(CCQ_ERR_ALIGN, "ccq_clean_fwd: q, k, saved must be 16-byte aligned");
   const bool varlen = cu_seqlens != nullptr;
   const int64_t tokens = (int64_t)B * T;
-  const CleanGeom g = clean_geom(tokens, B, T, N, varlen);
-  CleanSaved sv;
-  carve_clean_saved((char*)saved, g, N, H, K, varlen, &sv);
+  const WalkGeom g = walk_geom(tokens, B, T, N, K, varlen);
+  WalkSaved sv;
+  carve_walk_saved((char*)saved, g, tokens, N, H, K, varlen, &sv);
   hipStream_t st = (hipStream_t)stream;
   if (varlen) {
-    if (int s = hip_status(launch_chunk_index(cu_seqlens, N, kCleanBlk, sv.blk_off, sv.blk_idx, g.capb, st),
-                           "ccq_clean_fwd(index)"))
-      return s;
-    if (int s = hip_status(launch_chunk_index(cu_seqlens, N, kCleanSeg, sv.seg_off, sv.seg_idx, g.caps, st),
+    if (int s = hip_status(launch_chunk_index(cu_seqlens, N, g.cb, sv.chunk_off, sv.chunk_idx, g.ntg, st),
                            "ccq_clean_fwd(index)"))
       return s;
   }
-  CleanArgs a{};
-  fill_clean_common(a, q, k, lambda, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, N, position_offset,
-                    subtract_mean);
-  a.lam_out = lambda_out; a.qc = q_clean; a.qc32 = q_clean_f32; a.h_fin = h_final; a.m_fin = m_final;
-  if (int s = hip_status(timed("clean_segsum", st, [&] { return launch_clean_stage(kCleanSegsum, a, K, g.caps, g.capb, st); }),
-                         "ccq_clean_fwd(segsum)"))
-    return s;
-  return hip_status(timed("clean_fwd", st, [&] { return launch_clean_stage(kCleanFwd, a, K, g.caps, g.capb, st); }),
-                    "ccq_clean_fwd");
+  WalkArgs a{};
+  fill_walk_common(a, q, k, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, K, N, position_offset, subtract_mean);
+  a.lam = lambda; a.lam_out = lambda_out; a.qc = q_clean; a.qc32 = q_clean_f32; a.h_fin = h_final;
+  a.m_fin = subtract_mean ? m_final : nullptr;
+  return hip_status(timed("clean_fwd", st, [&] { return launch_cwalk(kWalkFwd, a, st); }), "ccq_clean_fwd");
 }
 
 int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
@@ -298,31 +270,28 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
   const bool gate = gate_w != nullptr;
   if (gate && (!gate_b || !dgate_w || !dgate_b))
     return fail(CCQ_ERR_NULL, "ccq_clean_bwd: gate needs gate_b, dgate_w, dgate_b");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(saved) || !aligned16(workspace) ||
+      !aligned16(dq_clean_f32 ? (const void*)dq_clean_f32 : dq_clean))
+    return fail(CCQ_ERR_ALIGN, "ccq_clean_bwd: q, k, saved, workspace, dq_clean must be 16-byte aligned");
   const bool varlen = cu_seqlens != nullptr;
   const int64_t tokens = (int64_t)B * T;
-  const CleanGeom g = clean_geom(tokens, B, T, N, varlen);
-  CleanSaved sv;
-  carve_clean_saved((char*)saved, g, N, H, K, varlen, &sv);
-  CleanWork wk;
-  carve_clean_work((char*)workspace, g, tokens, H, K, gate, &wk);
+  const WalkGeom g = walk_geom(tokens, B, T, N, K, varlen);
+  WalkSaved sv;
+  carve_walk_saved((char*)saved, g, tokens, N, H, K, varlen, &sv);
+  WalkWork wk;
+  carve_walk_work((char*)workspace, g, tokens, H, K, gate, &wk);
   hipStream_t st = (hipStream_t)stream;
-  CleanArgs a{};
-  fill_clean_common(a, q, k, lambda, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, N, position_offset,
-                    subtract_mean);
-  a.pseg = wk.pseg; a.he_hi = wk.he_hi; a.he_lo = wk.he_lo; a.sc = wk.sc; a.dmtot = wk.dmtot; a.carry = wk.carry;
-  a.dw_part = wk.dw_part; a.db_part = wk.db_part;
+  WalkArgs a{};
+  fill_walk_common(a, q, k, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, K, N, position_offset, subtract_mean);
+  a.lam_used = lambda; a.sc = wk.sc; a.dw_part = wk.dw_part; a.db_part = wk.db_part;
   a.dqc32 = dq_clean_f32; a.dqc16 = dq_clean_f32 ? nullptr : dq_clean; a.dk_extra = dk_extra;
   a.dh_fin = dh_final; a.dm_fin = subtract_mean ? dm_final : nullptr;
-  a.dq = dq; a.dq32 = dq_f32; a.dk = dk; a.dk32 = dk_f32; a.dlam = dlambda; a.dh0 = dh0;
+  a.dq = dq; a.dq32 = dq_f32; a.dk = dk; a.dk32 = dk_f32; a.dlam = gate ? nullptr : dlambda; a.dh0 = dh0;
   a.dm0 = subtract_mean ? dm0 : nullptr;
   struct StageName { int stage; const char* name; };
-  const StageName stages[] = {{kCleanBwdDq, "clean_bwd_dq"}, {kCleanBwdScan, "clean_bwd_scan"},
-                              {kCleanBwdDh0, "clean_bwd_dh0"}, {kCleanBwdDk, "clean_bwd_dk"}};
+  const StageName stages[] = {{kWalkRows, "clean_bwd_rows"}, {kWalkDq, "clean_bwd_dq"}, {kWalkDk, "clean_bwd_dk"}};
   for (const StageName& sn : stages) {
-    if (sn.stage == kCleanBwdDh0 && !dh0) continue;
-    if (int s = hip_status(timed(sn.name, st, [&] { return launch_clean_stage(sn.stage, a, K, g.caps, g.capb, st); }),
-                           sn.name))
-      return s;
+    if (int s = hip_status(timed(sn.name, st, [&] { return launch_cwalk(sn.stage, a, st); }), sn.name)) return s;
   }
   if (dm0 && !subtract_mean) {
     if (int s = hip_status(launch_fill_zero(dm0, (long)N * H * K, st), "ccq_clean_bwd(dm0)"))
@@ -331,8 +300,8 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
   if (gate) {
     float* red_b = wk.red + (size_t)kSumSlices * H * K;
     if (int s = hip_status(timed("clean_bwd_gate", st, [&] {
-                             const hipError_t e = launch_sum_rows(wk.dw_part, dgate_w, g.capb, H * K, wk.red, st);
-                             return e != hipSuccess ? e : launch_sum_rows(wk.db_part, dgate_b, g.capb, H, red_b, st);
+                             const hipError_t e = launch_sum_rows(wk.dw_part, dgate_w, g.ntg, H * K, wk.red, st);
+                             return e != hipSuccess ? e : launch_sum_rows(wk.db_part, dgate_b, g.ntg, H, red_b, st);
                            }),
                            "ccq_clean_bwd(dW, db)"))
       return s;

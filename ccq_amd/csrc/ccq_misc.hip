@@ -1,4 +1,5 @@
-// Small HBM-bound kernels: row L2 normalisation (forward/backward) and the varlen chunk index.
+// Small HBM-bound kernels: row L2 normalisation (forward/backward), the varlen chunk index and
+// column sums of partial rows.
 #include "ccq_tile.h"
 #include "ccq_params.h"
 
@@ -104,6 +105,37 @@ hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st) {
 hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
                               hipStream_t st) {
   hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, st, cu, N, size, chunk_off, chunk_idx, cap);
+  return hipGetLastError();
+}
+
+// Sum of partial rows over a slice: out[y * cols + j] = sum_{b in slice y} part[b * cols + j],
+// slice y = rows [y * rps, min(nblk, (y + 1) * rps)).  grid (ceil(cols / 64), slices); 4 groups of 64 threads.
+__global__ __launch_bounds__(kThreads) void ccq_sum_rows_kernel(const float* part, float* out, int nblk, int cols,
+                                                                int rps) {
+  __shared__ float sP[4][64];
+  const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int j = blockIdx.x * 64 + cl;
+  const int b0 = blockIdx.y * rps, b1 = min(nblk, b0 + rps);
+  float s = 0.f;
+  if (j < cols)
+    for (int b = b0 + grp; b < b1; b += 4) s += part[(long)b * cols + j];
+  sP[grp][cl] = s;
+  __syncthreads();
+  if (grp == 0 && j < cols) out[(long)blockIdx.y * cols + j] = sP[0][cl] + sP[1][cl] + sP[2][cl] + sP[3][cl];
+}
+
+// out[j] = sum_b part[b * cols + j]: kSumSlices partial sums into red[kSumSlices * cols], then one pass.
+hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, float* red, hipStream_t st) {
+  if (cols == 0) return hipSuccess;
+  const dim3 gx((cols + 63) / 64);
+  if (nblk <= 4 * kSumSlices || !red) {
+    hipLaunchKernelGGL(ccq_sum_rows_kernel, gx, dim3(kThreads), 0, st, part, out, nblk, cols, nblk);
+    return hipGetLastError();
+  }
+  const int rps = (nblk + kSumSlices - 1) / kSumSlices;
+  const int slices = (nblk + rps - 1) / rps;
+  hipLaunchKernelGGL(ccq_sum_rows_kernel, dim3(gx.x, slices), dim3(kThreads), 0, st, part, red, nblk, cols, rps);
+  hipLaunchKernelGGL(ccq_sum_rows_kernel, gx, dim3(kThreads), 0, st, (const float*)red, out, slices, cols, slices);
   return hipGetLastError();
 }
 

@@ -11,67 +11,8 @@
 
 namespace ccq {
 
-// Cleaning operator, chunk-parallel form.  Tokens are grouped in 32-token blocks and
-// 256-token segments (per sequence).  Buffers (caller-allocated):
-//   pseg [NSEG, H, K, K] fp32   per-segment sum of k k^T (forward) / q dz^T (backward)
-//   mseg [NSEG, H, K]    fp32   per-segment sum of k
-//   hs_hi/hs_lo [NSEG, H, K, K] bf16  state at each segment start, transposed, as a hi/lo pair
-//                                     (forward: h_seg; backward: E = G + G^T after the segment)
-//   ms   [NSEG, H, K]    fp32   key sum at each segment start
-//   sc   [tokens, H, 2]  fp32   (s_t, ds_t) of the backward
-//   dmtot/carry [NBLK, H, K] fp32  per-block sum of dm / sum of dm over later blocks (+ dm_final)
-enum CleanStage { kCleanSegsum = 0, kCleanFwd, kCleanBwdDq, kCleanBwdScan, kCleanBwdDh0, kCleanBwdDk };
-
-// slices of the first pass of the gate-gradient row sums
+// slices of the first pass of the column sums of partial rows (launch_sum_rows)
 constexpr int kSumSlices = 32;
-
-struct CleanArgs {
-  const void* q;            // bf16 [tokens, H, K]
-  const void* k;            // bf16 [tokens, H, K]
-  const float* lam;         // fp32 [tokens, H] (forward: unused when gate_w != nullptr)
-  const float* gate_w;      // fp32 [H, K] (nullable)
-  const float* gate_b;      // fp32 [H]
-  float* lam_out;           // fp32 [tokens, H] gate output (nullable)
-  const float* h0;          // fp32 [N, H, K, K] (nullable)
-  const float* m0;          // fp32 [N, H, K] (nullable)
-  const int64_t* cu;        // [N+1] (nullable)
-  const int* blk_idx;       // varlen: [cap, 2] (sequence, block) of 32-token blocks
-  const int* blk_off;       // varlen: [N+1]
-  const int* seg_idx;       // varlen: [cap, 2] (sequence, segment) of 256-token segments
-  const int* seg_off;       // varlen: [N+1]
-  float* pseg;
-  float* mseg;
-  void* hs_hi;
-  void* hs_lo;
-  float* ms;
-  void* he_hi;              // backward: E after each segment (hi/lo) [NSEG, H, K, K] bf16
-  void* he_lo;
-  // forward outputs
-  void* qc;                 // bf16 (nullable)
-  float* qc32;              // fp32 (nullable)
-  float* h_fin;             // fp32 [N, H, K, K] (nullable)
-  float* m_fin;             // fp32 [N, H, K] (nullable)
-  // backward
-  const float* dqc32;       // fp32 upstream gradient (or dqc16)
-  const void* dqc16;
-  const float* dk_extra;    // fp32 [tokens, H, K] (nullable)
-  const float* dh_fin;      // fp32 [N, H, K, K] (nullable)
-  const float* dm_fin;      // fp32 [N, H, K] (nullable)
-  float* sc;
-  float* dmtot;
-  float* carry;
-  void* dq;
-  float* dq32;
-  void* dk;
-  float* dk32;
-  float* dlam;              // fp32 [tokens, H] (nullable)
-  float* dw_part;           // fp32 [NBLK, H, K] gate partials
-  float* db_part;           // fp32 [NBLK, H]
-  float* dh0;               // fp32 [N, H, K, K] (nullable)
-  float* dm0;               // fp32 [N, H, K] (nullable)
-  int T, H, N, NB, NS;      // NB / NS: blocks / segments per sequence (dense) or capacities (varlen)
-  int pos_off, subtract_mean;
-};
 
 struct L2NormArgs {
   const void* x;            // bf16 [rows, D]
