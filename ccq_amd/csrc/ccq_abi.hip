@@ -182,6 +182,7 @@ size_t carve_walk_saved(char* base, const WalkGeom& g, int64_t tokens, int N, in
 
 struct WalkWork {
   float* sc;
+  float* dmsum;
   float* dw_part;
   float* db_part;
   float* red;  // first-pass row sums of dw_part / db_part
@@ -191,6 +192,7 @@ size_t carve_walk_work(char* base, const WalkGeom& g, int64_t tokens, int H, int
   Slicer sl{base};
   WalkWork t{};
   t.sc = sl.take<float>((size_t)tokens * H * 4);
+  t.dmsum = sl.take<float>((size_t)g.ntg * H * K);
   if (gate) {
     t.dw_part = sl.take<float>((size_t)g.ntg * H * K);
     t.db_part = sl.take<float>((size_t)g.ntg * H);
@@ -283,7 +285,8 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
   hipStream_t st = (hipStream_t)stream;
   WalkArgs a{};
   fill_walk_common(a, q, k, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, K, N, position_offset, subtract_mean);
-  a.lam_used = lambda; a.sc = wk.sc; a.dw_part = wk.dw_part; a.db_part = wk.db_part;
+  a.lam_used = lambda; a.sc = wk.sc; a.dmsum = subtract_mean ? wk.dmsum : nullptr;
+  a.dw_part = wk.dw_part; a.db_part = wk.db_part;
   a.dqc32 = dq_clean_f32; a.dqc16 = dq_clean_f32 ? nullptr : dq_clean; a.dk_extra = dk_extra;
   a.dh_fin = dh_final; a.dm_fin = subtract_mean ? dm_final : nullptr;
   a.dq = dq; a.dq32 = dq_f32; a.dk = dk; a.dk32 = dk_f32; a.dlam = gate ? nullptr : dlambda; a.dh0 = dh0;

@@ -101,14 +101,14 @@ __device__ __forceinline__ void store16(float* p32, bf16* p16, long base, long r
       for (int i = 0; i < 16; ++i) p32[base + acc_drow(i) * rs] = v[i];
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) p16[base + acc_drow(i) * rs] = (bf16)v[i];
+      for (int i = 0; i < 16; ++i) gmem(p16)[base + acc_drow(i) * rs] = (bf16)v[i];
     }
   } else {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       if (r0 + acc_drow(i) < nrows) {
         if (p32) p32[base + acc_drow(i) * rs] = v[i];
-        else p16[base + acc_drow(i) * rs] = (bf16)v[i];
+        else gmem(p16)[base + acc_drow(i) * rs] = (bf16)v[i];
       }
     }
   }
@@ -121,7 +121,7 @@ __device__ __forceinline__ void load16(const float* p32, const bf16* p16, long b
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const long e = base + (long)(r0 + acc_drow(i) < nrows ? r0 + acc_drow(i) : 0) * rs;
-    v[i] = p32 ? p32[e] : (float)p16[e];
+    v[i] = p32 ? p32[e] : (float)gmem(p16)[e];
   }
 }
 
@@ -147,50 +147,57 @@ __device__ __forceinline__ WalkUnit walk_unit(const WalkArgs& a) {
 }
 
 // dz_t = F_t dqc_t for a CB x K chunk (F_t = -lambda_t / pos_t, the first of the four row scalars),
-// prefetched by NTHR threads (local index lt; upstream gradient fp32 or bf16, four elements per
-// slot, rows beyond nvalid read from row 0 and zeroed when stored) and written to LDS as a hi/lo
-// bf16 pair, row-major.
+// prefetched by NTHR threads (local index lt) and written to LDS as a hi/lo bf16 pair, row-major.
+// Thread lt covers rows lt/8 + RP m (RP = NTHR/8) and columns 4 (lt%8) + 32 s: eight lanes read one
+// contiguous 128-byte piece of a row, and a thread needs the row scalar of only CB/RP rows.  The
+// upstream gradient is fp32 or bf16 (four elements per slot).  Rows at or beyond nvalid read row 0
+// (always valid) and are zeroed when stored.
 template <int K, int CB, int NTHR>
 struct PrefetchDzRows {
-  static constexpr int VPR = K / 4, TOT = CB * VPR;
-  static constexpr int N = (TOT + NTHR - 1) / NTHR;
+  static constexpr int RP = NTHR / 8, RPASS = (CB + RP - 1) / RP, CPASS = K / 32, N = RPASS * CPASS;
   f32x4 v[N];
-  float f[N];
+  float f[RPASS];
   __device__ __forceinline__ void load(const float* g32, const bf16* g16, long gstride, const float* sc,
                                        long sstride, int nvalid, int lt) {
+    const int r0 = lt >> 3, c0 = (lt & 7) * 4;
 #pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int idx = min(lt + j * NTHR, TOT - 1);
-      const int r = idx / VPR, c = (idx % VPR) * 4;
-      const long rr = r < nvalid ? r : 0;
-      if (g32) {
-        v[j] = *(const f32x4*)(g32 + rr * gstride + c);
-      } else {
-        const bf16x4 b = *(const bf16x4*)(g16 + rr * gstride + c);
+    for (int m = 0; m < RPASS; ++m) {
+      const int r = r0 + RP * m;
+      const long rr = (r < nvalid && r < CB) ? r : 0;
+      f[m] = sc[rr * sstride];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[j][i] = (float)b[i];
+      for (int s = 0; s < CPASS; ++s) {
+        const long e = rr * gstride + c0 + 32 * s;
+        if (g32) {
+          v[m * CPASS + s] = *(const f32x4*)(g32 + e);
+        } else {
+          const bf16x4 b = *(const bf16x4*)(g16 + e);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[m * CPASS + s][i] = (float)b[i];
+        }
       }
-      f[j] = sc[rr * sstride];
     }
   }
   __device__ __forceinline__ void store(bf16* hi, bf16* lo, int ld, int nvalid, int lt) const {
+    const int r0 = lt >> 3, c0 = (lt & 7) * 4;
 #pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int idx = lt + j * NTHR;
-      if (TOT % NTHR != 0 && idx >= TOT) continue;
-      const int r = idx / VPR, c = (idx % VPR) * 4;
-      f32x4 x = v[j];
-      if (r >= nvalid) x = f32x4{};
-      bf16x4 vh, vl;
+    for (int m = 0; m < RPASS; ++m) {
+      const int r = r0 + RP * m;
+      if (CB % RP != 0 && r >= CB) continue;
+      const float fm = (r < nvalid) ? f[m] : 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        bf16 a, b;
-        split2(x[i] * f[j], a, b);
-        vh[i] = a;
-        vl[i] = b;
+      for (int s = 0; s < CPASS; ++s) {
+        bf16x4 vh, vl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16 a, b;
+          split2(v[m * CPASS + s][i] * fm, a, b);
+          vh[i] = a;
+          vl[i] = b;
+        }
+        *(bf16x4*)(hi + r * ld + c0 + 32 * s) = vh;
+        *(bf16x4*)(lo + r * ld + c0 + 32 * s) = vl;
       }
-      *(bf16x4*)(hi + r * ld + c) = vh;
-      *(bf16x4*)(lo + r * ld + c) = vl;
     }
   }
 };
@@ -498,8 +505,10 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
 //              seg = tid / K (NSEG = 256 / K segments of RPS rows); local prefixes in LDS, segment
 //              offsets (m_prev + totals of earlier segments) applied when read
 //   row dots   thread = (row t = tid / TPR, column part): dqc . z_t and dqc . m_t
-//   scalars    -lambda/pos, ds, dlambda (or dlogit), -s/pos per token; dlambda; gate partials
-//              dW = sum_t dlogit_t q_t (same segment split), db = sum_t dlogit_t
+//   scalars    -lambda/pos, ds, dlambda (or dlogit), -s/pos per token; dlambda
+//   columns    per-chunk sums over t of dm_t = (lambda_t s_t/pos_t^2) dqc_t + ds_t q_t (the dk walk's
+//              carry) and the gate partials dW = sum_t dlogit_t q_t, db = sum_t dlogit_t (segment
+//              split as the key sums)
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
@@ -509,6 +518,7 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
   __shared__ float sOff[NSEG][K];                                // segment offsets of m
   __shared__ float sG[CB];                                       // dlogit_t (gate)
   __shared__ float sW[NSEG][K];                                  // gate partials per segment
+  __shared__ float sD[NSEG][K];                                  // dm column sums per segment
   const int gc = blockIdx.x / a.H, h = blockIdx.x % a.H, tid = threadIdx.x;
   const bool gate = a.gate_w != nullptr, mean = a.subtract_mean != 0;
   int n, c;
@@ -532,12 +542,17 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
   seq_bounds(a.cu, n, a.T, bos, len);
   const int t0 = c * CB, L = min(CB, len - t0);
   const long rs = (long)a.H * K, hb = (bos * a.H + h) * (long)K + (long)t0 * rs;
-  const int col = tid % K, seg = tid / K;  // key-sum / gate-partial role (tid < NSEG * K)
+  const int col = tid % K, seg = tid / K;  // column role (tid < NSEG * K)
 
   // row-dot role: loads first
   const int t = tid / TPR, part = tid % TPR;
   const long e0 = hb + (long)(t < L ? t : 0) * rs + part * PER;
   f32x4 zv[PER / 4], gv[PER / 4];
+  bf16x8 qv8[PER / 8];
+  if (mean) {
+#pragma unroll
+    for (int j = 0; j < PER / 8; ++j) qv8[j] = *(const bf16x8*)((const bf16*)a.q + e0 + 8 * j);
+  }
 #pragma unroll
   for (int j = 0; j < PER / 4; ++j) {
     zv[j] = *(const f32x4*)(a.z + e0 + 4 * j);
@@ -592,47 +607,74 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
   }
   dzd = group_sum(dzd, TPR);
   dmd = group_sum(dmd, TPR);
-  if (part == 0) {
-    float g = 0.f;
-    if (t < L) {
-      const long ti = (bos + t0 + t) * a.H + h;
-      const float lam = a.lam_used[ti];
-      const float p = cw_pos(t0 + t, a.pos_off);
-      const float s = mean ? a.srow[ti] : 0.f;
-      const float dcorr = dzd / p - (mean ? s * dmd / (p * p) : 0.f);  // dqc . corr
-      const float dlam = -dcorr;
-      g = gate ? dlam * lam * (1.f - lam) : dlam;
+  float g = 0.f, am = 0.f, ds = 0.f;
+  if (t < L) {
+    const long ti = (bos + t0 + t) * a.H + h;
+    const float lam = a.lam_used[ti];
+    const float p = cw_pos(t0 + t, a.pos_off);
+    const float s = mean ? a.srow[ti] : 0.f;
+    const float dcorr = dzd / p - (mean ? s * dmd / (p * p) : 0.f);  // dqc . corr
+    const float dlam = -dcorr;
+    g = gate ? dlam * lam * (1.f - lam) : dlam;
+    ds = mean ? lam * dmd / (p * p) : 0.f;
+    am = mean ? lam * s / (p * p) : 0.f;
+    if (part == 0) {
       f32x4 o;
       o[0] = -lam / p;
-      o[1] = mean ? lam * dmd / (p * p) : 0.f;
+      o[1] = ds;
       o[2] = g;
       o[3] = -s / p;
       *(f32x4*)(a.sc + ti * 4) = o;
       if (!gate && a.dlam) a.dlam[ti] = dlam;
     }
-    if (gate) sG[t] = g;
   }
-  if (gate) {
+  if (part == 0 && gate) sG[t] = g;
+  if (mean) {
+    // dm rows over this thread's own region of sMt (no other thread reads it after the dots)
+#pragma unroll
+    for (int j = 0; j < PER / 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int cc = part * PER + 4 * j + i;
+        sMt[t * LDM + cc] = am * gv[j][i] + ds * (float)qv8[j / 2][4 * (j % 2) + i];
+      }
+    }
+  }
+  if (mean || gate) {
     __syncthreads();
     if (tid < NSEG * K) {
-      const bf16* qp = (const bf16*)a.q + hb + col;
-      float qv[RPS];
+      if (mean) {
+        float acc = 0.f;
 #pragma unroll
-      for (int r = 0; r < RPS; ++r) {
-        const int row = seg * RPS + r;
-        qv[r] = (float)qp[(long)(row < L ? row : 0) * rs];
+        for (int r = 0; r < RPS; ++r) acc += sMt[(seg * RPS + r) * LDM + col];  // rows >= L are 0
+        sD[seg][col] = acc;
       }
-      float acc = 0.f;
+      if (gate) {
+        const bf16* qp = (const bf16*)a.q + hb + col;
+        float qv[RPS];
 #pragma unroll
-      for (int r = 0; r < RPS; ++r) acc += sG[seg * RPS + r] * qv[r];  // sG is 0 beyond L
-      sW[seg][col] = acc;
+        for (int r = 0; r < RPS; ++r) {
+          const int row = seg * RPS + r;
+          qv[r] = (float)qp[(long)(row < L ? row : 0) * rs];
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int r = 0; r < RPS; ++r) acc += sG[seg * RPS + r] * qv[r];  // sG is 0 beyond L
+        sW[seg][col] = acc;
+      }
     }
     __syncthreads();
     if (tid < K) {
-      float acc = 0.f;
-      for (int sg = 0; sg < NSEG; ++sg) acc += sW[sg][tid];
-      dwp[tid] = acc;
+      float accd = 0.f, accw = 0.f;
+      for (int sg = 0; sg < NSEG; ++sg) {
+        accd += sD[sg][tid];
+        accw += sW[sg][tid];
+      }
+      if (mean) a.dmsum[((long)gc * a.H + h) * K + tid] = accd;
+      if (gate) dwp[tid] = accw;
     }
+  }
+  if (gate) {
     // db on the first whole wave without a dW column (wave 0 when K == 256)
     constexpr int DBW = K >= kThreads ? 0 : ((K + 63) / 64) * 64;
     if (tid >= DBW && tid < DBW + 64) {
@@ -646,7 +688,8 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
 
 // ===========================================================================
 // cw_dq: grid N*H*(K/32); forward walk of C.  Same roles as cw_fwd (state waves load, output waves
-// store), one LDS buffer and three barriers per chunk:
+// store); for K <= 128 the staged tiles are double-buffered (two barriers per chunk, the stage of the
+// next chunk overlapping the output rows of this one), for K = 256 one buffer and three barriers:
 //   stage    state waves: dZ (hi/lo), K, C[:, cols] (hi/lo), row scalars, key sums
 //   phase 1  score blocks (dZ K^T)^T = K_J dZ_I^T, kept for s <= t
 //   phase 2  output waves: dq rows, then the load of their dqc slice of the next chunk (issued after
@@ -657,16 +700,16 @@ template <int K>
 __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
   using W = Walk<K>;
   constexpr int CB = W::CB, NB = W::NB, NSW = W::NSW, NRT = W::NRT, TPW = W::TPW, LDK = W::LDK, LDA = W::LDA;
-  constexpr int NLT = NSW * 64;
-  __shared__ __attribute__((aligned(16))) bf16 sZh[CB * LDK];  // dz rows, hi
-  __shared__ __attribute__((aligned(16))) bf16 sZl[CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sK[CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sCh[32 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sCl[32 * LDK];
+  constexpr int NLT = NSW * 64, NBUF = K > 128 ? 1 : 2;
+  __shared__ __attribute__((aligned(16))) bf16 sZh_[NBUF][CB * LDK];  // dz rows, hi
+  __shared__ __attribute__((aligned(16))) bf16 sZl_[NBUF][CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sK_[NBUF][CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sCh_[NBUF][32 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sCl_[NBUF][32 * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sAh[CB * LDA];  // dz_t . k_s (s <= t), hi
   __shared__ __attribute__((aligned(16))) bf16 sAl[CB * LDA];
-  __shared__ __attribute__((aligned(16))) f32x4 sR[CB];         // row scalars
-  __shared__ float sMp[32], sWc[32];
+  __shared__ __attribute__((aligned(16))) f32x4 sR_[NBUF][CB];  // row scalars
+  __shared__ float sMp_[NBUF][32], sWc[32];
 
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
   const WalkUnit u = walk_unit<K>(a);
@@ -701,7 +744,14 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
   if (sw >= 0 && u.nc > 0) issue(0);
 
   for (int c = 0; c < u.nc; ++c) {
-    const int t0 = c * CB, L = min(CB, u.len - t0);
+    const int t0 = c * CB, L = min(CB, u.len - t0), b = (NBUF == 2) ? (c & 1) : 0;
+    bf16* sZh = sZh_[b];
+    bf16* sZl = sZl_[b];
+    bf16* sK = sK_[b];
+    bf16* sCh = sCh_[b];
+    bf16* sCl = sCl_[b];
+    f32x4* sR = sR_[b];
+    float* sMp = sMp_[b];
     if (sw >= 0) {
       pz.store(sZh, sZl, LDK, L, lt);
       pk.store(sK, LDK, L, lt);
@@ -786,16 +836,20 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
         }
       }
     }
-    __syncthreads();
+    if (NBUF == 1) __syncthreads();
   }
 }
 
 // ===========================================================================
 // cw_dk: grid N*H*(K/32); reverse walk of E = G + G^T (G = dC_T + sum of q dz^T over later chunks).
+// The in-chunk suffix sums of dm_t = ds_t q_t - (s_t/pos_t) dz_t ride along the score products:
+//   dk_j = K E + sum_{t>=j} (B1[j][t] + ds_t) q_t + sum_{t>=j} (B2[j][t] - s_t/pos_t) dz_t + carry,
+// where the masked diagonal terms enter as their own hi/lo fragments (|s/pos| can exceed |q . k| by
+// orders of magnitude, so they are not added into the score blocks before the split), and
+// carry = dm_T + the per-chunk column sums of dm of the later chunks (from cw_rows).
 // Roles as cw_dq:
-//   stage    state waves: Q, K, dZ (hi/lo), E[:, cols] (hi/lo), row scalars
-//   phase 1  score blocks B1 = dz_t . k_j, B2 = q_t . k_j (t >= j) as [j][t]; wave 3: dm[:, cols]
-//            (transposed hi/lo) and its column totals (carry for the next, earlier chunk)
+//   stage    state waves: Q, K, dZ (hi/lo), E[:, cols] (hi/lo), row scalars, carry update
+//   phase 1  score blocks B1 = dz_t . k_j, B2 = q_t . k_j (t >= j) as [j][t]
 //   phase 2  output waves: dk rows, then the load of their dk_extra slice of the next chunk;
 //            state waves: E += Q^T dZ[:, cols] + dZ^T Q[:, cols] (and G += Q^T dZ[:, cols] when
 //            DH0: dC_0 is requested)
@@ -815,9 +869,8 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sB1l[CB * LDA];
   __shared__ __attribute__((aligned(16))) bf16 sB2h[CB * LDA];  // [j][t] = q_t . k_j (t >= j)
   __shared__ __attribute__((aligned(16))) bf16 sB2l[CB * LDA];
-  __shared__ __attribute__((aligned(16))) bf16 sDh[32 * LDA];   // dm[t][cols] as [col][t]
-  __shared__ __attribute__((aligned(16))) bf16 sDl[32 * LDA];
   __shared__ __attribute__((aligned(16))) f32x4 sR[CB];
+  __shared__ __attribute__((aligned(16))) float sDs[CB], sSp[CB];  // ds_t, -s_t/pos_t
   __shared__ float sCar[2][32];  // sum of dm over later chunks (+ dm_T), by chunk parity
 
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
@@ -837,14 +890,14 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
       E[j] += Tt[j];
     }
   }
-  if (tid < 32) {
-    sCar[0][tid] = (mean && a.dm_fin) ? a.dm_fin[(long)u.unit * K + u.c0 + tid] : 0.f;
-    sCar[1][tid] = 0.f;
-  }
+  // carry lanes: loader threads lt in [64, 96) own column lt - 64 of the carry
+  const bool carl = lt >= 64 && lt < 96;
+  if (carl) sCar[0][lt - 64] = (mean && a.dm_fin) ? a.dm_fin[(long)u.unit * K + u.c0 + lt - 64] : 0.f;
 
   PrefetchRows<K, CB, NLT> pq, pk;
   PrefetchDzRows<K, CB, NLT> pz;
   f32x4 prow;
+  float pdm = 0.f;
   auto issue = [&](int c) {
     const int L = min(CB, u.len - c * CB);
     const long off = u.hb + (long)c * CB * u.rs;
@@ -854,6 +907,7 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
     pz.load(a.dqc32 ? a.dqc32 + off : nullptr, a.dqc32 ? nullptr : (const bf16*)a.dqc16 + off, u.rs,
             a.sc + ti0 * 4, (long)a.H * 4, L, lt);
     if (lt < CB) prow = *(const f32x4*)(a.sc + (ti0 + (long)min(lt, L - 1) * a.H) * 4);
+    if (mean && carl) pdm = a.dmsum[((long)(u.gc0 + c) * a.H + u.h) * K + u.c0 + lt - 64];
   };
   float xcol[16];  // output waves: dk_extra at this lane's (row, column) positions of the current chunk
   const int orow = 32 * w + acc_row(0);
@@ -873,7 +927,13 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
       pq.store(sQ, LDK, L, lt);
       pk.store(sK, LDK, L, lt);
       pz.store(sZh, sZl, LDK, L, lt);
-      if (lt < CB) sR[lt] = (lt < L) ? prow : f32x4{};
+      if (lt < CB) {
+        const f32x4 r = (lt < L) ? prow : f32x4{};
+        sR[lt] = r;
+        sDs[lt] = r[1];
+        sSp[lt] = r[3];
+      }
+      if (carl) sCar[p ^ 1][lt - 64] = sCar[p][lt - 64] + pdm;
 #pragma unroll
       for (int j = 0; j < TPW; ++j) {
         const int rt = sw + NSW * j;
@@ -904,23 +964,6 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
       }
       acc_to_lds_t(b1h, sB1h + J * 32 * LDA, sB1l + J * 32 * LDA, LDA, 32 * T);
       acc_to_lds_t(b2, sB2h + J * 32 * LDA, sB2l + J * 32 * LDA, LDA, 32 * T);
-    } else if (w == 3 && mean) {
-      // dm[t][c] = -(s_t/pos_t) dz_t[c] + ds_t q_t[c]; lane = (column, half of the rows)
-      const int cc = l & 31, half = l >> 5;
-      float tot = 0.f;
-#pragma unroll 4
-      for (int t = half * (CB / 2); t < (half + 1) * (CB / 2); ++t) {
-        const f32x4 r = sR[t];
-        const int e = t * LDK + u.c0 + cc;
-        const float d = r[3] * ((float)sZh[e] + (float)sZl[e]) + r[1] * (float)sQ[e];
-        bf16 hh, ll;
-        split2(d, hh, ll);
-        sDh[cc * LDA + t] = hh;
-        sDl[cc * LDA + t] = ll;
-        tot += d;
-      }
-      tot += __shfl_xor(tot, 32);
-      if (l < 32) sCar[p ^ 1][cc] = sCar[p][cc] + tot;
     }
     __syncthreads();
 
@@ -943,12 +986,31 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
         const bf16x8 zhf = frag_cm(sZh + s0 * LDK + u.c0, LDK);
         const bf16x8 b2h = frag_rm(sB2h + J * 32 * LDA + s0, LDA);
         x = mfma(b2h, zhf, x);
-        x = mfma(b2h, frag_cm(sZl + s0 * LDK + u.c0, LDK), x);
+        const bf16x8 zlf = frag_cm(sZl + s0 * LDK + u.c0, LDK);
+        x = mfma(b2h, zlf, x);
         x = mfma(frag_rm(sB2l + J * 32 * LDA + s0, LDA), zhf, x);
         if (mean) {
-          const bf16x8 tri = frag_triu_ones(32 * J, s0);
-          x = mfma(tri, frag_rm(sDh + s0, LDA), x);
-          x = mfma(tri, frag_rm(sDl + s0, LDA), x);
+          // masked diagonals: (j, t) -> ds_t [t >= j] against q, -s_t/pos_t [t >= j] against dz
+          const int tb = s0 + ((l >> 5) << 3), jr = 32 * J + (l & 31);
+          const f32x4 d0 = *(const f32x4*)(sDs + tb), d1 = *(const f32x4*)(sDs + tb + 4);
+          const f32x4 p0 = *(const f32x4*)(sSp + tb), p1 = *(const f32x4*)(sSp + tb + 4);
+          bf16x8 dh, dl, ph, pl;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const bool keep = tb + i >= jr;
+            bf16 a1, a2, a3, a4;
+            split2(keep ? (i < 4 ? d0[i] : d1[i - 4]) : 0.f, a1, a2);
+            split2(keep ? (i < 4 ? p0[i] : p1[i - 4]) : 0.f, a3, a4);
+            dh[i] = a1;
+            dl[i] = a2;
+            ph[i] = a3;
+            pl[i] = a4;
+          }
+          x = mfma(dh, qf, x);
+          x = mfma(dl, qf, x);
+          x = mfma(ph, zhf, x);
+          x = mfma(ph, zlf, x);
+          x = mfma(pl, zhf, x);
         }
       }
       const float car = sCar[p][acc_col()];
@@ -988,7 +1050,7 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
   }
 
   if constexpr (DH0) store_slice<K>(G, a.dh0 + (long)u.unit * K * K, sw, u.c0);
-  if (a.dm0 && tid < 32) a.dm0[(long)u.unit * K + u.c0 + tid] = mean ? sCar[p][tid] : 0.f;
+  if (a.dm0 && carl) a.dm0[(long)u.unit * K + u.c0 + lt - 64] = mean ? sCar[p][lt - 64] : 0.f;
 }
 
 // ===========================================================================

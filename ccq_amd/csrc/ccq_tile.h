@@ -43,6 +43,17 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Global-memory view of a pointer.  Pointers cast from void* are not always inferred as global, and
+// a flat access also holds the LDS wait counter; spelling the address space keeps global_* code.
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gmem(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+
 __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 

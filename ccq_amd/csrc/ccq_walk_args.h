@@ -49,6 +49,7 @@ struct WalkArgs {
   float* dlam;              // fp32 [tokens, H] (nullable)
   float* dw_part;           // fp32 [NTG, H, K] gate partials
   float* db_part;           // fp32 [NTG, H]
+  float* dmsum;             // fp32 [NTG, H, K] per-chunk column sums of dm (subtract_mean)
   float* dh0;               // fp32 [N, H, K, K] (nullable)
   float* dm0;               // fp32 [N, H, K] (nullable)
   int T, H, N, NT, NTG, K, pos_off, subtract_mean;

@@ -19,6 +19,19 @@ def kern(a: torch.Tensor, b: torch.Tensor) -> float:
     return rel(a, b.detach().to(a.dtype))
 
 
+def faithful_excess(a: torch.Tensor, b: torch.Tensor) -> float:
+    """Largest amount by which an element of the kernel output `a` (bf16) lies further than one bf16
+    ulp from the exact value `b`, relative to the rms of `b`.  Zero when every element is one of the
+    two bf16 neighbours of the exact value (faithful rounding); unlike `kern`, a single near-tie on
+    a large element does not move it."""
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    mag = b.abs().clamp_min(torch.finfo(torch.float32).tiny)
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)  # bf16 keeps 8 significant bits
+    excess = ((a - b).abs() - ulp).clamp_min(0)
+    return float(excess.max() / b.pow(2).mean().sqrt())
+
+
 def bf(x: torch.Tensor) -> torch.Tensor:
     return x.to(torch.bfloat16)
 

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import ccq_oracle as O
-from tests._util import bf, gdn_inputs, kern, l2n, rel
+from tests._util import bf, faithful_excess, gdn_inputs, kern, l2n, rel
 
 pytestmark = pytest.mark.gpu
 
@@ -19,6 +19,9 @@ TOL_BF16 = 2e-3
 # The kernels keep every intermediate at ~16 significant bits, so their output differs from the
 # oracle's rounded to the same dtype only where a rounding flips: held to a quarter of the bar.
 TOL_KERNEL = 5e-4
+# Per element: a bf16 output within one bf16 ulp of the exact value, up to an absolute slack of
+# 1e-4 x rms for elements that are small differences of large terms.
+TOL_FAITHFUL = 1e-4
 
 
 def _cuda():
@@ -109,13 +112,13 @@ def test_clean_fwd_bwd(case):
         errs["dh0"] = rel(h0g.grad, r_dh0)
     if m0 is not None and sub:
         errs["dm0"] = rel(m0g.grad, r_dm0)
-    kerrs = {"dq": kern(qg.grad, r_dq), "dk": kern(kg.grad, r_dk)}
-    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+    kerrs = {"dq": faithful_excess(qg.grad, r_dq), "dk": faithful_excess(kg.grad, r_dk)}
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "faithful excess", {n: f"{e:.2e}" for n, e in kerrs.items()},
           flush=True)
     assert errs["q_clean"] <= TOL_BF16
     assert errs["q_clean_vs_bf16_ref"] <= TOL_KERNEL
     for n, e in kerrs.items():
-        assert e <= TOL_KERNEL, n
+        assert e <= TOL_FAITHFUL, n
     for n in ("dq", "dk"):
         assert errs[n] <= TOL_BF16, n
     for n in ("h_final", "m_final", "dh0", "dm0", "dlam"):  # fp32 outputs
