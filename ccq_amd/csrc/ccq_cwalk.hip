@@ -38,8 +38,6 @@ namespace ccq {
 
 namespace {
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-
 template <int K>
 struct Walk {
   static constexpr int CB = walk_chunk(K);          // tokens per chunk
@@ -67,25 +65,6 @@ __device__ __forceinline__ bf16x8 ones8() {
 // b = 0 -> (0, 0), 1 -> (1, 0), 2 -> (1, 1).
 __device__ __forceinline__ int blk_row(int b) { return b == 0 ? 0 : 1; }
 __device__ __forceinline__ int blk_col(int b) { return b == 2 ? 1 : 0; }
-
-// Write a 32 x 32 fp32 accumulator tile into LDS transposed (element (r, c) at [c * ld + r0 + r]) as
-// a hi/lo pair of bf16 arrays.  Four consecutive rows go out as one 8-byte store.
-__device__ __forceinline__ void acc_to_lds_t(const f32x16& acc, bf16* hi, bf16* lo, int ld, int r0) {
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    bf16x4 vh, vl;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      bf16 a, b;
-      split2(acc[4 * g + i], a, b);
-      vh[i] = a;
-      vl[i] = b;
-    }
-    const int e = acc_col() * ld + r0 + acc_row(4 * g);
-    *(bf16x4*)(hi + e) = vh;
-    *(bf16x4*)(lo + e) = vl;
-  }
-}
 
 // Offset (in rows) of accumulator element i from the lane's first row (acc_row(0)).
 __device__ __forceinline__ constexpr int acc_drow(int i) { return 8 * (i >> 2) + (i & 3); }

@@ -31,6 +31,9 @@ namespace {
 
 constexpr int BT = 64;
 
+// Offset (in rows) of accumulator element i from the lane's first row (acc_row(0)).
+__device__ __forceinline__ constexpr int acc_drow(int i) { return 8 * (i >> 2) + (i & 3); }
+
 struct Carver {
   char* p;
   template <typename T>
@@ -730,6 +733,210 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
 }
 
 // ===========================================================================
+// gdn_bwd_state for K <= 128: same recurrence as gdn_bwd_state_kernel, with every operand staged
+// once per chunk in the form its MFMA reads (hi/lo bf16 pairs, transposed tiles written as 8-byte
+// pieces of four consecutive rows):
+//   stage    P^T (hi/lo), dO^T, scale gamma dO^T (hi/lo), K, Qc^T (hi/lo), w^T, wl^T, dS'^T (hi/lo)
+//   phase A  waves 0, 1: dU rows, -dU^T (hi/lo) to LDS; waves 2, 3: dS' snapshot to HBM
+//   phase B  dS <- gamma_L dS' + Qc^T (scale gamma dO) - w^T dU
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_bwd_state_v2_kernel(const GdnArgs a, const int V) {
+  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, NRT = K / 32, TPW = (NRT + 3) / 4;
+  __shared__ __attribute__((aligned(16))) bf16 sPh[BT * LDB];   // P^T [r][t], hi
+  __shared__ __attribute__((aligned(16))) bf16 sPl[BT * LDB];
+  __shared__ __attribute__((aligned(16))) bf16 sdOT[VB * LDB];  // dO^T [v][t]
+  __shared__ __attribute__((aligned(16))) bf16 sgOh[VB * LDB];  // (scale gamma_t dO)^T, hi
+  __shared__ __attribute__((aligned(16))) bf16 sgOl[VB * LDB];
+  __shared__ __attribute__((aligned(16))) bf16 sK[BT * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sdSh[VB * LDK];  // dS'^T [v][k], hi
+  __shared__ __attribute__((aligned(16))) bf16 sdSl[VB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sdUh[VB * LDB];  // -dU^T [v][t], hi
+  __shared__ __attribute__((aligned(16))) bf16 sdUl[VB * LDB];
+  __shared__ __attribute__((aligned(16))) bf16 sQh[K * LDB];    // Qc^T [k][t], hi
+  __shared__ __attribute__((aligned(16))) bf16 sQl[K * LDB];
+  __shared__ __attribute__((aligned(16))) bf16 sWh[K * LDB];    // w^T [k][t]
+  __shared__ __attribute__((aligned(16))) bf16 sWl[K * LDB];    // wl^T [k][t]
+  __shared__ float sFac[BT], sGL[1];
+
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int nv = V / VB;
+  int unit, vt;
+  xcd_map(blockIdx.x, nv, a.N * a.H, unit, vt);
+  const int n = unit / a.H, h = unit % a.H;
+  long bos;
+  int len;
+  seq_bounds(a.cu, n, a.T, bos, len);
+  const int nc = (len + BT - 1) / BT;
+  const int gc0 = a.cu ? a.chunk_off[n] : n * a.NT;
+  const int v0 = vt * VB;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+
+  f32x16 dS[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    dS[j] = zero16();
+    const int rt = w + 4 * j;
+    if (rt < NRT && a.ds_fin) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        dS[j][i] = a.ds_fin[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()];
+    }
+  }
+
+  PrefetchF32Split<BT, BT> pP;
+  PatchBf16<VB, BT> pO;
+  PrefetchBf16<K, BT> pK;
+  PatchF32<K, BT> pQ;
+  PatchBf16<K, BT> pW, pWl;
+  float gsc[PatchBf16<VB, BT>::N][4];  // scale gamma of the rows of this thread's dO patches
+  float pgl = 0.f, pgt = 0.f;
+  auto issue = [&](int c) {
+    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
+    const long tok0 = bos + c0;
+    pP.load(a.PT + ((long)gc * a.H + h) * (BT * BT), BT, tid);
+    pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L, tid);
+    pK.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L);
+    pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K : nullptr,
+            a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K : nullptr, rsk, L, tid);
+    pW.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L, tid);
+    pWl.load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L, tid);
+#pragma unroll
+    for (int j = 0; j < PatchBf16<VB, BT>::N; ++j) {
+      int rg, cg;
+      PatchBf16<VB, BT>::coords(min(tid + j * kThreads, PatchBf16<VB, BT>::NP - 1), rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * rg + i;
+        gsc[j][i] = a.gcum[(tok0 + (r < L ? r : 0)) * a.H + h];  // exponentiated at the stage
+      }
+    }
+    if (tid < BT) {
+      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
+      pgt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
+    }
+  };
+  if (nc > 0) issue(nc - 1);
+
+  for (int c = nc - 1; c >= 0; --c) {
+    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
+    const long tok0 = bos + c0;
+    // ---- stage
+    pP.store(sPh, sPl, LDB, tid);
+    pO.store_t(sdOT, LDB, L, tid);
+    {
+      float rs[PatchBf16<VB, BT>::N][4];
+#pragma unroll
+      for (int j = 0; j < PatchBf16<VB, BT>::N; ++j) {
+        int rg, cg;
+        PatchBf16<VB, BT>::coords(min(tid + j * kThreads, PatchBf16<VB, BT>::NP - 1), rg, cg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rs[j][i] = (4 * rg + i < L) ? a.scale * __expf(gsc[j][i]) : 0.f;
+      }
+      pO.store_t_scaled(sgOh, sgOl, LDB, rs, tid);
+    }
+    pK.store(sK, LDK, nullptr, 0);
+    pQ.store_t(sQh, sQl, LDB, L, tid);
+    pW.store_t(sWh, LDB, L, tid);
+    pWl.store_t(sWl, LDB, L, tid);
+    if (tid < BT) {
+      sFac[tid] = __expf(pgl - pgt);
+      if (tid == 0) sGL[0] = __expf(pgl);
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) acc_to_lds_t(dS[j], sdSh, sdSl, LDK, rt * 32);
+    }
+    __syncthreads();
+    if (c > 0) issue(c - 1);
+
+    // ---- phase A
+    if (w < 2) {
+      f32x16 acc = zero16(), acc2 = zero16();
+#pragma unroll
+      for (int k0 = 0; k0 < BT; k0 += 16) {
+        const bf16x8 b = frag_rm(sdOT + k0, LDB);
+        acc = mfma(frag_rm(sPh + w * 32 * LDB + k0, LDB), b, acc);
+        acc = mfma(frag_rm(sPl + w * 32 * LDB + k0, LDB), b, acc);
+      }
+#pragma unroll 4
+      for (int k0 = 0; k0 < K; k0 += 16) {
+        const bf16x8 kf = frag_rm(sK + w * 32 * LDK + k0, LDK);
+        acc2 = mfma(kf, frag_rm(sdSh + k0, LDK), acc2);
+        acc2 = mfma(kf, frag_rm(sdSl + k0, LDK), acc2);
+      }
+      const int r0 = w * 32 + acc_row(0);
+      f32x16 du;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = r0 + acc_drow(i);
+        du[i] = (r < L) ? acc[i] + sFac[r] * acc2[i] : 0.f;
+      }
+      float* dug = a.dU + (tok0 + r0) * rsv + (long)h * V + v0 + acc_col();
+      if (r0 + 27 < L) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dug[acc_drow(i) * rsv] = du[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (r0 + acc_drow(i) < L) dug[acc_drow(i) * rsv] = du[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) du[i] = -du[i];
+      acc_to_lds_t(du, sdUh, sdUl, LDB, w * 32);
+    } else {
+      // dS' snapshot (hi/lo) to HBM for gdn_bwd_dqkw
+      constexpr int VPR = K / 8;
+      for (int idx = tid - 128; idx < 2 * VB * VPR; idx += 128) {
+        const int which = idx / (VB * VPR), e = idx % (VB * VPR);
+        const int r = e / VPR, cc = (e % VPR) * 8;
+        const bf16* src = which ? sdSl : sdSh;
+        bf16* dst = which ? (bf16*)a.dhTl : (bf16*)a.dhT;
+        *(bf16x8*)(gmem(dst) + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
+      }
+    }
+    __syncthreads();
+
+    // ---- phase B
+    const float gL = sGL[0];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dS[j][i] *= gL;
+#pragma unroll
+        for (int k0 = 0; k0 < BT; k0 += 16) {
+          const bf16x8 qh = frag_rm(sQh + rt * 32 * LDB + k0, LDB), ql = frag_rm(sQl + rt * 32 * LDB + k0, LDB);
+          const bf16x8 gh = frag_rm(sgOh + k0, LDB), gl = frag_rm(sgOl + k0, LDB);
+          dS[j] = mfma(qh, gh, dS[j]);
+          dS[j] = mfma(qh, gl, dS[j]);
+          dS[j] = mfma(ql, gh, dS[j]);
+          const bf16x8 wh = frag_rm(sWh + rt * 32 * LDB + k0, LDB), wl = frag_rm(sWl + rt * 32 * LDB + k0, LDB);
+          const bf16x8 dh = frag_rm(sdUh + k0, LDB), dl = frag_rm(sdUl + k0, LDB);
+          dS[j] = mfma(wh, dh, dS[j]);
+          dS[j] = mfma(wh, dl, dS[j]);
+          dS[j] = mfma(wl, dh, dS[j]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (a.ds0) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          a.ds0[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()] = dS[j][i];
+      }
+    }
+  }
+}
+
+// ===========================================================================
 // gdn_bwd_dqkw: grid (K/64, NTG, H)
 //   dQi = dO h^T, dKs = U dS'^T, dw = -dU h^T, dP = dO U^T   (contractions over V)
 //   dq = scale gamma dQi + dPs K,  dk = fac dKs + dPs^T Qc,  dPs = dP o scale Gamma (causal)
@@ -1274,7 +1481,11 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       hipLaunchKernelGGL(gdn_fwd_o_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdState:
-      hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+      if (K <= 128)
+        hipLaunchKernelGGL(gdn_bwd_state_v2_kernel<(K <= 128 ? K : 128)>, dim3((V / 32) * a.N * a.H), dim3(kThreads),
+                           0, st, a, V);
+      else
+        hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdDqkw:
       hipLaunchKernelGGL(gdn_bwd_dqkw_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);

@@ -390,6 +390,181 @@ struct PrefetchGrad {
   }
 };
 
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// Write a 32 x 32 fp32 accumulator tile into LDS transposed (element (r, c) at [c * ld + r0 + r]) as
+// a hi/lo pair of bf16 arrays.  Four consecutive rows go out as one 8-byte store.
+__device__ __forceinline__ void acc_to_lds_t(const f32x16& acc, bf16* hi, bf16* lo, int ld, int r0) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    bf16x4 vh, vl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bf16 a, b;
+      split2(acc[4 * g + i], a, b);
+      vh[i] = a;
+      vl[i] = b;
+    }
+    const int e = acc_col() * ld + r0 + acc_row(4 * g);
+    *(bf16x4*)(hi + e) = vh;
+    *(bf16x4*)(lo + e) = vl;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// four-row patch prefetch: a thread holds rows 4 rg .. 4 rg + 3 of one column group, so a
+// transposed copy goes out as 8-byte pieces of four consecutive rows.  Patch p of a thread:
+// rg = p % 4 + 4 (p / (4 CG)), cg = (p / 4) % CG -- four consecutive lanes take four row groups of
+// one column group, so an instruction reads whole rows.  Rows at or beyond nvalid read row 0 and
+// are zeroed when stored.  ROWS must be a multiple of 16.
+// ---------------------------------------------------------------------------
+template <int D, int ROWS, int NTHR = kThreads>
+struct PatchBf16 {
+  static constexpr int RG = ROWS / 4, CG = D / 8, NP = RG * CG, N = (NP + NTHR - 1) / NTHR;
+  bf16x8 v[N][4];
+  __device__ __forceinline__ static void coords(int p, int& rg, int& cg) {
+    rg = (p & 3) + 4 * (p / (4 * CG));
+    cg = (p >> 2) % CG;
+  }
+  __device__ __forceinline__ void load(const bf16* g, long gstride, int nvalid, int lt) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      int rg, cg;
+      coords(min(lt + j * NTHR, NP - 1), rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * rg + i;
+        v[j][i] = *(const bf16x8*)(g + (long)(r < nvalid ? r : 0) * gstride + 8 * cg);
+      }
+    }
+  }
+  // transposed copy: dst_t[c * ldt + r]
+  __device__ __forceinline__ void store_t(bf16* dst_t, int ldt, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int p = lt + j * NTHR;
+      if (NP % NTHR != 0 && p >= NP) continue;
+      int rg, cg;
+      coords(p, rg, cg);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        bf16x4 col;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) col[i] = (4 * rg + i < nvalid) ? v[j][i][c] : (bf16)0.f;
+        *(bf16x4*)(dst_t + (8 * cg + c) * ldt + 4 * rg) = col;
+      }
+    }
+  }
+  // transposed copy of rowscale[i] x value, split into hi/lo
+  __device__ __forceinline__ void store_t_scaled(bf16* hi_t, bf16* lo_t, int ldt, const float (&rowscale)[N][4],
+                                                 int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int p = lt + j * NTHR;
+      if (NP % NTHR != 0 && p >= NP) continue;
+      int rg, cg;
+      coords(p, rg, cg);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        bf16x4 ch, cl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16 a, b;
+          split2(rowscale[j][i] * (float)v[j][i][c], a, b);
+          ch[i] = a;
+          cl[i] = b;
+        }
+        *(bf16x4*)(hi_t + (8 * cg + c) * ldt + 4 * rg) = ch;
+        *(bf16x4*)(lo_t + (8 * cg + c) * ldt + 4 * rg) = cl;
+      }
+    }
+  }
+};
+
+// fp32 (or bf16) rows in four-row patches of 4 columns, stored transposed as a hi/lo bf16 pair.
+template <int D, int ROWS, int NTHR = kThreads>
+struct PatchF32 {
+  static constexpr int RG = ROWS / 4, CG = D / 4, NP = RG * CG, N = (NP + NTHR - 1) / NTHR;
+  f32x4 v[N][4];
+  __device__ __forceinline__ static void coords(int p, int& rg, int& cg) {
+    rg = (p & 3) + 4 * (p / (4 * CG));
+    cg = (p >> 2) % CG;
+  }
+  __device__ __forceinline__ void load(const float* g32, const bf16* g16, long gstride, int nvalid, int lt) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      int rg, cg;
+      coords(min(lt + j * NTHR, NP - 1), rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * rg + i;
+        const long e = (long)(r < nvalid ? r : 0) * gstride + 4 * cg;
+        if (g32) {
+          v[j][i] = *(const f32x4*)(g32 + e);
+        } else {
+          const bf16x4 b = *(const bf16x4*)(g16 + e);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[j][i][k] = (float)b[k];
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ void store_t(bf16* hi_t, bf16* lo_t, int ldt, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int p = lt + j * NTHR;
+      if (NP % NTHR != 0 && p >= NP) continue;
+      int rg, cg;
+      coords(p, rg, cg);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        bf16x4 ch, cl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16 a, b;
+          split2((4 * rg + i < nvalid) ? v[j][i][c] : 0.f, a, b);
+          ch[i] = a;
+          cl[i] = b;
+        }
+        *(bf16x4*)(hi_t + (4 * cg + c) * ldt + 4 * rg) = ch;
+        *(bf16x4*)(lo_t + (4 * cg + c) * ldt + 4 * rg) = cl;
+      }
+    }
+  }
+};
+
+// fp32 rows (ROWS x D, contiguous D) stored row-major as a hi/lo bf16 pair (8-byte pieces).
+template <int D, int ROWS, int NTHR = kThreads>
+struct PrefetchF32Split {
+  static constexpr int VPR = D / 4, TOT = ROWS * VPR, N = (TOT + NTHR - 1) / NTHR;
+  f32x4 v[N];
+  __device__ __forceinline__ void load(const float* g, long gstride, int lt) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = min(lt + j * NTHR, TOT - 1);
+      v[j] = *(const f32x4*)(g + (long)(idx / VPR) * gstride + (idx % VPR) * 4);
+    }
+  }
+  __device__ __forceinline__ void store(bf16* hi, bf16* lo, int ld, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = lt + j * NTHR;
+      if (TOT % NTHR != 0 && idx >= TOT) continue;
+      const int r = idx / VPR, c = (idx % VPR) * 4;
+      bf16x4 vh, vl;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bf16 a, b;
+        split2(v[j][i], a, b);
+        vh[i] = a;
+        vl[i] = b;
+      }
+      *(bf16x4*)(hi + r * ld + c) = vh;
+      *(bf16x4*)(lo + r * ld + c) = vl;
+    }
+  }
+};
+
 // Sum over the 2^log2n consecutive lanes that share a group (butterfly).
 __device__ __forceinline__ float group_sum(float x, int n) {
   for (int m = 1; m < n; m <<= 1) x += __shfl_xor(x, m);
