@@ -418,6 +418,166 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
 }
 
 // ===========================================================================
+// gdn_fwd_state for K <= 128: same walk as gdn_fwd_state_kernel with every operand staged once per
+// chunk in the form its MFMA reads:
+//   stage    w, wl (rows), K^T (four-row patches), u (fp32 rows), S^T (hi/lo)
+//   phase A  waves 0, 1: U = u - w S, (fac U)^T (hi/lo) to LDS; waves 2, 3: state snapshot to HBM
+//   phase B  S <- gamma_L S + K^T diag(fac) U
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_fwd_state_v2_kernel(const GdnArgs a, const int V) {
+  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDV = VB + 4, NRT = K / 32, TPW = (NRT + 3) / 4;
+  __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sWl[BT * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sKT[K * LDB];    // K^T [k][t]
+  __shared__ __attribute__((aligned(16))) bf16 sSh[VB * LDK];   // S^T [v][k], hi
+  __shared__ __attribute__((aligned(16))) bf16 sSl[VB * LDK];
+  __shared__ __attribute__((aligned(16))) float sU[BT * LDV];   // u [t][v]
+  __shared__ __attribute__((aligned(16))) bf16 sUh[VB * LDB];   // (fac U)^T [v][t], hi
+  __shared__ __attribute__((aligned(16))) bf16 sUl[VB * LDB];
+  __shared__ float sFac[BT], sGL[1];
+
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int nv = V / VB;
+  int unit, vt;
+  xcd_map(blockIdx.x, nv, a.N * a.H, unit, vt);
+  const int n = unit / a.H, h = unit % a.H;
+  long bos;
+  int len;
+  seq_bounds(a.cu, n, a.T, bos, len);
+  const int nc = (len + BT - 1) / BT;
+  const int gc0 = a.cu ? a.chunk_off[n] : n * a.NT;
+  const int v0 = vt * VB;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+
+  f32x16 S[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    S[j] = zero16();
+    const int rt = w + 4 * j;
+    if (rt < NRT && a.s0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S[j][i] = a.s0[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()];
+    }
+  }
+
+  PrefetchBf16<K, BT> pw, pwl;
+  PatchBf16<K, BT> pk;
+  PrefetchF32<VB, BT> pu;
+  float pg = 0.f, pgl = 0.f;
+  auto issue = [&](int c) {
+    const int c0 = c * BT, L = min(BT, len - c0);
+    const long tok0 = bos + c0;
+    pw.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L);
+    pwl.load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L);
+    pk.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L, tid);
+    pu.load(a.u + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+    if (tid < BT) {
+      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
+      pg = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
+    }
+  };
+  if (nc > 0) issue(0);
+
+  for (int c = 0; c < nc; ++c) {
+    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
+    const long tok0 = bos + c0;
+    // ---- stage
+    pw.store(sW, LDK, nullptr, 0);
+    pwl.store(sWl, LDK, nullptr, 0);
+    pk.store_t(sKT, LDB, L, tid);
+#pragma unroll
+    for (int j = 0; j < PrefetchF32<VB, BT>::N; ++j) {
+      const int idx = tid + j * kThreads;
+      if (idx < BT * (VB / 4)) *(f32x4*)(sU + (idx / (VB / 4)) * LDV + (idx % (VB / 4)) * 4) = pu.v[j];
+    }
+    if (tid < BT) {
+      sFac[tid] = __expf(pgl - pg);
+      if (tid == 0) sGL[0] = __expf(pgl);
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) acc_to_lds_t(S[j], sSh, sSl, LDK, rt * 32);
+    }
+    __syncthreads();
+    if (c + 1 < nc) issue(c + 1);
+
+    // ---- phase A
+    if (w < 2) {
+      f32x16 acc = zero16();
+      // w S with both operands as hi/lo pairs (lo x lo dropped)
+#pragma unroll 4
+      for (int k0 = 0; k0 < K; k0 += 16) {
+        const bf16x8 wf = frag_rm(sW + w * 32 * LDK + k0, LDK), sh = frag_rm(sSh + k0, LDK);
+        acc = mfma(wf, sh, acc);
+        acc = mfma(wf, frag_rm(sSl + k0, LDK), acc);
+        acc = mfma(frag_rm(sWl + w * 32 * LDK + k0, LDK), sh, acc);
+      }
+      const int r0 = w * 32 + acc_row(0), cc = acc_col();
+      f32x16 us;
+      float uo[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = r0 + acc_drow(i);
+        uo[i] = sU[r * LDV + cc] - acc[i];
+        us[i] = (r < L) ? sFac[r] * uo[i] : 0.f;
+      }
+      float* ug = a.U + (tok0 + r0) * rsv + (long)h * V + v0 + cc;
+      if (r0 + 27 < L) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ug[acc_drow(i) * rsv] = uo[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (r0 + acc_drow(i) < L) ug[acc_drow(i) * rsv] = uo[i];
+      }
+      acc_to_lds_t(us, sUh, sUl, LDB, w * 32);
+    } else {
+      // state snapshot (hi/lo) to HBM for the output kernel and the backward
+      constexpr int VPR = K / 8;
+      for (int idx = tid - 128; idx < 2 * VB * VPR; idx += 128) {
+        const int which = idx / (VB * VPR), e = idx % (VB * VPR);
+        const int r = e / VPR, cc = (e % VPR) * 8;
+        const bf16* src = which ? sSl : sSh;
+        bf16* dst = which ? (bf16*)a.hTl : (bf16*)a.hT;
+        *(bf16x8*)(gmem(dst) + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
+      }
+    }
+    __syncthreads();
+
+    // ---- phase B
+    const float gL = sGL[0];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[j][i] *= gL;
+#pragma unroll
+        for (int k0 = 0; k0 < BT; k0 += 16) {
+          const bf16x8 ka = frag_rm(sKT + rt * 32 * LDB + k0, LDB);
+          S[j] = mfma(ka, frag_rm(sUh + k0, LDB), S[j]);
+          S[j] = mfma(ka, frag_rm(sUl + k0, LDB), S[j]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (a.s_fin) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          a.s_fin[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()] = S[j][i];
+      }
+    }
+  }
+}
+
+// ===========================================================================
 // gdn_fwd_o: grid (NTG, H)
 // ===========================================================================
 template <int K>
@@ -1475,7 +1635,11 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       hipLaunchKernelGGL(gdn_prep_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnFwdState:
-      hipLaunchKernelGGL(gdn_fwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+      if (K <= 128)
+        hipLaunchKernelGGL(gdn_fwd_state_v2_kernel<(K <= 128 ? K : 128)>, dim3((V / 32) * a.N * a.H), dim3(kThreads),
+                           0, st, a, V);
+      else
+        hipLaunchKernelGGL(gdn_fwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnFwdO:
       hipLaunchKernelGGL(gdn_fwd_o_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
