@@ -1341,6 +1341,294 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_kernel(const GdnArgs a,
 }
 
 // ===========================================================================
+// gdn_bwd_dqkw (same grid and results as gdn_bwd_dqkw_kernel) with every operand staged once in
+// the form its MFMA reads: the state tiles h^T, dS'^T arrive as [v][k] rows and are stored [k][v]
+// from four-row patches; U, dU are stored as hi/lo rows; the post phase stores dPs^T, Qc^T, K^T
+// (hi/lo where fp32) and does its row / column reductions over LDS with all threads.
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_v2_kernel(const GdnArgs a, const int V) {
+  constexpr int LDB = 64 + 8, LDE = 64 + 4, TILE = 64 * LDB;
+  constexpr long kLoop = 9L * TILE * 2;
+  constexpr long kPost = 5L * TILE * 2 + 2L * 64 * LDE * 4;
+  constexpr long kBytes = kLoop > kPost ? kLoop : kPost;
+  __shared__ __attribute__((aligned(16))) char region[kBytes];
+  __shared__ __attribute__((aligned(16))) float sG[BT], sGam[BT], sFac[BT], sDG[BT], sTerm[BT], sMisc[8];
+  // loop views
+  bf16* sHk = (bf16*)region;  // h^T tile as [k][v]
+  bf16* sHkl = sHk + TILE;
+  bf16* sDk = sHkl + TILE;     // dS'^T tile as [k][v]
+  bf16* sDkl = sDk + TILE;
+  bf16* sdO = sDkl + TILE;     // dO [t][v]
+  bf16* sUh = sdO + TILE;      // U [t][v]
+  bf16* sUl = sUh + TILE;
+  bf16* sdUh = sUl + TILE;     // dU [t][v]
+  bf16* sdUl = sdUh + TILE;
+  // post views (same region)
+  bf16* sPh = (bf16*)region;   // dPs^T [s][t]
+  bf16* sPl = sPh + TILE;
+  bf16* sQh = sPl + TILE;      // Qc^T [k][t]
+  bf16* sQl = sQh + TILE;
+  bf16* sKt = sQl + TILE;      // K^T [k][t]
+  float* sE = (float*)(sKt + TILE);  // [64][LDE] products for row / column sums
+  float* sPT = sE + 64 * LDE;        // P^T [s][t] (kt == 0)
+
+  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int kt = blockIdx.x, gc = blockIdx.y, h = blockIdx.z;
+  int n, c0, L;
+  long bos;
+  if (!chunk_info(a, gc, n, c0, bos, L)) return;
+  const long tok0 = bos + c0;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  const int k0c = kt * 64;
+  const int tr = (w >> 1) * 32, tc = (w & 1) * 32;
+  const int pr = (w == 0) ? 0 : 32, pc = (w == 2) ? 32 : 0;
+  f32x16 dQi = zero16(), dKs = zero16(), dW = zero16(), dP = zero16();
+  float hds = 0.f;
+
+  PatchBf16<64, 64> pH, pHl, pD, pDl;
+  PrefetchBf16<64, 64> pO;
+  PrefetchF32Split<64, 64> pU, pdU;
+  PatchF32<64, 64> pQ;
+  PatchBf16<64, 64> pK;
+  PrefetchF32<BT, BT> pP;
+  float pgl = 0.f, pgt = 0.f;
+  auto issue_loop = [&](int v0) {
+    const long so = (((long)gc * a.H + h) * V + v0) * K + k0c;
+    pH.load((const bf16*)a.hT + so, K, 64, tid);
+    pHl.load((const bf16*)a.hTl + so, K, 64, tid);
+    pD.load((const bf16*)a.dhT + so, K, 64, tid);
+    pDl.load((const bf16*)a.dhTl + so, K, 64, tid);
+    pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L);
+    pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, tid, L);
+    pdU.load(a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, tid, L);
+  };
+  auto issue_post = [&]() {
+    pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + k0c : nullptr,
+            a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + k0c : nullptr, rsk, L, tid);
+    pK.load((const bf16*)a.k + (tok0 * a.H + h) * K + k0c, rsk, L, tid);
+    if (kt == 0) pP.load(a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT);
+    if (tid < BT) {
+      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
+      pgt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
+    }
+  };
+  issue_loop(0);
+
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    pH.store_t(sHk, LDB, 64, tid);
+    pHl.store_t(sHkl, LDB, 64, tid);
+    pD.store_t(sDk, LDB, 64, tid);
+    pDl.store_t(sDkl, LDB, 64, tid);
+    pO.store(sdO, LDB, nullptr, 0);
+    pU.store(sUh, sUl, LDB, tid, L);
+    pdU.store(sdUh, sdUl, LDB, tid, L);
+    __syncthreads();
+    if (v0 + 64 < V) issue_loop(v0 + 64);
+    else issue_post();
+    {
+      // <h, dS'> over the tile: row k = tid / 4, sixteen v per thread
+      const int kk = tid >> 2, vs = (tid & 3) * 16;
+#pragma unroll
+      for (int q = 0; q < 16; q += 8) {
+        const int e = kk * LDB + vs + q;
+        const bf16x8 x1 = *(const bf16x8*)(sHk + e), x2 = *(const bf16x8*)(sHkl + e);
+        const bf16x8 y1 = *(const bf16x8*)(sDk + e), y2 = *(const bf16x8*)(sDkl + e);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hds += ((float)x1[i] + (float)x2[i]) * ((float)y1[i] + (float)y2[i]);
+      }
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < 64; k0 += 16) {
+      const bf16x8 oa = frag_rm(sdO + tr * LDB + k0, LDB);
+      const bf16x8 hb = frag_rm(sHk + tc * LDB + k0, LDB), hbl = frag_rm(sHkl + tc * LDB + k0, LDB);
+      dQi = mfma(oa, hb, dQi);
+      dQi = mfma(oa, hbl, dQi);
+      const bf16x8 uh = frag_rm(sUh + tr * LDB + k0, LDB), ul = frag_rm(sUl + tr * LDB + k0, LDB);
+      const bf16x8 db = frag_rm(sDk + tc * LDB + k0, LDB), dbl = frag_rm(sDkl + tc * LDB + k0, LDB);
+      dKs = mfma(uh, db, dKs);
+      dKs = mfma(ul, db, dKs);
+      dKs = mfma(uh, dbl, dKs);
+      const bf16x8 dh = frag_rm(sdUh + tr * LDB + k0, LDB), dl = frag_rm(sdUl + tr * LDB + k0, LDB);
+      dW = mfma(dh, hb, dW);
+      dW = mfma(dl, hb, dW);
+      dW = mfma(dh, hbl, dW);
+      if (w < 3) {
+        const bf16x8 pa = frag_rm(sdO + pr * LDB + k0, LDB);
+        dP = mfma(pa, frag_rm(sUh + pc * LDB + k0, LDB), dP);
+        dP = mfma(pa, frag_rm(sUl + pc * LDB + k0, LDB), dP);
+      }
+    }
+    __syncthreads();
+  }
+  hds = group_sum(hds, 64);
+  if (l == 0) sMisc[w] = hds;
+
+  // ---- post stage (the loop ended with a barrier; its tiles are dead)
+  pQ.store_t(sQh, sQl, LDB, L, tid);
+  pK.store_t(sKt, LDB, L, tid);
+  if (kt == 0) {
+#pragma unroll
+    for (int j = 0; j < PrefetchF32<BT, BT>::N; ++j) {
+      const int idx = tid + j * kThreads;
+      if (idx < BT * (BT / 4)) *(f32x4*)(sPT + (idx / (BT / 4)) * LDE + (idx % (BT / 4)) * 4) = pP.v[j];
+    }
+  }
+  if (tid < BT) {
+    sG[tid] = pgt;
+    sGam[tid] = __expf(pgt);
+    sFac[tid] = __expf(pgl - pgt);
+    if (tid == 0) sMisc[4] = __expf(pgl);
+  }
+  __syncthreads();
+
+  // ---- dP: mask, decay terms of P (kt == 0), dPs^T as hi/lo
+  {
+    f32x16 ps;
+    if (w < 3) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = pr + acc_row(i), c = pc + acc_col();
+        const bool keep = r >= c;
+        dP[i] = keep ? dP[i] : 0.f;
+        ps[i] = keep ? dP[i] * a.scale * __expf(sG[r] - sG[c]) : 0.f;
+      }
+      if (kt == 0) {
+        const int c = pc + acc_col();
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int i4 = pr + acc_row(4 * g);
+          const f32x4 pv = *(const f32x4*)(sPT + c * LDE + i4);  // P[i][c] = P^T[c][i]
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) sE[(i4 + ii) * LDE + c] = dP[4 * g + ii] * pv[ii];
+        }
+      }
+      acc_to_lds_t(ps, sPh + pc * LDB, sPl + pc * LDB, LDB, pr);
+    } else {
+      if (kt == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sE[acc_row(i) * LDE + 32 + acc_col()] = 0.f;
+      }
+      acc_to_lds_t(zero16(), sPh + 32 * LDB, sPl + 32 * LDB, LDB, 0);
+    }
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float s = 0.f;
+    if (kt == 0) {
+#pragma unroll
+      for (int q = 0; q < 64; q += 4) {
+        const f32x4 x = *(const f32x4*)(sE + tid * LDE + q);
+        s += x[0] + x[1] + x[2] + x[3];
+      }
+    }
+    sDG[tid] = s;
+  } else if (tid < 128) {
+    float s = 0.f;
+    if (kt == 0) {
+#pragma unroll 8
+      for (int i = 0; i < 64; ++i) s += sE[i * LDE + tid - 64];
+    }
+    sTerm[tid - 64] = s;
+  }
+  __syncthreads();
+
+  // ---- dq tile = scale gamma dQi + dPs K[:, tile]; decay term of O: dG_i += sum_k dQi_ik qc_ik
+  {
+    const int c = tc + acc_col();
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int i4 = tr + acc_row(4 * g);
+      const f32x4 gm = *(const f32x4*)(sGam + i4);
+      const bf16x4 qh4 = *(const bf16x4*)(sQh + c * LDB + i4), ql4 = *(const bf16x4*)(sQl + c * LDB + i4);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int k = 4 * g + ii;
+        dQi[k] *= a.scale * gm[ii];
+        sE[(i4 + ii) * LDE + c] = dQi[k] * ((float)qh4[ii] + (float)ql4[ii]);
+      }
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 kb = frag_rm(sKt + tc * LDB + k0, LDB);
+      dQi = mfma(frag_cm(sPh + k0 * LDB + tr, LDB), kb, dQi);
+      dQi = mfma(frag_cm(sPl + k0 * LDB + tr, LDB), kb, dQi);
+    }
+    const int r0 = tr + acc_row(0);
+    float* dq = a.dq32 + (tok0 + r0) * rsk + (long)h * K + k0c + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (r0 + acc_drow(i) < L) dq[acc_drow(i) * rsk] = dQi[i];
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 64; q += 4) {
+      const f32x4 x = *(const f32x4*)(sE + tid * LDE + q);
+      s += x[0] + x[1] + x[2] + x[3];
+    }
+    sDG[tid] = sDG[tid] - sTerm[tid] + s;
+  }
+  __syncthreads();
+
+  // ---- dk tile = fac dKs + dPs^T Qc[:, tile];  state-update decay term_j = sum_k fac dKs_jk k_jk
+  {
+    const int c = tc + acc_col();
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int i4 = tr + acc_row(4 * g);
+      const f32x4 fc = *(const f32x4*)(sFac + i4);
+      const bf16x4 k4 = *(const bf16x4*)(sKt + c * LDB + i4);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int k = 4 * g + ii;
+        dKs[k] *= fc[ii];
+        sE[(i4 + ii) * LDE + c] = dKs[k] * (float)k4[ii];
+      }
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 ah = frag_rm(sPh + tr * LDB + k0, LDB), al = frag_rm(sPl + tr * LDB + k0, LDB);
+      const bf16x8 bh = frag_rm(sQh + tc * LDB + k0, LDB);
+      dKs = mfma(ah, bh, dKs);
+      dKs = mfma(ah, frag_rm(sQl + tc * LDB + k0, LDB), dKs);
+      dKs = mfma(al, bh, dKs);
+    }
+    const int r0 = tr + acc_row(0);
+    const long gi = (tok0 + r0) * rsk + (long)h * K + k0c + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (r0 + acc_drow(i) < L) {
+        a.dkp32[gi + acc_drow(i) * rsk] = dKs[i];
+        a.dw32[gi + acc_drow(i) * rsk] = -dW[i];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 64; q += 4) {
+      const f32x4 x = *(const f32x4*)(sE + tid * LDE + q);
+      s += x[0] + x[1] + x[2] + x[3];
+    }
+    sTerm[tid] = s;  // term_j
+  }
+  __syncthreads();
+  if (tid < L) {
+    float d = sDG[tid] - sTerm[tid];
+    if (tid == L - 1) {
+      float tot = 0.f;
+      for (int j = 0; j < L; ++j) tot += sTerm[j];
+      d += tot + sMisc[4] * (sMisc[0] + sMisc[1] + sMisc[2] + sMisc[3]);
+    }
+    const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
+    a.dgp[(long)kt * ntok * a.H + (tok0 + tid) * a.H + h] = d;
+  }
+}
+
+// ===========================================================================
 // gdn_bwd_wy: grid (NTG, H)  -- backward through w = T diag(beta gamma) K, u = T diag(beta) V,
 // T = (I + A)^-1, A = strict_lower(diag(beta) (K K^T o Gamma)).
 // ===========================================================================
@@ -1652,7 +1940,7 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
         hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdDqkw:
-      hipLaunchKernelGGL(gdn_bwd_dqkw_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdWy:
       hipLaunchKernelGGL(gdn_bwd_wy_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);

@@ -533,19 +533,21 @@ struct PatchF32 {
   }
 };
 
-// fp32 rows (ROWS x D, contiguous D) stored row-major as a hi/lo bf16 pair (8-byte pieces).
+// fp32 rows (ROWS x D, contiguous D) stored row-major as a hi/lo bf16 pair (8-byte pieces).  Rows at
+// or beyond nvalid read row 0 and are stored as zeros.
 template <int D, int ROWS, int NTHR = kThreads>
 struct PrefetchF32Split {
   static constexpr int VPR = D / 4, TOT = ROWS * VPR, N = (TOT + NTHR - 1) / NTHR;
   f32x4 v[N];
-  __device__ __forceinline__ void load(const float* g, long gstride, int lt) {
+  __device__ __forceinline__ void load(const float* g, long gstride, int lt, int nvalid = ROWS) {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
       const int idx = min(lt + j * NTHR, TOT - 1);
-      v[j] = *(const f32x4*)(g + (long)(idx / VPR) * gstride + (idx % VPR) * 4);
+      const int r = idx / VPR;
+      v[j] = *(const f32x4*)(g + (long)(r < nvalid ? r : 0) * gstride + (idx % VPR) * 4);
     }
   }
-  __device__ __forceinline__ void store(bf16* hi, bf16* lo, int ld, int lt) const {
+  __device__ __forceinline__ void store(bf16* hi, bf16* lo, int ld, int lt, int nvalid = ROWS) const {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
       const int idx = lt + j * NTHR;
@@ -555,7 +557,7 @@ struct PrefetchF32Split {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         bf16 a, b;
-        split2(v[j][i], a, b);
+        split2(r < nvalid ? v[j][i] : 0.f, a, b);
         vh[i] = a;
         vl[i] = b;
       }
