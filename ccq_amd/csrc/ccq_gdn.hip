@@ -34,6 +34,10 @@ constexpr int BT = 64;
 // Offset (in rows) of accumulator element i from the lane's first row (acc_row(0)).
 __device__ __forceinline__ constexpr int acc_drow(int i) { return 8 * (i >> 2) + (i & 3); }
 
+// Lower 32 x 32 block b of a 64 x 64 tile (row block, column block): 0 -> (0,0), 1 -> (1,0), 2 -> (1,1).
+__device__ __forceinline__ int blk_row3(int b) { return b == 0 ? 0 : 1; }
+__device__ __forceinline__ int blk_col3(int b) { return b == 2 ? 1 : 0; }
+
 struct Carver {
   char* p;
   template <typename T>
@@ -1913,6 +1917,330 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, c
 }
 
 // ===========================================================================
+// gdn_bwd_wy (same grid and results as gdn_bwd_wy_kernel) with every operand in the form its MFMA
+// reads.  Products whose transpose is needed later are computed in the transposed orientation and
+// written back transposed (acc_to_lds_t), so all fragments are 16-byte row reads:
+//   phase 1  (dT K-part)^T, (dT V-part)^T over key / value tiles; K K^T
+//   phase 2  M1 = dT T^T -> M1^T;  dA = -T^T M1 and dA^T = -M1^T T in registers
+//   phase 3  dbeta / dG terms of A;  dAs = dA o beta_r Gamma_rc stored as rows and as columns
+//   phase 4  per key tile: dk = dk_part + dAs K + dAs^T K + diag(beta gamma) T^T dw
+//   phase 5  per value tile: dv = diag(beta) T^T dU;  dbeta += (T^T dU) . v
+// Row / column reductions go through LDS and all threads.
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kThreads) void gdn_bwd_wy_v2_kernel(const GdnArgs a, const int V) {
+  constexpr int LDB = 64 + 8, LDE = 64 + 4, TILE = 64 * LDB, FT = 64 * LDE;
+  constexpr long kScr1 = 4L * TILE * 2;                    // phases 1-2: sX hi/lo + sR, then dT, M1^T
+  constexpr long kScr3 = 2L * FT * 4;                      // phase 3: two product tiles
+  constexpr long kScr4 = 3L * TILE * 2 + 2L * FT * 4;      // phase 4: K^T, dw^T hi/lo, dk_part, products
+  constexpr long kScr5 = 3L * TILE * 2 + 1L * FT * 4;      // phase 5: dU^T hi/lo, V, products
+  constexpr long kScr = kScr1 > kScr3 ? (kScr1 > kScr4 ? kScr1 : kScr4) : (kScr3 > kScr4 ? kScr3 : kScr4);
+  static_assert(kScr >= kScr5, "scratch");
+  __shared__ __attribute__((aligned(16))) bf16 sTh[TILE], sTl[TILE];    // T [r][c]
+  __shared__ __attribute__((aligned(16))) bf16 sTth[TILE], sTtl[TILE];  // T^T [r][c] = T[c][r]
+  __shared__ __attribute__((aligned(16))) bf16 sAh[TILE], sAl[TILE];    // dAs [r][c]
+  __shared__ __attribute__((aligned(16))) bf16 sATh[TILE], sATl[TILE];  // dAs^T [c][r]
+  __shared__ __attribute__((aligned(16))) char scr[kScr];
+  __shared__ __attribute__((aligned(16))) float sG[BT], sBeta[BT], sGam[BT], sDB[BT], sDG[BT], sRow[BT], sCol[BT];
+  // phase 1 views
+  bf16* sXh = (bf16*)scr;  // fp32 tile rows [t][c], hi
+  bf16* sXl = sXh + TILE;
+  bf16* sR = sXl + TILE;   // bf16 tile rows [t][c]
+  // phase 2 views
+  bf16* sDh = (bf16*)scr;  // dT [r][c]
+  bf16* sDl = sDh + TILE;
+  bf16* sMh = sDl + TILE;  // M1^T [c][r]
+  bf16* sMl = sMh + TILE;
+  // phase 3 views
+  float* sE1 = (float*)scr;
+  float* sE2 = sE1 + FT;
+  // phase 4 / 5 views
+  bf16* sCt = (bf16*)scr;  // K^T [k][t] (phase 4) / V [t][v] (phase 5)
+  bf16* sFh = sCt + TILE;  // dw^T [k][t] (phase 4) / dU^T [v][t] (phase 5), hi
+  bf16* sFl = sFh + TILE;
+  float* sE = (float*)(sFl + TILE);  // products [t][c]
+  float* sKp = sE + FT;              // dk_part [t][k] (phase 4)
+
+  const int tid = threadIdx.x, w = wave_id();
+  const int gc = blockIdx.x, h = blockIdx.y;
+  int n, c0, L;
+  long bos;
+  if (!chunk_info(a, gc, n, c0, bos, L)) return;
+  const long tok0 = bos + c0;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
+  const int nkt = K / 64, nv = V / 64;
+
+  // jobs (one fp32 tile, one bf16 tile, one more fp32 tile in phase 4), one ahead in registers:
+  // [0, nkt): dw, k   [nkt, nkt+nv): dU, v   [nkt+nv, 2nkt+nv): dw, k, dk_part   then dU, v
+  const int nA = nkt, nB = nkt + nv, nC = 2 * nkt + nv, njobs = 2 * (nkt + nv);
+  PatchF32<64, BT> pF, pF2;
+  PatchBf16<64, BT> pB;
+  auto issue = [&](int j) {
+    const bool kside = j < nA || (j >= nB && j < nC);
+    const int col = 64 * (j < nA ? j : j < nB ? j - nA : j < nC ? j - nB : j - nC);
+    if (kside) {
+      pF.load(a.dw32 + (tok0 * a.H + h) * K + col, nullptr, rsk, L, tid);
+      pB.load((const bf16*)a.k + (tok0 * a.H + h) * K + col, rsk, L, tid);
+      if (j >= nB) pF2.load(a.dkp32 + (tok0 * a.H + h) * K + col, nullptr, rsk, L, tid);
+    } else {
+      pF.load(a.dU + (tok0 * a.H + h) * (long)V + col, nullptr, rsv, L, tid);
+      pB.load((const bf16*)a.v + (tok0 * a.H + h) * (long)V + col, rsv, L, tid);
+    }
+  };
+  issue(0);
+  {
+    PatchF32<BT, BT> pT;
+    pT.load(a.tmat + ((long)gc * a.H + h) * (BT * BT), nullptr, BT, BT, tid);
+    if (tid < BT) {
+      const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
+      const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
+      sG[tid] = gt;
+      sGam[tid] = __expf(gt);
+      sBeta[tid] = (tid < L) ? a.beta[(tok0 + tid) * a.H + h] : 0.f;
+      float dg = 0.f;
+      if (tid < L)
+        for (int kt = 0; kt < nkt; ++kt) dg += a.dgp[(long)kt * ntok * a.H + (tok0 + tid) * a.H + h];
+      sDG[tid] = dg;
+      sDB[tid] = 0.f;
+    }
+    pT.store_rm(sTh, sTl, LDB, BT, tid);
+    pT.store_t(sTth, sTtl, LDB, BT, tid);
+  }
+  int job = 0;
+  const int R = blk_row3(w), C = blk_col3(w);  // lower 32 x 32 block of waves 0..2
+
+  // ---- phase 1
+  f32x16 dTk = zero16(), dTv = zero16(), kk = zero16();
+  for (; job < nB; ++job) {
+    pF.store_rm(sXh, sXl, LDB, L, tid);
+    pB.store_rm(sR, LDB, L, tid);
+    __syncthreads();
+    if (job + 1 < njobs) issue(job + 1);
+    if (w < 3) {
+      const bool kside = job < nA;
+#pragma unroll
+      for (int k0 = 0; k0 < 64; k0 += 16) {
+        const bf16x8 ac = frag_rm(sR + C * 32 * LDB + k0, LDB);  // rows c
+        const bf16x8 bh = frag_rm(sXh + R * 32 * LDB + k0, LDB), bl = frag_rm(sXl + R * 32 * LDB + k0, LDB);
+        if (kside) {
+          dTk = mfma(ac, bh, dTk);
+          dTk = mfma(ac, bl, dTk);
+          kk = mfma(frag_rm(sR + R * 32 * LDB + k0, LDB), ac, kk);  // K K^T, rows r, cols c
+        } else {
+          dTv = mfma(ac, bh, dTv);
+          dTv = mfma(ac, bl, dTv);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // dT (transposed orientation: rows c, cols r), masked r > c, written back as dT [r][c]
+  if (w < 3) {
+    f32x16 d;
+    const int r = R * 32 + acc_col();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = C * 32 + acc_row(i);
+      d[i] = (r > c) ? (dTk[i] * sGam[c] + dTv[i]) * sBeta[c] : 0.f;
+    }
+    acc_to_lds_t(d, sDh + R * 32 * LDB, sDl + R * 32 * LDB, LDB, C * 32);
+  } else {
+    acc_to_lds_t(zero16(), sDh, sDl, LDB, 32);  // dT[0..31][32..63] = 0
+  }
+  __syncthreads();
+
+  // ---- phase 2: M1 = dT T^T (rows r, cols c), masked, stored as M1^T [c][r]
+  if (w < 3) {
+    f32x16 m = zero16();
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 ah = frag_rm(sDh + R * 32 * LDB + k0, LDB), al = frag_rm(sDl + R * 32 * LDB + k0, LDB);
+      const bf16x8 bh = frag_rm(sTh + C * 32 * LDB + k0, LDB);
+      m = mfma(ah, bh, m);
+      m = mfma(ah, frag_rm(sTl + C * 32 * LDB + k0, LDB), m);
+      m = mfma(al, bh, m);
+    }
+    const int c = C * 32 + acc_col();
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (R * 32 + acc_row(i) <= c) m[i] = 0.f;
+    acc_to_lds_t(m, sMh + C * 32 * LDB, sMl + C * 32 * LDB, LDB, R * 32);
+  } else {
+    acc_to_lds_t(zero16(), sMh + 32 * LDB, sMl + 32 * LDB, LDB, 0);  // M1^T[32..63][0..31] = 0
+  }
+  __syncthreads();
+  f32x16 dA = zero16(), dAT = zero16();
+  if (w < 3) {
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 th = frag_rm(sTth + R * 32 * LDB + k0, LDB), tl = frag_rm(sTtl + R * 32 * LDB + k0, LDB);
+      const bf16x8 mh = frag_rm(sMh + C * 32 * LDB + k0, LDB), ml = frag_rm(sMl + C * 32 * LDB + k0, LDB);
+      dA = mfma(th, mh, dA);   // rows r, cols c
+      dA = mfma(th, ml, dA);
+      dA = mfma(tl, mh, dA);
+      dAT = mfma(mh, th, dAT);  // rows c, cols r
+      dAT = mfma(mh, tl, dAT);
+      dAT = mfma(ml, th, dAT);
+    }
+  }
+  __syncthreads();  // scratch (dT, M1^T) is reused below
+
+  // ---- phase 3
+  if (w < 3) {
+    f32x16 ds;
+    const int c = C * 32 + acc_col();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = R * 32 + acc_row(i);
+      const bool keep = r > c;
+      const float gam = keep ? __expf(sG[r] - sG[c]) : 0.f;
+      const float e = keep ? -dA[i] * gam * kk[i] : 0.f;  // dA = -(T^T M1)
+      sE1[r * LDE + c] = e;
+      sE2[r * LDE + c] = sBeta[r] * e;
+      ds[i] = keep ? -dA[i] * sBeta[r] * gam : 0.f;
+    }
+    acc_to_lds_t(ds, sATh + C * 32 * LDB, sATl + C * 32 * LDB, LDB, R * 32);  // dAs^T [c][r]
+    const int r = R * 32 + acc_col();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int cc = C * 32 + acc_row(i);
+      const bool keep = r > cc;
+      ds[i] = keep ? -dAT[i] * sBeta[r] * __expf(sG[r] - sG[cc]) : 0.f;
+    }
+    acc_to_lds_t(ds, sAh + R * 32 * LDB, sAl + R * 32 * LDB, LDB, C * 32);  // dAs [r][c]
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      sE1[acc_row(i) * LDE + 32 + acc_col()] = 0.f;
+      sE2[acc_row(i) * LDE + 32 + acc_col()] = 0.f;
+    }
+    acc_to_lds_t(zero16(), sATh + 32 * LDB, sATl + 32 * LDB, LDB, 0);
+    acc_to_lds_t(zero16(), sAh, sAl, LDB, 32);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 64; q += 4) {
+      const f32x4 x = *(const f32x4*)(sE1 + tid * LDE + q);
+      s += x[0] + x[1] + x[2] + x[3];
+    }
+    sRow[tid] = s;
+  } else if (tid < 128) {
+    float s = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < 64; ++i) s += sE2[i * LDE + tid - 64];
+    sCol[tid - 64] = s;
+  }
+  __syncthreads();
+  if (tid < BT) {
+    sDB[tid] += sRow[tid];
+    sDG[tid] += sBeta[tid] * sRow[tid] - sCol[tid];
+  }
+
+  // ---- phase 4: dk tiles
+  const int tr = (w >> 1) * 32, tc = (w & 1) * 32;
+  for (int kt = 0; kt < nkt; ++kt, ++job) {
+    pB.store_t(sCt, LDB, L, tid);
+    pF.store_t(sFh, sFl, LDB, L, tid);
+    pF2.store_rm_f32(sKp, LDE, L, tid);
+    __syncthreads();
+    if (job + 1 < njobs) issue(job + 1);
+    f32x16 acc = zero16(), acc2 = zero16();
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 kb = frag_rm(sCt + tc * LDB + k0, LDB);
+      acc = mfma(frag_rm(sAh + tr * LDB + k0, LDB), kb, acc);
+      acc = mfma(frag_rm(sAl + tr * LDB + k0, LDB), kb, acc);
+      acc = mfma(frag_rm(sATh + tr * LDB + k0, LDB), kb, acc);
+      acc = mfma(frag_rm(sATl + tr * LDB + k0, LDB), kb, acc);
+      const bf16x8 th = frag_rm(sTth + tr * LDB + k0, LDB);
+      const bf16x8 fh = frag_rm(sFh + tc * LDB + k0, LDB);
+      acc2 = mfma(th, fh, acc2);
+      acc2 = mfma(th, frag_rm(sFl + tc * LDB + k0, LDB), acc2);
+      acc2 = mfma(frag_rm(sTtl + tr * LDB + k0, LDB), fh, acc2);
+    }
+    const int c = tc + acc_col(), r0 = tr + acc_row(0);
+    float* dk = a.dk32 + (tok0 + r0) * rsk + (long)h * K + kt * 64 + c;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int i4 = tr + acc_row(4 * g);
+      const bf16x4 k4 = *(const bf16x4*)(sCt + c * LDB + i4);
+      const f32x4 bg = *(const f32x4*)(sBeta + i4), gm = *(const f32x4*)(sGam + i4);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int kx = 4 * g + ii, r = i4 + ii;
+        sE[r * LDE + c] = acc2[kx] * (float)k4[ii];
+        if (r < L) dk[acc_drow(kx) * rsk] = sKp[r * LDE + c] + acc[kx] + bg[ii] * gm[ii] * acc2[kx];
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < 64; q += 4) {
+        const f32x4 x = *(const f32x4*)(sE + tid * LDE + q);
+        s += x[0] + x[1] + x[2] + x[3];
+      }
+      sDB[tid] += sGam[tid] * s;
+      sDG[tid] += sBeta[tid] * sGam[tid] * s;
+    }
+    __syncthreads();
+  }
+  // ---- phase 5: dv tiles
+  for (int vt = 0; vt < nv; ++vt, ++job) {
+    pB.store_rm(sCt, LDB, L, tid);
+    pF.store_t(sFh, sFl, LDB, L, tid);
+    __syncthreads();
+    if (job + 1 < njobs) issue(job + 1);
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 th = frag_rm(sTth + tr * LDB + k0, LDB);
+      const bf16x8 fh = frag_rm(sFh + tc * LDB + k0, LDB);
+      acc = mfma(th, fh, acc);
+      acc = mfma(th, frag_rm(sFl + tc * LDB + k0, LDB), acc);
+      acc = mfma(frag_rm(sTtl + tr * LDB + k0, LDB), fh, acc);
+    }
+    const int c = tc + acc_col(), r0 = tr + acc_row(0);
+    bf16* dv = (bf16*)a.dv + (tok0 + r0) * rsv + (long)h * V + vt * 64 + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = r0 + acc_drow(i);
+      sE[r * LDE + c] = acc[i] * (float)sCt[r * LDB + c];
+      if (r < L) gmem(dv)[acc_drow(i) * rsv] = (bf16)(sBeta[r] * acc[i]);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < 64; q += 4) {
+        const f32x4 x = *(const f32x4*)(sE + tid * LDE + q);
+        s += x[0] + x[1] + x[2] + x[3];
+      }
+      sDB[tid] += s;
+    }
+    __syncthreads();
+  }
+  // ---- dg = reverse cumulative sum of dG within the chunk; dbeta
+  if (w == 0) {
+    const int ll = lane_id();
+    const int r = BT - 1 - ll;  // reverse order
+    float x = (r < L) ? sDG[r] : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(x, off);
+      if (ll >= off) x += y;
+    }
+    if (r < L) {
+      a.dg[(tok0 + r) * a.H + h] = x;
+      a.dbeta[(tok0 + r) * a.H + h] = sDB[r];
+    }
+  }
+}
+
+// ===========================================================================
 // launchers (one per kernel so the C ABI can time each launch)
 // ===========================================================================
 template <int K>
@@ -1943,7 +2271,7 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdWy:
-      hipLaunchKernelGGL(gdn_bwd_wy_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      hipLaunchKernelGGL(gdn_bwd_wy_v2_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     default:
       return hipErrorInvalidValue;

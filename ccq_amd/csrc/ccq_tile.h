@@ -455,6 +455,22 @@ struct PatchBf16 {
       }
     }
   }
+  // row-major copy: dst[r * ld + c]
+  __device__ __forceinline__ void store_rm(bf16* dst, int ld, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int p = lt + j * NTHR;
+      if (NP % NTHR != 0 && p >= NP) continue;
+      int rg, cg;
+      coords(p, rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bf16x8 x = v[j][i];
+        if (4 * rg + i >= nvalid) x = bf16x8{};
+        *(bf16x8*)(dst + (4 * rg + i) * ld + 8 * cg) = x;
+      }
+    }
+  }
   // transposed copy of rowscale[i] x value, split into hi/lo
   __device__ __forceinline__ void store_t_scaled(bf16* hi_t, bf16* lo_t, int ldt, const float (&rowscale)[N][4],
                                                  int lt) const {
@@ -507,6 +523,41 @@ struct PatchF32 {
           for (int k = 0; k < 4; ++k) v[j][i][k] = (float)b[k];
         }
       }
+    }
+  }
+  // row-major hi/lo copy: hi[r * ld + c], lo[r * ld + c]
+  __device__ __forceinline__ void store_rm(bf16* hi, bf16* lo, int ld, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int p = lt + j * NTHR;
+      if (NP % NTHR != 0 && p >= NP) continue;
+      int rg, cg;
+      coords(p, rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bf16x4 vh, vl;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          bf16 a, b;
+          split2((4 * rg + i < nvalid) ? v[j][i][k] : 0.f, a, b);
+          vh[k] = a;
+          vl[k] = b;
+        }
+        *(bf16x4*)(hi + (4 * rg + i) * ld + 4 * cg) = vh;
+        *(bf16x4*)(lo + (4 * rg + i) * ld + 4 * cg) = vl;
+      }
+    }
+  }
+  // row-major fp32 copy: dst[r * ld + c] (ld a multiple of 4)
+  __device__ __forceinline__ void store_rm_f32(float* dst, int ld, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int p = lt + j * NTHR;
+      if (NP % NTHR != 0 && p >= NP) continue;
+      int rg, cg;
+      coords(p, rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *(f32x4*)(dst + (4 * rg + i) * ld + 4 * cg) = (4 * rg + i < nvalid) ? v[j][i] : f32x4{};
     }
   }
   __device__ __forceinline__ void store_t(bf16* hi_t, bf16* lo_t, int ldt, int nvalid, int lt) const {
