@@ -72,12 +72,16 @@ MULTI_KERNEL_STAGES = ("clean_bwd_gate",)
 # reading for a known-size elementwise copy (fetch x2.000, write x1.000).  Re-measured whenever a
 # kernel changes; a stage absent here reports traffic null.
 MEASURED_TRAFFIC_BYTES = {
-    "gdn_bwd_dqkw": (1493.9e6, 419.4e6),
-    "gdn_bwd_state": (411.4e6, 402.7e6),
-    "gdn_bwd_wy": (958.5e6, 218.1e6),
-    "gdn_fwd_state": (277.0e6, 402.7e6),
-    "gdn_fwd_o": (478.4e6, 134.3e6),
-    "gdn_prep": (151.0e6, 276.8e6),
+    "gdn_bwd_dqkw": (1494.1e6, 419.4e6),
+    "gdn_bwd_state": (478.5e6, 402.7e6),
+    "clean_bwd_dk": (438.8e6, 67.2e6),
+    "gdn_bwd_wy": (972.1e6, 218.1e6),
+    "gdn_fwd_state": (344.1e6, 402.7e6),
+    "clean_fwd": (235.2e6, 287.3e6),
+    "clean_bwd_dq": (237.4e6, 67.9e6),
+    "gdn_fwd_o": (612.6e6, 134.4e6),
+    "gdn_prep": (151.3e6, 343.9e6),
+    "clean_bwd_rows": (491.7e6, 12.8e6),
 }
 
 
