@@ -25,6 +25,8 @@
 #include "ccq_tile.h"
 #include "ccq_params.h"
 
+#include <type_traits>
+
 namespace ccq {
 
 namespace {
@@ -422,26 +424,41 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
 }
 
 // ===========================================================================
-// gdn_fwd_state for K <= 128: same walk as gdn_fwd_state_kernel with every operand staged once per
-// chunk in the form its MFMA reads:
-//   stage    w, wl (rows), K^T (four-row patches), u (fp32 rows), S^T (hi/lo)
-//   phase A  waves 0, 1: U = u - w S, (fac U)^T (hi/lo) to LDS; waves 2, 3: state snapshot to HBM
-//   phase B  S <- gamma_L S + K^T diag(fac) U
+// gdn_fwd_state for K <= 128 with 8 wavefronts: waves 0-3 compute and issue no global access inside
+// the walk; waves 4-7 move memory two chunks ahead of its use.  Per chunk c:
+//   phase A  compute: U = u - w S (16x16 tiles, hi/lo operands), U rows (fp32) and (fac U)^T
+//                     (hi/lo) to LDS
+//            memory:  k of c to LDS (row-major); loads of k(c+2); state snapshot S_c to HBM
+//   phase B  compute: S <- gamma_L S + K^T diag(fac) U (K^T fragments by transposing LDS reads),
+//                     S^T (hi/lo) to LDS for chunk c+1
+//            memory:  w, wl, u, fac of c+1 to LDS; U rows of c to HBM; loads of w, wl, u, g(c+3)
+// LDS pitches: tiles read as mfma16 operands are K + 16 (or 64 + 16) elements wide, which keeps those
+// reads free of bank conflicts; rows are written by 16 consecutive lanes per row.
 // ===========================================================================
+constexpr int kWalk8 = 512;
+
 template <int K>
-__global__ __launch_bounds__(kThreads) void gdn_fwd_state_v2_kernel(const GdnArgs a, const int V) {
-  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDV = VB + 4, NRT = K / 32, TPW = (NRT + 3) / 4;
+__global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs a, const int V) {
+  constexpr int VB = 32, LDK = K + 16, LDB = BT + 16, LDV = VB + 4;
+  constexpr int NM = 256;               // memory threads
+  constexpr int RW = K / 4, NR16 = RW / 16;  // S rows per compute wave, in 16-row tiles
   __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sWl[BT * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sKT[K * LDB];    // K^T [k][t]
+  __shared__ __attribute__((aligned(16))) bf16 sK[BT * LDK];    // k [t][k]
   __shared__ __attribute__((aligned(16))) bf16 sSh[VB * LDK];   // S^T [v][k], hi
   __shared__ __attribute__((aligned(16))) bf16 sSl[VB * LDK];
-  __shared__ __attribute__((aligned(16))) float sU[BT * LDV];   // u [t][v]
   __shared__ __attribute__((aligned(16))) bf16 sUh[VB * LDB];   // (fac U)^T [v][t], hi
   __shared__ __attribute__((aligned(16))) bf16 sUl[VB * LDB];
-  __shared__ float sFac[BT], sGL[1];
+  __shared__ __attribute__((aligned(16))) float sU[BT * LDV];   // u [t][v]
+  __shared__ __attribute__((aligned(16))) float sUo[BT * LDV];  // U [t][v]
+  __shared__ __attribute__((aligned(16))) float sFac[BT];       // exp(g_L - g_t), 0 beyond the chunk
+  __shared__ float sGL[1];
 
-  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  // the wave index as a wave-uniform value: the role branches are then uniform, and the wait
+  // counts of one role's memory operations never merge with the other role's path
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const bool mem = w >= 4;
+  const int lm = tid - NM;
   const int nv = V / VB;
   int unit, vt;
   xcd_map(blockIdx.x, nv, a.N * a.H, unit, vt);
@@ -453,131 +470,192 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_v2_kernel(const GdnArg
   const int gc0 = a.cu ? a.chunk_off[n] : n * a.NT;
   const int v0 = vt * VB;
   const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  auto chunk_len = [&](int c) { return min(BT, len - c * BT); };
+  auto tok_of = [&](int c) { return bos + (long)c * BT; };
 
-  f32x16 S[TPW];
+  // compute waves: state rows [RW w, RW w + RW) x 32 value columns as 16x16 tiles
+  f32x4 S[NR16][2];
 #pragma unroll
-  for (int j = 0; j < TPW; ++j) {
-    S[j] = zero16();
-    const int rt = w + 4 * j;
-    if (rt < NRT && a.s0) {
+  for (int rt = 0; rt < NR16; ++rt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) S[j][i] = a.s0[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()];
-    }
-  }
+    for (int ct = 0; ct < 2; ++ct) S[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  PrefetchBf16<K, BT> pw, pwl;
-  PatchBf16<K, BT> pk;
-  PrefetchF32<VB, BT> pu;
-  float pg = 0.f, pgl = 0.f;
-  auto issue = [&](int c) {
-    const int c0 = c * BT, L = min(BT, len - c0);
-    const long tok0 = bos + c0;
-    pw.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L);
-    pwl.load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L);
-    pk.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L, tid);
-    pu.load(a.u + (tok0 * a.H + h) * (long)V + v0, rsv, L);
-    if (tid < BT) {
-      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
-      pg = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
+  // memory waves: operands two chunks ahead, in two register sets used by chunk parity
+  RowsBf16<K, BT, NM> pw[2], pwl[2], pk[2];
+  RowsF32<VB, BT, NM> pu[2];
+  float pg[2] = {0.f, 0.f};
+  auto load_wug = [&](int c, auto P) {
+    constexpr int p = decltype(P)::value;
+    const int L = chunk_len(c);
+    const long tok0 = tok_of(c);
+    pw[p].load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L, lm);
+    pwl[p].load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L, lm);
+    pu[p].load(a.u + (tok0 * a.H + h) * (long)V + v0, rsv, L, lm);
+    pg[p] = a.gcum[(tok0 + min(lm & (BT - 1), L - 1)) * a.H + h];
+  };
+  auto load_k = [&](int c, auto P) {
+    constexpr int p = decltype(P)::value;
+    pk[p].load((const bf16*)a.k + (tok_of(c) * a.H + h) * K, rsk, chunk_len(c), lm);
+  };
+  // w, wl, u, fac of chunk c to LDS (lane t of every memory wave holds g of token t of the chunk;
+  // wave 4 writes the factors)
+  auto stage_wug = [&](int c, auto P) {
+    constexpr int p = decltype(P)::value;
+    const int L = chunk_len(c);
+    pw[p].store(sW, LDK, L, lm);
+    pwl[p].store(sWl, LDK, L, lm);
+    pu[p].store(sU, LDV, L, lm);
+    const float pgl = __shfl(pg[p], L - 1);
+    const float fac = l < L ? __expf(pgl - pg[p]) : 0.f;
+    if (w == 4) {
+      sFac[l] = fac;
+      if (l == 0) sGL[0] = __expf(pgl);
     }
   };
-  if (nc > 0) issue(0);
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
 
-  for (int c = 0; c < nc; ++c) {
-    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
-    const long tok0 = bos + c0;
-    // ---- stage
-    pw.store(sW, LDK, nullptr, 0);
-    pwl.store(sWl, LDK, nullptr, 0);
-    pk.store_t(sKT, LDB, L, tid);
-#pragma unroll
-    for (int j = 0; j < PrefetchF32<VB, BT>::N; ++j) {
-      const int idx = tid + j * kThreads;
-      if (idx < BT * (VB / 4)) *(f32x4*)(sU + (idx / (VB / 4)) * LDV + (idx % (VB / 4)) * 4) = pu.v[j];
-    }
-    if (tid < BT) {
-      sFac[tid] = __expf(pgl - pg);
-      if (tid == 0) sGL[0] = __expf(pgl);
-    }
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const int rt = w + 4 * j;
-      if (rt < NRT) acc_to_lds_t(S[j], sSh, sSl, LDK, rt * 32);
+  // Each role runs its own loop (both pass the same 1 + 2 nc barriers), so the compiler's wait
+  // counts for the memory waves follow their own sequence of operations only.  Loads are
+  // unconditional (the last chunk again past the end): every pass issues the same memory
+  // operations, so each wait counts exactly the younger ones.
+  if (mem) {
+    const int cl = nc - 1;
+    if (nc > 0) {
+      load_wug(0, P0{});
+      load_k(0, P0{});
+      load_k(min(1, cl), P1{});
+      load_wug(min(1, cl), P1{});
+      stage_wug(0, P0{});
+      load_wug(min(2, cl), P0{});
     }
     __syncthreads();
-    if (c + 1 < nc) issue(c + 1);
-
-    // ---- phase A
-    if (w < 2) {
-      f32x16 acc = zero16();
-      // w S with both operands as hi/lo pairs (lo x lo dropped)
-#pragma unroll 4
-      for (int k0 = 0; k0 < K; k0 += 16) {
-        const bf16x8 wf = frag_rm(sW + w * 32 * LDK + k0, LDK), sh = frag_rm(sSh + k0, LDK);
-        acc = mfma(wf, sh, acc);
-        acc = mfma(wf, frag_rm(sSl + k0, LDK), acc);
-        acc = mfma(frag_rm(sWl + w * 32 * LDK + k0, LDK), sh, acc);
-      }
-      const int r0 = w * 32 + acc_row(0), cc = acc_col();
-      f32x16 us;
-      float uo[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = r0 + acc_drow(i);
-        uo[i] = sU[r * LDV + cc] - acc[i];
-        us[i] = (r < L) ? sFac[r] * uo[i] : 0.f;
-      }
-      float* ug = a.U + (tok0 + r0) * rsv + (long)h * V + v0 + cc;
-      if (r0 + 27 < L) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ug[acc_drow(i) * rsv] = uo[i];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (r0 + acc_drow(i) < L) ug[acc_drow(i) * rsv] = uo[i];
-      }
-      acc_to_lds_t(us, sUh, sUl, LDB, w * 32);
-    } else {
-      // state snapshot (hi/lo) to HBM for the output kernel and the backward
+    // chunk c with register sets P = c % 2 (k) and Q = (c + 1) % 2 (w, wl, u, g)
+    auto chunk = [&](int c, auto P, auto Q) {
+      const int L = chunk_len(c), gc = gc0 + c;
+      const long tok0 = tok_of(c);
+      // ---- phase A: k of c; loads of k(c+2); snapshot S_c
+      pk[decltype(P)::value].store(sK, LDK, L, lm);
+      load_k(min(c + 2, cl), P);
       constexpr int VPR = K / 8;
-      for (int idx = tid - 128; idx < 2 * VB * VPR; idx += 128) {
+#pragma unroll
+      for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
+        const int idx = lm + j * NM;
         const int which = idx / (VB * VPR), e = idx % (VB * VPR);
         const int r = e / VPR, cc = (e % VPR) * 8;
         const bf16* src = which ? sSl : sSh;
         bf16* dst = which ? (bf16*)a.hTl : (bf16*)a.hT;
         *(bf16x8*)(gmem(dst) + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
       }
+      __syncthreads();
+      // ---- phase B: w, wl, u, fac of c+1 first (the wait for their loads then covers no store);
+      // U rows of c to HBM; loads of w, wl, u, g(c+3)
+      stage_wug(min(c + 1, cl), Q);
+#pragma unroll
+      for (int j = 0; j < (BT * VB / 4) / NM; ++j) {
+        const int idx = lm + j * NM, r = idx / (VB / 4), cc = (idx % (VB / 4)) * 4;
+        if (r < L)
+          *(f32x4*)(gmem(a.U) + (tok0 + r) * rsv + (long)h * V + v0 + cc) = *(const f32x4*)(sUo + r * LDV + cc);
+      }
+      load_wug(min(c + 3, cl), Q);
+      __syncthreads();
+    };
+    // pairs of chunks, then the odd one: the loop is entered again only after an odd chunk, so
+    // the register sets hold the same chunks at every pass
+    int c = 0;
+    for (; c + 1 < nc; c += 2) {
+      chunk(c, P0{}, P1{});
+      chunk(c + 1, P1{}, P0{});
+    }
+    if (c < nc) chunk(c, P0{}, P1{});
+    return;
+  }
+
+  // compute waves
+  if (a.s0) {
+#pragma unroll
+    for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          S[rt][ct][i] = a.s0[((long)unit * K + RW * w + 16 * rt + 4 * (l >> 4) + i) * V + v0 + 16 * ct + (l & 15)];
+  }
+#pragma unroll
+  for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) acc16_to_lds_t(S[rt][ct], sSh + 16 * ct * LDK, sSl + 16 * ct * LDK, LDK, RW * w + 16 * rt);
+  __syncthreads();
+  for (int c = 0; c < nc; ++c) {
+    // ---- phase A: U = u - w S with both operands as hi/lo pairs (lo x lo dropped)
+    const float gL = sGL[0];
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      const bf16x8 wh = frag16_rm(sW + 16 * w * LDK + k0, LDK), wl = frag16_rm(sWl + 16 * w * LDK + k0, LDK);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x8 sh = frag16_rm(sSh + 16 * ct * LDK + k0, LDK);
+        acc[ct] = mfma16(wh, sh, acc[ct]);
+        acc[ct] = mfma16(wh, frag16_rm(sSl + 16 * ct * LDK + k0, LDK), acc[ct]);
+        acc[ct] = mfma16(wl, sh, acc[ct]);
+      }
+    }
+    // rows beyond the chunk hold u = 0 and w = 0, so U = 0 there and fac = 0 keeps it out of S
+    const int rb = 16 * w + 4 * (l >> 4);
+    const f32x4 fac = *(const f32x4*)(sFac + rb);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int cc = 16 * ct + (l & 15);
+      f32x4 us;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float uo = sU[(rb + i) * LDV + cc] - acc[ct][i];
+        sUo[(rb + i) * LDV + cc] = uo;
+        us[i] = fac[i] * uo;
+      }
+      acc16_to_lds_t(us, sUh + 16 * ct * LDB, sUl + 16 * ct * LDB, LDB, 16 * w);
     }
     __syncthreads();
 
-    // ---- phase B
-    const float gL = sGL[0];
+    // ---- phase B: S <- gamma_L S + K^T (fac U); S^T (hi/lo) for the next chunk
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const int rt = w + 4 * j;
-      if (rt < NRT) {
+    for (int rt = 0; rt < NR16; ++rt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) S[j][i] *= gL;
+      for (int ct = 0; ct < 2; ++ct) S[rt][ct] *= gL;
 #pragma unroll
-        for (int k0 = 0; k0 < BT; k0 += 16) {
-          const bf16x8 ka = frag_rm(sKT + rt * 32 * LDB + k0, LDB);
-          S[j] = mfma(ka, frag_rm(sUh + k0, LDB), S[j]);
-          S[j] = mfma(ka, frag_rm(sUl + k0, LDB), S[j]);
+    for (int k0 = 0; k0 < BT; k0 += 32) {
+      bf16x8 uh[2], ul[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        uh[ct] = frag16_rm(sUh + 16 * ct * LDB + k0, LDB);
+        ul[ct] = frag16_rm(sUl + 16 * ct * LDB + k0, LDB);
+      }
+#pragma unroll
+      for (int rt = 0; rt < NR16; ++rt) {
+        const bf16x8 ka = frag16_tr(sK + k0 * LDK + RW * w + 16 * rt, LDK);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          S[rt][ct] = mfma16(ka, uh[ct], S[rt][ct]);
+          S[rt][ct] = mfma16(ka, ul[ct], S[rt][ct]);
         }
       }
     }
+#pragma unroll
+    for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        acc16_to_lds_t(S[rt][ct], sSh + 16 * ct * LDK, sSl + 16 * ct * LDK, LDK, RW * w + 16 * rt);
     __syncthreads();
   }
   if (a.s_fin) {
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const int rt = w + 4 * j;
-      if (rt < NRT) {
+    for (int rt = 0; rt < NR16; ++rt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          a.s_fin[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()] = S[j][i];
-      }
-    }
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          a.s_fin[((long)unit * K + RW * w + 16 * rt + 4 * (l >> 4) + i) * V + v0 + 16 * ct + (l & 15)] = S[rt][ct][i];
   }
 }
 
@@ -2252,7 +2330,7 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       break;
     case kGdnFwdState:
       if (K <= 128)
-        hipLaunchKernelGGL(gdn_fwd_state_v2_kernel<(K <= 128 ? K : 128)>, dim3((V / 32) * a.N * a.H), dim3(kThreads),
+        hipLaunchKernelGGL(gdn_fwd_state_v3_kernel<(K <= 128 ? K : 128)>, dim3((V / 32) * a.N * a.H), dim3(kWalk8),
                            0, st, a, V);
       else
         hipLaunchKernelGGL(gdn_fwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);

@@ -43,6 +43,14 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// 16x16 output tiles with v_mfma_f32_16x16x32_bf16:
+//   A (16 x 32):  lane l holds row l%16, k = 8*(l/16) .. +7
+//   B (32 x 16):  lane l holds col l%16, k = 8*(l/16) .. +7
+//   C (16 x 16):  lane l holds col l%16, rows 4*(l/16) + i for i = 0..3
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 // Global-memory view of a pointer.  Pointers cast from void* are not always inferred as global, and
 // a flat access also holds the LDS wait counter; spelling the address space keeps global_* code.
 template <class T>
@@ -70,6 +78,26 @@ __device__ __forceinline__ void split2(float x, bf16& hi, bf16& lo) {
 __device__ __forceinline__ bf16x8 frag_rm(const bf16* p, int ld) {
   const int l = lane_id();
   return *(const bf16x8*)(p + (l & 31) * ld + ((l >> 5) << 3));
+}
+
+// 16x32 operand of mfma16, element (r, k) at p[r * ld + k] (one 16-byte read).
+__device__ __forceinline__ bf16x8 frag16_rm(const bf16* p, int ld) {
+  const int l = lane_id();
+  return *(const bf16x8*)(p + (l & 15) * ld + ((l >> 4) << 3));
+}
+
+// 16x32 operand of mfma16 whose contraction index runs down the rows of a row-major tile: element
+// (r, k) at p[k * ld + r].  Two transposing LDS reads (ds_read_b64_tr_b16): in each 16-lane group,
+// lane j names the 8-byte piece at row (j >> 2), columns 4 (j & 3) .. +3 of a 4 x 16 block, and lane
+// i receives column i of the block -- four consecutive contraction elements of operand row i.
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 frag16_tr(const bf16* p, int ld) {
+  const int l = lane_id(), j = l & 15;
+  const bf16* q = p + (8 * (l >> 4) + (j >> 2)) * ld + 4 * (j & 3);
+  typedef __attribute__((address_space(3))) bf16x4_t lds_b4;
+  const bf16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)q);
+  const bf16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)(q + 4 * ld));
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
 // Element (r, k) at p[k * ld + r]  (operand stored transposed: eight 2-byte reads).
@@ -411,6 +439,21 @@ __device__ __forceinline__ void acc_to_lds_t(const f32x16& acc, bf16* hi, bf16* 
   }
 }
 
+// Same for a 16 x 16 tile of mfma16 (element (r, c) at [c * ld + r0 + r]).
+__device__ __forceinline__ void acc16_to_lds_t(const f32x4& acc, bf16* hi, bf16* lo, int ld, int r0) {
+  bf16x4 vh, vl;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bf16 a, b;
+    split2(acc[i], a, b);
+    vh[i] = a;
+    vl[i] = b;
+  }
+  const int e = (lane_id() & 15) * ld + r0 + 4 * (lane_id() >> 4);
+  *(bf16x4*)(hi + e) = vh;
+  *(bf16x4*)(lo + e) = vl;
+}
+
 // ---------------------------------------------------------------------------
 // four-row patch prefetch: a thread holds rows 4 rg .. 4 rg + 3 of one column group, so a
 // transposed copy goes out as 8-byte pieces of four consecutive rows.  Patch p of a thread:
@@ -614,6 +657,54 @@ struct PrefetchF32Split {
       }
       *(bf16x4*)(hi + r * ld + c) = vh;
       *(bf16x4*)(lo + r * ld + c) = vl;
+    }
+  }
+};
+
+// Row-major register prefetch of a ROWS x D tile (bf16 or fp32) by NTHR threads: 16 consecutive
+// lanes cover one 256-byte row segment, so the global loads are whole rows and the LDS writes are
+// free of bank conflicts at any row pitch.  Rows at or beyond nvalid read row 0 and are stored as
+// zeros; every load is issued unconditionally.
+template <int D, int ROWS, int NTHR>
+struct RowsBf16 {
+  static constexpr int VPR = D / 8, TOT = ROWS * VPR, N = (TOT + NTHR - 1) / NTHR;
+  bf16x8 v[N];
+  __device__ __forceinline__ void load(const bf16* g, long gstride, int nvalid, int lt) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = min(lt + j * NTHR, TOT - 1), r = idx / VPR;
+      v[j] = *gmem((const bf16x8*)(g + (long)(r < nvalid ? r : 0) * gstride + (idx % VPR) * 8));
+    }
+  }
+  __device__ __forceinline__ void store(bf16* dst, int ld, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = lt + j * NTHR;
+      if (TOT % NTHR != 0 && idx >= TOT) continue;
+      const int r = idx / VPR;
+      *(bf16x8*)(dst + r * ld + (idx % VPR) * 8) = r < nvalid ? v[j] : bf16x8{};
+    }
+  }
+};
+
+template <int D, int ROWS, int NTHR>
+struct RowsF32 {
+  static constexpr int VPR = D / 4, TOT = ROWS * VPR, N = (TOT + NTHR - 1) / NTHR;
+  f32x4 v[N];
+  __device__ __forceinline__ void load(const float* g, long gstride, int nvalid, int lt) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = min(lt + j * NTHR, TOT - 1), r = idx / VPR;
+      v[j] = *gmem((const f32x4*)(g + (long)(r < nvalid ? r : 0) * gstride + (idx % VPR) * 4));
+    }
+  }
+  __device__ __forceinline__ void store(float* dst, int ld, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = lt + j * NTHR;
+      if (TOT % NTHR != 0 && idx >= TOT) continue;
+      const int r = idx / VPR;
+      *(f32x4*)(dst + r * ld + (idx % VPR) * 4) = r < nvalid ? v[j] : f32x4{};
     }
   }
 };
