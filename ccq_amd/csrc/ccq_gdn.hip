@@ -975,33 +975,44 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
 }
 
 // ===========================================================================
-// gdn_bwd_state for K <= 128: same recurrence as gdn_bwd_state_kernel, with every operand staged
-// once per chunk in the form its MFMA reads (hi/lo bf16 pairs, transposed tiles written as 8-byte
-// pieces of four consecutive rows):
-//   stage    P^T (hi/lo), dO^T, scale gamma dO^T (hi/lo), K, Qc^T (hi/lo), w^T, wl^T, dS'^T (hi/lo)
-//   phase A  waves 0, 1: dU rows, -dU^T (hi/lo) to LDS; waves 2, 3: dS' snapshot to HBM
-//   phase B  dS <- gamma_L dS' + Qc^T (scale gamma dO) - w^T dU
+// gdn_bwd_state for K <= 128 with 8 wavefronts (reverse walk over chunks).  Waves 0-3 compute and
+// load nothing inside the walk; waves 4-7 move memory.  Per chunk c (dS' = gradient of the state
+// after chunk c):
+//   phase A  compute: dU = P^T dO + fac (K dS') (16x16 tiles), dU rows to HBM, -dU^T (hi/lo) to LDS
+//            memory:  Qc, scale gamma dO (hi/lo), w, wl of c to LDS (row-major); loads of Qc, w, wl
+//                     of c-1; dS' snapshot to HBM
+//   phase B  compute: dS <- gamma_L dS' + Qc^T (scale gamma dO) - w^T dU (Qc^T, w^T and the dO
+//                     operand by transposing LDS reads), dS^T (hi/lo) to LDS for chunk c-1
+//            memory:  P^T, dO, k, fac of c-1 to LDS; loads of P^T, dO, k, g of c-2
 // ===========================================================================
-template <int K>
-__global__ __launch_bounds__(kThreads) void gdn_bwd_state_v2_kernel(const GdnArgs a, const int V) {
-  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, NRT = K / 32, TPW = (NRT + 3) / 4;
-  __shared__ __attribute__((aligned(16))) bf16 sPh[BT * LDB];   // P^T [r][t], hi
-  __shared__ __attribute__((aligned(16))) bf16 sPl[BT * LDB];
-  __shared__ __attribute__((aligned(16))) bf16 sdOT[VB * LDB];  // dO^T [v][t]
-  __shared__ __attribute__((aligned(16))) bf16 sgOh[VB * LDB];  // (scale gamma_t dO)^T, hi
-  __shared__ __attribute__((aligned(16))) bf16 sgOl[VB * LDB];
-  __shared__ __attribute__((aligned(16))) bf16 sK[BT * LDK];
+// Q32: the cleaned query arrives in fp32 (else bf16); a template parameter, so the memory loop has
+// a single path.
+template <int K, bool Q32>
+__global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs a, const int V) {
+  constexpr int VB = 32, LDK = K + 16, LDP = BT + 16, LDO = VB + 16;
+  constexpr int NM = 256;
+  constexpr int RW = K / 4, NR16 = RW / 16;
+  __shared__ __attribute__((aligned(16))) bf16 sPh[BT * LDP];   // P^T [r][t], hi
+  __shared__ __attribute__((aligned(16))) bf16 sPl[BT * LDP];
+  __shared__ __attribute__((aligned(16))) bf16 sdO[BT * LDO];   // dO [t][v]
+  __shared__ __attribute__((aligned(16))) bf16 sgOh[BT * LDO];  // scale gamma_t dO [t][v], hi
+  __shared__ __attribute__((aligned(16))) bf16 sgOl[BT * LDO];
+  __shared__ __attribute__((aligned(16))) bf16 sK[BT * LDK];    // k [t][k]
   __shared__ __attribute__((aligned(16))) bf16 sdSh[VB * LDK];  // dS'^T [v][k], hi
   __shared__ __attribute__((aligned(16))) bf16 sdSl[VB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sdUh[VB * LDB];  // -dU^T [v][t], hi
-  __shared__ __attribute__((aligned(16))) bf16 sdUl[VB * LDB];
-  __shared__ __attribute__((aligned(16))) bf16 sQh[K * LDB];    // Qc^T [k][t], hi
-  __shared__ __attribute__((aligned(16))) bf16 sQl[K * LDB];
-  __shared__ __attribute__((aligned(16))) bf16 sWh[K * LDB];    // w^T [k][t]
-  __shared__ __attribute__((aligned(16))) bf16 sWl[K * LDB];    // wl^T [k][t]
-  __shared__ float sFac[BT], sGL[1];
+  __shared__ __attribute__((aligned(16))) bf16 sdUh[VB * LDP];  // -dU^T [v][t], hi
+  __shared__ __attribute__((aligned(16))) bf16 sdUl[VB * LDP];
+  __shared__ __attribute__((aligned(16))) bf16 sQh[BT * LDK];   // Qc [t][k], hi
+  __shared__ __attribute__((aligned(16))) bf16 sQl[BT * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];    // w [t][k]
+  __shared__ __attribute__((aligned(16))) bf16 sWl[BT * LDK];
+  __shared__ __attribute__((aligned(16))) float sFac[BT];    // exp(g_L - g_t), 0 beyond the chunk
+  __shared__ __attribute__((aligned(16))) float sGam[BT];    // scale exp(g_t), 0 beyond the chunk
+  __shared__ float sGL[1];
 
-  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const bool mem = w >= 4;
+  const int lm = tid - NM;
   const int nv = V / VB;
   int unit, vt;
   xcd_map(blockIdx.x, nv, a.N * a.H, unit, vt);
@@ -1013,168 +1024,213 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_v2_kernel(const GdnArg
   const int gc0 = a.cu ? a.chunk_off[n] : n * a.NT;
   const int v0 = vt * VB;
   const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  auto chunk_len = [&](int c) { return min(BT, len - c * BT); };
+  auto tok_of = [&](int c) { return bos + (long)c * BT; };
 
-  f32x16 dS[TPW];
-#pragma unroll
-  for (int j = 0; j < TPW; ++j) {
-    dS[j] = zero16();
-    const int rt = w + 4 * j;
-    if (rt < NRT && a.ds_fin) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        dS[j][i] = a.ds_fin[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()];
-    }
-  }
-
-  PrefetchF32Split<BT, BT> pP;
-  PatchBf16<VB, BT> pO;
-  PrefetchBf16<K, BT> pK;
-  PatchF32<K, BT> pQ;
-  PatchBf16<K, BT> pW, pWl;
-  float gsc[PatchBf16<VB, BT>::N][4];  // scale gamma of the rows of this thread's dO patches
-  float pgl = 0.f, pgt = 0.f;
-  auto issue = [&](int c) {
-    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
-    const long tok0 = bos + c0;
-    pP.load(a.PT + ((long)gc * a.H + h) * (BT * BT), BT, tid);
-    pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L, tid);
-    pK.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L);
-    pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K : nullptr,
-            a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K : nullptr, rsk, L, tid);
-    pW.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L, tid);
-    pWl.load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L, tid);
-#pragma unroll
-    for (int j = 0; j < PatchBf16<VB, BT>::N; ++j) {
-      int rg, cg;
-      PatchBf16<VB, BT>::coords(min(tid + j * kThreads, PatchBf16<VB, BT>::NP - 1), rg, cg);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * rg + i;
-        gsc[j][i] = a.gcum[(tok0 + (r < L ? r : 0)) * a.H + h];  // exponentiated at the stage
+  if (mem) {
+    // operands of phase B (Qc, w, wl: chunk c) and of phase A (P^T, dO, k, g: chunk c-1)
+    RowsF32<K, BT, NM> pq;
+    RowsBf16<K, BT, NM> pw, pwl, pk;
+    RowsF32<BT, BT, NM> pp;
+    RowsBf16<VB, BT, NM> po;
+    float pgt = 0.f;  // g of token lm % 64
+    auto load_b = [&](int c) {
+      const long tok0 = tok_of(c);
+      const int L = chunk_len(c);
+      if constexpr (Q32)
+        pq.load(a.qc32 + (tok0 * a.H + h) * K, rsk, L, lm);
+      else
+        pq.load(nullptr, (const bf16*)a.qc16 + (tok0 * a.H + h) * K, rsk, L, lm);
+      pw.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L, lm);
+      pwl.load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L, lm);
+    };
+    auto load_a = [&](int c) {
+      const long tok0 = tok_of(c);
+      const int L = chunk_len(c);
+      pp.load(a.PT + ((long)(gc0 + c) * a.H + h) * (BT * BT), BT, BT, lm);
+      po.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L, lm);
+      pk.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L, lm);
+      pgt = a.gcum[(tok0 + min(lm & (BT - 1), L - 1)) * a.H + h];
+    };
+    // phase-A tiles of chunk c: P^T (hi/lo), dO, k; fac, gamma (lane t of wave 4)
+    auto stage_a = [&](int c) {
+      const int L = chunk_len(c);
+      pp.store_split(sPh, sPl, LDP, BT, lm);
+      po.store(sdO, LDO, L, lm);
+      pk.store(sK, LDK, L, lm);
+      const float pgl = __shfl(pgt, L - 1);
+      const float fac = l < L ? __expf(pgl - pgt) : 0.f;
+      const float gam = l < L ? a.scale * __expf(pgt) : 0.f;
+      if (w == 4) {
+        sFac[l] = fac;
+        sGam[l] = gam;
+        if (l == 0) sGL[0] = __expf(pgl);
       }
-    }
-    if (tid < BT) {
-      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
-      pgt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
-    }
-  };
-  if (nc > 0) issue(nc - 1);
-
-  for (int c = nc - 1; c >= 0; --c) {
-    const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
-    const long tok0 = bos + c0;
-    // ---- stage
-    pP.store(sPh, sPl, LDB, tid);
-    pO.store_t(sdOT, LDB, L, tid);
-    {
-      float rs[PatchBf16<VB, BT>::N][4];
+    };
+    // phase-B tiles of chunk c: Qc (hi/lo), w, wl; scale gamma dO (hi/lo) from the dO tile of c,
+    // which the compute waves only read during this phase
+    auto stage_b = [&](int c) {
+      const int L = chunk_len(c);
+      pq.store_split(sQh, sQl, LDK, L, lm);
+      pw.store(sW, LDK, L, lm);
+      pwl.store(sWl, LDK, L, lm);
+      const int r = lm / (VB / 8), cc = (lm % (VB / 8)) * 8;
+      const float sc = sGam[r];
+      const bf16x8 o = *(const bf16x8*)(sdO + r * LDO + cc);
+      bf16x8 vh, vl;
 #pragma unroll
-      for (int j = 0; j < PatchBf16<VB, BT>::N; ++j) {
-        int rg, cg;
-        PatchBf16<VB, BT>::coords(min(tid + j * kThreads, PatchBf16<VB, BT>::NP - 1), rg, cg);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) rs[j][i] = (4 * rg + i < L) ? a.scale * __expf(gsc[j][i]) : 0.f;
+      for (int i = 0; i < 8; ++i) {
+        bf16 x, y;
+        split2(sc * (float)o[i], x, y);
+        vh[i] = x;
+        vl[i] = y;
       }
-      pO.store_t_scaled(sgOh, sgOl, LDB, rs, tid);
-    }
-    pK.store(sK, LDK, nullptr, 0);
-    pQ.store_t(sQh, sQl, LDB, L, tid);
-    pW.store_t(sWh, LDB, L, tid);
-    pWl.store_t(sWl, LDB, L, tid);
-    if (tid < BT) {
-      sFac[tid] = __expf(pgl - pgt);
-      if (tid == 0) sGL[0] = __expf(pgl);
-    }
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const int rt = w + 4 * j;
-      if (rt < NRT) acc_to_lds_t(dS[j], sdSh, sdSl, LDK, rt * 32);
+      *(bf16x8*)(sgOh + r * LDO + cc) = vh;
+      *(bf16x8*)(sgOl + r * LDO + cc) = vl;
+    };
+    // Loads run one chunk ahead of their stage and are unconditional (chunk 0 again past the
+    // start), so every pass issues the same memory operations.
+    const int cl = nc - 1;
+    if (nc > 0) {
+      load_a(cl);
+      load_b(cl);
+      stage_a(cl);
+      load_a(max(cl - 1, 0));
     }
     __syncthreads();
-    if (c > 0) issue(c - 1);
-
-    // ---- phase A
-    if (w < 2) {
-      f32x16 acc = zero16(), acc2 = zero16();
-#pragma unroll
-      for (int k0 = 0; k0 < BT; k0 += 16) {
-        const bf16x8 b = frag_rm(sdOT + k0, LDB);
-        acc = mfma(frag_rm(sPh + w * 32 * LDB + k0, LDB), b, acc);
-        acc = mfma(frag_rm(sPl + w * 32 * LDB + k0, LDB), b, acc);
-      }
-#pragma unroll 4
-      for (int k0 = 0; k0 < K; k0 += 16) {
-        const bf16x8 kf = frag_rm(sK + w * 32 * LDK + k0, LDK);
-        acc2 = mfma(kf, frag_rm(sdSh + k0, LDK), acc2);
-        acc2 = mfma(kf, frag_rm(sdSl + k0, LDK), acc2);
-      }
-      const int r0 = w * 32 + acc_row(0);
-      f32x16 du;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = r0 + acc_drow(i);
-        du[i] = (r < L) ? acc[i] + sFac[r] * acc2[i] : 0.f;
-      }
-      float* dug = a.dU + (tok0 + r0) * rsv + (long)h * V + v0 + acc_col();
-      if (r0 + 27 < L) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) dug[acc_drow(i) * rsv] = du[i];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (r0 + acc_drow(i) < L) dug[acc_drow(i) * rsv] = du[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) du[i] = -du[i];
-      acc_to_lds_t(du, sdUh, sdUl, LDB, w * 32);
-    } else {
-      // dS' snapshot (hi/lo) to HBM for gdn_bwd_dqkw
+    for (int c = cl; c >= 0; --c) {
+      const int gc = gc0 + c;
+      // ---- phase A: phase-B tiles of c; loads of Qc, w, wl of c-1; dS' snapshot
+      stage_b(c);
+      load_b(max(c - 1, 0));
       constexpr int VPR = K / 8;
-      for (int idx = tid - 128; idx < 2 * VB * VPR; idx += 128) {
+#pragma unroll
+      for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
+        const int idx = lm + j * NM;
         const int which = idx / (VB * VPR), e = idx % (VB * VPR);
         const int r = e / VPR, cc = (e % VPR) * 8;
         const bf16* src = which ? sdSl : sdSh;
         bf16* dst = which ? (bf16*)a.dhTl : (bf16*)a.dhT;
-        *(bf16x8*)(gmem(dst) + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
+        *gmem((bf16x8*)(dst + (((long)gc * a.H + h) * V + v0 + r) * K + cc)) = *(const bf16x8*)(src + r * LDK + cc);
       }
+      __syncthreads();
+      // ---- phase B: phase-A tiles of c-1; loads of P^T, dO, k, g of c-2
+      stage_a(max(c - 1, 0));
+      load_a(max(c - 2, 0));
+      __syncthreads();
+    }
+    return;
+  }
+
+  // compute waves: dS rows [RW w, RW w + RW) x 32 value columns as 16x16 tiles
+  f32x4 dS[NR16][2];
+#pragma unroll
+  for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      dS[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (a.ds_fin) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dS[rt][ct][i] = a.ds_fin[((long)unit * K + RW * w + 16 * rt + 4 * (l >> 4) + i) * V + v0 + 16 * ct + (l & 15)];
+      }
+    }
+#pragma unroll
+  for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) acc16_to_lds_t(dS[rt][ct], sdSh + 16 * ct * LDK, sdSl + 16 * ct * LDK, LDK, RW * w + 16 * rt);
+  __syncthreads();
+  for (int c = nc - 1; c >= 0; --c) {
+    const int L = chunk_len(c);
+    const long tok0 = tok_of(c);
+    // ---- phase A: dU rows [16 w, 16 w + 16) = P^T dO + fac (K dS')
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 acc2[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 32) {
+      const bf16x8 ph = frag16_rm(sPh + 16 * w * LDP + k0, LDP), pl = frag16_rm(sPl + 16 * w * LDP + k0, LDP);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x8 o = frag16_tr(sdO + k0 * LDO + 16 * ct, LDO);
+        acc[ct] = mfma16(ph, o, acc[ct]);
+        acc[ct] = mfma16(pl, o, acc[ct]);
+      }
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      const bf16x8 kf = frag16_rm(sK + 16 * w * LDK + k0, LDK);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        acc2[ct] = mfma16(kf, frag16_rm(sdSh + 16 * ct * LDK + k0, LDK), acc2[ct]);
+        acc2[ct] = mfma16(kf, frag16_rm(sdSl + 16 * ct * LDK + k0, LDK), acc2[ct]);
+      }
+    }
+    const float gL = sGL[0];
+    const int rb = 16 * w + 4 * (l >> 4);
+    const f32x4 fac = *(const f32x4*)(sFac + rb);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int cc = 16 * ct + (l & 15);
+      f32x4 du, ndu;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        du[i] = rb + i < L ? acc[ct][i] + fac[i] * acc2[ct][i] : 0.f;
+        ndu[i] = -du[i];
+      }
+      auto dug = gmem(a.dU) + (tok0 + rb) * rsv + (long)h * V + v0 + cc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (rb + i < L) dug[i * rsv] = du[i];
+      acc16_to_lds_t(ndu, sdUh + 16 * ct * LDP, sdUl + 16 * ct * LDP, LDP, 16 * w);
     }
     __syncthreads();
 
-    // ---- phase B
-    const float gL = sGL[0];
+    // ---- phase B: dS <- gamma_L dS' + Qc^T (scale gamma dO) - w^T dU
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const int rt = w + 4 * j;
-      if (rt < NRT) {
+    for (int rt = 0; rt < NR16; ++rt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dS[j][i] *= gL;
+      for (int ct = 0; ct < 2; ++ct) dS[rt][ct] *= gL;
 #pragma unroll
-        for (int k0 = 0; k0 < BT; k0 += 16) {
-          const bf16x8 qh = frag_rm(sQh + rt * 32 * LDB + k0, LDB), ql = frag_rm(sQl + rt * 32 * LDB + k0, LDB);
-          const bf16x8 gh = frag_rm(sgOh + k0, LDB), gl = frag_rm(sgOl + k0, LDB);
-          dS[j] = mfma(qh, gh, dS[j]);
-          dS[j] = mfma(qh, gl, dS[j]);
-          dS[j] = mfma(ql, gh, dS[j]);
-          const bf16x8 wh = frag_rm(sWh + rt * 32 * LDB + k0, LDB), wl = frag_rm(sWl + rt * 32 * LDB + k0, LDB);
-          const bf16x8 dh = frag_rm(sdUh + k0, LDB), dl = frag_rm(sdUl + k0, LDB);
-          dS[j] = mfma(wh, dh, dS[j]);
-          dS[j] = mfma(wh, dl, dS[j]);
-          dS[j] = mfma(wl, dh, dS[j]);
+    for (int k0 = 0; k0 < BT; k0 += 32) {
+      bf16x8 gh[2], gl[2], dh[2], dl[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        gh[ct] = frag16_tr(sgOh + k0 * LDO + 16 * ct, LDO);
+        gl[ct] = frag16_tr(sgOl + k0 * LDO + 16 * ct, LDO);
+        dh[ct] = frag16_rm(sdUh + 16 * ct * LDP + k0, LDP);
+        dl[ct] = frag16_rm(sdUl + 16 * ct * LDP + k0, LDP);
+      }
+#pragma unroll
+      for (int rt = 0; rt < NR16; ++rt) {
+        const int m0 = RW * w + 16 * rt;
+        const bf16x8 qh = frag16_tr(sQh + k0 * LDK + m0, LDK), ql = frag16_tr(sQl + k0 * LDK + m0, LDK);
+        const bf16x8 wh = frag16_tr(sW + k0 * LDK + m0, LDK), wl = frag16_tr(sWl + k0 * LDK + m0, LDK);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          dS[rt][ct] = mfma16(qh, gh[ct], dS[rt][ct]);
+          dS[rt][ct] = mfma16(qh, gl[ct], dS[rt][ct]);
+          dS[rt][ct] = mfma16(ql, gh[ct], dS[rt][ct]);
+          dS[rt][ct] = mfma16(wh, dh[ct], dS[rt][ct]);
+          dS[rt][ct] = mfma16(wh, dl[ct], dS[rt][ct]);
+          dS[rt][ct] = mfma16(wl, dh[ct], dS[rt][ct]);
         }
       }
     }
+#pragma unroll
+    for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        acc16_to_lds_t(dS[rt][ct], sdSh + 16 * ct * LDK, sdSl + 16 * ct * LDK, LDK, RW * w + 16 * rt);
     __syncthreads();
   }
   if (a.ds0) {
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const int rt = w + 4 * j;
-      if (rt < NRT) {
+    for (int rt = 0; rt < NR16; ++rt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          a.ds0[((long)unit * K + rt * 32 + acc_row(i)) * V + v0 + acc_col()] = dS[j][i];
-      }
-    }
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          a.ds0[((long)unit * K + RW * w + 16 * rt + 4 * (l >> 4) + i) * V + v0 + 16 * ct + (l & 15)] = dS[rt][ct][i];
   }
 }
 
@@ -2340,8 +2396,13 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       break;
     case kGdnBwdState:
       if (K <= 128)
-        hipLaunchKernelGGL(gdn_bwd_state_v2_kernel<(K <= 128 ? K : 128)>, dim3((V / 32) * a.N * a.H), dim3(kThreads),
-                           0, st, a, V);
+      {
+        constexpr int KW = K <= 128 ? K : 128;
+        if (a.qc32)
+          hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, true>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
+        else
+          hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, false>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
+      }
       else
         hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;

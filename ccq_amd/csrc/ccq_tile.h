@@ -698,6 +698,20 @@ struct RowsF32 {
       v[j] = *gmem((const f32x4*)(g + (long)(r < nvalid ? r : 0) * gstride + (idx % VPR) * 4));
     }
   }
+  // fp32 rows, or bf16 rows widened (g32 == nullptr)
+  __device__ __forceinline__ void load(const float* g32, const bf16* g16, long gstride, int nvalid, int lt) {
+    if (g32) {
+      load(g32, gstride, nvalid, lt);
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = min(lt + j * NTHR, TOT - 1), r = idx / VPR;
+      const bf16x4 b = *gmem((const bf16x4*)(g16 + (long)(r < nvalid ? r : 0) * gstride + (idx % VPR) * 4));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[j][i] = (float)b[i];
+    }
+  }
   __device__ __forceinline__ void store(float* dst, int ld, int nvalid, int lt) const {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
@@ -705,6 +719,25 @@ struct RowsF32 {
       if (TOT % NTHR != 0 && idx >= TOT) continue;
       const int r = idx / VPR;
       *(f32x4*)(dst + r * ld + (idx % VPR) * 4) = r < nvalid ? v[j] : f32x4{};
+    }
+  }
+  // row-major hi/lo bf16 pair (8-byte pieces)
+  __device__ __forceinline__ void store_split(bf16* hi, bf16* lo, int ld, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = lt + j * NTHR;
+      if (TOT % NTHR != 0 && idx >= TOT) continue;
+      const int r = idx / VPR, e = r * ld + (idx % VPR) * 4;
+      bf16x4 vh, vl;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bf16 x, y;
+        split2(r < nvalid ? v[j][i] : 0.f, x, y);
+        vh[i] = x;
+        vl[i] = y;
+      }
+      *(bf16x4*)(hi + e) = vh;
+      *(bf16x4*)(lo + e) = vl;
     }
   }
 };
