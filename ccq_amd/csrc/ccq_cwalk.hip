@@ -478,6 +478,293 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
+// cw_fwd for K <= 128 (64-token chunks) with 8 wavefronts: waves 0-3 compute with 16x16x32 MFMA
+// tiles and hold the state slice C[:, cols] (rows [K/4 w, K/4 w + K/4)) and the key sums of those
+// rows; waves 4-7 stage Q and K (row-major, two LDS buffers) one chunk ahead.  Per chunk c:
+//   phase 1  memory waves: score tiles A^T = K Q^T (causal, 10 of 16 tiles, three interleaved per
+//            wave); compute waves: C += K^T K[:, cols] and the key sums; C^T and m (hi/lo) of
+//            chunk c+1 into the other LDS buffer.  K^T and K[:, cols] operands come from the row-major K tile by
+//            transposing LDS reads.
+//   phase 2  Z = Q C_prev + A K[:, cols], running key sums, the row scalars (m_prev . q_t, gate
+//            logit, score row sums: MFMAs against broadcast operands), q_clean; stores of z,
+//            q_clean, s_t
+// ===========================================================================
+// MEAN, GATE: subtract_mean and the fused gate as template parameters (straight-line code in the
+// chunk loop)
+template <int K, bool MEAN, bool GATE>
+__global__ __launch_bounds__(kWalk8) void cw_fwd_v3_kernel(const WalkArgs a) {
+  constexpr int CB = 64, LDK = K + 16, LDA = CB + 16, NM = 256;
+  constexpr int RW = K / 4, NR16 = RW / 16;
+  __shared__ __attribute__((aligned(16))) bf16 sQ[2][CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sCh[2][32 * LDK];   // C_prev^T [col][row], hi
+  __shared__ __attribute__((aligned(16))) bf16 sCl[2][32 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sAh[CB * LDA];      // scores A[t][s] (s <= t), hi
+  __shared__ __attribute__((aligned(16))) bf16 sAl[CB * LDA];
+  __shared__ __attribute__((aligned(16))) bf16 sMW[2][4 * LDK];    // rows m_hi, m_lo, w_hi, w_lo
+  __shared__ __attribute__((aligned(16))) float sM[2][K];          // key sum before the chunk
+  __shared__ __attribute__((aligned(16))) float sLam[2][CB];
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const WalkUnit u = walk_unit<K>(a);
+  constexpr bool mean = MEAN, gate = GATE;
+  auto chunk_len = [&](int c) { return min(CB, u.len - c * CB); };
+
+  if (w >= 4) {
+    // memory waves: Q, K (and the given lambda) of chunk c into buffer c % 2, one chunk ahead; the
+    // score tiles of the current chunk
+    const int lm = tid - NM;
+    RowsBf16<K, CB, NM> pq, pk;
+    float plam = 0.f;
+    auto load = [&](int c) {
+      const int L = chunk_len(c);
+      const long off = u.hb + (long)c * CB * u.rs;
+      pq.load((const bf16*)a.q + off, u.rs, L, lm);
+      pk.load((const bf16*)a.k + off, u.rs, L, lm);
+      if (!gate) plam = a.lam[(u.bos + (long)c * CB + min(lm & (CB - 1), L - 1)) * a.H + u.h];
+    };
+    auto stage = [&](int c) {
+      const int L = chunk_len(c), b = c & 1;
+      pq.store(sQ[b], LDK, L, lm);
+      pk.store(sK[b], LDK, L, lm);
+      if (!gate && lm < CB) sLam[b][lm] = lm < L ? plam : 0.f;
+    };
+    // score tiles of memory wave w: entries w - 4, w, w + 4 of (0,0) (1,0) (1,1) (2,0) (2,1) (2,2)
+    // (3,0) (3,1) (3,2) (3,3) as (I = t tile, J = s tile); waves 6 and 7 compute a third tile that
+    // they discard
+    int tI[3], tJ[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int e = (w - 4) + 4 * j < 10 ? (w - 4) + 4 * j : 0;
+      tI[j] = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
+      tJ[j] = e - tI[j] * (tI[j] + 1) / 2;
+    }
+    const bool third = w < 6;
+
+    const int cl = u.nc - 1;
+    if (u.nc > 0) {
+      load(0);
+      stage(0);
+      load(min(1, cl));
+    }
+    __syncthreads();
+    for (int c = 0; c < u.nc; ++c) {
+      // phase 1: chunk c+1 into the other buffer (last read in phase 2 of chunk c-1); loads of c+2.
+      // Past the end the last chunk is staged again into the idle buffer: every pass issues the
+      // same memory operations.
+      if (c + 1 <= cl) stage(c + 1);
+      load(min(c + 2, cl));
+      const int b = c & 1;
+      const bf16* Q = sQ[b];
+      const bf16* Kc = sK[b];
+      // score tiles A^T = K Q^T of chunk c (element (s, t), kept for s <= t), written to A[t][s]
+      {
+        f32x4 acc[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < K; k0 += 32)
+#pragma unroll
+          for (int j = 0; j < 3; ++j)
+            acc[j] = mfma16(frag16_rm(Kc + 16 * tJ[j] * LDK + k0, LDK), frag16_rm(Q + 16 * tI[j] * LDK + k0, LDK), acc[j]);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          if (j < 2 || third) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (tI[j] == tJ[j] && 4 * (l >> 4) + i > (l & 15)) acc[j][i] = 0.f;
+            acc16_to_lds_t(acc[j], sAh + 16 * tI[j] * LDA, sAl + 16 * tI[j] * LDA, LDA, 16 * tJ[j]);
+          }
+        }
+      }
+      __syncthreads();
+      __syncthreads();
+    }
+    return;
+  }
+
+  // ---- compute waves
+  const float gbias = gate ? a.gate_b[u.h] : 0.f;
+  f32x4 C[NR16][2], Mk[NR16];
+#pragma unroll
+  for (int rt = 0; rt < NR16; ++rt) {
+    const int kr = RW * w + 16 * rt + 4 * (l >> 4);  // first of this lane's four state rows
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        C[rt][ct][i] = a.h0 ? a.h0[((long)u.unit * K + kr + i) * K + u.c0 + 16 * ct + (l & 15)] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Mk[rt][i] = (mean && a.m0) ? a.m0[(long)u.unit * K + kr + i] : 0.f;
+  }
+  // state of a chunk into buffer b: C^T (hi/lo), key sum m (fp32 and hi/lo rows of sMW)
+  auto put_state = [&](int b) {
+#pragma unroll
+    for (int rt = 0; rt < NR16; ++rt) {
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        acc16_to_lds_t(C[rt][ct], sCh[b] + 16 * ct * LDK, sCl[b] + 16 * ct * LDK, LDK, RW * w + 16 * rt);
+      if ((l & 15) == 0) {
+        const int kr = RW * w + 16 * rt + 4 * (l >> 4);
+        bf16x4 hh, ll;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16 x, y;
+          split2(Mk[rt][i], x, y);
+          hh[i] = x;
+          ll[i] = y;
+        }
+        *(f32x4*)(sM[b] + kr) = Mk[rt];
+        *(bf16x4*)(sMW[b] + kr) = hh;
+        *(bf16x4*)(sMW[b] + LDK + kr) = ll;
+      }
+    }
+  };
+  // gate rows of sMW (both buffers); score tiles that are never computed but are read by the
+  // 32-wide steps of phase 2 stay zero
+  for (int i = tid; i < 2 * LDK; i += NM) {
+    const int r = i / LDK + 2, cc = i % LDK;
+    bf16 hh = (bf16)0.f, ll = (bf16)0.f;
+    if (gate && cc < K) split2(a.gate_w[(long)u.h * K + cc], hh, ll);
+    sMW[0][r * LDK + cc] = r == 2 ? hh : ll;
+    sMW[1][r * LDK + cc] = r == 2 ? hh : ll;
+  }
+  for (int i = tid; i < 2 * 16 * 16; i += NM) {
+    const int tile = i / 256, e = i % 256, rr = e / 16, cc = e % 16;
+    const int I = tile == 0 ? 0 : 2, J = I + 1;  // tiles (0, 1) and (2, 3)
+    sAh[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
+    sAl[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
+  }
+  put_state(0);
+  __syncthreads();
+
+  for (int c = 0; c < u.nc; ++c) {
+    const int b = c & 1, t0 = c * CB, L = chunk_len(c);
+    const bf16* Q = sQ[b];
+    const bf16* Kc = sK[b];
+    // ---- phase 1: state update (the memory waves compute the score tiles meanwhile)
+    // state update C += K^T K[:, cols] and key sums; the state of chunk c+1 into the other buffer
+#pragma unroll
+    for (int s0 = 0; s0 < CB; s0 += 32) {
+      bf16x8 kc[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) kc[ct] = frag16_tr(Kc + s0 * LDK + u.c0 + 16 * ct, LDK);
+#pragma unroll
+      for (int rt = 0; rt < NR16; ++rt) {
+        const bf16x8 kr = frag16_tr(Kc + s0 * LDK + RW * w + 16 * rt, LDK);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) C[rt][ct] = mfma16(kr, kc[ct], C[rt][ct]);
+        if (mean) Mk[rt] = mfma16(kr, ones8(), Mk[rt]);
+      }
+    }
+    put_state(b ^ 1);
+    __syncthreads();
+
+    // ---- phase 2: rows [16 w, 16 w + 16): Z = Q C_prev + A K[:, cols]; running key sums; the
+    // row scalars m_prev . q_t, gate logit and sum_s A[t][s] come out of the MFMA with broadcast
+    // operands (every column holds the row's value)
+    f32x4 zacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 cum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f}, lg = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      const bf16x8 qf = frag16_rm(Q + 16 * w * LDK + k0, LDK);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        zacc[ct] = mfma16(qf, frag16_rm(sCh[b] + 16 * ct * LDK + k0, LDK), zacc[ct]);
+        zacc[ct] = mfma16(qf, frag16_rm(sCl[b] + 16 * ct * LDK + k0, LDK), zacc[ct]);
+      }
+      if (mean) {
+        sv = mfma16(qf, frag16_rm(sMW[b] + k0, 0), sv);
+        sv = mfma16(qf, frag16_rm(sMW[b] + LDK + k0, 0), sv);
+      }
+      if (gate) {
+        lg = mfma16(qf, frag16_rm(sMW[b] + 2 * LDK + k0, 0), lg);
+        lg = mfma16(qf, frag16_rm(sMW[b] + 3 * LDK + k0, 0), lg);
+      }
+    }
+    const int smax = w < 2 ? 32 : 64;
+    for (int s0 = 0; s0 < smax; s0 += 32) {
+      const bf16x8 ah = frag16_rm(sAh + 16 * w * LDA + s0, LDA), al = frag16_rm(sAl + 16 * w * LDA + s0, LDA);
+      if (mean) {
+        sv = mfma16(ah, ones8(), sv);
+        sv = mfma16(al, ones8(), sv);
+      }
+      // lower-triangular ones: row t = 16 w + (l & 15), column s = s0 + 8 (l >> 4) + i
+      bf16x8 tri;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tri[i] = (s0 + 8 * (l >> 4) + i <= 16 * w + (l & 15)) ? (bf16)1.f : (bf16)0.f;
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x8 kf = frag16_tr(Kc + s0 * LDK + u.c0 + 16 * ct, LDK);
+        zacc[ct] = mfma16(ah, kf, zacc[ct]);
+        zacc[ct] = mfma16(al, kf, zacc[ct]);
+        if (mean) cum[ct] = mfma16(tri, kf, cum[ct]);
+      }
+    }
+    const int tb = 16 * w + 4 * (l >> 4);  // first of this lane's four rows
+    f32x4 lam, ip;
+    if (gate) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lam[i] = tb + i < L ? __builtin_amdgcn_rcpf(1.f + __expf(-(lg[i] + gbias))) : 0.f;
+    } else {
+      lam = *(const f32x4*)(sLam[b] + tb);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ip[i] = __builtin_amdgcn_rcpf(cw_pos(t0 + tb + i, a.pos_off));
+    float qv[2][4], mc[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      mc[ct] = sM[b][u.c0 + 16 * ct + (l & 15)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qv[ct][i] = (float)Q[(tb + i) * LDK + u.c0 + 16 * ct + (l & 15)];
+    }
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const long base = u.hb + (long)(t0 + tb) * u.rs + u.c0 + 16 * ct + (l & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (tb + i < L) {
+          const float qo = qv[ct][i] - lam[i] * (zacc[ct][i] * ip[i] - sv[i] * ip[i] * ip[i] * (mc[ct] + cum[ct][i]));
+          gmem(a.z)[base + i * u.rs] = zacc[ct][i];
+          if (a.qc32) gmem(a.qc32)[base + i * u.rs] = qo;
+          else gmem((bf16*)a.qc)[base + i * u.rs] = (bf16)qo;
+        }
+      }
+    }
+    if (u.ct == 0 && (l & 15) == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (tb + i < L) {
+          const long ti = (u.bos + t0 + tb + i) * a.H + u.h;
+          a.srow[ti] = sv[i];
+          if (gate && a.lam_out) a.lam_out[ti] = lam[i];
+        }
+      }
+    }
+    if (mean && u.ct == 0)
+      for (int i = tid; i < K; i += NM) a.mpre[((long)(u.gc0 + c) * a.H + u.h) * K + i] = sM[b][i];
+    __syncthreads();
+  }
+
+  if (a.h_fin) {
+#pragma unroll
+    for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          a.h_fin[((long)u.unit * K + RW * w + 16 * rt + 4 * (l >> 4) + i) * K + u.c0 + 16 * ct + (l & 15)] = C[rt][ct][i];
+  }
+  if (mean && u.ct == 0 && a.m_fin && (l & 15) == 0) {
+#pragma unroll
+    for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a.m_fin[(long)u.unit * K + RW * w + 16 * rt + 4 * (l >> 4) + i] = Mk[rt][i];
+  }
+}
+
+// ===========================================================================
 // cw_rows: grid NTG*H, one workgroup per (chunk, head); HBM-bound.  Every thread issues all of its
 // loads up front:
 //   key sums   m_t = m_prev + prefix of k over the chunk: column c = tid % K, row segment
@@ -1042,7 +1329,18 @@ hipError_t cwalk_k(int stage, const WalkArgs& a, hipStream_t st) {
   const long units = (long)a.N * a.H * (K / 32);
   switch (stage) {
     case kWalkFwd:
-      if (units > 0) hipLaunchKernelGGL(cw_fwd_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);
+      if (units > 0) {
+        if (K == 64 || K == 128) {
+          constexpr int KW = K == 64 ? 64 : 128;
+          const bool mean = a.subtract_mean != 0, gate = a.gate_w != nullptr;
+          const dim3 grid((unsigned)units), block(kWalk8);
+          if (mean && gate) hipLaunchKernelGGL((cw_fwd_v3_kernel<KW, true, true>), grid, block, 0, st, a);
+          else if (mean) hipLaunchKernelGGL((cw_fwd_v3_kernel<KW, true, false>), grid, block, 0, st, a);
+          else if (gate) hipLaunchKernelGGL((cw_fwd_v3_kernel<KW, false, true>), grid, block, 0, st, a);
+          else hipLaunchKernelGGL((cw_fwd_v3_kernel<KW, false, false>), grid, block, 0, st, a);
+        } else
+          hipLaunchKernelGGL(cw_fwd_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);
+      }
       break;
     case kWalkRows:
       if ((long)a.NTG * a.H > 0)

@@ -435,8 +435,6 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
 // LDS pitches: tiles read as mfma16 operands are K + 16 (or 64 + 16) elements wide, which keeps those
 // reads free of bank conflicts; rows are written by 16 consecutive lanes per row.
 // ===========================================================================
-constexpr int kWalk8 = 512;
-
 template <int K>
 __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs a, const int V) {
   constexpr int VB = 32, LDK = K + 16, LDB = BT + 16, LDV = VB + 4;
