@@ -1107,6 +1107,246 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
+// cw_dq for K <= 128 (64-token chunks) with 8 wavefronts, forward walk of C.  Waves 0-3 compute (16x16
+// tiles; state slice rows [K/4 w, +K/4)); waves 4-7 stage dZ (hi/lo, dZ_t = F_t dqc_t) and K one
+// chunk ahead into two LDS buffers, write the current chunk's dqc columns, row scalars and key sums,
+// and compute the score tiles.  Per chunk c:
+//   phase 1  compute: C_prev^T (hi/lo) into LDS, then C += K^T K[:, cols] (transposing LDS reads)
+//            memory:  dqc[:, cols], row scalars, m_prev[cols] of c; dZ, K of c+1; loads of c+2;
+//                     score tiles A^T = K dZ^T of c (kept for s <= t)
+//   phase 2  compute: dq = dqc + dZ C_prev + A K[:, cols] + ds (m_prev + running key sums)
+//                     + dlogit w[cols]; stores
+// DQ32: the upstream gradient is fp32 (else bf16); MEAN, GATE as in cw_fwd_v3.
+// ===========================================================================
+template <int K, bool DQ32, bool MEAN, bool GATE>
+__global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
+  constexpr int CB = 64, LDK = K + 16, LDA = CB + 16, LDG = 32 + 4, NM = 256;
+  constexpr int RW = K / 4, NR16 = RW / 16;
+  __shared__ __attribute__((aligned(16))) bf16 sZh[2][CB * LDK];  // dZ rows, hi
+  __shared__ __attribute__((aligned(16))) bf16 sZl[2][CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sCh[32 * LDK];     // C_prev^T [col][row], hi
+  __shared__ __attribute__((aligned(16))) bf16 sCl[32 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sAh[CB * LDA];     // A[t][s] = dz_t . k_s (s <= t), hi
+  __shared__ __attribute__((aligned(16))) bf16 sAl[CB * LDA];
+  __shared__ __attribute__((aligned(16))) float sG[CB * LDG];     // dqc[t][cols]
+  __shared__ __attribute__((aligned(16))) f32x4 sR[CB];           // row scalars
+  __shared__ __attribute__((aligned(16))) float sMp[32], sWc[32];
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const WalkUnit u = walk_unit<K>(a);
+  constexpr bool mean = MEAN, gate = GATE;
+  auto chunk_len = [&](int c) { return min(CB, u.len - c * CB); };
+  if (tid < 32) sWc[tid] = gate ? a.gate_w[(long)u.h * K + u.c0 + tid] : 0.f;
+
+  if (w >= 4) {
+    const int lm = tid - NM;
+    // dqc rows (fp32) with their row scale F_t, k rows, row scalars and key sums of the chunk
+    // staged next; dqc columns, row scalars and key sums of the current chunk
+    RowsF32<K, CB, NM> pz;
+    RowsBf16<K, CB, NM> pk;
+    float pf[RowsF32<K, CB, NM>::N];
+    f32x4 prow = f32x4{}, crow = f32x4{};
+    float pmp = 0.f, cmp = 0.f;
+    f32x4 ccol[RowsF32<K, CB, NM>::N];
+    constexpr int VPR = K / 4;  // f32x4 per row
+    const bool colln = (lm % VPR) >= u.c0 / 4 && (lm % VPR) < u.c0 / 4 + 8;  // lane holds dqc[:, cols]
+    auto load = [&](int c) {
+      const int L = chunk_len(c);
+      const long off = u.hb + (long)c * CB * u.rs;
+      const long ti0 = (u.bos + (long)c * CB) * a.H + u.h;
+      if constexpr (DQ32) pz.load(a.dqc32 + off, u.rs, L, lm);
+      else pz.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, lm);
+#pragma unroll
+      for (int j = 0; j < RowsF32<K, CB, NM>::N; ++j) {
+        const int r = (lm + j * NM) / VPR;
+        pf[j] = a.sc[(ti0 + (long)min(r, L - 1) * a.H) * 4];
+      }
+      pk.load((const bf16*)a.k + off, u.rs, L, lm);
+      prow = *gmem((const f32x4*)(a.sc + (ti0 + (long)min(lm & (CB - 1), L - 1) * a.H) * 4));
+      if (mean) pmp = a.mpre[((long)(u.gc0 + c) * a.H + u.h) * K + u.c0 + (lm & 31)];
+    };
+    // dZ (hi/lo) and K of chunk c into buffer c % 2; the chunk's dqc columns, row scalars and key
+    // sums move to the registers written at the next phase 1
+    auto stage = [&](int c) {
+      const int L = chunk_len(c), b = c & 1;
+#pragma unroll
+      for (int j = 0; j < RowsF32<K, CB, NM>::N; ++j) {
+        const int idx = lm + j * NM, r = idx / VPR, e = r * LDK + (idx % VPR) * 4;
+        bf16x4 vh, vl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16 x, y;
+          split2(r < L ? pf[j] * pz.v[j][i] : 0.f, x, y);
+          vh[i] = x;
+          vl[i] = y;
+        }
+        *(bf16x4*)(sZh[b] + e) = vh;
+        *(bf16x4*)(sZl[b] + e) = vl;
+        ccol[j] = r < L ? pz.v[j] : f32x4{};
+      }
+      pk.store(sK[b], LDK, L, lm);
+      crow = (lm & (CB - 1)) < L ? prow : f32x4{};
+      cmp = pmp;
+    };
+    auto put_cur = [&]() {
+      if (colln) {
+#pragma unroll
+        for (int j = 0; j < RowsF32<K, CB, NM>::N; ++j) {
+          const int idx = lm + j * NM, r = idx / VPR;
+          *(f32x4*)(sG + r * LDG + (idx % VPR) * 4 - u.c0) = ccol[j];
+        }
+      }
+      if (lm < CB) sR[lm] = crow;
+      if (lm < 32) sMp[lm] = cmp;
+    };
+    // score tiles of memory wave w: entries w - 4, w, w + 4 of (0,0) (1,0) (1,1) (2,0) (2,1) (2,2)
+    // (3,0) (3,1) (3,2) (3,3) as (I = t tile, J = s tile); waves 6 and 7 compute a third tile that
+    // they discard
+    int tI[3], tJ[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int e = (w - 4) + 4 * j < 10 ? (w - 4) + 4 * j : 0;
+      tI[j] = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
+      tJ[j] = e - tI[j] * (tI[j] + 1) / 2;
+    }
+    const bool third = w < 6;
+    const int cl = u.nc - 1;
+    if (u.nc > 0) {
+      load(0);
+      stage(0);
+      load(min(1, cl));
+    }
+    __syncthreads();
+    for (int c = 0; c < u.nc; ++c) {
+      // phase 1.  Past the end the last chunk is staged again into the idle buffer and loaded again:
+      // every pass issues the same memory operations.
+      put_cur();
+      stage(min(c + 1, cl));
+      load(min(c + 2, cl));
+      const int b = c & 1;
+      {
+        f32x4 acc[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < K; k0 += 32)
+#pragma unroll
+          for (int j = 0; j < 3; ++j) {
+            const bf16x8 kf = frag16_rm(sK[b] + 16 * tJ[j] * LDK + k0, LDK);
+            acc[j] = mfma16(kf, frag16_rm(sZh[b] + 16 * tI[j] * LDK + k0, LDK), acc[j]);
+            acc[j] = mfma16(kf, frag16_rm(sZl[b] + 16 * tI[j] * LDK + k0, LDK), acc[j]);
+          }
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          if (j < 2 || third) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (tI[j] == tJ[j] && 4 * (l >> 4) + i > (l & 15)) acc[j][i] = 0.f;
+            acc16_to_lds_t(acc[j], sAh + 16 * tI[j] * LDA, sAl + 16 * tI[j] * LDA, LDA, 16 * tJ[j]);
+          }
+        }
+      }
+      __syncthreads();
+      __syncthreads();
+    }
+    return;
+  }
+
+  // ---- compute waves
+  f32x4 C[NR16][2];
+#pragma unroll
+  for (int rt = 0; rt < NR16; ++rt) {
+    const int kr = RW * w + 16 * rt + 4 * (l >> 4);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        C[rt][ct][i] = a.h0 ? a.h0[((long)u.unit * K + kr + i) * K + u.c0 + 16 * ct + (l & 15)] : 0.f;
+  }
+  for (int i = tid; i < 2 * 16 * 16; i += NM) {
+    const int tile = i / 256, e = i % 256, rr = e / 16, cc = e % 16;
+    const int I = tile == 0 ? 0 : 2, J = I + 1;  // tiles (0, 1) and (2, 3) stay zero
+    sAh[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
+    sAl[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
+  }
+  __syncthreads();
+  for (int c = 0; c < u.nc; ++c) {
+    const int b = c & 1, t0 = c * CB, L = chunk_len(c);
+    const bf16* Kc = sK[b];
+    // ---- phase 1: C_prev^T (hi/lo) for phase 2, then C += K^T K[:, cols]
+#pragma unroll
+    for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        acc16_to_lds_t(C[rt][ct], sCh + 16 * ct * LDK, sCl + 16 * ct * LDK, LDK, RW * w + 16 * rt);
+#pragma unroll
+    for (int s0 = 0; s0 < CB; s0 += 32) {
+      bf16x8 kc[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) kc[ct] = frag16_tr(Kc + s0 * LDK + u.c0 + 16 * ct, LDK);
+#pragma unroll
+      for (int rt = 0; rt < NR16; ++rt) {
+        const bf16x8 kr = frag16_tr(Kc + s0 * LDK + RW * w + 16 * rt, LDK);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) C[rt][ct] = mfma16(kr, kc[ct], C[rt][ct]);
+      }
+    }
+    __syncthreads();
+
+    // ---- phase 2: rows [16 w, 16 w + 16) of dq
+    f32x4 x[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 cum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      const bf16x8 zh = frag16_rm(sZh[b] + 16 * w * LDK + k0, LDK), zl = frag16_rm(sZl[b] + 16 * w * LDK + k0, LDK);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x8 ch = frag16_rm(sCh + 16 * ct * LDK + k0, LDK);
+        x[ct] = mfma16(zh, ch, x[ct]);
+        x[ct] = mfma16(zh, frag16_rm(sCl + 16 * ct * LDK + k0, LDK), x[ct]);
+        x[ct] = mfma16(zl, ch, x[ct]);
+      }
+    }
+    const int smax = w < 2 ? 32 : 64;
+    for (int s0 = 0; s0 < smax; s0 += 32) {
+      const bf16x8 ah = frag16_rm(sAh + 16 * w * LDA + s0, LDA), al = frag16_rm(sAl + 16 * w * LDA + s0, LDA);
+      bf16x8 tri;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tri[i] = (s0 + 8 * (l >> 4) + i <= 16 * w + (l & 15)) ? (bf16)1.f : (bf16)0.f;
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x8 kf = frag16_tr(Kc + s0 * LDK + u.c0 + 16 * ct, LDK);
+        x[ct] = mfma16(ah, kf, x[ct]);
+        x[ct] = mfma16(al, kf, x[ct]);
+        if (mean) cum[ct] = mfma16(tri, kf, cum[ct]);
+      }
+    }
+    const int tb = 16 * w + 4 * (l >> 4);
+    f32x4 rw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rw[i] = sR[tb + i];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int cc = 16 * ct + (l & 15);
+      const float mc = sMp[cc], wc = sWc[cc];
+      const long base = u.hb + (long)(t0 + tb) * u.rs + u.c0 + cc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (tb + i < L) {
+          float d = sG[(tb + i) * LDG + cc] + x[ct][i];
+          if (mean) d += rw[i][1] * (mc + cum[ct][i]);
+          if (gate) d += rw[i][2] * wc;
+          if (a.dq32) gmem(a.dq32)[base + i * u.rs] = d;
+          else gmem((bf16*)a.dq)[base + i * u.rs] = (bf16)d;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
 // cw_dk: grid N*H*(K/32); reverse walk of E = G + G^T (G = dC_T + sum of q dz^T over later chunks).
 // The in-chunk suffix sums of dm_t = ds_t q_t - (s_t/pos_t) dz_t ride along the score products:
 //   dk_j = K E + sum_{t>=j} (B1[j][t] + ds_t) q_t + sum_{t>=j} (B2[j][t] - s_t/pos_t) dz_t + carry,
@@ -1347,7 +1587,23 @@ hipError_t cwalk_k(int stage, const WalkArgs& a, hipStream_t st) {
         hipLaunchKernelGGL(cw_rows_kernel<K>, dim3((unsigned)((long)a.NTG * a.H)), dim3(kThreads), 0, st, a);
       break;
     case kWalkDq:
-      if (units > 0) hipLaunchKernelGGL(cw_dq_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);
+      if (units > 0) {
+        if (K == 64 || K == 128) {
+          constexpr int KW = K == 64 ? 64 : 128;
+          const dim3 grid((unsigned)units), block(kWalk8);
+          const int sel = (a.dqc32 ? 4 : 0) + (a.subtract_mean ? 2 : 0) + (a.gate_w ? 1 : 0);
+#define CCQ_DQ3(S, A, B, C) \
+  case S: hipLaunchKernelGGL((cw_dq_v3_kernel<KW, A, B, C>), grid, block, 0, st, a); break;
+          switch (sel) {
+            CCQ_DQ3(0, false, false, false) CCQ_DQ3(1, false, false, true) CCQ_DQ3(2, false, true, false)
+            CCQ_DQ3(3, false, true, true) CCQ_DQ3(4, true, false, false) CCQ_DQ3(5, true, false, true)
+            CCQ_DQ3(6, true, true, false) CCQ_DQ3(7, true, true, true)
+          }
+#undef CCQ_DQ3
+        } else {
+          hipLaunchKernelGGL(cw_dq_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);
+        }
+      }
       break;
     case kWalkDk:
       if (units > 0) {
