@@ -186,6 +186,8 @@ struct WalkWork {
   float* dw_part;
   float* db_part;
   float* red;  // first-pass row sums of dw_part / db_part
+  void* dzh;   // dz hi/lo (K in {64, 128}: written by the per-token pass, read by the walks)
+  void* dzl;
 };
 
 size_t carve_walk_work(char* base, const WalkGeom& g, int64_t tokens, int H, int K, bool gate, WalkWork* out) {
@@ -197,6 +199,10 @@ size_t carve_walk_work(char* base, const WalkGeom& g, int64_t tokens, int H, int
     t.dw_part = sl.take<float>((size_t)g.ntg * H * K);
     t.db_part = sl.take<float>((size_t)g.ntg * H);
     t.red = sl.take<float>((size_t)kSumSlices * H * (K + 1));
+  }
+  if (K == 64 || K == 128) {
+    t.dzh = sl.take<uint16_t>((size_t)tokens * H * K);
+    t.dzl = sl.take<uint16_t>((size_t)tokens * H * K);
   }
   if (out) *out = t;
   return sl.off;
@@ -286,6 +292,7 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
   WalkArgs a{};
   fill_walk_common(a, q, k, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, K, N, position_offset, subtract_mean);
   a.lam_used = lambda; a.sc = wk.sc; a.dmsum = subtract_mean ? wk.dmsum : nullptr;
+  a.dzh = wk.dzh; a.dzl = wk.dzl;
   a.dw_part = wk.dw_part; a.db_part = wk.db_part;
   a.dqc32 = dq_clean_f32; a.dqc16 = dq_clean_f32 ? nullptr : dq_clean; a.dk_extra = dk_extra;
   a.dh_fin = dh_final; a.dm_fin = subtract_mean ? dm_final : nullptr;

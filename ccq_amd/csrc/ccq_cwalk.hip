@@ -893,6 +893,23 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
       *(f32x4*)(a.sc + ti * 4) = o;
       if (!gate && a.dlam) a.dlam[ti] = dlam;
     }
+    if (a.dzh) {
+      // dz_t = F_t dqc_t for this thread's columns, as a hi/lo bf16 pair
+      const float F = -lam / p;
+#pragma unroll
+      for (int j = 0; j < PER / 8; ++j) {
+        bf16x8 vh, vl;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          bf16 x, y;
+          split2(F * gv[2 * j + i / 4][i % 4], x, y);
+          vh[i] = x;
+          vl[i] = y;
+        }
+        *gmem((bf16x8*)((bf16*)a.dzh + e0 + 8 * j)) = vh;
+        *gmem((bf16x8*)((bf16*)a.dzl + e0 + 8 * j)) = vl;
+      }
+    }
   }
   if (part == 0 && gate) sG[t] = g;
   if (mean) {
@@ -1108,12 +1125,13 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
 
 // ===========================================================================
 // cw_dq for K <= 128 (64-token chunks) with 8 wavefronts, forward walk of C.  Waves 0-3 compute (16x16
-// tiles; state slice rows [K/4 w, +K/4)); waves 4-7 stage dZ (hi/lo, dZ_t = F_t dqc_t) and K one
-// chunk ahead into two LDS buffers, write the current chunk's dqc columns, row scalars and key sums,
-// and compute the score tiles.  Per chunk c:
-//   phase 1  compute: C_prev^T (hi/lo) into LDS, then C += K^T K[:, cols] (transposing LDS reads)
-//            memory:  dqc[:, cols], row scalars, m_prev[cols] of c; dZ, K of c+1; loads of c+2;
-//                     score tiles A^T = K dZ^T of c (kept for s <= t)
+// tiles; state slice rows [K/4 w, +K/4)); waves 4-7 stage dZ (the hi/lo pair written by cw_rows,
+// dZ_t = F_t dqc_t), K, row scalars and key sums one chunk ahead into two LDS buffers, write the
+// current chunk's dqc columns.  Per chunk c:
+//   phase 1  compute: C_prev^T (hi/lo) into LDS, C += K^T K[:, cols] (transposing LDS reads), score
+//                     tiles A^T = K dZ^T (kept for s <= t)
+//            memory:  dqc[:, cols] of c; dZ, K, row scalars, m_prev[cols] of c+1; loads of c+2
+//                     (dqc columns of c+1)
 //   phase 2  compute: dq = dqc + dZ C_prev + A K[:, cols] + ds (m_prev + running key sums)
 //                     + dlogit w[cols]; stores
 // DQ32: the upstream gradient is fp32 (else bf16); MEAN, GATE as in cw_fwd_v3.
@@ -1130,8 +1148,8 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sAh[CB * LDA];     // A[t][s] = dz_t . k_s (s <= t), hi
   __shared__ __attribute__((aligned(16))) bf16 sAl[CB * LDA];
   __shared__ __attribute__((aligned(16))) float sG[CB * LDG];     // dqc[t][cols]
-  __shared__ __attribute__((aligned(16))) f32x4 sR[CB];           // row scalars
-  __shared__ __attribute__((aligned(16))) float sMp[32], sWc[32];
+  __shared__ __attribute__((aligned(16))) f32x4 sR[2][CB];        // row scalars, by chunk parity
+  __shared__ __attribute__((aligned(16))) float sMp[2][32], sWc[32];
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
   const WalkUnit u = walk_unit<K>(a);
@@ -1141,112 +1159,52 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
 
   if (w >= 4) {
     const int lm = tid - NM;
-    // dqc rows (fp32) with their row scale F_t, k rows, row scalars and key sums of the chunk
-    // staged next; dqc columns, row scalars and key sums of the current chunk
-    RowsF32<K, CB, NM> pz;
-    RowsBf16<K, CB, NM> pk;
-    float pf[RowsF32<K, CB, NM>::N];
-    f32x4 prow = f32x4{}, crow = f32x4{};
-    float pmp = 0.f, cmp = 0.f;
-    f32x4 ccol[RowsF32<K, CB, NM>::N];
-    constexpr int VPR = K / 4;  // f32x4 per row
-    const bool colln = (lm % VPR) >= u.c0 / 4 && (lm % VPR) < u.c0 / 4 + 8;  // lane holds dqc[:, cols]
+    // dz (hi/lo, from the per-token pass), k rows, row scalars and key sums of the chunk staged
+    // next; the dqc columns of the chunk whose columns are written next
+    RowsBf16<K, CB, NM> pzh, pzl, pk;
+    RowsF32<32, CB, NM> pcol;
+    f32x4 prow = f32x4{};
+    float pmp = 0.f;
     auto load = [&](int c) {
       const int L = chunk_len(c);
       const long off = u.hb + (long)c * CB * u.rs;
       const long ti0 = (u.bos + (long)c * CB) * a.H + u.h;
-      if constexpr (DQ32) pz.load(a.dqc32 + off, u.rs, L, lm);
-      else pz.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, lm);
-#pragma unroll
-      for (int j = 0; j < RowsF32<K, CB, NM>::N; ++j) {
-        const int r = (lm + j * NM) / VPR;
-        pf[j] = a.sc[(ti0 + (long)min(r, L - 1) * a.H) * 4];
-      }
+      pzh.load((const bf16*)a.dzh + off, u.rs, L, lm);
+      pzl.load((const bf16*)a.dzl + off, u.rs, L, lm);
       pk.load((const bf16*)a.k + off, u.rs, L, lm);
       prow = *gmem((const f32x4*)(a.sc + (ti0 + (long)min(lm & (CB - 1), L - 1) * a.H) * 4));
       if (mean) pmp = a.mpre[((long)(u.gc0 + c) * a.H + u.h) * K + u.c0 + (lm & 31)];
     };
-    // dZ (hi/lo) and K of chunk c into buffer c % 2; the chunk's dqc columns, row scalars and key
-    // sums move to the registers written at the next phase 1
+    auto load_cols = [&](int c) {
+      const long off = u.hb + (long)c * CB * u.rs + u.c0;
+      if constexpr (DQ32) pcol.load(a.dqc32 + off, u.rs, chunk_len(c), lm);
+      else pcol.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, chunk_len(c), lm);
+    };
+    // dZ (hi/lo), K, row scalars and key sums of chunk c into buffer c % 2
     auto stage = [&](int c) {
       const int L = chunk_len(c), b = c & 1;
-#pragma unroll
-      for (int j = 0; j < RowsF32<K, CB, NM>::N; ++j) {
-        const int idx = lm + j * NM, r = idx / VPR, e = r * LDK + (idx % VPR) * 4;
-        bf16x4 vh, vl;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bf16 x, y;
-          split2(r < L ? pf[j] * pz.v[j][i] : 0.f, x, y);
-          vh[i] = x;
-          vl[i] = y;
-        }
-        *(bf16x4*)(sZh[b] + e) = vh;
-        *(bf16x4*)(sZl[b] + e) = vl;
-        ccol[j] = r < L ? pz.v[j] : f32x4{};
-      }
+      pzh.store(sZh[b], LDK, L, lm);
+      pzl.store(sZl[b], LDK, L, lm);
       pk.store(sK[b], LDK, L, lm);
-      crow = (lm & (CB - 1)) < L ? prow : f32x4{};
-      cmp = pmp;
+      if (lm < CB) sR[b][lm] = lm < L ? prow : f32x4{};
+      if (lm < 32) sMp[b][lm] = pmp;
     };
-    auto put_cur = [&]() {
-      if (colln) {
-#pragma unroll
-        for (int j = 0; j < RowsF32<K, CB, NM>::N; ++j) {
-          const int idx = lm + j * NM, r = idx / VPR;
-          *(f32x4*)(sG + r * LDG + (idx % VPR) * 4 - u.c0) = ccol[j];
-        }
-      }
-      if (lm < CB) sR[lm] = crow;
-      if (lm < 32) sMp[lm] = cmp;
-    };
-    // score tiles of memory wave w: entries w - 4, w, w + 4 of (0,0) (1,0) (1,1) (2,0) (2,1) (2,2)
-    // (3,0) (3,1) (3,2) (3,3) as (I = t tile, J = s tile); waves 6 and 7 compute a third tile that
-    // they discard
-    int tI[3], tJ[3];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int e = (w - 4) + 4 * j < 10 ? (w - 4) + 4 * j : 0;
-      tI[j] = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
-      tJ[j] = e - tI[j] * (tI[j] + 1) / 2;
-    }
-    const bool third = w < 6;
+    // Loads are unconditional (past the end the last chunk again, staged into the idle buffer), so
+    // every pass issues the same memory operations in the same order.
     const int cl = u.nc - 1;
     if (u.nc > 0) {
       load(0);
+      load_cols(0);
       stage(0);
       load(min(1, cl));
     }
     __syncthreads();
     for (int c = 0; c < u.nc; ++c) {
-      // phase 1.  Past the end the last chunk is staged again into the idle buffer and loaded again:
-      // every pass issues the same memory operations.
-      put_cur();
+      // phase 1
+      pcol.store(sG, LDG, chunk_len(c), lm);
+      load_cols(min(c + 1, cl));
       stage(min(c + 1, cl));
       load(min(c + 2, cl));
-      const int b = c & 1;
-      {
-        f32x4 acc[3];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k0 = 0; k0 < K; k0 += 32)
-#pragma unroll
-          for (int j = 0; j < 3; ++j) {
-            const bf16x8 kf = frag16_rm(sK[b] + 16 * tJ[j] * LDK + k0, LDK);
-            acc[j] = mfma16(kf, frag16_rm(sZh[b] + 16 * tI[j] * LDK + k0, LDK), acc[j]);
-            acc[j] = mfma16(kf, frag16_rm(sZl[b] + 16 * tI[j] * LDK + k0, LDK), acc[j]);
-          }
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          if (j < 2 || third) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (tI[j] == tJ[j] && 4 * (l >> 4) + i > (l & 15)) acc[j][i] = 0.f;
-            acc16_to_lds_t(acc[j], sAh + 16 * tI[j] * LDA, sAl + 16 * tI[j] * LDA, LDA, 16 * tJ[j]);
-          }
-        }
-      }
       __syncthreads();
       __syncthreads();
     }
@@ -1271,6 +1229,17 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
     sAl[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
   }
   __syncthreads();
+  // score tiles of wave w: entries w, w + 4, w + 8 of (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0)
+  // (3,1) (3,2) (3,3) as (I = t tile, J = s tile); waves 2 and 3 compute a third tile that they
+  // discard
+  int tI[3], tJ[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int e = w + 4 * j < 10 ? w + 4 * j : 0;
+    tI[j] = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
+    tJ[j] = e - tI[j] * (tI[j] + 1) / 2;
+  }
+  const bool third = w < 2;
   for (int c = 0; c < u.nc; ++c) {
     const int b = c & 1, t0 = c * CB, L = chunk_len(c);
     const bf16* Kc = sK[b];
@@ -1290,6 +1259,29 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
         const bf16x8 kr = frag16_tr(Kc + s0 * LDK + RW * w + 16 * rt, LDK);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) C[rt][ct] = mfma16(kr, kc[ct], C[rt][ct]);
+      }
+    }
+    // score tiles A^T = K dZ^T of this chunk (element (s, t), kept for s <= t), written to A[t][s]
+    {
+      f32x4 acc[3];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k0 = 0; k0 < K; k0 += 32)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const bf16x8 kf = frag16_rm(Kc + 16 * tJ[j] * LDK + k0, LDK);
+          acc[j] = mfma16(kf, frag16_rm(sZh[b] + 16 * tI[j] * LDK + k0, LDK), acc[j]);
+          acc[j] = mfma16(kf, frag16_rm(sZl[b] + 16 * tI[j] * LDK + k0, LDK), acc[j]);
+        }
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        if (j < 2 || third) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (tI[j] == tJ[j] && 4 * (l >> 4) + i > (l & 15)) acc[j][i] = 0.f;
+          acc16_to_lds_t(acc[j], sAh + 16 * tI[j] * LDA, sAl + 16 * tI[j] * LDA, LDA, 16 * tJ[j]);
+        }
       }
     }
     __syncthreads();
@@ -1325,11 +1317,11 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
     const int tb = 16 * w + 4 * (l >> 4);
     f32x4 rw[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rw[i] = sR[tb + i];
+    for (int i = 0; i < 4; ++i) rw[i] = sR[b][tb + i];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       const int cc = 16 * ct + (l & 15);
-      const float mc = sMp[cc], wc = sWc[cc];
+      const float mc = sMp[b][cc], wc = sWc[cc];
       const long base = u.hb + (long)(t0 + tb) * u.rs + u.c0 + cc;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {

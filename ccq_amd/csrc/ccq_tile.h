@@ -678,6 +678,15 @@ struct RowsBf16 {
     }
   }
   __device__ __forceinline__ void store(bf16* dst, int ld, int nvalid, int lt) const {
+    if (nvalid >= ROWS) {  // whole tiles: no zero fill
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const int idx = lt + j * NTHR;
+        if (TOT % NTHR != 0 && idx >= TOT) continue;
+        *(bf16x8*)(dst + (idx / VPR) * ld + (idx % VPR) * 8) = v[j];
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < N; ++j) {
       const int idx = lt + j * NTHR;

@@ -50,6 +50,8 @@ struct WalkArgs {
   float* dw_part;           // fp32 [NTG, H, K] gate partials
   float* db_part;           // fp32 [NTG, H]
   float* dmsum;             // fp32 [NTG, H, K] per-chunk column sums of dm (subtract_mean)
+  void* dzh;                // bf16 [tokens, H, K] dz_t = F_t dqc_t, hi (nullable: the walks form dz)
+  void* dzl;                // bf16 [tokens, H, K] low part
   float* dh0;               // fp32 [N, H, K, K] (nullable)
   float* dm0;               // fp32 [N, H, K] (nullable)
   int T, H, N, NT, NTG, K, pos_off, subtract_mean;
