@@ -1552,6 +1552,275 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
+// cw_dk for K <= 128 (64-token chunks) with 8 wavefronts, reverse walk of E = G + G^T.  Waves 0-3
+// (output waves) compute the score tiles and the dk rows; waves 4-7 (state waves) hold E[:, cols]
+// (and G when DH0) as 16x16 tiles (rows [K/4 (w-4), +K/4)), load the chunk operands one chunk ahead
+// and update the state.  Three barriers per chunk, one LDS buffer per tile:
+//   stage    state waves: Q, K, dZ (the hi/lo pair written by cw_rows), row scalars, dk_extra
+//            columns, carry; E^T (hi/lo) of the later chunks
+//   phase 1  output waves: B1[j][t] = dz_t . k_j, B2[j][t] = q_t . k_j (t >= j) as 16x16 tiles;
+//            state waves: loads of chunk c-1, E += Q^T dZ[:, cols] + dZ^T Q[:, cols] (G += Q^T dZ)
+//            with transposing LDS reads
+//   phase 2  output waves: dk = K E + (B1 + ds) Q[:, cols] + (B2 - s/pos) dZ[:, cols] + carry
+//            (+ dk_extra); the masked diagonal terms enter as their own hi/lo fragments
+// ===========================================================================
+template <int K, bool DH0, bool MEAN>
+__global__ __launch_bounds__(kWalk8) void cw_dk_v3_kernel(const WalkArgs a) {
+  constexpr int CB = 64, LDK = K + 16, LDA = CB + 16, LDX = 32 + 4, NM = 256;
+  constexpr int RW = K / 4, NR16 = RW / 16;
+  __shared__ __attribute__((aligned(16))) bf16 sQ[CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sK[CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sZh[CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sZl[CB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sEh[32 * LDK];    // E^T [col][row], hi
+  __shared__ __attribute__((aligned(16))) bf16 sEl[32 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sB1h[CB * LDA];   // [j][t] = dz_t . k_j (t >= j), hi
+  __shared__ __attribute__((aligned(16))) bf16 sB1l[CB * LDA];
+  __shared__ __attribute__((aligned(16))) bf16 sB2h[CB * LDA];   // [j][t] = q_t . k_j (t >= j), hi
+  __shared__ __attribute__((aligned(16))) bf16 sB2l[CB * LDA];
+  __shared__ __attribute__((aligned(16))) float sX[CB * LDX];    // dk_extra[t][cols]
+  __shared__ __attribute__((aligned(16))) float sDs[CB], sSp[CB];  // ds_t, -s_t/pos_t
+  __shared__ __attribute__((aligned(16))) float sCar[32];          // carry of this chunk
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const WalkUnit u = walk_unit<K>(a);
+  constexpr bool mean = MEAN;
+  auto chunk_len = [&](int c) { return min(CB, u.len - c * CB); };
+
+  if (w >= 4) {
+    // ---- state waves
+    const int lm = tid - NM, sw = w - 4;
+    f32x4 E[NR16][2], G[NR16][2];  // G is dead unless DH0
+#pragma unroll
+    for (int rt = 0; rt < NR16; ++rt) {
+      const int kr = RW * sw + 16 * rt + 4 * (l >> 4);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const int cc = u.c0 + 16 * ct + (l & 15);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float* dhf = a.dh_fin ? a.dh_fin + (long)u.unit * K * K : nullptr;
+          const float g = dhf ? dhf[(long)(kr + i) * K + cc] : 0.f;
+          const float gt = dhf ? dhf[(long)cc * K + kr + i] : 0.f;
+          G[rt][ct][i] = g;
+          E[rt][ct][i] = g + gt;
+        }
+      }
+    }
+    float car = (lm < 32 && mean && a.dm_fin) ? a.dm_fin[(long)u.unit * K + u.c0 + lm] : 0.f;
+    RowsBf16<K, CB, NM> pq, pk, pzh, pzl;
+    RowsF32<32, CB, NM> px;
+    f32x4 prow = f32x4{};
+    float pdm = 0.f;
+    auto load = [&](int c) {
+      const int L = chunk_len(c);
+      const long off = u.hb + (long)c * CB * u.rs;
+      const long ti0 = (u.bos + (long)c * CB) * a.H + u.h;
+      pq.load((const bf16*)a.q + off, u.rs, L, lm);
+      pk.load((const bf16*)a.k + off, u.rs, L, lm);
+      pzh.load((const bf16*)a.dzh + off, u.rs, L, lm);
+      pzl.load((const bf16*)a.dzl + off, u.rs, L, lm);
+      if (a.dk_extra) px.load(a.dk_extra + off + u.c0, u.rs, L, lm);
+      prow = *gmem((const f32x4*)(a.sc + (ti0 + (long)min(lm & (CB - 1), L - 1) * a.H) * 4));
+      if (mean) pdm = a.dmsum[((long)(u.gc0 + c) * a.H + u.h) * K + u.c0 + (lm & 31)];
+    };
+    const int cl = u.nc - 1;
+    if (u.nc > 0) load(cl);
+    for (int c = cl; c >= 0; --c) {
+      const int L = chunk_len(c);
+      // ---- stage
+      pq.store(sQ, LDK, L, lm);
+      pk.store(sK, LDK, L, lm);
+      pzh.store(sZh, LDK, L, lm);
+      pzl.store(sZl, LDK, L, lm);
+      if (a.dk_extra) px.store(sX, LDX, L, lm);
+      if (lm < CB) {
+        sDs[lm] = lm < L ? prow[1] : 0.f;
+        sSp[lm] = lm < L ? prow[3] : 0.f;
+      }
+      if (lm < 32) {
+        sCar[lm] = car;
+        car += pdm;
+      }
+#pragma unroll
+      for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+          acc16_to_lds_t(E[rt][ct], sEh + 16 * ct * LDK, sEl + 16 * ct * LDK, LDK, RW * sw + 16 * rt);
+      __syncthreads();
+      // ---- phase 1: loads of chunk c-1 (chunk 0 again at the start: every pass issues the same
+      // memory operations), state update
+      load(max(c - 1, 0));
+#pragma unroll
+      for (int t0 = 0; t0 < CB; t0 += 32) {
+        bf16x8 qc[2], zch[2], zcl[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          qc[ct] = frag16_tr(sQ + t0 * LDK + u.c0 + 16 * ct, LDK);
+          zch[ct] = frag16_tr(sZh + t0 * LDK + u.c0 + 16 * ct, LDK);
+          zcl[ct] = frag16_tr(sZl + t0 * LDK + u.c0 + 16 * ct, LDK);
+        }
+#pragma unroll
+        for (int rt = 0; rt < NR16; ++rt) {
+          const int m0 = RW * sw + 16 * rt;
+          const bf16x8 qr = frag16_tr(sQ + t0 * LDK + m0, LDK);
+          const bf16x8 zrh = frag16_tr(sZh + t0 * LDK + m0, LDK), zrl = frag16_tr(sZl + t0 * LDK + m0, LDK);
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) {
+            if constexpr (DH0) {
+              G[rt][ct] = mfma16(qr, zch[ct], G[rt][ct]);
+              G[rt][ct] = mfma16(qr, zcl[ct], G[rt][ct]);
+            }
+            E[rt][ct] = mfma16(qr, zch[ct], E[rt][ct]);
+            E[rt][ct] = mfma16(qr, zcl[ct], E[rt][ct]);
+            E[rt][ct] = mfma16(zrh, qc[ct], E[rt][ct]);
+            E[rt][ct] = mfma16(zrl, qc[ct], E[rt][ct]);
+          }
+        }
+      }
+      __syncthreads();
+      __syncthreads();
+    }
+    if constexpr (DH0) {
+#pragma unroll
+      for (int rt = 0; rt < NR16; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            a.dh0[((long)u.unit * K + RW * sw + 16 * rt + 4 * (l >> 4) + i) * K + u.c0 + 16 * ct + (l & 15)] =
+                G[rt][ct][i];
+    }
+    if (a.dm0 && lm < 32) a.dm0[(long)u.unit * K + u.c0 + lm] = mean ? car : 0.f;
+    return;
+  }
+
+  // ---- output waves
+  // score tile pairs of wave w: entries w, w + 4, w + 8 of (T, J) = (0,0) (1,0) (1,1) (2,0) (2,1)
+  // (2,2) (3,0) (3,1) (3,2) (3,3) (T = t tile, J = j tile, T >= J); waves 2 and 3 compute a third
+  // pair that they discard.  Tiles (J, T) = (1, 0) and (3, 2) are read by the 32-wide steps of
+  // phase 2 and stay zero.
+  int tT[3], tJ[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int e = w + 4 * j < 10 ? w + 4 * j : 0;
+    tT[j] = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
+    tJ[j] = e - tT[j] * (tT[j] + 1) / 2;
+  }
+  const bool third = w < 2;
+  for (int i = tid; i < 2 * 16 * 16; i += NM) {
+    const int tile = i / 256, e = i % 256, rr = e / 16, cc = e % 16;
+    const int J = tile == 0 ? 1 : 3, T = J - 1;
+    const int o = (16 * J + rr) * LDA + 16 * T + cc;
+    sB1h[o] = (bf16)0.f;
+    sB1l[o] = (bf16)0.f;
+    sB2h[o] = (bf16)0.f;
+    sB2l[o] = (bf16)0.f;
+  }
+  for (int c = u.nc - 1; c >= 0; --c) {
+    const int t0c = c * CB, L = chunk_len(c);
+    __syncthreads();
+    // ---- phase 1: score tiles, element (t, j) = (16 T + 4 (l >> 4) + i, 16 J + (l & 15)), kept for
+    // t >= j, written transposed to [j][t]
+    {
+      f32x4 b1[3], b2[3];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) b1[j] = b2[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k0 = 0; k0 < K; k0 += 32)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const bf16x8 kf = frag16_rm(sK + 16 * tJ[j] * LDK + k0, LDK);
+          b1[j] = mfma16(frag16_rm(sZh + 16 * tT[j] * LDK + k0, LDK), kf, b1[j]);
+          b1[j] = mfma16(frag16_rm(sZl + 16 * tT[j] * LDK + k0, LDK), kf, b1[j]);
+          b2[j] = mfma16(frag16_rm(sQ + 16 * tT[j] * LDK + k0, LDK), kf, b2[j]);
+        }
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        if (j < 2 || third) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (tT[j] == tJ[j] && 4 * (l >> 4) + i < (l & 15)) b1[j][i] = b2[j][i] = 0.f;
+          acc16_to_lds_t(b1[j], sB1h + 16 * tJ[j] * LDA, sB1l + 16 * tJ[j] * LDA, LDA, 16 * tT[j]);
+          acc16_to_lds_t(b2[j], sB2h + 16 * tJ[j] * LDA, sB2l + 16 * tJ[j] * LDA, LDA, 16 * tT[j]);
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- phase 2: dk rows j in [16 w, 16 w + 16)
+    f32x4 x[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      const bf16x8 kf = frag16_rm(sK + 16 * w * LDK + k0, LDK);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        x[ct] = mfma16(kf, frag16_rm(sEh + 16 * ct * LDK + k0, LDK), x[ct]);
+        x[ct] = mfma16(kf, frag16_rm(sEl + 16 * ct * LDK + k0, LDK), x[ct]);
+      }
+    }
+    const int tmin = w < 2 ? 0 : 32;
+    for (int t0 = tmin; t0 < CB; t0 += 32) {
+      const bf16x8 b1h = frag16_rm(sB1h + 16 * w * LDA + t0, LDA), b1l = frag16_rm(sB1l + 16 * w * LDA + t0, LDA);
+      const bf16x8 b2h = frag16_rm(sB2h + 16 * w * LDA + t0, LDA), b2l = frag16_rm(sB2l + 16 * w * LDA + t0, LDA);
+      // masked diagonals: row j = 16 w + (l & 15), column t = t0 + 8 (l >> 4) + i: ds_t [t >= j]
+      // against q, -s_t/pos_t [t >= j] against dz
+      bf16x8 dh, dl, ph, pl;
+      if (mean) {
+        const int tb = t0 + 8 * (l >> 4), jr = 16 * w + (l & 15);
+        const f32x4 d0 = *(const f32x4*)(sDs + tb), d1 = *(const f32x4*)(sDs + tb + 4);
+        const f32x4 p0 = *(const f32x4*)(sSp + tb), p1 = *(const f32x4*)(sSp + tb + 4);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const bool keep = tb + i >= jr;
+          bf16 a1, a2, a3, a4;
+          split2(keep ? (i < 4 ? d0[i] : d1[i - 4]) : 0.f, a1, a2);
+          split2(keep ? (i < 4 ? p0[i] : p1[i - 4]) : 0.f, a3, a4);
+          dh[i] = a1;
+          dl[i] = a2;
+          ph[i] = a3;
+          pl[i] = a4;
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x8 qf = frag16_tr(sQ + t0 * LDK + u.c0 + 16 * ct, LDK);
+        const bf16x8 zhf = frag16_tr(sZh + t0 * LDK + u.c0 + 16 * ct, LDK);
+        const bf16x8 zlf = frag16_tr(sZl + t0 * LDK + u.c0 + 16 * ct, LDK);
+        x[ct] = mfma16(b1h, qf, x[ct]);
+        x[ct] = mfma16(b1l, qf, x[ct]);
+        x[ct] = mfma16(b2h, zhf, x[ct]);
+        x[ct] = mfma16(b2h, zlf, x[ct]);
+        x[ct] = mfma16(b2l, zhf, x[ct]);
+        if (mean) {
+          x[ct] = mfma16(dh, qf, x[ct]);
+          x[ct] = mfma16(dl, qf, x[ct]);
+          x[ct] = mfma16(ph, zhf, x[ct]);
+          x[ct] = mfma16(ph, zlf, x[ct]);
+          x[ct] = mfma16(pl, zhf, x[ct]);
+        }
+      }
+    }
+    const int jb = 16 * w + 4 * (l >> 4);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int cc = 16 * ct + (l & 15);
+      const float car = sCar[cc];
+      const long base = u.hb + (long)(t0c + jb) * u.rs + u.c0 + cc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (jb + i < L) {
+          const float d = x[ct][i] + car + (a.dk_extra ? sX[(jb + i) * LDX + cc] : 0.f);
+          if (a.dk32) gmem(a.dk32)[base + i * u.rs] = d;
+          else gmem((bf16*)a.dk)[base + i * u.rs] = (bf16)d;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
 // launcher
 // ===========================================================================
 namespace {
@@ -1599,8 +1868,19 @@ hipError_t cwalk_k(int stage, const WalkArgs& a, hipStream_t st) {
       break;
     case kWalkDk:
       if (units > 0) {
-        if (a.dh0) hipLaunchKernelGGL((cw_dk_kernel<K, true>), dim3((unsigned)units), dim3(kThreads), 0, st, a);
-        else hipLaunchKernelGGL((cw_dk_kernel<K, false>), dim3((unsigned)units), dim3(kThreads), 0, st, a);
+        if (K == 64 || K == 128) {
+          constexpr int KW = K == 64 ? 64 : 128;
+          const dim3 grid((unsigned)units), block(kWalk8);
+          const bool dh0 = a.dh0 != nullptr, mean = a.subtract_mean != 0;
+          if (dh0 && mean) hipLaunchKernelGGL((cw_dk_v3_kernel<KW, true, true>), grid, block, 0, st, a);
+          else if (dh0) hipLaunchKernelGGL((cw_dk_v3_kernel<KW, true, false>), grid, block, 0, st, a);
+          else if (mean) hipLaunchKernelGGL((cw_dk_v3_kernel<KW, false, true>), grid, block, 0, st, a);
+          else hipLaunchKernelGGL((cw_dk_v3_kernel<KW, false, false>), grid, block, 0, st, a);
+        } else if (a.dh0) {
+          hipLaunchKernelGGL((cw_dk_kernel<K, true>), dim3((unsigned)units), dim3(kThreads), 0, st, a);
+        } else {
+          hipLaunchKernelGGL((cw_dk_kernel<K, false>), dim3((unsigned)units), dim3(kThreads), 0, st, a);
+        }
       }
       break;
     default:
