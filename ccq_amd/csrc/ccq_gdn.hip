@@ -1765,6 +1765,305 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_v2_kernel(const GdnArgs
 }
 
 // ===========================================================================
+// gdn_bwd_dqkw for K = 128 on 8 waves: one workgroup per (chunk, head) instead of one per 64-column
+// key tile.  Waves 0-3 (group 0) and 4-7 (group 1) each run the per-tile computation of
+// gdn_bwd_dqkw_v2_kernel for key columns [64 g, 64 g + 64); the value-side tiles (dO, U, dU), the
+// product dP = dO U^T with its masked, decayed form dPs and the decay terms of P are staged or
+// computed once and shared.  Each group writes its own decay-gradient partial.
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v3_kernel(const GdnArgs a, const int V) {
+  static_assert(K == 128, "two key tiles of 64");
+  constexpr int LDB = 64 + 8, LDE = 64 + 4, TILE = 64 * LDB, NG = 2;
+  constexpr long kLoop = (4L * NG + 5) * TILE * 2;
+  constexpr long kPost = (2L + 3 * NG) * TILE * 2 + (NG + 1L) * 64 * LDE * 4;
+  constexpr long kBytes = kLoop > kPost ? kLoop : kPost;
+  __shared__ __attribute__((aligned(16))) char region[kBytes];
+  __shared__ __attribute__((aligned(16))) float sG[BT], sGam[BT], sFac[BT];
+  __shared__ __attribute__((aligned(16))) float sDG[NG][BT], sTerm[NG][BT], sMisc[NG][8];
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const int g = w >> 2, gw = w & 3, gt = tid & 255;  // group (key tile), wave and thread in the group
+  const int gc = blockIdx.y, h = blockIdx.z;
+  int n, c0, L;
+  long bos;
+  if (!chunk_info(a, gc, n, c0, bos, L)) return;
+  const long tok0 = bos + c0;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  const int k0c = g * 64;
+  // loop views: shared value-side tiles, then four state tiles per group
+  bf16* sdO = (bf16*)region;   // dO [t][v]
+  bf16* sUh = sdO + TILE;      // U [t][v]
+  bf16* sUl = sUh + TILE;
+  bf16* sdUh = sUl + TILE;     // dU [t][v]
+  bf16* sdUl = sdUh + TILE;
+  bf16* sHk = sdUl + TILE + g * 4 * TILE;  // h^T tile as [k][v]
+  bf16* sHkl = sHk + TILE;
+  bf16* sDk = sHkl + TILE;                 // dS'^T tile as [k][v]
+  bf16* sDkl = sDk + TILE;
+  // post views (same region)
+  bf16* sPh = (bf16*)region;   // dPs^T [s][t] (shared)
+  bf16* sPl = sPh + TILE;
+  bf16* sQh = sPl + TILE + g * 3 * TILE;  // Qc^T [k][t] of this group's columns
+  bf16* sQl = sQh + TILE;
+  bf16* sKt = sQl + TILE;                 // K^T [k][t]
+  float* sEall = (float*)(region + (2L + 3 * NG) * TILE * 2);
+  float* sE = sEall + g * 64 * LDE;       // [64][LDE] products for row / column sums
+  float* sPT = sEall + NG * 64 * LDE;     // P^T [s][t]
+
+  const int tr = (gw >> 1) * 32, tc = (gw & 1) * 32;
+  const int pr = (gw == 0) ? 0 : 32, pc = (gw == 2) ? 32 : 0;
+  f32x16 dQi = zero16(), dKs = zero16(), dW = zero16(), dP = zero16();
+  float hds = 0.f;
+
+  PatchBf16<64, 64> pH, pHl, pD, pDl;
+  RowsBf16<64, 64, 256> pO;
+  PrefetchF32Split<64, 64> pU;  // group 0: U, group 1: dU
+  PatchF32<64, 64> pQ;
+  PatchBf16<64, 64> pK;
+  RowsF32<BT, BT, 256> pP;
+  float pgl = 0.f, pgt = 0.f;
+  auto issue_loop = [&](int v0) {
+    const long so = (((long)gc * a.H + h) * V + v0) * K + k0c;
+    pH.load((const bf16*)a.hT + so, K, 64, gt);
+    pHl.load((const bf16*)a.hTl + so, K, 64, gt);
+    pD.load((const bf16*)a.dhT + so, K, 64, gt);
+    pDl.load((const bf16*)a.dhTl + so, K, 64, gt);
+    if (g == 0) {
+      pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L, gt);
+      pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, gt, L);
+    } else {
+      pU.load(a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, gt, L);
+    }
+  };
+  auto issue_post = [&]() {
+    pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + k0c : nullptr,
+            a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + k0c : nullptr, rsk, L, gt);
+    pK.load((const bf16*)a.k + (tok0 * a.H + h) * K + k0c, rsk, L, gt);
+    if (g == 0) {
+      pP.load(a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT, gt);
+      if (gt < BT) {
+        pgl = a.gcum[(tok0 + L - 1) * a.H + h];
+        pgt = a.gcum[(tok0 + min(gt, L - 1)) * a.H + h];
+      }
+    }
+  };
+  issue_loop(0);
+
+  for (int v0 = 0; v0 < V; v0 += 64) {
+    pH.store_t(sHk, LDB, 64, gt);
+    pHl.store_t(sHkl, LDB, 64, gt);
+    pD.store_t(sDk, LDB, 64, gt);
+    pDl.store_t(sDkl, LDB, 64, gt);
+    if (g == 0) {
+      pO.store(sdO, LDB, L, gt);
+      pU.store(sUh, sUl, LDB, gt, L);
+    } else {
+      pU.store(sdUh, sdUl, LDB, gt, L);
+    }
+    __syncthreads();
+    if (v0 + 64 < V) issue_loop(v0 + 64);
+    {
+      // <h, dS'> over the tile: row k = gt / 4, sixteen v per thread
+      const int kk = gt >> 2, vs = (gt & 3) * 16;
+#pragma unroll
+      for (int q = 0; q < 16; q += 8) {
+        const int e = kk * LDB + vs + q;
+        const bf16x8 x1 = *(const bf16x8*)(sHk + e), x2 = *(const bf16x8*)(sHkl + e);
+        const bf16x8 y1 = *(const bf16x8*)(sDk + e), y2 = *(const bf16x8*)(sDkl + e);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hds += ((float)x1[i] + (float)x2[i]) * ((float)y1[i] + (float)y2[i]);
+      }
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < 64; k0 += 16) {
+      const bf16x8 oa = frag_rm(sdO + tr * LDB + k0, LDB);
+      const bf16x8 hb = frag_rm(sHk + tc * LDB + k0, LDB), hbl = frag_rm(sHkl + tc * LDB + k0, LDB);
+      dQi = mfma(oa, hb, dQi);
+      dQi = mfma(oa, hbl, dQi);
+      const bf16x8 uh = frag_rm(sUh + tr * LDB + k0, LDB), ul = frag_rm(sUl + tr * LDB + k0, LDB);
+      const bf16x8 db = frag_rm(sDk + tc * LDB + k0, LDB), dbl = frag_rm(sDkl + tc * LDB + k0, LDB);
+      dKs = mfma(uh, db, dKs);
+      dKs = mfma(ul, db, dKs);
+      dKs = mfma(uh, dbl, dKs);
+      const bf16x8 dh = frag_rm(sdUh + tr * LDB + k0, LDB), dl = frag_rm(sdUl + tr * LDB + k0, LDB);
+      dW = mfma(dh, hb, dW);
+      dW = mfma(dl, hb, dW);
+      dW = mfma(dh, hbl, dW);
+      if (g == 0 && gw < 3) {
+        const bf16x8 pa = frag_rm(sdO + pr * LDB + k0, LDB);
+        dP = mfma(pa, frag_rm(sUh + pc * LDB + k0, LDB), dP);
+        dP = mfma(pa, frag_rm(sUl + pc * LDB + k0, LDB), dP);
+      }
+    }
+    __syncthreads();
+  }
+  hds = group_sum(hds, 64);
+  if (l == 0) sMisc[g][gw] = hds;
+
+  // ---- post stage (the loop ended with a barrier; its tiles are dead).  Its operands are loaded
+  // here rather than during the last value block: with two waves per SIMD the registers do not
+  // hold both.
+  issue_post();
+  pQ.store_t(sQh, sQl, LDB, L, gt);
+  pK.store_t(sKt, LDB, L, gt);
+  if (g == 0) {
+    pP.store(sPT, LDE, BT, gt);
+    if (gt < BT) {
+      sG[gt] = pgt;
+      sGam[gt] = __expf(pgt);
+      sFac[gt] = __expf(pgl - pgt);
+      if (gt == 0) {
+        sMisc[0][4] = __expf(pgl);
+        sMisc[1][4] = __expf(pgl);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- dP (group 0): mask, decay terms of P, dPs^T as hi/lo
+  if (g == 0) {
+    f32x16 ps;
+    if (gw < 3) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = pr + acc_row(i), c = pc + acc_col();
+        const bool keep = r >= c;
+        dP[i] = keep ? dP[i] : 0.f;
+        ps[i] = keep ? dP[i] * a.scale * __expf(sG[r] - sG[c]) : 0.f;
+      }
+      const int c = pc + acc_col();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i4 = pr + acc_row(4 * q);
+        const f32x4 pv = *(const f32x4*)(sPT + c * LDE + i4);  // P[i][c] = P^T[c][i]
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) sE[(i4 + ii) * LDE + c] = dP[4 * q + ii] * pv[ii];
+      }
+      acc_to_lds_t(ps, sPh + pc * LDB, sPl + pc * LDB, LDB, pr);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sE[acc_row(i) * LDE + 32 + acc_col()] = 0.f;
+      acc_to_lds_t(zero16(), sPh + 32 * LDB, sPl + 32 * LDB, LDB, 0);
+    }
+  }
+  __syncthreads();
+  if (gt < 64) {
+    float s = 0.f;
+    if (g == 0) {
+#pragma unroll
+      for (int q = 0; q < 64; q += 4) {
+        const f32x4 x = *(const f32x4*)(sE + gt * LDE + q);
+        s += x[0] + x[1] + x[2] + x[3];
+      }
+    }
+    sDG[g][gt] = s;
+  } else if (gt < 128) {
+    float s = 0.f;
+    if (g == 0) {
+#pragma unroll 8
+      for (int i = 0; i < 64; ++i) s += sE[i * LDE + gt - 64];
+    }
+    sTerm[g][gt - 64] = s;
+  }
+  __syncthreads();
+
+  // ---- dq tile = scale gamma dQi + dPs K[:, tile]; decay term of O: dG_i += sum_k dQi_ik qc_ik
+  {
+    const int c = tc + acc_col();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i4 = tr + acc_row(4 * q);
+      const f32x4 gm = *(const f32x4*)(sGam + i4);
+      const bf16x4 qh4 = *(const bf16x4*)(sQh + c * LDB + i4), ql4 = *(const bf16x4*)(sQl + c * LDB + i4);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int k = 4 * q + ii;
+        dQi[k] *= a.scale * gm[ii];
+        sE[(i4 + ii) * LDE + c] = dQi[k] * ((float)qh4[ii] + (float)ql4[ii]);
+      }
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 kb = frag_rm(sKt + tc * LDB + k0, LDB);
+      dQi = mfma(frag_cm(sPh + k0 * LDB + tr, LDB), kb, dQi);
+      dQi = mfma(frag_cm(sPl + k0 * LDB + tr, LDB), kb, dQi);
+    }
+    const int r0 = tr + acc_row(0);
+    float* dq = a.dq32 + (tok0 + r0) * rsk + (long)h * K + k0c + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (r0 + acc_drow(i) < L) dq[acc_drow(i) * rsk] = dQi[i];
+  }
+  __syncthreads();
+  if (gt < 64) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 64; q += 4) {
+      const f32x4 x = *(const f32x4*)(sE + gt * LDE + q);
+      s += x[0] + x[1] + x[2] + x[3];
+    }
+    sDG[g][gt] = sDG[g][gt] - sTerm[g][gt] + s;
+  }
+  __syncthreads();
+
+  // ---- dk tile = fac dKs + dPs^T Qc[:, tile];  state-update decay term_j = sum_k fac dKs_jk k_jk
+  {
+    const int c = tc + acc_col();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i4 = tr + acc_row(4 * q);
+      const f32x4 fc = *(const f32x4*)(sFac + i4);
+      const bf16x4 k4 = *(const bf16x4*)(sKt + c * LDB + i4);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int k = 4 * q + ii;
+        dKs[k] *= fc[ii];
+        sE[(i4 + ii) * LDE + c] = dKs[k] * (float)k4[ii];
+      }
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < BT; k0 += 16) {
+      const bf16x8 ah = frag_rm(sPh + tr * LDB + k0, LDB), al = frag_rm(sPl + tr * LDB + k0, LDB);
+      const bf16x8 bh = frag_rm(sQh + tc * LDB + k0, LDB);
+      dKs = mfma(ah, bh, dKs);
+      dKs = mfma(ah, frag_rm(sQl + tc * LDB + k0, LDB), dKs);
+      dKs = mfma(al, bh, dKs);
+    }
+    const int r0 = tr + acc_row(0);
+    const long gi = (tok0 + r0) * rsk + (long)h * K + k0c + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (r0 + acc_drow(i) < L) {
+        a.dkp32[gi + acc_drow(i) * rsk] = dKs[i];
+        a.dw32[gi + acc_drow(i) * rsk] = -dW[i];
+      }
+    }
+  }
+  __syncthreads();
+  if (gt < 64) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 64; q += 4) {
+      const f32x4 x = *(const f32x4*)(sE + gt * LDE + q);
+      s += x[0] + x[1] + x[2] + x[3];
+    }
+    sTerm[g][gt] = s;  // term_j
+  }
+  __syncthreads();
+  if (gt < L) {
+    float d = sDG[g][gt] - sTerm[g][gt];
+    if (gt == L - 1) {
+      float tot = 0.f;
+      for (int j = 0; j < L; ++j) tot += sTerm[g][j];
+      d += tot + sMisc[g][4] * (sMisc[g][0] + sMisc[g][1] + sMisc[g][2] + sMisc[g][3]);
+    }
+    const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
+    a.dgp[(long)g * ntok * a.H + (tok0 + gt) * a.H + h] = d;
+  }
+}
+
+// ===========================================================================
 // gdn_bwd_wy: grid (NTG, H)  -- backward through w = T diag(beta gamma) K, u = T diag(beta) V,
 // T = (I + A)^-1, A = strict_lower(diag(beta) (K K^T o Gamma)).
 // ===========================================================================
@@ -2405,7 +2704,10 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
         hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdDqkw:
-      hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      if (K == 128)
+        hipLaunchKernelGGL(gdn_bwd_dqkw_v3_kernel<128>, dim3(1, a.NTG, a.H), dim3(kWalk8), 0, st, a, V);
+      else
+        hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdWy:
       hipLaunchKernelGGL(gdn_bwd_wy_v2_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
