@@ -72,16 +72,16 @@ MULTI_KERNEL_STAGES = ("clean_bwd_gate",)
 # reading for a known-size elementwise copy (fetch x2.000, write x1.000).  Re-measured whenever a
 # kernel changes; a stage absent here reports traffic null.
 MEASURED_TRAFFIC_BYTES = {
-    "gdn_bwd_dqkw": (1494.1e6, 419.4e6),
-    "gdn_bwd_state": (478.5e6, 402.7e6),
-    "clean_bwd_dk": (438.8e6, 67.2e6),
-    "gdn_bwd_wy": (972.1e6, 218.1e6),
-    "gdn_fwd_state": (344.1e6, 402.7e6),
-    "clean_fwd": (235.2e6, 287.3e6),
-    "clean_bwd_dq": (237.4e6, 67.9e6),
+    "gdn_bwd_wy": (972.0e6, 218.1e6),
+    "gdn_bwd_dqkw": (1174.3e6, 444.6e6),
     "gdn_fwd_o": (612.6e6, 134.4e6),
+    "clean_bwd_dk": (438.5e6, 67.1e6),
+    "gdn_bwd_state": (478.4e6, 402.7e6),
+    "clean_bwd_dq": (371.4e6, 67.1e6),
+    "gdn_fwd_state": (344.2e6, 402.7e6),
     "gdn_prep": (151.3e6, 343.9e6),
-    "clean_bwd_rows": (491.7e6, 12.8e6),
+    "clean_fwd": (144.7e6, 287.3e6),
+    "clean_bwd_rows": (496.1e6, 152.7e6),
 }
 
 
@@ -93,7 +93,7 @@ def kernel_work(k=K, v=V, bt=BT, cb=64):
     forward / dq, four in the dk walk with a second K x K update)."""
     return {
         "clean_fwd": (4 * k * k + 2 * k * cb, 2 * k + 2 * k + 4 + 4 * k + 4 * k + 4 + 4 * k // cb),
-        "clean_bwd_rows": (6 * k, 4 * k + 4 * k + 2 * k + 2 * k + 4 + 4 + 4 * k // cb + 16 + 4 * k // cb),
+        "clean_bwd_rows": (6 * k, 4 * k + 4 * k + 2 * k + 2 * k + 4 + 4 + 4 * k // cb + 16 + 4 * k // cb + 4 * k),
         "clean_bwd_dq": (4 * k * k + 2 * k * cb, 4 * k + 2 * k + 16 + 4 * k // cb + 2 * k),
         "clean_bwd_dk": (6 * k * k + 4 * k * cb, 2 * k + 2 * k + 4 * k + 16 + 4 * k + 2 * k),
         "gdn_prep": (2 * bt * (2 * k + v) + (2 * bt * bt) // 3, 2 * k + 2 * v + 8 + 2 * k + 4 * v + 4 + 4 * bt),
