@@ -72,16 +72,15 @@ MULTI_KERNEL_STAGES = ("clean_bwd_gate",)
 # reading for a known-size elementwise copy (fetch x2.000, write x1.000).  Re-measured whenever a
 # kernel changes; a stage absent here reports traffic null.
 MEASURED_TRAFFIC_BYTES = {
-    "gdn_bwd_wy": (972.0e6, 218.1e6),
-    "gdn_bwd_dqkw": (1174.3e6, 444.6e6),
-    "gdn_fwd_o": (612.6e6, 134.4e6),
+    "gdn_bwd_wy": (973.3e6, 218.1e6),
+    "gdn_bwd_dqkw": (1174.1e6, 444.6e6),
     "clean_bwd_dk": (438.5e6, 67.1e6),
+    "gdn_fwd_state": (478.5e6, 537.5e6),
     "gdn_bwd_state": (478.4e6, 402.7e6),
     "clean_bwd_dq": (371.4e6, 67.1e6),
-    "gdn_fwd_state": (344.2e6, 402.7e6),
     "gdn_prep": (151.3e6, 343.9e6),
-    "clean_fwd": (144.7e6, 287.3e6),
-    "clean_bwd_rows": (496.1e6, 152.7e6),
+    "clean_fwd": (144.0e6, 287.3e6),
+    "clean_bwd_rows": (496.2e6, 152.4e6),
 }
 
 
@@ -97,8 +96,11 @@ def kernel_work(k=K, v=V, bt=BT, cb=64):
         "clean_bwd_dq": (4 * k * k + 2 * k * cb, 4 * k + 2 * k + 16 + 4 * k // cb + 2 * k),
         "clean_bwd_dk": (6 * k * k + 4 * k * cb, 2 * k + 2 * k + 4 * k + 16 + 4 * k + 2 * k),
         "gdn_prep": (2 * bt * (2 * k + v) + (2 * bt * bt) // 3, 2 * k + 2 * v + 8 + 2 * k + 4 * v + 4 + 4 * bt),
-        "gdn_fwd_state": (4 * k * v, 4 * k + 4 * v + 4 * v + 4 * k * v // bt),
-        "gdn_fwd_o": (2 * bt * k + 2 * k * v + 2 * bt * v, 4 * k + 2 * k + 2 * k * v // bt + 4 * v + 2 * v + 4 * bt),
+        # the forward walk with the chunk output fused in: state path (U = u - w S, S update) plus
+        # Y = Qc S, P = Qc K^T and P U; reads k, w / wl, Qc (fp32), g, u; writes U, o, P^T and the
+        # per-chunk state snapshots (hi/lo)
+        "gdn_fwd_state": (4 * k * v + 2 * bt * k + 2 * k * v + 2 * bt * v,
+                          2 * k + 4 * k + 4 * k + 4 + 4 * v + 4 * v + 2 * v + 4 * bt + 4 * k * v // bt),
         "gdn_bwd_state": (2 * bt * v + 6 * k * v, 4 * bt + 2 * v + 2 * k + 4 * k + 2 * k + 4 * v + 4 * k * v // bt),
         "gdn_bwd_dqkw": (6 * k * v + 2 * bt * v + 4 * bt * k,
                          8 * k * v // bt + 2 * v + 4 * v + 4 * v + 4 * k + 2 * k + 4 * bt + 12 * k + 4),

@@ -425,7 +425,9 @@ int ccq_gdn_fwd(const void* q, const float* q_f32, const void* k, const void* v,
   hipStream_t st = (hipStream_t)stream;
   static const char* names[] = {"gdn_prep", "gdn_fwd_state", "gdn_fwd_o"};
   const int stages[] = {kGdnPrep, kGdnFwdState, kGdnFwdO};
-  for (int i = 0; i < 3; ++i) {
+  // for K <= 128 the forward walk also writes the output (no separate output pass)
+  const int nst = K <= 128 ? 2 : 3;
+  for (int i = 0; i < nst; ++i) {
     if (int s = hip_status(timed(names[i], st, [&] { return launch_gdn_stage(stages[i], a, K, V, st); }), names[i]))
       return s;
   }

@@ -424,33 +424,50 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
 }
 
 // ===========================================================================
-// gdn_fwd_state for K <= 128 with 8 wavefronts: waves 0-3 compute and issue no global access inside
-// the walk; waves 4-7 move memory two chunks ahead of its use.  Per chunk c:
-//   phase A  compute: U = u - w S (16x16 tiles, hi/lo operands), U rows (fp32) and (fac U)^T
-//                     (hi/lo) to LDS
-//            memory:  k of c to LDS (row-major); loads of k(c+2); state snapshot S_c to HBM
+// gdn_fwd_state for K <= 128 with 8 wavefronts, with the chunk output fused in: waves 0-3 compute
+// and issue no global access inside the walk; waves 4-7 move memory one or two chunks ahead of its
+// use and write every result row.  Compute wave w owns query / U rows [16 w, 16 w + 16) of every
+// chunk.  Per chunk c:
+//   phase A  compute: U = u - w S and Y = Qc S with the previous state (16x16 tiles, hi/lo
+//                     operands sharing the state fragments); U over u in LDS, (fac U)^T and U^T
+//                     (hi/lo) to LDS; the Qc fragments stay in registers
+//            memory:  k of c+1 to LDS (k and g in two buffers by chunk parity); loads of k(c+2);
+//                     state snapshot S_c and the output rows of c-1 to HBM
 //   phase B  compute: S <- gamma_L S + K^T diag(fac) U (K^T fragments by transposing LDS reads),
-//                     S^T (hi/lo) to LDS for chunk c+1
-//            memory:  w, wl, u, fac of c+1 to LDS; U rows of c to HBM; loads of w, wl, u, g(c+3)
+//                     S^T (hi/lo) to LDS for chunk c+1; P^T = K Qc^T for the wave's rows, masked to
+//                     s <= t and scaled by scale exp(g_t - g_s) (to HBM, one key tile per value
+//                     block); O = scale gamma_t Y + P U to LDS (bf16)
+//            memory:  U rows of c to HBM; w, wl, Qc (hi/lo), u, g of c+1 to LDS; loads of Qc(c+2)
+//                     and w, wl, u, g(c+3)
+// P never leaves the registers of the wave that forms it: its C tiles (lane = query row, four key
+// rows per lane group) feed the A operand of P U directly, with the contraction index permuted the
+// same way in the U^T operand (two 8-byte reads per lane).  Result rows leave through LDS as whole
+// 16-byte pieces: scattered 2- and 4-byte stores from the compute waves stall the shared
+// vector-memory path.
 // LDS pitches: tiles read as mfma16 operands are K + 16 (or 64 + 16) elements wide, which keeps those
-// reads free of bank conflicts; rows are written by 16 consecutive lanes per row.
+// reads free of bank conflicts; rows are written by 16 consecutive lanes per row.  For K = 128 the
+// buffers fill the 160 KiB of LDS.
 // ===========================================================================
-template <int K>
+template <int K, bool Q32>
 __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs a, const int V) {
-  constexpr int VB = 32, LDK = K + 16, LDB = BT + 16, LDV = VB + 4;
+  constexpr int VB = 32, LDK = K + 16, LDB = BT + 16, LDV = VB + 4, LDO = VB + 4;
   constexpr int NM = 256;               // memory threads
   constexpr int RW = K / 4, NR16 = RW / 16;  // S rows per compute wave, in 16-row tiles
+  constexpr int NK32 = K / 32, NT16 = BT / 16;
   __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sWl[BT * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sK[BT * LDK];    // k [t][k]
+  __shared__ __attribute__((aligned(16))) bf16 sQh[BT * LDK];   // Qc [t][k], hi
+  __shared__ __attribute__((aligned(16))) bf16 sQl[BT * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sK[2 * BT * LDK];  // k [t][k], by chunk parity
   __shared__ __attribute__((aligned(16))) bf16 sSh[VB * LDK];   // S^T [v][k], hi
   __shared__ __attribute__((aligned(16))) bf16 sSl[VB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sUh[VB * LDB];   // (fac U)^T [v][t], hi
   __shared__ __attribute__((aligned(16))) bf16 sUl[VB * LDB];
-  __shared__ __attribute__((aligned(16))) float sU[BT * LDV];   // u [t][v]
-  __shared__ __attribute__((aligned(16))) float sUo[BT * LDV];  // U [t][v]
-  __shared__ __attribute__((aligned(16))) float sFac[BT];       // exp(g_L - g_t), 0 beyond the chunk
-  __shared__ float sGL[1];
+  __shared__ __attribute__((aligned(16))) bf16 sVh[VB * LDB];   // U^T [v][t], hi
+  __shared__ __attribute__((aligned(16))) bf16 sVl[VB * LDB];
+  __shared__ __attribute__((aligned(16))) float sU[BT * LDV];   // u [t][v], then U
+  __shared__ __attribute__((aligned(16))) bf16 sO[BT * LDO];    // O [t][v]
+  __shared__ __attribute__((aligned(16))) float sG[2 * BT];     // g_t (the last token's beyond the chunk), by chunk parity
 
   // the wave index as a wave-uniform value: the role branches are then uniform, and the wait
   // counts of one role's memory operations never merge with the other role's path
@@ -478,9 +495,11 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) S[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // memory waves: operands two chunks ahead, in two register sets used by chunk parity
-  RowsBf16<K, BT, NM> pw[2], pwl[2], pk[2];
+  // memory waves: w, wl, u, g two chunks ahead in two register sets used by chunk parity; k and Qc
+  // one chunk ahead
+  RowsBf16<K, BT, NM> pw[2], pwl[2], pk;
   RowsF32<VB, BT, NM> pu[2];
+  RowsF32<K, BT, NM> pq;
   float pg[2] = {0.f, 0.f};
   auto load_wug = [&](int c, auto P) {
     constexpr int p = decltype(P)::value;
@@ -491,50 +510,64 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
     pu[p].load(a.u + (tok0 * a.H + h) * (long)V + v0, rsv, L, lm);
     pg[p] = a.gcum[(tok0 + min(lm & (BT - 1), L - 1)) * a.H + h];
   };
-  auto load_k = [&](int c, auto P) {
-    constexpr int p = decltype(P)::value;
-    pk[p].load((const bf16*)a.k + (tok_of(c) * a.H + h) * K, rsk, chunk_len(c), lm);
+  auto load_q = [&](int c) {
+    const long o = (tok_of(c) * a.H + h) * K;
+    if (Q32)
+      pq.load(a.qc32 + o, rsk, chunk_len(c), lm);
+    else
+      pq.load(nullptr, (const bf16*)a.qc16 + o, rsk, chunk_len(c), lm);
   };
-  // w, wl, u, fac of chunk c to LDS (lane t of every memory wave holds g of token t of the chunk;
-  // wave 4 writes the factors)
+  auto load_k = [&](int c) { pk.load((const bf16*)a.k + (tok_of(c) * a.H + h) * K, rsk, chunk_len(c), lm); };
+  // w, wl, Qc, u, g of chunk c to LDS (lane t of every memory wave holds g of token t of the chunk;
+  // wave 4 writes g); g goes to the buffer of the chunk's parity P
   auto stage_wug = [&](int c, auto P) {
     constexpr int p = decltype(P)::value;
     const int L = chunk_len(c);
     pw[p].store(sW, LDK, L, lm);
     pwl[p].store(sWl, LDK, L, lm);
+    pq.store_split(sQh, sQl, LDK, L, lm);
     pu[p].store(sU, LDV, L, lm);
-    const float pgl = __shfl(pg[p], L - 1);
-    const float fac = l < L ? __expf(pgl - pg[p]) : 0.f;
-    if (w == 4) {
-      sFac[l] = fac;
-      if (l == 0) sGL[0] = __expf(pgl);
-    }
+    if (w == 4) sG[p * BT + l] = pg[p];
+  };
+  // output rows of chunk c (bf16, 64 bytes per row and value block) from LDS to HBM: one 16-byte
+  // piece per memory thread; rows past the chunk write row L - 1 again (same value, same address), so
+  // every pass issues the same stores
+  auto store_o = [&](int c) {
+    const int r = min(lm >> 2, chunk_len(c) - 1), cc = (lm & 3) * 8;
+    const bf16* src = sO + r * LDO + cc;
+    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+    const bf16x8 o8 = __builtin_shufflevector(*(const b4*)src, *(const b4*)(src + 4), 0, 1, 2, 3, 4, 5, 6, 7);
+    *(bf16x8*)(gmem((bf16*)a.o) + (tok_of(c) + r) * rsv + (long)h * V + v0 + cc) = o8;
   };
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
 
   // Each role runs its own loop (both pass the same 1 + 2 nc barriers), so the compiler's wait
-  // counts for the memory waves follow their own sequence of operations only.  Loads are
-  // unconditional (the last chunk again past the end): every pass issues the same memory
-  // operations, so each wait counts exactly the younger ones.
+  // counts for the memory waves follow their own sequence of operations only.  Loads and stores
+  // are unconditional (the last chunk again past the end, row L - 1 again past the chunk): every
+  // pass issues the same memory operations, so each wait counts exactly the younger ones.
   if (mem) {
     const int cl = nc - 1;
     if (nc > 0) {
       load_wug(0, P0{});
-      load_k(0, P0{});
-      load_k(min(1, cl), P1{});
+      load_q(0);
+      load_k(0);
       load_wug(min(1, cl), P1{});
       stage_wug(0, P0{});
+      pk.store(sK, LDK, chunk_len(0), lm);
+      load_q(min(1, cl));
+      load_k(min(1, cl));
       load_wug(min(2, cl), P0{});
     }
     __syncthreads();
-    // chunk c with register sets P = c % 2 (k) and Q = (c + 1) % 2 (w, wl, u, g)
-    auto chunk = [&](int c, auto P, auto Q) {
-      const int L = chunk_len(c), gc = gc0 + c;
+    // chunk c with register set Q = (c + 1) % 2 (w, wl, u, g of chunk c + 1 on entry)
+    auto chunk = [&](int c, auto Q) {
+      constexpr int q = decltype(Q)::value;
+      const int gc = gc0 + c, L = chunk_len(c);
       const long tok0 = tok_of(c);
-      // ---- phase A: k of c; loads of k(c+2); snapshot S_c
-      pk[decltype(P)::value].store(sK, LDK, L, lm);
-      load_k(min(c + 2, cl), P);
+      // ---- phase A: k of c+1 to its buffer; loads of k(c+2); snapshot S_c; output rows of c-1
+      pk.store(sK + q * (BT * LDK), LDK, chunk_len(min(c + 1, cl)), lm);
+      load_k(min(c + 2, cl));
       constexpr int VPR = K / 8;
 #pragma unroll
       for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
@@ -545,16 +578,24 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
         bf16* dst = which ? (bf16*)a.hTl : (bf16*)a.hT;
         *(bf16x8*)(gmem(dst) + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
       }
+      store_o(max(c - 1, 0));
       __syncthreads();
-      // ---- phase B: w, wl, u, fac of c+1 first (the wait for their loads then covers no store);
-      // U rows of c to HBM; loads of w, wl, u, g(c+3)
+      // ---- phase B: U rows of c (read before u of c+1 replaces them: each thread reads exactly the
+      // pieces it overwrites), w, wl, Qc, u, g of c+1; loads of Qc(c+2) and w, wl, u, g(c+3)
+      constexpr int NU = (BT * VB / 4) / NM;
+      f32x4 urow[NU];
+#pragma unroll
+      for (int j = 0; j < NU; ++j) {
+        const int idx = lm + j * NM, r = idx / (VB / 4), cc = (idx % (VB / 4)) * 4;
+        urow[j] = *(const f32x4*)(sU + min(r, L - 1) * LDV + cc);
+      }
       stage_wug(min(c + 1, cl), Q);
 #pragma unroll
-      for (int j = 0; j < (BT * VB / 4) / NM; ++j) {
-        const int idx = lm + j * NM, r = idx / (VB / 4), cc = (idx % (VB / 4)) * 4;
-        if (r < L)
-          *(f32x4*)(gmem(a.U) + (tok0 + r) * rsv + (long)h * V + v0 + cc) = *(const f32x4*)(sUo + r * LDV + cc);
+      for (int j = 0; j < NU; ++j) {
+        const int idx = lm + j * NM, r = min(idx / (VB / 4), L - 1), cc = (idx % (VB / 4)) * 4;
+        *(f32x4*)(gmem(a.U) + (tok0 + r) * rsv + (long)h * V + v0 + cc) = urow[j];
       }
+      load_q(min(c + 2, cl));
       load_wug(min(c + 3, cl), Q);
       __syncthreads();
     };
@@ -562,10 +603,12 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
     // the register sets hold the same chunks at every pass
     int c = 0;
     for (; c + 1 < nc; c += 2) {
-      chunk(c, P0{}, P1{});
-      chunk(c + 1, P1{}, P0{});
+      chunk(c, P1{});
+      chunk(c + 1, P0{});
     }
-    if (c < nc) chunk(c, P0{}, P1{});
+    if (c < nc) chunk(c, P1{});
+    // the last chunk's output rows (written before the last barrier)
+    if (nc > 0) store_o(nc - 1);
     return;
   }
 
@@ -584,36 +627,57 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) acc16_to_lds_t(S[rt][ct], sSh + 16 * ct * LDK, sSl + 16 * ct * LDK, LDK, RW * w + 16 * rt);
   __syncthreads();
+  const int rb = 16 * w + 4 * (l >> 4);  // first of the lane's four rows in C tiles of this wave's rows
+  const int tq = 16 * w + (l & 15);      // the lane's query row in P^T tiles
   for (int c = 0; c < nc; ++c) {
-    // ---- phase A: U = u - w S with both operands as hi/lo pairs (lo x lo dropped)
-    const float gL = sGL[0];
+    const int L = chunk_len(c), gc = gc0 + c;
+    const bf16* sKc = sK + (c & 1) * (BT * LDK);
+    const float* sGc = sG + (c & 1) * BT;
+    // ---- phase A: U = u - w S and Y = Qc S, both with hi/lo operands (lo x lo dropped)
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 y[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    bf16x8 qh[NK32], ql[NK32];
 #pragma unroll
-    for (int k0 = 0; k0 < K; k0 += 32) {
+    for (int kk = 0; kk < NK32; ++kk) {
+      const int k0 = 32 * kk;
       const bf16x8 wh = frag16_rm(sW + 16 * w * LDK + k0, LDK), wl = frag16_rm(sWl + 16 * w * LDK + k0, LDK);
+      qh[kk] = frag16_rm(sQh + 16 * w * LDK + k0, LDK);
+      ql[kk] = frag16_rm(sQl + 16 * w * LDK + k0, LDK);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         const bf16x8 sh = frag16_rm(sSh + 16 * ct * LDK + k0, LDK);
+        const bf16x8 sl = frag16_rm(sSl + 16 * ct * LDK + k0, LDK);
         acc[ct] = mfma16(wh, sh, acc[ct]);
-        acc[ct] = mfma16(wh, frag16_rm(sSl + 16 * ct * LDK + k0, LDK), acc[ct]);
+        acc[ct] = mfma16(wh, sl, acc[ct]);
         acc[ct] = mfma16(wl, sh, acc[ct]);
+        y[ct] = mfma16(qh[kk], sh, y[ct]);
+        y[ct] = mfma16(qh[kk], sl, y[ct]);
+        y[ct] = mfma16(ql[kk], sh, y[ct]);
       }
     }
-    // rows beyond the chunk hold u = 0 and w = 0, so U = 0 there and fac = 0 keeps it out of S
-    const int rb = 16 * w + 4 * (l >> 4);
-    const f32x4 fac = *(const f32x4*)(sFac + rb);
+    // g of the lane's rows and of the chunk's last token; fac_t = exp(g_L - g_t), 0 beyond the chunk
+    // (rows beyond the chunk hold u = 0 and w = 0, so U = 0 there and fac = 0 keeps it out of S)
+    const float glast = sGc[L - 1];
+    const float gL = __expf(glast);
+    const f32x4 gr = *(const f32x4*)(sGc + rb);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       const int cc = 16 * ct + (l & 15);
-      f32x4 us;
+      f32x4 uo, us;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float uo = sU[(rb + i) * LDV + cc] - acc[ct][i];
-        sUo[(rb + i) * LDV + cc] = uo;
-        us[i] = fac[i] * uo;
+        float* pu_ = sU + (rb + i) * LDV + cc;
+        uo[i] = *pu_ - acc[ct][i];
+        *pu_ = uo[i];
+        us[i] = rb + i < L ? __expf(glast - gr[i]) * uo[i] : 0.f;
       }
       acc16_to_lds_t(us, sUh + 16 * ct * LDB, sUl + 16 * ct * LDB, LDB, 16 * w);
+      acc16_to_lds_t(uo, sVh + 16 * ct * LDB, sVl + 16 * ct * LDB, LDB, 16 * w);
     }
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[ct][i] *= a.scale * __expf(gr[i]);
     __syncthreads();
 
     // ---- phase B: S <- gamma_L S + K^T (fac U); S^T (hi/lo) for the next chunk
@@ -631,7 +695,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
       }
 #pragma unroll
       for (int rt = 0; rt < NR16; ++rt) {
-        const bf16x8 ka = frag16_tr(sK + k0 * LDK + RW * w + 16 * rt, LDK);
+        const bf16x8 ka = frag16_tr(sKc + k0 * LDK + RW * w + 16 * rt, LDK);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
           S[rt][ct] = mfma16(ka, uh[ct], S[rt][ct]);
@@ -639,6 +703,80 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
         }
       }
     }
+    // P^T tiles of key rows [16 i, 16 i + 16) against this wave's query rows (causal: i <= w), with
+    // the query fragments kept from phase A
+    f32x4 pt[NT16];
+#pragma unroll
+    for (int i = 0; i < NT16; ++i) {
+      pt[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (i <= w) {
+#pragma unroll
+        for (int kk = 0; kk < NK32; ++kk) {
+          const bf16x8 kf = frag16_rm(sKc + 16 * i * LDK + 32 * kk, LDK);
+          pt[i] = mfma16(kf, qh[kk], pt[i]);
+          pt[i] = mfma16(kf, ql[kk], pt[i]);
+        }
+      }
+    }
+    // P[t][s] = scale exp(g_t - g_s) (Qc_t . k_s) for s <= t < L, else 0 (the exponent is taken
+    // only where it is used, so masked entries never overflow)
+    const float gq = sGc[tq];
+#pragma unroll
+    for (int i = 0; i < NT16; ++i) {
+      const f32x4 gs = *(const f32x4*)(sGc + 16 * i + 4 * (l >> 4));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool keep = 16 * i + 4 * (l >> 4) + j <= tq && tq < L;
+        const float e = __expf(keep ? gq - gs[j] : 0.f);
+        pt[i][j] = keep ? a.scale * e * pt[i][j] : 0.f;
+      }
+    }
+    // P^T to HBM: every value block forms the whole tile; block vt writes the key tiles i with
+    // i % nv == vt (64-byte rows)
+    {
+      float* ptg = a.PT + ((long)gc * a.H + h) * (BT * BT);
+#pragma unroll
+      for (int i = 0; i < NT16; ++i)
+        if (i % nv == vt) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ptg[(16 * i + 4 * (l >> 4) + j) * BT + tq] = pt[i][j];
+        }
+    }
+    // A operands of P U: k slots 0-3 from key tile 2p, 4-7 from key tile 2p + 1
+    bf16x8 ph[NT16 / 2], pl[NT16 / 2];
+#pragma unroll
+    for (int p = 0; p < NT16 / 2; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bf16 x, z;
+        split2(pt[2 * p][j], x, z);
+        ph[p][j] = x;
+        pl[p][j] = z;
+        split2(pt[2 * p + 1][j], x, z);
+        ph[p][4 + j] = x;
+        pl[p][4 + j] = z;
+      }
+    // O = scale gamma Y + P U over the key tiles this wave's rows see
+#pragma unroll
+    for (int p = 0; p < NT16 / 2; ++p) {
+      if (2 * p <= w) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const int e = (16 * ct + (l & 15)) * LDB + 32 * p + 4 * (l >> 4);
+          const bf16x8 vh = __builtin_shufflevector(*(const bf16x4*)(sVh + e), *(const bf16x4*)(sVh + e + 16), 0,
+                                                    1, 2, 3, 4, 5, 6, 7);
+          const bf16x8 vl = __builtin_shufflevector(*(const bf16x4*)(sVl + e), *(const bf16x4*)(sVl + e + 16), 0,
+                                                    1, 2, 3, 4, 5, 6, 7);
+          y[ct] = mfma16(ph[p], vh, y[ct]);
+          y[ct] = mfma16(ph[p], vl, y[ct]);
+          y[ct] = mfma16(pl[p], vh, y[ct]);
+        }
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sO[(rb + i) * LDO + 16 * ct + (l & 15)] = (bf16)y[ct][i];
 #pragma unroll
     for (int rt = 0; rt < NR16; ++rt)
 #pragma unroll
@@ -2682,14 +2820,18 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       hipLaunchKernelGGL(gdn_prep_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnFwdState:
-      if (K <= 128)
-        hipLaunchKernelGGL(gdn_fwd_state_v3_kernel<(K <= 128 ? K : 128)>, dim3((V / 32) * a.N * a.H), dim3(kWalk8),
-                           0, st, a, V);
-      else
+      if (K <= 128) {
+        constexpr int KW = K <= 128 ? K : 128;
+        if (a.qc32)
+          hipLaunchKernelGGL((gdn_fwd_state_v3_kernel<KW, true>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
+        else
+          hipLaunchKernelGGL((gdn_fwd_state_v3_kernel<KW, false>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
+      } else
         hipLaunchKernelGGL(gdn_fwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnFwdO:
-      hipLaunchKernelGGL(gdn_fwd_o_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      // for K <= 128 the forward walk writes the output itself
+      if constexpr (K > 128) hipLaunchKernelGGL(gdn_fwd_o_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdState:
       if (K <= 128)
