@@ -2810,8 +2810,492 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_v2_kernel(const GdnArgs a
 }
 
 // ===========================================================================
+// gdn_bwd_wy for K, V in {64, 128}: persistent workgroups of 8 waves, one per CU, each taking the
+// (chunk, head) units blockIdx.x, blockIdx.x + gridDim.x, ...  Waves 4-7 load the next unit's
+// inputs (dw, dU, k, v, T, g, beta, dG partials) into registers while waves 0-3 work on the current
+// one, and write them into LDS as soon as the current unit no longer reads that buffer; every
+// operand of a unit is read from LDS only (one HBM read of each input).  Per unit, with 32x32 MFMA
+// tiles (waves 0-2 take the three lower 32x32 blocks (R, C) of a 64x64 matrix):
+//   P1  dT^T blocks (rows c, cols r) over k and v, K K^T in both orientations; dT [r][c] (masked
+//       r > c, scaled by beta_c (gamma_c k-part + v-part)) to LDS
+//   P2  M1 = dT T^T (masked r > c) to LDS as M1^T;  dA and dA^T = T^T M1 in both orientations
+//       (T^T fragments by transposing reads of T)
+//   P3  the dbeta / dG terms of A (row sums from dA^T, column sums from dA, both within a lane);
+//       dAs + dAs^T (symmetric, zero diagonal) to LDS
+//   P4  dk^T tiles: K^T (dAs + dAs^T) + (T^T dw)^T, plus dk_part (read by the compute waves
+//       just before P4); dk rows leave as 16-byte pieces; dbeta / dG terms of w
+//   P5  dv^T tiles: (T^T dU)^T; dv rows as 8-byte pieces; dbeta terms of u  (the next unit's dw
+//       and k are staged meanwhile)
+// Barriers per unit: B0 (staged), B1 (dT), B2 (M1^T), B3 (dAs), B4 (dw, k free), B5 (all free).
+// The memory waves issue the next unit's loads in three groups (after B0: dw, k; after B2: dU;
+// after B3: v, T and the per-token values), each ahead of a long compute phase, so issuing them
+// (which stalls while the memory system is busy) does not hold a barrier.  Loops keep several independent accumulators and load the next step's fragments before
+// the current step's MFMAs.  Per-row partial sums go to per-wave LDS slots and are added in a fixed
+// order (deterministic).
+// ===========================================================================
+template <int K, int V>
+__global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) {
+  constexpr int PT = BT + 8, PK = K + 8, PV = V + 8, NM = 256;
+  constexpr int NKB = K / 32, NVB = V / 32;  // 32-column blocks of dk and dv
+  constexpr int NJK = NKB / 2, NJV = NVB / 2;  // dk / dv tiles per wave
+  static_assert(NKB % 2 == 0 && NVB % 2 == 0, "two column groups of tiles");
+  __shared__ __attribute__((aligned(16))) bf16 sTh[BT * PT], sTl[BT * PT];  // T [a][c]
+  __shared__ __attribute__((aligned(16))) bf16 sXh[BT * PT], sXl[BT * PT];  // dT [r][c], then dAs + dAs^T
+  __shared__ __attribute__((aligned(16))) bf16 sMh[BT * PT], sMl[BT * PT];  // M1^T [c][r]
+  __shared__ __attribute__((aligned(16))) bf16 sWh[BT * PK], sWl[BT * PK];  // dw [t][k]
+  __shared__ __attribute__((aligned(16))) bf16 sK[BT * PK];                 // k [t][k]
+  __shared__ __attribute__((aligned(16))) bf16 sUh[BT * PV], sUl[BT * PV];  // dU [t][v]
+  __shared__ __attribute__((aligned(16))) bf16 sV[BT * PV];                 // v [t][v]
+  __shared__ __attribute__((aligned(16))) float sG[BT], sBeta[BT], sGam[BT];
+  __shared__ __attribute__((aligned(16))) float sDG0[2 * BT];               // summed dG partials, by unit parity
+  __shared__ __attribute__((aligned(16))) float sPB[4 * BT], sPG[4 * BT];  // per compute wave: dbeta, dG terms
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const int nunits = a.NTG * a.H;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
+  // first unit at or after u on this workgroup's stride that is not a padding entry of a varlen
+  // launch (both roles walk the same sequence)
+  auto valid_from = [&](int u) {
+    for (; u < nunits; u += gridDim.x) {
+      int n, c0, L;
+      long bos;
+      if (chunk_info(a, u / a.H, n, c0, bos, L)) break;
+    }
+    return u;
+  };
+
+  if (w >= 4) {
+    // ---------------- memory waves
+    const int lm = tid - NM;
+    RowsF32<K, BT, NM> pw;
+    RowsF32<V, BT, NM> pu;
+    RowsF32<BT, BT, NM> pt;
+    RowsBf16<K, BT, NM> pk;
+    RowsBf16<V, BT, NM> pv;
+    // per-token values of token l, kept as loaded (used at staging: consuming them earlier would make
+    // the wait for them cover the tile loads issued before them)
+    float pg = 0.f, pb = 0.f, pd[K / 64];
+    int L = 0;
+    long tok0 = 0;
+    int gc = 0, h = 0;
+    auto locate = [&](int u) {
+      gc = u / a.H;
+      h = u % a.H;
+      int n, c0;
+      long bos;
+      chunk_info(a, gc, n, c0, bos, L);
+      tok0 = bos + c0;
+    };
+    auto load_a = [&]() {
+      pw.load(a.dw32 + (tok0 * a.H + h) * K, rsk, L, lm);
+      pk.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L, lm);
+    };
+    auto load_b = [&]() { pu.load(a.dU + (tok0 * a.H + h) * (long)V, rsv, L, lm); };
+    auto load_c = [&]() {
+      pv.load((const bf16*)a.v + (tok0 * a.H + h) * (long)V, rsv, L, lm);
+      pt.load(a.tmat + ((long)gc * a.H + h) * (BT * BT), BT, BT, lm);
+      const long tk = (tok0 + min(l, L - 1)) * a.H + h;
+      pg = *gmem(a.gcum + tk);
+      pb = *gmem(a.beta + tk);
+#pragma unroll
+      for (int kt = 0; kt < K / 64; ++kt) pd[kt] = *gmem(a.dgp + (long)kt * ntok * a.H + tk);
+    };
+    auto stage_a = [&]() {
+      pw.store_split(sWh, sWl, PK, L, lm);
+      pk.store(sK, PK, L, lm);
+    };
+    // g of token l (the last token's beyond the chunk); beta and the summed dG partials 0 beyond it
+    auto stage_b = [&](int par) {
+      pu.store_split(sUh, sUl, PV, L, lm);
+      pv.store(sV, PV, L, lm);
+      pt.store_split(sTh, sTl, PT, BT, lm);
+      if (w == 4) {
+        float d = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < K / 64; ++kt) d += pd[kt];
+        sG[l] = pg;
+        sGam[l] = __expf(pg);
+        sBeta[l] = l < L ? pb : 0.f;
+        sDG0[par * BT + l] = l < L ? d : 0.f;
+      }
+    };
+    int u = valid_from(blockIdx.x), par = 0;
+    if (u < nunits) {
+      locate(u);
+      load_a();
+      load_b();
+      load_c();
+      stage_a();
+      stage_b(0);
+    }
+    int un = u < nunits ? valid_from(u + gridDim.x) : nunits;
+    while (u < nunits) {
+      const bool more = un < nunits;
+      if (more) locate(un);
+      __syncthreads();  // B0
+      if (more) load_a();
+      __syncthreads();  // B1
+      __syncthreads();  // B2
+      if (more) load_b();
+      __syncthreads();  // B3
+      if (more) load_c();
+      __syncthreads();  // B4
+      if (more) stage_a();
+      __syncthreads();  // B5
+      if (more) stage_b(par ^ 1);
+      u = un;
+      par ^= 1;
+      un = u < nunits ? valid_from(u + gridDim.x) : nunits;
+    }
+    return;
+  }
+
+  // ---------------- compute waves
+  const int R = blk_row3(w), C = blk_col3(w);  // lower 32 x 32 block of waves 0..2
+  const int tr = w >> 1;                       // 32-row block of this wave's dk / dv tiles
+  const int rr = tr * 32 + acc_col();          // the lane's row in dk^T / dv^T tiles
+  const int q4 = 4 * (l >> 5);                 // first row of the lane's 4-row groups in a C tile
+  int par = 0;
+  for (int u = valid_from(blockIdx.x); u < nunits; u = valid_from(u + gridDim.x), par ^= 1) {
+    const int gc = u / a.H, h = u % a.H;
+    int n, c0, L;
+    long bos;
+    chunk_info(a, gc, n, c0, bos, L);
+    const long tok0 = bos + c0;
+    __syncthreads();  // B0: the unit's operands are in LDS
+    sPB[w * BT + l] = 0.f;
+    sPG[w * BT + l] = 0.f;
+
+    // ---- P1: dT^T (rows c, cols r) = K_c dw_r^T gamma_c + V_c dU_r^T; K K^T both ways
+    f32x16 kk = zero16(), kkT = zero16();
+    if (w < 3) {
+      constexpr int NS = (K > V ? K : V) / 16;
+      f32x16 dTkh = zero16(), dTkl = zero16(), dTvh = zero16(), dTvl = zero16();
+      bf16x8 fa[2][7];
+      auto ld = [&](int s, bf16x8* f) {
+        if (s < K / 16) {
+          f[0] = frag_rm(sK + C * 32 * PK + 16 * s, PK);
+          f[1] = frag_rm(sK + R * 32 * PK + 16 * s, PK);
+          f[2] = frag_rm(sWh + R * 32 * PK + 16 * s, PK);
+          f[3] = frag_rm(sWl + R * 32 * PK + 16 * s, PK);
+        }
+        if (s < V / 16) {
+          f[4] = frag_rm(sV + C * 32 * PV + 16 * s, PV);
+          f[5] = frag_rm(sUh + R * 32 * PV + 16 * s, PV);
+          f[6] = frag_rm(sUl + R * 32 * PV + 16 * s, PV);
+        }
+      };
+      ld(0, fa[0]);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        if (s + 1 < NS) ld(s + 1, fa[(s + 1) & 1]);
+        const bf16x8* f = fa[s & 1];
+        if (s < K / 16) {
+          dTkh = mfma(f[0], f[2], dTkh);
+          kkT = mfma(f[0], f[1], kkT);
+          dTkl = mfma(f[0], f[3], dTkl);
+          kk = mfma(f[1], f[0], kk);
+        }
+        if (s < V / 16) {
+          dTvh = mfma(f[4], f[5], dTvh);
+          dTvl = mfma(f[4], f[6], dTvl);
+        }
+      }
+      f32x16 d;
+      const int r = R * 32 + acc_col();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = C * 32 + 8 * q + q4;
+        const f32x4 gm = *(const f32x4*)(sGam + c), bt = *(const f32x4*)(sBeta + c);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int i = 4 * q + ii;
+          d[i] = (r > c + ii) ? ((dTkh[i] + dTkl[i]) * gm[ii] + dTvh[i] + dTvl[i]) * bt[ii] : 0.f;
+        }
+      }
+      acc_to_lds_t(d, sXh + R * 32 * PT, sXl + R * 32 * PT, PT, C * 32);
+    } else {
+      acc_to_lds_t(zero16(), sXh, sXl, PT, 32);  // dT[0..31][32..63] = 0
+    }
+    __syncthreads();  // B1
+
+    // ---- P2: M1 = dT T^T (rows r, cols c), masked to r > c, to LDS as M1^T [c][r]
+    if (w < 3) {
+      f32x16 m1 = zero16(), m2 = zero16();
+      bf16x8 fa[2][4];
+      auto ld = [&](int s, bf16x8* f) {
+        f[0] = frag_rm(sXh + R * 32 * PT + 16 * s, PT);
+        f[1] = frag_rm(sXl + R * 32 * PT + 16 * s, PT);
+        f[2] = frag_rm(sTh + C * 32 * PT + 16 * s, PT);
+        f[3] = frag_rm(sTl + C * 32 * PT + 16 * s, PT);
+      };
+      ld(0, fa[0]);
+#pragma unroll
+      for (int s = 0; s < BT / 16; ++s) {
+        if (s + 1 < BT / 16) ld(s + 1, fa[(s + 1) & 1]);
+        const bf16x8* f = fa[s & 1];
+        m1 = mfma(f[0], f[2], m1);
+        m2 = mfma(f[0], f[3], m2);
+        m1 = mfma(f[1], f[2], m1);
+      }
+      const int c = C * 32 + acc_col();
+#pragma unroll
+      for (int i = 0; i < 16; ++i) m1[i] = (R * 32 + acc_row(i) > c) ? m1[i] + m2[i] : 0.f;
+      acc_to_lds_t(m1, sMh + C * 32 * PT, sMl + C * 32 * PT, PT, R * 32);
+    } else {
+      acc_to_lds_t(zero16(), sMh + 32 * PT, sMl + 32 * PT, PT, 0);  // M1^T[32..63][0..31] = 0
+    }
+    __syncthreads();  // B2
+
+    // ---- P2 (cont.): dA = T^T M1 (rows r, cols c) and dA^T (rows c, cols r); P3
+    if (w < 3) {
+      f32x16 dA = zero16(), dAT = zero16(), dA2 = zero16(), dAT2 = zero16();
+      bf16x8 fa[2][4];
+      auto ld = [&](int s, bf16x8* f) {
+        f[0] = frag32_tr(sTh + 16 * s * PT + R * 32, PT);
+        f[1] = frag32_tr(sTl + 16 * s * PT + R * 32, PT);
+        f[2] = frag_rm(sMh + C * 32 * PT + 16 * s, PT);
+        f[3] = frag_rm(sMl + C * 32 * PT + 16 * s, PT);
+      };
+      ld(0, fa[0]);
+#pragma unroll
+      for (int s = 0; s < BT / 16; ++s) {
+        if (s + 1 < BT / 16) ld(s + 1, fa[(s + 1) & 1]);
+        const bf16x8* f = fa[s & 1];
+        dA = mfma(f[0], f[2], dA);
+        dAT = mfma(f[2], f[0], dAT);
+        dA2 = mfma(f[0], f[3], dA2);
+        dAT2 = mfma(f[2], f[1], dAT2);
+        dA = mfma(f[1], f[2], dA);
+        dAT = mfma(f[3], f[0], dAT);
+      }
+      // the true dA is -(T^T M1); e = dA o Gamma o (K K^T), dAs = dA o beta_r Gamma (r > c)
+      f32x16 ds1, ds2;
+      float srow = 0.f, scol = 0.f;
+      {
+        const int r = R * 32 + acc_col();
+        const float gr_ = sG[r], br_ = sBeta[r];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = C * 32 + 8 * q + q4;
+          const f32x4 gcv = *(const f32x4*)(sG + c);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int i = 4 * q + ii;
+            const bool keep = r > c + ii;
+            const float x = -(dAT[i] + dAT2[i]);
+            const float gam = __expf(keep ? gr_ - gcv[ii] : 0.f);
+            srow += keep ? x * gam * kkT[i] : 0.f;
+            ds1[i] = keep ? x * br_ * gam : 0.f;
+          }
+        }
+      }
+      {
+        const int c = C * 32 + acc_col();
+        const float gc_ = sG[c];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = R * 32 + 8 * q + q4;
+          const f32x4 grv = *(const f32x4*)(sG + r), brv = *(const f32x4*)(sBeta + r);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int i = 4 * q + ii;
+            const bool keep = r + ii > c;
+            const float x = -(dA[i] + dA2[i]);
+            const float gam = __expf(keep ? grv[ii] - gc_ : 0.f);
+            scol += keep ? x * gam * kk[i] * brv[ii] : 0.f;
+            ds2[i] = keep ? x * brv[ii] * gam : 0.f;
+          }
+        }
+      }
+      srow += __shfl_xor(srow, 32);
+      scol += __shfl_xor(scol, 32);
+      // dAs at (r, c) from ds1 and at (c, r) from ds2: one symmetric operand; on a diagonal block both
+      // land in the same lane and element, so they are added first
+      if (R == C) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ds1[i] += ds2[i];
+        acc_to_lds_t(ds1, sXh + R * 32 * PT, sXl + R * 32 * PT, PT, C * 32);
+      } else {
+        acc_to_lds_t(ds1, sXh + R * 32 * PT, sXl + R * 32 * PT, PT, C * 32);
+        acc_to_lds_t(ds2, sXh + C * 32 * PT, sXl + C * 32 * PT, PT, R * 32);
+      }
+      if (l < 32) {
+        sPB[w * BT + R * 32 + l] += srow;
+        sPG[w * BT + R * 32 + l] += sBeta[R * 32 + l] * srow;
+        sPG[w * BT + C * 32 + l] -= scol;
+      }
+    }
+    // dk_part of this wave's dk tiles (rows past the chunk read row L - 1), used at the end of P4;
+    // issued before the barrier so that the compiler cannot move them next to their use
+    f32x4 dkp[NJK][4];
+#pragma unroll
+    for (int j = 0; j < NJK; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        dkp[j][g] = *gmem((const f32x4*)(a.dkp32 + (tok0 + min(rr, L - 1)) * rsk + (long)h * K +
+                                         ((w & 1) * NJK + j) * 32 + 8 * g + q4));
+    __syncthreads();  // B3
+
+    // the unit's dk / dv rows as buffers ending after row L - 1 (stores of later rows are dropped)
+    const __amdgpu_buffer_rsrc_t rdk = buf_rsrc(a.dk32 + (tok0 * a.H + h) * K, (int)(((L - 1) * rsk + K) * 4));
+    const __amdgpu_buffer_rsrc_t rdv =
+        buf_rsrc((const bf16*)a.dv + (tok0 * a.H + h) * (long)V, (int)(((L - 1) * rsv + V) * 2));
+    const float br = sBeta[rr], gmr = sGam[rr];
+    float s4 = 0.f, s5 = 0.f;
+    // ---- P4: dk^T tiles (rows kk, cols r); the dAs and T fragments are shared by the wave's tiles
+    {
+      f32x16 acc[NJK], acc2[NJK];
+#pragma unroll
+      for (int j = 0; j < NJK; ++j) acc[j] = acc2[j] = zero16();
+      bf16x8 fa[2][4 + 3 * NJK];
+      auto ld = [&](int s, bf16x8* f) {
+        f[0] = frag_rm(sXh + tr * 32 * PT + 16 * s, PT);
+        f[1] = frag_rm(sXl + tr * 32 * PT + 16 * s, PT);
+        f[2] = frag32_tr(sTh + 16 * s * PT + tr * 32, PT);
+        f[3] = frag32_tr(sTl + 16 * s * PT + tr * 32, PT);
+#pragma unroll
+        for (int j = 0; j < NJK; ++j) {
+          const int tc = (w & 1) * NJK + j;
+          f[4 + 3 * j] = frag32_tr(sK + 16 * s * PK + tc * 32, PK);
+          f[5 + 3 * j] = frag32_tr(sWh + 16 * s * PK + tc * 32, PK);
+          f[6 + 3 * j] = frag32_tr(sWl + 16 * s * PK + tc * 32, PK);
+        }
+      };
+      ld(0, fa[0]);
+#pragma unroll
+      for (int s = 0; s < BT / 16; ++s) {
+        if (s + 1 < BT / 16) ld(s + 1, fa[(s + 1) & 1]);
+        const bf16x8* f = fa[s & 1];
+#pragma unroll
+        for (int j = 0; j < NJK; ++j) {
+          acc[j] = mfma(f[4 + 3 * j], f[0], acc[j]);
+          acc2[j] = mfma(f[5 + 3 * j], f[2], acc2[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NJK; ++j) {
+          acc[j] = mfma(f[4 + 3 * j], f[1], acc[j]);
+          acc2[j] = mfma(f[5 + 3 * j], f[3], acc2[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NJK; ++j) acc2[j] = mfma(f[6 + 3 * j], f[2], acc2[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < NJK; ++j) {
+        const int tc = (w & 1) * NJK + j;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int kc = tc * 32 + 8 * g + q4;
+          const bf16x4 k4 = *(const bf16x4*)(sK + rr * PK + kc);
+          f32x4 o;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int i = 4 * g + ii;
+            const float t2 = acc2[j][i];
+            o[ii] = dkp[j][g][ii] + acc[j][i] + br * gmr * t2;
+            s4 += t2 * (float)k4[ii];
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), rdk, (int)((rr * rsk + kc) * 4), 0, 0);
+        }
+      }
+    }
+    __syncthreads();  // B4: dw and k are free (the memory waves stage the next unit's)
+
+    // ---- P5: dv^T tiles (rows v, cols r)
+    {
+      f32x16 acc[NJV], acc2[NJV];
+#pragma unroll
+      for (int j = 0; j < NJV; ++j) acc[j] = acc2[j] = zero16();
+      bf16x8 fa[2][2 + 2 * NJV];
+      auto ld = [&](int s, bf16x8* f) {
+        f[0] = frag32_tr(sTh + 16 * s * PT + tr * 32, PT);
+        f[1] = frag32_tr(sTl + 16 * s * PT + tr * 32, PT);
+#pragma unroll
+        for (int j = 0; j < NJV; ++j) {
+          const int tc = (w & 1) * NJV + j;
+          f[2 + 2 * j] = frag32_tr(sUh + 16 * s * PV + tc * 32, PV);
+          f[3 + 2 * j] = frag32_tr(sUl + 16 * s * PV + tc * 32, PV);
+        }
+      };
+      ld(0, fa[0]);
+#pragma unroll
+      for (int s = 0; s < BT / 16; ++s) {
+        if (s + 1 < BT / 16) ld(s + 1, fa[(s + 1) & 1]);
+        const bf16x8* f = fa[s & 1];
+#pragma unroll
+        for (int j = 0; j < NJV; ++j) {
+          acc[j] = mfma(f[2 + 2 * j], f[0], acc[j]);
+          acc2[j] = mfma(f[2 + 2 * j], f[1], acc2[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NJV; ++j) acc[j] = mfma(f[3 + 2 * j], f[0], acc[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < NJV; ++j) {
+        const int tc = (w & 1) * NJV + j;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int vc = tc * 32 + 8 * g + q4;
+          const bf16x4 v4 = *(const bf16x4*)(sV + rr * PV + vc);
+          bf16x4 o;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const float x = acc[j][4 * g + ii] + acc2[j][4 * g + ii];
+            o[ii] = (bf16)(br * x);
+            s5 += x * (float)v4[ii];
+          }
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), rdv, (int)((rr * rsv + vc) * 2), 0, 0);
+        }
+      }
+    }
+    s4 += __shfl_xor(s4, 32);
+    s5 += __shfl_xor(s5, 32);
+    if (l < 32) {
+      sPB[w * BT + rr] += gmr * s4 + s5;
+      sPG[w * BT + rr] += br * gmr * s4;
+    }
+    __syncthreads();  // B5: every LDS read of the unit done; the memory waves stage the rest
+
+    // ---- dbeta, and dg = reverse cumulative sum of dG within the chunk
+    if (w == 0) {
+      const int r = BT - 1 - l;  // reverse order
+      float db = 0.f, x = sDG0[par * BT + r];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        db += sPB[q * BT + r];
+        x += sPG[q * BT + r];
+      }
+      if (r >= L) x = 0.f;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(x, off);
+        if (l >= off) x += y;
+      }
+      if (r < L) {
+        a.dg[(tok0 + r) * a.H + h] = x;
+        a.dbeta[(tok0 + r) * a.H + h] = db;
+      }
+    }
+  }
+}
+
+// ===========================================================================
 // launchers (one per kernel so the C ABI can time each launch)
 // ===========================================================================
+// Compute units of the current device (the persistent kernels launch one workgroup per CU).
+static int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cache[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 template <int K>
 static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st) {
   if (a.NTG == 0) return hipSuccess;
@@ -2852,7 +3336,16 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
         hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdWy:
-      hipLaunchKernelGGL(gdn_bwd_wy_v2_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      if (K <= 128 && (V == 64 || V == 128)) {
+        constexpr int KW = K <= 128 ? K : 128;
+        const int grid = min(a.NTG * a.H, cu_count());
+        if (V == 128)
+          hipLaunchKernelGGL((gdn_bwd_wy_v3_kernel<KW, 128>), dim3(grid), dim3(kWalk8), 0, st, a);
+        else
+          hipLaunchKernelGGL((gdn_bwd_wy_v3_kernel<KW, 64>), dim3(grid), dim3(kWalk8), 0, st, a);
+      } else {
+        hipLaunchKernelGGL(gdn_bwd_wy_v2_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      }
       break;
     default:
       return hipErrorInvalidValue;

@@ -101,6 +101,28 @@ __device__ __forceinline__ bf16x8 frag16_tr(const bf16* p, int ld) {
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// Buffer resource over `bytes` bytes from p (gfx9 raw buffer, stride 0): a buffer store whose byte
+// offset is at or beyond `bytes` is dropped by the hardware, so rows past a chunk can be stored
+// without a branch (a branch lets the compiler sink the loads that feed the stored values into it).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+// 32x16 operand of mfma (32x32x16) whose contraction index runs down the rows of a row-major tile:
+// element (r, k) at p[k * ld + r].  Two transposing LDS reads; 16-lane group g covers operand rows
+// 16 (g & 1) .. +15 and contraction elements 8 (g >> 1) .. +7 (lane j of the group names the 8-byte
+// piece at row j >> 2, columns 4 (j & 3) .. +3 of its 4 x 16 block).
+__device__ __forceinline__ bf16x8 frag32_tr(const bf16* p, int ld) {
+  const int l = lane_id(), j = l & 15;
+  const bf16* q = p + (8 * (l >> 5) + (j >> 2)) * ld + 16 * ((l >> 4) & 1) + 4 * (j & 3);
+  typedef __attribute__((address_space(3))) bf16x4_t lds_b4;
+  const bf16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)q);
+  const bf16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)(q + 4 * ld));
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 // Element (r, k) at p[k * ld + r]  (operand stored transposed: eight 2-byte reads).
 __device__ __forceinline__ bf16x8 frag_cm(const bf16* p, int ld) {
   const int l = lane_id();

@@ -132,6 +132,9 @@ GDN_CASES = [
     (1, 200, 2, 128, 128, False, None),
     (1, 96, 1, 256, 128, True, None),
     (1, 150, 2, 64, 128, True, [0, 20, 85, 150]),
+    # more (chunk, head) units than CUs: the persistent WY backward takes several units per workgroup
+    (2, 2048, 8, 128, 128, False, None),
+    (1, 2048, 8, 128, 128, True, [0, 700, 1500, 2048]),
 ]
 
 
