@@ -282,6 +282,366 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, con
 }
 
 // ===========================================================================
+// gdn_prep for K, V in {64, 128}: persistent workgroups of 8 waves, one per CU, over the (chunk,
+// head) units.  Waves 4-7 load the next unit's k, v, g and beta into registers while waves 0-3 work,
+// and write them into LDS (with the in-chunk cumulative g, which they also store) once the current
+// unit is done.  Per unit, on waves 0-3:
+//   P1  A = strict_lower(beta_r Gamma_rc (K K^T)_rc) (three 32x32 MFMA blocks), fp32 in LDS
+//   P2  the four 16x16 diagonal blocks D_I = (I + A_II)^-1 by forward substitution (fp32, one
+//       column per lane)
+//   P3  the 32-level blocks T_{2p+1,2p} = -D_{2p+1} A_{2p+1,2p} D_{2p} (fp32 on the VALU)
+//   P4  the 64-level block T_10 = -T_1 (A_10 T_0) (32x32 MFMA products on hi/lo operands)
+//   P5  T diag(beta gamma) and T diag(beta) as hi/lo row tiles; T (fp32, hi + lo) to HBM
+//   P6  w^T = K^T (T diag(beta gamma))^T and u^T = V^T (T diag(beta))^T tiles, staged per wave in
+//       the A / T buffers and stored as whole rows (w as its hi/lo pair); rows past the chunk are
+//       dropped by range-checked buffer stores
+// T is unit lower triangular; its upper blocks are zeroed once and never written.
+// ===========================================================================
+template <int K, int V>
+__global__ __launch_bounds__(kWalk8) void gdn_prep_v3_kernel(const GdnArgs a) {
+  constexpr int PT = BT + 8, PF = BT + 4, PK = K + 8, PV = V + 8, PX = 32 + 40, NM = 256;
+  constexpr int NKB = K / 32, NVB = V / 32, NJK = NKB / 2, NJV = NVB / 2;
+  static_assert(NKB % 2 == 0 && NVB % 2 == 0, "two column groups of tiles");
+  __shared__ __attribute__((aligned(16))) bf16 sK[BT * PK];                 // k [t][k]
+  __shared__ __attribute__((aligned(16))) bf16 sV[BT * PV];                 // v [t][v]
+  __shared__ __attribute__((aligned(16))) float sA[BT * PF];                // A [r][c]
+  __shared__ __attribute__((aligned(16))) float sTf[BT * PF];               // T, blocks formed on the VALU
+  __shared__ __attribute__((aligned(16))) bf16 sTh[BT * PT], sTl[BT * PT];  // T [r][c]
+  __shared__ __attribute__((aligned(16))) bf16 sXh[32 * PX], sXl[32 * PX];  // X = A_10 T_0 [r][c]
+  __shared__ __attribute__((aligned(16))) bf16 sBh[BT * PT], sBl[BT * PT];  // T diag(beta gamma) [t][s]
+  __shared__ __attribute__((aligned(16))) bf16 sCh[BT * PT], sCl[BT * PT];  // T diag(beta) [t][s]
+  __shared__ __attribute__((aligned(16))) float sG[BT], sBeta[BT], sBG[BT];
+  __shared__ __attribute__((aligned(16))) float sY[2 * 256];                // A_{2p+1,2p} D_{2p}
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const int nunits = a.NTG * a.H;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  auto valid_from = [&](int u) {
+    for (; u < nunits; u += gridDim.x) {
+      int n, c0, L;
+      long bos;
+      if (chunk_info(a, u / a.H, n, c0, bos, L)) break;
+    }
+    return u;
+  };
+
+  if (w >= 4) {
+    // ---------------- memory waves
+    const int lm = tid - NM;
+    RowsBf16<K, BT, NM> pk;
+    RowsBf16<V, BT, NM> pv;
+    float pg = 0.f, pb = 0.f;  // raw g and beta of token l (consumed at staging)
+    int L = 0, h = 0;
+    long tok0 = 0;
+    auto locate = [&](int u) {
+      h = u % a.H;
+      int n, c0;
+      long bos;
+      chunk_info(a, u / a.H, n, c0, bos, L);
+      tok0 = bos + c0;
+    };
+    auto load = [&]() {
+      pk.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L, lm);
+      pv.load((const bf16*)a.v + (tok0 * a.H + h) * (long)V, rsv, L, lm);
+      const long tk = (tok0 + min(l, L - 1)) * a.H + h;
+      pg = a.g ? *gmem(a.g + tk) : 0.f;
+      pb = *gmem(a.beta + tk);
+    };
+    // k, v rows (zero past the chunk); wave 4: in-chunk inclusive cumsum of g (the last token's
+    // beyond the chunk), beta (0 beyond it), beta gamma, and the cumulative g to HBM
+    auto stage = [&]() {
+      pk.store(sK, PK, L, lm);
+      pv.store(sV, PV, L, lm);
+      if (w == 4) {
+        float x = l < L ? pg : 0.f;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const float y = __shfl_up(x, off);
+          if (l >= off) x += y;
+        }
+        const float b = l < L ? pb : 0.f;
+        sG[l] = x;
+        sBeta[l] = b;
+        sBG[l] = b * __expf(x);
+        if (l < L) a.gcum[(tok0 + l) * a.H + h] = x;
+      }
+    };
+    int u = valid_from(blockIdx.x);
+    if (u < nunits) {
+      locate(u);
+      load();
+      stage();
+    }
+    int un = u < nunits ? valid_from(u + gridDim.x) : nunits;
+    while (u < nunits) {
+      const bool more = un < nunits;
+      if (more) locate(un);
+      __syncthreads();  // B0
+      if (more) load();
+      __syncthreads();  // B1
+      __syncthreads();  // B2
+      __syncthreads();  // B3
+      __syncthreads();  // B4
+      __syncthreads();  // B5
+      __syncthreads();  // B6
+      __syncthreads();  // B7
+      if (more) stage();
+      u = un;
+      un = u < nunits ? valid_from(u + gridDim.x) : nunits;
+    }
+    return;
+  }
+
+  // ---------------- compute waves
+  // T's upper blocks (16x16 blocks (0,1), (2,3) and the 32x32 block (0,1)) stay zero
+  for (int e = tid; e < BT * BT; e += NM) {
+    const int r = e >> 6, c = e & 63;
+    sTh[r * PT + c] = (bf16)0.f;
+    sTl[r * PT + c] = (bf16)0.f;
+  }
+  const int R = blk_row3(w), C = blk_col3(w);
+  const int tr = w >> 1;
+  const int q4 = 4 * (l >> 5);
+  const int ct = tid;  // 0..255
+  for (int u = valid_from(blockIdx.x); u < nunits; u = valid_from(u + gridDim.x)) {
+    const int gc = u / a.H, h = u % a.H;
+    int n, c0, L;
+    long bos;
+    chunk_info(a, gc, n, c0, bos, L);
+    const long tok0 = bos + c0;
+    __syncthreads();  // B0: k, v, g, beta of the unit are in LDS
+
+    // ---- P1: A (rows r, cols c) for the lower 32x32 blocks
+    if (w < 3) {
+      f32x16 acc = zero16(), acc2 = zero16();
+#pragma unroll
+      for (int k0 = 0; k0 < K; k0 += 32) {
+        acc = mfma(frag_rm(sK + R * 32 * PK + k0, PK), frag_rm(sK + C * 32 * PK + k0, PK), acc);
+        acc2 = mfma(frag_rm(sK + R * 32 * PK + k0 + 16, PK), frag_rm(sK + C * 32 * PK + k0 + 16, PK), acc2);
+      }
+      const int c = C * 32 + acc_col();
+      const float gc_ = sG[c];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r0 = R * 32 + 8 * q + q4;
+        const f32x4 grv = *(const f32x4*)(sG + r0), brv = *(const f32x4*)(sBeta + r0);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const bool keep = r0 + ii > c;
+          const float e = __expf(keep ? grv[ii] - gc_ : 0.f);
+          sA[(r0 + ii) * PF + c] = keep ? brv[ii] * e * (acc[4 * q + ii] + acc2[4 * q + ii]) : 0.f;
+        }
+      }
+    }
+    __syncthreads();  // B1
+
+    // ---- P2: D_I = (I + A_II)^-1, block I = w, column l (lanes 0..15)
+    if (l < 16) {
+      const int b0 = 16 * w;
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float s = (i == l) ? 1.f : 0.f;
+#pragma unroll
+        for (int m = 0; m < i; ++m) s -= sA[(b0 + i) * PF + b0 + m] * x[m];
+        x[i] = s;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        sTf[(b0 + i) * PF + b0 + l] = x[i];
+        bf16 hi, lo;
+        split2(x[i], hi, lo);
+        sTh[(b0 + i) * PT + b0 + l] = hi;
+        sTl[(b0 + i) * PT + b0 + l] = lo;
+      }
+    }
+    __syncthreads();  // B2
+
+    // ---- P3: Y_p = A_{2p+1,2p} D_{2p};  T_{2p+1,2p} = -D_{2p+1} Y_p   (p = 0, 1; 16x16 each)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = ct + 256 * j, p = e >> 8, r = (e >> 4) & 15, c = e & 15;
+      const float* ar = sA + (32 * p + 16 + r) * PF + 32 * p;
+      const float* dc = sTf + (32 * p) * PF + 32 * p + c;
+      float s = 0.f;
+#pragma unroll
+      for (int m = 0; m < 16; m += 4) {
+        const f32x4 av = *(const f32x4*)(ar + m);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) s += av[ii] * dc[(m + ii) * PF];
+      }
+      sY[e] = s;
+    }
+    __syncthreads();  // B3
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = ct + 256 * j, p = e >> 8, r = (e >> 4) & 15, c = e & 15;
+      const float* dr = sTf + (32 * p + 16 + r) * PF + 32 * p + 16;
+      const float* yc = sY + p * 256 + c;
+      float s = 0.f;
+#pragma unroll
+      for (int m = 0; m < 16; m += 4) {
+        const f32x4 dv = *(const f32x4*)(dr + m);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) s += dv[ii] * yc[(m + ii) * 16];
+      }
+      const int row = 32 * p + 16 + r, col = 32 * p + c;
+      bf16 hi, lo;
+      split2(-s, hi, lo);
+      sTh[row * PT + col] = hi;
+      sTl[row * PT + col] = lo;
+    }
+    __syncthreads();  // B4
+
+    // ---- P4 (wave 0): X^T = (A_10 T_0)^T (rows c, cols r), then T_10^T = -(T_1 X)^T
+    if (w == 0) {
+      f32x16 xt = zero16();
+#pragma unroll
+      for (int m0 = 0; m0 < 32; m0 += 16) {
+        const bf16x8 th = frag32_tr(sTh + m0 * PT, PT), tl = frag32_tr(sTl + m0 * PT, PT);
+        bf16x8 ah, al;
+        frag_rm_f32(sA + 32 * PF + m0, PF, ah, al);
+        xt = mfma(th, ah, xt);
+        xt = mfma(th, al, xt);
+        xt = mfma(tl, ah, xt);
+      }
+      acc_to_lds_t(xt, sXh, sXl, PX, 0);  // X [r][c]
+      f32x16 tt = zero16();
+#pragma unroll
+      for (int m0 = 0; m0 < 32; m0 += 16) {
+        const bf16x8 xh = frag32_tr(sXh + m0 * PX, PX), xl = frag32_tr(sXl + m0 * PX, PX);
+        const bf16x8 bh = frag_rm(sTh + 32 * PT + 32 + m0, PT), bl = frag_rm(sTl + 32 * PT + 32 + m0, PT);
+        tt = mfma(xh, bh, tt);
+        tt = mfma(xh, bl, tt);
+        tt = mfma(xl, bh, tt);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tt[i] = -tt[i];
+      acc_to_lds_t(tt, sTh + 32 * PT, sTl + 32 * PT, PT, 0);  // T[32 + r][c]
+    }
+    __syncthreads();  // B5
+
+    // ---- P5: T diag(beta gamma), T diag(beta) (hi/lo rows) and T (fp32) to HBM; thread: rows
+    // (ct >> 4) + 16 q, columns 4 (ct & 15) .. +3 (each row of T leaves as one 256-byte line)
+    {
+      const int c = 4 * (ct & 15);
+      float* tg = a.tmat + ((long)gc * a.H + h) * (BT * BT) + c;
+      const f32x4 bg = *(const f32x4*)(sBG + c), bt = *(const f32x4*)(sBeta + c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = (ct >> 4) + 16 * q;
+        const bf16x4 th = *(const bf16x4*)(sTh + t * PT + c), tl = *(const bf16x4*)(sTl + t * PT + c);
+        f32x4 x;
+        bf16x4 bh, bl, ch, cl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[i] = (float)th[i] + (float)tl[i];
+          bf16 p, r;
+          split2(x[i] * bg[i], p, r);
+          bh[i] = p;
+          bl[i] = r;
+          split2(x[i] * bt[i], p, r);
+          ch[i] = p;
+          cl[i] = r;
+        }
+        *gmem((f32x4*)(tg + t * BT)) = x;
+        *(bf16x4*)(sBh + t * PT + c) = bh;
+        *(bf16x4*)(sBl + t * PT + c) = bl;
+        *(bf16x4*)(sCh + t * PT + c) = ch;
+        *(bf16x4*)(sCl + t * PT + c) = cl;
+      }
+    }
+    __syncthreads();  // B6
+
+    // ---- P6: w^T tiles (rows k, cols t) and u^T tiles (rows v, cols t)
+    {
+      const __amdgpu_buffer_rsrc_t rw = buf_rsrc((const bf16*)a.w + (tok0 * a.H + h) * K, (int)(((L - 1) * rsk + K) * 2));
+      const __amdgpu_buffer_rsrc_t rwl = buf_rsrc((const bf16*)a.wl + (tok0 * a.H + h) * K, (int)(((L - 1) * rsk + K) * 2));
+      const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u + (tok0 * a.H + h) * (long)V, (int)(((L - 1) * rsv + V) * 4));
+      f32x16 aw[NJK], av[NJV];
+#pragma unroll
+      for (int j = 0; j < NJK; ++j) aw[j] = zero16();
+#pragma unroll
+      for (int j = 0; j < NJV; ++j) av[j] = zero16();
+#pragma unroll
+      for (int s0 = 0; s0 < BT; s0 += 16) {
+        const bf16x8 bh = frag_rm(sBh + tr * 32 * PT + s0, PT), bl = frag_rm(sBl + tr * 32 * PT + s0, PT);
+        const bf16x8 ch = frag_rm(sCh + tr * 32 * PT + s0, PT), cl = frag_rm(sCl + tr * 32 * PT + s0, PT);
+#pragma unroll
+        for (int j = 0; j < NJK; ++j) {
+          const bf16x8 kt = frag32_tr(sK + s0 * PK + ((w & 1) * NJK + j) * 32, PK);
+          aw[j] = mfma(kt, bh, aw[j]);
+          aw[j] = mfma(kt, bl, aw[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NJV; ++j) {
+          const bf16x8 vt = frag32_tr(sV + s0 * PV + ((w & 1) * NJV + j) * 32, PV);
+          av[j] = mfma(vt, ch, av[j]);
+          av[j] = mfma(vt, cl, av[j]);
+        }
+      }
+      // the wave's tiles go through a private staging area in the A / T buffers (dead after P5) and
+      // leave as whole rows: w hi / lo as [32][WK] bf16, then u as [32][WV] fp32 (pitch 68)
+      constexpr int WK = NJK * 32, WV = NJV * 32, PS = 68;
+      bf16* swh = (bf16*)((char*)(w < 2 ? sA : sTf) + (w & 1) * (32 * PS * 4));
+      bf16* swl = swh + 32 * PS;
+      float* su = (float*)swh;
+      const int rl = acc_col();  // the lane's row within the wave's 32 rows
+#pragma unroll
+      for (int j = 0; j < NJK; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int kc = 32 * j + 8 * g + q4;
+          bf16x4 hi4, lo4;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            bf16 p, q;
+            split2(aw[j][4 * g + ii], p, q);
+            hi4[ii] = p;
+            lo4[ii] = q;
+          }
+          *(bf16x4*)(swh + rl * PS + kc) = hi4;
+          *(bf16x4*)(swl + rl * PS + kc) = lo4;
+        }
+      {
+        constexpr int LPR = WK / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
+        const int c = 8 * (l % LPR), kbase = (w & 1) * WK;
+#pragma unroll
+        for (int rep = 0; rep < 32 / RPI; ++rep) {
+          const int t = RPI * rep + l / LPR;
+          const int off = (int)(((tr * 32 + t) * rsk + kbase + c) * 2);
+          const bf16x8 hv = __builtin_shufflevector(*(const bf16x4*)(swh + t * PS + c),
+                                                    *(const bf16x4*)(swh + t * PS + c + 4), 0, 1, 2, 3, 4, 5, 6, 7);
+          const bf16x8 lv = __builtin_shufflevector(*(const bf16x4*)(swl + t * PS + c),
+                                                    *(const bf16x4*)(swl + t * PS + c + 4), 0, 1, 2, 3, 4, 5, 6, 7);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hv), rw, off, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lv), rwl, off, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NJV; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int vc = 32 * j + 8 * g + q4;
+          *(f32x4*)(su + rl * PS + vc) = f32x4{av[j][4 * g], av[j][4 * g + 1], av[j][4 * g + 2], av[j][4 * g + 3]};
+        }
+      {
+        constexpr int LPR = WV / 4, RPI = 64 / LPR;
+        const int c = 4 * (l % LPR), vbase = (w & 1) * WV;
+#pragma unroll
+        for (int rep = 0; rep < 32 / RPI; ++rep) {
+          const int t = RPI * rep + l / LPR;
+          const f32x4 x = *(const f32x4*)(su + t * PS + c);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ru,
+                                                 (int)(((tr * 32 + t) * rsv + vbase + c) * 4), 0, 0);
+        }
+      }
+    }
+    __syncthreads();  // B7: k, v, g, beta free for the next unit
+  }
+}
+
+// ===========================================================================
 // gdn_fwd_state: grid ((V/32) * N * H)
 // ===========================================================================
 template <int K>
@@ -3301,7 +3661,16 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
   if (a.NTG == 0) return hipSuccess;
   switch (stage) {
     case kGdnPrep:
-      hipLaunchKernelGGL(gdn_prep_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      if (K <= 128 && (V == 64 || V == 128)) {
+        constexpr int KW = K <= 128 ? K : 128;
+        const int grid = min(a.NTG * a.H, cu_count());
+        if (V == 128)
+          hipLaunchKernelGGL((gdn_prep_v3_kernel<KW, 128>), dim3(grid), dim3(kWalk8), 0, st, a);
+        else
+          hipLaunchKernelGGL((gdn_prep_v3_kernel<KW, 64>), dim3(grid), dim3(kWalk8), 0, st, a);
+      } else {
+        hipLaunchKernelGGL(gdn_prep_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      }
       break;
     case kGdnFwdState:
       if (K <= 128) {
