@@ -1133,7 +1133,8 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
 //            memory:  dqc[:, cols] of c; dZ, K, row scalars, m_prev[cols] of c+1; loads of c+2
 //                     (dqc columns of c+1)
 //   phase 2  compute: dq = dqc + dZ C_prev + A K[:, cols] + ds (m_prev + running key sums)
-//                     + dlogit w[cols]; stores
+//                     + dlogit w[cols], in place over the dqc columns; the memory waves store its
+//                     rows at the start of the next chunk's phase 1 as 16-byte pieces
 // DQ32: the upstream gradient is fp32 (else bf16); MEAN, GATE as in cw_fwd_v3.
 // ===========================================================================
 template <int K, bool DQ32, bool MEAN, bool GATE>
@@ -1147,7 +1148,7 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sCl[32 * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sAh[CB * LDA];     // A[t][s] = dz_t . k_s (s <= t), hi
   __shared__ __attribute__((aligned(16))) bf16 sAl[CB * LDA];
-  __shared__ __attribute__((aligned(16))) float sG[CB * LDG];     // dqc[t][cols]
+  __shared__ __attribute__((aligned(16))) float sG[CB * LDG];     // dqc[t][cols], then dq (in place)
   __shared__ __attribute__((aligned(16))) f32x4 sR[2][CB];        // row scalars, by chunk parity
   __shared__ __attribute__((aligned(16))) float sMp[2][32], sWc[32];
 
@@ -1189,8 +1190,31 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
       if (lm < CB) sR[b][lm] = lm < L ? prow : f32x4{};
       if (lm < 32) sMp[b][lm] = pmp;
     };
+    // dq rows of chunk c (the compute waves leave them in sG, over the dqc columns they read):
+    // each thread stores the pieces that pcol.store overwrites next (same mapping), rows past the
+    // chunk are dropped by the buffer's range check, so every pass issues the same stores
+    auto store_dq = [&](int c) {
+      const int Lc = chunk_len(c);
+      const long base = u.hb + (long)c * CB * u.rs + u.c0;
+      const int nrec = (int)((Lc - 1) * u.rs + 32);
+      const __amdgpu_buffer_rsrc_t rs = a.dq32 ? buf_rsrc(a.dq32 + base, nrec * 4) : buf_rsrc((bf16*)a.dq + base, nrec * 2);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int idx = lm + NM * j, r = idx >> 3, cc = (idx & 7) * 4;
+        const f32x4 x = *(const f32x4*)(sG + r * LDG + cc);
+        if (a.dq32) {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rs, (int)((r * u.rs + cc) * 4), 0, 0);
+        } else {
+          bf16x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = (bf16)x[i];
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), rs, (int)((r * u.rs + cc) * 2), 0, 0);
+        }
+      }
+    };
     // Loads are unconditional (past the end the last chunk again, staged into the idle buffer), so
-    // every pass issues the same memory operations in the same order.
+    // every pass issues the same memory operations in the same order.  At c = 0 the rows of chunk
+    // 0 are written before sG holds them and again one chunk later.
     const int cl = u.nc - 1;
     if (u.nc > 0) {
       load(0);
@@ -1200,7 +1224,8 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
     }
     __syncthreads();
     for (int c = 0; c < u.nc; ++c) {
-      // phase 1
+      // phase 1: the dq rows of chunk c-1 out of sG, then the dqc columns of chunk c into it
+      store_dq(max(c - 1, 0));
       pcol.store(sG, LDG, chunk_len(c), lm);
       load_cols(min(c + 1, cl));
       stage(min(c + 1, cl));
@@ -1208,6 +1233,7 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
       __syncthreads();
       __syncthreads();
     }
+    if (u.nc > 0) store_dq(cl);  // written before the last barrier
     return;
   }
 
@@ -1322,16 +1348,12 @@ __global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
     for (int ct = 0; ct < 2; ++ct) {
       const int cc = 16 * ct + (l & 15);
       const float mc = sMp[b][cc], wc = sWc[cc];
-      const long base = u.hb + (long)(t0 + tb) * u.rs + u.c0 + cc;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (tb + i < L) {
-          float d = sG[(tb + i) * LDG + cc] + x[ct][i];
-          if (mean) d += rw[i][1] * (mc + cum[ct][i]);
-          if (gate) d += rw[i][2] * wc;
-          if (a.dq32) gmem(a.dq32)[base + i * u.rs] = d;
-          else gmem((bf16*)a.dq)[base + i * u.rs] = (bf16)d;
-        }
+        float d = sG[(tb + i) * LDG + cc] + x[ct][i];
+        if (mean) d += rw[i][1] * (mc + cum[ct][i]);
+        if (gate) d += rw[i][2] * wc;
+        sG[(tb + i) * LDG + cc] = d;
       }
     }
     __syncthreads();
@@ -1581,6 +1603,7 @@ __global__ __launch_bounds__(kWalk8) void cw_dk_v3_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) float sX[CB * LDX];    // dk_extra[t][cols]
   __shared__ __attribute__((aligned(16))) float sDs[CB], sSp[CB];  // ds_t, -s_t/pos_t
   __shared__ __attribute__((aligned(16))) float sCar[32];          // carry of this chunk
+  __shared__ __attribute__((aligned(16))) float sO[CB * LDX];      // dk[t][cols] of the chunk just done
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
   const WalkUnit u = walk_unit<K>(a);
@@ -1624,16 +1647,41 @@ __global__ __launch_bounds__(kWalk8) void cw_dk_v3_kernel(const WalkArgs a) {
       prow = *gmem((const f32x4*)(a.sc + (ti0 + (long)min(lm & (CB - 1), L - 1) * a.H) * 4));
       if (mean) pdm = a.dmsum[((long)(u.gc0 + c) * a.H + u.h) * K + u.c0 + (lm & 31)];
     };
+    // dk rows of chunk c (written by the output waves into sO) as 16-byte pieces; rows past the chunk
+    // write row L - 1 again (same value, same address), so every pass issues the same stores
+    auto store_dk = [&](int c) {
+      const int Lc = chunk_len(c);
+      const long base = u.hb + (long)c * CB * u.rs + u.c0;
+      if (a.dk32) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int idx = lm + NM * j, r = min(idx >> 3, Lc - 1), cc = (idx & 7) * 4;
+          *gmem((f32x4*)(a.dk32 + base + (long)r * u.rs + cc)) = *(const f32x4*)(sO + r * LDX + cc);
+        }
+      } else {
+        const int r = min(lm >> 2, Lc - 1), cc = (lm & 3) * 8;
+        const f32x4 x0 = *(const f32x4*)(sO + r * LDX + cc), x1 = *(const f32x4*)(sO + r * LDX + cc + 4);
+        bf16x8 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o[i] = (bf16)x0[i];
+          o[4 + i] = (bf16)x1[i];
+        }
+        *gmem((bf16x8*)((bf16*)a.dk + base + (long)r * u.rs + cc)) = o;
+      }
+    };
     const int cl = u.nc - 1;
     if (u.nc > 0) load(cl);
     for (int c = cl; c >= 0; --c) {
       const int L = chunk_len(c);
-      // ---- stage
+      // ---- stage (and the dk rows of chunk c + 1; at c = cl the buffer holds no chunk yet and the
+      // rows written to chunk cl are written again with its values one chunk later)
       pq.store(sQ, LDK, L, lm);
       pk.store(sK, LDK, L, lm);
       pzh.store(sZh, LDK, L, lm);
       pzl.store(sZl, LDK, L, lm);
       if (a.dk_extra) px.store(sX, LDX, L, lm);
+      store_dk(min(c + 1, cl));
       if (lm < CB) {
         sDs[lm] = lm < L ? prow[1] : 0.f;
         sSp[lm] = lm < L ? prow[3] : 0.f;
@@ -1692,6 +1740,8 @@ __global__ __launch_bounds__(kWalk8) void cw_dk_v3_kernel(const WalkArgs a) {
                 G[rt][ct][i];
     }
     if (a.dm0 && lm < 32) a.dm0[(long)u.unit * K + u.c0 + lm] = mean ? car : 0.f;
+    // chunk 0's dk rows (written by the output waves before the last barrier)
+    if (u.nc > 0) store_dk(0);
     return;
   }
 
@@ -1718,7 +1768,6 @@ __global__ __launch_bounds__(kWalk8) void cw_dk_v3_kernel(const WalkArgs a) {
     sB2l[o] = (bf16)0.f;
   }
   for (int c = u.nc - 1; c >= 0; --c) {
-    const int t0c = c * CB, L = chunk_len(c);
     __syncthreads();
     // ---- phase 1: score tiles, element (t, j) = (16 T + 4 (l >> 4) + i, 16 J + (l & 15)), kept for
     // t >= j, written transposed to [j][t]
@@ -1806,15 +1855,9 @@ __global__ __launch_bounds__(kWalk8) void cw_dk_v3_kernel(const WalkArgs a) {
     for (int ct = 0; ct < 2; ++ct) {
       const int cc = 16 * ct + (l & 15);
       const float car = sCar[cc];
-      const long base = u.hb + (long)(t0c + jb) * u.rs + u.c0 + cc;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (jb + i < L) {
-          const float d = x[ct][i] + car + (a.dk_extra ? sX[(jb + i) * LDX + cc] : 0.f);
-          if (a.dk32) gmem(a.dk32)[base + i * u.rs] = d;
-          else gmem((bf16*)a.dk)[base + i * u.rs] = (bf16)d;
-        }
-      }
+      for (int i = 0; i < 4; ++i)
+        sO[(jb + i) * LDX + cc] = x[ct][i] + car + (a.dk_extra ? sX[(jb + i) * LDX + cc] : 0.f);
     }
     __syncthreads();
   }
