@@ -814,10 +814,14 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
   const int t = tid / TPR, part = tid % TPR;
   const long e0 = hb + (long)(t < L ? t : 0) * rs + part * PER;
   f32x4 zv[PER / 4], gv[PER / 4];
-  bf16x8 qv8[PER / 8];
-  if (mean) {
+  bf16x8 qv8[PER / 8], kv8[PER / 8];
+  if (mean || gate) {
 #pragma unroll
     for (int j = 0; j < PER / 8; ++j) qv8[j] = *(const bf16x8*)((const bf16*)a.q + e0 + 8 * j);
+  }
+  if (mean) {
+#pragma unroll
+    for (int j = 0; j < PER / 8; ++j) kv8[j] = *(const bf16x8*)((const bf16*)a.k + e0 + 8 * j);
   }
 #pragma unroll
   for (int j = 0; j < PER / 4; ++j) {
@@ -830,22 +834,30 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
       for (int i = 0; i < 4; ++i) gv[j][i] = (float)bv[i];
     }
   }
-  if (mean && tid < NSEG * K) {
-    const bf16* kp = (const bf16*)a.k + hb + col;
-    float kv[RPS];
+  if (mean) {
+    // k rows into LDS (zero past the chunk), then local column prefixes over each row segment
 #pragma unroll
-    for (int r = 0; r < RPS; ++r) {
-      const int row = seg * RPS + r;
-      kv[r] = (float)kp[(long)(row < L ? row : 0) * rs];
-    }
-    float acc = 0.f;
+    for (int j = 0; j < PER / 8; ++j) {
+      f32x4 k0, k1;
 #pragma unroll
-    for (int r = 0; r < RPS; ++r) {
-      const int row = seg * RPS + r;
-      acc += (row < L) ? kv[r] : 0.f;
-      sMt[row * LDM + col] = acc;
+      for (int i = 0; i < 4; ++i) {
+        k0[i] = t < L ? (float)kv8[j][i] : 0.f;
+        k1[i] = t < L ? (float)kv8[j][4 + i] : 0.f;
+      }
+      *(f32x4*)(sMt + t * LDM + part * PER + 8 * j) = k0;
+      *(f32x4*)(sMt + t * LDM + part * PER + 8 * j + 4) = k1;
     }
-    sOff[seg][col] = acc;  // segment total for now
+    __syncthreads();
+    if (tid < NSEG * K) {
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r < RPS; ++r) {
+        float* m = sMt + (seg * RPS + r) * LDM + col;
+        acc += *m;
+        *m = acc;
+      }
+      sOff[seg][col] = acc;  // segment total for now
+    }
   }
   __syncthreads();
   if (mean && tid < K) {
@@ -925,24 +937,24 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
   }
   if (mean || gate) {
     __syncthreads();
-    if (tid < NSEG * K) {
-      if (mean) {
+    if (mean && tid < NSEG * K) {
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r < RPS; ++r) acc += sMt[(seg * RPS + r) * LDM + col];  // rows >= L are 0
+      sD[seg][col] = acc;
+    }
+    if (gate) {
+      // dlogit_t q_t rows over this thread's region of sMt (0 past the chunk), then column sums
+      if (mean) __syncthreads();
+#pragma unroll
+      for (int j = 0; j < PER / 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sMt[t * LDM + part * PER + 8 * j + i] = g * (float)qv8[j][i];
+      __syncthreads();
+      if (tid < NSEG * K) {
         float acc = 0.f;
 #pragma unroll
-        for (int r = 0; r < RPS; ++r) acc += sMt[(seg * RPS + r) * LDM + col];  // rows >= L are 0
-        sD[seg][col] = acc;
-      }
-      if (gate) {
-        const bf16* qp = (const bf16*)a.q + hb + col;
-        float qv[RPS];
-#pragma unroll
-        for (int r = 0; r < RPS; ++r) {
-          const int row = seg * RPS + r;
-          qv[r] = (float)qp[(long)(row < L ? row : 0) * rs];
-        }
-        float acc = 0.f;
-#pragma unroll
-        for (int r = 0; r < RPS; ++r) acc += sG[seg * RPS + r] * qv[r];  // sG is 0 beyond L
+        for (int r = 0; r < RPS; ++r) acc += sMt[(seg * RPS + r) * LDM + col];
         sW[seg][col] = acc;
       }
     }
