@@ -3641,6 +3641,541 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
 }
 
 // ===========================================================================
+// gdn_bwd_dqkw for K = 128, V in {64, 128} and fp32 q_clean: a persistent kernel, one 8-wave
+// workgroup per CU over the (chunk, head) units, same results as gdn_bwd_dqkw_v3_kernel.  The
+// operands stream through two 64 KiB LDS slots by direct-to-LDS loads (global_load_lds_dwordx4:
+// no registers held, no staging pass): a unit is V/32 value pieces (h and dS' rows [32 v][128 k]
+// as hi/lo pairs, U, dU and dO columns [64 t][32 v]) and one post piece (q_clean, k, P^T).  While
+// one slot is being computed on, the next piece loads into the other, and the next unit's first
+// two pieces load during this unit's post stage.  Each piece is 8 load instructions per wave, so
+// "the piece before the newest has landed" is s_waitcnt vmcnt(8) (stores issued in between only
+// make that wait longer).  Rows are stored with an XOR swizzle of their 16-byte pieces so that
+// the MFMA operand reads (row pieces and ds_read_b64_tr_b16 column reads) are free of bank
+// conflicts; rows past the chunk are loaded from its last row and masked in the products.
+// Waves: w & 1 = 32-row half of the chunk (tr), w >> 1 = 32-column quarter of K (kc); waves 0, 1
+// and 3 also hold the 32 x 32 tiles (0,0), (32,0), (32,32) of dP = dO U^T.  The decay gradient
+// is written whole into partial 0 (partial 1 = 0).
+// ===========================================================================
+namespace dq4 {
+constexpr int SLOT = 65536;
+// value piece regions (bytes): h, h_lo, dS', dS'_lo [32 v][128 k] bf16; U, dU [64 t][32 v] fp32;
+// dO [64 t][32 v] bf16
+constexpr int RH = 0, RHL = 8192, RDH = 16384, RDHL = 24576, RU = 32768, RDU = 40960, RDO = 49152;
+// post piece regions: q_clean [64 t][128 k] fp32, k [64 t][128 k] bf16, P^T [64 s][64 t] fp32
+constexpr int RQ = 0, RK = 32768, RP = 49152;
+constexpr int LDP = 80;  // dPs rows (bf16): 160 bytes, conflict-free transposing reads
+
+// Direct-to-LDS loads: wave-uniform global base + 32-bit lane byte offset; lane i's 16 (4) bytes
+// land at LDS s + 16 i (4 i), s wave-uniform.  Written as inline assembly so that the compiler does
+// not track them: with the builtin it drains all loads (vmcnt(0)) before LDS reads it cannot tell
+// apart, which serialises the two slots.  Their completion is waited for by wait_vm alone.  The
+// instruction reads M0 one wait state after it is written (the s_nop).
+typedef __attribute__((address_space(3))) char lds_char;
+__device__ __forceinline__ void dma16(const void* base, unsigned off, char* s) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_char*)s);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(off), "s"(base) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, unsigned off, char* s) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_char*)s);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(off), "s"(base) : "memory", "m0");
+}
+// this lane's index through an opaque copy: addresses derived from it are recomputed where they
+// are used instead of being merged across the unrolled pieces (which keeps them live throughout)
+__device__ __forceinline__ int fresh_lane() {
+  int l = threadIdx.x & 63;
+  asm volatile("" : "+v"(l));
+  return l;
+}
+// s_waitcnt vmcnt(N) lgkmcnt(0)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
+}
+// workgroup barrier after this wave's LDS operations completed; a compiler fence on both sides
+// (no global wait: the direct-to-LDS loads are waited for by wait_vm)
+__device__ __forceinline__ void bar() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// Scalar loads of read-only launch tables (varlen offsets): a vector load here would make the
+// compiler drain every outstanding load, direct-to-LDS ones included, before its use.
+__device__ __forceinline__ int sld_i32(const int* p) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+  return v;
+}
+__device__ __forceinline__ long sld_i64(const int64_t* p) {
+  long v;
+  asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+  return v;
+}
+// byte offsets of swizzled elements
+__device__ __forceinline__ int off_h(int r, int k) {  // bf16 rows of 256 bytes, piece ^= 2 (r & 3)
+  return r * 256 + ((((k >> 3) ^ (2 * (r & 3))) << 4) | ((k & 7) << 1));
+}
+__device__ __forceinline__ int off_u(int r, int v) {  // fp32 rows of 128 bytes, piece ^= r & 7
+  return r * 128 + ((((v >> 2) ^ (r & 7)) << 4) | ((v & 3) << 2));
+}
+__device__ __forceinline__ int off_o(int r, int v) {  // bf16 rows of 64 bytes, piece ^= (r >> 1) & 3
+  return r * 64 + ((((v >> 3) ^ ((r >> 1) & 3)) << 4) | ((v & 7) << 1));
+}
+__device__ __forceinline__ int off_p(int s, int t) {  // fp32 rows of 256 bytes, piece ^= s & 15
+  return s * 256 + ((((t >> 2) ^ (s & 15)) << 4) | ((t & 3) << 2));
+}
+// B operand (contraction down the rows) from a swizzled [rows][128] bf16 region: columns c0 .. +31,
+// contraction rows r0 .. +15 (r0 a multiple of 16): two transposing reads (frag32_tr's lane map)
+__device__ __forceinline__ bf16x8 frag_tr_h(const char* R, int r0, int c0, int l) {
+  const int j = l & 15;
+  const int r = r0 + 8 * (l >> 5) + (j >> 2), c = c0 + 16 * ((l >> 4) & 1) + 4 * (j & 3);
+  typedef __attribute__((address_space(3))) bf16x4_t lds_b4;
+  const char* q = R + off_h(r, c);
+  const bf16x4_t x = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)q);
+  const bf16x4_t y = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)(q + 4 * 256));
+  return bf16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+// A/B operand rows r0 + l % 32, contraction v0 + 8 (l / 32) .. +7 of a swizzled fp32 [64][32] region,
+// split into hi/lo
+__device__ __forceinline__ void frag_u(const char* R, int r0, int v0, bf16x8& hi, bf16x8& lo, int l) {
+  const int r = r0 + (l & 31), c = (v0 >> 2) + 2 * (l >> 5);
+  const f32x4 x = *(const f32x4*)(R + r * 128 + ((c ^ (r & 7)) << 4));
+  const f32x4 y = *(const f32x4*)(R + r * 128 + (((c + 1) ^ (r & 7)) << 4));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bf16 h, o;
+    split2(x[i], h, o);
+    hi[i] = h;
+    lo[i] = o;
+    split2(y[i], h, o);
+    hi[4 + i] = h;
+    lo[4 + i] = o;
+  }
+}
+// A operand rows r0 + l % 32, contraction v0 + 8 (l / 32) .. +7 of the swizzled dO region
+__device__ __forceinline__ bf16x8 frag_o(const char* R, int r0, int v0, int l) {
+  const int r = r0 + (l & 31), c = (v0 >> 3) + (l >> 5);
+  return *(const bf16x8*)(R + r * 64 + ((c ^ ((r >> 1) & 3)) << 4));
+}
+// frag_rm / frag32_tr / acc_row with the lane index passed in
+__device__ __forceinline__ bf16x8 frag_rm_l(const bf16* p, int ld, int l) {
+  return *(const bf16x8*)(p + (l & 31) * ld + ((l >> 5) << 3));
+}
+__device__ __forceinline__ bf16x8 frag32_tr_l(const bf16* p, int ld, int l) {
+  const int j = l & 15;
+  const bf16* q = p + (8 * (l >> 5) + (j >> 2)) * ld + 16 * ((l >> 4) & 1) + 4 * (j & 3);
+  typedef __attribute__((address_space(3))) bf16x4_t lds_b4;
+  const bf16x4_t x = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)q);
+  const bf16x4_t y = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)(q + 4 * ld));
+  return bf16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+__device__ __forceinline__ int arow(int i, int l) { return ((i >> 2) << 3) + ((l >> 5) << 2) + (i & 3); }
+// Value held by lane l ^ M, moved by DPP (M < 16) or v_permlane16/32_swap, not through the LDS pipe
+// (ds_bpermute waits behind the direct-to-LDS traffic).
+template <int C>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), C, 0xf, 0xf, false));
+}
+template <int M>
+__device__ __forceinline__ float xlane(float x, int l) {
+  if constexpr (M == 1) {
+    return dpp_mov<0xB1>(x);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (M == 2) {
+    return dpp_mov<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (M == 4) {
+    const float up = dpp_mov<0x104>(x), dn = dpp_mov<0x114>(x);  // row_shl:4 (lane + 4), row_shr:4 (lane - 4)
+    return (l & 4) ? dn : up;
+  } else if constexpr (M == 8) {
+    return dpp_mov<0x128>(x);  // row_ror:8
+  } else if constexpr (M == 16) {
+    // odd 16-lane rows of the first operand swap with even rows of the second
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+    return __builtin_bit_cast(float, (l & 16) ? r[0] : r[1]);
+  } else {
+    static_assert(M == 32, "lane distance");
+    // rows 2, 3 of the first operand swap with rows 0, 1 of the second
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+    return __builtin_bit_cast(float, (l & 32) ? r[0] : r[1]);
+  }
+}
+__device__ __forceinline__ float wave_sum(float x, int l) {
+  x += xlane<1>(x, l);
+  x += xlane<2>(x, l);
+  x += xlane<4>(x, l);
+  x += xlane<8>(x, l);
+  x += xlane<16>(x, l);
+  return x + xlane<32>(x, l);
+}
+// Row sums of a 32 x 32 C tile: reduce-scatter over the 32 lanes of each half-wave.  Returns the
+// sum of row acc_row((l >> 1) & 15) (lanes l and l ^ 1 hold the same value).
+__device__ __forceinline__ float rowsum32(const f32x16& ev, int l) {
+  // the elements as opaque scalars: "c ? v[i] : v[j]" on the vector is otherwise turned into an
+  // index chosen at run time, i.e. a 16-way select per element
+  float e[16], a8[8], a4[4], a2[2];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    e[i] = ev[i];
+    asm volatile("" : "+v"(e[i]));
+  }
+  const bool b4 = (l >> 4) & 1, b3 = (l >> 3) & 1, b2 = (l >> 2) & 1, b1 = (l >> 1) & 1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float send = b4 ? e[i] : e[i + 8], keep = b4 ? e[i + 8] : e[i];
+    a8[i] = keep + xlane<16>(send, l);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float send = b3 ? a8[i] : a8[i + 4], keep = b3 ? a8[i + 4] : a8[i];
+    a4[i] = keep + xlane<8>(send, l);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float send = b2 ? a4[i] : a4[i + 2], keep = b2 ? a4[i + 2] : a4[i];
+    a2[i] = keep + xlane<4>(send, l);
+  }
+  const float send = b1 ? a2[0] : a2[1], keep = b1 ? a2[1] : a2[0];
+  const float a1 = keep + xlane<2>(send, l);
+  return a1 + xlane<1>(a1, l);
+}
+}  // namespace dq4
+
+template <int V>
+__global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v4_kernel(const GdnArgs a) {
+  using namespace dq4;
+  constexpr int K = 128, NP = V / 32;
+  static_assert(NP % 2 == 0, "an even number of value pieces: each unit's post piece lands in its first slot");
+  __shared__ __attribute__((aligned(1024))) char sA[SLOT];
+  __shared__ __attribute__((aligned(1024))) char sB[SLOT];
+  __shared__ __attribute__((aligned(16))) bf16 sPh[BT * LDP], sPl[BT * LDP];  // dPs [t][s] hi/lo
+  __shared__ __attribute__((aligned(16))) float sGr[8][BT];  // g of the unit's tokens (one copy per wave)
+  __shared__ __attribute__((aligned(16))) float sRP[3][32], sCP[3][32];      // dP o P row / column sums per dP tile
+  __shared__ __attribute__((aligned(16))) float sRQ[4][BT], sRK[4][BT];      // per K quarter: dQ o q_clean, dK o k
+  __shared__ __attribute__((aligned(16))) float sHD[8];
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const int tr = 32 * (w & 1), kc = 32 * (w >> 1);
+  const int dpi = w == 0 ? 0 : w == 1 ? 1 : w == 3 ? 2 : -1;  // dP tile of this wave
+  const int tp = dpi == 0 ? 0 : 32, sp = dpi == 2 ? 32 : 0;
+  const int nunits = a.NTG * a.H;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
+
+  struct Unit {
+    int u, gc, h, L;
+    long tok0;
+  };
+  // chunk_info with wave-uniform values and scalar loads
+  auto chunk_s = [&](int gc, int& L, long& tok0) {
+    if (a.cu) {
+      const int n = sld_i32(a.chunk_idx + 2 * gc);
+      if (n < 0) return false;
+      const int c = sld_i32(a.chunk_idx + 2 * gc + 1);
+      const long b0 = sld_i64(a.cu + n), b1 = sld_i64(a.cu + n + 1);
+      tok0 = b0 + (long)c * BT;
+      L = min(BT, (int)(b1 - b0) - c * BT);
+    } else {
+      const int n = gc / a.NT, c = gc - n * a.NT;
+      tok0 = (long)n * a.T + (long)c * BT;
+      L = min(BT, a.T - c * BT);
+    }
+    return true;
+  };
+  auto valid_from = [&](int u) {
+    for (; u < nunits; u += gridDim.x) {
+      int L;
+      long t0;
+      if (chunk_s(__builtin_amdgcn_readfirstlane(u / a.H), L, t0)) break;
+    }
+    return u;
+  };
+  auto locate = [&](int u) {
+    Unit x{u, 0, 0, 1, 0};
+    if (u < nunits) {
+      x.gc = __builtin_amdgcn_readfirstlane(u / a.H);
+      x.h = u - x.gc * a.H;
+      chunk_s(x.gc, x.L, x.tok0);
+    }
+    return x;
+  };
+
+  // ---- direct-to-LDS loads of one piece: 8 instructions per wave (9 for the post piece)
+  auto issue_v = [&](char* S, const Unit& x, int vb) {
+    const int v0 = 32 * vb, l = fresh_lane();
+    {
+      const long ub = (((long)x.gc * a.H + x.h) * V + v0) * K;
+      const int r = 4 * w + (l >> 4), p = l & 15;
+      const unsigned off = (unsigned)((r * K + 8 * (p ^ (2 * (r & 3)))) * 2);
+      dma16((const bf16*)a.hT + ub, off, S + RH + 1024 * w);
+      dma16((const bf16*)a.hTl + ub, off, S + RHL + 1024 * w);
+      dma16((const bf16*)a.dhT + ub, off, S + RDH + 1024 * w);
+      dma16((const bf16*)a.dhTl + ub, off, S + RDHL + 1024 * w);
+    }
+    const long ub = x.tok0 * rsv + (long)x.h * V + v0;
+    {
+      const int r = 8 * w + (l >> 3), p = l & 7;
+      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsv + 4 * (p ^ (r & 7))) * 4);
+      dma16(a.U + ub, off, S + RU + 1024 * w);
+      dma16(a.dU + ub, off, S + RDU + 1024 * w);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * w + jj, r = 4 * j + (l >> 4), d = l & 15;
+      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsv + 8 * ((d >> 2) ^ ((r >> 1) & 3)) + 2 * (d & 3)) * 2);
+      dma4((const bf16*)a.dout + ub, off, S + RDO + 256 * j);
+    }
+  };
+  auto issue_p = [&](char* S, const Unit& x) {
+    const int l = fresh_lane();
+    const long ub = x.tok0 * rsk + (long)x.h * K;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = 4 * w + jj, r = 2 * j + (l >> 5);
+      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsk + 4 * (l & 31)) * 4);
+      dma16(a.qc32 + ub, off, S + RQ + 1024 * j);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * w + jj, r = 4 * j + (l >> 4), p = l & 15;
+      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsk + 8 * (p ^ (2 * (r & 3)))) * 2);
+      dma16((const bf16*)a.k + ub, off, S + RK + 1024 * j);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * w + jj, s = 4 * j + (l >> 4), p = l & 15;
+      const unsigned off = (unsigned)((s * BT + 4 * (p ^ (s & 15))) * 4);
+      dma16(a.PT + ((long)x.gc * a.H + x.h) * (BT * BT), off, S + RP + 1024 * j);
+    }
+    // g of the unit's tokens (the last token's past the chunk), a copy per wave
+    dma4(a.gcum + x.tok0 * a.H + x.h, (unsigned)(min(l, x.L - 1) * a.H * 4), (char*)&sGr[w][0]);
+  };
+
+  f32x16 dQi, dKs, dW, dP;
+  float hds;
+
+  // ---- one value piece: <h, dS'>, dQi += dO h^T, dKs += U dS'^T, dW += dU h^T, dP += dO U^T
+  auto compute_v = [&](const char* S) {
+    const int l = fresh_lane();
+    {
+      const int o = 16 * (64 * w + l);
+      const bf16x8 x1 = *(const bf16x8*)(S + RH + o), x2 = *(const bf16x8*)(S + RHL + o);
+      const bf16x8 y1 = *(const bf16x8*)(S + RDH + o), y2 = *(const bf16x8*)(S + RDHL + o);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hds += ((float)x1[i] + (float)x2[i]) * ((float)y1[i] + (float)y2[i]);
+    }
+#pragma unroll
+    for (int v0 = 0; v0 < 32; v0 += 16) {
+      const bf16x8 oa = frag_o(S + RDO, tr, v0, l);
+      const bf16x8 hb = frag_tr_h(S + RH, v0, kc, l), hbl = frag_tr_h(S + RHL, v0, kc, l);
+      const bf16x8 db = frag_tr_h(S + RDH, v0, kc, l), dbl = frag_tr_h(S + RDHL, v0, kc, l);
+      bf16x8 uh, ul, dh, dl;
+      frag_u(S + RU, tr, v0, uh, ul, l);
+      frag_u(S + RDU, tr, v0, dh, dl, l);
+      dQi = mfma(oa, hb, dQi);
+      dQi = mfma(oa, hbl, dQi);
+      dKs = mfma(uh, db, dKs);
+      dKs = mfma(ul, db, dKs);
+      dKs = mfma(uh, dbl, dKs);
+      dW = mfma(dh, hb, dW);
+      dW = mfma(dl, hb, dW);
+      dW = mfma(dh, hbl, dW);
+      if (dpi == 0 || dpi == 2) {
+        dP = mfma(oa, uh, dP);
+        dP = mfma(oa, ul, dP);
+      } else if (dpi == 1) {
+        bf16x8 sh, sl;
+        frag_u(S + RU, 0, v0, sh, sl, l);
+        dP = mfma(oa, sh, dP);
+        dP = mfma(oa, sl, dP);
+      }
+    }
+  };
+
+  // ---- post stage on the post piece in S
+  auto post = [&](const char* S, const Unit& x) {
+    const int L = x.L, l = fresh_lane();
+    // dP (waves 0, 1, 3): causal and chunk mask, dPs = scale dP Gamma as hi/lo [t][s], dP o P sums
+    if (dpi >= 0) {
+      const int c = sp + (l & 31);
+      const float gcol = sGr[0][c];
+      f32x16 e;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r4 = tp + arow(4 * q, l);
+        const f32x4 pv = *(const f32x4*)(S + RP + off_p(c, r4));  // P[r][c] = P^T[c][r]
+        const f32x4 gr = *(const f32x4*)&sGr[0][r4];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int i = 4 * q + ii, r = r4 + ii;
+          const bool keep = r >= c && r < L;
+          const float d = keep ? dP[i] : 0.f;
+          const float ev = __expf(gr[ii] - gcol);  // (overflow only where masked)
+          const float ps = keep ? d * a.scale * ev : 0.f;
+          bf16 hi, lo;
+          split2(ps, hi, lo);
+          sPh[r * LDP + c] = hi;
+          sPl[r * LDP + c] = lo;
+          e[i] = d * pv[ii];
+        }
+      }
+      float cs = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) cs += e[i];
+      cs += xlane<32>(cs, l);
+      if (l < 32) sCP[dpi][l] = cs;
+      const float rs = rowsum32(e, l);
+      if ((l & 1) == 0) sRP[dpi][arow((l >> 1) & 15, l)] = rs;
+    }
+    // scale the state parts; dG terms sum_k dQ q_clean and sum_k dK k over this wave's columns
+    {
+      const int c = kc + (l & 31);
+      const float gl = sGr[0][L - 1];
+      f32x16 e, f, gv;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 g4 = *(const f32x4*)&sGr[0][tr + arow(4 * q, l)];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) gv[4 * q + ii] = g4[ii];
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = tr + arow(i, l);
+        const float g = gv[i];
+        dQi[i] *= a.scale * __expf(g);
+        e[i] = dQi[i] * *(const float*)(S + RQ + r * 512 + 4 * c);
+        dKs[i] *= __expf(gl - g);
+        f[i] = dKs[i] * (float)*(const bf16*)(S + RK + off_h(r, c));
+      }
+      const float re = rowsum32(e, l), rf = rowsum32(f, l);
+      if ((l & 1) == 0) {
+        const int r = tr + arow((l >> 1) & 15, l);
+        sRQ[w >> 1][r] = re;
+        sRK[w >> 1][r] = rf;
+      }
+    }
+    {
+      const float s = wave_sum(hds, l);
+      if (l == 0) sHD[w] = s;
+    }
+    bar();
+    // dq = scale gamma dQi + dPs k (s <= t: the t < 32 half needs s < 32 only)
+    {
+#pragma unroll
+      for (int s0 = 0; s0 < BT; s0 += 16) {
+        if (tr == 0 && s0 >= 32) break;
+        const bf16x8 kb = frag_tr_h(S + RK, s0, kc, l);
+        dQi = mfma(frag_rm_l(sPh + tr * LDP + s0, LDP, l), kb, dQi);
+        dQi = mfma(frag_rm_l(sPl + tr * LDP + s0, LDP, l), kb, dQi);
+      }
+      const auto rs = buf_rsrc(a.dq32 + x.tok0 * rsk + (long)x.h * K, (int)(((L - 1) * rsk + K) * 4));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = tr + arow(i, l);
+        const float x = dQi[i];  // (bit_cast of a vector element reference reads element 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), rs, (int)((r * rsk + kc + (l & 31)) * 4), 0, 0);
+      }
+    }
+    // dk = fac dKs + dPs^T q_clean (i >= j: the j >= 32 half needs i >= 32 only); dw = -dW
+    {
+      const int c = kc + (l & 31);
+#pragma unroll
+      for (int i0 = 0; i0 < BT; i0 += 16) {
+        if (tr == 32 && i0 < 32) continue;
+        const bf16x8 ah = frag32_tr_l(sPh + i0 * LDP + tr, LDP, l), al = frag32_tr_l(sPl + i0 * LDP + tr, LDP, l);
+        bf16x8 bh, bl;
+        const int ib = i0 + 8 * (l >> 5);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          bf16 hh, oo;
+          split2(*(const float*)(S + RQ + (ib + e) * 512 + 4 * c), hh, oo);
+          bh[e] = hh;
+          bl[e] = oo;
+        }
+        dKs = mfma(ah, bh, dKs);
+        dKs = mfma(ah, bl, dKs);
+        dKs = mfma(al, bh, dKs);
+      }
+      const int bytes = (int)(((L - 1) * rsk + K) * 4);
+      const auto rk = buf_rsrc(a.dkp32 + x.tok0 * rsk + (long)x.h * K, bytes);
+      const auto rw = buf_rsrc(a.dw32 + x.tok0 * rsk + (long)x.h * K, bytes);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = tr + arow(i, l), off = (int)((r * rsk + c) * 4);
+        const float xk = dKs[i], xw = -dW[i];
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, xk), rk, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, xw), rw, off, 0, 0);
+      }
+    }
+    bar();
+    // decay gradient of token t: (dP o P) row t - column t + dQ o q_clean - dK o k; the last token
+    // also takes every dK o k term and e^{G_L} <h, dS'>
+    if (w == 0) {
+      const int t = l;
+      const float term = t < L ? sRK[0][t] + sRK[1][t] + sRK[2][t] + sRK[3][t] : 0.f;
+      const float tot = wave_sum(term, l);
+      if (t < L) {
+        float d = t < 32 ? sRP[0][t] - sCP[0][t] - sCP[1][t]
+                         : sRP[1][t - 32] + sRP[2][t - 32] - sCP[2][t - 32];
+        d += sRQ[0][t] + sRQ[1][t] + sRQ[2][t] + sRQ[3][t] - term;
+        if (t == L - 1) {
+          float hsum = 0.f;
+#pragma unroll
+          for (int ww = 0; ww < 8; ++ww) hsum += sHD[ww];
+          d += tot + __expf(sGr[0][L - 1]) * hsum;
+        }
+        const long gi = (x.tok0 + t) * a.H + x.h;
+        a.dgp[gi] = d;
+        a.dgp[ntok * a.H + gi] = 0.f;
+      }
+    }
+  };
+
+  // ---- one unit: value pieces alternate X, Y, X, ...; the post piece lands in X
+  auto unit = [&](char* X, char* Y, const Unit& cur, const Unit& nxt) {
+    const bool more = nxt.u < nunits;
+    dQi = zero16();
+    dKs = zero16();
+    dW = zero16();
+    dP = zero16();
+    hds = 0.f;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      char* S = (j & 1) ? Y : X;
+      if (j == NP - 1) wait_vm<9>();  // the post piece is the newer one in flight
+      else wait_vm<8>();
+      bar();
+      compute_v(S);
+      bar();
+      if (j + 2 < NP) issue_v(S, cur, j + 2);
+      else if (j + 2 == NP) issue_p(S, cur);
+      else if (more) issue_v(S, nxt, 0);
+    }
+    if (more) wait_vm<8>();
+    else wait_vm<0>();
+    bar();
+    post(X, cur);
+    bar();
+    if (more) issue_v(X, nxt, 1);
+  };
+
+  Unit cur = locate(valid_from(blockIdx.x));
+  if (cur.u >= nunits) return;
+  Unit nxt = locate(valid_from(cur.u + gridDim.x));
+  issue_v(sA, cur, 0);
+  issue_v(sB, cur, 1);
+  while (true) {
+    unit(sA, sB, cur, nxt);
+    if (nxt.u >= nunits) break;
+    cur = nxt;
+    nxt = locate(valid_from(cur.u + gridDim.x));
+    unit(sB, sA, cur, nxt);
+    if (nxt.u >= nunits) break;
+    cur = nxt;
+    nxt = locate(valid_from(cur.u + gridDim.x));
+  }
+}
+
+// ===========================================================================
 // launchers (one per kernel so the C ABI can time each launch)
 // ===========================================================================
 // Compute units of the current device (the persistent kernels launch one workgroup per CU).
@@ -3699,7 +4234,13 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
         hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdDqkw:
-      if (K == 128)
+      if (K == 128 && a.qc32 && (V == 64 || V == 128)) {
+        const int grid = min(a.NTG * a.H, cu_count());
+        if (V == 128)
+          hipLaunchKernelGGL(gdn_bwd_dqkw_v4_kernel<128>, dim3(grid), dim3(kWalk8), 0, st, a);
+        else
+          hipLaunchKernelGGL(gdn_bwd_dqkw_v4_kernel<64>, dim3(grid), dim3(kWalk8), 0, st, a);
+      } else if (K == 128)
         hipLaunchKernelGGL(gdn_bwd_dqkw_v3_kernel<128>, dim3(1, a.NTG, a.H), dim3(kWalk8), 0, st, a, V);
       else
         hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);

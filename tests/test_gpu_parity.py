@@ -178,10 +178,14 @@ def test_gdn_backbone(case):
 
 
 FUSED_CASES = [
-    # B, T, H, K, V, l2norm-in-kernel, states, pos_off
+    # B, T, H, K, V, l2norm-in-kernel, states, pos_off[, varlen]
     (2, 130, 2, 64, 64, True, True, 0),
     (1, 256, 2, 128, 128, True, False, 0),
     (1, 100, 1, 128, 64, False, True, 5),
+    # more (chunk, head) units than CUs, ragged last chunk: the persistent dq/dk/dw backward streams
+    # several units per workgroup
+    (2, 2000, 8, 128, 128, False, False, 0),
+    (1, 3000, 8, 128, 64, True, False, 0, [0, 900, 1700, 3000]),
 ]
 
 
@@ -189,7 +193,9 @@ FUSED_CASES = [
 def test_fused_ccq_gdn(case):
     dev = _cuda()
     from ccq_amd import fused_chunk_ccq_gdn
-    B, T, H, K, V, use_l2, st, off = case
+    B, T, H, K, V, use_l2, st, off = case[:8]
+    cu = case[8] if len(case) > 8 else None
+    cu_t = torch.tensor(cu, dtype=torch.int64) if cu is not None else None
     x, gen = gdn_inputs(B, T, H, K, V, seed=3, with_state=st, device="cpu")
     if use_l2:  # un-normalised q, k so the l2norm matters
         x["q"] = bf(torch.randn(B, T, H, K, generator=gen))
@@ -205,14 +211,14 @@ def test_fused_ccq_gdn(case):
     o_r, s_r, h_r, m_r = O.ccq_gdn_forward(ref["q"], ref["k"], ref["v"], ref["lam"], ref["g"], ref["beta"],
                                            h0=ref["s0"], h0_cov=ref.get("h0"), m0=ref.get("m0"),
                                            position_offset=off, use_qk_l2norm=use_l2,
-                                           l2norm_dtype=torch.bfloat16)
+                                           l2norm_dtype=torch.bfloat16, cu_seqlens=cu_t)
     (o_r * do.to(d)).sum().backward()
 
     g = {n: (t.to(dev).requires_grad_() if t is not None else None) for n, t in x.items()}
     o, s, h, m = fused_chunk_ccq_gdn(g["q"], g["k"], g["v"], g["lam"], g["g"], g["beta"], initial_state=g["s0"],
                                      initial_cov_state=g.get("h0"), initial_mean_state=g.get("m0"),
                                      output_final_state=True, use_qk_l2norm_in_kernel=use_l2,
-                                     position_offset=off)
+                                     position_offset=off, cu_seqlens=cu_t.to(dev) if cu_t is not None else None)
     (o.float() * do.to(dev).float()).sum().backward()
     torch.cuda.synchronize()
     errs = {"o": rel(o, o_r), "S": rel(s, s_r), "C": rel(h, h_r), "m": rel(m, m_r)}
