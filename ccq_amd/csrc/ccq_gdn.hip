@@ -4176,6 +4176,361 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v4_kernel(const GdnArgs a
 }
 
 // ===========================================================================
+// gdn_bwd_dqkw for K = V = 128 and fp32 q_clean, three-slot form of gdn_bwd_dqkw_v4_kernel: a
+// unit is six pieces in three 52 KiB LDS slots -- value pieces V0 .. V3 (slots 0 1 2 0), then
+// q_clean (slot 1) and k with P^T (slot 2; dPs is formed in that slot's tail).  A piece is loaded
+// one to two phases ahead, during the compute of an earlier piece (the next unit's V0 during the
+// post stage, its V1 as soon as the post stage's products are done), and the load instructions
+// are issued between MFMAs (waves 0-3 after the first 16-value step, waves 4-7 after the second),
+// so that the two waves of a SIMD stall on issue at different times.  One barrier per piece.
+// Loads per wave: value piece 8, q_clean piece 4 (5 for wave 0, which also loads g), k/P^T piece
+// 4; the wait before a piece is vmcnt(loads issued after it).
+// ===========================================================================
+namespace dq5 {
+constexpr int SLOT = 53248;
+constexpr int RK = 0, RP = 16384;     // k [64 t][128 k] bf16, P^T [64 s][64 t] fp32
+constexpr int RPH = 32768, RPL = RPH + dq4::LDP * BT * 2;  // dPs hi / lo [t][s] in the k/P^T slot
+}  // namespace dq5
+
+__global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a) {
+  using namespace dq4;
+  using dq5::SLOT;
+  constexpr int K = 128, V = 128;
+  __shared__ __attribute__((aligned(1024))) char s0[SLOT];
+  __shared__ __attribute__((aligned(1024))) char s1[SLOT];
+  __shared__ __attribute__((aligned(1024))) char s2[SLOT];
+  __shared__ __attribute__((aligned(16))) float sRP[3][32], sCP[3][32];  // dP o P row / column sums per dP tile
+  __shared__ __attribute__((aligned(16))) float sRQ[4][BT], sRK[4][BT];  // per K quarter: dQ o q_clean, dK o k
+  __shared__ __attribute__((aligned(16))) float sHD[8];
+  __shared__ __attribute__((aligned(16))) float sG[BT];                  // g of the unit's tokens
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int tr = 32 * (w & 1), kc = 32 * (w >> 1);
+  const int dpi = w == 0 ? 0 : w == 1 ? 1 : w == 3 ? 2 : -1;  // dP tile of this wave
+  const int tp = dpi == 0 ? 0 : 32, sp = dpi == 2 ? 32 : 0;
+  const bool early = w < 4;  // issues its loads after the first 16-value step
+  const int nunits = a.NTG * a.H;
+  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
+  const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
+  bf16* const sPh = (bf16*)(s2 + dq5::RPH);
+  bf16* const sPl = (bf16*)(s2 + dq5::RPL);
+
+  struct Unit {
+    int u, gc, h, L;
+    long tok0;
+  };
+  auto chunk_s = [&](int gc, int& L, long& tok0) {
+    if (a.cu) {
+      const int n = sld_i32(a.chunk_idx + 2 * gc);
+      if (n < 0) return false;
+      const int c = sld_i32(a.chunk_idx + 2 * gc + 1);
+      const long b0 = sld_i64(a.cu + n), b1 = sld_i64(a.cu + n + 1);
+      tok0 = b0 + (long)c * BT;
+      L = min(BT, (int)(b1 - b0) - c * BT);
+    } else {
+      const int n = gc / a.NT, c = gc - n * a.NT;
+      tok0 = (long)n * a.T + (long)c * BT;
+      L = min(BT, a.T - c * BT);
+    }
+    return true;
+  };
+  auto valid_from = [&](int u) {
+    for (; u < nunits; u += gridDim.x) {
+      int L;
+      long t0;
+      if (chunk_s(__builtin_amdgcn_readfirstlane(u / a.H), L, t0)) break;
+    }
+    return u;
+  };
+  auto locate = [&](int u) {
+    Unit x{u, 0, 0, 1, 0};
+    if (u < nunits) {
+      x.gc = __builtin_amdgcn_readfirstlane(u / a.H);
+      x.h = u - x.gc * a.H;
+      chunk_s(x.gc, x.L, x.tok0);
+    }
+    return x;
+  };
+
+  // ---- direct-to-LDS loads
+  auto issue_v = [&](char* S, const Unit& x, int vb) {  // 8 per wave
+    const int v0 = 32 * vb, l = fresh_lane();
+    {
+      const long ub = (((long)x.gc * a.H + x.h) * V + v0) * K;
+      const int r = 4 * w + (l >> 4), p = l & 15;
+      const unsigned off = (unsigned)((r * K + 8 * (p ^ (2 * (r & 3)))) * 2);
+      dma16((const bf16*)a.hT + ub, off, S + RH + 1024 * w);
+      dma16((const bf16*)a.hTl + ub, off, S + RHL + 1024 * w);
+      dma16((const bf16*)a.dhT + ub, off, S + RDH + 1024 * w);
+      dma16((const bf16*)a.dhTl + ub, off, S + RDHL + 1024 * w);
+    }
+    const long ub = x.tok0 * rsv + (long)x.h * V + v0;
+    {
+      const int r = 8 * w + (l >> 3), p = l & 7;
+      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsv + 4 * (p ^ (r & 7))) * 4);
+      dma16(a.U + ub, off, S + RU + 1024 * w);
+      dma16(a.dU + ub, off, S + RDU + 1024 * w);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * w + jj, r = 4 * j + (l >> 4), d = l & 15;
+      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsv + 8 * ((d >> 2) ^ ((r >> 1) & 3)) + 2 * (d & 3)) * 2);
+      dma4((const bf16*)a.dout + ub, off, S + RDO + 256 * j);
+    }
+  };
+  auto issue_qa = [&](char* S, const Unit& x) {  // q_clean (+ g on wave 0): 4 per wave, 5 on wave 0
+    const int l = fresh_lane();
+    const long ub = x.tok0 * rsk + (long)x.h * K;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = 4 * w + jj, r = 2 * j + (l >> 5);
+      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsk + 4 * (l & 31)) * 4);
+      dma16(a.qc32 + ub, off, S + RQ + 1024 * j);
+    }
+    // g of the unit's tokens (the last token's past the chunk)
+    if (w == 0) dma4(a.gcum + x.tok0 * a.H + x.h, (unsigned)(min(l, x.L - 1) * a.H * 4), (char*)sG);
+  };
+  auto issue_kp = [&](char* S, const Unit& x) {  // k + P^T: 4 per wave
+    const int l = fresh_lane();
+    const long ub = x.tok0 * rsk + (long)x.h * K;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * w + jj, r = 4 * j + (l >> 4), p = l & 15;
+      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsk + 8 * (p ^ (2 * (r & 3)))) * 2);
+      dma16((const bf16*)a.k + ub, off, S + dq5::RK + 1024 * j);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * w + jj, s = 4 * j + (l >> 4), p = l & 15;
+      const unsigned off = (unsigned)((s * BT + 4 * (p ^ (s & 15))) * 4);
+      dma16(a.PT + ((long)x.gc * a.H + x.h) * (BT * BT), off, S + dq5::RP + 1024 * j);
+    }
+  };
+
+  f32x16 dQi, dKs, dW, dP;
+  float hds;
+
+  // ---- one value piece (as gdn_bwd_dqkw_v4_kernel); `iss` issues this phase's loads between the
+  // two 16-value steps (early waves) or after them (the others)
+  auto compute_v = [&](const char* S, auto&& iss) {
+    const int l = fresh_lane();
+    {
+      const int o = 16 * (64 * w + l);
+      const bf16x8 x1 = *(const bf16x8*)(S + RH + o), x2 = *(const bf16x8*)(S + RHL + o);
+      const bf16x8 y1 = *(const bf16x8*)(S + RDH + o), y2 = *(const bf16x8*)(S + RDHL + o);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hds += ((float)x1[i] + (float)x2[i]) * ((float)y1[i] + (float)y2[i]);
+    }
+#pragma unroll
+    for (int v0 = 0; v0 < 32; v0 += 16) {
+      const bf16x8 oa = frag_o(S + RDO, tr, v0, l);
+      const bf16x8 hb = frag_tr_h(S + RH, v0, kc, l), hbl = frag_tr_h(S + RHL, v0, kc, l);
+      const bf16x8 db = frag_tr_h(S + RDH, v0, kc, l), dbl = frag_tr_h(S + RDHL, v0, kc, l);
+      bf16x8 uh, ul, dh, dl;
+      frag_u(S + RU, tr, v0, uh, ul, l);
+      frag_u(S + RDU, tr, v0, dh, dl, l);
+      dQi = mfma(oa, hb, dQi);
+      dQi = mfma(oa, hbl, dQi);
+      dKs = mfma(uh, db, dKs);
+      dKs = mfma(ul, db, dKs);
+      dKs = mfma(uh, dbl, dKs);
+      dW = mfma(dh, hb, dW);
+      dW = mfma(dl, hb, dW);
+      dW = mfma(dh, hbl, dW);
+      if (dpi == 0 || dpi == 2) {
+        dP = mfma(oa, uh, dP);
+        dP = mfma(oa, ul, dP);
+      } else if (dpi == 1) {
+        bf16x8 sh, sl;
+        frag_u(S + RU, 0, v0, sh, sl, l);
+        dP = mfma(oa, sh, dP);
+        dP = mfma(oa, sl, dP);
+      }
+      if ((v0 == 0) == early) iss();
+    }
+  };
+
+  // ---- post stage on the q_clean piece Q and the k/P^T piece KP
+  auto post = [&](const char* Q, const char* KP, const Unit& x, auto&& iss, auto&& iss_after) {
+    const int L = x.L, l = fresh_lane();
+    if (early) iss();
+    // dP (waves 0, 1, 3): causal and chunk mask, dPs = scale dP Gamma as hi/lo [t][s], dP o P sums
+    if (dpi >= 0) {
+      const int c = sp + (l & 31);
+      const float gcol = sG[c];
+      f32x16 e;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r4 = tp + arow(4 * q, l);
+        const f32x4 pv = *(const f32x4*)(KP + dq5::RP + off_p(c, r4));  // P[r][c] = P^T[c][r]
+        const f32x4 gr = *(const f32x4*)&sG[r4];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int i = 4 * q + ii, r = r4 + ii;
+          const bool keep = r >= c && r < L;
+          const float d = keep ? dP[i] : 0.f;
+          const float ev = __expf(gr[ii] - gcol);  // (overflow only where masked)
+          const float ps = keep ? d * a.scale * ev : 0.f;
+          bf16 hi, lo;
+          split2(ps, hi, lo);
+          sPh[r * LDP + c] = hi;
+          sPl[r * LDP + c] = lo;
+          e[i] = d * pv[ii];
+        }
+      }
+      float cs = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) cs += e[i];
+      cs += xlane<32>(cs, l);
+      if (l < 32) sCP[dpi][l] = cs;
+      const float rs = rowsum32(e, l);
+      if ((l & 1) == 0) sRP[dpi][arow((l >> 1) & 15, l)] = rs;
+    }
+    // scale the state parts; dG terms sum_k dQ q_clean and sum_k dK k over this wave's columns
+    {
+      const int c = kc + (l & 31);
+      const float gl = sG[L - 1];
+      f32x16 e, f, gv;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 g4 = *(const f32x4*)&sG[tr + arow(4 * q, l)];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) gv[4 * q + ii] = g4[ii];
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = tr + arow(i, l);
+        const float g = gv[i];
+        dQi[i] *= a.scale * __expf(g);
+        e[i] = dQi[i] * *(const float*)(Q + RQ + r * 512 + 4 * c);
+        dKs[i] *= __expf(gl - g);
+        f[i] = dKs[i] * (float)*(const bf16*)(KP + dq5::RK + off_h(r, c));
+      }
+      const float re = rowsum32(e, l), rf = rowsum32(f, l);
+      if ((l & 1) == 0) {
+        const int r = tr + arow((l >> 1) & 15, l);
+        sRQ[w >> 1][r] = re;
+        sRK[w >> 1][r] = rf;
+      }
+    }
+    {
+      const float s = wave_sum(hds, l);
+      if (l == 0) sHD[w] = s;
+    }
+    if (!early) iss();
+    bar();
+    // dq = scale gamma dQi + dPs k (s <= t: the t < 32 half needs s < 32 only)
+    {
+#pragma unroll
+      for (int s0 = 0; s0 < BT; s0 += 16) {
+        if (tr == 0 && s0 >= 32) break;
+        const bf16x8 kb = frag_tr_h(KP + dq5::RK, s0, kc, l);
+        dQi = mfma(frag_rm_l(sPh + tr * LDP + s0, LDP, l), kb, dQi);
+        dQi = mfma(frag_rm_l(sPl + tr * LDP + s0, LDP, l), kb, dQi);
+      }
+      const auto rs = buf_rsrc(a.dq32 + x.tok0 * rsk + (long)x.h * K, (int)(((L - 1) * rsk + K) * 4));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = tr + arow(i, l);
+        const float xq = dQi[i];  // (bit_cast of a vector element reference reads element 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, xq), rs, (int)((r * rsk + kc + (l & 31)) * 4), 0, 0);
+      }
+    }
+    // dk = fac dKs + dPs^T q_clean (i >= j: the j >= 32 half needs i >= 32 only); dw = -dW
+    {
+      const int c = kc + (l & 31);
+#pragma unroll
+      for (int i0 = 0; i0 < BT; i0 += 16) {
+        if (tr == 32 && i0 < 32) continue;
+        const bf16x8 ah = frag32_tr_l(sPh + i0 * LDP + tr, LDP, l), al = frag32_tr_l(sPl + i0 * LDP + tr, LDP, l);
+        bf16x8 bh, bl;
+        const int ib = i0 + 8 * (l >> 5);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          bf16 hh, oo;
+          split2(*(const float*)(Q + RQ + (ib + e) * 512 + 4 * c), hh, oo);
+          bh[e] = hh;
+          bl[e] = oo;
+        }
+        dKs = mfma(ah, bh, dKs);
+        dKs = mfma(ah, bl, dKs);
+        dKs = mfma(al, bh, dKs);
+      }
+      const int bytes = (int)(((L - 1) * rsk + K) * 4);
+      const auto rk = buf_rsrc(a.dkp32 + x.tok0 * rsk + (long)x.h * K, bytes);
+      const auto rw = buf_rsrc(a.dw32 + x.tok0 * rsk + (long)x.h * K, bytes);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = tr + arow(i, l), off = (int)((r * rsk + c) * 4);
+        const float xk = dKs[i], xw = -dW[i];
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, xk), rk, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, xw), rw, off, 0, 0);
+      }
+    }
+    bar();
+    iss_after();  // the q_clean slot is free
+    // decay gradient of token t: (dP o P) row t - column t + dQ o q_clean - dK o k; the last token
+    // also takes every dK o k term and e^{G_L} <h, dS'>
+    if (w == 0) {
+      const int t = l;
+      const float term = t < L ? sRK[0][t] + sRK[1][t] + sRK[2][t] + sRK[3][t] : 0.f;
+      const float tot = wave_sum(term, l);
+      if (t < L) {
+        float d = t < 32 ? sRP[0][t] - sCP[0][t] - sCP[1][t]
+                         : sRP[1][t - 32] + sRP[2][t - 32] - sCP[2][t - 32];
+        d += sRQ[0][t] + sRQ[1][t] + sRQ[2][t] + sRQ[3][t] - term;
+        if (t == L - 1) {
+          float hsum = 0.f;
+#pragma unroll
+          for (int ww = 0; ww < 8; ++ww) hsum += sHD[ww];
+          d += tot + __expf(sG[L - 1]) * hsum;
+        }
+        const long gi = (x.tok0 + t) * a.H + x.h;
+        a.dgp[gi] = d;
+        a.dgp[ntok * a.H + gi] = 0.f;
+      }
+    }
+  };
+
+  // ---- unit loop.  Slots: V0 s0, V1 s1, V2 s2, V3 s0, q_clean s1, k/P^T s2; the next unit's V0
+  // is loaded during this unit's post stage, its V1 right after the post stage's products, its V2
+  // during its own V0 phase.
+  Unit cur = locate(valid_from(blockIdx.x));
+  if (cur.u >= nunits) return;
+  issue_v(s0, cur, 0);
+  issue_v(s1, cur, 1);
+  while (true) {
+    const Unit nxt = locate(valid_from(cur.u + gridDim.x));
+    const bool more = nxt.u < nunits;
+    dQi = zero16();
+    dKs = zero16();
+    dW = zero16();
+    dP = zero16();
+    hds = 0.f;
+    wait_vm<8>();  // V0 (V1 newer; the previous post stage's stores drain with V0)
+    bar();
+    compute_v(s0, [&] { issue_v(s2, cur, 2); });
+    wait_vm<8>();  // V1 (V2 newer)
+    bar();
+    compute_v(s1, [&] { issue_v(s0, cur, 3); });
+    wait_vm<8>();  // V2 (V3 newer)
+    bar();
+    compute_v(s2, [&] { issue_qa(s1, cur); });
+    if (w == 0) wait_vm<5>();  // V3 (the q_clean piece newer)
+    else wait_vm<4>();
+    bar();
+    compute_v(s0, [&] { issue_kp(s2, cur); });
+    wait_vm<0>();  // q_clean and k/P^T pieces
+    bar();
+    post(
+        s1, s2, cur, [&] { if (more) issue_v(s0, nxt, 0); },
+        [&] { if (more) issue_v(s1, nxt, 1); });
+    if (!more) break;
+    cur = nxt;
+  }
+}
+
+// ===========================================================================
 // launchers (one per kernel so the C ABI can time each launch)
 // ===========================================================================
 // Compute units of the current device (the persistent kernels launch one workgroup per CU).
@@ -4237,7 +4592,7 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       if (K == 128 && a.qc32 && (V == 64 || V == 128)) {
         const int grid = min(a.NTG * a.H, cu_count());
         if (V == 128)
-          hipLaunchKernelGGL(gdn_bwd_dqkw_v4_kernel<128>, dim3(grid), dim3(kWalk8), 0, st, a);
+          hipLaunchKernelGGL(gdn_bwd_dqkw_v5_kernel, dim3(grid), dim3(kWalk8), 0, st, a);
         else
           hipLaunchKernelGGL(gdn_bwd_dqkw_v4_kernel<64>, dim3(grid), dim3(kWalk8), 0, st, a);
       } else if (K == 128)
