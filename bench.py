@@ -72,14 +72,14 @@ MULTI_KERNEL_STAGES = ("clean_bwd_gate",)
 # reading for a known-size elementwise copy (fetch x2.000, write x1.000).  Re-measured whenever a
 # kernel changes; a stage absent here reports traffic null.
 MEASURED_TRAFFIC_BYTES = {
-    "gdn_bwd_dqkw": (1174.3e6, 444.6e6),
-    "gdn_fwd_state": (478.7e6, 537.6e6),
+    "gdn_bwd_dqkw": (1166.9e6, 419.4e6),
+    "gdn_fwd_state": (478.5e6, 537.5e6),
     "gdn_bwd_state": (478.4e6, 402.7e6),
     "clean_bwd_dk": (438.6e6, 67.1e6),
-    "clean_fwd": (142.4e6, 287.3e6),
-    "clean_bwd_dq": (371.4e6, 67.1e6),
+    "clean_fwd": (148.9e6, 287.3e6),
+    "clean_bwd_dq": (371.6e6, 67.1e6),
     "gdn_bwd_wy": (638.0e6, 218.1e6),
-    "clean_bwd_rows": (430.9e6, 157.1e6),
+    "clean_bwd_rows": (428.8e6, 153.6e6),
     "gdn_prep": (151.3e6, 343.9e6),
 }
 
