@@ -186,6 +186,7 @@ FUSED_CASES = [
     # several units per workgroup
     (2, 2000, 8, 128, 128, False, False, 0),
     (1, 3000, 8, 128, 64, True, False, 0, [0, 900, 1700, 3000]),
+    (1, 2500, 8, 128, 128, False, False, 0, [0, 333, 1400, 1401, 2500]),
 ]
 
 
