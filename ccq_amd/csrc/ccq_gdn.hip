@@ -4176,15 +4176,16 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v4_kernel(const GdnArgs a
 }
 
 // ===========================================================================
-// gdn_bwd_dqkw for K = V = 128 and fp32 q_clean, three-slot form of gdn_bwd_dqkw_v4_kernel: a
+// gdn_bwd_dqkw for K = V = 128 (q_clean fp32 or bf16), three-slot form of gdn_bwd_dqkw_v4_kernel: a
 // unit is six pieces in three 52 KiB LDS slots -- value pieces V0 .. V3 (slots 0 1 2 0), then
 // q_clean (slot 1) and k with P^T (slot 2; dPs is formed in that slot's tail).  A piece is loaded
 // one to two phases ahead, during the compute of an earlier piece (the next unit's V0 during the
 // post stage, its V1 as soon as the post stage's products are done), and the load instructions
 // are issued between MFMAs (waves 0-3 after the first 16-value step, waves 4-7 after the second),
 // so that the two waves of a SIMD stall on issue at different times.  One barrier per piece.
-// Loads per wave: value piece 8, q_clean piece 4 (5 for wave 0, which also loads g), k/P^T piece
-// 4; the wait before a piece is vmcnt(loads issued after it).
+// Loads per wave: value piece 8, q_clean piece 4 fp32 / 2 bf16 (one more on wave 0, which also
+// loads g), k/P^T piece 4; the wait before a piece is vmcnt(loads issued after it).  A bf16
+// q_clean is stored swizzled like k and read with transposing reads; its lo part is zero.
 // ===========================================================================
 namespace dq5 {
 constexpr int SLOT = 53248;
@@ -4192,6 +4193,7 @@ constexpr int RK = 0, RP = 16384;     // k [64 t][128 k] bf16, P^T [64 s][64 t] 
 constexpr int RPH = 32768, RPL = RPH + dq4::LDP * BT * 2;  // dPs hi / lo [t][s] in the k/P^T slot
 }  // namespace dq5
 
+template <bool Q32>
 __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a) {
   using namespace dq4;
   using dq5::SLOT;
@@ -4278,14 +4280,23 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a
       dma4((const bf16*)a.dout + ub, off, S + RDO + 256 * j);
     }
   };
-  auto issue_qa = [&](char* S, const Unit& x) {  // q_clean (+ g on wave 0): 4 per wave, 5 on wave 0
+  auto issue_qa = [&](char* S, const Unit& x) {  // q_clean (+ g on wave 0)
     const int l = fresh_lane();
     const long ub = x.tok0 * rsk + (long)x.h * K;
+    if constexpr (Q32) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int j = 4 * w + jj, r = 2 * j + (l >> 5);
-      const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsk + 4 * (l & 31)) * 4);
-      dma16(a.qc32 + ub, off, S + RQ + 1024 * j);
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = 4 * w + jj, r = 2 * j + (l >> 5);
+        const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsk + 4 * (l & 31)) * 4);
+        dma16(a.qc32 + ub, off, S + RQ + 1024 * j);
+      }
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * w + jj, r = 4 * j + (l >> 4), p = l & 15;
+        const unsigned off = (unsigned)((min(r, x.L - 1) * (int)rsk + 8 * (p ^ (2 * (r & 3)))) * 2);
+        dma16((const bf16*)a.qc16 + ub, off, S + 1024 * j);
+      }
     }
     // g of the unit's tokens (the last token's past the chunk)
     if (w == 0) dma4(a.gcum + x.tok0 * a.H + x.h, (unsigned)(min(l, x.L - 1) * a.H * 4), (char*)sG);
@@ -4402,7 +4413,8 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a
         const int r = tr + arow(i, l);
         const float g = gv[i];
         dQi[i] *= a.scale * __expf(g);
-        e[i] = dQi[i] * *(const float*)(Q + RQ + r * 512 + 4 * c);
+        const float qv = Q32 ? *(const float*)(Q + RQ + r * 512 + 4 * c) : (float)*(const bf16*)(Q + off_h(r, c));
+        e[i] = dQi[i] * qv;
         dKs[i] *= __expf(gl - g);
         f[i] = dKs[i] * (float)*(const bf16*)(KP + dq5::RK + off_h(r, c));
       }
@@ -4443,18 +4455,24 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a
       for (int i0 = 0; i0 < BT; i0 += 16) {
         if (tr == 32 && i0 < 32) continue;
         const bf16x8 ah = frag32_tr_l(sPh + i0 * LDP + tr, LDP, l), al = frag32_tr_l(sPl + i0 * LDP + tr, LDP, l);
-        bf16x8 bh, bl;
-        const int ib = i0 + 8 * (l >> 5);
+        if constexpr (Q32) {
+          bf16x8 bh, bl;
+          const int ib = i0 + 8 * (l >> 5);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          bf16 hh, oo;
-          split2(*(const float*)(Q + RQ + (ib + e) * 512 + 4 * c), hh, oo);
-          bh[e] = hh;
-          bl[e] = oo;
+          for (int e = 0; e < 8; ++e) {
+            bf16 hh, oo;
+            split2(*(const float*)(Q + RQ + (ib + e) * 512 + 4 * c), hh, oo);
+            bh[e] = hh;
+            bl[e] = oo;
+          }
+          dKs = mfma(ah, bh, dKs);
+          dKs = mfma(ah, bl, dKs);
+          dKs = mfma(al, bh, dKs);
+        } else {
+          const bf16x8 bh = frag_tr_h(Q, i0, kc, l);
+          dKs = mfma(ah, bh, dKs);
+          dKs = mfma(al, bh, dKs);
         }
-        dKs = mfma(ah, bh, dKs);
-        dKs = mfma(ah, bl, dKs);
-        dKs = mfma(al, bh, dKs);
       }
       const int bytes = (int)(((L - 1) * rsk + K) * 4);
       const auto rk = buf_rsrc(a.dkp32 + x.tok0 * rsk + (long)x.h * K, bytes);
@@ -4516,8 +4534,9 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a
     wait_vm<8>();  // V2 (V3 newer)
     bar();
     compute_v(s2, [&] { issue_qa(s1, cur); });
-    if (w == 0) wait_vm<5>();  // V3 (the q_clean piece newer)
-    else wait_vm<4>();
+    // V3 (the q_clean piece newer)
+    if (w == 0) wait_vm<Q32 ? 5 : 3>();
+    else wait_vm<Q32 ? 4 : 2>();
     bar();
     compute_v(s0, [&] { issue_kp(s2, cur); });
     wait_vm<0>();  // q_clean and k/P^T pieces
@@ -4589,12 +4608,14 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
         hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdDqkw:
-      if (K == 128 && a.qc32 && (V == 64 || V == 128)) {
+      if (K == 128 && V == 128) {
         const int grid = min(a.NTG * a.H, cu_count());
-        if (V == 128)
-          hipLaunchKernelGGL(gdn_bwd_dqkw_v5_kernel, dim3(grid), dim3(kWalk8), 0, st, a);
+        if (a.qc32)
+          hipLaunchKernelGGL(gdn_bwd_dqkw_v5_kernel<true>, dim3(grid), dim3(kWalk8), 0, st, a);
         else
-          hipLaunchKernelGGL(gdn_bwd_dqkw_v4_kernel<64>, dim3(grid), dim3(kWalk8), 0, st, a);
+          hipLaunchKernelGGL(gdn_bwd_dqkw_v5_kernel<false>, dim3(grid), dim3(kWalk8), 0, st, a);
+      } else if (K == 128 && V == 64 && a.qc32) {
+        hipLaunchKernelGGL(gdn_bwd_dqkw_v4_kernel<64>, dim3(min(a.NTG * a.H, cu_count())), dim3(kWalk8), 0, st, a);
       } else if (K == 128)
         hipLaunchKernelGGL(gdn_bwd_dqkw_v3_kernel<128>, dim3(1, a.NTG, a.H), dim3(kWalk8), 0, st, a, V);
       else
