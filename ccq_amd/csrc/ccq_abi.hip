@@ -18,7 +18,8 @@
 
 namespace ccq {
 hipError_t launch_cwalk(int stage, const WalkArgs& a, hipStream_t st);
-hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, float* red, hipStream_t st);
+hipError_t launch_sum_rows2(const float* partA, float* outA, int colsA, const float* partB, float* outB, int colsB,
+                            int nblk, float* red, hipStream_t st);
 hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st);
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
@@ -308,10 +309,9 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
       return s;
   }
   if (gate) {
-    float* red_b = wk.red + (size_t)kSumSlices * H * K;
     if (int s = hip_status(timed("clean_bwd_gate", st, [&] {
-                             const hipError_t e = launch_sum_rows(wk.dw_part, dgate_w, g.ntg, H * K, wk.red, st);
-                             return e != hipSuccess ? e : launch_sum_rows(wk.db_part, dgate_b, g.ntg, H, red_b, st);
+                             return launch_sum_rows2(wk.dw_part, dgate_w, H * K, wk.db_part, dgate_b, H, g.ntg,
+                                                     wk.red, st);
                            }),
                            "ccq_clean_bwd(dW, db)"))
       return s;

@@ -108,13 +108,24 @@ hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off
   return hipGetLastError();
 }
 
-// Sum of partial rows over a slice: out[y * cols + j] = sum_{b in slice y} part[b * cols + j],
-// slice y = rows [y * rps, min(nblk, (y + 1) * rps)).  grid (ceil(cols / 64), slices); 4 groups of 64 threads.
-__global__ __launch_bounds__(kThreads) void ccq_sum_rows_kernel(const float* part, float* out, int nblk, int cols,
-                                                                int rps) {
+// Two row-sum reductions over the same number of partial rows in one launch per pass (the gate's
+// dW [nblk][colsA] and db [nblk][colsB] partials): blocks [0, nbx0) reduce A, the rest B.  Block
+// (x, y): 64 columns, rows [y * rps, min(nblk, (y + 1) * rps)); 4 groups of 64 threads.
+struct SumRowsPair {
+  const float* part[2];
+  float* out[2];
+  int cols[2];
+  int nbx0;
+};
+__global__ __launch_bounds__(kThreads) void ccq_sum_rows2_kernel(const SumRowsPair p, int nblk, int rps) {
   __shared__ float sP[4][64];
+  const int which = blockIdx.x >= (unsigned)p.nbx0 ? 1 : 0;
+  const int bx = which ? blockIdx.x - p.nbx0 : blockIdx.x;
+  const float* part = which ? p.part[1] : p.part[0];
+  float* out = which ? p.out[1] : p.out[0];
+  const int cols = which ? p.cols[1] : p.cols[0];
   const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
-  const int j = blockIdx.x * 64 + cl;
+  const int j = bx * 64 + cl;
   const int b0 = blockIdx.y * rps, b1 = min(nblk, b0 + rps);
   float s = 0.f;
   if (j < cols)
@@ -124,18 +135,23 @@ __global__ __launch_bounds__(kThreads) void ccq_sum_rows_kernel(const float* par
   if (grp == 0 && j < cols) out[(long)blockIdx.y * cols + j] = sP[0][cl] + sP[1][cl] + sP[2][cl] + sP[3][cl];
 }
 
-// out[j] = sum_b part[b * cols + j]: kSumSlices partial sums into red[kSumSlices * cols], then one pass.
-hipError_t launch_sum_rows(const float* part, float* out, int nblk, int cols, float* red, hipStream_t st) {
-  if (cols == 0) return hipSuccess;
-  const dim3 gx((cols + 63) / 64);
+// outA[j] = sum_b partA[b * colsA + j] and outB likewise: kSumSlices partial sums over row slices
+// [y * rps, (y + 1) * rps) into red[kSumSlices * (colsA + colsB)], then one pass over the slices.
+hipError_t launch_sum_rows2(const float* partA, float* outA, int colsA, const float* partB, float* outB, int colsB,
+                            int nblk, float* red, hipStream_t st) {
+  if (colsA == 0 && colsB == 0) return hipSuccess;
+  const int nbA = (colsA + 63) / 64, nbB = (colsB + 63) / 64;
+  SumRowsPair p{{partA, partB}, {outA, outB}, {colsA, colsB}, nbA};
   if (nblk <= 4 * kSumSlices || !red) {
-    hipLaunchKernelGGL(ccq_sum_rows_kernel, gx, dim3(kThreads), 0, st, part, out, nblk, cols, nblk);
+    hipLaunchKernelGGL(ccq_sum_rows2_kernel, dim3(nbA + nbB), dim3(kThreads), 0, st, p, nblk, nblk);
     return hipGetLastError();
   }
   const int rps = (nblk + kSumSlices - 1) / kSumSlices;
   const int slices = (nblk + rps - 1) / rps;
-  hipLaunchKernelGGL(ccq_sum_rows_kernel, dim3(gx.x, slices), dim3(kThreads), 0, st, part, red, nblk, cols, rps);
-  hipLaunchKernelGGL(ccq_sum_rows_kernel, gx, dim3(kThreads), 0, st, (const float*)red, out, slices, cols, slices);
+  SumRowsPair p1{{partA, partB}, {red, red + (size_t)kSumSlices * colsA}, {colsA, colsB}, nbA};
+  hipLaunchKernelGGL(ccq_sum_rows2_kernel, dim3(nbA + nbB, slices), dim3(kThreads), 0, st, p1, nblk, rps);
+  SumRowsPair p2{{red, red + (size_t)kSumSlices * colsA}, {outA, outB}, {colsA, colsB}, nbA};
+  hipLaunchKernelGGL(ccq_sum_rows2_kernel, dim3(nbA + nbB), dim3(kThreads), 0, st, p2, slices, slices);
   return hipGetLastError();
 }
 
