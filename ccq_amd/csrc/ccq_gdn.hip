@@ -3641,8 +3641,9 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
 }
 
 // ===========================================================================
-// gdn_bwd_dqkw for K = 128, V in {64, 128} and fp32 q_clean: a persistent kernel, one 8-wave
-// workgroup per CU over the (chunk, head) units, same results as gdn_bwd_dqkw_v3_kernel.  The
+// gdn_bwd_dqkw for K = 128, V in {64, 128} and fp32 q_clean (launched for V = 64; V = 128 takes
+// the three-slot form below): a persistent kernel, one 8-wave workgroup per CU over the (chunk,
+// head) units, same results as gdn_bwd_dqkw_v3_kernel.  The
 // operands stream through two 64 KiB LDS slots by direct-to-LDS loads (global_load_lds_dwordx4:
 // no registers held, no staging pass): a unit is V/32 value pieces (h and dS' rows [32 v][128 k]
 // as hi/lo pairs, U, dU and dO columns [64 t][32 v]) and one post piece (q_clean, k, P^T).  While
