@@ -235,3 +235,47 @@ def test_fused_ccq_gdn(case):
         assert e <= TOL_BF16, n
     for n, e in kerrs.items():
         assert e <= TOL_KERNEL, n
+
+
+GATE_CASES = [
+    # B, T, H, K, V: the fused per-head gate lambda = sigmoid(W[h] . q + b[h]) of the benchmark
+    # workload, with its dW / db row reductions in one pass (few chunk groups) and in two passes
+    # (more than 128 chunk groups)
+    (1, 320, 2, 128, 128),
+    (2, 4160, 2, 128, 128),
+]
+
+
+@pytest.mark.parametrize("case", GATE_CASES, ids=[str(i) for i in range(len(GATE_CASES))])
+def test_fused_ccq_gdn_gate(case):
+    dev = _cuda()
+    from ccq_amd import fused_chunk_ccq_gdn
+    B, T, H, K, V = case
+    x, gen = gdn_inputs(B, T, H, K, V, seed=5, with_state=False, device="cpu")
+    w = torch.randn(H, K, generator=gen) * 0.5
+    b = torch.randn(H, generator=gen) * 0.5
+    do = bf(torch.randn(B, T, H, V, generator=gen))
+    d = torch.float64
+    ref = {n: (t.to(d).requires_grad_() if t is not None else None) for n, t in x.items()}
+    wr, br = w.to(d).requires_grad_(), b.to(d).requires_grad_()
+    lam = O.lambda_gate(ref["q"], wr, br).unsqueeze(-1)
+    o_r, _, _, _ = O.ccq_gdn_forward(ref["q"], ref["k"], ref["v"], lam, ref["g"], ref["beta"])
+    (o_r * do.to(d)).sum().backward()
+
+    g = {n: (t.to(dev).requires_grad_() if t is not None else None) for n, t in x.items()}
+    wg, bg = w.to(dev).requires_grad_(), b.to(dev).requires_grad_()
+    o, _, _, _ = fused_chunk_ccq_gdn(g["q"], g["k"], g["v"], None, g["g"], g["beta"], gate_w=wg, gate_b=bg)
+    (o.float() * do.to(dev).float()).sum().backward()
+    torch.cuda.synchronize()
+    errs = {"o": rel(o, o_r), "dW": rel(wg.grad, wr.grad), "db": rel(bg.grad, br.grad)}
+    kerrs = {"o": kern(o, o_r)}
+    for n in ("q", "k", "v", "g", "beta"):
+        errs["d" + n] = rel(g[n].grad, ref[n].grad)
+        if g[n].grad.dtype == torch.bfloat16:
+            kerrs["d" + n] = kern(g[n].grad, ref[n].grad)
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
+    for n, e in errs.items():
+        assert e <= TOL_BF16, n
+    for n, e in kerrs.items():
+        assert e <= TOL_KERNEL, n
