@@ -243,6 +243,8 @@ GATE_CASES = [
     # (more than 128 chunk groups)
     (1, 320, 2, 128, 128),
     (2, 4160, 2, 128, 128),
+    # varlen: padding chunk entries contribute zero partials; V = 64
+    (1, 1500, 2, 128, 64, [0, 100, 901, 1500]),
 ]
 
 
@@ -250,7 +252,9 @@ GATE_CASES = [
 def test_fused_ccq_gdn_gate(case):
     dev = _cuda()
     from ccq_amd import fused_chunk_ccq_gdn
-    B, T, H, K, V = case
+    B, T, H, K, V = case[:5]
+    cu = case[5] if len(case) > 5 else None
+    cu_t = torch.tensor(cu, dtype=torch.int64) if cu is not None else None
     x, gen = gdn_inputs(B, T, H, K, V, seed=5, with_state=False, device="cpu")
     w = torch.randn(H, K, generator=gen) * 0.5
     b = torch.randn(H, generator=gen) * 0.5
@@ -259,12 +263,13 @@ def test_fused_ccq_gdn_gate(case):
     ref = {n: (t.to(d).requires_grad_() if t is not None else None) for n, t in x.items()}
     wr, br = w.to(d).requires_grad_(), b.to(d).requires_grad_()
     lam = O.lambda_gate(ref["q"], wr, br).unsqueeze(-1)
-    o_r, _, _, _ = O.ccq_gdn_forward(ref["q"], ref["k"], ref["v"], lam, ref["g"], ref["beta"])
+    o_r, _, _, _ = O.ccq_gdn_forward(ref["q"], ref["k"], ref["v"], lam, ref["g"], ref["beta"], cu_seqlens=cu_t)
     (o_r * do.to(d)).sum().backward()
 
     g = {n: (t.to(dev).requires_grad_() if t is not None else None) for n, t in x.items()}
     wg, bg = w.to(dev).requires_grad_(), b.to(dev).requires_grad_()
-    o, _, _, _ = fused_chunk_ccq_gdn(g["q"], g["k"], g["v"], None, g["g"], g["beta"], gate_w=wg, gate_b=bg)
+    o, _, _, _ = fused_chunk_ccq_gdn(g["q"], g["k"], g["v"], None, g["g"], g["beta"], gate_w=wg, gate_b=bg,
+                                     cu_seqlens=cu_t.to(dev) if cu_t is not None else None)
     (o.float() * do.to(dev).float()).sum().backward()
     torch.cuda.synchronize()
     errs = {"o": rel(o, o_r), "dW": rel(wg.grad, wr.grad), "db": rel(bg.grad, br.grad)}
