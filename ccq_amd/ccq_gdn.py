@@ -19,8 +19,8 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, stream_of
-from .clean import (_check_qk, _f32, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd, reduce_dlambda,
-                    reshape_lambda_3d, seq_count)
+from .clean import (_check_qk, _f32, check_device, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd,
+                    norm_cu_seqlens, reduce_dlambda, reshape_lambda_3d, seq_count)
 
 __all__ = ["chunk_ccq_gdn", "fused_chunk_ccq_gdn", "fused_recurrent_ccq_gdn", "fused_ccq_clean",
            "chunk_gated_delta_rule", "ChunkCCQGDNFunction"]
@@ -74,6 +74,8 @@ def _gdn_backward(q16, q32, k, v, g32, beta32, ch: _Chunks, saved, do, dsfin, sc
     dg = torch.empty(B, T, H, device=dev, dtype=torch.float32)
     ds0 = torch.empty(ch.N, H, K, V, device=dev, dtype=torch.float32) if want_ds0 else None
     do = do.contiguous().to(torch.bfloat16)
+    if do.data_ptr() % 16:  # read with 16-byte loads: a view at an odd offset gets its own buffer
+        do = do.clone()
     dsfin = _f32(dsfin)  # bound to a name: the buffer must outlive the launch
     call("ccq_gdn_bwd", ptr(q16), ptr(q32), ptr(k), ptr(v), ptr(g32), ptr(beta32), ptr(ch.cu), ptr(ch.index),
          ptr(ch.offsets), ch.count, ptr(saved), ptr(do), ptr(dsfin), ptr(ws), ptr(dq32), ptr(dk32), ptr(dv),
@@ -91,6 +93,10 @@ class ChunkCCQGDNFunction(torch.autograd.Function):
         _check_qk(q, k)
         if v.dtype != torch.bfloat16 or v.ndim != 4 or v.shape[:3] != q.shape[:3]:
             raise ValueError("v must be bf16 [B, T, H, V] matching q")
+        check_device(q.device, v=v, lambda_h=lambda_h, g=g, beta=beta, initial_state=initial_state,
+                     initial_cov_state=initial_cov_state, initial_mean_state=initial_mean_state, gate_w=gate_w,
+                     gate_b=gate_b)
+        cu_seqlens = norm_cu_seqlens(cu_seqlens, q)
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         B, T, H, K = q.shape
         ch = _Chunks(B, T, cu_seqlens, q.device)

@@ -19,8 +19,8 @@ import torch
 from . import _lib
 from ._lib import call, ptr, stream_of
 from .ccq_gdn import _Chunks, _default_scale
-from .clean import _check_qk, _f32, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd, reduce_dlambda, \
-    reshape_lambda_3d
+from .clean import _check_qk, _f32, check_device, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd, \
+    norm_cu_seqlens, reduce_dlambda, reshape_lambda_3d
 
 __all__ = ["chunk_ccq_gla", "fused_chunk_ccq_gla", "fused_recurrent_ccq_gla", "chunk_gla", "ChunkCCQGLAFunction"]
 
@@ -50,6 +50,8 @@ def _gla_backward(q16, q32, k, v, gk32, ch: _Chunks, saved, do, dsfin, sfin, sca
     dgk = torch.empty(B, T, H, K, device=dev, dtype=torch.float32) if want_dgk else None
     ds0 = torch.empty(ch.N, H, K, V, device=dev, dtype=torch.float32) if want_ds0 else None
     do = do.contiguous().to(torch.bfloat16)
+    if do.data_ptr() % 16:  # read with 16-byte loads: a view at an odd offset gets its own buffer
+        do = do.clone()
     dsfin = _f32(dsfin)  # bound to a name: the buffer must outlive the launch
     call("ccq_gla_bwd", ptr(q16), ptr(q32), ptr(k), ptr(v), ptr(gk32), ptr(ch.cu), ptr(ch.index), ptr(ch.offsets),
          ch.count, ptr(saved), ptr(do), ptr(dsfin), ptr(sfin), ptr(ws), ptr(dq32), ptr(dk32), None if dv_f32 else ptr(dv),
@@ -71,6 +73,10 @@ class ChunkCCQGLAFunction(torch.autograd.Function):
             raise ValueError("v must be bf16 [B, T, H, V] matching q")
         if gk is not None and gk.shape != q.shape:
             raise ValueError(f"gk must have q's shape {tuple(q.shape)} (got {tuple(gk.shape)})")
+        check_device(q.device, v=v, lambda_h=lambda_h, gk=gk, initial_state=initial_state,
+                     initial_cov_state=initial_cov_state, initial_mean_state=initial_mean_state, gate_w=gate_w,
+                     gate_b=gate_b)
+        cu_seqlens = norm_cu_seqlens(cu_seqlens, q)
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         B, T, H, K = q.shape
         ch = _Chunks(B, T, cu_seqlens, q.device)

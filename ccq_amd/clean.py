@@ -17,6 +17,7 @@ from . import _lib
 from ._lib import call, ptr, stream_of
 
 __all__ = ["fused_ccq_clean_read", "FusedCCQCleanRead", "reshape_lambda_3d", "reduce_dlambda", "seq_count",
+           "norm_cu_seqlens", "check_device",
            "l2norm_fwd", "l2norm_bwd", "_CCQCleanQ", "_ccq_compute_z_and_sum_kk"]
 
 
@@ -57,9 +58,33 @@ def reduce_dlambda(dlam3: torch.Tensor, lam) -> Optional[torch.Tensor]:
     return dl.to(lam.dtype)
 
 
+def norm_cu_seqlens(cu_seqlens: Optional[torch.Tensor], q: torch.Tensor) -> Optional[torch.Tensor]:
+    """``cu_seqlens`` as the kernels read it: int64, contiguous, on q's device.  The reference takes
+    int32 as well (fla's ``get_unpad_data`` and HF packing produce it; ``fused_read.py:115-116, 468``
+    widen it to int64), and varlen inputs are a single packed row (B == 1)."""
+    if cu_seqlens is None:
+        return None
+    if not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D tensor [N + 1] of sequence boundaries")
+    if cu_seqlens.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"cu_seqlens must be int32 or int64 (got {cu_seqlens.dtype})")
+    if q.shape[0] != 1:
+        raise ValueError(f"varlen inputs (cu_seqlens) are one packed row: batch size 1, not {q.shape[0]}")
+    return cu_seqlens.to(device=q.device, dtype=torch.int64).contiguous()
+
+
+def check_device(device: torch.device, **tensors) -> None:
+    """Every tensor argument must live on the inputs' GPU: the kernels dereference raw pointers."""
+    for name, t in tensors.items():
+        if isinstance(t, torch.Tensor) and t.device != device:
+            raise ValueError(f"{name} must be on {device} like q (got {t.device})")
+
+
 def _check_qk(q: torch.Tensor, k: torch.Tensor):
     if not (q.is_cuda and k.is_cuda):
         raise RuntimeError("ccq_amd ops run on the GPU only (inputs are on the CPU)")
+    if q.device != k.device:
+        raise ValueError(f"q and k must be on one device (got {q.device}, {k.device})")
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
         raise TypeError(f"ccq_amd kernels take bf16 q/k (got {q.dtype}, {k.dtype})")
     if q.shape != k.shape or q.ndim != 4:
@@ -162,6 +187,9 @@ class FusedCCQCleanRead(torch.autograd.Function):
     def forward(ctx, q, k, lambda_h, position_offset, initial_cov_state, initial_mean_state, output_final_state,
                 subtract_mean, cu_seqlens, gate_w=None, gate_b=None):
         _check_qk(q, k)
+        check_device(q.device, lambda_h=lambda_h, initial_cov_state=initial_cov_state,
+                     initial_mean_state=initial_mean_state, gate_w=gate_w, gate_b=gate_b)
+        cu_seqlens = norm_cu_seqlens(cu_seqlens, q)
         q, k = q.contiguous(), k.contiguous()
         gw, gb = _f32(gate_w), _f32(gate_b)
         lam3 = None if gw is not None else reshape_lambda_3d(lambda_h, q)
@@ -213,8 +241,8 @@ class _CCQCleanQ(torch.autograd.Function):
     ``ccq/ops/common/clean.py:691-748``): ``q_clean = q - λ (z/pos - (m·q) m/pos²)`` with the running
     key sum ``m`` (initial ``initial_state_K``).  Returns ``(q_clean, final_state_K | None)``.
 
-    The backward also returns the gradient of ``initial_state_K`` and folds the gradient of the
-    final key sum into ``dk`` (the reference drops both)."""
+    Gradients are the reference's (``clean.py:720-748``): dq, dk, dz and dλ; the gradient arriving
+    at ``final_state_K`` is not propagated and ``initial_state_K`` gets none."""
 
     @staticmethod
     def forward(ctx, q, k, z, lambda_h, position_offset, initial_state_K, output_final_state, subtract_mean,
@@ -223,6 +251,8 @@ class _CCQCleanQ(torch.autograd.Function):
         _check_qk(q, k)
         if z.shape != q.shape:
             raise ValueError(f"z must have q's shape {tuple(q.shape)} (got {tuple(z.shape)})")
+        check_device(q.device, z=z, lambda_h=lambda_h, initial_state_K=initial_state_K)
+        cu_seqlens = norm_cu_seqlens(cu_seqlens, q)
         q, k = q.contiguous(), k.contiguous()
         z16 = z.contiguous().to(torch.bfloat16)
         B, T, H, K = q.shape
@@ -239,7 +269,6 @@ class _CCQCleanQ(torch.autograd.Function):
         ctx.ch = ch
         ctx.lambda_h = lambda_h if isinstance(lambda_h, torch.Tensor) else None
         ctx.z_dtype = z.dtype
-        ctx.has_m0 = initial_state_K is not None
         ctx.position_offset = int(position_offset)
         ctx.subtract_mean = bool(subtract_mean)
         return qc, mfin
@@ -254,18 +283,15 @@ class _CCQCleanQ(torch.autograd.Function):
         dqc = dqc.contiguous()
         d32 = dqc if dqc.dtype == torch.float32 else None
         d16 = None if d32 is not None else dqc.to(torch.bfloat16)
-        dmfin = _f32(dmfin)
         dq, dk, dz = torch.empty_like(q), torch.empty_like(k), torch.empty_like(q)
         want_dlam = ctx.lambda_h is not None and ctx.lambda_h.requires_grad
         dlam = torch.empty(B, T, H, device=q.device, dtype=torch.float32) if want_dlam else None
-        dm0 = torch.empty(ch.N, H, K, device=q.device, dtype=torch.float32) if ctx.has_m0 else None
+        # dm_final / dm0 (the ABI's extension) stay off: the reference drops both
         call("ccq_clean_z_bwd", ptr(q), ptr(k), ptr(z16), ptr(lam3), ptr(cu_seqlens), ptr(ch.index), ptr(ch.offsets),
-             ch.count, ptr(saved), ptr(d16), ptr(d32), ptr(dmfin), ptr(dq), ptr(dk), ptr(dz), ptr(dlam), ptr(dm0),
+             ch.count, ptr(saved), ptr(d16), ptr(d32), None, ptr(dq), ptr(dk), ptr(dz), ptr(dlam), None,
              ptr(ws), B, T, H, K, ch.N, ctx.position_offset, int(ctx.subtract_mean), stream_of(q))
         dl = reduce_dlambda(dlam, ctx.lambda_h) if dlam is not None else None
-        if dm0 is not None and not ctx.subtract_mean:
-            dm0.zero_()
-        return dq, dk, dz.to(ctx.z_dtype), dl, None, dm0, None, None, None
+        return dq, dk, dz.to(ctx.z_dtype), dl, None, None, None, None, None
 
 
 class _CovarianceRead(torch.autograd.Function):
@@ -277,6 +303,8 @@ class _CovarianceRead(torch.autograd.Function):
         from .ccq_gdn import _Chunks
         from .ccq_gla import _gla_forward
         _check_qk(q, k)
+        check_device(q.device, initial_state=initial_state)
+        cu_seqlens = norm_cu_seqlens(cu_seqlens, q)
         q, k = q.contiguous(), k.contiguous()
         B, T, H, K = q.shape
         ch = _Chunks(B, T, cu_seqlens, q.device)

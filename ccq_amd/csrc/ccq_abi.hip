@@ -443,6 +443,10 @@ int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v,
   if ((!q && !q_f32) || !k || !v || !beta || !saved || !d_o || !workspace || !dq_f32 || !dk_f32 || !dv || !dbeta ||
       !dg)
     return fail(CCQ_ERR_NULL, "ccq_gdn_bwd: null input/output");
+  // the dq/dk/dw kernels read dO with 16-byte direct-to-LDS loads; dv leaves as 16-byte pieces
+  if (!aligned16(q) || !aligned16(q_f32) || !aligned16(k) || !aligned16(v) || !aligned16(d_o) || !aligned16(dv) ||
+      !aligned16(saved) || !aligned16(workspace) || !aligned16(dq_f32) || !aligned16(dk_f32))
+    return fail(CCQ_ERR_ALIGN, "ccq_gdn_bwd: tensors must be 16-byte aligned");
   const int64_t tokens = (int64_t)B * T;
   GdnSaved sv;
   carve_saved((char*)saved, tokens, num_chunks, H, K, V, &sv);

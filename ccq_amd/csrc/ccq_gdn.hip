@@ -1735,248 +1735,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
 //   dQi = dO h^T, dKs = U dS'^T, dw = -dU h^T, dP = dO U^T   (contractions over V)
 //   dq = scale gamma dQi + dPs K,  dk = fac dKs + dPs^T Qc,  dPs = dP o scale Gamma (causal)
 //   dG partials: decay terms of O, P and the state update
-// ===========================================================================
-template <int K>
-__global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_kernel(const GdnArgs a, const int V) {
-  constexpr int LDB = 64 + 8, LDF = 64 + 4, LDP = 64 + 1;
-  constexpr long kLoop = 5L * 64 * LDB * 2 + 2L * BT * LDF * 4;
-  constexpr long kPost = 4L * BT * LDP * 4 + 2L * 64 * LDB * 2;
-  constexpr long kBytes = (kLoop > kPost ? kLoop : kPost) + 6 * BT * 4 + 4 * 4 + 64;
-  __shared__ __attribute__((aligned(16))) char smem[kBytes];
-  Carver cv{smem};
-  char* region = cv.p;
-  // loop-phase views
-  bf16* sHt = (bf16*)region;        // [64 v][LDB]  h[k][v] stored [v][k] for k in the tile
-  bf16* sDSt = sHt + 64 * LDB;      // [64 v][LDB]
-  bf16* sHtl = sDSt + 64 * LDB;     // low parts
-  bf16* sDStl = sHtl + 64 * LDB;
-  bf16* sdO = sDStl + 64 * LDB;     // [64 t][LDB]
-  float* sU = (float*)(sdO + 64 * LDB);  // [64 t][LDF]
-  float* sdU = sU + BT * LDF;            // [64 t][LDF]
-  // post-phase views (same region)
-  float* sdP = (float*)region;     // [64][LDP]  dP, then dPs
-  float* sQcT = sdP + BT * LDP;    // [64 k][LDP]
-  float* sRed = sQcT + 64 * LDP;   // [64][LDP]
-  float* sPt = sRed + BT * LDP;    // [64][LDP]  P^T rows (kt == 0)
-  bf16* sKt = (bf16*)(sPt + BT * LDP);  // [64 k][LDB]  K transposed
-  bf16* sKr = sKt + 64 * LDB;           // [64 t][LDB]
-  cv.p = region + (kLoop > kPost ? kLoop : kPost);
-  float* sG = cv.take<float>(BT);
-  float* sGam = cv.take<float>(BT);
-  float* sFac = cv.take<float>(BT);
-  float* sDG = cv.take<float>(BT);
-  float* sTerm = cv.take<float>(BT);
-  float* sMisc = cv.take<float>(8);
-
-  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
-  const int kt = blockIdx.x, gc = blockIdx.y, h = blockIdx.z;
-  int n, c0, L;
-  long bos;
-  if (!chunk_info(a, gc, n, c0, bos, L)) return;
-  const long tok0 = bos + c0;
-  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
-  const int k0c = kt * 64;
-
-  const int tr = (w >> 1) * 32, tc = (w & 1) * 32;
-  const int pr = (w == 0) ? 0 : 32, pc = (w == 2) ? 32 : 0;
-  f32x16 dQi = zero16(), dKs = zero16(), dW = zero16(), dP = zero16();
-  float hds = 0.f;
-
-  // Tiles of the next value block (or, in the last iteration, of the post phase) are loaded into
-  // registers while the current block is in the MFMA pipe.
-  PrefetchBf16<64, 64> pH, pHl, pD, pDl, pO;
-  PrefetchF32<64, BT> pU, pdU;
-  PrefetchGrad<64, BT> pQ;
-  PrefetchBf16<64, BT> pK;
-  PrefetchF32<BT, BT> pP;
-  float pgl = 0.f, pgt = 0.f;
-  auto issue_loop = [&](int v0) {
-    const long so = (((long)gc * a.H + h) * V + v0) * K + k0c;
-    pH.load((const bf16*)a.hT + so, K, 64);
-    pD.load((const bf16*)a.dhT + so, K, 64);
-    pHl.load((const bf16*)a.hTl + so, K, 64);
-    pDl.load((const bf16*)a.dhTl + so, K, 64);
-    pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L);
-    pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, L);
-    pdU.load(a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, L);
-  };
-  auto issue_post = [&]() {
-    pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + k0c : nullptr,
-            a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + k0c : nullptr, rsk, L);
-    pK.load((const bf16*)a.k + (tok0 * a.H + h) * K + k0c, rsk, L);
-    if (kt == 0) pP.load(a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT);
-    if (tid < BT) {
-      pgl = a.gcum[(tok0 + L - 1) * a.H + h];
-      pgt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
-    }
-  };
-  issue_loop(0);
-
-  for (int v0 = 0; v0 < V; v0 += 64) {
-    pH.store(sHt, LDB, nullptr, 0);
-    pD.store(sDSt, LDB, nullptr, 0);
-    pHl.store(sHtl, LDB, nullptr, 0);
-    pDl.store(sDStl, LDB, nullptr, 0);
-    pO.store(sdO, LDB, nullptr, 0);
-    pU.store(sU, LDF, nullptr, 0);
-    pdU.store(sdU, LDF, nullptr, 0);
-    __syncthreads();
-    if (v0 + 64 < V) issue_loop(v0 + 64);
-    else issue_post();
-    for (int e = tid; e < 64 * 64; e += kThreads) {
-      const int vv = e >> 6, kk = e & 63;
-      hds += ((float)sHt[vv * LDB + kk] + (float)sHtl[vv * LDB + kk]) *
-             ((float)sDSt[vv * LDB + kk] + (float)sDStl[vv * LDB + kk]);
-    }
-    for (int k0 = 0; k0 < 64; k0 += 16) {
-      const bf16x8 hb = frag_cm(sHt + k0 * LDB + tc, LDB);
-      const bf16x8 hbl = frag_cm(sHtl + k0 * LDB + tc, LDB);
-      const bf16x8 db = frag_cm(sDSt + k0 * LDB + tc, LDB);
-      const bf16x8 dbl = frag_cm(sDStl + k0 * LDB + tc, LDB);
-      const bf16x8 oa = frag_rm(sdO + tr * LDB + k0, LDB);
-      dQi = mfma(oa, hb, dQi);
-      dQi = mfma(oa, hbl, dQi);
-      bf16x8 uhi, ulo, dhi, dlo;
-      frag_rm_f32(sU + tr * LDF + k0, LDF, uhi, ulo);
-      dKs = mfma(uhi, db, dKs);
-      dKs = mfma(ulo, db, dKs);
-      dKs = mfma(uhi, dbl, dKs);
-      frag_rm_f32(sdU + tr * LDF + k0, LDF, dhi, dlo);
-      dW = mfma(dhi, hb, dW);
-      dW = mfma(dlo, hb, dW);
-      dW = mfma(dhi, hbl, dW);
-      if (w < 3) {
-        bf16x8 phi, plo;
-        frag_rm_f32(sU + pc * LDF + k0, LDF, phi, plo);
-        const bf16x8 pa = frag_rm(sdO + pr * LDB + k0, LDB);
-        dP = mfma(pa, phi, dP);
-        dP = mfma(pa, plo, dP);
-      }
-    }
-    __syncthreads();
-  }
-  // <dS', h> over this column tile
-  hds = group_sum(hds, 64);
-  if (l == 0) sMisc[w] = hds;
-
-  // post phase (its tiles were loaded during the last value block)
-  pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
-  pK.store(sKr, LDB, sKt, LDB);
-  if (kt == 0) pP.store(sPt, LDP, nullptr, 0);
-  if (tid < BT) {
-    sG[tid] = pgt;
-    sGam[tid] = __expf(pgt);
-    sFac[tid] = __expf(pgl - pgt);
-    if (tid == 0) sMisc[4] = __expf(pgl);
-  }
-  // dP -> LDS (masked, zero upper tile)
-  if (w < 3) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = pr + acc_row(i), c = pc + acc_col();
-      sdP[r * LDP + c] = (r >= c && r < L) ? dP[i] : 0.f;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sdP[acc_row(i) * LDP + 32 + acc_col()] = 0.f;
-  }
-  __syncthreads();
-
-  // dG from P (once per chunk):  dG_i += sum_j dP_ij P_ij ;  dG_j -= sum_i dP_ij P_ij
-  if (tid < BT) {
-    float s = 0.f;
-    if (kt == 0) {
-      for (int j = 0; j < BT; ++j) s += sdP[tid * LDP + j] * sPt[j * LDP + tid];  // row tid
-      for (int i = 0; i < BT; ++i) s -= sdP[i * LDP + tid] * sPt[tid * LDP + i];  // column tid
-    }
-    sDG[tid] = s;
-  }
-  __syncthreads();
-  // dPs = dP o scale Gamma
-  for (int e = tid; e < BT * BT; e += kThreads) {
-    const int r = e >> 6, c = e & 63;
-    if (r >= c) sdP[r * LDP + c] *= a.scale * __expf(sG[r] - sG[c]);
-  }
-  __syncthreads();
-
-  // dq tile = scale gamma dQi + dPs K[:, tile]
-  {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) dQi[i] *= a.scale * sGam[tr + acc_row(i)];
-    // decay term of O: dG_i += sum_k dQi_ik qc_ik
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = tr + acc_row(i), c = tc + acc_col();
-      sRed[r * LDP + c] = dQi[i] * sQcT[c * LDP + r];
-    }
-    for (int k0 = 0; k0 < BT; k0 += 16) {
-      bf16x8 hi, lo;
-      frag_rm_f32(sdP + tr * LDP + k0, LDP, hi, lo);
-      const bf16x8 b = frag_rm(sKt + tc * LDB + k0, LDB);
-      dQi = mfma(hi, b, dQi);
-      dQi = mfma(lo, b, dQi);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = tr + acc_row(i);
-      if (r < L) a.dq32[(tok0 + r) * rsk + (long)h * K + k0c + tc + acc_col()] = dQi[i];
-    }
-  }
-  __syncthreads();
-  if (tid < BT) {
-    float s = 0.f;
-    for (int c = 0; c < 64; ++c) s += sRed[tid * LDP + c];
-    sDG[tid] += s;
-  }
-  __syncthreads();
-  // dk tile = fac dKs + dPs^T Qc[:, tile];  state-update decay term
-  {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = tr + acc_row(i), c = tc + acc_col();
-      dKs[i] *= sFac[r];
-      sRed[r * LDP + c] = dKs[i] * (float)sKr[r * LDB + c];
-    }
-    for (int k0 = 0; k0 < BT; k0 += 16) {
-      bf16x8 ahi, alo, bhi, blo;
-      frag_cm_f32(sdP + k0 * LDP + tr, LDP, ahi, alo);
-      frag_rm_f32(sQcT + tc * LDP + k0, LDP, bhi, blo);
-      dKs = mfma(ahi, bhi, dKs);
-      dKs = mfma(ahi, blo, dKs);
-      dKs = mfma(alo, bhi, dKs);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = tr + acc_row(i);
-      if (r < L) {
-        const long gi = (tok0 + r) * rsk + (long)h * K + k0c + tc + acc_col();
-        a.dkp32[gi] = dKs[i];
-        a.dw32[gi] = -dW[i];
-      }
-    }
-  }
-  __syncthreads();
-  if (tid < BT) {
-    float s = 0.f;
-    for (int c = 0; c < 64; ++c) s += sRed[tid * LDP + c];
-    sTerm[tid] = s;  // term_j
-  }
-  __syncthreads();
-  if (tid < BT && tid < L) {
-    float d = sDG[tid] - sTerm[tid];
-    if (tid == L - 1) {
-      float tot = 0.f;
-      for (int j = 0; j < L; ++j) tot += sTerm[j];
-      d += tot + sMisc[4] * (sMisc[0] + sMisc[1] + sMisc[2] + sMisc[3]);
-    }
-    const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
-    a.dgp[(long)kt * ntok * a.H + (tok0 + tid) * a.H + h] = d;
-  }
-}
-
-// ===========================================================================
-// gdn_bwd_dqkw (same grid and results as gdn_bwd_dqkw_kernel) with every operand staged once in
-// the form its MFMA reads: the state tiles h^T, dS'^T arrive as [v][k] rows and are stored [k][v]
+// Every operand is staged once in the form its MFMA reads: the state tiles h^T, dS'^T arrive as [v][k] rows and are stored [k][v]
 // from four-row patches; U, dU are stored as hi/lo rows; the post phase stores dPs^T, Qc^T, K^T
 // (hi/lo where fp32) and does its row / column reductions over LDS with all threads.
 // ===========================================================================
@@ -2563,291 +2322,8 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v3_kernel(const GdnArgs a
 
 // ===========================================================================
 // gdn_bwd_wy: grid (NTG, H)  -- backward through w = T diag(beta gamma) K, u = T diag(beta) V,
-// T = (I + A)^-1, A = strict_lower(diag(beta) (K K^T o Gamma)).
-// ===========================================================================
-template <int K>
-__global__ __launch_bounds__(kThreads) void gdn_bwd_wy_kernel(const GdnArgs a, const int V) {
-  constexpr int LDB = 64 + 8, LDF = 64 + 4, LDP = 64 + 1, NK = K / 64;
-  constexpr long kBytes = 6L * BT * LDP * 4 + 2L * 64 * LDB * 2 + 2L * BT * LDF * 4 + 8 * BT * 4 + 64;
-  __shared__ __attribute__((aligned(16))) char smem[kBytes];
-  Carver cv{smem};
-  float* sT = cv.take<float>(BT * LDP);
-  float* sdT = cv.take<float>(BT * LDP);   // dT, then dA, then dAs
-  float* sM1T = cv.take<float>(BT * LDP);  // (dT T^T)^T
-  float* sKK = cv.take<float>(BT * LDP);
-  float* sRed = cv.take<float>(BT * LDP);
-  float* sXT = cv.take<float>(BT * LDP);   // a transposed fp32 operand tile [64 cols][64 rows]
-  bf16* sR = cv.take<bf16>(64 * LDB);      // bf16 rows tile [t][c]
-  bf16* sCT = cv.take<bf16>(64 * LDB);     // bf16 transposed tile [c][t]
-  float* sX = cv.take<float>(BT * LDF);    // fp32 rows tile [t][c]
-  float* sY = cv.take<float>(BT * LDF);
-  float* sG = cv.take<float>(BT);
-  float* sBeta = cv.take<float>(BT);
-  float* sGam = cv.take<float>(BT);
-  float* sDB = cv.take<float>(BT);
-  float* sDG = cv.take<float>(BT);
-  float* sTmp = cv.take<float>(BT);
-
-  const int tid = threadIdx.x, w = wave_id();
-  const int gc = blockIdx.x, h = blockIdx.y;
-  int n, c0, L;
-  long bos;
-  if (!chunk_info(a, gc, n, c0, bos, L)) return;
-  const long tok0 = bos + c0;
-  const long rsk = (long)a.H * K, rsv = (long)a.H * V;
-  const long ntok = a.cu ? (long)a.cu[a.N] : (long)a.N * a.T;
-  const int nkt = K / 64;
-
-  // Global tiles come in "jobs" of one fp32 and one bf16 64 x 64 tile, loaded one job ahead into
-  // registers: kinds A (dw, k) per key tile and B (dU, v) per value tile feed dT; kinds C (dw, k,
-  // dk_part) and D (dU, v) feed the dk / dv epilogues.  The M1 / dA phase between B and C runs
-  // while the first C job is in flight.
-  const int nv = V / 64, nA = nkt, nB = nkt + nv, nC = 2 * nkt + nv, njobs = 2 * (nkt + nv);
-  PrefetchF32<64, BT> pX, pY;
-  PrefetchBf16<64, BT> pR;
-  auto issue = [&](int j) {
-    const bool kside = j < nA || (j >= nB && j < nC);
-    const int col = 64 * (j < nA ? j : j < nB ? j - nA : j < nC ? j - nB : j - nC);
-    if (kside) {
-      pX.load(a.dw32 + (tok0 * a.H + h) * K + col, rsk, L);
-      pR.load((const bf16*)a.k + (tok0 * a.H + h) * K + col, rsk, L);
-      if (j >= nB) pY.load(a.dkp32 + (tok0 * a.H + h) * K + col, rsk, L);
-    } else {
-      pX.load(a.dU + (tok0 * a.H + h) * (long)V + col, rsv, L);
-      pR.load((const bf16*)a.v + (tok0 * a.H + h) * (long)V + col, rsv, L);
-    }
-  };
-  issue(0);
-  {
-    PrefetchF32<64, BT> pT;
-    pT.load(a.tmat + ((long)gc * a.H + h) * (BT * BT), BT, BT);
-    if (tid < BT) {
-      const float gl = a.gcum[(tok0 + L - 1) * a.H + h];
-      const float gt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : gl;
-      sG[tid] = gt;
-      sGam[tid] = __expf(gt);
-      sBeta[tid] = (tid < L) ? a.beta[(tok0 + tid) * a.H + h] : 0.f;
-      float dg = 0.f;
-      if (tid < L)
-        for (int kt = 0; kt < nkt; ++kt) dg += a.dgp[(long)kt * ntok * a.H + (tok0 + tid) * a.H + h];
-      sDG[tid] = dg;
-      sDB[tid] = 0.f;
-    }
-    pT.store(sT, LDP, nullptr, 0);
-  }
-  int job = 0;
-
-  // --- dT (lower incl. diagonal tiles) and K K^T -------------------------------------
-  const int lr = (w == 0) ? 0 : 32, lc = (w == 2) ? 32 : 0;
-  f32x16 dTk = zero16(), dTv = zero16(), kk = zero16();
-  for (int kt = 0; kt < nkt; ++kt, ++job) {
-    pX.store(sX, LDF, nullptr, 0);
-    pR.store(sR, LDB, nullptr, 0);
-    __syncthreads();
-    if (job + 1 < njobs) issue(job + 1);
-    if (w < 3) {
-      for (int k0 = 0; k0 < 64; k0 += 16) {
-        bf16x8 hi, lo;
-        frag_rm_f32(sX + lr * LDF + k0, LDF, hi, lo);
-        const bf16x8 b = frag_rm(sR + lc * LDB + k0, LDB);
-        dTk = mfma(hi, b, dTk);
-        dTk = mfma(lo, b, dTk);
-        kk = mfma(frag_rm(sR + lr * LDB + k0, LDB), b, kk);
-      }
-    }
-    __syncthreads();
-  }
-  for (int v0 = 0; v0 < V; v0 += 64, ++job) {
-    pX.store(sX, LDF, nullptr, 0);
-    pR.store(sR, LDB, nullptr, 0);
-    __syncthreads();
-    if (job + 1 < njobs) issue(job + 1);
-    if (w < 3) {
-      for (int k0 = 0; k0 < 64; k0 += 16) {
-        bf16x8 hi, lo;
-        frag_rm_f32(sX + lr * LDF + k0, LDF, hi, lo);
-        const bf16x8 b = frag_rm(sR + lc * LDB + k0, LDB);
-        dTv = mfma(hi, b, dTv);
-        dTv = mfma(lo, b, dTv);
-      }
-    }
-    __syncthreads();
-  }
-  if (w < 3) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = lr + acc_row(i), c = lc + acc_col();
-      const float v = dTk[i] * sBeta[c] * sGam[c] + dTv[i] * sBeta[c];
-      sdT[r * LDP + c] = (r > c) ? v : 0.f;
-      sKK[r * LDP + c] = (r > c) ? kk[i] : 0.f;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      sdT[acc_row(i) * LDP + 32 + acc_col()] = 0.f;
-      sKK[acc_row(i) * LDP + 32 + acc_col()] = 0.f;
-    }
-  }
-  __syncthreads();
-
-  // --- M1 = dT T^T (strictly-lower part), stored transposed ---------------------------------
-  if (w < 3) {
-    f32x16 acc = zero16();
-    for (int k0 = 0; k0 < BT; k0 += 16) {
-      bf16x8 ahi, alo, bhi, blo;
-      frag_rm_f32(sdT + lr * LDP + k0, LDP, ahi, alo);
-      frag_rm_f32(sT + lc * LDP + k0, LDP, bhi, blo);
-      acc = mfma(ahi, bhi, acc);
-      acc = mfma(ahi, blo, acc);
-      acc = mfma(alo, bhi, acc);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = lr + acc_row(i), c = lc + acc_col();
-      sM1T[c * LDP + r] = (r > c) ? acc[i] : 0.f;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sM1T[(32 + acc_col()) * LDP + acc_row(i)] = 0.f;
-  }
-  __syncthreads();
-  // --- dA = -T^T M1 (strict lower) -----------------------------------------------------------
-  if (w < 3) {
-    f32x16 acc = zero16();
-    for (int k0 = 0; k0 < BT; k0 += 16) {
-      bf16x8 ahi, alo, bhi, blo;
-      frag_cm_f32(sT + k0 * LDP + lr, LDP, ahi, alo);
-      frag_rm_f32(sM1T + lc * LDP + k0, LDP, bhi, blo);
-      acc = mfma(ahi, bhi, acc);
-      acc = mfma(ahi, blo, acc);
-      acc = mfma(alo, bhi, acc);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = lr + acc_row(i), c = lc + acc_col();
-      sdT[r * LDP + c] = (r > c) ? -acc[i] : 0.f;  // dA
-    }
-  }
-  __syncthreads();
-  // dbeta_i += sum_j dA_ij Gamma_ij KK_ij ; dG_i += sum_j dA_ij A_ij ; dG_j -= sum_i dA_ij A_ij
-  // (four threads per row, each over a quarter of the columns)
-  {
-    const int r = tid >> 2, part = tid & 3;
-    float db = 0.f, dgc = 0.f;
-    for (int j = part; j < BT; j += 4) {
-      if (j < r) db += sdT[r * LDP + j] * __expf(sG[r] - sG[j]) * sKK[r * LDP + j];
-      if (j > r) dgc += sdT[j * LDP + r] * sBeta[j] * __expf(sG[j] - sG[r]) * sKK[j * LDP + r];
-    }
-    db = group_sum(db, 4);
-    dgc = group_sum(dgc, 4);
-    if (part == 0) {
-      sTmp[r] = sBeta[r] * db - dgc;
-      sDB[r] += db;
-    }
-  }
-  __syncthreads();
-  if (tid < BT) sDG[tid] += sTmp[tid];
-  // dAs = dA o beta_i Gamma_ij
-  for (int e = tid; e < BT * BT; e += kThreads) {
-    const int r = e >> 6, c = e & 63;
-    if (r > c) sdT[r * LDP + c] *= sBeta[r] * __expf(sG[r] - sG[c]);
-  }
-  __syncthreads();
-
-  // --- dk tiles: dk_part + dAs K + dAs^T K + diag(beta gamma) T^T dw -------------------------
-  const int tr = (w >> 1) * 32, tc = (w & 1) * 32;
-  for (int kt = 0; kt < nkt; ++kt, ++job) {
-    const int kc = kt * 64;
-    pR.store(sR, LDB, sCT, LDB);
-    pX.store(nullptr, 0, sXT, LDP);
-    pY.store(sY, LDF, nullptr, 0);
-    __syncthreads();
-    if (job + 1 < njobs) issue(job + 1);
-    f32x16 acc = zero16(), acc2 = zero16();
-    for (int k0 = 0; k0 < BT; k0 += 16) {
-      const bf16x8 kb = frag_rm(sCT + tc * LDB + k0, LDB);
-      bf16x8 hi, lo;
-      frag_rm_f32(sdT + tr * LDP + k0, LDP, hi, lo);
-      acc = mfma(hi, kb, acc);
-      acc = mfma(lo, kb, acc);
-      frag_cm_f32(sdT + k0 * LDP + tr, LDP, hi, lo);
-      acc = mfma(hi, kb, acc);
-      acc = mfma(lo, kb, acc);
-      bf16x8 thi, tlo, dhi, dlo;
-      frag_cm_f32(sT + k0 * LDP + tr, LDP, thi, tlo);
-      frag_rm_f32(sXT + tc * LDP + k0, LDP, dhi, dlo);
-      acc2 = mfma(thi, dhi, acc2);
-      acc2 = mfma(thi, dlo, acc2);
-      acc2 = mfma(tlo, dhi, acc2);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = tr + acc_row(i), c = tc + acc_col();
-      const float kv = (float)sR[r * LDB + c];
-      sRed[r * LDP + c] = acc2[i] * kv;
-      if (r < L) {
-        const long gi = (tok0 + r) * rsk + (long)h * K + kc + c;
-        a.dk32[gi] = sY[r * LDF + c] + acc[i] + sBeta[r] * sGam[r] * acc2[i];
-      }
-    }
-    __syncthreads();
-    if (tid < BT) {
-      float s = 0.f;
-      for (int c = 0; c < 64; ++c) s += sRed[tid * LDP + c];
-      sDB[tid] += sGam[tid] * s;
-      sDG[tid] += sBeta[tid] * sGam[tid] * s;
-    }
-    __syncthreads();
-  }
-  // --- dv tiles: beta_j (T^T dU)_j ; dbeta_j += (T^T dU)_j . v_j ------------------------------
-  for (int v0 = 0; v0 < V; v0 += 64, ++job) {
-    pR.store(sR, LDB, nullptr, 0);
-    pX.store(nullptr, 0, sXT, LDP);
-    __syncthreads();
-    if (job + 1 < njobs) issue(job + 1);
-    f32x16 acc = zero16();
-    for (int k0 = 0; k0 < BT; k0 += 16) {
-      bf16x8 thi, tlo, dhi, dlo;
-      frag_cm_f32(sT + k0 * LDP + tr, LDP, thi, tlo);
-      frag_rm_f32(sXT + tc * LDP + k0, LDP, dhi, dlo);
-      acc = mfma(thi, dhi, acc);
-      acc = mfma(thi, dlo, acc);
-      acc = mfma(tlo, dhi, acc);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = tr + acc_row(i), c = tc + acc_col();
-      sRed[r * LDP + c] = acc[i] * (float)sR[r * LDB + c];
-      if (r < L) ((bf16*)a.dv)[(tok0 + r) * rsv + (long)h * V + v0 + c] = (bf16)(sBeta[r] * acc[i]);
-    }
-    __syncthreads();
-    if (tid < BT) {
-      float s = 0.f;
-      for (int c = 0; c < 64; ++c) s += sRed[tid * LDP + c];
-      sDB[tid] += s;
-    }
-    __syncthreads();
-  }
-  // --- dg = reverse cumulative sum of dG within the chunk; dbeta ------------------------------
-  if (w == 0) {
-    const int ll = lane_id();
-    const int r = BT - 1 - ll;  // reverse order
-    float x = (r < L) ? sDG[r] : 0.f;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(x, off);
-      if (ll >= off) x += y;
-    }
-    if (r < L) {
-      a.dg[(tok0 + r) * a.H + h] = x;
-      a.dbeta[(tok0 + r) * a.H + h] = sDB[r];
-    }
-  }
-}
-
-// ===========================================================================
-// gdn_bwd_wy (same grid and results as gdn_bwd_wy_kernel) with every operand in the form its MFMA
-// reads.  Products whose transpose is needed later are computed in the transposed orientation and
+// T = (I + A)^-1, A = strict_lower(diag(beta) (K K^T o Gamma)), with every operand in the form its
+// MFMA reads.  Products whose transpose is needed later are computed in the transposed orientation and
 // written back transposed (acc_to_lds_t), so all fragments are 16-byte row reads:
 //   phase 1  (dT K-part)^T, (dT V-part)^T over key / value tiles; K K^T
 //   phase 2  M1 = dT T^T -> M1^T;  dA = -T^T M1 and dA^T = -M1^T T in registers

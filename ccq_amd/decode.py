@@ -12,7 +12,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, stream_of
-from .clean import _check_qk, _f32, reshape_lambda_3d, seq_count
+from .clean import _check_qk, _f32, check_device, norm_cu_seqlens, reshape_lambda_3d, seq_count
 
 __all__ = ["gdn_decode", "gla_decode", "needs_grad"]
 
@@ -22,10 +22,12 @@ def needs_grad(*xs) -> bool:
     return torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in xs)
 
 
-def _prep(q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, enable_ccq):
+def _prep(q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, enable_ccq, **others):
     _check_qk(q, k)
     if v.dtype != torch.bfloat16 or v.ndim != 4 or v.shape[:3] != q.shape[:3]:
         raise ValueError("v must be bf16 [B, T, H, V] matching q")
+    check_device(q.device, v=v, lambda_h=lambda_h, gate_w=gate_w, gate_b=gate_b, **others)
+    cu_seqlens = norm_cu_seqlens(cu_seqlens, q)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     gw, gb = _f32(gate_w), _f32(gate_b)
     lam = None
@@ -34,7 +36,7 @@ def _prep(q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, enable_ccq):
     B, T, H, K = q.shape
     N = seq_count(B, cu_seqlens)
     ws = torch.empty(_lib.load().ccq_decode_workspace_bytes(B * T, H, K), device=q.device, dtype=torch.uint8)
-    return q, k, v, lam, gw, gb, N, ws
+    return q, k, v, lam, gw, gb, N, ws, cu_seqlens
 
 
 def _states(N, H, K, V, dev, want, enable_ccq, subtract_mean):
@@ -48,7 +50,9 @@ def gdn_decode(q, k, v, lambda_h, g, beta, scale, initial_state=None, initial_co
                initial_mean_state=None, output_final_state=True, use_l2norm=True, cu_seqlens=None,
                position_offset=0, subtract_mean=True, enable_ccq=True, gate_w=None, gate_b=None):
     """One recurrent CCQ-GDN call.  Returns ``(o, S, C, m)`` (states None unless requested)."""
-    q, k, v, lam, gw, gb, N, ws = _prep(q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, enable_ccq)
+    q, k, v, lam, gw, gb, N, ws, cu_seqlens = _prep(
+        q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, enable_ccq, g=g, beta=beta, initial_state=initial_state,
+        initial_cov_state=initial_cov_state, initial_mean_state=initial_mean_state)
     B, T, H, K = q.shape
     V = v.shape[-1]
     if beta is None:
@@ -68,7 +72,9 @@ def gla_decode(q, k, v, lambda_h, gk, scale, initial_state=None, initial_cov_sta
                output_final_state=True, cu_seqlens=None, position_offset=0, subtract_mean=True, gate_w=None,
                gate_b=None):
     """One recurrent CCQ-GLA call (l2norm of q and k always on, as the reference).  Returns ``(o, S, C, m)``."""
-    q, k, v, lam, gw, gb, N, ws = _prep(q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, True)
+    q, k, v, lam, gw, gb, N, ws, cu_seqlens = _prep(
+        q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, True, gk=gk, initial_state=initial_state,
+        initial_cov_state=initial_cov_state, initial_mean_state=initial_mean_state)
     B, T, H, K = q.shape
     V = v.shape[-1]
     if gk is not None and gk.shape != q.shape:

@@ -516,12 +516,12 @@ def ccq_gdn_forward(q, k, v, lam, g, beta, *, scale=None, h0=None, h0_cov=None, 
 
     Returns ``(o, S_final, h_final, m_final)``.
     """
+    if use_qk_l2norm:   # with enable_ccq off the backbone normalises (use_qk_l2norm_in_kernel, :35-40)
+        q, k = _l2norm_io(q, k, l2norm_dtype)
     if not enable_ccq:
         fn = gdn_chunked if chunked else gdn_recurrent
         o, S = fn(q, k, v, g, beta, scale=scale, h0=h0, cu_seqlens=cu_seqlens)
         return o, S, None, None
-    if use_qk_l2norm:
-        q, k = _l2norm_io(q, k, l2norm_dtype)
     cl = clean_fwd_chunked if chunked else clean_fwd_bruteforce
     qc, hf, mf = cl(q, k, lam, position_offset=position_offset, h0=h0_cov,
                     m0=m0 if subtract_mean else None, subtract_mean=subtract_mean, cu_seqlens=cu_seqlens)

@@ -202,3 +202,36 @@ def test_layer_attention_mask(kind, oracle_ops):
     assert torch.count_nonzero(o.cpu()[~keep]).item() == 0
     print(kind, f"masked {err:.2e}", flush=True)
     assert err <= TOL
+
+
+def test_layer_c2_shape(oracle_ops):
+    """BASELINE C2's layer shape (d_model 1024, H 4, d_k 256, d_v 512: expand_v 2) at a reduced
+    length: one training step, output and every parameter gradient."""
+    dev = _cuda()
+    from ccq_amd import CCQGDN
+    B, T = 1, 140
+    torch.manual_seed(5)
+    ref = CCQGDN(hidden_size=1024, head_dim=256, num_heads=4, expand_v=2, mode="fused_chunk", layer_idx=0)
+    with torch.no_grad():
+        ref.erase_lambda_proj.bias.fill_(0.0)
+    ref = ref.double().train()
+    gpu = copy.deepcopy(ref).float().to(dev).train()
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(B, T, 1024, generator=g).bfloat16().float()
+    do = torch.randn(B, T, 1024, generator=g)
+    print("test_layer_c2_shape", flush=True)
+    with oracle_ops:
+        xr = x.to(D).requires_grad_()
+        o_r, _, _ = ref(xr)
+        (o_r * do.to(D)).sum().backward()
+    xg = x.to(dev).requires_grad_()
+    o, _, _ = gpu(xg)
+    (o * do.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    errs = {"o": rel(o, o_r), "dx": rel(xg.grad, xr.grad)}
+    for (n, p_r), (_, p) in zip(ref.named_parameters(), gpu.named_parameters()):
+        if p_r.grad is not None:
+            errs["d" + n] = rel(p.grad, p_r.grad)
+    print("C2 layer", {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    for n, e in errs.items():
+        assert e <= TOL, n

@@ -96,10 +96,9 @@ def test_clean_given_z(case):
            dict(q=q, k=k, z=z, lam=lam.to(torch.bfloat16), m0=m0).items()}
     qc_r, mf_r = O.clean_given_z(ref["q"], ref["k"], ref["z"], ref["lam"], position_offset=off, m0=ref["m0"],
                                  subtract_mean=sub, cu_seqlens=cu_t)
-    loss = (qc_r * dqc.to(d)).sum()
-    if sub:
-        loss = loss + (mf_r * dmf.to(d)).sum()
-    loss.backward()
+    # the reference's _CCQCleanQ.backward (clean.py:720-748) ignores the gradient of final_state_K
+    # and returns none for initial_state_K: its gradients are those of q_clean alone
+    (qc_r * dqc.to(d)).sum().backward()
     print(f"test_clean_given_z {case}", flush=True)
     g = {n: (t.to(dev).requires_grad_() if t is not None else None) for n, t in
          dict(q=q, k=k, z=z, lam=lam, m0=m0).items()}
@@ -117,8 +116,8 @@ def test_clean_given_z(case):
             "dz": rel(g["z"].grad, ref["z"].grad), "dlam": rel(g["lam"].grad, ref["lam"].grad)}
     if sub:
         errs["m_final"] = rel(mf, mf_r)
-        if wm0:
-            errs["dm0"] = rel(g["m0"].grad, ref["m0"].grad)
+    if wm0:
+        assert g["m0"].grad is None
     print(case, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
     for n in ("q_clean", "dq", "dk", "dz"):
         assert errs[n] <= TOL_BF16, n

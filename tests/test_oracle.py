@@ -207,6 +207,58 @@ def test_gdn_delta_rule_overwrites():
     assert torch.allclose(s[0, 0, 1], v[0, 1, 0], atol=1e-14)
 
 
+def test_gdn_decayed_prediction_closed_form():
+    # q_t = k_t (unit keys), scale 1: o_t = S_t^T k_t.  With S_{-1} = s0 and any g, beta:
+    #   o_0 = (1 - b0) a0 s0^T k0 + b0 v0
+    #   o_1 = (1 - b1) a1 S_0^T k1 + b1 v1,  S_0^T k1 = a0 s0^T k1 + b0 (v0 - a0 s0^T k0) (k0 . k1)
+    # The prediction inside the write must use the decayed state: an undecayed prediction, a
+    # missing (1 - beta) or a transposed state each break it.
+    q, k, v, g, beta, s0 = _gdn_in(1, 2, 3, 8, 5, seed=11)
+    g = g * 3.0  # strong decay, well away from 1
+    a = torch.exp(g)
+    for fn in (O.gdn_recurrent, O.gdn_chunked):
+        o, _ = fn(k, k, v, g, beta, scale=1.0, h0=s0)
+        for h in range(3):
+            k0, k1, v0, v1 = k[0, 0, h], k[0, 1, h], v[0, 0, h], v[0, 1, h]
+            a0, a1, b0, b1 = a[0, 0, h], a[0, 1, h], beta[0, 0, h], beta[0, 1, h]
+            S = s0[0, h]
+            e0 = (1 - b0) * a0 * (S.T @ k0) + b0 * v0
+            S0k1 = a0 * (S.T @ k1) + b0 * (v0 - a0 * (S.T @ k0)) * (k0 @ k1)
+            e1 = (1 - b1) * a1 * S0k1 + b1 * v1
+            assert torch.allclose(o[0, 0, h], e0, atol=1e-13), fn.__name__
+            assert torch.allclose(o[0, 1, h], e1, atol=1e-13), fn.__name__
+
+
+def test_gdn_overwrite_with_decay():
+    # beta = 1 and a unit key: S_t^T k_t = v_t exactly, whatever the decay and the history
+    q, k, v, g, beta, s0 = _gdn_in(1, 37, 2, 8, 4, seed=12)
+    beta = torch.ones_like(beta)
+    for fn in (O.gdn_recurrent, lambda *a, **kw: O.gdn_chunked(*a, BT=16, **kw)):
+        o, _ = fn(k, k, v, g * 4.0, beta, scale=1.0, h0=s0)
+        assert torch.allclose(o, v, atol=1e-12)
+
+
+def test_gla_single_write_decayed_readback():
+    # one write at t = 0 (k_t = 0 afterwards): S_t = diag(e^{G_t - G_0}) k_0 v_0^T, so
+    # o_t = scale (q_t . (k_0 o e^{G_t - G_0})) v_0, with G the running sum of gk (decay applied
+    # before the write of the same step)
+    B, T, H, K, V = 1, 70, 2, 8, 3
+    g = torch.Generator().manual_seed(13)
+    q = torch.randn(B, T, H, K, generator=g, dtype=D)
+    k = torch.zeros(B, T, H, K, dtype=D)
+    k[:, 0] = torch.randn(B, H, K, generator=g, dtype=D)
+    v = torch.randn(B, T, H, V, generator=g, dtype=D)
+    gk = torch.nn.functional.logsigmoid(torch.randn(B, T, H, K, generator=g, dtype=D)) / 4
+    G = torch.cumsum(gk, 1)
+    decay = torch.exp(G - G[:, :1])                                  # [B,T,H,K]
+    expect = (8 ** -0.5) * (q * decay * k[:, :1]).sum(-1, keepdim=True) * v[:, :1]
+    for fn in (O.gla_recurrent, lambda *a, **kw: O.gla_chunked(*a, BT=16, **kw)):
+        o, s = fn(q, k, v, gk)
+        assert torch.allclose(o, expect, atol=1e-13)
+        assert torch.allclose(s[0], (decay[0, -1][..., None] * k[0, 0][..., None]) * v[0, 0][:, None, :],
+                              atol=1e-13)
+
+
 def test_gla_no_decay_is_masked_linear_attention():
     q, k, v, _, _, _ = _gdn_in(1, 40, 2, 8, 5)
     o, _ = O.gla_chunked(q, k, v, None, BT=16)
@@ -303,3 +355,28 @@ def test_clean_given_z_composes_to_bruteforce(sub):
     else:
         assert mf is None and mr is None
 
+
+
+# ----------------------------------------------------------------------------- BASELINE C0
+
+
+def test_c0_fp32_chunked_vs_fp64_bruteforce():
+    """C0: the cleaning op alone on the CPU in fp32 (chunked path, gate lambda = sigma(W q + b)),
+    B=1, T=512, H=4, d_k=64, chunk 64, seed 0, q and k ~ N(0, 1) L2-normalised, W ~ N(0, 0.02^2),
+    b = 0, ones upstream gradient; q_clean, dq, dk, dW and db against the per-token fp64 loop."""
+    B, T, H, K = 1, 512, 4, 64
+    g = torch.Generator().manual_seed(0)
+    q = O.l2norm(torch.randn(B, T, H, K, generator=g))
+    k = O.l2norm(torch.randn(B, T, H, K, generator=g))
+    w = torch.randn(H, K, generator=g) * 0.02
+    b = torch.zeros(H)
+    res = {}
+    for dt, fn in ((torch.float32, O.clean_fwd_chunked), (D, O.clean_fwd_bruteforce)):
+        leaves = [t.detach().to(dt).clone().requires_grad_() for t in (q, k, w, b)]
+        lam = O.lambda_gate(leaves[0], leaves[2], leaves[3])
+        qc, _, _ = fn(leaves[0], leaves[1], lam)
+        qc.sum().backward()
+        res[dt] = [qc.detach()] + [t.grad for t in leaves]
+    for name, a, r in zip(("q_clean", "dq", "dk", "dW", "db"), res[torch.float32], res[D]):
+        err = ((a.double() - r).norm() / r.norm()).item()
+        assert err <= 1e-5, (name, err)
