@@ -25,6 +25,7 @@ hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
+hipError_t decode_scratch(hipStream_t st, void** out);
 hipError_t launch_zclean(int stage, const ZCleanArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
@@ -713,6 +714,29 @@ int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lam
   if (!beta) return fail(CCQ_ERR_NULL, "ccq_gdn_decode: beta is required");
   a.g = g; a.beta = beta; a.gla = 0;
   return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gdn_decode");
+}
+
+static_assert(CCQ_DECODE_SCRATCH_BYTES == ccq::kDecodeScratchBytes, "scratch size in the header and the library");
+
+int ccq_gdn_decode_noalloc(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                           const float* gate_b, const float* g, const float* beta, const float* state,
+                           const float* cov_state, const float* mean_state, const int64_t* cu_seqlens, void* o,
+                           float* state_out, float* cov_state_out, float* mean_state_out, int B, int T, int H, int K,
+                           int V, int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq,
+                           float scale, void* stream) {
+  if (int s = check_common(B, T, H, N, cu_seqlens)) return s;
+  if (!clean_k_ok(K)) return fail(CCQ_ERR_SHAPE, "ccq_gdn_decode_noalloc: K=%d not in {32, 64, 128, 256}", K);
+  const size_t need = carve_decode_work(nullptr, (int64_t)B * T, H, K, nullptr, nullptr);
+  if (need > kDecodeScratchBytes)
+    return fail(CCQ_ERR_SHAPE,
+                "ccq_gdn_decode_noalloc: %lld tokens x %d heads x K=%d need %zu bytes of scratch, above its "
+                "fixed %zu (8 bytes per token, head and key channel); use ccq_gdn_decode with a workspace",
+                (long long)B * T, H, K, need, kDecodeScratchBytes);
+  void* ws = nullptr;
+  if (int s = hip_status(decode_scratch((hipStream_t)stream, &ws), "ccq_gdn_decode_noalloc")) return s;
+  return ccq_gdn_decode(q, k, v, lambda, gate_w, gate_b, g, beta, state, cov_state, mean_state, cu_seqlens, o,
+                        state_out, cov_state_out, mean_state_out, ws, B, T, H, K, V, N, position_offset,
+                        subtract_mean, use_l2norm, enable_ccq, scale, stream);
 }
 
 int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,

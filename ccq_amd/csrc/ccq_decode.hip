@@ -14,6 +14,8 @@
 //   decode_backbone grid (N*H, V/64): each workgroup owns 64 columns of S, reads the cleaned query.
 // Thread (column j = tid % 64, row group tid / 64) holds K/4 consecutive rows of its column, so
 // every state access is a coalesced 256-byte row segment.
+#include <mutex>
+
 #include "ccq_tile.h"
 #include "ccq_decode_args.h"
 
@@ -195,6 +197,37 @@ hipError_t launch_decode_k(const DecodeArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(decode_clean_kernel<K>, dim3(units, (K + 63) / 64), dim3(kThreads), 0, st, a);
   hipLaunchKernelGGL(decode_backbone_kernel<K>, dim3(units, a.V / 64), dim3(kThreads), 0, st, a);
   return hipGetLastError();
+}
+
+// Scratch of the decode entry point that allocates nothing (ccq_gdn_decode_noalloc): a file-scope
+// device array, one copy per GPU, held until the process ends.  Its device address is looked up
+// once per device (with that device current) and kept; host code never passes the array's name
+// itself to a kernel.
+static __device__ __align__(256) char scratch[kDecodeScratchBytes];
+
+hipError_t decode_scratch(hipStream_t st, void** out) {
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int cur = 0, dev = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return e;
+  dev = cur;
+  if (st != nullptr && (e = hipStreamGetDevice(st, &dev)) != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> g(mu);
+  if (ptrs[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return e;
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st) {

@@ -2,9 +2,15 @@
 // kernels and the C-ABI entry points).
 #pragma once
 
+#include <stddef.h>
 #include <stdint.h>
 
 namespace ccq {
+
+// Size of the per-device scratch array of ccq_gdn_decode_noalloc (the decode workspace: the fp32
+// cleaned query and key of the call's tokens, 8 bytes per token, head and key channel).
+constexpr size_t kDecodeScratchBytes = (size_t)8 << 20;
+constexpr int kMaxDevices = 64;
 
 struct DecodeArgs {
   const void* q;           // bf16 [tokens, H, K]

@@ -206,6 +206,22 @@ int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lam
                    float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
                    int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq, float scale,
                    void* stream);
+/*
+ * ccq_gdn_decode without a workspace argument, for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same arguments, results and kernels as ccq_gdn_decode; its scratch is a fixed
+ * per-device array of CCQ_DECODE_SCRATCH_BYTES (8 bytes per token x head x key channel: B*T*H*K
+ * up to 1 Mi elements, e.g. 1,024 tokens of 4 heads at K = 256), and a larger call returns
+ * CCQ_ERR_SHAPE.  It calls no allocator.  Calls on one GPU share that array: calls that overlap
+ * in time on one GPU (different streams or host threads) race; calls in one stream are ordered.
+ */
+#define CCQ_DECODE_SCRATCH_BYTES ((size_t)8 << 20)
+int ccq_gdn_decode_noalloc(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                           const float* gate_b, const float* g, const float* beta, const float* state,
+                           const float* cov_state, const float* mean_state, const int64_t* cu_seqlens, void* o,
+                           float* state_out, float* cov_state_out, float* mean_state_out, int B, int T, int H, int K,
+                           int V, int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq,
+                           float scale, void* stream);
 int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
                    const float* gate_b, const float* gk, const float* state, const float* cov_state,
                    const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,

@@ -157,3 +157,14 @@ def test_gla_buffer_sizes(K, V):
     ws = lib.ccq_gla_bwd_workspace_bytes(tokens, nt, H, K, V)
     expect = 2 * nt * H * V * K * 2 + nt * H * K * 4
     assert expect <= ws <= expect + 3 * 256
+
+
+def test_decode_noalloc_rejects_calls_beyond_its_scratch():
+    # 2048 tokens x 4 heads x K=256 need 16 MiB of scratch, above the fixed 8 MiB: refused on the
+    # host, before any device work
+    lib = _lib.load()
+    p = _fake()
+    st = lib.ccq_gdn_decode_noalloc(p, p, p, p, None, None, None, p, None, None, None, None, p, None, None, None,
+                                    1, 2048, 4, 256, 512, 1, 0, 1, 1, 1, 0.0625, None)
+    assert st == CCQ_ERR_SHAPE
+    assert b"scratch" in lib.ccq_last_error()
