@@ -91,7 +91,8 @@ def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args), name)
 
 
-KERNELS = ("clean_fwd", "clean_bwd_rows", "clean_bwd_dq", "clean_bwd_dk", "clean_bwd_gate",
+KERNELS = ("clean_fwd_sum", "clean_fwd", "clean_bwd_rows", "clean_bwd_dq", "clean_bwd_gsum", "clean_bwd_dk",
+           "clean_bwd_gate",
            "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy",
            "gla_intra", "gla_fwd_state", "gla_fwd_o", "gla_bwd_state", "gla_bwd_dv", "gla_bwd_dqk", "gla_bwd_gk",
            "clean_z_fwd", "clean_z_bwd")

@@ -25,6 +25,9 @@ hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
+hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st);
+int cseg_count(int N, int H, int T);
+bool cseg_supported(int K);
 hipError_t decode_scratch(hipStream_t st, void** out);
 hipError_t launch_zclean(int stage, const ZCleanArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
@@ -165,9 +168,14 @@ struct WalkSaved {
   float* z;
   float* srow;
   float* mpre;
+  float* segD;  // segment walks: per-segment sums of k k^T and of k
+  float* segM;
+  int nseg;
 };
 
-size_t carve_walk_saved(char* base, const WalkGeom& g, int64_t tokens, int N, int H, int K, bool varlen,
+// Forward-to-backward buffer of the cleaning: for K in {64, 128} (segment walks) the per-segment
+// state totals; otherwise (column walks) the covariance read z, s_t and the chunk-start key sums.
+size_t carve_walk_saved(char* base, const WalkGeom& g, int64_t tokens, int N, int H, int K, int T, bool varlen,
                         WalkSaved* out) {
   Slicer sl{base};
   WalkSaved t{};
@@ -175,9 +183,15 @@ size_t carve_walk_saved(char* base, const WalkGeom& g, int64_t tokens, int N, in
     t.chunk_idx = sl.take<int>((size_t)g.ntg * 2);
     t.chunk_off = sl.take<int>((size_t)N + 1);
   }
-  t.z = sl.take<float>((size_t)tokens * H * K);
-  t.srow = sl.take<float>((size_t)tokens * H);
-  t.mpre = sl.take<float>((size_t)g.ntg * H * K);
+  if (cseg_supported(K)) {
+    t.nseg = cseg_count(N, H, T);
+    t.segD = sl.take<float>((size_t)N * H * t.nseg * K * K);
+    t.segM = sl.take<float>((size_t)N * H * t.nseg * K);
+  } else {
+    t.z = sl.take<float>((size_t)tokens * H * K);
+    t.srow = sl.take<float>((size_t)tokens * H);
+    t.mpre = sl.take<float>((size_t)g.ntg * H * K);
+  }
   if (out) *out = t;
   return sl.off;
 }
@@ -188,23 +202,26 @@ struct WalkWork {
   float* dw_part;
   float* db_part;
   float* red;  // first-pass row sums of dw_part / db_part
-  void* dzh;   // dz hi/lo (K in {64, 128}: written by the per-token pass, read by the walks)
-  void* dzl;
+  float* segG;  // segment walks: per-segment sums of q dz^T and of dm
+  float* segDM;
 };
 
-size_t carve_walk_work(char* base, const WalkGeom& g, int64_t tokens, int H, int K, bool gate, WalkWork* out) {
+size_t carve_walk_work(char* base, const WalkGeom& g, int64_t tokens, int N, int H, int K, int T, bool gate,
+                       WalkWork* out) {
   Slicer sl{base};
   WalkWork t{};
   t.sc = sl.take<float>((size_t)tokens * H * 4);
-  t.dmsum = sl.take<float>((size_t)g.ntg * H * K);
+  if (cseg_supported(K)) {
+    const int nseg = cseg_count(N, H, T);
+    t.segG = sl.take<float>((size_t)N * H * nseg * K * K);
+    t.segDM = sl.take<float>((size_t)N * H * nseg * K);
+  } else {
+    t.dmsum = sl.take<float>((size_t)g.ntg * H * K);
+  }
   if (gate) {
     t.dw_part = sl.take<float>((size_t)g.ntg * H * K);
     t.db_part = sl.take<float>((size_t)g.ntg * H);
     t.red = sl.take<float>((size_t)kSumSlices * H * (K + 1));
-  }
-  if (K == 64 || K == 128) {
-    t.dzh = sl.take<uint16_t>((size_t)tokens * H * K);
-    t.dzl = sl.take<uint16_t>((size_t)tokens * H * K);
   }
   if (out) *out = t;
   return sl.off;
@@ -215,7 +232,7 @@ void fill_walk_common(WalkArgs& a, const void* q, const void* k, const float* ga
                       int T, int H, int K, int N, int pos_off, int subtract_mean) {
   a.q = q; a.k = k; a.gate_w = gate_w; a.gate_b = gate_b; a.h0 = h0; a.m0 = subtract_mean ? m0 : nullptr;
   a.cu = cu; a.chunk_idx = sv.chunk_idx; a.chunk_off = sv.chunk_off;
-  a.z = sv.z; a.srow = sv.srow; a.mpre = sv.mpre;
+  a.z = sv.z; a.srow = sv.srow; a.mpre = sv.mpre; a.segD = sv.segD; a.segM = sv.segM; a.nseg = sv.nseg;
   a.T = T; a.H = H; a.N = N; a.NT = g.nt; a.NTG = g.ntg; a.K = K; a.pos_off = pos_off;
   a.subtract_mean = subtract_mean ? 1 : 0;
 }
@@ -226,12 +243,12 @@ extern "C" {
 
 size_t ccq_clean_saved_bytes(int64_t tokens, int B, int T, int N, int H, int K, int varlen) {
   const WalkGeom g = walk_geom(tokens, B, T, N, K, varlen != 0);
-  return carve_walk_saved(nullptr, g, tokens, N, H, K, varlen != 0, nullptr);
+  return carve_walk_saved(nullptr, g, tokens, N, H, K, T, varlen != 0, nullptr);
 }
 
 size_t ccq_clean_bwd_workspace_bytes(int64_t tokens, int B, int T, int N, int H, int K, int varlen, int gate) {
   const WalkGeom g = walk_geom(tokens, B, T, N, K, varlen != 0);
-  return carve_walk_work(nullptr, g, tokens, H, K, gate != 0, nullptr);
+  return carve_walk_work(nullptr, g, tokens, N, H, K, T, gate != 0, nullptr);
 }
 
 int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float* gate_w, const float* gate_b,
@@ -250,7 +267,7 @@ int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float
   const int64_t tokens = (int64_t)B * T;
   const WalkGeom g = walk_geom(tokens, B, T, N, K, varlen);
   WalkSaved sv;
-  carve_walk_saved((char*)saved, g, tokens, N, H, K, varlen, &sv);
+  carve_walk_saved((char*)saved, g, tokens, N, H, K, T, varlen, &sv);
   hipStream_t st = (hipStream_t)stream;
   if (varlen) {
     if (int s = hip_status(launch_chunk_index(cu_seqlens, N, g.cb, sv.chunk_off, sv.chunk_idx, g.ntg, st),
@@ -261,6 +278,11 @@ int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float
   fill_walk_common(a, q, k, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, K, N, position_offset, subtract_mean);
   a.lam = lambda; a.lam_out = lambda_out; a.qc = q_clean; a.qc32 = q_clean_f32; a.h_fin = h_final;
   a.m_fin = subtract_mean ? m_final : nullptr;
+  if (cseg_supported(K)) {
+    if (int s = hip_status(timed("clean_fwd_sum", st, [&] { return launch_cseg(kSegSum, a, st); }), "clean_fwd_sum"))
+      return s;
+    return hip_status(timed("clean_fwd", st, [&] { return launch_cseg(kSegFwd, a, st); }), "ccq_clean_fwd");
+  }
   return hip_status(timed("clean_fwd", st, [&] { return launch_cwalk(kWalkFwd, a, st); }), "ccq_clean_fwd");
 }
 
@@ -287,23 +309,37 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
   const int64_t tokens = (int64_t)B * T;
   const WalkGeom g = walk_geom(tokens, B, T, N, K, varlen);
   WalkSaved sv;
-  carve_walk_saved((char*)saved, g, tokens, N, H, K, varlen, &sv);
+  carve_walk_saved((char*)saved, g, tokens, N, H, K, T, varlen, &sv);
   WalkWork wk;
-  carve_walk_work((char*)workspace, g, tokens, H, K, gate, &wk);
+  carve_walk_work((char*)workspace, g, tokens, N, H, K, T, gate, &wk);
   hipStream_t st = (hipStream_t)stream;
   WalkArgs a{};
   fill_walk_common(a, q, k, gate_w, gate_b, h0, m0, cu_seqlens, sv, g, T, H, K, N, position_offset, subtract_mean);
   a.lam_used = lambda; a.sc = wk.sc; a.dmsum = subtract_mean ? wk.dmsum : nullptr;
-  a.dzh = wk.dzh; a.dzl = wk.dzl;
+  a.segG = wk.segG; a.segDM = wk.segDM;
   a.dw_part = wk.dw_part; a.db_part = wk.db_part;
   a.dqc32 = dq_clean_f32; a.dqc16 = dq_clean_f32 ? nullptr : dq_clean; a.dk_extra = dk_extra;
   a.dh_fin = dh_final; a.dm_fin = subtract_mean ? dm_final : nullptr;
   a.dq = dq; a.dq32 = dq_f32; a.dk = dk; a.dk32 = dk_f32; a.dlam = gate ? nullptr : dlambda; a.dh0 = dh0;
   a.dm0 = subtract_mean ? dm0 : nullptr;
   struct StageName { int stage; const char* name; };
-  const StageName stages[] = {{kWalkRows, "clean_bwd_rows"}, {kWalkDq, "clean_bwd_dq"}, {kWalkDk, "clean_bwd_dk"}};
-  for (const StageName& sn : stages) {
-    if (int s = hip_status(timed(sn.name, st, [&] { return launch_cwalk(sn.stage, a, st); }), sn.name)) return s;
+  if (cseg_supported(K)) {
+    if (gate && varlen) {
+      // the walks write the gate partials of real chunks only: clear the padding entries' too
+      if (int s = hip_status(launch_fill_zero(wk.dw_part, (long)g.ntg * H * K, st), "ccq_clean_bwd(dW parts)"))
+        return s;
+      if (int s = hip_status(launch_fill_zero(wk.db_part, (long)g.ntg * H, st), "ccq_clean_bwd(db parts)"))
+        return s;
+    }
+    const StageName stages[] = {{kSegDq, "clean_bwd_dq"}, {kSegGsum, "clean_bwd_gsum"}, {kSegDk, "clean_bwd_dk"}};
+    for (const StageName& sn : stages) {
+      if (int s = hip_status(timed(sn.name, st, [&] { return launch_cseg(sn.stage, a, st); }), sn.name)) return s;
+    }
+  } else {
+    const StageName stages[] = {{kWalkRows, "clean_bwd_rows"}, {kWalkDq, "clean_bwd_dq"}, {kWalkDk, "clean_bwd_dk"}};
+    for (const StageName& sn : stages) {
+      if (int s = hip_status(timed(sn.name, st, [&] { return launch_cwalk(sn.stage, a, st); }), sn.name)) return s;
+    }
   }
   if (dm0 && !subtract_mean) {
     if (int s = hip_status(launch_fill_zero(dm0, (long)N * H * K, st), "ccq_clean_bwd(dm0)"))

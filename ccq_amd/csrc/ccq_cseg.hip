@@ -1,0 +1,1161 @@
+// CCQ read-side cleaning on gfx950: segment walks (K in {64, 128}), forward and backward.
+//
+// Mathematics (reference ccq/ops/common/fused_read.py:11-25):
+//   C_t = h_0 + sum_{j<=t} k_j k_j^T   m_t = m_0 + sum_{j<=t} k_j
+//   z_t = C_t^T q_t   s_t = m_t . q_t   corr_t = z_t/pos_t - s_t m_t/pos_t^2 (mean term optional)
+//   q_clean_t = q_t - lambda_t corr_t
+// Backward, with dz_t = f_t dqc_t, f_t = -lambda_t/pos_t:
+//   dlambda_t = -dqc_t . corr_t   ds_t = lambda_t (dqc_t . m_t)/pos_t^2
+//   dm_t = -(s_t/pos_t) dz_t + ds_t q_t
+//   dq_t = dqc_t + ds_t m_t + C_t dz_t (+ gate: dlogit_t w, dlogit_t = dlambda_t lambda_t (1 - lambda_t))
+//   dk_j = E_j k_j + sum_{t>=j} dm_t + dm_T,  E_j = sum_{t>=j} (q_t dz_t^T + dz_t q_t^T) + dC_T + dC_T^T
+//   dC_0 = sum_t q_t dz_t^T + dC_T,   dm_0 = sum_t dm_t + dm_T
+// C is symmetric (h_0 is taken as symmetric: it is a sum of k k^T in every caller).
+//
+// Layout of the work.  Both state recurrences are plain sums (C and m forward, E and the dm carry
+// backward), so the state at any chunk is a prefix of per-chunk products.  Each (sequence, head) is
+// cut into `nseg` time segments of whole 64-token chunks:
+//   cs_sum    (forward)  per segment: sum of K^T K and of k          -> segD, segM (saved)
+//   cs_fwd    (forward)  walk of one segment from h_0 + earlier segD: q_clean
+//   cs_dq     (backward) walk of one segment, recomputing z: dq, the per-token scalars, gate partials
+//   cs_gsum   (backward) per segment: sum of Q^T dZ and of dm        -> segG, segDM
+//   cs_dk     (backward) reverse walk of one segment from the later segments' totals: dk, dC_0, dm_0
+// One workgroup takes one segment; inside it each wavefront owns 16 state columns over all K rows,
+// as 16x16 MFMA accumulator tiles in registers, so the state never goes through LDS.  Products that
+// read the state take it as their B operand straight from the accumulator layout (lane = column,
+// four consecutive rows per 16-lane group), with the contraction slots of the A operand permuted to
+// match (two 8-byte LDS reads per lane, frag16_rm_acc).  Row scalars that contract over all of K
+// (m . q, the gate logit) are MFMAs against broadcast operands; per-row dot products over the
+// columns (dqc . corr, dqc . m) are summed within a wave by DPP and across waves through LDS.
+// Every product keeps ~16 significant bits: fp32 operands enter as hi/lo bf16 pairs, q and k are
+// exact.  Chunk operands are prefetched into registers one chunk ahead and staged into LDS after
+// the chunk's last read; results are staged in LDS and leave as whole 16-byte row pieces after the
+// prefetch has been waited for (a single in-order counter covers loads and stores, so a store
+// issued before a load would hold the load's wait).
+#include "ccq_tile.h"
+#include "ccq_walk_args.h"
+
+namespace ccq {
+
+namespace {
+
+constexpr int SB = 64;  // tokens per chunk
+
+__device__ __forceinline__ float seg_pos(int t, int off) {
+  const float p = (float)(t + 1 + off);
+  return p < 1.f ? 1.f : p;
+}
+
+__device__ __forceinline__ bf16x8 ones8_() {
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)1.f;
+  return v;
+}
+
+// A operand of mfma16 (row r = lane % 16) whose contraction slots follow the accumulator layout of
+// two 16-row C tiles: lane group g, slot j -> k = 4 g + j (j < 4) and 16 + 4 g + (j - 4) (j >= 4).
+// Element (r, k) at p[r * ld + k]: two 8-byte reads.
+__device__ __forceinline__ bf16x8 frag16_rm_acc(const bf16* p, int ld) {
+  const int l = lane_id();
+  const bf16* q = p + (l & 15) * ld + 4 * (l >> 4);
+  const bf16x4 a = *(const bf16x4*)q, b = *(const bf16x4*)(q + 16);
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// B operand (hi/lo) of a 32-deep contraction step from two accumulator tiles holding rows
+// [k0, k0 + 16) and [k0 + 16, k0 + 32): slot order of frag16_rm_acc.
+__device__ __forceinline__ void acc_pair_split(const f32x4& t0, const f32x4& t1, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bf16 a, b;
+    split2(t0[i], a, b);
+    hi[i] = a;
+    lo[i] = b;
+    split2(t1[i], a, b);
+    hi[4 + i] = a;
+    lo[4 + i] = b;
+  }
+}
+
+// Lower-triangular (inclusive) ones as the A operand of mfma16: row t = 16 tt + lane % 16,
+// contraction slots s = 32 ss + 8 (lane / 16) + j.
+__device__ __forceinline__ bf16x8 tril16(int tt, int ss) {
+  const int l = lane_id(), t = 16 * tt + (l & 15), s = 32 * ss + 8 * (l >> 4);
+  bf16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = (s + j <= t) ? (bf16)1.f : (bf16)0.f;
+  return v;
+}
+
+// Causal score tile e (0..9) as (t tile, s tile): (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) ...
+__device__ __forceinline__ int tile_t(int e) { return e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3; }
+__device__ __forceinline__ int tile_s(int e) { return e - tile_t(e) * (tile_t(e) + 1) / 2; }
+
+template <int C>
+__device__ __forceinline__ float dppf(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), C, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a row (lanes 16 g .. 16 g + 15), every lane receives it: quad_perm
+// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dppf<0xB1>(x);
+  x += dppf<0x4E>(x);
+  x += dppf<0x141>(x);
+  x += dppf<0x140>(x);
+  return x;
+}
+
+// One segment of one (sequence, head): chunks [cb, ce) of the sequence's nc chunks.
+struct SegUnit {
+  int unit, seg, n, h, len, nc, cb, ce, gc0;
+  long bos, hb, rs;
+};
+
+template <int K>
+__device__ __forceinline__ SegUnit seg_unit(const WalkArgs& a) {
+  SegUnit u;
+  xcd_map(blockIdx.x, a.nseg, a.N * a.H, u.unit, u.seg);
+  u.n = u.unit / a.H;
+  u.h = u.unit % a.H;
+  seq_bounds(a.cu, u.n, a.T, u.bos, u.len);
+  u.nc = (u.len + SB - 1) / SB;
+  const int per = (u.nc + a.nseg - 1) / a.nseg;
+  u.cb = min(u.nc, u.seg * per);
+  u.ce = min(u.nc, u.cb + per);
+  u.gc0 = a.cu ? a.chunk_off[u.n] : u.n * a.NT;
+  u.rs = (long)a.H * K;
+  u.hb = (u.bos * a.H + u.h) * K;
+  return u;
+}
+
+// fp32 rows staged in LDS (ld elements apart) to HBM as fp32 and/or bf16, with an optional fp32
+// addend read from HBM; rows at or beyond L are skipped.  Thread piece mapping of RowsF32<K, SB, NT>.
+template <int K, int NT>
+__device__ __forceinline__ void store_rows(const float* src, int ld, float* g32, bf16* g16, const float* add32,
+                                           long base, long rs, int L, int tid) {
+  constexpr int VPR = K / 4, TOT = SB * VPR, N = TOT / NT;
+  static_assert(TOT % NT == 0, "whole passes");
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int idx = tid + j * NT, r = idx / VPR, c = (idx % VPR) * 4;
+    if (r < L) {
+      f32x4 v = *(const f32x4*)(src + r * ld + c);
+      const long e = base + (long)r * rs + c;
+      if (add32) v += *gmem((const f32x4*)(add32 + e));
+      if (g32) *gmem((f32x4*)(g32 + e)) = v;
+      if (g16) *gmem((bf16x4*)(g16 + e)) = bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+    }
+  }
+}
+
+// Sum of the segment totals tot[unit][s] for s in [s0, s1) into the lane's accumulator tiles
+// (rows 16 kt + g4 + i, column col), optionally plus the transposed tiles (tot[.][col][k]).
+template <int K, bool TRANS>
+__device__ __forceinline__ void add_seg_tiles(f32x4 (&X)[K / 16], const float* tot, long unit, int nseg, int s0,
+                                              int s1, int col, int g4) {
+  for (int s = s0; s < s1; ++s) {
+    const float* p = tot + ((long)unit * nseg + s) * K * K;
+#pragma unroll
+    for (int kt = 0; kt < K / 16; ++kt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) X[kt][i] += p[(long)(16 * kt + g4 + i) * K + col];
+      if (TRANS) X[kt] += *(const f32x4*)(p + (long)col * K + 16 * kt + g4);
+    }
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+// cs_sum: grid N*H*nseg, K/16 waves.  segD = sum over the segment's chunks of K^T K, segM = sum of
+// k (every workgroup writes its totals, zero for an empty segment).  Two chunks in flight.
+// ===========================================================================
+template <int K>
+__global__ __launch_bounds__(K * 4) void cs_sum_kernel(const WalkArgs a) {
+  constexpr int NW = K / 16, NT = 64 * NW, LDK = K + 16, NKT = K / 16;
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][SB * LDK];
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const SegUnit u = seg_unit<K>(a);
+  const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
+  auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
+  f32x4 D[NKT];
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) D[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float msum = 0.f;
+  RowsBf16<K, SB, NT> p0, p1;
+  auto kptr = [&](int c) { return (const bf16*)a.k + u.hb + (long)c * SB * u.rs; };
+  const int nloc = u.ce - u.cb;
+  if (nloc > 0) p0.load(kptr(u.cb), u.rs, chunk_len(u.cb), tid);
+  if (nloc > 1) p1.load(kptr(u.cb + 1), u.rs, chunk_len(u.cb + 1), tid);
+  if (nloc > 0) p0.store(sK[0], LDK, chunk_len(u.cb), tid);
+  __syncthreads();
+  auto step = [&](int i, RowsBf16<K, SB, NT>& cur, RowsBf16<K, SB, NT>& nxt) {
+    // chunk cb + i is in buffer i & 1; `cur` is free (staged), `nxt` holds chunk cb + i + 1
+    const bf16* Kc = sK[i & 1];
+    if (i + 2 < nloc) cur.load(kptr(u.cb + i + 2), u.rs, chunk_len(u.cb + i + 2), tid);
+    bf16x8 kcol[2];
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) kcol[ss] = frag16_tr(Kc + 32 * ss * LDK + c0, LDK);
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) {
+      tot = mfma16(tril16(3, ss), kcol[ss], tot);
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) D[kt] = mfma16(frag16_tr(Kc + 32 * ss * LDK + 16 * kt, LDK), kcol[ss], D[kt]);
+    }
+    msum += __shfl(tot[3], 48 + (l & 15));
+    if (i + 1 < nloc) nxt.store(sK[(i + 1) & 1], LDK, chunk_len(u.cb + i + 1), tid);
+    __syncthreads();
+  };
+  int i = 0;
+  for (; i + 1 < nloc; i += 2) {
+    step(i, p0, p1);
+    step(i + 1, p1, p0);
+  }
+  if (i < nloc) step(i, p0, p1);
+  float* dst = a.segD + ((long)u.unit * a.nseg + u.seg) * K * K;
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[(long)(16 * kt + g4 + r) * K + col] = D[kt][r];
+  if (l < 16) a.segM[((long)u.unit * a.nseg + u.seg) * K + col] = msum;
+}
+
+// ===========================================================================
+// cs_fwd: grid N*H*nseg, K/16 waves (one per 16 state columns).  Per chunk:
+//   scores   A = (Q K^T) o M: 10 causal 16x16 tiles spread over the waves, to LDS as hi/lo bf16
+//   scalars  s_t = m_prev . q_t + sum_s A[t][s], the gate logit w . q_t: MFMAs against broadcast
+//            operands, one 16-row tile per wave of the last four
+//   per wave Z[:, cols] = Q C_prev[:, cols] + A K[:, cols]; running key sums (lower-triangular ones
+//            times K[:, cols]); q_clean to LDS; C[:, cols] += K^T K[:, cols]
+//   all      chunk c+1 from registers into the other LDS buffers; q_clean rows to HBM
+// Outputs: q_clean (bf16 and/or fp32), the gate's lambda, C_T and m_T (last segment).
+// ===========================================================================
+template <int K, bool MEAN, bool GATE>
+__global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
+  constexpr int NW = K / 16, NT = 64 * NW;
+  constexpr int LDK = K + 16, LDA = SB + 16, LDO = K + 4;
+  constexpr int NKS = K / 32, NKT = K / 16;
+  __shared__ __attribute__((aligned(16))) bf16 sQ[2][SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sAh[SB * LDA];   // scores A[t][s] (s <= t), hi
+  __shared__ __attribute__((aligned(16))) bf16 sAl[SB * LDA];
+  __shared__ __attribute__((aligned(16))) float sO[SB * LDO];   // q_clean rows
+  __shared__ __attribute__((aligned(16))) bf16 sMW[2][4 * LDK];  // rows: m hi, m lo, gate w hi, lo
+  __shared__ __attribute__((aligned(16))) float sS[SB];          // s_t
+  __shared__ __attribute__((aligned(16))) float sLam[SB];        // lambda_t
+  __shared__ __attribute__((aligned(16))) float sLamIn[2][SB];   // given lambda, by buffer
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const SegUnit u = seg_unit<K>(a);
+  const bool last = u.seg == a.nseg - 1;
+  if (u.cb >= u.ce && !last) return;
+  const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
+  auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
+
+  // state at the segment start: h_0 + the earlier segments' K^T K; the lane's column of the key sum
+  f32x4 C[NKT];
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) C[kt][i] = a.h0 ? a.h0[((long)u.unit * K + 16 * kt + g4 + i) * K + col] : 0.f;
+  add_seg_tiles<K, false>(C, a.segD, u.unit, a.nseg, 0, u.seg, col, g4);
+  float mcol = 0.f;
+  if (MEAN) {
+    mcol = a.m0 ? a.m0[(long)u.unit * K + col] : 0.f;
+    for (int s = 0; s < u.seg; ++s) mcol += a.segM[((long)u.unit * a.nseg + s) * K + col];
+  }
+
+  // LDS set-up: scores above the diagonal tiles stay zero; gate rows of both buffers; key sums
+  for (int i = tid; i < SB * LDA; i += NT) {
+    sAh[i] = (bf16)0.f;
+    sAl[i] = (bf16)0.f;
+  }
+  for (int i = tid; i < 2 * K; i += NT) {
+    const int r = i / K, cc = i % K;
+    bf16 hh = (bf16)0.f, ll = (bf16)0.f;
+    if (GATE) split2(a.gate_w[(long)u.h * K + cc], hh, ll);
+    sMW[0][(2 + r) * LDK + cc] = r == 0 ? hh : ll;
+    sMW[1][(2 + r) * LDK + cc] = r == 0 ? hh : ll;
+  }
+  auto put_m = [&](int b) {
+    if (l < 16) {
+      bf16 x, y;
+      split2(mcol, x, y);
+      sMW[b][col] = x;
+      sMW[b][LDK + col] = y;
+    }
+  };
+  if (MEAN) put_m(u.cb & 1);
+
+  RowsBf16<K, SB, NT> pq, pk;
+  float plam = 0.f;
+  auto load = [&](int c) {
+    const int L = chunk_len(c);
+    const long off = u.hb + (long)c * SB * u.rs;
+    pk.load((const bf16*)a.k + off, u.rs, L, tid);
+    pq.load((const bf16*)a.q + off, u.rs, L, tid);
+    if (!GATE && tid < SB) plam = a.lam[(u.bos + (long)c * SB + min(tid, L - 1)) * a.H + u.h];
+  };
+  auto stage = [&](int c) {
+    const int L = chunk_len(c), b = c & 1;
+    pk.store(sK[b], LDK, L, tid);
+    pq.store(sQ[b], LDK, L, tid);
+    if (!GATE && tid < SB) sLamIn[b][tid] = tid < L ? plam : 0.f;
+  };
+  if (u.cb < u.ce) {
+    load(u.cb);
+    stage(u.cb);
+  }
+  __syncthreads();
+
+  const float gbias = GATE ? a.gate_b[u.h] : 0.f;
+  for (int c = u.cb; c < u.ce; ++c) {
+    const int b = c & 1, L = chunk_len(c), t0 = c * SB;
+    const bf16* Qc = sQ[b];
+    const bf16* Kc = sK[b];
+    if (c + 1 < u.ce) load(c + 1);
+    bf16x8 kcol[2];
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) kcol[ss] = frag16_tr(Kc + 32 * ss * LDK + c0, LDK);
+
+    // ---- scores (tiles w, w + NW, w + 2 NW) and row scalars (t tile w - (NW - 4))
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int e = w + j * NW;
+      if (e < 10) {
+        const int I = tile_t(e), J = tile_s(e);
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+          acc = mfma16(frag16_rm(Kc + 16 * J * LDK + 32 * ks, LDK), frag16_rm(Qc + 16 * I * LDK + 32 * ks, LDK), acc);
+        if (I == J) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (g4 + i > (l & 15)) acc[i] = 0.f;
+        }
+        acc16_to_lds_t(acc, sAh + 16 * I * LDA, sAl + 16 * I * LDA, LDA, 16 * J);
+      }
+    }
+    if (w >= NW - 4) {
+      const int tt = w - (NW - 4), tb = 16 * tt + g4;
+      f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f}, lg = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const bf16x8 qf = frag16_rm(Qc + 16 * tt * LDK + 32 * ks, LDK);
+        if (MEAN) {
+          sv = mfma16(qf, frag16_rm(sMW[b] + 32 * ks, 0), sv);
+          sv = mfma16(qf, frag16_rm(sMW[b] + LDK + 32 * ks, 0), sv);
+        }
+        if (GATE) {
+          lg = mfma16(qf, frag16_rm(sMW[b] + 2 * LDK + 32 * ks, 0), lg);
+          lg = mfma16(qf, frag16_rm(sMW[b] + 3 * LDK + 32 * ks, 0), lg);
+        }
+      }
+      // (the score row sums join s_t after the barrier: other waves write those tiles)
+      if ((l & 15) == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = tb + i;
+          float lam;
+          if (GATE) lam = t < L ? __builtin_amdgcn_rcpf(1.f + __expf(-(lg[i] + gbias))) : 0.f;
+          else lam = sLamIn[b][t];
+          sLam[t] = lam;
+          sS[t] = sv[i];
+          if (GATE && a.lam_out && t < L) a.lam_out[(u.bos + t0 + t) * a.H + u.h] = lam;
+        }
+      }
+    }
+    __syncthreads();
+    if (MEAN) {
+      if (w >= NW - 4) {
+        const int tt = w - (NW - 4), tb = 16 * tt + g4;
+        f32x4 rsum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) {
+          if (ss <= (tt >> 1)) {
+            rsum = mfma16(frag16_rm(sAh + 16 * tt * LDA + 32 * ss, LDA), ones8_(), rsum);
+            rsum = mfma16(frag16_rm(sAl + 16 * tt * LDA + 32 * ss, LDA), ones8_(), rsum);
+          }
+        }
+        if ((l & 15) == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sS[tb + i] += rsum[i];
+        }
+      }
+      __syncthreads();
+    }
+
+    // ---- per wave: Z[:, cols] = Q C_prev[:, cols] + A K[:, cols]; key sums; q_clean to LDS.  One
+    // 16-row tile at a time (a runtime loop keeps the live registers few); the state's hi/lo B
+    // operands are formed per contraction step, hi and lo products go to separate accumulators
+    f32x4 cum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int tt = 0; tt < 4; ++tt) {
+      f32x4 zh = f32x4{0.f, 0.f, 0.f, 0.f}, zl = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        bf16x8 chh, chl;
+        acc_pair_split(C[2 * ks], C[2 * ks + 1], chh, chl);
+        const bf16x8 qa = frag16_rm_acc(Qc + 16 * tt * LDK + 32 * ks, LDK);
+        zh = mfma16(qa, chh, zh);
+        zl = mfma16(qa, chl, zl);
+      }
+      cum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss) {
+        if (ss <= (tt >> 1)) {
+          zh = mfma16(frag16_rm(sAh + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zh);
+          zl = mfma16(frag16_rm(sAl + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zl);
+          if (MEAN) cum = mfma16(tril16(tt, ss), kcol[ss], cum);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * tt + g4 + i;
+        const float ip = __builtin_amdgcn_rcpf(seg_pos(t0 + t, a.pos_off));
+        float corr = (zh[i] + zl[i]) * ip;
+        if (MEAN) corr -= sS[t] * ip * ip * (mcol + cum[i]);
+        sO[t * LDO + col] = (float)Qc[t * LDK + col] - sLam[t] * corr;
+      }
+    }
+    // key-sum total of the chunk: row 63 of the running sums (rows past the chunk hold k = 0)
+    if (MEAN) mcol += __shfl(cum[3], 48 + (l & 15));
+
+    // ---- state update C[:, cols] += K^T K[:, cols]
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss)
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) C[kt] = mfma16(frag16_tr(Kc + 32 * ss * LDK + 16 * kt, LDK), kcol[ss], C[kt]);
+    if (MEAN) put_m(b ^ 1);
+    if (c + 1 < u.ce) stage(c + 1);
+    __syncthreads();
+    store_rows<K, NT>(sO, LDO, a.qc32, (bf16*)a.qc, nullptr, u.hb + (long)t0 * u.rs, u.rs, L, tid);
+  }
+
+  if (last) {
+    if (a.h_fin) {
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a.h_fin[((long)u.unit * K + 16 * kt + g4 + i) * K + col] = C[kt][i];
+    }
+    if (MEAN && a.m_fin && l < 16) a.m_fin[(long)u.unit * K + col] = mcol;
+  }
+}
+
+// ===========================================================================
+// cs_dq: grid N*H*nseg, K/16 waves; the forward walk again, with the upstream gradient.  Per chunk
+// (dZ = diag(f) dQc hi/lo in LDS, staged with the chunk):
+//   1  scores A = (Q K^T) o M and B = (dZ K^T) o M (20 tiles over the waves); s_t (last four waves)
+//   2  per wave and 16-row tile: Z = Q C + A K, W = dZ C + B K, m_t; partial row dots over the
+//      wave's columns of dqc . corr and dqc . m_t; dqc + W in place
+//   3  row totals of the partial dots (threads 0..127)
+//   4  per wave: dlambda, ds, dlogit; dq = dqc + W + ds m_t (+ dlogit w) in place; the per-token
+//      scalars (wave 0); gate partials; C, m update
+//   5  dq rows to HBM, chunk c+1 into LDS (each thread overwrites exactly the pieces it stored)
+// ===========================================================================
+template <int K, bool MEAN, bool GATE>
+__global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
+  constexpr int NW = K / 16, NT = 64 * NW;
+  constexpr int LDK = K + 16, LDA = SB + 16, LDD = K + 4;
+  constexpr int NKS = K / 32, NKT = K / 16;
+  __shared__ __attribute__((aligned(16))) bf16 sQ[SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sK[SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];   // dZ = diag(f) dQc, hi
+  __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDK];
+  __shared__ __attribute__((aligned(16))) float sD[SB * LDD];   // dQc, then dQc + W, then dq
+  __shared__ __attribute__((aligned(16))) bf16 sAh[SB * LDA];   // (Q K^T) o M
+  __shared__ __attribute__((aligned(16))) bf16 sAl[SB * LDA];
+  __shared__ __attribute__((aligned(16))) bf16 sBh[SB * LDA];   // (dZ K^T) o M
+  __shared__ __attribute__((aligned(16))) bf16 sBl[SB * LDA];
+  __shared__ __attribute__((aligned(16))) bf16 sMW[2 * LDK];     // m_prev hi, lo
+  __shared__ __attribute__((aligned(16))) float sPart[NW][2][SB];  // per-wave partial row dots
+  __shared__ __attribute__((aligned(16))) float sTot[2][SB];
+  __shared__ __attribute__((aligned(16))) float sS[SB], sLam[SB], sF[SB], sGw[K];
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const SegUnit u = seg_unit<K>(a);
+  if (u.cb >= u.ce) return;
+  const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
+  auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
+
+  f32x4 C[NKT];
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) C[kt][i] = a.h0 ? a.h0[((long)u.unit * K + 16 * kt + g4 + i) * K + col] : 0.f;
+  add_seg_tiles<K, false>(C, a.segD, u.unit, a.nseg, 0, u.seg, col, g4);
+  float mcol = 0.f;
+  if (MEAN) {
+    mcol = a.m0 ? a.m0[(long)u.unit * K + col] : 0.f;
+    for (int s = 0; s < u.seg; ++s) mcol += a.segM[((long)u.unit * a.nseg + s) * K + col];
+  }
+  for (int i = tid; i < SB * LDA; i += NT) {
+    sAh[i] = (bf16)0.f;
+    sAl[i] = (bf16)0.f;
+    sBh[i] = (bf16)0.f;
+    sBl[i] = (bf16)0.f;
+  }
+  if (GATE)
+    for (int i = tid; i < K; i += NT) sGw[i] = a.gate_w[(long)u.h * K + i];
+  auto put_m = [&]() {
+    if (l < 16) {
+      bf16 x, y;
+      split2(mcol, x, y);
+      sMW[col] = x;
+      sMW[LDK + col] = y;
+    }
+  };
+  if (MEAN) put_m();
+
+  RowsBf16<K, SB, NT> pq, pk;
+  RowsF32<K, SB, NT> pd;
+  constexpr int ND = RowsF32<K, SB, NT>::N, VPR = K / 4;
+  float pl[ND], plam = 0.f;
+  auto load = [&](int c) {
+    const int L = chunk_len(c);
+    const long off = u.hb + (long)c * SB * u.rs;
+    pk.load((const bf16*)a.k + off, u.rs, L, tid);
+    pq.load((const bf16*)a.q + off, u.rs, L, tid);
+    pd.load(a.dqc32 ? a.dqc32 + off : nullptr, a.dqc32 ? nullptr : (const bf16*)a.dqc16 + off, u.rs, L, tid);
+    const long tb = u.bos + (long)c * SB;
+#pragma unroll
+    for (int j = 0; j < ND; ++j) pl[j] = a.lam_used[(tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h];
+    if (tid < SB) plam = a.lam_used[(tb + min(tid, L - 1)) * a.H + u.h];
+  };
+  auto stage = [&](int c) {
+    const int L = chunk_len(c), t0 = c * SB;
+    pk.store(sK, LDK, L, tid);
+    pq.store(sQ, LDK, L, tid);
+    pd.store(sD, LDD, L, tid);
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
+      const float f = r < L ? -pl[j] * __builtin_amdgcn_rcpf(seg_pos(t0 + r, a.pos_off)) : 0.f;
+      bf16x4 hh, ll;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf16 x, y;
+        split2(f * pd.v[j][e], x, y);
+        hh[e] = x;
+        ll[e] = y;
+      }
+      *(bf16x4*)(sZh + r * LDK + cc) = hh;
+      *(bf16x4*)(sZl + r * LDK + cc) = ll;
+    }
+    if (tid < SB) {
+      const bool ok = tid < L;
+      sLam[tid] = ok ? plam : 0.f;
+      sF[tid] = ok ? -plam * __builtin_amdgcn_rcpf(seg_pos(t0 + tid, a.pos_off)) : 0.f;
+    }
+  };
+  load(u.cb);
+  stage(u.cb);
+  __syncthreads();
+
+  for (int c = u.cb; c < u.ce; ++c) {
+    const int L = chunk_len(c), t0 = c * SB;
+    if (c + 1 < u.ce) load(c + 1);
+    bf16x8 kcol[2];
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) kcol[ss] = frag16_tr(sK + 32 * ss * LDK + c0, LDK);
+
+    // ---- 1: score tiles (e < 10: A, else B) and s_t
+#pragma unroll
+    for (int j = 0; j < (20 + NW - 1) / NW; ++j) {
+      const int e = w + j * NW;
+      if (e < 20) {
+        const int ee = e < 10 ? e : e - 10, I = tile_t(ee), J = tile_s(ee);
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (e < 10) {
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks)
+            acc = mfma16(frag16_rm(sK + 16 * J * LDK + 32 * ks, LDK), frag16_rm(sQ + 16 * I * LDK + 32 * ks, LDK), acc);
+        } else {
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            const bf16x8 kf = frag16_rm(sK + 16 * J * LDK + 32 * ks, LDK);
+            acc = mfma16(kf, frag16_rm(sZh + 16 * I * LDK + 32 * ks, LDK), acc);
+            acc = mfma16(kf, frag16_rm(sZl + 16 * I * LDK + 32 * ks, LDK), acc);
+          }
+        }
+        if (I == J) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (g4 + i > (l & 15)) acc[i] = 0.f;
+        }
+        if (e < 10) acc16_to_lds_t(acc, sAh + 16 * I * LDA, sAl + 16 * I * LDA, LDA, 16 * J);
+        else acc16_to_lds_t(acc, sBh + 16 * I * LDA, sBl + 16 * I * LDA, LDA, 16 * J);
+      }
+    }
+    if (MEAN && w >= NW - 4) {
+      const int tt = w - (NW - 4), tb = 16 * tt + g4;
+      f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const bf16x8 qf = frag16_rm(sQ + 16 * tt * LDK + 32 * ks, LDK);
+        sv = mfma16(qf, frag16_rm(sMW + 32 * ks, 0), sv);
+        sv = mfma16(qf, frag16_rm(sMW + LDK + 32 * ks, 0), sv);
+      }
+      if ((l & 15) == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sS[tb + i] = sv[i];
+      }
+    }
+    __syncthreads();
+    if (MEAN) {
+      if (w >= NW - 4) {
+        const int tt = w - (NW - 4), tb = 16 * tt + g4;
+        f32x4 rsum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) {
+          if (ss <= (tt >> 1)) {
+            rsum = mfma16(frag16_rm(sAh + 16 * tt * LDA + 32 * ss, LDA), ones8_(), rsum);
+            rsum = mfma16(frag16_rm(sAl + 16 * tt * LDA + 32 * ss, LDA), ones8_(), rsum);
+          }
+        }
+        if ((l & 15) == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sS[tb + i] += rsum[i];
+        }
+      }
+      __syncthreads();
+    }
+
+    // ---- 2: per wave, one 16-row tile at a time
+#pragma unroll 1
+    for (int tt = 0; tt < 4; ++tt) {
+      f32x4 zh = f32x4{0.f, 0.f, 0.f, 0.f}, zl = f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 wh = f32x4{0.f, 0.f, 0.f, 0.f}, wl = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        bf16x8 chh, chl;
+        acc_pair_split(C[2 * ks], C[2 * ks + 1], chh, chl);
+        const bf16x8 qa = frag16_rm_acc(sQ + 16 * tt * LDK + 32 * ks, LDK);
+        const bf16x8 da = frag16_rm_acc(sZh + 16 * tt * LDK + 32 * ks, LDK);
+        const bf16x8 dl = frag16_rm_acc(sZl + 16 * tt * LDK + 32 * ks, LDK);
+        zh = mfma16(qa, chh, zh);
+        zl = mfma16(qa, chl, zl);
+        wh = mfma16(da, chh, wh);
+        wl = mfma16(dl, chh, wl);
+        wl = mfma16(da, chl, wl);
+      }
+      f32x4 cum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss) {
+        if (ss <= (tt >> 1)) {
+          zh = mfma16(frag16_rm(sAh + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zh);
+          zl = mfma16(frag16_rm(sAl + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zl);
+          wh = mfma16(frag16_rm(sBh + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], wh);
+          wl = mfma16(frag16_rm(sBl + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], wl);
+          if (MEAN) cum = mfma16(tril16(tt, ss), kcol[ss], cum);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * tt + g4 + i;
+        const float ip = __builtin_amdgcn_rcpf(seg_pos(t0 + t, a.pos_off));
+        float* pd_ = sD + t * LDD + col;
+        const float dqc = *pd_;
+        const float mt = mcol + cum[i];
+        float corr = (zh[i] + zl[i]) * ip;
+        if (MEAN) corr -= sS[t] * ip * ip * mt;
+        const float p1 = row16_sum(dqc * corr);
+        const float p2 = MEAN ? row16_sum(dqc * mt) : 0.f;
+        *pd_ = dqc + (wh[i] + wl[i]);
+        if ((l & 15) == 0) {
+          sPart[w][0][t] = p1;
+          if (MEAN) sPart[w][1][t] = p2;
+        }
+      }
+    }
+    __syncthreads();
+    // ---- 3: row totals
+    if (tid < 2 * SB) {
+      const int q = tid / SB, t = tid % SB;
+      if (q == 0 || MEAN) {
+        float s = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) s += sPart[ww][q][t];
+        sTot[q][t] = s;
+      }
+    }
+    __syncthreads();
+
+    // ---- 4: dq, per-token scalars, gate partials, state update
+    float gsum = 0.f, dbsum = 0.f;
+    f32x4 cum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int tt = 0; tt < 4; ++tt) {
+      cum = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (MEAN) {
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss)
+          if (ss <= (tt >> 1)) cum = mfma16(tril16(tt, ss), kcol[ss], cum);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * tt + g4 + i;
+        const float ip = __builtin_amdgcn_rcpf(seg_pos(t0 + t, a.pos_off));
+        const float lam = sLam[t];
+        const float dlam = t < L ? -sTot[0][t] : 0.f;
+        const float ds = MEAN ? lam * sTot[1][t] * ip * ip : 0.f;
+        const float dlogit = dlam * lam * (1.f - lam);
+        float* pd_ = sD + t * LDD + col;
+        float dq = *pd_ + ds * (mcol + cum[i]);
+        if (GATE) {
+          dq += dlogit * sGw[col];
+          gsum += dlogit * (float)sQ[t * LDK + col];
+          dbsum += dlogit;
+        }
+        *pd_ = dq;
+        if (w == 0 && (l & 15) == 0 && t < L) {
+          const long ti = (u.bos + t0 + t) * a.H + u.h;
+          *(f32x4*)(a.sc + ti * 4) = f32x4{sF[t], ds, GATE ? dlogit : dlam, MEAN ? -sS[t] * ip : 0.f};
+          if (!GATE && a.dlam) a.dlam[ti] = dlam;
+        }
+      }
+    }
+    if (GATE) {
+      // column sums over the chunk's rows: one column's lanes across the four lane groups
+      gsum += __shfl_xor(gsum, 16);
+      gsum += __shfl_xor(gsum, 32);
+      const long gi = (long)(u.gc0 + c) * a.H + u.h;
+      if (l < 16) a.dw_part[gi * K + col] = gsum;
+      if (w == 0) {
+        // the 16 lanes of a group hold the same rows: one lane per group counts them
+        float d = (l & 15) == 0 ? dbsum : 0.f;
+        d += __shfl_xor(d, 16);
+        d += __shfl_xor(d, 32);
+        if (l == 0) a.db_part[gi] = d;
+      }
+    }
+    if (MEAN) mcol += __shfl(cum[3], 48 + (l & 15));
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss)
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) C[kt] = mfma16(frag16_tr(sK + 32 * ss * LDK + 16 * kt, LDK), kcol[ss], C[kt]);
+    __syncthreads();
+
+    // ---- 5: dq rows out; chunk c+1 in (same thread-piece mapping for sD)
+    store_rows<K, NT>(sD, LDD, a.dq32, (bf16*)a.dq, nullptr, u.hb + (long)t0 * u.rs, u.rs, L, tid);
+    if (MEAN) put_m();
+    if (c + 1 < u.ce) stage(c + 1);
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
+// cs_gsum: grid N*H*nseg, K/16 waves.  segG = sum over the segment of Q^T dZ (dZ = diag(f) dQc),
+// segDM = sum of dm_t = -(s_t/pos_t) dz_t + ds_t q_t (every workgroup writes, zero when empty).
+// ===========================================================================
+template <int K, bool MEAN>
+__global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
+  constexpr int NW = K / 16, NT = 64 * NW, LDK = K + 16, NKT = K / 16, VPR = K / 4;
+  __shared__ __attribute__((aligned(16))) bf16 sQ[SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDK];
+  __shared__ __attribute__((aligned(16))) float sDs[SB], sSp[SB];
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const SegUnit u = seg_unit<K>(a);
+  const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
+  auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
+  f32x4 G[NKT];
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) G[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float dmc = 0.f;
+  RowsBf16<K, SB, NT> pq;
+  RowsF32<K, SB, NT> pd;
+  constexpr int ND = RowsF32<K, SB, NT>::N;
+  float pf[ND];
+  f32x4 psc = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto load = [&](int c) {
+    const int L = chunk_len(c);
+    const long off = u.hb + (long)c * SB * u.rs, tb = u.bos + (long)c * SB;
+    pq.load((const bf16*)a.q + off, u.rs, L, tid);
+    pd.load(a.dqc32 ? a.dqc32 + off : nullptr, a.dqc32 ? nullptr : (const bf16*)a.dqc16 + off, u.rs, L, tid);
+#pragma unroll
+    for (int j = 0; j < ND; ++j) pf[j] = a.sc[((tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h) * 4];
+    if (tid < SB) psc = *(const f32x4*)(a.sc + ((tb + min(tid, L - 1)) * a.H + u.h) * 4);
+  };
+  auto stage = [&](int c) {
+    const int L = chunk_len(c);
+    pq.store(sQ, LDK, L, tid);
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
+      const float f = r < L ? pf[j] : 0.f;
+      bf16x4 hh, ll;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf16 x, y;
+        split2(f * pd.v[j][e], x, y);
+        hh[e] = x;
+        ll[e] = y;
+      }
+      *(bf16x4*)(sZh + r * LDK + cc) = hh;
+      *(bf16x4*)(sZl + r * LDK + cc) = ll;
+    }
+    if (tid < SB) {
+      sDs[tid] = tid < L ? psc[1] : 0.f;
+      sSp[tid] = tid < L ? psc[3] : 0.f;
+    }
+  };
+  if (u.cb < u.ce) {
+    load(u.cb);
+    stage(u.cb);
+  }
+  __syncthreads();
+  for (int c = u.cb; c < u.ce; ++c) {
+    if (c + 1 < u.ce) load(c + 1);
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) {
+      const bf16x8 bh = frag16_tr(sZh + 32 * ss * LDK + c0, LDK), bl = frag16_tr(sZl + 32 * ss * LDK + c0, LDK);
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) {
+        const bf16x8 qa = frag16_tr(sQ + 32 * ss * LDK + 16 * kt, LDK);
+        G[kt] = mfma16(qa, bh, G[kt]);
+        G[kt] = mfma16(qa, bl, G[kt]);
+      }
+    }
+    if (MEAN) {
+      // column sums of dm over the chunk: lane group g takes rows g, g + 4, ...
+#pragma unroll 4
+      for (int r = (l >> 4); r < SB; r += 4) {
+        const int e = r * LDK + col;
+        dmc += sSp[r] * ((float)sZh[e] + (float)sZl[e]) + sDs[r] * (float)sQ[e];
+      }
+    }
+    __syncthreads();
+    if (c + 1 < u.ce) stage(c + 1);
+    __syncthreads();
+  }
+  float* dst = a.segG + ((long)u.unit * a.nseg + u.seg) * K * K;
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[(long)(16 * kt + g4 + r) * K + col] = G[kt][r];
+  if (MEAN) {
+    dmc += __shfl_xor(dmc, 16);
+    dmc += __shfl_xor(dmc, 32);
+    if (l < 16) a.segDM[((long)u.unit * a.nseg + u.seg) * K + col] = dmc;
+  }
+}
+
+// ===========================================================================
+// cs_dk: grid N*H*nseg, K/16 waves, reverse walk of one segment.  State E[:, cols] (E = G + G^T +
+// dC_T + dC_T^T over the chunks after the current one) and the dm carry start from the later
+// segments' totals.  Per chunk (rows j, t of the chunk):
+//   dK[:, cols] = K E[:, cols] + ((dZ K^T) o M)^T Q[:, cols] + ((Q K^T) o M)^T dZ[:, cols]
+//                + sum_{t >= j} dm_t[cols] + carry[cols]     (+ dk_extra at the store)
+//   E[:, cols] += Q^T dZ[:, cols] + dZ^T Q[:, cols];  carry += sum_t dm_t[cols]
+// The dm suffix sums are two masked products: (t >= j ? ds_t : 0) against Q and (t >= j ?
+// -s_t/pos_t : 0) against dZ.  Segment 0 also writes dC_0 = dC_T + sum_t q_t dz_t^T and dm_0.
+// ===========================================================================
+template <int K, bool MEAN>
+__global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
+  constexpr int NW = K / 16, NT = 64 * NW;
+  constexpr int LDK = K + 16, LDA = SB + 16, LDO = K + 4;
+  constexpr int NKS = K / 32, NKT = K / 16, VPR = K / 4;
+  __shared__ __attribute__((aligned(16))) bf16 sQ[SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sK[SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sAh[SB * LDA];   // (Q K^T) o M
+  __shared__ __attribute__((aligned(16))) bf16 sAl[SB * LDA];
+  __shared__ __attribute__((aligned(16))) bf16 sBh[SB * LDA];   // (dZ K^T) o M
+  __shared__ __attribute__((aligned(16))) bf16 sBl[SB * LDA];
+  __shared__ __attribute__((aligned(16))) float sO[SB * LDO];   // dk rows
+  __shared__ __attribute__((aligned(16))) float sDs[SB], sSp[SB];
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
+  const SegUnit u = seg_unit<K>(a);
+  const bool first = u.seg == 0;
+  if (u.cb >= u.ce && !first) return;
+  const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
+  auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
+
+  // E at the end of the segment: later segments' G + G^T, plus dC_T + dC_T^T
+  f32x4 E[NKT];
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) {
+    E[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (a.dh_fin) {
+      const float* p = a.dh_fin + (long)u.unit * K * K;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) E[kt][i] = p[(long)(16 * kt + g4 + i) * K + col];
+      E[kt] += *(const f32x4*)(p + (long)col * K + 16 * kt + g4);
+    }
+  }
+  add_seg_tiles<K, true>(E, a.segG, u.unit, a.nseg, u.seg + 1, a.nseg, col, g4);
+  float carry = 0.f;
+  if (MEAN) {
+    carry = a.dm_fin ? a.dm_fin[(long)u.unit * K + col] : 0.f;
+    for (int s = u.seg + 1; s < a.nseg; ++s) carry += a.segDM[((long)u.unit * a.nseg + s) * K + col];
+  }
+  for (int i = tid; i < SB * LDA; i += NT) {
+    sAh[i] = (bf16)0.f;
+    sAl[i] = (bf16)0.f;
+    sBh[i] = (bf16)0.f;
+    sBl[i] = (bf16)0.f;
+  }
+
+  RowsBf16<K, SB, NT> pq, pk;
+  RowsF32<K, SB, NT> pd;
+  constexpr int ND = RowsF32<K, SB, NT>::N;
+  float pf[ND];
+  f32x4 psc = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto load = [&](int c) {
+    const int L = chunk_len(c);
+    const long off = u.hb + (long)c * SB * u.rs, tb = u.bos + (long)c * SB;
+    pk.load((const bf16*)a.k + off, u.rs, L, tid);
+    pq.load((const bf16*)a.q + off, u.rs, L, tid);
+    pd.load(a.dqc32 ? a.dqc32 + off : nullptr, a.dqc32 ? nullptr : (const bf16*)a.dqc16 + off, u.rs, L, tid);
+#pragma unroll
+    for (int j = 0; j < ND; ++j) pf[j] = a.sc[((tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h) * 4];
+    if (tid < SB) psc = *(const f32x4*)(a.sc + ((tb + min(tid, L - 1)) * a.H + u.h) * 4);
+  };
+  auto stage = [&](int c) {
+    const int L = chunk_len(c);
+    pk.store(sK, LDK, L, tid);
+    pq.store(sQ, LDK, L, tid);
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
+      const float f = r < L ? pf[j] : 0.f;
+      bf16x4 hh, ll;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf16 x, y;
+        split2(f * pd.v[j][e], x, y);
+        hh[e] = x;
+        ll[e] = y;
+      }
+      *(bf16x4*)(sZh + r * LDK + cc) = hh;
+      *(bf16x4*)(sZl + r * LDK + cc) = ll;
+    }
+    if (tid < SB) {
+      sDs[tid] = tid < L ? psc[1] : 0.f;
+      sSp[tid] = tid < L ? psc[3] : 0.f;
+    }
+  };
+  if (u.cb < u.ce) {
+    load(u.ce - 1);
+    stage(u.ce - 1);
+  }
+  __syncthreads();
+
+  for (int c = u.ce - 1; c >= u.cb; --c) {
+    const int L = chunk_len(c), t0 = c * SB;
+    if (c - 1 >= u.cb) load(c - 1);
+    // ---- scores (e < 10: A = (Q K^T) o M, else B = (dZ K^T) o M)
+#pragma unroll
+    for (int j = 0; j < (20 + NW - 1) / NW; ++j) {
+      const int e = w + j * NW;
+      if (e < 20) {
+        const int ee = e < 10 ? e : e - 10, I = tile_t(ee), J = tile_s(ee);
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (e < 10) {
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks)
+            acc = mfma16(frag16_rm(sK + 16 * J * LDK + 32 * ks, LDK), frag16_rm(sQ + 16 * I * LDK + 32 * ks, LDK), acc);
+        } else {
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            const bf16x8 kf = frag16_rm(sK + 16 * J * LDK + 32 * ks, LDK);
+            acc = mfma16(kf, frag16_rm(sZh + 16 * I * LDK + 32 * ks, LDK), acc);
+            acc = mfma16(kf, frag16_rm(sZl + 16 * I * LDK + 32 * ks, LDK), acc);
+          }
+        }
+        if (I == J) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (g4 + i > (l & 15)) acc[i] = 0.f;
+        }
+        if (e < 10) acc16_to_lds_t(acc, sAh + 16 * I * LDA, sAl + 16 * I * LDA, LDA, 16 * J);
+        else acc16_to_lds_t(acc, sBh + 16 * I * LDA, sBl + 16 * I * LDA, LDA, 16 * J);
+      }
+    }
+    __syncthreads();
+
+    // ---- dK rows, one 16-row tile (jt) at a time; the dm total of the chunk (row 0 of the suffix)
+    bf16x8 qcol[2], zcolh[2], zcoll[2];
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts) {
+      qcol[ts] = frag16_tr(sQ + 32 * ts * LDK + c0, LDK);
+      zcolh[ts] = frag16_tr(sZh + 32 * ts * LDK + c0, LDK);
+      zcoll[ts] = frag16_tr(sZl + 32 * ts * LDK + c0, LDK);
+    }
+    float dmtot = 0.f;
+#pragma unroll 1
+    for (int jt = 0; jt < 4; ++jt) {
+      f32x4 xh = f32x4{0.f, 0.f, 0.f, 0.f}, xl = f32x4{0.f, 0.f, 0.f, 0.f}, sfx = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        bf16x8 eh, el;
+        acc_pair_split(E[2 * ks], E[2 * ks + 1], eh, el);
+        const bf16x8 ka = frag16_rm_acc(sK + 16 * jt * LDK + 32 * ks, LDK);
+        xh = mfma16(ka, eh, xh);
+        xl = mfma16(ka, el, xl);
+      }
+#pragma unroll
+      for (int ts = 0; ts < 2; ++ts) {
+        if (ts >= (jt >> 1)) {
+          // B^T Q and A^T dZ: rows j of the transposed score tiles (transposing reads of [t][j])
+          const bf16x8 bth = frag16_tr(sBh + 32 * ts * LDA + 16 * jt, LDA);
+          const bf16x8 btl = frag16_tr(sBl + 32 * ts * LDA + 16 * jt, LDA);
+          const bf16x8 ath = frag16_tr(sAh + 32 * ts * LDA + 16 * jt, LDA);
+          const bf16x8 atl = frag16_tr(sAl + 32 * ts * LDA + 16 * jt, LDA);
+          xh = mfma16(bth, qcol[ts], xh);
+          xl = mfma16(btl, qcol[ts], xl);
+          xh = mfma16(ath, zcolh[ts], xh);
+          xl = mfma16(atl, zcolh[ts], xl);
+          xl = mfma16(ath, zcoll[ts], xl);
+          if (MEAN) {
+            // masked diagonals: row j = 16 jt + (l & 15), slots t = 32 ts + 8 (l >> 4) + i
+            const int tb = 32 * ts + 8 * (l >> 4), jr = 16 * jt + (l & 15);
+            const f32x4 d0 = *(const f32x4*)(sDs + tb), d1 = *(const f32x4*)(sDs + tb + 4);
+            const f32x4 p0 = *(const f32x4*)(sSp + tb), p1 = *(const f32x4*)(sSp + tb + 4);
+            bf16x8 dh, dl, ph, pl;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const bool keep = tb + i >= jr;
+              bf16 a1, a2, a3, a4;
+              split2(keep ? (i < 4 ? d0[i] : d1[i - 4]) : 0.f, a1, a2);
+              split2(keep ? (i < 4 ? p0[i] : p1[i - 4]) : 0.f, a3, a4);
+              dh[i] = a1;
+              dl[i] = a2;
+              ph[i] = a3;
+              pl[i] = a4;
+            }
+            sfx = mfma16(dh, qcol[ts], sfx);
+            sfx = mfma16(dl, qcol[ts], sfx);
+            sfx = mfma16(ph, zcolh[ts], sfx);
+            sfx = mfma16(ph, zcoll[ts], sfx);
+            sfx = mfma16(pl, zcolh[ts], sfx);
+          }
+        }
+      }
+      if (MEAN && jt == 0) dmtot = __shfl(sfx[0], l & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sO[(16 * jt + g4 + i) * LDO + col] = xh[i] + xl[i] + sfx[i] + carry;
+    }
+    if (MEAN) carry += dmtot;
+
+    // ---- E[:, cols] += Q^T dZ[:, cols] + dZ^T Q[:, cols]
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) {
+        const bf16x8 qa = frag16_tr(sQ + 32 * ts * LDK + 16 * kt, LDK);
+        const bf16x8 za = frag16_tr(sZh + 32 * ts * LDK + 16 * kt, LDK);
+        const bf16x8 zb = frag16_tr(sZl + 32 * ts * LDK + 16 * kt, LDK);
+        E[kt] = mfma16(qa, zcolh[ts], E[kt]);
+        E[kt] = mfma16(qa, zcoll[ts], E[kt]);
+        E[kt] = mfma16(za, qcol[ts], E[kt]);
+        E[kt] = mfma16(zb, qcol[ts], E[kt]);
+      }
+    __syncthreads();
+    store_rows<K, NT>(sO, LDO, a.dk32, (bf16*)a.dk, a.dk_extra, u.hb + (long)t0 * u.rs, u.rs, L, tid);
+    if (c - 1 >= u.cb) stage(c - 1);
+    __syncthreads();
+  }
+
+  if (first) {
+    if (a.dh0) {
+      f32x4 D[NKT];
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          D[kt][i] = a.dh_fin ? a.dh_fin[((long)u.unit * K + 16 * kt + g4 + i) * K + col] : 0.f;
+      }
+      add_seg_tiles<K, false>(D, a.segG, u.unit, a.nseg, 0, a.nseg, col, g4);
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a.dh0[((long)u.unit * K + 16 * kt + g4 + i) * K + col] = D[kt][i];
+    }
+    if (MEAN && a.dm0 && l < 16) a.dm0[(long)u.unit * K + col] = carry;
+  }
+}
+
+// ===========================================================================
+// launchers
+// ===========================================================================
+namespace {
+
+int seg_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cache[dev] <= 0) {
+    int nn = 0;
+    if (hipDeviceGetAttribute(&nn, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || nn <= 0) nn = 256;
+    cache[dev] = nn;
+  }
+  return cache[dev];
+}
+
+template <int K>
+hipError_t cseg_k(int stage, const WalkArgs& a, hipStream_t st) {
+  const long wgs = (long)a.N * a.H * a.nseg;
+  if (wgs <= 0) return hipSuccess;
+  const dim3 grid((unsigned)wgs), block(K * 4);
+  const bool mean = a.subtract_mean != 0, gate = a.gate_w != nullptr;
+  switch (stage) {
+    case kSegSum:
+      hipLaunchKernelGGL(cs_sum_kernel<K>, grid, block, 0, st, a);
+      break;
+    case kSegFwd:
+      if (mean && gate) hipLaunchKernelGGL((cs_fwd_kernel<K, true, true>), grid, block, 0, st, a);
+      else if (mean) hipLaunchKernelGGL((cs_fwd_kernel<K, true, false>), grid, block, 0, st, a);
+      else if (gate) hipLaunchKernelGGL((cs_fwd_kernel<K, false, true>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((cs_fwd_kernel<K, false, false>), grid, block, 0, st, a);
+      break;
+    case kSegDq:
+      if (mean && gate) hipLaunchKernelGGL((cs_dq_kernel<K, true, true>), grid, block, 0, st, a);
+      else if (mean) hipLaunchKernelGGL((cs_dq_kernel<K, true, false>), grid, block, 0, st, a);
+      else if (gate) hipLaunchKernelGGL((cs_dq_kernel<K, false, true>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((cs_dq_kernel<K, false, false>), grid, block, 0, st, a);
+      break;
+    case kSegGsum:
+      if (mean) hipLaunchKernelGGL((cs_gsum_kernel<K, true>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((cs_gsum_kernel<K, false>), grid, block, 0, st, a);
+      break;
+    case kSegDk:
+      if (mean) hipLaunchKernelGGL((cs_dk_kernel<K, true>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((cs_dk_kernel<K, false>), grid, block, 0, st, a);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Segments per sequence: enough workgroups to cover the CUs, at least two chunks per segment
+// (T: the dense length, or the packed length of a varlen batch).
+int cseg_count(int N, int H, int T) {
+  const long units = (long)N * H;
+  if (units <= 0) return 1;
+  const int chunks = (T + SB - 1) / SB;
+  int nseg = (int)((seg_cu_count() + units - 1) / units);
+  nseg = min(nseg, max(1, chunks / 2));
+  return max(1, min(nseg, 16));
+}
+
+bool cseg_supported(int K) { return K == 64 || K == 128; }
+
+hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st) {
+  switch (a.K) {
+    case 64: return cseg_k<64>(stage, a, st);
+    case 128: return cseg_k<128>(stage, a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ccq

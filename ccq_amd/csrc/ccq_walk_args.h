@@ -54,10 +54,18 @@ struct WalkArgs {
   void* dzl;                // bf16 [tokens, H, K] low part
   float* dh0;               // fp32 [N, H, K, K] (nullable)
   float* dm0;               // fp32 [N, H, K] (nullable)
+  // segment walks (K in {64, 128}): per (sequence, head, segment) totals
+  float* segD;              // saved: fp32 [N*H, nseg, K, K] sum of k k^T over the segment
+  float* segM;              // saved: fp32 [N*H, nseg, K] sum of k over the segment
+  float* segG;              // workspace: fp32 [N*H, nseg, K, K] sum of q dz^T over the segment
+  float* segDM;             // workspace: fp32 [N*H, nseg, K] sum of dm over the segment
   int T, H, N, NT, NTG, K, pos_off, subtract_mean;
+  int nseg;                 // time segments per sequence of the segment walks
 };
 
 // stages of launch_cwalk
 enum WalkStage { kWalkFwd = 0, kWalkRows, kWalkDq, kWalkDk };
+// stages of launch_cseg (segment walks, K in {64, 128})
+enum SegStage { kSegSum = 0, kSegFwd, kSegDq, kSegGsum, kSegDk };
 
 }  // namespace ccq

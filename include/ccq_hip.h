@@ -240,8 +240,9 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
 /*
  * Kernel timing (measurement facility; no counterpart in the reference).  While enabled, each
  * entry point records a HIP event pair around every launch of its kernels on the caller's
- * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: clean_fwd,
- * clean_bwd_rows, clean_bwd_dq, clean_bwd_dk, clean_bwd_gate, gdn_prep, gdn_fwd_state, gdn_fwd_o,
+ * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: clean_fwd_sum,
+ * clean_fwd, clean_bwd_rows, clean_bwd_dq, clean_bwd_gsum, clean_bwd_dk, clean_bwd_gate, gdn_prep,
+ * gdn_fwd_state, gdn_fwd_o,
  * gdn_bwd_state, gdn_bwd_dqkw, gdn_bwd_wy, gla_intra, gla_fwd_state, gla_fwd_o, gla_bwd_state,
  * gla_bwd_dv, gla_bwd_dqk, gla_bwd_gk, clean_z_fwd, clean_z_bwd) and returns the summed
  * milliseconds and the number of launches since the last ccq_timing_reset.

@@ -108,17 +108,26 @@ def test_workspace_sizes_are_consistent(K, V):
     expect = tokens * H * 4 + nt * H * 4096 * 4 + 2 * tokens * H * K * 2 + tokens * H * V * 4 \
         + 2 * nt * H * V * K * 2 + tokens * H * V * 4 + nt * H * 4096 * 4
     assert expect <= saved <= expect + 8 * 256
-    # cleaning walks: saved = z (fp32 per token) + s_t + key sum before each chunk; workspace = four
-    # fp32 row scalars per token + per-chunk column sums of dm (+ gate partials) (+ dz as a bf16 hi/lo
-    # pair for K in {64, 128}); no K x K state is stored
-    cb = 32 if K > 128 else 64
-    nc = tokens // cb
     csaved = lib.ccq_clean_saved_bytes(tokens, 1, tokens, 1, H, K, 0)
-    cexpect = tokens * H * K * 4 + tokens * H * 4 + nc * H * K * 4
-    assert cexpect <= csaved <= cexpect + 3 * 256
     ws = lib.ccq_clean_bwd_workspace_bytes(tokens, 1, tokens, 1, H, K, 0, 0)
-    wexpect = tokens * H * 16 + nc * H * K * 4 + (tokens * H * K * 4 if K in (64, 128) else 0)
-    assert wexpect <= ws <= wexpect + 4 * 256
+    if K in (64, 128):
+        # segment walks: saved = per-segment sums of k k^T and k; workspace = four fp32 row scalars
+        # per token + per-segment sums of q dz^T and dm.  The segment count (1..16, at least two
+        # chunks each) depends on the device's CU count; no per-token tensor is saved
+        per_seg = H * (K * K + K) * 4
+        nseg = [n for n in range(1, 17) if n * per_seg <= csaved <= n * per_seg + 2 * 256]
+        assert len(nseg) == 1
+        wexpect = tokens * H * 16 + nseg[0] * per_seg
+        assert wexpect <= ws <= wexpect + 3 * 256
+    else:
+        # column walks: saved = z (fp32 per token) + s_t + key sum before each chunk; workspace = four
+        # fp32 row scalars per token + per-chunk column sums of dm (+ gate partials)
+        cb = 32 if K > 128 else 64
+        nc = tokens // cb
+        cexpect = tokens * H * K * 4 + tokens * H * 4 + nc * H * K * 4
+        assert cexpect <= csaved <= cexpect + 3 * 256
+        wexpect = tokens * H * 16 + nc * H * K * 4
+        assert wexpect <= ws <= wexpect + 4 * 256
     assert lib.ccq_clean_bwd_workspace_bytes(tokens, 1, tokens, 1, H, K, 0, 1) > ws
     assert lib.ccq_clean_saved_bytes(tokens, 1, tokens, 3, H, K, 1) > csaved  # varlen adds the indexes
 
