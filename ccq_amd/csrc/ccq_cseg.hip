@@ -63,19 +63,36 @@ __device__ __forceinline__ bf16x8 frag16_rm_acc(const bf16* p, int ld) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Two fp32 values as packed bf16 hi/lo pairs: hi = the upper 16 bits (truncation), lo = the rest
+// rounded to bf16.  hi + lo keeps ~16 significant bits; six VALU operations per pair.
+__device__ __forceinline__ void split_pair(float x0, float x1, unsigned& hi, unsigned& lo) {
+  const unsigned b0 = __builtin_bit_cast(unsigned, x0), b1 = __builtin_bit_cast(unsigned, x1);
+  hi = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+  const float r0 = x0 - __builtin_bit_cast(float, b0 & 0xffff0000u);
+  const float r1 = x1 - __builtin_bit_cast(float, b1 & 0xffff0000u);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  lo = __builtin_bit_cast(unsigned, bf16x2_t{(bf16)r0, (bf16)r1});
+}
+
 // B operand (hi/lo) of a 32-deep contraction step from two accumulator tiles holding rows
 // [k0, k0 + 16) and [k0 + 16, k0 + 32): slot order of frag16_rm_acc.
 __device__ __forceinline__ void acc_pair_split(const f32x4& t0, const f32x4& t1, bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    bf16 a, b;
-    split2(t0[i], a, b);
-    hi[i] = a;
-    lo[i] = b;
-    split2(t1[i], a, b);
-    hi[4 + i] = a;
-    lo[4 + i] = b;
-  }
+  unsigned h0, h1, h2, h3, o0, o1, o2, o3;
+  split_pair(t0[0], t0[1], h0, o0);
+  split_pair(t0[2], t0[3], h1, o1);
+  split_pair(t1[0], t1[1], h2, o2);
+  split_pair(t1[2], t1[3], h3, o3);
+  hi = __builtin_bit_cast(bf16x8, u32x4{h0, h1, h2, h3});
+  lo = __builtin_bit_cast(bf16x8, u32x4{o0, o1, o2, o3});
+}
+
+// Four fp32 values as packed hi/lo bf16x4 (for staged rows).
+__device__ __forceinline__ void split4(const f32x4& v, bf16x4& hi, bf16x4& lo) {
+  unsigned h0, h1, o0, o1;
+  split_pair(v[0], v[1], h0, o0);
+  split_pair(v[2], v[3], h1, o1);
+  hi = __builtin_bit_cast(bf16x4, u32x2{h0, h1});
+  lo = __builtin_bit_cast(bf16x4, u32x2{o0, o1});
 }
 
 // Lower-triangular (inclusive) ones as the A operand of mfma16: row t = 16 tt + lane % 16,
@@ -87,6 +104,27 @@ __device__ __forceinline__ bf16x8 tril16(int tt, int ss) {
   for (int j = 0; j < 8; ++j) v[j] = (s + j <= t) ? (bf16)1.f : (bf16)0.f;
   return v;
 }
+
+// The lower-triangular ones fragments a (row tile tt, contraction step ss) pair needs: all ones
+// below the diagonal block, tril16(0, 0) for even tt and tril16(1, 0) for odd tt on it (the
+// diagonal pattern repeats every 32 rows).
+struct Tril {
+  bf16x8 even, odd, ones;
+  __device__ __forceinline__ void init() {
+    even = tril16(0, 0);
+    odd = tril16(1, 0);
+    ones = ones8_();
+  }
+  __device__ __forceinline__ bf16x8 at(int tt, int ss) const {
+    // selects between values (a conditional between the members would take their addresses)
+    const u32x4 e = __builtin_bit_cast(u32x4, even), o = __builtin_bit_cast(u32x4, odd);
+    const u32x4 n = __builtin_bit_cast(u32x4, ones);
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = ss < (tt >> 1) ? n[i] : ((tt & 1) ? o[i] : e[i]);
+    return __builtin_bit_cast(bf16x8, r);
+  }
+};
 
 // Causal score tile e (0..9) as (t tile, s tile): (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) ...
 __device__ __forceinline__ int tile_t(int e) { return e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3; }
@@ -105,6 +143,15 @@ __device__ __forceinline__ float row16_sum(float x) {
   x += dppf<0x141>(x);
   x += dppf<0x140>(x);
   return x;
+}
+
+// Marks a value loaded from HBM as settled: the empty asm consumes it (the load's wait is placed
+// here, before the chunk loop) and yields a register value of its own.  Without it, a loop-carried
+// value first loaded before the loop keeps the loop's wait analysis pessimistic: a full wait for
+// every outstanding load and store at its first use in every pass.
+template <typename T>
+__device__ __forceinline__ void settle(T& x) {
+  asm volatile("" : "+v"(x));
 }
 
 // One segment of one (sequence, head): chunks [cb, ce) of the sequence's nc chunks.
@@ -130,25 +177,65 @@ __device__ __forceinline__ SegUnit seg_unit(const WalkArgs& a) {
   return u;
 }
 
-// fp32 rows staged in LDS (ld elements apart) to HBM as fp32 and/or bf16, with an optional fp32
-// addend read from HBM; rows at or beyond L are skipped.  Thread piece mapping of RowsF32<K, SB, NT>.
+// Buffer resource over rows [0, L) of a token-major tensor (row stride rs elements, row_elems
+// elements used per row, esize bytes each) from p: accesses to rows at or beyond L -- or to anything,
+// when p is null -- are dropped by the hardware (stores) or read as zero (loads).  Every thread then
+// issues the same memory operations whatever L is, so the compiler's wait counts follow one fixed
+// sequence and a wait for a load never covers a younger store.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* p, long rs, int L, int row_elems,
+                                                            int esize) {
+  return buf_rsrc(p, (p != nullptr && L > 0) ? (int)(((long)(L - 1) * rs + row_elems) * esize) : 0);
+}
+
+// One thread's pieces of a SB x K fp32 tile in the piece mapping of RowsF32<K, SB, NT> (16 consecutive
+// lanes per 256-byte row segment): read from LDS, written to HBM as fp32 and / or bf16 rows.
 template <int K, int NT>
-__device__ __forceinline__ void store_rows(const float* src, int ld, float* g32, bf16* g16, const float* add32,
-                                           long base, long rs, int L, int tid) {
-  constexpr int VPR = K / 4, TOT = SB * VPR, N = TOT / NT;
-  static_assert(TOT % NT == 0, "whole passes");
+struct TileOut {
+  static constexpr int VPR = K / 4, N = SB * VPR / NT;
+  static_assert((SB * VPR) % NT == 0, "whole passes");
+  f32x4 v[N];
+  __device__ __forceinline__ void read(const float* src, int ld, int tid) {
 #pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const int idx = tid + j * NT, r = idx / VPR, c = (idx % VPR) * 4;
-    if (r < L) {
-      f32x4 v = *(const f32x4*)(src + r * ld + c);
-      const long e = base + (long)r * rs + c;
-      if (add32) v += *gmem((const f32x4*)(add32 + e));
-      if (g32) *gmem((f32x4*)(g32 + e)) = v;
-      if (g16) *gmem((bf16x4*)(g16 + e)) = bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + j * NT;
+      v[j] = *(const f32x4*)(src + (idx / VPR) * ld + (idx % VPR) * 4);
     }
   }
-}
+  __device__ __forceinline__ void store(__amdgpu_buffer_rsrc_t r32, __amdgpu_buffer_rsrc_t r16, long rs,
+                                        int tid) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + j * NT;
+      const int e = (int)((idx / VPR) * rs + (idx % VPR) * 4);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[j]), r32, e * 4, 0, 0);
+      const bf16x4 b = bf16x4{(bf16)v[j][0], (bf16)v[j][1], (bf16)v[j][2], (bf16)v[j][3]};
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, b), r16, e * 2, 0, 0);
+    }
+  }
+};
+
+// fp32 rows of a chunk into registers through a rows_rsrc resource (zero past the chunk or when the
+// tensor is absent), in the piece mapping of TileOut.
+template <int K, int NT>
+struct TileIn {
+  static constexpr int VPR = K / 4, N = SB * VPR / NT;
+  f32x4 v[N];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, long rs, int tid) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + j * NT;
+      const int e = (int)((idx / VPR) * rs + (idx % VPR) * 4);
+      v[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, e * 4, 0, 0));
+    }
+  }
+  __device__ __forceinline__ void store(float* dst, int ld, int tid) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + j * NT;
+      *(f32x4*)(dst + (idx / VPR) * ld + (idx % VPR) * 4) = v[j];
+    }
+  }
+};
 
 // Sum of the segment totals tot[unit][s] for s in [s0, s1) into the lane's accumulator tiles
 // (rows 16 kt + g4 + i, column col), optionally plus the transposed tiles (tot[.][col][k]).
@@ -187,14 +274,19 @@ __global__ __launch_bounds__(K * 4) void cs_sum_kernel(const WalkArgs a) {
   RowsBf16<K, SB, NT> p0, p1;
   auto kptr = [&](int c) { return (const bf16*)a.k + u.hb + (long)c * SB * u.rs; };
   const int nloc = u.ce - u.cb;
-  if (nloc > 0) p0.load(kptr(u.cb), u.rs, chunk_len(u.cb), tid);
-  if (nloc > 1) p1.load(kptr(u.cb + 1), u.rs, chunk_len(u.cb + 1), tid);
-  if (nloc > 0) p0.store(sK[0], LDK, chunk_len(u.cb), tid);
+  // past the end the last chunk is loaded and staged again (into the idle buffer): every pass issues
+  // the same memory operations
+  auto cl = [&](int i) { return min(u.cb + i, u.ce - 1); };
+  if (nloc > 0) {
+    p0.load(kptr(cl(0)), u.rs, chunk_len(cl(0)), tid);
+    p1.load(kptr(cl(1)), u.rs, chunk_len(cl(1)), tid);
+    p0.store(sK[0], LDK, chunk_len(cl(0)), tid);
+  }
   __syncthreads();
   auto step = [&](int i, RowsBf16<K, SB, NT>& cur, RowsBf16<K, SB, NT>& nxt) {
     // chunk cb + i is in buffer i & 1; `cur` is free (staged), `nxt` holds chunk cb + i + 1
     const bf16* Kc = sK[i & 1];
-    if (i + 2 < nloc) cur.load(kptr(u.cb + i + 2), u.rs, chunk_len(u.cb + i + 2), tid);
+    cur.load(kptr(cl(i + 2)), u.rs, chunk_len(cl(i + 2)), tid);
     bf16x8 kcol[2];
 #pragma unroll
     for (int ss = 0; ss < 2; ++ss) kcol[ss] = frag16_tr(Kc + 32 * ss * LDK + c0, LDK);
@@ -206,7 +298,7 @@ __global__ __launch_bounds__(K * 4) void cs_sum_kernel(const WalkArgs a) {
       for (int kt = 0; kt < NKT; ++kt) D[kt] = mfma16(frag16_tr(Kc + 32 * ss * LDK + 16 * kt, LDK), kcol[ss], D[kt]);
     }
     msum += __shfl(tot[3], 48 + (l & 15));
-    if (i + 1 < nloc) nxt.store(sK[(i + 1) & 1], LDK, chunk_len(u.cb + i + 1), tid);
+    nxt.store(sK[(i + 1) & 1], LDK, chunk_len(cl(i + 1)), tid);
     __syncthreads();
   };
   int i = 0;
@@ -244,8 +336,9 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sAl[SB * LDA];
   __shared__ __attribute__((aligned(16))) float sO[SB * LDO];   // q_clean rows
   __shared__ __attribute__((aligned(16))) bf16 sMW[2][4 * LDK];  // rows: m hi, m lo, gate w hi, lo
-  __shared__ __attribute__((aligned(16))) float sS[SB];          // s_t
+  __shared__ __attribute__((aligned(16))) float sS[SB];          // s_t, then s_t / pos_t^2
   __shared__ __attribute__((aligned(16))) float sLam[SB];        // lambda_t
+  __shared__ __attribute__((aligned(16))) float sIp[SB];         // 1 / pos_t
   __shared__ __attribute__((aligned(16))) float sLamIn[2][SB];   // given lambda, by buffer
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
@@ -254,6 +347,8 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
   if (u.cb >= u.ce && !last) return;
   const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
   auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
+  Tril tri;
+  tri.init();
 
   // state at the segment start: h_0 + the earlier segments' K^T K; the lane's column of the key sum
   f32x4 C[NKT];
@@ -267,6 +362,9 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
     mcol = a.m0 ? a.m0[(long)u.unit * K + col] : 0.f;
     for (int s = 0; s < u.seg; ++s) mcol += a.segM[((long)u.unit * a.nseg + s) * K + col];
   }
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) settle(C[kt]);
+  settle(mcol);
 
   // LDS set-up: scores above the diagonal tiles stay zero; gate rows of both buffers; key sums
   for (int i = tid; i < SB * LDA; i += NT) {
@@ -292,31 +390,33 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
 
   RowsBf16<K, SB, NT> pq, pk;
   float plam = 0.f;
+  // chunk loads and stages: unconditional (past the end the last chunk again, into the idle buffer)
   auto load = [&](int c) {
     const int L = chunk_len(c);
     const long off = u.hb + (long)c * SB * u.rs;
     pk.load((const bf16*)a.k + off, u.rs, L, tid);
     pq.load((const bf16*)a.q + off, u.rs, L, tid);
-    if (!GATE && tid < SB) plam = a.lam[(u.bos + (long)c * SB + min(tid, L - 1)) * a.H + u.h];
+    if (!GATE) plam = a.lam[(u.bos + (long)c * SB + min(tid & (SB - 1), L - 1)) * a.H + u.h];
   };
-  auto stage = [&](int c) {
-    const int L = chunk_len(c), b = c & 1;
+  auto stage = [&](int c, int b) {
+    const int L = chunk_len(c);
     pk.store(sK[b], LDK, L, tid);
     pq.store(sQ[b], LDK, L, tid);
     if (!GATE && tid < SB) sLamIn[b][tid] = tid < L ? plam : 0.f;
   };
   if (u.cb < u.ce) {
     load(u.cb);
-    stage(u.cb);
+    stage(u.cb, u.cb & 1);
+    load(min(u.cb + 1, u.ce - 1));
   }
   __syncthreads();
 
-  const float gbias = GATE ? a.gate_b[u.h] : 0.f;
+  float gbias = GATE ? a.gate_b[u.h] : 0.f;
+  settle(gbias);
   for (int c = u.cb; c < u.ce; ++c) {
     const int b = c & 1, L = chunk_len(c), t0 = c * SB;
     const bf16* Qc = sQ[b];
     const bf16* Kc = sK[b];
-    if (c + 1 < u.ce) load(c + 1);
     bf16x8 kcol[2];
 #pragma unroll
     for (int ss = 0; ss < 2; ++ss) kcol[ss] = frag16_tr(Kc + 32 * ss * LDK + c0, LDK);
@@ -364,7 +464,7 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
           else lam = sLamIn[b][t];
           sLam[t] = lam;
           sS[t] = sv[i];
-          if (GATE && a.lam_out && t < L) a.lam_out[(u.bos + t0 + t) * a.H + u.h] = lam;
+          sIp[t] = __builtin_amdgcn_rcpf(seg_pos(t0 + t, a.pos_off));
         }
       }
     }
@@ -382,26 +482,30 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
         }
         if ((l & 15) == 0) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sS[tb + i] += rsum[i];
+          for (int i = 0; i < 4; ++i) {
+            const float ip = sIp[tb + i];
+            sS[tb + i] = (sS[tb + i] + rsum[i]) * ip * ip;
+          }
         }
       }
       __syncthreads();
     }
 
-    // ---- per wave: Z[:, cols] = Q C_prev[:, cols] + A K[:, cols]; key sums; q_clean to LDS.  One
-    // 16-row tile at a time (a runtime loop keeps the live registers few); the state's hi/lo B
-    // operands are formed per contraction step, hi and lo products go to separate accumulators
+    // ---- per wave: Z[:, cols] = Q C_prev[:, cols] + A K[:, cols]; key sums; q_clean to LDS.  The
+    // state's hi/lo B operands are formed once per chunk; then one 16-row tile at a time (a runtime
+    // loop keeps the live registers few), hi and lo products in separate accumulators
+    bf16x8 chh[NKS], chl[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) acc_pair_split(C[2 * ks], C[2 * ks + 1], chh[ks], chl[ks]);
     f32x4 cum = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
     for (int tt = 0; tt < 4; ++tt) {
       f32x4 zh = f32x4{0.f, 0.f, 0.f, 0.f}, zl = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        bf16x8 chh, chl;
-        acc_pair_split(C[2 * ks], C[2 * ks + 1], chh, chl);
         const bf16x8 qa = frag16_rm_acc(Qc + 16 * tt * LDK + 32 * ks, LDK);
-        zh = mfma16(qa, chh, zh);
-        zl = mfma16(qa, chl, zl);
+        zh = mfma16(qa, chh[ks], zh);
+        zl = mfma16(qa, chl[ks], zl);
       }
       cum = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -409,16 +513,18 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
         if (ss <= (tt >> 1)) {
           zh = mfma16(frag16_rm(sAh + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zh);
           zl = mfma16(frag16_rm(sAl + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zl);
-          if (MEAN) cum = mfma16(tril16(tt, ss), kcol[ss], cum);
+          if (MEAN) cum = mfma16(tri.at(tt, ss), kcol[ss], cum);
         }
       }
+      const int tb = 16 * tt + g4;
+      const f32x4 ipv = *(const f32x4*)(sIp + tb), lamv = *(const f32x4*)(sLam + tb);
+      f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (MEAN) sv = *(const f32x4*)(sS + tb);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * tt + g4 + i;
-        const float ip = __builtin_amdgcn_rcpf(seg_pos(t0 + t, a.pos_off));
-        float corr = (zh[i] + zl[i]) * ip;
-        if (MEAN) corr -= sS[t] * ip * ip * (mcol + cum[i]);
-        sO[t * LDO + col] = (float)Qc[t * LDK + col] - sLam[t] * corr;
+        float corr = (zh[i] + zl[i]) * ipv[i];
+        if (MEAN) corr -= sv[i] * (mcol + cum[i]);
+        sO[(tb + i) * LDO + col] = (float)Qc[(tb + i) * LDK + col] - lamv[i] * corr;
       }
     }
     // key-sum total of the chunk: row 63 of the running sums (rows past the chunk hold k = 0)
@@ -430,9 +536,23 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt) C[kt] = mfma16(frag16_tr(Kc + 32 * ss * LDK + 16 * kt, LDK), kcol[ss], C[kt]);
     if (MEAN) put_m(b ^ 1);
-    if (c + 1 < u.ce) stage(c + 1);
+    stage(min(c + 1, u.ce - 1), b ^ 1);
+    const float lamo = sLam[tid & (SB - 1)];  // (rewritten before the next chunk's first barrier)
     __syncthreads();
-    store_rows<K, NT>(sO, LDO, a.qc32, (bf16*)a.qc, nullptr, u.hb + (long)t0 * u.rs, u.rs, L, tid);
+    // results of chunk c out, after the loads of chunk c+2 (a later wait for those loads then
+    // leaves these stores in flight)
+    TileOut<K, NT> out;
+    out.read(sO, LDO, tid);
+    load(min(c + 2, u.ce - 1));
+    const long ob = u.hb + (long)t0 * u.rs;
+    out.store(rows_rsrc(a.qc32 ? a.qc32 + ob : nullptr, u.rs, L, K, 4),
+              rows_rsrc(a.qc ? (const bf16*)a.qc + ob : nullptr, u.rs, L, K, 2), u.rs, tid);
+    if (GATE) {
+      const __amdgpu_buffer_rsrc_t rl =
+          rows_rsrc(a.lam_out ? a.lam_out + (u.bos + t0) * a.H + u.h : nullptr, a.H, L, 1, 4);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, lamo), rl,
+                                            tid < SB ? tid * a.H * 4 : 0x7ffffff0, 0, 0);
+    }
   }
 
   if (last) {
@@ -457,7 +577,7 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
 //      scalars (wave 0); gate partials; C, m update
 //   5  dq rows to HBM, chunk c+1 into LDS (each thread overwrites exactly the pieces it stored)
 // ===========================================================================
-template <int K, bool MEAN, bool GATE>
+template <int K, bool MEAN, bool GATE, bool DQ32>
 __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
   constexpr int NW = K / 16, NT = 64 * NW;
   constexpr int LDK = K + 16, LDA = SB + 16, LDD = K + 4;
@@ -474,13 +594,18 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sMW[2 * LDK];     // m_prev hi, lo
   __shared__ __attribute__((aligned(16))) float sPart[NW][2][SB];  // per-wave partial row dots
   __shared__ __attribute__((aligned(16))) float sTot[2][SB];
-  __shared__ __attribute__((aligned(16))) float sS[SB], sLam[SB], sF[SB], sGw[K];
+  __shared__ __attribute__((aligned(16))) float sS[SB], sLam[SB], sF[SB], sIp[SB], sGw[K];
+  __shared__ __attribute__((aligned(16))) f32x4 sScO[SB];   // per-token scalars of the chunk (out)
+  __shared__ __attribute__((aligned(16))) float sDlO[SB];   // dlambda (out)
+  __shared__ __attribute__((aligned(16))) float sGp[K + 4];  // gate partials: dW columns, db (out)
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
   const SegUnit u = seg_unit<K>(a);
   if (u.cb >= u.ce) return;
   const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
   auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
+  Tril tri;
+  tri.init();
 
   f32x4 C[NKT];
 #pragma unroll
@@ -493,6 +618,9 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
     mcol = a.m0 ? a.m0[(long)u.unit * K + col] : 0.f;
     for (int s = 0; s < u.seg; ++s) mcol += a.segM[((long)u.unit * a.nseg + s) * K + col];
   }
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) settle(C[kt]);
+  settle(mcol);
   for (int i = tid; i < SB * LDA; i += NT) {
     sAh[i] = (bf16)0.f;
     sAl[i] = (bf16)0.f;
@@ -520,11 +648,13 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
     const long off = u.hb + (long)c * SB * u.rs;
     pk.load((const bf16*)a.k + off, u.rs, L, tid);
     pq.load((const bf16*)a.q + off, u.rs, L, tid);
-    pd.load(a.dqc32 ? a.dqc32 + off : nullptr, a.dqc32 ? nullptr : (const bf16*)a.dqc16 + off, u.rs, L, tid);
+    // (the upstream gradient's dtype is a template parameter: one load sequence)
+    if (DQ32) pd.load(a.dqc32 + off, u.rs, L, tid);
+    else pd.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, tid);
     const long tb = u.bos + (long)c * SB;
 #pragma unroll
     for (int j = 0; j < ND; ++j) pl[j] = a.lam_used[(tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h];
-    if (tid < SB) plam = a.lam_used[(tb + min(tid, L - 1)) * a.H + u.h];
+    plam = a.lam_used[(tb + min(tid & (SB - 1), L - 1)) * a.H + u.h];
   };
   auto stage = [&](int c) {
     const int L = chunk_len(c), t0 = c * SB;
@@ -536,29 +666,26 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
       const float f = r < L ? -pl[j] * __builtin_amdgcn_rcpf(seg_pos(t0 + r, a.pos_off)) : 0.f;
       bf16x4 hh, ll;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bf16 x, y;
-        split2(f * pd.v[j][e], x, y);
-        hh[e] = x;
-        ll[e] = y;
-      }
+      split4(f * pd.v[j], hh, ll);
       *(bf16x4*)(sZh + r * LDK + cc) = hh;
       *(bf16x4*)(sZl + r * LDK + cc) = ll;
     }
     if (tid < SB) {
       const bool ok = tid < L;
+      const float ip = __builtin_amdgcn_rcpf(seg_pos(t0 + tid, a.pos_off));
       sLam[tid] = ok ? plam : 0.f;
-      sF[tid] = ok ? -plam * __builtin_amdgcn_rcpf(seg_pos(t0 + tid, a.pos_off)) : 0.f;
+      sF[tid] = ok ? -plam * ip : 0.f;
+      sIp[tid] = ip;
     }
   };
+  // chunk loads and stages: unconditional (past the end the last chunk again)
   load(u.cb);
   stage(u.cb);
+  load(min(u.cb + 1, u.ce - 1));
   __syncthreads();
 
   for (int c = u.cb; c < u.ce; ++c) {
     const int L = chunk_len(c), t0 = c * SB;
-    if (c + 1 < u.ce) load(c + 1);
     bf16x8 kcol[2];
 #pragma unroll
     for (int ss = 0; ss < 2; ++ss) kcol[ss] = frag16_tr(sK + 32 * ss * LDK + c0, LDK);
@@ -625,23 +752,24 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       __syncthreads();
     }
 
-    // ---- 2: per wave, one 16-row tile at a time
+    // ---- 2: per wave, one 16-row tile at a time (the state's hi/lo B operands formed once)
+    bf16x8 chh[NKS], chl[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) acc_pair_split(C[2 * ks], C[2 * ks + 1], chh[ks], chl[ks]);
 #pragma unroll 1
     for (int tt = 0; tt < 4; ++tt) {
       f32x4 zh = f32x4{0.f, 0.f, 0.f, 0.f}, zl = f32x4{0.f, 0.f, 0.f, 0.f};
       f32x4 wh = f32x4{0.f, 0.f, 0.f, 0.f}, wl = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        bf16x8 chh, chl;
-        acc_pair_split(C[2 * ks], C[2 * ks + 1], chh, chl);
         const bf16x8 qa = frag16_rm_acc(sQ + 16 * tt * LDK + 32 * ks, LDK);
         const bf16x8 da = frag16_rm_acc(sZh + 16 * tt * LDK + 32 * ks, LDK);
         const bf16x8 dl = frag16_rm_acc(sZl + 16 * tt * LDK + 32 * ks, LDK);
-        zh = mfma16(qa, chh, zh);
-        zl = mfma16(qa, chl, zl);
-        wh = mfma16(da, chh, wh);
-        wl = mfma16(dl, chh, wl);
-        wl = mfma16(da, chl, wl);
+        zh = mfma16(qa, chh[ks], zh);
+        zl = mfma16(qa, chl[ks], zl);
+        wh = mfma16(da, chh[ks], wh);
+        wl = mfma16(dl, chh[ks], wl);
+        wl = mfma16(da, chl[ks], wl);
       }
       f32x4 cum = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -651,25 +779,33 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
           zl = mfma16(frag16_rm(sAl + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zl);
           wh = mfma16(frag16_rm(sBh + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], wh);
           wl = mfma16(frag16_rm(sBl + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], wl);
-          if (MEAN) cum = mfma16(tril16(tt, ss), kcol[ss], cum);
+          if (MEAN) cum = mfma16(tri.at(tt, ss), kcol[ss], cum);
         }
+      }
+      const int tb = 16 * tt + g4;
+      const f32x4 ipv = *(const f32x4*)(sIp + tb);
+      f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (MEAN) sv = *(const f32x4*)(sS + tb);
+      f32x4 p1, p2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float* pd_ = sD + (tb + i) * LDD + col;
+        const float dqc = *pd_;
+        const float mt = mcol + cum[i];
+        float corr = (zh[i] + zl[i]) * ipv[i];
+        if (MEAN) corr -= sv[i] * ipv[i] * ipv[i] * mt;
+        p1[i] = dqc * corr;
+        p2[i] = dqc * mt;
+        *pd_ = dqc + (wh[i] + wl[i]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * tt + g4 + i;
-        const float ip = __builtin_amdgcn_rcpf(seg_pos(t0 + t, a.pos_off));
-        float* pd_ = sD + t * LDD + col;
-        const float dqc = *pd_;
-        const float mt = mcol + cum[i];
-        float corr = (zh[i] + zl[i]) * ip;
-        if (MEAN) corr -= sS[t] * ip * ip * mt;
-        const float p1 = row16_sum(dqc * corr);
-        const float p2 = MEAN ? row16_sum(dqc * mt) : 0.f;
-        *pd_ = dqc + (wh[i] + wl[i]);
-        if ((l & 15) == 0) {
-          sPart[w][0][t] = p1;
-          if (MEAN) sPart[w][1][t] = p2;
-        }
+        p1[i] = row16_sum(p1[i]);
+        if (MEAN) p2[i] = row16_sum(p2[i]);
+      }
+      if ((l & 15) == 0) {
+        *(f32x4*)(&sPart[w][0][tb]) = p1;
+        if (MEAN) *(f32x4*)(&sPart[w][1][tb]) = p2;
       }
     }
     __syncthreads();
@@ -687,6 +823,7 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
 
     // ---- 4: dq, per-token scalars, gate partials, state update
     float gsum = 0.f, dbsum = 0.f;
+    const float gwc = GATE ? sGw[col] : 0.f;
     f32x4 cum = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
     for (int tt = 0; tt < 4; ++tt) {
@@ -694,28 +831,40 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       if (MEAN) {
 #pragma unroll
         for (int ss = 0; ss < 2; ++ss)
-          if (ss <= (tt >> 1)) cum = mfma16(tril16(tt, ss), kcol[ss], cum);
+          if (ss <= (tt >> 1)) cum = mfma16(tri.at(tt, ss), kcol[ss], cum);
       }
+      const int tb = 16 * tt + g4;
+      const f32x4 ipv = *(const f32x4*)(sIp + tb), lamv = *(const f32x4*)(sLam + tb);
+      const f32x4 t0v = *(const f32x4*)(&sTot[0][tb]);
+      f32x4 t1v = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (MEAN) {
+        t1v = *(const f32x4*)(&sTot[1][tb]);
+        sv = *(const f32x4*)(sS + tb);
+      }
+      f32x4 dlamv, dsv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * tt + g4 + i;
-        const float ip = __builtin_amdgcn_rcpf(seg_pos(t0 + t, a.pos_off));
-        const float lam = sLam[t];
-        const float dlam = t < L ? -sTot[0][t] : 0.f;
-        const float ds = MEAN ? lam * sTot[1][t] * ip * ip : 0.f;
+        const float lam = lamv[i];
+        const float dlam = tb + i < L ? -t0v[i] : 0.f;
+        const float ds = MEAN ? lam * t1v[i] * ipv[i] * ipv[i] : 0.f;
         const float dlogit = dlam * lam * (1.f - lam);
-        float* pd_ = sD + t * LDD + col;
+        float* pd_ = sD + (tb + i) * LDD + col;
         float dq = *pd_ + ds * (mcol + cum[i]);
         if (GATE) {
-          dq += dlogit * sGw[col];
-          gsum += dlogit * (float)sQ[t * LDK + col];
+          dq += dlogit * gwc;
+          gsum += dlogit * (float)sQ[(tb + i) * LDK + col];
           dbsum += dlogit;
         }
         *pd_ = dq;
-        if (w == 0 && (l & 15) == 0 && t < L) {
-          const long ti = (u.bos + t0 + t) * a.H + u.h;
-          *(f32x4*)(a.sc + ti * 4) = f32x4{sF[t], ds, GATE ? dlogit : dlam, MEAN ? -sS[t] * ip : 0.f};
-          if (!GATE && a.dlam) a.dlam[ti] = dlam;
+        dlamv[i] = GATE ? dlogit : dlam;
+        dsv[i] = ds;
+      }
+      if (w == 0 && (l & 15) == 0) {
+        const f32x4 fv = *(const f32x4*)(sF + tb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sScO[tb + i] = f32x4{fv[i], dsv[i], dlamv[i], MEAN ? -sv[i] * ipv[i] : 0.f};
+          sDlO[tb + i] = dlamv[i];
         }
       }
     }
@@ -723,14 +872,13 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       // column sums over the chunk's rows: one column's lanes across the four lane groups
       gsum += __shfl_xor(gsum, 16);
       gsum += __shfl_xor(gsum, 32);
-      const long gi = (long)(u.gc0 + c) * a.H + u.h;
-      if (l < 16) a.dw_part[gi * K + col] = gsum;
+      if (l < 16) sGp[col] = gsum;
       if (w == 0) {
         // the 16 lanes of a group hold the same rows: one lane per group counts them
         float d = (l & 15) == 0 ? dbsum : 0.f;
         d += __shfl_xor(d, 16);
         d += __shfl_xor(d, 32);
-        if (l == 0) a.db_part[gi] = d;
+        if (l == 0) sGp[K] = d;
       }
     }
     if (MEAN) mcol += __shfl(cum[3], 48 + (l & 15));
@@ -740,11 +888,42 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       for (int kt = 0; kt < NKT; ++kt) C[kt] = mfma16(frag16_tr(sK + 32 * ss * LDK + 16 * kt, LDK), kcol[ss], C[kt]);
     __syncthreads();
 
-    // ---- 5: dq rows out; chunk c+1 in (same thread-piece mapping for sD)
-    store_rows<K, NT>(sD, LDD, a.dq32, (bf16*)a.dq, nullptr, u.hb + (long)t0 * u.rs, u.rs, L, tid);
+    // ---- 5: results of chunk c to registers; chunk c+1 in (each thread overwrites exactly the sD
+    // pieces it read); loads of chunk c+2; then the stores (after those loads: a later wait for
+    // them leaves the stores in flight)
+    TileOut<K, NT> out;
+    out.read(sD, LDD, tid);
+    const f32x4 sco = sScO[tid & (SB - 1)];
+    const float dlo = sDlO[tid & (SB - 1)];
+    f32x4 gpo = f32x4{0.f, 0.f, 0.f, 0.f};
+    float dbo = 0.f;
+    if (GATE) {
+      gpo = *(const f32x4*)(sGp + 4 * (tid % (K / 4)));
+      dbo = sGp[K];
+    }
     if (MEAN) put_m();
-    if (c + 1 < u.ce) stage(c + 1);
+    stage(min(c + 1, u.ce - 1));
     __syncthreads();
+    load(min(c + 2, u.ce - 1));
+    const long ob = u.hb + (long)t0 * u.rs, tb0 = (u.bos + t0) * a.H + u.h;
+    out.store(rows_rsrc(a.dq32 ? a.dq32 + ob : nullptr, u.rs, L, K, 4),
+              rows_rsrc(a.dq ? (const bf16*)a.dq + ob : nullptr, u.rs, L, K, 2), u.rs, tid);
+    // per-token outputs: row tid of the chunk for the first SB threads, an offset past any resource
+    // (dropped) for the others
+    constexpr int kPast = 0x7ffffff0;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sco), rows_rsrc(a.sc + tb0 * 4, a.H * 4, L, 4, 4),
+                                           tid < SB ? tid * a.H * 16 : kPast, 0, 0);
+    if (!GATE)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, dlo),
+                                            rows_rsrc(a.dlam ? a.dlam + tb0 : nullptr, a.H, L, 1, 4),
+                                            tid < SB ? tid * a.H * 4 : kPast, 0, 0);
+    if (GATE) {
+      const long gi = (long)(u.gc0 + c) * a.H + u.h;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, gpo), buf_rsrc(a.dw_part + gi * K, K * 4),
+                                             tid < K / 4 ? tid * 16 : kPast, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, dbo), buf_rsrc(a.db_part + gi, 4),
+                                            tid == 0 ? 0 : kPast, 0, 0);
+    }
   }
 }
 
@@ -752,7 +931,7 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
 // cs_gsum: grid N*H*nseg, K/16 waves.  segG = sum over the segment of Q^T dZ (dZ = diag(f) dQc),
 // segDM = sum of dm_t = -(s_t/pos_t) dz_t + ds_t q_t (every workgroup writes, zero when empty).
 // ===========================================================================
-template <int K, bool MEAN>
+template <int K, bool MEAN, bool DQ32>
 __global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
   constexpr int NW = K / 16, NT = 64 * NW, LDK = K + 16, NKT = K / 16, VPR = K / 4;
   __shared__ __attribute__((aligned(16))) bf16 sQ[SB * LDK];
@@ -776,10 +955,12 @@ __global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
     const int L = chunk_len(c);
     const long off = u.hb + (long)c * SB * u.rs, tb = u.bos + (long)c * SB;
     pq.load((const bf16*)a.q + off, u.rs, L, tid);
-    pd.load(a.dqc32 ? a.dqc32 + off : nullptr, a.dqc32 ? nullptr : (const bf16*)a.dqc16 + off, u.rs, L, tid);
+    // (the upstream gradient's dtype is a template parameter: one load sequence)
+    if (DQ32) pd.load(a.dqc32 + off, u.rs, L, tid);
+    else pd.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, tid);
 #pragma unroll
     for (int j = 0; j < ND; ++j) pf[j] = a.sc[((tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h) * 4];
-    if (tid < SB) psc = *(const f32x4*)(a.sc + ((tb + min(tid, L - 1)) * a.H + u.h) * 4);
+    psc = *(const f32x4*)(a.sc + ((tb + min(tid & (SB - 1), L - 1)) * a.H + u.h) * 4);
   };
   auto stage = [&](int c) {
     const int L = chunk_len(c);
@@ -789,13 +970,7 @@ __global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
       const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
       const float f = r < L ? pf[j] : 0.f;
       bf16x4 hh, ll;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bf16 x, y;
-        split2(f * pd.v[j][e], x, y);
-        hh[e] = x;
-        ll[e] = y;
-      }
+      split4(f * pd.v[j], hh, ll);
       *(bf16x4*)(sZh + r * LDK + cc) = hh;
       *(bf16x4*)(sZl + r * LDK + cc) = ll;
     }
@@ -804,13 +979,14 @@ __global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
       sSp[tid] = tid < L ? psc[3] : 0.f;
     }
   };
+  // chunk loads and stages: unconditional (past the end the last chunk again)
   if (u.cb < u.ce) {
     load(u.cb);
     stage(u.cb);
+    load(min(u.cb + 1, u.ce - 1));
   }
   __syncthreads();
   for (int c = u.cb; c < u.ce; ++c) {
-    if (c + 1 < u.ce) load(c + 1);
 #pragma unroll
     for (int ss = 0; ss < 2; ++ss) {
       const bf16x8 bh = frag16_tr(sZh + 32 * ss * LDK + c0, LDK), bl = frag16_tr(sZl + 32 * ss * LDK + c0, LDK);
@@ -830,8 +1006,9 @@ __global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
       }
     }
     __syncthreads();
-    if (c + 1 < u.ce) stage(c + 1);
+    stage(min(c + 1, u.ce - 1));
     __syncthreads();
+    load(min(c + 2, u.ce - 1));
   }
   float* dst = a.segG + ((long)u.unit * a.nseg + u.seg) * K * K;
 #pragma unroll
@@ -855,7 +1032,7 @@ __global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
 // The dm suffix sums are two masked products: (t >= j ? ds_t : 0) against Q and (t >= j ?
 // -s_t/pos_t : 0) against dZ.  Segment 0 also writes dC_0 = dC_T + sum_t q_t dz_t^T and dm_0.
 // ===========================================================================
-template <int K, bool MEAN>
+template <int K, bool MEAN, bool DQ32>
 __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
   constexpr int NW = K / 16, NT = 64 * NW;
   constexpr int LDK = K + 16, LDA = SB + 16, LDO = K + 4;
@@ -869,7 +1046,7 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sBh[SB * LDA];   // (dZ K^T) o M
   __shared__ __attribute__((aligned(16))) bf16 sBl[SB * LDA];
   __shared__ __attribute__((aligned(16))) float sO[SB * LDO];   // dk rows
-  __shared__ __attribute__((aligned(16))) float sDs[SB], sSp[SB];
+  __shared__ __attribute__((aligned(16))) bf16 sDsH[SB], sDsL[SB], sSpH[SB], sSpL[SB];  // hi/lo of ds, -s/pos
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
   const SegUnit u = seg_unit<K>(a);
   const bool first = u.seg == 0;
@@ -895,6 +1072,9 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
     carry = a.dm_fin ? a.dm_fin[(long)u.unit * K + col] : 0.f;
     for (int s = u.seg + 1; s < a.nseg; ++s) carry += a.segDM[((long)u.unit * a.nseg + s) * K + col];
   }
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) settle(E[kt]);
+  settle(carry);
   for (int i = tid; i < SB * LDA; i += NT) {
     sAh[i] = (bf16)0.f;
     sAl[i] = (bf16)0.f;
@@ -904,6 +1084,7 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
 
   RowsBf16<K, SB, NT> pq, pk;
   RowsF32<K, SB, NT> pd;
+  TileIn<K, NT> pe;  // dk_extra rows (zero when absent)
   constexpr int ND = RowsF32<K, SB, NT>::N;
   float pf[ND];
   f32x4 psc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -912,44 +1093,59 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
     const long off = u.hb + (long)c * SB * u.rs, tb = u.bos + (long)c * SB;
     pk.load((const bf16*)a.k + off, u.rs, L, tid);
     pq.load((const bf16*)a.q + off, u.rs, L, tid);
-    pd.load(a.dqc32 ? a.dqc32 + off : nullptr, a.dqc32 ? nullptr : (const bf16*)a.dqc16 + off, u.rs, L, tid);
+    // (the upstream gradient's dtype is a template parameter: one load sequence)
+    if (DQ32) pd.load(a.dqc32 + off, u.rs, L, tid);
+    else pd.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, tid);
+    pe.load(rows_rsrc(a.dk_extra ? a.dk_extra + off : nullptr, u.rs, L, K, 4), u.rs, tid);
 #pragma unroll
     for (int j = 0; j < ND; ++j) pf[j] = a.sc[((tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h) * 4];
-    if (tid < SB) psc = *(const f32x4*)(a.sc + ((tb + min(tid, L - 1)) * a.H + u.h) * 4);
+    psc = *(const f32x4*)(a.sc + ((tb + min(tid & (SB - 1), L - 1)) * a.H + u.h) * 4);
   };
+  // chunk c into LDS; the dk rows start as dk_extra (each thread writes the sO pieces it stores)
   auto stage = [&](int c) {
     const int L = chunk_len(c);
     pk.store(sK, LDK, L, tid);
     pq.store(sQ, LDK, L, tid);
+    pe.store(sO, LDO, tid);
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
       const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
       const float f = r < L ? pf[j] : 0.f;
       bf16x4 hh, ll;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bf16 x, y;
-        split2(f * pd.v[j][e], x, y);
-        hh[e] = x;
-        ll[e] = y;
-      }
+      split4(f * pd.v[j], hh, ll);
       *(bf16x4*)(sZh + r * LDK + cc) = hh;
       *(bf16x4*)(sZl + r * LDK + cc) = ll;
     }
     if (tid < SB) {
-      sDs[tid] = tid < L ? psc[1] : 0.f;
-      sSp[tid] = tid < L ? psc[3] : 0.f;
+      const float ds = tid < L ? psc[1] : 0.f, sp = tid < L ? psc[3] : 0.f;
+      bf16 x, y;
+      split2(ds, x, y);
+      sDsH[tid] = x;
+      sDsL[tid] = y;
+      split2(sp, x, y);
+      sSpH[tid] = x;
+      sSpL[tid] = y;
     }
   };
+  // masks of the suffix products' diagonal blocks: slot t = 8 (lane / 16) + j of row j' = lane % 16
+  // (even row tiles) or 16 + lane % 16 (odd row tiles) is kept when t >= j'
+  u32x4 mask_even, mask_odd;
+#pragma unroll
+  for (int wd = 0; wd < 4; ++wd) {
+    const int t = 8 * (l >> 4) + 2 * wd, j = l & 15;
+    mask_even[wd] = (t >= j ? 0x0000ffffu : 0u) | (t + 1 >= j ? 0xffff0000u : 0u);
+    mask_odd[wd] = (t >= 16 + j ? 0x0000ffffu : 0u) | (t + 1 >= 16 + j ? 0xffff0000u : 0u);
+  }
+  // chunk loads and stages: unconditional (past the start of the segment its first chunk again)
   if (u.cb < u.ce) {
     load(u.ce - 1);
     stage(u.ce - 1);
+    load(max(u.ce - 2, u.cb));
   }
   __syncthreads();
 
   for (int c = u.ce - 1; c >= u.cb; --c) {
     const int L = chunk_len(c), t0 = c * SB;
-    if (c - 1 >= u.cb) load(c - 1);
     // ---- scores (e < 10: A = (Q K^T) o M, else B = (dZ K^T) o M)
 #pragma unroll
     for (int j = 0; j < (20 + NW - 1) / NW; ++j) {
@@ -988,17 +1184,18 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
       zcolh[ts] = frag16_tr(sZh + 32 * ts * LDK + c0, LDK);
       zcoll[ts] = frag16_tr(sZl + 32 * ts * LDK + c0, LDK);
     }
+    bf16x8 eh[NKS], el[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) acc_pair_split(E[2 * ks], E[2 * ks + 1], eh[ks], el[ks]);
     float dmtot = 0.f;
 #pragma unroll 1
     for (int jt = 0; jt < 4; ++jt) {
       f32x4 xh = f32x4{0.f, 0.f, 0.f, 0.f}, xl = f32x4{0.f, 0.f, 0.f, 0.f}, sfx = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        bf16x8 eh, el;
-        acc_pair_split(E[2 * ks], E[2 * ks + 1], eh, el);
         const bf16x8 ka = frag16_rm_acc(sK + 16 * jt * LDK + 32 * ks, LDK);
-        xh = mfma16(ka, eh, xh);
-        xl = mfma16(ka, el, xl);
+        xh = mfma16(ka, eh[ks], xh);
+        xl = mfma16(ka, el[ks], xl);
       }
 #pragma unroll
       for (int ts = 0; ts < 2; ++ts) {
@@ -1014,22 +1211,15 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
           xl = mfma16(atl, zcolh[ts], xl);
           xl = mfma16(ath, zcoll[ts], xl);
           if (MEAN) {
-            // masked diagonals: row j = 16 jt + (l & 15), slots t = 32 ts + 8 (l >> 4) + i
-            const int tb = 32 * ts + 8 * (l >> 4), jr = 16 * jt + (l & 15);
-            const f32x4 d0 = *(const f32x4*)(sDs + tb), d1 = *(const f32x4*)(sDs + tb + 4);
-            const f32x4 p0 = *(const f32x4*)(sSp + tb), p1 = *(const f32x4*)(sSp + tb + 4);
-            bf16x8 dh, dl, ph, pl;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const bool keep = tb + i >= jr;
-              bf16 a1, a2, a3, a4;
-              split2(keep ? (i < 4 ? d0[i] : d1[i - 4]) : 0.f, a1, a2);
-              split2(keep ? (i < 4 ? p0[i] : p1[i - 4]) : 0.f, a3, a4);
-              dh[i] = a1;
-              dl[i] = a2;
-              ph[i] = a3;
-              pl[i] = a4;
-            }
+            // masked diagonals: row j = 16 jt + (l & 15), slots t = 32 ts + 8 (l >> 4) + i, kept
+            // for t >= j (whole step below the diagonal block, else the block's mask)
+            const int tb = 32 * ts + 8 * (l >> 4);
+            u32x4 m = u32x4{~0u, ~0u, ~0u, ~0u};
+            if (ts == (jt >> 1)) m = (jt & 1) ? mask_odd : mask_even;
+            const bf16x8 dh = __builtin_bit_cast(bf16x8, *(const u32x4*)(sDsH + tb) & m);
+            const bf16x8 dl = __builtin_bit_cast(bf16x8, *(const u32x4*)(sDsL + tb) & m);
+            const bf16x8 ph = __builtin_bit_cast(bf16x8, *(const u32x4*)(sSpH + tb) & m);
+            const bf16x8 pl = __builtin_bit_cast(bf16x8, *(const u32x4*)(sSpL + tb) & m);
             sfx = mfma16(dh, qcol[ts], sfx);
             sfx = mfma16(dl, qcol[ts], sfx);
             sfx = mfma16(ph, zcolh[ts], sfx);
@@ -1040,7 +1230,7 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
       }
       if (MEAN && jt == 0) dmtot = __shfl(sfx[0], l & 15);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sO[(16 * jt + g4 + i) * LDO + col] = xh[i] + xl[i] + sfx[i] + carry;
+      for (int i = 0; i < 4; ++i) sO[(16 * jt + g4 + i) * LDO + col] += xh[i] + xl[i] + sfx[i] + carry;
     }
     if (MEAN) carry += dmtot;
 
@@ -1058,9 +1248,15 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
         E[kt] = mfma16(zb, qcol[ts], E[kt]);
       }
     __syncthreads();
-    store_rows<K, NT>(sO, LDO, a.dk32, (bf16*)a.dk, a.dk_extra, u.hb + (long)t0 * u.rs, u.rs, L, tid);
-    if (c - 1 >= u.cb) stage(c - 1);
+    // dk rows of chunk c to registers; chunk c-1 in; loads of chunk c-2; then the stores
+    TileOut<K, NT> out;
+    out.read(sO, LDO, tid);
+    stage(max(c - 1, u.cb));
     __syncthreads();
+    load(max(c - 2, u.cb));
+    const long ob = u.hb + (long)t0 * u.rs;
+    out.store(rows_rsrc(a.dk32 ? a.dk32 + ob : nullptr, u.rs, L, K, 4),
+              rows_rsrc(a.dk ? (const bf16*)a.dk + ob : nullptr, u.rs, L, K, 2), u.rs, tid);
   }
 
   if (first) {
@@ -1115,19 +1311,35 @@ hipError_t cseg_k(int stage, const WalkArgs& a, hipStream_t st) {
       else if (gate) hipLaunchKernelGGL((cs_fwd_kernel<K, false, true>), grid, block, 0, st, a);
       else hipLaunchKernelGGL((cs_fwd_kernel<K, false, false>), grid, block, 0, st, a);
       break;
-    case kSegDq:
-      if (mean && gate) hipLaunchKernelGGL((cs_dq_kernel<K, true, true>), grid, block, 0, st, a);
-      else if (mean) hipLaunchKernelGGL((cs_dq_kernel<K, true, false>), grid, block, 0, st, a);
-      else if (gate) hipLaunchKernelGGL((cs_dq_kernel<K, false, true>), grid, block, 0, st, a);
-      else hipLaunchKernelGGL((cs_dq_kernel<K, false, false>), grid, block, 0, st, a);
+    case kSegDq: {
+      const int sel = (a.dqc32 ? 4 : 0) + (mean ? 2 : 0) + (gate ? 1 : 0);
+#define CCQ_SEG_DQ(S, A, B, C) \
+  case S: hipLaunchKernelGGL((cs_dq_kernel<K, B, C, A>), grid, block, 0, st, a); break;
+      switch (sel) {
+        CCQ_SEG_DQ(0, false, false, false) CCQ_SEG_DQ(1, false, false, true) CCQ_SEG_DQ(2, false, true, false)
+        CCQ_SEG_DQ(3, false, true, true) CCQ_SEG_DQ(4, true, false, false) CCQ_SEG_DQ(5, true, false, true)
+        CCQ_SEG_DQ(6, true, true, false) CCQ_SEG_DQ(7, true, true, true)
+      }
+#undef CCQ_SEG_DQ
       break;
+    }
     case kSegGsum:
-      if (mean) hipLaunchKernelGGL((cs_gsum_kernel<K, true>), grid, block, 0, st, a);
-      else hipLaunchKernelGGL((cs_gsum_kernel<K, false>), grid, block, 0, st, a);
+      if (a.dqc32) {
+        if (mean) hipLaunchKernelGGL((cs_gsum_kernel<K, true, true>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((cs_gsum_kernel<K, false, true>), grid, block, 0, st, a);
+      } else {
+        if (mean) hipLaunchKernelGGL((cs_gsum_kernel<K, true, false>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((cs_gsum_kernel<K, false, false>), grid, block, 0, st, a);
+      }
       break;
     case kSegDk:
-      if (mean) hipLaunchKernelGGL((cs_dk_kernel<K, true>), grid, block, 0, st, a);
-      else hipLaunchKernelGGL((cs_dk_kernel<K, false>), grid, block, 0, st, a);
+      if (a.dqc32) {
+        if (mean) hipLaunchKernelGGL((cs_dk_kernel<K, true, true>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((cs_dk_kernel<K, false, true>), grid, block, 0, st, a);
+      } else {
+        if (mean) hipLaunchKernelGGL((cs_dk_kernel<K, true, false>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((cs_dk_kernel<K, false, false>), grid, block, 0, st, a);
+      }
       break;
     default:
       return hipErrorInvalidValue;
