@@ -130,9 +130,12 @@ struct Tril {
 __device__ __forceinline__ int tile_t(int e) { return e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3; }
 __device__ __forceinline__ int tile_s(int e) { return e - tile_t(e) * (tile_t(e) + 1) / 2; }
 
+// Value of another lane of the same 16-lane row by DPP.  Written as an update with a zero old value
+// and bound_ctrl set (every control used here reads a valid lane, so neither takes effect) so that
+// the move folds into the consuming add (v_add_f32_dpp).
 template <int C>
 __device__ __forceinline__ float dppf(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), C, 0xf, 0xf, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), C, 0xf, 0xf, true));
 }
 
 // Sum over the 16 lanes of a row (lanes 16 g .. 16 g + 15), every lane receives it: quad_perm
@@ -152,6 +155,20 @@ __device__ __forceinline__ float row16_sum(float x) {
 template <typename T>
 __device__ __forceinline__ void settle(T& x) {
   asm volatile("" : "+v"(x));
+}
+
+// Causal score tile (accumulator of A = K rows 16 J.., B = Q or dZ rows 16 I..: lane = t column,
+// rows s) into LDS transposed, as hi/lo bf16: element (t, s) at [16 I + t][16 J + s] of the hi
+// plane at p and of the lo plane at p + plane.  `uoff` (the tile's offset, wave-uniform) passes
+// through an empty asm so that the per-tile addresses are formed where they are used, not hoisted
+// out of the chunk loop into registers that would then be spilled.
+__device__ __forceinline__ void score_to_lds(const f32x4& acc, bf16* p, int plane, int ld, int uoff) {
+  asm volatile("" : "+s"(uoff));
+  bf16x4 hh, ll;
+  split4(acc, hh, ll);
+  const int e = uoff + (lane_id() & 15) * ld + 4 * (lane_id() >> 4);
+  *(bf16x4*)(p + e) = hh;
+  *(bf16x4*)(p + plane + e) = ll;
 }
 
 // One segment of one (sequence, head): chunks [cb, ce) of the sequence's nc chunks.
@@ -328,12 +345,15 @@ __global__ __launch_bounds__(K * 4) void cs_sum_kernel(const WalkArgs a) {
 template <int K, bool MEAN, bool GATE>
 __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
   constexpr int NW = K / 16, NT = 64 * NW;
-  constexpr int LDK = K + 16, LDA = SB + 16, LDO = K + 4;
+  // row pitch of the q / k tiles: K + 8 bf16 (a pitch of 4 banks mod 32 spreads the 16 rows of a
+  // fragment read; measured faster here than K + 16)
+  constexpr int LDK = K + 8, LDA = SB + 16, LDO = K + 4;
   constexpr int NKS = K / 32, NKT = K / 16;
   __shared__ __attribute__((aligned(16))) bf16 sQ[2][SB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sK[2][SB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sAh[SB * LDA];   // scores A[t][s] (s <= t), hi
-  __shared__ __attribute__((aligned(16))) bf16 sAl[SB * LDA];
+  __shared__ __attribute__((aligned(16))) bf16 sA[2 * SB * LDA];  // scores A[t][s] (s <= t): hi, lo planes
+  bf16* const sAh = sA;
+  bf16* const sAl = sA + SB * LDA;
   __shared__ __attribute__((aligned(16))) float sO[SB * LDO];   // q_clean rows
   __shared__ __attribute__((aligned(16))) bf16 sMW[2][4 * LDK];  // rows: m hi, m lo, gate w hi, lo
   __shared__ __attribute__((aligned(16))) float sS[SB];          // s_t, then s_t / pos_t^2
@@ -436,7 +456,7 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
           for (int i = 0; i < 4; ++i)
             if (g4 + i > (l & 15)) acc[i] = 0.f;
         }
-        acc16_to_lds_t(acc, sAh + 16 * I * LDA, sAl + 16 * I * LDA, LDA, 16 * J);
+        score_to_lds(acc, sA, SB * LDA, LDA, 16 * I * LDA + 16 * J);
       }
     }
     if (w >= NW - 4) {
@@ -587,10 +607,12 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];   // dZ = diag(f) dQc, hi
   __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDK];
   __shared__ __attribute__((aligned(16))) float sD[SB * LDD];   // dQc, then dQc + W, then dq
-  __shared__ __attribute__((aligned(16))) bf16 sAh[SB * LDA];   // (Q K^T) o M
-  __shared__ __attribute__((aligned(16))) bf16 sAl[SB * LDA];
-  __shared__ __attribute__((aligned(16))) bf16 sBh[SB * LDA];   // (dZ K^T) o M
-  __shared__ __attribute__((aligned(16))) bf16 sBl[SB * LDA];
+  // score planes: (Q K^T) o M hi, lo; (dZ K^T) o M hi, lo
+  __shared__ __attribute__((aligned(16))) bf16 sAB[4 * SB * LDA];
+  bf16* const sAh = sAB;
+  bf16* const sAl = sAB + SB * LDA;
+  bf16* const sBh = sAB + 2 * SB * LDA;
+  bf16* const sBl = sAB + 3 * SB * LDA;
   __shared__ __attribute__((aligned(16))) bf16 sMW[2 * LDK];     // m_prev hi, lo
   __shared__ __attribute__((aligned(16))) float sPart[NW][2][SB];  // per-wave partial row dots
   __shared__ __attribute__((aligned(16))) float sTot[2][SB];
@@ -714,8 +736,7 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
           for (int i = 0; i < 4; ++i)
             if (g4 + i > (l & 15)) acc[i] = 0.f;
         }
-        if (e < 10) acc16_to_lds_t(acc, sAh + 16 * I * LDA, sAl + 16 * I * LDA, LDA, 16 * J);
-        else acc16_to_lds_t(acc, sBh + 16 * I * LDA, sBl + 16 * I * LDA, LDA, 16 * J);
+        score_to_lds(acc, sAB, SB * LDA, LDA, (e < 10 ? 0 : 2 * SB * LDA) + 16 * I * LDA + 16 * J);
       }
     }
     if (MEAN && w >= NW - 4) {
@@ -1041,10 +1062,12 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sK[SB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sAh[SB * LDA];   // (Q K^T) o M
-  __shared__ __attribute__((aligned(16))) bf16 sAl[SB * LDA];
-  __shared__ __attribute__((aligned(16))) bf16 sBh[SB * LDA];   // (dZ K^T) o M
-  __shared__ __attribute__((aligned(16))) bf16 sBl[SB * LDA];
+  // score planes: (Q K^T) o M hi, lo; (dZ K^T) o M hi, lo
+  __shared__ __attribute__((aligned(16))) bf16 sAB[4 * SB * LDA];
+  bf16* const sAh = sAB;
+  bf16* const sAl = sAB + SB * LDA;
+  bf16* const sBh = sAB + 2 * SB * LDA;
+  bf16* const sBl = sAB + 3 * SB * LDA;
   __shared__ __attribute__((aligned(16))) float sO[SB * LDO];   // dk rows
   __shared__ __attribute__((aligned(16))) bf16 sDsH[SB], sDsL[SB], sSpH[SB], sSpL[SB];  // hi/lo of ds, -s/pos
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
@@ -1127,15 +1150,19 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
       sSpL[tid] = y;
     }
   };
-  // masks of the suffix products' diagonal blocks: slot t = 8 (lane / 16) + j of row j' = lane % 16
-  // (even row tiles) or 16 + lane % 16 (odd row tiles) is kept when t >= j'
-  u32x4 mask_even, mask_odd;
+  // mask of the suffix products' diagonal blocks: slot t = 8 (lane / 16) + j of row j' = lane % 16
+  // (even row tiles) or 16 + lane % 16 (odd row tiles) is kept when t >= j' (formed where used: a
+  // few compares are cheaper than eight registers held across the walk)
+  auto diag_mask = [&](bool odd) {
+    u32x4 m;
+    const int j = (l & 15) + (odd ? 16 : 0);
 #pragma unroll
-  for (int wd = 0; wd < 4; ++wd) {
-    const int t = 8 * (l >> 4) + 2 * wd, j = l & 15;
-    mask_even[wd] = (t >= j ? 0x0000ffffu : 0u) | (t + 1 >= j ? 0xffff0000u : 0u);
-    mask_odd[wd] = (t >= 16 + j ? 0x0000ffffu : 0u) | (t + 1 >= 16 + j ? 0xffff0000u : 0u);
-  }
+    for (int wd = 0; wd < 4; ++wd) {
+      const int t = 8 * (l >> 4) + 2 * wd;
+      m[wd] = (t >= j ? 0x0000ffffu : 0u) | (t + 1 >= j ? 0xffff0000u : 0u);
+    }
+    return m;
+  };
   // chunk loads and stages: unconditional (past the start of the segment its first chunk again)
   if (u.cb < u.ce) {
     load(u.ce - 1);
@@ -1170,8 +1197,7 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
           for (int i = 0; i < 4; ++i)
             if (g4 + i > (l & 15)) acc[i] = 0.f;
         }
-        if (e < 10) acc16_to_lds_t(acc, sAh + 16 * I * LDA, sAl + 16 * I * LDA, LDA, 16 * J);
-        else acc16_to_lds_t(acc, sBh + 16 * I * LDA, sBl + 16 * I * LDA, LDA, 16 * J);
+        score_to_lds(acc, sAB, SB * LDA, LDA, (e < 10 ? 0 : 2 * SB * LDA) + 16 * I * LDA + 16 * J);
       }
     }
     __syncthreads();
@@ -1215,7 +1241,7 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
             // for t >= j (whole step below the diagonal block, else the block's mask)
             const int tb = 32 * ts + 8 * (l >> 4);
             u32x4 m = u32x4{~0u, ~0u, ~0u, ~0u};
-            if (ts == (jt >> 1)) m = (jt & 1) ? mask_odd : mask_even;
+            if (ts == (jt >> 1)) m = diag_mask(jt & 1);
             const bf16x8 dh = __builtin_bit_cast(bf16x8, *(const u32x4*)(sDsH + tb) & m);
             const bf16x8 dl = __builtin_bit_cast(bf16x8, *(const u32x4*)(sDsL + tb) & m);
             const bf16x8 ph = __builtin_bit_cast(bf16x8, *(const u32x4*)(sSpH + tb) & m);

@@ -1,4 +1,5 @@
-// CCQ read-side cleaning operator on gfx950: column walks (forward and backward).
+// CCQ read-side cleaning operator on gfx950: column walks (forward and backward) for K = 32 and
+// K = 256 (K = 64 and 128 run as segment walks, ccq_cseg.hip).
 //
 // Mathematics (per sequence and head; reference ccq/ops/common/fused_read.py:11-25):
 //   C_t = h_0 + sum_{j<=t} k_j k_j^T     m_t = m_0 + sum_{j<=t} k_j
@@ -478,293 +479,6 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
-// cw_fwd for K <= 128 (64-token chunks) with 8 wavefronts: waves 0-3 compute with 16x16x32 MFMA
-// tiles and hold the state slice C[:, cols] (rows [K/4 w, K/4 w + K/4)) and the key sums of those
-// rows; waves 4-7 stage Q and K (row-major, two LDS buffers) one chunk ahead.  Per chunk c:
-//   phase 1  memory waves: score tiles A^T = K Q^T (causal, 10 of 16 tiles, three interleaved per
-//            wave); compute waves: C += K^T K[:, cols] and the key sums; C^T and m (hi/lo) of
-//            chunk c+1 into the other LDS buffer.  K^T and K[:, cols] operands come from the row-major K tile by
-//            transposing LDS reads.
-//   phase 2  Z = Q C_prev + A K[:, cols], running key sums, the row scalars (m_prev . q_t, gate
-//            logit, score row sums: MFMAs against broadcast operands), q_clean; stores of z,
-//            q_clean, s_t
-// ===========================================================================
-// MEAN, GATE: subtract_mean and the fused gate as template parameters (straight-line code in the
-// chunk loop)
-template <int K, bool MEAN, bool GATE>
-__global__ __launch_bounds__(kWalk8) void cw_fwd_v3_kernel(const WalkArgs a) {
-  constexpr int CB = 64, LDK = K + 16, LDA = CB + 16, NM = 256;
-  constexpr int RW = K / 4, NR16 = RW / 16;
-  __shared__ __attribute__((aligned(16))) bf16 sQ[2][CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sCh[2][32 * LDK];   // C_prev^T [col][row], hi
-  __shared__ __attribute__((aligned(16))) bf16 sCl[2][32 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sAh[CB * LDA];      // scores A[t][s] (s <= t), hi
-  __shared__ __attribute__((aligned(16))) bf16 sAl[CB * LDA];
-  __shared__ __attribute__((aligned(16))) bf16 sMW[2][4 * LDK];    // rows m_hi, m_lo, w_hi, w_lo
-  __shared__ __attribute__((aligned(16))) float sM[2][K];          // key sum before the chunk
-  __shared__ __attribute__((aligned(16))) float sLam[2][CB];
-
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
-  const WalkUnit u = walk_unit<K>(a);
-  constexpr bool mean = MEAN, gate = GATE;
-  auto chunk_len = [&](int c) { return min(CB, u.len - c * CB); };
-
-  if (w >= 4) {
-    // memory waves: Q, K (and the given lambda) of chunk c into buffer c % 2, one chunk ahead; the
-    // score tiles of the current chunk
-    const int lm = tid - NM;
-    RowsBf16<K, CB, NM> pq, pk;
-    float plam = 0.f;
-    auto load = [&](int c) {
-      const int L = chunk_len(c);
-      const long off = u.hb + (long)c * CB * u.rs;
-      pq.load((const bf16*)a.q + off, u.rs, L, lm);
-      pk.load((const bf16*)a.k + off, u.rs, L, lm);
-      if (!gate) plam = a.lam[(u.bos + (long)c * CB + min(lm & (CB - 1), L - 1)) * a.H + u.h];
-    };
-    auto stage = [&](int c) {
-      const int L = chunk_len(c), b = c & 1;
-      pq.store(sQ[b], LDK, L, lm);
-      pk.store(sK[b], LDK, L, lm);
-      if (!gate && lm < CB) sLam[b][lm] = lm < L ? plam : 0.f;
-    };
-    // score tiles of memory wave w: entries w - 4, w, w + 4 of (0,0) (1,0) (1,1) (2,0) (2,1) (2,2)
-    // (3,0) (3,1) (3,2) (3,3) as (I = t tile, J = s tile); waves 6 and 7 compute a third tile that
-    // they discard
-    int tI[3], tJ[3];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int e = (w - 4) + 4 * j < 10 ? (w - 4) + 4 * j : 0;
-      tI[j] = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
-      tJ[j] = e - tI[j] * (tI[j] + 1) / 2;
-    }
-    const bool third = w < 6;
-
-    const int cl = u.nc - 1;
-    if (u.nc > 0) {
-      load(0);
-      stage(0);
-      load(min(1, cl));
-    }
-    __syncthreads();
-    for (int c = 0; c < u.nc; ++c) {
-      // phase 1: chunk c+1 into the other buffer (last read in phase 2 of chunk c-1); loads of c+2.
-      // Past the end the last chunk is staged again into the idle buffer: every pass issues the
-      // same memory operations.
-      if (c + 1 <= cl) stage(c + 1);
-      load(min(c + 2, cl));
-      const int b = c & 1;
-      const bf16* Q = sQ[b];
-      const bf16* Kc = sK[b];
-      // score tiles A^T = K Q^T of chunk c (element (s, t), kept for s <= t), written to A[t][s]
-      {
-        f32x4 acc[3];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k0 = 0; k0 < K; k0 += 32)
-#pragma unroll
-          for (int j = 0; j < 3; ++j)
-            acc[j] = mfma16(frag16_rm(Kc + 16 * tJ[j] * LDK + k0, LDK), frag16_rm(Q + 16 * tI[j] * LDK + k0, LDK), acc[j]);
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          if (j < 2 || third) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (tI[j] == tJ[j] && 4 * (l >> 4) + i > (l & 15)) acc[j][i] = 0.f;
-            acc16_to_lds_t(acc[j], sAh + 16 * tI[j] * LDA, sAl + 16 * tI[j] * LDA, LDA, 16 * tJ[j]);
-          }
-        }
-      }
-      __syncthreads();
-      __syncthreads();
-    }
-    return;
-  }
-
-  // ---- compute waves
-  const float gbias = gate ? a.gate_b[u.h] : 0.f;
-  f32x4 C[NR16][2], Mk[NR16];
-#pragma unroll
-  for (int rt = 0; rt < NR16; ++rt) {
-    const int kr = RW * w + 16 * rt + 4 * (l >> 4);  // first of this lane's four state rows
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        C[rt][ct][i] = a.h0 ? a.h0[((long)u.unit * K + kr + i) * K + u.c0 + 16 * ct + (l & 15)] : 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) Mk[rt][i] = (mean && a.m0) ? a.m0[(long)u.unit * K + kr + i] : 0.f;
-  }
-  // state of a chunk into buffer b: C^T (hi/lo), key sum m (fp32 and hi/lo rows of sMW)
-  auto put_state = [&](int b) {
-#pragma unroll
-    for (int rt = 0; rt < NR16; ++rt) {
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-        acc16_to_lds_t(C[rt][ct], sCh[b] + 16 * ct * LDK, sCl[b] + 16 * ct * LDK, LDK, RW * w + 16 * rt);
-      if ((l & 15) == 0) {
-        const int kr = RW * w + 16 * rt + 4 * (l >> 4);
-        bf16x4 hh, ll;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bf16 x, y;
-          split2(Mk[rt][i], x, y);
-          hh[i] = x;
-          ll[i] = y;
-        }
-        *(f32x4*)(sM[b] + kr) = Mk[rt];
-        *(bf16x4*)(sMW[b] + kr) = hh;
-        *(bf16x4*)(sMW[b] + LDK + kr) = ll;
-      }
-    }
-  };
-  // gate rows of sMW (both buffers); score tiles that are never computed but are read by the
-  // 32-wide steps of phase 2 stay zero
-  for (int i = tid; i < 2 * LDK; i += NM) {
-    const int r = i / LDK + 2, cc = i % LDK;
-    bf16 hh = (bf16)0.f, ll = (bf16)0.f;
-    if (gate && cc < K) split2(a.gate_w[(long)u.h * K + cc], hh, ll);
-    sMW[0][r * LDK + cc] = r == 2 ? hh : ll;
-    sMW[1][r * LDK + cc] = r == 2 ? hh : ll;
-  }
-  for (int i = tid; i < 2 * 16 * 16; i += NM) {
-    const int tile = i / 256, e = i % 256, rr = e / 16, cc = e % 16;
-    const int I = tile == 0 ? 0 : 2, J = I + 1;  // tiles (0, 1) and (2, 3)
-    sAh[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
-    sAl[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
-  }
-  put_state(0);
-  __syncthreads();
-
-  for (int c = 0; c < u.nc; ++c) {
-    const int b = c & 1, t0 = c * CB, L = chunk_len(c);
-    const bf16* Q = sQ[b];
-    const bf16* Kc = sK[b];
-    // ---- phase 1: state update (the memory waves compute the score tiles meanwhile)
-    // state update C += K^T K[:, cols] and key sums; the state of chunk c+1 into the other buffer
-#pragma unroll
-    for (int s0 = 0; s0 < CB; s0 += 32) {
-      bf16x8 kc[2];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) kc[ct] = frag16_tr(Kc + s0 * LDK + u.c0 + 16 * ct, LDK);
-#pragma unroll
-      for (int rt = 0; rt < NR16; ++rt) {
-        const bf16x8 kr = frag16_tr(Kc + s0 * LDK + RW * w + 16 * rt, LDK);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) C[rt][ct] = mfma16(kr, kc[ct], C[rt][ct]);
-        if (mean) Mk[rt] = mfma16(kr, ones8(), Mk[rt]);
-      }
-    }
-    put_state(b ^ 1);
-    __syncthreads();
-
-    // ---- phase 2: rows [16 w, 16 w + 16): Z = Q C_prev + A K[:, cols]; running key sums; the
-    // row scalars m_prev . q_t, gate logit and sum_s A[t][s] come out of the MFMA with broadcast
-    // operands (every column holds the row's value)
-    f32x4 zacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    f32x4 cum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f}, lg = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k0 = 0; k0 < K; k0 += 32) {
-      const bf16x8 qf = frag16_rm(Q + 16 * w * LDK + k0, LDK);
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        zacc[ct] = mfma16(qf, frag16_rm(sCh[b] + 16 * ct * LDK + k0, LDK), zacc[ct]);
-        zacc[ct] = mfma16(qf, frag16_rm(sCl[b] + 16 * ct * LDK + k0, LDK), zacc[ct]);
-      }
-      if (mean) {
-        sv = mfma16(qf, frag16_rm(sMW[b] + k0, 0), sv);
-        sv = mfma16(qf, frag16_rm(sMW[b] + LDK + k0, 0), sv);
-      }
-      if (gate) {
-        lg = mfma16(qf, frag16_rm(sMW[b] + 2 * LDK + k0, 0), lg);
-        lg = mfma16(qf, frag16_rm(sMW[b] + 3 * LDK + k0, 0), lg);
-      }
-    }
-    const int smax = w < 2 ? 32 : 64;
-    for (int s0 = 0; s0 < smax; s0 += 32) {
-      const bf16x8 ah = frag16_rm(sAh + 16 * w * LDA + s0, LDA), al = frag16_rm(sAl + 16 * w * LDA + s0, LDA);
-      if (mean) {
-        sv = mfma16(ah, ones8(), sv);
-        sv = mfma16(al, ones8(), sv);
-      }
-      // lower-triangular ones: row t = 16 w + (l & 15), column s = s0 + 8 (l >> 4) + i
-      bf16x8 tri;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) tri[i] = (s0 + 8 * (l >> 4) + i <= 16 * w + (l & 15)) ? (bf16)1.f : (bf16)0.f;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const bf16x8 kf = frag16_tr(Kc + s0 * LDK + u.c0 + 16 * ct, LDK);
-        zacc[ct] = mfma16(ah, kf, zacc[ct]);
-        zacc[ct] = mfma16(al, kf, zacc[ct]);
-        if (mean) cum[ct] = mfma16(tri, kf, cum[ct]);
-      }
-    }
-    const int tb = 16 * w + 4 * (l >> 4);  // first of this lane's four rows
-    f32x4 lam, ip;
-    if (gate) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) lam[i] = tb + i < L ? __builtin_amdgcn_rcpf(1.f + __expf(-(lg[i] + gbias))) : 0.f;
-    } else {
-      lam = *(const f32x4*)(sLam[b] + tb);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ip[i] = __builtin_amdgcn_rcpf(cw_pos(t0 + tb + i, a.pos_off));
-    float qv[2][4], mc[2];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      mc[ct] = sM[b][u.c0 + 16 * ct + (l & 15)];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qv[ct][i] = (float)Q[(tb + i) * LDK + u.c0 + 16 * ct + (l & 15)];
-    }
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const long base = u.hb + (long)(t0 + tb) * u.rs + u.c0 + 16 * ct + (l & 15);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (tb + i < L) {
-          const float qo = qv[ct][i] - lam[i] * (zacc[ct][i] * ip[i] - sv[i] * ip[i] * ip[i] * (mc[ct] + cum[ct][i]));
-          gmem(a.z)[base + i * u.rs] = zacc[ct][i];
-          if (a.qc32) gmem(a.qc32)[base + i * u.rs] = qo;
-          else gmem((bf16*)a.qc)[base + i * u.rs] = (bf16)qo;
-        }
-      }
-    }
-    if (u.ct == 0 && (l & 15) == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (tb + i < L) {
-          const long ti = (u.bos + t0 + tb + i) * a.H + u.h;
-          a.srow[ti] = sv[i];
-          if (gate && a.lam_out) a.lam_out[ti] = lam[i];
-        }
-      }
-    }
-    if (mean && u.ct == 0)
-      for (int i = tid; i < K; i += NM) a.mpre[((long)(u.gc0 + c) * a.H + u.h) * K + i] = sM[b][i];
-    __syncthreads();
-  }
-
-  if (a.h_fin) {
-#pragma unroll
-    for (int rt = 0; rt < NR16; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          a.h_fin[((long)u.unit * K + RW * w + 16 * rt + 4 * (l >> 4) + i) * K + u.c0 + 16 * ct + (l & 15)] = C[rt][ct][i];
-  }
-  if (mean && u.ct == 0 && a.m_fin && (l & 15) == 0) {
-#pragma unroll
-    for (int rt = 0; rt < NR16; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a.m_fin[(long)u.unit * K + RW * w + 16 * rt + 4 * (l >> 4) + i] = Mk[rt][i];
-  }
-}
-
-// ===========================================================================
 // cw_rows: grid NTG*H, one workgroup per (chunk, head); HBM-bound.  Every thread issues all of its
 // loads up front:
 //   key sums   m_t = m_prev + prefix of k over the chunk: column c = tid % K, row segment
@@ -1006,7 +720,7 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
   __shared__ __attribute__((aligned(16))) f32x4 sR_[NBUF][CB];  // row scalars
   __shared__ float sMp_[NBUF][32], sWc[32];
 
-  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int tid = threadIdx.x, w = wave_id();
   const WalkUnit u = walk_unit<K>(a);
   const bool mean = a.subtract_mean != 0, gate = a.gate_w != nullptr;
   const int sw = w - NB, lt = tid - NB * 64;
@@ -1132,243 +846,6 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
       }
     }
     if (NBUF == 1) __syncthreads();
-  }
-}
-
-// ===========================================================================
-// cw_dq for K <= 128 (64-token chunks) with 8 wavefronts, forward walk of C.  Waves 0-3 compute (16x16
-// tiles; state slice rows [K/4 w, +K/4)); waves 4-7 stage dZ (the hi/lo pair written by cw_rows,
-// dZ_t = F_t dqc_t), K, row scalars and key sums one chunk ahead into two LDS buffers, write the
-// current chunk's dqc columns.  Per chunk c:
-//   phase 1  compute: C_prev^T (hi/lo) into LDS, C += K^T K[:, cols] (transposing LDS reads), score
-//                     tiles A^T = K dZ^T (kept for s <= t)
-//            memory:  dqc[:, cols] of c; dZ, K, row scalars, m_prev[cols] of c+1; loads of c+2
-//                     (dqc columns of c+1)
-//   phase 2  compute: dq = dqc + dZ C_prev + A K[:, cols] + ds (m_prev + running key sums)
-//                     + dlogit w[cols], in place over the dqc columns; the memory waves store its
-//                     rows at the start of the next chunk's phase 1 as 16-byte pieces
-// DQ32: the upstream gradient is fp32 (else bf16); MEAN, GATE as in cw_fwd_v3.
-// ===========================================================================
-template <int K, bool DQ32, bool MEAN, bool GATE>
-__global__ __launch_bounds__(kWalk8) void cw_dq_v3_kernel(const WalkArgs a) {
-  constexpr int CB = 64, LDK = K + 16, LDA = CB + 16, LDG = 32 + 4, NM = 256;
-  constexpr int RW = K / 4, NR16 = RW / 16;
-  __shared__ __attribute__((aligned(16))) bf16 sZh[2][CB * LDK];  // dZ rows, hi
-  __shared__ __attribute__((aligned(16))) bf16 sZl[2][CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sCh[32 * LDK];     // C_prev^T [col][row], hi
-  __shared__ __attribute__((aligned(16))) bf16 sCl[32 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sAh[CB * LDA];     // A[t][s] = dz_t . k_s (s <= t), hi
-  __shared__ __attribute__((aligned(16))) bf16 sAl[CB * LDA];
-  __shared__ __attribute__((aligned(16))) float sG[CB * LDG];     // dqc[t][cols], then dq (in place)
-  __shared__ __attribute__((aligned(16))) f32x4 sR[2][CB];        // row scalars, by chunk parity
-  __shared__ __attribute__((aligned(16))) float sMp[2][32], sWc[32];
-
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
-  const WalkUnit u = walk_unit<K>(a);
-  constexpr bool mean = MEAN, gate = GATE;
-  auto chunk_len = [&](int c) { return min(CB, u.len - c * CB); };
-  if (tid < 32) sWc[tid] = gate ? a.gate_w[(long)u.h * K + u.c0 + tid] : 0.f;
-
-  if (w >= 4) {
-    const int lm = tid - NM;
-    // dz (hi/lo, from the per-token pass), k rows, row scalars and key sums of the chunk staged
-    // next; the dqc columns of the chunk whose columns are written next
-    RowsBf16<K, CB, NM> pzh, pzl, pk;
-    RowsF32<32, CB, NM> pcol;
-    f32x4 prow = f32x4{};
-    float pmp = 0.f;
-    auto load = [&](int c) {
-      const int L = chunk_len(c);
-      const long off = u.hb + (long)c * CB * u.rs;
-      const long ti0 = (u.bos + (long)c * CB) * a.H + u.h;
-      pzh.load((const bf16*)a.dzh + off, u.rs, L, lm);
-      pzl.load((const bf16*)a.dzl + off, u.rs, L, lm);
-      pk.load((const bf16*)a.k + off, u.rs, L, lm);
-      prow = *gmem((const f32x4*)(a.sc + (ti0 + (long)min(lm & (CB - 1), L - 1) * a.H) * 4));
-      if (mean) pmp = a.mpre[((long)(u.gc0 + c) * a.H + u.h) * K + u.c0 + (lm & 31)];
-    };
-    auto load_cols = [&](int c) {
-      const long off = u.hb + (long)c * CB * u.rs + u.c0;
-      if constexpr (DQ32) pcol.load(a.dqc32 + off, u.rs, chunk_len(c), lm);
-      else pcol.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, chunk_len(c), lm);
-    };
-    // dZ (hi/lo), K, row scalars and key sums of chunk c into buffer c % 2
-    auto stage = [&](int c) {
-      const int L = chunk_len(c), b = c & 1;
-      pzh.store(sZh[b], LDK, L, lm);
-      pzl.store(sZl[b], LDK, L, lm);
-      pk.store(sK[b], LDK, L, lm);
-      if (lm < CB) sR[b][lm] = lm < L ? prow : f32x4{};
-      if (lm < 32) sMp[b][lm] = pmp;
-    };
-    // dq rows of chunk c (the compute waves leave them in sG, over the dqc columns they read):
-    // each thread stores the pieces that pcol.store overwrites next (same mapping), rows past the
-    // chunk are dropped by the buffer's range check, so every pass issues the same stores
-    auto store_dq = [&](int c) {
-      const int Lc = chunk_len(c);
-      const long base = u.hb + (long)c * CB * u.rs + u.c0;
-      const int nrec = (int)((Lc - 1) * u.rs + 32);
-      const __amdgpu_buffer_rsrc_t rs = a.dq32 ? buf_rsrc(a.dq32 + base, nrec * 4) : buf_rsrc((bf16*)a.dq + base, nrec * 2);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int idx = lm + NM * j, r = idx >> 3, cc = (idx & 7) * 4;
-        const f32x4 x = *(const f32x4*)(sG + r * LDG + cc);
-        if (a.dq32) {
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rs, (int)((r * u.rs + cc) * 4), 0, 0);
-        } else {
-          bf16x4 o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = (bf16)x[i];
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), rs, (int)((r * u.rs + cc) * 2), 0, 0);
-        }
-      }
-    };
-    // Loads are unconditional (past the end the last chunk again, staged into the idle buffer), so
-    // every pass issues the same memory operations in the same order.  At c = 0 the rows of chunk
-    // 0 are written before sG holds them and again one chunk later.
-    const int cl = u.nc - 1;
-    if (u.nc > 0) {
-      load(0);
-      load_cols(0);
-      stage(0);
-      load(min(1, cl));
-    }
-    __syncthreads();
-    for (int c = 0; c < u.nc; ++c) {
-      // phase 1: the dq rows of chunk c-1 out of sG, then the dqc columns of chunk c into it
-      store_dq(max(c - 1, 0));
-      pcol.store(sG, LDG, chunk_len(c), lm);
-      load_cols(min(c + 1, cl));
-      stage(min(c + 1, cl));
-      load(min(c + 2, cl));
-      __syncthreads();
-      __syncthreads();
-    }
-    if (u.nc > 0) store_dq(cl);  // written before the last barrier
-    return;
-  }
-
-  // ---- compute waves
-  f32x4 C[NR16][2];
-#pragma unroll
-  for (int rt = 0; rt < NR16; ++rt) {
-    const int kr = RW * w + 16 * rt + 4 * (l >> 4);
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        C[rt][ct][i] = a.h0 ? a.h0[((long)u.unit * K + kr + i) * K + u.c0 + 16 * ct + (l & 15)] : 0.f;
-  }
-  for (int i = tid; i < 2 * 16 * 16; i += NM) {
-    const int tile = i / 256, e = i % 256, rr = e / 16, cc = e % 16;
-    const int I = tile == 0 ? 0 : 2, J = I + 1;  // tiles (0, 1) and (2, 3) stay zero
-    sAh[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
-    sAl[(16 * I + rr) * LDA + 16 * J + cc] = (bf16)0.f;
-  }
-  __syncthreads();
-  // score tiles of wave w: entries w, w + 4, w + 8 of (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0)
-  // (3,1) (3,2) (3,3) as (I = t tile, J = s tile); waves 2 and 3 compute a third tile that they
-  // discard
-  int tI[3], tJ[3];
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const int e = w + 4 * j < 10 ? w + 4 * j : 0;
-    tI[j] = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
-    tJ[j] = e - tI[j] * (tI[j] + 1) / 2;
-  }
-  const bool third = w < 2;
-  for (int c = 0; c < u.nc; ++c) {
-    const int b = c & 1, t0 = c * CB, L = chunk_len(c);
-    const bf16* Kc = sK[b];
-    // ---- phase 1: C_prev^T (hi/lo) for phase 2, then C += K^T K[:, cols]
-#pragma unroll
-    for (int rt = 0; rt < NR16; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-        acc16_to_lds_t(C[rt][ct], sCh + 16 * ct * LDK, sCl + 16 * ct * LDK, LDK, RW * w + 16 * rt);
-#pragma unroll
-    for (int s0 = 0; s0 < CB; s0 += 32) {
-      bf16x8 kc[2];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) kc[ct] = frag16_tr(Kc + s0 * LDK + u.c0 + 16 * ct, LDK);
-#pragma unroll
-      for (int rt = 0; rt < NR16; ++rt) {
-        const bf16x8 kr = frag16_tr(Kc + s0 * LDK + RW * w + 16 * rt, LDK);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) C[rt][ct] = mfma16(kr, kc[ct], C[rt][ct]);
-      }
-    }
-    // score tiles A^T = K dZ^T of this chunk (element (s, t), kept for s <= t), written to A[t][s]
-    {
-      f32x4 acc[3];
-#pragma unroll
-      for (int j = 0; j < 3; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k0 = 0; k0 < K; k0 += 32)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          const bf16x8 kf = frag16_rm(Kc + 16 * tJ[j] * LDK + k0, LDK);
-          acc[j] = mfma16(kf, frag16_rm(sZh[b] + 16 * tI[j] * LDK + k0, LDK), acc[j]);
-          acc[j] = mfma16(kf, frag16_rm(sZl[b] + 16 * tI[j] * LDK + k0, LDK), acc[j]);
-        }
-#pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        if (j < 2 || third) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (tI[j] == tJ[j] && 4 * (l >> 4) + i > (l & 15)) acc[j][i] = 0.f;
-          acc16_to_lds_t(acc[j], sAh + 16 * tI[j] * LDA, sAl + 16 * tI[j] * LDA, LDA, 16 * tJ[j]);
-        }
-      }
-    }
-    __syncthreads();
-
-    // ---- phase 2: rows [16 w, 16 w + 16) of dq
-    f32x4 x[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    f32x4 cum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int k0 = 0; k0 < K; k0 += 32) {
-      const bf16x8 zh = frag16_rm(sZh[b] + 16 * w * LDK + k0, LDK), zl = frag16_rm(sZl[b] + 16 * w * LDK + k0, LDK);
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const bf16x8 ch = frag16_rm(sCh + 16 * ct * LDK + k0, LDK);
-        x[ct] = mfma16(zh, ch, x[ct]);
-        x[ct] = mfma16(zh, frag16_rm(sCl + 16 * ct * LDK + k0, LDK), x[ct]);
-        x[ct] = mfma16(zl, ch, x[ct]);
-      }
-    }
-    const int smax = w < 2 ? 32 : 64;
-    for (int s0 = 0; s0 < smax; s0 += 32) {
-      const bf16x8 ah = frag16_rm(sAh + 16 * w * LDA + s0, LDA), al = frag16_rm(sAl + 16 * w * LDA + s0, LDA);
-      bf16x8 tri;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) tri[i] = (s0 + 8 * (l >> 4) + i <= 16 * w + (l & 15)) ? (bf16)1.f : (bf16)0.f;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const bf16x8 kf = frag16_tr(Kc + s0 * LDK + u.c0 + 16 * ct, LDK);
-        x[ct] = mfma16(ah, kf, x[ct]);
-        x[ct] = mfma16(al, kf, x[ct]);
-        if (mean) cum[ct] = mfma16(tri, kf, cum[ct]);
-      }
-    }
-    const int tb = 16 * w + 4 * (l >> 4);
-    f32x4 rw[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rw[i] = sR[b][tb + i];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int cc = 16 * ct + (l & 15);
-      const float mc = sMp[b][cc], wc = sWc[cc];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float d = sG[(tb + i) * LDG + cc] + x[ct][i];
-        if (mean) d += rw[i][1] * (mc + cum[ct][i]);
-        if (gate) d += rw[i][2] * wc;
-        sG[(tb + i) * LDG + cc] = d;
-      }
-    }
-    __syncthreads();
   }
 }
 
@@ -1586,296 +1063,6 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
-// cw_dk for K <= 128 (64-token chunks) with 8 wavefronts, reverse walk of E = G + G^T.  Waves 0-3
-// (output waves) compute the score tiles and the dk rows; waves 4-7 (state waves) hold E[:, cols]
-// (and G when DH0) as 16x16 tiles (rows [K/4 (w-4), +K/4)), load the chunk operands one chunk ahead
-// and update the state.  Three barriers per chunk, one LDS buffer per tile:
-//   stage    state waves: Q, K, dZ (the hi/lo pair written by cw_rows), row scalars, dk_extra
-//            columns, carry; E^T (hi/lo) of the later chunks
-//   phase 1  output waves: B1[j][t] = dz_t . k_j, B2[j][t] = q_t . k_j (t >= j) as 16x16 tiles;
-//            state waves: loads of chunk c-1, E += Q^T dZ[:, cols] + dZ^T Q[:, cols] (G += Q^T dZ)
-//            with transposing LDS reads
-//   phase 2  output waves: dk = K E + (B1 + ds) Q[:, cols] + (B2 - s/pos) dZ[:, cols] + carry
-//            (+ dk_extra); the masked diagonal terms enter as their own hi/lo fragments
-// ===========================================================================
-template <int K, bool DH0, bool MEAN>
-__global__ __launch_bounds__(kWalk8) void cw_dk_v3_kernel(const WalkArgs a) {
-  constexpr int CB = 64, LDK = K + 16, LDA = CB + 16, LDX = 32 + 4, NM = 256;
-  constexpr int RW = K / 4, NR16 = RW / 16;
-  __shared__ __attribute__((aligned(16))) bf16 sQ[CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sK[CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sZh[CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sZl[CB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sEh[32 * LDK];    // E^T [col][row], hi
-  __shared__ __attribute__((aligned(16))) bf16 sEl[32 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sB1h[CB * LDA];   // [j][t] = dz_t . k_j (t >= j), hi
-  __shared__ __attribute__((aligned(16))) bf16 sB1l[CB * LDA];
-  __shared__ __attribute__((aligned(16))) bf16 sB2h[CB * LDA];   // [j][t] = q_t . k_j (t >= j), hi
-  __shared__ __attribute__((aligned(16))) bf16 sB2l[CB * LDA];
-  __shared__ __attribute__((aligned(16))) float sX[CB * LDX];    // dk_extra[t][cols]
-  __shared__ __attribute__((aligned(16))) float sDs[CB], sSp[CB];  // ds_t, -s_t/pos_t
-  __shared__ __attribute__((aligned(16))) float sCar[32];          // carry of this chunk
-  __shared__ __attribute__((aligned(16))) float sO[CB * LDX];      // dk[t][cols] of the chunk just done
-
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
-  const WalkUnit u = walk_unit<K>(a);
-  constexpr bool mean = MEAN;
-  auto chunk_len = [&](int c) { return min(CB, u.len - c * CB); };
-
-  if (w >= 4) {
-    // ---- state waves
-    const int lm = tid - NM, sw = w - 4;
-    f32x4 E[NR16][2], G[NR16][2];  // G is dead unless DH0
-#pragma unroll
-    for (int rt = 0; rt < NR16; ++rt) {
-      const int kr = RW * sw + 16 * rt + 4 * (l >> 4);
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int cc = u.c0 + 16 * ct + (l & 15);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float* dhf = a.dh_fin ? a.dh_fin + (long)u.unit * K * K : nullptr;
-          const float g = dhf ? dhf[(long)(kr + i) * K + cc] : 0.f;
-          const float gt = dhf ? dhf[(long)cc * K + kr + i] : 0.f;
-          G[rt][ct][i] = g;
-          E[rt][ct][i] = g + gt;
-        }
-      }
-    }
-    float car = (lm < 32 && mean && a.dm_fin) ? a.dm_fin[(long)u.unit * K + u.c0 + lm] : 0.f;
-    RowsBf16<K, CB, NM> pq, pk, pzh, pzl;
-    RowsF32<32, CB, NM> px;
-    f32x4 prow = f32x4{};
-    float pdm = 0.f;
-    auto load = [&](int c) {
-      const int L = chunk_len(c);
-      const long off = u.hb + (long)c * CB * u.rs;
-      const long ti0 = (u.bos + (long)c * CB) * a.H + u.h;
-      pq.load((const bf16*)a.q + off, u.rs, L, lm);
-      pk.load((const bf16*)a.k + off, u.rs, L, lm);
-      pzh.load((const bf16*)a.dzh + off, u.rs, L, lm);
-      pzl.load((const bf16*)a.dzl + off, u.rs, L, lm);
-      if (a.dk_extra) px.load(a.dk_extra + off + u.c0, u.rs, L, lm);
-      prow = *gmem((const f32x4*)(a.sc + (ti0 + (long)min(lm & (CB - 1), L - 1) * a.H) * 4));
-      if (mean) pdm = a.dmsum[((long)(u.gc0 + c) * a.H + u.h) * K + u.c0 + (lm & 31)];
-    };
-    // dk rows of chunk c (written by the output waves into sO) as 16-byte pieces; rows past the chunk
-    // write row L - 1 again (same value, same address), so every pass issues the same stores
-    auto store_dk = [&](int c) {
-      const int Lc = chunk_len(c);
-      const long base = u.hb + (long)c * CB * u.rs + u.c0;
-      if (a.dk32) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int idx = lm + NM * j, r = min(idx >> 3, Lc - 1), cc = (idx & 7) * 4;
-          *gmem((f32x4*)(a.dk32 + base + (long)r * u.rs + cc)) = *(const f32x4*)(sO + r * LDX + cc);
-        }
-      } else {
-        const int r = min(lm >> 2, Lc - 1), cc = (lm & 3) * 8;
-        const f32x4 x0 = *(const f32x4*)(sO + r * LDX + cc), x1 = *(const f32x4*)(sO + r * LDX + cc + 4);
-        bf16x8 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          o[i] = (bf16)x0[i];
-          o[4 + i] = (bf16)x1[i];
-        }
-        *gmem((bf16x8*)((bf16*)a.dk + base + (long)r * u.rs + cc)) = o;
-      }
-    };
-    const int cl = u.nc - 1;
-    if (u.nc > 0) load(cl);
-    for (int c = cl; c >= 0; --c) {
-      const int L = chunk_len(c);
-      // ---- stage (and the dk rows of chunk c + 1; at c = cl the buffer holds no chunk yet and the
-      // rows written to chunk cl are written again with its values one chunk later)
-      pq.store(sQ, LDK, L, lm);
-      pk.store(sK, LDK, L, lm);
-      pzh.store(sZh, LDK, L, lm);
-      pzl.store(sZl, LDK, L, lm);
-      if (a.dk_extra) px.store(sX, LDX, L, lm);
-      store_dk(min(c + 1, cl));
-      if (lm < CB) {
-        sDs[lm] = lm < L ? prow[1] : 0.f;
-        sSp[lm] = lm < L ? prow[3] : 0.f;
-      }
-      if (lm < 32) {
-        sCar[lm] = car;
-        car += pdm;
-      }
-#pragma unroll
-      for (int rt = 0; rt < NR16; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-          acc16_to_lds_t(E[rt][ct], sEh + 16 * ct * LDK, sEl + 16 * ct * LDK, LDK, RW * sw + 16 * rt);
-      __syncthreads();
-      // ---- phase 1: loads of chunk c-1 (chunk 0 again at the start: every pass issues the same
-      // memory operations), state update
-      load(max(c - 1, 0));
-#pragma unroll
-      for (int t0 = 0; t0 < CB; t0 += 32) {
-        bf16x8 qc[2], zch[2], zcl[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          qc[ct] = frag16_tr(sQ + t0 * LDK + u.c0 + 16 * ct, LDK);
-          zch[ct] = frag16_tr(sZh + t0 * LDK + u.c0 + 16 * ct, LDK);
-          zcl[ct] = frag16_tr(sZl + t0 * LDK + u.c0 + 16 * ct, LDK);
-        }
-#pragma unroll
-        for (int rt = 0; rt < NR16; ++rt) {
-          const int m0 = RW * sw + 16 * rt;
-          const bf16x8 qr = frag16_tr(sQ + t0 * LDK + m0, LDK);
-          const bf16x8 zrh = frag16_tr(sZh + t0 * LDK + m0, LDK), zrl = frag16_tr(sZl + t0 * LDK + m0, LDK);
-#pragma unroll
-          for (int ct = 0; ct < 2; ++ct) {
-            if constexpr (DH0) {
-              G[rt][ct] = mfma16(qr, zch[ct], G[rt][ct]);
-              G[rt][ct] = mfma16(qr, zcl[ct], G[rt][ct]);
-            }
-            E[rt][ct] = mfma16(qr, zch[ct], E[rt][ct]);
-            E[rt][ct] = mfma16(qr, zcl[ct], E[rt][ct]);
-            E[rt][ct] = mfma16(zrh, qc[ct], E[rt][ct]);
-            E[rt][ct] = mfma16(zrl, qc[ct], E[rt][ct]);
-          }
-        }
-      }
-      __syncthreads();
-      __syncthreads();
-    }
-    if constexpr (DH0) {
-#pragma unroll
-      for (int rt = 0; rt < NR16; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            a.dh0[((long)u.unit * K + RW * sw + 16 * rt + 4 * (l >> 4) + i) * K + u.c0 + 16 * ct + (l & 15)] =
-                G[rt][ct][i];
-    }
-    if (a.dm0 && lm < 32) a.dm0[(long)u.unit * K + u.c0 + lm] = mean ? car : 0.f;
-    // chunk 0's dk rows (written by the output waves before the last barrier)
-    if (u.nc > 0) store_dk(0);
-    return;
-  }
-
-  // ---- output waves
-  // score tile pairs of wave w: entries w, w + 4, w + 8 of (T, J) = (0,0) (1,0) (1,1) (2,0) (2,1)
-  // (2,2) (3,0) (3,1) (3,2) (3,3) (T = t tile, J = j tile, T >= J); waves 2 and 3 compute a third
-  // pair that they discard.  Tiles (J, T) = (1, 0) and (3, 2) are read by the 32-wide steps of
-  // phase 2 and stay zero.
-  int tT[3], tJ[3];
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const int e = w + 4 * j < 10 ? w + 4 * j : 0;
-    tT[j] = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
-    tJ[j] = e - tT[j] * (tT[j] + 1) / 2;
-  }
-  const bool third = w < 2;
-  for (int i = tid; i < 2 * 16 * 16; i += NM) {
-    const int tile = i / 256, e = i % 256, rr = e / 16, cc = e % 16;
-    const int J = tile == 0 ? 1 : 3, T = J - 1;
-    const int o = (16 * J + rr) * LDA + 16 * T + cc;
-    sB1h[o] = (bf16)0.f;
-    sB1l[o] = (bf16)0.f;
-    sB2h[o] = (bf16)0.f;
-    sB2l[o] = (bf16)0.f;
-  }
-  for (int c = u.nc - 1; c >= 0; --c) {
-    __syncthreads();
-    // ---- phase 1: score tiles, element (t, j) = (16 T + 4 (l >> 4) + i, 16 J + (l & 15)), kept for
-    // t >= j, written transposed to [j][t]
-    {
-      f32x4 b1[3], b2[3];
-#pragma unroll
-      for (int j = 0; j < 3; ++j) b1[j] = b2[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k0 = 0; k0 < K; k0 += 32)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          const bf16x8 kf = frag16_rm(sK + 16 * tJ[j] * LDK + k0, LDK);
-          b1[j] = mfma16(frag16_rm(sZh + 16 * tT[j] * LDK + k0, LDK), kf, b1[j]);
-          b1[j] = mfma16(frag16_rm(sZl + 16 * tT[j] * LDK + k0, LDK), kf, b1[j]);
-          b2[j] = mfma16(frag16_rm(sQ + 16 * tT[j] * LDK + k0, LDK), kf, b2[j]);
-        }
-#pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        if (j < 2 || third) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (tT[j] == tJ[j] && 4 * (l >> 4) + i < (l & 15)) b1[j][i] = b2[j][i] = 0.f;
-          acc16_to_lds_t(b1[j], sB1h + 16 * tJ[j] * LDA, sB1l + 16 * tJ[j] * LDA, LDA, 16 * tT[j]);
-          acc16_to_lds_t(b2[j], sB2h + 16 * tJ[j] * LDA, sB2l + 16 * tJ[j] * LDA, LDA, 16 * tT[j]);
-        }
-      }
-    }
-    __syncthreads();
-
-    // ---- phase 2: dk rows j in [16 w, 16 w + 16)
-    f32x4 x[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int k0 = 0; k0 < K; k0 += 32) {
-      const bf16x8 kf = frag16_rm(sK + 16 * w * LDK + k0, LDK);
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        x[ct] = mfma16(kf, frag16_rm(sEh + 16 * ct * LDK + k0, LDK), x[ct]);
-        x[ct] = mfma16(kf, frag16_rm(sEl + 16 * ct * LDK + k0, LDK), x[ct]);
-      }
-    }
-    const int tmin = w < 2 ? 0 : 32;
-    for (int t0 = tmin; t0 < CB; t0 += 32) {
-      const bf16x8 b1h = frag16_rm(sB1h + 16 * w * LDA + t0, LDA), b1l = frag16_rm(sB1l + 16 * w * LDA + t0, LDA);
-      const bf16x8 b2h = frag16_rm(sB2h + 16 * w * LDA + t0, LDA), b2l = frag16_rm(sB2l + 16 * w * LDA + t0, LDA);
-      // masked diagonals: row j = 16 w + (l & 15), column t = t0 + 8 (l >> 4) + i: ds_t [t >= j]
-      // against q, -s_t/pos_t [t >= j] against dz
-      bf16x8 dh, dl, ph, pl;
-      if (mean) {
-        const int tb = t0 + 8 * (l >> 4), jr = 16 * w + (l & 15);
-        const f32x4 d0 = *(const f32x4*)(sDs + tb), d1 = *(const f32x4*)(sDs + tb + 4);
-        const f32x4 p0 = *(const f32x4*)(sSp + tb), p1 = *(const f32x4*)(sSp + tb + 4);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const bool keep = tb + i >= jr;
-          bf16 a1, a2, a3, a4;
-          split2(keep ? (i < 4 ? d0[i] : d1[i - 4]) : 0.f, a1, a2);
-          split2(keep ? (i < 4 ? p0[i] : p1[i - 4]) : 0.f, a3, a4);
-          dh[i] = a1;
-          dl[i] = a2;
-          ph[i] = a3;
-          pl[i] = a4;
-        }
-      }
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const bf16x8 qf = frag16_tr(sQ + t0 * LDK + u.c0 + 16 * ct, LDK);
-        const bf16x8 zhf = frag16_tr(sZh + t0 * LDK + u.c0 + 16 * ct, LDK);
-        const bf16x8 zlf = frag16_tr(sZl + t0 * LDK + u.c0 + 16 * ct, LDK);
-        x[ct] = mfma16(b1h, qf, x[ct]);
-        x[ct] = mfma16(b1l, qf, x[ct]);
-        x[ct] = mfma16(b2h, zhf, x[ct]);
-        x[ct] = mfma16(b2h, zlf, x[ct]);
-        x[ct] = mfma16(b2l, zhf, x[ct]);
-        if (mean) {
-          x[ct] = mfma16(dh, qf, x[ct]);
-          x[ct] = mfma16(dl, qf, x[ct]);
-          x[ct] = mfma16(ph, zhf, x[ct]);
-          x[ct] = mfma16(ph, zlf, x[ct]);
-          x[ct] = mfma16(pl, zhf, x[ct]);
-        }
-      }
-    }
-    const int jb = 16 * w + 4 * (l >> 4);
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int cc = 16 * ct + (l & 15);
-      const float car = sCar[cc];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        sO[(jb + i) * LDX + cc] = x[ct][i] + car + (a.dk_extra ? sX[(jb + i) * LDX + cc] : 0.f);
-    }
-    __syncthreads();
-  }
-}
-
-// ===========================================================================
 // launcher
 // ===========================================================================
 namespace {
@@ -1885,57 +1072,19 @@ hipError_t cwalk_k(int stage, const WalkArgs& a, hipStream_t st) {
   const long units = (long)a.N * a.H * (K / 32);
   switch (stage) {
     case kWalkFwd:
-      if (units > 0) {
-        if (K == 64 || K == 128) {
-          constexpr int KW = K == 64 ? 64 : 128;
-          const bool mean = a.subtract_mean != 0, gate = a.gate_w != nullptr;
-          const dim3 grid((unsigned)units), block(kWalk8);
-          if (mean && gate) hipLaunchKernelGGL((cw_fwd_v3_kernel<KW, true, true>), grid, block, 0, st, a);
-          else if (mean) hipLaunchKernelGGL((cw_fwd_v3_kernel<KW, true, false>), grid, block, 0, st, a);
-          else if (gate) hipLaunchKernelGGL((cw_fwd_v3_kernel<KW, false, true>), grid, block, 0, st, a);
-          else hipLaunchKernelGGL((cw_fwd_v3_kernel<KW, false, false>), grid, block, 0, st, a);
-        } else
-          hipLaunchKernelGGL(cw_fwd_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);
-      }
+      if (units > 0) hipLaunchKernelGGL(cw_fwd_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);
       break;
     case kWalkRows:
       if ((long)a.NTG * a.H > 0)
         hipLaunchKernelGGL(cw_rows_kernel<K>, dim3((unsigned)((long)a.NTG * a.H)), dim3(kThreads), 0, st, a);
       break;
     case kWalkDq:
-      if (units > 0) {
-        if (K == 64 || K == 128) {
-          constexpr int KW = K == 64 ? 64 : 128;
-          const dim3 grid((unsigned)units), block(kWalk8);
-          const int sel = (a.dqc32 ? 4 : 0) + (a.subtract_mean ? 2 : 0) + (a.gate_w ? 1 : 0);
-#define CCQ_DQ3(S, A, B, C) \
-  case S: hipLaunchKernelGGL((cw_dq_v3_kernel<KW, A, B, C>), grid, block, 0, st, a); break;
-          switch (sel) {
-            CCQ_DQ3(0, false, false, false) CCQ_DQ3(1, false, false, true) CCQ_DQ3(2, false, true, false)
-            CCQ_DQ3(3, false, true, true) CCQ_DQ3(4, true, false, false) CCQ_DQ3(5, true, false, true)
-            CCQ_DQ3(6, true, true, false) CCQ_DQ3(7, true, true, true)
-          }
-#undef CCQ_DQ3
-        } else {
-          hipLaunchKernelGGL(cw_dq_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);
-        }
-      }
+      if (units > 0) hipLaunchKernelGGL(cw_dq_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);
       break;
     case kWalkDk:
       if (units > 0) {
-        if (K == 64 || K == 128) {
-          constexpr int KW = K == 64 ? 64 : 128;
-          const dim3 grid((unsigned)units), block(kWalk8);
-          const bool dh0 = a.dh0 != nullptr, mean = a.subtract_mean != 0;
-          if (dh0 && mean) hipLaunchKernelGGL((cw_dk_v3_kernel<KW, true, true>), grid, block, 0, st, a);
-          else if (dh0) hipLaunchKernelGGL((cw_dk_v3_kernel<KW, true, false>), grid, block, 0, st, a);
-          else if (mean) hipLaunchKernelGGL((cw_dk_v3_kernel<KW, false, true>), grid, block, 0, st, a);
-          else hipLaunchKernelGGL((cw_dk_v3_kernel<KW, false, false>), grid, block, 0, st, a);
-        } else if (a.dh0) {
-          hipLaunchKernelGGL((cw_dk_kernel<K, true>), dim3((unsigned)units), dim3(kThreads), 0, st, a);
-        } else {
-          hipLaunchKernelGGL((cw_dk_kernel<K, false>), dim3((unsigned)units), dim3(kThreads), 0, st, a);
-        }
+        if (a.dh0) hipLaunchKernelGGL((cw_dk_kernel<K, true>), dim3((unsigned)units), dim3(kThreads), 0, st, a);
+        else hipLaunchKernelGGL((cw_dk_kernel<K, false>), dim3((unsigned)units), dim3(kThreads), 0, st, a);
       }
       break;
     default:
@@ -1948,9 +1097,8 @@ hipError_t cwalk_k(int stage, const WalkArgs& a, hipStream_t st) {
 
 hipError_t launch_cwalk(int stage, const WalkArgs& a, hipStream_t st) {
   switch (a.K) {
+    // (K = 64 and 128 run as segment walks)
     case 32: return cwalk_k<32>(stage, a, st);
-    case 64: return cwalk_k<64>(stage, a, st);
-    case 128: return cwalk_k<128>(stage, a, st);
     case 256: return cwalk_k<256>(stage, a, st);
     default: return hipErrorInvalidValue;
   }
