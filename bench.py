@@ -67,34 +67,57 @@ def gpu_step(x):
 
 MULTI_KERNEL_STAGES = ("clean_bwd_gate",)
 
-# HBM bytes per launch at the metric shape, measured with rocprofv3 --pmc FETCH_SIZE and
-# --pmc WRITE_SIZE on this workload (bench.py --copy-calibration), each scaled by the counter's
-# reading for a known-size elementwise copy (fetch x2.000, write x1.000).  Re-measured whenever a
-# kernel changes; a stage absent here reports traffic null.
-MEASURED_TRAFFIC_BYTES = {
-    "gdn_bwd_dqkw": (1166.9e6, 419.4e6),
-    "gdn_fwd_state": (478.5e6, 537.5e6),
-    "gdn_bwd_state": (478.4e6, 402.7e6),
-    "clean_bwd_dk": (438.6e6, 67.1e6),
-    "clean_fwd": (148.9e6, 287.3e6),
-    "clean_bwd_dq": (371.6e6, 67.1e6),
-    "gdn_bwd_wy": (638.0e6, 218.1e6),
-    "clean_bwd_rows": (428.8e6, 153.6e6),
-    "gdn_prep": (151.3e6, 343.9e6),
+# HBM bytes per launch at the metric shape, read from the committed rocprofv3 FETCH_SIZE /
+# WRITE_SIZE summary (written by `bench.py --ingest-pmc`, which scales the counters by the
+# reading for a known-size copy); a stage absent there reports traffic null.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_fused_ccq_gdn_B8_T4096_H8_K128.json")
+
+
+def measured_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return {k: tuple(v) for k, v in json.load(f)["per_launch_bytes"].items()}
+    except (OSError, ValueError, KeyError):
+        return {}
+
+
+# Compulsory work per token x head of each phase of the step, as the survey's measurement section
+# defines it: FLOP (dense BT x BT tiles, fwd+bwd = 3 x fwd, the backward = 2 x fwd) and bytes (each
+# input read once, each output written once, bf16 activations, fp32 lambda / g / beta).
+def phase_work(k=K, v=V, bt=BT):
+    clean_fwd = 4 * k * k + 4 * bt * k
+    gdn_fwd = 6 * k * v + bt * (6 * k + 4 * v) + (2 * bt * bt) // 3
+    return {
+        "cleaning fwd": (clean_fwd, 6 * k + 4),
+        "cleaning bwd": (2 * clean_fwd, 10 * k + 8),
+        "GDN fwd": (gdn_fwd, 4 * k + 4 * v + 8),
+        "GDN bwd": (2 * gdn_fwd, 8 * k + 6 * v + 16),
+    }
+
+
+PHASE_OF = {
+    "clean_fwd_sum": "cleaning fwd", "clean_fwd": "cleaning fwd",
+    "clean_bwd_dq": "cleaning bwd", "clean_bwd_gsum": "cleaning bwd", "clean_bwd_dk": "cleaning bwd",
+    "clean_bwd_gate": "cleaning bwd",
+    "gdn_prep": "GDN fwd", "gdn_fwd_state": "GDN fwd",
+    "gdn_bwd_state": "GDN bwd", "gdn_bwd_dqkw": "GDN bwd", "gdn_bwd_wy": "GDN bwd",
 }
 
 
 def kernel_work(k=K, v=V, bt=BT, cb=64):
-    """Algorithmic FLOP and bytes per token x head of each timed stage (its own inputs read once,
-    its own outputs written once), for the metric's call (fp32 q_clean into the delta rule, fp32
-    upstream gradients, bf16 dq / dk).  Cleaning walks over cb-token chunks: per token a K x K state
-    read and update (2 K^2 each) plus causal scores over the chunk (K cb per product, two products
-    forward / dq, four in the dk walk with a second K x K update)."""
+    """The design's own FLOP and bytes per token x head of each timed stage (its inputs read once,
+    its outputs written once, in the formats this implementation uses: fp32 q_clean into the
+    delta rule, fp32 upstream gradients, per-chunk state snapshots), for comparison with the
+    compulsory figures of phase_work()."""
+    # fp32 K x K totals of 4 time segments per (sequence, head), each written once and read by
+    # the later segments: about 4 K^2 bytes per segment of T / 4 tokens
+    seg = 4 * k * k * 4 // T
     return {
-        "clean_fwd": (4 * k * k + 2 * k * cb, 2 * k + 2 * k + 4 + 4 * k + 4 * k + 4 + 4 * k // cb),
-        "clean_bwd_rows": (6 * k, 4 * k + 4 * k + 2 * k + 2 * k + 4 + 4 + 4 * k // cb + 16 + 4 * k // cb + 4 * k),
-        "clean_bwd_dq": (4 * k * k + 2 * k * cb, 4 * k + 2 * k + 16 + 4 * k // cb + 2 * k),
-        "clean_bwd_dk": (6 * k * k + 4 * k * cb, 2 * k + 2 * k + 4 * k + 16 + 4 * k + 2 * k),
+        "clean_fwd_sum": (2 * k * k, 2 * k + seg),
+        "clean_fwd": (4 * k * k + 4 * k * cb, 2 * k + 2 * k + 4 * k + 4 + seg),
+        "clean_bwd_dq": (6 * k * k + 8 * k * cb, 2 * k + 2 * k + 4 * k + 4 + 2 * k + 16 + seg),
+        "clean_bwd_gsum": (2 * k * k + 2 * k * cb, 2 * k + 4 * k + 16 + seg),
+        "clean_bwd_dk": (6 * k * k + 8 * k * cb, 2 * k + 2 * k + 4 * k + 16 + 4 * k + 2 * k + seg),
         "gdn_prep": (2 * bt * (2 * k + v) + (2 * bt * bt) // 3, 2 * k + 2 * v + 8 + 2 * k + 4 * v + 4 + 4 * bt),
         # the forward walk with the chunk output fused in: state path (U = u - w S, S update) plus
         # Y = Qc S, P = Qc K^T and P U; reads k, w / wl, Qc (fp32), g, u; writes U, o, P^T and the
@@ -109,25 +132,38 @@ def kernel_work(k=K, v=V, bt=BT, cb=64):
     }
 
 
-def roofline(step_kernel_ms, launches_per_step):
-    """Roofline object for the kernel with the largest share of the step."""
-    work = kernel_work()
-    # stages that launch several kernels (the gate's two row sums) are left out so that the average
-    # launch time compares one-to-one with a kernel trace
-    single = [n for n in step_kernel_ms if n in work and n not in MULTI_KERNEL_STAGES]
+def step_roofline(ms_per_step, units=B * T * H):
+    """Whole step against min(MFMA peak, AI x HBM bandwidth) with the compulsory figures."""
+    flop = sum(f for f, _ in phase_work().values()) * units
+    byts = sum(b for _, b in phase_work().values()) * units
+    ideal_s = max(flop / PEAK_BF16, byts / PEAK_HBM)
+    return {"flop": flop, "bytes": byts, "ai": flop / byts, "bound": "hbm" if byts / PEAK_HBM >= flop / PEAK_BF16
+            else "mfma", "ideal_us": ideal_s * 1e6, "frac": ideal_s / (ms_per_step * 1e-3)}
+
+
+def roofline(step_kernel_ms, launches_per_step, units=B * T * H):
+    """Roofline object for the kernel with the largest share of the step.  Its algorithmic work is
+    the compulsory work of the whole phase it belongs to (phase_work(): the survey defines it per
+    phase, not per kernel), charged to this one kernel -- an upper bound of the kernel's share, so
+    `frac` is an upper bound too.  The design's own per-kernel bytes are kept beside it."""
+    single = [n for n in step_kernel_ms if n in PHASE_OF and n not in MULTI_KERNEL_STAGES]
     name = max(single, key=lambda n: step_kernel_ms[n])
-    flop, byts = work[name]
-    units = B * T * H
+    phase = PHASE_OF[name]
+    flop, byts = phase_work()[phase]
     avg_s = step_kernel_ms[name] / launches_per_step[name] * 1e-3
-    ai = flop / byts
-    if ai >= PEAK_BF16 / PEAK_HBM:
+    if flop / byts >= PEAK_BF16 / PEAK_HBM:
         achieved, peak, unit, bound = flop * units / avg_s / 1e12, PEAK_BF16 / 1e12, "TFLOP/s", "mfma"
     else:
         achieved, peak, unit, bound = byts * units / avg_s / 1e9, PEAK_HBM / 1e9, "GB/s", "hbm"
-    traffic = sum(MEASURED_TRAFFIC_BYTES[name]) if name in MEASURED_TRAFFIC_BYTES else None
-    return {"kernel": name, "bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
-            "frac": achieved / peak, "traffic": traffic, "avg_launch_us": avg_s * 1e6,
-            "algorithmic_flop_per_launch": flop * units, "algorithmic_bytes_per_launch": byts * units}
+    traffic = measured_traffic().get(name)
+    dflop, dbytes = kernel_work()[name]
+    return {"kernel": name, "phase": phase, "bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+            "frac": achieved / peak, "traffic": sum(traffic) if traffic else None,
+            "avg_launch_us": avg_s * 1e6, "algorithmic_flop_per_launch": flop * units,
+            "algorithmic_bytes_per_launch": byts * units,
+            "attribution": f"compulsory work of the whole {phase} phase charged to this kernel (upper bound)",
+            "design_bytes_per_launch": dbytes * units, "design_flop_per_launch": dflop * units,
+            "mfma_frac_design_flop": dflop * units / avg_s / PEAK_BF16}
 
 
 def cpu_baseline(seconds_budget=25.0):
@@ -160,21 +196,26 @@ def cpu_baseline(seconds_budget=25.0):
                       f"median of {len(times)} after 1 warm-up"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="after the timed steps, run one elementwise copy of 512 MiB (read) + 512 MiB (write), "
-                         "the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counts")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for {args.gpus}); this build has no multi-GPU path",
-              file=sys.stderr)
-        sys.exit(2)
-    dev = torch.device("cuda:0")
+def _timed_steps(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def _line(metric, value, unit, args, ms, dtype, data, config, higher=True, **extra):
+    out = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": ms, "higher_is_better": higher, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+           "data": data, "config": config}
+    out.update(extra)
+    return out
+
+
+def run_c1(args, dev):
     x = make_inputs(dev)
     for n in LEAVES:
         x[n].requires_grad_()
@@ -203,29 +244,209 @@ def main():
         if n:
             kms[name], klaunch[name] = ms_tot / args.steps, n / args.steps
     ms = elapsed / args.steps * 1e3
-    tokens_per_s = B * T * args.steps / elapsed
     flops = FLOP_PER_TOKEN_HEAD * B * T * H
-    out = {
-        "metric": "cleaning+chunk fwd+bwd tokens/s at B8·T4096·H8·dk128 bf16; % MFMA peak",
-        "value": tokens_per_s,
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded, BASELINE.json configs[1] + configs[2] GDN conventions)",
-        "config": {"workload": "fused CCQ cleaning (per-head gate) + GDN chunk fwd+bwd", "B": B, "T": T, "H": H,
-                   "d_k": K, "d_v": V, "chunk": BT, "algorithmic_flop_per_step": flops,
-                   "mfma_peak_fraction": flops / (ms * 1e-3) / PEAK_BF16,
-                   "kernel_ms_per_step": {n: round(v, 4) for n, v in kms.items()}},
-        "roofline": roofline(kms, klaunch),
-    }
+    out = _line("cleaning+chunk fwd+bwd tokens/s at B8·T4096·H8·dk128 bf16; % MFMA peak", B * T * args.steps / elapsed,
+                "tokens/s", args, ms, "bf16", "synthetic (seeded, BASELINE.json configs[1] + configs[2] GDN conventions)",
+                {"workload": "fused CCQ cleaning (per-head gate) + GDN chunk fwd+bwd", "B": B, "T": T, "H": H,
+                 "d_k": K, "d_v": V, "chunk": BT, "algorithmic_flop_per_step": flops,
+                 "mfma_peak_fraction": flops / (ms * 1e-3) / PEAK_BF16,
+                 "kernel_ms_per_step": {n: round(v, 4) for n, v in kms.items()}},
+                roofline=roofline(kms, klaunch), step_roofline=step_roofline(ms))
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
+    return out
+
+
+def run_decode(args, dev, layers=24, b=16, h=4, k=256, v=512):
+    """C4's recurrent decode at its per-layer state shapes: `layers` CCQ-GDN decode steps (per-head
+    gate, subtract_mean, l2norm) captured in one HIP graph, one token per sequence per replay.
+    Inputs of the token are written into the steps' buffers once (their values do not change the
+    work); the states carry over from replay to replay."""
+    from ccq_amd.graph import CapturedDecode, DecodeStep
+    gen = torch.Generator().manual_seed(0)
+    steps = []
+    for _ in range(layers):
+        st = DecodeStep(b, h, k, v, mode="gdn", gate=True, device=dev)
+        st.q.copy_(torch.randn(b, 1, h, k, generator=gen))
+        st.k.copy_(torch.randn(b, 1, h, k, generator=gen))
+        st.v.copy_(torch.randn(b, 1, h, v, generator=gen))
+        st.g.copy_(-torch.rand(b, 1, h, generator=gen))
+        st.beta.copy_(torch.rand(b, 1, h, generator=gen))
+        st.gate_b.uniform_(-1.0, 1.0)
+        kk = torch.nn.functional.normalize(torch.randn(b, h, 64, k, generator=gen), dim=-1)
+        st.load_state((0.01 * torch.randn(b, h, k, v, generator=gen)).to(dev), (kk.transpose(-1, -2) @ kk).to(dev),
+                      kk.sum(-2).to(dev), 16384)
+        steps.append(st)
+    cap = CapturedDecode(steps).capture()
+    t_graph = _timed_steps(cap.replay, args.steps, args.warmup)
+    t_eager = _timed_steps(cap.eager, args.steps, args.warmup)
+    state_bytes = sum(s.state_bytes() for s in steps)
+    io_bytes = layers * b * h * (2 * k + 2 * k + 2 * v + 2 * v + 4 + 4)
+    byts = state_bytes + io_bytes
+    achieved = byts / t_graph / 1e9
+    return _line("CCQ-GDN decode step latency (24 layers, B16, H4, d_k256, d_v512; captured HIP graph)",
+                 t_graph * 1e3, "ms/step", args, t_graph * 1e3, "f32 states, bf16 q/k/v/o",
+                 "synthetic (seeded; states of a 16,384-token prefill shape, random values)",
+                 {"workload": "C4 decode: recurrent CCQ-GDN step of every layer, one token per sequence",
+                  "layers": layers, "B": b, "H": h, "d_k": k, "d_v": v, "tokens_per_s": b / t_graph,
+                  "eager_ms_per_step": t_eager * 1e3, "state_bytes_per_step": state_bytes,
+                  "survey_bound_ms_with_weights": 0.42},
+                 higher=False,
+                 roofline={"kernel": "decode step (clean + backbone + finish, all layers)", "bound": "hbm",
+                           "achieved": achieved, "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": achieved * 1e9 /
+                           PEAK_HBM, "traffic": None, "algorithmic_bytes_per_step": byts,
+                           "ideal_ms": byts / PEAK_HBM * 1e3})
+
+
+def _gdn_inputs(dev, b, t, h, k, v, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    l2 = lambda x: torch.nn.functional.normalize(x, dim=-1)  # noqa: E731
+    q = l2(torch.randn(b, t, h, k, generator=gen)).to(torch.bfloat16)
+    kk = l2(torch.randn(b, t, h, k, generator=gen)).to(torch.bfloat16)
+    vv = torch.randn(b, t, h, v, generator=gen).to(torch.bfloat16)
+    a_log = torch.empty(h).uniform_(0.0, math.log(16.0), generator=gen)
+    g = (-torch.nn.functional.softplus(torch.randn(b, t, h, generator=gen)) * a_log.exp()).float()
+    beta = torch.sigmoid(torch.randn(b, t, h, generator=gen)).float()
+    w = (torch.randn(h, k, generator=gen) * 0.02).float()
+    bias = torch.empty(h).uniform_(-1.0, 1.0, generator=gen).float()
+    do = torch.randn(b, t, h, v, generator=gen).to(torch.bfloat16)
+    xs = dict(q=q, k=kk, v=vv, g=g, beta=beta, w=w, b=bias, do=do)
+    return {n: x.to(dev) for n, x in xs.items()}
+
+
+def run_readme(args, dev, b=1, t=32768, h=6, k=256, v=512):
+    """The reference README's published shape (32K tokens, 6 heads, K=256, V=512, fwd+bwd): the
+    cleaning overhead = fused CCQ-GDN fwd+bwd minus the plain GDN chunk fwd+bwd on the same inputs."""
+    from ccq_amd import chunk_gated_delta_rule, fused_chunk_ccq_gdn
+    x = _gdn_inputs(dev, b, t, h, k, v)
+    for n in LEAVES:
+        x[n].requires_grad_()
+
+    def ccq():
+        o, _, _, _ = fused_chunk_ccq_gdn(x["q"], x["k"], x["v"], None, x["g"], x["beta"], gate_w=x["w"],
+                                         gate_b=x["b"])
+        torch.autograd.grad(o, [x[n] for n in LEAVES], x["do"])
+
+    plain_leaves = ("q", "k", "v", "g", "beta")
+
+    def plain():
+        o, _ = chunk_gated_delta_rule(x["q"], x["k"], x["v"], x["g"], x["beta"])
+        torch.autograd.grad(o, [x[n] for n in plain_leaves], x["do"])
+
+    t_ccq = _timed_steps(ccq, args.steps, args.warmup)
+    t_plain = _timed_steps(plain, args.steps, args.warmup)
+    return _line("CCQ cleaning overhead over plain GDN, fwd+bwd, 32K tokens, H6, d_k256, d_v512 (README shape)",
+                 (t_ccq - t_plain) * 1e3, "ms", args, t_ccq * 1e3, "bf16",
+                 "synthetic (seeded; q, k L2-normalised, C2 decay convention, per-head gate)",
+                 {"workload": "fused_chunk_ccq_gdn vs chunk_gated_delta_rule fwd+bwd", "B": b, "T": t, "H": h,
+                  "d_k": k, "d_v": v, "ccq_gdn_ms": t_ccq * 1e3, "plain_gdn_ms": t_plain * 1e3,
+                  "tokens_per_s": b * t / t_ccq,
+                  "reference_published_overhead_ms_h200": [4.2, 7.1]},
+                 higher=False)
+
+
+def run_layer(args, dev, which):
+    """C2 (CCQ-GDN layer, d_model 1024, H4, K256, V512, B4 T4096) or C3 (CCQ-GLA layer, H4, K128,
+    V256, B4 T8192, short conv on) forward + backward, random init, bf16."""
+    from ccq_amd.layers import CCQGDN, CCQGLA
+    torch.manual_seed(0)
+    if which == "c2":
+        b, t = 4, 4096
+        layer = CCQGDN(hidden_size=1024, head_dim=256, num_heads=4, expand_v=2, mode="fused_chunk", layer_idx=0)
+        desc = "CCQ-GDN layer fwd+bwd, d_model1024, H4, d_k256, d_v512, B4, T4096 (fused_chunk)"
+    else:
+        b, t = 4, 8192
+        layer = CCQGLA(mode="fused_chunk", hidden_size=1024, expand_k=0.5, expand_v=1.0, num_heads=4,
+                       use_short_conv=True, layer_idx=0)
+        desc = "CCQ-GLA layer fwd+bwd, d_model1024, H4, d_k128, d_v256, B4, T8192 (fused_chunk, short conv)"
+    layer = layer.to(dev, torch.bfloat16)
+    gen = torch.Generator().manual_seed(0)
+    xin = torch.randn(b, t, 1024, generator=gen).to(dev, torch.bfloat16).requires_grad_()
+    dy = torch.randn(b, t, 1024, generator=gen).to(dev, torch.bfloat16)
+    params = [p for p in layer.parameters() if p.requires_grad]
+
+    def step():
+        y = layer(xin)[0]
+        torch.autograd.grad(y, [xin] + params, dy)
+
+    dt = _timed_steps(step, args.steps, args.warmup)
+    return _line(desc, b * t / dt, "tokens/s", args, dt * 1e3, "bf16",
+                 "synthetic (seeded; x ~ N(0,1); the reference layer's own random init)",
+                 {"workload": f"{which.upper()} single layer fwd+bwd", "B": b, "T": t})
+
+
+def ingest_pmc(fetch_dir, write_dir, out_path):
+    """Per-launch HBM bytes of each timed stage from two rocprofv3 --pmc runs of this script with
+    --copy-calibration (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by the counter's
+    reading for the calibration copy (torch neg over 512 MiB read + 512 MiB written)."""
+    import csv
+    import glob
+    import re
+    kernel_stage = {
+        "cs_sum_kernel": "clean_fwd_sum", "cs_fwd_kernel": "clean_fwd", "cs_dq_kernel": "clean_bwd_dq",
+        "cs_gsum_kernel": "clean_bwd_gsum", "cs_dk_kernel": "clean_bwd_dk", "gdn_prep": "gdn_prep",
+        "gdn_fwd_state": "gdn_fwd_state", "gdn_bwd_state": "gdn_bwd_state", "gdn_bwd_dqkw": "gdn_bwd_dqkw",
+        "gdn_bwd_wy": "gdn_bwd_wy",
+    }
+
+    def read(d, counter):
+        per, calib = {}, []
+        for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(fn)):
+                if r["Counter_Name"] != counter:
+                    continue
+                name = r["Kernel_Name"]
+                val = float(r["Counter_Value"]) * 1024.0
+                if "neg" in name:
+                    calib.append(val)
+                    continue
+                for key, stage in kernel_stage.items():
+                    if re.search(r"\b" + key, name):
+                        per.setdefault(stage, []).append(val)
+        return {k: sum(v) / len(v) for k, v in per.items()}, (max(calib) if calib else None)
+
+    fetch, fcal = read(fetch_dir, "FETCH_SIZE")
+    write, wcal = read(write_dir, "WRITE_SIZE")
+    ref = 512.0 * 2 ** 20
+    fs, ws = ref / fcal, ref / wcal
+    data = {"scale": {"fetch": fs, "write": ws},
+            "per_launch_bytes": {k: [fetch[k] * fs, write.get(k, 0.0) * ws] for k in sorted(fetch)}}
+    with open(out_path, "w") as f:
+        json.dump(data, f, indent=1)
+    print(json.dumps(data))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=("c1", "decode", "readme", "c2", "c3"), default="c1",
+                    help="c1: the metric (default); decode: C4's captured decode step; readme: the reference "
+                         "README's cleaning-overhead shape; c2 / c3: single-layer fwd+bwd")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed steps, run one elementwise copy of 512 MiB (read) + 512 MiB (write), "
+                         "the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counts")
+    ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write the per-launch traffic file from two rocprofv3 --pmc output folders and exit")
+    args = ap.parse_args()
+    if args.ingest_pmc:
+        ingest_pmc(args.ingest_pmc[0], args.ingest_pmc[1], TRAFFIC_FILE)
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    if args.workload == "c1":
+        out = run_c1(args, dev)
+    elif args.workload == "decode":
+        out = run_decode(args, dev)
+    elif args.workload == "readme":
+        out = run_readme(args, dev)
+    else:
+        out = run_layer(args, dev, args.workload)
     print(json.dumps(out), flush=True)
 
 

@@ -41,6 +41,9 @@ SIGNATURES = {
     "ccq_gdn_decode": (_I, [_P] * 17 + [_I] * 10 + [_F, _P]),
     "ccq_gla_decode": (_I, [_P] * 16 + [_I] * 9 + [_F, _P]),
     "ccq_gdn_decode_noalloc": (_I, [_P] * 16 + [_I] * 10 + [_F, _P]),
+    "ccq_decode_step_workspace_bytes": (_SZ, [_I] * 4),
+    "ccq_gdn_decode_step": (_I, [_P] * 14 + [_I] * 8 + [_F, _P]),
+    "ccq_gla_decode_step": (_I, [_P] * 13 + [_I] * 7 + [_F, _P]),
     "ccq_clean_z_saved_bytes": (_SZ, [_I, _I, _I]),
     "ccq_clean_z_bwd_workspace_bytes": (_SZ, [_I, _I, _I]),
     "ccq_clean_z_fwd": (_I, [_P] * 8 + [_I] + [_P] * 3 + [_I] * 7 + [_P]),

@@ -29,6 +29,7 @@ hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st);
 int cseg_count(int N, int H, int T);
 bool cseg_supported(int K);
 hipError_t decode_scratch(hipStream_t st, void** out);
+hipError_t launch_decode_finish(float* m, const float* m_new, long n, int* pos, int advance, hipStream_t st);
 hipError_t launch_zclean(int stage, const ZCleanArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
@@ -788,6 +789,74 @@ int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lam
   if (K > 256) return fail(CCQ_ERR_SHAPE, "ccq_gla_decode: K=%d", K);
   a.gk = gk; a.gla = 1;
   return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gla_decode");
+}
+
+// ---- decode step with in-place states and a device-held position (graph capture) ----
+size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K) {
+  Slicer sl{nullptr};
+  sl.take<char>(carve_decode_work(nullptr, (int64_t)B * T, H, K, nullptr, nullptr));
+  sl.take<float>((size_t)B * H * K);
+  return sl.off;
+}
+
+}  // extern "C"
+
+namespace {
+
+int decode_step(const char* who, bool gla, const void* q, const void* k, const void* v, const float* lambda,
+                const float* gate_w, const float* gate_b, const float* g, const float* beta, const float* gk,
+                float* state, float* cov_state, float* mean_state, int* position, void* o, void* workspace, int B,
+                int T, int H, int K, int V, int subtract_mean, int use_l2norm, int enable_ccq, float scale,
+                void* stream) {
+  if (!state || !position) return fail(CCQ_ERR_NULL, "%s: state and position are required", who);
+  if (enable_ccq && (!cov_state || (subtract_mean && !mean_state)))
+    return fail(CCQ_ERR_NULL, "%s: cov_state (and mean_state with subtract_mean) are required", who);
+  if (!gla && !beta) return fail(CCQ_ERR_NULL, "%s: beta is required", who);
+  DecodeArgs a{};
+  // the key sum goes to the workspace tail and is copied back after the step
+  Slicer sl{(char*)workspace};
+  sl.take<char>(carve_decode_work(nullptr, (int64_t)B * T, H, K, nullptr, nullptr));
+  float* m_new = workspace ? sl.take<float>((size_t)B * H * K) : nullptr;
+  const bool mean = enable_ccq && subtract_mean;
+  if (int s = decode_common(who, a, q, k, v, lambda, gate_w, gate_b, state, cov_state, mean ? mean_state : nullptr,
+                            nullptr, o, state, cov_state, mean ? m_new : nullptr, workspace, B, T, H, K, V, B, 0,
+                            subtract_mean, use_l2norm, enable_ccq, scale))
+    return s;
+  a.pos_dev = position;
+  if (gla) {
+    a.gk = gk;
+    a.gla = 1;
+  } else {
+    a.g = g;
+    a.beta = beta;
+  }
+  const hipStream_t st = (hipStream_t)stream;
+  if (int s = hip_status(launch_decode(a, st), who)) return s;
+  return hip_status(launch_decode_finish(mean ? mean_state : nullptr, m_new, mean ? (long)B * H * K : 0, position, T,
+                                         st),
+                    who);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ccq_gdn_decode_step(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                        const float* gate_b, const float* g, const float* beta, float* state, float* cov_state,
+                        float* mean_state, int* position, void* o, void* workspace, int B, int T, int H, int K, int V,
+                        int subtract_mean, int use_l2norm, int enable_ccq, float scale, void* stream) {
+  return decode_step("ccq_gdn_decode_step", false, q, k, v, lambda, gate_w, gate_b, g, beta, nullptr, state,
+                     cov_state, mean_state, position, o, workspace, B, T, H, K, V, subtract_mean, use_l2norm,
+                     enable_ccq, scale, stream);
+}
+
+int ccq_gla_decode_step(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                        const float* gate_b, const float* gk, float* state, float* cov_state, float* mean_state,
+                        int* position, void* o, void* workspace, int B, int T, int H, int K, int V, int subtract_mean,
+                        int use_l2norm, float scale, void* stream) {
+  return decode_step("ccq_gla_decode_step", true, q, k, v, lambda, gate_w, gate_b, nullptr, nullptr, gk, state,
+                     cov_state, mean_state, position, o, workspace, B, T, H, K, V, subtract_mean, use_l2norm, 1, scale,
+                     stream);
 }
 
 }  // extern "C"

@@ -14,6 +14,7 @@
 //   decode_backbone grid (N*H, V/64): each workgroup owns 64 columns of S, reads the cleaned query.
 // Thread (column j = tid % 64, row group tid / 64) holds K/4 consecutive rows of its column, so
 // every state access is a coalesced 256-byte row segment.
+#include <algorithm>
 #include <mutex>
 
 #include "ccq_tile.h"
@@ -68,6 +69,7 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
   seq_bounds(a.cu, n, a.T, bos, len);
   const bool own = j < K;  // K = 32 launches one 64-column slice with half of it idle
 
+  const int pos_off = a.pos_dev ? *a.pos_dev : a.pos_off;
   float creg[RPT];
   const float* Cin = a.C_in ? a.C_in + (long)unit * K * K : nullptr;
 #pragma unroll
@@ -109,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
     __syncthreads();
     if (rg == 0 && own) {
       const float z = sz[0][jj] + sz[1][jj] + sz[2][jj] + sz[3][jj];
-      float pos = (float)(t + 1 + a.pos_off);
+      float pos = (float)(t + 1 + pos_off);
       pos = pos < 1.f ? 1.f : pos;
       float corr = z / pos;
       if (a.subtract_mean) corr -= s * sm[j] / (pos * pos);
@@ -189,6 +191,21 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
 #pragma unroll
     for (int r = 0; r < RPT; ++r) So[(long)(rg * RPT + r) * V + v] = sreg[r];
   }
+}
+
+// End of a step with device-held position and in-place states: the new key sum (written beside
+// the cached one: every clean workgroup reads all of the cached sum) replaces it, and the position
+// offset advances by the step's tokens.  Launched after the step's kernels (stream order).
+__global__ __launch_bounds__(kThreads) void decode_finish_kernel(float* m, const float* m_new, long n, int* pos,
+                                                                 int advance) {
+  for (long i = (long)blockIdx.x * kThreads + threadIdx.x; i < n; i += (long)gridDim.x * kThreads) m[i] = m_new[i];
+  if (pos && blockIdx.x == 0 && threadIdx.x == 0) *pos += advance;
+}
+
+hipError_t launch_decode_finish(float* m, const float* m_new, long n, int* pos, int advance, hipStream_t st) {
+  const long blocks = n > 0 ? std::min<long>((n + kThreads - 1) / kThreads, 1024) : 1;
+  hipLaunchKernelGGL(decode_finish_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, st, m, m_new, n, pos, advance);
+  return hipGetLastError();
 }
 
 template <int K>

@@ -32,6 +32,7 @@ struct DecodeArgs {
   float* qc;               // workspace fp32 [tokens, H, K]: cleaned query
   float* kn;               // workspace fp32 [tokens, H, K]: (normalised) key
   const int64_t* cu;       // [N+1] (nullable)
+  const int* pos_dev;      // device int: the position offset (nullable: pos_off)
   float scale;
   int T, H, N, K, V, pos_off, subtract_mean, l2norm, ccq, gla;
 };

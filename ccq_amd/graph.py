@@ -1,0 +1,163 @@
+"""Captured decode loop: the per-token CCQ-GDN / CCQ-GLA recurrent step of one or more layers in a
+single HIP graph.
+
+The reference generates one token at a time by calling ``fused_recurrent_ccq_gdn`` (or ``_gla``)
+once per layer with the cache tuple ``(S, C, m, position_offset)`` (``ccq/gdn/layer.py:318-336,
+397``; ``ccq/ops/ccq_gdn/fused_recurrent.py:18-75``).  Per layer and token that is a handful of
+launches plus host work, and the token's latency is launch-bound.  Here each layer's step is the
+library's ``ccq_gdn_decode_step`` / ``ccq_gla_decode_step``: three kernels over static buffers,
+with the states updated in place and the position offset held in device memory (advanced by the
+step itself), so the same captured graph is replayed for every generated token.
+
+``DecodeStep`` owns one layer's buffers: the token inputs (``q``, ``k``, ``v``, ``g``/``beta`` or
+``gk``, ``lam``), the per-head gate (``gate_w``, ``gate_b``), the states ``S``, ``C``, ``m``, the
+position and the output ``o``.  A caller writes the new token's inputs into the input buffers
+(``copy_``), replays, and reads ``o``.  ``CapturedDecode`` captures the steps of several layers
+in order (e.g. the 24 layers of a model) and replays them as one graph.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr
+
+__all__ = ["DecodeStep", "CapturedDecode"]
+
+
+class DecodeStep:
+    """Static buffers and the in-place decode step of one CCQ-GDN (``mode="gdn"``) or CCQ-GLA
+    (``mode="gla"``) layer: ``B`` sequences, ``T`` new tokens each (normally 1), ``H`` heads.
+
+    ``gate=True`` computes lambda in the kernel from ``gate_w [H, K]`` / ``gate_b [H]`` (the
+    per-head gate of the reference layer); otherwise ``lam [B, T, H]`` (fp32) is read as given
+    (the reference ops round lambda to q's dtype first; a caller that mirrors them writes
+    bf16-rounded values).  GLA takes the
+    per-channel log decay ``gk [B, T, H, K]`` (``use_gk=False``: no decay) and always
+    L2-normalises q and k, as the reference's recurrent GLA op does."""
+
+    def __init__(self, B: int, H: int, K: int, V: int, *, T: int = 1, mode: str = "gdn", gate: bool = True,
+                 use_gk: bool = True, subtract_mean: bool = True, use_l2norm: bool = True, enable_ccq: bool = True,
+                 scale: Optional[float] = None, device=None):
+        if mode not in ("gdn", "gla"):
+            raise ValueError(f"mode must be 'gdn' or 'gla' (got {mode!r})")
+        if mode == "gla" and not enable_ccq:
+            raise ValueError("the GLA step always cleans the query (enable_ccq=True)")
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        if dev.type != "cuda":
+            raise ValueError(f"DecodeStep runs on a GPU (got device {dev})")
+        self.B, self.T, self.H, self.K, self.V, self.mode = B, T, H, K, V, mode
+        self.gate, self.subtract_mean, self.use_l2norm = gate, subtract_mean, use_l2norm
+        self.enable_ccq = enable_ccq
+        self.scale = float(K ** -0.5 if scale is None else scale)
+        bf, f32 = torch.bfloat16, torch.float32
+        z = lambda *shape, dtype=f32: torch.zeros(*shape, device=dev, dtype=dtype)  # noqa: E731
+        self.q, self.k, self.v = z(B, T, H, K, dtype=bf), z(B, T, H, K, dtype=bf), z(B, T, H, V, dtype=bf)
+        self.lam = None if gate or not enable_ccq else z(B, T, H)
+        self.gate_w = z(H, K) if gate and enable_ccq else None
+        self.gate_b = z(H) if gate and enable_ccq else None
+        if mode == "gdn":
+            self.g, self.beta, self.gk = z(B, T, H), torch.ones(B, T, H, device=dev, dtype=f32), None
+        else:
+            self.g, self.beta = None, None
+            self.gk = z(B, T, H, K) if use_gk else None
+        self.S = z(B, H, K, V)
+        self.C = z(B, H, K, K) if enable_ccq else None
+        self.m = z(B, H, K) if enable_ccq and subtract_mean else None
+        self.position = torch.zeros(1, device=dev, dtype=torch.int32)
+        self.o = z(B, T, H, V, dtype=bf)
+        nbytes = _lib.load().ccq_decode_step_workspace_bytes(B, T, H, K)
+        self.workspace = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+
+    # ---- state ----
+    def load_state(self, S: torch.Tensor, C: Optional[torch.Tensor] = None, m: Optional[torch.Tensor] = None,
+                   position: int = 0) -> None:
+        """Copy a cached state (e.g. the prefill's final S, C, m and its token count) into the
+        step's buffers (absent C / m: zero)."""
+        self.S.copy_(S)
+        for buf, src in ((self.C, C), (self.m, m)):
+            if buf is None:
+                continue
+            if src is None:
+                buf.zero_()
+            else:
+                buf.copy_(src)
+        self.position.fill_(int(position))
+
+    def state(self):
+        """(S, C, m, position) -- the buffers themselves (position as a 1-element int32 tensor)."""
+        return self.S, self.C, self.m, self.position
+
+    # ---- one step ----
+    def launch(self, stream=None) -> None:
+        """Run the step on ``stream`` (default: the current stream; under capture, the capture
+        stream)."""
+        st = _lib.stream_of(self.q) if stream is None else stream
+        if self.mode == "gdn":
+            call("ccq_gdn_decode_step", ptr(self.q), ptr(self.k), ptr(self.v), ptr(self.lam), ptr(self.gate_w),
+                 ptr(self.gate_b), ptr(self.g), ptr(self.beta), ptr(self.S), ptr(self.C), ptr(self.m),
+                 ptr(self.position), ptr(self.o), ptr(self.workspace), self.B, self.T, self.H, self.K, self.V,
+                 int(self.subtract_mean), int(self.use_l2norm), int(self.enable_ccq), self.scale, st)
+        else:
+            call("ccq_gla_decode_step", ptr(self.q), ptr(self.k), ptr(self.v), ptr(self.lam), ptr(self.gate_w),
+                 ptr(self.gate_b), ptr(self.gk), ptr(self.S), ptr(self.C), ptr(self.m), ptr(self.position),
+                 ptr(self.o), ptr(self.workspace), self.B, self.T, self.H, self.K, self.V, int(self.subtract_mean),
+                 1, self.scale, st)
+
+    def state_bytes(self) -> int:
+        """HBM bytes of the states one step reads and writes (each element once each way)."""
+        n = self.S.numel() + (self.C.numel() if self.C is not None else 0) + (self.m.numel() if self.m is not None
+                                                                               else 0)
+        return 2 * 4 * n
+
+
+class CapturedDecode:
+    """The steps of several layers captured in one graph.  ``capture()`` records them in order;
+    ``replay()`` runs one token for all of them (inputs from the steps' input buffers, states and
+    positions advanced in place).  The capture itself runs no step: the steps' kernels are loaded
+    by one eager step whose state changes are undone before recording."""
+
+    def __init__(self, steps: Sequence[DecodeStep]):
+        if not steps:
+            raise ValueError("no steps")
+        self.steps: List[DecodeStep] = list(steps)
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    def _snapshot(self):
+        return [[t.clone() if t is not None else None for t in (s.S, s.C, s.m, s.position, s.o)] for s in self.steps]
+
+    def _restore(self, snap) -> None:
+        for s, saved in zip(self.steps, snap):
+            for dst, src in zip((s.S, s.C, s.m, s.position, s.o), saved):
+                if dst is not None:
+                    dst.copy_(src)
+
+    def capture(self) -> "CapturedDecode":
+        snap = self._snapshot()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for s in self.steps:
+                s.launch()
+        torch.cuda.current_stream().wait_stream(side)
+        self._restore(snap)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            for s in self.steps:
+                s.launch()
+        torch.cuda.synchronize()
+        return self
+
+    def replay(self) -> None:
+        if self.graph is None:
+            raise RuntimeError("capture() first")
+        self.graph.replay()
+
+    def eager(self) -> None:
+        """The same steps launched one by one (no graph)."""
+        for s in self.steps:
+            s.launch()

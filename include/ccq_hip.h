@@ -229,6 +229,28 @@ int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lam
                    int N, int position_offset, int subtract_mean, int use_l2norm, float scale, void* stream);
 
 /*
+ * Decode step for a captured (HIP-graph) generation loop: ccq_gdn_decode / ccq_gla_decode on B
+ * sequences of T new tokens each, with the cached states S, C, m updated in place and the position
+ * offset read from device memory (`position`, one int) and advanced by T after the step, so one
+ * captured graph can be replayed token after token.  Replaces the same reference calls as
+ * ccq_gdn_decode, as the reference layers make them once per generated token with the cache tuple
+ * (S, C, m, position_offset) (ccq/gdn/layer.py:318-336, 397; ccq/gla/layer.py); the position lives
+ * on the device here because a captured launch cannot take a new host value per replay.
+ * workspace: ccq_decode_step_workspace_bytes(B, T, H, K) (the decode workspace plus the new key
+ * sum, copied over mean_state at the end of the step).  Launches three kernels, no allocation and
+ * no memset.
+ */
+size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K);
+int ccq_gdn_decode_step(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                        const float* gate_b, const float* g, const float* beta, float* state, float* cov_state,
+                        float* mean_state, int* position, void* o, void* workspace, int B, int T, int H, int K, int V,
+                        int subtract_mean, int use_l2norm, int enable_ccq, float scale, void* stream);
+int ccq_gla_decode_step(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
+                        const float* gate_b, const float* gk, float* state, float* cov_state, float* mean_state,
+                        int* position, void* o, void* workspace, int B, int T, int H, int K, int V, int subtract_mean,
+                        int use_l2norm, float scale, void* stream);
+
+/*
  * Row L2 normalisation y = x / sqrt(sum x^2 + eps) (bf16 rows of D <= 512) and its backward.
  * Replaces fla l2norm as called by the reference (ccq/ops/ccq_gdn/fused_chunk.py:43-44).
  * rstd fp32 [rows] is written by the forward and read by the backward.

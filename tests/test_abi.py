@@ -177,3 +177,19 @@ def test_decode_noalloc_rejects_calls_beyond_its_scratch():
                                     1, 2048, 4, 256, 512, 1, 0, 1, 1, 1, 0.0625, None)
     assert st == CCQ_ERR_SHAPE
     assert b"scratch" in lib.ccq_last_error()
+
+
+def test_decode_step_checks_and_workspace():
+    lib = _lib.load()
+    p = _fake()
+    # position (device int) and state are required; checked before any device work
+    st = lib.ccq_gdn_decode_step(p, p, p, None, p, p, p, p, p, p, p, None, p, p, 2, 1, 4, 256, 512, 1, 1, 1, 0.0625,
+                                 None)
+    assert st == CCQ_ERR_NULL and b"position" in lib.ccq_last_error()
+    st = lib.ccq_gla_decode_step(p, p, p, None, p, p, p, None, p, p, p, p, p, 2, 1, 4, 256, 512, 1, 1, 0.0625, None)
+    assert st == CCQ_ERR_NULL
+    # the decode workspace plus the new key sum [B, H, K] fp32
+    B, T, H, K = 16, 1, 4, 256
+    ws = lib.ccq_decode_step_workspace_bytes(B, T, H, K)
+    base = lib.ccq_decode_workspace_bytes(B * T, H, K)
+    assert base + B * H * K * 4 <= ws <= base + B * H * K * 4 + 256

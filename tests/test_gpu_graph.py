@@ -1,0 +1,110 @@
+"""GPU checks of the captured decode loop (ccq_amd.graph): the in-place decode step with a
+device-held position, recorded in one HIP graph over several layers, replayed token after token.
+
+Each replay is compared with the eager, allocating decode op (``gdn_decode`` / ``gla_decode``,
+itself held to the CPU oracle by test_gpu_decode.py) fed the same inputs and the previous step's
+states: the same kernels see the same numbers, so outputs, states and positions must be
+bit-identical.  Eager work and synchronisations run between the replays, and every replay is
+checked, not only the last."""
+
+import pytest
+import torch
+
+from tests._util import bf, l2n
+
+pytestmark = pytest.mark.gpu
+
+
+def _cuda():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import ccq_amd  # noqa: F401
+    return torch.device("cuda")
+
+
+CASES = [
+    # mode, layers, B, H, K, V, gate, subtract_mean, steps
+    ("gdn", 2, 2, 2, 64, 128, True, True, 4),
+    ("gdn", 3, 3, 4, 256, 512, False, True, 3),
+    ("gdn", 1, 2, 2, 128, 64, True, False, 3),
+    ("gla", 2, 2, 2, 128, 256, True, True, 3),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(i) for i in range(len(CASES))])
+def test_captured_decode_matches_eager(case):
+    dev = _cuda()
+    from ccq_amd.decode import gdn_decode, gla_decode
+    from ccq_amd.graph import CapturedDecode, DecodeStep
+
+    mode, L, B, H, K, V, gate, sub, steps = case
+    print(f"captured decode case {case}", flush=True)
+    gen = torch.Generator().manual_seed(11)
+    pos0 = 29
+    layers = []
+    for _ in range(L):
+        st = DecodeStep(B, H, K, V, mode=mode, gate=gate, subtract_mean=sub, device=dev)
+        kk = l2n(torch.randn(B, H, pos0, K, generator=gen))
+        S0 = (torch.randn(B, H, K, V, generator=gen) * 0.1).float()
+        st.load_state(S0.to(dev), (kk.transpose(-1, -2) @ kk).float().to(dev), kk.sum(-2).float().to(dev), pos0)
+        if gate:
+            st.gate_w.copy_(0.1 * torch.randn(H, K, generator=gen))
+            st.gate_b.copy_(torch.rand(H, generator=gen) * 2 - 1)
+        layers.append(st)
+    # eager reference states (copies)
+    ref = [[t.clone() if t is not None else None for t in (s.S, s.C, s.m)] for s in layers]
+    graph = CapturedDecode(layers).capture()
+    for step in range(steps):
+        ins = []
+        for st in layers:
+            q = bf(torch.randn(B, 1, H, K, generator=gen) * 2)
+            k = bf(torch.randn(B, 1, H, K, generator=gen) * 2)
+            v = bf(torch.randn(B, 1, H, V, generator=gen))
+            x = {"q": q, "k": k, "v": v}
+            if not gate:
+                # (the op rounds lambda to q's dtype, as the reference does; the step reads it as given)
+                x["lam"] = torch.sigmoid(torch.randn(B, 1, H, generator=gen)).to(torch.bfloat16).float()
+            if mode == "gdn":
+                x["g"] = -torch.rand(B, 1, H, generator=gen) * 3
+                x["beta"] = torch.rand(B, 1, H, generator=gen)
+            else:
+                x["gk"] = -torch.rand(B, 1, H, K, generator=gen) * 0.5
+            for name, t in x.items():
+                getattr(st, name).copy_(t)
+            ins.append({n: t.to(dev) for n, t in x.items()})
+        graph.replay()
+        torch.cuda.synchronize()
+        for li, (st, x) in enumerate(zip(layers, ins)):
+            S, C, m = ref[li]
+            gw, gb = (st.gate_w, st.gate_b) if gate else (None, None)
+            if mode == "gdn":
+                o, S2, C2, m2 = gdn_decode(x["q"], x["k"], x["v"], x.get("lam"), x["g"], x["beta"], st.scale,
+                                           initial_state=S, initial_cov_state=C, initial_mean_state=m,
+                                           position_offset=pos0 + step, subtract_mean=sub, gate_w=gw, gate_b=gb)
+            else:
+                o, S2, C2, m2 = gla_decode(x["q"], x["k"], x["v"], x.get("lam"), x["gk"], st.scale,
+                                           initial_state=S, initial_cov_state=C, initial_mean_state=m,
+                                           position_offset=pos0 + step, subtract_mean=sub, gate_w=gw, gate_b=gb)
+            torch.cuda.synchronize()
+            assert torch.equal(st.o, o), f"layer {li} step {step}: output"
+            assert torch.equal(st.S, S2), f"layer {li} step {step}: S"
+            assert torch.equal(st.C, C2), f"layer {li} step {step}: C"
+            if sub:
+                assert torch.equal(st.m, m2), f"layer {li} step {step}: m"
+            assert int(st.position.item()) == pos0 + step + 1
+            ref[li] = [S2, C2, m2 if sub else None]
+        # eager work of the program between replays
+        torch.cuda.synchronize()
+
+
+def test_decode_step_rejects_missing_state():
+    _cuda()
+    from ccq_amd import _lib
+    from ccq_amd.graph import DecodeStep
+    st = DecodeStep(1, 1, 64, 64, device="cuda")
+    lib = _lib.load()
+    from ccq_amd._lib import ptr
+    status = lib.ccq_gdn_decode_step(ptr(st.q), ptr(st.k), ptr(st.v), None, ptr(st.gate_w), ptr(st.gate_b),
+                                     ptr(st.g), ptr(st.beta), ptr(st.S), ptr(st.C), ptr(st.m), None, ptr(st.o),
+                                     ptr(st.workspace), 1, 1, 1, 64, 64, 1, 1, 1, 0.125, None)
+    assert status == -2 and b"position" in lib.ccq_last_error()
