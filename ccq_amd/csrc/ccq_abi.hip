@@ -26,7 +26,8 @@ hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
 hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st);
-int cseg_count(int N, int H, int T);
+int cseg_count(int N, int H, int T, int K);
+bool cseg_sums_supported(int K);
 bool cseg_supported(int K);
 hipError_t decode_scratch(hipStream_t st, void** out);
 hipError_t launch_decode_finish(float* m, const float* m_new, long n, int* pos, int advance, hipStream_t st);
@@ -174,8 +175,19 @@ struct WalkSaved {
   int nseg;
 };
 
+// Time segments of the cleaning walks: the segment walks (K in {64, 128}) always; the column walks
+// of K = 256 when more than one segment fits the device; K = 32 walks whole sequences.
+int walk_segments(int N, int H, int T, int K) {
+  if (!cseg_sums_supported(K)) return 1;
+  return cseg_count(N, H, T, K);
+}
+bool walk_segmented(int N, int H, int T, int K) {
+  return cseg_supported(K) || (cseg_sums_supported(K) && walk_segments(N, H, T, K) > 1);
+}
+
 // Forward-to-backward buffer of the cleaning: for K in {64, 128} (segment walks) the per-segment
-// state totals; otherwise (column walks) the covariance read z, s_t and the chunk-start key sums.
+// state totals; otherwise (column walks) the covariance read z, s_t and the chunk-start key sums,
+// plus the per-segment totals when the column walks are cut into segments.
 size_t carve_walk_saved(char* base, const WalkGeom& g, int64_t tokens, int N, int H, int K, int T, bool varlen,
                         WalkSaved* out) {
   Slicer sl{base};
@@ -184,11 +196,12 @@ size_t carve_walk_saved(char* base, const WalkGeom& g, int64_t tokens, int N, in
     t.chunk_idx = sl.take<int>((size_t)g.ntg * 2);
     t.chunk_off = sl.take<int>((size_t)N + 1);
   }
-  if (cseg_supported(K)) {
-    t.nseg = cseg_count(N, H, T);
+  if (walk_segmented(N, H, T, K)) {
+    t.nseg = walk_segments(N, H, T, K);
     t.segD = sl.take<float>((size_t)N * H * t.nseg * K * K);
     t.segM = sl.take<float>((size_t)N * H * t.nseg * K);
-  } else {
+  }
+  if (!cseg_supported(K)) {
     t.z = sl.take<float>((size_t)tokens * H * K);
     t.srow = sl.take<float>((size_t)tokens * H);
     t.mpre = sl.take<float>((size_t)g.ntg * H * K);
@@ -212,13 +225,12 @@ size_t carve_walk_work(char* base, const WalkGeom& g, int64_t tokens, int N, int
   Slicer sl{base};
   WalkWork t{};
   t.sc = sl.take<float>((size_t)tokens * H * 4);
-  if (cseg_supported(K)) {
-    const int nseg = cseg_count(N, H, T);
+  if (walk_segmented(N, H, T, K)) {
+    const int nseg = walk_segments(N, H, T, K);
     t.segG = sl.take<float>((size_t)N * H * nseg * K * K);
     t.segDM = sl.take<float>((size_t)N * H * nseg * K);
-  } else {
-    t.dmsum = sl.take<float>((size_t)g.ntg * H * K);
   }
+  if (!cseg_supported(K)) t.dmsum = sl.take<float>((size_t)g.ntg * H * K);
   if (gate) {
     t.dw_part = sl.take<float>((size_t)g.ntg * H * K);
     t.db_part = sl.take<float>((size_t)g.ntg * H);
@@ -284,6 +296,10 @@ int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float
       return s;
     return hip_status(timed("clean_fwd", st, [&] { return launch_cseg(kSegFwd, a, st); }), "ccq_clean_fwd");
   }
+  if (sv.segD) {
+    if (int s = hip_status(timed("clean_fwd_sum", st, [&] { return launch_cseg(kSegSum, a, st); }), "clean_fwd_sum"))
+      return s;
+  }
   return hip_status(timed("clean_fwd", st, [&] { return launch_cwalk(kWalkFwd, a, st); }), "ccq_clean_fwd");
 }
 
@@ -339,6 +355,12 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
   } else {
     const StageName stages[] = {{kWalkRows, "clean_bwd_rows"}, {kWalkDq, "clean_bwd_dq"}, {kWalkDk, "clean_bwd_dk"}};
     for (const StageName& sn : stages) {
+      if (sn.stage == kWalkDk && sv.segD) {
+        // the dk walk's later segments enter through their totals (from the per-token scalars)
+        if (int s = hip_status(timed("clean_bwd_gsum", st, [&] { return launch_cseg(kSegGsum, a, st); }),
+                               "clean_bwd_gsum"))
+          return s;
+      }
       if (int s = hip_status(timed(sn.name, st, [&] { return launch_cwalk(sn.stage, a, st); }), sn.name)) return s;
     }
   }

@@ -171,16 +171,28 @@ __device__ __forceinline__ void score_to_lds(const f32x4& acc, bf16* p, int plan
   *(bf16x4*)(p + plane + e) = ll;
 }
 
-// One segment of one (sequence, head): chunks [cb, ce) of the sequence's nc chunks.
+// State columns per workgroup of the segment kernels (one 16-column tile per wavefront) and column
+// blocks per (sequence, head): K = 256 splits its columns over two workgroups (the segment sums only;
+// the walks of K = 256 are column walks).
+template <int K>
+struct SegCols {
+  static constexpr int CW = K > 128 ? 128 : K, NCB = K / CW, NW = CW / 16, NT = 64 * NW;
+};
+
+// One segment of one (sequence, head) and one column block: chunks [cb, ce) of the sequence's nc
+// chunks, state columns [cbase, cbase + CW).
 struct SegUnit {
-  int unit, seg, n, h, len, nc, cb, ce, gc0;
+  int unit, seg, cbase, n, h, len, nc, cb, ce, gc0;
   long bos, hb, rs;
 };
 
 template <int K>
 __device__ __forceinline__ SegUnit seg_unit(const WalkArgs& a) {
   SegUnit u;
-  xcd_map(blockIdx.x, a.nseg, a.N * a.H, u.unit, u.seg);
+  int sub;
+  xcd_map(blockIdx.x, a.nseg * SegCols<K>::NCB, a.N * a.H, u.unit, sub);
+  u.seg = sub / SegCols<K>::NCB;
+  u.cbase = (sub % SegCols<K>::NCB) * SegCols<K>::CW;
   u.n = u.unit / a.H;
   u.h = u.unit % a.H;
   seq_bounds(a.cu, u.n, a.T, u.bos, u.len);
@@ -273,16 +285,17 @@ __device__ __forceinline__ void add_seg_tiles(f32x4 (&X)[K / 16], const float* t
 }  // namespace
 
 // ===========================================================================
-// cs_sum: grid N*H*nseg, K/16 waves.  segD = sum over the segment's chunks of K^T K, segM = sum of
-// k (every workgroup writes its totals, zero for an empty segment).  Two chunks in flight.
+// cs_sum: grid N*H*nseg*NCB, CW/16 waves.  segD[:, cols] = sum over the segment's chunks of
+// K^T K[:, cols], segM[cols] = sum of k (every workgroup writes its totals, zero for an empty
+// segment).  Two chunks in flight.
 // ===========================================================================
 template <int K>
-__global__ __launch_bounds__(K * 4) void cs_sum_kernel(const WalkArgs a) {
-  constexpr int NW = K / 16, NT = 64 * NW, LDK = K + 16, NKT = K / 16;
+__global__ __launch_bounds__(SegCols<K>::NT) void cs_sum_kernel(const WalkArgs a) {
+  constexpr int NT = SegCols<K>::NT, LDK = K + 16, NKT = K / 16;
   __shared__ __attribute__((aligned(16))) bf16 sK[2][SB * LDK];
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
   const SegUnit u = seg_unit<K>(a);
-  const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
+  const int c0 = u.cbase + 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
   auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
   f32x4 D[NKT];
 #pragma unroll
@@ -344,6 +357,7 @@ __global__ __launch_bounds__(K * 4) void cs_sum_kernel(const WalkArgs a) {
 // ===========================================================================
 template <int K, bool MEAN, bool GATE>
 __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
+  static_assert(K <= 128, "segment walks hold all K columns of a (sequence, head) in one workgroup");
   constexpr int NW = K / 16, NT = 64 * NW;
   // row pitch of the q / k tiles: K + 8 bf16 (a pitch of 4 banks mod 32 spreads the 16 rows of a
   // fragment read; measured faster here than K + 16)
@@ -599,6 +613,7 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
 // ===========================================================================
 template <int K, bool MEAN, bool GATE, bool DQ32>
 __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
+  static_assert(K <= 128, "segment walks hold all K columns of a (sequence, head) in one workgroup");
   constexpr int NW = K / 16, NT = 64 * NW;
   constexpr int LDK = K + 16, LDA = SB + 16, LDD = K + 4;
   constexpr int NKS = K / 32, NKT = K / 16;
@@ -949,19 +964,21 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
-// cs_gsum: grid N*H*nseg, K/16 waves.  segG = sum over the segment of Q^T dZ (dZ = diag(f) dQc),
-// segDM = sum of dm_t = -(s_t/pos_t) dz_t + ds_t q_t (every workgroup writes, zero when empty).
+// cs_gsum: grid N*H*nseg*NCB, CW/16 waves.  segG[:, cols] = sum over the segment of Q^T dZ[:, cols]
+// (dZ = diag(f) dQc), segDM[cols] = sum of dm_t = -(s_t/pos_t) dz_t + ds_t q_t (every workgroup
+// writes, zero when empty).  Reads the per-token scalars (f, ds, -s/pos) written by the dq walk
+// (K <= 128) or by the per-token pass of the column walks (K = 256).
 // ===========================================================================
 template <int K, bool MEAN, bool DQ32>
-__global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
-  constexpr int NW = K / 16, NT = 64 * NW, LDK = K + 16, NKT = K / 16, VPR = K / 4;
+__global__ __launch_bounds__(SegCols<K>::NT) void cs_gsum_kernel(const WalkArgs a) {
+  constexpr int NT = SegCols<K>::NT, LDK = K + 16, NKT = K / 16, VPR = K / 4;
   __shared__ __attribute__((aligned(16))) bf16 sQ[SB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDK];
   __shared__ __attribute__((aligned(16))) float sDs[SB], sSp[SB];
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
   const SegUnit u = seg_unit<K>(a);
-  const int c0 = 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
+  const int c0 = u.cbase + 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
   auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
   f32x4 G[NKT];
 #pragma unroll
@@ -1055,6 +1072,7 @@ __global__ __launch_bounds__(K * 4) void cs_gsum_kernel(const WalkArgs a) {
 // ===========================================================================
 template <int K, bool MEAN, bool DQ32>
 __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
+  static_assert(K <= 128, "segment walks hold all K columns of a (sequence, head) in one workgroup");
   constexpr int NW = K / 16, NT = 64 * NW;
   constexpr int LDK = K + 16, LDA = SB + 16, LDO = K + 4;
   constexpr int NKS = K / 32, NKT = K / 16, VPR = K / 4;
@@ -1321,6 +1339,32 @@ int seg_cu_count() {
   return cache[dev];
 }
 
+// The segment sums of K = 256 (the sums and the gradient sums; its walks are column walks).
+template <int K>
+hipError_t cseg_sums_k(int stage, const WalkArgs& a, hipStream_t st) {
+  const long wgs = (long)a.N * a.H * a.nseg * SegCols<K>::NCB;
+  if (wgs <= 0) return hipSuccess;
+  const dim3 grid((unsigned)wgs), block(SegCols<K>::NT);
+  const bool mean = a.subtract_mean != 0;
+  switch (stage) {
+    case kSegSum:
+      hipLaunchKernelGGL(cs_sum_kernel<K>, grid, block, 0, st, a);
+      break;
+    case kSegGsum:
+      if (a.dqc32) {
+        if (mean) hipLaunchKernelGGL((cs_gsum_kernel<K, true, true>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((cs_gsum_kernel<K, false, true>), grid, block, 0, st, a);
+      } else {
+        if (mean) hipLaunchKernelGGL((cs_gsum_kernel<K, true, false>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((cs_gsum_kernel<K, false, false>), grid, block, 0, st, a);
+      }
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int K>
 hipError_t cseg_k(int stage, const WalkArgs& a, hipStream_t st) {
   const long wgs = (long)a.N * a.H * a.nseg;
@@ -1375,23 +1419,29 @@ hipError_t cseg_k(int stage, const WalkArgs& a, hipStream_t st) {
 
 }  // namespace
 
-// Segments per sequence: enough workgroups to cover the CUs, at least two chunks per segment
-// (T: the dense length, or the packed length of a varlen batch).
-int cseg_count(int N, int H, int T) {
+// Segments per sequence, at least two 64-token chunks each (T: the dense length, or the packed
+// length of a varlen batch).  Segment walks (K in {64, 128}): enough workgroups to cover the CUs.
+// K = 256: its column walks run K / 32 workgroups per (sequence, head) and segment, one per CU:
+// as many segments as fill the CUs without a second round of workgroups.
+int cseg_count(int N, int H, int T, int K) {
   const long units = (long)N * H;
   if (units <= 0) return 1;
   const int chunks = (T + SB - 1) / SB;
-  int nseg = (int)((seg_cu_count() + units - 1) / units);
+  int nseg;
+  if (K > 128) nseg = (int)(seg_cu_count() / (units * (K / 32)));
+  else nseg = (int)((seg_cu_count() + units - 1) / units);
   nseg = min(nseg, max(1, chunks / 2));
   return max(1, min(nseg, 16));
 }
 
 bool cseg_supported(int K) { return K == 64 || K == 128; }
+bool cseg_sums_supported(int K) { return K == 64 || K == 128 || K == 256; }
 
 hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st) {
   switch (a.K) {
     case 64: return cseg_k<64>(stage, a, st);
     case 128: return cseg_k<128>(stage, a, st);
+    case 256: return cseg_sums_k<256>(stage, a, st);
     default: return hipErrorInvalidValue;
   }
 }

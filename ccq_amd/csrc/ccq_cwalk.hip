@@ -105,21 +105,36 @@ __device__ __forceinline__ void load16(const float* p32, const bf16* p16, long b
   }
 }
 
+// One walk: (sequence, head, 32-column tile, time segment).  Chunks [cb, ce) of the sequence's nc
+// chunks; with one segment that is the whole sequence.  Segments are whole 64-token blocks (the
+// blocks of the segment sums, ccq_cseg.hip): nc64 blocks cut into pieces of ceil(nc64 / nseg).
 struct WalkUnit {
-  int unit, ct, c0, h, n, len, nc, gc0;
+  int unit, ct, c0, seg, nseg, h, n, len, nc, cb, ce, gc0;
   long bos, hb, rs;
 };
 
-// Workgroup -> (sequence, head, 32-column tile); the K/32 tiles of one (sequence, head) share an XCD.
+// Workgroup -> (sequence, head, 32-column tile, segment); the workgroups of one (sequence, head)
+// share an XCD.
 template <int K>
 __device__ __forceinline__ WalkUnit walk_unit(const WalkArgs& a) {
   WalkUnit u;
-  xcd_map(blockIdx.x, K / 32, a.N * a.H, u.unit, u.ct);
+  u.nseg = a.segD ? a.nseg : 1;
+  int sub;
+  xcd_map(blockIdx.x, (K / 32) * u.nseg, a.N * a.H, u.unit, sub);
+  u.ct = sub % (K / 32);
+  u.seg = sub / (K / 32);
   u.n = u.unit / a.H;
   u.h = u.unit % a.H;
   u.c0 = u.ct * 32;
   seq_bounds(a.cu, u.n, a.T, u.bos, u.len);
   u.nc = (u.len + Walk<K>::CB - 1) / Walk<K>::CB;
+  {
+    constexpr int R = 64 / Walk<K>::CB;  // walk chunks per 64-token block
+    const int nb = (u.len + 63) / 64, per = (nb + u.nseg - 1) / u.nseg;
+    const int b0 = min(nb, u.seg * per), b1 = min(nb, b0 + per);
+    u.cb = min(u.nc, b0 * R);
+    u.ce = min(u.nc, b1 * R);
+  }
   u.gc0 = a.cu ? a.chunk_off[u.n] : u.n * a.NT;
   u.rs = (long)a.H * K;
   u.hb = (u.bos * a.H + u.h) * (long)K;  // element (t, c) of the sequence: hb + t * rs + c
@@ -242,10 +257,31 @@ __device__ __forceinline__ void store_slice(const f32x16 (&S)[Walk<K>::TPW], flo
   }
 }
 
+// Add the segment totals tot[unit][s] (fp32 [K, K] each) for s in [s0, s1) to a state slice
+// (tiles as load_slice), optionally with their transposes.
+template <int K>
+__device__ __forceinline__ void add_seg_slice(f32x16 (&S)[Walk<K>::TPW], const float* tot, long unit, int nseg, int s0,
+                                              int s1, int sw, int c0, bool with_transpose) {
+  for (int s = s0; s < s1; ++s) {
+    const float* p = tot + ((long)unit * nseg + s) * K * K;
+#pragma unroll
+    for (int j = 0; j < Walk<K>::TPW; ++j) {
+      const int rt = sw + Walk<K>::NSW * j;
+      if (sw >= 0 && rt < Walk<K>::NRT) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int r = rt * 32 + acc_row(i), c = c0 + acc_col();
+          S[j][i] += p[(long)r * K + c] + (with_transpose ? p[(long)c * K + r] : 0.f);
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 // ===========================================================================
-// cw_fwd: grid N*H*(K/32).  Roles: output waves (0..NB-1) compute the chunk's rows and do every
+// cw_fwd: grid N*H*(K/32)*nseg.  Roles: output waves (0..NB-1) compute the chunk's rows and do every
 // global store; state waves (NB..3) own the state slice and do every global load (one chunk ahead),
 // so a wave that stores never waits for a load and vice versa.
 //   stage    state waves: Q, K, lambda, C[:, cols] (hi/lo), m_prev (fp32 + hi/lo) into LDS
@@ -279,14 +315,17 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
   const int lt = tid - NB * 64;  // loader-thread index (state waves)
   const float gbias = gate ? a.gate_b[u.h] : 0.f;
 
+  // state at the segment start: h_0 (+ the earlier segments' K^T K and key sums)
   f32x16 C[TPW], Mk[TPW];
   load_slice<K>(C, a.h0 ? a.h0 + (long)u.unit * K * K : nullptr, sw, u.c0, false);
+  if (u.seg > 0) add_seg_slice<K>(C, a.segD, u.unit, u.nseg, 0, u.seg, sw, u.c0, false);
 #pragma unroll
   for (int j = 0; j < TPW; ++j) {
     const int rt = sw + NSW * j;
     Mk[j] = zero16();
-    if (mean && a.m0 && sw >= 0 && rt < NRT) {
-      const float m = a.m0[(long)u.unit * K + rt * 32 + acc_col()];
+    if (mean && sw >= 0 && rt < NRT) {
+      float m = a.m0 ? a.m0[(long)u.unit * K + rt * 32 + acc_col()] : 0.f;
+      for (int s2 = 0; s2 < u.seg; ++s2) m += a.segM[((long)u.unit * u.nseg + s2) * K + rt * 32 + acc_col()];
 #pragma unroll
       for (int i = 0; i < 16; ++i) Mk[j][i] = m;
     }
@@ -309,9 +348,9 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
     pk.load((const bf16*)a.k + off, u.rs, L, lt);
     if (!gate && lt < CB) plam = a.lam[(u.bos + (long)c * CB + min(lt, L - 1)) * a.H + u.h];
   };
-  if (sw >= 0 && u.nc > 0) issue(0);
+  if (sw >= 0 && u.cb < u.ce) issue(u.cb);
 
-  for (int c = 0; c < u.nc; ++c) {
+  for (int c = u.cb; c < u.ce; ++c) {
     const int b = c & 1, t0 = c * CB, L = min(CB, u.len - t0);
     bf16* Q = sQ[b];
     bf16* Kc = sK[b];
@@ -339,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
     __syncthreads();
 
     // ---- phase 1
-    if (sw >= 0 && c + 1 < u.nc) issue(c + 1);
+    if (sw >= 0 && c + 1 < u.ce) issue(c + 1);
     if (w < W::NBLK) {
       // score block A^T = K_J Q_I^T: element (s, t) = k_s . q_t, kept for s <= t
       const int I = blk_row(w), J = blk_col(w);
@@ -468,8 +507,9 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
     }
   }
 
-  if (a.h_fin) store_slice<K>(C, a.h_fin + (long)u.unit * K * K, sw, u.c0);
-  if (mean && u.ct == 0 && a.m_fin && sw >= 0 && l < 32) {
+  const bool last = u.seg == u.nseg - 1;
+  if (last && a.h_fin) store_slice<K>(C, a.h_fin + (long)u.unit * K * K, sw, u.c0);
+  if (last && mean && u.ct == 0 && a.m_fin && sw >= 0 && l < 32) {
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
       const int rt = sw + NSW * j;
@@ -696,7 +736,7 @@ __global__ __launch_bounds__(kThreads) void cw_rows_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
-// cw_dq: grid N*H*(K/32); forward walk of C.  Same roles as cw_fwd (state waves load, output waves
+// cw_dq: grid N*H*(K/32)*nseg; forward walk of C (from the segment's start state).  Same roles as cw_fwd (state waves load, output waves
 // store); for K <= 128 the staged tiles are double-buffered (two barriers per chunk, the stage of the
 // next chunk overlapping the output rows of this one), for K = 256 one buffer and three barriers:
 //   stage    state waves: dZ (hi/lo), K, C[:, cols] (hi/lo), row scalars, key sums
@@ -727,6 +767,7 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
 
   f32x16 C[TPW];
   load_slice<K>(C, a.h0 ? a.h0 + (long)u.unit * K * K : nullptr, sw, u.c0, false);
+  if (u.seg > 0) add_seg_slice<K>(C, a.segD, u.unit, u.nseg, 0, u.seg, sw, u.c0, false);
   if (tid < 32) sWc[tid] = gate ? a.gate_w[(long)u.h * K + u.c0 + tid] : 0.f;
 
   PrefetchDzRows<K, CB, NLT> pz;
@@ -739,7 +780,7 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
     const long base = u.hb + (long)c * CB * u.rs + u.c0 + acc_col();
     load16(a.dqc32, (const bf16*)a.dqc16, base, u.rs, gcol, orow, min(CB, u.len - c * CB));
   };
-  if (w < NB && u.nc > 0) issue_cols(0);
+  if (w < NB && u.cb < u.ce) issue_cols(u.cb);
   auto issue = [&](int c) {
     const int L = min(CB, u.len - c * CB);
     const long off = u.hb + (long)c * CB * u.rs;
@@ -750,9 +791,9 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
     if (lt < CB) prow = *(const f32x4*)(a.sc + (ti0 + (long)min(lt, L - 1) * a.H) * 4);
     if (mean && lt >= 64 && lt < 96) pmp = a.mpre[((long)(u.gc0 + c) * a.H + u.h) * K + u.c0 + lt - 64];
   };
-  if (sw >= 0 && u.nc > 0) issue(0);
+  if (sw >= 0 && u.cb < u.ce) issue(u.cb);
 
-  for (int c = 0; c < u.nc; ++c) {
+  for (int c = u.cb; c < u.ce; ++c) {
     const int t0 = c * CB, L = min(CB, u.len - t0), b = (NBUF == 2) ? (c & 1) : 0;
     bf16* sZh = sZh_[b];
     bf16* sZl = sZl_[b];
@@ -775,7 +816,7 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
     __syncthreads();
 
     // ---- phase 1
-    if (sw >= 0 && c + 1 < u.nc) issue(c + 1);
+    if (sw >= 0 && c + 1 < u.ce) issue(c + 1);
     if (w < W::NBLK) {
       const int I = blk_row(w), J = blk_col(w);
       f32x16 ah = zero16();
@@ -831,7 +872,7 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
         if (gate) d[i] += dlv[i] * wc;
       }
       store16(a.dq32, (bf16*)a.dq, rowbase, u.rs, d, r0, L);
-      if (c + 1 < u.nc) issue_cols(c + 1);
+      if (c + 1 < u.ce) issue_cols(c + 1);
     } else {
       bf16x8 kc[CB / 16];
 #pragma unroll
@@ -850,7 +891,8 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
-// cw_dk: grid N*H*(K/32); reverse walk of E = G + G^T (G = dC_T + sum of q dz^T over later chunks).
+// cw_dk: grid N*H*(K/32)*nseg; reverse walk of E = G + G^T (G = dC_T + sum of q dz^T over later
+// chunks; the later segments enter through their totals, segG and segDM).
 // The in-chunk suffix sums of dm_t = ds_t q_t - (s_t/pos_t) dz_t ride along the score products:
 //   dk_j = K E + sum_{t>=j} (B1[j][t] + ds_t) q_t + sum_{t>=j} (B2[j][t] - s_t/pos_t) dz_t + carry,
 // where the masked diagonal terms enter as their own hi/lo fragments (|s/pos| can exceed |q . k| by
@@ -887,6 +929,9 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
   const bool mean = a.subtract_mean != 0;
   const int sw = w - NB, lt = tid - NB * 64;
 
+  // E at the end of the segment: dC_T + dC_T^T (+ the later segments' G + G^T); G (dC_0, written
+  // by the first segment) starts from dC_T + the later segments' G
+  const bool first = u.seg == 0;
   f32x16 E[TPW], G[TPW];  // G is dead unless DH0
   {
     const float* dhf = a.dh_fin ? a.dh_fin + (long)u.unit * K * K : nullptr;
@@ -898,10 +943,20 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
       if constexpr (DH0) G[j] = E[j];
       E[j] += Tt[j];
     }
+    if (u.seg + 1 < u.nseg) {
+      add_seg_slice<K>(E, a.segG, u.unit, u.nseg, u.seg + 1, u.nseg, sw, u.c0, true);
+      if constexpr (DH0) add_seg_slice<K>(G, a.segG, u.unit, u.nseg, u.seg + 1, u.nseg, sw, u.c0, false);
+    }
   }
-  // carry lanes: loader threads lt in [64, 96) own column lt - 64 of the carry
+  // carry lanes: loader threads lt in [64, 96) own column lt - 64 of the carry (dm_T + the later
+  // segments' dm sums)
   const bool carl = lt >= 64 && lt < 96;
-  if (carl) sCar[0][lt - 64] = (mean && a.dm_fin) ? a.dm_fin[(long)u.unit * K + u.c0 + lt - 64] : 0.f;
+  if (carl) {
+    float car = (mean && a.dm_fin) ? a.dm_fin[(long)u.unit * K + u.c0 + lt - 64] : 0.f;
+    if (mean)
+      for (int s2 = u.seg + 1; s2 < u.nseg; ++s2) car += a.segDM[((long)u.unit * u.nseg + s2) * K + u.c0 + lt - 64];
+    sCar[0][lt - 64] = car;
+  }
 
   PrefetchRows<K, CB, NLT> pq, pk;
   PrefetchDzRows<K, CB, NLT> pz;
@@ -924,13 +979,13 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
     const long base = u.hb + (long)c * CB * u.rs + u.c0 + acc_col();
     load16(a.dk_extra, nullptr, base, u.rs, xcol, orow, min(CB, u.len - c * CB));
   };
-  if (u.nc > 0) {
-    if (sw >= 0) issue(u.nc - 1);
-    else if (a.dk_extra) issue_cols(u.nc - 1);
+  if (u.cb < u.ce) {
+    if (sw >= 0) issue(u.ce - 1);
+    else if (a.dk_extra) issue_cols(u.ce - 1);
   }
 
   int p = 0;
-  for (int c = u.nc - 1; c >= 0; --c, p ^= 1) {
+  for (int c = u.ce - 1; c >= u.cb; --c, p ^= 1) {
     const int t0 = c * CB, L = min(CB, u.len - t0);
     if (sw >= 0) {
       pq.store(sQ, LDK, L, lt);
@@ -952,7 +1007,7 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
     __syncthreads();
 
     // ---- phase 1
-    if (sw >= 0 && c > 0) issue(c - 1);
+    if (sw >= 0 && c > u.cb) issue(c - 1);
     if (w < W::NBLK) {
       const int T = blk_row(w), J = blk_col(w);
       f32x16 b1h = zero16(), b2 = zero16();
@@ -1029,7 +1084,7 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) d[i] = x[i] + car + (a.dk_extra ? xcol[i] : 0.f);
       store16(a.dk32, (bf16*)a.dk, rowbase, u.rs, d, r0, L);
-      if (a.dk_extra && c > 0) issue_cols(c - 1);
+      if (a.dk_extra && c > u.cb) issue_cols(c - 1);
     } else {
 #pragma unroll
       for (int s = 0; s < CB / 16; ++s) {
@@ -1043,7 +1098,7 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
             const bf16x8 qr = frag_cm(sQ + s * 16 * LDK + rt * 32, LDK);   // (r, t) = q_t[rt*32 + r]
             const bf16x8 zr = frag_cm(sZh + s * 16 * LDK + rt * 32, LDK);  // (r, t) = dz_t[rt*32 + r]
             const bf16x8 zrl = frag_cm(sZl + s * 16 * LDK + rt * 32, LDK);
-            if constexpr (DH0) {
+            if (DH0 && first) {
               G[j] = mfma(qr, zc, G[j]);
               G[j] = mfma(qr, zcl, G[j]);
             }
@@ -1058,8 +1113,10 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
     __syncthreads();
   }
 
-  if constexpr (DH0) store_slice<K>(G, a.dh0 + (long)u.unit * K * K, sw, u.c0);
-  if (a.dm0 && carl) a.dm0[(long)u.unit * K + u.c0 + lt - 64] = mean ? sCar[p][lt - 64] : 0.f;
+  if constexpr (DH0) {
+    if (first) store_slice<K>(G, a.dh0 + (long)u.unit * K * K, sw, u.c0);
+  }
+  if (first && a.dm0 && carl) a.dm0[(long)u.unit * K + u.c0 + lt - 64] = mean ? sCar[p][lt - 64] : 0.f;
 }
 
 // ===========================================================================
@@ -1069,7 +1126,7 @@ namespace {
 
 template <int K>
 hipError_t cwalk_k(int stage, const WalkArgs& a, hipStream_t st) {
-  const long units = (long)a.N * a.H * (K / 32);
+  const long units = (long)a.N * a.H * (K / 32) * (a.segD ? a.nseg : 1);
   switch (stage) {
     case kWalkFwd:
       if (units > 0) hipLaunchKernelGGL(cw_fwd_kernel<K>, dim3((unsigned)units), dim3(kThreads), 0, st, a);

@@ -56,6 +56,10 @@ CLEAN_CASES = [
     # several 256-token segments per sequence (segment prefix + cross-segment state)
     (1, 1000, 2, 128, True, True, 0, True, None),
     (1, 900, 2, 64, False, True, 2, True, [0, 300, 301, 301, 900]),
+    # K = 256: column walks cut into time segments (segment totals from the segment sums)
+    (1, 1000, 2, 256, True, True, 0, True, None),
+    (1, 900, 2, 256, False, True, 2, True, [0, 300, 301, 301, 900]),
+    (2, 700, 1, 256, True, False, 5, False, None),
 ]
 
 
