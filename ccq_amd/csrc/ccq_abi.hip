@@ -30,7 +30,6 @@ int cseg_count(int N, int H, int T, int K);
 bool cseg_sums_supported(int K);
 bool cseg_supported(int K);
 hipError_t decode_scratch(hipStream_t st, void** out);
-hipError_t launch_decode_finish(float* m, const float* m_new, long n, int* pos, int advance, hipStream_t st);
 hipError_t launch_zclean(int stage, const ZCleanArgs& a, hipStream_t st);
 hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_chunk_index(const int64_t* cu, int N, int size, int* chunk_off, int* chunk_idx, int cap,
@@ -845,6 +844,12 @@ int decode_step(const char* who, bool gla, const void* q, const void* k, const v
                             subtract_mean, use_l2norm, enable_ccq, scale))
     return s;
   a.pos_dev = position;
+  a.pos_adv = position;
+  if (mean) {
+    a.m_dst = mean_state;
+    a.m_src = m_new;
+    a.m_count = (long)B * H * K;
+  }
   if (gla) {
     a.gk = gk;
     a.gla = 1;
@@ -852,11 +857,7 @@ int decode_step(const char* who, bool gla, const void* q, const void* k, const v
     a.g = g;
     a.beta = beta;
   }
-  const hipStream_t st = (hipStream_t)stream;
-  if (int s = hip_status(launch_decode(a, st), who)) return s;
-  return hip_status(launch_decode_finish(mean ? mean_state : nullptr, m_new, mean ? (long)B * H * K : 0, position, T,
-                                         st),
-                    who);
+  return hip_status(launch_decode(a, (hipStream_t)stream), who);
 }
 
 }  // namespace

@@ -9,12 +9,12 @@
 //   GLA: S <- diag(e^gk) S + k v^T;  o = S^T (scale q_clean)
 //
 // The step is HBM-bound (each state element is read and written once per call).  Two launches:
-//   decode_clean   grid (N*H, K/64): each workgroup owns 64 columns of C (held in registers across
+//   decode_clean   grid (N*H, K/32): each workgroup owns 32 columns of C (held in registers across
 //                  the call's tokens) and writes the fp32 cleaned query of those columns;
-//   decode_backbone grid (N*H, V/64): each workgroup owns 64 columns of S, reads the cleaned query.
-// Thread (column j = tid % 64, row group tid / 64) holds K/4 consecutive rows of its column, so
-// every state access is a coalesced 256-byte row segment.
-#include <algorithm>
+//   decode_backbone grid (N*H, V/32): each workgroup owns 32 columns of S, reads the cleaned query;
+//                  an in-place step (device-held position) also moves the new key sum over the
+//                  cached one and advances the position here.
+// Thread (column j = tid % 32, row group tid / 32) holds K/8 consecutive rows of its column.
 #include <mutex>
 
 #include "ccq_tile.h"
@@ -55,25 +55,30 @@ __device__ __forceinline__ void load_qk(const DecodeArgs& a, long tok, int h, fl
 
 }  // namespace
 
+// Column blocks: a workgroup owns DC = 32 columns of a state and all of its rows, RG = 8 row groups
+// of K / 8 rows per thread: every state access of a wave is two coalesced 128-byte row pieces, and
+// many small workgroups keep several per CU in flight, so one workgroup's loads overlap another's
+// stores.
+constexpr int DC = 32, RG = kThreads / DC;
+
 template <int K>
 __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs a) {
-  constexpr int RPT = K / 4;  // rows per thread
+  constexpr int RPT = K / RG;  // rows per thread
   __shared__ float sq[K], sk[K], sm[K];
-  __shared__ float sz[4][64];
+  __shared__ float sz[RG][DC];
   __shared__ float red[4];
-  const int tid = threadIdx.x, jj = tid & 63, rg = tid >> 6;
+  const int tid = threadIdx.x, jj = tid % DC, rg = tid / DC;
   const int unit = blockIdx.x, n = unit / a.H, h = unit % a.H;
-  const int j = blockIdx.y * 64 + jj;
+  const int j = blockIdx.y * DC + jj;
   long bos;
   int len;
   seq_bounds(a.cu, n, a.T, bos, len);
-  const bool own = j < K;  // K = 32 launches one 64-column slice with half of it idle
 
   const int pos_off = a.pos_dev ? *a.pos_dev : a.pos_off;
   float creg[RPT];
   const float* Cin = a.C_in ? a.C_in + (long)unit * K * K : nullptr;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) creg[r] = (Cin && own) ? Cin[(long)(rg * RPT + r) * K + j] : 0.f;
+  for (int r = 0; r < RPT; ++r) creg[r] = Cin ? Cin[(long)(rg * RPT + r) * K + j] : 0.f;
   if (tid < K) sm[tid] = a.m_in ? a.m_in[(long)unit * K + tid] : 0.f;
   __syncthreads();
 
@@ -99,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
     __syncthreads();
     const float s = block_sum256(tid < K ? sm[tid] * sq[tid] : 0.f, red);
     // C column update and partial z over this thread's rows
-    const float kj = own ? sk[j] : 0.f;
+    const float kj = sk[j];
     float zp = 0.f;
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
@@ -109,8 +114,10 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
     }
     sz[rg][jj] = zp;
     __syncthreads();
-    if (rg == 0 && own) {
-      const float z = sz[0][jj] + sz[1][jj] + sz[2][jj] + sz[3][jj];
+    if (rg == 0) {
+      float z = 0.f;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) z += sz[g][jj];
       float pos = (float)(t + 1 + pos_off);
       pos = pos < 1.f ? 1.f : pos;
       float corr = z / pos;
@@ -119,22 +126,22 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
     }
     __syncthreads();
   }
-  if (a.C_out && own) {
+  if (a.C_out) {
     float* Co = a.C_out + (long)unit * K * K;
 #pragma unroll
     for (int r = 0; r < RPT; ++r) Co[(long)(rg * RPT + r) * K + j] = creg[r];
   }
-  if (a.m_out && rg == 0 && own) a.m_out[(long)unit * K + j] = sm[j];
+  if (a.m_out && rg == 0) a.m_out[(long)unit * K + j] = sm[j];
 }
 
 template <int K>
 __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeArgs a) {
-  constexpr int RPT = K / 4;
+  constexpr int RPT = K / RG;
   __shared__ float sq[K], sk[K], sgk[K];
-  __shared__ float sp[4][64];
-  const int tid = threadIdx.x, vv = tid & 63, rg = tid >> 6;
+  __shared__ float sp[RG][DC];
+  const int tid = threadIdx.x, vv = tid % DC, rg = tid / DC;
   const int unit = blockIdx.x, n = unit / a.H, h = unit % a.H;
-  const int V = a.V, v = blockIdx.y * 64 + vv;
+  const int V = a.V, v = blockIdx.y * DC + vv;
   long bos;
   int len;
   seq_bounds(a.cu, n, a.T, bos, len);
@@ -143,6 +150,16 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
   const float* Sin = a.S_in ? a.S_in + (long)unit * K * V : nullptr;
 #pragma unroll
   for (int r = 0; r < RPT; ++r) sreg[r] = Sin ? Sin[(long)(rg * RPT + r) * V + v] : 0.f;
+
+  // end of an in-place step (the clean kernel, launched before in the same stream, has read the
+  // cached key sum and the position): the new key sum replaces the cached one, the position
+  // advances by the step's tokens
+  if (a.m_dst) {
+    const long nthreads = (long)gridDim.x * gridDim.y * kThreads;
+    const long gid = ((long)blockIdx.y * gridDim.x + blockIdx.x) * kThreads + tid;
+    for (long i = gid; i < a.m_count; i += nthreads) a.m_dst[i] = a.m_src[i];
+  }
+  if (a.pos_adv && blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *a.pos_adv += a.T;
 
   for (int t = 0; t < len; ++t) {
     const long tok = bos + t;
@@ -169,7 +186,9 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
       }
       sp[rg][vv] = p;
       __syncthreads();
-      const float ks = sp[0][vv] + sp[1][vv] + sp[2][vv] + sp[3][vv];
+      float ks = 0.f;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) ks += sp[g][vv];
       const float u = a.beta[tok * a.H + h] * (vt - ks);
 #pragma unroll
       for (int r = 0; r < RPT; ++r) sreg[r] += sk[rg * RPT + r] * u;
@@ -181,8 +200,10 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
     sp[rg][vv] = po;
     __syncthreads();
     if (rg == 0) {
-      const float o = a.scale * (sp[0][vv] + sp[1][vv] + sp[2][vv] + sp[3][vv]);
-      ((bf16*)a.o)[(tok * a.H + h) * V + v] = (bf16)o;
+      float o = 0.f;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) o += sp[g][vv];
+      ((bf16*)a.o)[(tok * a.H + h) * V + v] = (bf16)(a.scale * o);
     }
     __syncthreads();
   }
@@ -193,26 +214,11 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
   }
 }
 
-// End of a step with device-held position and in-place states: the new key sum (written beside
-// the cached one: every clean workgroup reads all of the cached sum) replaces it, and the position
-// offset advances by the step's tokens.  Launched after the step's kernels (stream order).
-__global__ __launch_bounds__(kThreads) void decode_finish_kernel(float* m, const float* m_new, long n, int* pos,
-                                                                 int advance) {
-  for (long i = (long)blockIdx.x * kThreads + threadIdx.x; i < n; i += (long)gridDim.x * kThreads) m[i] = m_new[i];
-  if (pos && blockIdx.x == 0 && threadIdx.x == 0) *pos += advance;
-}
-
-hipError_t launch_decode_finish(float* m, const float* m_new, long n, int* pos, int advance, hipStream_t st) {
-  const long blocks = n > 0 ? std::min<long>((n + kThreads - 1) / kThreads, 1024) : 1;
-  hipLaunchKernelGGL(decode_finish_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, st, m, m_new, n, pos, advance);
-  return hipGetLastError();
-}
-
 template <int K>
 hipError_t launch_decode_k(const DecodeArgs& a, hipStream_t st) {
   const int units = a.N * a.H;
-  hipLaunchKernelGGL(decode_clean_kernel<K>, dim3(units, (K + 63) / 64), dim3(kThreads), 0, st, a);
-  hipLaunchKernelGGL(decode_backbone_kernel<K>, dim3(units, a.V / 64), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL(decode_clean_kernel<K>, dim3(units, K / DC), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL(decode_backbone_kernel<K>, dim3(units, a.V / DC), dim3(kThreads), 0, st, a);
   return hipGetLastError();
 }
 

@@ -33,6 +33,11 @@ struct DecodeArgs {
   float* kn;               // workspace fp32 [tokens, H, K]: (normalised) key
   const int64_t* cu;       // [N+1] (nullable)
   const int* pos_dev;      // device int: the position offset (nullable: pos_off)
+  // in-place step (nullable): after the clean kernel, m_dst[0, m_count) = m_src and *pos_adv += T
+  float* m_dst;
+  const float* m_src;
+  long m_count;
+  int* pos_adv;
   float scale;
   int T, H, N, K, V, pos_off, subtract_mean, l2norm, ccq, gla;
 };

@@ -5,7 +5,7 @@ The reference generates one token at a time by calling ``fused_recurrent_ccq_gdn
 once per layer with the cache tuple ``(S, C, m, position_offset)`` (``ccq/gdn/layer.py:318-336,
 397``; ``ccq/ops/ccq_gdn/fused_recurrent.py:18-75``).  Per layer and token that is a handful of
 launches plus host work, and the token's latency is launch-bound.  Here each layer's step is the
-library's ``ccq_gdn_decode_step`` / ``ccq_gla_decode_step``: three kernels over static buffers,
+library's ``ccq_gdn_decode_step`` / ``ccq_gla_decode_step``: two kernels over static buffers,
 with the states updated in place and the position offset held in device memory (advanced by the
 step itself), so the same captured graph is replayed for every generated token.
 

@@ -237,8 +237,8 @@ int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lam
  * (S, C, m, position_offset) (ccq/gdn/layer.py:318-336, 397; ccq/gla/layer.py); the position lives
  * on the device here because a captured launch cannot take a new host value per replay.
  * workspace: ccq_decode_step_workspace_bytes(B, T, H, K) (the decode workspace plus the new key
- * sum, copied over mean_state at the end of the step).  Launches three kernels, no allocation and
- * no memset.
+ * sum, copied over mean_state by the step's second kernel).  Launches two kernels, no allocation
+ * and no memset.
  */
 size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K);
 int ccq_gdn_decode_step(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
