@@ -39,7 +39,7 @@ SIGNATURES = {
     "ccq_gla_bwd": (_I, [_P] * 8 + [_I] + [_P] * 11 + [_I] * 6 + [_F, _P]),
     "ccq_decode_workspace_bytes": (_SZ, [_I64, _I, _I]),
     "ccq_gdn_decode": (_I, [_P] * 17 + [_I] * 10 + [_F, _P]),
-    "ccq_gla_decode": (_I, [_P] * 16 + [_I] * 9 + [_F, _P]),
+    "ccq_gla_decode": (_I, [_P] * 17 + [_I] * 10 + [_F, _P]),
     "ccq_gdn_decode_noalloc": (_I, [_P] * 16 + [_I] * 10 + [_F, _P]),
     "ccq_decode_step_workspace_bytes": (_SZ, [_I] * 4),
     "ccq_gdn_decode_step": (_I, [_P] * 14 + [_I] * 8 + [_F, _P]),

@@ -19,6 +19,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, stream_of
+from .clean import as_kernel_dtype, in_dtype
 from .clean import (_check_qk, _f32, check_device, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd,
                     norm_cu_seqlens, reduce_dlambda, reshape_lambda_3d, seq_count)
 
@@ -182,10 +183,13 @@ def fused_chunk_ccq_gdn(q, k, v, lambda_h, g, beta, scale=None, initial_state=No
     if kwargs:
         unknown = ", ".join(sorted(kwargs))
         raise TypeError(f"fused_chunk_ccq_gdn: unsupported keyword arguments: {unknown}")
+    dt = q.dtype
+    q, k, v = as_kernel_dtype(q, k, v)
     o, sfin, hfin, mfin = ChunkCCQGDNFunction.apply(
         q, k, v, lambda_h, g, beta, _default_scale(scale, q.shape[-1]), initial_state, initial_cov_state,
         initial_mean_state if subtract_mean else None, bool(output_final_state), bool(use_qk_l2norm_in_kernel),
         cu_seqlens, int(position_offset), bool(subtract_mean), bool(enable_ccq), gate_w, gate_b)
+    o = in_dtype(o, dt)
     if not output_final_state:
         return o, None, None, None
     return o, sfin, hfin, mfin
@@ -233,9 +237,12 @@ def fused_recurrent_ccq_gdn(q, k, v, lambda_h, g=None, gk=None, gv=None, beta=No
         s0 = initial_state
         if transpose_state_layout and s0 is not None:
             s0 = s0.transpose(-1, -2)
+        dt = q.dtype
+        q, k, v = as_kernel_dtype(q, k, v)
         o, s, c, m = gdn_decode(q, k, v, lambda_h, g, beta, _default_scale(scale, q.shape[-1]), s0, initial_cov_state,
                                 initial_mean_state if subtract_mean else None, bool(output_final_state),
                                 bool(use_qk_l2norm_in_kernel), cu_seqlens, position_offset, subtract_mean, enable_ccq)
+        o = in_dtype(o, dt)
         if not output_final_state:
             return o, None, None, None
         if transpose_state_layout:

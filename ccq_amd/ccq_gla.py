@@ -19,6 +19,7 @@ import torch
 from . import _lib
 from ._lib import call, ptr, stream_of
 from .ccq_gdn import _Chunks, _default_scale
+from .clean import as_kernel_dtype, in_dtype
 from .clean import _check_qk, _f32, check_device, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd, \
     norm_cu_seqlens, reduce_dlambda, reshape_lambda_3d
 
@@ -149,10 +150,13 @@ def fused_chunk_ccq_gla(q, k, v, lambda_h, g=None, scale=None, initial_state=Non
     Returns ``(o, final_state, final_cov_state, final_mean_state)``; the last three are None unless
     ``output_final_state``.  ``gate_w``/``gate_b`` (optional) select the fused per-head gate.
     """
+    dt = q.dtype
+    q, k, v = as_kernel_dtype(q, k, v)
     o, sfin, hfin, mfin = ChunkCCQGLAFunction.apply(
         q, k, v, lambda_h, g, _default_scale(scale, q.shape[-1]), initial_state, initial_cov_state,
         initial_mean_state if subtract_mean else None, bool(output_final_state), True, cu_seqlens,
         int(position_offset), bool(subtract_mean), True, gate_w, gate_b)
+    o = in_dtype(o, dt)
     if not output_final_state:
         return o, None, None, None
     return o, sfin, hfin, mfin
@@ -172,31 +176,80 @@ def fused_recurrent_ccq_gla(q, k, v, lambda_h, gk=None, gv=None, scale=None, ini
                             reverse=False, cu_seqlens=None, position_offset=0, subtract_mean=True):
     """CCQ-GLA, recurrent mode (reference ``ccq/ops/ccq_gla/fused_recurrent.py:9-51``), used for
     decode and (in the reference layer, also in training) for sequences of at most 64 tokens.
+    ``gk`` / ``gv`` decay the backbone state's rows / columns; ``reverse`` runs the backbone
+    recurrence from the last token to the first (the cleaning runs forwards, as in the reference).
     Without autograd it runs the decode kernels; when a gradient is needed it runs the chunk
-    kernels (same recurrence, with a backward)."""
+    kernels (same recurrence, with a backward): with ``reverse``, the cleaning followed by the GLA
+    backbone on the time-reversed sequences.  Gradients with ``gv`` are not supported."""
     from .decode import gla_decode, needs_grad
-    if gv is not None:
-        raise NotImplementedError("fused_recurrent_ccq_gla: per-value gates (gv) are not supported")
-    if reverse:
-        raise NotImplementedError("fused_recurrent_ccq_gla: reverse=True is not supported")
-    if not needs_grad(q, k, v, lambda_h, gk, initial_state, initial_cov_state, initial_mean_state):
+    if not needs_grad(q, k, v, lambda_h, gk, gv, initial_state, initial_cov_state, initial_mean_state):
+        dt = q.dtype
+        q, k, v = as_kernel_dtype(q, k, v)
         o, s, c, m = gla_decode(q, k, v, lambda_h, gk, _default_scale(scale, q.shape[-1]), initial_state,
                                 initial_cov_state, initial_mean_state if subtract_mean else None,
-                                bool(output_final_state), cu_seqlens, position_offset, subtract_mean)
+                                bool(output_final_state), cu_seqlens, position_offset, subtract_mean, gv=gv,
+                                reverse=bool(reverse))
+        o = in_dtype(o, dt)
         if not output_final_state:
             return o, None, None, None
         return o, s, c, m
+    if gv is not None:
+        raise NotImplementedError("fused_recurrent_ccq_gla: gradients through the per-value decay gv are not "
+                                  "supported (inference with gv runs on the decode kernels)")
+    if reverse:
+        return _reverse_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state, initial_mean_state,
+                            output_final_state, cu_seqlens, position_offset, subtract_mean)
     return fused_chunk_ccq_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state, initial_mean_state,
                                output_final_state, cu_seqlens, position_offset, subtract_mean)
 
 
+def _time_flip(x):
+    """Each sequence reversed in time: dense [B, T, ...] along T; a packed batch [1, total, ...]
+    along its whole length, which also reverses the order of its sequences."""
+    return None if x is None else x.flip(1)
+
+
+def _reverse_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state, initial_mean_state,
+                 output_final_state, cu_seqlens, position_offset, subtract_mean):
+    """Differentiable CCQ-GLA with the backbone run backwards in time: the forward cleaning
+    (l2norm, covariance read, cleaning), then the GLA backbone on the time-reversed cleaned
+    queries, keys, values and decays, whose outputs are reversed back.  Reversing a packed batch
+    also reverses the order of its sequences: the cu_seqlens of the reversed batch are the mirrored
+    offsets, and the backbone's initial / final states are taken and returned in the reversed
+    order."""
+    from .clean import fused_ccq_clean_read
+    from .l2norm import l2norm
+    qn, kn = l2norm(q), l2norm(k)
+    qc, hf, mf = fused_ccq_clean_read(qn, kn, lambda_h, position_offset=position_offset,
+                                      initial_cov_state=initial_cov_state,
+                                      initial_mean_state=initial_mean_state if subtract_mean else None,
+                                      output_final_state=output_final_state, subtract_mean=subtract_mean,
+                                      cu_seqlens=cu_seqlens)
+    cu_r, s0 = None, initial_state
+    if cu_seqlens is not None:
+        cu_r = (cu_seqlens[-1] - cu_seqlens.flip(0)).contiguous()
+        if s0 is not None:
+            s0 = s0.flip(0)
+    o_r, s = chunk_gla(_time_flip(qc), _time_flip(kn), _time_flip(v), _time_flip(gk), scale=scale, initial_state=s0,
+                       output_final_state=output_final_state, cu_seqlens=cu_r)
+    o = o_r.flip(1)
+    if not output_final_state:
+        return o, None, None, None
+    if cu_seqlens is not None:
+        s = s.flip(0)
+    return o, s, hf, mf
+
+
 def chunk_gla(q, k, v, g=None, scale=None, initial_state=None, output_final_state=False, cu_seqlens=None, **kwargs):
     """The GLA backbone alone (fla's ``chunk_gla`` signature as the reference calls it,
-    ``ccq/ops/ccq_gla/fused_chunk.py:42-45``).  q, k, v bf16; g the per-channel log decay."""
+    ``ccq/ops/ccq_gla/fused_chunk.py:42-45``).  q, k, v bf16, fp16 or fp32 (computed on bf16
+    operands, returned in the input dtype); g the per-channel log decay."""
     if kwargs:
         unknown = ", ".join(sorted(kwargs))
         raise TypeError(f"chunk_gla: unsupported keyword arguments: {unknown}")
+    dt = q.dtype
+    q, k, v = as_kernel_dtype(q, k, v)
     o, sfin, _, _ = ChunkCCQGLAFunction.apply(
         q, k, v, None, g, _default_scale(scale, q.shape[-1]), initial_state, None, None, bool(output_final_state),
         False, cu_seqlens, 0, True, False, None, None)
-    return o, (sfin if output_final_state else None)
+    return in_dtype(o, dt), (sfin if output_final_state else None)

@@ -91,6 +91,28 @@ def _check_qk(q: torch.Tensor, k: torch.Tensor):
         raise ValueError(f"q and k must both be [B, T, H, K] (got {tuple(q.shape)}, {tuple(k.shape)})")
 
 
+ACCEPTED_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def as_kernel_dtype(*xs):
+    """The activations (q, k, v) as the kernels take them, bf16: the operands of every product
+    enter the matrix cores as bf16, with fp32 accumulation and fp32 states.  The reference runs
+    its kernels in the input dtype; here fp16 and fp32 inputs are rounded to bf16 on the way in
+    (a differentiable cast, so gradients return in the input dtype) and the callers return their
+    outputs in the input dtype.  Other dtypes raise."""
+    out = []
+    for x in xs:
+        if x is not None and x.dtype not in ACCEPTED_DTYPES:
+            raise TypeError(f"ccq_amd ops take bf16, fp16 or fp32 activations (got {x.dtype})")
+        out.append(x if x is None or x.dtype == torch.bfloat16 else x.to(torch.bfloat16))
+    return tuple(out)
+
+
+def in_dtype(x: Optional[torch.Tensor], dtype: torch.dtype) -> Optional[torch.Tensor]:
+    """An output back in the caller's input dtype (no-op for bf16 inputs)."""
+    return x if x is None or x.dtype == dtype else x.to(dtype)
+
+
 def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     return None if t is None else t.float().contiguous()
 
@@ -224,11 +246,13 @@ def fused_ccq_clean_read(q, k, lambda_h, *, position_offset=0, initial_cov_state
 
     Returns ``(q_clean, final_cov_state, final_mean_state)``; the states are None unless requested.
     """
+    dt = q.dtype
+    q, k = as_kernel_dtype(q, k)
     qc, hf, mf = FusedCCQCleanRead.apply(q, k, lambda_h, int(position_offset), initial_cov_state, initial_mean_state,
                                          bool(output_final_state), bool(subtract_mean), cu_seqlens, gate_w, gate_b)
     if not output_final_state:
         hf, mf = None, None
-    return qc, hf, mf
+    return in_dtype(qc, dt), hf, mf
 
 
 # ---------------------------------------------------------------------------

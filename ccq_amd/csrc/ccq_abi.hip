@@ -798,17 +798,18 @@ int ccq_gdn_decode_noalloc(const void* q, const void* k, const void* v, const fl
 }
 
 int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
-                   const float* gate_b, const float* gk, const float* state, const float* cov_state,
+                   const float* gate_b, const float* gk, const float* gv, const float* state, const float* cov_state,
                    const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
                    float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
-                   int N, int position_offset, int subtract_mean, int use_l2norm, float scale, void* stream) {
+                   int N, int position_offset, int subtract_mean, int use_l2norm, int reverse, float scale,
+                   void* stream) {
   DecodeArgs a{};
   if (int s = decode_common("ccq_gla_decode", a, q, k, v, lambda, gate_w, gate_b, state, cov_state, mean_state,
                             cu_seqlens, o, state_out, cov_state_out, mean_state_out, workspace, B, T, H, K, V, N,
                             position_offset, subtract_mean, use_l2norm, 1, scale))
     return s;
   if (K > 256) return fail(CCQ_ERR_SHAPE, "ccq_gla_decode: K=%d", K);
-  a.gk = gk; a.gla = 1;
+  a.gk = gk; a.gv = gv; a.gla = 1; a.reverse = reverse ? 1 : 0;
   return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gla_decode");
 }
 

@@ -6,7 +6,8 @@
 //   C <- C + k k^T;  m <- m + k;  z = C^T q;  s = m . q;  pos = max(t + 1 + position_offset, 1)
 //   q_clean = q - lambda (z / pos - s m / pos^2)          (mean term only with subtract_mean)
 //   GDN: S <- e^g S;  u = beta (v - S^T k);  S <- S + k u^T;  o = S^T (scale q_clean)
-//   GLA: S <- diag(e^gk) S + k v^T;  o = S^T (scale q_clean)
+//   GLA: S <- diag(e^gk) S diag(e^gv) + k v^T;  o = S^T (scale q_clean)  (optionally from the last
+//        token to the first: `reverse`, the cleaning itself always runs forwards)
 //
 // The step is HBM-bound (each state element is read and written once per call).  Two launches:
 //   decode_clean   grid (N*H, K/32): each workgroup owns 32 columns of C (held in registers across
@@ -161,7 +162,9 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
   }
   if (a.pos_adv && blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *a.pos_adv += a.T;
 
-  for (int t = 0; t < len; ++t) {
+  for (int tt = 0; tt < len; ++tt) {
+    // (the cleaned queries of every token are ready: the backbone may run backwards in time)
+    const int t = a.reverse ? len - 1 - tt : tt;
     const long tok = bos + t;
     if (tid < K) {
       sq[tid] = a.qc[(tok * a.H + h) * K + tid];
@@ -171,10 +174,11 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
     __syncthreads();
     const float vt = (float)((const bf16*)a.v)[(tok * a.H + h) * V + v];
     if (a.gla) {
+      const float dv = a.gv ? __expf(a.gv[(tok * a.H + h) * V + v]) : 1.f;
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
         const int i = rg * RPT + r;
-        sreg[r] = sgk[i] * sreg[r] + sk[i] * vt;
+        sreg[r] = sgk[i] * sreg[r] * dv + sk[i] * vt;
       }
     } else {
       const float dec = a.g ? __expf(a.g[tok * a.H + h]) : 1.f;

@@ -21,7 +21,8 @@ struct DecodeArgs {
   const float* gate_b;     // fp32 [H]
   const float* g;          // GDN: fp32 [tokens, H] log decay (nullable)
   const float* beta;       // GDN: fp32 [tokens, H]
-  const float* gk;         // GLA: fp32 [tokens, H, K] log decay (nullable)
+  const float* gk;         // GLA: fp32 [tokens, H, K] log decay of the key rows (nullable)
+  const float* gv;         // GLA: fp32 [tokens, H, V] log decay of the value columns (nullable)
   const float* S_in;       // [N, H, K, V] (nullable = 0)
   const float* C_in;       // [N, H, K, K] (nullable = 0)
   const float* m_in;       // [N, H, K] (nullable = 0)
@@ -40,6 +41,7 @@ struct DecodeArgs {
   int* pos_adv;
   float scale;
   int T, H, N, K, V, pos_off, subtract_mean, l2norm, ccq, gla;
+  int reverse;             // GLA: the backbone recurrence runs from the last token to the first
 };
 
 }  // namespace ccq

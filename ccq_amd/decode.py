@@ -70,20 +70,24 @@ def gdn_decode(q, k, v, lambda_h, g, beta, scale, initial_state=None, initial_co
 
 def gla_decode(q, k, v, lambda_h, gk, scale, initial_state=None, initial_cov_state=None, initial_mean_state=None,
                output_final_state=True, cu_seqlens=None, position_offset=0, subtract_mean=True, gate_w=None,
-               gate_b=None):
-    """One recurrent CCQ-GLA call (l2norm of q and k always on, as the reference).  Returns ``(o, S, C, m)``."""
+               gate_b=None, gv=None, reverse=False):
+    """One recurrent CCQ-GLA call (l2norm of q and k always on, as the reference).  ``gk`` / ``gv``:
+    log decays of the state's rows ``[B, T, H, K]`` and columns ``[B, T, H, V]``; ``reverse`` runs
+    the backbone recurrence from the last token to the first.  Returns ``(o, S, C, m)``."""
     q, k, v, lam, gw, gb, N, ws, cu_seqlens = _prep(
-        q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, True, gk=gk, initial_state=initial_state,
+        q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, True, gk=gk, gv=gv, initial_state=initial_state,
         initial_cov_state=initial_cov_state, initial_mean_state=initial_mean_state)
     B, T, H, K = q.shape
     V = v.shape[-1]
     if gk is not None and gk.shape != q.shape:
         raise ValueError(f"gk must have q's shape {tuple(q.shape)} (got {tuple(gk.shape)})")
+    if gv is not None and gv.shape != v.shape:
+        raise ValueError(f"gv must have v's shape {tuple(v.shape)} (got {tuple(gv.shape)})")
     o = torch.empty(B, T, H, V, device=q.device, dtype=v.dtype)
     S, C, m = _states(N, H, K, V, q.device, output_final_state, True, subtract_mean)
-    gk32, s0, c0, m0 = (_f32(x) for x in (gk, initial_state, initial_cov_state, initial_mean_state))
-    call("ccq_gla_decode", ptr(q), ptr(k), ptr(v), ptr(lam), ptr(gw), ptr(gb), ptr(gk32),
+    gk32, gv32, s0, c0, m0 = (_f32(x) for x in (gk, gv, initial_state, initial_cov_state, initial_mean_state))
+    call("ccq_gla_decode", ptr(q), ptr(k), ptr(v), ptr(lam), ptr(gw), ptr(gb), ptr(gk32), ptr(gv32),
          ptr(s0), ptr(c0), ptr(m0), ptr(cu_seqlens),
          ptr(o), ptr(S), ptr(C), ptr(m), ptr(ws), B, T, H, K, V, N, int(position_offset), int(bool(subtract_mean)),
-         1, float(scale), stream_of(q))
+         1, int(bool(reverse)), float(scale), stream_of(q))
     return o, S, C, m

@@ -6,7 +6,7 @@ from __future__ import annotations
 
 import torch
 
-from .clean import l2norm_bwd, l2norm_fwd
+from .clean import as_kernel_dtype, in_dtype, l2norm_bwd, l2norm_fwd
 
 __all__ = ["l2norm", "L2NormFunction"]
 
@@ -15,7 +15,7 @@ class L2NormFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, eps):
         if not x.is_cuda or x.dtype != torch.bfloat16:
-            raise TypeError("ccq_amd l2norm takes a bf16 CUDA tensor")
+            raise TypeError("ccq_amd l2norm runs on bf16 CUDA tensors (l2norm() converts other dtypes)")
         x = x.contiguous()
         y, rstd = l2norm_fwd(x, eps)
         ctx.save_for_backward(x, rstd)
@@ -28,4 +28,6 @@ class L2NormFunction(torch.autograd.Function):
 
 
 def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    return L2NormFunction.apply(x, float(eps))
+    """fp16 / fp32 rows are normalised as bf16 and returned in their own dtype."""
+    (xb,) = as_kernel_dtype(x)
+    return in_dtype(L2NormFunction.apply(xb, float(eps)), x.dtype)

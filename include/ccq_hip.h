@@ -222,11 +222,19 @@ int ccq_gdn_decode_noalloc(const void* q, const void* k, const void* v, const fl
                            float* state_out, float* cov_state_out, float* mean_state_out, int B, int T, int H, int K,
                            int V, int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq,
                            float scale, void* stream);
+/*
+ * GLA backbone options of the recurrent op (fla fused_recurrent_gla as the reference calls it,
+ * ccq/ops/ccq_gla/fused_recurrent.py:41-49): gk fp32 [tokens, H, K] and gv fp32 [tokens, H, V] log
+ * decays of the state's rows and columns (nullable), S <- diag(e^gk) S diag(e^gv) + k v^T; reverse
+ * != 0 runs the backbone recurrence from each sequence's last token to its first (the cleaning runs
+ * forwards, as in the reference).
+ */
 int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
-                   const float* gate_b, const float* gk, const float* state, const float* cov_state,
+                   const float* gate_b, const float* gk, const float* gv, const float* state, const float* cov_state,
                    const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
                    float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
-                   int N, int position_offset, int subtract_mean, int use_l2norm, float scale, void* stream);
+                   int N, int position_offset, int subtract_mean, int use_l2norm, int reverse, float scale,
+                   void* stream);
 
 /*
  * Decode step for a captured (HIP-graph) generation loop: ccq_gdn_decode / ccq_gla_decode on B

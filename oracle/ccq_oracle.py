@@ -422,14 +422,17 @@ def gdn_chunked(q, k, v, g, beta, *, scale=None, h0=None, cu_seqlens=None, BT=64
     return o, torch.stack(finals, 0)
 
 
-def gla_recurrent(q, k, v, gk, *, scale=None, h0=None, cu_seqlens=None):
+def gla_recurrent(q, k, v, gk, *, scale=None, h0=None, cu_seqlens=None, gv=None, reverse=False):
     """Gated linear attention, one token at a time (arXiv:2312.06635; fla's
     naive recurrence for ``chunk_gla`` / ``fused_recurrent_gla``)::
 
-        S ← diag(exp(gk_t)) S + k_t v_tᵀ;   o_t = Sᵀ (scale q_t)
+        S ← diag(exp(gk_t)) S diag(exp(gv_t)) + k_t v_tᵀ;   o_t = Sᵀ (scale q_t)
 
-    ``gk`` is the per-channel log decay ``[B,T,H,K]`` (``None`` means no decay).
-    Returns ``(o, S_final [N,H,K,V])``.  Differentiable.
+    ``gk`` is the per-channel log decay of the state's rows ``[B,T,H,K]``, ``gv`` that of its
+    columns ``[B,T,H,V]`` (``None`` means no decay); ``reverse`` visits each sequence from its
+    last token to its first (``fused_recurrent_gla(reverse=True)``, as the reference forwards it,
+    ``ccq/ops/ccq_gla/fused_recurrent.py:41-49``).  Returns ``(o, S_final [N,H,K,V])``.
+    Differentiable.
     """
     B, T, H, K = q.shape
     V = v.shape[-1]
@@ -438,9 +441,11 @@ def gla_recurrent(q, k, v, gk, *, scale=None, h0=None, cu_seqlens=None):
     finals = []
     for n, b, s0, s1 in _segments(B, T, cu_seqlens):
         S = h0[n].to(q.dtype) if h0 is not None else torch.zeros(H, K, V, dtype=q.dtype)
-        for t in range(s0, s1):
+        for t in (range(s1 - 1, s0 - 1, -1) if reverse else range(s0, s1)):
             if gk is not None:
                 S = S * torch.exp(gk[b, t])[:, :, None]
+            if gv is not None:
+                S = S * torch.exp(gv[b, t])[:, None, :]
             S = S + k[b, t][:, :, None] * v[b, t][:, None, :]
             rows[b][t] = torch.einsum("hkv,hk->hv", S, q[b, t] * scale)
         finals.append(S)
@@ -564,10 +569,14 @@ def ccq_decode_gdn(q, k, v, lam, g, beta, S, C, m, pos, *, scale=None, subtract_
     return o, S2, C2, m2, pos + q.shape[1]
 
 
-def ccq_decode_gla(q, k, v, lam, gk, S, C, m, pos, *, scale=None, subtract_mean=True):
-    """Recurrent CCQ-GLA (``ccq/ops/ccq_gla/fused_recurrent.py:9-51``)."""
+def ccq_decode_gla(q, k, v, lam, gk, S, C, m, pos, *, scale=None, subtract_mean=True, gv=None, reverse=False,
+                   cu_seqlens=None):
+    """Recurrent CCQ-GLA (``ccq/ops/ccq_gla/fused_recurrent.py:9-51``): l2norm, the cleaning
+    (forwards in time), then the GLA recurrence with the row / column decays gk / gv, backwards
+    in time with ``reverse`` (``:41-49``)."""
     q, k = l2norm(q), l2norm(k)
     qc, C2, m2 = clean_fwd_bruteforce(q, k, lam, position_offset=pos, h0=C,
-                                      m0=m if subtract_mean else None, subtract_mean=subtract_mean)
-    o, S2 = gla_recurrent(qc, k, v, gk, scale=scale, h0=S)
+                                      m0=m if subtract_mean else None, subtract_mean=subtract_mean,
+                                      cu_seqlens=cu_seqlens)
+    o, S2 = gla_recurrent(qc, k, v, gk, scale=scale, h0=S, gv=gv, reverse=reverse, cu_seqlens=cu_seqlens)
     return o, S2, C2, m2, pos + q.shape[1]

@@ -145,3 +145,74 @@ def test_prefill_then_decode_matches_one_pass(bb):
     # reference row inside the last (partial) chunk moves with its length, so only fp32 rounding differs
     assert err_pre <= 2e-4
     assert err_dec <= TOL_BF16
+
+
+GLA_OPTION_CASES = [
+    # B, T, H, K, V, gv, reverse, cu
+    (2, 40, 2, 64, 128, True, False, None),
+    (2, 40, 2, 64, 128, True, True, None),
+    (1, 70, 2, 128, 64, False, True, [0, 30, 31, 70]),
+]
+
+
+@pytest.mark.parametrize("case", GLA_OPTION_CASES, ids=[str(i) for i in range(len(GLA_OPTION_CASES))])
+def test_gla_recurrent_value_decay_and_reverse(case):
+    """fused_recurrent_ccq_gla with the per-value decay gv and reverse=True (the reference forwards
+    both to fla's fused_recurrent_gla, ccq/ops/ccq_gla/fused_recurrent.py:41-49): inference on the
+    decode kernels, and with reverse also the gradients (the cleaning, then the GLA backbone on the
+    time-reversed sequences), against the oracle."""
+    dev = _cuda()
+    from ccq_amd import fused_recurrent_ccq_gla
+    B, T, H, K, V, use_gv, rev, cu = case
+    print(f"gla option case {case}", flush=True)
+    gen = torch.Generator().manual_seed(17)
+    # unit rows already (the op's own l2norm rounds its output to bf16; on unit rows that is a no-op
+    # up to rounding, so the fp64 oracle and the kernels see the same query and key)
+    q = bf(l2n(torch.randn(B, T, H, K, generator=gen)))
+    k = bf(l2n(torch.randn(B, T, H, K, generator=gen)))
+    v = bf(torch.randn(B, T, H, V, generator=gen))
+    lam = bf(torch.sigmoid(torch.randn(B, T, H, 1, generator=gen)))
+    gk = (F.logsigmoid(torch.randn(B, T, H, K, generator=gen)) / 16).float()
+    gv = (F.logsigmoid(torch.randn(B, T, H, V, generator=gen)) / 16).float() if use_gv else None
+    N = B if cu is None else len(cu) - 1
+    S0 = (torch.randn(N, H, K, V, generator=gen) * 0.1).float()
+    cu_t = torch.tensor(cu, dtype=torch.int64) if cu is not None else None
+    d = torch.float64
+    o_r, S_r, C_r, m_r, _ = O.ccq_decode_gla(q.to(d), k.to(d), v.to(d), lam.to(d).squeeze(-1), gk.to(d), S0.to(d),
+                                             None, None, 0, gv=None if gv is None else gv.to(d), reverse=rev,
+                                             cu_seqlens=cu_t)
+    dv_ = lambda x: None if x is None else x.to(dev)  # noqa: E731
+    with torch.no_grad():
+        o, S2, C2, m2 = fused_recurrent_ccq_gla(q.to(dev), k.to(dev), v.to(dev), lam.to(dev), gk=gk.to(dev),
+                                                gv=dv_(gv), initial_state=S0.to(dev), output_final_state=True,
+                                                reverse=rev, cu_seqlens=dv_(cu_t))
+    torch.cuda.synchronize()
+    errs = {"o": rel(o, o_r), "S": rel(S2, S_r), "C": rel(C2, C_r), "m": rel(m2, m_r)}
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    assert errs["o"] <= TOL_BF16
+    for n in ("S", "C", "m"):
+        assert errs[n] <= 1e-3, n
+    if not rev or use_gv:
+        return
+    # gradients through the reversed backbone.  This path hands the cleaned query to the backbone
+    # in q's dtype, as the reference's _CCQCleanQ does (ccq/ops/common/clean.py): the oracle rounds
+    # it to bf16 at the same place
+    do = bf(torch.randn(B, T, H, V, generator=gen))
+    xs = [x.to(d).requires_grad_() for x in (q, k, v)]
+    qn, kn = O.l2norm(xs[0]), O.l2norm(xs[1])
+    qc, _, _ = O.clean_fwd_bruteforce(qn, kn, lam.to(d).squeeze(-1), cu_seqlens=cu_t)
+    o_r, _ = O.gla_recurrent(O.round_through(qc, torch.bfloat16), kn, xs[2], gk.to(d), h0=S0.to(d), reverse=True,
+                             cu_seqlens=cu_t)
+    g_r = torch.autograd.grad(o_r, xs, do.to(d))
+    xg = [x.to(dev).requires_grad_() for x in (q, k, v)]
+    o, _, _, _ = fused_recurrent_ccq_gla(xg[0], xg[1], xg[2], lam.to(dev), gk=gk.to(dev), initial_state=S0.to(dev),
+                                         reverse=True, cu_seqlens=dv_(cu_t))
+    g = torch.autograd.grad(o, xg, do.to(dev).to(o.dtype))
+    gerrs = {n: rel(a, b) for n, a, b in zip(("dq", "dk", "dv"), g, g_r)}
+    print("grads", {n: f"{e:.2e}" for n, e in gerrs.items()}, flush=True)
+    assert rel(o, o_r) <= TOL_BF16
+    # the gradient of the cleaned query also crosses back from the backbone in bf16 (as fla returns
+    # it in q's dtype to the reference's _CCQCleanQ): one more bf16 rounding (2^-9 relative) on dq
+    # and dk than the fused path has, against an oracle whose gradients stay in fp64
+    for n, e in gerrs.items():
+        assert e <= 4e-3, n

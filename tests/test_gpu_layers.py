@@ -30,27 +30,46 @@ def _cuda():
     return torch.device("cuda")
 
 
-def _lam64(lambda_h, q):
-    # the operators round lambda's value through q's dtype inside the autograd function, so its
-    # gradient is not rounded (straight through)
+def _lam64(lambda_h, dtype):
+    # the operators round lambda's value through their operand type (bf16) inside the autograd
+    # function, so its gradient is not rounded (straight through)
     lam = lambda_h.squeeze(-1) if lambda_h.ndim == 4 else lambda_h
-    return O.round_through(lam.to(D), q.dtype)
+    return O.round_through(lam.to(D), dtype)
+
+
+def q_dtype_of(x):
+    """The dtype the operators see q in: bf16 for every accepted input dtype."""
+    return torch.bfloat16
 
 
 def _f64(x):
     return None if x is None else x.to(D)
 
 
+def _operands(q, k, v):
+    """q, k, v as the operators use them: values rounded to bf16 (their operand type, whatever the
+    layer's dtype), gradients passed straight through the rounding as through the operators' cast."""
+    return tuple(O.round_through(x.to(D), torch.bfloat16) for x in (q, k, v))
+
+
+def _output(o, v):
+    """o as the operators return it: computed into bf16 and handed back in v's dtype, so that its
+    gradient also arrives through bf16."""
+    return o.to(torch.bfloat16).to(v.dtype)
+
+
 def oracle_gdn(q, k, v, lambda_h, g=None, beta=None, initial_state=None, initial_cov_state=None,
                initial_mean_state=None, output_final_state=False, cu_seqlens=None, use_qk_l2norm_in_kernel=False,
                position_offset=0, subtract_mean=True, enable_ccq=True, **_):
-    o, S, C, m = O.ccq_gdn_forward(q.to(D), k.to(D), v.to(D), _lam64(lambda_h, q), g.to(D), beta.to(D),
+    v_in = v
+    q, k, v = _operands(q, k, v)
+    o, S, C, m = O.ccq_gdn_forward(q, k, v, _lam64(lambda_h, q_dtype_of(v_in)), g.to(D), beta.to(D),
                                    h0=_f64(initial_state), h0_cov=_f64(initial_cov_state),
                                    m0=_f64(initial_mean_state), position_offset=position_offset,
                                    subtract_mean=subtract_mean, cu_seqlens=cu_seqlens,
                                    use_qk_l2norm=use_qk_l2norm_in_kernel, enable_ccq=enable_ccq,
                                    l2norm_dtype=torch.bfloat16)
-    o = o.to(v.dtype)   # the operators return o in v's dtype, so its gradient arrives in that dtype too
+    o = _output(o, v_in)
     return (o, S, C, m) if output_final_state else (o, None, None, None)
 
 
@@ -58,11 +77,13 @@ def oracle_gla(q, k, v, lambda_h, g=None, gk=None, initial_state=None, initial_c
                initial_mean_state=None, output_final_state=False, cu_seqlens=None, position_offset=0,
                subtract_mean=True, **_):
     gate = g if g is not None else gk
-    o, S, C, m = O.ccq_gla_forward(q.to(D), k.to(D), v.to(D), _lam64(lambda_h, q), gate.to(D),
+    v_in = v
+    q, k, v = _operands(q, k, v)
+    o, S, C, m = O.ccq_gla_forward(q, k, v, _lam64(lambda_h, q_dtype_of(v_in)), gate.to(D),
                                    h0=_f64(initial_state), h0_cov=_f64(initial_cov_state),
                                    m0=_f64(initial_mean_state), position_offset=position_offset,
                                    subtract_mean=subtract_mean, cu_seqlens=cu_seqlens, l2norm_dtype=torch.bfloat16)
-    o = o.to(v.dtype)
+    o = _output(o, v_in)
     return (o, S, C, m) if output_final_state else (o, None, None, None)
 
 

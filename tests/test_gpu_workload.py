@@ -213,3 +213,58 @@ def test_int32_cu_seqlens():
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_input_dtypes(dtype):
+    """fp32 / fp16 activations: outputs and gradients come back in the input dtype, and equal the
+    results of the same inputs rounded to bf16 (the kernels' operand type) bit for bit.  One op per
+    backward pass: gradients of an input shared by several ops would be summed in the input dtype
+    here and in bf16 in the bf16 run."""
+    dev = _cuda()
+    from ccq_amd import fused_ccq_clean_read, fused_chunk_ccq_gdn, fused_chunk_ccq_gla, fused_recurrent_ccq_gdn, l2norm
+    dt = getattr(torch, dtype)
+    print(f"input dtype {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(5)
+    B, T, H, K, V = 1, 150, 2, 64, 64
+    base = {n: torch.randn(B, T, H, d, generator=gen) for n, d in (("q", K), ("k", K), ("v", V))}
+    g = (-torch.rand(B, T, H, generator=gen)).to(dev)
+    beta = torch.rand(B, T, H, generator=gen).to(dev)
+    gk = (-torch.rand(B, T, H, K, generator=gen) * 0.2).to(dev)
+    lam = torch.rand(B, T, H, 1, generator=gen).to(dev)
+    # (bf16 values: the upstream gradient reaches the kernels unrounded from either run, where an
+    # fp16 output would otherwise round it twice, through fp16 and then bf16)
+    do = torch.randn(B, T, H, V, generator=gen).to(torch.bfloat16).float().to(dev)
+    ops = {
+        "gdn": lambda x: fused_chunk_ccq_gdn(x["q"], x["k"], x["v"], lam, g, beta, use_qk_l2norm_in_kernel=True)[0],
+        "gla": lambda x: fused_chunk_ccq_gla(x["q"], x["k"], x["v"], lam, gk)[0],
+        "clean": lambda x: fused_ccq_clean_read(x["q"], x["k"], lam)[0],
+        "l2norm": lambda x: l2norm(x["q"]),
+    }
+
+    def run(cast, op):
+        xs = {n: cast(x).to(dev).requires_grad_() for n, x in base.items()}
+        out = ops[op](xs)
+        w = do if out.shape[-1] == V else do[..., :1]
+        grads = torch.autograd.grad((out.float() * w).sum(), [xs["q"], xs["k"], xs["v"]], allow_unused=True)
+        return out, grads
+
+    for op in ops:
+        out, grads = run(lambda x: x.to(dt), op)
+        ref, ref_grads = run(lambda x: x.to(dt).to(torch.bfloat16), op)
+        assert out.dtype == dt and torch.equal(out, ref.to(dt)), op
+        for gr, r in zip(grads, ref_grads):
+            if r is None:
+                assert gr is None
+                continue
+            assert gr.dtype == dt and torch.equal(gr, r.to(dt)), op
+    with torch.no_grad():
+        x = {n: b.to(dt).to(dev) for n, b in base.items()}
+        od, _, _, _ = fused_recurrent_ccq_gdn(x["q"][:, :3], x["k"][:, :3], x["v"][:, :3], lam[:, :3], g[:, :3],
+                                              beta=beta[:, :3], use_qk_l2norm_in_kernel=True)
+        x = {n: b.to(dt).to(torch.bfloat16).to(dev) for n, b in base.items()}
+        rd, _, _, _ = fused_recurrent_ccq_gdn(x["q"][:, :3], x["k"][:, :3], x["v"][:, :3], lam[:, :3], g[:, :3],
+                                              beta=beta[:, :3], use_qk_l2norm_in_kernel=True)
+    assert od.dtype == dt and torch.equal(od, rd.to(dt))
+    with pytest.raises(TypeError):
+        fused_ccq_clean_read(base["q"].double().to(dev), base["k"].double().to(dev), lam)

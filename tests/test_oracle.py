@@ -380,3 +380,48 @@ def test_c0_fp32_chunked_vs_fp64_bruteforce():
     for name, a, r in zip(("q_clean", "dq", "dk", "dW", "db"), res[torch.float32], res[D]):
         err = ((a.double() - r).norm() / r.norm()).item()
         assert err <= 1e-5, (name, err)
+
+
+def test_gla_value_decay_single_write_readback():
+    # gv only, one write at t = 0: S_t = k_0 (v_0 o e^{Gv_t - Gv_0})^T, so
+    # o_t = scale (q_t . k_0) (v_0 o e^{Gv_t - Gv_0}), with Gv the running sum of gv
+    B, T, H, K, V = 1, 30, 2, 6, 5
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(B, T, H, K, generator=g, dtype=D)
+    k = torch.zeros(B, T, H, K, dtype=D)
+    k[:, 0] = torch.randn(B, H, K, generator=g, dtype=D)
+    v = torch.randn(B, T, H, V, generator=g, dtype=D)
+    gv = torch.nn.functional.logsigmoid(torch.randn(B, T, H, V, generator=g, dtype=D)) / 3
+    Gv = torch.cumsum(gv, 1)
+    expect = (6 ** -0.5) * (q * k[:, :1]).sum(-1, keepdim=True) * v[:, :1] * torch.exp(Gv - Gv[:, :1])
+    o, s = O.gla_recurrent(q, k, v, None, gv=gv)
+    assert torch.allclose(o, expect, atol=1e-13)
+    # with both decays the state's rows and columns decay independently
+    gk = torch.nn.functional.logsigmoid(torch.randn(B, T, H, K, generator=g, dtype=D)) / 3
+    G = torch.cumsum(gk, 1)
+    o, s = O.gla_recurrent(q, k, v, gk, gv=gv)
+    rows = torch.exp(G - G[:, :1]) * k[:, :1]
+    expect = (6 ** -0.5) * (q * rows).sum(-1, keepdim=True) * v[:, :1] * torch.exp(Gv - Gv[:, :1])
+    assert torch.allclose(o, expect, atol=1e-13)
+
+
+def test_gla_reverse_is_the_time_reversed_recurrence():
+    # reverse=True on each sequence equals the forward recurrence on the sequence read backwards
+    q, k, v, _, _, s0 = _gdn_in(1, 50, 2, 8, 6)
+    gk = torch.nn.functional.logsigmoid(torch.randn(1, 50, 2, 8, dtype=D)) / 8
+    gv = torch.nn.functional.logsigmoid(torch.randn(1, 50, 2, 6, dtype=D)) / 8
+    cu = [0, 17, 17, 50]
+    cu_t = torch.tensor(cu)
+    o, s = O.gla_recurrent(q, k, v, gk, gv=gv, h0=s0[:1].expand(3, -1, -1, -1).contiguous(), cu_seqlens=cu_t,
+                           reverse=True)
+    for n, (a, b) in enumerate(zip(cu[:-1], cu[1:])):
+        if a == b:
+            assert torch.allclose(s[n], s0[0])
+            continue
+        f = lambda x: x[:, a:b].flip(1)  # noqa: E731
+        o_f, s_f = O.gla_recurrent(f(q), f(k), f(v), f(gk), gv=f(gv), h0=s0[:1])
+        assert torch.allclose(o[:, a:b], o_f.flip(1), atol=1e-12)
+        assert torch.allclose(s[n], s_f[0], atol=1e-12)
+    # and differs from the forward recurrence (the order matters)
+    o_fwd, _ = O.gla_recurrent(q, k, v, gk, gv=gv, h0=s0[:1].expand(3, -1, -1, -1).contiguous(), cu_seqlens=cu_t)
+    assert not torch.allclose(o, o_fwd, atol=1e-6)
