@@ -38,9 +38,9 @@ SIGNATURES = {
     "ccq_gla_fwd": (_I, [_P] * 9 + [_I] + [_P] * 3 + [_I] * 6 + [_F, _P]),
     "ccq_gla_bwd": (_I, [_P] * 8 + [_I] + [_P] * 11 + [_I] * 6 + [_F, _P]),
     "ccq_decode_workspace_bytes": (_SZ, [_I64, _I, _I]),
-    "ccq_gdn_decode": (_I, [_P] * 17 + [_I] * 10 + [_F, _P]),
+    "ccq_gdn_decode": (_I, [_P] * 19 + [_I] * 10 + [_F, _P]),
     "ccq_gla_decode": (_I, [_P] * 17 + [_I] * 10 + [_F, _P]),
-    "ccq_gdn_decode_noalloc": (_I, [_P] * 16 + [_I] * 10 + [_F, _P]),
+    "ccq_gdn_decode_noalloc": (_I, [_P] * 18 + [_I] * 10 + [_F, _P]),
     "ccq_decode_step_workspace_bytes": (_SZ, [_I] * 4),
     "ccq_gdn_decode_step": (_I, [_P] * 14 + [_I] * 8 + [_F, _P]),
     "ccq_gla_decode_step": (_I, [_P] * 13 + [_I] * 7 + [_F, _P]),

@@ -225,15 +225,14 @@ def fused_recurrent_ccq_gdn(q, k, v, lambda_h, g=None, gk=None, gv=None, beta=No
     """CCQ-GDN, recurrent (decode) mode (reference ``ccq/ops/ccq_gdn/fused_recurrent.py:18-75``).
 
     Without autograd (decode, generation) this runs the decode kernels: rank-1 updates of the
-    cached S, C and m per token.  When a gradient is needed it runs the chunk kernels, which
-    compute the same recurrence and have a backward.
+    cached S, C and m per token, with the optional per-key / per-value decays ``gk`` / ``gv`` of
+    fla's recurrent gated delta rule.  When a gradient is needed it runs the chunk kernels, which
+    compute the same recurrence (without gk / gv) and have a backward.
     """
     from .decode import gdn_decode, needs_grad
-    if gk is not None or gv is not None:
-        raise NotImplementedError("fused_recurrent_ccq_gdn: per-key/per-value gates (gk, gv) are not supported")
     if beta is None:
         beta = torch.ones(q.shape[:3], device=q.device, dtype=torch.float32)
-    if not needs_grad(q, k, v, lambda_h, g, beta, initial_state, initial_cov_state, initial_mean_state):
+    if not needs_grad(q, k, v, lambda_h, g, gk, gv, beta, initial_state, initial_cov_state, initial_mean_state):
         s0 = initial_state
         if transpose_state_layout and s0 is not None:
             s0 = s0.transpose(-1, -2)
@@ -241,13 +240,17 @@ def fused_recurrent_ccq_gdn(q, k, v, lambda_h, g=None, gk=None, gv=None, beta=No
         q, k, v = as_kernel_dtype(q, k, v)
         o, s, c, m = gdn_decode(q, k, v, lambda_h, g, beta, _default_scale(scale, q.shape[-1]), s0, initial_cov_state,
                                 initial_mean_state if subtract_mean else None, bool(output_final_state),
-                                bool(use_qk_l2norm_in_kernel), cu_seqlens, position_offset, subtract_mean, enable_ccq)
+                                bool(use_qk_l2norm_in_kernel), cu_seqlens, position_offset, subtract_mean, enable_ccq,
+                                gk=gk, gv=gv)
         o = in_dtype(o, dt)
         if not output_final_state:
             return o, None, None, None
         if transpose_state_layout:
             s = s.transpose(-1, -2).contiguous()
         return o, s, c, m
+    if gk is not None or gv is not None:
+        raise NotImplementedError("fused_recurrent_ccq_gdn: gradients through the per-key / per-value decays "
+                                  "(gk, gv) are not supported (inference with them runs on the decode kernels)")
     return chunk_ccq_gdn(q, k, v, lambda_h, g, beta, scale, initial_state, initial_cov_state, initial_mean_state,
                          output_final_state, use_qk_l2norm_in_kernel, cu_seqlens, None, transpose_state_layout,
                          position_offset, subtract_mean, enable_ccq)

@@ -759,7 +759,8 @@ size_t ccq_decode_workspace_bytes(int64_t tokens, int H, int K) {
 }
 
 int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
-                   const float* gate_b, const float* g, const float* beta, const float* state, const float* cov_state,
+                   const float* gate_b, const float* g, const float* beta, const float* gk, const float* gv,
+                   const float* state, const float* cov_state,
                    const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
                    float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
                    int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq, float scale,
@@ -770,14 +771,15 @@ int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lam
                             position_offset, subtract_mean, use_l2norm, enable_ccq, scale))
     return s;
   if (!beta) return fail(CCQ_ERR_NULL, "ccq_gdn_decode: beta is required");
-  a.g = g; a.beta = beta; a.gla = 0;
+  a.g = g; a.beta = beta; a.gk = gk; a.gv = gv; a.gla = 0;
   return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gdn_decode");
 }
 
 static_assert(CCQ_DECODE_SCRATCH_BYTES == ccq::kDecodeScratchBytes, "scratch size in the header and the library");
 
 int ccq_gdn_decode_noalloc(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
-                           const float* gate_b, const float* g, const float* beta, const float* state,
+                           const float* gate_b, const float* g, const float* beta, const float* gk, const float* gv,
+                           const float* state,
                            const float* cov_state, const float* mean_state, const int64_t* cu_seqlens, void* o,
                            float* state_out, float* cov_state_out, float* mean_state_out, int B, int T, int H, int K,
                            int V, int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq,
@@ -792,7 +794,7 @@ int ccq_gdn_decode_noalloc(const void* q, const void* k, const void* v, const fl
                 (long long)B * T, H, K, need, kDecodeScratchBytes);
   void* ws = nullptr;
   if (int s = hip_status(decode_scratch((hipStream_t)stream, &ws), "ccq_gdn_decode_noalloc")) return s;
-  return ccq_gdn_decode(q, k, v, lambda, gate_w, gate_b, g, beta, state, cov_state, mean_state, cu_seqlens, o,
+  return ccq_gdn_decode(q, k, v, lambda, gate_w, gate_b, g, beta, gk, gv, state, cov_state, mean_state, cu_seqlens, o,
                         state_out, cov_state_out, mean_state_out, ws, B, T, H, K, V, N, position_offset,
                         subtract_mean, use_l2norm, enable_ccq, scale, stream);
 }

@@ -5,7 +5,8 @@
 //   q, k <- l2norm(q), l2norm(k)   (optional, outputs rounded to bf16 as fla's l2norm returns them)
 //   C <- C + k k^T;  m <- m + k;  z = C^T q;  s = m . q;  pos = max(t + 1 + position_offset, 1)
 //   q_clean = q - lambda (z / pos - s m / pos^2)          (mean term only with subtract_mean)
-//   GDN: S <- e^g S;  u = beta (v - S^T k);  S <- S + k u^T;  o = S^T (scale q_clean)
+//   GDN: S <- e^g diag(e^gk) S diag(e^gv) (gk, gv optional);  u = beta (v - S^T k);  S <- S + k u^T;
+//        o = S^T (scale q_clean)
 //   GLA: S <- diag(e^gk) S diag(e^gv) + k v^T;  o = S^T (scale q_clean)  (optionally from the last
 //        token to the first: `reverse`, the cleaning itself always runs forwards)
 //
@@ -169,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
     if (tid < K) {
       sq[tid] = a.qc[(tok * a.H + h) * K + tid];
       sk[tid] = a.kn[(tok * a.H + h) * K + tid];
-      if (a.gla) sgk[tid] = a.gk ? __expf(a.gk[(tok * a.H + h) * K + tid]) : 1.f;
+      sgk[tid] = a.gk ? __expf(a.gk[(tok * a.H + h) * K + tid]) : 1.f;
     }
     __syncthreads();
     const float vt = (float)((const bf16*)a.v)[(tok * a.H + h) * V + v];
@@ -181,11 +182,11 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
         sreg[r] = sgk[i] * sreg[r] * dv + sk[i] * vt;
       }
     } else {
-      const float dec = a.g ? __expf(a.g[tok * a.H + h]) : 1.f;
+      const float dec = (a.g ? __expf(a.g[tok * a.H + h]) : 1.f) * (a.gv ? __expf(a.gv[(tok * a.H + h) * V + v]) : 1.f);
       float p = 0.f;
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
-        sreg[r] *= dec;
+        sreg[r] *= dec * sgk[rg * RPT + r];
         p += sreg[r] * sk[rg * RPT + r];
       }
       sp[rg][vv] = p;

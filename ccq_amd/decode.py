@@ -48,11 +48,17 @@ def _states(N, H, K, V, dev, want, enable_ccq, subtract_mean):
 
 def gdn_decode(q, k, v, lambda_h, g, beta, scale, initial_state=None, initial_cov_state=None,
                initial_mean_state=None, output_final_state=True, use_l2norm=True, cu_seqlens=None,
-               position_offset=0, subtract_mean=True, enable_ccq=True, gate_w=None, gate_b=None):
-    """One recurrent CCQ-GDN call.  Returns ``(o, S, C, m)`` (states None unless requested)."""
+               position_offset=0, subtract_mean=True, enable_ccq=True, gate_w=None, gate_b=None, gk=None, gv=None):
+    """One recurrent CCQ-GDN call; ``gk`` ``[B, T, H, K]`` / ``gv`` ``[B, T, H, V]`` optionally decay
+    the state's rows / columns besides the scalar ``g``.  Returns ``(o, S, C, m)`` (states None
+    unless requested)."""
     q, k, v, lam, gw, gb, N, ws, cu_seqlens = _prep(
-        q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, enable_ccq, g=g, beta=beta, initial_state=initial_state,
-        initial_cov_state=initial_cov_state, initial_mean_state=initial_mean_state)
+        q, k, v, lambda_h, gate_w, gate_b, cu_seqlens, enable_ccq, g=g, beta=beta, gk=gk, gv=gv,
+        initial_state=initial_state, initial_cov_state=initial_cov_state, initial_mean_state=initial_mean_state)
+    if gk is not None and gk.shape != q.shape:
+        raise ValueError(f"gk must have q's shape {tuple(q.shape)} (got {tuple(gk.shape)})")
+    if gv is not None and gv.shape != v.shape:
+        raise ValueError(f"gv must have v's shape {tuple(v.shape)} (got {tuple(gv.shape)})")
     B, T, H, K = q.shape
     V = v.shape[-1]
     if beta is None:
@@ -60,9 +66,10 @@ def gdn_decode(q, k, v, lambda_h, g, beta, scale, initial_state=None, initial_co
     o = torch.empty(B, T, H, V, device=q.device, dtype=v.dtype)
     S, C, m = _states(N, H, K, V, q.device, output_final_state, enable_ccq, subtract_mean)
     # every converted copy is bound to a name so that its buffer outlives the launch
-    g32, b32, s0, c0, m0 = (_f32(x) for x in (g, beta, initial_state, initial_cov_state, initial_mean_state))
-    call("ccq_gdn_decode", ptr(q), ptr(k), ptr(v), ptr(lam), ptr(gw), ptr(gb), ptr(g32), ptr(b32),
-         ptr(s0), ptr(c0), ptr(m0), ptr(cu_seqlens),
+    g32, b32, gk32, gv32, s0, c0, m0 = (_f32(x) for x in (g, beta, gk, gv, initial_state, initial_cov_state,
+                                                           initial_mean_state))
+    call("ccq_gdn_decode", ptr(q), ptr(k), ptr(v), ptr(lam), ptr(gw), ptr(gb), ptr(g32), ptr(b32), ptr(gk32),
+         ptr(gv32), ptr(s0), ptr(c0), ptr(m0), ptr(cu_seqlens),
          ptr(o), ptr(S), ptr(C), ptr(m), ptr(ws), B, T, H, K, V, N, int(position_offset), int(bool(subtract_mean)),
          int(bool(use_l2norm)), int(bool(enable_ccq)), float(scale), stream_of(q))
     return o, S, C, m

@@ -190,7 +190,9 @@ int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v,
  * (ccq/ops/ccq_gla/fused_recurrent.py:9-51, backbone fla fused_recurrent_gla(gk)).  Per token:
  *   q, k <- l2norm (if use_l2norm; results rounded to bf16); C += k k^T; m += k; z = C^T q;
  *   q_clean = q - lambda (z/pos - (m.q) m/pos^2), pos = max(t + 1 + position_offset, 1);
- *   GDN: S <- e^g S; u = beta (v - S^T k); S += k u^T.  GLA: S <- diag(e^gk) S + k v^T.
+ *   GDN: S <- e^g diag(e^gk) S diag(e^gv); u = beta (v - S^T k); S += k u^T (gk fp32 [tokens, H, K]
+ *   and gv fp32 [tokens, H, V] optional, as fla's fused_recurrent_gated_delta_rule takes them from
+ *   the reference, ccq/ops/ccq_gdn/fused_recurrent.py:66-74).  GLA: S <- diag(e^gk) S + k v^T.
  *   o = S^T (scale q_clean)  (bf16 [tokens, H, V]).
  * state/cov_state/mean_state: cached fp32 S [N, H, K, V], C [N, H, K, K], m [N, H, K] (nullable =
  * zero); the *_out buffers receive the updated states (nullable = not written).  state_out and
@@ -201,7 +203,8 @@ int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v,
  */
 size_t ccq_decode_workspace_bytes(int64_t tokens, int H, int K);
 int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
-                   const float* gate_b, const float* g, const float* beta, const float* state, const float* cov_state,
+                   const float* gate_b, const float* g, const float* beta, const float* gk, const float* gv,
+                   const float* state, const float* cov_state,
                    const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
                    float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
                    int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq, float scale,
@@ -217,7 +220,8 @@ int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lam
  */
 #define CCQ_DECODE_SCRATCH_BYTES ((size_t)8 << 20)
 int ccq_gdn_decode_noalloc(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
-                           const float* gate_b, const float* g, const float* beta, const float* state,
+                           const float* gate_b, const float* g, const float* beta, const float* gk, const float* gv,
+                           const float* state,
                            const float* cov_state, const float* mean_state, const int64_t* cu_seqlens, void* o,
                            float* state_out, float* cov_state_out, float* mean_state_out, int B, int T, int H, int K,
                            int V, int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq,

@@ -345,12 +345,17 @@ def clean_given_z(q, k, z, lam, *, position_offset=0, m0=None, subtract_mean=Tru
 # backbones
 # ---------------------------------------------------------------------------
 
-def gdn_recurrent(q, k, v, g, beta, *, scale=None, h0=None, cu_seqlens=None):
+def gdn_recurrent(q, k, v, g, beta, *, scale=None, h0=None, cu_seqlens=None, gk=None, gv=None):
     """Gated delta rule, one token at a time (arXiv:2412.06464; fla's naive
     recurrence that ``chunk_gated_delta_rule`` implements)::
 
         S ← exp(g_t) S;   u = β_t (v_t − Sᵀ k_t);   S ← S + k_t uᵀ;   o_t = Sᵀ (scale q_t)
 
+    ``gk`` ``[B,T,H,K]`` / ``gv`` ``[B,T,H,V]`` (optional) also decay the state's rows / columns
+    before the delta step, ``S ← exp(g_t) diag(exp(gk_t)) S diag(exp(gv_t))``: the per-key /
+    per-value gates that the reference hands to fla's ``fused_recurrent_gated_delta_rule``
+    (``ccq/ops/ccq_gdn/fused_recurrent.py:66-74``); fla is not available here, so these two
+    follow its published recurrence and are pinned by closed forms only.
     ``scale`` defaults to ``K**-0.5``.  Returns ``(o, S_final [N,H,K,V])``.
     Differentiable.
     """
@@ -363,6 +368,10 @@ def gdn_recurrent(q, k, v, g, beta, *, scale=None, h0=None, cu_seqlens=None):
         S = h0[n].to(q.dtype) if h0 is not None else torch.zeros(H, K, V, dtype=q.dtype)
         for t in range(s0, s1):
             S = S * torch.exp(g[b, t])[:, None, None]
+            if gk is not None:
+                S = S * torch.exp(gk[b, t])[:, :, None]
+            if gv is not None:
+                S = S * torch.exp(gv[b, t])[:, None, :]
             u = beta[b, t][:, None] * (v[b, t] - torch.einsum("hkv,hk->hv", S, k[b, t]))
             S = S + k[b, t][:, :, None] * u[:, None, :]
             rows[b][t] = torch.einsum("hkv,hk->hv", S, q[b, t] * scale)
@@ -552,7 +561,7 @@ def ccq_gla_forward(q, k, v, lam, gk, *, scale=None, h0=None, h0_cov=None, m0=No
 
 
 def ccq_decode_gdn(q, k, v, lam, g, beta, S, C, m, pos, *, scale=None, subtract_mean=True,
-                   use_qk_l2norm=True):
+                   use_qk_l2norm=True, gk=None, gv=None):
     """Recurrent CCQ-GDN over a few tokens from a cache ``(S, C, m, pos)``.
 
     ``fused_recurrent_ccq_gdn`` (``ccq/ops/ccq_gdn/fused_recurrent.py:18-75``) ->
@@ -565,7 +574,7 @@ def ccq_decode_gdn(q, k, v, lam, g, beta, S, C, m, pos, *, scale=None, subtract_
         q, k = l2norm(q), l2norm(k)
     qc, C2, m2 = clean_fwd_bruteforce(q, k, lam, position_offset=pos, h0=C,
                                       m0=m if subtract_mean else None, subtract_mean=subtract_mean)
-    o, S2 = gdn_recurrent(qc, k, v, g, beta, scale=scale, h0=S)
+    o, S2 = gdn_recurrent(qc, k, v, g, beta, scale=scale, h0=S, gk=gk, gv=gv)
     return o, S2, C2, m2, pos + q.shape[1]
 
 

@@ -176,8 +176,8 @@ def test_decode_noalloc_rejects_calls_beyond_its_scratch():
     # host, before any device work
     lib = _lib.load()
     p = _fake()
-    st = lib.ccq_gdn_decode_noalloc(p, p, p, p, None, None, None, p, None, None, None, None, p, None, None, None,
-                                    1, 2048, 4, 256, 512, 1, 0, 1, 1, 1, 0.0625, None)
+    st = lib.ccq_gdn_decode_noalloc(p, p, p, p, None, None, None, p, None, None, None, None, None, None, p, None,
+                                    None, None, 1, 2048, 4, 256, 512, 1, 0, 1, 1, 1, 0.0625, None)
     assert st == CCQ_ERR_SHAPE
     assert b"scratch" in lib.ccq_last_error()
 

@@ -216,3 +216,42 @@ def test_gla_recurrent_value_decay_and_reverse(case):
     # and dk than the fused path has, against an oracle whose gradients stay in fp64
     for n, e in gerrs.items():
         assert e <= 4e-3, n
+
+
+def test_gdn_recurrent_key_value_decays():
+    """fused_recurrent_ccq_gdn with the per-key / per-value decays gk, gv (forwarded by the
+    reference to fla's fused_recurrent_gated_delta_rule, ccq/ops/ccq_gdn/fused_recurrent.py:66-74)
+    on the decode kernels, against the oracle."""
+    dev = _cuda()
+    from ccq_amd import fused_recurrent_ccq_gdn
+    B, T, H, K, V, pos = 2, 5, 2, 128, 128, 33
+    gen = torch.Generator().manual_seed(23)
+    q = bf(l2n(torch.randn(B, T, H, K, generator=gen)))
+    k = bf(l2n(torch.randn(B, T, H, K, generator=gen)))
+    v = bf(torch.randn(B, T, H, V, generator=gen))
+    lam = bf(torch.sigmoid(torch.randn(B, T, H, 1, generator=gen)))
+    g = (-F.softplus(torch.randn(B, T, H, generator=gen)) * 0.3).float()
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen)).float()
+    gk = (F.logsigmoid(torch.randn(B, T, H, K, generator=gen)) / 8).float()
+    gv = (F.logsigmoid(torch.randn(B, T, H, V, generator=gen)) / 8).float()
+    S, C, m = _cache(B, H, K, V, gen, pos)
+    d = torch.float64
+    print("gdn gk/gv decode", flush=True)
+    o_r, S_r, C_r, m_r, _ = O.ccq_decode_gdn(q.to(d), k.to(d), v.to(d), lam.to(d).squeeze(-1), g.to(d), beta.to(d),
+                                             S.to(d), C.to(d), m.to(d), pos, use_qk_l2norm=False, gk=gk.to(d),
+                                             gv=gv.to(d))
+    with torch.no_grad():
+        o, S2, C2, m2 = fused_recurrent_ccq_gdn(q.to(dev), k.to(dev), v.to(dev), lam.to(dev), g=g.to(dev),
+                                                gk=gk.to(dev), gv=gv.to(dev), beta=beta.to(dev),
+                                                initial_state=S.to(dev), initial_cov_state=C.to(dev),
+                                                initial_mean_state=m.to(dev), output_final_state=True,
+                                                position_offset=pos)
+    torch.cuda.synchronize()
+    errs = {"o": rel(o, o_r), "S": rel(S2, S_r), "C": rel(C2, C_r), "m": rel(m2, m_r)}
+    print({n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    assert errs["o"] <= TOL_BF16
+    for n in ("S", "C", "m"):
+        assert errs[n] <= TOL_STATE, n
+    with pytest.raises(NotImplementedError):
+        fused_recurrent_ccq_gdn(q.to(dev).requires_grad_(), k.to(dev), v.to(dev), lam.to(dev), g=g.to(dev),
+                                gk=gk.to(dev), beta=beta.to(dev))

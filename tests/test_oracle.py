@@ -425,3 +425,23 @@ def test_gla_reverse_is_the_time_reversed_recurrence():
     # and differs from the forward recurrence (the order matters)
     o_fwd, _ = O.gla_recurrent(q, k, v, gk, gv=gv, h0=s0[:1].expand(3, -1, -1, -1).contiguous(), cu_seqlens=cu_t)
     assert not torch.allclose(o, o_fwd, atol=1e-6)
+
+
+def test_gdn_key_value_decays_closed_forms():
+    # beta = 0 (no writes): S_T = S_0 o exp(sum g) exp(sum gk)[:, None] exp(sum gv)[None, :]
+    q, k, v, g, beta, s0 = _gdn_in(1, 20, 2, 6, 5, seed=3)
+    gk = torch.nn.functional.logsigmoid(torch.randn(1, 20, 2, 6, dtype=D)) / 4
+    gv = torch.nn.functional.logsigmoid(torch.randn(1, 20, 2, 5, dtype=D)) / 4
+    _, s = O.gdn_recurrent(q, k, v, g, torch.zeros_like(beta), h0=s0, gk=gk, gv=gv)
+    expect = s0[0] * torch.exp(g[0].sum(0))[:, None, None] * torch.exp(gk[0].sum(0))[:, :, None] \
+        * torch.exp(gv[0].sum(0))[:, None, :]
+    assert torch.allclose(s[0], expect, atol=1e-12)
+    # beta = 1 with a unit key overwrites the decayed state's read-back along k exactly:
+    # S_1^T k_1 = v_1 whatever the decays did to S_0
+    _, s1 = O.gdn_recurrent(q[:, :1], k[:, :1], v[:, :1], g[:, :1], torch.ones_like(beta[:, :1]), h0=s0,
+                            gk=gk[:, :1], gv=gv[:, :1])
+    assert torch.allclose(torch.einsum("hkv,hk->hv", s1[0], k[0, 0]), v[0, 0], atol=1e-12)
+    # gk = gv = 0 is the plain gated delta rule
+    o_a, _ = O.gdn_recurrent(q, k, v, g, beta, h0=s0, gk=torch.zeros_like(gk), gv=torch.zeros_like(gv))
+    o_b, _ = O.gdn_recurrent(q, k, v, g, beta, h0=s0)
+    assert torch.allclose(o_a, o_b, atol=1e-14)

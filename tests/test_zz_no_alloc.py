@@ -31,8 +31,8 @@ def _run(x, B, T, H, K, V, pos, noalloc):
     S = torch.empty(B, H, K, V, device=dev)
     C = torch.empty(B, H, K, K, device=dev)
     m = torch.empty(B, H, K, device=dev)
-    head = [ptr(x["q"]), ptr(x["k"]), ptr(x["v"]), ptr(x["lam"]), None, None, ptr(x["g"]), ptr(x["beta"]),
-            ptr(x["S"]), ptr(x["C"]), ptr(x["m"]), None, ptr(o), ptr(S), ptr(C), ptr(m)]
+    head = [ptr(x["q"]), ptr(x["k"]), ptr(x["v"]), ptr(x["lam"]), None, None, ptr(x["g"]), ptr(x["beta"]), None,
+            None, ptr(x["S"]), ptr(x["C"]), ptr(x["m"]), None, ptr(o), ptr(S), ptr(C), ptr(m)]
     tail = [B, T, H, K, V, B, pos, 1, 1, 1, K ** -0.5, stream_of(x["q"])]
     if noalloc:
         st = lib.ccq_gdn_decode_noalloc(*head, *tail)
