@@ -48,6 +48,12 @@ SIGNATURES = {
     "ccq_clean_z_bwd_workspace_bytes": (_SZ, [_I, _I, _I]),
     "ccq_clean_z_fwd": (_I, [_P] * 8 + [_I] + [_P] * 3 + [_I] * 7 + [_P]),
     "ccq_clean_z_bwd": (_I, [_P] * 7 + [_I] + [_P] * 10 + [_I] * 7 + [_P]),
+    "ccq_conv_bwd_workspace_bytes": (_SZ, [_I64, _I, _I]),
+    "ccq_conv_fwd": (_I, [_P] * 9 + [_I] * 7 + [_F, _P]),
+    "ccq_conv_bwd": (_I, [_P] * 12 + [_I] * 7 + [_P]),
+    "ccq_gated_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I]),
+    "ccq_gated_rmsnorm_fwd": (_I, [_P] * 5 + [_I64, _I, _F, _P]),
+    "ccq_gated_rmsnorm_bwd": (_I, [_P] * 9 + [_I64, _I, _P]),
     "ccq_l2norm_fwd": (_I, [_P, _P, _P, _I64, _I, _F, _P]),
     "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
     "ccq_timing_enable": (_I, [_I]),
@@ -94,7 +100,8 @@ def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args), name)
 
 
-KERNELS = ("clean_fwd_sum", "clean_fwd", "clean_bwd_rows", "clean_bwd_dq", "clean_bwd_gsum", "clean_bwd_dk",
+KERNELS = ("conv_fwd", "conv_bwd", "gnorm_fwd", "gnorm_bwd",
+           "clean_fwd_sum", "clean_fwd", "clean_bwd_rows", "clean_bwd_dq", "clean_bwd_gsum", "clean_bwd_dk",
            "clean_bwd_gate",
            "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy",
            "gla_intra", "gla_fwd_state", "gla_fwd_o", "gla_bwd_state", "gla_bwd_dv", "gla_bwd_dqk", "gla_bwd_gk",

@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libccq_hip.so")
-SOURCES = ["ccq_abi.hip", "ccq_cwalk.hip", "ccq_gdn.hip", "ccq_gla.hip", "ccq_decode.hip", "ccq_zclean.hip", "ccq_misc.hip", "ccq_cseg.hip"]
+SOURCES = ["ccq_abi.hip", "ccq_cwalk.hip", "ccq_gdn.hip", "ccq_gla.hip", "ccq_decode.hip", "ccq_zclean.hip", "ccq_misc.hip", "ccq_cseg.hip", "ccq_prologue.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [

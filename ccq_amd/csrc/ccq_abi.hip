@@ -1,6 +1,7 @@
 // C ABI of libccq_hip.so: argument checks, buffer carving, kernel launches.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -22,6 +23,8 @@ hipError_t launch_sum_rows2(const float* partA, float* outA, int colsA, const fl
                             int nblk, float* red, hipStream_t st);
 hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream_t st);
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
+hipError_t launch_conv(int stage, const ConvArgs& a, int blocks, hipStream_t st);
+hipError_t launch_gnorm(int stage, const GNormArgs& a, int blocks, hipStream_t st);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
@@ -543,6 +546,145 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
   L2NormArgs a{};
   a.x = x; a.rstd = const_cast<float*>(rstd); a.dy32 = dy_f32; a.dy16 = dy_f32 ? nullptr : dy; a.dx = dx; a.rows = rows; a.D = D;
   return hip_status(launch_l2norm_bwd(a, (hipStream_t)stream), "ccq_l2norm_bwd");
+}
+
+}  // extern "C"
+
+// ---- layer prologue / epilogue: short convolution (+ l2norm), gated RMSNorm ----
+namespace {
+
+constexpr int kConvBlocks = 512;   // workgroups of the backward passes (one partial row each)
+
+int conv_blocks(int64_t tokens) { return (int)std::max<int64_t>(1, std::min<int64_t>((tokens + 15) / 16, kConvBlocks)); }
+int gnorm_blocks(int64_t rows) { return (int)std::max<int64_t>(1, std::min<int64_t>((rows + 3) / 4, kConvBlocks)); }
+
+struct ConvWork {
+  float* dw_part;
+  float* db_part;
+  float* red;
+};
+size_t carve_conv_work(char* base, int64_t tokens, int D, int W, ConvWork* out) {
+  Slicer sl{base};
+  const int nb = conv_blocks(tokens);
+  ConvWork t{};
+  t.dw_part = sl.take<float>((size_t)nb * D * W);
+  t.db_part = sl.take<float>((size_t)nb * D);
+  t.red = sl.take<float>((size_t)kSumSlices * D * (W + 1));
+  if (out) *out = t;
+  return sl.off;
+}
+
+int conv_check(const char* who, int B, int T, int N, int D, int W, int head_dim, const int64_t* cu) {
+  if (int s = check_common(B, T, 1, N, cu)) return s;
+  if (D <= 0 || D % 8 != 0) return fail(CCQ_ERR_SHAPE, "%s: D=%d must be a positive multiple of 8", who, D);
+  if (W < 1 || W > 8) return fail(CCQ_ERR_SHAPE, "%s: kernel size W=%d not in [1, 8]", who, W);
+  if (head_dim && (head_dim < 8 || head_dim > 512 || (head_dim & (head_dim - 1)) || D % head_dim))
+    return fail(CCQ_ERR_SHAPE, "%s: head_dim=%d must be a power of two in [8, 512] dividing D=%d", who, head_dim, D);
+  return CCQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ccq_conv_bwd_workspace_bytes(int64_t tokens, int D, int W) {
+  return carve_conv_work(nullptr, tokens, D, W, nullptr);
+}
+
+int ccq_conv_fwd(const void* x, const float* weight, const float* bias, const float* cache_in,
+                 const int64_t* cu_seqlens, void* y, void* y_norm, float* rstd, float* cache_out, int B, int T, int N,
+                 int D, int W, int head_dim, int activation, float eps, void* stream) {
+  if (int s = conv_check("ccq_conv_fwd", B, T, N, D, W, y_norm ? head_dim : 0, cu_seqlens)) return s;
+  if (!x || !weight || (!y && !y_norm)) return fail(CCQ_ERR_NULL, "ccq_conv_fwd: x, weight and an output are required");
+  if (y_norm && !rstd) return fail(CCQ_ERR_NULL, "ccq_conv_fwd: y_norm needs rstd");
+  if (!aligned16(x) || !aligned16(y) || !aligned16(y_norm))
+    return fail(CCQ_ERR_ALIGN, "ccq_conv_fwd: x, y, y_norm must be 16-byte aligned");
+  ConvArgs a{};
+  a.x = x; a.w = weight; a.bias = bias; a.cache_in = cache_in; a.cu = cu_seqlens; a.y = y; a.yn = y_norm;
+  a.rstd = rstd; a.cache_out = cache_out; a.tokens = (long)B * T; a.T = T; a.N = N; a.D = D; a.W = W;
+  a.hd = y_norm ? head_dim : 8; a.act = activation ? 1 : 0; a.eps = eps;
+  hipStream_t st = (hipStream_t)stream;
+  if (cache_out) {
+    if (int s = hip_status(launch_conv(2, a, 1, st), "ccq_conv_fwd(cache)")) return s;
+  }
+  return hip_status(timed("conv_fwd", st, [&] {
+                      return launch_conv(0, a, (int)std::min<int64_t>(((int64_t)B * T + 15) / 16, 4096), st);
+                    }),
+                    "ccq_conv_fwd");
+}
+
+int ccq_conv_bwd(const void* x, const float* weight, const float* bias, const float* cache_in,
+                 const int64_t* cu_seqlens, const void* dy, const void* dy_norm, const float* rstd, void* dx,
+                 float* dweight, float* dbias, void* workspace, int B, int T, int N, int D, int W, int head_dim,
+                 int activation, void* stream) {
+  if (int s = conv_check("ccq_conv_bwd", B, T, N, D, W, dy_norm ? head_dim : 0, cu_seqlens)) return s;
+  if (!x || !weight || !dx || !dweight || !workspace || (!dy && !dy_norm))
+    return fail(CCQ_ERR_NULL, "ccq_conv_bwd: x, weight, dx, dweight, workspace and a gradient are required");
+  if (dy_norm && !rstd) return fail(CCQ_ERR_NULL, "ccq_conv_bwd: dy_norm needs the forward's rstd");
+  if (!aligned16(x) || !aligned16(dx) || !aligned16(dy) || !aligned16(dy_norm) || !aligned16(workspace))
+    return fail(CCQ_ERR_ALIGN, "ccq_conv_bwd: x, dx, dy, dy_norm, workspace must be 16-byte aligned");
+  const int64_t tokens = (int64_t)B * T;
+  ConvWork wk;
+  carve_conv_work((char*)workspace, tokens, D, W, &wk);
+  ConvArgs a{};
+  a.x = x; a.w = weight; a.bias = bias; a.cache_in = cache_in; a.cu = cu_seqlens; a.dy = dy; a.dyn = dy_norm;
+  a.rstd = const_cast<float*>(rstd); a.dx = dx; a.dw_part = wk.dw_part; a.db_part = dbias ? wk.db_part : nullptr;
+  a.tokens = tokens; a.T = T; a.N = N; a.D = D; a.W = W; a.hd = dy_norm ? head_dim : 8;
+  a.act = activation ? 1 : 0;
+  hipStream_t st = (hipStream_t)stream;
+  const int nb = conv_blocks(tokens);
+  if (tokens == 0) {
+    if (int s = hip_status(launch_fill_zero(dweight, (long)D * W, st), "ccq_conv_bwd(dweight)")) return s;
+    return dbias ? hip_status(launch_fill_zero(dbias, (long)D, st), "ccq_conv_bwd(dbias)") : CCQ_OK;
+  }
+  if (int s = hip_status(timed("conv_bwd", st, [&] { return launch_conv(1, a, nb, st); }), "ccq_conv_bwd")) return s;
+  return hip_status(launch_sum_rows2(wk.dw_part, dweight, D * W, dbias ? wk.db_part : nullptr, dbias, dbias ? D : 0,
+                                     nb, wk.red, st),
+                    "ccq_conv_bwd(dweight, dbias)");
+}
+
+size_t ccq_gated_rmsnorm_bwd_workspace_bytes(int64_t rows, int dv) {
+  Slicer sl{nullptr};
+  sl.take<float>((size_t)gnorm_blocks(rows) * dv);
+  sl.take<float>((size_t)kSumSlices * dv);
+  return sl.off;
+}
+
+int ccq_gated_rmsnorm_fwd(const void* x, const void* g, const float* weight, void* y, float* rstd, int64_t rows,
+                          int dv, float eps, void* stream) {
+  if (!x || !g || !y || !rstd) return fail(CCQ_ERR_NULL, "ccq_gated_rmsnorm_fwd: x, g, y, rstd are required");
+  if (rows < 0 || dv <= 0 || dv > 512 || dv % 8)
+    return fail(CCQ_ERR_SHAPE, "ccq_gated_rmsnorm_fwd: dv=%d must be a multiple of 8 in [8, 512]", dv);
+  if (!aligned16(x) || !aligned16(g) || !aligned16(y))
+    return fail(CCQ_ERR_ALIGN, "ccq_gated_rmsnorm_fwd: x, g, y must be 16-byte aligned");
+  GNormArgs a{};
+  a.x = x; a.g = g; a.w = weight; a.y = y; a.rstd = rstd; a.rows = rows; a.dv = dv; a.eps = eps;
+  hipStream_t st = (hipStream_t)stream;
+  return hip_status(timed("gnorm_fwd", st, [&] { return launch_gnorm(0, a, 0, st); }), "ccq_gated_rmsnorm_fwd");
+}
+
+int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, const float* rstd, const void* dy,
+                          void* dx, void* dg, float* dweight, void* workspace, int64_t rows, int dv, void* stream) {
+  if (!x || !g || !rstd || !dy || !dx || !dg) return fail(CCQ_ERR_NULL, "ccq_gated_rmsnorm_bwd: null pointer");
+  if (dweight && !workspace) return fail(CCQ_ERR_NULL, "ccq_gated_rmsnorm_bwd: dweight needs the workspace");
+  if (rows < 0 || dv <= 0 || dv > 512 || dv % 8)
+    return fail(CCQ_ERR_SHAPE, "ccq_gated_rmsnorm_bwd: dv=%d must be a multiple of 8 in [8, 512]", dv);
+  if (!aligned16(x) || !aligned16(g) || !aligned16(dy) || !aligned16(dx) || !aligned16(dg))
+    return fail(CCQ_ERR_ALIGN, "ccq_gated_rmsnorm_bwd: x, g, dy, dx, dg must be 16-byte aligned");
+  const int nb = gnorm_blocks(rows);
+  Slicer sl{(char*)workspace};
+  float* part = workspace ? sl.take<float>((size_t)nb * dv) : nullptr;
+  float* red = workspace ? sl.take<float>((size_t)kSumSlices * dv) : nullptr;
+  GNormArgs a{};
+  a.x = x; a.g = g; a.w = weight; a.rstd = const_cast<float*>(rstd); a.dy = dy; a.dx = dx; a.dg = dg;
+  a.dw_part = dweight ? part : nullptr; a.rows = rows; a.dv = dv;
+  hipStream_t st = (hipStream_t)stream;
+  if (rows == 0) return dweight ? hip_status(launch_fill_zero(dweight, dv, st), "ccq_gated_rmsnorm_bwd") : CCQ_OK;
+  if (int s = hip_status(timed("gnorm_bwd", st, [&] { return launch_gnorm(1, a, nb, st); }), "ccq_gated_rmsnorm_bwd"))
+    return s;
+  if (!dweight) return CCQ_OK;
+  return hip_status(launch_sum_rows2(part, dweight, dv, nullptr, nullptr, 0, nb, red, st),
+                    "ccq_gated_rmsnorm_bwd(dweight)");
 }
 
 }  // extern "C"

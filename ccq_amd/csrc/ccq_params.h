@@ -14,6 +14,46 @@ namespace ccq {
 // slices of the first pass of the column sums of partial rows (launch_sum_rows)
 constexpr int kSumSlices = 32;
 
+// Short causal depthwise convolution (+ activation, + per-head L2 normalisation) of the layer
+// prologue: x, y, yn, dy, dyn, dx bf16 [tokens, D]; weight fp32 [D, W] (tap W-1 on the current
+// token); caches fp32 [N, D, W-1] (the previous W-1 inputs of each sequence).
+struct ConvArgs {
+  const void* x;
+  const float* w;
+  const float* bias;        // [D] (nullable)
+  const float* cache_in;    // (nullable = zeros)
+  const int64_t* cu;        // [N+1] (nullable: N sequences of T tokens)
+  void* y;                  // act(conv(x)) (nullable)
+  void* yn;                 // per-head L2-normalised y (nullable)
+  float* rstd;              // fp32 [tokens, D / hd] (with yn)
+  float* cache_out;         // (nullable)
+  const void* dy;           // bwd: gradient of y (nullable)
+  const void* dyn;          // bwd: gradient of yn (nullable)
+  void* dx;
+  float* dw_part;           // fp32 [blocks, D * W] per-workgroup partial weight gradients
+  float* db_part;           // fp32 [blocks, D] (nullable)
+  long tokens;
+  int T, N, D, W, hd, act;
+  float eps;
+};
+
+// Gated RMSNorm of the layer epilogue: y = x / sqrt(mean(x^2) + eps) * w * silu(g) per row of dv
+// (x, g, y, dy, dx, dg bf16 [rows, dv]; w fp32 [dv] (nullable = ones); rstd fp32 [rows]).
+struct GNormArgs {
+  const void* x;
+  const void* g;
+  const float* w;
+  void* y;
+  float* rstd;
+  const void* dy;
+  void* dx;
+  void* dg;
+  float* dw_part;           // fp32 [blocks, dv] (nullable)
+  long rows;
+  int dv;
+  float eps;
+};
+
 struct L2NormArgs {
   const void* x;            // bf16 [rows, D]
   void* y;                  // bf16 [rows, D]

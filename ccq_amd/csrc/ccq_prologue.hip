@@ -1,0 +1,482 @@
+// The layer's prologue and epilogue around the CCQ operators, on gfx950 (reference
+// ccq/gdn/layer.py:266-296, 402-408; ccq/gla/layer.py:211-241):
+//   short convolution: y = act(bias + sum_w weight[:, w] x[t - (W-1) + w]) per channel (causal,
+//                      depthwise, act = SiLU or none), the first W-1 positions of a sequence read
+//                      the cached inputs of the previous call; optionally the per-head L2
+//                      normalisation of y (yn = y_h / sqrt(|y_h|^2 + eps), computed from y rounded
+//                      to bf16, as the operators normalise their bf16 inputs) -- the q / k prologue
+//                      in one pass instead of projection -> conv -> SiLU -> l2norm round trips;
+//   gated RMSNorm:     y = x / sqrt(mean(x^2) + eps) * weight * silu(g) per row of head_v_dim.
+// All are HBM-bound streaming passes.  Layout: token-major rows of D channels (bf16); a thread
+// owns 8 consecutive channels (one 16-byte piece per row) and walks a tile of tokens; the
+// channels of one head are consecutive lanes of one wavefront, so per-head sums are lane
+// shuffles.  Weight / bias gradients are per-workgroup partial sums, reduced by a second pass.
+#include "ccq_tile.h"
+#include "ccq_params.h"
+
+namespace ccq {
+
+namespace {
+
+constexpr int kConvTB = 16;     // tokens per tile of a thread
+
+__device__ __forceinline__ float silu_(float a) { return a / (1.f + __expf(-a)); }
+__device__ __forceinline__ float dsilu_(float a) {
+  const float s = 1.f / (1.f + __expf(-a));
+  return s * (1.f + a * (1.f - s));
+}
+
+// sum over the `n` consecutive lanes (n a power of two <= 64) that share a head
+__device__ __forceinline__ float head_sum(float x, int n) {
+  for (int m = 1; m < n; m <<= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+// Sequence of packed token p: [start, end) and index.  Dense batches: sequences of T tokens.
+struct SeqOf {
+  long start, end;
+  int n;
+};
+__device__ __forceinline__ SeqOf seq_of(const ConvArgs& a, long p) {
+  SeqOf s;
+  if (!a.cu) {
+    s.n = (int)(p / a.T);
+    s.start = (long)s.n * a.T;
+    s.end = s.start + a.T;
+    return s;
+  }
+  int lo = 0, hi = a.N;  // largest n with cu[n] <= p (skipping empty sequences)
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (a.cu[mid] <= p) lo = mid;
+    else hi = mid;
+  }
+  while (lo + 1 < a.N && a.cu[lo + 1] <= p) ++lo;
+  s.n = lo;
+  s.start = a.cu[lo];
+  s.end = a.cu[lo + 1];
+  return s;
+}
+
+// Eight channels [c, c + 8) of token p: 0 <= p < tokens
+__device__ __forceinline__ void load8(const bf16* x, long p, int D, int c, float (&v)[8]) {
+  const bf16x8 b = *(const bf16x8*)(x + p * D + c);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)b[i];
+}
+
+// Input at position rel (relative to its sequence start; rel < 0 reads the cached inputs) of
+// sequence sq, channels [c, c + 8).
+__device__ __forceinline__ void window_in(const ConvArgs& a, const SeqOf& sq, long rel, int c, float (&v)[8]) {
+  if (rel >= 0) {
+    load8((const bf16*)a.x, sq.start + rel, a.D, c, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[i] = a.cache_in ? a.cache_in[((long)sq.n * a.D + c + i) * (a.W - 1) + (a.W - 1) + rel] : 0.f;
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// forward: grid (tiles over the packed tokens (grid-stride), D / 2048), 256 threads
+// ---------------------------------------------------------------------------
+template <int W>
+__global__ __launch_bounds__(kThreads) void conv_fwd_kernel(const ConvArgs a) {
+  const int c = (blockIdx.y * kThreads + threadIdx.x) * 8;
+  const bool own = c < a.D;
+  const int cc = own ? c : 0;
+  float wt[8][W], bs[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bs[i] = a.bias ? a.bias[cc + i] : 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) wt[i][w] = w < W ? a.w[(long)(cc + i) * W + w] : 0.f;
+  }
+  const int hl = a.hd / 8;  // lanes per head
+  const long ntiles = (a.tokens + kConvTB - 1) / kConvTB;
+  for (long tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const long p0 = tile * kConvTB, p1 = min(p0 + (long)kConvTB, a.tokens);
+    SeqOf sq = seq_of(a, p0);
+    // window: inputs at positions p - (W-1) .. p - 1 of the current sequence
+    float win[W][8];
+    auto fill = [&](long p) {
+#pragma unroll
+      for (int w = 0; w < W - 1; ++w)
+        if (w < W - 1) window_in(a, sq, (p - sq.start) - (W - 1) + w, cc, win[w]);
+    };
+    fill(p0);
+    for (long p = p0; p < p1; ++p) {
+      if (p >= sq.end) {
+        sq = seq_of(a, p);
+        fill(p);
+      }
+      float xv[8];
+      load8((const bf16*)a.x, p, a.D, cc, xv);
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float acc = bs[i] + wt[i][W - 1] * xv[i];
+#pragma unroll
+        for (int w = 0; w < W - 1; ++w)
+          if (w < W - 1) acc += wt[i][w] * win[w][i];
+        y[i] = a.act ? silu_(acc) : acc;
+      }
+      // shift the window
+#pragma unroll
+      for (int w = 0; w < W - 2; ++w)
+        if (w < W - 2)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) win[w][i] = win[w + 1][i];
+      if (W >= 2)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) win[W - 2][i] = xv[i];
+      bf16x8 yb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) yb[i] = (bf16)y[i];
+      if (own && a.y) *(bf16x8*)((bf16*)a.y + p * a.D + c) = yb;
+      if (a.yn) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += (float)yb[i] * (float)yb[i];
+        ss = head_sum(own ? ss : 0.f, hl);
+        const float r = rsqrtf(ss + a.eps);
+        bf16x8 nb;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nb[i] = (bf16)((float)yb[i] * r);
+        if (own) {
+          *(bf16x8*)((bf16*)a.yn + p * a.D + c) = nb;
+          if ((threadIdx.x & (hl - 1)) == 0) a.rstd[p * (a.D / a.hd) + c / a.hd] = r;
+        }
+      }
+    }
+  }
+}
+
+// Final cache: the last W-1 inputs of every sequence (cached inputs of earlier calls for a
+// sequence shorter than W-1).  grid (N, ceil(D / 256)).
+__global__ __launch_bounds__(kThreads) void conv_cache_kernel(const ConvArgs a) {
+  const int n = blockIdx.x, c = blockIdx.y * kThreads + threadIdx.x;
+  if (c >= a.D) return;
+  const long s0 = a.cu ? a.cu[n] : (long)n * a.T, len = a.cu ? a.cu[n + 1] - a.cu[n] : a.T;
+  for (int j = 0; j < a.W - 1; ++j) {
+    const long rel = len - (a.W - 1) + j;
+    float v;
+    if (rel >= 0) v = (float)((const bf16*)a.x)[(s0 + rel) * a.D + c];
+    else v = a.cache_in ? a.cache_in[((long)n * a.D + c) * (a.W - 1) + (a.W - 1) + rel] : 0.f;
+    a.cache_out[((long)n * a.D + c) * (a.W - 1) + j] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward: grid (tiles (grid-stride), D / 2048), 256 threads.  Per token the pre-activation is
+// recomputed from x; da = (dy + l2norm backward of dyn) * act'(a); dx[q] = sum_w weight[w] da[q +
+// (W-1) - w] over the same sequence; dweight / dbias partials per workgroup.
+// ---------------------------------------------------------------------------
+template <int W>
+__global__ __launch_bounds__(kThreads) void conv_bwd_kernel(const ConvArgs a) {
+  const int c = (blockIdx.y * kThreads + threadIdx.x) * 8;
+  const bool own = c < a.D;
+  const int cc = own ? c : 0;
+  float wt[8][W], bs[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bs[i] = a.bias ? a.bias[cc + i] : 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) wt[i][w] = w < W ? a.w[(long)(cc + i) * W + w] : 0.f;
+  }
+  float gw[8][W], gb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    gb[i] = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) gw[i][w] = 0.f;
+  }
+  const int hl = a.hd / 8;
+  const long ntiles = (a.tokens + kConvTB - 1) / kConvTB;
+  for (long tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const long p0 = tile * kConvTB, p1 = min(p0 + (long)kConvTB, a.tokens);
+    // da of the tokens [p, p + W - 1) after the current one, kept for dx (zero past the sequence)
+    float dan[W][8];
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dan[w][i] = 0.f;
+    SeqOf sq = seq_of(a, p0);
+    float win[W][8];
+    auto fill = [&](long p) {
+#pragma unroll
+      for (int w = 0; w < W - 1; ++w)
+        if (w < W - 1) window_in(a, sq, (p - sq.start) - (W - 1) + w, cc, win[w]);
+    };
+    fill(p0);
+    // tokens p0 .. p1 - 1 of the tile plus up to W - 1 more of the last token's sequence
+    const SeqOf slast = seq_of(a, p1 - 1);
+    const long ptop = min(p1 + (long)(W - 1), slast.end);
+    for (long p = p0; p < ptop; ++p) {
+      if (p >= sq.end) {
+        sq = seq_of(a, p);
+        fill(p);
+      }
+      float xv[8];
+      load8((const bf16*)a.x, p, a.D, cc, xv);
+      float pre[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float acc = bs[i] + wt[i][W - 1] * xv[i];
+#pragma unroll
+        for (int w = 0; w < W - 1; ++w)
+          if (w < W - 1) acc += wt[i][w] * win[w][i];
+        pre[i] = acc;
+      }
+      // upstream gradient of y at p
+      float g[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) g[i] = 0.f;
+      if (a.dy) {
+        const bf16x8 d = *(const bf16x8*)((const bf16*)a.dy + p * a.D + cc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) g[i] = (float)d[i];
+      }
+      if (a.dyn) {
+        // yn = bf16(y) r: dy += r (dyn - yn (yn . dyn)) over the head
+        const float r = a.rstd[p * (a.D / a.hd) + cc / a.hd];
+        const bf16x8 d = *(const bf16x8*)((const bf16*)a.dyn + p * a.D + cc);
+        float yn[8], dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float yv = a.act ? silu_(pre[i]) : pre[i];
+          yn[i] = (float)(bf16)yv * r;
+          dot += yn[i] * (float)d[i];
+        }
+        dot = head_sum(own ? dot : 0.f, hl);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) g[i] += r * ((float)d[i] - yn[i] * dot);
+      }
+      float da[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) da[i] = a.act ? g[i] * dsilu_(pre[i]) : g[i];
+      // weight / bias gradients of the tile's own tokens
+      if (p < p1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          gb[i] += da[i];
+          gw[i][W - 1] += da[i] * xv[i];
+#pragma unroll
+          for (int w = 0; w < W - 1; ++w)
+            if (w < W - 1) gw[i][w] += da[i] * win[w][i];
+        }
+      }
+      // da of p enters dx of the tokens p - (W-1) .. p of its sequence: shift it in
+#pragma unroll
+      for (int w = 0; w < W - 1; ++w)
+        if (w < W - 1)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dan[w][i] = dan[w + 1][i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dan[W - 1][i] = da[i];
+      // dx of q = p - (W-1) (dan[j] = da of q + j): sum_w weight[w] da[q + (W-1) - w]
+      const long q = p - (W - 1);
+      if (q >= p0 && q < p1 && q >= sq.start) {
+        bf16x8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float s = 0.f;
+#pragma unroll
+          for (int w = 0; w < W; ++w)
+            if (w < W) s += wt[i][w] * dan[W - 1 - w][i];
+          o[i] = (bf16)s;
+        }
+        if (own) *(bf16x8*)((bf16*)a.dx + q * a.D + c) = o;
+      }
+      // shift the input window
+#pragma unroll
+      for (int w = 0; w < W - 2; ++w)
+        if (w < W - 2)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) win[w][i] = win[w + 1][i];
+      if (W >= 2)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) win[W - 2][i] = xv[i];
+      // at the end of a sequence, the tile's tokens whose window ran past it get their dx from
+      // the da collected so far (the later ones are zero)
+      if (p + 1 == sq.end) {
+        for (int j = 1; j < W; ++j) {
+          const long q2 = p - (W - 1) + j;
+          // shift zeros in
+#pragma unroll
+          for (int w = 0; w < W - 1; ++w)
+            if (w < W - 1)
+#pragma unroll
+              for (int i = 0; i < 8; ++i) dan[w][i] = dan[w + 1][i];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dan[W - 1][i] = 0.f;
+          if (q2 >= p0 && q2 < p1 && q2 >= sq.start) {
+            bf16x8 o;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              float s = 0.f;
+#pragma unroll
+              for (int w = 0; w < W; ++w)
+                if (w < W) s += wt[i][w] * dan[W - 1 - w][i];
+              o[i] = (bf16)s;
+            }
+            if (own) *(bf16x8*)((bf16*)a.dx + q2 * a.D + c) = o;
+          }
+        }
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dan[w][i] = 0.f;
+      }
+    }
+  }
+  // this workgroup's partial sums
+  if (own) {
+    float* dwp = a.dw_part + (long)blockIdx.x * a.D * W;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+        if (w < W) dwp[(long)(c + i) * W + w] = gw[i][w];
+      if (a.db_part) a.db_part[(long)blockIdx.x * a.D + c + i] = gb[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gated RMSNorm: one wavefront per row of dv <= 512 (lane: 8 consecutive elements)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void gnorm_fwd_kernel(const GNormArgs a) {
+  const long row = (long)blockIdx.x * 4 + wave_id();
+  if (row >= a.rows) return;
+  const int l = lane_id(), e = l * 8;
+  const bool own = e < a.dv;
+  float x[8], g[8];
+  if (own) {
+    const bf16x8 xb = *(const bf16x8*)((const bf16*)a.x + row * a.dv + e);
+    const bf16x8 gb = *(const bf16x8*)((const bf16*)a.g + row * a.dv + e);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[i] = (float)xb[i];
+      g[i] = (float)gb[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = g[i] = 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+  ss = group_sum(ss, 64);
+  const float r = rsqrtf(ss / (float)a.dv + a.eps);
+  if (own) {
+    bf16x8 yb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float w = a.w ? a.w[e + i] : 1.f;
+      yb[i] = (bf16)(x[i] * r * w * silu_(g[i]));
+    }
+    *(bf16x8*)((bf16*)a.y + row * a.dv + e) = yb;
+  }
+  if (l == 0) a.rstd[row] = r;
+}
+
+// dL/dxh = dy w silu(g); dx = r (dxh - xh mean(dxh xh)); dg = dy xh w silu'(g); dw += dy xh silu(g)
+// (partials per workgroup, rows of the grid-stride loop)
+__global__ __launch_bounds__(kThreads) void gnorm_bwd_kernel(const GNormArgs a) {
+  const int l = lane_id(), e = l * 8;
+  const bool own = e < a.dv;
+  float gw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) gw[i] = 0.f;
+  __shared__ float sW[4][512];
+  for (long row = (long)blockIdx.x * 4 + wave_id(); row < a.rows; row += (long)gridDim.x * 4) {
+    float x[8], g[8], dy[8];
+    if (own) {
+      const bf16x8 xb = *(const bf16x8*)((const bf16*)a.x + row * a.dv + e);
+      const bf16x8 gb = *(const bf16x8*)((const bf16*)a.g + row * a.dv + e);
+      const bf16x8 db = *(const bf16x8*)((const bf16*)a.dy + row * a.dv + e);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x[i] = (float)xb[i];
+        g[i] = (float)gb[i];
+        dy[i] = (float)db[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = g[i] = dy[i] = 0.f;
+    }
+    const float r = a.rstd[row];
+    float dxh[8], xh[8], dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float w = (a.w && own) ? a.w[e + i] : 1.f;
+      xh[i] = x[i] * r;
+      const float s = silu_(g[i]);
+      dxh[i] = dy[i] * w * s;
+      dot += dxh[i] * xh[i];
+      gw[i] += dy[i] * xh[i] * s;
+      g[i] = dy[i] * xh[i] * w * dsilu_(g[i]);  // dg
+    }
+    dot = group_sum(dot, 64) / (float)a.dv;
+    if (own) {
+      bf16x8 dxb, dgb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dxb[i] = (bf16)(r * (dxh[i] - xh[i] * dot));
+        dgb[i] = (bf16)g[i];
+      }
+      *(bf16x8*)((bf16*)a.dx + row * a.dv + e) = dxb;
+      *(bf16x8*)((bf16*)a.dg + row * a.dv + e) = dgb;
+    }
+  }
+  if (!a.dw_part) return;
+  // the workgroup's four waves summed through LDS, one partial row per workgroup
+  if (own)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sW[wave_id()][e + i] = gw[i];
+  __syncthreads();
+  for (int j = threadIdx.x; j < a.dv; j += kThreads)
+    a.dw_part[(long)blockIdx.x * a.dv + j] = sW[0][j] + sW[1][j] + sW[2][j] + sW[3][j];
+}
+
+hipError_t launch_conv(int stage, const ConvArgs& a, int blocks, hipStream_t st) {
+  if (a.tokens <= 0 && stage != 2) return hipSuccess;
+  const dim3 grid((unsigned)blocks, (unsigned)((a.D + 8 * kThreads - 1) / (8 * kThreads)));
+  switch (stage) {
+    case 0:
+    case 1:
+      switch (a.W) {
+#define CCQ_CONV_W(N)                                                                      \
+  case N:                                                                                  \
+    if (stage == 0) hipLaunchKernelGGL(conv_fwd_kernel<N>, grid, dim3(kThreads), 0, st, a); \
+    else hipLaunchKernelGGL(conv_bwd_kernel<N>, grid, dim3(kThreads), 0, st, a);             \
+    break;
+        CCQ_CONV_W(1) CCQ_CONV_W(2) CCQ_CONV_W(3) CCQ_CONV_W(4) CCQ_CONV_W(5) CCQ_CONV_W(6) CCQ_CONV_W(7)
+        CCQ_CONV_W(8)
+#undef CCQ_CONV_W
+        default: return hipErrorInvalidValue;
+      }
+      break;
+    case 2:
+      if (a.N > 0 && a.W > 1)
+        hipLaunchKernelGGL(conv_cache_kernel, dim3((unsigned)a.N, (unsigned)((a.D + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, st, a);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gnorm(int stage, const GNormArgs& a, int blocks, hipStream_t st) {
+  if (a.rows <= 0) return hipSuccess;
+  if (stage == 0)
+    hipLaunchKernelGGL(gnorm_fwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(gnorm_bwd_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace ccq

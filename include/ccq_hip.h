@@ -263,6 +263,44 @@ int ccq_gla_decode_step(const void* q, const void* k, const void* v, const float
                         int use_l2norm, float scale, void* stream);
 
 /*
+ * Layer prologue: short causal depthwise convolution over time, y = act(bias + sum_w weight[:, w]
+ * x[t - (W-1) + w]) with act = SiLU (activation != 0) or none, fused with the per-head L2
+ * normalisation of y (y_norm, computed from y rounded to bf16).  Replaces the reference layers'
+ * q/k/v ShortConvolution (fla, ccq/gdn/layer.py:266-284, ccq/gla/layer.py:211-229) followed by the
+ * operators' l2norm of q and k (ccq/ops/ccq_gdn/fused_chunk.py:43-44): one pass over x instead of
+ * conv, activation and normalisation round trips.  x, y, y_norm bf16 [tokens, D] (tokens = B*T;
+ * varlen: B == 1 and cu_seqlens [N+1], each sequence restarts the window); weight fp32 [D, W]
+ * (tap W-1 on the current token), bias fp32 [D] (nullable); cache_in / cache_out fp32 [N, D, W-1]
+ * (the previous W-1 inputs of each sequence; nullable = zeros / not written).  y or y_norm may be
+ * null (not written); y_norm needs rstd fp32 [tokens, D / head_dim] (kept for the backward).
+ * D % 8 == 0; W in [1, 8]; head_dim a power of two in [8, 512] dividing D.
+ * Backward: dy (gradient of y) and / or dy_norm (of y_norm) bf16 -> dx bf16, dweight fp32 [D, W],
+ * dbias fp32 [D] (nullable); the cached inputs get no gradient.  workspace:
+ * ccq_conv_bwd_workspace_bytes(tokens, D, W).
+ */
+size_t ccq_conv_bwd_workspace_bytes(int64_t tokens, int D, int W);
+int ccq_conv_fwd(const void* x, const float* weight, const float* bias, const float* cache_in,
+                 const int64_t* cu_seqlens, void* y, void* y_norm, float* rstd, float* cache_out, int B, int T, int N,
+                 int D, int W, int head_dim, int activation, float eps, void* stream);
+int ccq_conv_bwd(const void* x, const float* weight, const float* bias, const float* cache_in,
+                 const int64_t* cu_seqlens, const void* dy, const void* dy_norm, const float* rstd, void* dx,
+                 float* dweight, float* dbias, void* workspace, int B, int T, int N, int D, int W, int head_dim,
+                 int activation, void* stream);
+
+/*
+ * Layer epilogue: gated RMSNorm y = x / sqrt(mean(x^2) + eps) * weight * silu(g) over rows of dv
+ * (the reference's o_norm = fla FusedRMSNormGated, ccq/gdn/layer.py:402-404).  x, g, y, dy, dx,
+ * dg bf16 [rows, dv]; weight fp32 [dv] (nullable = ones); rstd fp32 [rows] (written by the
+ * forward, read by the backward); dweight fp32 [dv] (nullable) with workspace
+ * ccq_gated_rmsnorm_bwd_workspace_bytes(rows, dv).  dv % 8 == 0, dv <= 512.
+ */
+size_t ccq_gated_rmsnorm_bwd_workspace_bytes(int64_t rows, int dv);
+int ccq_gated_rmsnorm_fwd(const void* x, const void* g, const float* weight, void* y, float* rstd, int64_t rows,
+                          int dv, float eps, void* stream);
+int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, const float* rstd, const void* dy,
+                          void* dx, void* dg, float* dweight, void* workspace, int64_t rows, int dv, void* stream);
+
+/*
  * Row L2 normalisation y = x / sqrt(sum x^2 + eps) (bf16 rows of D <= 512) and its backward.
  * Replaces fla l2norm as called by the reference (ccq/ops/ccq_gdn/fused_chunk.py:43-44).
  * rstd fp32 [rows] is written by the forward and read by the backward.
@@ -274,11 +312,11 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
 /*
  * Kernel timing (measurement facility; no counterpart in the reference).  While enabled, each
  * entry point records a HIP event pair around every launch of its kernels on the caller's
- * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: clean_fwd_sum,
- * clean_fwd, clean_bwd_rows, clean_bwd_dq, clean_bwd_gsum, clean_bwd_dk, clean_bwd_gate, gdn_prep,
- * gdn_fwd_state, gdn_fwd_o,
- * gdn_bwd_state, gdn_bwd_dqkw, gdn_bwd_wy, gla_intra, gla_fwd_state, gla_fwd_o, gla_bwd_state,
- * gla_bwd_dv, gla_bwd_dqk, gla_bwd_gk, clean_z_fwd, clean_z_bwd) and returns the summed
+ * stream.  ccq_timing_read waits for the recorded events of `kernel` (names: conv_fwd, conv_bwd,
+ * gnorm_fwd, gnorm_bwd, clean_fwd_sum, clean_fwd, clean_bwd_rows, clean_bwd_dq, clean_bwd_gsum,
+ * clean_bwd_dk, clean_bwd_gate, gdn_prep, gdn_fwd_state, gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw,
+ * gdn_bwd_wy, gla_intra, gla_fwd_state, gla_fwd_o, gla_bwd_state, gla_bwd_dv, gla_bwd_dqk,
+ * gla_bwd_gk, clean_z_fwd, clean_z_bwd) and returns the summed
  * milliseconds and the number of launches since the last ccq_timing_reset.
  */
 int ccq_timing_enable(int on);
