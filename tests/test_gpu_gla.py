@@ -134,3 +134,22 @@ def test_fused_ccq_gla(case):
         assert e <= TOL_BF16, n
     for n, e in kerrs.items():
         assert e <= TOL_KERNEL, n
+
+
+def test_gla_decay_range_guard():
+    """A log decay whose 16-token window sum falls below -80 (beyond the chunk kernels' split
+    decay factor) raises instead of returning inf / NaN; one just inside the bound runs."""
+    dev = _cuda()
+    from ccq_amd import fused_chunk_ccq_gla
+    B, T, H, K, V = 1, 64, 1, 64, 64
+    q = torch.randn(B, T, H, K, device=dev).bfloat16()
+    k = torch.randn(B, T, H, K, device=dev).bfloat16()
+    v = torch.randn(B, T, H, V, device=dev).bfloat16()
+    lam = torch.full((B, T, H, 1), 0.5, device=dev)
+    gk = torch.full((B, T, H, K), -0.1, device=dev)
+    gk[0, 20:36, 0, 3] = -5.2                 # 16 tokens summing to -83.2
+    with pytest.raises(ValueError, match="log decay"):
+        fused_chunk_ccq_gla(q, k, v, lam, gk)
+    gk[0, 20:36, 0, 3] = -4.9                 # -78.4 over the window: representable
+    o, _, _, _ = fused_chunk_ccq_gla(q, k, v, lam, gk)
+    assert torch.isfinite(o.float()).all()
