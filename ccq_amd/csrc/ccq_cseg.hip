@@ -601,13 +601,15 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
 }
 
 // ===========================================================================
-// cs_dq: grid N*H*nseg, K/16 waves; the forward walk again, with the upstream gradient.  Per chunk
-// (dZ = diag(f) dQc hi/lo in LDS, staged with the chunk):
-//   1  scores A = (Q K^T) o M and B = (dZ K^T) o M (20 tiles over the waves); s_t (last four waves)
-//   2  per wave and 16-row tile: Z = Q C + A K, W = dZ C + B K, m_t; partial row dots over the
-//      wave's columns of dqc . corr and dqc . m_t; dqc + W in place
-//   3  row totals of the partial dots (threads 0..127)
-//   4  per wave: dlambda, ds, dlogit; dq = dqc + W + ds m_t (+ dlogit w) in place; the per-token
+// cs_dq: grid N*H*nseg, K/16 waves; the forward walk again, with the upstream gradient.  The
+// backward needs z_t only through dqc_t . z_t = q_t . (C_t dqc_t) (C_t symmetric), so the walk forms
+// W'_t = C_t dqc_t alone -- no Q C, no (Q K^T) o M scores -- and dq_t's state term is f_t W'_t.
+// Per chunk (dQc hi/lo in LDS, staged with the chunk):
+//   1  score tiles B = (dQc K^T) o M (10 tiles over the waves)
+//   2  per wave and 16-row tile: W' = dQc C + B K and m_t; partial row dots over the wave's columns
+//      of q . W' (= dqc . z), dqc . m_t and q . m_t (= s_t); dqc + f W' in place
+//   3  row totals of the partial dots
+//   4  per wave: dlambda, ds, dlogit; dq = dqc + f W' + ds m_t (+ dlogit w) in place; the per-token
 //      scalars (wave 0); gate partials; C, m update
 //   5  dq rows to HBM, chunk c+1 into LDS (each thread overwrites exactly the pieces it stored)
 // ===========================================================================
@@ -617,21 +619,20 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
   constexpr int NW = K / 16, NT = 64 * NW;
   constexpr int LDK = K + 16, LDA = SB + 16, LDD = K + 4;
   constexpr int NKS = K / 32, NKT = K / 16;
+  constexpr int NP = MEAN ? 3 : 1;  // partial row dots per token
+  static_assert(NT >= NP * SB, "one thread per row total");
   __shared__ __attribute__((aligned(16))) bf16 sQ[SB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sK[SB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];   // dZ = diag(f) dQc, hi
+  __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];   // dQc, hi
   __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDK];
-  __shared__ __attribute__((aligned(16))) float sD[SB * LDD];   // dQc, then dQc + W, then dq
-  // score planes: (Q K^T) o M hi, lo; (dZ K^T) o M hi, lo
-  __shared__ __attribute__((aligned(16))) bf16 sAB[4 * SB * LDA];
-  bf16* const sAh = sAB;
-  bf16* const sAl = sAB + SB * LDA;
-  bf16* const sBh = sAB + 2 * SB * LDA;
-  bf16* const sBl = sAB + 3 * SB * LDA;
-  __shared__ __attribute__((aligned(16))) bf16 sMW[2 * LDK];     // m_prev hi, lo
-  __shared__ __attribute__((aligned(16))) float sPart[NW][2][SB];  // per-wave partial row dots
-  __shared__ __attribute__((aligned(16))) float sTot[2][SB];
-  __shared__ __attribute__((aligned(16))) float sS[SB], sLam[SB], sF[SB], sIp[SB], sGw[K];
+  __shared__ __attribute__((aligned(16))) float sD[SB * LDD];   // dQc, then dQc + f W', then dq
+  // score planes: (dQc K^T) o M hi, lo
+  __shared__ __attribute__((aligned(16))) bf16 sB[2 * SB * LDA];
+  bf16* const sBh = sB;
+  bf16* const sBl = sB + SB * LDA;
+  __shared__ __attribute__((aligned(16))) float sPart[NW][NP][SB];  // per-wave partial row dots
+  __shared__ __attribute__((aligned(16))) float sTot[NP][SB];
+  __shared__ __attribute__((aligned(16))) float sLam[SB], sF[SB], sIp[SB], sGw[K];
   __shared__ __attribute__((aligned(16))) f32x4 sScO[SB];   // per-token scalars of the chunk (out)
   __shared__ __attribute__((aligned(16))) float sDlO[SB];   // dlambda (out)
   __shared__ __attribute__((aligned(16))) float sGp[K + 4];  // gate partials: dW columns, db (out)
@@ -659,27 +660,16 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
   for (int kt = 0; kt < NKT; ++kt) settle(C[kt]);
   settle(mcol);
   for (int i = tid; i < SB * LDA; i += NT) {
-    sAh[i] = (bf16)0.f;
-    sAl[i] = (bf16)0.f;
     sBh[i] = (bf16)0.f;
     sBl[i] = (bf16)0.f;
   }
   if (GATE)
     for (int i = tid; i < K; i += NT) sGw[i] = a.gate_w[(long)u.h * K + i];
-  auto put_m = [&]() {
-    if (l < 16) {
-      bf16 x, y;
-      split2(mcol, x, y);
-      sMW[col] = x;
-      sMW[LDK + col] = y;
-    }
-  };
-  if (MEAN) put_m();
 
   RowsBf16<K, SB, NT> pq, pk;
   RowsF32<K, SB, NT> pd;
   constexpr int ND = RowsF32<K, SB, NT>::N, VPR = K / 4;
-  float pl[ND], plam = 0.f;
+  float plam = 0.f;
   auto load = [&](int c) {
     const int L = chunk_len(c);
     const long off = u.hb + (long)c * SB * u.rs;
@@ -688,10 +678,7 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
     // (the upstream gradient's dtype is a template parameter: one load sequence)
     if (DQ32) pd.load(a.dqc32 + off, u.rs, L, tid);
     else pd.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, tid);
-    const long tb = u.bos + (long)c * SB;
-#pragma unroll
-    for (int j = 0; j < ND; ++j) pl[j] = a.lam_used[(tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h];
-    plam = a.lam_used[(tb + min(tid & (SB - 1), L - 1)) * a.H + u.h];
+    plam = a.lam_used[(u.bos + (long)c * SB + min(tid & (SB - 1), L - 1)) * a.H + u.h];
   };
   auto stage = [&](int c) {
     const int L = chunk_len(c), t0 = c * SB;
@@ -701,9 +688,8 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
       const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
-      const float f = r < L ? -pl[j] * __builtin_amdgcn_rcpf(seg_pos(t0 + r, a.pos_off)) : 0.f;
       bf16x4 hh, ll;
-      split4(f * pd.v[j], hh, ll);
+      split4(pd.v[j], hh, ll);
       *(bf16x4*)(sZh + r * LDK + cc) = hh;
       *(bf16x4*)(sZl + r * LDK + cc) = ll;
     }
@@ -727,66 +713,28 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
 #pragma unroll
     for (int ss = 0; ss < 2; ++ss) kcol[ss] = frag16_tr(sK + 32 * ss * LDK + c0, LDK);
 
-    // ---- 1: score tiles (e < 10: A, else B) and s_t
+    // ---- 1: score tiles
 #pragma unroll
-    for (int j = 0; j < (20 + NW - 1) / NW; ++j) {
+    for (int j = 0; j < (10 + NW - 1) / NW; ++j) {
       const int e = w + j * NW;
-      if (e < 20) {
-        const int ee = e < 10 ? e : e - 10, I = tile_t(ee), J = tile_s(ee);
+      if (e < 10) {
+        const int I = tile_t(e), J = tile_s(e);
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (e < 10) {
 #pragma unroll
-          for (int ks = 0; ks < NKS; ++ks)
-            acc = mfma16(frag16_rm(sK + 16 * J * LDK + 32 * ks, LDK), frag16_rm(sQ + 16 * I * LDK + 32 * ks, LDK), acc);
-        } else {
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            const bf16x8 kf = frag16_rm(sK + 16 * J * LDK + 32 * ks, LDK);
-            acc = mfma16(kf, frag16_rm(sZh + 16 * I * LDK + 32 * ks, LDK), acc);
-            acc = mfma16(kf, frag16_rm(sZl + 16 * I * LDK + 32 * ks, LDK), acc);
-          }
+        for (int ks = 0; ks < NKS; ++ks) {
+          const bf16x8 kf = frag16_rm(sK + 16 * J * LDK + 32 * ks, LDK);
+          acc = mfma16(kf, frag16_rm(sZh + 16 * I * LDK + 32 * ks, LDK), acc);
+          acc = mfma16(kf, frag16_rm(sZl + 16 * I * LDK + 32 * ks, LDK), acc);
         }
         if (I == J) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             if (g4 + i > (l & 15)) acc[i] = 0.f;
         }
-        score_to_lds(acc, sAB, SB * LDA, LDA, (e < 10 ? 0 : 2 * SB * LDA) + 16 * I * LDA + 16 * J);
-      }
-    }
-    if (MEAN && w >= NW - 4) {
-      const int tt = w - (NW - 4), tb = 16 * tt + g4;
-      f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const bf16x8 qf = frag16_rm(sQ + 16 * tt * LDK + 32 * ks, LDK);
-        sv = mfma16(qf, frag16_rm(sMW + 32 * ks, 0), sv);
-        sv = mfma16(qf, frag16_rm(sMW + LDK + 32 * ks, 0), sv);
-      }
-      if ((l & 15) == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sS[tb + i] = sv[i];
+        score_to_lds(acc, sB, SB * LDA, LDA, 16 * I * LDA + 16 * J);
       }
     }
     __syncthreads();
-    if (MEAN) {
-      if (w >= NW - 4) {
-        const int tt = w - (NW - 4), tb = 16 * tt + g4;
-        f32x4 rsum = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ss = 0; ss < 2; ++ss) {
-          if (ss <= (tt >> 1)) {
-            rsum = mfma16(frag16_rm(sAh + 16 * tt * LDA + 32 * ss, LDA), ones8_(), rsum);
-            rsum = mfma16(frag16_rm(sAl + 16 * tt * LDA + 32 * ss, LDA), ones8_(), rsum);
-          }
-        }
-        if ((l & 15) == 0) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sS[tb + i] += rsum[i];
-        }
-      }
-      __syncthreads();
-    }
 
     // ---- 2: per wave, one 16-row tile at a time (the state's hi/lo B operands formed once)
     bf16x8 chh[NKS], chl[NKS];
@@ -794,15 +742,11 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
     for (int ks = 0; ks < NKS; ++ks) acc_pair_split(C[2 * ks], C[2 * ks + 1], chh[ks], chl[ks]);
 #pragma unroll 1
     for (int tt = 0; tt < 4; ++tt) {
-      f32x4 zh = f32x4{0.f, 0.f, 0.f, 0.f}, zl = f32x4{0.f, 0.f, 0.f, 0.f};
       f32x4 wh = f32x4{0.f, 0.f, 0.f, 0.f}, wl = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        const bf16x8 qa = frag16_rm_acc(sQ + 16 * tt * LDK + 32 * ks, LDK);
         const bf16x8 da = frag16_rm_acc(sZh + 16 * tt * LDK + 32 * ks, LDK);
         const bf16x8 dl = frag16_rm_acc(sZl + 16 * tt * LDK + 32 * ks, LDK);
-        zh = mfma16(qa, chh[ks], zh);
-        zl = mfma16(qa, chl[ks], zl);
         wh = mfma16(da, chh[ks], wh);
         wl = mfma16(dl, chh[ks], wl);
         wl = mfma16(da, chl[ks], wl);
@@ -811,49 +755,50 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
 #pragma unroll
       for (int ss = 0; ss < 2; ++ss) {
         if (ss <= (tt >> 1)) {
-          zh = mfma16(frag16_rm(sAh + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zh);
-          zl = mfma16(frag16_rm(sAl + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], zl);
           wh = mfma16(frag16_rm(sBh + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], wh);
           wl = mfma16(frag16_rm(sBl + 16 * tt * LDA + 32 * ss, LDA), kcol[ss], wl);
           if (MEAN) cum = mfma16(tri.at(tt, ss), kcol[ss], cum);
         }
       }
       const int tb = 16 * tt + g4;
-      const f32x4 ipv = *(const f32x4*)(sIp + tb);
-      f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (MEAN) sv = *(const f32x4*)(sS + tb);
-      f32x4 p1, p2;
+      const f32x4 fv = *(const f32x4*)(sF + tb);
+      f32x4 p1, p2, p3;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float* pd_ = sD + (tb + i) * LDD + col;
         const float dqc = *pd_;
+        const float qv = (float)sQ[(tb + i) * LDK + col];
+        const float wv = wh[i] + wl[i];
         const float mt = mcol + cum[i];
-        float corr = (zh[i] + zl[i]) * ipv[i];
-        if (MEAN) corr -= sv[i] * ipv[i] * ipv[i] * mt;
-        p1[i] = dqc * corr;
+        p1[i] = qv * wv;
         p2[i] = dqc * mt;
-        *pd_ = dqc + (wh[i] + wl[i]);
+        p3[i] = qv * mt;
+        *pd_ = dqc + fv[i] * wv;
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         p1[i] = row16_sum(p1[i]);
-        if (MEAN) p2[i] = row16_sum(p2[i]);
+        if (MEAN) {
+          p2[i] = row16_sum(p2[i]);
+          p3[i] = row16_sum(p3[i]);
+        }
       }
       if ((l & 15) == 0) {
         *(f32x4*)(&sPart[w][0][tb]) = p1;
-        if (MEAN) *(f32x4*)(&sPart[w][1][tb]) = p2;
+        if (MEAN) {
+          *(f32x4*)(&sPart[w][MEAN ? 1 : 0][tb]) = p2;
+          *(f32x4*)(&sPart[w][MEAN ? 2 : 0][tb]) = p3;
+        }
       }
     }
     __syncthreads();
-    // ---- 3: row totals
-    if (tid < 2 * SB) {
+    // ---- 3: row totals: dqc . z, dqc . m, s
+    if (tid < NP * SB) {
       const int q = tid / SB, t = tid % SB;
-      if (q == 0 || MEAN) {
-        float s = 0.f;
+      float s = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < NW; ++ww) s += sPart[ww][q][t];
-        sTot[q][t] = s;
-      }
+      for (int ww = 0; ww < NW; ++ww) s += sPart[ww][q][t];
+      sTot[q][t] = s;
     }
     __syncthreads();
 
@@ -874,15 +819,18 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       const f32x4 t0v = *(const f32x4*)(&sTot[0][tb]);
       f32x4 t1v = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
       if (MEAN) {
-        t1v = *(const f32x4*)(&sTot[1][tb]);
-        sv = *(const f32x4*)(sS + tb);
+        t1v = *(const f32x4*)(&sTot[MEAN ? 1 : 0][tb]);
+        sv = *(const f32x4*)(&sTot[MEAN ? 2 : 0][tb]);
       }
       f32x4 dlamv, dsv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float lam = lamv[i];
-        const float dlam = tb + i < L ? -t0v[i] : 0.f;
-        const float ds = MEAN ? lam * t1v[i] * ipv[i] * ipv[i] : 0.f;
+        const float lam = lamv[i], ip = ipv[i];
+        // dqc . corr = (dqc . z)/pos - s (dqc . m)/pos^2
+        float dcorr = t0v[i] * ip;
+        if (MEAN) dcorr -= sv[i] * ip * ip * t1v[i];
+        const float dlam = tb + i < L ? -dcorr : 0.f;
+        const float ds = MEAN ? lam * t1v[i] * ip * ip : 0.f;
         const float dlogit = dlam * lam * (1.f - lam);
         float* pd_ = sD + (tb + i) * LDD + col;
         float dq = *pd_ + ds * (mcol + cum[i]);
@@ -937,7 +885,6 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       gpo = *(const f32x4*)(sGp + 4 * (tid % (K / 4)));
       dbo = sGp[K];
     }
-    if (MEAN) put_m();
     stage(min(c + 1, u.ce - 1));
     __syncthreads();
     load(min(c + 2, u.ce - 1));

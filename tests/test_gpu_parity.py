@@ -19,9 +19,12 @@ TOL_BF16 = 2e-3
 # The kernels keep every intermediate at ~16 significant bits, so their output differs from the
 # oracle's rounded to the same dtype only where a rounding flips: held to a quarter of the bar.
 TOL_KERNEL = 5e-4
-# Per element: a bf16 output within one bf16 ulp of the exact value, up to an absolute slack of
-# 1e-4 x rms for elements that are small differences of large terms.
-TOL_FAITHFUL = 1e-4
+# Per element: a bf16 output within one bf16 ulp of the exact value, up to an absolute slack for
+# elements that are small differences of large terms.  Each term carries ~16 significant bits
+# (hi/lo bf16 operands, 2^-17 relative), and terms reach ~10x the rms of dk: on the first token of a
+# sequence with no initial state (corr_0 = 0, so its own terms cancel exactly) dk_0 is such a
+# difference, 2^-17 x 10 x rms ~ 1e-4 x rms away; the slack is twice that.
+TOL_FAITHFUL = 2e-4
 
 
 def _cuda():
