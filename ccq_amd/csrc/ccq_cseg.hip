@@ -230,15 +230,17 @@ struct TileOut {
       v[j] = *(const f32x4*)(src + (idx / VPR) * ld + (idx % VPR) * 4);
     }
   }
+  // w32 / w16 (uniform over the launch) select the outputs asked for: a store to an absent output
+  // would be dropped by its resource, but it would still take the vector-memory issue slots.
   __device__ __forceinline__ void store(__amdgpu_buffer_rsrc_t r32, __amdgpu_buffer_rsrc_t r16, long rs,
-                                        int tid) const {
+                                        int tid, bool w32, bool w16) const {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
       const int idx = tid + j * NT;
       const int e = (int)((idx / VPR) * rs + (idx % VPR) * 4);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[j]), r32, e * 4, 0, 0);
+      if (w32) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[j]), r32, e * 4, 0, 0);
       const bf16x4 b = bf16x4{(bf16)v[j][0], (bf16)v[j][1], (bf16)v[j][2], (bf16)v[j][3]};
-      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, b), r16, e * 2, 0, 0);
+      if (w16) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, b), r16, e * 2, 0, 0);
     }
   }
 };
@@ -580,12 +582,13 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
     load(min(c + 2, u.ce - 1));
     const long ob = u.hb + (long)t0 * u.rs;
     out.store(rows_rsrc(a.qc32 ? a.qc32 + ob : nullptr, u.rs, L, K, 4),
-              rows_rsrc(a.qc ? (const bf16*)a.qc + ob : nullptr, u.rs, L, K, 2), u.rs, tid);
-    if (GATE) {
-      const __amdgpu_buffer_rsrc_t rl =
-          rows_rsrc(a.lam_out ? a.lam_out + (u.bos + t0) * a.H + u.h : nullptr, a.H, L, 1, 4);
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, lamo), rl,
-                                            tid < SB ? tid * a.H * 4 : 0x7ffffff0, 0, 0);
+              rows_rsrc(a.qc ? (const bf16*)a.qc + ob : nullptr, u.rs, L, K, 2), u.rs, tid, a.qc32 != nullptr,
+              a.qc != nullptr);
+    if (GATE && w == 0 && a.lam_out) {
+      // the chunk's SB gate values from wave 0 (row = lane)
+      static_assert(SB == 64, "per-token outputs fit wave 0");
+      const __amdgpu_buffer_rsrc_t rl = rows_rsrc(a.lam_out + (u.bos + t0) * a.H + u.h, a.H, L, 1, 4);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, lamo), rl, tid * a.H * 4, 0, 0);
     }
   }
 
@@ -608,10 +611,13 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
 //   1  score tiles B = (dQc K^T) o M (10 tiles over the waves)
 //   2  per wave and 16-row tile: W' = dQc C + B K and m_t; partial row dots over the wave's columns
 //      of q . W' (= dqc . z), dqc . m_t and q . m_t (= s_t); dqc + f W' in place
-//   3  row totals of the partial dots
-//   4  per wave: dlambda, ds, dlogit; dq = dqc + f W' + ds m_t (+ dlogit w) in place; the per-token
-//      scalars (wave 0); gate partials; C, m update
-//   5  dq rows to HBM, chunk c+1 into LDS (each thread overwrites exactly the pieces it stored)
+//   3  wave 0, lane = token: row totals of the partial dots, then dlambda, ds, dlogit and the
+//      per-token outputs
+//   4  per wave: dq = dqc + f W' + ds m_t (+ dlogit w) in place; gate partials; C, m update
+//   5  results to registers, chunk c+1 into LDS (each thread overwrites exactly the pieces it stored)
+// The results of chunk c leave during the products of chunk c+1, and the upstream gradient of chunk
+// c+1 is loaded during them too: the vector-memory traffic spreads over the pass instead of
+// queueing behind one barrier in every workgroup at once.
 // ===========================================================================
 template <int K, bool MEAN, bool GATE, bool DQ32>
 __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
@@ -631,7 +637,7 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
   bf16* const sBh = sB;
   bf16* const sBl = sB + SB * LDA;
   __shared__ __attribute__((aligned(16))) float sPart[NW][NP][SB];  // per-wave partial row dots
-  __shared__ __attribute__((aligned(16))) float sTot[NP][SB];
+  __shared__ __attribute__((aligned(16))) float sDs[SB], sDg[SB];  // per token: ds, dlogit
   __shared__ __attribute__((aligned(16))) float sLam[SB], sF[SB], sIp[SB], sGw[K];
   __shared__ __attribute__((aligned(16))) f32x4 sScO[SB];   // per-token scalars of the chunk (out)
   __shared__ __attribute__((aligned(16))) float sDlO[SB];   // dlambda (out)
@@ -670,15 +676,21 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
   RowsF32<K, SB, NT> pd;
   constexpr int ND = RowsF32<K, SB, NT>::N, VPR = K / 4;
   float plam = 0.f;
-  auto load = [&](int c) {
+  // chunk loads in two parts, issued at different points of a pass so that the vector-memory
+  // traffic of all workgroups spreads over the pass: k, q, lambda; the upstream gradient
+  auto load_a = [&](int c) {
     const int L = chunk_len(c);
     const long off = u.hb + (long)c * SB * u.rs;
     pk.load((const bf16*)a.k + off, u.rs, L, tid);
     pq.load((const bf16*)a.q + off, u.rs, L, tid);
+    plam = a.lam_used[(u.bos + (long)c * SB + min(tid & (SB - 1), L - 1)) * a.H + u.h];
+  };
+  auto load_b = [&](int c) {
+    const int L = chunk_len(c);
+    const long off = u.hb + (long)c * SB * u.rs;
     // (the upstream gradient's dtype is a template parameter: one load sequence)
     if (DQ32) pd.load(a.dqc32 + off, u.rs, L, tid);
     else pd.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, tid);
-    plam = a.lam_used[(u.bos + (long)c * SB + min(tid & (SB - 1), L - 1)) * a.H + u.h];
   };
   auto stage = [&](int c) {
     const int L = chunk_len(c), t0 = c * SB;
@@ -701,10 +713,40 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       sIp[tid] = ip;
     }
   };
+  // results of a chunk, held in registers from the end of its pass to the next pass's stores
+  TileOut<K, NT> out;
+  f32x4 sco = f32x4{0.f, 0.f, 0.f, 0.f}, gpo = f32x4{0.f, 0.f, 0.f, 0.f};
+  float dlo = 0.f, dbo = 0.f;
+  // the stores of chunk pc (the previous pass's): dq rows, and the per-token outputs from wave 0
+  // (the chunk's SB rows are its 64 lanes)
+  auto put_out = [&](int pc) {
+    const int L = chunk_len(pc), t0 = pc * SB;
+    const long ob = u.hb + (long)t0 * u.rs, tb0 = (u.bos + t0) * a.H + u.h;
+    out.store(rows_rsrc(a.dq32 ? a.dq32 + ob : nullptr, u.rs, L, K, 4),
+              rows_rsrc(a.dq ? (const bf16*)a.dq + ob : nullptr, u.rs, L, K, 2), u.rs, tid, a.dq32 != nullptr,
+              a.dq != nullptr);
+    if (w == 0) {
+      static_assert(SB == 64 && K / 4 <= 64, "per-token outputs fit wave 0");
+      constexpr int kPast = 0x7ffffff0;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sco),
+                                             rows_rsrc(a.sc + tb0 * 4, a.H * 4, L, 4, 4), tid * a.H * 16, 0, 0);
+      if (!GATE && a.dlam)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, dlo), rows_rsrc(a.dlam + tb0, a.H, L, 1, 4),
+                                              tid * a.H * 4, 0, 0);
+      if (GATE) {
+        const long gi = (long)(u.gc0 + pc) * a.H + u.h;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, gpo), buf_rsrc(a.dw_part + gi * K, K * 4),
+                                               tid < K / 4 ? tid * 16 : kPast, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, dbo), buf_rsrc(a.db_part + gi, 4),
+                                              tid == 0 ? 0 : kPast, 0, 0);
+      }
+    }
+  };
   // chunk loads and stages: unconditional (past the end the last chunk again)
-  load(u.cb);
+  load_a(u.cb);
+  load_b(u.cb);
   stage(u.cb);
-  load(min(u.cb + 1, u.ce - 1));
+  load_a(min(u.cb + 1, u.ce - 1));
   __syncthreads();
 
   for (int c = u.cb; c < u.ce; ++c) {
@@ -735,6 +777,8 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       }
     }
     __syncthreads();
+    // the previous chunk's results leave while this chunk's products run
+    if (c > u.cb) put_out(c - 1);
 
     // ---- 2: per wave, one 16-row tile at a time (the state's hi/lo B operands formed once)
     bf16x8 chh[NKS], chl[NKS];
@@ -742,14 +786,15 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
     for (int ks = 0; ks < NKS; ++ks) acc_pair_split(C[2 * ks], C[2 * ks + 1], chh[ks], chl[ks]);
 #pragma unroll 1
     for (int tt = 0; tt < 4; ++tt) {
-      f32x4 wh = f32x4{0.f, 0.f, 0.f, 0.f}, wl = f32x4{0.f, 0.f, 0.f, 0.f};
+      // three independent accumulator chains: hi x hi, lo x hi, hi x lo
+      f32x4 wh = f32x4{0.f, 0.f, 0.f, 0.f}, wl = f32x4{0.f, 0.f, 0.f, 0.f}, wm = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
         const bf16x8 da = frag16_rm_acc(sZh + 16 * tt * LDK + 32 * ks, LDK);
         const bf16x8 dl = frag16_rm_acc(sZl + 16 * tt * LDK + 32 * ks, LDK);
         wh = mfma16(da, chh[ks], wh);
         wl = mfma16(dl, chh[ks], wl);
-        wl = mfma16(da, chl[ks], wl);
+        wm = mfma16(da, chl[ks], wm);
       }
       f32x4 cum = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -768,7 +813,7 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
         float* pd_ = sD + (tb + i) * LDD + col;
         const float dqc = *pd_;
         const float qv = (float)sQ[(tb + i) * LDK + col];
-        const float wv = wh[i] + wl[i];
+        const float wv = wh[i] + (wl[i] + wm[i]);
         const float mt = mcol + cum[i];
         p1[i] = qv * wv;
         p2[i] = dqc * mt;
@@ -791,22 +836,45 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
         }
       }
     }
+    // the upstream gradient of chunk c+1 (its registers were staged at the end of the last pass)
+    load_b(min(c + 1, u.ce - 1));
     __syncthreads();
-    // ---- 3: row totals: dqc . z, dqc . m, s
-    if (tid < NP * SB) {
-      const int q = tid / SB, t = tid % SB;
-      float s = 0.f;
+    // ---- 3: per token (wave 0, lane = token): the row totals dqc . z, dqc . m, s and from them
+    // dlambda, ds, dlogit; the per-token outputs; the gate bias partial
+    if (w == 0) {
+      const int t = l;
+      float t0 = 0.f, t1 = 0.f, sv = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < NW; ++ww) s += sPart[ww][q][t];
-      sTot[q][t] = s;
+      for (int ww = 0; ww < NW; ++ww) {
+        t0 += sPart[ww][0][t];
+        if (MEAN) {
+          t1 += sPart[ww][MEAN ? 1 : 0][t];
+          sv += sPart[ww][MEAN ? 2 : 0][t];
+        }
+      }
+      const float lam = sLam[t], ip = sIp[t];
+      // dqc . corr = (dqc . z)/pos - s (dqc . m)/pos^2
+      float dcorr = t0 * ip;
+      if (MEAN) dcorr -= sv * ip * ip * t1;
+      const float dlam = t < L ? -dcorr : 0.f;
+      const float ds = MEAN ? lam * t1 * ip * ip : 0.f;
+      const float dlogit = dlam * lam * (1.f - lam);
+      sDs[t] = ds;
+      sDg[t] = dlogit;
+      sScO[t] = f32x4{sF[t], ds, GATE ? dlogit : dlam, MEAN ? -sv * ip : 0.f};
+      sDlO[t] = GATE ? dlogit : dlam;
+      if (GATE) {
+        const float d = group_sum(dlogit, 64);
+        if (l == 0) sGp[K] = d;
+      }
     }
     __syncthreads();
 
-    // ---- 4: dq, per-token scalars, gate partials, state update
-    float gsum = 0.f, dbsum = 0.f;
+    // ---- 4: dq (+ ds m_t, + dlogit w), gate column partials, state update
+    float gsum = 0.f;
     const float gwc = GATE ? sGw[col] : 0.f;
     f32x4 cum = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
+#pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       cum = f32x4{0.f, 0.f, 0.f, 0.f};
       if (MEAN) {
@@ -815,41 +883,19 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
           if (ss <= (tt >> 1)) cum = mfma16(tri.at(tt, ss), kcol[ss], cum);
       }
       const int tb = 16 * tt + g4;
-      const f32x4 ipv = *(const f32x4*)(sIp + tb), lamv = *(const f32x4*)(sLam + tb);
-      const f32x4 t0v = *(const f32x4*)(&sTot[0][tb]);
-      f32x4 t1v = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (MEAN) {
-        t1v = *(const f32x4*)(&sTot[MEAN ? 1 : 0][tb]);
-        sv = *(const f32x4*)(&sTot[MEAN ? 2 : 0][tb]);
-      }
-      f32x4 dlamv, dsv;
+      const f32x4 dsv = *(const f32x4*)(sDs + tb);
+      f32x4 dgv = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (GATE) dgv = *(const f32x4*)(sDg + tb);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float lam = lamv[i], ip = ipv[i];
-        // dqc . corr = (dqc . z)/pos - s (dqc . m)/pos^2
-        float dcorr = t0v[i] * ip;
-        if (MEAN) dcorr -= sv[i] * ip * ip * t1v[i];
-        const float dlam = tb + i < L ? -dcorr : 0.f;
-        const float ds = MEAN ? lam * t1v[i] * ip * ip : 0.f;
-        const float dlogit = dlam * lam * (1.f - lam);
         float* pd_ = sD + (tb + i) * LDD + col;
-        float dq = *pd_ + ds * (mcol + cum[i]);
+        float dq = *pd_;
+        if (MEAN) dq += dsv[i] * (mcol + cum[i]);
         if (GATE) {
-          dq += dlogit * gwc;
-          gsum += dlogit * (float)sQ[(tb + i) * LDK + col];
-          dbsum += dlogit;
+          dq += dgv[i] * gwc;
+          gsum += dgv[i] * (float)sQ[(tb + i) * LDK + col];
         }
         *pd_ = dq;
-        dlamv[i] = GATE ? dlogit : dlam;
-        dsv[i] = ds;
-      }
-      if (w == 0 && (l & 15) == 0) {
-        const f32x4 fv = *(const f32x4*)(sF + tb);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sScO[tb + i] = f32x4{fv[i], dsv[i], dlamv[i], MEAN ? -sv[i] * ipv[i] : 0.f};
-          sDlO[tb + i] = dlamv[i];
-        }
       }
     }
     if (GATE) {
@@ -857,13 +903,6 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       gsum += __shfl_xor(gsum, 16);
       gsum += __shfl_xor(gsum, 32);
       if (l < 16) sGp[col] = gsum;
-      if (w == 0) {
-        // the 16 lanes of a group hold the same rows: one lane per group counts them
-        float d = (l & 15) == 0 ? dbsum : 0.f;
-        d += __shfl_xor(d, 16);
-        d += __shfl_xor(d, 32);
-        if (l == 0) sGp[K] = d;
-      }
     }
     if (MEAN) mcol += __shfl(cum[3], 48 + (l & 15));
 #pragma unroll
@@ -872,42 +911,20 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       for (int kt = 0; kt < NKT; ++kt) C[kt] = mfma16(frag16_tr(sK + 32 * ss * LDK + 16 * kt, LDK), kcol[ss], C[kt]);
     __syncthreads();
 
-    // ---- 5: results of chunk c to registers; chunk c+1 in (each thread overwrites exactly the sD
-    // pieces it read); loads of chunk c+2; then the stores (after those loads: a later wait for
-    // them leaves the stores in flight)
-    TileOut<K, NT> out;
+    // ---- 5: results of chunk c to registers (stored during the next pass); chunk c+1 in (each
+    // thread overwrites exactly the sD pieces it read); k, q of chunk c+2
     out.read(sD, LDD, tid);
-    const f32x4 sco = sScO[tid & (SB - 1)];
-    const float dlo = sDlO[tid & (SB - 1)];
-    f32x4 gpo = f32x4{0.f, 0.f, 0.f, 0.f};
-    float dbo = 0.f;
+    sco = sScO[tid & (SB - 1)];
+    dlo = sDlO[tid & (SB - 1)];
     if (GATE) {
       gpo = *(const f32x4*)(sGp + 4 * (tid % (K / 4)));
       dbo = sGp[K];
     }
     stage(min(c + 1, u.ce - 1));
     __syncthreads();
-    load(min(c + 2, u.ce - 1));
-    const long ob = u.hb + (long)t0 * u.rs, tb0 = (u.bos + t0) * a.H + u.h;
-    out.store(rows_rsrc(a.dq32 ? a.dq32 + ob : nullptr, u.rs, L, K, 4),
-              rows_rsrc(a.dq ? (const bf16*)a.dq + ob : nullptr, u.rs, L, K, 2), u.rs, tid);
-    // per-token outputs: row tid of the chunk for the first SB threads, an offset past any resource
-    // (dropped) for the others
-    constexpr int kPast = 0x7ffffff0;
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sco), rows_rsrc(a.sc + tb0 * 4, a.H * 4, L, 4, 4),
-                                           tid < SB ? tid * a.H * 16 : kPast, 0, 0);
-    if (!GATE)
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, dlo),
-                                            rows_rsrc(a.dlam ? a.dlam + tb0 : nullptr, a.H, L, 1, 4),
-                                            tid < SB ? tid * a.H * 4 : kPast, 0, 0);
-    if (GATE) {
-      const long gi = (long)(u.gc0 + c) * a.H + u.h;
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, gpo), buf_rsrc(a.dw_part + gi * K, K * 4),
-                                             tid < K / 4 ? tid * 16 : kPast, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, dbo), buf_rsrc(a.db_part + gi, 4),
-                                            tid == 0 ? 0 : kPast, 0, 0);
-    }
+    load_a(min(c + 2, u.ce - 1));
   }
+  put_out(u.ce - 1);
 }
 
 // ===========================================================================
@@ -1247,7 +1264,8 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
     load(max(c - 2, u.cb));
     const long ob = u.hb + (long)t0 * u.rs;
     out.store(rows_rsrc(a.dk32 ? a.dk32 + ob : nullptr, u.rs, L, K, 4),
-              rows_rsrc(a.dk ? (const bf16*)a.dk + ob : nullptr, u.rs, L, K, 2), u.rs, tid);
+              rows_rsrc(a.dk ? (const bf16*)a.dk + ob : nullptr, u.rs, L, K, 2), u.rs, tid, a.dk32 != nullptr,
+              a.dk != nullptr);
   }
 
   if (first) {
