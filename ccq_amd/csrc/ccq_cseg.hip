@@ -148,6 +148,11 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Value of lane `src` (a constant) of x, for every lane (v_readlane).
+__device__ __forceinline__ float lane_value(float x, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), src));
+}
+
 // Marks a value loaded from HBM as settled: the empty asm consumes it (the load's wait is placed
 // here, before the chunk loop) and yields a register value of its own.  Without it, a loop-carried
 // value first loaded before the loop keeps the loop's wait analysis pessimistic: a full wait for
@@ -264,6 +269,14 @@ struct TileIn {
     for (int j = 0; j < N; ++j) {
       const int idx = tid + j * NT;
       *(f32x4*)(dst + (idx / VPR) * ld + (idx % VPR) * 4) = v[j];
+    }
+  }
+  // zeros over the pieces store() writes
+  __device__ __forceinline__ void zero(float* dst, int ld, int tid) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + j * NT;
+      *(f32x4*)(dst + (idx / VPR) * ld + (idx % VPR) * 4) = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
 };
@@ -864,8 +877,10 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       sScO[t] = f32x4{sF[t], ds, GATE ? dlogit : dlam, MEAN ? -sv * ip : 0.f};
       sDlO[t] = GATE ? dlogit : dlam;
       if (GATE) {
-        const float d = group_sum(dlogit, 64);
-        if (l == 0) sGp[K] = d;
+        // wave sum: within each 16-lane row by DPP, then the four row sums
+        const float d = row16_sum(dlogit);
+        const float tot = (lane_value(d, 0) + lane_value(d, 16)) + (lane_value(d, 32) + lane_value(d, 48));
+        if (l == 0) sGp[K] = tot;
       }
     }
     __syncthreads();
@@ -1091,31 +1106,38 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
   RowsF32<K, SB, NT> pd;
   TileIn<K, NT> pe;  // dk_extra rows (zero when absent)
   constexpr int ND = RowsF32<K, SB, NT>::N;
-  float pf[ND];
-  f32x4 psc = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto load = [&](int c) {
+  f32x4 psc = f32x4{0.f, 0.f, 0.f, 0.f};  // per-token scalars of token (lane) of the chunk
+  // chunk loads in two parts, issued at different points of a pass so that the vector-memory
+  // traffic of all workgroups spreads over the pass: k, q, the per-token scalars; the upstream
+  // gradient and dk_extra
+  auto load_a = [&](int c) {
     const int L = chunk_len(c);
     const long off = u.hb + (long)c * SB * u.rs, tb = u.bos + (long)c * SB;
     pk.load((const bf16*)a.k + off, u.rs, L, tid);
     pq.load((const bf16*)a.q + off, u.rs, L, tid);
+    psc = *(const f32x4*)(a.sc + ((tb + min(tid & (SB - 1), L - 1)) * a.H + u.h) * 4);
+  };
+  auto load_b = [&](int c) {
+    const int L = chunk_len(c);
+    const long off = u.hb + (long)c * SB * u.rs;
     // (the upstream gradient's dtype is a template parameter: one load sequence)
     if (DQ32) pd.load(a.dqc32 + off, u.rs, L, tid);
     else pd.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, tid);
-    pe.load(rows_rsrc(a.dk_extra ? a.dk_extra + off : nullptr, u.rs, L, K, 4), u.rs, tid);
-#pragma unroll
-    for (int j = 0; j < ND; ++j) pf[j] = a.sc[((tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h) * 4];
-    psc = *(const f32x4*)(a.sc + ((tb + min(tid & (SB - 1), L - 1)) * a.H + u.h) * 4);
+    if (a.dk_extra) pe.load(rows_rsrc(a.dk_extra + off, u.rs, L, K, 4), u.rs, tid);
   };
   // chunk c into LDS; the dk rows start as dk_extra (each thread writes the sO pieces it stores)
   auto stage = [&](int c) {
     const int L = chunk_len(c);
     pk.store(sK, LDK, L, tid);
     pq.store(sQ, LDK, L, tid);
-    pe.store(sO, LDO, tid);
+    if (a.dk_extra) pe.store(sO, LDO, tid);
+    else TileIn<K, NT>{}.zero(sO, LDO, tid);
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
       const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
-      const float f = r < L ? pf[j] : 0.f;
+      // f of row r from lane r (lane = token in psc)
+      const float fr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * r, __builtin_bit_cast(int, psc[0])));
+      const float f = r < L ? fr : 0.f;
       bf16x4 hh, ll;
       split4(f * pd.v[j], hh, ll);
       *(bf16x4*)(sZh + r * LDK + cc) = hh;
@@ -1145,11 +1167,21 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
     }
     return m;
   };
+  // dk rows of a chunk, held in registers from the end of its pass to the next pass's stores
+  TileOut<K, NT> out;
+  auto put_out = [&](int pc) {
+    const int L = chunk_len(pc);
+    const long ob = u.hb + (long)pc * SB * u.rs;
+    out.store(rows_rsrc(a.dk32 ? a.dk32 + ob : nullptr, u.rs, L, K, 4),
+              rows_rsrc(a.dk ? (const bf16*)a.dk + ob : nullptr, u.rs, L, K, 2), u.rs, tid, a.dk32 != nullptr,
+              a.dk != nullptr);
+  };
   // chunk loads and stages: unconditional (past the start of the segment its first chunk again)
   if (u.cb < u.ce) {
-    load(u.ce - 1);
+    load_a(u.ce - 1);
+    load_b(u.ce - 1);
     stage(u.ce - 1);
-    load(max(u.ce - 2, u.cb));
+    load_a(max(u.ce - 2, u.cb));
   }
   __syncthreads();
 
@@ -1183,6 +1215,8 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
       }
     }
     __syncthreads();
+    // the previous (later) chunk's dk rows leave while this chunk's products run
+    if (c < u.ce - 1) put_out(c + 1);
 
     // ---- dK rows, one 16-row tile (jt) at a time; the dm total of the chunk (row 0 of the suffix)
     bf16x8 qcol[2], zcolh[2], zcoll[2];
@@ -1241,6 +1275,9 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
       for (int i = 0; i < 4; ++i) sO[(16 * jt + g4 + i) * LDO + col] += xh[i] + xl[i] + sfx[i] + carry;
     }
     if (MEAN) carry += dmtot;
+    // the upstream gradient and dk_extra of chunk c-1 (their registers were staged at the end of the
+    // last pass)
+    load_b(max(c - 1, u.cb));
 
     // ---- E[:, cols] += Q^T dZ[:, cols] + dZ^T Q[:, cols]
 #pragma unroll
@@ -1256,17 +1293,13 @@ __global__ __launch_bounds__(K * 4) void cs_dk_kernel(const WalkArgs a) {
         E[kt] = mfma16(zb, qcol[ts], E[kt]);
       }
     __syncthreads();
-    // dk rows of chunk c to registers; chunk c-1 in; loads of chunk c-2; then the stores
-    TileOut<K, NT> out;
+    // dk rows of chunk c to registers (stored during the next pass); chunk c-1 in; k, q of chunk c-2
     out.read(sO, LDO, tid);
     stage(max(c - 1, u.cb));
     __syncthreads();
-    load(max(c - 2, u.cb));
-    const long ob = u.hb + (long)t0 * u.rs;
-    out.store(rows_rsrc(a.dk32 ? a.dk32 + ob : nullptr, u.rs, L, K, 4),
-              rows_rsrc(a.dk ? (const bf16*)a.dk + ob : nullptr, u.rs, L, K, 2), u.rs, tid, a.dk32 != nullptr,
-              a.dk != nullptr);
+    load_a(max(c - 2, u.cb));
   }
+  if (u.cb < u.ce) put_out(u.cb);
 
   if (first) {
     if (a.dh0) {
