@@ -367,7 +367,8 @@ __global__ __launch_bounds__(SegCols<K>::NT) void cs_sum_kernel(const WalkArgs a
 //            operands, one 16-row tile per wave of the last four
 //   per wave Z[:, cols] = Q C_prev[:, cols] + A K[:, cols]; running key sums (lower-triangular ones
 //            times K[:, cols]); q_clean to LDS; C[:, cols] += K^T K[:, cols]
-//   all      chunk c+1 from registers into the other LDS buffers; q_clean rows to HBM
+//   all      chunk c+1 from registers into the other LDS buffers; q_clean rows to registers, to HBM
+//            during the next chunk's products
 // Outputs: q_clean (bf16 and/or fp32), the gate's lambda, C_T and m_T (last segment).
 // ===========================================================================
 template <int K, bool MEAN, bool GATE>
@@ -459,6 +460,23 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
     load(min(u.cb + 1, u.ce - 1));
   }
   __syncthreads();
+  // q_clean rows and gate values of a chunk, held in registers from the end of its pass to the
+  // next pass's stores (which then overlap that pass's products)
+  TileOut<K, NT> out;
+  float lamo = 0.f;
+  auto put_out = [&](int pc) {
+    const int L = chunk_len(pc), t0 = pc * SB;
+    const long ob = u.hb + (long)t0 * u.rs;
+    out.store(rows_rsrc(a.qc32 ? a.qc32 + ob : nullptr, u.rs, L, K, 4),
+              rows_rsrc(a.qc ? (const bf16*)a.qc + ob : nullptr, u.rs, L, K, 2), u.rs, tid, a.qc32 != nullptr,
+              a.qc != nullptr);
+    if (GATE && w == 0 && a.lam_out) {
+      // the chunk's SB gate values from wave 0 (row = lane)
+      static_assert(SB == 64, "per-token outputs fit wave 0");
+      const __amdgpu_buffer_rsrc_t rl = rows_rsrc(a.lam_out + (u.bos + t0) * a.H + u.h, a.H, L, 1, 4);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, lamo), rl, tid * a.H * 4, 0, 0);
+    }
+  };
 
   float gbias = GATE ? a.gate_b[u.h] : 0.f;
   settle(gbias);
@@ -518,6 +536,7 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
       }
     }
     __syncthreads();
+    if (c > u.cb) put_out(c - 1);
     if (MEAN) {
       if (w >= NW - 4) {
         const int tt = w - (NW - 4), tb = 16 * tt + g4;
@@ -586,24 +605,13 @@ __global__ __launch_bounds__(K * 4) void cs_fwd_kernel(const WalkArgs a) {
       for (int kt = 0; kt < NKT; ++kt) C[kt] = mfma16(frag16_tr(Kc + 32 * ss * LDK + 16 * kt, LDK), kcol[ss], C[kt]);
     if (MEAN) put_m(b ^ 1);
     stage(min(c + 1, u.ce - 1), b ^ 1);
-    const float lamo = sLam[tid & (SB - 1)];  // (rewritten before the next chunk's first barrier)
+    lamo = sLam[tid & (SB - 1)];  // (rewritten before the next chunk's first barrier)
     __syncthreads();
-    // results of chunk c out, after the loads of chunk c+2 (a later wait for those loads then
-    // leaves these stores in flight)
-    TileOut<K, NT> out;
+    // results of chunk c to registers (stored during the next pass); loads of chunk c+2
     out.read(sO, LDO, tid);
     load(min(c + 2, u.ce - 1));
-    const long ob = u.hb + (long)t0 * u.rs;
-    out.store(rows_rsrc(a.qc32 ? a.qc32 + ob : nullptr, u.rs, L, K, 4),
-              rows_rsrc(a.qc ? (const bf16*)a.qc + ob : nullptr, u.rs, L, K, 2), u.rs, tid, a.qc32 != nullptr,
-              a.qc != nullptr);
-    if (GATE && w == 0 && a.lam_out) {
-      // the chunk's SB gate values from wave 0 (row = lane)
-      static_assert(SB == 64, "per-token outputs fit wave 0");
-      const __amdgpu_buffer_rsrc_t rl = rows_rsrc(a.lam_out + (u.bos + t0) * a.H + u.h, a.H, L, 1, 4);
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, lamo), rl, tid * a.H * 4, 0, 0);
-    }
   }
+  if (u.cb < u.ce) put_out(u.ce - 1);
 
   if (last) {
     if (a.h_fin) {
