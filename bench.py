@@ -115,7 +115,7 @@ def kernel_work(k=K, v=V, bt=BT, cb=64):
     return {
         "clean_fwd_sum": (2 * k * k, 2 * k + seg),
         "clean_fwd": (4 * k * k + 4 * k * cb, 2 * k + 2 * k + 4 * k + 4 + seg),
-        "clean_bwd_dq": (6 * k * k + 8 * k * cb, 2 * k + 2 * k + 4 * k + 4 + 2 * k + 16 + seg),
+        "clean_bwd_dq": (4 * k * k + 6 * k * cb, 2 * k + 2 * k + 4 * k + 4 + 2 * k + 16 + seg),
         "clean_bwd_gsum": (2 * k * k + 2 * k * cb, 2 * k + 4 * k + 16 + seg),
         "clean_bwd_dk": (6 * k * k + 8 * k * cb, 2 * k + 2 * k + 4 * k + 16 + 4 * k + 2 * k + seg),
         "gdn_prep": (2 * bt * (2 * k + v) + (2 * bt * bt) // 3, 2 * k + 2 * v + 8 + 2 * k + 4 * v + 4 + 4 * bt),
