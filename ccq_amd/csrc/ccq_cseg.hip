@@ -153,15 +153,6 @@ __device__ __forceinline__ float lane_value(float x, int src) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), src));
 }
 
-// Marks a value loaded from HBM as settled: the empty asm consumes it (the load's wait is placed
-// here, before the chunk loop) and yields a register value of its own.  Without it, a loop-carried
-// value first loaded before the loop keeps the loop's wait analysis pessimistic: a full wait for
-// every outstanding load and store at its first use in every pass.
-template <typename T>
-__device__ __forceinline__ void settle(T& x) {
-  asm volatile("" : "+v"(x));
-}
-
 // Causal score tile (accumulator of A = K rows 16 J.., B = Q or dZ rows 16 I..: lane = t column,
 // rows s) into LDS transposed, as hi/lo bf16: element (t, s) at [16 I + t][16 J + s] of the hi
 // plane at p and of the lo plane at p + plane.  `uoff` (the tile's offset, wave-uniform) passes

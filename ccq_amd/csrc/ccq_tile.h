@@ -684,6 +684,16 @@ struct PrefetchF32Split {
   }
 };
 
+// Marks a value loaded from HBM as settled: the empty asm consumes it (the load's wait is placed
+// here) and yields a register value of its own.  Without it, a loop-carried value first loaded
+// before a loop keeps the loop's wait analysis pessimistic: at the loop header the compiler merges
+// the pending loads of the entry path with those of the back edge and waits for the shorter
+// sequence's count in every pass.
+template <typename T>
+__device__ __forceinline__ void settle(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
 // Row-major register prefetch of a ROWS x D tile (bf16 or fp32) by NTHR threads: 16 consecutive
 // lanes cover one 256-byte row segment, so the global loads are whole rows and the LDS writes are
 // free of bank conflicts at any row pitch.  Rows at or beyond nvalid read row 0 and are stored as
