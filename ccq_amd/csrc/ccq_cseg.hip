@@ -167,12 +167,13 @@ __device__ __forceinline__ void score_to_lds(const f32x4& acc, bf16* p, int plan
   *(bf16x4*)(p + plane + e) = ll;
 }
 
-// State columns per workgroup of the segment kernels (one 16-column tile per wavefront) and column
-// blocks per (sequence, head): K = 256 splits its columns over two workgroups (the segment sums only;
-// the walks of K = 256 are column walks).
+// State columns per workgroup of the segment sums (one 16-column tile per wavefront) and column
+// blocks per (sequence, head): 64-column blocks, so that K = 128 runs two 4-wave workgroups per
+// (sequence, head, segment) -- two resident per CU -- instead of one 8-wave workgroup.  The walks
+// (K in {64, 128}) keep all K columns in one workgroup.
 template <int K>
 struct SegCols {
-  static constexpr int CW = K > 128 ? 128 : K, NCB = K / CW, NW = CW / 16, NT = 64 * NW;
+  static constexpr int CW = K > 64 ? 64 : K, NCB = K / CW, NW = CW / 16, NT = 64 * NW;
 };
 
 // One segment of one (sequence, head) and one column block: chunks [cb, ce) of the sequence's nc
@@ -182,13 +183,14 @@ struct SegUnit {
   long bos, hb, rs;
 };
 
-template <int K>
+// NCB column blocks per (sequence, head, segment): 1 for the walks, SegCols<K>::NCB for the sums.
+template <int K, int NCB = 1>
 __device__ __forceinline__ SegUnit seg_unit(const WalkArgs& a) {
   SegUnit u;
   int sub;
-  xcd_map(blockIdx.x, a.nseg * SegCols<K>::NCB, a.N * a.H, u.unit, sub);
-  u.seg = sub / SegCols<K>::NCB;
-  u.cbase = (sub % SegCols<K>::NCB) * SegCols<K>::CW;
+  xcd_map(blockIdx.x, a.nseg * NCB, a.N * a.H, u.unit, sub);
+  u.seg = sub / NCB;
+  u.cbase = (sub % NCB) * (K / NCB);
   u.n = u.unit / a.H;
   u.h = u.unit % a.H;
   seq_bounds(a.cu, u.n, a.T, u.bos, u.len);
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(SegCols<K>::NT) void cs_sum_kernel(const WalkArgs a
   constexpr int NT = SegCols<K>::NT, LDK = K + 16, NKT = K / 16;
   __shared__ __attribute__((aligned(16))) bf16 sK[2][SB * LDK];
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
-  const SegUnit u = seg_unit<K>(a);
+  const SegUnit u = seg_unit<K, SegCols<K>::NCB>(a);
   const int c0 = u.cbase + 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
   auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
   f32x4 D[NKT];
@@ -945,37 +947,38 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
 // cs_gsum: grid N*H*nseg*NCB, CW/16 waves.  segG[:, cols] = sum over the segment of Q^T dZ[:, cols]
 // (dZ = diag(f) dQc), segDM[cols] = sum of dm_t = -(s_t/pos_t) dz_t + ds_t q_t (every workgroup
 // writes, zero when empty).  Reads the per-token scalars (f, ds, -s/pos) written by the dq walk
-// (K <= 128) or by the per-token pass of the column walks (K = 256).
+// (K <= 128) or by the per-token pass of the column walks (K = 256).  A workgroup loads q whole
+// (the rows of G) and dQc only for its columns; the dm column sums are MFMAs of the per-token
+// scalars (hi/lo, every output row the same) against the dZ and Q columns.
 // ===========================================================================
 template <int K, bool MEAN, bool DQ32>
 __global__ __launch_bounds__(SegCols<K>::NT) void cs_gsum_kernel(const WalkArgs a) {
-  constexpr int NT = SegCols<K>::NT, LDK = K + 16, NKT = K / 16, VPR = K / 4;
+  constexpr int CW = SegCols<K>::CW, NT = SegCols<K>::NT, LDK = K + 16, LDZ = CW + 16, NKT = K / 16;
+  constexpr int VPR = CW / 4;
   __shared__ __attribute__((aligned(16))) bf16 sQ[SB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDK];
-  __shared__ __attribute__((aligned(16))) float sDs[SB], sSp[SB];
+  __shared__ __attribute__((aligned(16))) bf16 sZh[SB * LDZ];  // dZ[:, cols], hi
+  __shared__ __attribute__((aligned(16))) bf16 sZl[SB * LDZ];
+  // per token: ds, -s/pos as hi/lo bf16
+  __shared__ __attribute__((aligned(16))) bf16 sDsH[SB], sDsL[SB], sSpH[SB], sSpL[SB];
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(wave_id()), l = lane_id();
-  const SegUnit u = seg_unit<K>(a);
-  const int c0 = u.cbase + 16 * w, col = c0 + (l & 15), g4 = 4 * (l >> 4);
+  const SegUnit u = seg_unit<K, SegCols<K>::NCB>(a);
+  const int c0 = 16 * w, col = u.cbase + c0 + (l & 15), g4 = 4 * (l >> 4);
   auto chunk_len = [&](int c) { return min(SB, u.len - c * SB); };
   f32x4 G[NKT];
 #pragma unroll
   for (int kt = 0; kt < NKT; ++kt) G[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float dmc = 0.f;
+  f32x4 dm = f32x4{0.f, 0.f, 0.f, 0.f};
   RowsBf16<K, SB, NT> pq;
-  RowsF32<K, SB, NT> pd;
-  constexpr int ND = RowsF32<K, SB, NT>::N;
-  float pf[ND];
-  f32x4 psc = f32x4{0.f, 0.f, 0.f, 0.f};
+  RowsF32<CW, SB, NT> pd;
+  constexpr int ND = RowsF32<CW, SB, NT>::N;
+  f32x4 psc = f32x4{0.f, 0.f, 0.f, 0.f};  // per-token scalars of token (lane) of the chunk
   auto load = [&](int c) {
     const int L = chunk_len(c);
     const long off = u.hb + (long)c * SB * u.rs, tb = u.bos + (long)c * SB;
     pq.load((const bf16*)a.q + off, u.rs, L, tid);
     // (the upstream gradient's dtype is a template parameter: one load sequence)
-    if (DQ32) pd.load(a.dqc32 + off, u.rs, L, tid);
-    else pd.load(nullptr, (const bf16*)a.dqc16 + off, u.rs, L, tid);
-#pragma unroll
-    for (int j = 0; j < ND; ++j) pf[j] = a.sc[((tb + min((tid + j * NT) / VPR, L - 1)) * a.H + u.h) * 4];
+    if (DQ32) pd.load(a.dqc32 + off + u.cbase, u.rs, L, tid);
+    else pd.load(nullptr, (const bf16*)a.dqc16 + off + u.cbase, u.rs, L, tid);
     psc = *(const f32x4*)(a.sc + ((tb + min(tid & (SB - 1), L - 1)) * a.H + u.h) * 4);
   };
   auto stage = [&](int c) {
@@ -984,15 +987,23 @@ __global__ __launch_bounds__(SegCols<K>::NT) void cs_gsum_kernel(const WalkArgs 
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
       const int idx = tid + j * NT, r = idx / VPR, cc = (idx % VPR) * 4;
-      const float f = r < L ? pf[j] : 0.f;
+      // f of row r from lane r (lane = token in psc)
+      const float fr = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * r, __builtin_bit_cast(int, psc[0])));
+      const float f = r < L ? fr : 0.f;
       bf16x4 hh, ll;
       split4(f * pd.v[j], hh, ll);
-      *(bf16x4*)(sZh + r * LDK + cc) = hh;
-      *(bf16x4*)(sZl + r * LDK + cc) = ll;
+      *(bf16x4*)(sZh + r * LDZ + cc) = hh;
+      *(bf16x4*)(sZl + r * LDZ + cc) = ll;
     }
-    if (tid < SB) {
-      sDs[tid] = tid < L ? psc[1] : 0.f;
-      sSp[tid] = tid < L ? psc[3] : 0.f;
+    if (MEAN && tid < SB) {
+      const float ds = tid < L ? psc[1] : 0.f, sp = tid < L ? psc[3] : 0.f;
+      bf16 x, y;
+      split2(ds, x, y);
+      sDsH[tid] = x;
+      sDsL[tid] = y;
+      split2(sp, x, y);
+      sSpH[tid] = x;
+      sSpL[tid] = y;
     }
   };
   // chunk loads and stages: unconditional (past the end the last chunk again)
@@ -1005,20 +1016,25 @@ __global__ __launch_bounds__(SegCols<K>::NT) void cs_gsum_kernel(const WalkArgs 
   for (int c = u.cb; c < u.ce; ++c) {
 #pragma unroll
     for (int ss = 0; ss < 2; ++ss) {
-      const bf16x8 bh = frag16_tr(sZh + 32 * ss * LDK + c0, LDK), bl = frag16_tr(sZl + 32 * ss * LDK + c0, LDK);
+      const bf16x8 bh = frag16_tr(sZh + 32 * ss * LDZ + c0, LDZ), bl = frag16_tr(sZl + 32 * ss * LDZ + c0, LDZ);
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt) {
         const bf16x8 qa = frag16_tr(sQ + 32 * ss * LDK + 16 * kt, LDK);
         G[kt] = mfma16(qa, bh, G[kt]);
         G[kt] = mfma16(qa, bl, G[kt]);
       }
-    }
-    if (MEAN) {
-      // column sums of dm over the chunk: lane group g takes rows g, g + 4, ...
-#pragma unroll 4
-      for (int r = (l >> 4); r < SB; r += 4) {
-        const int e = r * LDK + col;
-        dmc += sSp[r] * ((float)sZh[e] + (float)sZl[e]) + sDs[r] * (float)sQ[e];
+      if (MEAN) {
+        // dm[cols] += sum_t (-s_t/pos_t) dz_t[cols] + ds_t q_t[cols]: A operands broadcast the
+        // per-token scalars of slots t = 32 ss + 8 (lane / 16) + j to every row
+        const int tb = 32 * ss + 8 * (l >> 4);
+        const bf16x8 qc = frag16_tr(sQ + 32 * ss * LDK + u.cbase + c0, LDK);
+        const bf16x8 ph = *(const bf16x8*)(sSpH + tb), pl = *(const bf16x8*)(sSpL + tb);
+        const bf16x8 dh = *(const bf16x8*)(sDsH + tb), dl = *(const bf16x8*)(sDsL + tb);
+        dm = mfma16(ph, bh, dm);
+        dm = mfma16(ph, bl, dm);
+        dm = mfma16(pl, bh, dm);
+        dm = mfma16(dh, qc, dm);
+        dm = mfma16(dl, qc, dm);
       }
     }
     __syncthreads();
@@ -1031,11 +1047,8 @@ __global__ __launch_bounds__(SegCols<K>::NT) void cs_gsum_kernel(const WalkArgs 
   for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) dst[(long)(16 * kt + g4 + r) * K + col] = G[kt][r];
-  if (MEAN) {
-    dmc += __shfl_xor(dmc, 16);
-    dmc += __shfl_xor(dmc, 32);
-    if (l < 16) a.segDM[((long)u.unit * a.nseg + u.seg) * K + col] = dmc;
-  }
+  // every row of the dm tile holds the column sums
+  if (MEAN && l < 16) a.segDM[((long)u.unit * a.nseg + u.seg) * K + col] = dm[0];
 }
 
 // ===========================================================================
@@ -1336,7 +1349,8 @@ int seg_cu_count() {
   return cache[dev];
 }
 
-// The segment sums of K = 256 (the sums and the gradient sums; its walks are column walks).
+// The segment sums (the sums and the gradient sums), SegCols<K>::NCB workgroups per (sequence, head,
+// segment); for K = 256 the only segment kernels (its walks are column walks).
 template <int K>
 hipError_t cseg_sums_k(int stage, const WalkArgs& a, hipStream_t st) {
   const long wgs = (long)a.N * a.H * a.nseg * SegCols<K>::NCB;
@@ -1364,14 +1378,12 @@ hipError_t cseg_sums_k(int stage, const WalkArgs& a, hipStream_t st) {
 
 template <int K>
 hipError_t cseg_k(int stage, const WalkArgs& a, hipStream_t st) {
+  if (stage == kSegSum || stage == kSegGsum) return cseg_sums_k<K>(stage, a, st);
   const long wgs = (long)a.N * a.H * a.nseg;
   if (wgs <= 0) return hipSuccess;
   const dim3 grid((unsigned)wgs), block(K * 4);
   const bool mean = a.subtract_mean != 0, gate = a.gate_w != nullptr;
   switch (stage) {
-    case kSegSum:
-      hipLaunchKernelGGL(cs_sum_kernel<K>, grid, block, 0, st, a);
-      break;
     case kSegFwd:
       if (mean && gate) hipLaunchKernelGGL((cs_fwd_kernel<K, true, true>), grid, block, 0, st, a);
       else if (mean) hipLaunchKernelGGL((cs_fwd_kernel<K, true, false>), grid, block, 0, st, a);
@@ -1390,15 +1402,6 @@ hipError_t cseg_k(int stage, const WalkArgs& a, hipStream_t st) {
 #undef CCQ_SEG_DQ
       break;
     }
-    case kSegGsum:
-      if (a.dqc32) {
-        if (mean) hipLaunchKernelGGL((cs_gsum_kernel<K, true, true>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((cs_gsum_kernel<K, false, true>), grid, block, 0, st, a);
-      } else {
-        if (mean) hipLaunchKernelGGL((cs_gsum_kernel<K, true, false>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((cs_gsum_kernel<K, false, false>), grid, block, 0, st, a);
-      }
-      break;
     case kSegDk:
       if (a.dqc32) {
         if (mean) hipLaunchKernelGGL((cs_dk_kernel<K, true, true>), grid, block, 0, st, a);
