@@ -1334,14 +1334,22 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     }
   }
 
-  // Everything a step reads except dS itself is loaded one step ahead into registers
-  // (for K = 256 the query / w halves are staged inside the step instead).
+  // Everything a step reads except dS itself is loaded one step ahead into registers.  For K = 256
+  // the query / w rows go through LDS in KH-column slices (one slice per pass of the dS update);
+  // each slice is loaded one pass ahead (the next chunk's first slice during the last pass).
   constexpr bool kPreQW = (NKH == 1);
   PrefetchF32<BT, BT> pP;
   PrefetchBf16<VB, BT> pO;
   PrefetchBf16<K, BT> pK;
-  PrefetchGrad<kPreQW ? KH : 8, BT> pQ;
-  PrefetchBf16<kPreQW ? KH : 8, BT> pW, pWl;
+  PrefetchGrad<KH, BT> pQ;
+  PrefetchBf16<KH, BT> pW, pWl;
+  auto issue_qw = [&](int cc, int hb) {
+    const int cx = cc * BT, Lx = min(BT, len - cx);
+    const long tx = ((bos + cx) * a.H + h) * K + hb * KH;
+    pQ.load(a.qc32 ? a.qc32 + tx : nullptr, a.qc16 ? (const bf16*)a.qc16 + tx : nullptr, rsk, Lx);
+    pW.load((const bf16*)a.w + tx, rsk, Lx);
+    pWl.load((const bf16*)a.wl + tx, rsk, Lx);
+  };
   float pgl = 0.f, pgt = 0.f;
   auto issue = [&](int c) {
     const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
@@ -1361,6 +1369,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     }
   };
   if (nc > 0) issue(nc - 1);
+  if (!kPreQW && nc > 0) issue_qw(nc - 1, 0);
 
   for (int c = nc - 1; c >= 0; --c) {
     const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
@@ -1424,10 +1433,12 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     const float gL = sGL[0];
     for (int hb = 0; hb < NKH; ++hb) {
       if (!kPreQW) {
-        stage_any_f32<KH>(nullptr, 0, sQcT, LDP, a.qc32 ? a.qc32 + (tok0 * a.H + h) * K + hb * KH : nullptr,
-                          a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K + hb * KH : nullptr, rsk, BT, L);
-        stage_bf16<KH>(nullptr, 0, swT, LDB, (const bf16*)a.w + (tok0 * a.H + h) * K + hb * KH, rsk, BT, L);
-        stage_bf16<KH>(nullptr, 0, swTl, LDB, (const bf16*)a.wl + (tok0 * a.H + h) * K + hb * KH, rsk, BT, L);
+        // slice hb (loaded one pass ahead) into LDS; the next slice's loads
+        pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
+        pW.store(nullptr, 0, swT, LDB);
+        pWl.store(nullptr, 0, swTl, LDB);
+        if (hb + 1 < NKH) issue_qw(c, hb + 1);
+        else if (c > 0) issue_qw(c - 1, 0);
         __syncthreads();
       }
 #pragma unroll
