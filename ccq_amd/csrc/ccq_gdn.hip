@@ -646,10 +646,11 @@ __global__ __launch_bounds__(kWalk8) void gdn_prep_v3_kernel(const GdnArgs a) {
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a, const int V) {
-  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDU = BT + 1, LDV = VB + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
+  constexpr int VB = 32, LDK = K + 8, LDKR = K + 16, LDU = BT + 1, LDV = VB + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
   __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sWl[BT * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sKT[K * LDB];
+  // k rows [t][k] (row-major: whole 16-byte writes; the state update reads K^T by transposing reads)
+  __shared__ __attribute__((aligned(16))) bf16 sK[BT * LDKR];
   __shared__ __attribute__((aligned(16))) bf16 sST[VB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sSTl[VB * LDK];
   __shared__ float sU[BT * LDV];
@@ -704,22 +705,17 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
     const long tok0 = bos + c0;
     pw.store(sW, LDK, nullptr, 0);
     pwl.store(sWl, LDK, nullptr, 0);
-    pk.store(nullptr, 0, sKT, LDB);
+    pk.store(sK, LDKR, nullptr, 0);
     pu.store(sU, LDV, nullptr, 0);
     if (tid < BT) {
       sFac[tid] = __expf(pgl - pg);
       if (tid == 0) sGL[0] = __expf(pgl);
     }
+    // S^T (hi/lo) as 8-byte pieces of four consecutive state rows
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
       const int rt = w + 4 * j;
-      if (rt < NRT) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int e = acc_col() * LDK + rt * 32 + acc_row(i);
-          split2(S[j][i], sST[e], sSTl[e]);
-        }
-      }
+      if (rt < NRT) acc_to_lds_t(S[j], sST, sSTl, LDK, rt * 32);
     }
     __syncthreads();
     if (c + 1 < nc) issue(c + 1);
@@ -760,7 +756,7 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
 #pragma unroll
         for (int i = 0; i < 16; ++i) S[j][i] *= gL;
         for (int k0 = 0; k0 < BT; k0 += 16) {
-          const bf16x8 ka = frag_rm(sKT + rt * 32 * LDB + k0, LDB);
+          const bf16x8 ka = frag32_tr(sK + k0 * LDKR + rt * 32, LDKR);
           bf16x8 hi, lo;
           frag_rm_f32(sUsT + k0, LDU, hi, lo);
           S[j] = mfma(ka, hi, S[j]);
@@ -1288,23 +1284,26 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a, const int V) {
-  constexpr int VB = 32, LDK = K + 8, LDB = BT + 8, LDP = BT + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
+  constexpr int VB = 32, LDK = K + 8, LDP = BT + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
   constexpr int KH = K > 128 ? 64 : K, NKH = K / KH;  // query / w rows staged per pass
-  constexpr long kBytes = (long)BT * LDP * 4 + (long)VB * LDB * 2 + (long)BT * LDK * 2 + (long)VB * LDK * 2 +
-                          2L * VB * LDP * 4 + (long)KH * LDP * 4 + 2L * KH * LDB * 2 + 3L * BT * 4 +
+  // row-major tiles read as transposed operands (transposing LDS reads): pitches of 16-element
+  // multiples plus 16
+  constexpr int LDO = VB + 16, LDW = KH + 16;
+  constexpr long kBytes = (long)BT * LDP * 4 + (long)BT * LDO * 2 + (long)BT * LDK * 2 + (long)VB * LDK * 2 +
+                          2L * VB * LDP * 4 + (long)KH * LDP * 4 + 2L * BT * LDW * 2 + 3L * BT * 4 +
                           (long)VB * LDK * 2 + 16 * 12;
   __shared__ __attribute__((aligned(16))) char smem[kBytes];
   Carver cv{smem};
   float* sPT = cv.take<float>(BT * LDP);
-  bf16* sdOT = cv.take<bf16>(VB * LDB);
+  bf16* sdO = cv.take<bf16>(BT * LDO);      // dO [t][v]
   bf16* sK = cv.take<bf16>(BT * LDK);
   bf16* sdST = cv.take<bf16>(VB * LDK);
   bf16* sdSTl = cv.take<bf16>(VB * LDK);
   float* sdUT = cv.take<float>(VB * LDP);   // -dU, [v][t]
   float* sgdOT = cv.take<float>(VB * LDP);  // scale gamma_t dO[t][v], [v][t]
   float* sQcT = cv.take<float>(KH * LDP);
-  bf16* swT = cv.take<bf16>(KH * LDB);
-  bf16* swTl = cv.take<bf16>(KH * LDB);
+  bf16* sW = cv.take<bf16>(BT * LDW);       // w [t][k slice], hi
+  bf16* sWl = cv.take<bf16>(BT * LDW);
   float* sFac = cv.take<float>(BT);
   float* sGam = cv.take<float>(BT);
   float* sGL = cv.take<float>(4);
@@ -1375,28 +1374,23 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     const int c0 = c * BT, L = min(BT, len - c0), gc = gc0 + c;
     const long tok0 = bos + c0;
     pP.store(sPT, LDP, nullptr, 0);
-    pO.store(nullptr, 0, sdOT, LDB);
+    pO.store(sdO, LDO, nullptr, 0);
     pK.store(sK, LDK, nullptr, 0);
     if (kPreQW) {
       pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
-      pW.store(nullptr, 0, swT, LDB);
-      pWl.store(nullptr, 0, swTl, LDB);
+      pW.store(sW, LDW, nullptr, 0);
+      pWl.store(sWl, LDW, nullptr, 0);
     }
     if (tid < BT) {
       sFac[tid] = __expf(pgl - pgt);
       sGam[tid] = (tid < L) ? __expf(pgt) : 0.f;
       if (tid == 0) sGL[0] = __expf(pgl);
     }
+    // dS'^T (hi/lo) as 8-byte pieces of four consecutive state rows
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
       const int rt = w + 4 * j;
-      if (rt < NRT) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int e = acc_col() * LDK + rt * 32 + acc_row(i);
-          split2(dS[j][i], sdST[e], sdSTl[e]);
-        }
-      }
+      if (rt < NRT) acc_to_lds_t(dS[j], sdST, sdSTl, LDK, rt * 32);
     }
     __syncthreads();
     if (c > 0) issue(c - 1);
@@ -1407,7 +1401,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
       for (int k0 = 0; k0 < BT; k0 += 16) {
         bf16x8 hi, lo;
         frag_rm_f32(sPT + w * 32 * LDP + k0, LDP, hi, lo);
-        const bf16x8 b = frag_rm(sdOT + k0, LDB);
+        const bf16x8 b = frag32_tr(sdO + k0 * LDO, LDO);
         acc = mfma(hi, b, acc);
         acc = mfma(lo, b, acc);
       }
@@ -1426,7 +1420,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     } else {
       for (int e = tid - 128; e < VB * BT; e += 128) {
         const int vv = e / BT, t = e % BT;
-        sgdOT[vv * LDP + t] = a.scale * sGam[t] * (float)sdOT[vv * LDB + t];
+        sgdOT[vv * LDP + t] = a.scale * sGam[t] * (float)sdO[t * LDO + vv];
       }
     }
     __syncthreads();
@@ -1435,8 +1429,8 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
       if (!kPreQW) {
         // slice hb (loaded one pass ahead) into LDS; the next slice's loads
         pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
-        pW.store(nullptr, 0, swT, LDB);
-        pWl.store(nullptr, 0, swTl, LDB);
+        pW.store(sW, LDW, nullptr, 0);
+        pWl.store(sWl, LDW, nullptr, 0);
         if (hb + 1 < NKH) issue_qw(c, hb + 1);
         else if (c > 0) issue_qw(c - 1, 0);
         __syncthreads();
@@ -1455,8 +1449,8 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
             dS[j] = mfma(qhi, ghi, dS[j]);
             dS[j] = mfma(qhi, glo, dS[j]);
             dS[j] = mfma(qlo, ghi, dS[j]);
-            const bf16x8 wa = frag_rm(swT + lr * LDB + k0, LDB);
-            const bf16x8 wal = frag_rm(swTl + lr * LDB + k0, LDB);
+            const bf16x8 wa = frag32_tr(sW + k0 * LDW + lr, LDW);
+            const bf16x8 wal = frag32_tr(sWl + k0 * LDW + lr, LDW);
             bf16x8 dhi, dlo;
             frag_rm_f32(sdUT + k0, LDP, dhi, dlo);
             dS[j] = mfma(wa, dhi, dS[j]);
