@@ -1282,28 +1282,39 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
 //   dU = P^T dO + diag(gamma_L/gamma) K dS'
 //   dS <- gamma_L dS' + Qc^T diag(scale gamma) dO - w^T dU
 // ===========================================================================
-template <int K>
+// Q32: q_clean arrives in fp32 (else bf16), a template parameter so that only one set of prefetch
+// registers exists.
+template <int K, bool Q32>
 __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a, const int V) {
   constexpr int VB = 32, LDK = K + 8, LDP = BT + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
-  constexpr int KH = K > 128 ? 64 : K, NKH = K / KH;  // query / w rows staged per pass
+  // query / w columns staged per pass of the dS update: 128 (four 32-row tiles, one per wave)
+  constexpr int KH = K > 128 ? 128 : K, NKH = K / KH;
   // row-major tiles read as transposed operands (transposing LDS reads): pitches of 16-element
   // multiples plus 16
   constexpr int LDO = VB + 16, LDW = KH + 16;
-  constexpr long kBytes = (long)BT * LDP * 4 + (long)BT * LDO * 2 + (long)BT * LDK * 2 + (long)VB * LDK * 2 +
-                          2L * VB * LDP * 4 + (long)KH * LDP * 4 + 2L * BT * LDW * 2 + 3L * BT * 4 +
-                          (long)VB * LDK * 2 + 16 * 12;
+  auto r16 = [](long b) { return (b + 15) & ~15L; };
+  // k (the dU phase) and the query / w slices (the dS passes, K > 128) are never live together: one
+  // region (with a single pass the slices are staged beside k at the chunk start)
+  constexpr bool kAlias = NKH > 1;
+  constexpr long kK = (((long)BT * LDK * 2) + 15) & ~15L;
+  constexpr long kQW = ((((long)KH * LDP * 4) + 15) & ~15L) + 2 * ((((long)BT * LDW * 2) + 15) & ~15L);
+  constexpr long kRegion = kAlias ? (kK > kQW ? kK : kQW) : kK + kQW;
+  constexpr long kBytes = (long)BT * LDP * 4 + (long)BT * LDO * 2 + kRegion + (long)VB * LDK * 2 +
+                          2L * VB * LDP * 4 + 3L * BT * 4 + (long)VB * LDK * 2 + 16 * 16;
   __shared__ __attribute__((aligned(16))) char smem[kBytes];
   Carver cv{smem};
   float* sPT = cv.take<float>(BT * LDP);
   bf16* sdO = cv.take<bf16>(BT * LDO);      // dO [t][v]
-  bf16* sK = cv.take<bf16>(BT * LDK);
+  char* region = cv.p;
+  cv.p += kRegion;
+  bf16* sK = (bf16*)region;                 // k [t][k] (dU phase)
+  float* sQcT = (float*)(region + (kAlias ? 0 : kK));  // Qc^T slice [k][t] (dS passes)
+  bf16* sW = (bf16*)((char*)sQcT + r16((long)KH * LDP * 4));  // w [t][k slice], hi
+  bf16* sWl = sW + r16((long)BT * LDW * 2) / 2;
   bf16* sdST = cv.take<bf16>(VB * LDK);
   bf16* sdSTl = cv.take<bf16>(VB * LDK);
   float* sdUT = cv.take<float>(VB * LDP);   // -dU, [v][t]
   float* sgdOT = cv.take<float>(VB * LDP);  // scale gamma_t dO[t][v], [v][t]
-  float* sQcT = cv.take<float>(KH * LDP);
-  bf16* sW = cv.take<bf16>(BT * LDW);       // w [t][k slice], hi
-  bf16* sWl = cv.take<bf16>(BT * LDW);
   float* sFac = cv.take<float>(BT);
   float* sGam = cv.take<float>(BT);
   float* sGL = cv.take<float>(4);
@@ -1340,14 +1351,32 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
   PrefetchF32<BT, BT> pP;
   PrefetchBf16<VB, BT> pO;
   PrefetchBf16<K, BT> pK;
-  PrefetchGrad<KH, BT> pQ;
+  using QPre = typename std::conditional<Q32, PrefetchF32<KH, BT>, PrefetchBf16<KH, BT>>::type;
+  QPre pQ;
   PrefetchBf16<KH, BT> pW, pWl;
   auto issue_qw = [&](int cc, int hb) {
     const int cx = cc * BT, Lx = min(BT, len - cx);
     const long tx = ((bos + cx) * a.H + h) * K + hb * KH;
-    pQ.load(a.qc32 ? a.qc32 + tx : nullptr, a.qc16 ? (const bf16*)a.qc16 + tx : nullptr, rsk, Lx);
+    if constexpr (Q32) pQ.load(a.qc32 + tx, rsk, Lx);
+    else pQ.load((const bf16*)a.qc16 + tx, rsk, Lx);
     pW.load((const bf16*)a.w + tx, rsk, Lx);
     pWl.load((const bf16*)a.wl + tx, rsk, Lx);
+  };
+  // Qc^T slice (fp32, [k][t]) from the prefetch registers
+  auto store_q = [&]() {
+    if constexpr (Q32) {
+      pQ.store(nullptr, 0, sQcT, LDP);
+    } else {
+      constexpr int VPR = KH / 8;
+#pragma unroll
+      for (int j = 0; j < QPre::N; ++j) {
+        const int idx = threadIdx.x + j * kThreads;
+        if (idx >= BT * VPR) continue;
+        const int r = idx / VPR, c = (idx % VPR) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sQcT[(c + i) * LDP + r] = (float)pQ.v[j][i];
+      }
+    }
   };
   float pgl = 0.f, pgt = 0.f;
   auto issue = [&](int c) {
@@ -1356,12 +1385,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     pP.load(a.PT + ((long)gc * a.H + h) * (BT * BT), BT, BT);
     pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L);
     pK.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L);
-    if (kPreQW) {
-      pQ.load(a.qc32 ? a.qc32 + (tok0 * a.H + h) * K : nullptr,
-              a.qc16 ? (const bf16*)a.qc16 + (tok0 * a.H + h) * K : nullptr, rsk, L);
-      pW.load((const bf16*)a.w + (tok0 * a.H + h) * K, rsk, L);
-      pWl.load((const bf16*)a.wl + (tok0 * a.H + h) * K, rsk, L);
-    }
+    if (kPreQW) issue_qw(c, 0);
     if (tid < BT) {
       pgl = a.gcum[(tok0 + L - 1) * a.H + h];
       pgt = (tid < L) ? a.gcum[(tok0 + tid) * a.H + h] : pgl;
@@ -1377,7 +1401,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     pO.store(sdO, LDO, nullptr, 0);
     pK.store(sK, LDK, nullptr, 0);
     if (kPreQW) {
-      pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
+      store_q();
       pW.store(sW, LDW, nullptr, 0);
       pWl.store(sWl, LDW, nullptr, 0);
     }
@@ -1428,7 +1452,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     for (int hb = 0; hb < NKH; ++hb) {
       if (!kPreQW) {
         // slice hb (loaded one pass ahead) into LDS; the next slice's loads
-        pQ.store(a.qc32 != nullptr, nullptr, 0, sQcT, LDP);
+        store_q();
         pW.store(sW, LDW, nullptr, 0);
         pWl.store(sWl, LDW, nullptr, 0);
         if (hb + 1 < NKH) issue_qw(c, hb + 1);
@@ -4087,7 +4111,12 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
           hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, false>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
       }
       else
-        hipLaunchKernelGGL(gdn_bwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+      {
+        if (a.qc32)
+          hipLaunchKernelGGL((gdn_bwd_state_kernel<K, true>), dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+        else
+          hipLaunchKernelGGL((gdn_bwd_state_kernel<K, false>), dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
+      }
       break;
     case kGdnBwdDqkw:
       if (K == 128 && V == 128) {
