@@ -646,7 +646,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_prep_v3_kernel(const GdnArgs a) {
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a, const int V) {
-  constexpr int VB = 32, LDK = K + 8, LDKR = K + 16, LDU = BT + 1, LDV = VB + 1, NRT = K / 32, TPW = (NRT + 3) / 4;
+  constexpr int VB = 32, LDK = K + 8, LDKR = K + 16, LDU = BT + 1, LDV = VB + 4, NRT = K / 32, TPW = (NRT + 3) / 4;
   __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sWl[BT * LDK];
   // k rows [t][k] (row-major: whole 16-byte writes; the state update reads K^T by transposing reads)
@@ -718,7 +718,9 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
       if (rt < NRT) acc_to_lds_t(S[j], sST, sSTl, LDK, rt * 32);
     }
     __syncthreads();
-    if (c + 1 < nc) issue(c + 1);
+    // the next chunk's loads: waves 2-3 (which store the snapshot) at once, waves 0-1 after their
+    // products (issuing them first held the products behind a stalled memory queue)
+    if (w >= 2 && c + 1 < nc) issue(c + 1);
     if (w < 2) {
       f32x16 acc = zero16();
       // w S with both operands as hi/lo pairs (lo x lo dropped)
@@ -731,11 +733,12 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
         float us = 0.f;
         if (r < L) {
           const float uu = sU[r * LDV + cc] - acc[i];
-          a.U[(tok0 + r) * rsv + (long)h * V + v0 + cc] = uu;
+          sU[r * LDV + cc] = uu;  // U rows leave from LDS after the barrier
           us = sFac[r] * uu;
         }
         sUsT[cc * LDU + r] = us;
       }
+      if (c + 1 < nc) issue(c + 1);
     } else {
       // state snapshot (hi/lo) to HBM for the output kernel and the backward
       constexpr int VPR = K / 8;
@@ -748,6 +751,12 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
       }
     }
     __syncthreads();
+    // U rows of the chunk to HBM as 16-byte pieces
+#pragma unroll
+    for (int j = 0; j < (BT * VB / 4) / kThreads; ++j) {
+      const int idx = tid + j * kThreads, r = idx / (VB / 4), c4 = (idx % (VB / 4)) * 4;
+      if (r < L) *(f32x4*)(a.U + (tok0 + r) * rsv + (long)h * V + v0 + c4) = *(const f32x4*)(sU + r * LDV + c4);
+    }
     const float gL = sGL[0];
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
