@@ -1426,7 +1426,9 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
       if (rt < NRT) acc_to_lds_t(dS[j], sdST, sdSTl, LDK, rt * 32);
     }
     __syncthreads();
-    if (c > 0) issue(c - 1);
+    // the previous chunk's loads: waves 2-3 at once, waves 0-1 after their dU products (issued
+    // first, a stalled memory queue held the products)
+    if (w >= 2 && c > 0) issue(c - 1);
     lds_to_global_bf16<K>((bf16*)a.dhT + (((long)gc * a.H + h) * V + v0) * K, K, sdST, LDK, VB);
     lds_to_global_bf16<K>((bf16*)a.dhTl + (((long)gc * a.H + h) * V + v0) * K, K, sdSTl, LDK, VB);
     if (w < 2) {
@@ -1443,13 +1445,10 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = w * 32 + acc_row(i), cc = acc_col();
-        float du = 0.f;
-        if (r < L) {
-          du = acc[i] + sFac[r] * acc2[i];
-          a.dU[(tok0 + r) * rsv + (long)h * V + v0 + cc] = du;
-        }
-        sdUT[cc * LDP + r] = -du;
+        const float du = r < L ? acc[i] + sFac[r] * acc2[i] : 0.f;
+        sdUT[cc * LDP + r] = -du;  // dU rows leave from LDS after the barrier
       }
+      if (c > 0) issue(c - 1);
     } else {
       for (int e = tid - 128; e < VB * BT; e += 128) {
         const int vv = e / BT, t = e % BT;
@@ -1457,6 +1456,16 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
       }
     }
     __syncthreads();
+    // dU rows of the chunk to HBM as 16-byte pieces (from the negated transposed copy)
+#pragma unroll
+    for (int j = 0; j < (BT * VB / 4) / kThreads; ++j) {
+      const int idx = tid + j * kThreads, r = idx / (VB / 4), c4 = (idx % (VB / 4)) * 4;
+      if (r < L) {
+        const f32x4 du = f32x4{-sdUT[c4 * LDP + r], -sdUT[(c4 + 1) * LDP + r], -sdUT[(c4 + 2) * LDP + r],
+                               -sdUT[(c4 + 3) * LDP + r]};
+        *(f32x4*)(a.dU + (tok0 + r) * rsv + (long)h * V + v0 + c4) = du;
+      }
+    }
     const float gL = sGL[0];
     for (int hb = 0; hb < NKH; ++hb) {
       if (!kPreQW) {
