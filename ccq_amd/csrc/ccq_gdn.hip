@@ -1300,16 +1300,16 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
   constexpr int KH = K > 128 ? 128 : K, NKH = K / KH;
   // row-major tiles read as transposed operands (transposing LDS reads): pitches of 16-element
   // multiples plus 16
-  constexpr int LDO = VB + 16, LDW = KH + 16;
+  constexpr int LDO = VB + 16, LDW = KH + 16, LDG = BT + 8;
   auto r16 = [](long b) { return (b + 15) & ~15L; };
   // k (the dU phase) and the query / w slices (the dS passes, K > 128) are never live together: one
   // region (with a single pass the slices are staged beside k at the chunk start)
   constexpr bool kAlias = NKH > 1;
   constexpr long kK = (((long)BT * LDK * 2) + 15) & ~15L;
-  constexpr long kQW = ((((long)KH * LDP * 4) + 15) & ~15L) + 2 * ((((long)BT * LDW * 2) + 15) & ~15L);
+  constexpr long kQW = 4 * ((((long)BT * LDW * 2) + 15) & ~15L);
   constexpr long kRegion = kAlias ? (kK > kQW ? kK : kQW) : kK + kQW;
   constexpr long kBytes = (long)BT * LDP * 4 + (long)BT * LDO * 2 + kRegion + (long)VB * LDK * 2 +
-                          2L * VB * LDP * 4 + 3L * BT * 4 + (long)VB * LDK * 2 + 16 * 16;
+                          (long)VB * LDP * 4 + 4L * VB * LDG * 2 + 3L * BT * 4 + (long)VB * LDK * 2 + 16 * 16;
   __shared__ __attribute__((aligned(16))) char smem[kBytes];
   Carver cv{smem};
   float* sPT = cv.take<float>(BT * LDP);
@@ -1317,13 +1317,18 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
   char* region = cv.p;
   cv.p += kRegion;
   bf16* sK = (bf16*)region;                 // k [t][k] (dU phase)
-  float* sQcT = (float*)(region + (kAlias ? 0 : kK));  // Qc^T slice [k][t] (dS passes)
-  bf16* sW = (bf16*)((char*)sQcT + r16((long)KH * LDP * 4));  // w [t][k slice], hi
+  // (dS passes) Qc and w slices [t][k slice] as hi/lo pairs, read as transposed operands
+  bf16* sQh = (bf16*)(region + (kAlias ? 0 : kK));
+  bf16* sQl = sQh + r16((long)BT * LDW * 2) / 2;
+  bf16* sW = sQl + r16((long)BT * LDW * 2) / 2;
   bf16* sWl = sW + r16((long)BT * LDW * 2) / 2;
   bf16* sdST = cv.take<bf16>(VB * LDK);
   bf16* sdSTl = cv.take<bf16>(VB * LDK);
-  float* sdUT = cv.take<float>(VB * LDP);   // -dU, [v][t]
-  float* sgdOT = cv.take<float>(VB * LDP);  // scale gamma_t dO[t][v], [v][t]
+  float* sdUT = cv.take<float>(VB * LDP);   // -dU, [v][t] (for the dU rows to HBM)
+  bf16* sdUh = cv.take<bf16>(VB * LDG);     // -dU, [v][t], hi / lo (operands)
+  bf16* sdUl = cv.take<bf16>(VB * LDG);
+  bf16* sgOh = cv.take<bf16>(VB * LDG);     // scale gamma_t dO[t][v], [v][t], hi / lo
+  bf16* sgOl = cv.take<bf16>(VB * LDG);
   float* sFac = cv.take<float>(BT);
   float* sGam = cv.take<float>(BT);
   float* sGL = cv.take<float>(4);
@@ -1371,10 +1376,26 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     pW.load((const bf16*)a.w + tx, rsk, Lx);
     pWl.load((const bf16*)a.wl + tx, rsk, Lx);
   };
-  // Qc^T slice (fp32, [k][t]) from the prefetch registers
+  // Qc slice [t][k] as hi/lo bf16 (rows past the chunk were loaded as zeros)
   auto store_q = [&]() {
     if constexpr (Q32) {
-      pQ.store(nullptr, 0, sQcT, LDP);
+      constexpr int VPR = KH / 4;
+#pragma unroll
+      for (int j = 0; j < QPre::N; ++j) {
+        const int idx = threadIdx.x + j * kThreads;
+        if (idx >= BT * VPR) continue;
+        const int r = idx / VPR, c = (idx % VPR) * 4;
+        bf16x4 hh, ll;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16 x, y;
+          split2(pQ.v[j][i], x, y);
+          hh[i] = x;
+          ll[i] = y;
+        }
+        *(bf16x4*)(sQh + r * LDW + c) = hh;
+        *(bf16x4*)(sQl + r * LDW + c) = ll;
+      }
     } else {
       constexpr int VPR = KH / 8;
 #pragma unroll
@@ -1382,8 +1403,8 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
         const int idx = threadIdx.x + j * kThreads;
         if (idx >= BT * VPR) continue;
         const int r = idx / VPR, c = (idx % VPR) * 8;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) sQcT[(c + i) * LDP + r] = (float)pQ.v[j][i];
+        *(bf16x8*)(sQh + r * LDW + c) = pQ.v[j];
+        *(bf16x8*)(sQl + r * LDW + c) = bf16x8{};
       }
     }
   };
@@ -1442,17 +1463,19 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
       }
       mma_rr(acc2, sK + w * 32 * LDK, LDK, sdST, LDK, K);
       mma_rr(acc2, sK + w * 32 * LDK, LDK, sdSTl, LDK, K);
+      f32x16 ndu;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = w * 32 + acc_row(i), cc = acc_col();
-        const float du = r < L ? acc[i] + sFac[r] * acc2[i] : 0.f;
-        sdUT[cc * LDP + r] = -du;  // dU rows leave from LDS after the barrier
+        ndu[i] = r < L ? -(acc[i] + sFac[r] * acc2[i]) : 0.f;
+        sdUT[cc * LDP + r] = ndu[i];  // dU rows leave from LDS after the barrier
       }
+      acc_to_lds_t(ndu, sdUh, sdUl, LDG, w * 32);
       if (c > 0) issue(c - 1);
     } else {
       for (int e = tid - 128; e < VB * BT; e += 128) {
         const int vv = e / BT, t = e % BT;
-        sgdOT[vv * LDP + t] = a.scale * sGam[t] * (float)sdO[t * LDO + vv];
+        split2(a.scale * sGam[t] * (float)sdO[t * LDO + vv], sgOh[vv * LDG + t], sgOl[vv * LDG + t]);
       }
     }
     __syncthreads();
@@ -1484,21 +1507,23 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
           const int lr = rt * 32 - hb * KH;
 #pragma unroll
           for (int i = 0; i < 16; ++i) dS[j][i] *= gL;
+          // Qc^T (scale gamma dO) into dS, -w^T dU into a second accumulator chain
+          f32x16 d2 = zero16();
+#pragma unroll
           for (int k0 = 0; k0 < BT; k0 += 16) {
-            bf16x8 qhi, qlo, ghi, glo;
-            frag_rm_f32(sQcT + lr * LDP + k0, LDP, qhi, qlo);
-            frag_rm_f32(sgdOT + k0, LDP, ghi, glo);
-            dS[j] = mfma(qhi, ghi, dS[j]);
-            dS[j] = mfma(qhi, glo, dS[j]);
-            dS[j] = mfma(qlo, ghi, dS[j]);
-            const bf16x8 wa = frag32_tr(sW + k0 * LDW + lr, LDW);
-            const bf16x8 wal = frag32_tr(sWl + k0 * LDW + lr, LDW);
-            bf16x8 dhi, dlo;
-            frag_rm_f32(sdUT + k0, LDP, dhi, dlo);
-            dS[j] = mfma(wa, dhi, dS[j]);
-            dS[j] = mfma(wa, dlo, dS[j]);
-            dS[j] = mfma(wal, dhi, dS[j]);
+            const bf16x8 qh = frag32_tr(sQh + k0 * LDW + lr, LDW), ql = frag32_tr(sQl + k0 * LDW + lr, LDW);
+            const bf16x8 gh = frag_rm(sgOh + k0, LDG), gl = frag_rm(sgOl + k0, LDG);
+            const bf16x8 wa = frag32_tr(sW + k0 * LDW + lr, LDW), wal = frag32_tr(sWl + k0 * LDW + lr, LDW);
+            const bf16x8 dh = frag_rm(sdUh + k0, LDG), dl = frag_rm(sdUl + k0, LDG);
+            dS[j] = mfma(qh, gh, dS[j]);
+            d2 = mfma(wa, dh, d2);
+            dS[j] = mfma(qh, gl, dS[j]);
+            d2 = mfma(wa, dl, d2);
+            dS[j] = mfma(ql, gh, dS[j]);
+            d2 = mfma(wal, dh, d2);
           }
+#pragma unroll
+          for (int i = 0; i < 16; ++i) dS[j][i] += d2[i];
         }
       }
       __syncthreads();
