@@ -1461,13 +1461,19 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
         acc = mfma(hi, b, acc);
         acc = mfma(lo, b, acc);
       }
-      mma_rr(acc2, sK + w * 32 * LDK, LDK, sdST, LDK, K);
-      mma_rr(acc2, sK + w * 32 * LDK, LDK, sdSTl, LDK, K);
+      // K dS' with dS' as hi/lo: two independent accumulator chains
+      f32x16 acc3 = zero16();
+#pragma unroll 4
+      for (int k0 = 0; k0 < K; k0 += 16) {
+        const bf16x8 ka = frag_rm(sK + w * 32 * LDK + k0, LDK);
+        acc2 = mfma(ka, frag_rm(sdST + k0, LDK), acc2);
+        acc3 = mfma(ka, frag_rm(sdSTl + k0, LDK), acc3);
+      }
       f32x16 ndu;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = w * 32 + acc_row(i), cc = acc_col();
-        ndu[i] = r < L ? -(acc[i] + sFac[r] * acc2[i]) : 0.f;
+        ndu[i] = r < L ? -(acc[i] + sFac[r] * (acc2[i] + acc3[i])) : 0.f;
         sdUT[cc * LDP + r] = ndu[i];  // dU rows leave from LDS after the barrier
       }
       acc_to_lds_t(ndu, sdUh, sdUl, LDG, w * 32);
