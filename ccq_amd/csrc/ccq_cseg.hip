@@ -130,29 +130,6 @@ struct Tril {
 __device__ __forceinline__ int tile_t(int e) { return e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3; }
 __device__ __forceinline__ int tile_s(int e) { return e - tile_t(e) * (tile_t(e) + 1) / 2; }
 
-// Value of another lane of the same 16-lane row by DPP.  Written as an update with a zero old value
-// and bound_ctrl set (every control used here reads a valid lane, so neither takes effect) so that
-// the move folds into the consuming add (v_add_f32_dpp).
-template <int C>
-__device__ __forceinline__ float dppf(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), C, 0xf, 0xf, true));
-}
-
-// Sum over the 16 lanes of a row (lanes 16 g .. 16 g + 15), every lane receives it: quad_perm
-// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dppf<0xB1>(x);
-  x += dppf<0x4E>(x);
-  x += dppf<0x141>(x);
-  x += dppf<0x140>(x);
-  return x;
-}
-
-// Value of lane `src` (a constant) of x, for every lane (v_readlane).
-__device__ __forceinline__ float lane_value(float x, int src) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), src));
-}
-
 // Causal score tile (accumulator of A = K rows 16 J.., B = Q or dZ rows 16 I..: lane = t column,
 // rows s) into LDS transposed, as hi/lo bf16: element (t, s) at [16 I + t][16 J + s] of the hi
 // plane at p and of the lo plane at p + plane.  `uoff` (the tile's offset, wave-uniform) passes
@@ -879,8 +856,7 @@ __global__ __launch_bounds__(K * 4) void cs_dq_kernel(const WalkArgs a) {
       sDlO[t] = GATE ? dlogit : dlam;
       if (GATE) {
         // wave sum: within each 16-lane row by DPP, then the four row sums
-        const float d = row16_sum(dlogit);
-        const float tot = (lane_value(d, 0) + lane_value(d, 16)) + (lane_value(d, 32) + lane_value(d, 48));
+        const float tot = wave_total(dlogit);
         if (l == 0) sGp[K] = tot;
       }
     }

@@ -26,8 +26,9 @@ namespace ccq {
 
 namespace {
 
+// (every thread of the workgroup calls it)
 __device__ __forceinline__ float block_sum256(float x, float* red) {
-  x = group_sum(x, 64);
+  x = wave_total(x);
   if (lane_id() == 0) red[wave_id()] = x;
   __syncthreads();
   const float s = red[0] + red[1] + red[2] + red[3];
@@ -57,30 +58,60 @@ __device__ __forceinline__ void load_qk(const DecodeArgs& a, long tok, int h, fl
 
 }  // namespace
 
-// Column blocks: a workgroup owns DC = 32 columns of a state and all of its rows, RG = 8 row groups
-// of K / 8 rows per thread: every state access of a wave is two coalesced 128-byte row pieces, and
-// many small workgroups keep several per CU in flight, so one workgroup's loads overlap another's
-// stores.
-constexpr int DC = 32, RG = kThreads / DC;
+// Column blocks: a workgroup owns DC = 32 columns of a state and all of its rows.  A thread holds
+// four consecutive columns (one 16-byte piece) of RPT = K / RG consecutive rows, RG = 32 row groups:
+// every state load or store of a wave covers eight whole 128-byte row pieces, so a 32-column slice
+// moves in K / 32 wide instructions per thread (one 4-byte access per instruction moved only a
+// quarter of that per issue slot).  Column sums over the rows go through LDS in two levels.
+constexpr int DC = 32, NQ = DC / 4, RG = kThreads / NQ;
+
+// Sum over the RG row groups of each of the DC columns (every thread holds four columns of one row
+// group, x): within a wave over its eight row groups (lanes l, l ^ 8, l ^ 16, ...: DPP, then two
+// lane swaps), then across the four waves through LDS; on return tot[c] (c < DC) holds the totals.
+// Two barriers.
+__device__ __forceinline__ void colsum(float (*mid)[DC], float* tot, const f32x4& x) {
+  f32x4 y;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float v = x[c] + dppf<0x128>(x[c]);  // row_ror:8 (lane l ^ 8 of the 16-lane row)
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    y[c] = v;
+  }
+  const int l = lane_id();
+  if (l < NQ) *(f32x4*)&mid[wave_id()][4 * l] = y;
+  __syncthreads();
+  if (threadIdx.x < DC) tot[threadIdx.x] = (mid[0][threadIdx.x] + mid[1][threadIdx.x]) + (mid[2][threadIdx.x] + mid[3][threadIdx.x]);
+  __syncthreads();
+}
+
+// A thread's RPT rows x 4 columns of a state slice to HBM (row stride ld).
+template <int K>
+__device__ __forceinline__ void store_cols(float* base, int ld, int rg, int c4, const f32x4 (&x)[K / RG]) {
+#pragma unroll
+  for (int r = 0; r < K / RG; ++r) *(f32x4*)(base + (long)(rg * (K / RG) + r) * ld + c4) = x[r];
+}
 
 template <int K>
 __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs a) {
   constexpr int RPT = K / RG;  // rows per thread
-  __shared__ float sq[K], sk[K], sm[K];
-  __shared__ float sz[RG][DC];
+  static_assert(RPT >= 1, "K >= 32");
+  __shared__ __attribute__((aligned(16))) float sq[K], sk[K], sm[K];
+  __shared__ __attribute__((aligned(16))) float sz[4][DC], szt[DC];
   __shared__ float red[4];
-  const int tid = threadIdx.x, jj = tid % DC, rg = tid / DC;
+  const int tid = threadIdx.x, cq = tid % NQ, rg = tid / NQ;
   const int unit = blockIdx.x, n = unit / a.H, h = unit % a.H;
-  const int j = blockIdx.y * DC + jj;
+  const int j0 = blockIdx.y * DC, j4 = j0 + 4 * cq;
   long bos;
   int len;
   seq_bounds(a.cu, n, a.T, bos, len);
 
   const int pos_off = a.pos_dev ? *a.pos_dev : a.pos_off;
-  float creg[RPT];
+  f32x4 creg[RPT];
   const float* Cin = a.C_in ? a.C_in + (long)unit * K * K : nullptr;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) creg[r] = Cin ? Cin[(long)(rg * RPT + r) * K + j] : 0.f;
+  for (int r = 0; r < RPT; ++r)
+    creg[r] = Cin ? *(const f32x4*)(Cin + (long)(rg * RPT + r) * K + j4) : f32x4{0.f, 0.f, 0.f, 0.f};
   if (tid < K) sm[tid] = a.m_in ? a.m_in[(long)unit * K + tid] : 0.f;
   __syncthreads();
 
@@ -106,52 +137,50 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
     __syncthreads();
     const float s = block_sum256(tid < K ? sm[tid] * sq[tid] : 0.f, red);
     // C column update and partial z over this thread's rows
-    const float kj = sk[j];
-    float zp = 0.f;
+    const f32x4 kj = *(const f32x4*)(sk + j4);
+    f32x4 zp = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
       const int i = rg * RPT + r;
       creg[r] += sk[i] * kj;
       zp += creg[r] * sq[i];
     }
-    sz[rg][jj] = zp;
-    __syncthreads();
-    if (rg == 0) {
-      float z = 0.f;
-#pragma unroll
-      for (int g = 0; g < RG; ++g) z += sz[g][jj];
+    // the final state leaves as soon as it is formed (its stores overlap the reduction below)
+    if (t == len - 1 && a.C_out) store_cols<K>(a.C_out + (long)unit * K * K, K, rg, j4, creg);
+    colsum(sz, szt, zp);
+    if (tid < DC) {
+      const int j = j0 + tid;
       float pos = (float)(t + 1 + pos_off);
       pos = pos < 1.f ? 1.f : pos;
-      float corr = z / pos;
+      float corr = szt[tid] / pos;
       if (a.subtract_mean) corr -= s * sm[j] / (pos * pos);
       a.qc[(tok * a.H + h) * K + j] = sq[j] - lam * corr;
     }
     __syncthreads();
   }
-  if (a.C_out) {
-    float* Co = a.C_out + (long)unit * K * K;
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) Co[(long)(rg * RPT + r) * K + j] = creg[r];
-  }
-  if (a.m_out && rg == 0) a.m_out[(long)unit * K + j] = sm[j];
+  // (no token, or the plain step without cleaning: the state as it came in)
+  if (a.C_out && (len == 0 || !a.ccq)) store_cols<K>(a.C_out + (long)unit * K * K, K, rg, j4, creg);
+  if (a.m_out && tid < DC) a.m_out[(long)unit * K + j0 + tid] = sm[j0 + tid];
 }
 
 template <int K>
 __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeArgs a) {
   constexpr int RPT = K / RG;
-  __shared__ float sq[K], sk[K], sgk[K];
-  __shared__ float sp[RG][DC];
-  const int tid = threadIdx.x, vv = tid % DC, rg = tid / DC;
+  static_assert(RPT >= 1, "K >= 32");
+  __shared__ __attribute__((aligned(16))) float sq[K], sk[K], sgk[K];
+  __shared__ __attribute__((aligned(16))) float sp[4][DC], spt[DC];
+  const int tid = threadIdx.x, cq = tid % NQ, rg = tid / NQ;
   const int unit = blockIdx.x, n = unit / a.H, h = unit % a.H;
-  const int V = a.V, v = blockIdx.y * DC + vv;
+  const int V = a.V, v0 = blockIdx.y * DC, v4 = v0 + 4 * cq;
   long bos;
   int len;
   seq_bounds(a.cu, n, a.T, bos, len);
 
-  float sreg[RPT];
+  f32x4 sreg[RPT];
   const float* Sin = a.S_in ? a.S_in + (long)unit * K * V : nullptr;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) sreg[r] = Sin ? Sin[(long)(rg * RPT + r) * V + v] : 0.f;
+  for (int r = 0; r < RPT; ++r)
+    sreg[r] = Sin ? *(const f32x4*)(Sin + (long)(rg * RPT + r) * V + v4) : f32x4{0.f, 0.f, 0.f, 0.f};
 
   // end of an in-place step (the clean kernel, launched before in the same stream, has read the
   // cached key sum and the position): the new key sum replaces the cached one, the position
@@ -173,50 +202,46 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
       sgk[tid] = a.gk ? __expf(a.gk[(tok * a.H + h) * K + tid]) : 1.f;
     }
     __syncthreads();
-    const float vt = (float)((const bf16*)a.v)[(tok * a.H + h) * V + v];
+    const long vo = (tok * a.H + h) * V + v4;
+    f32x4 vt, dv = f32x4{1.f, 1.f, 1.f, 1.f};
+    {
+      const bf16x4 vb = *(const bf16x4*)((const bf16*)a.v + vo);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) vt[c] = (float)vb[c];
+      if (a.gv) {
+        const f32x4 gv = *(const f32x4*)(a.gv + vo);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dv[c] = __expf(gv[c]);
+      }
+    }
     if (a.gla) {
-      const float dv = a.gv ? __expf(a.gv[(tok * a.H + h) * V + v]) : 1.f;
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
         const int i = rg * RPT + r;
         sreg[r] = sgk[i] * sreg[r] * dv + sk[i] * vt;
       }
     } else {
-      const float dec = (a.g ? __expf(a.g[tok * a.H + h]) : 1.f) * (a.gv ? __expf(a.gv[(tok * a.H + h) * V + v]) : 1.f);
-      float p = 0.f;
+      const f32x4 dec = (a.g ? __expf(a.g[tok * a.H + h]) : 1.f) * dv;
+      f32x4 p = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
         sreg[r] *= dec * sgk[rg * RPT + r];
         p += sreg[r] * sk[rg * RPT + r];
       }
-      sp[rg][vv] = p;
-      __syncthreads();
-      float ks = 0.f;
-#pragma unroll
-      for (int g = 0; g < RG; ++g) ks += sp[g][vv];
-      const float u = a.beta[tok * a.H + h] * (vt - ks);
+      colsum(sp, spt, p);
+      const f32x4 ks = *(const f32x4*)(spt + 4 * cq);
+      const f32x4 u = a.beta[tok * a.H + h] * (vt - ks);
 #pragma unroll
       for (int r = 0; r < RPT; ++r) sreg[r] += sk[rg * RPT + r] * u;
-      __syncthreads();
     }
-    float po = 0.f;
+    if (tt == len - 1 && a.S_out) store_cols<K>(a.S_out + (long)unit * K * V, V, rg, v4, sreg);
+    f32x4 po = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < RPT; ++r) po += sreg[r] * sq[rg * RPT + r];
-    sp[rg][vv] = po;
-    __syncthreads();
-    if (rg == 0) {
-      float o = 0.f;
-#pragma unroll
-      for (int g = 0; g < RG; ++g) o += sp[g][vv];
-      ((bf16*)a.o)[(tok * a.H + h) * V + v] = (bf16)(a.scale * o);
-    }
-    __syncthreads();
+    colsum(sp, spt, po);
+    if (tid < DC) ((bf16*)a.o)[(tok * a.H + h) * V + v0 + tid] = (bf16)(a.scale * spt[tid]);
   }
-  if (a.S_out) {
-    float* So = a.S_out + (long)unit * K * V;
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) So[(long)(rg * RPT + r) * V + v] = sreg[r];
-  }
+  if (a.S_out && len == 0) store_cols<K>(a.S_out + (long)unit * K * V, V, rg, v4, sreg);
 }
 
 template <int K>

@@ -790,4 +790,34 @@ __device__ __forceinline__ float group_sum(float x, int n) {
   return x;
 }
 
+// Value of another lane of the same 16-lane row by DPP.  Written as an update with a zero old value
+// and bound_ctrl set (every control used here reads a valid lane, so neither takes effect) so that
+// the move folds into the consuming add (v_add_f32_dpp).
+template <int C>
+__device__ __forceinline__ float dppf(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), C, 0xf, 0xf, true));
+}
+
+// Sum over the 16 lanes of a row (lanes 16 g .. 16 g + 15), every lane receives it: quad_perm
+// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dppf<0xB1>(x);
+  x += dppf<0x4E>(x);
+  x += dppf<0x141>(x);
+  x += dppf<0x140>(x);
+  return x;
+}
+
+// Value of lane `src` (a constant) of x, for every lane (v_readlane).
+__device__ __forceinline__ float lane_value(float x, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), src));
+}
+
+// Sum over the wavefront's 64 lanes, every lane receiving it: DPP within each row, then the four
+// row sums.  Every lane must be active.
+__device__ __forceinline__ float wave_total(float x) {
+  x = row16_sum(x);
+  return (lane_value(x, 0) + lane_value(x, 16)) + (lane_value(x, 32) + lane_value(x, 48));
+}
+
 }  // namespace ccq
