@@ -440,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
         zacc = mfma(qf, frag_rm(sCl[b] + k0, LDK), zacc);
       }
       for (int s0 = 0; s0 < 32 * (I + 1); s0 += 16) {
-        const bf16x8 kf = frag_cm(Kc + s0 * LDK + u.c0, LDK);
+        const bf16x8 kf = frag32_tr(Kc + s0 * LDK + u.c0, LDK);
         zacc = mfma(frag_rm(sAh + I * 32 * LDA + s0, LDA), kf, zacc);
         zacc = mfma(frag_rm(sAl + I * 32 * LDA + s0, LDA), kf, zacc);
         if (mean) cum = mfma(frag_tril_ones(32 * I, s0), kf, cum);
@@ -491,14 +491,14 @@ __global__ __launch_bounds__(kThreads) void cw_fwd_kernel(const WalkArgs a) {
     } else {
       bf16x8 kc[CB / 16];
 #pragma unroll
-      for (int s = 0; s < CB / 16; ++s) kc[s] = frag_cm(Kc + s * 16 * LDK + u.c0, LDK);
+      for (int s = 0; s < CB / 16; ++s) kc[s] = frag32_tr(Kc + s * 16 * LDK + u.c0, LDK);
 #pragma unroll
       for (int j = 0; j < TPW; ++j) {
         const int rt = sw + NSW * j;
         if (rt < NRT) {
 #pragma unroll
           for (int s = 0; s < CB / 16; ++s) {
-            const bf16x8 kr = frag_cm(Kc + s * 16 * LDK + rt * 32, LDK);  // (r, s) = k_s[rt*32 + r]
+            const bf16x8 kr = frag32_tr(Kc + s * 16 * LDK + rt * 32, LDK);  // (r, s) = k_s[rt*32 + r]
             C[j] = mfma(kr, kc[s], C[j]);
             if (mean) Mk[j] = mfma(ones8(), kr, Mk[j]);
           }
@@ -849,7 +849,7 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
         x = mfma(frag_rm(Zl + k0, LDK), ch, x);
       }
       for (int s0 = 0; s0 < 32 * (I + 1); s0 += 16) {
-        const bf16x8 kf = frag_cm(sK + s0 * LDK + u.c0, LDK);
+        const bf16x8 kf = frag32_tr(sK + s0 * LDK + u.c0, LDK);
         x = mfma(frag_rm(sAh + I * 32 * LDA + s0, LDA), kf, x);
         x = mfma(frag_rm(sAl + I * 32 * LDA + s0, LDA), kf, x);
         if (mean) cum = mfma(frag_tril_ones(32 * I, s0), kf, cum);
@@ -876,13 +876,13 @@ __global__ __launch_bounds__(kThreads) void cw_dq_kernel(const WalkArgs a) {
     } else {
       bf16x8 kc[CB / 16];
 #pragma unroll
-      for (int s = 0; s < CB / 16; ++s) kc[s] = frag_cm(sK + s * 16 * LDK + u.c0, LDK);
+      for (int s = 0; s < CB / 16; ++s) kc[s] = frag32_tr(sK + s * 16 * LDK + u.c0, LDK);
 #pragma unroll
       for (int j = 0; j < TPW; ++j) {
         const int rt = sw + NSW * j;
         if (rt < NRT) {
 #pragma unroll
-          for (int s = 0; s < CB / 16; ++s) C[j] = mfma(frag_cm(sK + s * 16 * LDK + rt * 32, LDK), kc[s], C[j]);
+          for (int s = 0; s < CB / 16; ++s) C[j] = mfma(frag32_tr(sK + s * 16 * LDK + rt * 32, LDK), kc[s], C[j]);
         }
       }
     }
@@ -1044,13 +1044,13 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
       }
 #pragma unroll 2
       for (int s0 = 32 * J; s0 < CB; s0 += 16) {
-        const bf16x8 qf = frag_cm(sQ + s0 * LDK + u.c0, LDK);
+        const bf16x8 qf = frag32_tr(sQ + s0 * LDK + u.c0, LDK);
         x = mfma(frag_rm(sB1h + J * 32 * LDA + s0, LDA), qf, x);
         x = mfma(frag_rm(sB1l + J * 32 * LDA + s0, LDA), qf, x);
-        const bf16x8 zhf = frag_cm(sZh + s0 * LDK + u.c0, LDK);
+        const bf16x8 zhf = frag32_tr(sZh + s0 * LDK + u.c0, LDK);
         const bf16x8 b2h = frag_rm(sB2h + J * 32 * LDA + s0, LDA);
         x = mfma(b2h, zhf, x);
-        const bf16x8 zlf = frag_cm(sZl + s0 * LDK + u.c0, LDK);
+        const bf16x8 zlf = frag32_tr(sZl + s0 * LDK + u.c0, LDK);
         x = mfma(b2h, zlf, x);
         x = mfma(frag_rm(sB2l + J * 32 * LDA + s0, LDA), zhf, x);
         if (mean) {
@@ -1088,16 +1088,16 @@ __global__ __launch_bounds__(kThreads) void cw_dk_kernel(const WalkArgs a) {
     } else {
 #pragma unroll
       for (int s = 0; s < CB / 16; ++s) {
-        const bf16x8 qc = frag_cm(sQ + s * 16 * LDK + u.c0, LDK);
-        const bf16x8 zc = frag_cm(sZh + s * 16 * LDK + u.c0, LDK);
-        const bf16x8 zcl = frag_cm(sZl + s * 16 * LDK + u.c0, LDK);
+        const bf16x8 qc = frag32_tr(sQ + s * 16 * LDK + u.c0, LDK);
+        const bf16x8 zc = frag32_tr(sZh + s * 16 * LDK + u.c0, LDK);
+        const bf16x8 zcl = frag32_tr(sZl + s * 16 * LDK + u.c0, LDK);
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
           const int rt = sw + NSW * j;
           if (rt < NRT) {
-            const bf16x8 qr = frag_cm(sQ + s * 16 * LDK + rt * 32, LDK);   // (r, t) = q_t[rt*32 + r]
-            const bf16x8 zr = frag_cm(sZh + s * 16 * LDK + rt * 32, LDK);  // (r, t) = dz_t[rt*32 + r]
-            const bf16x8 zrl = frag_cm(sZl + s * 16 * LDK + rt * 32, LDK);
+            const bf16x8 qr = frag32_tr(sQ + s * 16 * LDK + rt * 32, LDK);   // (r, t) = q_t[rt*32 + r]
+            const bf16x8 zr = frag32_tr(sZh + s * 16 * LDK + rt * 32, LDK);  // (r, t) = dz_t[rt*32 + r]
+            const bf16x8 zrl = frag32_tr(sZl + s * 16 * LDK + rt * 32, LDK);
             if (DH0 && first) {
               G[j] = mfma(qr, zc, G[j]);
               G[j] = mfma(qr, zcl, G[j]);

@@ -2022,8 +2022,8 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_v2_kernel(const GdnArgs
 #pragma unroll
     for (int k0 = 0; k0 < BT; k0 += 16) {
       const bf16x8 kb = frag_rm(sKt + tc * LDB + k0, LDB);
-      dQi = mfma(frag_cm(sPh + k0 * LDB + tr, LDB), kb, dQi);
-      dQi = mfma(frag_cm(sPl + k0 * LDB + tr, LDB), kb, dQi);
+      dQi = mfma(frag32_tr(sPh + k0 * LDB + tr, LDB), kb, dQi);
+      dQi = mfma(frag32_tr(sPl + k0 * LDB + tr, LDB), kb, dQi);
     }
     const int r0 = tr + acc_row(0);
     float* dq = a.dq32 + (tok0 + r0) * rsk + (long)h * K + k0c + c;
@@ -2321,8 +2321,8 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v3_kernel(const GdnArgs a
 #pragma unroll
     for (int k0 = 0; k0 < BT; k0 += 16) {
       const bf16x8 kb = frag_rm(sKt + tc * LDB + k0, LDB);
-      dQi = mfma(frag_cm(sPh + k0 * LDB + tr, LDB), kb, dQi);
-      dQi = mfma(frag_cm(sPl + k0 * LDB + tr, LDB), kb, dQi);
+      dQi = mfma(frag32_tr(sPh + k0 * LDB + tr, LDB), kb, dQi);
+      dQi = mfma(frag32_tr(sPl + k0 * LDB + tr, LDB), kb, dQi);
     }
     const int r0 = tr + acc_row(0);
     float* dq = a.dq32 + (tok0 + r0) * rsk + (long)h * K + k0c + c;

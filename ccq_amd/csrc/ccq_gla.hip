@@ -577,10 +577,10 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dqk_kernel(const GlaArgs a) 
     for (int k0 = 0; k0 < 64; k0 += 16) {
       const bf16x8 oa = frag_rm(sO + tr * 32 * LDH + k0, LDH);
       const bf16x8 va = frag_rm(sV + tr * 32 * LDH + k0, LDH);
-      dqr = mfma(oa, frag_cm(sSh + k0 * LDH + tc * 32, LDH), dqr);
-      dqr = mfma(oa, frag_cm(sSl + k0 * LDH + tc * 32, LDH), dqr);
-      dkr = mfma(va, frag_cm(sDh + k0 * LDH + tc * 32, LDH), dkr);
-      dkr = mfma(va, frag_cm(sDl + k0 * LDH + tc * 32, LDH), dkr);
+      dqr = mfma(oa, frag32_tr(sSh + k0 * LDH + tc * 32, LDH), dqr);
+      dqr = mfma(oa, frag32_tr(sSl + k0 * LDH + tc * 32, LDH), dqr);
+      dkr = mfma(va, frag32_tr(sDh + k0 * LDH + tc * 32, LDH), dkr);
+      dkr = mfma(va, frag32_tr(sDl + k0 * LDH + tc * 32, LDH), dkr);
       if (w < 3) dA = mfma(frag_rm(sO + I * 32 * LDH + k0, LDH), frag_rm(sV + J * 32 * LDH + k0, LDH), dA);
     }
     __syncthreads();
