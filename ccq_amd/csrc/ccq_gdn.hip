@@ -145,11 +145,7 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(const GdnArgs a, con
   stage_bf16<K>(sK, LDK, sKT, LDB, (const bf16*)a.k + (tok0 * a.H + h) * K, rsk, BT, L);
   if (w == 0) {
     float x = (l < L && a.g) ? a.g[(tok0 + l) * a.H + h] : 0.f;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(x, off);
-      if (l >= off) x += y;
-    }
+    x = wave_scan_incl(x);
     sG[l] = x;
     sBeta[l] = (l < L) ? a.beta[(tok0 + l) * a.H + h] : 0.f;
     sGam[l] = __expf(x);
@@ -354,11 +350,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_prep_v3_kernel(const GdnArgs a) {
       pv.store(sV, PV, L, lm);
       if (w == 4) {
         float x = l < L ? pg : 0.f;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const float y = __shfl_up(x, off);
-          if (l >= off) x += y;
-        }
+        x = wave_scan_incl(x);
         const float b = l < L ? pb : 0.f;
         sG[l] = x;
         sBeta[l] = b;
@@ -2711,11 +2703,7 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_v2_kernel(const GdnArgs a
     const int ll = lane_id();
     const int r = BT - 1 - ll;  // reverse order
     float x = (r < L) ? sDG[r] : 0.f;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(x, off);
-      if (ll >= off) x += y;
-    }
+    x = wave_scan_incl(x);
     if (r < L) {
       a.dg[(tok0 + r) * a.H + h] = x;
       a.dbeta[(tok0 + r) * a.H + h] = sDB[r];
@@ -2741,9 +2729,11 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_wy_v2_kernel(const GdnArgs a
 //   P5  dv^T tiles: (T^T dU)^T; dv rows as 8-byte pieces; dbeta terms of u  (the next unit's dw
 //       and k are staged meanwhile)
 // Barriers per unit: B0 (staged), B1 (dT), B2 (M1^T), B3 (dAs), B4 (dw, k free), B5 (all free).
-// The memory waves issue the next unit's loads in three groups (after B0: dw, k; after B2: dU;
-// after B3: v, T and the per-token values), each ahead of a long compute phase, so issuing them
-// (which stalls while the memory system is busy) does not hold a barrier.  Loops keep several independent accumulators and load the next step's fragments before
+// The memory waves issue the next unit's loads in two groups (after B0: dw, k; after B2: dU, v, T
+// and the per-token values), each ahead of a long compute phase, so issuing them (which stalls
+// while the memory system is busy) does not hold a barrier, and each lands well before its staging.
+// The compute waves run the key part of P1 (k and dw are staged before B5) ahead of B0, while the
+// memory waves stage the value side.  Loops keep several independent accumulators and load the next step's fragments before
 // the current step's MFMAs.  Per-row partial sums go to per-wave LDS slots and are added in a fixed
 // order (deterministic).
 // ===========================================================================
@@ -2851,9 +2841,11 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
       if (more) load_a();
       __syncthreads();  // B1
       __syncthreads();  // B2
-      if (more) load_b();
+      if (more) {
+        load_b();
+        load_c();
+      }
       __syncthreads();  // B3
-      if (more) load_c();
       __syncthreads();  // B4
       if (more) stage_a();
       __syncthreads();  // B5
@@ -2871,50 +2863,65 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
   const int rr = tr * 32 + acc_col();          // the lane's row in dk^T / dv^T tiles
   const int q4 = 4 * (l >> 5);                 // first row of the lane's 4-row groups in a C tile
   int par = 0;
+  bool first = true;
   for (int u = valid_from(blockIdx.x); u < nunits; u = valid_from(u + gridDim.x), par ^= 1) {
     const int gc = u / a.H, h = u % a.H;
     int n, c0, L;
     long bos;
     chunk_info(a, gc, n, c0, bos, L);
     const long tok0 = bos + c0;
-    __syncthreads();  // B0: the unit's operands are in LDS
-    sPB[w * BT + l] = 0.f;
-    sPG[w * BT + l] = 0.f;
-
-    // ---- P1: dT^T (rows c, cols r) = K_c dw_r^T gamma_c + V_c dU_r^T; K K^T both ways
-    f32x16 kk = zero16(), kkT = zero16();
-    if (w < 3) {
-      constexpr int NS = (K > V ? K : V) / 16;
-      f32x16 dTkh = zero16(), dTkl = zero16(), dTvh = zero16(), dTvl = zero16();
-      bf16x8 fa[2][7];
-      auto ld = [&](int s, bf16x8* f) {
-        if (s < K / 16) {
+    // ---- P1, key part: K_c dw_r^T and K K^T both ways.  k and dw of a unit are staged before the
+    // previous unit's B5, so this runs ahead of B0 (which waits for the value-side staging); the
+    // first unit's operands are all staged before its B0.
+    f32x16 kk = zero16(), kkT = zero16(), dTkh = zero16(), dTkl = zero16();
+    auto p1_key = [&]() {
+      if (w < 3) {
+        bf16x8 fa[2][4];
+        auto ld = [&](int s, bf16x8* f) {
           f[0] = frag_rm(sK + C * 32 * PK + 16 * s, PK);
           f[1] = frag_rm(sK + R * 32 * PK + 16 * s, PK);
           f[2] = frag_rm(sWh + R * 32 * PK + 16 * s, PK);
           f[3] = frag_rm(sWl + R * 32 * PK + 16 * s, PK);
-        }
-        if (s < V / 16) {
-          f[4] = frag_rm(sV + C * 32 * PV + 16 * s, PV);
-          f[5] = frag_rm(sUh + R * 32 * PV + 16 * s, PV);
-          f[6] = frag_rm(sUl + R * 32 * PV + 16 * s, PV);
-        }
-      };
-      ld(0, fa[0]);
+        };
+        ld(0, fa[0]);
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        if (s + 1 < NS) ld(s + 1, fa[(s + 1) & 1]);
-        const bf16x8* f = fa[s & 1];
-        if (s < K / 16) {
+        for (int s = 0; s < K / 16; ++s) {
+          if (s + 1 < K / 16) ld(s + 1, fa[(s + 1) & 1]);
+          const bf16x8* f = fa[s & 1];
           dTkh = mfma(f[0], f[2], dTkh);
           kkT = mfma(f[0], f[1], kkT);
           dTkl = mfma(f[0], f[3], dTkl);
           kk = mfma(f[1], f[0], kk);
         }
-        if (s < V / 16) {
-          dTvh = mfma(f[4], f[5], dTvh);
-          dTvl = mfma(f[4], f[6], dTvl);
-        }
+      }
+    };
+    if (first) {
+      __syncthreads();  // B0: the unit's operands are in LDS
+      p1_key();
+    } else {
+      p1_key();
+      __syncthreads();  // B0: the value-side operands are in LDS
+    }
+    first = false;
+    sPB[w * BT + l] = 0.f;
+    sPG[w * BT + l] = 0.f;
+
+    // ---- P1, value part: dT^T (rows c, cols r) = K_c dw_r^T gamma_c + V_c dU_r^T
+    if (w < 3) {
+      f32x16 dTvh = zero16(), dTvl = zero16();
+      bf16x8 fa[2][3];
+      auto ld = [&](int s, bf16x8* f) {
+        f[0] = frag_rm(sV + C * 32 * PV + 16 * s, PV);
+        f[1] = frag_rm(sUh + R * 32 * PV + 16 * s, PV);
+        f[2] = frag_rm(sUl + R * 32 * PV + 16 * s, PV);
+      };
+      ld(0, fa[0]);
+#pragma unroll
+      for (int s = 0; s < V / 16; ++s) {
+        if (s + 1 < V / 16) ld(s + 1, fa[(s + 1) & 1]);
+        const bf16x8* f = fa[s & 1];
+        dTvh = mfma(f[0], f[1], dTvh);
+        dTvl = mfma(f[0], f[2], dTvl);
       }
       f32x16 d;
       const int r = R * 32 + acc_col();
@@ -3181,11 +3188,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
         x += sPG[q * BT + r];
       }
       if (r >= L) x = 0.f;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(x, off);
-        if (l >= off) x += y;
-      }
+      x = wave_scan_incl(x);
       if (r < L) {
         a.dg[(tok0 + r) * a.H + h] = x;
         a.dbeta[(tok0 + r) * a.H + h] = db;

@@ -808,6 +808,26 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// DPP move with a row mask: rows outside RM (bit r = lanes 16 r .. 16 r + 15) receive 0.
+template <int C, int RM>
+__device__ __forceinline__ float dppf_rows(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), C, RM, 0xf, false));
+}
+
+// Inclusive prefix sum over the 64 lanes (lane l receives x_0 + ... + x_l): row_shr 1, 2, 4, 8 within
+// each row of 16 lanes (lanes shifted in from outside the row read 0), then row_bcast:15 adds the
+// last lane of rows 0 and 2 to rows 1 and 3, and row_bcast:31 adds lane 31 to rows 2 and 3.  Every
+// lane must be active.
+__device__ __forceinline__ float wave_scan_incl(float x) {
+  x += dppf<0x111>(x);
+  x += dppf<0x112>(x);
+  x += dppf<0x114>(x);
+  x += dppf<0x118>(x);
+  x += dppf_rows<0x142, 0xA>(x);
+  x += dppf_rows<0x143, 0xC>(x);
+  return x;
+}
+
 // Value of lane `src` (a constant) of x, for every lane (v_readlane).
 __device__ __forceinline__ float lane_value(float x, int src) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), src));
