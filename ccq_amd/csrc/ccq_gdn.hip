@@ -1544,9 +1544,9 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
 // gdn_bwd_state for K <= 128 with 8 wavefronts (reverse walk over chunks).  Waves 0-3 compute and
 // load nothing inside the walk; waves 4-7 move memory.  Per chunk c (dS' = gradient of the state
 // after chunk c):
-//   phase A  compute: dU = P^T dO + fac (K dS') (16x16 tiles), dU rows to HBM, -dU^T (hi/lo) to LDS
-//            memory:  Qc, scale gamma dO (hi/lo), w, wl of c to LDS (row-major); loads of Qc, w, wl
-//                     of c-1; dS' snapshot to HBM
+//   phase A  compute: dU = P^T dO + fac (K dS') (16x16 tiles), dU rows to HBM, -dU^T (hi/lo) to LDS;
+//                     then the dS' snapshot to HBM and scale gamma dO (hi/lo) to LDS
+//            memory:  Qc, w, wl of c to LDS (row-major); loads of Qc, w, wl of c-1
 //   phase B  compute: dS <- gamma_L dS' + Qc^T (scale gamma dO) - w^T dU (Qc^T, w^T and the dO
 //                     operand by transposing LDS reads), dS^T (hi/lo) to LDS for chunk c-1
 //            memory:  P^T, dO, k, fac of c-1 to LDS; loads of P^T, dO, k, g of c-2
@@ -1633,26 +1633,12 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
         if (l == 0) sGL[0] = __expf(pgl);
       }
     };
-    // phase-B tiles of chunk c: Qc (hi/lo), w, wl; scale gamma dO (hi/lo) from the dO tile of c,
-    // which the compute waves only read during this phase
+    // phase-B tiles of chunk c: Qc (hi/lo), w, wl
     auto stage_b = [&](int c) {
       const int L = chunk_len(c);
       pq.store_split(sQh, sQl, LDK, L, lm);
       pw.store(sW, LDK, L, lm);
       pwl.store(sWl, LDK, L, lm);
-      const int r = lm / (VB / 8), cc = (lm % (VB / 8)) * 8;
-      const float sc = sGam[r];
-      const bf16x8 o = *(const bf16x8*)(sdO + r * LDO + cc);
-      bf16x8 vh, vl;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        bf16 x, y;
-        split2(sc * (float)o[i], x, y);
-        vh[i] = x;
-        vl[i] = y;
-      }
-      *(bf16x8*)(sgOh + r * LDO + cc) = vh;
-      *(bf16x8*)(sgOl + r * LDO + cc) = vl;
     };
     // Loads run one chunk ahead of their stage and are unconditional (chunk 0 again past the
     // start), so every pass issues the same memory operations.
@@ -1665,20 +1651,9 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
     }
     __syncthreads();
     for (int c = cl; c >= 0; --c) {
-      const int gc = gc0 + c;
-      // ---- phase A: phase-B tiles of c; loads of Qc, w, wl of c-1; dS' snapshot
+      // ---- phase A: phase-B tiles of c; loads of Qc, w, wl of c-1
       stage_b(c);
       load_b(max(c - 1, 0));
-      constexpr int VPR = K / 8;
-#pragma unroll
-      for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
-        const int idx = lm + j * NM;
-        const int which = idx / (VB * VPR), e = idx % (VB * VPR);
-        const int r = e / VPR, cc = (e % VPR) * 8;
-        const bf16* src = which ? sdSl : sdSh;
-        bf16* dst = which ? (bf16*)a.dhTl : (bf16*)a.dhT;
-        *gmem((bf16x8*)(dst + (((long)gc * a.H + h) * V + v0 + r) * K + cc)) = *(const bf16x8*)(src + r * LDK + cc);
-      }
       __syncthreads();
       // ---- phase B: phase-A tiles of c-1; loads of P^T, dO, k, g of c-2
       stage_a(max(c - 1, 0));
@@ -1748,6 +1723,34 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
       for (int i = 0; i < 4; ++i)
         if (rb + i < L) dug[i * rsv] = du[i];
       acc16_to_lds_t(ndu, sdUh + 16 * ct * LDP, sdUl + 16 * ct * LDP, LDP, 16 * w);
+    }
+    // with the products done: the dS' snapshot (hi/lo [v][k] rows, 16-byte pieces) to HBM, and scale
+    // gamma dO (hi/lo) of chunk c for phase B (the memory waves are the longer path in this phase)
+    {
+      constexpr int VPR = K / 8;
+      const int gc = gc0 + c;
+#pragma unroll
+      for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
+        const int idx = tid + j * NM;
+        const int which = idx / (VB * VPR), e = idx % (VB * VPR);
+        const int r = e / VPR, cc = (e % VPR) * 8;
+        const bf16* src = which ? sdSl : sdSh;
+        bf16* dst = which ? (bf16*)a.dhTl : (bf16*)a.dhT;
+        *gmem((bf16x8*)(dst + (((long)gc * a.H + h) * V + v0 + r) * K + cc)) = *(const bf16x8*)(src + r * LDK + cc);
+      }
+      const int r = tid / (VB / 8), cc = (tid % (VB / 8)) * 8;
+      const float sc = sGam[r];
+      const bf16x8 o = *(const bf16x8*)(sdO + r * LDO + cc);
+      bf16x8 vh, vl;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        bf16 x, y;
+        split2(sc * (float)o[i], x, y);
+        vh[i] = x;
+        vl[i] = y;
+      }
+      *(bf16x8*)(sgOh + r * LDO + cc) = vh;
+      *(bf16x8*)(sgOl + r * LDO + cc) = vl;
     }
     __syncthreads();
 
