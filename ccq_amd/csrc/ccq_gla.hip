@@ -536,9 +536,11 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dv_kernel(const GlaArgs a) {
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void gla_bwd_dqk_kernel(const GlaArgs a) {
-  // loop phase: dO, V [64][LDH] bf16 and S, dS pieces [v][c] hi/lo; post phase: q, k, b, dA, dG
+  // loop phase: dO, V [64][LDH] bf16 and S, dS pieces [v][c] hi/lo; post phase: q (then dG in its
+  // place: each element of dG is written by the one thread that last reads that element of q), k,
+  // b, dA.  Under 80 KiB, so two workgroups share a CU.
   constexpr long kLoop = 6L * 64 * LDH * 2;
-  constexpr long kPost = 4L * BT * LDF * 4 + (long)BT * (BT + 1) * 4;
+  constexpr long kPost = 3L * BT * LDF * 4 + (long)BT * (BT + 1) * 4;
   __shared__ __attribute__((aligned(16))) char smem[kLoop > kPost ? kLoop : kPost];
   __shared__ float sPart[4 * KS];
   __shared__ float sTerm[KS];
@@ -551,8 +553,8 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dqk_kernel(const GlaArgs a) 
   float* sQ = (float*)smem;
   float* sK = sQ + BT * LDF;
   float* sBb = sK + BT * LDF;
-  float* sG = sBb + BT * LDF;
-  float* sdA = sG + BT * LDF;
+  float* sG = sQ;
+  float* sdA = sBb + BT * LDF;
 
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
   const int gc = blockIdx.x, h = blockIdx.y, s0 = blockIdx.z * KS;
