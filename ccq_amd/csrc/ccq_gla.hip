@@ -255,13 +255,15 @@ __global__ __launch_bounds__(kThreads) void gla_intra_kernel(const GlaArgs a) {
 //   DIR 1: dS_prev = diag(e^{b_L}) dS + (scale Q o e^b)^T dO, walking backwards, snapshots of dS
 //          (the gradient of the state after each chunk).
 // Every state element evolves independently (diagonal decay), so tiles never exchange data.
+// Lane l holds token l of the chunk; it writes its rows of the operands as 16-byte pieces
+// ([token][column], row-major) and the MFMAs read them with transposing LDS reads.
 // ===========================================================================
 template <int DIR>
 __global__ __launch_bounds__(64) void gla_state_kernel(const GlaArgs a) {
-  constexpr int LDT = BT + 8;
-  __shared__ __attribute__((aligned(16))) bf16 sXh[32 * LDT];  // A operand [channel][token], hi
-  __shared__ __attribute__((aligned(16))) bf16 sXl[32 * LDT];  // lo
-  __shared__ __attribute__((aligned(16))) bf16 sY[32 * LDT];   // B operand [value col][token]
+  constexpr int LDR = 32 + 8;  // bank-conflict-free 16-byte row writes, 8-byte aligned transposing reads
+  __shared__ __attribute__((aligned(16))) bf16 sXh[BT * LDR];  // A operand rows [token][channel], hi
+  __shared__ __attribute__((aligned(16))) bf16 sXl[BT * LDR];  // lo
+  __shared__ __attribute__((aligned(16))) bf16 sY[BT * LDR];   // B operand rows [token][value col]
   __shared__ float sBL[32];
 
   const int l = threadIdx.x;
@@ -345,17 +347,23 @@ __global__ __launch_bounds__(64) void gla_state_kernel(const GlaArgs a) {
     __syncthreads();
     const bool xf32 = DIR == 1 && a.q32 != nullptr;
 #pragma unroll
-    for (int cc = 0; cc < 32; ++cc) {
-      const float bt = pb[cc >> 2][cc & 3];
-      const float xv = xf32 ? pq[cc >> 2][cc & 3] : (float)px[cc >> 3][cc & 7];
-      const float val = DIR == 0 ? xv * __expf(sBL[cc] - bt) : a.scale * xv * __expf(bt);
-      bf16 hh, ll;
-      split2(val, hh, ll);
-      sXh[cc * LDT + l] = hh;
-      sXl[cc * LDT + l] = ll;
-    }
+    for (int j = 0; j < 4; ++j) {
+      bf16x8 xh, xl;
 #pragma unroll
-    for (int vv = 0; vv < 32; ++vv) sY[vv * LDT + l] = py[vv >> 3][vv & 7];
+      for (int i = 0; i < 8; ++i) {
+        const int cc = 8 * j + i;
+        const float bt = pb[cc >> 2][cc & 3];
+        const float xv = xf32 ? pq[cc >> 2][cc & 3] : (float)px[j][i];
+        const float val = DIR == 0 ? xv * __expf(sBL[cc] - bt) : a.scale * xv * __expf(bt);
+        bf16 hh, ll;
+        split2(val, hh, ll);
+        xh[i] = hh;
+        xl[i] = ll;
+      }
+      *(bf16x8*)(sXh + l * LDR + 8 * j) = xh;
+      *(bf16x8*)(sXl + l * LDR + 8 * j) = xl;
+      *(bf16x8*)(sY + l * LDR + 8 * j) = py[j];
+    }
     float dec[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) dec[i] = __expf(sBL[acc_row(i)]);
@@ -386,9 +394,9 @@ __global__ __launch_bounds__(64) void gla_state_kernel(const GlaArgs a) {
     for (int i = 0; i < 16; ++i) S[i] *= dec[i];
 #pragma unroll
     for (int k0 = 0; k0 < BT; k0 += 16) {
-      const bf16x8 ah = frag_rm(sXh + k0, LDT);
-      const bf16x8 al = frag_rm(sXl + k0, LDT);
-      const bf16x8 b = frag_rm(sY + k0, LDT);
+      const bf16x8 ah = frag32_tr(sXh + k0 * LDR, LDR);
+      const bf16x8 al = frag32_tr(sXl + k0 * LDR, LDR);
+      const bf16x8 b = frag32_tr(sY + k0 * LDR, LDR);
       S = mfma(ah, b, S);
       S = mfma(al, b, S);
     }
