@@ -638,15 +638,15 @@ __global__ __launch_bounds__(kWalk8) void gdn_prep_v3_kernel(const GdnArgs a) {
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a, const int V) {
-  constexpr int VB = 32, LDK = K + 8, LDKR = K + 16, LDU = BT + 1, LDV = VB + 4, NRT = K / 32, TPW = (NRT + 3) / 4;
+  constexpr int VB = 32, LDK = K + 8, LDKR = K + 16, LDU = BT + 4, LDV = VB + 4, NRT = K / 32, TPW = (NRT + 3) / 4;
   __shared__ __attribute__((aligned(16))) bf16 sW[BT * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sWl[BT * LDK];
   // k rows [t][k] (row-major: whole 16-byte writes; the state update reads K^T by transposing reads)
   __shared__ __attribute__((aligned(16))) bf16 sK[BT * LDKR];
   __shared__ __attribute__((aligned(16))) bf16 sST[VB * LDK];
   __shared__ __attribute__((aligned(16))) bf16 sSTl[VB * LDK];
-  __shared__ float sU[BT * LDV];
-  __shared__ float sUsT[VB * LDU];
+  __shared__ __attribute__((aligned(16))) float sU[BT * LDV];
+  __shared__ __attribute__((aligned(16))) float sUsT[VB * LDU];  // (fac U)^T, rows read as 16-byte pieces
   __shared__ float sFac[BT];
   __shared__ float sGL[1];
 
