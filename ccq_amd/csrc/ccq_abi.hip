@@ -104,9 +104,12 @@ hipError_t timed(const char* name, hipStream_t st, F&& launch) {
     std::lock_guard<std::mutex> g(t.mu);
     if (!t.on) return launch();
   }
+  // timing-only events: no system-scope fence on record (that fence writes back and invalidates
+  // the caches between every two timed kernels and shows up as idle time before each of them)
+  constexpr unsigned kFlags = hipEventDisableSystemFence;
   hipEvent_t a, b;
-  if (hipEventCreate(&a) != hipSuccess) return launch();
-  if (hipEventCreate(&b) != hipSuccess) {
+  if (hipEventCreateWithFlags(&a, kFlags) != hipSuccess) return launch();
+  if (hipEventCreateWithFlags(&b, kFlags) != hipSuccess) {
     (void)hipEventDestroy(a);
     return launch();
   }
