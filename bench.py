@@ -383,6 +383,77 @@ def run_layer(args, dev, which):
                  {"workload": f"{which.upper()} single layer fwd+bwd", "B": b, "T": t})
 
 
+def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_steps=256):
+    """C4: a random-init 24-layer CCQ-GDN stack (RMSNorm -> CCQGDN -> residual, RMSNorm -> gated MLP
+    -> residual; token embedding, final norm, LM head; bf16) over B x T uniform-random token ids:
+    chunked prefill with the recurrent cache, then greedy decode steps carrying (S, C, m, position)
+    and the short-convolution states.  The blocks around the layer are the measurement harness
+    (the reference takes them from its HF model classes, which this library does not provide); the
+    layers run their own mode switch (`chunk` for the prompt, `fused_recurrent` for one token).
+    The decode steps are eager (one launch per op, host-side positions), so their latency includes
+    the launches; the decode kernels' own step time and HBM rate are the `decode` workload's."""
+    import torch.nn as nn
+    import torch.nn.functional as F
+    from ccq_amd.layers import CCQGDN, LayerCache, RMSNorm
+
+    inter = 256 * ((int(d * 4 * 2 / 3) + 255) // 256)  # fla GatedMLP's intermediate size (hidden_ratio 4)
+
+    class Block(nn.Module):
+        def __init__(self, i):
+            super().__init__()
+            self.attn_norm = RMSNorm(d)
+            self.attn = CCQGDN(hidden_size=d, head_dim=256, num_heads=4, expand_v=2, mode="chunk", layer_idx=i)
+            self.mlp_norm = RMSNorm(d)
+            self.gate_up = nn.Linear(d, 2 * inter, bias=False)
+            self.down = nn.Linear(inter, d, bias=False)
+
+        def forward(self, x, cache):
+            x = x + self.attn(self.attn_norm(x), past_key_values=cache, use_cache=True)[0]
+            gt, up = self.gate_up(self.mlp_norm(x)).chunk(2, -1)
+            return x + self.down(F.silu(gt) * up)
+
+    torch.manual_seed(0)
+    embed = nn.Embedding(vocab, d).to(dev, torch.bfloat16)
+    blocks = nn.ModuleList(Block(i) for i in range(layers)).to(dev, torch.bfloat16).eval()
+    norm = RMSNorm(d).to(dev, torch.bfloat16)
+    head = nn.Linear(d, vocab, bias=False).to(dev, torch.bfloat16)
+    gen = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, vocab, (b, t), generator=gen).to(dev)
+
+    def forward(ids, cache):
+        x = embed(ids)
+        for blk in blocks:
+            x = blk(x, cache)
+        return head(norm(x[:, -1]))  # logits of the last position only
+
+    with torch.no_grad():
+        forward(prompt, LayerCache())  # warm-up at full size (kernel loads, the allocator's pools)
+        torch.cuda.synchronize()
+        cache = LayerCache()
+        t0 = time.perf_counter()
+        logits = forward(prompt, cache)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        nxt = logits.argmax(-1)
+        warm = min(3, decode_steps)
+        for _ in range(warm):
+            nxt = forward(nxt[:, None], cache).argmax(-1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(decode_steps - warm):
+            nxt = forward(nxt[:, None], cache).argmax(-1)
+        torch.cuda.synchronize()
+        t_decode = (time.perf_counter() - t0) / max(decode_steps - warm, 1)
+    assert cache.get_seq_length() == t + decode_steps
+    return _line("C4 whole-model prefill tokens/s (24 CCQ-GDN layers, d_model1024, H4, d_k256, d_v512, B16, "
+                 "T16384) + greedy decode", b * t / t_prefill, "tokens/s", args, t_prefill * 1e3, "bf16",
+                 "synthetic (uniform-random token ids; random-init weights)",
+                 {"workload": "C4: chunked prefill with the recurrent cache, then greedy recurrent decode",
+                  "layers": layers, "B": b, "T": t, "d_model": d, "vocab": vocab, "mlp_intermediate": inter,
+                  "prefill_s": t_prefill, "decode_steps": decode_steps,
+                  "decode_ms_per_step_eager": t_decode * 1e3})
+
+
 def ingest_pmc(fetch_dir, write_dir, out_path):
     """Per-launch HBM bytes of each timed stage from two rocprofv3 --pmc runs of this script with
     --copy-calibration (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by the counter's
@@ -429,9 +500,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=("c1", "decode", "readme", "c2", "c3"), default="c1",
+    ap.add_argument("--workload", choices=("c1", "decode", "readme", "c2", "c3", "c4"), default="c1",
                     help="c1: the metric (default); decode: C4's captured decode step; readme: the reference "
-                         "README's cleaning-overhead shape; c2 / c3: single-layer fwd+bwd")
+                         "README's cleaning-overhead shape; c2 / c3: single-layer fwd+bwd; c4: the 24-layer "
+                         "model's prefill and greedy decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed steps, run one elementwise copy of 512 MiB (read) + 512 MiB (write), "
@@ -453,6 +525,8 @@ def main():
         out = run_decode(args, dev)
     elif args.workload == "readme":
         out = run_readme(args, dev)
+    elif args.workload == "c4":
+        out = run_c4(args, dev)
     else:
         out = run_layer(args, dev, args.workload)
     print(json.dumps(out), flush=True)
