@@ -383,20 +383,30 @@ def run_layer(args, dev, which):
                  {"workload": f"{which.upper()} single layer fwd+bwd", "B": b, "T": t})
 
 
-def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_steps=256):
+def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_steps=256, check_steps=4):
     """C4: a random-init 24-layer CCQ-GDN stack (RMSNorm -> CCQGDN -> residual, RMSNorm -> gated MLP
     -> residual; token embedding, final norm, LM head; bf16) over B x T uniform-random token ids:
     chunked prefill with the recurrent cache, then greedy decode steps carrying (S, C, m, position)
     and the short-convolution states.  The blocks around the layer are the measurement harness
-    (the reference takes them from its HF model classes, which this library does not provide); the
-    layers run their own mode switch (`chunk` for the prompt, `fused_recurrent` for one token).
-    The decode steps are eager (one launch per op, host-side positions), so their latency includes
-    the launches; the decode kernels' own step time and HBM rate are the `decode` workload's."""
+    (the reference takes them from its HF model classes, which this library does not provide).
+
+    Decode runs two ways from the same prefill state: eager (the layers' own recurrent mode, one
+    launch per op from Python) and as one captured HIP graph of the whole model's step, in which
+    each layer's token step is the layer's own projections, fused prologue and output norm around
+    the library's in-place decode step (``DecodeStep``: states updated in place, position held on
+    the device) and the greedy token is written back into the graph's input.  The graph is
+    replayed on the eager path's first tokens and each replay's logits are checked against the
+    eager layers' before it is timed."""
     import torch.nn as nn
     import torch.nn.functional as F
-    from ccq_amd.layers import CCQGDN, LayerCache, RMSNorm
+    from ccq_amd.graph import DecodeStep
+    from ccq_amd.layers import CCQGDN, LayerCache, _heads
 
     inter = 256 * ((int(d * 4 * 2 / 3) + 255) // 256)  # fla GatedMLP's intermediate size (hidden_ratio 4)
+
+    # block norms: torch's RMSNorm (x rsqrt(mean(x^2) + eps) w, as fla's), one fused op per call
+    def RMSNorm(n):
+        return nn.RMSNorm(n, eps=1e-5)
 
     class Block(nn.Module):
         def __init__(self, i):
@@ -407,10 +417,12 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
             self.gate_up = nn.Linear(d, 2 * inter, bias=False)
             self.down = nn.Linear(inter, d, bias=False)
 
-        def forward(self, x, cache):
-            x = x + self.attn(self.attn_norm(x), past_key_values=cache, use_cache=True)[0]
+        def mlp(self, x):
             gt, up = self.gate_up(self.mlp_norm(x)).chunk(2, -1)
             return x + self.down(F.silu(gt) * up)
+
+        def forward(self, x, cache):
+            return self.mlp(x + self.attn(self.attn_norm(x), past_key_values=cache, use_cache=True)[0])
 
     torch.manual_seed(0)
     embed = nn.Embedding(vocab, d).to(dev, torch.bfloat16)
@@ -426,6 +438,64 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
             x = blk(x, cache)
         return head(norm(x[:, -1]))  # logits of the last position only
 
+    def snapshot(cache):
+        out = []
+        for st in cache.states:
+            S, C, m, pos = st["recurrent_state"]
+            out.append(((S.clone(), C.clone(), m.clone(), pos), tuple(c.clone() for c in st["conv_state"])))
+        return out
+
+    # the captured step: static token ids, per-layer DecodeStep buffers and conv states
+    ids = torch.zeros(b, 1, dtype=torch.long, device=dev)
+    A0 = blocks[0].attn
+    steps = [DecodeStep(b, A0.num_heads, A0.head_k_dim, A0.head_v_dim, mode="gdn", gate=False,
+                        subtract_mean=blk.attn.subtract_mean, use_l2norm=False, device=dev) for blk in blocks]
+    convs = None
+
+    def load(snap):
+        nonlocal convs
+        for st, ((S, C, m, pos), _) in zip(steps, snap):
+            st.load_state(S, C, m, pos)
+        convs = [tuple(c.clone() for c in cs) for _, cs in snap] if convs is None else convs
+        for dst, (_, cs) in zip(convs, snap):
+            for a, c in zip(dst, cs):
+                a.copy_(c)
+
+    # the six input projections of a layer as one GEMM (the layers' own weights, concatenated once)
+    proj = [torch.cat([blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight,
+                       blk.attn.a_proj.weight, blk.attn.b_proj.weight, blk.attn.g_proj.weight]) for blk in blocks]
+    L0 = blocks[0].attn
+    splits = [L0.q_proj.out_features, L0.k_proj.out_features, L0.v_proj.out_features, L0.a_proj.out_features,
+              L0.b_proj.out_features, L0.g_proj.out_features]
+
+    def token_step(L, st, cs, wp, h):
+        """CCQGDN.forward for one token (recurrent mode, fused prologue) over in-place buffers."""
+        cq, ck, cv = cs
+        qx, kx, vx, ax, bx, gx = F.linear(h, wp).split(splits, -1)
+        q, qn, ncq = L.q_conv1d.forward_norm(qx, cq, True, None, L.head_k_dim)
+        _, kn, nck = L.k_conv1d.forward_norm(kx, ck, True, None, L.head_k_dim, want_y=False)
+        v, ncv = L.v_conv1d(vx, cv, True, None)
+        cq.copy_(ncq)
+        ck.copy_(nck)
+        cv.copy_(ncv)
+        st.lam.copy_(torch.sigmoid(L.erase_lambda_proj(q)))
+        st.g.copy_(-L.A_log.float().exp() * F.softplus(ax.float() + L.dt_bias))
+        st.beta.copy_(bx.sigmoid())
+        st.q.copy_(_heads(qn, L.head_k_dim))
+        st.k.copy_(_heads(kn, L.head_k_dim))
+        st.v.copy_(_heads(v, L.head_v_dim))
+        st.launch()
+        o = L.o_norm(st.o, _heads(gx, L.head_v_dim))
+        return L.o_proj(o.reshape(*o.shape[:-2], -1))
+
+    def graph_step():
+        x = embed(ids)
+        for blk, st, cs, wp in zip(blocks, steps, convs, proj):
+            x = blk.mlp(x + token_step(blk.attn, st, cs, wp, blk.attn_norm(x)))
+        logits = head(norm(x[:, -1]))
+        ids.copy_(logits.argmax(-1, keepdim=True))
+        return logits
+
     with torch.no_grad():
         forward(prompt, LayerCache())  # warm-up at full size (kernel loads, the allocator's pools)
         torch.cuda.synchronize()
@@ -434,24 +504,61 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
         logits = forward(prompt, cache)
         torch.cuda.synchronize()
         t_prefill = time.perf_counter() - t0
-        nxt = logits.argmax(-1)
+        tok0 = logits.argmax(-1)
+        snap = snapshot(cache)
+
+        # eager decode (the first check_steps tokens and logits are the captured graph's reference)
+        ref_in, ref_logits, nxt = [], [], tok0
         warm = min(3, decode_steps)
+        for i in range(decode_steps):
+            if i == warm:
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+            ref_in.append(nxt)
+            lg = forward(nxt[:, None], cache)
+            if i < check_steps:
+                ref_logits.append(lg.float())
+            nxt = lg.argmax(-1)
+        torch.cuda.synchronize()
+        t_eager = (time.perf_counter() - t0) / max(decode_steps - warm, 1)
+        assert cache.get_seq_length() == t + decode_steps
+
+        # captured decode: warm up the step eagerly (libraries pick their kernels), restore the
+        # prefill state, capture, then replay on the eager tokens and compare every replay
+        load(snap)
+        ids.copy_(tok0[:, None])
+        graph_step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits_g = graph_step()
+        load(snap)
+        errs = []
+        for i in range(check_steps):
+            ids.copy_(ref_in[i][:, None])
+            graph.replay()
+            torch.cuda.synchronize()
+            errs.append(((logits_g.float() - ref_logits[i]).norm() / ref_logits[i].norm()).item())
+        if max(errs) > 2e-2:
+            raise RuntimeError(f"captured decode step disagrees with the eager layers: rel-L2 {errs}")
+        load(snap)
+        ids.copy_(tok0[:, None])
         for _ in range(warm):
-            nxt = forward(nxt[:, None], cache).argmax(-1)
+            graph.replay()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(decode_steps - warm):
-            nxt = forward(nxt[:, None], cache).argmax(-1)
+            graph.replay()
         torch.cuda.synchronize()
-        t_decode = (time.perf_counter() - t0) / max(decode_steps - warm, 1)
-    assert cache.get_seq_length() == t + decode_steps
+        t_graph = (time.perf_counter() - t0) / max(decode_steps - warm, 1)
     return _line("C4 whole-model prefill tokens/s (24 CCQ-GDN layers, d_model1024, H4, d_k256, d_v512, B16, "
                  "T16384) + greedy decode", b * t / t_prefill, "tokens/s", args, t_prefill * 1e3, "bf16",
                  "synthetic (uniform-random token ids; random-init weights)",
                  {"workload": "C4: chunked prefill with the recurrent cache, then greedy recurrent decode",
                   "layers": layers, "B": b, "T": t, "d_model": d, "vocab": vocab, "mlp_intermediate": inter,
                   "prefill_s": t_prefill, "decode_steps": decode_steps,
-                  "decode_ms_per_step_eager": t_decode * 1e3})
+                  "decode_ms_per_step_graph": t_graph * 1e3, "decode_ms_per_step_eager": t_eager * 1e3,
+                  "graph_vs_eager_logits_rel_l2": errs})
 
 
 def ingest_pmc(fetch_dir, write_dir, out_path):

@@ -610,8 +610,12 @@ int ccq_conv_fwd(const void* x, const float* weight, const float* bias, const fl
   if (cache_out) {
     if (int s = hip_status(launch_conv(2, a, 1, st), "ccq_conv_fwd(cache)")) return s;
   }
+  // Tiles of 16 consecutive tokens (one window fill per tile) while that still gives >= 1024
+  // tiles; fewer tokens per tile below, down to one token per tile for a decode step, where every
+  // token starts its own sequence and a 16-token tile would walk 16 window fills in a row.
+  a.tb = (int)std::max<int64_t>(1, std::min<int64_t>(16, a.tokens / 1024));
   return hip_status(timed("conv_fwd", st, [&] {
-                      return launch_conv(0, a, (int)std::min<int64_t>(((int64_t)B * T + 15) / 16, 4096), st);
+                      return launch_conv(0, a, (int)std::min<int64_t>((a.tokens + a.tb - 1) / a.tb, 4096), st);
                     }),
                     "ccq_conv_fwd");
 }

@@ -34,6 +34,7 @@ struct ConvArgs {
   float* db_part;           // fp32 [blocks, D] (nullable)
   long tokens;
   int T, N, D, W, hd, act;
+  int tb;                   // fwd: tokens per tile (consecutive tokens one thread walks with a sliding window)
   float eps;
 };
 

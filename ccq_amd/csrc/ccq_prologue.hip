@@ -18,7 +18,7 @@ namespace ccq {
 
 namespace {
 
-constexpr int kConvTB = 16;     // tokens per tile of a thread
+constexpr int kConvTB = 16;     // tokens per tile of a thread (backward; the forward's is per launch)
 
 __device__ __forceinline__ float silu_(float a) { return a / (1.f + __expf(-a)); }
 __device__ __forceinline__ float dsilu_(float a) {
@@ -95,9 +95,9 @@ __global__ __launch_bounds__(kThreads) void conv_fwd_kernel(const ConvArgs a) {
     for (int w = 0; w < W; ++w) wt[i][w] = w < W ? a.w[(long)(cc + i) * W + w] : 0.f;
   }
   const int hl = a.hd / 8;  // lanes per head
-  const long ntiles = (a.tokens + kConvTB - 1) / kConvTB;
+  const long ntiles = (a.tokens + a.tb - 1) / a.tb;
   for (long tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const long p0 = tile * kConvTB, p1 = min(p0 + (long)kConvTB, a.tokens);
+    const long p0 = tile * a.tb, p1 = min(p0 + (long)a.tb, a.tokens);
     SeqOf sq = seq_of(a, p0);
     // window: inputs at positions p - (W-1) .. p - 1 of the current sequence
     float win[W][8];
