@@ -1804,7 +1804,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
 }
 
 // ===========================================================================
-// gdn_bwd_dqkw: grid (K/64, NTG, H)
+// gdn_bwd_dqkw: grid (K/64) * NTG * H, XCD-mapped (key-column block, chunk, head)
 //   dQi = dO h^T, dKs = U dS'^T, dw = -dU h^T, dP = dO U^T   (contractions over V)
 //   dq = scale gamma dQi + dPs K,  dk = fac dKs + dPs^T Qc,  dPs = dP o scale Gamma (causal)
 //   dG partials: decay terms of O, P and the state update
@@ -1840,7 +1840,11 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_v2_kernel(const GdnArgs
   float* sPT = sE + 64 * LDE;        // P^T [s][t] (kt == 0)
 
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
-  const int kt = blockIdx.x, gc = blockIdx.y, h = blockIdx.z;
+  // the K / 64 key-column blocks of a (chunk, head) unit share the unit's dO, U, dU and P^T: they
+  // run on one XCD (one L2) when the unit count allows it
+  int unit, kt;
+  xcd_map(blockIdx.x, K / 64, a.NTG * a.H, unit, kt);
+  const int gc = unit / a.H, h = unit % a.H;
   int n, c0, L;
   long bos;
   if (!chunk_info(a, gc, n, c0, bos, L)) return;
@@ -4185,7 +4189,7 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       } else if (K == 128)
         hipLaunchKernelGGL(gdn_bwd_dqkw_v3_kernel<128>, dim3(1, a.NTG, a.H), dim3(kWalk8), 0, st, a, V);
       else
-        hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3(K / 64, a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+        hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3((K / 64) * a.NTG * a.H), dim3(kThreads), 0, st, a, V);
       break;
     case kGdnBwdWy:
       if (K <= 128 && (V == 64 || V == 128)) {

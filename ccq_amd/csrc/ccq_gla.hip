@@ -410,7 +410,7 @@ __global__ __launch_bounds__(64) void gla_state_kernel(const GlaArgs a) {
 }
 
 // ===========================================================================
-// gla_fwd_o: grid (NTG, H, V/64).  O[:, tile] = scale (Q o e^b) S[:, tile] + A V[:, tile]
+// gla_fwd_o: grid NTG * H * (V/64), XCD-mapped.  O[:, tile] = scale (Q o e^b) S[:, tile] + A V[:, tile]
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void gla_fwd_o_kernel(const GlaArgs a) {
@@ -422,7 +422,10 @@ __global__ __launch_bounds__(kThreads) void gla_fwd_o_kernel(const GlaArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sVt[64 * LDH];  // V tile [v][s]
 
   const int tid = threadIdx.x, w = wave_id();
-  const int gc = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * 64;
+  // the V / 64 value blocks of a (chunk, head) unit share its operands: one XCD (L2) per unit
+  int unit, vb;
+  xcd_map(blockIdx.x, a.V / 64, a.NTG * a.H, unit, vb);
+  const int gc = unit / a.H, h = unit % a.H, v0 = vb * 64;
   int n, c0, L;
   long bos;
   if (!gla_chunk(a, gc, n, c0, bos, L)) return;
@@ -472,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void gla_fwd_o_kernel(const GlaArgs a) {
 }
 
 // ===========================================================================
-// gla_bwd_dv: grid (NTG, H, V/64).  dv[:, tile] = A^T dO[:, tile] + (K o e^{b_L - b}) dS[:, tile]
+// gla_bwd_dv: grid NTG * H * (V/64), XCD-mapped.  dv[:, tile] = A^T dO[:, tile] + (K o e^{b_L - b}) dS[:, tile]
 // ===========================================================================
 template <int K>
 __global__ __launch_bounds__(kThreads) void gla_bwd_dv_kernel(const GlaArgs a) {
@@ -484,7 +487,10 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dv_kernel(const GlaArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sOt[64 * LDH];   // dO tile [v][t]
 
   const int tid = threadIdx.x, w = wave_id();
-  const int gc = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * 64;
+  // the V / 64 value blocks of a (chunk, head) unit share its operands: one XCD (L2) per unit
+  int unit, vb;
+  xcd_map(blockIdx.x, a.V / 64, a.NTG * a.H, unit, vb);
+  const int gc = unit / a.H, h = unit % a.H, v0 = vb * 64;
   int n, c0, L;
   long bos;
   if (!gla_chunk(a, gc, n, c0, bos, L)) return;
@@ -539,7 +545,7 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dv_kernel(const GlaArgs a) {
 }
 
 // ===========================================================================
-// gla_bwd_dqk: grid (NTG, H, K/64).  dq, dk and dG for one 64-channel slab, then the in-chunk
+// gla_bwd_dqk: grid NTG * H * (K/64), XCD-mapped.  dq, dk and dG for one 64-channel slab, then the in-chunk
 // suffix sums of dG (dgk before the carry of later chunks) and the chunk totals.
 // ===========================================================================
 template <int K>
@@ -565,7 +571,10 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dqk_kernel(const GlaArgs a) 
   float* sdA = sBb + BT * LDF;
 
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
-  const int gc = blockIdx.x, h = blockIdx.y, s0 = blockIdx.z * KS;
+  // the K / KS key blocks of a (chunk, head) unit share its operands: one XCD (L2) per unit
+  int unit, kb;
+  xcd_map(blockIdx.x, K / KS, a.NTG * a.H, unit, kb);
+  const int gc = unit / a.H, h = unit % a.H, s0 = kb * KS;
   int n, c0, L;
   long bos;
   if (!gla_chunk(a, gc, n, c0, bos, L)) return;
@@ -765,16 +774,16 @@ hipError_t launch_gla_k(int stage, const GlaArgs& a, hipStream_t st) {
       hipLaunchKernelGGL(gla_state_kernel<0>, dim3(a.N * H * (K / 32) * (a.V / 32)), dim3(64), 0, st, a);
       break;
     case kGlaFwdO:
-      hipLaunchKernelGGL(gla_fwd_o_kernel<K>, dim3(NTG, H, a.V / 64), blk, 0, st, a);
+      hipLaunchKernelGGL(gla_fwd_o_kernel<K>, dim3(NTG * H * (a.V / 64)), blk, 0, st, a);
       break;
     case kGlaBwdState:
       hipLaunchKernelGGL(gla_state_kernel<1>, dim3(a.N * H * (K / 32) * (a.V / 32)), dim3(64), 0, st, a);
       break;
     case kGlaBwdDv:
-      hipLaunchKernelGGL(gla_bwd_dv_kernel<K>, dim3(NTG, H, a.V / 64), blk, 0, st, a);
+      hipLaunchKernelGGL(gla_bwd_dv_kernel<K>, dim3(NTG * H * (a.V / 64)), blk, 0, st, a);
       break;
     case kGlaBwdDqk:
-      hipLaunchKernelGGL(gla_bwd_dqk_kernel<K>, dim3(NTG, H, K / KS), blk, 0, st, a);
+      hipLaunchKernelGGL(gla_bwd_dqk_kernel<K>, dim3(NTG * H * (K / KS)), blk, 0, st, a);
       break;
     case kGlaBwdGk:
       hipLaunchKernelGGL(gla_gk_carry_kernel, dim3(a.N * H), blk, 0, st, a);
