@@ -70,6 +70,10 @@ CONV_CASES = [
     (1, 120, 512, 4, True, 128, True, [0, 3, 3, 50, 120], True),
     (2, 70, 128, 3, False, None, True, None, True),
     (1, 300, 1024, 4, True, 256, False, [0, 1, 2, 300], False),
+    # enough tokens for the forward's multi-token tiles (16 per tile from 16,384 tokens, 5 at 5,202),
+    # with sequence starts inside tiles (window refills mid-tile)
+    (1, 16500, 256, 4, True, 64, False, [0, 5, 4099, 9000, 16500], True),
+    (2, 2601, 128, 4, True, 128, True, None, True),
 ]
 
 
