@@ -108,3 +108,22 @@ def test_decode_step_rejects_missing_state():
                                      ptr(st.g), ptr(st.beta), ptr(st.S), ptr(st.C), ptr(st.m), None, ptr(st.o),
                                      ptr(st.workspace), 1, 1, 1, 64, 64, 1, 1, 1, 0.125, None)
     assert status == -2 and b"position" in lib.ccq_last_error()
+
+
+def test_whole_model_decode_graph_matches_eager():
+    """BASELINE C4's harness (``bench.run_c4``) at a reduced size: 2 CCQ-GDN layers (d_k 256, d_v
+    512), 2 sequences of 256 tokens, 6 greedy decode steps.  The harness prefills, decodes eagerly
+    through the layers' recurrent mode, then captures the whole model's token step (the layers'
+    projections, prologue and output norm around the in-place decode kernels) in one graph and
+    raises unless each of the first replays, fed the eager path's tokens, reproduces the eager
+    logits."""
+    dev = _cuda()
+    import types
+
+    import bench
+    print("test_whole_model_decode_graph_matches_eager layers=2 b=2 t=256", flush=True)
+    out = bench.run_c4(types.SimpleNamespace(steps=0, warmup=0), dev, layers=2, b=2, t=256, decode_steps=6,
+                       check_steps=4)
+    errs = out["config"]["graph_vs_eager_logits_rel_l2"]
+    print("captured vs eager logits rel-L2", errs, flush=True)
+    assert len(errs) == 4 and max(errs) <= 2e-2
