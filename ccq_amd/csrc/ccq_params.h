@@ -35,6 +35,8 @@ struct ConvArgs {
   long tokens;
   int T, N, D, W, hd, act;
   int tb;                   // fwd: tokens per tile (consecutive tokens one thread walks with a sliding window)
+  int cg;                   // channel groups (8 channels each) per workgroup, a power of two <= 256
+  int nvb;                  // virtual workgroups: a workgroup holds 256 / cg token lanes, each one of them
   float eps;
 };
 

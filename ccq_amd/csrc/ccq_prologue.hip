@@ -84,7 +84,10 @@ __device__ __forceinline__ void window_in(const ConvArgs& a, const SeqOf& sq, lo
 // ---------------------------------------------------------------------------
 template <int W>
 __global__ __launch_bounds__(kThreads) void conv_fwd_kernel(const ConvArgs a) {
-  const int c = (blockIdx.y * kThreads + threadIdx.x) * 8;
+  const int cg = threadIdx.x & (a.cg - 1);
+  const long vb = (long)blockIdx.x * (kThreads / a.cg) + threadIdx.x / a.cg;  // this lane's virtual workgroup
+  if (vb >= a.nvb) return;  // (whole token lanes: the per-head lane groups stay complete)
+  const int c = (blockIdx.y * a.cg + cg) * 8;
   const bool own = c < a.D;
   const int cc = own ? c : 0;
   float wt[8][W], bs[8];
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void conv_fwd_kernel(const ConvArgs a) {
   }
   const int hl = a.hd / 8;  // lanes per head
   const long ntiles = (a.tokens + a.tb - 1) / a.tb;
-  for (long tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  for (long tile = vb; tile < ntiles; tile += a.nvb) {
     const long p0 = tile * a.tb, p1 = min(p0 + (long)a.tb, a.tokens);
     SeqOf sq = seq_of(a, p0);
     // window: inputs at positions p - (W-1) .. p - 1 of the current sequence
@@ -176,7 +179,10 @@ __global__ __launch_bounds__(kThreads) void conv_cache_kernel(const ConvArgs a) 
 // ---------------------------------------------------------------------------
 template <int W>
 __global__ __launch_bounds__(kThreads) void conv_bwd_kernel(const ConvArgs a) {
-  const int c = (blockIdx.y * kThreads + threadIdx.x) * 8;
+  const int cg = threadIdx.x & (a.cg - 1);
+  const long vb = (long)blockIdx.x * (kThreads / a.cg) + threadIdx.x / a.cg;  // this lane's virtual workgroup
+  if (vb >= a.nvb) return;  // (whole token lanes: the per-head lane groups stay complete)
+  const int c = (blockIdx.y * a.cg + cg) * 8;
   const bool own = c < a.D;
   const int cc = own ? c : 0;
   float wt[8][W], bs[8];
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void conv_bwd_kernel(const ConvArgs a) {
   }
   const int hl = a.hd / 8;
   const long ntiles = (a.tokens + kConvTB - 1) / kConvTB;
-  for (long tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  for (long tile = vb; tile < ntiles; tile += a.nvb) {
     const long p0 = tile * kConvTB, p1 = min(p0 + (long)kConvTB, a.tokens);
     // da of the tokens [p, p + W - 1) after the current one, kept for dx (zero past the sequence)
     float dan[W][8];
@@ -332,15 +338,15 @@ __global__ __launch_bounds__(kThreads) void conv_bwd_kernel(const ConvArgs a) {
       }
     }
   }
-  // this workgroup's partial sums
+  // this virtual workgroup's partial sums
   if (own) {
-    float* dwp = a.dw_part + (long)blockIdx.x * a.D * W;
+    float* dwp = a.dw_part + vb * a.D * W;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
 #pragma unroll
       for (int w = 0; w < W; ++w)
         if (w < W) dwp[(long)(c + i) * W + w] = gw[i][w];
-      if (a.db_part) a.db_part[(long)blockIdx.x * a.D + c + i] = gb[i];
+      if (a.db_part) a.db_part[vb * a.D + c + i] = gb[i];
     }
   }
 }
@@ -442,9 +448,18 @@ __global__ __launch_bounds__(kThreads) void gnorm_bwd_kernel(const GNormArgs a) 
     a.dw_part[(long)blockIdx.x * a.dv + j] = sW[0][j] + sW[1][j] + sW[2][j] + sW[3][j];
 }
 
-hipError_t launch_conv(int stage, const ConvArgs& a, int blocks, hipStream_t st) {
-  if (a.tokens <= 0 && stage != 2) return hipSuccess;
-  const dim3 grid((unsigned)blocks, (unsigned)((a.D + 8 * kThreads - 1) / (8 * kThreads)));
+// `blocks` virtual workgroups (the backward's partial rows); each workgroup covers cg groups of 8
+// channels (the next power of two of D / 8, at most 256) and 256 / cg token lanes, so narrow
+// layers (D / 8 < 256) keep every thread busy instead of leaving the channel groups past D idle.
+hipError_t launch_conv(int stage, const ConvArgs& args, int blocks, hipStream_t st) {
+  if (args.tokens <= 0 && stage != 2) return hipSuccess;
+  ConvArgs a = args;
+  int cg = 1;
+  while (cg < kThreads && cg * 8 < a.D) cg <<= 1;
+  a.cg = cg;
+  a.nvb = blocks;
+  const int lanes = kThreads / cg;
+  const dim3 grid((unsigned)((blocks + lanes - 1) / lanes), (unsigned)((a.D + 8 * cg - 1) / (8 * cg)));
   switch (stage) {
     case 0:
     case 1:
