@@ -54,6 +54,7 @@ struct GNormArgs {
   float* dw_part;           // fp32 [blocks, dv] (nullable)
   long rows;
   int dv;
+  int lr;                   // lanes per row: the next power of two of dv / 8 (64 / lr rows per wavefront)
   float eps;
 };
 

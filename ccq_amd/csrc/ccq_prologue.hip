@@ -352,12 +352,14 @@ __global__ __launch_bounds__(kThreads) void conv_bwd_kernel(const ConvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// gated RMSNorm: one wavefront per row of dv <= 512 (lane: 8 consecutive elements)
+// gated RMSNorm over rows of dv <= 512: lr lanes per row (lane: 8 consecutive elements), 64 / lr
+// rows per wavefront, so rows narrower than 512 leave no lane idle
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void gnorm_fwd_kernel(const GNormArgs a) {
-  const long row = (long)blockIdx.x * 4 + wave_id();
-  if (row >= a.rows) return;
-  const int l = lane_id(), e = l * 8;
+  const int l = lane_id(), rpw = 64 / a.lr;
+  const long row = ((long)blockIdx.x * 4 + wave_id()) * rpw + l / a.lr;
+  if (row >= a.rows) return;  // (whole lane groups: a row's lanes stay together)
+  const int e = (l & (a.lr - 1)) * 8;
   const bool own = e < a.dv;
   float x[8], g[8];
   if (own) {
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void gnorm_fwd_kernel(const GNormArgs a) 
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
-  ss = group_sum(ss, 64);
+  ss = group_sum(ss, a.lr);
   const float r = rsqrtf(ss / (float)a.dv + a.eps);
   if (own) {
     bf16x8 yb;
@@ -386,19 +388,19 @@ __global__ __launch_bounds__(kThreads) void gnorm_fwd_kernel(const GNormArgs a) 
     }
     *(bf16x8*)((bf16*)a.y + row * a.dv + e) = yb;
   }
-  if (l == 0) a.rstd[row] = r;
+  if ((l & (a.lr - 1)) == 0) a.rstd[row] = r;
 }
 
 // dL/dxh = dy w silu(g); dx = r (dxh - xh mean(dxh xh)); dg = dy xh w silu'(g); dw += dy xh silu(g)
 // (partials per workgroup, rows of the grid-stride loop)
 __global__ __launch_bounds__(kThreads) void gnorm_bwd_kernel(const GNormArgs a) {
-  const int l = lane_id(), e = l * 8;
+  const int l = lane_id(), rpw = 64 / a.lr, e = (l & (a.lr - 1)) * 8;
   const bool own = e < a.dv;
   float gw[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) gw[i] = 0.f;
   __shared__ float sW[4][512];
-  for (long row = (long)blockIdx.x * 4 + wave_id(); row < a.rows; row += (long)gridDim.x * 4) {
+  for (long row = ((long)blockIdx.x * 4 + wave_id()) * rpw + l / a.lr; row < a.rows; row += (long)gridDim.x * 4 * rpw) {
     float x[8], g[8], dy[8];
     if (own) {
       const bf16x8 xb = *(const bf16x8*)((const bf16*)a.x + row * a.dv + e);
@@ -426,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void gnorm_bwd_kernel(const GNormArgs a) 
       gw[i] += dy[i] * xh[i] * s;
       g[i] = dy[i] * xh[i] * w * dsilu_(g[i]);  // dg
     }
-    dot = group_sum(dot, 64) / (float)a.dv;
+    dot = group_sum(dot, a.lr) / (float)a.dv;
     if (own) {
       bf16x8 dxb, dgb;
 #pragma unroll
@@ -439,8 +441,12 @@ __global__ __launch_bounds__(kThreads) void gnorm_bwd_kernel(const GNormArgs a) 
     }
   }
   if (!a.dw_part) return;
-  // the workgroup's four waves summed through LDS, one partial row per workgroup
-  if (own)
+  // the wave's row groups summed by lane swaps (lanes l, l ^ lr, ... hold the same columns), then
+  // the workgroup's four waves through LDS, one partial row per workgroup
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    for (int m = a.lr; m < 64; m <<= 1) gw[i] += __shfl_xor(gw[i], m);
+  if (own && l < a.lr)
 #pragma unroll
     for (int i = 0; i < 8; ++i) sW[wave_id()][e + i] = gw[i];
   __syncthreads();
@@ -485,10 +491,15 @@ hipError_t launch_conv(int stage, const ConvArgs& args, int blocks, hipStream_t 
   return hipGetLastError();
 }
 
-hipError_t launch_gnorm(int stage, const GNormArgs& a, int blocks, hipStream_t st) {
-  if (a.rows <= 0) return hipSuccess;
+hipError_t launch_gnorm(int stage, const GNormArgs& args, int blocks, hipStream_t st) {
+  if (args.rows <= 0) return hipSuccess;
+  GNormArgs a = args;
+  a.lr = 1;
+  while (a.lr < 64 && a.lr * 8 < a.dv) a.lr <<= 1;
+  const long rows_per_block = 4L * (64 / a.lr);
   if (stage == 0)
-    hipLaunchKernelGGL(gnorm_fwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(gnorm_fwd_kernel, dim3((unsigned)((a.rows + rows_per_block - 1) / rows_per_block)),
+                       dim3(kThreads), 0, st, a);
   else
     hipLaunchKernelGGL(gnorm_bwd_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, st, a);
   return hipGetLastError();
