@@ -43,6 +43,77 @@ __global__ __launch_bounds__(kThreads) void l2norm_bwd_kernel(const L2NormArgs a
   }
 }
 
+// The same two passes with 16-byte pieces (D % 8 == 0, 16-byte aligned rows): lr lanes of 8
+// consecutive elements per row, 64 / lr rows per wavefront (a row's lanes are one aligned group).
+__global__ __launch_bounds__(kThreads) void l2norm_fwd_v_kernel(const L2NormArgs a) {
+  const int l = lane_id();
+  const long row = ((long)blockIdx.x * 4 + wave_id()) * (64 / a.lr) + l / a.lr;
+  if (row >= a.rows) return;  // (whole lane groups)
+  const int e = (l & (a.lr - 1)) * 8;
+  const bool own = e < a.D;
+  float v[8];
+  if (own) {
+    const bf16x8 xb = *(const bf16x8*)((const bf16*)a.x + row * a.D + e);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float)xb[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += v[i] * v[i];
+  s = group_sum(s, a.lr);
+  const float r = rsqrtf(s + a.eps);
+  if (own) {
+    bf16x8 yb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) yb[i] = (bf16)(v[i] * r);
+    *(bf16x8*)((bf16*)a.y + row * a.D + e) = yb;
+  }
+  if ((l & (a.lr - 1)) == 0 && a.rstd) a.rstd[row] = r;
+}
+
+__global__ __launch_bounds__(kThreads) void l2norm_bwd_v_kernel(const L2NormArgs a) {
+  const int l = lane_id();
+  const long row = ((long)blockIdx.x * 4 + wave_id()) * (64 / a.lr) + l / a.lr;
+  if (row >= a.rows) return;  // (whole lane groups)
+  const int e = (l & (a.lr - 1)) * 8;
+  const bool own = e < a.D;
+  const float r = a.rstd[row];
+  float x[8], dy[8];
+  if (own) {
+    const bf16x8 xb = *(const bf16x8*)((const bf16*)a.x + row * a.D + e);
+    if (a.dy32) {
+      const f32x4 d0 = *(const f32x4*)(a.dy32 + row * a.D + e), d1 = *(const f32x4*)(a.dy32 + row * a.D + e + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dy[i] = d0[i];
+        dy[4 + i] = d1[i];
+      }
+    } else {
+      const bf16x8 db = *(const bf16x8*)((const bf16*)a.dy16 + row * a.D + e);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dy[i] = (float)db[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = (float)xb[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = dy[i] = 0.f;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += x[i] * r * dy[i];
+  s = group_sum(s, a.lr);
+  if (own) {
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (bf16)(r * (dy[i] - x[i] * r * s));
+    *(bf16x8*)((bf16*)a.dx + row * a.D + e) = o;
+  }
+}
+
 // chunk_off[n] = first global `size`-token chunk of sequence n (exclusive scan of ceil(len/size));
 // chunk_idx[2c], [2c+1] = (sequence, chunk within sequence) for c < total, -1 beyond it (up to cap).
 __global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int64_t* cu, int N, int size, int* chunk_off,
@@ -90,15 +161,42 @@ hipError_t launch_fill_zero(float* out, long n, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st) {
-  if (a.rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(l2norm_fwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
+namespace {
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// the vector kernels' lanes per row, or 0 where the rows are not whole aligned 16-byte pieces
+int l2norm_lanes(const L2NormArgs& a, bool bwd) {
+  if (a.D % 8 || !al16(a.x) || !al16(bwd ? a.dx : a.y)) return 0;
+  if (bwd && !(a.dy32 ? al16(a.dy32) : al16(a.dy16))) return 0;
+  int lr = 1;
+  while (lr < 64 && lr * 8 < a.D) lr <<= 1;
+  return lr;
+}
+}  // namespace
+
+hipError_t launch_l2norm_fwd(const L2NormArgs& args, hipStream_t st) {
+  if (args.rows == 0) return hipSuccess;
+  L2NormArgs a = args;
+  a.lr = l2norm_lanes(a, false);
+  if (a.lr) {
+    const long per = 4L * (64 / a.lr);
+    hipLaunchKernelGGL(l2norm_fwd_v_kernel, dim3((unsigned)((a.rows + per - 1) / per)), dim3(kThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(l2norm_fwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
+  }
   return hipGetLastError();
 }
 
-hipError_t launch_l2norm_bwd(const L2NormArgs& a, hipStream_t st) {
-  if (a.rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(l2norm_bwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
+hipError_t launch_l2norm_bwd(const L2NormArgs& args, hipStream_t st) {
+  if (args.rows == 0) return hipSuccess;
+  L2NormArgs a = args;
+  a.lr = l2norm_lanes(a, true);
+  if (a.lr) {
+    const long per = 4L * (64 / a.lr);
+    hipLaunchKernelGGL(l2norm_bwd_v_kernel, dim3((unsigned)((a.rows + per - 1) / per)), dim3(kThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(l2norm_bwd_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(kThreads), 0, st, a);
+  }
   return hipGetLastError();
 }
 

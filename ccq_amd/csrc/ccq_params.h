@@ -67,6 +67,7 @@ struct L2NormArgs {
   void* dx;                 // bf16 [rows, D]
   long rows;
   int D;
+  int lr;                   // vector kernels: lanes per row (next power of two of D / 8), 64 / lr rows per wave
   float eps;
 };
 

@@ -214,3 +214,28 @@ def test_gdn_layer_fused_prologue_matches_unfused():
     print({n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
     for n, e in errs.items():
         assert e <= 1e-2, n
+
+
+@pytest.mark.parametrize("rows,D,dy32", [(1000, 128, True), (333, 256, False), (77, 64, True), (50, 512, False),
+                                         (41, 100, True), (9, 24, False)])
+def test_l2norm(rows, D, dy32):
+    """Row L2 normalisation (the op's l2norm, fla's at ccq/ops/ccq_gdn/fused_chunk.py:43-44) and its
+    backward against fp32 PyTorch on the same bf16 inputs: the 16-byte kernels (D % 8 == 0, several
+    rows per wavefront below D = 512) and the scalar ones (D = 100); fp32 and bf16 upstream
+    gradients, row counts that leave a wavefront partly filled."""
+    dev = _cuda()
+    from ccq_amd.clean import l2norm_bwd, l2norm_fwd
+    print(f"l2norm rows={rows} D={D} dy32={dy32}", flush=True)
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(rows, D, generator=gen).bfloat16().to(dev)
+    dy = torch.randn(rows, D, generator=gen)
+    dy = dy.to(dev) if dy32 else dy.bfloat16().to(dev)
+    y, rstd = l2norm_fwd(x, 1e-6)
+    dx = l2norm_bwd(x, rstd, dy)
+    xr = x.float().requires_grad_()
+    yr = xr / torch.sqrt((xr * xr).sum(-1, keepdim=True) + 1e-6)
+    (dxr,) = torch.autograd.grad(yr, xr, dy.float())
+    torch.cuda.synchronize()
+    errs = {"y": rel(y, yr), "rstd": rel(rstd, 1.0 / torch.sqrt((xr * xr).sum(-1) + 1e-6)), "dx": rel(dx, dxr)}
+    print(errs, flush=True)
+    assert errs["y"] <= TOL and errs["dx"] <= TOL and errs["rstd"] <= 1e-6
