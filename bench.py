@@ -462,8 +462,9 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
                 a.copy_(c)
 
     # the six input projections of a layer as one GEMM (the layers' own weights, concatenated once)
-    proj = [torch.cat([blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight,
-                       blk.attn.a_proj.weight, blk.attn.b_proj.weight, blk.attn.g_proj.weight]) for blk in blocks]
+    with torch.no_grad():
+        proj = [torch.cat([blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight,
+                           blk.attn.a_proj.weight, blk.attn.b_proj.weight, blk.attn.g_proj.weight]) for blk in blocks]
     L0 = blocks[0].attn
     splits = [L0.q_proj.out_features, L0.k_proj.out_features, L0.v_proj.out_features, L0.a_proj.out_features,
               L0.b_proj.out_features, L0.g_proj.out_features]
