@@ -5,7 +5,8 @@
 
 namespace ccq {
 
-// y = x / sqrt(sum x^2 + eps), one 64-lane wavefront per row (D <= 512, D % 8 == 0).
+// y = x / sqrt(sum x^2 + eps), one 64-lane wavefront per row, element by element (any D <= 512:
+// the rows the 16-byte kernels below cannot take).
 __global__ __launch_bounds__(kThreads) void l2norm_fwd_kernel(const L2NormArgs a) {
   const long row = (long)blockIdx.x * 4 + wave_id();
   if (row >= a.rows) return;
