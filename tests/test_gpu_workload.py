@@ -44,7 +44,7 @@ def _report(case, errs, kerrs):
         assert e <= TOL_KERNEL, n
 
 
-@pytest.mark.parametrize("T", [4096])
+@pytest.mark.parametrize("T", [4096, 1000])  # 1000: a partial last chunk under the full decay
 def test_bench_workload(T):
     """bench.py's step at one sequence: o and the gradients of q, k, v, g, beta, W, b."""
     dev = _cuda()
