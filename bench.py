@@ -166,6 +166,18 @@ def roofline(step_kernel_ms, launches_per_step, units=B * T * H):
             "mfma_frac_design_flop": dflop * units / avg_s / PEAK_BF16}
 
 
+def cpu_model_name() -> str:
+    """The host CPU's model name, as ``lscpu`` reports it (read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds_budget=25.0):
     """fp32 PyTorch restatement of the reference's non-fused algorithm (oracle/) on the host:
     lambda gate, cleaning (chunked), gated delta rule (chunked WY form), autograd fwd+bwd,
@@ -192,6 +204,7 @@ def cpu_baseline(seconds_budget=25.0):
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     return {"value": t_s / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": cpu_model_name(),
             "sample": f"1 sequence x {t_s} tokens x {H} heads (d_k=d_v={K}), fp32 autograd fwd+bwd, "
                       f"median of {len(times)} after 1 warm-up"}
 

@@ -60,6 +60,22 @@ int hip_status(hipError_t e, const char* where) {
 
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// The cleaning's buffer sizes (its number of time segments) and the persistent kernels' grids follow
+// the CU count of the device that is current when they are queried and launched.  A stream of
+// another device would run launches shaped, and buffers sized, for the wrong device: refuse it.
+int check_stream_device(void* stream, const char* who) {
+  int cur = 0;
+  if (hipError_t e = hipGetDevice(&cur); e != hipSuccess) return hip_status(e, who);
+  if (!stream) return CCQ_OK;
+  hipDevice_t sd = -1;
+  if (hipError_t e = hipStreamGetDevice((hipStream_t)stream, &sd); e != hipSuccess) return hip_status(e, who);
+  if (sd != cur)
+    return fail(CCQ_ERR_DEVICE,
+                "%s: the stream belongs to device %d but device %d is current; make the stream's device current "
+                "(buffer sizes and launch shapes follow the current device)", who, (int)sd, cur);
+  return CCQ_OK;
+}
+
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Consecutive sub-buffers of a caller-provided byte buffer.
@@ -279,6 +295,7 @@ int ccq_clean_fwd(const void* q, const void* k, const float* lambda, const float
   if (!gate_w && !lambda) return fail(CCQ_ERR_NULL, "ccq_clean_fwd: lambda or gate_w is required");
   if (gate_w && !gate_b) return fail(CCQ_ERR_NULL, "ccq_clean_fwd: gate_w needs gate_b");
   if (!q_clean && !q_clean_f32) return fail(CCQ_ERR_NULL, "ccq_clean_fwd: no output (q_clean / q_clean_f32)");
+  if (int s = check_stream_device(stream, "ccq_clean_fwd")) return s;
   if (!aligned16(q) || !aligned16(k) || !aligned16(saved))
     return fail(CCQ_ERR_ALIGN, "ccq_clean_fwd: q, k, saved must be 16-byte aligned");
   const bool varlen = cu_seqlens != nullptr;
@@ -321,6 +338,7 @@ int ccq_clean_bwd(const void* q, const void* k, const float* lambda, const float
   if (!dq_clean_f32 && !dq_clean) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: upstream gradient missing");
   if (!dq && !dq_f32) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: no dq output");
   if (!dk && !dk_f32) return fail(CCQ_ERR_NULL, "ccq_clean_bwd: no dk output");
+  if (int s = check_stream_device(stream, "ccq_clean_bwd")) return s;
   const bool gate = gate_w != nullptr;
   if (gate && (!gate_b || !dgate_w || !dgate_b))
     return fail(CCQ_ERR_NULL, "ccq_clean_bwd: gate needs gate_b, dgate_w, dgate_b");
@@ -476,6 +494,7 @@ int ccq_gdn_fwd(const void* q, const float* q_f32, const void* k, const void* v,
                 int H, int K, int V, int N, float scale, void* stream) {
   if (int s = gdn_check("ccq_gdn_fwd", B, T, H, K, V, N, cu_seqlens, chunk_index, chunk_offsets, num_chunks)) return s;
   if ((!q && !q_f32) || !k || !v || !beta || !o || !saved) return fail(CCQ_ERR_NULL, "ccq_gdn_fwd: null input/output");
+  if (int s = check_stream_device(stream, "ccq_gdn_fwd")) return s;
   if (!aligned16(q) || !aligned16(q_f32) || !aligned16(k) || !aligned16(v) || !aligned16(saved))
     return fail(CCQ_ERR_ALIGN, "ccq_gdn_fwd: tensors must be 16-byte aligned");
   const int64_t tokens = (int64_t)B * T;
@@ -508,6 +527,7 @@ int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v,
   if ((!q && !q_f32) || !k || !v || !beta || !saved || !d_o || !workspace || !dq_f32 || !dk_f32 || !dv || !dbeta ||
       !dg)
     return fail(CCQ_ERR_NULL, "ccq_gdn_bwd: null input/output");
+  if (int s = check_stream_device(stream, "ccq_gdn_bwd")) return s;
   // the dq/dk/dw kernels read dO with 16-byte direct-to-LDS loads; dv leaves as 16-byte pieces
   if (!aligned16(q) || !aligned16(q_f32) || !aligned16(k) || !aligned16(v) || !aligned16(d_o) || !aligned16(dv) ||
       !aligned16(saved) || !aligned16(workspace) || !aligned16(dq_f32) || !aligned16(dk_f32))
@@ -887,6 +907,9 @@ int decode_common(const char* who, DecodeArgs& a, const void* q, const void* k, 
     return fail(CCQ_ERR_SHAPE, "%s: mean_state_out may not alias mean_state (every workgroup reads all of it)", who);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(workspace))
     return fail(CCQ_ERR_ALIGN, "%s: tensors must be 16-byte aligned", who);
+  // the state slices move as 16-byte pieces of four columns (loads and stores)
+  if (!aligned16(state) || !aligned16(cov_state) || !aligned16(state_out) || !aligned16(cov_state_out))
+    return fail(CCQ_ERR_ALIGN, "%s: state, cov_state and their outputs must be 16-byte aligned", who);
   const int64_t tokens = (int64_t)B * T;
   carve_decode_work((char*)workspace, tokens, H, K, &a.qc, &a.kn);
   a.q = q; a.k = k; a.v = v; a.lam = lambda; a.gate_w = gate_w; a.gate_b = gate_b;
@@ -920,6 +943,7 @@ int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lam
                             position_offset, subtract_mean, use_l2norm, enable_ccq, scale))
     return s;
   if (!beta) return fail(CCQ_ERR_NULL, "ccq_gdn_decode: beta is required");
+  if (!aligned16(gv)) return fail(CCQ_ERR_ALIGN, "ccq_gdn_decode: gv must be 16-byte aligned");
   a.g = g; a.beta = beta; a.gk = gk; a.gv = gv; a.gla = 0;
   return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gdn_decode");
 }
@@ -960,6 +984,7 @@ int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lam
                             position_offset, subtract_mean, use_l2norm, 1, scale))
     return s;
   if (K > 256) return fail(CCQ_ERR_SHAPE, "ccq_gla_decode: K=%d", K);
+  if (!aligned16(gv)) return fail(CCQ_ERR_ALIGN, "ccq_gla_decode: gv must be 16-byte aligned");
   a.gk = gk; a.gv = gv; a.gla = 1; a.reverse = reverse ? 1 : 0;
   return hip_status(launch_decode(a, (hipStream_t)stream), "ccq_gla_decode");
 }

@@ -10,6 +10,10 @@
  * backward pass needs from its forward ("saved") and scratch
  * space ("workspace") are caller-provided, sized by the *_bytes() queries.
  *
+ * The cleaning and GDN chunk entry points size their buffers (the *_bytes() queries) and shape
+ * their launches by the CU count of the device that is current; they return CCQ_ERR_DEVICE when the
+ * stream belongs to another device.  Make the stream's device current for the queries and calls.
+ *
  * Layouts follow the reference (token-major, head-interleaved):
  *   q, k [tokens, H, K] bf16; v, o [tokens, H, V] bf16; per-token scalars
  *   [tokens, H] fp32; tokens = B*T (dense) or the packed length (varlen:
@@ -31,6 +35,7 @@ extern "C" {
 #define CCQ_ERR_NULL (-2)      /* a required pointer is NULL */
 #define CCQ_ERR_ALIGN (-3)     /* a pointer is not 16-byte aligned */
 #define CCQ_ERR_HIP (-4)       /* a HIP runtime error (see ccq_last_error) */
+#define CCQ_ERR_DEVICE (-5)    /* the stream belongs to a device other than the current one */
 
 int ccq_abi_version(void);
 const char* ccq_last_error(void);
@@ -199,7 +204,9 @@ int ccq_gla_bwd(const void* q, const float* q_f32, const void* k, const void* v,
  * cov_state_out may alias their inputs (in-place cache update); mean_state_out may not.
  * lambda fp32 [tokens, H] or gate_w/gate_b as in ccq_clean_fwd.  enable_ccq = 0 (GDN only) skips
  * the cleaning and the C/m states.  workspace: ccq_decode_workspace_bytes().
- * K in {32, 64, 128, 256}; V a multiple of 64 (<= 1024).
+ * K in {32, 64, 128, 256}; V a multiple of 64 (<= 1024).  q, k, v, o, the workspace, state,
+ * cov_state, their outputs and gv must be 16-byte aligned (CCQ_ERR_ALIGN otherwise): the kernels move
+ * state slices and gv as 16-byte pieces of four columns.
  */
 size_t ccq_decode_workspace_bytes(int64_t tokens, int H, int K);
 int ccq_gdn_decode(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,

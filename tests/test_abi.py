@@ -196,3 +196,22 @@ def test_decode_step_checks_and_workspace():
     ws = lib.ccq_decode_step_workspace_bytes(B, T, H, K)
     base = lib.ccq_decode_workspace_bytes(B * T, H, K)
     assert base + B * H * K * 4 <= ws <= base + B * H * K * 4 + 256
+
+
+def test_decode_rejects_unaligned_states_and_gv():
+    # the decode kernels move state slices and gv as 16-byte pieces: an unaligned pointer is refused
+    # on the host, before any device work
+    lib = _lib.load()
+    p, odd, m_out = _fake(), ctypes.c_void_p(0x1004), ctypes.c_void_p(0x2000)   # m_out may not alias m
+    CCQ_ERR_ALIGN = -3
+
+    def call(state=p, cov=p, state_out=p, cov_out=p, gv=None):
+        return lib.ccq_gdn_decode(p, p, p, p, None, None, None, p, None, gv, state, cov, p, None, p, state_out,
+                                  cov_out, m_out, p, 2, 1, 4, 64, 64, 2, 0, 1, 1, 1, 0.125, None)
+
+    for kw in ({"state": odd}, {"cov": odd}, {"state_out": odd}, {"cov_out": odd}, {"gv": odd}):
+        assert call(**kw) == CCQ_ERR_ALIGN, kw
+        assert b"aligned" in lib.ccq_last_error()
+    st = lib.ccq_gla_decode(p, p, p, p, None, None, None, odd, p, p, p, None, p, p, p, m_out, p, 2, 1, 4, 64, 64, 2, 0, 1,
+                            1, 0, 0.125, None)
+    assert st == CCQ_ERR_ALIGN

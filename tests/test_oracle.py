@@ -306,6 +306,49 @@ def test_gate_weight_zero_is_sigmoid_bias():
     assert torch.allclose(lam, torch.sigmoid(b).expand(2, 5, 3))
 
 
+def test_gate_one_hot_row_reads_one_coordinate():
+    # W[h] = c_h e_{j_h}: the contraction W[h]·q_t,h must pick coordinate j_h of head h's own query,
+    # scaled by c_h, so lambda = sigmoid(c_h q[b, t, h, j_h] + b_h).  A dropped or transposed
+    # contraction, or one that mixes heads, fails this.
+    B, T, H, K = 2, 6, 3, 5
+    q = torch.randn(B, T, H, K, dtype=D)
+    js, cs = [4, 0, 2], [1.0, -3.0, 0.5]
+    w = torch.zeros(H, K, dtype=D)
+    for h in range(H):
+        w[h, js[h]] = cs[h]
+    b = torch.tensor([0.25, -1.0, 2.0], dtype=D)
+    lam = O.lambda_gate(q, w, b)
+    want = torch.empty(B, T, H, dtype=D)
+    for bb in range(B):
+        for t in range(T):
+            for h in range(H):
+                want[bb, t, h] = 1.0 / (1.0 + math.exp(-(cs[h] * float(q[bb, t, h, js[h]]) + float(b[h]))))
+    assert torch.allclose(lam, want, atol=1e-15)
+
+
+def test_reshape_lambda_every_form_written_out():
+    B, T, H = 2, 3, 2
+    # python scalar and 0-d tensor: one value everywhere
+    assert torch.equal(O.reshape_lambda(0.75, B, T, H), torch.full((B, T, H), 0.75, dtype=D))
+    assert torch.equal(O.reshape_lambda(torch.tensor(0.5), B, T, H), torch.full((B, T, H), 0.5, dtype=D))
+    # (H,): head h's value at every token
+    lam_h = torch.tensor([0.1, 0.9])
+    want = torch.tensor([[[0.1, 0.9]] * T] * B, dtype=D)
+    assert torch.equal(O.reshape_lambda(lam_h, B, T, H), lam_h.to(D).expand(B, T, H))
+    assert torch.equal(O.reshape_lambda(lam_h, B, T, H), want.to(torch.float32).to(D))
+    # [B, T, H, 1]: the trailing unit dimension dropped, values kept in place
+    lam4 = torch.arange(B * T * H, dtype=D).view(B, T, H, 1) / 10
+    out = O.reshape_lambda(lam4, B, T, H)
+    assert out.shape == (B, T, H)
+    for bb in range(B):
+        for t in range(T):
+            for h in range(H):
+                assert out[bb, t, h] == (bb * T * H + t * H + h) / 10
+    # [B, T, H]: unchanged
+    lam3 = torch.rand(B, T, H, dtype=D)
+    assert torch.equal(O.reshape_lambda(lam3, B, T, H), lam3)
+
+
 def test_round_through_keeps_gradient():
     x = torch.randn(10, dtype=D, requires_grad=True)
     y = O.round_through(x, torch.bfloat16)
