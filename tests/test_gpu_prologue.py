@@ -3,9 +3,12 @@ convolution (+ SiLU, + per-head L2 normalisation) and the gated RMSNorm, forward
 against plain float32 PyTorch restatements of the same operations on the same bf16 inputs; and a
 bf16 CCQ-GDN layer with the fused prologue against the same layer with the unfused one.
 
-Tolerances: relative L2 <= 4e-3 on bf16 outputs and gradients (each is rounded to bf16 once more
-than the fp32 restatement, 2^-9 relative per rounding); fp32 weight gradients <= 1e-3; caches
-exact (they are copies of inputs)."""
+Tolerances: relative L2 <= 2e-3 on bf16 outputs and gradients (north star; the bf16 rounding of
+the output alone is ~1.66e-3 of it), and the kernels' own error -- the bf16 output against the fp32
+restatement rounded to bf16 -- <= 5e-4; fp32 weight gradients <= 1e-3; caches exact (they are
+copies of inputs).  The fused-versus-unfused layer comparison at the end compares two bf16 layers
+(both sides rounded), so it is a consistency check at 1e-2; the layer's bar is held against the
+fp64 restatement in test_gpu_layers_bf16.py."""
 
 import copy
 
@@ -13,11 +16,12 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from tests._util import rel
+from tests._util import kern, rel
 
 pytestmark = pytest.mark.gpu
 
-TOL = 4e-3
+TOL = 2e-3
+TOL_KERNEL = 5e-4
 
 
 def _cuda():
@@ -109,14 +113,18 @@ def test_short_conv(case):
     torch.cuda.synchronize()
 
     errs = {"y": rel(y, y_r), "dx": rel(grads[0], grads_r[0]), "dw": rel(grads[1], grads_r[1])}
+    kerrs = {"y": kern(y, y_r), "dx": kern(grads[0], grads_r[0])}
     if hd:
         errs["yn"] = rel(yn, yn_r)
+        kerrs["yn"] = kern(yn, yn_r)
     if b is not None:
         errs["db"] = rel(grads[2], grads_r[2])
-    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
     for n in ("y", "yn", "dx"):
         if n in errs:
             assert errs[n] <= TOL, n
+            assert kerrs[n] <= TOL_KERNEL, n
     for n in ("dw", "db"):
         if n in errs:
             assert errs[n] <= 1e-3, n
@@ -135,7 +143,7 @@ def test_short_conv_matches_the_layer_module_path():
     y_f, s_f = m(x, None, True)
     y_t, s_t = ShortConvolution.forward(m.float(), x.float(), None, True)  # fp32 inputs: the torch path
     torch.cuda.synchronize()
-    assert rel(y_f, y_t) <= TOL
+    assert rel(y_f, y_t) <= TOL and kern(y_f, y_t) <= TOL_KERNEL
     assert torch.equal(s_f.float(), s_t.float())
 
 
@@ -162,11 +170,15 @@ def test_gated_rmsnorm(rows, dv, with_w):
     grads_r = torch.autograd.grad((yr * dy.float()).sum(), [xr, gr] + ([wr] if wr is not None else []))
     torch.cuda.synchronize()
     errs = {"y": rel(y, yr), "dx": rel(grads[0], grads_r[0]), "dg": rel(grads[1], grads_r[1])}
+    kerrs = {"y": kern(y, yr), "dx": kern(grads[0], grads_r[0]), "dg": kern(grads[1], grads_r[1])}
     if w is not None:
         errs["dw"] = rel(grads[2], grads_r[2])
-    print({n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    print({n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
     for n, e in errs.items():
         assert e <= (1e-3 if n == "dw" else TOL), n
+    for n, e in kerrs.items():
+        assert e <= TOL_KERNEL, n
 
 
 def test_gdn_layer_fused_prologue_matches_unfused():
