@@ -166,6 +166,16 @@ class ChunkCCQGDNFunction(torch.autograd.Function):
                 None, None, dgw, dgb)
 
 
+def _stock_mean(x):
+    """Key-sum gradients of the reference's stock cleaning path: ``chunk`` mode, the recurrent ops and
+    ``fused_ccq_clean`` clean through ``_CCQCleanQ`` (``ccq/ops/common/clean.py:691-748``), whose
+    backward returns no gradient for the initial key sum and ignores the one arriving at the final key
+    sum.  Detaching the initial key sum going in and the final one coming out of the fused operator
+    gives those gradients; the covariance states keep theirs (the reference reads z through fla's
+    GLA kernels, which differentiate the initial and the final covariance state)."""
+    return None if x is None else x.detach()
+
+
 def _default_scale(scale, K):
     return K ** -0.5 if scale is None else float(scale)
 
@@ -202,20 +212,21 @@ def chunk_ccq_gdn(q, k, v, lambda_h, g, beta, scale=None, initial_state=None, in
     """CCQ-GDN, stock ``chunk`` mode (reference ``ccq/ops/ccq_gdn/chunk.py:12-84``).
 
     Same mathematics as ``fused_chunk_ccq_gdn``; the reference's z-read + clean + backbone
-    pipeline is computed by the same kernels here.  ``transpose_state_layout`` selects
-    ``[N, H, V, K]`` backbone states (fla's option); ``cp_context`` (context parallelism) is
-    not supported on one GPU.
+    pipeline is computed by the same kernels here, with that pipeline's key-sum gradients
+    (``_stock_mean``: none for ``initial_mean_state``, none taken from the final key sum).
+    ``transpose_state_layout`` selects ``[N, H, V, K]`` backbone states (fla's option);
+    ``cp_context`` (context parallelism) is not supported on one GPU.
     """
     if cp_context is not None:
         raise NotImplementedError("chunk_ccq_gdn: context parallelism (cp_context) is not supported")
     if transpose_state_layout and initial_state is not None:
         initial_state = initial_state.transpose(-1, -2)
     o, s, c, m = fused_chunk_ccq_gdn(q, k, v, lambda_h, g, beta, scale, initial_state, initial_cov_state,
-                                     initial_mean_state, output_final_state, use_qk_l2norm_in_kernel, cu_seqlens,
-                                     position_offset, subtract_mean, enable_ccq, **kwargs)
+                                     _stock_mean(initial_mean_state), output_final_state, use_qk_l2norm_in_kernel,
+                                     cu_seqlens, position_offset, subtract_mean, enable_ccq, **kwargs)
     if transpose_state_layout and s is not None:
         s = s.transpose(-1, -2).contiguous()
-    return o, s, c, m
+    return o, s, c, _stock_mean(m)
 
 
 def fused_recurrent_ccq_gdn(q, k, v, lambda_h, g=None, gk=None, gv=None, beta=None, scale=None, initial_state=None,
@@ -227,7 +238,8 @@ def fused_recurrent_ccq_gdn(q, k, v, lambda_h, g=None, gk=None, gv=None, beta=No
     Without autograd (decode, generation) this runs the decode kernels: rank-1 updates of the
     cached S, C and m per token, with the optional per-key / per-value decays ``gk`` / ``gv`` of
     fla's recurrent gated delta rule.  When a gradient is needed it runs the chunk kernels, which
-    compute the same recurrence (without gk / gv) and have a backward.
+    compute the same recurrence (without gk / gv) and have a backward, with the reference's
+    key-sum gradients for this path (``_stock_mean``).
     """
     from .decode import gdn_decode, needs_grad
     if beta is None:
@@ -269,7 +281,8 @@ def fused_ccq_clean(q, k, lambda_h, *, initial_cov_state=None, initial_mean_stat
                     use_chunk=True, chunk_size=64):
     """Cleaning for the decode / short-sequence path (reference ``ccq/ops/ccq_gdn/fused_clean.py:34-83``).
 
-    Returns ``(q_clean, k, final_cov_state, final_mean_state, use_qk_l2norm_in_kernel)``.
+    Returns ``(q_clean, k, final_cov_state, final_mean_state, use_qk_l2norm_in_kernel)``; the key-sum
+    gradients are those of the reference's ``_CCQCleanQ`` (``_stock_mean``).
     """
     from .clean import fused_ccq_clean_read
     from .l2norm import l2norm
@@ -278,7 +291,8 @@ def fused_ccq_clean(q, k, lambda_h, *, initial_cov_state=None, initial_mean_stat
         k = l2norm(k, eps=1e-6)
         use_qk_l2norm_in_kernel = False
     qc, hf, mf = fused_ccq_clean_read(q, k, lambda_h, position_offset=position_offset,
-                                      initial_cov_state=initial_cov_state, initial_mean_state=initial_mean_state,
+                                      initial_cov_state=initial_cov_state,
+                                      initial_mean_state=_stock_mean(initial_mean_state),
                                       output_final_state=output_final_state, subtract_mean=subtract_mean,
                                       cu_seqlens=cu_seqlens)
-    return qc, k, hf, mf, use_qk_l2norm_in_kernel
+    return qc, k, hf, _stock_mean(mf), use_qk_l2norm_in_kernel

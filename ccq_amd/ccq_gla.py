@@ -18,7 +18,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, stream_of
-from .ccq_gdn import _Chunks, _default_scale
+from .ccq_gdn import _Chunks, _default_scale, _stock_mean
 from .clean import as_kernel_dtype, in_dtype
 from .clean import _check_qk, _f32, check_device, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd, \
     norm_cu_seqlens, reduce_dlambda, reshape_lambda_3d
@@ -197,9 +197,12 @@ def chunk_ccq_gla(q, k, v, lambda_h, g=None, scale=None, initial_state=None, ini
                   initial_mean_state=None, output_final_state=False, cu_seqlens=None, position_offset=0,
                   subtract_mean=True):
     """CCQ-GLA, stock ``chunk`` mode (reference ``ccq/ops/ccq_gla/chunk.py:17-59``).  Same mathematics as
-    ``fused_chunk_ccq_gla`` (z-read, cleaning, backbone); computed by the same kernels."""
-    return fused_chunk_ccq_gla(q, k, v, lambda_h, g, scale, initial_state, initial_cov_state, initial_mean_state,
-                               output_final_state, cu_seqlens, position_offset, subtract_mean)
+    ``fused_chunk_ccq_gla`` (z-read, cleaning, backbone); computed by the same kernels, with the stock
+    path's key-sum gradients (``_stock_mean``: the reference cleans through ``_CCQCleanQ`` here)."""
+    o, s, c, m = fused_chunk_ccq_gla(q, k, v, lambda_h, g, scale, initial_state, initial_cov_state,
+                                     _stock_mean(initial_mean_state), output_final_state, cu_seqlens, position_offset,
+                                     subtract_mean)
+    return o, s, c, _stock_mean(m)
 
 
 def fused_recurrent_ccq_gla(q, k, v, lambda_h, gk=None, gv=None, scale=None, initial_state=None,
@@ -211,7 +214,8 @@ def fused_recurrent_ccq_gla(q, k, v, lambda_h, gk=None, gv=None, scale=None, ini
     recurrence from the last token to the first (the cleaning runs forwards, as in the reference).
     Without autograd it runs the decode kernels; when a gradient is needed it runs the chunk
     kernels (same recurrence, with a backward): with ``reverse``, the cleaning followed by the GLA
-    backbone on the time-reversed sequences.  Gradients with ``gv`` are not supported."""
+    backbone on the time-reversed sequences, with the reference's key-sum gradients for this path
+    (``_stock_mean``).  Gradients with ``gv`` are not supported."""
     from .decode import gla_decode, needs_grad
     if not needs_grad(q, k, v, lambda_h, gk, gv, initial_state, initial_cov_state, initial_mean_state):
         dt = q.dtype
@@ -230,8 +234,8 @@ def fused_recurrent_ccq_gla(q, k, v, lambda_h, gk=None, gv=None, scale=None, ini
     if reverse:
         return _reverse_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state, initial_mean_state,
                             output_final_state, cu_seqlens, position_offset, subtract_mean)
-    return fused_chunk_ccq_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state, initial_mean_state,
-                               output_final_state, cu_seqlens, position_offset, subtract_mean)
+    return chunk_ccq_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state, initial_mean_state,
+                         output_final_state, cu_seqlens, position_offset, subtract_mean)
 
 
 def _time_flip(x):
@@ -253,7 +257,7 @@ def _reverse_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state,
     qn, kn = l2norm(q), l2norm(k)
     qc, hf, mf = fused_ccq_clean_read(qn, kn, lambda_h, position_offset=position_offset,
                                       initial_cov_state=initial_cov_state,
-                                      initial_mean_state=initial_mean_state if subtract_mean else None,
+                                      initial_mean_state=_stock_mean(initial_mean_state) if subtract_mean else None,
                                       output_final_state=output_final_state, subtract_mean=subtract_mean,
                                       cu_seqlens=cu_seqlens)
     cu_r, s0 = None, initial_state
@@ -268,7 +272,7 @@ def _reverse_gla(q, k, v, lambda_h, gk, scale, initial_state, initial_cov_state,
         return o, None, None, None
     if cu_seqlens is not None:
         s = s.flip(0)
-    return o, s, hf, mf
+    return o, s, hf, _stock_mean(mf)
 
 
 def chunk_gla(q, k, v, g=None, scale=None, initial_state=None, output_final_state=False, cu_seqlens=None, **kwargs):

@@ -22,6 +22,21 @@ from .clean import check_device
 __all__ = ["short_conv", "gated_rmsnorm"]
 
 
+def last_inputs(cache: Optional[torch.Tensor], W: int) -> Optional[torch.Tensor]:
+    """A convolution cache as this library keeps it, ``[N, D, W-1]`` (each sequence's previous W-1
+    inputs, oldest first).  A cache of width W -- the last W inputs, the form fla's ShortConvolution is
+    understood to keep (not pinned: fla is not available here) -- is accepted and its last W-1 columns
+    used; other widths raise."""
+    if cache is None:
+        return None
+    if cache.shape[-1] == W:
+        return cache[..., 1:]
+    if cache.shape[-1] != W - 1:
+        raise ValueError(f"convolution cache of width {cache.shape[-1]} for a kernel of {W} taps "
+                         f"(expected {W - 1}, or {W})")
+    return cache
+
+
 def _seqs(x: torch.Tensor, cu_seqlens: Optional[torch.Tensor]):
     B, T = x.shape[:2]
     if cu_seqlens is None:
@@ -84,9 +99,11 @@ def short_conv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tenso
                output_final_state: bool = False, eps: float = 1e-6):
     """Causal depthwise convolution over time of ``x [B, T, D]`` (bf16, CUDA) with ``weight``
     ``[D, 1, W]`` (or ``[D, W]``), optional ``bias [D]``, SiLU when ``activation``; ``cache``
-    ``[N, D, W-1]`` holds each sequence's previous W-1 inputs.  With ``head_dim`` it also returns the
+    ``[N, D, W-1]`` holds each sequence's previous W-1 inputs (``[N, D, W]`` is accepted:
+    ``last_inputs``); the returned cache is ``[N, D, W-1]``.  With ``head_dim`` it also returns the
     per-head L2-normalised output.  Returns ``(y, y_norm, final_cache)`` (None where not asked)."""
     check_device(x.device, weight=weight, bias=bias, cache=cache)
+    cache = last_inputs(cache, weight.shape[-1])
     want_norm = head_dim is not None
     return ShortConvFunction.apply(x, weight, bias, cache, cu_seqlens, bool(activation),
                                    int(head_dim) if want_norm else 8, bool(want_y), want_norm,

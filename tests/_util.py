@@ -52,3 +52,22 @@ def gdn_inputs(B, T, H, K, V, seed=0, with_state=False, device="cuda"):
     s0 = torch.randn(B, H, K, V, generator=gen) * 0.1 if with_state else None
     out = dict(q=q, k=k, v=v, g=g, beta=beta, s0=s0)
     return {n: (t.to(device) if t is not None else None) for n, t in out.items()}, gen
+
+
+class _RoundBoth(torch.autograd.Function):
+    """A tensor boundary in a narrower dtype between two operators: the value is rounded to that dtype
+    and so is the gradient that crosses it (what autograd does to a bf16 tensor that one op returns and
+    the next consumes)."""
+
+    @staticmethod
+    def forward(ctx, x, dtype):
+        ctx.dtype = dtype
+        return x.to(dtype).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(ctx.dtype).to(g.dtype), None
+
+
+def round_both(x: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:
+    return _RoundBoth.apply(x, dtype)

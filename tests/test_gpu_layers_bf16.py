@@ -37,7 +37,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import ccq_oracle as O
-from tests._util import faithful_excess, kern, rel
+from tests._util import faithful_excess, kern, rel, round_both
 
 pytestmark = pytest.mark.gpu
 
@@ -53,18 +53,6 @@ def _cuda():
         pytest.skip("no GPU")
     import ccq_amd  # noqa: F401
     return torch.device("cuda")
-
-
-class _Round(torch.autograd.Function):
-    """A bf16 tensor boundary: the value is rounded to bf16, and so is the gradient that crosses it."""
-
-    @staticmethod
-    def forward(ctx, x):
-        return x.to(BF).to(x.dtype)
-
-    @staticmethod
-    def backward(ctx, g):
-        return g.to(BF).to(g.dtype)
 
 
 def _r(x):
@@ -88,7 +76,7 @@ class _SigmoidBF(torch.autograd.Function):
         return _r(_r(_r(g) * _r(1 - y)) * y)
 
 
-_Q = _Round.apply
+_Q = round_both          # a bf16 tensor boundary: value and gradient rounded to bf16
 _sig = _SigmoidBF.apply
 
 

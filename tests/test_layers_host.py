@@ -40,3 +40,19 @@ def test_short_convolution_cache_and_varlen():
     cu = torch.tensor([0, 20, 40])
     pk, _ = conv(x.reshape(1, 40, 8), cu_seqlens=cu)
     assert torch.allclose(pk.view(2, 20, 8), full)
+
+
+def test_conv_cache_width_w_is_accepted():
+    # a cache holding the last W inputs gives the same result as one holding the last W - 1
+    import torch
+    from ccq_amd.layers import ShortConvolution
+    torch.manual_seed(0)
+    m = ShortConvolution(16, 4, bias=False, activation='silu').double()
+    x = torch.randn(2, 5, 16, dtype=torch.float64)
+    full = torch.randn(2, 16, 4, dtype=torch.float64)
+    y_w, c_w = m(x, full, True)
+    y_w1, c_w1 = m(x, full[..., 1:], True)
+    assert torch.equal(y_w, y_w1) and torch.equal(c_w, c_w1) and c_w.shape == (2, 16, 3)
+    import pytest
+    with pytest.raises(ValueError):
+        m(x, full[..., :2], True)
