@@ -60,36 +60,6 @@ def _gla_backward(q16, q32, k, v, gk32, ch: _Chunks, saved, do, dsfin, sfin, sca
     return dq32, dk32, dv, dgk, ds0
 
 
-# The chunk kernels split the pairwise decay e^(b_t - b_s) inside a 64-token chunk at a reference
-# row in the middle of each 32-token block; a factor above 1 then spans at most 16 tokens, and the
-# split is exact while 16 consecutive tokens' log decay stays above this bound (e^80 < fp32 max).
-DECAY_WINDOW, DECAY_FLOOR = 16, -80.0
-
-
-def check_decay_range(gk32: Optional[torch.Tensor], cu_seqlens: Optional[torch.Tensor]) -> None:
-    """Raise for a log decay the chunk kernels cannot represent: some DECAY_WINDOW consecutive
-    tokens of one sequence summing below DECAY_FLOOR in a channel.  That needs a per-token decay
-    below DECAY_FLOOR / DECAY_WINDOW somewhere, which is checked first (one device reduction);
-    only then are the windows summed.  Skipped while a graph is being captured."""
-    if gk32 is None or gk32.numel() == 0 or torch.cuda.is_current_stream_capturing():
-        return
-    if bool((gk32.amin() >= DECAY_FLOOR / DECAY_WINDOW).item()):
-        return
-    B, T = gk32.shape[:2]
-    bounds = [0, T] if cu_seqlens is None else [int(x) for x in cu_seqlens.tolist()]
-    for b in range(B):
-        for s0, s1 in zip(bounds[:-1], bounds[1:]):
-            g = gk32[b, s0:s1]
-            if g.shape[0] == 0:
-                continue
-            c = torch.cumsum(g, 0)
-            c = torch.cat([torch.zeros_like(c[:1]), c], 0)
-            w = min(DECAY_WINDOW, g.shape[0])
-            if bool(((c[w:] - c[:-w]).amin() < DECAY_FLOOR).item()):
-                raise ValueError(f"gk: the log decay over {DECAY_WINDOW} consecutive tokens falls below {DECAY_FLOOR}, "
-                                 "which the chunk kernels cannot represent (e^80 bounds their split decay factor)")
-
-
 class ChunkCCQGLAFunction(torch.autograd.Function):
     """l2norm -> CCQ cleaning -> gated linear attention (chunk form), forward and backward on the GPU.
 
@@ -116,8 +86,7 @@ class ChunkCCQGLAFunction(torch.autograd.Function):
         if use_l2norm:
             qn, rq = l2norm_fwd(q)
             kn, rk = l2norm_fwd(k)
-        gk32 = _f32(gk)
-        check_decay_range(gk32, cu_seqlens)
+        gk32 = _f32(gk)   # any log decay <= 0: the kernels never form a factor above e^80
         s0 = _f32(initial_state)
         gw, gb = _f32(gate_w), _f32(gate_b)
         h0 = _f32(initial_cov_state)

@@ -13,10 +13,15 @@
 //   dv = A^T dO + (K o e^{b_L - b}) dS
 //   dG_t = q_t o dq_t - k_t o dk_t (+ rowsum(dS_final o S_final) at the last token),
 //   dgk = suffix sum of dG over the sequence.
-// The pairwise factors e^{b_t - b_s} inside a chunk are split at a reference row m in the middle
-// of each 32-row block (m = 16, 48, clamped to the last valid row): e^{b_t - b_m} e^{b_m - b_s}.
-// A factor is > 1 only for a token at most 16 rows from m, so the split stays exact in fp32 while
-// the log decay over any 16 consecutive tokens stays above -80 (e^80 < fp32 max).
+// The pairwise factors e^{b_t - b_s} (s <= t) inside a chunk enter the products split at a
+// reference row m, e^{b_t - b_m} e^{b_m - b_s}, with decays gk <= 0:
+// * between the two 32-row blocks (t >= 32 > s) at m = 32, where both factors are <= 1: exact
+//   for any decay;
+// * inside a diagonal 32-row block at its middle row (16, 48, clamped to the last valid row), where
+//   a factor is > 1 only across half the block: used while the log decay over each half stays above
+//   -kSplitRange in every channel of the wave (e^80 < fp32 max); otherwise that block is formed with
+//   one exponential per pair, e^{b_t - b_s} <= 1, as a sum over the channels in fp32.
+// So every decay gives a finite result; the per-pair form only costs time in the blocks that need it.
 //
 // Kernels:
 //   gla_intra        chunk-parallel: b (written for the later stages) and A
@@ -42,6 +47,17 @@ constexpr int BT = 64;
 constexpr int KS = 64;            // channel slab of the chunk-parallel kernels
 constexpr int LDF = KS + 4;       // fp32 slab row stride (LDS)
 constexpr int LDH = 64 + 8;       // bf16 64-wide row stride (LDS)
+constexpr float kSplitRange = 80.f;   // largest log factor a split decay may carry (e^80 < fp32 max)
+
+// True when the split of the pairwise decay factors at row m of the 32-row block starting at row
+// r0 stays below e^kSplitRange for channel column c of b (rows past L - 1 hold b_{L-1}), in every
+// lane of the wave; a NaN range counts as unsafe.
+__device__ __forceinline__ bool split_ok(const float* b, int ld, int r0, int m, int L, int c) {
+  const int first = min(r0, L - 1), last = min(r0 + 31, L - 1);
+  const float bm = b[m * ld + c];
+  const float r = fmaxf(b[first * ld + c] - bm, bm - b[last * ld + c]);
+  return __ballot(!(r <= kSplitRange)) == 0;
+}
 
 __device__ __forceinline__ bool gla_chunk(const GlaArgs& a, int gc, int& n, int& c0, long& bos, int& L) {
   if (a.cu) {
@@ -62,13 +78,17 @@ __device__ __forceinline__ bool gla_chunk(const GlaArgs& a, int gc, int& n, int&
   return true;
 }
 
-// 64 rows x 64 columns of fp32 (g32) or bf16 (g16) global rows into fp32 LDS [64][LDF]; rows >= nvalid = 0.
-__device__ __forceinline__ void slab_to_f32(float* dst, const float* g32, const bf16* g16, long gstride, int nvalid) {
+// 64 rows x 64 columns of fp32 (g32) or bf16 (g16) global rows into fp32 LDS [64][LDF]; rows >= nvalid
+// = 0, or (hold_last, fp32 only) a copy of row nvalid - 1 -- for the cumulative decay, which stays at
+// its last value past the end of a chunk.
+__device__ __forceinline__ void slab_to_f32(float* dst, const float* g32, const bf16* g16, long gstride, int nvalid,
+                                            bool hold_last = false) {
   if (g32) {
     for (int idx = threadIdx.x; idx < BT * 16; idx += kThreads) {
       const int r = idx >> 4, c = (idx & 15) * 4;
       f32x4 v;
       if (r < nvalid) v = *(const f32x4*)(g32 + (long)r * gstride + c);
+      else if (hold_last) v = *(const f32x4*)(g32 + (long)(nvalid - 1) * gstride + c);
       else v[0] = v[1] = v[2] = v[3] = 0.f;
       *(f32x4*)(dst + r * LDF + c) = v;
     }
@@ -186,7 +206,10 @@ __global__ __launch_bounds__(kThreads) void gla_intra_kernel(const GlaArgs a) {
   const long tok0 = bos + c0;
   const long rsk = (long)a.H * K;
   const int I = (w == 0) ? 0 : 1, J = (w == 2) ? 1 : 0;
-  const int mI = min(32 * I + 16, L - 1);  // reference row (clamped into the valid rows)
+  // reference row: the block boundary for the off-diagonal block, the middle of a diagonal block
+  // (clamped into the valid rows)
+  const bool diag = I == J;
+  const int mI = diag ? min(32 * I + 16, L - 1) : min(32, L - 1);
 
   f32x16 acc = zero16();
   for (int s0 = 0; s0 < K; s0 += KS) {
@@ -216,7 +239,7 @@ __global__ __launch_bounds__(kThreads) void gla_intra_kernel(const GlaArgs a) {
                 a.q32 ? nullptr : (const bf16*)a.q16 + tok0 * rsk + (long)h * K + s0, rsk, L);
     slab_to_f32(sK, nullptr, (const bf16*)a.k + tok0 * rsk + (long)h * K + s0, rsk, L);
     __syncthreads();
-    if (w < 3) {
+    if (w < 3 && (!diag || split_ok(sB, LDF, 32 * I, mI, L, l))) {
       const int r = 32 * I + (l & 31), s = 32 * J + (l & 31);
       for (int k0 = 0; k0 < KS; k0 += 16) {
         const int kb = k0 + ((l >> 5) << 3);
@@ -232,6 +255,18 @@ __global__ __launch_bounds__(kThreads) void gla_intra_kernel(const GlaArgs a) {
         split8(xa, ah, al);
         split8(xb, bh, bl);
         mfma3(acc, ah, al, bh, bl);
+      }
+    } else if (w < 3) {
+      // a diagonal block whose decay is too steep to split: one exponential per pair (<= 1)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = 32 * I + acc_row(i), s = 32 * J + acc_col();
+        if (s <= t && t < L) {
+          float sum = 0.f;
+          for (int c = 0; c < KS; ++c)
+            sum += sQ[t * LDF + c] * sK[s * LDF + c] * __expf(sB[t * LDF + c] - sB[s * LDF + c]);
+          acc[i] += sum;
+        }
       }
     }
     __syncthreads();
@@ -609,7 +644,7 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dqk_kernel(const GlaArgs a) 
   slab_to_f32(sQ, a.q32 ? a.q32 + tok0 * rsk + (long)h * K + s0 : nullptr,
               a.q32 ? nullptr : (const bf16*)a.q16 + tok0 * rsk + (long)h * K + s0, rsk, L);
   slab_to_f32(sK, nullptr, (const bf16*)a.k + tok0 * rsk + (long)h * K + s0, rsk, L);
-  slab_to_f32(sBb, a.bcum + tok0 * rsk + (long)h * K + s0, nullptr, rsk, L);
+  slab_to_f32(sBb, a.bcum + tok0 * rsk + (long)h * K + s0, nullptr, rsk, L, true);
   if (w < 3) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -643,51 +678,107 @@ __global__ __launch_bounds__(kThreads) void gla_bwd_dqk_kernel(const GlaArgs a) 
                      : 0.f;
   }
 
-  // intra-chunk parts: dq rows of block tr use reference row mI = 32 tr + 16 and keys s < 32 (tr + 1);
-  // dk rows (keys) of block tr use reference mJ = 32 tr + 16 and queries t >= 32 tr.
-  const int mR = min(32 * tr + 16, L - 1);
-  f32x16 dqi = zero16(), dki = zero16();
+  // intra-chunk parts.  The dq rows of block tr take the keys of block tr (the diagonal block) and,
+  // for tr = 1, the keys of block 0; the dk rows (keys) of block tr take the queries of block tr and,
+  // for tr = 0, the queries of block 1.  The off-diagonal block (dxo) splits its pairwise factor at
+  // row mB = 32, where both factors are <= 1; the diagonal block at its middle row mR while that is
+  // safe for this wave's channels (split_ok), else with one exponential per pair, in which case dqi
+  // and dki carry their factors whole.
+  const int mR = min(32 * tr + 16, L - 1), mB = min(32, L - 1);
+  f32x16 dqi = zero16(), dki = zero16(), dxo = zero16();
+  const bool fast = split_ok(sBb, LDF, 32 * tr, mR, L, tc * 32 + (l & 31));
   {
     const int c = tc * 32 + (l & 31);
-    const float bm = sBb[mR * LDF + c];
-    for (int k0 = 0; k0 < 32 * (tr + 1); k0 += 16) {
-      bf16x8 ah, al, bh, bl;
-      frag_rm_f32(sdA + tr * 32 * (BT + 1) + k0, BT + 1, ah, al);
-      float xb[8];
-      const int kb = k0 + ((l >> 5) << 3);
+    const float bm = sBb[mR * LDF + c], bb = sBb[mB * LDF + c];
+    if (tr == 1) {
+      for (int k0 = 0; k0 < 32; k0 += 16) {      // dq: keys of block 0
+        bf16x8 ah, al, bh, bl;
+        frag_rm_f32(sdA + 32 * (BT + 1) + k0, BT + 1, ah, al);
+        float xb[8];
+        const int kb = k0 + ((l >> 5) << 3);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int s = kb + i;
-        xb[i] = sK[s * LDF + c] * __expf(bm - sBb[s * LDF + c]);
+        for (int i = 0; i < 8; ++i) {
+          const int s = kb + i;
+          xb[i] = sK[s * LDF + c] * __expf(bb - sBb[s * LDF + c]);
+        }
+        split8(xb, bh, bl);
+        mfma3(dxo, ah, al, bh, bl);
       }
-      split8(xb, bh, bl);
-      mfma3(dqi, ah, al, bh, bl);
+    } else {
+      for (int k0 = 32; k0 < BT; k0 += 16) {     // dk: queries of block 1
+        bf16x8 ah, al, bh, bl;
+        frag_cm_f32(sdA + k0 * (BT + 1), BT + 1, ah, al);
+        float xb[8];
+        const int kb = k0 + ((l >> 5) << 3);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int t = kb + i;
+          xb[i] = sQ[t * LDF + c] * __expf(sBb[t * LDF + c] - bb);
+        }
+        split8(xb, bh, bl);
+        mfma3(dxo, ah, al, bh, bl);
+      }
     }
-    for (int k0 = 32 * tr; k0 < BT; k0 += 16) {
-      bf16x8 ah, al, bh, bl;
-      frag_cm_f32(sdA + tr * 32 + k0 * (BT + 1), BT + 1, ah, al);
-      float xb[8];
-      const int kb = k0 + ((l >> 5) << 3);
+    if (fast) {
+      for (int k0 = 32 * tr; k0 < 32 * tr + 32; k0 += 16) {
+        bf16x8 ah, al, bh, bl;
+        frag_rm_f32(sdA + tr * 32 * (BT + 1) + k0, BT + 1, ah, al);
+        float xb[8];
+        const int kb = k0 + ((l >> 5) << 3);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int t = kb + i;
-        xb[i] = sQ[t * LDF + c] * __expf(sBb[t * LDF + c] - bm);
+        for (int i = 0; i < 8; ++i) {
+          const int s = kb + i;
+          xb[i] = sK[s * LDF + c] * __expf(bm - sBb[s * LDF + c]);
+        }
+        split8(xb, bh, bl);
+        mfma3(dqi, ah, al, bh, bl);
       }
-      split8(xb, bh, bl);
-      mfma3(dki, ah, al, bh, bl);
+      for (int k0 = 32 * tr; k0 < 32 * tr + 32; k0 += 16) {
+        bf16x8 ah, al, bh, bl;
+        frag_cm_f32(sdA + tr * 32 + k0 * (BT + 1), BT + 1, ah, al);
+        float xb[8];
+        const int kb = k0 + ((l >> 5) << 3);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int t = kb + i;
+          xb[i] = sQ[t * LDF + c] * __expf(sBb[t * LDF + c] - bm);
+        }
+        split8(xb, bh, bl);
+        mfma3(dki, ah, al, bh, bl);
+      }
+    } else {
+      // dq_r = sum_{s <= r} dA_rs k_s e^{b_r - b_s},  dk_r = sum_{t >= r} dA_tr q_t e^{b_t - b_r}
+      // over the block's valid rows, one exponential (<= 1) per pair
+      const int cc = tc * 32 + acc_col(), r0 = 32 * tr, r1 = min(32 * tr + 32, L);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = r0 + acc_row(i);
+        float sq = 0.f, sk = 0.f;
+        if (r < L) {
+          const float br = sBb[r * LDF + cc];
+          for (int j = r0; j <= r; ++j)
+            sq += sdA[r * (BT + 1) + j] * sK[j * LDF + cc] * __expf(br - sBb[j * LDF + cc]);
+          for (int j = r; j < r1; ++j)
+            sk += sdA[j * (BT + 1) + r] * sQ[j * LDF + cc] * __expf(sBb[j * LDF + cc] - br);
+        }
+        dqi[i] = sq;
+        dki[i] = sk;
+      }
     }
   }
   __syncthreads();
   // combine, write dq/dk, form dG
   {
     const int c = tc * 32 + acc_col();
-    const float bm = sBb[mR * LDF + c], bl_ = sBb[(L - 1) * LDF + c];
+    const float bm = sBb[mR * LDF + c], bb = sBb[mB * LDF + c], bl_ = sBb[(L - 1) * LDF + c];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int t = tr * 32 + acc_row(i);
       const float bt = sBb[t * LDF + c];
-      const float dq = a.scale * __expf(bt) * dqr[i] + __expf(bt - bm) * dqi[i];
-      const float dk = __expf(bl_ - bt) * dkr[i] + __expf(bm - bt) * dki[i];
+      float dq = a.scale * __expf(bt) * dqr[i] + (fast ? __expf(bt - bm) * dqi[i] : dqi[i]);
+      float dk = __expf(bl_ - bt) * dkr[i] + (fast ? __expf(bm - bt) * dki[i] : dki[i]);
+      if (tr == 1) dq += __expf(bt - bb) * dxo[i];
+      else dk += __expf(bb - bt) * dxo[i];
       float g = 0.f;
       if (t < L) {
         a.dq32[(tok0 + t) * rsk + (long)h * K + s0 + c] = dq;

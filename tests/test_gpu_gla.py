@@ -136,20 +136,68 @@ def test_fused_ccq_gla(case):
         assert e <= TOL_KERNEL, n
 
 
-def test_gla_decay_range_guard():
-    """A log decay whose 16-token window sum falls below -80 (beyond the chunk kernels' split
-    decay factor) raises instead of returning inf / NaN; one just inside the bound runs."""
+STEEP_CASES = [
+    # T, K, V, kind
+    (150, 64, 64, "window"),    # one channel: 16 tokens at -6.5 (-104 over the window) inside a mild decay
+    (200, 128, 64, "steep"),    # every channel: -2 .. -12 per token (-30 .. -190 over 16 tokens)
+    (96, 64, 128, "mixed"),     # half the channels steep, half mild; a partial last chunk
+]
+
+
+@pytest.mark.parametrize("case", STEEP_CASES, ids=[c[3] for c in STEEP_CASES])
+def test_gla_steep_decay(case):
+    """Log decays whose 16-token sums fall far below -80, where a split of the pairwise factor
+    e^(b_t - b_s) in the middle of a 32-token block would overflow: the kernels form those blocks with
+    one exponential per pair, the blocks between the two halves of a chunk at their boundary.  Output,
+    final state and every gradient (dgk included) against the oracle, whose chunked form takes
+    differences of cumulative decays in fp64."""
     dev = _cuda()
-    from ccq_amd import fused_chunk_ccq_gla
-    B, T, H, K, V = 1, 64, 1, 64, 64
-    q = torch.randn(B, T, H, K, device=dev).bfloat16()
-    k = torch.randn(B, T, H, K, device=dev).bfloat16()
-    v = torch.randn(B, T, H, V, device=dev).bfloat16()
-    lam = torch.full((B, T, H, 1), 0.5, device=dev)
-    gk = torch.full((B, T, H, K), -0.1, device=dev)
-    gk[0, 20:36, 0, 3] = -5.2                 # 16 tokens summing to -83.2
-    with pytest.raises(ValueError, match="log decay"):
-        fused_chunk_ccq_gla(q, k, v, lam, gk)
-    gk[0, 20:36, 0, 3] = -4.9                 # -78.4 over the window: representable
-    o, _, _, _ = fused_chunk_ccq_gla(q, k, v, lam, gk)
-    assert torch.isfinite(o.float()).all()
+    from ccq_amd import chunk_gla, fused_chunk_ccq_gla
+    T, K, V, kind = case
+    B, H = 1, 2
+    print(f"test_gla_steep_decay {case}", flush=True)
+    gen = torch.Generator().manual_seed(41)
+    gk = (F.logsigmoid(torch.randn(B, T, H, K, generator=gen) * 2.0) / 16)
+    if kind == "window":
+        gk[0, 40:56, 1, 5] = -6.5
+    elif kind == "steep":
+        gk = -(2.0 + 10.0 * torch.rand(B, T, H, K, generator=gen))
+    else:
+        gk[..., : K // 2] = -(3.0 + 9.0 * torch.rand(B, T, H, K // 2, generator=gen))
+    x = {
+        "q": bf(l2n(torch.randn(B, T, H, K, generator=gen))),
+        "k": bf(l2n(torch.randn(B, T, H, K, generator=gen))),
+        "v": bf(torch.randn(B, T, H, V, generator=gen)),
+        "gk": gk.float(),
+        "s0": torch.randn(B, H, K, V, generator=gen) * 0.1,
+    }
+    do = bf(torch.randn(B, T, H, V, generator=gen))
+    dsf = torch.randn(B, H, K, V, generator=gen) * 0.1
+    d = torch.float64
+    ref = {n: t.to(d).requires_grad_() for n, t in x.items()}
+    o_r, s_r = O.gla_chunked(ref["q"], ref["k"], ref["v"], ref["gk"], h0=ref["s0"])
+    ((o_r * do.to(d)).sum() + (s_r * dsf.to(d)).sum()).backward()
+    g = {n: t.to(dev).requires_grad_() for n, t in x.items()}
+    o, s = chunk_gla(g["q"], g["k"], g["v"], g["gk"], initial_state=g["s0"], output_final_state=True)
+    ((o.float() * do.to(dev).float()).sum() + (s * dsf.to(dev)).sum()).backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all() and all(torch.isfinite(g[n].grad).all() for n in g)
+    errs = {"o": rel(o, o_r), "S": rel(s, s_r)}
+    kerrs = {"o": kern(o, o_r)}
+    for n in x:
+        errs["d" + n] = rel(g[n].grad, ref[n].grad)
+        if g[n].grad.dtype == torch.bfloat16:
+            kerrs["d" + n] = kern(g[n].grad, ref[n].grad)
+    print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
+          flush=True)
+    for n, e in errs.items():
+        assert e <= TOL_BF16, n
+    for n, e in kerrs.items():
+        assert e <= TOL_KERNEL, n
+    # the same decay behind the cleaning (fused op): finite and equal to the oracle
+    lam = bf(torch.sigmoid(torch.randn(B, T, H, 1, generator=gen)))
+    o2, _, _, _ = fused_chunk_ccq_gla(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), lam.to(dev), x["gk"].to(dev))
+    o2_r, _, _, _ = O.ccq_gla_forward(x["q"].to(d), x["k"].to(d), x["v"].to(d), lam.to(d), x["gk"].to(d),
+                                      l2norm_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert rel(o2, o2_r) <= TOL_BF16
