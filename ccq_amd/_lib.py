@@ -56,8 +56,10 @@ SIGNATURES = {
     "ccq_gated_rmsnorm_bwd": (_I, [_P] * 9 + [_I64, _I, _P]),
     "ccq_l2norm_fwd": (_I, [_P, _P, _P, _I64, _I, _F, _P]),
     "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
+    "ccq_gdn_decode_prologue": (_I, [_P] * 5 + [_I64] + [_P] * 19 + [_I] * 7 + [_F, _P]),
     "ccq_timing_enable": (_I, [_I]),
     "ccq_timing_reset": (_I, []),
+    "ccq_timing_select": (_I, [ctypes.c_char_p]),
     "ccq_timing_read": (_I, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
 }
 
@@ -110,6 +112,11 @@ KERNELS = ("conv_fwd", "conv_bwd", "gnorm_fwd", "gnorm_bwd",
 
 def timing_enable(on: bool) -> None:
     call("ccq_timing_enable", int(bool(on)))
+
+
+def timing_select(kernel) -> None:
+    """Record timing events for `kernel` only (None: every kernel)."""
+    call("ccq_timing_select", None if kernel is None else kernel.encode())
 
 
 def timing_reset() -> None:

@@ -25,6 +25,7 @@ hipError_t launch_gdn_stage(int stage, const GdnArgs& a, int K, int V, hipStream
 hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_conv(int stage, const ConvArgs& a, int blocks, hipStream_t st);
 hipError_t launch_gnorm(int stage, const GNormArgs& a, int blocks, hipStream_t st);
+hipError_t launch_decode_prologue(const DecProArgs& a, hipStream_t st);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
@@ -103,6 +104,7 @@ int clean_k_ok(int K) { return K == 32 || K == 64 || K == 128 || K == 256; }
 struct TimingState {
   std::mutex mu;
   bool on = false;
+  std::string only;   // non-empty: time only the kernel of this name
   std::map<std::string, std::vector<std::pair<hipEvent_t, hipEvent_t>>> pending;
   std::map<std::string, std::pair<double, int64_t>> done;
 };
@@ -118,7 +120,7 @@ hipError_t timed(const char* name, hipStream_t st, F&& launch) {
   TimingState& t = timing();
   {
     std::lock_guard<std::mutex> g(t.mu);
-    if (!t.on) return launch();
+    if (!t.on || (!t.only.empty() && t.only != name)) return launch();
   }
   // timing-only events: no system-scope fence on record (that fence writes back and invalidates
   // the caches between every two timed kernels and shows up as idle time before each of them)
@@ -714,6 +716,34 @@ int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, con
                     "ccq_gated_rmsnorm_bwd(dweight)");
 }
 
+int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, const void* xa, const void* xb,
+                            int64_t ldx, const void* wq, const void* wk, const void* wv, const void* bq,
+                            const void* bk, const void* bv, void* cq, void* ck, void* cv, const void* lam_w,
+                            const void* lam_b, const void* A_log, const void* dt_bias, void* q, void* k, void* v,
+                            float* lam, float* g, float* beta, int B, int T, int H, int K, int V, int W,
+                            int allow_neg_eigval, float eps, void* stream) {
+  const char* who = "ccq_gdn_decode_prologue";
+  if (B < 0 || T < 0) return fail(CCQ_ERR_SHAPE, "%s: negative sizes (B=%d T=%d)", who, B, T);
+  if (H < 1 || H > 32) return fail(CCQ_ERR_SHAPE, "%s: H=%d not in [1, 32]", who, H);
+  if (K < 8 || K > 512 || (K & (K - 1))) return fail(CCQ_ERR_SHAPE, "%s: K=%d must be a power of two in [8, 512]", who, K);
+  if (V <= 0 || V % 8) return fail(CCQ_ERR_SHAPE, "%s: V=%d must be a positive multiple of 8", who, V);
+  if (W < 1 || W > 8) return fail(CCQ_ERR_SHAPE, "%s: kernel size W=%d not in [1, 8]", who, W);
+  if (ldx < 0 || ldx % 8) return fail(CCQ_ERR_ALIGN, "%s: row stride ldx=%lld must be a multiple of 8", who, (long long)ldx);
+  if (!xq || !xk || !xv || !xa || !xb || !wq || !wk || !wv || !lam_w || !A_log || !dt_bias || !q || !k || !v || !lam ||
+      !g || !beta)
+    return fail(CCQ_ERR_NULL, "%s: a required pointer is NULL", who);
+  if (W > 1 && (!cq || !ck || !cv)) return fail(CCQ_ERR_NULL, "%s: W > 1 needs the three caches", who);
+  if (!aligned16(xq) || !aligned16(xk) || !aligned16(xv) || !aligned16(q) || !aligned16(k) || !aligned16(v))
+    return fail(CCQ_ERR_ALIGN, "%s: the q, k, v rows and outputs must be 16-byte aligned", who);
+  DecProArgs a{};
+  a.xq = xq; a.xk = xk; a.xv = xv; a.xa = xa; a.xb = xb; a.ldx = ldx;
+  a.wq = wq; a.wk = wk; a.wv = wv; a.bq = bq; a.bk = bk; a.bv = bv; a.cq = cq; a.ck = ck; a.cv = cv;
+  a.lw = lam_w; a.lb = lam_b; a.alog = A_log; a.dtb = dt_bias; a.q = q; a.k = k; a.v = v;
+  a.lam = lam; a.g = g; a.beta = beta;
+  a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.W = W; a.neg_eig = allow_neg_eigval ? 1 : 0; a.eps = eps;
+  return hip_status(launch_decode_prologue(a, (hipStream_t)stream), who);
+}
+
 }  // extern "C"
 
 extern "C" {
@@ -722,6 +752,13 @@ int ccq_timing_enable(int on) {
   TimingState& t = timing();
   std::lock_guard<std::mutex> g(t.mu);
   t.on = on != 0;
+  return CCQ_OK;
+}
+
+int ccq_timing_select(const char* kernel) {
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> g(t.mu);
+  t.only = kernel ? kernel : "";
   return CCQ_OK;
 }
 

@@ -40,6 +40,42 @@ struct ConvArgs {
   float eps;
 };
 
+// Decode prologue of a CCQ-GDN layer (one token step of B sequences, T tokens each): from the rows of
+// the layer's input projections (bf16, row r = b T + t, `ldx` elements apart) -- q, k, v (conv inputs)
+// and a, b (decay and beta logits) -- the short convolutions + SiLU with in-place bf16 caches
+// [B, D, W-1], the per-head L2 normalisation of q and k, lambda = sigmoid(lw . q_act + lb) (the
+// layer's dense gate on the un-normalised activation), beta = sigmoid(b) and
+// g = -exp(A_log) softplus(a + dt_bias), written to the decode step's input buffers.
+struct DecProArgs {
+  const void* xq;           // bf16 rows: q projection (H K), k projection (H K), v projection (H V)
+  const void* xk;
+  const void* xv;
+  const void* xa;           // bf16 rows: a projection (H), b projection (H)
+  const void* xb;
+  long ldx;                 // elements between consecutive token rows
+  const void* wq;           // bf16 [D, W] convolution weights (the modules' [D, 1, W])
+  const void* wk;
+  const void* wv;
+  const void* bq;           // bf16 [D] convolution biases (nullable)
+  const void* bk;
+  const void* bv;
+  void* cq;                 // bf16 [B, D, W-1] convolution caches, updated in place
+  void* ck;
+  void* cv;
+  const void* lw;           // bf16 [H, H K] gate weight, [H] gate bias
+  const void* lb;
+  const void* alog;         // bf16 [H] A_log, dt_bias
+  const void* dtb;
+  void* q;                  // bf16 [B, T, H, K] normalised q, k; [B, T, H, V] v
+  void* k;
+  void* v;
+  float* lam;               // fp32 [B, T, H]
+  float* g;
+  float* beta;
+  int B, T, H, K, V, W, neg_eig;
+  float eps;
+};
+
 // Gated RMSNorm of the layer epilogue: y = x / sqrt(mean(x^2) + eps) * w * silu(g) per row of dv
 // (x, g, y, dy, dx, dg bf16 [rows, dv]; w fp32 [dv] (nullable = ones); rstd fp32 [rows]).
 struct GNormArgs {

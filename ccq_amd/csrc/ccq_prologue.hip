@@ -19,6 +19,7 @@ namespace ccq {
 namespace {
 
 constexpr int kConvTB = 16;     // tokens per tile of a thread (backward; the forward's is per launch)
+constexpr int kDecProMaxH = 32;  // heads of a layer the decode prologue takes
 
 __device__ __forceinline__ float silu_(float a) { return a / (1.f + __expf(-a)); }
 __device__ __forceinline__ float dsilu_(float a) {
@@ -452,6 +453,154 @@ __global__ __launch_bounds__(kThreads) void gnorm_bwd_kernel(const GNormArgs a) 
   __syncthreads();
   for (int j = threadIdx.x; j < a.dv; j += kThreads)
     a.dw_part[(long)blockIdx.x * a.dv + j] = sW[0][j] + sW[1][j] + sW[2][j] + sW[3][j];
+}
+
+// ---------------------------------------------------------------------------
+// decode prologue of a CCQ-GDN layer: grid B (one workgroup per sequence), 256 threads.  A thread
+// takes groups of 8 channels: the q groups (H K / 8), then the k groups, then the v groups; the lanes
+// of one head are consecutive lanes of one wavefront (K / 8 of them), so its sum of squares is a lane
+// shuffle in the convolution kernel's order (the same roundings as the layer's unfused path: y to
+// bf16, y / sqrt(|y_h|^2 + eps) from the rounded y, to bf16).  The gate then reads the token's q
+// activations from LDS.  The caches are read for every token of the call and rewritten at the end
+// (each channel by the thread that owns it).
+// ---------------------------------------------------------------------------
+template <int W>
+__global__ __launch_bounds__(kThreads) void decode_prologue_kernel(const DecProArgs a) {
+  extern __shared__ float sQ[];                 // the token's q activations (bf16 values), H K
+  __shared__ float sPart[kThreads / 64][kDecProMaxH];
+  const int b = blockIdx.x, tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const int Dq = a.H * a.K, Dv = a.H * a.V;
+  const int nq = Dq / 8, nv = Dv / 8, ng = 2 * nq + nv;
+  const int hl = a.K / 8;
+  const bf16* lw = (const bf16*)a.lw;
+  // channel group -> tensor, first channel, width
+  auto group = [&](int grp, int& kind, int& c, int& D) {
+    if (grp < nq) {
+      kind = 0; c = 8 * grp; D = Dq;
+    } else if (grp < 2 * nq) {
+      kind = 1; c = 8 * (grp - nq); D = Dq;
+    } else {
+      kind = 2; c = 8 * (grp - 2 * nq); D = Dv;
+    }
+  };
+  auto input8 = [&](int kind, int D, int c, int p, float (&v)[8]) {  // input at call position p (< 0: cache)
+    const bf16* x = (const bf16*)(kind == 0 ? a.xq : kind == 1 ? a.xk : a.xv);
+    const bf16* cache = (const bf16*)(kind == 0 ? a.cq : kind == 1 ? a.ck : a.cv);
+    if (p >= 0) {
+      const bf16x8 xb = *(const bf16x8*)(x + ((long)b * a.T + p) * a.ldx + c);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (float)xb[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (float)cache[((long)b * D + c + i) * (W - 1) + (W - 1) + p];
+    }
+  };
+  for (int t = 0; t < a.T; ++t) {
+    const long row = (long)b * a.T + t;
+    for (int g0 = 0; g0 < ng; g0 += kThreads) {
+      const int grp = g0 + tid;
+      const bool on = grp < ng;
+      int kind = 2, c = 0, D = Dv;
+      if (on) group(grp, kind, c, D);
+      bf16x8 yb;
+      if (on) {
+        const bf16* wt = (const bf16*)(kind == 0 ? a.wq : kind == 1 ? a.wk : a.wv);
+        const bf16* bs = (const bf16*)(kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv);
+        float xv[8], win[W][8];
+        input8(kind, D, c, t, xv);
+#pragma unroll
+        for (int w = 0; w < W - 1; ++w)
+          if (w < W - 1) input8(kind, D, c, t - (W - 1) + w, win[w]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float acc = (bs ? (float)bs[c + i] : 0.f) + (float)wt[(long)(c + i) * W + W - 1] * xv[i];
+#pragma unroll
+          for (int w = 0; w < W - 1; ++w)
+            if (w < W - 1) acc += (float)wt[(long)(c + i) * W + w] * win[w][i];
+          yb[i] = (bf16)silu_(acc);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) yb[i] = (bf16)0.f;
+      }
+      // per-head sum of squares (every lane takes part; v and idle lanes form their own groups)
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += (float)yb[i] * (float)yb[i];
+      ss = head_sum(ss, hl);
+      if (!on) continue;
+      if (kind == 2) {
+        *(bf16x8*)((bf16*)a.v + row * Dv + c) = yb;
+        continue;
+      }
+      const float r = rsqrtf(ss + a.eps);
+      bf16x8 nb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) nb[i] = (bf16)((float)yb[i] * r);
+      *(bf16x8*)((bf16*)(kind == 0 ? a.q : a.k) + row * Dq + c) = nb;
+      if (kind == 0)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sQ[c + i] = (float)yb[i];
+    }
+    __syncthreads();
+    // gate logits: per head, partial dot products of the q activations with the head's weight row
+    for (int h = 0; h < a.H; ++h) {
+      float part = 0.f;
+      for (int j = tid; j < Dq; j += kThreads) part += (float)lw[(long)h * Dq + j] * sQ[j];
+      part = head_sum(part, 64);
+      if (l == 0) sPart[wv][h] = part;
+    }
+    __syncthreads();
+    if (tid < a.H) {
+      const int h = tid;
+      float logit = (a.lb ? (float)((const bf16*)a.lb)[h] : 0.f);
+      for (int ww = 0; ww < kThreads / 64; ++ww) logit += sPart[ww][h];
+      const float lg = (float)(bf16)logit;                   // the gate projection's bf16 output
+      a.lam[row * a.H + h] = (float)(bf16)(1.f / (1.f + expf(-lg)));
+      const float xb = (float)((const bf16*)a.xb)[row * a.ldx + h];
+      float be = (float)(bf16)(1.f / (1.f + expf(-xb)));
+      if (a.neg_eig) be *= 2.f;
+      a.beta[row * a.H + h] = be;
+      const float xa = (float)((const bf16*)a.xa)[row * a.ldx + h] + (float)((const bf16*)a.dtb)[h];
+      const float sp = xa > 20.f ? xa : log1pf(expf(xa));     // softplus (threshold 20)
+      a.g[row * a.H + h] = -expf((float)((const bf16*)a.alog)[h]) * sp;
+    }
+    __syncthreads();
+  }
+  // caches: the inputs at call positions T - (W-1) .. T - 1 (before the call's first token: the
+  // cached ones), read in full before any is written
+  if (W > 1) {
+    for (int grp = tid; grp < ng; grp += kThreads) {
+      int kind, c, D;
+      group(grp, kind, c, D);
+      float nw[W][8];
+#pragma unroll
+      for (int w = 0; w < W - 1; ++w)
+        if (w < W - 1) input8(kind, D, c, a.T - (W - 1) + w, nw[w]);
+      bf16* cache = (bf16*)(kind == 0 ? a.cq : kind == 1 ? a.ck : a.cv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int w = 0; w < W - 1; ++w)
+          if (w < W - 1) cache[((long)b * D + c + i) * (W - 1) + w] = (bf16)nw[w][i];
+    }
+  }
+}
+
+hipError_t launch_decode_prologue(const DecProArgs& a, hipStream_t st) {
+  if (a.B <= 0 || a.T <= 0) return hipSuccess;
+  const size_t lds = (size_t)a.H * a.K * sizeof(float);
+  switch (a.W) {
+#define CCQ_DECPRO_W(N)                                                                         \
+  case N:                                                                                       \
+    hipLaunchKernelGGL(decode_prologue_kernel<N>, dim3((unsigned)a.B), dim3(kThreads), lds, st, a); \
+    break;
+    CCQ_DECPRO_W(1) CCQ_DECPRO_W(2) CCQ_DECPRO_W(3) CCQ_DECPRO_W(4) CCQ_DECPRO_W(5) CCQ_DECPRO_W(6)
+    CCQ_DECPRO_W(7) CCQ_DECPRO_W(8)
+#undef CCQ_DECPRO_W
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 // `blocks` virtual workgroups (the backward's partial rows); each workgroup covers cg groups of 8

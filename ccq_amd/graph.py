@@ -14,6 +14,12 @@ step itself), so the same captured graph is replayed for every generated token.
 position and the output ``o``.  A caller writes the new token's inputs into the input buffers
 (``copy_``), replays, and reads ``o``.  ``CapturedDecode`` captures the steps of several layers
 in order (e.g. the 24 layers of a model) and replays them as one graph.
+
+``GDNLayerDecode`` is a whole ``CCQGDN`` layer's token step around a ``DecodeStep``: one GEMM for the
+layer's input projections, one kernel for everything between them and the recurrent op
+(``ccq_gdn_decode_prologue``), the in-place decode step, and the layer's output norm and projection --
+five launches per layer and token instead of the recurrent mode's few dozen small ones, on static
+buffers, so that a model's whole token step can be captured.
 """
 
 from __future__ import annotations
@@ -22,10 +28,12 @@ from typing import List, Optional, Sequence
 
 import torch
 
+import torch.nn.functional as F
+
 from . import _lib
 from ._lib import call, ptr
 
-__all__ = ["DecodeStep", "CapturedDecode"]
+__all__ = ["DecodeStep", "CapturedDecode", "GDNLayerDecode"]
 
 
 class DecodeStep:
@@ -161,3 +169,95 @@ class CapturedDecode:
         """The same steps launched one by one (no graph)."""
         for s in self.steps:
             s.launch()
+
+
+class GDNLayerDecode:
+    """The token step of one ``CCQGDN`` layer (recurrent mode with a cache, ``ccq/gdn/layer.py:253-412``)
+    on static buffers: ``__call__(h)`` maps the layer input ``h [B, T, hidden]`` (bf16; normally T = 1) to
+    the layer output, advancing the layer's states, convolution caches and position in place.
+
+    The step is the layer's input projections as one GEMM over their concatenated weights (taken at
+    construction; ``refresh()`` after the weights change), ``ccq_gdn_decode_prologue`` (short
+    convolutions + SiLU with in-place caches, lambda, beta, g, per-head l2norm of q and k, with the
+    roundings of the layer's own bf16 operations), the in-place decode step (``DecodeStep``, lambda as
+    given, no l2norm), the gated output norm and the output projection.  For a bf16 layer on the GPU
+    with short convolutions and one key / value head per query head (the reference configurations);
+    other layers run their recurrent mode as usual."""
+
+    def __init__(self, layer, B: int, T: int = 1):
+        L = layer
+        if not L.use_short_conv:
+            raise ValueError("GDNLayerDecode needs a layer with short convolutions")
+        if L.num_kv_heads != L.num_heads or L.num_v_heads != L.num_heads:
+            raise ValueError("GDNLayerDecode needs one key / value head per query head")
+        params = [L.q_proj.weight, L.k_proj.weight, L.v_proj.weight, L.a_proj.weight, L.b_proj.weight,
+                  L.erase_lambda_proj.weight, L.A_log, L.dt_bias, L.q_conv1d.weight]
+        if any(p.dtype != torch.bfloat16 or not p.is_cuda for p in params):
+            raise ValueError("GDNLayerDecode runs a bf16 layer on the GPU")
+        self.layer, self.B, self.T = L, B, T
+        self.H, self.K, self.V, self.W = L.num_heads, L.head_k_dim, L.head_v_dim, L.conv_size
+        dev = L.q_proj.weight.device
+        self.step = DecodeStep(B, self.H, self.K, self.V, T=T, mode="gdn", gate=False,
+                               subtract_mean=L.subtract_mean, use_l2norm=False, enable_ccq=L.enable_ccq,
+                               device=dev)
+        dq, dv = self.H * self.K, self.H * self.V
+        self.conv = [torch.zeros(B, d, self.W - 1, device=dev, dtype=torch.bfloat16) for d in (dq, dq, dv)]
+        # rows of the concatenated projection: q, k, v, g (output gate), a, b, zero padding to 8 elements
+        widths = [dq, dq, dv, dv if L.use_gate else 0, self.H, self.H]
+        self.offsets = [sum(widths[:i]) for i in range(len(widths))]
+        self.pad = (-sum(widths)) % 8
+        self.width = sum(widths) + self.pad
+        self.refresh()
+
+    def refresh(self) -> None:
+        """Concatenate the layer's current input-projection weights."""
+        L = self.layer
+        parts = [L.q_proj.weight, L.k_proj.weight, L.v_proj.weight]
+        if L.use_gate:
+            parts.append(L.g_proj.weight)
+        parts += [L.a_proj.weight, L.b_proj.weight]
+        if self.pad:
+            parts.append(L.q_proj.weight.new_zeros(self.pad, L.hidden_size))
+        with torch.no_grad():
+            self.w_in = torch.cat([p.detach() for p in parts]).contiguous()
+            w = getattr(L.o_norm, "weight", None)
+            self.norm_w = w.detach().float().contiguous() if w is not None else None
+
+    def load(self, entry) -> None:
+        """Copy one layer's entry of a ``LayerCache`` (``{'recurrent_state': (S, C, m, pos),
+        'conv_state': (q, k, v caches)}``, e.g. after a chunked prefill) into the step's buffers."""
+        from .layers import unpack_recurrent_state
+        from .prologue import last_inputs
+        S, C, m, pos = unpack_recurrent_state(entry["recurrent_state"])
+        self.step.load_state(S, C, m, pos)
+        for dst, src in zip(self.conv, entry["conv_state"]):
+            dst.copy_(last_inputs(src, self.W))
+
+    def __call__(self, h: torch.Tensor) -> torch.Tensor:
+        L, st = self.layer, self.step
+        B, T, H, K, V = self.B, self.T, self.H, self.K, self.V
+        if h.shape[:2] != (B, T) or h.dtype != torch.bfloat16:
+            raise ValueError(f"expected bf16 input [{B}, {T}, hidden] (got {tuple(h.shape)} {h.dtype})")
+        x = F.linear(h, self.w_in)
+        o_q, o_k, o_v, o_g, o_a, o_b = self.offsets
+        cw = [c.weight for c in (L.q_conv1d, L.k_conv1d, L.v_conv1d)]
+        cb = [c.bias for c in (L.q_conv1d, L.k_conv1d, L.v_conv1d)]
+        base = x.data_ptr()
+        at = lambda off: base + 2 * off  # noqa: E731  (bf16 elements)
+        call("ccq_gdn_decode_prologue", at(o_q), at(o_k), at(o_v), at(o_a), at(o_b), self.width,
+             ptr(cw[0]), ptr(cw[1]), ptr(cw[2]), ptr(cb[0]), ptr(cb[1]), ptr(cb[2]),
+             ptr(self.conv[0]), ptr(self.conv[1]), ptr(self.conv[2]),
+             ptr(L.erase_lambda_proj.weight), ptr(L.erase_lambda_proj.bias), ptr(L.A_log), ptr(L.dt_bias),
+             ptr(st.q), ptr(st.k), ptr(st.v), ptr(st.lam), ptr(st.g), ptr(st.beta),
+             B, T, H, K, V, self.W, int(L.allow_neg_eigval), 1e-6, _lib.stream_of(x))
+        st.launch()
+        if L.use_gate:
+            # the gated RMSNorm kernel on contiguous gate rows, with the weight converted in refresh()
+            gx = x[..., o_g:o_g + H * V].contiguous()
+            o = torch.empty_like(st.o)
+            rstd = torch.empty(B * T * H, device=x.device, dtype=torch.float32)
+            call("ccq_gated_rmsnorm_fwd", ptr(st.o), ptr(gx), ptr(self.norm_w), ptr(o), ptr(rstd), B * T * H, V,
+                 float(L.o_norm.eps), _lib.stream_of(x))
+        else:
+            o = L.o_norm(st.o)
+        return L.o_proj(o.reshape(B, T, H * V))

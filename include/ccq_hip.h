@@ -260,6 +260,27 @@ int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lam
  * and no memset.
  */
 size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K);
+/*
+ * The CCQ-GDN layer's per-token prologue in one launch, ahead of ccq_gdn_decode_step: what the
+ * reference layer computes between its input projections and fused_recurrent_ccq_gdn
+ * (ccq/gdn/layer.py:266-316) -- the q, k, v short convolutions + SiLU with their caches (fla
+ * ShortConvolution), lambda = sigmoid(erase_lambda_proj(q)) on the un-normalised activation,
+ * beta = sigmoid(b_proj x) (x 2 with allow_neg_eigval), g = -exp(A_log) softplus(a_proj x + dt_bias)
+ * and the per-head L2 normalisation of q and k -- with the same bf16 roundings as that sequence of
+ * bf16 operations.  xq, xk, xv, xa, xb: bf16 rows of the q (H*K), k (H*K), v (H*V), a (H) and b (H)
+ * projections of token r = b*T + t at element offset r*ldx (ldx % 8 == 0, q/k/v rows 16-byte
+ * aligned); wq/wk/wv bf16 [D, W] convolution weights, bq/bk/bv bf16 [D] biases (nullable); cq/ck/cv
+ * bf16 [B, D, W-1] caches (each sequence's previous W-1 inputs), updated in place; lam_w bf16
+ * [H, H*K], lam_b bf16 [H] (nullable), A_log, dt_bias bf16 [H].  Outputs: q, k bf16 [B, T, H, K], v
+ * bf16 [B, T, H, V], lam, g, beta fp32 [B, T, H] -- the decode step's inputs with use_l2norm = 0.
+ * H <= 32; K a power of two in [8, 512]; V % 8 == 0; W in [1, 8].  No allocation; one kernel.
+ */
+int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, const void* xa, const void* xb,
+                            int64_t ldx, const void* wq, const void* wk, const void* wv, const void* bq,
+                            const void* bk, const void* bv, void* cq, void* ck, void* cv, const void* lam_w,
+                            const void* lam_b, const void* A_log, const void* dt_bias, void* q, void* k, void* v,
+                            float* lam, float* g, float* beta, int B, int T, int H, int K, int V, int W,
+                            int allow_neg_eigval, float eps, void* stream);
 int ccq_gdn_decode_step(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
                         const float* gate_b, const float* g, const float* beta, float* state, float* cov_state,
                         float* mean_state, int* position, void* o, void* workspace, int B, int T, int H, int K, int V,
@@ -324,9 +345,12 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
  * clean_bwd_dk, clean_bwd_gate, gdn_prep, gdn_fwd_state, gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw,
  * gdn_bwd_wy, gla_intra, gla_fwd_state, gla_fwd_o, gla_bwd_state, gla_bwd_dv, gla_bwd_dqk,
  * gla_bwd_gk, clean_z_fwd, clean_z_bwd) and returns the summed
- * milliseconds and the number of launches since the last ccq_timing_reset.
+ * milliseconds and the number of launches since the last ccq_timing_reset.  ccq_timing_select
+ * restricts the events to the kernel of that name (NULL: every kernel), so that a timed loop carries
+ * one event pair per step instead of one per kernel.
  */
 int ccq_timing_enable(int on);
+int ccq_timing_select(const char* kernel);
 int ccq_timing_reset(void);
 int ccq_timing_read(const char* kernel, double* total_ms, int64_t* launches);
 

@@ -127,3 +127,78 @@ def test_whole_model_decode_graph_matches_eager():
     errs = out["config"]["graph_vs_eager_logits_rel_l2"]
     print("captured vs eager logits rel-L2", errs, flush=True)
     assert len(errs) == 4 and max(errs) <= 2e-2
+
+
+@pytest.mark.parametrize("H,K,expand_v,T0", [(4, 256, 2, 70), (2, 128, 1, 33)])
+def test_layer_decode_matches_recurrent_mode(H, K, expand_v, T0):
+    """GDNLayerDecode (one GEMM for the input projections, the decode prologue kernel, the in-place
+    decode step, the output norm and projection) against the bf16 layer's own recurrent mode
+    (CCQGDN.forward with a LayerCache, one token per call) from the same chunked prefill: outputs,
+    states, convolution caches and position after every token; then the same step captured in a
+    graph and replayed token after token from the prefill state again."""
+    dev = _cuda()
+    import copy
+
+    from ccq_amd import CCQGDN, LayerCache
+    from ccq_amd.graph import GDNLayerDecode
+    from tests._util import rel
+    B, steps = 3, 4
+    print(f"test_layer_decode_matches_recurrent_mode H={H} K={K} expand_v={expand_v}", flush=True)
+    torch.manual_seed(0)
+    layer = CCQGDN(hidden_size=512, head_dim=K, num_heads=H, expand_v=expand_v, mode="chunk", layer_idx=0)
+    with torch.no_grad():
+        layer.erase_lambda_proj.bias.fill_(0.0)
+    layer = layer.to(dev, torch.bfloat16).eval()
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(B, T0 + steps, 512, generator=gen).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        cache = LayerCache()
+        layer(x[:, :T0], past_key_values=cache, use_cache=True)
+        prefill = copy.deepcopy(cache)
+        ld = GDNLayerDecode(layer, B)
+        ld.load(prefill.get(0))
+        for t in range(T0, T0 + steps):
+            o_e = layer(x[:, t:t + 1], past_key_values=cache, use_cache=True)[0]
+            o_f = ld(x[:, t:t + 1])
+            torch.cuda.synchronize()
+            S, C, m, pos = cache.get(0)["recurrent_state"]
+            errs = {"o": rel(o_f, o_e), "S": rel(ld.step.S, S), "C": rel(ld.step.C, C), "m": rel(ld.step.m, m)}
+            print(t, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+            assert errs["o"] <= 2e-3
+            for n in ("S", "C", "m"):
+                assert errs[n] <= 1e-5, n
+            assert int(ld.step.position.item()) == pos == t + 1
+            # the caches hold the projections' outputs, which here come from one GEMM over the
+            # concatenated weights and there from one GEMM per projection: equal up to roundings
+            # that the different summation orders move across a tie
+            for a, b in zip(ld.conv, cache.get(0)["conv_state"]):
+                assert rel(a, b) <= 1e-3, "convolution cache"
+        # captured: the same steps replayed from the prefill state
+        h = torch.zeros(B, 1, 512, device=dev, dtype=torch.bfloat16)
+        ld.load(prefill.get(0))
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            ld(h)                              # loads the kernels; its state change is undone below
+        torch.cuda.current_stream().wait_stream(side)
+        ld.load(prefill.get(0))
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = ld(h)
+        ld.load(prefill.get(0))
+        ref = GDNLayerDecode(layer, B)
+        ref.load(prefill.get(0))
+        # (the projection GEMM may take another algorithm under capture than eagerly, so the replays are
+        # held to the same tolerances, not to bit equality)
+        for t in range(T0, T0 + steps):
+            h.copy_(x[:, t:t + 1])
+            graph.replay()
+            o_r = ref(x[:, t:t + 1])
+            torch.cuda.synchronize()
+            errs = {"o": rel(out, o_r), "S": rel(ld.step.S, ref.step.S), "C": rel(ld.step.C, ref.step.C),
+                    "conv": rel(ld.conv[0], ref.conv[0])}
+            print("replay", t, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+            assert errs["o"] <= 2e-3 and errs["conv"] <= 1e-3
+            assert errs["S"] <= 1e-5 and errs["C"] <= 1e-5
+            assert int(ld.step.position.item()) == t + 1
