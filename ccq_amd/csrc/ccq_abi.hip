@@ -508,6 +508,7 @@ int ccq_gdn_fwd(const void* q, const float* q_f32, const void* k, const void* v,
   a.gcum = sv.gcum; a.tmat = sv.tmat; a.w = sv.w; a.wl = sv.wl; a.u = sv.u; a.hT = sv.hT; a.hTl = sv.hTl; a.U = sv.U; a.PT = sv.PT;
   a.o = o; a.s_fin = final_state; a.scale = scale;
   a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NTG = num_chunks;
+  a.snap16 = (K == 128 && V == 128) ? 1 : 0;   // the dq/dk/dw kernel of that shape reads int16 block-floating-point snapshots
   hipStream_t st = (hipStream_t)stream;
   static const char* names[] = {"gdn_prep", "gdn_fwd_state", "gdn_fwd_o"};
   const int stages[] = {kGdnPrep, kGdnFwdState, kGdnFwdO};
@@ -546,6 +547,7 @@ int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v,
   a.dout = d_o; a.ds_fin = d_final_state; a.dU = wk.dU; a.dhT = wk.dhT; a.dhTl = wk.dhTl; a.dq32 = dq_f32; a.dkp32 = wk.dkp32;
   a.dw32 = wk.dw32; a.dgp = wk.dgp; a.dk32 = dk_f32; a.dv = dv; a.dbeta = dbeta; a.dg = dg; a.ds0 = d_initial_state;
   a.scale = scale; a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NTG = num_chunks;
+  a.snap16 = (K == 128 && V == 128) ? 1 : 0;
   hipStream_t st = (hipStream_t)stream;
   static const char* names[] = {"gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy"};
   const int stages[] = {kGdnBwdState, kGdnBwdDqkw, kGdnBwdWy};

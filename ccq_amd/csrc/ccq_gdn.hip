@@ -781,6 +781,61 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
 }
 
 // ===========================================================================
+// Snapshot rows in block floating point: 16-bit integers with a power-of-two scale per row.  A
+// [rows][K] snapshot held in LDS as hi/lo bf16 pairs leaves as round(x / 2^e_r) in int16 and 2^e_r in
+// fp32, e_r = floor(log2 max_k |x|) - 14: the row's largest element keeps 15 significant bits and
+// every element an absolute error of at most 2^-16 of it -- about the hi/lo pair's precision on the
+// dense rows of a state, in half its bytes (an fp16 row keeps 11 bits per element, which the dk of
+// the backward measurably felt).  The scale stays a normal fp32 number (e_r >= -126): a row whose
+// largest element is below 2^-112 keeps an absolute error below 2^-127.  The K / 8 consecutive lanes
+// that hold a row (8 elements each) find its largest magnitude by DPP lane moves within the wave's
+// 16-lane rows, so no barrier and no LDS round trip is needed; every lane of the wave takes part.
+// A consumer multiplies the integer back by the exact power-of-two scale in fp32 and splits the
+// value into its usual hi/lo pair.
+// ===========================================================================
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+
+// Maximum of v over each aligned group of G consecutive lanes (G a power of two, 2..64): quad
+// permutations for lanes 1 and 2 apart, the half-row and row mirrors for 4 and 8 apart (after the
+// steps before them every lane of a quad, then of a half-row, holds the same value), a lane swap
+// beyond 16.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (G >= 2) v = fmaxf(v, dpp_move<0xB1>(v));    // quad_perm [1, 0, 3, 2]
+  if constexpr (G >= 4) v = fmaxf(v, dpp_move<0x4E>(v));    // quad_perm [2, 3, 0, 1]
+  if constexpr (G >= 8) v = fmaxf(v, dpp_move<0x141>(v));   // row_half_mirror
+  if constexpr (G >= 16) v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+  if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+template <int K>
+__device__ __forceinline__ void snap16_store(const bf16* hi, const bf16* lo, short* dst, float* dst_scale, int lane) {
+  constexpr int G = K / 8;  // lanes per row
+  float x[8], mx = 0.f;
+  const bf16x8 h8 = *(const bf16x8*)hi, l8 = *(const bf16x8*)lo;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    x[i] = (float)h8[i] + (float)l8[i];
+    mx = fmaxf(mx, fabsf(x[i]));
+  }
+  mx = group_max<G>(mx);
+  // floor(log2 mx) from the exponent field (0 and subnormal maxima land on the lower clamp)
+  const int e = min(max((int)((__float_as_uint(mx) >> 23) & 0xff) - 127 - 14, -126), 113);
+  i16x8 out;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = (short)__builtin_amdgcn_fmed3f(rintf(ldexpf(x[i], -e)), -32767.f, 32767.f);
+  *gmem((i16x8*)dst) = out;
+  if ((lane & (G - 1)) == 0) *gmem(dst_scale) = ldexpf(1.f, e);
+}
+
+// ===========================================================================
 // gdn_fwd_state for K <= 128 with 8 wavefronts, with the chunk output fused in: waves 0-3 compute
 // and issue no global access inside the walk; waves 4-7 move memory one or two chunks ahead of its
 // use and write every result row.  Compute wave w owns query / U rows [16 w, 16 w + 16) of every
@@ -926,14 +981,23 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
       pk.store(sK + q * (BT * LDK), LDK, chunk_len(min(c + 1, cl)), lm);
       load_k(min(c + 2, cl));
       constexpr int VPR = K / 8;
+      if (a.snap16) {
 #pragma unroll
-      for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
-        const int idx = lm + j * NM;
-        const int which = idx / (VB * VPR), e = idx % (VB * VPR);
-        const int r = e / VPR, cc = (e % VPR) * 8;
-        const bf16* src = which ? sSl : sSh;
-        bf16* dst = which ? (bf16*)a.hTl : (bf16*)a.hT;
-        *(bf16x8*)(gmem(dst) + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
+        for (int j = 0; j < (VB * VPR) / NM; ++j) {
+          const int idx = lm + j * NM, r = idx / VPR, cc = (idx % VPR) * 8;
+          const long row = ((long)gc * a.H + h) * V + v0 + r;
+          snap16_store<K>(sSh + r * LDK + cc, sSl + r * LDK + cc, (short*)a.hT + row * K + cc, (float*)a.hTl + row, lm);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
+          const int idx = lm + j * NM;
+          const int which = idx / (VB * VPR), e = idx % (VB * VPR);
+          const int r = e / VPR, cc = (e % VPR) * 8;
+          const bf16* src = which ? sSl : sSh;
+          bf16* dst = which ? (bf16*)a.hTl : (bf16*)a.hT;
+          *(bf16x8*)(gmem(dst) + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
+        }
       }
       store_o(max(c - 1, 0));
       __syncthreads();
@@ -1729,14 +1793,23 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
     {
       constexpr int VPR = K / 8;
       const int gc = gc0 + c;
+      if (a.snap16) {
 #pragma unroll
-      for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
-        const int idx = tid + j * NM;
-        const int which = idx / (VB * VPR), e = idx % (VB * VPR);
-        const int r = e / VPR, cc = (e % VPR) * 8;
-        const bf16* src = which ? sdSl : sdSh;
-        bf16* dst = which ? (bf16*)a.dhTl : (bf16*)a.dhT;
-        *gmem((bf16x8*)(dst + (((long)gc * a.H + h) * V + v0 + r) * K + cc)) = *(const bf16x8*)(src + r * LDK + cc);
+        for (int j = 0; j < (VB * VPR) / NM; ++j) {
+          const int idx = tid + j * NM, r = idx / VPR, cc = (idx % VPR) * 8;
+          const long row = ((long)gc * a.H + h) * V + v0 + r;
+          snap16_store<K>(sdSh + r * LDK + cc, sdSl + r * LDK + cc, (short*)a.dhT + row * K + cc, (float*)a.dhTl + row, tid);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < (2 * VB * VPR) / NM; ++j) {
+          const int idx = tid + j * NM;
+          const int which = idx / (VB * VPR), e = idx % (VB * VPR);
+          const int r = e / VPR, cc = (e % VPR) * 8;
+          const bf16* src = which ? sdSl : sdSh;
+          bf16* dst = which ? (bf16*)a.dhTl : (bf16*)a.dhT;
+          *gmem((bf16x8*)(dst + (((long)gc * a.H + h) * V + v0 + r) * K + cc)) = *(const bf16x8*)(src + r * LDK + cc);
+        }
       }
       const int r = tid / (VB / 8), cc = (tid % (VB / 8)) * 8;
       const float sc = sGam[r];
@@ -3301,6 +3374,21 @@ __device__ __forceinline__ bf16x8 frag_tr_h(const char* R, int r0, int c0, int l
   const bf16x4_t y = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_b4*)(q + 4 * 256));
   return bf16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
 }
+// The same B operand from a block-floating-point snapshot region (int16 rows with power-of-two scales;
+// sc: the region's 32 row scales, fp32): each element times its row's scale, split into hi/lo bf16
+__device__ __forceinline__ void frag_tr_h16(const char* R, const char* sc, int r0, int c0, int l, bf16x8& hi,
+                                            bf16x8& lo) {
+  const i16x8 x = __builtin_bit_cast(i16x8, frag_tr_h(R, r0, c0, l));
+  const int v = r0 + 8 * (l >> 5);
+  const f32x4 s0 = *(const f32x4*)(sc + 4 * v), s1 = *(const f32x4*)(sc + 4 * v + 16);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bf16 h, o;
+    split2((float)x[i] * (i < 4 ? s0[i] : s1[i - 4]), h, o);
+    hi[i] = h;
+    lo[i] = o;
+  }
+}
 // A/B operand rows r0 + l % 32, contraction v0 + 8 (l / 32) .. +7 of a swizzled fp32 [64][32] region,
 // split into hi/lo
 __device__ __forceinline__ void frag_u(const char* R, int r0, int v0, bf16x8& hi, bf16x8& lo, int l) {
@@ -3751,6 +3839,10 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v4_kernel(const GdnArgs a
 // Loads per wave: value piece 8, q_clean piece 4 fp32 / 2 bf16 (one more on wave 0, which also
 // loads g), k/P^T piece 4; the wait before a piece is vmcnt(loads issued after it).  A bf16
 // q_clean is stored swizzled like k and read with transposing reads; its lo part is zero.
+// The state and state-gradient snapshots arrive as int16 rows with a power-of-two scale per row (the
+// walks write that form for K = V = 128: half the bytes of hi/lo pairs); a value piece holds the
+// two int16 regions and, in place of their lo parts, each wave's copy of the 32 row scales, so it is
+// still 8 load instructions per wave.  The B operands are rebuilt as hi/lo pairs of scale x value.
 // ===========================================================================
 namespace dq5 {
 constexpr int SLOT = 53248;
@@ -3823,13 +3915,14 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a
   auto issue_v = [&](char* S, const Unit& x, int vb) {  // 8 per wave
     const int v0 = 32 * vb, l = fresh_lane();
     {
-      const long ub = (((long)x.gc * a.H + x.h) * V + v0) * K;
+      // h and dS' rows as fp16 (RH, RDH) and their 32 row scales, one copy per wave (RHL, RDHL)
+      const long ub = (((long)x.gc * a.H + x.h) * V + v0) * K, sb = ((long)x.gc * a.H + x.h) * V + v0;
       const int r = 4 * w + (l >> 4), p = l & 15;
-      const unsigned off = (unsigned)((r * K + 8 * (p ^ (2 * (r & 3)))) * 2);
+      const unsigned off = (unsigned)((r * K + 8 * (p ^ (2 * (r & 3)))) * 2), offs = (unsigned)((l & 31) * 4);
       dma16((const bf16*)a.hT + ub, off, S + RH + 1024 * w);
-      dma16((const bf16*)a.hTl + ub, off, S + RHL + 1024 * w);
+      dma4((const float*)a.hTl + sb, offs, S + RHL + 256 * w);
       dma16((const bf16*)a.dhT + ub, off, S + RDH + 1024 * w);
-      dma16((const bf16*)a.dhTl + ub, off, S + RDHL + 1024 * w);
+      dma4((const float*)a.dhTl + sb, offs, S + RDHL + 256 * w);
     }
     const long ub = x.tok0 * rsv + (long)x.h * V + v0;
     {
@@ -3890,18 +3983,22 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a
   // two 16-value steps (early waves) or after them (the others)
   auto compute_v = [&](const char* S, auto&& iss) {
     const int l = fresh_lane();
+    const char* const sch = S + RHL + 256 * w;   // this wave's copy of the h / dS' row scales
+    const char* const scd = S + RDHL + 256 * w;
     {
-      const int o = 16 * (64 * w + l);
-      const bf16x8 x1 = *(const bf16x8*)(S + RH + o), x2 = *(const bf16x8*)(S + RHL + o);
-      const bf16x8 y1 = *(const bf16x8*)(S + RDH + o), y2 = *(const bf16x8*)(S + RDHL + o);
+      const int o = 16 * (64 * w + l), r = (64 * w + l) >> 4;
+      const i16x8 x1 = *(const i16x8*)(S + RH + o), y1 = *(const i16x8*)(S + RDH + o);
+      float d = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) hds += ((float)x1[i] + (float)x2[i]) * ((float)y1[i] + (float)y2[i]);
+      for (int i = 0; i < 8; ++i) d += (float)x1[i] * (float)y1[i];
+      hds += d * (*(const float*)(sch + 4 * r) * *(const float*)(scd + 4 * r));
     }
 #pragma unroll
     for (int v0 = 0; v0 < 32; v0 += 16) {
       const bf16x8 oa = frag_o(S + RDO, tr, v0, l);
-      const bf16x8 hb = frag_tr_h(S + RH, v0, kc, l), hbl = frag_tr_h(S + RHL, v0, kc, l);
-      const bf16x8 db = frag_tr_h(S + RDH, v0, kc, l), dbl = frag_tr_h(S + RDHL, v0, kc, l);
+      bf16x8 hb, hbl, db, dbl;
+      frag_tr_h16(S + RH, sch, v0, kc, l, hb, hbl);
+      frag_tr_h16(S + RDH, scd, v0, kc, l, db, dbl);
       bf16x8 uh, ul, dh, dl;
       frag_u(S + RU, tr, v0, uh, ul, l);
       frag_u(S + RDU, tr, v0, dh, dl, l);

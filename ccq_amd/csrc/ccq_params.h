@@ -163,6 +163,10 @@ struct GdnArgs {
   float* ds0;               // fp32 [N, H, K, V] (nullable)
   float scale;
   int T, H, N, NT, NTG;     // NT: chunks per sequence (dense); NTG: total chunks
+  // state and state-gradient snapshots as int16 rows with a power-of-two scale per row (hT / dhT hold
+  // the integers, hTl / dhTl the fp32 row scales [NTG * H, V]) instead of hi/lo bf16 pairs: set for
+  // K = V = 128, whose dq/dk/dw kernel reads that form
+  int snap16;
 };
 
 }  // namespace ccq
