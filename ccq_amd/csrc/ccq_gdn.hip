@@ -106,6 +106,61 @@ __device__ __forceinline__ void lds_to_global_bf16(bf16* g, long gstride, const 
   }
 }
 
+// ===========================================================================
+// Snapshot rows in block floating point: 16-bit integers with a power-of-two scale per row.  A
+// [rows][K] snapshot held in LDS as hi/lo bf16 pairs leaves as round(x / 2^e_r) in int16 and 2^e_r in
+// fp32, e_r = floor(log2 max_k |x|) - 14: the row's largest element keeps 15 significant bits and
+// every element an absolute error of at most 2^-16 of it -- about the hi/lo pair's precision on the
+// dense rows of a state, in half its bytes (an fp16 row keeps 11 bits per element, which the dk of
+// the backward measurably felt).  The scale stays a normal fp32 number (e_r >= -126): a row whose
+// largest element is below 2^-112 keeps an absolute error below 2^-127.  The K / 8 consecutive lanes
+// that hold a row (8 elements each) find its largest magnitude by DPP lane moves within the wave's
+// 16-lane rows, so no barrier and no LDS round trip is needed; every lane of the wave takes part.
+// A consumer multiplies the integer back by the exact power-of-two scale in fp32 and splits the
+// value into its usual hi/lo pair.
+// ===========================================================================
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+
+// Maximum of v over each aligned group of G consecutive lanes (G a power of two, 2..64): quad
+// permutations for lanes 1 and 2 apart, the half-row and row mirrors for 4 and 8 apart (after the
+// steps before them every lane of a quad, then of a half-row, holds the same value), a lane swap
+// beyond 16.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (G >= 2) v = fmaxf(v, dpp_move<0xB1>(v));    // quad_perm [1, 0, 3, 2]
+  if constexpr (G >= 4) v = fmaxf(v, dpp_move<0x4E>(v));    // quad_perm [2, 3, 0, 1]
+  if constexpr (G >= 8) v = fmaxf(v, dpp_move<0x141>(v));   // row_half_mirror
+  if constexpr (G >= 16) v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+  if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+template <int K>
+__device__ __forceinline__ void snap16_store(const bf16* hi, const bf16* lo, short* dst, float* dst_scale, int lane) {
+  constexpr int G = K / 8;  // lanes per row
+  float x[8], mx = 0.f;
+  const bf16x8 h8 = *(const bf16x8*)hi, l8 = *(const bf16x8*)lo;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    x[i] = (float)h8[i] + (float)l8[i];
+    mx = fmaxf(mx, fabsf(x[i]));
+  }
+  mx = group_max<G>(mx);
+  // floor(log2 mx) from the exponent field (0 and subnormal maxima land on the lower clamp)
+  const int e = min(max((int)((__float_as_uint(mx) >> 23) & 0xff) - 127 - 14, -126), 113);
+  i16x8 out;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = (short)__builtin_amdgcn_fmed3f(rintf(ldexpf(x[i], -e)), -32767.f, 32767.f);
+  *gmem((i16x8*)dst) = out;
+  if ((lane & (G - 1)) == 0) *gmem(dst_scale) = ldexpf(1.f, e);
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -732,14 +787,25 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
       }
       if (c + 1 < nc) issue(c + 1);
     } else {
-      // state snapshot (hi/lo) to HBM for the output kernel and the backward
+      // state snapshot to HBM for the output kernel and the backward: int16 rows with a scale per
+      // row (a row's K / 8 lanes are an aligned lane group of waves 2-3), else hi/lo pairs
       constexpr int VPR = K / 8;
-      for (int idx = tid - 128; idx < 2 * VB * VPR; idx += 128) {
-        const int which = idx / (VB * VPR), e = idx % (VB * VPR);
-        const int r = e / VPR, cc = (e % VPR) * 8;
-        const bf16* src = which ? sSTl : sST;
-        bf16* dst = which ? (bf16*)a.hTl : (bf16*)a.hT;
-        *(bf16x8*)(dst + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
+      if (a.snap16 & 1) {
+#pragma unroll
+        for (int j = 0; j < (VB * VPR) / 128; ++j) {
+          const int idx = tid - 128 + j * 128, r = idx / VPR, cc = (idx % VPR) * 8;
+          const long row = ((long)gc * a.H + h) * V + v0 + r;
+          snap16_store<K>(sST + r * LDK + cc, sSTl + r * LDK + cc, (short*)a.hT + row * K + cc, (float*)a.hTl + row,
+                          tid);
+        }
+      } else {
+        for (int idx = tid - 128; idx < 2 * VB * VPR; idx += 128) {
+          const int which = idx / (VB * VPR), e = idx % (VB * VPR);
+          const int r = e / VPR, cc = (e % VPR) * 8;
+          const bf16* src = which ? sSTl : sST;
+          bf16* dst = which ? (bf16*)a.hTl : (bf16*)a.hT;
+          *(bf16x8*)(dst + (((long)gc * a.H + h) * V + v0 + r) * K + cc) = *(const bf16x8*)(src + r * LDK + cc);
+        }
       }
     }
     __syncthreads();
@@ -780,60 +846,6 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
   }
 }
 
-// ===========================================================================
-// Snapshot rows in block floating point: 16-bit integers with a power-of-two scale per row.  A
-// [rows][K] snapshot held in LDS as hi/lo bf16 pairs leaves as round(x / 2^e_r) in int16 and 2^e_r in
-// fp32, e_r = floor(log2 max_k |x|) - 14: the row's largest element keeps 15 significant bits and
-// every element an absolute error of at most 2^-16 of it -- about the hi/lo pair's precision on the
-// dense rows of a state, in half its bytes (an fp16 row keeps 11 bits per element, which the dk of
-// the backward measurably felt).  The scale stays a normal fp32 number (e_r >= -126): a row whose
-// largest element is below 2^-112 keeps an absolute error below 2^-127.  The K / 8 consecutive lanes
-// that hold a row (8 elements each) find its largest magnitude by DPP lane moves within the wave's
-// 16-lane rows, so no barrier and no LDS round trip is needed; every lane of the wave takes part.
-// A consumer multiplies the integer back by the exact power-of-two scale in fp32 and splits the
-// value into its usual hi/lo pair.
-// ===========================================================================
-typedef short i16x8 __attribute__((ext_vector_type(8)));
-
-// Maximum of v over each aligned group of G consecutive lanes (G a power of two, 2..64): quad
-// permutations for lanes 1 and 2 apart, the half-row and row mirrors for 4 and 8 apart (after the
-// steps before them every lane of a quad, then of a half-row, holds the same value), a lane swap
-// beyond 16.
-template <int CTRL>
-__device__ __forceinline__ float dpp_move(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-
-template <int G>
-__device__ __forceinline__ float group_max(float v) {
-  if constexpr (G >= 2) v = fmaxf(v, dpp_move<0xB1>(v));    // quad_perm [1, 0, 3, 2]
-  if constexpr (G >= 4) v = fmaxf(v, dpp_move<0x4E>(v));    // quad_perm [2, 3, 0, 1]
-  if constexpr (G >= 8) v = fmaxf(v, dpp_move<0x141>(v));   // row_half_mirror
-  if constexpr (G >= 16) v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
-  if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16));
-  if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
-}
-
-template <int K>
-__device__ __forceinline__ void snap16_store(const bf16* hi, const bf16* lo, short* dst, float* dst_scale, int lane) {
-  constexpr int G = K / 8;  // lanes per row
-  float x[8], mx = 0.f;
-  const bf16x8 h8 = *(const bf16x8*)hi, l8 = *(const bf16x8*)lo;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    x[i] = (float)h8[i] + (float)l8[i];
-    mx = fmaxf(mx, fabsf(x[i]));
-  }
-  mx = group_max<G>(mx);
-  // floor(log2 mx) from the exponent field (0 and subnormal maxima land on the lower clamp)
-  const int e = min(max((int)((__float_as_uint(mx) >> 23) & 0xff) - 127 - 14, -126), 113);
-  i16x8 out;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) out[i] = (short)__builtin_amdgcn_fmed3f(rintf(ldexpf(x[i], -e)), -32767.f, 32767.f);
-  *gmem((i16x8*)dst) = out;
-  if ((lane & (G - 1)) == 0) *gmem(dst_scale) = ldexpf(1.f, e);
-}
 
 // ===========================================================================
 // gdn_fwd_state for K <= 128 with 8 wavefronts, with the chunk output fused in: waves 0-3 compute
@@ -981,7 +993,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
       pk.store(sK + q * (BT * LDK), LDK, chunk_len(min(c + 1, cl)), lm);
       load_k(min(c + 2, cl));
       constexpr int VPR = K / 8;
-      if (a.snap16) {
+      if (a.snap16 & 1) {
 #pragma unroll
         for (int j = 0; j < (VB * VPR) / NM; ++j) {
           const int idx = lm + j * NM, r = idx / VPR, cc = (idx % VPR) * 8;
@@ -1219,10 +1231,11 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
 // ===========================================================================
 // gdn_fwd_o: grid (NTG, H)
 // ===========================================================================
-template <int K>
+// S16: the state snapshots are int16 rows with a scale per row (else hi/lo pairs)
+template <int K, bool S16>
 __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, const int V) {
   constexpr int LDQ = K + 4, LDK = K + 8, LDP = BT + 1;
-  // the state enters as a hi/lo pair, staged per 64 value columns x KS key rows
+  // the state is staged as a hi/lo pair per 64 value columns x KS key rows
   constexpr int KS = K > 128 ? 128 : K, NKS = K / KS, LDS_ = KS + 8;
   constexpr long kRegion = (long)BT * LDK * 2 > 2L * 64 * LDS_ * 2 ? (long)BT * LDK * 2 : 2L * 64 * LDS_ * 2;
   constexpr long kBytes = (long)BT * LDQ * 4 + kRegion + 2L * BT * LDP * 4 + 2 * BT * 4 + 64;
@@ -1249,13 +1262,18 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
 
   // state slice (hi/lo) of step `it` = (value block it / NKS, key slice it % NKS) and, at a new value
   // block, its U, one step ahead
-  PrefetchBf16<KS, 64> pS, pSl;
+  PrefetchBf16<KS, 64> pS;
+  PrefetchBf16<S16 ? 8 : KS, S16 ? 1 : 64> pSl;  // the lo parts (hi/lo snapshots only)
+  float sc[PrefetchBf16<KS, 64>::N];              // row scales (int16 snapshots)
   PrefetchF32<64, BT> pU;
   auto issue = [&](int it) {
     const int v0 = (it / NKS) * 64, ks = (it % NKS) * KS;
     const long so = (((long)gc * a.H + h) * V + v0) * K + ks;
     pS.load((const bf16*)a.hT + so, K, 64);
-    pSl.load((const bf16*)a.hTl + so, K, 64);
+    if constexpr (S16)
+      pS.load_scales((const float*)a.hTl + ((long)gc * a.H + h) * V + v0, 64, sc);
+    else
+      pSl.load((const bf16*)a.hTl + so, K, 64);
     if (ks == 0) pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, L);
   };
   issue(0);
@@ -1304,8 +1322,12 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_o_kernel(const GdnArgs a, co
   f32x16 acc = zero16();
   for (int it = 0; it < nit; ++it) {
     const int v0 = (it / NKS) * 64, ks = (it % NKS) * KS;
-    pS.store(sHt, LDS_, nullptr, 0);
-    pSl.store(sHtl, LDS_, nullptr, 0);
+    if constexpr (S16) {
+      pS.store_s16_split(sHt, sHtl, LDS_, sc);
+    } else {
+      pS.store(sHt, LDS_, nullptr, 0);
+      pSl.store(sHtl, LDS_, nullptr, 0);
+    }
     if (ks == 0) pU.store(nullptr, 0, sUT, LDP);
     __syncthreads();
     if (it + 1 < nit) issue(it + 1);
@@ -1506,8 +1528,20 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
     // the previous chunk's loads: waves 2-3 at once, waves 0-1 after their dU products (issued
     // first, a stalled memory queue held the products)
     if (w >= 2 && c > 0) issue(c - 1);
-    lds_to_global_bf16<K>((bf16*)a.dhT + (((long)gc * a.H + h) * V + v0) * K, K, sdST, LDK, VB);
-    lds_to_global_bf16<K>((bf16*)a.dhTl + (((long)gc * a.H + h) * V + v0) * K, K, sdSTl, LDK, VB);
+    if (a.snap16 & 2) {
+      // int16 rows with a scale per row (a row's K / 8 lanes are an aligned lane group)
+      constexpr int VPR = K / 8;
+#pragma unroll
+      for (int j = 0; j < (VB * VPR) / kThreads; ++j) {
+        const int idx = tid + j * kThreads, r = idx / VPR, cc = (idx % VPR) * 8;
+        const long row = ((long)gc * a.H + h) * V + v0 + r;
+        snap16_store<K>(sdST + r * LDK + cc, sdSTl + r * LDK + cc, (short*)a.dhT + row * K + cc,
+                        (float*)a.dhTl + row, tid);
+      }
+    } else {
+      lds_to_global_bf16<K>((bf16*)a.dhT + (((long)gc * a.H + h) * V + v0) * K, K, sdST, LDK, VB);
+      lds_to_global_bf16<K>((bf16*)a.dhTl + (((long)gc * a.H + h) * V + v0) * K, K, sdSTl, LDK, VB);
+    }
     if (w < 2) {
       f32x16 acc = zero16(), acc2 = zero16();
       for (int k0 = 0; k0 < BT; k0 += 16) {
@@ -1793,7 +1827,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
     {
       constexpr int VPR = K / 8;
       const int gc = gc0 + c;
-      if (a.snap16) {
+      if (a.snap16 & 2) {
 #pragma unroll
         for (int j = 0; j < (VB * VPR) / NM; ++j) {
           const int idx = tid + j * NM, r = idx / VPR, cc = (idx % VPR) * 8;
@@ -1885,7 +1919,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
 // from four-row patches; U, dU are stored as hi/lo rows; the post phase stores dPs^T, Qc^T, K^T
 // (hi/lo where fp32) and does its row / column reductions over LDS with all threads.
 // ===========================================================================
-template <int K>
+template <int K, bool SH, bool SD>
 __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_v2_kernel(const GdnArgs a, const int V) {
   constexpr int LDB = 64 + 8, LDE = 64 + 4, TILE = 64 * LDB;
   constexpr long kLoop = 9L * TILE * 2;
@@ -1929,7 +1963,11 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_v2_kernel(const GdnArgs
   f32x16 dQi = zero16(), dKs = zero16(), dW = zero16(), dP = zero16();
   float hds = 0.f;
 
-  PatchBf16<64, 64> pH, pHl, pD, pDl;
+  // the state (SH) and state-gradient (SD) snapshots: int16 rows with row scales, else hi/lo pairs
+  PatchBf16<64, 64> pH, pD;
+  PatchBf16<64, SH ? 4 : 64> pHl;
+  PatchBf16<64, SD ? 4 : 64> pDl;
+  float scH[PatchBf16<64, 64>::N][4], scD[PatchBf16<64, 64>::N][4];
   PrefetchBf16<64, 64> pO;
   PrefetchF32Split<64, 64> pU, pdU;
   PatchF32<64, 64> pQ;
@@ -1939,9 +1977,16 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_v2_kernel(const GdnArgs
   auto issue_loop = [&](int v0) {
     const long so = (((long)gc * a.H + h) * V + v0) * K + k0c;
     pH.load((const bf16*)a.hT + so, K, 64, tid);
-    pHl.load((const bf16*)a.hTl + so, K, 64, tid);
     pD.load((const bf16*)a.dhT + so, K, 64, tid);
-    pDl.load((const bf16*)a.dhTl + so, K, 64, tid);
+    const long sb = ((long)gc * a.H + h) * V + v0;
+    if constexpr (SH)
+      pH.load_scales((const float*)a.hTl + sb, 64, tid, scH);
+    else
+      pHl.load((const bf16*)a.hTl + so, K, 64, tid);
+    if constexpr (SD)
+      pD.load_scales((const float*)a.dhTl + sb, 64, tid, scD);
+    else
+      pDl.load((const bf16*)a.dhTl + so, K, 64, tid);
     pO.load((const bf16*)a.dout + (tok0 * a.H + h) * (long)V + v0, rsv, L);
     pU.load(a.U + (tok0 * a.H + h) * (long)V + v0, rsv, tid, L);
     pdU.load(a.dU + (tok0 * a.H + h) * (long)V + v0, rsv, tid, L);
@@ -1959,10 +2004,18 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_dqkw_v2_kernel(const GdnArgs
   issue_loop(0);
 
   for (int v0 = 0; v0 < V; v0 += 64) {
-    pH.store_t(sHk, LDB, 64, tid);
-    pHl.store_t(sHkl, LDB, 64, tid);
-    pD.store_t(sDk, LDB, 64, tid);
-    pDl.store_t(sDkl, LDB, 64, tid);
+    if constexpr (SH) {
+      pH.store_t_s16(sHk, sHkl, LDB, scH, tid);
+    } else {
+      pH.store_t(sHk, LDB, 64, tid);
+      pHl.store_t(sHkl, LDB, 64, tid);
+    }
+    if constexpr (SD) {
+      pD.store_t_s16(sDk, sDkl, LDB, scD, tid);
+    } else {
+      pD.store_t(sDk, LDB, 64, tid);
+      pDl.store_t(sDkl, LDB, 64, tid);
+    }
     pO.store(sdO, LDB, nullptr, 0);
     pU.store(sUh, sUl, LDB, tid, L);
     pdU.store(sdUh, sdUl, LDB, tid, L);
@@ -4255,7 +4308,12 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       break;
     case kGdnFwdO:
       // for K <= 128 the forward walk writes the output itself
-      if constexpr (K > 128) hipLaunchKernelGGL(gdn_fwd_o_kernel<K>, dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      if constexpr (K > 128) {
+        if (a.snap16 & 1)
+          hipLaunchKernelGGL((gdn_fwd_o_kernel<K, true>), dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+        else
+          hipLaunchKernelGGL((gdn_fwd_o_kernel<K, false>), dim3(a.NTG, a.H), dim3(kThreads), 0, st, a, V);
+      }
       break;
     case kGdnBwdState:
       if (K <= 128)
@@ -4285,8 +4343,15 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
         hipLaunchKernelGGL(gdn_bwd_dqkw_v4_kernel<64>, dim3(min(a.NTG * a.H, cu_count())), dim3(kWalk8), 0, st, a);
       } else if (K == 128)
         hipLaunchKernelGGL(gdn_bwd_dqkw_v3_kernel<128>, dim3(1, a.NTG, a.H), dim3(kWalk8), 0, st, a, V);
-      else
-        hipLaunchKernelGGL(gdn_bwd_dqkw_v2_kernel<K>, dim3((K / 64) * a.NTG * a.H), dim3(kThreads), 0, st, a, V);
+      else {
+        const dim3 grid((K / 64) * a.NTG * a.H);
+        switch (a.snap16 & 3) {
+          case 3: hipLaunchKernelGGL((gdn_bwd_dqkw_v2_kernel<K, true, true>), grid, dim3(kThreads), 0, st, a, V); break;
+          case 1: hipLaunchKernelGGL((gdn_bwd_dqkw_v2_kernel<K, true, false>), grid, dim3(kThreads), 0, st, a, V); break;
+          case 2: hipLaunchKernelGGL((gdn_bwd_dqkw_v2_kernel<K, false, true>), grid, dim3(kThreads), 0, st, a, V); break;
+          default: hipLaunchKernelGGL((gdn_bwd_dqkw_v2_kernel<K, false, false>), grid, dim3(kThreads), 0, st, a, V);
+        }
+      }
       break;
     case kGdnBwdWy:
       if (K <= 128 && (V == 64 || V == 128)) {

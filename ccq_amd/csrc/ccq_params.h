@@ -116,11 +116,13 @@ namespace ccq {
 //   tmat [NTG, H, 64, 64] fp32    T = (I + A)^-1 of the WY representation
 //   w, wl [tokens, H, K] bf16     w = T diag(beta exp(G)) K as a hi/lo pair
 //   u    [tokens, H, V] fp32      u = T diag(beta) V
-//   hT   [NTG, H, V, K] bf16      state at each chunk start (transposed); hTl its low part
+//   hT   [NTG, H, V, K] 16-bit    state at each chunk start (transposed): int16 rows with hTl
+//                                 [NTG, H, V] fp32 their power-of-two scales (snap16), else bf16
+//                                 with hTl [NTG, H, V, K] bf16 its low part
 //   U    [tokens, H, V] fp32      U = u - w S (pseudo-values after the delta correction)
 //   PT   [NTG, H, 64, 64] fp32    P^T, P = scale (Qc K^T o Gamma), causal incl. diagonal
 //   dU   [tokens, H, V] fp32      gradient of U
-//   dhT  [NTG, H, V, K] bf16      gradient of the state after each chunk (transposed); dhTl low part
+//   dhT  [NTG, H, V, K] 16-bit    gradient of the state after each chunk (transposed), dhTl as hTl
 //   dq32 / dkp32 / dw32 [tokens, H, K] fp32, dgp [K/64, tokens, H] fp32
 enum GdnStage { kGdnPrep = 0, kGdnFwdState, kGdnFwdO, kGdnBwdState, kGdnBwdDqkw, kGdnBwdWy };
 
@@ -141,7 +143,7 @@ struct GdnArgs {
   void* wl;                 // bf16 low part of w (w + wl ~ fp32)
   float* u;
   void* hT;
-  void* hTl;                // bf16 low parts of hT (hT + hTl ~ fp32 state)
+  void* hTl;                // row scales of hT (snap16), else its bf16 low parts
   float* U;
   float* PT;
   void* o;                  // bf16 [tokens, H, V]
@@ -151,7 +153,7 @@ struct GdnArgs {
   const float* ds_fin;      // fp32 [N, H, K, V] (nullable)
   float* dU;
   void* dhT;
-  void* dhTl;               // bf16 low parts of dhT
+  void* dhTl;               // row scales of dhT (snap16), else its bf16 low parts
   float* dq32;              // gradient of the cleaned query
   float* dkp32;             // gradient of k (state/output part)
   float* dw32;
@@ -165,7 +167,7 @@ struct GdnArgs {
   int T, H, N, NT, NTG;     // NT: chunks per sequence (dense); NTG: total chunks
   // state and state-gradient snapshots as int16 rows with a power-of-two scale per row (hT / dhT hold
   // the integers, hTl / dhTl the fp32 row scales [NTG * H, V]) instead of hi/lo bf16 pairs: set for
-  // K = V = 128, whose dq/dk/dw kernel reads that form
+  // K = 64 and 256 and for K = V = 128, whose dq/dk/dw (and K = 256 output) kernels read that form
   int snap16;
 };
 

@@ -20,6 +20,7 @@ namespace ccq {
 
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));  // int16 bit patterns of a 16-byte piece
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -377,6 +378,36 @@ struct PrefetchBf16 {
       }
     }
   }
+  // The pieces hold int16 rows of a block-floating-point tile (each row an integer vector times a
+  // power-of-two scale): the scale of each piece's row from `scales` (one per row, nvalid rows)
+  __device__ __forceinline__ void load_scales(const float* scales, int nvalid, float (&sc)[N]) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = threadIdx.x + j * kThreads, r = idx / VPR;
+      sc[j] = (idx < ROWS * VPR && r < nvalid) ? scales[r] : 0.f;
+    }
+  }
+  // row-major copy of scale x integer as a hi/lo pair (exact: the value has at most 16 significant bits)
+  __device__ __forceinline__ void store_s16_split(bf16* hi, bf16* lo, int ld, const float (&sc)[N]) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      if (idx >= ROWS * VPR) continue;
+      const int r = idx / VPR, c = (idx % VPR) * 8;
+      // reinterpret the whole piece: a bit cast of one vector element reads element 0 here
+      const s16x8 x = __builtin_bit_cast(s16x8, v[j]);
+      bf16x8 h8, l8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        bf16 a, b;
+        split2(sc[j] * (float)x[i], a, b);
+        h8[i] = a;
+        l8[i] = b;
+      }
+      *(bf16x8*)(hi + r * ld + c) = h8;
+      *(bf16x8*)(lo + r * ld + c) = l8;
+    }
+  }
 };
 
 template <int D, int ROWS>
@@ -534,6 +565,44 @@ struct PatchBf16 {
         bf16x8 x = v[j][i];
         if (4 * rg + i >= nvalid) x = bf16x8{};
         *(bf16x8*)(dst + (4 * rg + i) * ld + 8 * cg) = x;
+      }
+    }
+  }
+  // int16 rows of a block-floating-point tile: the scale of each of a patch's four rows (nvalid rows)
+  __device__ __forceinline__ void load_scales(const float* scales, int nvalid, int lt, float (&sc)[N][4]) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      int rg, cg;
+      coords(min(lt + j * NTHR, NP - 1), rg, cg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[j][i] = scales[4 * rg + i < nvalid ? 4 * rg + i : 0];
+    }
+  }
+  // transposed copy of rowscale[i] x integer (the pieces hold int16 bit patterns), split into hi/lo
+  // (exact: the value has at most 16 significant bits)
+  __device__ __forceinline__ void store_t_s16(bf16* hi_t, bf16* lo_t, int ldt, const float (&rowscale)[N][4],
+                                              int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int p = lt + j * NTHR;
+      if (NP % NTHR != 0 && p >= NP) continue;
+      int rg, cg;
+      coords(p, rg, cg);
+      s16x8 x[4];  // whole pieces reinterpreted (a bit cast of one vector element reads element 0)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = __builtin_bit_cast(s16x8, v[j][i]);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        bf16x4 ch, cl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16 a, b;
+          split2(rowscale[j][i] * (float)x[i][c], a, b);
+          ch[i] = a;
+          cl[i] = b;
+        }
+        *(bf16x4*)(hi_t + (8 * cg + c) * ldt + 4 * rg) = ch;
+        *(bf16x4*)(lo_t + (8 * cg + c) * ldt + 4 * rg) = cl;
       }
     }
   }
