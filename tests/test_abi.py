@@ -104,10 +104,17 @@ def test_workspace_sizes_are_consistent(K, V):
     tokens, H = 4096, 4
     nt = tokens // 64
     saved = lib.ccq_gdn_saved_bytes(tokens, nt, H, K, V)
-    # gcum + T + w (hi, lo) + u + hT (hi, lo) + U + P^T, each rounded up to 256 bytes
+    # gcum + T + w (hi, lo) + u + hT + U + P^T, each rounded up to 256 bytes; at these shapes the state
+    # snapshots hT are int16 rows with one fp32 scale per row
     expect = tokens * H * 4 + nt * H * 4096 * 4 + 2 * tokens * H * K * 2 + tokens * H * V * 4 \
-        + 2 * nt * H * V * K * 2 + tokens * H * V * 4 + nt * H * 4096 * 4
+        + nt * H * V * (K * 2 + 4) + tokens * H * V * 4 + nt * H * 4096 * 4
     assert expect <= saved <= expect + 8 * 256
+    # the backward's workspace: dU + dhT + dk (state part) + dw + per-block dg partials; the
+    # state-gradient snapshots dhT are int16 rows with row scales at K = V = 128, hi/lo pairs elsewhere
+    gws = lib.ccq_gdn_bwd_workspace_bytes(tokens, nt, H, K, V)
+    dh = nt * H * V * (K * 2 + 4) if (K, V) == (128, 128) else 2 * nt * H * V * K * 2
+    gexpect = tokens * H * V * 4 + dh + 2 * tokens * H * K * 4 + (K // 64) * tokens * H * 4
+    assert gexpect <= gws <= gexpect + 6 * 256
     csaved = lib.ccq_clean_saved_bytes(tokens, 1, tokens, 1, H, K, 0)
     ws = lib.ccq_clean_bwd_workspace_bytes(tokens, 1, tokens, 1, H, K, 0, 0)
     if K in (64, 128):
