@@ -872,7 +872,8 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_state_kernel(const GdnArgs a
 // reads free of bank conflicts; rows are written by 16 consecutive lanes per row.  For K = 128 the
 // buffers fill the 160 KiB of LDS.
 // ===========================================================================
-template <int K, bool Q32>
+// S16: the state snapshots leave as int16 rows with row scales (else hi/lo pairs)
+template <int K, bool Q32, bool S16>
 __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs a, const int V) {
   constexpr int VB = 32, LDK = K + 16, LDB = BT + 16, LDV = VB + 4, LDO = VB + 4;
   constexpr int NM = 256;               // memory threads
@@ -993,7 +994,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_fwd_state_v3_kernel(const GdnArgs 
       pk.store(sK + q * (BT * LDK), LDK, chunk_len(min(c + 1, cl)), lm);
       load_k(min(c + 2, cl));
       constexpr int VPR = K / 8;
-      if (a.snap16 & 1) {
+      if constexpr (S16) {
 #pragma unroll
         for (int j = 0; j < (VB * VPR) / NM; ++j) {
           const int idx = lm + j * NM, r = idx / VPR, cc = (idx % VPR) * 8;
@@ -1651,7 +1652,8 @@ __global__ __launch_bounds__(kThreads) void gdn_bwd_state_kernel(const GdnArgs a
 // ===========================================================================
 // Q32: the cleaned query arrives in fp32 (else bf16); a template parameter, so the memory loop has
 // a single path.
-template <int K, bool Q32>
+// SD: the state-gradient snapshots leave as int16 rows with row scales (else hi/lo pairs)
+template <int K, bool Q32, bool SD>
 __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs a, const int V) {
   constexpr int VB = 32, LDK = K + 16, LDP = BT + 16, LDO = VB + 16;
   constexpr int NM = 256;
@@ -1827,7 +1829,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_state_v3_kernel(const GdnArgs 
     {
       constexpr int VPR = K / 8;
       const int gc = gc0 + c;
-      if (a.snap16 & 2) {
+      if constexpr (SD) {
 #pragma unroll
         for (int j = 0; j < (VB * VPR) / NM; ++j) {
           const int idx = tid + j * NM, r = idx / VPR, cc = (idx % VPR) * 8;
@@ -4299,10 +4301,16 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
     case kGdnFwdState:
       if (K <= 128) {
         constexpr int KW = K <= 128 ? K : 128;
-        if (a.qc32)
-          hipLaunchKernelGGL((gdn_fwd_state_v3_kernel<KW, true>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
+        const dim3 grid((V / 32) * a.N * a.H);
+        const bool s16 = a.snap16 & 1;
+        if (a.qc32 && s16)
+          hipLaunchKernelGGL((gdn_fwd_state_v3_kernel<KW, true, true>), grid, dim3(kWalk8), 0, st, a, V);
+        else if (a.qc32)
+          hipLaunchKernelGGL((gdn_fwd_state_v3_kernel<KW, true, false>), grid, dim3(kWalk8), 0, st, a, V);
+        else if (s16)
+          hipLaunchKernelGGL((gdn_fwd_state_v3_kernel<KW, false, true>), grid, dim3(kWalk8), 0, st, a, V);
         else
-          hipLaunchKernelGGL((gdn_fwd_state_v3_kernel<KW, false>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
+          hipLaunchKernelGGL((gdn_fwd_state_v3_kernel<KW, false, false>), grid, dim3(kWalk8), 0, st, a, V);
       } else
         hipLaunchKernelGGL(gdn_fwd_state_kernel<K>, dim3((V / 32) * a.N * a.H), dim3(kThreads), 0, st, a, V);
       break;
@@ -4319,10 +4327,16 @@ static hipError_t gdn_stage_k(int stage, const GdnArgs& a, int V, hipStream_t st
       if (K <= 128)
       {
         constexpr int KW = K <= 128 ? K : 128;
-        if (a.qc32)
-          hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, true>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
+        const dim3 grid((V / 32) * a.N * a.H);
+        const bool s16 = a.snap16 & 2;
+        if (a.qc32 && s16)
+          hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, true, true>), grid, dim3(kWalk8), 0, st, a, V);
+        else if (a.qc32)
+          hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, true, false>), grid, dim3(kWalk8), 0, st, a, V);
+        else if (s16)
+          hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, false, true>), grid, dim3(kWalk8), 0, st, a, V);
         else
-          hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, false>), dim3((V / 32) * a.N * a.H), dim3(kWalk8), 0, st, a, V);
+          hipLaunchKernelGGL((gdn_bwd_state_v3_kernel<KW, false, false>), grid, dim3(kWalk8), 0, st, a, V);
       }
       else
       {
