@@ -414,6 +414,8 @@ def run_layer(args, dev, which):
         torch.autograd.grad(y, [xin] + params, dy)
 
     dt = _timed_steps(step, args.steps, args.warmup)
+    if args.copy_calibration:
+        copy_calibration(dev)
     return _line(desc, b * t / dt, "tokens/s", args, dt * 1e3, "bf16",
                  "synthetic (seeded; x ~ N(0,1); the reference layer's own random init)",
                  {"workload": f"{which.upper()} single layer fwd+bwd", "B": b, "T": t})
