@@ -54,6 +54,9 @@ SIGNATURES = {
     "ccq_gated_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I]),
     "ccq_gated_rmsnorm_fwd": (_I, [_P] * 5 + [_I64, _I, _F, _P]),
     "ccq_gated_rmsnorm_bwd": (_I, [_P] * 9 + [_I64, _I, _P]),
+    "ccq_narrow_linear_bwd_workspace_bytes": (_SZ, [_I64, _I, _I]),
+    "ccq_narrow_linear_fwd": (_I, [_P, _I64, _P, _P, _P, _I64, _I, _I, _P]),
+    "ccq_narrow_linear_bwd": (_I, [_P, _I64] + [_P] * 6 + [_I64, _I, _I, _P]),
     "ccq_l2norm_fwd": (_I, [_P, _P, _P, _I64, _I, _F, _P]),
     "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
     "ccq_gdn_decode_prologue": (_I, [_P] * 5 + [_I64] + [_P] * 19 + [_I] * 7 + [_F, _P]),
@@ -107,7 +110,7 @@ KERNELS = ("conv_fwd", "conv_bwd", "gnorm_fwd", "gnorm_bwd",
            "clean_bwd_gate",
            "gdn_prep", "gdn_fwd_state", "gdn_fwd_o", "gdn_bwd_state", "gdn_bwd_dqkw", "gdn_bwd_wy",
            "gla_intra", "gla_fwd_state", "gla_fwd_o", "gla_bwd_state", "gla_bwd_dv", "gla_bwd_dqk", "gla_bwd_gk",
-           "clean_z_fwd", "clean_z_bwd")
+           "clean_z_fwd", "clean_z_bwd", "narrow_fwd", "narrow_bwd")
 
 
 def timing_enable(on: bool) -> None:

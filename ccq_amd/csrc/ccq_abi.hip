@@ -26,6 +26,8 @@ hipError_t launch_l2norm_fwd(const L2NormArgs& a, hipStream_t st);
 hipError_t launch_conv(int stage, const ConvArgs& a, int blocks, hipStream_t st);
 hipError_t launch_gnorm(int stage, const GNormArgs& a, int blocks, hipStream_t st);
 hipError_t launch_decode_prologue(const DecProArgs& a, hipStream_t st);
+hipError_t launch_narrow(int stage, const NarrowArgs& a, hipStream_t st);
+int narrow_blocks(long M);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
@@ -686,6 +688,63 @@ int ccq_conv_bwd(const void* x, const float* weight, const float* bias, const fl
   return hip_status(launch_sum_rows2(wk.dw_part, dweight, D * W, dbias ? wk.db_part : nullptr, dbias, dbias ? D : 0,
                                      nb, wk.red, st),
                     "ccq_conv_bwd(dweight, dbias)");
+}
+
+size_t ccq_narrow_linear_bwd_workspace_bytes(int64_t rows, int K, int N) {
+  Slicer sl{nullptr};
+  const int nb = narrow_blocks(rows);
+  sl.take<float>((size_t)nb * N * K);
+  sl.take<float>((size_t)nb * N);
+  sl.take<float>((size_t)kSumSlices * N * (K + 1));
+  return sl.off;
+}
+
+static int narrow_check(const char* who, int64_t rows, int K, int N, int64_t ldx) {
+  if (rows < 0 || N < 1 || N > 16 || K < 32 || K > 2016 || K % 32 || ldx < K || ldx % 8)
+    return fail(CCQ_ERR_SHAPE, "%s: rows=%lld K=%d N=%d ldx=%lld (need 1 <= N <= 16, K a multiple of 32 in [32, 2016], "
+                "ldx >= K and a multiple of 8)", who, (long long)rows, K, N, (long long)ldx);
+  return CCQ_OK;
+}
+
+int ccq_narrow_linear_fwd(const void* x, int64_t ldx, const void* weight, const float* bias, void* y, int64_t rows,
+                          int K, int N, void* stream) {
+  if (int s = narrow_check("ccq_narrow_linear_fwd", rows, K, N, ldx)) return s;
+  if (!x || !weight || !y) return fail(CCQ_ERR_NULL, "ccq_narrow_linear_fwd: x, weight, y are required");
+  if (!aligned16(x) || !aligned16(weight))
+    return fail(CCQ_ERR_ALIGN, "ccq_narrow_linear_fwd: x and weight must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (int s = check_stream_device(st, "ccq_narrow_linear_fwd")) return s;
+  NarrowArgs a{};
+  a.x = x; a.ldx = ldx; a.w = weight; a.b = bias; a.y = y; a.M = rows; a.K = K; a.N = N;
+  return hip_status(timed("narrow_fwd", st, [&] { return launch_narrow(0, a, st); }), "ccq_narrow_linear_fwd");
+}
+
+int ccq_narrow_linear_bwd(const void* x, int64_t ldx, const void* weight, const void* dy, void* dx, float* dweight,
+                          float* dbias, void* workspace, int64_t rows, int K, int N, void* stream) {
+  if (int s = narrow_check("ccq_narrow_linear_bwd", rows, K, N, ldx)) return s;
+  if (!x || !weight || !dy || !dweight || !workspace)
+    return fail(CCQ_ERR_NULL, "ccq_narrow_linear_bwd: x, weight, dy, dweight and the workspace are required");
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(dx) || !aligned16(workspace))
+    return fail(CCQ_ERR_ALIGN, "ccq_narrow_linear_bwd: x, weight, dx, workspace must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (int s = check_stream_device(st, "ccq_narrow_linear_bwd")) return s;
+  if (rows == 0) {
+    if (int s = hip_status(launch_fill_zero(dweight, (long)N * K, st), "ccq_narrow_linear_bwd(dweight)")) return s;
+    return dbias ? hip_status(launch_fill_zero(dbias, (long)N, st), "ccq_narrow_linear_bwd(dbias)") : CCQ_OK;
+  }
+  const int nb = narrow_blocks(rows);
+  Slicer sl{(char*)workspace};
+  float* dw_part = sl.take<float>((size_t)nb * N * K);
+  float* db_part = sl.take<float>((size_t)nb * N);
+  float* red = sl.take<float>((size_t)kSumSlices * N * (K + 1));
+  NarrowArgs a{};
+  a.x = x; a.ldx = ldx; a.w = weight; a.dy = dy; a.dx = dx; a.dw_part = dw_part; a.db_part = dbias ? db_part : nullptr;
+  a.M = rows; a.K = K; a.N = N;
+  if (int s = hip_status(timed("narrow_bwd", st, [&] { return launch_narrow(1, a, st); }), "ccq_narrow_linear_bwd"))
+    return s;
+  return hip_status(launch_sum_rows2(dw_part, dweight, N * K, dbias ? db_part : nullptr, dbias, dbias ? N : 0, nb, red,
+                                     st),
+                    "ccq_narrow_linear_bwd(dweight, dbias)");
 }
 
 size_t ccq_gated_rmsnorm_bwd_workspace_bytes(int64_t rows, int dv) {

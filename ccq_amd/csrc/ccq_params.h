@@ -13,6 +13,8 @@ namespace ccq {
 
 // slices of the first pass of the column sums of partial rows (launch_sum_rows)
 constexpr int kSumSlices = 32;
+// partial rows of the narrow linear backward (64-row groups, at most this many)
+constexpr int kNarrowBlocks = 256;
 
 // Short causal depthwise convolution (+ activation, + per-head L2 normalisation) of the layer
 // prologue: x, y, yn, dy, dyn, dx bf16 [tokens, D]; weight fp32 [D, W] (tap W-1 on the current
@@ -78,6 +80,26 @@ struct DecProArgs {
 
 // Gated RMSNorm of the layer epilogue: y = x / sqrt(mean(x^2) + eps) * w * silu(g) per row of dv
 // (x, g, y, dy, dx, dg bf16 [rows, dv]; w fp32 [dv] (nullable = ones); rstd fp32 [rows]).
+// Narrow linear map y = x W^T (+ b) with at most 16 outputs per row (the layers' gate projections:
+// d_model -> heads, key_dim -> heads, the low-rank log gate): x [M, K] bf16 (row stride ldx), W [N, K]
+// bf16, b [N] fp32 (nullable), y [M, N] bf16; backward dx [M, K] bf16 (row stride K) and per-block
+// partial rows of dW [blocks, N * K] and db [blocks, N], fp32.
+struct NarrowArgs {
+  const void* x;
+  long ldx;
+  const void* w;
+  const float* b;
+  void* y;
+  const void* dy;           // bf16 [M, N]
+  void* dx;                 // bf16 [M, K] (nullable: no input gradient)
+  float* dw_part;
+  float* db_part;           // nullable
+  long M;
+  int K;
+  int N;
+  int rpb;                  // rows per block (backward)
+};
+
 struct GNormArgs {
   const void* x;
   const void* g;

@@ -7,10 +7,16 @@
 //                      to bf16, as the operators normalise their bf16 inputs) -- the q / k prologue
 //                      in one pass instead of projection -> conv -> SiLU -> l2norm round trips;
 //   gated RMSNorm:     y = x / sqrt(mean(x^2) + eps) * weight * silu(g) per row of head_v_dim.
+//   narrow linear:     y = x W^T (+ b) with N <= 16 outputs per row (the gate projections
+//                      a_proj, b_proj, erase_lambda_proj, gk_proj[0]: ccq/gdn/layer.py:292, 312-316;
+//                      ccq/gla/layer.py:162-163) -- a library GEMM tiles N = 4 as it would N = 1024
+//                      and spends ~100 us on what is one 34 MB read; here one MFMA pass over x.
 // All are HBM-bound streaming passes.  Layout: token-major rows of D channels (bf16); a thread
 // owns 8 consecutive channels (one 16-byte piece per row) and walks a tile of tokens; the
 // channels of one head are consecutive lanes of one wavefront, so per-head sums are lane
 // shuffles.  Weight / bias gradients are per-workgroup partial sums, reduced by a second pass.
+#include <algorithm>
+
 #include "ccq_tile.h"
 #include "ccq_params.h"
 
@@ -587,6 +593,126 @@ __global__ __launch_bounds__(kThreads) void decode_prologue_kernel(const DecProA
   }
 }
 
+// ===========================================================================
+// Narrow linear forward: one wavefront per 16-row tile of x, y[16 x 16] = x[16 x K] W^T[K x 16] by
+// 16x16x32 MFMAs with the x fragments loaded straight from HBM (16 bytes per lane, eight steps in
+// flight) and W (rows past N zero) in LDS.  Output row r, column n: lane (n, r / 4), element r % 4.
+// ===========================================================================
+__global__ __launch_bounds__(kThreads) void narrow_fwd_kernel(const NarrowArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char narrow_smem[];
+  bf16* sw = (bf16*)narrow_smem;  // [16][K + 8]
+  const int K = a.K, LDW = K + 8, KV = K / 8;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  for (int idx = tid; idx < 16 * KV; idx += kThreads) {
+    const int n = idx / KV, c = (idx % KV) * 8;
+    bf16x8 v = bf16x8{};
+    if (n < a.N) v = *gmem((const bf16x8*)((const bf16*)a.w + (long)n * K + c));
+    *(bf16x8*)(sw + n * LDW + c) = v;
+  }
+  __syncthreads();
+  const long ntile = (a.M + 15) / 16;
+  const bf16* wrow = sw + (l & 15) * LDW + 8 * (l >> 4);
+  const int n = l & 15;
+  const float bn = (a.b && n < a.N) ? a.b[n] : 0.f;
+  for (long tile = (long)blockIdx.x * 4 + w; tile < ntile; tile += (long)gridDim.x * 4) {
+    const long row = min(tile * 16 + (l & 15), a.M - 1);
+    const bf16* xr = (const bf16*)a.x + row * a.ldx + 8 * (l >> 4);
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < K; k0 += 256) {
+      bf16x8 xa[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (k0 + 32 * j < K) xa[j] = *gmem((const bf16x8*)(xr + k0 + 32 * j));
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (k0 + 32 * j < K) acc = mfma16(xa[j], *(const bf16x8*)(wrow + k0 + 32 * j), acc);
+    }
+    if (n < a.N) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const long r = tile * 16 + 4 * (l >> 4) + i;
+        if (r < a.M) ((bf16*)a.y)[r * a.N + n] = (bf16)(acc[i] + bn);
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// Narrow linear backward: a workgroup of roundup64(K / 8) threads takes rpb consecutive rows, a
+// thread the same 8 columns of every row.  Per row: dx[8] = sum_n dy[n] W[n][8 cols] (fp32, one
+// 16-byte bf16 store), dW[n][8 cols] += dy[n] x[8 cols], db[n] += dy[n] (thread 0).  dy rows are staged
+// in LDS 64 at a time (broadcast reads); the block's dW / db go out as one partial row each.
+// ===========================================================================
+template <int NP>
+__global__ __launch_bounds__(kThreads) void narrow_bwd_kernel(const NarrowArgs a) {
+  __shared__ float sdy[64][NP];
+  const int K = a.K, KV = K / 8;
+  const int t = threadIdx.x;
+  const bool on = t < KV;
+  const int c = (on ? t : 0) * 8;
+  bf16x8 wv[NP];
+#pragma unroll
+  for (int n = 0; n < NP; ++n) wv[n] = (on && n < a.N) ? *gmem((const bf16x8*)((const bf16*)a.w + (long)n * K + c)) : bf16x8{};
+  float dw[NP][8], db[NP];
+#pragma unroll
+  for (int n = 0; n < NP; ++n) {
+    db[n] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dw[n][j] = 0.f;
+  }
+  const long r0 = (long)blockIdx.x * a.rpb, r1 = min(a.M, r0 + a.rpb);
+  for (long rb = r0; rb < r1; rb += 64) {
+    const int nr = (int)min(64L, r1 - rb);
+    __syncthreads();
+    for (int idx = t; idx < 64 * NP; idx += blockDim.x) {
+      const int rr = idx / NP, n = idx % NP;
+      sdy[rr][n] = (rr < nr && n < a.N) ? (float)((const bf16*)a.dy)[(rb + rr) * a.N + n] : 0.f;
+    }
+    __syncthreads();
+    if (!on) continue;
+    for (int rr = 0; rr < nr; ++rr) {
+      const long r = rb + rr;
+      const bf16x8 xv = *gmem((const bf16x8*)((const bf16*)a.x + r * a.ldx + c));
+      float x8[8], d8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x8[j] = (float)xv[j];
+        d8[j] = 0.f;
+      }
+#pragma unroll
+      for (int n = 0; n < NP; ++n) {
+        const float g = sdy[rr][n];
+        db[n] += g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          d8[j] += g * (float)wv[n][j];
+          dw[n][j] += g * x8[j];
+        }
+      }
+      if (a.dx) {
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = (bf16)d8[j];
+        *gmem((bf16x8*)((bf16*)a.dx + r * K + c)) = o;
+      }
+    }
+  }
+  if (!on) return;
+  float* part = a.dw_part + (long)blockIdx.x * a.N * K;
+#pragma unroll
+  for (int n = 0; n < NP; ++n) {
+    if (n < a.N) {
+      *gmem((f32x4*)(part + (long)n * K + c)) = f32x4{dw[n][0], dw[n][1], dw[n][2], dw[n][3]};
+      *gmem((f32x4*)(part + (long)n * K + c + 4)) = f32x4{dw[n][4], dw[n][5], dw[n][6], dw[n][7]};
+    }
+  }
+  if (a.db_part && t == 0) {
+#pragma unroll
+    for (int n = 0; n < NP; ++n)
+      if (n < a.N) a.db_part[(long)blockIdx.x * a.N + n] = db[n];
+  }
+}
+
 hipError_t launch_decode_prologue(const DecProArgs& a, hipStream_t st) {
   if (a.B <= 0 || a.T <= 0) return hipSuccess;
   const size_t lds = (size_t)a.H * a.K * sizeof(float);
@@ -637,6 +763,31 @@ hipError_t launch_conv(int stage, const ConvArgs& args, int blocks, hipStream_t 
       break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+// Backward blocks of the narrow linear map: 64-row groups, at most kNarrowBlocks partial rows.
+int narrow_blocks(long M) { return (int)std::max<long>(1, std::min<long>((M + 63) / 64, kNarrowBlocks)); }
+
+hipError_t launch_narrow(int stage, const NarrowArgs& args, hipStream_t st) {
+  if (args.M <= 0) return hipSuccess;
+  NarrowArgs a = args;
+  if (stage == 0) {
+    const long tiles = (a.M + 15) / 16;
+    const unsigned grid = (unsigned)std::min<long>((tiles + 3) / 4, 4096);
+    const size_t lds = (size_t)16 * (a.K + 8) * sizeof(bf16);
+    hipLaunchKernelGGL(narrow_fwd_kernel, dim3(grid), dim3(kThreads), lds, st, a);
+    return hipGetLastError();
+  }
+  const int nb = narrow_blocks(a.M);
+  a.rpb = (int)((a.M + nb - 1) / nb);
+  const dim3 block((unsigned)(((a.K / 8 + 63) / 64) * 64));
+  if (a.N <= 4)
+    hipLaunchKernelGGL(narrow_bwd_kernel<4>, dim3(nb), block, 0, st, a);
+  else if (a.N <= 8)
+    hipLaunchKernelGGL(narrow_bwd_kernel<8>, dim3(nb), block, 0, st, a);
+  else
+    hipLaunchKernelGGL(narrow_bwd_kernel<16>, dim3(nb), block, 0, st, a);
   return hipGetLastError();
 }
 

@@ -19,7 +19,7 @@ from . import _lib
 from ._lib import call, ptr, stream_of
 from .clean import check_device
 
-__all__ = ["short_conv", "gated_rmsnorm"]
+__all__ = ["short_conv", "gated_rmsnorm", "narrow_linear", "narrow_ok"]
 
 
 def last_inputs(cache: Optional[torch.Tensor], W: int) -> Optional[torch.Tensor]:
@@ -148,3 +148,57 @@ def gated_rmsnorm(x: torch.Tensor, g: torch.Tensor, weight: Optional[torch.Tenso
     <= 512 wide)."""
     check_device(x.device, g=g, weight=weight)
     return GatedRMSNormFunction.apply(x, g, weight, float(eps))
+
+
+class NarrowLinearFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        K, N = x.shape[-1], weight.shape[0]
+        x2 = x.reshape(-1, K)
+        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        w16 = weight.detach().to(torch.bfloat16).contiguous()
+        b32 = bias.detach().float().contiguous() if bias is not None else None
+        y = torch.empty(x2.shape[0], N, device=x.device, dtype=torch.bfloat16)
+        call("ccq_narrow_linear_fwd", ptr(x2), x2.stride(0), ptr(w16), ptr(b32), ptr(y), x2.shape[0], K, N,
+             stream_of(x))
+        ctx.save_for_backward(x2, w16)
+        ctx.meta = (x.shape, weight.dtype, None if bias is None else bias.dtype)
+        return y.view(*x.shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w16 = ctx.saved_tensors
+        shape, wdtype, bdtype = ctx.meta
+        M, K = x2.shape
+        N = w16.shape[0]
+        d2 = dy.to(torch.bfloat16).reshape(M, N).contiguous()
+        dx = torch.empty(M, K, device=x2.device, dtype=torch.bfloat16) if ctx.needs_input_grad[0] else None
+        dw = torch.empty(N, K, device=x2.device, dtype=torch.float32)
+        db = torch.empty(N, device=x2.device, dtype=torch.float32) if bdtype is not None else None
+        ws = torch.empty(_lib.load().ccq_narrow_linear_bwd_workspace_bytes(M, K, N), device=x2.device,
+                         dtype=torch.uint8)
+        call("ccq_narrow_linear_bwd", ptr(x2), x2.stride(0), ptr(w16), ptr(d2), ptr(dx), ptr(dw), ptr(db), ptr(ws),
+             M, K, N, stream_of(x2))
+        return (dx.view(shape) if dx is not None else None, dw.to(wdtype),
+                db.to(bdtype) if db is not None else None)
+
+
+def narrow_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether ``narrow_linear`` takes this call: bf16 activations and weights on the GPU, at most 16
+    outputs, an input width that is a multiple of 32 in [32, 2016]."""
+    K = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and weight.dim() == 2
+            and weight.shape[0] <= 16 and weight.shape[1] == K and K % 32 == 0 and 32 <= K <= 2016)
+
+
+def narrow_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x @ weight.T + bias`` for a weight of at most 16 rows (bf16, CUDA; fp32 accumulation, one
+    bf16 rounding, as a bf16 GEMM): one MFMA pass over x forward, one pass over x and dy backward
+    (``ccq_narrow_linear_fwd`` / ``_bwd``).  See ``narrow_ok`` for the shapes it takes."""
+    if not narrow_ok(x, weight):
+        raise ValueError(f"narrow_linear: x {tuple(x.shape)} {x.dtype} on {x.device}, weight "
+                         f"{tuple(weight.shape)} {weight.dtype}: needs bf16 on the GPU, <= 16 outputs and an input "
+                         f"width that is a multiple of 32 in [32, 2016]")
+    check_device(x.device, weight=weight, bias=bias)
+    return NarrowLinearFunction.apply(x, weight, bias)

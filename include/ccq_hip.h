@@ -329,6 +329,23 @@ int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, con
                           void* dx, void* dg, float* dweight, void* workspace, int64_t rows, int dv, void* stream);
 
 /*
+ * Narrow linear map y = x W^T (+ b) with N <= 16 outputs per row, and its backward: the layers'
+ * gate projections, nn.Linear in the reference -- erase_lambda_proj on q, a_proj and b_proj on the
+ * hidden states (ccq/gdn/layer.py:174, 183-184, 292, 312, 316), the first factor of the low-rank
+ * log gate and erase_lambda_proj (ccq/gla/layer.py:131, 162, 237-238).  x bf16 [rows, K] with row
+ * stride ldx (a multiple of 8, >= K), weight bf16 [N, K], bias fp32 [N] (nullable), y bf16 [rows, N]
+ * (fp32 accumulation, one rounding, as a bf16 GEMM).  Backward: dy bf16 [rows, N]; dx bf16
+ * [rows, K] contiguous (nullable: not needed); dweight fp32 [N, K]; dbias fp32 [N] (nullable); the
+ * workspace holds ccq_narrow_linear_bwd_workspace_bytes(rows, K, N) bytes.  1 <= N <= 16; K a
+ * multiple of 32 in [32, 2016]; x, weight, dx, workspace 16-byte aligned.
+ */
+size_t ccq_narrow_linear_bwd_workspace_bytes(int64_t rows, int K, int N);
+int ccq_narrow_linear_fwd(const void* x, int64_t ldx, const void* weight, const float* bias, void* y, int64_t rows,
+                          int K, int N, void* stream);
+int ccq_narrow_linear_bwd(const void* x, int64_t ldx, const void* weight, const void* dy, void* dx, float* dweight,
+                          float* dbias, void* workspace, int64_t rows, int K, int N, void* stream);
+
+/*
  * Row L2 normalisation y = x / sqrt(sum x^2 + eps) (bf16 rows of D <= 512) and its backward.
  * Replaces fla l2norm as called by the reference (ccq/ops/ccq_gdn/fused_chunk.py:43-44).
  * rstd fp32 [rows] is written by the forward and read by the backward.
@@ -344,7 +361,7 @@ int ccq_l2norm_bwd(const void* x, const float* rstd, const float* dy_f32, const 
  * gnorm_fwd, gnorm_bwd, clean_fwd_sum, clean_fwd, clean_bwd_rows, clean_bwd_dq, clean_bwd_gsum,
  * clean_bwd_dk, clean_bwd_gate, gdn_prep, gdn_fwd_state, gdn_fwd_o, gdn_bwd_state, gdn_bwd_dqkw,
  * gdn_bwd_wy, gla_intra, gla_fwd_state, gla_fwd_o, gla_bwd_state, gla_bwd_dv, gla_bwd_dqk,
- * gla_bwd_gk, clean_z_fwd, clean_z_bwd) and returns the summed
+ * gla_bwd_gk, clean_z_fwd, clean_z_bwd, narrow_fwd, narrow_bwd) and returns the summed
  * milliseconds and the number of launches since the last ccq_timing_reset.  ccq_timing_select
  * restricts the events to the kernel of that name (NULL: every kernel), so that a timed loop carries
  * one event pair per step instead of one per kernel.
