@@ -808,8 +808,13 @@ int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, cons
       !g || !beta)
     return fail(CCQ_ERR_NULL, "%s: a required pointer is NULL", who);
   if (W > 1 && (!cq || !ck || !cv)) return fail(CCQ_ERR_NULL, "%s: W > 1 needs the three caches", who);
+  if (H * K > 2048) return fail(CCQ_ERR_SHAPE, "%s: H*K=%d above 2048 (one workgroup holds the whole q row)", who, H * K);
   if (!aligned16(xq) || !aligned16(xk) || !aligned16(xv) || !aligned16(q) || !aligned16(k) || !aligned16(v))
     return fail(CCQ_ERR_ALIGN, "%s: the q, k, v rows and outputs must be 16-byte aligned", who);
+  if (!aligned16(wq) || !aligned16(wk) || !aligned16(wv) || !aligned16(bq) || !aligned16(bk) || !aligned16(bv) ||
+      !aligned16(cq) || !aligned16(ck) || !aligned16(cv) || !aligned16(lam_w))
+    return fail(CCQ_ERR_ALIGN, "%s: the convolution weights, biases, caches and the gate weight must be 16-byte aligned",
+                who);
   DecProArgs a{};
   a.xq = xq; a.xk = xk; a.xv = xv; a.xa = xa; a.xb = xb; a.ldx = ldx;
   a.wq = wq; a.wk = wk; a.wv = wv; a.bq = bq; a.bk = bk; a.bv = bv; a.cq = cq; a.ck = ck; a.cv = cv;

@@ -462,97 +462,120 @@ __global__ __launch_bounds__(kThreads) void gnorm_bwd_kernel(const GNormArgs a) 
 }
 
 // ---------------------------------------------------------------------------
-// decode prologue of a CCQ-GDN layer: grid B (one workgroup per sequence), 256 threads.  A thread
-// takes groups of 8 channels: the q groups (H K / 8), then the k groups, then the v groups; the lanes
-// of one head are consecutive lanes of one wavefront (K / 8 of them), so its sum of squares is a lane
-// shuffle in the convolution kernel's order (the same roundings as the layer's unfused path: y to
-// bf16, y / sqrt(|y_h|^2 + eps) from the rounded y, to bf16).  The gate then reads the token's q
-// activations from LDS.  The caches are read for every token of the call and rewritten at the end
-// (each channel by the thread that owns it).
+// decode prologue of a CCQ-GDN layer: grid (B, slices), 256 threads.  Slice 0 takes the q channels
+// (all of them: the gate reads the whole q activation), the λ gate and β / g; the next slices take the
+// k channels and then the v channels, up to 256 groups of 8 channels each.  A thread owns one group:
+// its convolution weights (W 16-byte pieces: the group's [8][W] block), bias and cache window
+// ((W-1) 16-byte pieces: the group's [8][W-1] block) are loaded once, the window slides over the
+// call's tokens in registers, and the last W-1 inputs go back to the cache from the registers.  The
+// lanes of one head are consecutive lanes of one wavefront (K / 8 of them), so the head's sum of
+// squares is a lane shuffle in the convolution kernel's order (the same roundings as the layer's
+// unfused path: y to bf16, y / sqrt(|y_h|^2 + eps) from the rounded y, to bf16).  The gate's logit
+// of head h is the dot product of the whole q activation with row h of its weight: each q thread
+// takes its 8 channels against a 16-byte piece of every row, then lane shuffles and one LDS pass.
 // ---------------------------------------------------------------------------
 template <int W>
 __global__ __launch_bounds__(kThreads) void decode_prologue_kernel(const DecProArgs a) {
-  extern __shared__ float sQ[];                 // the token's q activations (bf16 values), H K
   __shared__ float sPart[kThreads / 64][kDecProMaxH];
-  const int b = blockIdx.x, tid = threadIdx.x, l = lane_id(), wv = wave_id();
+  const int b = blockIdx.x, sl = blockIdx.y, tid = threadIdx.x, l = lane_id(), wv = wave_id();
   const int Dq = a.H * a.K, Dv = a.H * a.V;
-  const int nq = Dq / 8, nv = Dv / 8, ng = 2 * nq + nv;
+  const int nq = Dq / 8, nv = Dv / 8, nks = (nq + kThreads - 1) / kThreads;
   const int hl = a.K / 8;
-  const bf16* lw = (const bf16*)a.lw;
-  // channel group -> tensor, first channel, width
-  auto group = [&](int grp, int& kind, int& c, int& D) {
-    if (grp < nq) {
-      kind = 0; c = 8 * grp; D = Dq;
-    } else if (grp < 2 * nq) {
-      kind = 1; c = 8 * (grp - nq); D = Dq;
-    } else {
-      kind = 2; c = 8 * (grp - 2 * nq); D = Dv;
-    }
-  };
-  auto input8 = [&](int kind, int D, int c, int p, float (&v)[8]) {  // input at call position p (< 0: cache)
-    const bf16* x = (const bf16*)(kind == 0 ? a.xq : kind == 1 ? a.xk : a.xv);
-    const bf16* cache = (const bf16*)(kind == 0 ? a.cq : kind == 1 ? a.ck : a.cv);
-    if (p >= 0) {
-      const bf16x8 xb = *(const bf16x8*)(x + ((long)b * a.T + p) * a.ldx + c);
+  int kind, g0, ng, D;
+  if (sl == 0) {
+    kind = 0; g0 = 0; ng = nq; D = Dq;
+  } else if (sl <= nks) {
+    kind = 1; g0 = (sl - 1) * kThreads; ng = min(kThreads, nq - g0); D = Dq;
+  } else {
+    kind = 2; g0 = (sl - 1 - nks) * kThreads; ng = min(kThreads, nv - g0); D = Dv;
+  }
+  const bool on = tid < ng;
+  const int c = 8 * (g0 + (on ? tid : 0));
+  const bf16* x = (const bf16*)(kind == 0 ? a.xq : kind == 1 ? a.xk : a.xv);
+  const bf16* wt = (const bf16*)(kind == 0 ? a.wq : kind == 1 ? a.wk : a.wv);
+  const bf16* bs = (const bf16*)(kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv);
+  bf16* cache = (bf16*)(kind == 0 ? a.cq : kind == 1 ? a.ck : a.cv);
+  bf16* out = (bf16*)(kind == 0 ? a.q : kind == 1 ? a.k : a.v);
+
+  // the group's weights [8][W], bias, cache window [8][W-1] (in call order: hist[0] the oldest)
+  float wgt[8][W], bias[8], hist[W > 1 ? W - 1 : 1][8];
+  {
+    bf16x8 pw[W];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = (float)xb[i];
+    for (int j = 0; j < W; ++j) pw[j] = *gmem((const bf16x8*)(wt + (long)c * W + 8 * j));
+#pragma unroll
+    for (int e = 0; e < 8 * W; ++e) wgt[e / W][e % W] = (float)pw[e / 8][e % 8];
+    if (bs) {
+      const bf16x8 pb = *gmem((const bf16x8*)(bs + c));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) bias[i] = (float)pb[i];
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = (float)cache[((long)b * D + c + i) * (W - 1) + (W - 1) + p];
+      for (int i = 0; i < 8; ++i) bias[i] = 0.f;
     }
-  };
+    if constexpr (W > 1) {
+      bf16x8 pc[W - 1];
+#pragma unroll
+      for (int j = 0; j < W - 1; ++j) pc[j] = *gmem((const bf16x8*)(cache + ((long)b * D + c) * (W - 1) + 8 * j));
+#pragma unroll
+      for (int e = 0; e < 8 * (W - 1); ++e) hist[e % (W - 1)][e / (W - 1)] = (float)pc[e / 8][e % 8];
+    }
+  }
+  // slice 0: the gate weights of this thread's channels, one 16-byte piece per head
+  bf16x8 lwp[kDecProMaxH];
+  if (kind == 0) {
+#pragma unroll
+    for (int h = 0; h < kDecProMaxH; ++h)
+      if (h < a.H) lwp[h] = *gmem((const bf16x8*)((const bf16*)a.lw + (long)h * Dq + c));
+  }
+
   for (int t = 0; t < a.T; ++t) {
     const long row = (long)b * a.T + t;
-    for (int g0 = 0; g0 < ng; g0 += kThreads) {
-      const int grp = g0 + tid;
-      const bool on = grp < ng;
-      int kind = 2, c = 0, D = Dv;
-      if (on) group(grp, kind, c, D);
-      bf16x8 yb;
-      if (on) {
-        const bf16* wt = (const bf16*)(kind == 0 ? a.wq : kind == 1 ? a.wk : a.wv);
-        const bf16* bs = (const bf16*)(kind == 0 ? a.bq : kind == 1 ? a.bk : a.bv);
-        float xv[8], win[W][8];
-        input8(kind, D, c, t, xv);
+    float xv[8];
+    {
+      const bf16x8 xb = *gmem((const bf16x8*)(x + row * a.ldx + c));
 #pragma unroll
-        for (int w = 0; w < W - 1; ++w)
-          if (w < W - 1) input8(kind, D, c, t - (W - 1) + w, win[w]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float acc = (bs ? (float)bs[c + i] : 0.f) + (float)wt[(long)(c + i) * W + W - 1] * xv[i];
-#pragma unroll
-          for (int w = 0; w < W - 1; ++w)
-            if (w < W - 1) acc += (float)wt[(long)(c + i) * W + w] * win[w][i];
-          yb[i] = (bf16)silu_(acc);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) yb[i] = (bf16)0.f;
-      }
-      // per-head sum of squares (every lane takes part; v and idle lanes form their own groups)
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss += (float)yb[i] * (float)yb[i];
-      ss = head_sum(ss, hl);
-      if (!on) continue;
-      if (kind == 2) {
-        *(bf16x8*)((bf16*)a.v + row * Dv + c) = yb;
-        continue;
-      }
-      const float r = rsqrtf(ss + a.eps);
-      bf16x8 nb;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) nb[i] = (bf16)((float)yb[i] * r);
-      *(bf16x8*)((bf16*)(kind == 0 ? a.q : a.k) + row * Dq + c) = nb;
-      if (kind == 0)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) sQ[c + i] = (float)yb[i];
+      for (int i = 0; i < 8; ++i) xv[i] = (float)xb[i];
     }
-    __syncthreads();
-    // gate logits: per head, partial dot products of the q activations with the head's weight row
-    for (int h = 0; h < a.H; ++h) {
+    bf16x8 yb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float acc = bias[i] + wgt[i][W - 1] * xv[i];
+#pragma unroll
+      for (int w = 0; w < W - 1; ++w) acc += wgt[i][w] * hist[w][i];
+      yb[i] = on ? (bf16)silu_(acc) : (bf16)0.f;
+    }
+    if constexpr (W > 1) {
+#pragma unroll
+      for (int w = 0; w + 1 < W - 1; ++w)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hist[w][i] = hist[w + 1][i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hist[W - 2][i] = xv[i];
+    }
+    if (kind == 2) {
+      if (on) *gmem((bf16x8*)(out + row * Dv + c)) = yb;
+      continue;
+    }
+    // per-head sum of squares (every lane takes part; idle lanes form their own groups)
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += (float)yb[i] * (float)yb[i];
+    ss = head_sum(ss, hl);
+    const float r = rsqrtf(ss + a.eps);
+    bf16x8 nb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) nb[i] = (bf16)((float)yb[i] * r);
+    if (on) *gmem((bf16x8*)(out + row * Dq + c)) = nb;
+    if (kind != 0) continue;
+    // gate logits: this thread's channels against every head's weight row, then the workgroup's sum
+#pragma unroll
+    for (int h = 0; h < kDecProMaxH; ++h) {
+      if (h >= a.H) break;
       float part = 0.f;
-      for (int j = tid; j < Dq; j += kThreads) part += (float)lw[(long)h * Dq + j] * sQ[j];
+      if (on)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part += (float)lwp[h][i] * (float)yb[i];
       part = head_sum(part, 64);
       if (l == 0) sPart[wv][h] = part;
     }
@@ -573,22 +596,14 @@ __global__ __launch_bounds__(kThreads) void decode_prologue_kernel(const DecProA
     }
     __syncthreads();
   }
-  // caches: the inputs at call positions T - (W-1) .. T - 1 (before the call's first token: the
-  // cached ones), read in full before any is written
-  if (W > 1) {
-    for (int grp = tid; grp < ng; grp += kThreads) {
-      int kind, c, D;
-      group(grp, kind, c, D);
-      float nw[W][8];
+  // the cache: the last W-1 inputs of the call (or the kept ones, for T < W-1), from the registers
+  if constexpr (W > 1) {
+    if (on) {
+      bf16x8 pc[W - 1];
 #pragma unroll
-      for (int w = 0; w < W - 1; ++w)
-        if (w < W - 1) input8(kind, D, c, a.T - (W - 1) + w, nw[w]);
-      bf16* cache = (bf16*)(kind == 0 ? a.cq : kind == 1 ? a.ck : a.cv);
+      for (int e = 0; e < 8 * (W - 1); ++e) pc[e / 8][e % 8] = (bf16)hist[e % (W - 1)][e / (W - 1)];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int w = 0; w < W - 1; ++w)
-          if (w < W - 1) cache[((long)b * D + c + i) * (W - 1) + w] = (bf16)nw[w][i];
+      for (int j = 0; j < W - 1; ++j) *gmem((bf16x8*)(cache + ((long)b * D + c) * (W - 1) + 8 * j)) = pc[j];
     }
   }
 }
@@ -715,11 +730,13 @@ __global__ __launch_bounds__(kThreads) void narrow_bwd_kernel(const NarrowArgs a
 
 hipError_t launch_decode_prologue(const DecProArgs& a, hipStream_t st) {
   if (a.B <= 0 || a.T <= 0) return hipSuccess;
-  const size_t lds = (size_t)a.H * a.K * sizeof(float);
+  const int nq = a.H * a.K / 8, nv = a.H * a.V / 8;
+  if (nq > kThreads) return hipErrorInvalidValue;  // the q slice holds every q channel group
+  const dim3 grid((unsigned)a.B, (unsigned)(1 + (nq + kThreads - 1) / kThreads + (nv + kThreads - 1) / kThreads));
   switch (a.W) {
-#define CCQ_DECPRO_W(N)                                                                         \
-  case N:                                                                                       \
-    hipLaunchKernelGGL(decode_prologue_kernel<N>, dim3((unsigned)a.B), dim3(kThreads), lds, st, a); \
+#define CCQ_DECPRO_W(N)                                                        \
+  case N:                                                                      \
+    hipLaunchKernelGGL(decode_prologue_kernel<N>, grid, dim3(kThreads), 0, st, a); \
     break;
     CCQ_DECPRO_W(1) CCQ_DECPRO_W(2) CCQ_DECPRO_W(3) CCQ_DECPRO_W(4) CCQ_DECPRO_W(5) CCQ_DECPRO_W(6)
     CCQ_DECPRO_W(7) CCQ_DECPRO_W(8)

@@ -273,7 +273,9 @@ size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K);
  * bf16 [B, D, W-1] caches (each sequence's previous W-1 inputs), updated in place; lam_w bf16
  * [H, H*K], lam_b bf16 [H] (nullable), A_log, dt_bias bf16 [H].  Outputs: q, k bf16 [B, T, H, K], v
  * bf16 [B, T, H, V], lam, g, beta fp32 [B, T, H] -- the decode step's inputs with use_l2norm = 0.
- * H <= 32; K a power of two in [8, 512]; V % 8 == 0; W in [1, 8].  No allocation; one kernel.
+ * H <= 32; K a power of two in [8, 512]; H*K <= 2048; V % 8 == 0; W in [1, 8]; the convolution
+ * weights, biases, caches and lam_w 16-byte aligned.  No allocation; one kernel (a workgroup per
+ * sequence and slice: the q channels with the gates, then up to 2048 k or v channels each).
  */
 int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, const void* xa, const void* xb,
                             int64_t ldx, const void* wq, const void* wk, const void* wv, const void* bq,
