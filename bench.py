@@ -125,12 +125,13 @@ def kernel_work(k=K, v=V, bt=BT, cb=64):
         "gdn_prep": (2 * bt * (2 * k + v) + (2 * bt * bt) // 3, 2 * k + 2 * v + 8 + 2 * k + 4 * v + 4 + 4 * bt),
         # the forward walk with the chunk output fused in: state path (U = u - w S, S update) plus
         # Y = Qc S, P = Qc K^T and P U; reads k, w / wl, Qc (fp32), g, u; writes U, o, P^T and the
-        # per-chunk state snapshots (hi/lo)
+        # per-chunk state snapshots (int16 rows + one fp32 scale per row)
         "gdn_fwd_state": (4 * k * v + 2 * bt * k + 2 * k * v + 2 * bt * v,
-                          2 * k + 4 * k + 4 * k + 4 + 4 * v + 4 * v + 2 * v + 4 * bt + 4 * k * v // bt),
-        "gdn_bwd_state": (2 * bt * v + 6 * k * v, 4 * bt + 2 * v + 2 * k + 4 * k + 2 * k + 4 * v + 4 * k * v // bt),
+                          2 * k + 4 * k + 4 * k + 4 + 4 * v + 4 * v + 2 * v + 4 * bt + (2 * k + 4) * v // bt),
+        "gdn_bwd_state": (2 * bt * v + 6 * k * v,
+                          4 * bt + 2 * v + 2 * k + 4 * k + 2 * k + 4 * v + (2 * k + 4) * v // bt),
         "gdn_bwd_dqkw": (6 * k * v + 2 * bt * v + 4 * bt * k,
-                         8 * k * v // bt + 2 * v + 4 * v + 4 * v + 4 * k + 2 * k + 4 * bt + 12 * k + 4),
+                         2 * (2 * k + 4) * v // bt + 2 * v + 4 * v + 4 * v + 4 * k + 2 * k + 4 * bt + 12 * k + 4),
         "gdn_bwd_wy": (10 * bt * k + 4 * bt * v + 4 * bt * bt,
                        4 * bt + 4 * k + 4 * v + 2 * k + 2 * v + 4 * k + 4 * k + 2 * v + 8),
     }
@@ -437,7 +438,7 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
     checked against the eager layers' before it is timed."""
     import torch.nn as nn
     import torch.nn.functional as F
-    from ccq_amd.graph import GDNLayerDecode
+    from ccq_amd.graph import GDNLayerDecode, decode_linear
     from ccq_amd.layers import CCQGDN, LayerCache
 
     inter = 256 * ((int(d * 4 * 2 / 3) + 255) // 256)  # fla GatedMLP's intermediate size (hidden_ratio 4)
@@ -458,6 +459,12 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
         def mlp(self, x):
             gt, up = self.gate_up(self.mlp_norm(x)).chunk(2, -1)
             return x + self.down(F.silu(gt) * up)
+
+        def mlp_step(self, x):
+            # the captured decode step's MLP: the two projections as decode_linear launches, the
+            # residual added inside the second
+            gt, up = decode_linear(self.mlp_norm(x), self.gate_up.weight).chunk(2, -1)
+            return decode_linear(F.silu(gt) * up, self.down.weight, x)
 
         def forward(self, x, cache):
             return self.mlp(x + self.attn(self.attn_norm(x), past_key_values=cache, use_cache=True)[0])
@@ -494,7 +501,7 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
     def graph_step():
         x = embed(ids)
         for blk, ld in zip(blocks, lds):
-            x = blk.mlp(x + ld(blk.attn_norm(x)))
+            x = blk.mlp_step(ld(blk.attn_norm(x), x))
         logits = head(norm(x[:, -1]))
         ids.copy_(logits.argmax(-1, keepdim=True))
         return logits

@@ -31,6 +31,8 @@ int narrow_blocks(long M);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
+hipError_t launch_decode_linear(const void* x, long ldx, const void* w, const void* r, long ldr, void* y, long ldy,
+                                int M, int K, int N, hipStream_t st);
 hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st);
 int cseg_count(int N, int H, int T, int K);
 bool cseg_sums_supported(int K);
@@ -789,6 +791,18 @@ int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, con
   if (!dweight) return CCQ_OK;
   return hip_status(launch_sum_rows2(part, dweight, dv, nullptr, nullptr, 0, nb, red, st),
                     "ccq_gated_rmsnorm_bwd(dweight)");
+}
+
+int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
+                      int64_t ldy, int M, int K, int N, void* stream) {
+  const char* who = "ccq_decode_linear";
+  if (M < 0 || M > 16 || N < 0 || K < 32 || K > 4096 || K % 32 || ldx < K || ldx % 8 || ldy < N ||
+      (residual && ldr < N))
+    return fail(CCQ_ERR_SHAPE, "%s: M=%d K=%d N=%d ldx=%lld ldy=%lld (need M <= 16, K a multiple of 32 in [32, 4096], "
+                "ldx >= K a multiple of 8, ldy >= N, ldr >= N)", who, M, K, N, (long long)ldx, (long long)ldy);
+  if (!x || !weight || !y) return fail(CCQ_ERR_NULL, "%s: x, weight, y are required", who);
+  if (!aligned16(x) || !aligned16(weight)) return fail(CCQ_ERR_ALIGN, "%s: x and weight must be 16-byte aligned", who);
+  return hip_status(launch_decode_linear(x, ldx, weight, residual, ldr, y, ldy, M, K, N, (hipStream_t)stream), who);
 }
 
 int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, const void* xa, const void* xb,

@@ -283,6 +283,74 @@ hipError_t decode_scratch(hipStream_t st, void** out) {
   return hipSuccess;
 }
 
+// ===========================================================================
+// Decode linear map: y[m][n] = sum_k x[m][k] W[n][k] (+ r[m][n]) for M <= 16 token rows (a decode
+// step's projections: the weight is read once and dominates the bytes).  Workgroup: 16 output
+// columns, 8 waves splitting the contraction into interleaved 32-wide steps; per step a 16x16x32 MFMA
+// with the weight's 16 rows as the A operand (16 bytes per lane, straight from HBM, every step of
+// the wave in flight at once) and the token rows as the B operand (L2-resident).  The waves' partial
+// 16x16 tiles meet in LDS; the result (lane (m, n / 4): four consecutive columns of row m) is rounded
+// to bf16 and, with a residual, added to the residual row in fp32 and rounded again -- the roundings
+// of `residual + linear(x)` on bf16 tensors.
+// ===========================================================================
+constexpr int kDlWaves = 8, kDlMaxSteps = 16;  // K <= 8 * 16 * 32 = 4096
+__global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, long ldx, const void* w_,
+                                                                       const void* r_, long ldr, void* y_, long ldy,
+                                                                       int M, int K, int N) {
+  __shared__ f32x4 sAcc[kDlWaves][64];
+  const bf16* x = (const bf16*)x_;
+  const bf16* w = (const bf16*)w_;
+  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+  const int n0 = blockIdx.x * 16;
+  const int steps = K / 32;
+  const int nw = min(n0 + (l & 15), N - 1);            // weight row of this lane (rows past N repeat the last)
+  const int mx = min(l & 15, M - 1);                    // token row of this lane (rows past M repeat the last)
+  const bf16* wr = w + (long)nw * K + 8 * (l >> 4);
+  const bf16* xr = x + (long)mx * ldx + 8 * (l >> 4);
+  bf16x8 wa[kDlMaxSteps], xb[kDlMaxSteps];
+#pragma unroll
+  for (int j = 0; j < kDlMaxSteps; ++j) {
+    const int st = wv + kDlWaves * j;
+    if (st < steps) {
+      wa[j] = *gmem((const bf16x8*)(wr + 32 * st));
+      xb[j] = *gmem((const bf16x8*)(xr + 32 * st));
+    }
+  }
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kDlMaxSteps; ++j)
+    if (wv + kDlWaves * j < steps) acc = mfma16(wa[j], xb[j], acc);
+  sAcc[wv][l] = acc;
+  __syncthreads();
+  if (wv != 0) return;
+  f32x4 sum = sAcc[0][l];
+#pragma unroll
+  for (int q = 1; q < kDlWaves; ++q) {
+    const f32x4 v = sAcc[q][l];
+    sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
+  }
+  // sum[i] = y[m = l & 15][n = n0 + 4 (l >> 4) + i]
+  const int m = l & 15, nb = n0 + 4 * (l >> 4);
+  if (m >= M) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = nb + i;
+    if (n < N) {
+      float v = (float)(bf16)sum[i];
+      if (r_) v += (float)((const bf16*)r_)[(long)m * ldr + n];
+      ((bf16*)y_)[(long)m * ldy + n] = (bf16)v;
+    }
+  }
+}
+
+hipError_t launch_decode_linear(const void* x, long ldx, const void* w, const void* r, long ldr, void* y, long ldy,
+                                int M, int K, int N, hipStream_t st) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  hipLaunchKernelGGL(decode_linear_kernel, dim3((unsigned)((N + 15) / 16)), dim3(kDlWaves * 64), 0, st, x, ldx, w, r,
+                     ldr, y, ldy, M, K, N);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st) {
   if (a.N <= 0 || a.H <= 0) return hipSuccess;
   switch (a.K) {

@@ -33,7 +33,43 @@ import torch.nn.functional as F
 from . import _lib
 from ._lib import call, ptr
 
-__all__ = ["DecodeStep", "CapturedDecode", "GDNLayerDecode"]
+__all__ = ["DecodeStep", "CapturedDecode", "GDNLayerDecode", "decode_linear", "decode_linear_ok"]
+
+
+def decode_linear_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether ``decode_linear`` takes this call: bf16 on the GPU, at most 16 rows, a contraction
+    width that is a multiple of 32 in [32, 4096], 16-byte aligned operands."""
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    return (x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and weight.dim() == 2
+            and weight.shape[1] == K and 1 <= rows <= 16 and K % 32 == 0 and 32 <= K <= 4096
+            and weight.is_contiguous() and weight.data_ptr() % 16 == 0)
+
+
+def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x @ weight.T (+ residual)`` for a decode step's few token rows (``ccq_decode_linear``: the
+    weight streamed once by MFMA tiles; fp32 accumulation rounded to bf16, then the residual added
+    and rounded again, as ``residual + linear(x)`` on bf16 tensors).  Inference only (no autograd).
+    ``decode_linear_ok`` gives the shapes it takes."""
+    if not decode_linear_ok(x, weight):
+        raise ValueError(f"decode_linear: x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)} {weight.dtype}: "
+                         f"needs bf16 on the GPU, <= 16 rows and a width that is a multiple of 32 in [32, 4096]")
+    K, N = x.shape[-1], weight.shape[0]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.bfloat16)
+    r2 = None
+    if residual is not None:
+        if residual.shape != y.shape or residual.dtype != torch.bfloat16:
+            raise ValueError(f"decode_linear: residual {tuple(residual.shape)} {residual.dtype}, expected "
+                             f"{tuple(y.shape)} bf16")
+        r2 = residual.reshape(-1, N)
+        if r2.stride(-1) != 1:
+            r2 = r2.contiguous()
+    call("ccq_decode_linear", ptr(x2), x2.stride(0), ptr(weight), ptr(r2), r2.stride(0) if r2 is not None else 0,
+         ptr(y), N, x2.shape[0], K, N, _lib.stream_of(x))
+    return y
 
 
 class DecodeStep:
@@ -173,16 +209,18 @@ class CapturedDecode:
 
 class GDNLayerDecode:
     """The token step of one ``CCQGDN`` layer (recurrent mode with a cache, ``ccq/gdn/layer.py:253-412``)
-    on static buffers: ``__call__(h)`` maps the layer input ``h [B, T, hidden]`` (bf16; normally T = 1) to
-    the layer output, advancing the layer's states, convolution caches and position in place.
+    on static buffers: ``__call__(h, residual=None)`` maps the layer input ``h [B, T, hidden]`` (bf16;
+    normally T = 1) to the layer output (plus ``residual``, with the roundings of ``residual + output``),
+    advancing the layer's states, convolution caches and position in place.
 
     The step is the layer's input projections as one GEMM over their concatenated weights (taken at
     construction; ``refresh()`` after the weights change), ``ccq_gdn_decode_prologue`` (short
     convolutions + SiLU with in-place caches, lambda, beta, g, per-head l2norm of q and k, with the
     roundings of the layer's own bf16 operations), the in-place decode step (``DecodeStep``, lambda as
-    given, no l2norm), the gated output norm and the output projection.  For a bf16 layer on the GPU
-    with short convolutions and one key / value head per query head (the reference configurations);
-    other layers run their recurrent mode as usual."""
+    given, no l2norm), the gated output norm and the output projection.  With at most 16 token rows
+    per step the two projections are ``decode_linear`` launches (the weights streamed once).  For a
+    bf16 layer on the GPU with short convolutions and one key / value head per query head (the
+    reference configurations); other layers run their recurrent mode as usual."""
 
     def __init__(self, layer, B: int, T: int = 1):
         L = layer
@@ -208,6 +246,9 @@ class GDNLayerDecode:
         self.pad = (-sum(widths)) % 8
         self.width = sum(widths) + self.pad
         self.refresh()
+        # the projections as decode_linear launches when the step has at most 16 token rows
+        self.fast = B * T <= 16 and decode_linear_ok(torch.empty(B * T, L.hidden_size, device=dev,
+                                                                 dtype=torch.bfloat16), self.w_in)
 
     def refresh(self) -> None:
         """Concatenate the layer's current input-projection weights."""
@@ -233,12 +274,12 @@ class GDNLayerDecode:
         for dst, src in zip(self.conv, entry["conv_state"]):
             dst.copy_(last_inputs(src, self.W))
 
-    def __call__(self, h: torch.Tensor) -> torch.Tensor:
+    def __call__(self, h: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         L, st = self.layer, self.step
         B, T, H, K, V = self.B, self.T, self.H, self.K, self.V
         if h.shape[:2] != (B, T) or h.dtype != torch.bfloat16:
             raise ValueError(f"expected bf16 input [{B}, {T}, hidden] (got {tuple(h.shape)} {h.dtype})")
-        x = F.linear(h, self.w_in)
+        x = decode_linear(h, self.w_in) if self.fast else F.linear(h, self.w_in)
         o_q, o_k, o_v, o_g, o_a, o_b = self.offsets
         cw = [c.weight for c in (L.q_conv1d, L.k_conv1d, L.v_conv1d)]
         cb = [c.bias for c in (L.q_conv1d, L.k_conv1d, L.v_conv1d)]
@@ -260,4 +301,8 @@ class GDNLayerDecode:
                  float(L.o_norm.eps), _lib.stream_of(x))
         else:
             o = L.o_norm(st.o)
-        return L.o_proj(o.reshape(B, T, H * V))
+        o = o.reshape(B, T, H * V)
+        if self.fast and decode_linear_ok(o, L.o_proj.weight):
+            return decode_linear(o, L.o_proj.weight, residual)
+        y = L.o_proj(o)
+        return y if residual is None else residual + y

@@ -261,6 +261,18 @@ int ccq_gla_decode(const void* q, const void* k, const void* v, const float* lam
  */
 size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K);
 /*
+ * Decode linear map y = x W^T (+ residual) for at most 16 token rows: the projections of a decode
+ * step (the reference layer's nn.Linear q/k/v/a/b/g projections and o_proj, ccq/gdn/layer.py:
+ * 286-316, 408, at one token per sequence), where the weight is read once and is nearly all the
+ * bytes.  x bf16 [M, K] (row stride ldx, a multiple of 8, 16-byte aligned), weight bf16 [N, K]
+ * (16-byte aligned), residual bf16 [M, N] with row stride ldr (nullable), y bf16 [M, N] with row
+ * stride ldy.  fp32 accumulation rounded to bf16, then the residual added in fp32 and rounded again
+ * (the roundings of residual + linear(x) on bf16 tensors).  M <= 16, K a multiple of 32 in
+ * [32, 4096].  One kernel, no allocation, graph-capturable.
+ */
+int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
+                      int64_t ldy, int M, int K, int N, void* stream);
+/*
  * The CCQ-GDN layer's per-token prologue in one launch, ahead of ccq_gdn_decode_step: what the
  * reference layer computes between its input projections and fused_recurrent_ccq_gdn
  * (ccq/gdn/layer.py:266-316) -- the q, k, v short convolutions + SiLU with their caches (fla
