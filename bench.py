@@ -461,10 +461,10 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
             return x + self.down(F.silu(gt) * up)
 
         def mlp_step(self, x):
-            # the captured decode step's MLP: the two projections as decode_linear launches, the
-            # residual added inside the second
+            # the captured decode step's MLP: the two projections as decode_linear launches, silu(gate) *
+            # up formed inside the second and the residual added there
             gt, up = decode_linear(self.mlp_norm(x), self.gate_up.weight).chunk(2, -1)
-            return decode_linear(F.silu(gt) * up, self.down.weight, x)
+            return decode_linear(gt, self.down.weight, x, up=up)
 
         def forward(self, x, cache):
             return self.mlp(x + self.attn(self.attn_norm(x), past_key_values=cache, use_cache=True)[0])

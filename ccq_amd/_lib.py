@@ -54,6 +54,7 @@ SIGNATURES = {
     "ccq_gated_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I]),
     "ccq_gated_rmsnorm_fwd": (_I, [_P] * 5 + [_I64, _I, _F, _P]),
     "ccq_gated_rmsnorm_bwd": (_I, [_P] * 9 + [_I64, _I, _P]),
+    "ccq_gated_rmsnorm_fwd_strided": (_I, [_P, _P, _I64, _I, _P, _P, _P, _I64, _I, _F, _P]),
     "ccq_narrow_linear_bwd_workspace_bytes": (_SZ, [_I64, _I, _I]),
     "ccq_narrow_linear_fwd": (_I, [_P, _I64, _P, _P, _P, _I64, _I, _I, _P]),
     "ccq_narrow_linear_bwd": (_I, [_P, _I64] + [_P] * 6 + [_I64, _I, _I, _P]),
@@ -61,6 +62,7 @@ SIGNATURES = {
     "ccq_l2norm_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P]),
     "ccq_gdn_decode_prologue": (_I, [_P] * 5 + [_I64] + [_P] * 19 + [_I] * 7 + [_F, _P]),
     "ccq_decode_linear": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _P]),
+    "ccq_decode_linear_glu": (_I, [_P, _P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _P]),
     "ccq_timing_enable": (_I, [_I]),
     "ccq_timing_reset": (_I, []),
     "ccq_timing_select": (_I, [ctypes.c_char_p]),

@@ -31,8 +31,8 @@ int narrow_blocks(long M);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
-hipError_t launch_decode_linear(const void* x, long ldx, const void* w, const void* r, long ldr, void* y, long ldy,
-                                int M, int K, int N, hipStream_t st);
+hipError_t launch_decode_linear(const void* x, const void* u, long ldx, const void* w, const void* r, long ldr, void* y,
+                                long ldy, int M, int K, int N, hipStream_t st);
 hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st);
 int cseg_count(int N, int H, int T, int K);
 bool cseg_sums_supported(int K);
@@ -765,8 +765,27 @@ int ccq_gated_rmsnorm_fwd(const void* x, const void* g, const float* weight, voi
     return fail(CCQ_ERR_ALIGN, "ccq_gated_rmsnorm_fwd: x, g, y must be 16-byte aligned");
   GNormArgs a{};
   a.x = x; a.g = g; a.w = weight; a.y = y; a.rstd = rstd; a.rows = rows; a.dv = dv; a.eps = eps;
+  a.ldg = dv; a.gper = 1;
   hipStream_t st = (hipStream_t)stream;
   return hip_status(timed("gnorm_fwd", st, [&] { return launch_gnorm(0, a, 0, st); }), "ccq_gated_rmsnorm_fwd");
+}
+
+int ccq_gated_rmsnorm_fwd_strided(const void* x, const void* g, int64_t ldg, int g_group, const float* weight, void* y,
+                                  float* rstd, int64_t rows, int dv, float eps, void* stream) {
+  if (!x || !g || !y || !rstd) return fail(CCQ_ERR_NULL, "ccq_gated_rmsnorm_fwd_strided: x, g, y, rstd are required");
+  if (rows < 0 || dv <= 0 || dv > 512 || dv % 8)
+    return fail(CCQ_ERR_SHAPE, "ccq_gated_rmsnorm_fwd_strided: dv=%d must be a multiple of 8 in [8, 512]", dv);
+  if (g_group < 1 || ldg < (int64_t)g_group * dv || ldg % 8)
+    return fail(CCQ_ERR_SHAPE, "ccq_gated_rmsnorm_fwd_strided: g_group=%d, ldg=%lld (need ldg >= g_group * dv, a "
+                "multiple of 8)", g_group, (long long)ldg);
+  if (!aligned16(x) || !aligned16(g) || !aligned16(y))
+    return fail(CCQ_ERR_ALIGN, "ccq_gated_rmsnorm_fwd_strided: x, g, y must be 16-byte aligned");
+  GNormArgs a{};
+  a.x = x; a.g = g; a.w = weight; a.y = y; a.rstd = rstd; a.rows = rows; a.dv = dv; a.eps = eps;
+  a.ldg = ldg; a.gper = g_group;
+  hipStream_t st = (hipStream_t)stream;
+  return hip_status(timed("gnorm_fwd", st, [&] { return launch_gnorm(0, a, 0, st); }),
+                    "ccq_gated_rmsnorm_fwd_strided");
 }
 
 int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, const float* rstd, const void* dy,
@@ -793,16 +812,28 @@ int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, con
                     "ccq_gated_rmsnorm_bwd(dweight)");
 }
 
-int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
-                      int64_t ldy, int M, int K, int N, void* stream) {
-  const char* who = "ccq_decode_linear";
+static int decode_linear_entry(const char* who, const void* x, const void* u, int64_t ldx, const void* weight,
+                               const void* residual, int64_t ldr, void* y, int64_t ldy, int M, int K, int N,
+                               void* stream) {
   if (M < 0 || M > 16 || N < 0 || K < 32 || K > 4096 || K % 32 || ldx < K || ldx % 8 || ldy < N ||
       (residual && ldr < N))
     return fail(CCQ_ERR_SHAPE, "%s: M=%d K=%d N=%d ldx=%lld ldy=%lld (need M <= 16, K a multiple of 32 in [32, 4096], "
                 "ldx >= K a multiple of 8, ldy >= N, ldr >= N)", who, M, K, N, (long long)ldx, (long long)ldy);
   if (!x || !weight || !y) return fail(CCQ_ERR_NULL, "%s: x, weight, y are required", who);
-  if (!aligned16(x) || !aligned16(weight)) return fail(CCQ_ERR_ALIGN, "%s: x and weight must be 16-byte aligned", who);
-  return hip_status(launch_decode_linear(x, ldx, weight, residual, ldr, y, ldy, M, K, N, (hipStream_t)stream), who);
+  if (!aligned16(x) || !aligned16(u) || !aligned16(weight))
+    return fail(CCQ_ERR_ALIGN, "%s: the inputs and the weight must be 16-byte aligned", who);
+  return hip_status(launch_decode_linear(x, u, ldx, weight, residual, ldr, y, ldy, M, K, N, (hipStream_t)stream), who);
+}
+
+int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
+                      int64_t ldy, int M, int K, int N, void* stream) {
+  return decode_linear_entry("ccq_decode_linear", x, nullptr, ldx, weight, residual, ldr, y, ldy, M, K, N, stream);
+}
+
+int ccq_decode_linear_glu(const void* gate, const void* up, int64_t ldx, const void* weight, const void* residual,
+                          int64_t ldr, void* y, int64_t ldy, int M, int K, int N, void* stream) {
+  if (!up) return fail(CCQ_ERR_NULL, "ccq_decode_linear_glu: up is required");
+  return decode_linear_entry("ccq_decode_linear_glu", gate, up, ldx, weight, residual, ldr, y, ldy, M, K, N, stream);
 }
 
 int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, const void* xa, const void* xb,

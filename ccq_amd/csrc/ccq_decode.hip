@@ -286,40 +286,56 @@ hipError_t decode_scratch(hipStream_t st, void** out) {
 // ===========================================================================
 // Decode linear map: y[m][n] = sum_k x[m][k] W[n][k] (+ r[m][n]) for M <= 16 token rows (a decode
 // step's projections: the weight is read once and dominates the bytes).  Workgroup: 16 output
-// columns, 8 waves splitting the contraction into interleaved 32-wide steps; per step a 16x16x32 MFMA
+// columns, 16 waves splitting the contraction into interleaved 32-wide steps (at most 8 per wave, so
+// four waves per SIMD keep a whole workgroup's loads in flight at once); per step a 16x16x32 MFMA
 // with the weight's 16 rows as the A operand (16 bytes per lane, straight from HBM, every step of
 // the wave in flight at once) and the token rows as the B operand (L2-resident).  The waves' partial
 // 16x16 tiles meet in LDS; the result (lane (m, n / 4): four consecutive columns of row m) is rounded
 // to bf16 and, with a residual, added to the residual row in fp32 and rounded again -- the roundings
-// of `residual + linear(x)` on bf16 tensors.
+// of `residual + linear(x)` on bf16 tensors.  With a second input u (a gated MLP's down projection),
+// the contraction runs over bf16(bf16(silu(x)) * u) formed as the fragments arrive, the roundings of
+// `silu(x) * u` on bf16 tensors.
 // ===========================================================================
-constexpr int kDlWaves = 8, kDlMaxSteps = 16;  // K <= 8 * 16 * 32 = 4096
-__global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, long ldx, const void* w_,
-                                                                       const void* r_, long ldr, void* y_, long ldy,
-                                                                       int M, int K, int N) {
+constexpr int kDlWaves = 16, kDlMaxSteps = 8;  // K <= 16 * 8 * 32 = 4096
+// SPW: 32-wide steps per wave (every wave takes SPW; steps past K read the last step's address and
+// contribute a zero x fragment, so the code has no branch around a load or an MFMA)
+template <int SPW, bool GLU>
+__global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, const void* u_, long ldx,
+                                                                       const void* w_, const void* r_, long ldr,
+                                                                       void* y_, long ldy, int M, int K, int N) {
   __shared__ f32x4 sAcc[kDlWaves][64];
   const bf16* x = (const bf16*)x_;
   const bf16* w = (const bf16*)w_;
-  const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+  const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
   const int n0 = blockIdx.x * 16;
   const int steps = K / 32;
   const int nw = min(n0 + (l & 15), N - 1);            // weight row of this lane (rows past N repeat the last)
   const int mx = min(l & 15, M - 1);                    // token row of this lane (rows past M repeat the last)
   const bf16* wr = w + (long)nw * K + 8 * (l >> 4);
   const bf16* xr = x + (long)mx * ldx + 8 * (l >> 4);
-  bf16x8 wa[kDlMaxSteps], xb[kDlMaxSteps];
+  const bf16* ur = (const bf16*)(GLU ? u_ : x_) + (long)mx * ldx + 8 * (l >> 4);
+  // every load of the wave is issued before the first use (the gated form's second input too)
+  bf16x8 wa[SPW], xb[SPW], ub[GLU ? SPW : 1];
 #pragma unroll
-  for (int j = 0; j < kDlMaxSteps; ++j) {
-    const int st = wv + kDlWaves * j;
-    if (st < steps) {
-      wa[j] = *gmem((const bf16x8*)(wr + 32 * st));
-      xb[j] = *gmem((const bf16x8*)(xr + 32 * st));
-    }
+  for (int j = 0; j < SPW; ++j) {
+    const int st = min(wv + kDlWaves * j, steps - 1);
+    wa[j] = *gmem((const bf16x8*)(wr + 32 * st));
+    xb[j] = *gmem((const bf16x8*)(xr + 32 * st));
+    if constexpr (GLU) ub[j] = *gmem((const bf16x8*)(ur + 32 * st));
   }
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < kDlMaxSteps; ++j)
-    if (wv + kDlWaves * j < steps) acc = mfma16(wa[j], xb[j], acc);
+  for (int j = 0; j < SPW; ++j) {
+    const bool live = wv + kDlWaves * j < steps;
+    bf16x8 xf;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = (float)xb[j][i];
+      if constexpr (GLU) v = (float)(bf16)((float)(bf16)(v / (1.f + expf(-v))) * (float)ub[j][i]);
+      xf[i] = (bf16)(live ? v : 0.f);
+    }
+    acc = mfma16(wa[j], xf, acc);
+  }
   sAcc[wv][l] = acc;
   __syncthreads();
   if (wv != 0) return;
@@ -343,11 +359,32 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   }
 }
 
-hipError_t launch_decode_linear(const void* x, long ldx, const void* w, const void* r, long ldr, void* y, long ldy,
-                                int M, int K, int N, hipStream_t st) {
+template <int SPW>
+static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const void* x, const void* u, long ldx,
+                      const void* w, const void* r, long ldr, void* y, long ldy, int M, int K, int N) {
+  if (glu)
+    hipLaunchKernelGGL((decode_linear_kernel<SPW, true>), grid, block, 0, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N);
+  else
+    hipLaunchKernelGGL((decode_linear_kernel<SPW, false>), grid, block, 0, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N);
+}
+
+hipError_t launch_decode_linear(const void* x, const void* u, long ldx, const void* w, const void* r, long ldr, void* y,
+                                long ldy, int M, int K, int N, hipStream_t st) {
   if (M <= 0 || N <= 0) return hipSuccess;
-  hipLaunchKernelGGL(decode_linear_kernel, dim3((unsigned)((N + 15) / 16)), dim3(kDlWaves * 64), 0, st, x, ldx, w, r,
-                     ldr, y, ldy, M, K, N);
+  const dim3 grid((unsigned)((N + 15) / 16)), block(kDlWaves * 64);
+  const int spw = (K / 32 + kDlWaves - 1) / kDlWaves;
+  const bool glu = u != nullptr;
+  switch (spw) {
+    case 1: launch_dl<1>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 2: launch_dl<2>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 3: launch_dl<3>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 4: launch_dl<4>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 5: launch_dl<5>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 6: launch_dl<6>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 7: launch_dl<7>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 8: launch_dl<8>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -114,6 +114,8 @@ struct GNormArgs {
   int dv;
   int lr;                   // lanes per row: the next power of two of dv / 8 (64 / lr rows per wavefront)
   float eps;
+  long ldg;                 // forward: gate row r at g + (r / gper) * ldg + (r % gper) * dv
+  int gper;                 //   (contiguous rows: gper = 1, ldg = dv)
 };
 
 struct L2NormArgs {

@@ -371,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void gnorm_fwd_kernel(const GNormArgs a) 
   float x[8], g[8];
   if (own) {
     const bf16x8 xb = *(const bf16x8*)((const bf16*)a.x + row * a.dv + e);
-    const bf16x8 gb = *(const bf16x8*)((const bf16*)a.g + row * a.dv + e);
+    const bf16x8 gb = *(const bf16x8*)((const bf16*)a.g + (row / a.gper) * a.ldg + (row % a.gper) * a.dv + e);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       x[i] = (float)xb[i];

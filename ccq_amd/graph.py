@@ -46,18 +46,28 @@ def decode_linear_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
             and weight.is_contiguous() and weight.data_ptr() % 16 == 0)
 
 
-def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                  up: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``x @ weight.T (+ residual)`` for a decode step's few token rows (``ccq_decode_linear``: the
     weight streamed once by MFMA tiles; fp32 accumulation rounded to bf16, then the residual added
-    and rounded again, as ``residual + linear(x)`` on bf16 tensors).  Inference only (no autograd).
-    ``decode_linear_ok`` gives the shapes it takes."""
+    and rounded again, as ``residual + linear(x)`` on bf16 tensors).  With ``up`` (same shape and row
+    stride as x) the map runs over ``silu(x) * up`` formed in the kernel (``ccq_decode_linear_glu``:
+    a gated MLP's down projection, with the roundings of those two bf16 ops).  Inference only (no
+    autograd).  ``decode_linear_ok`` gives the shapes it takes."""
     if not decode_linear_ok(x, weight):
         raise ValueError(f"decode_linear: x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)} {weight.dtype}: "
                          f"needs bf16 on the GPU, <= 16 rows and a width that is a multiple of 32 in [32, 4096]")
     K, N = x.shape[-1], weight.shape[0]
     x2 = x.reshape(-1, K)
-    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+    u2 = up.reshape(-1, K) if up is not None else None
+    if up is not None and (up.shape != x.shape or up.dtype != torch.bfloat16):
+        raise ValueError(f"decode_linear: up {tuple(up.shape)} {up.dtype}, expected {tuple(x.shape)} bf16")
+
+    def usable(t):
+        return t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+    if not usable(x2) or (u2 is not None and (not usable(u2) or u2.stride(0) != x2.stride(0))):
         x2 = x2.contiguous()
+        u2 = u2.contiguous() if u2 is not None else None
     y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.bfloat16)
     r2 = None
     if residual is not None:
@@ -67,8 +77,13 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torc
         r2 = residual.reshape(-1, N)
         if r2.stride(-1) != 1:
             r2 = r2.contiguous()
-    call("ccq_decode_linear", ptr(x2), x2.stride(0), ptr(weight), ptr(r2), r2.stride(0) if r2 is not None else 0,
-         ptr(y), N, x2.shape[0], K, N, _lib.stream_of(x))
+    ldr = r2.stride(0) if r2 is not None else 0
+    if u2 is None:
+        call("ccq_decode_linear", ptr(x2), x2.stride(0), ptr(weight), ptr(r2), ldr, ptr(y), N, x2.shape[0], K, N,
+             _lib.stream_of(x))
+    else:
+        call("ccq_decode_linear_glu", ptr(x2), ptr(u2), x2.stride(0), ptr(weight), ptr(r2), ldr, ptr(y), N,
+             x2.shape[0], K, N, _lib.stream_of(x))
     return y
 
 
@@ -293,12 +308,12 @@ class GDNLayerDecode:
              B, T, H, K, V, self.W, int(L.allow_neg_eigval), 1e-6, _lib.stream_of(x))
         st.launch()
         if L.use_gate:
-            # the gated RMSNorm kernel on contiguous gate rows, with the weight converted in refresh()
-            gx = x[..., o_g:o_g + H * V].contiguous()
+            # the gated RMSNorm kernel reading the gate rows in place from the projection output (H rows
+            # of V per token, the projection's row width apart), with the weight converted in refresh()
             o = torch.empty_like(st.o)
             rstd = torch.empty(B * T * H, device=x.device, dtype=torch.float32)
-            call("ccq_gated_rmsnorm_fwd", ptr(st.o), ptr(gx), ptr(self.norm_w), ptr(o), ptr(rstd), B * T * H, V,
-                 float(L.o_norm.eps), _lib.stream_of(x))
+            call("ccq_gated_rmsnorm_fwd_strided", ptr(st.o), at(o_g), self.width, H, ptr(self.norm_w), ptr(o),
+                 ptr(rstd), B * T * H, V, float(L.o_norm.eps), _lib.stream_of(x))
         else:
             o = L.o_norm(st.o)
         o = o.reshape(B, T, H * V)

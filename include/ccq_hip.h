@@ -273,6 +273,14 @@ size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K);
 int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
                       int64_t ldy, int M, int K, int N, void* stream);
 /*
+ * The same map over silu(gate) * up (bf16 roundings of silu(gate) and of the product, as torch's bf16
+ * ops make them): a gated MLP's down projection with its input formed as the operands arrive.  No
+ * counterpart in the reference's operators (its MLP is fla's); for a decode step's MLP, which the
+ * C4 harness runs around the layers.  gate and up: bf16 [M, K] with row stride ldx, 16-byte aligned.
+ */
+int ccq_decode_linear_glu(const void* gate, const void* up, int64_t ldx, const void* weight, const void* residual,
+                          int64_t ldr, void* y, int64_t ldy, int M, int K, int N, void* stream);
+/*
  * The CCQ-GDN layer's per-token prologue in one launch, ahead of ccq_gdn_decode_step: what the
  * reference layer computes between its input projections and fused_recurrent_ccq_gdn
  * (ccq/gdn/layer.py:266-316) -- the q, k, v short convolutions + SiLU with their caches (fla
@@ -341,6 +349,14 @@ int ccq_gated_rmsnorm_fwd(const void* x, const void* g, const float* weight, voi
                           int dv, float eps, void* stream);
 int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, const float* rstd, const void* dy,
                           void* dx, void* dg, float* dweight, void* workspace, int64_t rows, int dv, void* stream);
+/*
+ * The same forward with the gate rows read in place from a wider tensor: gate row r (of dv) at
+ * g + (r / g_group) * ldg + (r % g_group) * dv elements -- e.g. the output-gate columns of a decode
+ * step's concatenated projection, g_group = heads, ldg = the projection's row width -- so no copy
+ * makes them contiguous.  ldg >= g_group * dv and a multiple of 8; g 16-byte aligned.
+ */
+int ccq_gated_rmsnorm_fwd_strided(const void* x, const void* g, int64_t ldg, int g_group, const float* weight, void* y,
+                                  float* rstd, int64_t rows, int dv, float eps, void* stream);
 
 /*
  * Narrow linear map y = x W^T (+ b) with N <= 16 outputs per row, and its backward: the layers'

@@ -1,0 +1,102 @@
+"""GPU checks of the decode step's projection kernels: ``decode_linear`` (``ccq_decode_linear``) and
+its gated-input form (``ccq_decode_linear_glu``) against a float64 restatement with the bf16 roundings
+of the torch ops they replace (``residual + linear(x)``; ``linear(silu(gate) * up)``), and the
+gated RMSNorm that reads its gate rows in place (``ccq_gated_rmsnorm_fwd_strided``) against the
+contiguous kernel on a copy of those rows.
+
+Tolerance: outputs are bf16 rounded once from an fp32 accumulation: against the float64 value
+rounded at the same points, relative L2 <= 5e-4 (the accumulation order moves a few elements across
+a tie); the strided and contiguous norms must agree bit for bit.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tests._util import kern
+
+pytestmark = pytest.mark.gpu
+
+D = torch.float64
+BF = torch.bfloat16
+
+
+def _cuda():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import ccq_amd  # noqa: F401
+    return torch.device("cuda")
+
+
+def _r(x):
+    return x.to(BF).to(D)
+
+
+CASES = [
+    # M, K, N, residual
+    (16, 1024, 6160, False),   # C4: a layer's concatenated input projections
+    (16, 2048, 1024, True),    # C4: o_proj with the residual
+    (3, 1024, 5632, False),    # three tokens
+    (1, 4096, 100, True),      # one token, the widest K, N not a multiple of 16
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(c) for c in CASES])
+def test_decode_linear(case):
+    dev = _cuda()
+    from ccq_amd.graph import decode_linear
+    M, K, N, with_res = case
+    print("test_decode_linear", case, flush=True)
+    gen = torch.Generator().manual_seed(M * 7 + K + N)
+    x = torch.randn(M, K, generator=gen).to(BF)
+    w = (torch.randn(N, K, generator=gen) * 0.03).to(BF)
+    res = torch.randn(M, N, generator=gen).to(BF) if with_res else None
+    ref = _r(x.to(D) @ w.to(D).T)
+    if res is not None:
+        ref = res.to(D) + ref
+    y = decode_linear(x.to(dev), w.to(dev), res.to(dev) if res is not None else None)
+    torch.cuda.synchronize()
+    e = kern(y, ref)
+    print(case, f"kernel {e:.2e}", flush=True)
+    assert y.shape == (M, N) and e <= 5e-4
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 2816, 1024), (5, 1024, 256)])
+def test_decode_linear_glu(M, K, N):
+    dev = _cuda()
+    from ccq_amd.graph import decode_linear
+    print("test_decode_linear_glu", M, K, N, flush=True)
+    gen = torch.Generator().manual_seed(K + N)
+    gu = torch.randn(M, 2 * K, generator=gen).to(BF).to(dev)
+    w = (torch.randn(N, K, generator=gen) * 0.03).to(BF).to(dev)
+    res = torch.randn(M, N, generator=gen).to(BF).to(dev)
+    gt, up = gu.chunk(2, -1)                       # views with the row stride of gu
+    hm = F.silu(gt) * up                           # torch's bf16 ops: the roundings restated
+    ref = res.double().cpu() + _r(hm.double().cpu() @ w.double().cpu().T)
+    y = decode_linear(gt, w, res, up=up)
+    torch.cuda.synchronize()
+    e = kern(y, ref)
+    print((M, K, N), f"kernel {e:.2e}", flush=True)
+    assert e <= 5e-4
+
+
+def test_gated_rmsnorm_strided_gate_rows():
+    dev = _cuda()
+    from ccq_amd import _lib
+    from ccq_amd._lib import call, ptr
+    T, H, V, width = 16, 4, 512, 6160
+    gen = torch.Generator().manual_seed(3)
+    proj = torch.randn(T, width, generator=gen).to(BF).to(dev)
+    o = torch.randn(T * H, V, generator=gen).to(BF).to(dev)
+    w = torch.rand(V, generator=gen).float().to(dev)
+    og = 2 * 1024 + 2048
+    g = proj[:, og:og + H * V].contiguous().view(T * H, V)
+    y0, y1 = torch.empty_like(o), torch.empty_like(o)
+    r0 = torch.empty(T * H, device=dev)
+    r1 = torch.empty(T * H, device=dev)
+    s = _lib.stream_of(o)
+    call("ccq_gated_rmsnorm_fwd", ptr(o), ptr(g), ptr(w), ptr(y0), ptr(r0), T * H, V, 1e-5, s)
+    call("ccq_gated_rmsnorm_fwd_strided", ptr(o), proj.data_ptr() + 2 * og, width, H, ptr(w), ptr(y1), ptr(r1),
+         T * H, V, 1e-5, s)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1) and torch.equal(r0, r1)
