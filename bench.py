@@ -438,7 +438,7 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
     checked against the eager layers' before it is timed."""
     import torch.nn as nn
     import torch.nn.functional as F
-    from ccq_amd.graph import GDNLayerDecode, decode_linear
+    from ccq_amd.graph import GDNLayerDecode, decode_linear, decode_linear_glu
     from ccq_amd.layers import CCQGDN, LayerCache
 
     inter = 256 * ((int(d * 4 * 2 / 3) + 255) // 256)  # fla GatedMLP's intermediate size (hidden_ratio 4)
@@ -461,10 +461,9 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
             return x + self.down(F.silu(gt) * up)
 
         def mlp_step(self, x):
-            # the captured decode step's MLP: the two projections as decode_linear launches, silu(gate) *
-            # up formed inside the second and the residual added there
-            gt, up = decode_linear(self.mlp_norm(x), self.gate_up.weight).chunk(2, -1)
-            return decode_linear(gt, self.down.weight, x, up=up)
+            # the captured decode step's MLP: silu(gate) * up out of the up projection's kernel, the
+            # down projection with the residual added in it
+            return decode_linear(decode_linear_glu(self.mlp_norm(x), self.gate_up.weight), self.down.weight, x)
 
         def forward(self, x, cache):
             return self.mlp(x + self.attn(self.attn_norm(x), past_key_values=cache, use_cache=True)[0])

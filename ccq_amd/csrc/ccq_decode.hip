@@ -292,18 +292,19 @@ hipError_t decode_scratch(hipStream_t st, void** out) {
 // the wave in flight at once) and the token rows as the B operand (L2-resident).  The waves' partial
 // 16x16 tiles meet in LDS; the result (lane (m, n / 4): four consecutive columns of row m) is rounded
 // to bf16 and, with a residual, added to the residual row in fp32 and rounded again -- the roundings
-// of `residual + linear(x)` on bf16 tensors.  With a second input u (a gated MLP's down projection),
-// the contraction runs over bf16(bf16(silu(x)) * u) formed as the fragments arrive, the roundings of
-// `silu(x) * u` on bf16 tensors.
+// of `residual + linear(x)` on bf16 tensors.  Gated form (a gated MLP's up projection): the weight
+// has 2N rows; output column n is h = bf16(bf16(silu(g)) * u) of g = bf16(row n . x) and
+// u = bf16(row N + n . x), the roundings of `silu(gate) * up` after `linear(x).chunk(2, -1)` on bf16
+// tensors.
 // ===========================================================================
 constexpr int kDlWaves = 16, kDlMaxSteps = 8;  // K <= 16 * 8 * 32 = 4096
 // SPW: 32-wide steps per wave (every wave takes SPW; steps past K read the last step's address and
 // contribute a zero x fragment, so the code has no branch around a load or an MFMA)
 template <int SPW, bool GLU>
-__global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, const void* u_, long ldx,
-                                                                       const void* w_, const void* r_, long ldr,
-                                                                       void* y_, long ldy, int M, int K, int N) {
-  __shared__ f32x4 sAcc[kDlWaves][64];
+__global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, long ldx, const void* w_,
+                                                                       const void* r_, long ldr, void* y_, long ldy,
+                                                                       int M, int K, int N) {
+  __shared__ f32x4 sAcc[GLU ? 2 : 1][kDlWaves][64];
   const bf16* x = (const bf16*)x_;
   const bf16* w = (const bf16*)w_;
   const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
@@ -312,38 +313,49 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   const int nw = min(n0 + (l & 15), N - 1);            // weight row of this lane (rows past N repeat the last)
   const int mx = min(l & 15, M - 1);                    // token row of this lane (rows past M repeat the last)
   const bf16* wr = w + (long)nw * K + 8 * (l >> 4);
+  const bf16* wu = w + (long)(GLU ? N + nw : nw) * K + 8 * (l >> 4);  // the up half's row (gated form)
   const bf16* xr = x + (long)mx * ldx + 8 * (l >> 4);
-  const bf16* ur = (const bf16*)(GLU ? u_ : x_) + (long)mx * ldx + 8 * (l >> 4);
-  // every load of the wave is issued before the first use (the gated form's second input too)
-  bf16x8 wa[SPW], xb[SPW], ub[GLU ? SPW : 1];
+  // every load of the wave is issued before the first use
+  bf16x8 wa[SPW], wb[GLU ? SPW : 1], xb[SPW];
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
     const int st = min(wv + kDlWaves * j, steps - 1);
     wa[j] = *gmem((const bf16x8*)(wr + 32 * st));
+    if constexpr (GLU) wb[j] = *gmem((const bf16x8*)(wu + 32 * st));
     xb[j] = *gmem((const bf16x8*)(xr + 32 * st));
-    if constexpr (GLU) ub[j] = *gmem((const bf16x8*)(ur + 32 * st));
   }
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, acu = acc;
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
     const bool live = wv + kDlWaves * j < steps;
     bf16x8 xf;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = (float)xb[j][i];
-      if constexpr (GLU) v = (float)(bf16)((float)(bf16)(v / (1.f + expf(-v))) * (float)ub[j][i]);
-      xf[i] = (bf16)(live ? v : 0.f);
-    }
+    for (int i = 0; i < 8; ++i) xf[i] = live ? xb[j][i] : (bf16)0.f;
     acc = mfma16(wa[j], xf, acc);
+    if constexpr (GLU) acu = mfma16(wb[j], xf, acu);
   }
-  sAcc[wv][l] = acc;
+  sAcc[0][wv][l] = acc;
+  if constexpr (GLU) sAcc[GLU ? 1 : 0][wv][l] = acu;
   __syncthreads();
   if (wv != 0) return;
-  f32x4 sum = sAcc[0][l];
+  f32x4 sum = sAcc[0][0][l];
 #pragma unroll
   for (int q = 1; q < kDlWaves; ++q) {
-    const f32x4 v = sAcc[q][l];
+    const f32x4 v = sAcc[0][q][l];
     sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
+  }
+  if constexpr (GLU) {
+    f32x4 su = sAcc[GLU ? 1 : 0][0][l];
+#pragma unroll
+    for (int q = 1; q < kDlWaves; ++q) {
+      const f32x4 v = sAcc[GLU ? 1 : 0][q][l];
+      su[0] += v[0]; su[1] += v[1]; su[2] += v[2]; su[3] += v[3];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float g = (float)(bf16)sum[i];
+      sum[i] = (float)(bf16)(g / (1.f + expf(-g))) * (float)(bf16)su[i];  // rounded once more at the store
+    }
   }
   // sum[i] = y[m = l & 15][n = n0 + 4 (l >> 4) + i]
   const int m = l & 15, nb = n0 + 4 * (l >> 4);
@@ -352,7 +364,7 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   for (int i = 0; i < 4; ++i) {
     const int n = nb + i;
     if (n < N) {
-      float v = (float)(bf16)sum[i];
+      float v = GLU ? sum[i] : (float)(bf16)sum[i];
       if (r_) v += (float)((const bf16*)r_)[(long)m * ldr + n];
       ((bf16*)y_)[(long)m * ldy + n] = (bf16)v;
     }
@@ -360,29 +372,28 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
 }
 
 template <int SPW>
-static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const void* x, const void* u, long ldx,
-                      const void* w, const void* r, long ldr, void* y, long ldy, int M, int K, int N) {
+static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const void* x, long ldx, const void* w,
+                      const void* r, long ldr, void* y, long ldy, int M, int K, int N) {
   if (glu)
-    hipLaunchKernelGGL((decode_linear_kernel<SPW, true>), grid, block, 0, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N);
+    hipLaunchKernelGGL((decode_linear_kernel<SPW, true>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N);
   else
-    hipLaunchKernelGGL((decode_linear_kernel<SPW, false>), grid, block, 0, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N);
+    hipLaunchKernelGGL((decode_linear_kernel<SPW, false>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N);
 }
 
-hipError_t launch_decode_linear(const void* x, const void* u, long ldx, const void* w, const void* r, long ldr, void* y,
+hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
                                 long ldy, int M, int K, int N, hipStream_t st) {
   if (M <= 0 || N <= 0) return hipSuccess;
   const dim3 grid((unsigned)((N + 15) / 16)), block(kDlWaves * 64);
   const int spw = (K / 32 + kDlWaves - 1) / kDlWaves;
-  const bool glu = u != nullptr;
   switch (spw) {
-    case 1: launch_dl<1>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 2: launch_dl<2>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 3: launch_dl<3>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 4: launch_dl<4>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 5: launch_dl<5>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 6: launch_dl<6>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 7: launch_dl<7>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 8: launch_dl<8>(glu, grid, block, st, x, u, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

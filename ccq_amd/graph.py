@@ -33,7 +33,8 @@ import torch.nn.functional as F
 from . import _lib
 from ._lib import call, ptr
 
-__all__ = ["DecodeStep", "CapturedDecode", "GDNLayerDecode", "decode_linear", "decode_linear_ok"]
+__all__ = ["DecodeStep", "CapturedDecode", "GDNLayerDecode", "decode_linear", "decode_linear_glu",
+           "decode_linear_ok"]
 
 
 def decode_linear_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
@@ -46,28 +47,23 @@ def decode_linear_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
             and weight.is_contiguous() and weight.data_ptr() % 16 == 0)
 
 
-def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor] = None,
-                  up: Optional[torch.Tensor] = None) -> torch.Tensor:
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2
+
+
+def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``x @ weight.T (+ residual)`` for a decode step's few token rows (``ccq_decode_linear``: the
     weight streamed once by MFMA tiles; fp32 accumulation rounded to bf16, then the residual added
-    and rounded again, as ``residual + linear(x)`` on bf16 tensors).  With ``up`` (same shape and row
-    stride as x) the map runs over ``silu(x) * up`` formed in the kernel (``ccq_decode_linear_glu``:
-    a gated MLP's down projection, with the roundings of those two bf16 ops).  Inference only (no
-    autograd).  ``decode_linear_ok`` gives the shapes it takes."""
+    and rounded again, as ``residual + linear(x)`` on bf16 tensors).  Inference only (no autograd).
+    ``decode_linear_ok`` gives the shapes it takes."""
     if not decode_linear_ok(x, weight):
         raise ValueError(f"decode_linear: x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)} {weight.dtype}: "
                          f"needs bf16 on the GPU, <= 16 rows and a width that is a multiple of 32 in [32, 4096]")
     K, N = x.shape[-1], weight.shape[0]
-    x2 = x.reshape(-1, K)
-    u2 = up.reshape(-1, K) if up is not None else None
-    if up is not None and (up.shape != x.shape or up.dtype != torch.bfloat16):
-        raise ValueError(f"decode_linear: up {tuple(up.shape)} {up.dtype}, expected {tuple(x.shape)} bf16")
-
-    def usable(t):
-        return t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
-    if not usable(x2) or (u2 is not None and (not usable(u2) or u2.stride(0) != x2.stride(0))):
-        x2 = x2.contiguous()
-        u2 = u2.contiguous() if u2 is not None else None
+    x2 = _rows(x)
     y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.bfloat16)
     r2 = None
     if residual is not None:
@@ -77,13 +73,24 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torc
         r2 = residual.reshape(-1, N)
         if r2.stride(-1) != 1:
             r2 = r2.contiguous()
-    ldr = r2.stride(0) if r2 is not None else 0
-    if u2 is None:
-        call("ccq_decode_linear", ptr(x2), x2.stride(0), ptr(weight), ptr(r2), ldr, ptr(y), N, x2.shape[0], K, N,
-             _lib.stream_of(x))
-    else:
-        call("ccq_decode_linear_glu", ptr(x2), ptr(u2), x2.stride(0), ptr(weight), ptr(r2), ldr, ptr(y), N,
-             x2.shape[0], K, N, _lib.stream_of(x))
+    call("ccq_decode_linear", ptr(x2), x2.stride(0), ptr(weight), ptr(r2), r2.stride(0) if r2 is not None else 0,
+         ptr(y), N, x2.shape[0], K, N, _lib.stream_of(x))
+    return y
+
+
+def decode_linear_glu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """A gated MLP's up projection for a decode step: ``silu(gate) * up`` with
+    ``gate, up = (x @ weight.T).chunk(2, -1)`` (``ccq_decode_linear_glu``; the bf16 roundings of those
+    torch ops made in the kernel, the [rows, 2N] projection never written).  weight [2N, K]."""
+    if not decode_linear_ok(x, weight) or weight.shape[0] % 2:
+        raise ValueError(f"decode_linear_glu: x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)} "
+                         f"{weight.dtype}: needs bf16 on the GPU, <= 16 rows, an even number of weight rows and a "
+                         f"width that is a multiple of 32 in [32, 4096]")
+    K, N = x.shape[-1], weight.shape[0] // 2
+    x2 = _rows(x)
+    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.bfloat16)
+    call("ccq_decode_linear_glu", ptr(x2), x2.stride(0), ptr(weight), ptr(y), N, x2.shape[0], K, N,
+         _lib.stream_of(x))
     return y
 
 

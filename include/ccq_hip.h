@@ -273,13 +273,14 @@ size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K);
 int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
                       int64_t ldy, int M, int K, int N, void* stream);
 /*
- * The same map over silu(gate) * up (bf16 roundings of silu(gate) and of the product, as torch's bf16
- * ops make them): a gated MLP's down projection with its input formed as the operands arrive.  No
- * counterpart in the reference's operators (its MLP is fla's); for a decode step's MLP, which the
- * C4 harness runs around the layers.  gate and up: bf16 [M, K] with row stride ldx, 16-byte aligned.
+ * A gated MLP's up projection in the same form: weight bf16 [2N, K] (the gate rows, then the up rows),
+ * y bf16 [M, N] = silu(gate) * up with gate, up = (x weight^T).chunk(2, -1) -- the bf16 roundings of
+ * those torch ops (each projection, silu, the product) made in the kernel's epilogue, so the
+ * [M, 2N] projection never leaves the chip.  No counterpart in the reference's operators (its MLP is
+ * fla's); for a decode step's MLP, which the C4 harness runs around the layers.
  */
-int ccq_decode_linear_glu(const void* gate, const void* up, int64_t ldx, const void* weight, const void* residual,
-                          int64_t ldr, void* y, int64_t ldy, int M, int K, int N, void* stream);
+int ccq_decode_linear_glu(const void* x, int64_t ldx, const void* weight, void* y, int64_t ldy, int M, int K, int N,
+                          void* stream);
 /*
  * The CCQ-GDN layer's per-token prologue in one launch, ahead of ccq_gdn_decode_step: what the
  * reference layer computes between its input projections and fused_recurrent_ccq_gdn

@@ -1,6 +1,7 @@
 """GPU checks of the decode step's projection kernels: ``decode_linear`` (``ccq_decode_linear``) and
-its gated-input form (``ccq_decode_linear_glu``) against a float64 restatement with the bf16 roundings
-of the torch ops they replace (``residual + linear(x)``; ``linear(silu(gate) * up)``), and the
+its gated up-projection form (``ccq_decode_linear_glu``) against a float64 restatement with the bf16
+roundings of the torch ops they replace (``residual + linear(x)``; ``silu(gate) * up`` of
+``linear(x).chunk(2, -1)``), and the
 gated RMSNorm that reads its gate rows in place (``ccq_gated_rmsnorm_fwd_strided``) against the
 contiguous kernel on a copy of those rows.
 
@@ -61,23 +62,22 @@ def test_decode_linear(case):
     assert y.shape == (M, N) and e <= 5e-4
 
 
-@pytest.mark.parametrize("M,K,N", [(16, 2816, 1024), (5, 1024, 256)])
+@pytest.mark.parametrize("M,K,N", [(16, 1024, 2816), (5, 512, 100)])
 def test_decode_linear_glu(M, K, N):
     dev = _cuda()
-    from ccq_amd.graph import decode_linear
+    from ccq_amd.graph import decode_linear_glu
     print("test_decode_linear_glu", M, K, N, flush=True)
     gen = torch.Generator().manual_seed(K + N)
-    gu = torch.randn(M, 2 * K, generator=gen).to(BF).to(dev)
-    w = (torch.randn(N, K, generator=gen) * 0.03).to(BF).to(dev)
-    res = torch.randn(M, N, generator=gen).to(BF).to(dev)
-    gt, up = gu.chunk(2, -1)                       # views with the row stride of gu
-    hm = F.silu(gt) * up                           # torch's bf16 ops: the roundings restated
-    ref = res.double().cpu() + _r(hm.double().cpu() @ w.double().cpu().T)
-    y = decode_linear(gt, w, res, up=up)
+    x = torch.randn(M, K, generator=gen).to(BF).to(dev)
+    w = (torch.randn(2 * N, K, generator=gen) * 0.03).to(BF).to(dev)
+    gt, up = (x.double().cpu() @ w.double().cpu().T).chunk(2, -1)
+    # torch's bf16 ops restated: each projection rounded, silu rounded, the product rounded
+    ref = _r(_r(F.silu(_r(gt))) * _r(up))
+    y = decode_linear_glu(x, w)
     torch.cuda.synchronize()
     e = kern(y, ref)
     print((M, K, N), f"kernel {e:.2e}", flush=True)
-    assert e <= 5e-4
+    assert y.shape == (M, N) and e <= 5e-4
 
 
 def test_gated_rmsnorm_strided_gate_rows():
