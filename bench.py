@@ -621,6 +621,9 @@ def main():
                          "README's cleaning-overhead shape; c2 / c3: single-layer fwd+bwd; c4: the 24-layer "
                          "model's prefill and greedy decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--c4-prefill", type=int, default=16384,
+                    help="c4: prompt tokens per sequence (BASELINE C4: 16384; a short prompt profiles the decode step)")
+    ap.add_argument("--c4-decode-steps", type=int, default=256, help="c4: greedy decode steps")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed steps, run one elementwise copy of 512 MiB (read) + 512 MiB (write), "
                          "the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counts")
@@ -642,7 +645,7 @@ def main():
     elif args.workload == "readme":
         out = run_readme(args, dev)
     elif args.workload == "c4":
-        out = run_c4(args, dev)
+        out = run_c4(args, dev, t=args.c4_prefill, decode_steps=args.c4_decode_steps)
     else:
         out = run_layer(args, dev, args.workload)
     print(json.dumps(out), flush=True)
