@@ -461,9 +461,11 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
             return x + self.down(F.silu(gt) * up)
 
         def mlp_step(self, x):
-            # the captured decode step's MLP: silu(gate) * up out of the up projection's kernel, the
-            # down projection with the residual added in it
-            return decode_linear(decode_linear_glu(self.mlp_norm(x), self.gate_up.weight), self.down.weight, x)
+            # the captured decode step's MLP: the norm folded into the up projection's kernel, which
+            # also forms silu(gate) * up; the down projection with the residual added in it
+            h = decode_linear_glu(x, self.gate_up.weight, norm_weight=self.mlp_norm.weight,
+                                  norm_eps=self.mlp_norm.eps)
+            return decode_linear(h, self.down.weight, x)
 
         def forward(self, x, cache):
             return self.mlp(x + self.attn(self.attn_norm(x), past_key_values=cache, use_cache=True)[0])
@@ -500,7 +502,7 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
     def graph_step():
         x = embed(ids)
         for blk, ld in zip(blocks, lds):
-            x = blk.mlp_step(ld(blk.attn_norm(x), x))
+            x = blk.mlp_step(ld(x, x, norm=blk.attn_norm))
         logits = head(norm(x[:, -1]))
         ids.copy_(logits.argmax(-1, keepdim=True))
         return logits

@@ -32,7 +32,7 @@ hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
 hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
-                                long ldy, int M, int K, int N, hipStream_t st);
+                                long ldy, int M, int K, int N, const void* nw, float eps, hipStream_t st);
 hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st);
 int cseg_count(int N, int H, int T, int K);
 bool cseg_sums_supported(int K);
@@ -814,26 +814,29 @@ int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, con
 
 static int decode_linear_entry(const char* who, bool glu, const void* x, int64_t ldx, const void* weight,
                                const void* residual, int64_t ldr, void* y, int64_t ldy, int M, int K, int N,
-                               void* stream) {
+                               const void* norm_weight, float norm_eps, void* stream) {
   if (M < 0 || M > 16 || N < 0 || K < 32 || K > 4096 || K % 32 || ldx < K || ldx % 8 || ldy < N ||
       (residual && ldr < N))
     return fail(CCQ_ERR_SHAPE, "%s: M=%d K=%d N=%d ldx=%lld ldy=%lld (need M <= 16, K a multiple of 32 in [32, 4096], "
                 "ldx >= K a multiple of 8, ldy >= N, ldr >= N)", who, M, K, N, (long long)ldx, (long long)ldy);
   if (!x || !weight || !y) return fail(CCQ_ERR_NULL, "%s: x, weight, y are required", who);
-  if (!aligned16(x) || !aligned16(weight))
-    return fail(CCQ_ERR_ALIGN, "%s: x and the weight must be 16-byte aligned", who);
-  return hip_status(launch_decode_linear(glu, x, ldx, weight, residual, ldr, y, ldy, M, K, N, (hipStream_t)stream),
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(norm_weight))
+    return fail(CCQ_ERR_ALIGN, "%s: x, the weight and the norm weight must be 16-byte aligned", who);
+  return hip_status(launch_decode_linear(glu, x, ldx, weight, residual, ldr, y, ldy, M, K, N, norm_weight, norm_eps,
+                                         (hipStream_t)stream),
                     who);
 }
 
 int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
-                      int64_t ldy, int M, int K, int N, void* stream) {
-  return decode_linear_entry("ccq_decode_linear", false, x, ldx, weight, residual, ldr, y, ldy, M, K, N, stream);
+                      int64_t ldy, int M, int K, int N, const void* norm_weight, float norm_eps, void* stream) {
+  return decode_linear_entry("ccq_decode_linear", false, x, ldx, weight, residual, ldr, y, ldy, M, K, N, norm_weight,
+                             norm_eps, stream);
 }
 
 int ccq_decode_linear_glu(const void* x, int64_t ldx, const void* weight, void* y, int64_t ldy, int M, int K, int N,
-                          void* stream) {
-  return decode_linear_entry("ccq_decode_linear_glu", true, x, ldx, weight, nullptr, 0, y, ldy, M, K, N, stream);
+                          const void* norm_weight, float norm_eps, void* stream) {
+  return decode_linear_entry("ccq_decode_linear_glu", true, x, ldx, weight, nullptr, 0, y, ldy, M, K, N, norm_weight,
+                             norm_eps, stream);
 }
 
 int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, const void* xa, const void* xb,

@@ -295,16 +295,21 @@ hipError_t decode_scratch(hipStream_t st, void** out) {
 // of `residual + linear(x)` on bf16 tensors.  Gated form (a gated MLP's up projection): the weight
 // has 2N rows; output column n is h = bf16(bf16(silu(g)) * u) of g = bf16(row n . x) and
 // u = bf16(row N + n . x), the roundings of `silu(gate) * up` after `linear(x).chunk(2, -1)` on bf16
-// tensors.
+// tensors.  Normed form (the block's RMSNorm ahead of the projection): each token row enters as
+// bf16(x * r * w_norm) with r = 1 / sqrt(mean(x^2) + eps) -- the rounding of a bf16 nn.RMSNorm -- the
+// row's sum of squares formed from the fragments every wave already holds (lane shuffles across the
+// four lane groups of a row, then one LDS exchange across the waves).
 // ===========================================================================
 constexpr int kDlWaves = 16, kDlMaxSteps = 8;  // K <= 16 * 8 * 32 = 4096
 // SPW: 32-wide steps per wave (every wave takes SPW; steps past K read the last step's address and
 // contribute a zero x fragment, so the code has no branch around a load or an MFMA)
-template <int SPW, bool GLU>
+template <int SPW, bool GLU, bool NORM>
 __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, long ldx, const void* w_,
                                                                        const void* r_, long ldr, void* y_, long ldy,
-                                                                       int M, int K, int N) {
+                                                                       int M, int K, int N, const void* nw_,
+                                                                       float eps) {
   __shared__ f32x4 sAcc[GLU ? 2 : 1][kDlWaves][64];
+  __shared__ float sSS[NORM ? kDlWaves : 1][16];
   const bf16* x = (const bf16*)x_;
   const bf16* w = (const bf16*)w_;
   const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
@@ -316,13 +321,36 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   const bf16* wu = w + (long)(GLU ? N + nw : nw) * K + 8 * (l >> 4);  // the up half's row (gated form)
   const bf16* xr = x + (long)mx * ldx + 8 * (l >> 4);
   // every load of the wave is issued before the first use
-  bf16x8 wa[SPW], wb[GLU ? SPW : 1], xb[SPW];
+  bf16x8 wa[SPW], wb[GLU ? SPW : 1], xb[SPW], gw[NORM ? SPW : 1];
+  const bf16* nr = (const bf16*)(NORM ? nw_ : w_) + 8 * (l >> 4);
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
     const int st = min(wv + kDlWaves * j, steps - 1);
     wa[j] = *gmem((const bf16x8*)(wr + 32 * st));
     if constexpr (GLU) wb[j] = *gmem((const bf16x8*)(wu + 32 * st));
     xb[j] = *gmem((const bf16x8*)(xr + 32 * st));
+    if constexpr (NORM) gw[j] = *gmem((const bf16x8*)(nr + 32 * st));
+  }
+  float rs = 1.f;
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const bool live = wv + kDlWaves * j < steps;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = (float)xb[j][i];
+        ss += live ? v * v : 0.f;
+      }
+    }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    if (l < 16) sSS[wv][l] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < kDlWaves; ++q) tot += sSS[q][l & 15];
+    rs = rsqrtf(tot / (float)K + eps);
   }
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, acu = acc;
 #pragma unroll
@@ -330,7 +358,11 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
     const bool live = wv + kDlWaves * j < steps;
     bf16x8 xf;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xf[i] = live ? xb[j][i] : (bf16)0.f;
+    for (int i = 0; i < 8; ++i) {
+      bf16 v = xb[j][i];
+      if constexpr (NORM) v = (bf16)((float)v * rs * (float)gw[j][i]);
+      xf[i] = live ? v : (bf16)0.f;
+    }
     acc = mfma16(wa[j], xf, acc);
     if constexpr (GLU) acu = mfma16(wb[j], xf, acu);
   }
@@ -373,27 +405,32 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
 
 template <int SPW>
 static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const void* x, long ldx, const void* w,
-                      const void* r, long ldr, void* y, long ldy, int M, int K, int N) {
-  if (glu)
-    hipLaunchKernelGGL((decode_linear_kernel<SPW, true>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N);
-  else
-    hipLaunchKernelGGL((decode_linear_kernel<SPW, false>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N);
+                      const void* r, long ldr, void* y, long ldy, int M, int K, int N, const void* nw, float eps) {
+#define CCQ_DL(G, NM)                                                                                        \
+  hipLaunchKernelGGL((decode_linear_kernel<SPW, G, NM>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N, \
+                     nw, eps)
+  if (glu) {
+    if (nw) CCQ_DL(true, true); else CCQ_DL(true, false);
+  } else {
+    if (nw) CCQ_DL(false, true); else CCQ_DL(false, false);
+  }
+#undef CCQ_DL
 }
 
 hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
-                                long ldy, int M, int K, int N, hipStream_t st) {
+                                long ldy, int M, int K, int N, const void* nw, float eps, hipStream_t st) {
   if (M <= 0 || N <= 0) return hipSuccess;
   const dim3 grid((unsigned)((N + 15) / 16)), block(kDlWaves * 64);
   const int spw = (K / 32 + kDlWaves - 1) / kDlWaves;
   switch (spw) {
-    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
-    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N); break;
+    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
+    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
+    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
+    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
+    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
+    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
+    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
+    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

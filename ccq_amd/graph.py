@@ -54,10 +54,23 @@ def _rows(x: torch.Tensor) -> torch.Tensor:
     return x2
 
 
-def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+def _norm_arg(x: torch.Tensor, norm_weight: Optional[torch.Tensor]):
+    if norm_weight is None:
+        return None
+    if (norm_weight.shape != (x.shape[-1],) or norm_weight.dtype != torch.bfloat16 or not norm_weight.is_contiguous()
+            or norm_weight.data_ptr() % 16):
+        raise ValueError(f"norm_weight {tuple(norm_weight.shape)} {norm_weight.dtype}: expected a contiguous bf16 "
+                         f"[{x.shape[-1]}]")
+    return norm_weight
+
+
+def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                  norm_weight: Optional[torch.Tensor] = None, norm_eps: float = 1e-5) -> torch.Tensor:
     """``x @ weight.T (+ residual)`` for a decode step's few token rows (``ccq_decode_linear``: the
     weight streamed once by MFMA tiles; fp32 accumulation rounded to bf16, then the residual added
-    and rounded again, as ``residual + linear(x)`` on bf16 tensors).  Inference only (no autograd).
+    and rounded again, as ``residual + linear(x)`` on bf16 tensors).  With ``norm_weight`` the rows
+    of x first go through a bf16 RMSNorm (``x * norm_weight / sqrt(mean(x^2) + norm_eps)``, one
+    rounding, as ``nn.RMSNorm`` does) inside the same kernel.  Inference only (no autograd).
     ``decode_linear_ok`` gives the shapes it takes."""
     if not decode_linear_ok(x, weight):
         raise ValueError(f"decode_linear: x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)} {weight.dtype}: "
@@ -74,14 +87,16 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torc
         if r2.stride(-1) != 1:
             r2 = r2.contiguous()
     call("ccq_decode_linear", ptr(x2), x2.stride(0), ptr(weight), ptr(r2), r2.stride(0) if r2 is not None else 0,
-         ptr(y), N, x2.shape[0], K, N, _lib.stream_of(x))
+         ptr(y), N, x2.shape[0], K, N, ptr(_norm_arg(x, norm_weight)), float(norm_eps), _lib.stream_of(x))
     return y
 
 
-def decode_linear_glu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+def decode_linear_glu(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
+                      norm_eps: float = 1e-5) -> torch.Tensor:
     """A gated MLP's up projection for a decode step: ``silu(gate) * up`` with
     ``gate, up = (x @ weight.T).chunk(2, -1)`` (``ccq_decode_linear_glu``; the bf16 roundings of those
-    torch ops made in the kernel, the [rows, 2N] projection never written).  weight [2N, K]."""
+    torch ops made in the kernel, the [rows, 2N] projection never written).  weight [2N, K];
+    ``norm_weight`` / ``norm_eps`` as in ``decode_linear``."""
     if not decode_linear_ok(x, weight) or weight.shape[0] % 2:
         raise ValueError(f"decode_linear_glu: x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)} "
                          f"{weight.dtype}: needs bf16 on the GPU, <= 16 rows, an even number of weight rows and a "
@@ -90,7 +105,7 @@ def decode_linear_glu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     x2 = _rows(x)
     y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.bfloat16)
     call("ccq_decode_linear_glu", ptr(x2), x2.stride(0), ptr(weight), ptr(y), N, x2.shape[0], K, N,
-         _lib.stream_of(x))
+         ptr(_norm_arg(x, norm_weight)), float(norm_eps), _lib.stream_of(x))
     return y
 
 
@@ -231,8 +246,10 @@ class CapturedDecode:
 
 class GDNLayerDecode:
     """The token step of one ``CCQGDN`` layer (recurrent mode with a cache, ``ccq/gdn/layer.py:253-412``)
-    on static buffers: ``__call__(h, residual=None)`` maps the layer input ``h [B, T, hidden]`` (bf16;
-    normally T = 1) to the layer output (plus ``residual``, with the roundings of ``residual + output``),
+    on static buffers: ``__call__(h, residual=None, norm=None)`` maps the layer input ``h [B, T, hidden]``
+    (bf16; normally T = 1; with ``norm``, an ``nn.RMSNorm`` with a bf16 weight and an explicit eps, the
+    input before that norm, which the input projection then applies) to the layer output (plus
+    ``residual``, with the roundings of ``residual + output``),
     advancing the layer's states, convolution caches and position in place.
 
     The step is the layer's input projections as one GEMM over their concatenated weights (taken at
@@ -296,12 +313,18 @@ class GDNLayerDecode:
         for dst, src in zip(self.conv, entry["conv_state"]):
             dst.copy_(last_inputs(src, self.W))
 
-    def __call__(self, h: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def __call__(self, h: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                 norm: Optional[torch.nn.Module] = None) -> torch.Tensor:
         L, st = self.layer, self.step
         B, T, H, K, V = self.B, self.T, self.H, self.K, self.V
         if h.shape[:2] != (B, T) or h.dtype != torch.bfloat16:
             raise ValueError(f"expected bf16 input [{B}, {T}, hidden] (got {tuple(h.shape)} {h.dtype})")
-        x = decode_linear(h, self.w_in) if self.fast else F.linear(h, self.w_in)
+        if self.fast:
+            # (with norm: the block's RMSNorm of h folded into the input projection)
+            x = decode_linear(h, self.w_in, norm_weight=None if norm is None else norm.weight,
+                              norm_eps=1e-5 if norm is None else norm.eps)
+        else:
+            x = F.linear(h if norm is None else norm(h), self.w_in)
         o_q, o_k, o_v, o_g, o_a, o_b = self.offsets
         cw = [c.weight for c in (L.q_conv1d, L.k_conv1d, L.v_conv1d)]
         cb = [c.bias for c in (L.q_conv1d, L.k_conv1d, L.v_conv1d)]

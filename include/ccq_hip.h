@@ -267,11 +267,13 @@ size_t ccq_decode_step_workspace_bytes(int B, int T, int H, int K);
  * bytes.  x bf16 [M, K] (row stride ldx, a multiple of 8, 16-byte aligned), weight bf16 [N, K]
  * (16-byte aligned), residual bf16 [M, N] with row stride ldr (nullable), y bf16 [M, N] with row
  * stride ldy.  fp32 accumulation rounded to bf16, then the residual added in fp32 and rounded again
- * (the roundings of residual + linear(x) on bf16 tensors).  M <= 16, K a multiple of 32 in
- * [32, 4096].  One kernel, no allocation, graph-capturable.
+ * (the roundings of residual + linear(x) on bf16 tensors).  With norm_weight (bf16 [K], 16-byte
+ * aligned; nullable) each row of x first becomes bf16(x * norm_weight / sqrt(mean(x^2) + norm_eps)),
+ * the rounding of a bf16 nn.RMSNorm ahead of the projection (a pre-norm block's norm, folded in).
+ * M <= 16, K a multiple of 32 in [32, 4096].  One kernel, no allocation, graph-capturable.
  */
 int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
-                      int64_t ldy, int M, int K, int N, void* stream);
+                      int64_t ldy, int M, int K, int N, const void* norm_weight, float norm_eps, void* stream);
 /*
  * A gated MLP's up projection in the same form: weight bf16 [2N, K] (the gate rows, then the up rows),
  * y bf16 [M, N] = silu(gate) * up with gate, up = (x weight^T).chunk(2, -1) -- the bf16 roundings of
@@ -280,7 +282,7 @@ int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void
  * fla's); for a decode step's MLP, which the C4 harness runs around the layers.
  */
 int ccq_decode_linear_glu(const void* x, int64_t ldx, const void* weight, void* y, int64_t ldy, int M, int K, int N,
-                          void* stream);
+                          const void* norm_weight, float norm_eps, void* stream);
 /*
  * The CCQ-GDN layer's per-token prologue in one launch, ahead of ccq_gdn_decode_step: what the
  * reference layer computes between its input projections and fused_recurrent_ccq_gdn

@@ -80,6 +80,34 @@ def test_decode_linear_glu(M, K, N):
     assert y.shape == (M, N) and e <= 5e-4
 
 
+@pytest.mark.parametrize("glu", [False, True])
+def test_decode_linear_folded_rmsnorm(glu):
+    """The RMSNorm folded into the projection equals torch's bf16 nn.RMSNorm followed by the same
+    projection kernel (the norm's output is rounded once; the row's sum of squares runs in another
+    order, which can move a rare element of the normalised row by one ulp)."""
+    dev = _cuda()
+    import torch.nn as nn
+    from ccq_amd.graph import decode_linear, decode_linear_glu
+    M, K, N = 16, 1024, 1024
+    gen = torch.Generator().manual_seed(5)
+    norm = nn.RMSNorm(K, eps=1e-5)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(K, generator=gen) * 2)
+    norm = norm.to(dev, BF)
+    x = (torch.randn(M, K, generator=gen) * 3).to(BF).to(dev)
+    w = (torch.randn((2 if glu else 1) * N, K, generator=gen) * 0.03).to(BF).to(dev)
+    if glu:
+        ref = decode_linear_glu(norm(x), w)
+        y = decode_linear_glu(x, w, norm_weight=norm.weight, norm_eps=norm.eps)
+    else:
+        ref = decode_linear(norm(x), w)
+        y = decode_linear(x, w, norm_weight=norm.weight, norm_eps=norm.eps)
+    torch.cuda.synchronize()
+    e = kern(y, ref.double().cpu())
+    print("folded rmsnorm", glu, f"{e:.2e}", flush=True)
+    assert e <= 5e-4
+
+
 def test_gated_rmsnorm_strided_gate_rows():
     dev = _cuda()
     from ccq_amd import _lib
