@@ -427,6 +427,9 @@ namespace {
 // K = V = 128: dk is the most sensitive output to them (measured kernel error of dk at K = 256 rose
 // from 1.8e-4 to 5.4e-4 with int16 dS', and stayed at 1.8e-4 with int16 S alone).
 int gdn_snap16(int K, int V) { return (K == 128 && V == 128) ? 3 : (K == 64 || K == 256) ? 1 : 0; }
+// the state part of dk and dw travel from the dq/dk/dw kernel to the WY backward as int16 rows with
+// a power-of-two scale per 32 columns where both kernels read and write that form
+bool gdn_grad16(int K, int V) { return K == 128 && V == 128; }
 
 struct GdnSaved {
   float* gcum;
@@ -465,6 +468,8 @@ struct GdnWork {
   void* dhTl;
   float* dkp32;
   float* dw32;
+  float* dkp_sc;
+  float* dw_sc;
   float* dgp;
 };
 
@@ -477,8 +482,16 @@ size_t carve_work(char* base, int64_t tokens, int NTG, int H, int K, int V, GdnW
     t.dhTl = sl.take<float>((size_t)NTG * H * V);
   else
     t.dhTl = sl.take<uint16_t>((size_t)NTG * H * V * K);
-  t.dkp32 = sl.take<float>((size_t)tokens * H * K);
-  t.dw32 = sl.take<float>((size_t)tokens * H * K);
+  if (gdn_grad16(K, V)) {
+    t.dkp32 = (float*)sl.take<int16_t>((size_t)tokens * H * K);
+    t.dw32 = (float*)sl.take<int16_t>((size_t)tokens * H * K);
+    t.dkp_sc = sl.take<float>((size_t)tokens * H * (K / 32));
+    t.dw_sc = sl.take<float>((size_t)tokens * H * (K / 32));
+  } else {
+    t.dkp32 = sl.take<float>((size_t)tokens * H * K);
+    t.dw32 = sl.take<float>((size_t)tokens * H * K);
+    t.dkp_sc = t.dw_sc = nullptr;
+  }
   t.dgp = sl.take<float>((size_t)(K / 64) * tokens * H);
   if (s) *s = t;
   return sl.off;
@@ -563,7 +576,7 @@ int ccq_gdn_bwd(const void* q, const float* q_f32, const void* k, const void* v,
   a.cu = cu_seqlens; a.chunk_idx = chunk_index; a.chunk_off = chunk_offsets;
   a.gcum = sv.gcum; a.tmat = sv.tmat; a.w = sv.w; a.wl = sv.wl; a.u = sv.u; a.hT = sv.hT; a.hTl = sv.hTl; a.U = sv.U; a.PT = sv.PT;
   a.dout = d_o; a.ds_fin = d_final_state; a.dU = wk.dU; a.dhT = wk.dhT; a.dhTl = wk.dhTl; a.dq32 = dq_f32; a.dkp32 = wk.dkp32;
-  a.dw32 = wk.dw32; a.dgp = wk.dgp; a.dk32 = dk_f32; a.dv = dv; a.dbeta = dbeta; a.dg = dg; a.ds0 = d_initial_state;
+  a.dw32 = wk.dw32; a.dkp_sc = wk.dkp_sc; a.dw_sc = wk.dw_sc; a.dgp = wk.dgp; a.dk32 = dk_f32; a.dv = dv; a.dbeta = dbeta; a.dg = dg; a.ds0 = d_initial_state;
   a.scale = scale; a.T = T; a.H = H; a.N = N; a.NT = (T + 63) / 64; a.NTG = num_chunks;
   a.snap16 = gdn_snap16(K, V);
   hipStream_t st = (hipStream_t)stream;

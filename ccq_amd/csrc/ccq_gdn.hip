@@ -2877,6 +2877,9 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
   constexpr int PT = BT + 8, PK = K + 8, PV = V + 8, NM = 256;
   constexpr int NKB = K / 32, NVB = V / 32;  // 32-column blocks of dk and dv
   constexpr int NJK = NKB / 2, NJV = NVB / 2;  // dk / dv tiles per wave
+  // dw and the state part of dk arrive as int16 rows with a scale per 32 columns (dkp_sc / dw_sc)
+  // from the K = V = 128 dq/dk/dw kernel, else as fp32
+  constexpr bool G16 = K == 128 && V == 128;
   static_assert(NKB % 2 == 0 && NVB % 2 == 0, "two column groups of tiles");
   __shared__ __attribute__((aligned(16))) bf16 sTh[BT * PT], sTl[BT * PT];  // T [a][c]
   __shared__ __attribute__((aligned(16))) bf16 sXh[BT * PT], sXl[BT * PT];  // dT [r][c], then dAs + dAs^T
@@ -2907,7 +2910,7 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
   if (w >= 4) {
     // ---------------- memory waves
     const int lm = tid - NM;
-    RowsF32<K, BT, NM> pw;
+    std::conditional_t<G16, RowsQ16<K, BT, NM>, RowsF32<K, BT, NM>> pw;
     RowsF32<V, BT, NM> pu;
     RowsF32<BT, BT, NM> pt;
     RowsBf16<K, BT, NM> pk;
@@ -2927,7 +2930,10 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
       tok0 = bos + c0;
     };
     auto load_a = [&]() {
-      pw.load(a.dw32 + (tok0 * a.H + h) * K, rsk, L, lm);
+      if constexpr (G16)
+        pw.load((const short*)a.dw32 + (tok0 * a.H + h) * K, a.dw_sc + (tok0 * a.H + h) * (K / 32), rsk, rsk / 32, L, lm);
+      else
+        pw.load(a.dw32 + (tok0 * a.H + h) * K, rsk, L, lm);
       pk.load((const bf16*)a.k + (tok0 * a.H + h) * K, rsk, L, lm);
     };
     auto load_b = [&]() { pu.load(a.dU + (tok0 * a.H + h) * (long)V, rsv, L, lm); };
@@ -3185,13 +3191,27 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
     }
     // dk_part of this wave's dk tiles (rows past the chunk read row L - 1), used at the end of P4;
     // issued before the barrier so that the compiler cannot move them next to their use
-    f32x4 dkp[NJK][4];
+    f32x4 dkp[G16 ? 1 : NJK][4];
+    s16x4 dkq[G16 ? NJK : 1][4];  // (int16 form: the values and their scale per 32-column block)
+    float dks[G16 ? NJK : 1];
+    if constexpr (G16) {
+      const long row = tok0 + min(rr, L - 1);
 #pragma unroll
-    for (int j = 0; j < NJK; ++j)
+      for (int j = 0; j < NJK; ++j) {
+        dks[j] = *gmem(a.dkp_sc + row * (rsk / 32) + (long)h * (K / 32) + (w & 1) * NJK + j);
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        dkp[j][g] = *gmem((const f32x4*)(a.dkp32 + (tok0 + min(rr, L - 1)) * rsk + (long)h * K +
-                                         ((w & 1) * NJK + j) * 32 + 8 * g + q4));
+        for (int g = 0; g < 4; ++g)
+          dkq[j][g] = *gmem((const s16x4*)((const short*)a.dkp32 + row * rsk + (long)h * K +
+                                           ((w & 1) * NJK + j) * 32 + 8 * g + q4));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJK; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          dkp[j][g] = *gmem((const f32x4*)(a.dkp32 + (tok0 + min(rr, L - 1)) * rsk + (long)h * K +
+                                           ((w & 1) * NJK + j) * 32 + 8 * g + q4));
+    }
     __syncthreads();  // B3
 
     // the unit's dk / dv rows as buffers ending after row L - 1 (stores of later rows are dropped)
@@ -3249,7 +3269,8 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_wy_v3_kernel(const GdnArgs a) 
           for (int ii = 0; ii < 4; ++ii) {
             const int i = 4 * g + ii;
             const float t2 = acc2[j][i];
-            o[ii] = dkp[j][g][ii] + acc[j][i] + br * gmr * t2;
+            const float part = G16 ? dks[j] * (float)dkq[j][g][ii] : dkp[G16 ? 0 : j][g][ii];
+            o[ii] = part + acc[j][i] + br * gmr * t2;
             s4 += t2 * (float)k4[ii];
           }
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), rdk, (int)((rr * rsk + kc) * 4), 0, 0);
@@ -3545,6 +3566,30 @@ __device__ __forceinline__ float rowsum32(const f32x16& ev, int l) {
   const float send = b1 ? a2[0] : a2[1], keep = b1 ? a2[1] : a2[0];
   const float a1 = keep + xlane<2>(send, l);
   return a1 + xlane<1>(a1, l);
+}
+// Largest |x| of each of the lane's 16 rows of a 32 x 32 C tile, over the row's 32 columns (the 32
+// lanes of the half-wave); every lane ends with the maxima of its own rows.
+__device__ __forceinline__ f32x16 rowmax32_all(const f32x16& v, int l) {
+  f32x16 m;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float x = fabsf(v[i]);
+    x = fmaxf(x, xlane<1>(x, l));
+    x = fmaxf(x, xlane<2>(x, l));
+    x = fmaxf(x, xlane<4>(x, l));
+    x = fmaxf(x, xlane<8>(x, l));
+    x = fmaxf(x, xlane<16>(x, l));
+    m[i] = x;
+  }
+  return m;
+}
+// Exponent e of the power-of-two scale of an int16 row piece with largest magnitude mx: mx / 2^e in
+// [2^14, 2^15) (floor(log2 mx) from the exponent field; 0 and subnormal maxima land on the lower clamp).
+__device__ __forceinline__ int q16_exp(float mx) {
+  return min(max((int)((__float_as_uint(mx) >> 23) & 0xff) - 127 - 14, -126), 113);
+}
+__device__ __forceinline__ unsigned short q16(float x, int e) {
+  return (unsigned short)(short)__builtin_amdgcn_fmed3f(rintf(ldexpf(x, -e)), -32767.f, 32767.f);
 }
 }  // namespace dq4
 
@@ -4191,15 +4236,33 @@ __global__ __launch_bounds__(kWalk8) void gdn_bwd_dqkw_v5_kernel(const GdnArgs a
           dKs = mfma(al, bh, dKs);
         }
       }
-      const int bytes = (int)(((L - 1) * rsk + K) * 4);
-      const auto rk = buf_rsrc(a.dkp32 + x.tok0 * rsk + (long)x.h * K, bytes);
-      const auto rw = buf_rsrc(a.dw32 + x.tok0 * rsk + (long)x.h * K, bytes);
+      // int16 rows with a power-of-two scale per row and 32-column block (this wave's columns): the
+      // row maxima by lane exchanges within the half-wave, one scale store per row (lane i of the
+      // half-wave stores that of its element i)
+      const int bytes = (int)(((L - 1) * rsk + K) * 2);
+      const auto rk = buf_rsrc((short*)a.dkp32 + x.tok0 * rsk + (long)x.h * K, bytes);
+      const auto rw = buf_rsrc((short*)a.dw32 + x.tok0 * rsk + (long)x.h * K, bytes);
+      const f32x16 mk = rowmax32_all(dKs, l), mw = rowmax32_all(dW, l);
+      float sk = 0.f, sw = 0.f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int r = tr + arow(i, l), off = (int)((r * rsk + c) * 4);
-        const float xk = dKs[i], xw = -dW[i];
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, xk), rk, off, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, xw), rw, off, 0, 0);
+        const int r = tr + arow(i, l), off = (int)((r * rsk + c) * 2);
+        const int ek = q16_exp(mk[i]), ew = q16_exp(mw[i]);
+        __builtin_amdgcn_raw_buffer_store_b16(q16(dKs[i], ek), rk, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(q16(-dW[i], ew), rw, off, 0, 0);
+        if ((l & 31) == i) {
+          sk = ldexpf(1.f, ek);
+          sw = ldexpf(1.f, ew);
+        }
+      }
+      if ((l & 31) < 16) {
+        const long rsc = (long)a.H * (K / 32);
+        const int sbytes = (int)(((L - 1) * rsc + K / 32) * 4);
+        const auto rks = buf_rsrc(a.dkp_sc + x.tok0 * rsc + (long)x.h * (K / 32), sbytes);
+        const auto rws = buf_rsrc(a.dw_sc + x.tok0 * rsc + (long)x.h * (K / 32), sbytes);
+        const int off = (int)(((tr + arow(l & 15, l)) * rsc + kc / 32) * 4);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, sk), rks, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, sw), rws, off, 0, 0);
       }
     }
     bar();

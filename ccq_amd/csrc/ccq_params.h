@@ -147,7 +147,9 @@ namespace ccq {
 //   PT   [NTG, H, 64, 64] fp32    P^T, P = scale (Qc K^T o Gamma), causal incl. diagonal
 //   dU   [tokens, H, V] fp32      gradient of U
 //   dhT  [NTG, H, V, K] 16-bit    gradient of the state after each chunk (transposed), dhTl as hTl
-//   dq32 / dkp32 / dw32 [tokens, H, K] fp32, dgp [K/64, tokens, H] fp32
+//   dq32 / dkp32 / dw32 [tokens, H, K] fp32, dgp [K/64, tokens, H] fp32; for K = V = 128 dkp32 and
+//                                 dw32 hold int16 [tokens, H, K] with fp32 power-of-two scales
+//                                 dkp_sc / dw_sc [tokens, H, K/32] (one per row and 32-column block)
 enum GdnStage { kGdnPrep = 0, kGdnFwdState, kGdnFwdO, kGdnBwdState, kGdnBwdDqkw, kGdnBwdWy };
 
 struct GdnArgs {
@@ -181,6 +183,8 @@ struct GdnArgs {
   float* dq32;              // gradient of the cleaned query
   float* dkp32;             // gradient of k (state/output part)
   float* dw32;
+  float* dkp_sc;            // scales of dkp32 / dw32 in their int16 form (nullable: fp32)
+  float* dw_sc;
   float* dgp;
   float* dk32;              // gradient of k (total GDN part)
   void* dv;                 // bf16 [tokens, H, V]

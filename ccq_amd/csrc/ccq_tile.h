@@ -21,6 +21,7 @@ namespace ccq {
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));  // int16 bit patterns of a 16-byte piece
+typedef short s16x4 __attribute__((ext_vector_type(4)));  // int16 values of an 8-byte piece
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -849,6 +850,45 @@ struct RowsF32 {
       }
       *(bf16x4*)(hi + e) = vh;
       *(bf16x4*)(lo + e) = vl;
+    }
+  }
+};
+
+// ROWS x D int16 rows with an fp32 scale per row and 32-column block (row stride gstride elements,
+// scale row stride sstride), staged through registers like RowsF32: 16-byte pieces of 8 values.
+template <int D, int ROWS, int NTHR>
+struct RowsQ16 {
+  static constexpr int VPR = D / 8, TOT = ROWS * VPR, N = (TOT + NTHR - 1) / NTHR;
+  static_assert(D % 32 == 0, "32-column scale blocks");
+  s16x8 v[N];
+  float sc[N];
+  __device__ __forceinline__ void load(const short* g, const float* gs, long gstride, long sstride, int nvalid,
+                                       int lt) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = min(lt + j * NTHR, TOT - 1), r = idx / VPR, p = idx % VPR;
+      const long rr = r < nvalid ? r : 0;
+      v[j] = *gmem((const s16x8*)(g + rr * gstride + p * 8));
+      sc[j] = *gmem(gs + rr * sstride + p / 4);
+    }
+  }
+  // row-major hi/lo bf16 pair of scale x value (16-byte pieces; exact: 16 significant bits)
+  __device__ __forceinline__ void store_split(bf16* hi, bf16* lo, int ld, int nvalid, int lt) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = lt + j * NTHR;
+      if (TOT % NTHR != 0 && idx >= TOT) continue;
+      const int r = idx / VPR, e = r * ld + (idx % VPR) * 8;
+      bf16x8 vh, vl;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        bf16 x, y;
+        split2(r < nvalid ? sc[j] * (float)v[j][i] : 0.f, x, y);
+        vh[i] = x;
+        vl[i] = y;
+      }
+      *(bf16x8*)(hi + e) = vh;
+      *(bf16x8*)(lo + e) = vl;
     }
   }
 };
