@@ -438,7 +438,7 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
     checked against the eager layers' before it is timed."""
     import torch.nn as nn
     import torch.nn.functional as F
-    from ccq_amd.graph import GDNLayerDecode, decode_linear, decode_linear_glu
+    from ccq_amd.graph import GDNLayerDecode, decode_linear_glu, decode_linear_split, split_plan, split_workspace
     from ccq_amd.layers import CCQGDN, LayerCache
 
     inter = 256 * ((int(d * 4 * 2 / 3) + 255) // 256)  # fla GatedMLP's intermediate size (hidden_ratio 4)
@@ -462,10 +462,14 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
 
         def mlp_step(self, x):
             # the captured decode step's MLP: the norm folded into the up projection's kernel, which
-            # also forms silu(gate) * up; the down projection with the residual added in it
+            # also forms silu(gate) * up; the down projection with the residual added in it, its
+            # contraction split over several workgroups per column block (workspace: zeroed once)
             h = decode_linear_glu(x, self.gate_up.weight, norm_weight=self.mlp_norm.weight,
                                   norm_eps=self.mlp_norm.eps)
-            return decode_linear(h, self.down.weight, x)
+            if not hasattr(self, "down_ws"):
+                self.down_splits = split_plan(inter, d)
+                self.down_ws = split_workspace(d, self.down_splits, x.device)
+            return decode_linear_split(h, self.down.weight, x, self.down_splits, self.down_ws)
 
         def forward(self, x, cache):
             return self.mlp(x + self.attn(self.attn_norm(x), past_key_values=cache, use_cache=True)[0])

@@ -63,6 +63,8 @@ SIGNATURES = {
     "ccq_gdn_decode_prologue": (_I, [_P] * 5 + [_I64] + [_P] * 19 + [_I] * 7 + [_F, _P]),
     "ccq_decode_linear": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _P, _F, _P]),
     "ccq_decode_linear_glu": (_I, [_P, _I64, _P, _P, _I64, _I, _I, _I, _P, _F, _P]),
+    "ccq_decode_linear_split": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _P]),
+    "ccq_decode_linear_split_workspace_bytes": (_SZ, [_I, _I]),
     "ccq_timing_enable": (_I, [_I]),
     "ccq_timing_reset": (_I, []),
     "ccq_timing_select": (_I, [ctypes.c_char_p]),

@@ -32,7 +32,9 @@ hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
 hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
-                                long ldy, int M, int K, int N, const void* nw, float eps, hipStream_t st);
+                                long ldy, int M, int K, int N, const void* nw, float eps, int splits, void* ws,
+                                hipStream_t st);
+size_t decode_linear_split_bytes(int N, int splits);
 hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st);
 int cseg_count(int N, int H, int T, int K);
 bool cseg_sums_supported(int K);
@@ -827,7 +829,8 @@ int ccq_gated_rmsnorm_bwd(const void* x, const void* g, const float* weight, con
 
 static int decode_linear_entry(const char* who, bool glu, const void* x, int64_t ldx, const void* weight,
                                const void* residual, int64_t ldr, void* y, int64_t ldy, int M, int K, int N,
-                               const void* norm_weight, float norm_eps, void* stream) {
+                               const void* norm_weight, float norm_eps, void* stream, int splits = 1,
+                               void* workspace = nullptr) {
   if (M < 0 || M > 16 || N < 0 || K < 32 || K > 4096 || K % 32 || ldx < K || ldx % 8 || ldy < N ||
       (residual && ldr < N))
     return fail(CCQ_ERR_SHAPE, "%s: M=%d K=%d N=%d ldx=%lld ldy=%lld (need M <= 16, K a multiple of 32 in [32, 4096], "
@@ -836,8 +839,23 @@ static int decode_linear_entry(const char* who, bool glu, const void* x, int64_t
   if (!aligned16(x) || !aligned16(weight) || !aligned16(norm_weight))
     return fail(CCQ_ERR_ALIGN, "%s: x, the weight and the norm weight must be 16-byte aligned", who);
   return hip_status(launch_decode_linear(glu, x, ldx, weight, residual, ldr, y, ldy, M, K, N, norm_weight, norm_eps,
-                                         (hipStream_t)stream),
+                                         splits, workspace, (hipStream_t)stream),
                     who);
+}
+
+size_t ccq_decode_linear_split_workspace_bytes(int N, int splits) {
+  return N < 0 || splits < 1 ? 0 : decode_linear_split_bytes(N, splits);
+}
+
+int ccq_decode_linear_split(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
+                            int64_t ldy, int M, int K, int N, int splits, void* workspace, void* stream) {
+  const char* who = "ccq_decode_linear_split";
+  if (splits < 1 || splits > 8 || splits > K / 32)
+    return fail(CCQ_ERR_SHAPE, "%s: splits=%d not in [1, min(8, K/32)] (K=%d)", who, splits, K);
+  if (splits > 1 && !workspace) return fail(CCQ_ERR_NULL, "%s: splits > 1 needs the workspace", who);
+  if (!aligned16(workspace)) return fail(CCQ_ERR_ALIGN, "%s: the workspace must be 16-byte aligned", who);
+  return decode_linear_entry(who, false, x, ldx, weight, residual, ldr, y, ldy, M, K, N, nullptr, 1e-5f, stream,
+                             splits, workspace);
 }
 
 int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,

@@ -301,20 +301,40 @@ hipError_t decode_scratch(hipStream_t st, void** out) {
 // four lane groups of a row, then one LDS exchange across the waves).
 // ===========================================================================
 constexpr int kDlWaves = 16, kDlMaxSteps = 8;  // K <= 16 * 8 * 32 = 4096
-// SPW: 32-wide steps per wave (every wave takes SPW; steps past K read the last step's address and
-// contribute a zero x fragment, so the code has no branch around a load or an MFMA)
+constexpr int kDlMaxSplits = 8;
+
+// Split contraction (plain form only): workgroup (b, s) of a (blocks, S) grid takes the 32-wide
+// steps [s sps, (s + 1) sps) of column block b and leaves its 16 x 16 partial tile in part (fp32,
+// [S][blocks][256]) with device-scope stores; the last of the block's S workgroups to count itself in
+// cnt[b] (an atomic increment: it sees S - 1) adds the S tiles in split order -- the same order
+// whichever arrives last, so the result does not depend on timing -- finishes the block, and
+// returns cnt[b] to zero.  No workgroup waits for another.
+struct DlSplit {
+  int S, sps;
+  float* part;
+  unsigned* cnt;
+};
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// SPW: 32-wide steps per wave (every wave takes SPW; steps past its range read the range's last
+// step's address and contribute a zero x fragment, so the code has no branch around a load or an MFMA)
 template <int SPW, bool GLU, bool NORM>
 __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, long ldx, const void* w_,
                                                                        const void* r_, long ldr, void* y_, long ldy,
                                                                        int M, int K, int N, const void* nw_,
-                                                                       float eps) {
+                                                                       float eps, const DlSplit sp) {
   __shared__ f32x4 sAcc[GLU ? 2 : 1][kDlWaves][64];
   __shared__ float sSS[NORM ? kDlWaves : 1][16];
   const bf16* x = (const bf16*)x_;
   const bf16* w = (const bf16*)w_;
   const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
   const int n0 = blockIdx.x * 16;
-  const int steps = K / 32;
+  const int s0 = blockIdx.y * sp.sps, steps = min(K / 32, s0 + sp.sps);  // this workgroup's steps [s0, steps)
   const int nw = min(n0 + (l & 15), N - 1);            // weight row of this lane (rows past N repeat the last)
   const int mx = min(l & 15, M - 1);                    // token row of this lane (rows past M repeat the last)
   const bf16* wr = w + (long)nw * K + 8 * (l >> 4);
@@ -325,7 +345,7 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   const bf16* nr = (const bf16*)(NORM ? nw_ : w_) + 8 * (l >> 4);
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
-    const int st = min(wv + kDlWaves * j, steps - 1);
+    const int st = min(s0 + wv + kDlWaves * j, steps - 1);
     wa[j] = *gmem((const bf16x8*)(wr + 32 * st));
     if constexpr (GLU) wb[j] = *gmem((const bf16x8*)(wu + 32 * st));
     xb[j] = *gmem((const bf16x8*)(xr + 32 * st));
@@ -336,7 +356,7 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
-      const bool live = wv + kDlWaves * j < steps;
+      const bool live = s0 + wv + kDlWaves * j < steps;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float v = (float)xb[j][i];
@@ -355,7 +375,7 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, acu = acc;
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
-    const bool live = wv + kDlWaves * j < steps;
+    const bool live = s0 + wv + kDlWaves * j < steps;
     bf16x8 xf;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -375,6 +395,25 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   for (int q = 1; q < kDlWaves; ++q) {
     const f32x4 v = sAcc[0][q][l];
     sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
+  }
+  if (sp.S > 1) {
+    // this split's tile out, counted in; the last to arrive adds the S tiles in split order
+    float* const part = sp.part + (long)blockIdx.x * 256 + 4 * l;
+    const long pstride = (long)gridDim.x * 256;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st_dev(part + blockIdx.y * pstride + i, sum[i]);
+    __builtin_amdgcn_s_waitcnt(0);  // the stores acknowledged before the count
+    unsigned old = 0;
+    if (l == 0) old = __hip_atomic_fetch_add(sp.cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != (unsigned)(sp.S - 1)) return;
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < sp.S; ++q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tot[i] += q == (int)blockIdx.y ? sum[i] : ld_dev(part + q * pstride + i);
+    }
+    sum = tot;
+    if (l == 0) __hip_atomic_store(sp.cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if constexpr (GLU) {
     f32x4 su = sAcc[GLU ? 1 : 0][0][l];
@@ -405,10 +444,11 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
 
 template <int SPW>
 static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const void* x, long ldx, const void* w,
-                      const void* r, long ldr, void* y, long ldy, int M, int K, int N, const void* nw, float eps) {
+                      const void* r, long ldr, void* y, long ldy, int M, int K, int N, const void* nw, float eps,
+                      const DlSplit& sp) {
 #define CCQ_DL(G, NM)                                                                                        \
   hipLaunchKernelGGL((decode_linear_kernel<SPW, G, NM>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N, \
-                     nw, eps)
+                     nw, eps, sp)
   if (glu) {
     if (nw) CCQ_DL(true, true); else CCQ_DL(true, false);
   } else {
@@ -417,20 +457,35 @@ static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const voi
 #undef CCQ_DL
 }
 
+// Workspace of the split form: the block counters (zero between calls), then the partial tiles.
+size_t decode_linear_split_bytes(int N, int splits) {
+  const size_t blocks = (size_t)(N + 15) / 16;
+  return ((blocks * 4 + 255) / 256) * 256 + (size_t)splits * blocks * 256 * 4;
+}
+
 hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
-                                long ldy, int M, int K, int N, const void* nw, float eps, hipStream_t st) {
+                                long ldy, int M, int K, int N, const void* nw, float eps, int splits, void* ws,
+                                hipStream_t st) {
   if (M <= 0 || N <= 0) return hipSuccess;
-  const dim3 grid((unsigned)((N + 15) / 16)), block(kDlWaves * 64);
-  const int spw = (K / 32 + kDlWaves - 1) / kDlWaves;
+  const int blocks = (N + 15) / 16, steps = K / 32;
+  DlSplit sp{1, steps, nullptr, nullptr};
+  if (splits > 1) {
+    sp.sps = (steps + splits - 1) / splits;
+    sp.S = (steps + sp.sps - 1) / sp.sps;  // (no empty split)
+    sp.cnt = (unsigned*)ws;
+    sp.part = (float*)((char*)ws + ((size_t)blocks * 4 + 255) / 256 * 256);
+  }
+  const dim3 grid((unsigned)blocks, (unsigned)sp.S), block(kDlWaves * 64);
+  const int spw = (sp.sps + kDlWaves - 1) / kDlWaves;
   switch (spw) {
-    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
-    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
-    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
-    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
-    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
-    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
-    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
-    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps); break;
+    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
+    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
+    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
+    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
+    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
+    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
+    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
+    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

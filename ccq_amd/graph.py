@@ -91,6 +91,43 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torc
     return y
 
 
+def split_plan(K: int, N: int) -> int:
+    """Workgroups per 16 output columns for ``decode_linear_split``: enough for about 256 workgroups
+    (one per CU), at most 8 and at least 4 contraction steps of 32 per workgroup."""
+    blocks = (N + 15) // 16
+    return max(1, min(8, (K // 32) // 4, -(-256 // blocks)))
+
+
+def split_workspace(N: int, splits: int, device) -> torch.Tensor:
+    """A zeroed workspace for ``decode_linear_split`` (its counters start at zero; every call leaves
+    them so)."""
+    n = _lib.load().ccq_decode_linear_split_workspace_bytes(N, splits)
+    return torch.zeros(max(n, 16), device=device, dtype=torch.uint8)
+
+
+def decode_linear_split(x: torch.Tensor, weight: torch.Tensor, residual: Optional[torch.Tensor], splits: int,
+                        workspace: Optional[torch.Tensor]) -> torch.Tensor:
+    """``decode_linear`` with the contraction split over ``splits`` workgroups per 16 output columns
+    (``ccq_decode_linear_split``): the partial tiles are added by the last workgroup of each block to
+    finish, in split order.  ``workspace`` from ``split_workspace(N, splits)``; calls sharing one
+    workspace must not overlap (one stream)."""
+    if not decode_linear_ok(x, weight):
+        raise ValueError(f"decode_linear_split: x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)} "
+                         f"{weight.dtype}: needs bf16 on the GPU, <= 16 rows, a width that is a multiple of 32 "
+                         f"in [32, 4096]")
+    K, N = x.shape[-1], weight.shape[0]
+    x2 = _rows(x)
+    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.bfloat16)
+    r2 = None
+    if residual is not None:
+        if residual.shape != y.shape:
+            raise ValueError(f"residual {tuple(residual.shape)}: expected {tuple(y.shape)}")
+        r2 = _rows(residual)
+    call("ccq_decode_linear_split", ptr(x2), x2.stride(0), ptr(weight), ptr(r2), 0 if r2 is None else r2.stride(0),
+         ptr(y), N, x2.shape[0], K, N, int(splits), ptr(workspace), _lib.stream_of(x))
+    return y
+
+
 def decode_linear_glu(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
                       norm_eps: float = 1e-5) -> torch.Tensor:
     """A gated MLP's up projection for a decode step: ``silu(gate) * up`` with
@@ -288,6 +325,9 @@ class GDNLayerDecode:
         # the projections as decode_linear launches when the step has at most 16 token rows
         self.fast = B * T <= 16 and decode_linear_ok(torch.empty(B * T, L.hidden_size, device=dev,
                                                                  dtype=torch.bfloat16), self.w_in)
+        # the output projection (N = hidden, about 1024: few column blocks) with its contraction split
+        self.o_splits = split_plan(dv, L.o_proj.weight.shape[0])
+        self.o_ws = split_workspace(L.o_proj.weight.shape[0], self.o_splits, dev) if self.o_splits > 1 else None
 
     def refresh(self) -> None:
         """Concatenate the layer's current input-projection weights."""
@@ -348,6 +388,8 @@ class GDNLayerDecode:
             o = L.o_norm(st.o)
         o = o.reshape(B, T, H * V)
         if self.fast and decode_linear_ok(o, L.o_proj.weight):
+            if self.o_splits > 1:
+                return decode_linear_split(o, L.o_proj.weight, residual, self.o_splits, self.o_ws)
             return decode_linear(o, L.o_proj.weight, residual)
         y = L.o_proj(o)
         return y if residual is None else residual + y

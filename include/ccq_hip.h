@@ -284,6 +284,20 @@ int ccq_decode_linear(const void* x, int64_t ldx, const void* weight, const void
 int ccq_decode_linear_glu(const void* x, int64_t ldx, const void* weight, void* y, int64_t ldy, int M, int K, int N,
                           const void* norm_weight, float norm_eps, void* stream);
 /*
+ * ccq_decode_linear (without the norm) with the contraction split over `splits` workgroups per 16
+ * output columns (1 <= splits <= min(8, K/32)): for the narrow projections of a decode step (N about
+ * 1024: o_proj, an MLP's down projection), which otherwise run as N/16 workgroups, too few to keep
+ * the weight's bytes in flight.  Each workgroup leaves an fp32 partial tile in the workspace; the
+ * last of a column block's workgroups to arrive (an atomic count) adds the tiles in split order, so
+ * the result is the same whichever finishes last, and rounds as ccq_decode_linear does.  workspace:
+ * ccq_decode_linear_split_workspace_bytes(N, splits) bytes, 16-byte aligned, zero before the first
+ * call (its counters; every call leaves them zero); calls that overlap on one workspace race.
+ * No counterpart in the reference (its projections are nn.Linear: ccq/gdn/layer.py:408).
+ */
+size_t ccq_decode_linear_split_workspace_bytes(int N, int splits);
+int ccq_decode_linear_split(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
+                            int64_t ldy, int M, int K, int N, int splits, void* workspace, void* stream);
+/*
  * The CCQ-GDN layer's per-token prologue in one launch, ahead of ccq_gdn_decode_step: what the
  * reference layer computes between its input projections and fused_recurrent_ccq_gdn
  * (ccq/gdn/layer.py:266-316) -- the q, k, v short convolutions + SiLU with their caches (fla

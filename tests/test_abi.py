@@ -224,3 +224,15 @@ def test_decode_rejects_unaligned_states_and_gv():
     st = lib.ccq_gla_decode(p, p, p, p, None, None, None, odd, p, p, p, None, p, p, p, m_out, p, 2, 1, 4, 64, 64, 2, 0, 1,
                             1, 0, 0.125, None)
     assert st == CCQ_ERR_ALIGN
+
+
+def test_decode_linear_split_checks_and_workspace():
+    # counters (one per 16 output columns, rounded up to 256 bytes) then splits x blocks partial tiles
+    lib = _lib.load()
+    p = _fake()
+    assert lib.ccq_decode_linear_split_workspace_bytes(1024, 4) == 256 + 4 * 64 * 256 * 4
+    assert lib.ccq_decode_linear_split_workspace_bytes(100, 3) == 256 + 3 * 7 * 256 * 4
+    # splits outside [1, min(8, K/32)] and a split call without its workspace are refused on the host
+    assert lib.ccq_decode_linear_split(p, 64, p, None, 0, p, 40, 1, 64, 40, 3, p, None) == CCQ_ERR_SHAPE
+    assert lib.ccq_decode_linear_split(p, 2048, p, None, 0, p, 40, 1, 2048, 40, 9, p, None) == CCQ_ERR_SHAPE
+    assert lib.ccq_decode_linear_split(p, 2048, p, None, 0, p, 40, 1, 2048, 40, 4, None, None) == CCQ_ERR_NULL

@@ -1,5 +1,6 @@
-"""GPU checks of the decode step's projection kernels: ``decode_linear`` (``ccq_decode_linear``) and
-its gated up-projection form (``ccq_decode_linear_glu``) against a float64 restatement with the bf16
+"""GPU checks of the decode step's projection kernels: ``decode_linear`` (``ccq_decode_linear``), its
+split-contraction form (``ccq_decode_linear_split``) and its gated up-projection form
+(``ccq_decode_linear_glu``) against a float64 restatement with the bf16
 roundings of the torch ops they replace (``residual + linear(x)``; ``silu(gate) * up`` of
 ``linear(x).chunk(2, -1)``), and the
 gated RMSNorm that reads its gate rows in place (``ccq_gated_rmsnorm_fwd_strided``) against the
@@ -128,3 +129,29 @@ def test_gated_rmsnorm_strided_gate_rows():
          T * H, V, 1e-5, s)
     torch.cuda.synchronize()
     assert torch.equal(y0, y1) and torch.equal(r0, r1)
+
+
+@pytest.mark.parametrize("M,K,N,splits", [(16, 2816, 1024, 4), (16, 2048, 1024, 4), (3, 1024, 100, 3),
+                                          (1, 96, 40, 3), (16, 4096, 520, 8)])
+def test_decode_linear_split(M, K, N, splits):
+    """The split contraction (partial tiles added by the last workgroup of each column block) against
+    float64, over three calls in a row on one workspace (its counters must come back to zero; the
+    second call with other inputs), and against the unsplit kernel."""
+    dev = _cuda()
+    from ccq_amd.graph import decode_linear, decode_linear_split, split_workspace
+    print("test_decode_linear_split", M, K, N, splits, flush=True)
+    ws = split_workspace(N, splits, dev)  # (the block counters lead it)
+    gen = torch.Generator().manual_seed(K + N + splits)
+    for call in range(3):
+        x = torch.randn(M, K, generator=gen).to(BF)
+        w = (torch.randn(N, K, generator=gen) * 0.03).to(BF)
+        res = torch.randn(M, N, generator=gen).to(BF)
+        ref = res.to(D) + _r(x.to(D) @ w.to(D).T)
+        y = decode_linear_split(x.to(dev), w.to(dev), res.to(dev), splits, ws)
+        y1 = decode_linear(x.to(dev), w.to(dev), res.to(dev))
+        torch.cuda.synchronize()
+        e, e1 = kern(y, ref), kern(y, y1.double().cpu())
+        print((M, K, N, splits), call, f"kernel {e:.2e} vs unsplit {e1:.2e}", flush=True)
+        assert y.shape == (M, N) and e <= 5e-4 and e1 <= 5e-4
+        blocks = (N + 15) // 16
+        assert int(ws[:4 * blocks].view(torch.int32).abs().sum()) == 0, "counters not back to zero"
