@@ -42,6 +42,8 @@ SIGNATURES = {
     "ccq_gla_decode": (_I, [_P] * 17 + [_I] * 10 + [_F, _P]),
     "ccq_gdn_decode_noalloc": (_I, [_P] * 18 + [_I] * 10 + [_F, _P]),
     "ccq_decode_step_workspace_bytes": (_SZ, [_I] * 4),
+    "ccq_gdn_decode_in_proj": (_I, [_P, _I64, _P, _P, _I64, _I, _I, _I, _P, _F] + [_I] * 9 + [_P] * 13 + [_I, _P]),
+    "ccq_gdn_layer_decode_step": (_I, [_P, _I64, _I, _I, _I] + [_P] * 10 + [_I] * 7 + [_F, _F, _P]),
     "ccq_gdn_decode_step": (_I, [_P] * 14 + [_I] * 8 + [_F, _P]),
     "ccq_gla_decode_step": (_I, [_P] * 13 + [_I] * 7 + [_F, _P]),
     "ccq_clean_z_saved_bytes": (_SZ, [_I, _I, _I]),

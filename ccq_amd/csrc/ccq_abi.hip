@@ -31,9 +31,15 @@ int narrow_blocks(long M);
 hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
+struct DlConv;
 hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
                                 long ldy, int M, int K, int N, const void* nw, float eps, int splits, void* ws,
-                                hipStream_t st);
+                                const DlConv* conv, hipStream_t st);
+hipError_t launch_decode_in_proj(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N,
+                                 const void* nw, float eps, int oq, int ok, int ov, int oa, int ob, int Dq, int Dv,
+                                 int H, int T, int neg_eig, const void* wq, const void* wk, const void* wv,
+                                 const void* bq, const void* bk, const void* bv, void* cq, void* ck, void* cv,
+                                 const void* alog, const void* dtb, float* g, float* beta, hipStream_t st);
 size_t decode_linear_split_bytes(int N, int splits);
 hipError_t launch_cseg(int stage, const WalkArgs& a, hipStream_t st);
 int cseg_count(int N, int H, int T, int K);
@@ -839,7 +845,32 @@ static int decode_linear_entry(const char* who, bool glu, const void* x, int64_t
   if (!aligned16(x) || !aligned16(weight) || !aligned16(norm_weight))
     return fail(CCQ_ERR_ALIGN, "%s: x, the weight and the norm weight must be 16-byte aligned", who);
   return hip_status(launch_decode_linear(glu, x, ldx, weight, residual, ldr, y, ldy, M, K, N, norm_weight, norm_eps,
-                                         splits, workspace, (hipStream_t)stream),
+                                         splits, workspace, nullptr, (hipStream_t)stream),
+                    who);
+}
+
+int ccq_gdn_decode_in_proj(const void* x, int64_t ldx, const void* weight, void* y, int64_t ldy, int M, int K, int N,
+                           const void* norm_weight, float norm_eps, int off_q, int off_k, int off_v, int off_a,
+                           int off_b, int H, int Dq, int Dv, int T, const void* wq, const void* wk, const void* wv,
+                           const void* bq, const void* bk, const void* bv, void* cq, void* ck, void* cv,
+                           const void* A_log, const void* dt_bias, float* g, float* beta, int allow_neg_eigval,
+                           void* stream) {
+  const char* who = "ccq_gdn_decode_in_proj";
+  if (T < 1 || M % T) return fail(CCQ_ERR_SHAPE, "%s: M=%d rows are not whole sequences of T=%d tokens", who, M, T);
+  if (H < 1 || Dq < 1 || Dv < 1 || off_q < 0 || off_k < 0 || off_v < 0 || off_a < 0 || off_b < 0 ||
+      off_q + Dq > N || off_k + Dq > N || off_v + Dv > N || off_a + H > N || off_b + H > N)
+    return fail(CCQ_ERR_SHAPE, "%s: a column block lies outside the N=%d projection columns", who, N);
+  if (!wq || !wk || !wv || !cq || !ck || !cv || !A_log || !dt_bias || !g || !beta)
+    return fail(CCQ_ERR_NULL, "%s: the convolution weights and caches, A_log, dt_bias, g and beta are required", who);
+  if (M < 0 || M > 16 || N < 0 || K < 32 || K > 4096 || K % 32 || ldx < K || ldx % 8 || ldy < N)
+    return fail(CCQ_ERR_SHAPE, "%s: M=%d K=%d N=%d ldx=%lld ldy=%lld (need M <= 16, K a multiple of 32 in [32, 4096], "
+                "ldx >= K a multiple of 8, ldy >= N)", who, M, K, N, (long long)ldx, (long long)ldy);
+  if (!x || !weight || !y) return fail(CCQ_ERR_NULL, "%s: x, weight, y are required", who);
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(norm_weight))
+    return fail(CCQ_ERR_ALIGN, "%s: x, the weight and the norm weight must be 16-byte aligned", who);
+  return hip_status(launch_decode_in_proj(x, ldx, weight, y, ldy, M, K, N, norm_weight, norm_eps, off_q, off_k,
+                                          off_v, off_a, off_b, Dq, Dv, H, T, allow_neg_eigval ? 1 : 0, wq, wk, wv,
+                                          bq, bk, bv, cq, ck, cv, A_log, dt_bias, g, beta, (hipStream_t)stream),
                     who);
 }
 
@@ -1091,17 +1122,20 @@ int decode_common(const char* who, DecodeArgs& a, const void* q, const void* k, 
                   const float* gate_w, const float* gate_b, const float* state, const float* cov_state,
                   const float* mean_state, const int64_t* cu_seqlens, void* o, float* state_out,
                   float* cov_state_out, float* mean_state_out, void* workspace, int B, int T, int H, int K, int V,
-                  int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq, float scale) {
+                  int N, int position_offset, int subtract_mean, int use_l2norm, int enable_ccq, float scale,
+                  bool layer = false) {
   if (int s = check_common(B, T, H, N, cu_seqlens)) return s;
   if (!clean_k_ok(K)) return fail(CCQ_ERR_SHAPE, "%s: K=%d not in {32, 64, 128, 256}", who, K);
   if (V <= 0 || V % 64 != 0 || V > 1024)
     return fail(CCQ_ERR_SHAPE, "%s: V=%d must be a positive multiple of 64 (<= 1024)", who, V);
-  if (!q || !k || !v || !o || !workspace) return fail(CCQ_ERR_NULL, "%s: q, k, v, o and workspace are required", who);
-  if (enable_ccq && !lambda && !gate_w) return fail(CCQ_ERR_NULL, "%s: lambda or gate_w is required", who);
+  // (the layer form reads q, k, v from the projection rows and forms lambda itself)
+  if ((!layer && (!q || !k || !v)) || !o || !workspace)
+    return fail(CCQ_ERR_NULL, "%s: q, k, v, o and workspace are required", who);
+  if (!layer && enable_ccq && !lambda && !gate_w) return fail(CCQ_ERR_NULL, "%s: lambda or gate_w is required", who);
   if (gate_w && !gate_b) return fail(CCQ_ERR_NULL, "%s: gate_w needs gate_b", who);
   if (mean_state_out && mean_state_out == mean_state)
     return fail(CCQ_ERR_SHAPE, "%s: mean_state_out may not alias mean_state (every workgroup reads all of it)", who);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(workspace))
+  if ((!layer && (!aligned16(q) || !aligned16(k) || !aligned16(v))) || !aligned16(o) || !aligned16(workspace))
     return fail(CCQ_ERR_ALIGN, "%s: tensors must be 16-byte aligned", who);
   // the state slices move as 16-byte pieces of four columns (loads and stores)
   if (!aligned16(state) || !aligned16(cov_state) || !aligned16(state_out) || !aligned16(cov_state_out))
@@ -1201,7 +1235,7 @@ int decode_step(const char* who, bool gla, const void* q, const void* k, const v
                 const float* gate_w, const float* gate_b, const float* g, const float* beta, const float* gk,
                 float* state, float* cov_state, float* mean_state, int* position, void* o, void* workspace, int B,
                 int T, int H, int K, int V, int subtract_mean, int use_l2norm, int enable_ccq, float scale,
-                void* stream) {
+                void* stream, const DecodeLayer* layer = nullptr, long vld = 0) {
   if (!state || !position) return fail(CCQ_ERR_NULL, "%s: state and position are required", who);
   if (enable_ccq && (!cov_state || (subtract_mean && !mean_state)))
     return fail(CCQ_ERR_NULL, "%s: cov_state (and mean_state with subtract_mean) are required", who);
@@ -1214,8 +1248,12 @@ int decode_step(const char* who, bool gla, const void* q, const void* k, const v
   const bool mean = enable_ccq && subtract_mean;
   if (int s = decode_common(who, a, q, k, v, lambda, gate_w, gate_b, state, cov_state, mean ? mean_state : nullptr,
                             nullptr, o, state, cov_state, mean ? m_new : nullptr, workspace, B, T, H, K, V, B, 0,
-                            subtract_mean, use_l2norm, enable_ccq, scale))
+                            subtract_mean, use_l2norm, enable_ccq, scale, layer != nullptr))
     return s;
+  if (layer) {
+    a.lay = *layer;
+    a.vld = vld;
+  }
   a.pos_dev = position;
   a.pos_adv = position;
   if (mean) {
@@ -1244,6 +1282,32 @@ int ccq_gdn_decode_step(const void* q, const void* k, const void* v, const float
   return decode_step("ccq_gdn_decode_step", false, q, k, v, lambda, gate_w, gate_b, g, beta, nullptr, state,
                      cov_state, mean_state, position, o, workspace, B, T, H, K, V, subtract_mean, use_l2norm,
                      enable_ccq, scale, stream);
+}
+
+int ccq_gdn_layer_decode_step(const void* x, int64_t ldx, int off_q, int off_k, int off_v, const void* lam_w,
+                              const void* lam_b, const float* g, const float* beta, float* state, float* cov_state,
+                              float* mean_state, int* position, void* o, void* workspace, int B, int T, int H, int K,
+                              int V, int subtract_mean, int enable_ccq, float scale, float l2_eps, void* stream) {
+  const char* who = "ccq_gdn_layer_decode_step";
+  if (H * K > kDecodeLayerMaxQ) return fail(CCQ_ERR_SHAPE, "%s: H*K=%d above %d", who, H * K, kDecodeLayerMaxQ);
+  if (!x || !lam_w || !g || !beta) return fail(CCQ_ERR_NULL, "%s: x, lam_w, g and beta are required", who);
+  if (off_q < 0 || off_k < 0 || off_v < 0 || off_q + (int64_t)H * K > ldx || off_k + (int64_t)H * K > ldx ||
+      off_v + (int64_t)H * V > ldx)
+    return fail(CCQ_ERR_SHAPE, "%s: a column block lies outside the rows (ldx=%lld)", who, (long long)ldx);
+  // the backbone reads v as 8-byte pieces
+  if ((((uintptr_t)x + 2 * (uintptr_t)off_v) & 7) || (ldx & 3) || (V & 3))
+    return fail(CCQ_ERR_ALIGN, "%s: the v rows must be 8-byte aligned", who);
+  DecodeLayer lay{};
+  lay.x = x;
+  lay.ldx = (long)ldx;
+  lay.oq = off_q;
+  lay.ok = off_k;
+  lay.lw = lam_w;
+  lay.lb = lam_b;
+  lay.l2eps = l2_eps;
+  return decode_step(who, false, nullptr, nullptr, (const uint16_t*)x + off_v, nullptr, nullptr, nullptr, g, beta,
+                     nullptr, state, cov_state, mean_state, position, o, workspace, B, T, H, K, V, subtract_mean, 0,
+                     enable_ccq, scale, stream, &lay, (long)ldx);
 }
 
 int ccq_gla_decode_step(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,

@@ -92,7 +92,9 @@ __device__ __forceinline__ void store_cols(float* base, int ld, int rg, int c4, 
   for (int r = 0; r < K / RG; ++r) *(f32x4*)(base + (long)(rg * (K / RG) + r) * ld + c4) = x[r];
 }
 
-template <int K>
+// LAYER: q and k from the layer's projection rows (after the short convolutions), L2-normalised per
+// head here, and lambda from the whole q activation (ccq/gdn/layer.py:288-316)
+template <int K, bool LAYER>
 __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs a) {
   constexpr int RPT = K / RG;  // rows per thread
   static_assert(RPT >= 1, "K >= 32");
@@ -117,7 +119,32 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
 
   for (int t = 0; t < len; ++t) {
     const long tok = bos + t;
-    load_qk<K>(a, tok, h, sq, sk, red);
+    float lam_layer = 0.f;
+    if constexpr (LAYER) {
+      const DecodeLayer& L = a.lay;
+      const bf16* xr = (const bf16*)L.x + tok * L.ldx;
+      const bf16* lw = (const bf16*)L.lw + (long)h * a.H * K;
+      const int D = a.H * K;
+      float part = 0.f;  // the lambda gate's logit: this thread's channels of q
+#pragma unroll
+      for (int j = 0; j < kDecodeLayerMaxQ / kThreads; ++j) {
+        const int c = tid + j * kThreads;
+        if (c < D) part += (float)lw[c] * (float)xr[L.oq + c];
+      }
+      const float yq = tid < K ? (float)xr[L.oq + h * K + tid] : 0.f;
+      const float yk = tid < K ? (float)xr[L.ok + h * K + tid] : 0.f;
+      const float rq = rsqrtf(block_sum256(yq * yq, red) + L.l2eps);
+      const float rk = rsqrtf(block_sum256(yk * yk, red) + L.l2eps);
+      const float lg = (float)(bf16)(block_sum256(part, red) + (L.lb ? (float)((const bf16*)L.lb)[h] : 0.f));
+      lam_layer = (float)(bf16)(1.f / (1.f + expf(-lg)));
+      if (tid < K) {
+        sq[tid] = (float)(bf16)(yq * rq);
+        sk[tid] = (float)(bf16)(yk * rk);
+      }
+      __syncthreads();
+    } else {
+      load_qk<K>(a, tok, h, sq, sk, red);
+    }
     if (blockIdx.y == 0 && tid < K) a.kn[(tok * a.H + h) * K + tid] = sk[tid];
     if (!a.ccq) {
       if (blockIdx.y == 0 && tid < K) a.qc[(tok * a.H + h) * K + tid] = sq[tid];
@@ -126,7 +153,9 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
     }
     // lambda
     float lam;
-    if (a.gate_w) {
+    if (LAYER) {
+      lam = lam_layer;
+    } else if (a.gate_w) {
       const float x = tid < K ? a.gate_w[(long)h * K + tid] * sq[tid] : 0.f;
       lam = sigmoidf_(block_sum256(x, red) + a.gate_b[h]);
     } else {
@@ -205,7 +234,7 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
     const long vo = (tok * a.H + h) * V + v4;
     f32x4 vt, dv = f32x4{1.f, 1.f, 1.f, 1.f};
     {
-      const bf16x4 vb = *(const bf16x4*)((const bf16*)a.v + vo);
+      const bf16x4 vb = *(const bf16x4*)((const bf16*)a.v + (a.vld ? tok * a.vld + (long)h * V + v4 : vo));
 #pragma unroll
       for (int c = 0; c < 4; ++c) vt[c] = (float)vb[c];
       if (a.gv) {
@@ -247,7 +276,10 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
 template <int K>
 hipError_t launch_decode_k(const DecodeArgs& a, hipStream_t st) {
   const int units = a.N * a.H;
-  hipLaunchKernelGGL(decode_clean_kernel<K>, dim3(units, K / DC), dim3(kThreads), 0, st, a);
+  if (a.lay.x)
+    hipLaunchKernelGGL((decode_clean_kernel<K, true>), dim3(units, K / DC), dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((decode_clean_kernel<K, false>), dim3(units, K / DC), dim3(kThreads), 0, st, a);
   hipLaunchKernelGGL(decode_backbone_kernel<K>, dim3(units, a.V / DC), dim3(kThreads), 0, st, a);
   return hipGetLastError();
 }
@@ -321,13 +353,30 @@ __device__ __forceinline__ float ld_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Convolution epilogue (a CCQ-GDN layer's input projections in a decode step, ahead of its decode
+// kernels): the q, k and v column blocks leave as bf16(SiLU(short convolution)) of the projection,
+// rounded to bf16 first, over the sequence's last kConvW inputs (earlier tokens of the call from the
+// lanes holding their rows, older ones from the caches, which the call's last token advances), and
+// the a and b columns also give g = -exp(A_log) softplus(a + dt_bias) and beta = sigmoid(b) (x 2
+// with negative eigenvalues) -- the per-channel part of the decode prologue, with its roundings;
+// the per-head L2 normalisation and lambda, which need whole heads, are left to the decode kernels.
+constexpr int kConvW = 4;
+struct DlConv {
+  int oq, ok, ov, oa, ob;  // first columns of the q (Dq), k (Dq), v (Dv), a (H) and b (H) blocks
+  int Dq, Dv, H, T, neg_eig;
+  const void *wq, *wk, *wv, *bq, *bk, *bv;  // bf16 [D, kConvW] taps, [D] biases (nullable)
+  void *cq, *ck, *cv;                       // bf16 [B, D, kConvW - 1] caches
+  const void *alog, *dtb;                   // bf16 [H]
+  float *g, *beta;                          // fp32 [M, H]
+};
+
 // SPW: 32-wide steps per wave (every wave takes SPW; steps past its range read the range's last
 // step's address and contribute a zero x fragment, so the code has no branch around a load or an MFMA)
-template <int SPW, bool GLU, bool NORM>
+template <int SPW, bool GLU, bool NORM, bool CONV = false>
 __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, long ldx, const void* w_,
                                                                        const void* r_, long ldr, void* y_, long ldy,
                                                                        int M, int K, int N, const void* nw_,
-                                                                       float eps, const DlSplit sp) {
+                                                                       float eps, const DlSplit sp, const DlConv cv) {
   __shared__ f32x4 sAcc[GLU ? 2 : 1][kDlWaves][64];
   __shared__ float sSS[NORM ? kDlWaves : 1][16];
   const bf16* x = (const bf16*)x_;
@@ -386,9 +435,99 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
     acc = mfma16(wa[j], xf, acc);
     if constexpr (GLU) acu = mfma16(wb[j], xf, acu);
   }
+  // convolution epilogue: thread (row tid / 16, column tid % 16) of the first four waves takes one
+  // result; its column's taps, bias, its row's cache window and the gate constants are loaded after
+  // the products, while the other waves finish theirs
+  const int er = tid >> 4, ec = tid & 15;
+  int ekind = 0, ech = 0;  // column kind (0 none, 1 q, 2 k, 3 v, 4 a, 5 b) and channel / head
+  float cw[CONV ? kConvW : 1], cb = 0.f, cc[CONV ? kConvW - 1 : 1], ca = 0.f, cd = 0.f;
+  if constexpr (CONV) {
+    const int n = n0 + ec;
+    if (n >= cv.oq && n < cv.oq + cv.Dq) { ekind = 1; ech = n - cv.oq; }
+    else if (n >= cv.ok && n < cv.ok + cv.Dq) { ekind = 2; ech = n - cv.ok; }
+    else if (n >= cv.ov && n < cv.ov + cv.Dv) { ekind = 3; ech = n - cv.ov; }
+    else if (n >= cv.oa && n < cv.oa + cv.H) { ekind = 4; ech = n - cv.oa; }
+    else if (n >= cv.ob && n < cv.ob + cv.H) { ekind = 5; ech = n - cv.ob; }
+#pragma unroll
+    for (int j = 0; j < kConvW; ++j) cw[j] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kConvW - 1; ++j) cc[j] = 0.f;
+    if (tid < 256 && ekind >= 1 && ekind <= 3) {
+      const int k = ekind, c = ech, D = k == 3 ? cv.Dv : cv.Dq, b = min(er, M - 1) / cv.T;
+      const bf16* tw = (const bf16*)(k == 1 ? cv.wq : k == 2 ? cv.wk : cv.wv) + (long)c * kConvW;
+      const bf16* tb = (const bf16*)(k == 1 ? cv.bq : k == 2 ? cv.bk : cv.bv);
+      const bf16* tc = (const bf16*)(k == 1 ? cv.cq : k == 2 ? cv.ck : cv.cv) + ((long)b * D + c) * (kConvW - 1);
+#pragma unroll
+      for (int j = 0; j < kConvW; ++j) cw[j] = (float)tw[j];
+      if (tb) cb = (float)tb[c];
+#pragma unroll
+      for (int j = 0; j < kConvW - 1; ++j) cc[j] = (float)tc[j];
+    } else if (tid < 256 && ekind == 4) {
+      ca = (float)((const bf16*)cv.alog)[ech];
+      cd = (float)((const bf16*)cv.dtb)[ech];
+    }
+  }
   sAcc[0][wv][l] = acc;
   if constexpr (GLU) sAcc[GLU ? 1 : 0][wv][l] = acu;
   __syncthreads();
+  if constexpr (CONV) {
+    // wave 0: the tile's projection as bf16 values into LDS (row m, column n - n0), for every
+    // thread of the first four waves to read its window's earlier rows
+    __shared__ float sY[16][17];
+    if (wv == 0) {
+      f32x4 t4 = sAcc[0][0][l];
+#pragma unroll
+      for (int q = 1; q < kDlWaves; ++q) {
+        const f32x4 v = sAcc[0][q][l];
+        t4[0] += v[0]; t4[1] += v[1]; t4[2] += v[2]; t4[3] += v[3];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sY[l & 15][4 * (l >> 4) + i] = (float)(bf16)t4[i];
+    }
+    __syncthreads();
+    if (tid >= 256) return;
+    const int m = er, n = n0 + ec;
+    if (m >= M || n >= N) return;
+    const int b = m / cv.T, t = m - b * cv.T;
+    const float yr = sY[m][ec];
+    // input d tokens back (d <= t: row m - d of the tile; else cache slot kConvW - 1 + t - d)
+    auto input = [&](int d) {
+      float v = d == 0 ? yr : 0.f;
+#pragma unroll
+      for (int q = 0; q < kConvW - 1; ++q)
+        if (d > t && q == kConvW - 1 + t - d) v = cc[q];
+#pragma unroll
+      for (int e = 1; e < kConvW; ++e)
+        if (d == e && e <= t) v = sY[m - e][ec];
+      return v;
+    };
+    float out = yr;
+    if (ekind >= 1 && ekind <= 3) {
+      float acc2 = cb + cw[kConvW - 1] * yr;
+#pragma unroll
+      for (int j = 0; j < kConvW - 1; ++j) acc2 += cw[j] * input(kConvW - 1 - j);
+      out = (float)(bf16)(acc2 / (1.f + __expf(-acc2)));
+      if (t == cv.T - 1) {
+        // the call's last kConvW - 1 inputs into the cache
+        const int D = ekind == 3 ? cv.Dv : cv.Dq;
+        bf16* tc = (bf16*)(ekind == 1 ? cv.cq : ekind == 2 ? cv.ck : cv.cv) + ((long)b * D + ech) * (kConvW - 1);
+        float nwin[kConvW - 1];
+#pragma unroll
+        for (int q = 0; q < kConvW - 1; ++q) nwin[q] = input(kConvW - 2 - q);
+#pragma unroll
+        for (int q = 0; q < kConvW - 1; ++q) tc[q] = (bf16)nwin[q];
+      }
+    } else if (ekind == 4) {
+      const float xa = yr + cd;
+      cv.g[(long)m * cv.H + ech] = -expf(ca) * (xa > 20.f ? xa : log1pf(expf(xa)));
+    } else if (ekind == 5) {
+      float be = (float)(bf16)(1.f / (1.f + expf(-yr)));
+      if (cv.neg_eig) be *= 2.f;
+      cv.beta[(long)m * cv.H + ech] = be;
+    }
+    ((bf16*)y_)[(long)m * ldy + n] = (bf16)out;
+    return;
+  }
   if (wv != 0) return;
   f32x4 sum = sAcc[0][0][l];
 #pragma unroll
@@ -445,11 +584,19 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
 template <int SPW>
 static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const void* x, long ldx, const void* w,
                       const void* r, long ldr, void* y, long ldy, int M, int K, int N, const void* nw, float eps,
-                      const DlSplit& sp) {
+                      const DlSplit& sp, const DlConv* conv) {
+  const DlConv cv = conv ? *conv : DlConv{};
 #define CCQ_DL(G, NM)                                                                                        \
   hipLaunchKernelGGL((decode_linear_kernel<SPW, G, NM>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N, \
-                     nw, eps, sp)
-  if (glu) {
+                     nw, eps, sp, cv)
+  if (conv) {
+    if (nw)
+      hipLaunchKernelGGL((decode_linear_kernel<SPW, false, true, true>), grid, block, 0, st, x, ldx, w, r, ldr, y,
+                         ldy, M, K, N, nw, eps, sp, cv);
+    else
+      hipLaunchKernelGGL((decode_linear_kernel<SPW, false, false, true>), grid, block, 0, st, x, ldx, w, r, ldr, y,
+                         ldy, M, K, N, nw, eps, sp, cv);
+  } else if (glu) {
     if (nw) CCQ_DL(true, true); else CCQ_DL(true, false);
   } else {
     if (nw) CCQ_DL(false, true); else CCQ_DL(false, false);
@@ -465,7 +612,7 @@ size_t decode_linear_split_bytes(int N, int splits) {
 
 hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
                                 long ldy, int M, int K, int N, const void* nw, float eps, int splits, void* ws,
-                                hipStream_t st) {
+                                const DlConv* conv, hipStream_t st) {
   if (M <= 0 || N <= 0) return hipSuccess;
   const int blocks = (N + 15) / 16, steps = K / 32;
   DlSplit sp{1, steps, nullptr, nullptr};
@@ -478,17 +625,26 @@ hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w
   const dim3 grid((unsigned)blocks, (unsigned)sp.S), block(kDlWaves * 64);
   const int spw = (sp.sps + kDlWaves - 1) / kDlWaves;
   switch (spw) {
-    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
-    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
-    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
-    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
-    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
-    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
-    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
-    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp); break;
+    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
+    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
+    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
+    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
+    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
+    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
+    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
+    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_decode_in_proj(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N,
+                                 const void* nw, float eps, int oq, int ok, int ov, int oa, int ob, int Dq, int Dv,
+                                 int H, int T, int neg_eig, const void* wq, const void* wk, const void* wv,
+                                 const void* bq, const void* bk, const void* bv, void* cq, void* ck, void* cv,
+                                 const void* alog, const void* dtb, float* g, float* beta, hipStream_t st) {
+  DlConv c{oq, ok, ov, oa, ob, Dq, Dv, H, T, neg_eig, wq, wk, wv, bq, bk, bv, cq, ck, cv, alog, dtb, g, beta};
+  return launch_decode_linear(false, x, ldx, w, nullptr, 0, y, ldy, M, K, N, nw, eps, 1, nullptr, &c, st);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st) {

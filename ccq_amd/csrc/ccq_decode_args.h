@@ -11,6 +11,19 @@ namespace ccq {
 // cleaned query and key of the call's tokens, 8 bytes per token, head and key channel).
 constexpr size_t kDecodeScratchBytes = (size_t)8 << 20;
 constexpr int kMaxDevices = 64;
+constexpr int kDecodeLayerMaxQ = 2048;  // H K of the layer form
+
+// The layer form (ccq_gdn_layer_decode_step): q and k read from the layer's projection rows, after
+// the short convolutions and SiLU that the projection kernel's epilogue applied, and L2-normalised
+// here; lambda = sigmoid(lambda gate of the whole q activation).
+struct DecodeLayer {
+  const void* x;           // bf16 rows [B T, ldx]: q (H K) at column oq, k (H K) at ok
+  long ldx;
+  int oq, ok;
+  const void* lw;          // bf16 [H, H K] lambda gate weight, [H] bias (nullable)
+  const void* lb;
+  float l2eps;
+};
 
 struct DecodeArgs {
   const void* q;           // bf16 [tokens, H, K]
@@ -42,6 +55,8 @@ struct DecodeArgs {
   float scale;
   int T, H, N, K, V, pos_off, subtract_mean, l2norm, ccq, gla;
   int reverse;             // GLA: the backbone recurrence runs from the last token to the first
+  long vld;                // elements between the v rows of consecutive tokens (0: H V)
+  DecodeLayer lay;         // the layer form (lay.x set)
 };
 
 }  // namespace ccq

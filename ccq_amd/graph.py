@@ -325,6 +325,9 @@ class GDNLayerDecode:
         # the projections as decode_linear launches when the step has at most 16 token rows
         self.fast = B * T <= 16 and decode_linear_ok(torch.empty(B * T, L.hidden_size, device=dev,
                                                                  dtype=torch.bfloat16), self.w_in)
+        # the short convolutions in the input projections' epilogue (width 4) and the decode step over
+        # their rows where its limits allow (H K <= 2048)
+        self.conv_in_proj = self.W == 4 and self.H * self.K <= 2048
         # the output projection (N = hidden, about 1024: few column blocks) with its contraction split
         self.o_splits = split_plan(dv, L.o_proj.weight.shape[0])
         self.o_ws = split_workspace(L.o_proj.weight.shape[0], self.o_splits, dev) if self.o_splits > 1 else None
@@ -359,24 +362,41 @@ class GDNLayerDecode:
         B, T, H, K, V = self.B, self.T, self.H, self.K, self.V
         if h.shape[:2] != (B, T) or h.dtype != torch.bfloat16:
             raise ValueError(f"expected bf16 input [{B}, {T}, hidden] (got {tuple(h.shape)} {h.dtype})")
-        if self.fast:
-            # (with norm: the block's RMSNorm of h folded into the input projection)
-            x = decode_linear(h, self.w_in, norm_weight=None if norm is None else norm.weight,
-                              norm_eps=1e-5 if norm is None else norm.eps)
-        else:
-            x = F.linear(h if norm is None else norm(h), self.w_in)
         o_q, o_k, o_v, o_g, o_a, o_b = self.offsets
         cw = [c.weight for c in (L.q_conv1d, L.k_conv1d, L.v_conv1d)]
         cb = [c.bias for c in (L.q_conv1d, L.k_conv1d, L.v_conv1d)]
+        nw, neps = (None, 1e-5) if norm is None else (norm.weight, norm.eps)
+        if self.fast and self.conv_in_proj:
+            # the input projections with the short convolutions, g and beta in their epilogue
+            # (ccq_gdn_decode_in_proj), then the decode step over those rows, which normalises q and k
+            # and forms lambda (ccq_gdn_layer_decode_step): three launches fewer than the prologue path
+            x = torch.empty(B, T, self.width, device=h.device, dtype=torch.bfloat16)
+            h2 = _rows(h)
+            call("ccq_gdn_decode_in_proj", ptr(h2), h2.stride(0), ptr(self.w_in), ptr(x), self.width, B * T,
+                 L.hidden_size, self.width, ptr(_norm_arg(h, nw)), float(neps), o_q, o_k, o_v, o_a, o_b, H, H * K,
+                 H * V, T, ptr(cw[0]), ptr(cw[1]), ptr(cw[2]), ptr(cb[0]), ptr(cb[1]), ptr(cb[2]),
+                 ptr(self.conv[0]), ptr(self.conv[1]), ptr(self.conv[2]), ptr(L.A_log), ptr(L.dt_bias), ptr(st.g),
+                 ptr(st.beta), int(L.allow_neg_eigval), _lib.stream_of(h))
+            call("ccq_gdn_layer_decode_step", ptr(x), self.width, o_q, o_k, o_v, ptr(L.erase_lambda_proj.weight),
+                 ptr(L.erase_lambda_proj.bias), ptr(st.g), ptr(st.beta), ptr(st.S), ptr(st.C), ptr(st.m),
+                 ptr(st.position), ptr(st.o), ptr(st.workspace), B, T, H, K, V, int(st.subtract_mean),
+                 int(st.enable_ccq), st.scale, 1e-6, _lib.stream_of(x))
+        else:
+            if self.fast:
+                # (with norm: the block's RMSNorm of h folded into the input projection)
+                x = decode_linear(h, self.w_in, norm_weight=nw, norm_eps=neps)
+            else:
+                x = F.linear(h if norm is None else norm(h), self.w_in)
+            call("ccq_gdn_decode_prologue", x.data_ptr() + 2 * o_q, x.data_ptr() + 2 * o_k, x.data_ptr() + 2 * o_v,
+                 x.data_ptr() + 2 * o_a, x.data_ptr() + 2 * o_b, self.width,
+                 ptr(cw[0]), ptr(cw[1]), ptr(cw[2]), ptr(cb[0]), ptr(cb[1]), ptr(cb[2]),
+                 ptr(self.conv[0]), ptr(self.conv[1]), ptr(self.conv[2]),
+                 ptr(L.erase_lambda_proj.weight), ptr(L.erase_lambda_proj.bias), ptr(L.A_log), ptr(L.dt_bias),
+                 ptr(st.q), ptr(st.k), ptr(st.v), ptr(st.lam), ptr(st.g), ptr(st.beta),
+                 B, T, H, K, V, self.W, int(L.allow_neg_eigval), 1e-6, _lib.stream_of(x))
+            st.launch()
         base = x.data_ptr()
         at = lambda off: base + 2 * off  # noqa: E731  (bf16 elements)
-        call("ccq_gdn_decode_prologue", at(o_q), at(o_k), at(o_v), at(o_a), at(o_b), self.width,
-             ptr(cw[0]), ptr(cw[1]), ptr(cw[2]), ptr(cb[0]), ptr(cb[1]), ptr(cb[2]),
-             ptr(self.conv[0]), ptr(self.conv[1]), ptr(self.conv[2]),
-             ptr(L.erase_lambda_proj.weight), ptr(L.erase_lambda_proj.bias), ptr(L.A_log), ptr(L.dt_bias),
-             ptr(st.q), ptr(st.k), ptr(st.v), ptr(st.lam), ptr(st.g), ptr(st.beta),
-             B, T, H, K, V, self.W, int(L.allow_neg_eigval), 1e-6, _lib.stream_of(x))
-        st.launch()
         if L.use_gate:
             # the gated RMSNorm kernel reading the gate rows in place from the projection output (H rows
             # of V per token, the projection's row width apart), with the weight converted in refresh()

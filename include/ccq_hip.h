@@ -320,6 +320,37 @@ int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, cons
                             const void* lam_b, const void* A_log, const void* dt_bias, void* q, void* k, void* v,
                             float* lam, float* g, float* beta, int B, int T, int H, int K, int V, int W,
                             int allow_neg_eigval, float eps, void* stream);
+/*
+ * A CCQ-GDN layer's input projections for a decode step with the per-channel part of its decode
+ * prologue in the epilogue (ccq_decode_linear's projection and optional folded RMSNorm, then): the
+ * q, k and v column blocks (at off_q, off_k: Dq columns; off_v: Dv) leave as
+ * bf16(SiLU(short convolution)) over each sequence's last 4 inputs (bf16 projection values; earlier
+ * tokens of the call from their rows, older ones from the caches cq, ck, cv bf16 [B, D, 3], which
+ * the call's last token advances), and the a and b columns (off_a, off_b: H each) also give
+ * g = -exp(A_log) softplus(a + dt_bias) and beta = sigmoid(b) (x 2 with allow_neg_eigval) in fp32
+ * [M, H] -- the roundings of ccq_gdn_decode_prologue, whose per-head L2 normalisation and lambda
+ * gate ccq_gdn_layer_decode_step then applies.  Other columns (the output gate) are the projection.
+ * M = B T rows (T tokens per sequence, M <= 16); convolution width 4 (taps bf16 [D, 4], biases
+ * [D] nullable).  Follows ccq/gdn/layer.py:266-316 with ccq_gdn_decode_prologue.
+ */
+int ccq_gdn_decode_in_proj(const void* x, int64_t ldx, const void* weight, void* y, int64_t ldy, int M, int K, int N,
+                           const void* norm_weight, float norm_eps, int off_q, int off_k, int off_v, int off_a,
+                           int off_b, int H, int Dq, int Dv, int T, const void* wq, const void* wk, const void* wv,
+                           const void* bq, const void* bk, const void* bv, void* cq, void* ck, void* cv,
+                           const void* A_log, const void* dt_bias, float* g, float* beta, int allow_neg_eigval,
+                           void* stream);
+/*
+ * ccq_gdn_decode_step over the rows ccq_gdn_decode_in_proj leaves: q and k (H K each, at off_q /
+ * off_k of each token's row of x, row stride ldx) are L2-normalised per head here (l2_eps) and
+ * lambda = sigmoid(lam_w q + lam_b) over the whole q activation (lam_w bf16 [H, H K], lam_b [H]
+ * nullable), v is read in place (off_v), g and beta as given (fp32 [B T, H]).  States, position,
+ * workspace (ccq_decode_step_workspace_bytes) and the output o bf16 [B, T, H, V] as
+ * ccq_gdn_decode_step.  H K <= 2048.  Two kernels, no allocation.
+ */
+int ccq_gdn_layer_decode_step(const void* x, int64_t ldx, int off_q, int off_k, int off_v, const void* lam_w,
+                              const void* lam_b, const float* g, const float* beta, float* state, float* cov_state,
+                              float* mean_state, int* position, void* o, void* workspace, int B, int T, int H, int K,
+                              int V, int subtract_mean, int enable_ccq, float scale, float l2_eps, void* stream);
 int ccq_gdn_decode_step(const void* q, const void* k, const void* v, const float* lambda, const float* gate_w,
                         const float* gate_b, const float* g, const float* beta, float* state, float* cov_state,
                         float* mean_state, int* position, void* o, void* workspace, int B, int T, int H, int K, int V,

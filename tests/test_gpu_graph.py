@@ -202,3 +202,48 @@ def test_layer_decode_matches_recurrent_mode(H, K, expand_v, T0):
             assert errs["o"] <= 2e-3 and errs["conv"] <= 1e-3
             assert errs["S"] <= 1e-5 and errs["C"] <= 1e-5
             assert int(ld.step.position.item()) == t + 1
+
+
+@pytest.mark.parametrize("H,K,expand_v,T", [(4, 256, 2, 1), (2, 128, 1, 2), (2, 64, 2, 3)])
+def test_layer_decode_in_proj_path_matches_prologue_path(H, K, expand_v, T):
+    """GDNLayerDecode's two paths on the same inputs: the short convolutions, g and beta in the input
+    projections' epilogue with the decode step normalising q and k and forming lambda
+    (``ccq_gdn_decode_in_proj`` + ``ccq_gdn_layer_decode_step``), against the input projections, the
+    decode prologue kernel and the decode step.  Outputs within a bf16 unit on rare elements (the
+    per-head sums of squares and the lambda logit run in another order), states to fp32 roundings,
+    convolution caches and position equal; T tokens per call."""
+    dev = _cuda()
+    import copy
+
+    from ccq_amd import CCQGDN, LayerCache
+    from ccq_amd.graph import GDNLayerDecode
+    from tests._util import rel
+    B, T0, steps = 3, 37, 3
+    print(f"test_layer_decode_in_proj_path_matches_prologue_path H={H} K={K} expand_v={expand_v} T={T}", flush=True)
+    torch.manual_seed(0)
+    layer = CCQGDN(hidden_size=256, head_dim=K, num_heads=H, expand_v=expand_v, mode="chunk", layer_idx=0)
+    layer = layer.to(dev, torch.bfloat16).eval()
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(B, T0 + steps * T, 256, generator=gen).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        cache = LayerCache()
+        layer(x[:, :T0], past_key_values=cache, use_cache=True)
+        fused, plain = GDNLayerDecode(layer, B, T), GDNLayerDecode(layer, B, T)
+        assert fused.conv_in_proj and fused.fast
+        plain.conv_in_proj = False
+        for ld in (fused, plain):
+            ld.load(copy.deepcopy(cache).get(0))
+        for s in range(steps):
+            h = x[:, T0 + s * T:T0 + (s + 1) * T]
+            o_f, o_p = fused(h), plain(h)
+            torch.cuda.synchronize()
+            errs = {"o": rel(o_f, o_p), "S": rel(fused.step.S, plain.step.S), "C": rel(fused.step.C, plain.step.C),
+                    "m": rel(fused.step.m, plain.step.m)}
+            print(s, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+            assert errs["o"] <= 1e-3
+            for n in ("S", "C", "m"):
+                assert errs[n] <= 1e-5, n
+            for a, b in zip(fused.conv, plain.conv):
+                assert torch.equal(a, b), "convolution cache"
+            assert torch.equal(fused.step.g, plain.step.g) and torch.equal(fused.step.beta, plain.step.beta)
+            assert int(fused.step.position.item()) == int(plain.step.position.item()) == T0 + (s + 1) * T
