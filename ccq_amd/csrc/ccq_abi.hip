@@ -32,9 +32,13 @@ hipError_t launch_fill_zero(float* out, long n, hipStream_t st);
 hipError_t launch_gla_stage(int stage, const GlaArgs& a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st);
 struct DlConv;
+struct DlGate;
 hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
                                 long ldy, int M, int K, int N, const void* nw, float eps, int splits, void* ws,
-                                const DlConv* conv, hipStream_t st);
+                                const DlConv* conv, hipStream_t st, const DlGate* gate);
+hipError_t launch_decode_linear_gnorm(const void* x, long ldx, const void* g, long ldg, const float* gw, int dv,
+                                      float geps, const void* w, const void* r, long ldr, void* y, long ldy, int M,
+                                      int K, int N, void* ws, hipStream_t st);
 hipError_t launch_decode_in_proj(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N,
                                  const void* nw, float eps, int oq, int ok, int ov, int oa, int ob, int Dq, int Dv,
                                  int H, int T, int neg_eig, const void* wq, const void* wk, const void* wv,
@@ -845,7 +849,28 @@ static int decode_linear_entry(const char* who, bool glu, const void* x, int64_t
   if (!aligned16(x) || !aligned16(weight) || !aligned16(norm_weight))
     return fail(CCQ_ERR_ALIGN, "%s: x, the weight and the norm weight must be 16-byte aligned", who);
   return hip_status(launch_decode_linear(glu, x, ldx, weight, residual, ldr, y, ldy, M, K, N, norm_weight, norm_eps,
-                                         splits, workspace, nullptr, (hipStream_t)stream),
+                                         splits, workspace, nullptr, (hipStream_t)stream, nullptr),
+                    who);
+}
+
+int ccq_decode_linear_gnorm(const void* x, int64_t ldx, const void* gate, int64_t ldg, const float* norm_weight,
+                            int dv, float norm_eps, const void* weight, const void* residual, int64_t ldr, void* y,
+                            int64_t ldy, int M, int K, int N, void* workspace, void* stream) {
+  const char* who = "ccq_decode_linear_gnorm";
+  if (dv < 32 || dv % 32 || K % dv || K / dv > 8)
+    return fail(CCQ_ERR_SHAPE, "%s: head width dv=%d must be a multiple of 32 dividing K=%d into at most 8 heads", who,
+                dv, K);
+  if (M < 0 || M > 16 || N < 0 || K < 32 || K > 4096 || ldx < K || ldx % 8 || ldy < N || (residual && ldr < N))
+    return fail(CCQ_ERR_SHAPE, "%s: M=%d K=%d N=%d ldx=%lld ldy=%lld (need M <= 16, K <= 4096, ldx >= K a multiple "
+                "of 8, ldy >= N, ldr >= N)", who, M, K, N, (long long)ldx, (long long)ldy);
+  if (!x || !gate || !weight || !y) return fail(CCQ_ERR_NULL, "%s: x, gate, weight, y are required", who);
+  if (K / dv > 1 && !workspace) return fail(CCQ_ERR_NULL, "%s: more than one head needs the workspace", who);
+  if (ldg < K || ldg % 8 || !aligned16(x) || !aligned16(gate) || !aligned16(weight) || !aligned16(norm_weight) ||
+      !aligned16(workspace))
+    return fail(CCQ_ERR_ALIGN, "%s: x, gate (row stride ldg >= K, a multiple of 8), the weights and the workspace "
+                "must be 16-byte aligned", who);
+  return hip_status(launch_decode_linear_gnorm(x, ldx, gate, ldg, norm_weight, dv, norm_eps, weight, residual, ldr, y,
+                                               ldy, M, K, N, workspace, (hipStream_t)stream),
                     who);
 }
 

@@ -370,15 +370,28 @@ struct DlConv {
   float *g, *beta;                          // fp32 [M, H]
 };
 
+// Gated-norm form (a layer's gated output norm folded into its output projection, the contraction
+// split so that each workgroup's steps are exactly one head of dv columns): each operand element
+// enters as bf16(x r w[k mod dv] silu(g)) with r = 1 / sqrt(mean of x^2 over the head + eps) from the
+// workgroup's own fragments, and the gate g read in place (row stride ldg) -- the arithmetic of the
+// gated RMSNorm kernel.
+struct DlGate {
+  const void* g;   // bf16 gate rows
+  long ldg;
+  const float* w;  // fp32 [dv] (nullable: ones)
+  int dv;
+};
+
 // SPW: 32-wide steps per wave (every wave takes SPW; steps past its range read the range's last
 // step's address and contribute a zero x fragment, so the code has no branch around a load or an MFMA)
-template <int SPW, bool GLU, bool NORM, bool CONV = false>
+template <int SPW, bool GLU, bool NORM, bool CONV = false, bool GN = false>
 __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, long ldx, const void* w_,
                                                                        const void* r_, long ldr, void* y_, long ldy,
                                                                        int M, int K, int N, const void* nw_,
-                                                                       float eps, const DlSplit sp, const DlConv cv) {
+                                                                       float eps, const DlSplit sp, const DlConv cv,
+                                                                       const DlGate gt) {
   __shared__ f32x4 sAcc[GLU ? 2 : 1][kDlWaves][64];
-  __shared__ float sSS[NORM ? kDlWaves : 1][16];
+  __shared__ float sSS[NORM || GN ? kDlWaves : 1][16];
   const bf16* x = (const bf16*)x_;
   const bf16* w = (const bf16*)w_;
   const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
@@ -390,8 +403,10 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   const bf16* wu = w + (long)(GLU ? N + nw : nw) * K + 8 * (l >> 4);  // the up half's row (gated form)
   const bf16* xr = x + (long)mx * ldx + 8 * (l >> 4);
   // every load of the wave is issued before the first use
-  bf16x8 wa[SPW], wb[GLU ? SPW : 1], xb[SPW], gw[NORM ? SPW : 1];
+  bf16x8 wa[SPW], wb[GLU ? SPW : 1], xb[SPW], gw[NORM || GN ? SPW : 1];
+  f32x4 gn0[GN ? SPW : 1], gn1[GN ? SPW : 1];  // gated-norm form: the norm weight of the step's columns
   const bf16* nr = (const bf16*)(NORM ? nw_ : w_) + 8 * (l >> 4);
+  const bf16* gr = GN ? (const bf16*)gt.g + (long)mx * gt.ldg + 8 * (l >> 4) : x;
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
     const int st = min(s0 + wv + kDlWaves * j, steps - 1);
@@ -399,9 +414,19 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
     if constexpr (GLU) wb[j] = *gmem((const bf16x8*)(wu + 32 * st));
     xb[j] = *gmem((const bf16x8*)(xr + 32 * st));
     if constexpr (NORM) gw[j] = *gmem((const bf16x8*)(nr + 32 * st));
+    if constexpr (GN) {
+      gw[j] = *gmem((const bf16x8*)(gr + 32 * st));  // the gate
+      const int kh = 32 * (st - s0) + 8 * (l >> 4);  // column within the head
+      if (gt.w) {
+        gn0[j] = *gmem((const f32x4*)(gt.w + kh));
+        gn1[j] = *gmem((const f32x4*)(gt.w + kh + 4));
+      } else {
+        gn0[j] = gn1[j] = f32x4{1.f, 1.f, 1.f, 1.f};
+      }
+    }
   }
   float rs = 1.f;
-  if constexpr (NORM) {
+  if constexpr (NORM || GN) {
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -419,7 +444,7 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
     float tot = 0.f;
 #pragma unroll
     for (int q = 0; q < kDlWaves; ++q) tot += sSS[q][l & 15];
-    rs = rsqrtf(tot / (float)K + eps);
+    rs = rsqrtf(tot / (float)(GN ? gt.dv : K) + eps);
   }
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, acu = acc;
 #pragma unroll
@@ -430,6 +455,10 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
     for (int i = 0; i < 8; ++i) {
       bf16 v = xb[j][i];
       if constexpr (NORM) v = (bf16)((float)v * rs * (float)gw[j][i]);
+      if constexpr (GN) {
+        const float g = (float)gw[j][i], wn = i < 4 ? gn0[j][i] : gn1[j][i - 4];
+        v = (bf16)((float)v * rs * wn * (g / (1.f + __expf(-g))));
+      }
       xf[i] = live ? v : (bf16)0.f;
     }
     acc = mfma16(wa[j], xf, acc);
@@ -584,18 +613,22 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
 template <int SPW>
 static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const void* x, long ldx, const void* w,
                       const void* r, long ldr, void* y, long ldy, int M, int K, int N, const void* nw, float eps,
-                      const DlSplit& sp, const DlConv* conv) {
+                      const DlSplit& sp, const DlConv* conv, const DlGate* gate) {
   const DlConv cv = conv ? *conv : DlConv{};
+  const DlGate gt = gate ? *gate : DlGate{};
 #define CCQ_DL(G, NM)                                                                                        \
   hipLaunchKernelGGL((decode_linear_kernel<SPW, G, NM>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N, \
-                     nw, eps, sp, cv)
-  if (conv) {
+                     nw, eps, sp, cv, gt)
+  if (gate) {
+    hipLaunchKernelGGL((decode_linear_kernel<SPW, false, false, false, true>), grid, block, 0, st, x, ldx, w, r, ldr,
+                       y, ldy, M, K, N, nw, eps, sp, cv, gt);
+  } else if (conv) {
     if (nw)
       hipLaunchKernelGGL((decode_linear_kernel<SPW, false, true, true>), grid, block, 0, st, x, ldx, w, r, ldr, y,
-                         ldy, M, K, N, nw, eps, sp, cv);
+                         ldy, M, K, N, nw, eps, sp, cv, gt);
     else
       hipLaunchKernelGGL((decode_linear_kernel<SPW, false, false, true>), grid, block, 0, st, x, ldx, w, r, ldr, y,
-                         ldy, M, K, N, nw, eps, sp, cv);
+                         ldy, M, K, N, nw, eps, sp, cv, gt);
   } else if (glu) {
     if (nw) CCQ_DL(true, true); else CCQ_DL(true, false);
   } else {
@@ -612,7 +645,7 @@ size_t decode_linear_split_bytes(int N, int splits) {
 
 hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w, const void* r, long ldr, void* y,
                                 long ldy, int M, int K, int N, const void* nw, float eps, int splits, void* ws,
-                                const DlConv* conv, hipStream_t st) {
+                                const DlConv* conv, hipStream_t st, const DlGate* gate) {
   if (M <= 0 || N <= 0) return hipSuccess;
   const int blocks = (N + 15) / 16, steps = K / 32;
   DlSplit sp{1, steps, nullptr, nullptr};
@@ -625,14 +658,14 @@ hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w
   const dim3 grid((unsigned)blocks, (unsigned)sp.S), block(kDlWaves * 64);
   const int spw = (sp.sps + kDlWaves - 1) / kDlWaves;
   switch (spw) {
-    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
-    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
-    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
-    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
-    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
-    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
-    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
-    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv); break;
+    case 1: launch_dl<1>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv, gate); break;
+    case 2: launch_dl<2>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv, gate); break;
+    case 3: launch_dl<3>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv, gate); break;
+    case 4: launch_dl<4>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv, gate); break;
+    case 5: launch_dl<5>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv, gate); break;
+    case 6: launch_dl<6>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv, gate); break;
+    case 7: launch_dl<7>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv, gate); break;
+    case 8: launch_dl<8>(glu, grid, block, st, x, ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, conv, gate); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -644,7 +677,16 @@ hipError_t launch_decode_in_proj(const void* x, long ldx, const void* w, void* y
                                  const void* bq, const void* bk, const void* bv, void* cq, void* ck, void* cv,
                                  const void* alog, const void* dtb, float* g, float* beta, hipStream_t st) {
   DlConv c{oq, ok, ov, oa, ob, Dq, Dv, H, T, neg_eig, wq, wk, wv, bq, bk, bv, cq, ck, cv, alog, dtb, g, beta};
-  return launch_decode_linear(false, x, ldx, w, nullptr, 0, y, ldy, M, K, N, nw, eps, 1, nullptr, &c, st);
+  return launch_decode_linear(false, x, ldx, w, nullptr, 0, y, ldy, M, K, N, nw, eps, 1, nullptr, &c, st, nullptr);
+}
+
+// The output projection with the gated output norm folded in: the contraction split per head (K / dv
+// workgroups per column block, one head each).
+hipError_t launch_decode_linear_gnorm(const void* x, long ldx, const void* g, long ldg, const float* gw, int dv,
+                                      float geps, const void* w, const void* r, long ldr, void* y, long ldy, int M,
+                                      int K, int N, void* ws, hipStream_t st) {
+  const DlGate gt{g, ldg, gw, dv};
+  return launch_decode_linear(false, x, ldx, w, r, ldr, y, ldy, M, K, N, nullptr, geps, K / dv, ws, nullptr, st, &gt);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st) {

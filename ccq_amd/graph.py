@@ -128,6 +128,37 @@ def decode_linear_split(x: torch.Tensor, weight: torch.Tensor, residual: Optiona
     return y
 
 
+def decode_linear_gnorm(x: torch.Tensor, gate: torch.Tensor, norm_weight: Optional[torch.Tensor], dv: int,
+                        norm_eps: float, weight: torch.Tensor, residual: Optional[torch.Tensor],
+                        workspace: Optional[torch.Tensor]) -> torch.Tensor:
+    """A gated-norm layer's output projection with the norm folded in (``ccq_decode_linear_gnorm``):
+    ``linear(bf16(x r w silu(gate)), weight) (+ residual)``, ``r`` the reciprocal RMS of each
+    ``dv``-wide head of ``x``, the contraction split per head.  ``gate`` a [rows, K] bf16 view (rows
+    may be strided, e.g. columns of the input projections' output); ``norm_weight`` fp32 [dv] or
+    None; ``workspace`` from ``split_workspace(N, K // dv)`` (None for one head)."""
+    K = x.shape[-1]
+    if not decode_linear_ok(x, weight) or dv % 32 or K % dv or K // dv > 8:
+        raise ValueError(f"decode_linear_gnorm: x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)}, dv={dv}: "
+                         f"needs bf16 on the GPU, <= 16 rows, K a multiple of 32 in [32, 4096] and dv a multiple "
+                         f"of 32 dividing K into at most 8 heads")
+    x2 = _rows(x)
+    M, N = x2.shape[0], weight.shape[0]
+    if gate.dtype != torch.bfloat16 or gate.shape != (M, K) or gate.stride(1) != 1:
+        raise ValueError(f"gate {tuple(gate.shape)} {gate.dtype}: expected a bf16 [{M}, {K}] view, unit column stride")
+    if norm_weight is not None and (norm_weight.shape != (dv,) or norm_weight.dtype != torch.float32):
+        raise ValueError(f"norm_weight {tuple(norm_weight.shape)} {norm_weight.dtype}: expected fp32 [{dv}]")
+    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.bfloat16)
+    r2 = None
+    if residual is not None:
+        if residual.shape != y.shape:
+            raise ValueError(f"residual {tuple(residual.shape)}: expected {tuple(y.shape)}")
+        r2 = _rows(residual)
+    call("ccq_decode_linear_gnorm", ptr(x2), x2.stride(0), ptr(gate), gate.stride(0), ptr(norm_weight), dv,
+         float(norm_eps), ptr(weight), ptr(r2), 0 if r2 is None else r2.stride(0), ptr(y), N, M, K, N,
+         ptr(workspace), _lib.stream_of(x))
+    return y
+
+
 def decode_linear_glu(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
                       norm_eps: float = 1e-5) -> torch.Tensor:
     """A gated MLP's up projection for a decode step: ``silu(gate) * up`` with
@@ -330,6 +361,10 @@ class GDNLayerDecode:
         self.conv_in_proj = self.W == 4 and self.H * self.K <= 2048
         # the output projection (N = hidden, about 1024: few column blocks) with its contraction split
         self.o_splits = split_plan(dv, L.o_proj.weight.shape[0])
+        # the gated output norm folded into the output projection (split per head) where its limits allow
+        self.gnorm_in_proj = L.use_gate and self.V % 32 == 0 and self.H <= 8 and self.conv_in_proj
+        if self.gnorm_in_proj:
+            self.o_splits = self.H
         self.o_ws = split_workspace(L.o_proj.weight.shape[0], self.o_splits, dev) if self.o_splits > 1 else None
 
     def refresh(self) -> None:
@@ -397,6 +432,11 @@ class GDNLayerDecode:
             st.launch()
         base = x.data_ptr()
         at = lambda off: base + 2 * off  # noqa: E731  (bf16 elements)
+        if self.fast and self.gnorm_in_proj and decode_linear_ok(st.o.view(B, T, H * V), L.o_proj.weight):
+            # the gated output norm folded into the output projection, the gate rows read in place
+            gate = x.view(B * T, self.width)[:, o_g:o_g + H * V]
+            return decode_linear_gnorm(st.o.view(B, T, H * V), gate, self.norm_w, V, float(L.o_norm.eps),
+                                       L.o_proj.weight, residual, self.o_ws)
         if L.use_gate:
             # the gated RMSNorm kernel reading the gate rows in place from the projection output (H rows
             # of V per token, the projection's row width apart), with the weight converted in refresh()

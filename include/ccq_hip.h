@@ -294,6 +294,23 @@ int ccq_decode_linear_glu(const void* x, int64_t ldx, const void* weight, void* 
  * call (its counters; every call leaves them zero); calls that overlap on one workspace race.
  * No counterpart in the reference (its projections are nn.Linear: ccq/gdn/layer.py:408).
  */
+/*
+ * The output projection of a gated-norm layer with the norm folded in: y = (gnorm(x, gate) W^T)
+ * (+ residual), gnorm(x, g) = bf16(x r norm_weight[k mod dv] silu(g)) per head of dv columns with
+ * r = 1 / sqrt(mean over the head of x^2 + norm_eps) -- the arithmetic of
+ * ccq_gated_rmsnorm_fwd_strided, so that this equals that norm followed by ccq_decode_linear_split
+ * (up to the order of the head's sum of squares, which can move a rare normed element by one bf16
+ * unit), without the norm's launch and the normed rows' round trip.  The contraction is split per
+ * head (K / dv workgroups per 16 output columns, each forming its head's sum from its own operands);
+ * workspace: ccq_decode_linear_split_workspace_bytes(N, K / dv) bytes as for
+ * ccq_decode_linear_split (zero before the first call, left zero; not needed for one head).
+ * gate: bf16 rows (row stride ldg >= K, a multiple of 8) in x's head layout; norm_weight fp32 [dv]
+ * (nullable: ones); dv a multiple of 32, K / dv <= 8.  Follows FusedRMSNormGated + o_proj
+ * (ccq/gdn/layer.py:402-408).
+ */
+int ccq_decode_linear_gnorm(const void* x, int64_t ldx, const void* gate, int64_t ldg, const float* norm_weight,
+                            int dv, float norm_eps, const void* weight, const void* residual, int64_t ldr, void* y,
+                            int64_t ldy, int M, int K, int N, void* workspace, void* stream);
 size_t ccq_decode_linear_split_workspace_bytes(int N, int splits);
 int ccq_decode_linear_split(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
                             int64_t ldy, int M, int K, int N, int splits, void* workspace, void* stream);

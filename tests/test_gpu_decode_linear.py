@@ -155,3 +155,45 @@ def test_decode_linear_split(M, K, N, splits):
         assert y.shape == (M, N) and e <= 5e-4 and e1 <= 5e-4
         blocks = (N + 15) // 16
         assert int(ws[:4 * blocks].view(torch.int32).abs().sum()) == 0, "counters not back to zero"
+
+
+@pytest.mark.parametrize("M,H,V,N,weighted", [(16, 4, 512, 1024, True), (1, 8, 128, 200, False), (5, 1, 256, 64, True)])
+def test_decode_linear_folded_gated_norm(M, H, V, N, weighted):
+    """The gated output norm folded into the output projection (``ccq_decode_linear_gnorm``: the
+    contraction split per head, the gate rows read in place from a wider projection output) against
+    the strided gated-norm kernel followed by ``decode_linear`` (the head's sum of squares runs in
+    another order, which can move a rare normed element by one bf16 unit) and against float64, over
+    two calls on one workspace."""
+    dev = _cuda()
+    from ccq_amd import _lib
+    from ccq_amd._lib import call, ptr
+    from ccq_amd.graph import decode_linear, decode_linear_gnorm, split_workspace
+    print("test_decode_linear_folded_gated_norm", M, H, V, N, weighted, flush=True)
+    K, og = H * V, 96
+    width = og + K + 40
+    ws = split_workspace(N, H, dev) if H > 1 else None
+    gen = torch.Generator().manual_seed(M + H + V)
+    for call_no in range(2):
+        proj = (torch.randn(M, width, generator=gen) * 2).to(BF).to(dev)
+        o = (torch.randn(M, K, generator=gen) * 3).to(BF).to(dev)
+        nw = (torch.rand(V, generator=gen) * 2).float().to(dev) if weighted else None
+        w = (torch.randn(N, K, generator=gen) * 0.03).to(BF).to(dev)
+        res = torch.randn(M, N, generator=gen).to(BF).to(dev)
+        gate = proj[:, og:og + K]
+        y = decode_linear_gnorm(o, gate, nw, V, 1e-5, w, res, ws)
+        normed = torch.empty_like(o)
+        rstd = torch.empty(M * H, device=dev)
+        call("ccq_gated_rmsnorm_fwd_strided", ptr(o), ptr(gate), width, H, ptr(nw), ptr(normed), ptr(rstd), M * H, V,
+             1e-5, _lib.stream_of(o))
+        ref = decode_linear(normed, w, res)
+        torch.cuda.synchronize()
+        e = kern(y, ref.double().cpu())
+        od, gd = o.double().cpu().view(M, H, V), gate.double().cpu().view(M, H, V)
+        r = 1.0 / torch.sqrt((od * od).mean(-1, keepdim=True) + 1e-5)
+        wd = nw.double().cpu() if weighted else torch.ones(V, dtype=D)
+        xn = _r((od * r * wd * F.silu(gd)).reshape(M, K))
+        e64 = kern(y, res.double().cpu() + _r(xn @ w.double().cpu().T))
+        print((M, H, V, N), call_no, f"vs unfolded {e:.2e} vs float64 {e64:.2e}", flush=True)
+        assert y.shape == (M, N) and e <= 5e-4 and e64 <= 5e-4
+        if ws is not None:
+            assert int(ws[:4 * ((N + 15) // 16)].view(torch.int32).abs().sum()) == 0, "counters"

@@ -208,8 +208,9 @@ def test_layer_decode_matches_recurrent_mode(H, K, expand_v, T0):
 def test_layer_decode_in_proj_path_matches_prologue_path(H, K, expand_v, T):
     """GDNLayerDecode's two paths on the same inputs: the short convolutions, g and beta in the input
     projections' epilogue with the decode step normalising q and k and forming lambda
-    (``ccq_gdn_decode_in_proj`` + ``ccq_gdn_layer_decode_step``), against the input projections, the
-    decode prologue kernel and the decode step.  Outputs within a bf16 unit on rare elements (the
+    (``ccq_gdn_decode_in_proj`` + ``ccq_gdn_layer_decode_step``) and the gated output norm folded into
+    the output projection (``ccq_decode_linear_gnorm``), against the input projections, the decode
+    prologue kernel, the decode step, the gated norm kernel and the output projection.  Outputs within a bf16 unit on rare elements (the
     per-head sums of squares and the lambda logit run in another order), states to fp32 roundings,
     convolution caches and position equal; T tokens per call."""
     dev = _cuda()
@@ -229,8 +230,8 @@ def test_layer_decode_in_proj_path_matches_prologue_path(H, K, expand_v, T):
         cache = LayerCache()
         layer(x[:, :T0], past_key_values=cache, use_cache=True)
         fused, plain = GDNLayerDecode(layer, B, T), GDNLayerDecode(layer, B, T)
-        assert fused.conv_in_proj and fused.fast
-        plain.conv_in_proj = False
+        assert fused.conv_in_proj and fused.fast and fused.gnorm_in_proj
+        plain.conv_in_proj = plain.gnorm_in_proj = False
         for ld in (fused, plain):
             ld.load(copy.deepcopy(cache).get(0))
         for s in range(steps):
