@@ -438,7 +438,8 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
     checked against the eager layers' before it is timed."""
     import torch.nn as nn
     import torch.nn.functional as F
-    from ccq_amd.graph import GDNLayerDecode, decode_linear_glu, decode_linear_split, split_plan, split_workspace
+    from ccq_amd.graph import (GDNLayerDecode, decode_linear, decode_linear_glu, decode_linear_split, split_plan,
+                               split_workspace)
     from ccq_amd.layers import CCQGDN, LayerCache
 
     inter = 256 * ((int(d * 4 * 2 / 3) + 255) // 256)  # fla GatedMLP's intermediate size (hidden_ratio 4)
@@ -507,7 +508,8 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
         x = embed(ids)
         for blk, ld in zip(blocks, lds):
             x = blk.mlp_step(ld(x, x, norm=blk.attn_norm))
-        logits = head(norm(x[:, -1]))
+        # the final RMSNorm folded into the LM head's projection (one launch, the same kernel)
+        logits = decode_linear(x[:, -1], head.weight, norm_weight=norm.weight, norm_eps=norm.eps)
         ids.copy_(logits.argmax(-1, keepdim=True))
         return logits
 
