@@ -109,39 +109,79 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
   seq_bounds(a.cu, n, a.T, bos, len);
 
   const int pos_off = a.pos_dev ? *a.pos_dev : a.pos_off;
-  f32x4 creg[RPT];
-  const float* Cin = a.C_in ? a.C_in + (long)unit * K * K : nullptr;
+  // (the cached key sum reaches LDS after the state's loads are issued, so that nothing waits for it
+  // before they are)
+  const float m_first = (tid < K && a.m_in) ? a.m_in[(long)unit * K + min(tid, K - 1)] : 0.f;
+  // layer form: a token's q / k values and lambda-gate operands from the projection rows (every load
+  // unconditional, from a clamped address, and masked after: guarded loads would each be a branch and a
+  // wait of their own), then its normalised q and k into LDS and its lambda
+  constexpr int QJ = LAYER ? kDecodeLayerMaxQ / kThreads : 1;
+  struct Rows {  // (bf16 bit patterns, one per register as loaded: packing or converting them at the
+                 // load would wait for them there)
+    unsigned lw[QJ], q[QJ], yq, yk, lb;
+  };
+  auto u16 = [](const bf16* p) { return (unsigned)*(const unsigned short*)p; };
+  auto f16 = [](unsigned b) { return (float)__builtin_bit_cast(bf16, (unsigned short)b); };
+  auto layer_load = [&](long tok) {
+    const DecodeLayer& L = a.lay;
+    const bf16* xr = (const bf16*)L.x + tok * L.ldx;
+    const bf16* lw = (const bf16*)L.lw + (long)h * a.H * K;
+    const int D = a.H * K, ck = min(tid, K - 1);
+    Rows r;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r)
-    creg[r] = Cin ? *(const f32x4*)(Cin + (long)(rg * RPT + r) * K + j4) : f32x4{0.f, 0.f, 0.f, 0.f};
-  if (tid < K) sm[tid] = a.m_in ? a.m_in[(long)unit * K + tid] : 0.f;
+    for (int j = 0; j < QJ; ++j) {
+      const int c = min(tid + j * kThreads, D - 1);
+      r.lw[j] = u16(lw + c);
+      r.q[j] = u16(xr + L.oq + c);
+    }
+    r.yq = u16(xr + L.oq + h * K + ck);
+    r.yk = u16(xr + L.ok + h * K + ck);
+    r.lb = u16((const bf16*)(L.lb ? L.lb : L.lw) + (L.lb ? h : 0));
+    return r;
+  };
+  auto layer_qk = [&](const Rows& r) {
+    const int D = a.H * K;
+    float part = 0.f;  // the lambda gate's logit: this thread's channels of q
+#pragma unroll
+    for (int j = 0; j < QJ; ++j) part += tid + j * kThreads < D ? f16(r.lw[j]) * f16(r.q[j]) : 0.f;
+    const float yq = tid < K ? f16(r.yq) : 0.f, yk = tid < K ? f16(r.yk) : 0.f;
+    const float rq = rsqrtf(block_sum256(yq * yq, red) + a.lay.l2eps);
+    const float rk = rsqrtf(block_sum256(yk * yk, red) + a.lay.l2eps);
+    const float lg = (float)(bf16)(block_sum256(part, red) + (a.lay.lb ? f16(r.lb) : 0.f));
+    if (tid < K) {
+      sq[tid] = (float)(bf16)(yq * rq);
+      sk[tid] = (float)(bf16)(yk * rk);
+    }
+    return (float)(bf16)(1.f / (1.f + expf(-lg)));
+  };
+  // the first token's row loads go out ahead of the covariance slice's and its sums run while the
+  // slice is in flight (a wait for the older loads does not wait for the slice's); unconditional, as
+  // a load under a branch is waited for at the branch's end (the layer form has a token per sequence)
+  Rows first{};
+  if constexpr (LAYER) first = layer_load(bos);
+  // the covariance slice through a buffer resource of no records when there is no state (loads past
+  // the records return zeros): no branch around the loads, whose join would make the first wait
+  // after it cover them
+  f32x4 creg[RPT];
+  {
+    const auto rc = buf_rsrc(a.C_in ? a.C_in + (long)unit * K * K : nullptr, a.C_in ? K * K * 4 : 0);
+#pragma unroll
+    for (int r = 0; r < RPT; ++r)
+      creg[r] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, ((rg * RPT + r) * K + j4) * 4, 0, 0));
+  }
+  float lam_first = 0.f;
+  if constexpr (LAYER) lam_first = layer_qk(first);
+  if (tid < K) sm[tid] = m_first;
   __syncthreads();
 
   for (int t = 0; t < len; ++t) {
     const long tok = bos + t;
-    float lam_layer = 0.f;
+    float lam_layer = lam_first;
     if constexpr (LAYER) {
-      const DecodeLayer& L = a.lay;
-      const bf16* xr = (const bf16*)L.x + tok * L.ldx;
-      const bf16* lw = (const bf16*)L.lw + (long)h * a.H * K;
-      const int D = a.H * K;
-      float part = 0.f;  // the lambda gate's logit: this thread's channels of q
-#pragma unroll
-      for (int j = 0; j < kDecodeLayerMaxQ / kThreads; ++j) {
-        const int c = tid + j * kThreads;
-        if (c < D) part += (float)lw[c] * (float)xr[L.oq + c];
+      if (t > 0) {
+        lam_layer = layer_qk(layer_load(tok));
+        __syncthreads();
       }
-      const float yq = tid < K ? (float)xr[L.oq + h * K + tid] : 0.f;
-      const float yk = tid < K ? (float)xr[L.ok + h * K + tid] : 0.f;
-      const float rq = rsqrtf(block_sum256(yq * yq, red) + L.l2eps);
-      const float rk = rsqrtf(block_sum256(yk * yk, red) + L.l2eps);
-      const float lg = (float)(bf16)(block_sum256(part, red) + (L.lb ? (float)((const bf16*)L.lb)[h] : 0.f));
-      lam_layer = (float)(bf16)(1.f / (1.f + expf(-lg)));
-      if (tid < K) {
-        sq[tid] = (float)(bf16)(yq * rq);
-        sk[tid] = (float)(bf16)(yk * rk);
-      }
-      __syncthreads();
     } else {
       load_qk<K>(a, tok, h, sq, sk, red);
     }
