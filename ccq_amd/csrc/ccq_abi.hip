@@ -939,9 +939,9 @@ int ccq_gdn_decode_prologue(const void* xq, const void* xk, const void* xv, cons
   if (V <= 0 || V % 8) return fail(CCQ_ERR_SHAPE, "%s: V=%d must be a positive multiple of 8", who, V);
   if (W < 1 || W > 8) return fail(CCQ_ERR_SHAPE, "%s: kernel size W=%d not in [1, 8]", who, W);
   if (ldx < 0 || ldx % 8) return fail(CCQ_ERR_ALIGN, "%s: row stride ldx=%lld must be a multiple of 8", who, (long long)ldx);
-  if (!xq || !xk || !xv || !xa || !xb || !wq || !wk || !wv || !lam_w || !A_log || !dt_bias || !q || !k || !v || !lam ||
-      !g || !beta)
+  if (!xq || !xk || !xv || !xa || !xb || !wq || !wk || !wv || !A_log || !dt_bias || !q || !k || !v || !g || !beta)
     return fail(CCQ_ERR_NULL, "%s: a required pointer is NULL", who);
+  if (lam && !lam_w) return fail(CCQ_ERR_NULL, "%s: the lambda output needs the gate weight", who);
   if (W > 1 && (!cq || !ck || !cv)) return fail(CCQ_ERR_NULL, "%s: W > 1 needs the three caches", who);
   if (H * K > 2048) return fail(CCQ_ERR_SHAPE, "%s: H*K=%d above 2048 (one workgroup holds the whole q row)", who, H * K);
   if (!aligned16(xq) || !aligned16(xk) || !aligned16(xv) || !aligned16(q) || !aligned16(k) || !aligned16(v))
@@ -1319,9 +1319,13 @@ int ccq_gdn_layer_decode_step(const void* x, int64_t ldx, int off_q, int off_k, 
   if (off_q < 0 || off_k < 0 || off_v < 0 || off_q + (int64_t)H * K > ldx || off_k + (int64_t)H * K > ldx ||
       off_v + (int64_t)H * V > ldx)
     return fail(CCQ_ERR_SHAPE, "%s: a column block lies outside the rows (ldx=%lld)", who, (long long)ldx);
-  // the backbone reads v as 8-byte pieces
+  // the backbone reads v as 8-byte pieces, the clean kernel the q row and the gate weight row as
+  // 16-byte pieces of 8 channels
   if ((((uintptr_t)x + 2 * (uintptr_t)off_v) & 7) || (ldx & 3) || (V & 3))
     return fail(CCQ_ERR_ALIGN, "%s: the v rows must be 8-byte aligned", who);
+  if (!aligned16(x) || (ldx & 7) || (off_q & 7) || !aligned16(lam_w))
+    return fail(CCQ_ERR_ALIGN, "%s: x, lam_w, the row stride and off_q must allow 16-byte pieces (ldx %% 8 == 0)",
+                who);
   DecodeLayer lay{};
   lay.x = x;
   lay.ldx = (long)ldx;

@@ -36,26 +36,6 @@ __device__ __forceinline__ float block_sum256(float x, float* red) {
   return s;
 }
 
-// Normalised (optionally) q and k of one token into LDS as fp32 values of bf16 numbers.
-template <int K>
-__device__ __forceinline__ void load_qk(const DecodeArgs& a, long tok, int h, float* sq, float* sk, float* red) {
-  const int tid = threadIdx.x;
-  const bf16* qg = (const bf16*)a.q + (tok * a.H + h) * K;
-  const bf16* kg = (const bf16*)a.k + (tok * a.H + h) * K;
-  const float qv = tid < K ? (float)qg[tid] : 0.f;
-  const float kv = tid < K ? (float)kg[tid] : 0.f;
-  float rq = 1.f, rk = 1.f;
-  if (a.l2norm) {
-    rq = rsqrtf(block_sum256(qv * qv, red) + 1e-6f);
-    rk = rsqrtf(block_sum256(kv * kv, red) + 1e-6f);
-  }
-  if (tid < K) {
-    sq[tid] = a.l2norm ? (float)(bf16)(qv * rq) : qv;
-    sk[tid] = a.l2norm ? (float)(bf16)(kv * rk) : kv;
-  }
-  __syncthreads();
-}
-
 }  // namespace
 
 // Column blocks: a workgroup owns DC = 32 columns of a state and all of its rows.  A thread holds
@@ -92,76 +72,83 @@ __device__ __forceinline__ void store_cols(float* base, int ld, int rg, int c4, 
   for (int r = 0; r < K / RG; ++r) *(f32x4*)(base + (long)(rg * (K / RG) + r) * ld + c4) = x[r];
 }
 
+// Sums of three values over the workgroup with one barrier (each wave's totals, then the four waves'
+// in order); every thread calls it, and consecutive uses of `red` are a barrier apart.
+__device__ __forceinline__ void block_sum3(float& x, float& y, float& z, float (*red)[4]) {
+  x = wave_total(x);
+  y = wave_total(y);
+  z = wave_total(z);
+  if (lane_id() == 0) {
+    red[0][wave_id()] = x;
+    red[1][wave_id()] = y;
+    red[2][wave_id()] = z;
+  }
+  __syncthreads();
+  x = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+  y = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  z = red[2][0] + red[2][1] + red[2][2] + red[2][3];
+}
+
 // LAYER: q and k from the layer's projection rows (after the short convolutions), L2-normalised per
-// head here, and lambda from the whole q activation (ccq/gdn/layer.py:288-316)
+// head here, and lambda from the whole q activation (ccq/gdn/layer.py:288-316).
+// Per token: one barrier for the three sums of the front (|q|^2, |k|^2, the lambda logit), one after
+// the normalised q and k reach LDS, one for the column sums of z, which carry s = m . q along; the
+// running key sum stays in registers (row tid for s, column j0 + tid for the correction).
 template <int K, bool LAYER>
 __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs a) {
   constexpr int RPT = K / RG;  // rows per thread
   static_assert(RPT >= 1, "K >= 32");
-  __shared__ __attribute__((aligned(16))) float sq[K], sk[K], sm[K];
-  __shared__ __attribute__((aligned(16))) float sz[4][DC], szt[DC];
-  __shared__ float red[4];
+  __shared__ __attribute__((aligned(16))) float sq[K], sk[K];
+  __shared__ __attribute__((aligned(16))) float mid[4][DC + 4];  // per wave: z column sums, then s
+  __shared__ float red[3][4], red2[4];
   const int tid = threadIdx.x, cq = tid % NQ, rg = tid / NQ;
   const int unit = blockIdx.x, n = unit / a.H, h = unit % a.H;
   const int j0 = blockIdx.y * DC, j4 = j0 + 4 * cq;
   long bos;
   int len;
   seq_bounds(a.cu, n, a.T, bos, len);
-
   const int pos_off = a.pos_dev ? *a.pos_dev : a.pos_off;
-  // (the cached key sum reaches LDS after the state's loads are issued, so that nothing waits for it
-  // before they are)
-  const float m_first = (tid < K && a.m_in) ? a.m_in[(long)unit * K + min(tid, K - 1)] : 0.f;
-  // layer form: a token's q / k values and lambda-gate operands from the projection rows (every load
-  // unconditional, from a clamped address, and masked after: guarded loads would each be a branch and a
-  // wait of their own), then its normalised q and k into LDS and its lambda
-  constexpr int QJ = LAYER ? kDecodeLayerMaxQ / kThreads : 1;
-  struct Rows {  // (bf16 bit patterns, one per register as loaded: packing or converting them at the
-                 // load would wait for them there)
-    unsigned lw[QJ], q[QJ], yq, yk, lb;
+
+  // layer form: a token's q / k values and the lambda gate's operands from the projection rows, as
+  // bf16 bit patterns (converting them at the load would wait for them there); every load
+  // unconditional, from a clamped address, masked after (a load under a branch is waited for at the
+  // branch's end).  The gate's q row and weight row come as one 16-byte piece of 8 channels per thread.
+  constexpr int QV = kDecodeLayerMaxQ / kThreads;
+  static_assert(QV == 8, "one 16-byte piece of the q row per thread");
+  struct Rows {
+    u32x4 q, lw;
+    unsigned yq, yk, lb;
   };
   auto u16 = [](const bf16* p) { return (unsigned)*(const unsigned short*)p; };
-  auto f16 = [](unsigned b) { return (float)__builtin_bit_cast(bf16, (unsigned short)b); };
+  auto f16 = [](unsigned b) { return __uint_as_float(b << 16); };
   auto layer_load = [&](long tok) {
     const DecodeLayer& L = a.lay;
     const bf16* xr = (const bf16*)L.x + tok * L.ldx;
-    const bf16* lw = (const bf16*)L.lw + (long)h * a.H * K;
-    const int D = a.H * K, ck = min(tid, K - 1);
+    const int D = a.H * K, c8 = min(QV * tid, D - QV), ck = min(tid, K - 1);
     Rows r;
-#pragma unroll
-    for (int j = 0; j < QJ; ++j) {
-      const int c = min(tid + j * kThreads, D - 1);
-      r.lw[j] = u16(lw + c);
-      r.q[j] = u16(xr + L.oq + c);
-    }
+    r.q = *(const u32x4*)(xr + L.oq + c8);
+    r.lw = *(const u32x4*)((const bf16*)L.lw + (long)h * D + c8);
     r.yq = u16(xr + L.oq + h * K + ck);
     r.yk = u16(xr + L.ok + h * K + ck);
     r.lb = u16((const bf16*)(L.lb ? L.lb : L.lw) + (L.lb ? h : 0));
     return r;
   };
-  auto layer_qk = [&](const Rows& r) {
-    const int D = a.H * K;
-    float part = 0.f;  // the lambda gate's logit: this thread's channels of q
-#pragma unroll
-    for (int j = 0; j < QJ; ++j) part += tid + j * kThreads < D ? f16(r.lw[j]) * f16(r.q[j]) : 0.f;
-    const float yq = tid < K ? f16(r.yq) : 0.f, yk = tid < K ? f16(r.yk) : 0.f;
-    const float rq = rsqrtf(block_sum256(yq * yq, red) + a.lay.l2eps);
-    const float rk = rsqrtf(block_sum256(yk * yk, red) + a.lay.l2eps);
-    const float lg = (float)(bf16)(block_sum256(part, red) + (a.lay.lb ? f16(r.lb) : 0.f));
-    if (tid < K) {
-      sq[tid] = (float)(bf16)(yq * rq);
-      sk[tid] = (float)(bf16)(yk * rk);
-    }
-    return (float)(bf16)(1.f / (1.f + expf(-lg)));
-  };
-  // the first token's row loads go out ahead of the covariance slice's and its sums run while the
-  // slice is in flight (a wait for the older loads does not wait for the slice's); unconditional, as
-  // a load under a branch is waited for at the branch's end (the layer form has a token per sequence)
   Rows first{};
   if constexpr (LAYER) first = layer_load(bos);
-  // the covariance slice through a buffer resource of no records when there is no state (loads past
-  // the records return zeros): no branch around the loads, whose join would make the first wait
-  // after it cover them
+  // (the rows' and the key sum's loads go out ahead of the slice's: the compiler would otherwise
+  // issue the slice's first, whose addresses are ready earlier)
+  __builtin_amdgcn_sched_barrier(0);
+  // the cached key sum of row tid and of column j0 + tid through a buffer resource of no records when
+  // there is none (loads past the records return zeros: no branch)
+  float m_row, m_col;
+  {
+    const auto rm = buf_rsrc(a.m_in ? a.m_in + (long)unit * K : nullptr, a.m_in ? K * 4 : 0);
+    m_row = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, tid * 4, 0, 0));
+    m_col = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (j0 + (tid & (DC - 1))) * 4, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // the covariance slice, issued after the rows and the key sum (a wait for those does not wait for
+  // the slice), through a buffer resource of no records when there is no state
   f32x4 creg[RPT];
   {
     const auto rc = buf_rsrc(a.C_in ? a.C_in + (long)unit * K * K : nullptr, a.C_in ? K * K * 4 : 0);
@@ -169,42 +156,59 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
     for (int r = 0; r < RPT; ++r)
       creg[r] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, ((rg * RPT + r) * K + j4) * 4, 0, 0));
   }
-  float lam_first = 0.f;
-  if constexpr (LAYER) lam_first = layer_qk(first);
-  if (tid < K) sm[tid] = m_first;
-  __syncthreads();
 
-  for (int t = 0; t < len; ++t) {
+  const bool norm = LAYER || a.l2norm;
+  // token t of the sequence (layer form: its rows r)
+  auto token = [&](int t, const Rows& r) {
     const long tok = bos + t;
-    float lam_layer = lam_first;
+    float yq, yk, part = 0.f, lb = 0.f;
     if constexpr (LAYER) {
-      if (t > 0) {
-        lam_layer = layer_qk(layer_load(tok));
-        __syncthreads();
+      yq = tid < K ? f16(r.yq) : 0.f;
+      yk = tid < K ? f16(r.yk) : 0.f;
+      if (QV * tid < a.H * K) {
+#pragma unroll
+        for (int e = 0; e < QV / 2; ++e) {
+          part += __uint_as_float(r.lw[e] << 16) * __uint_as_float(r.q[e] << 16);
+          part += __uint_as_float(r.lw[e] & 0xffff0000u) * __uint_as_float(r.q[e] & 0xffff0000u);
+        }
       }
+      lb = a.lay.lb ? f16(r.lb) : 0.f;
     } else {
-      load_qk<K>(a, tok, h, sq, sk, red);
+      const bf16* qg = (const bf16*)a.q + (tok * a.H + h) * K;
+      const bf16* kg = (const bf16*)a.k + (tok * a.H + h) * K;
+      yq = tid < K ? (float)qg[tid] : 0.f;
+      yk = tid < K ? (float)kg[tid] : 0.f;
     }
-    if (blockIdx.y == 0 && tid < K) a.kn[(tok * a.H + h) * K + tid] = sk[tid];
+    float ssq = yq * yq, ssk = yk * yk;
+    if (norm) block_sum3(ssq, ssk, part, red);
+    const float eps = LAYER ? a.lay.l2eps : 1e-6f;
+    const float qv = norm ? (float)(bf16)(yq * rsqrtf(ssq + eps)) : yq;
+    const float kv = norm ? (float)(bf16)(yk * rsqrtf(ssk + eps)) : yk;
+    if (tid < K) {
+      sq[tid] = qv;
+      sk[tid] = kv;
+    }
+    if (blockIdx.y == 0 && tid < K) a.kn[(tok * a.H + h) * K + tid] = kv;
     if (!a.ccq) {
-      if (blockIdx.y == 0 && tid < K) a.qc[(tok * a.H + h) * K + tid] = sq[tid];
+      if (blockIdx.y == 0 && tid < K) a.qc[(tok * a.H + h) * K + tid] = qv;
       __syncthreads();
-      continue;
+      return;
     }
     // lambda
     float lam;
-    if (LAYER) {
-      lam = lam_layer;
+    if constexpr (LAYER) {
+      lam = (float)(bf16)(1.f / (1.f + expf(-(float)(bf16)(part + lb))));
     } else if (a.gate_w) {
-      const float x = tid < K ? a.gate_w[(long)h * K + tid] * sq[tid] : 0.f;
-      lam = sigmoidf_(block_sum256(x, red) + a.gate_b[h]);
+      const float x = tid < K ? a.gate_w[(long)h * K + tid] * qv : 0.f;
+      lam = sigmoidf_(block_sum256(x, red2) + a.gate_b[h]);
     } else {
       lam = a.lam[tok * a.H + h];
     }
-    // running key sum and s = m . q
-    if (tid < K) sm[tid] += sk[tid];
+    // running key sum; this thread's term of s = m . q
+    m_row += kv;
+    const float sp = m_row * qv;
     __syncthreads();
-    const float s = block_sum256(tid < K ? sm[tid] * sq[tid] : 0.f, red);
+    m_col += sk[j0 + (tid & (DC - 1))];
     // C column update and partial z over this thread's rows
     const f32x4 kj = *(const f32x4*)(sk + j4);
     f32x4 zp = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -216,20 +220,46 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
     }
     // the final state leaves as soon as it is formed (its stores overlap the reduction below)
     if (t == len - 1 && a.C_out) store_cols<K>(a.C_out + (long)unit * K * K, K, rg, j4, creg);
-    colsum(sz, szt, zp);
-    if (tid < DC) {
-      const int j = j0 + tid;
-      float pos = (float)(t + 1 + pos_off);
-      pos = pos < 1.f ? 1.f : pos;
-      float corr = szt[tid] / pos;
-      if (a.subtract_mean) corr -= s * sm[j] / (pos * pos);
-      a.qc[(tok * a.H + h) * K + j] = sq[j] - lam * corr;
+    // column sums of z within each wave (its eight row groups: DPP, then two lane swaps) and the
+    // wave's total of s, to LDS; after one barrier thread tid < DC adds the four waves' parts
+    {
+      f32x4 y;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float v = zp[c] + dppf<0x128>(zp[c]);  // row_ror:8 (lane l ^ 8 of the 16-lane row)
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        y[c] = v;
+      }
+      const float sw = wave_total(sp);
+      const int l = lane_id();
+      if (l < NQ) *(f32x4*)&mid[wave_id()][4 * l] = y;
+      if (l == 0) mid[wave_id()][DC] = sw;
     }
     __syncthreads();
+    if (tid < DC) {
+      const float z = (mid[0][tid] + mid[1][tid]) + (mid[2][tid] + mid[3][tid]);
+      const float s = (mid[0][DC] + mid[1][DC]) + (mid[2][DC] + mid[3][DC]);
+      float pos = (float)(t + 1 + pos_off);
+      pos = pos < 1.f ? 1.f : pos;
+      float corr = z / pos;
+      if (a.subtract_mean) corr -= s * m_col / (pos * pos);
+      a.qc[(tok * a.H + h) * K + j0 + tid] = sq[j0 + tid] - lam * corr;
+    }
+    // (without the front's barrier the next token's q and k would overwrite what this one reads)
+    if (!norm) __syncthreads();
+  };
+  // the first token apart from the others: a path shared with their row loads would wait for those
+  // at its join, which on the first token's path covers the slice's loads
+  if (len > 0) token(0, first);
+  for (int t = 1; t < len; ++t) {
+    Rows r{};
+    if constexpr (LAYER) r = layer_load(bos + t);
+    token(t, r);
   }
   // (no token, or the plain step without cleaning: the state as it came in)
   if (a.C_out && (len == 0 || !a.ccq)) store_cols<K>(a.C_out + (long)unit * K * K, K, rg, j4, creg);
-  if (a.m_out && tid < DC) a.m_out[(long)unit * K + j0 + tid] = sm[j0 + tid];
+  if (a.m_out && tid < DC) a.m_out[(long)unit * K + j0 + tid] = m_col;
 }
 
 template <int K>

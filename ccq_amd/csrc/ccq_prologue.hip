@@ -523,7 +523,7 @@ __global__ __launch_bounds__(kThreads) void decode_prologue_kernel(const DecProA
   }
   // slice 0: the gate weights of this thread's channels, one 16-byte piece per head
   bf16x8 lwp[kDecProMaxH];
-  if (kind == 0) {
+  if (kind == 0 && a.lam) {
 #pragma unroll
     for (int h = 0; h < kDecProMaxH; ++h)
       if (h < a.H) lwp[h] = *gmem((const bf16x8*)((const bf16*)a.lw + (long)h * Dq + c));
@@ -569,9 +569,10 @@ __global__ __launch_bounds__(kThreads) void decode_prologue_kernel(const DecProA
     if (on) *gmem((bf16x8*)(out + row * Dq + c)) = nb;
     if (kind != 0) continue;
     // gate logits: this thread's channels against every head's weight row, then the workgroup's sum
+    // (no lambda output: a layer without cleaning)
 #pragma unroll
     for (int h = 0; h < kDecProMaxH; ++h) {
-      if (h >= a.H) break;
+      if (h >= a.H || !a.lam) break;
       float part = 0.f;
       if (on)
 #pragma unroll
@@ -585,7 +586,7 @@ __global__ __launch_bounds__(kThreads) void decode_prologue_kernel(const DecProA
       float logit = (a.lb ? (float)((const bf16*)a.lb)[h] : 0.f);
       for (int ww = 0; ww < kThreads / 64; ++ww) logit += sPart[ww][h];
       const float lg = (float)(bf16)logit;                   // the gate projection's bf16 output
-      a.lam[row * a.H + h] = (float)(bf16)(1.f / (1.f + expf(-lg)));
+      if (a.lam) a.lam[row * a.H + h] = (float)(bf16)(1.f / (1.f + expf(-lg)));
       const float xb = (float)((const bf16*)a.xb)[row * a.ldx + h];
       float be = (float)(bf16)(1.f / (1.f + expf(-xb)));
       if (a.neg_eig) be *= 2.f;

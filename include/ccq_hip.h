@@ -326,7 +326,8 @@ int ccq_decode_linear_split(const void* x, int64_t ldx, const void* weight, cons
  * aligned); wq/wk/wv bf16 [D, W] convolution weights, bq/bk/bv bf16 [D] biases (nullable); cq/ck/cv
  * bf16 [B, D, W-1] caches (each sequence's previous W-1 inputs), updated in place; lam_w bf16
  * [H, H*K], lam_b bf16 [H] (nullable), A_log, dt_bias bf16 [H].  Outputs: q, k bf16 [B, T, H, K], v
- * bf16 [B, T, H, V], lam, g, beta fp32 [B, T, H] -- the decode step's inputs with use_l2norm = 0.
+ * bf16 [B, T, H, V], lam, g, beta fp32 [B, T, H] -- the decode step's inputs with use_l2norm = 0
+ * (lam may be NULL for a layer without cleaning: then lam_w and lam_b are not read).
  * H <= 32; K a power of two in [8, 512]; H*K <= 2048; V % 8 == 0; W in [1, 8]; the convolution
  * weights, biases, caches and lam_w 16-byte aligned.  No allocation; one kernel (a workgroup per
  * sequence and slice: the q channels with the gates, then up to 2048 k or v channels each).
@@ -362,7 +363,8 @@ int ccq_gdn_decode_in_proj(const void* x, int64_t ldx, const void* weight, void*
  * lambda = sigmoid(lam_w q + lam_b) over the whole q activation (lam_w bf16 [H, H K], lam_b [H]
  * nullable), v is read in place (off_v), g and beta as given (fp32 [B T, H]).  States, position,
  * workspace (ccq_decode_step_workspace_bytes) and the output o bf16 [B, T, H, V] as
- * ccq_gdn_decode_step.  H K <= 2048.  Two kernels, no allocation.
+ * ccq_gdn_decode_step.  H K <= 2048; x and lam_w 16-byte aligned, ldx and off_q multiples of 8, the v
+ * rows 8-byte aligned.  Two kernels, no allocation.
  */
 int ccq_gdn_layer_decode_step(const void* x, int64_t ldx, int off_q, int off_k, int off_v, const void* lam_w,
                               const void* lam_b, const float* g, const float* beta, float* state, float* cov_state,

@@ -204,15 +204,18 @@ def test_layer_decode_matches_recurrent_mode(H, K, expand_v, T0):
             assert int(ld.step.position.item()) == t + 1
 
 
-@pytest.mark.parametrize("H,K,expand_v,T", [(4, 256, 2, 1), (2, 128, 1, 2), (2, 64, 2, 3)])
-def test_layer_decode_in_proj_path_matches_prologue_path(H, K, expand_v, T):
+@pytest.mark.parametrize("H,K,expand_v,T,flags", [(4, 256, 2, 1, {}), (2, 128, 1, 2, {}), (2, 64, 2, 3, {}),
+                                                   (2, 128, 1, 2, {"subtract_mean": False}),
+                                                   (2, 128, 1, 1, {"enable_ccq": False})])
+def test_layer_decode_in_proj_path_matches_prologue_path(H, K, expand_v, T, flags):
     """GDNLayerDecode's two paths on the same inputs: the short convolutions, g and beta in the input
     projections' epilogue with the decode step normalising q and k and forming lambda
     (``ccq_gdn_decode_in_proj`` + ``ccq_gdn_layer_decode_step``) and the gated output norm folded into
     the output projection (``ccq_decode_linear_gnorm``), against the input projections, the decode
     prologue kernel, the decode step, the gated norm kernel and the output projection.  Outputs within a bf16 unit on rare elements (the
     per-head sums of squares and the lambda logit run in another order), states to fp32 roundings,
-    convolution caches and position equal; T tokens per call."""
+    convolution caches and position equal; T tokens per call.  Also a layer without the running mean
+    (``subtract_mean=False``) and one without cleaning (``enable_ccq=False``: no covariance, no lambda)."""
     dev = _cuda()
     import copy
 
@@ -220,9 +223,10 @@ def test_layer_decode_in_proj_path_matches_prologue_path(H, K, expand_v, T):
     from ccq_amd.graph import GDNLayerDecode
     from tests._util import rel
     B, T0, steps = 3, 37, 3
-    print(f"test_layer_decode_in_proj_path_matches_prologue_path H={H} K={K} expand_v={expand_v} T={T}", flush=True)
+    print(f"test_layer_decode_in_proj_path_matches_prologue_path H={H} K={K} expand_v={expand_v} T={T} {flags}",
+          flush=True)
     torch.manual_seed(0)
-    layer = CCQGDN(hidden_size=256, head_dim=K, num_heads=H, expand_v=expand_v, mode="chunk", layer_idx=0)
+    layer = CCQGDN(hidden_size=256, head_dim=K, num_heads=H, expand_v=expand_v, mode="chunk", layer_idx=0, **flags)
     layer = layer.to(dev, torch.bfloat16).eval()
     gen = torch.Generator().manual_seed(2)
     x = torch.randn(B, T0 + steps * T, 256, generator=gen).to(dev, torch.bfloat16)
@@ -238,11 +242,15 @@ def test_layer_decode_in_proj_path_matches_prologue_path(H, K, expand_v, T):
             h = x[:, T0 + s * T:T0 + (s + 1) * T]
             o_f, o_p = fused(h), plain(h)
             torch.cuda.synchronize()
-            errs = {"o": rel(o_f, o_p), "S": rel(fused.step.S, plain.step.S), "C": rel(fused.step.C, plain.step.C),
-                    "m": rel(fused.step.m, plain.step.m)}
+            errs = {"o": rel(o_f, o_p), "S": rel(fused.step.S, plain.step.S)}
+            for n in ("C", "m"):
+                a, b = getattr(fused.step, n), getattr(plain.step, n)
+                assert (a is None) == (b is None), n
+                if a is not None:
+                    errs[n] = rel(a, b)
             print(s, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
             assert errs["o"] <= 1e-3
-            for n in ("S", "C", "m"):
+            for n in errs.keys() - {"o"}:
                 assert errs[n] <= 1e-5, n
             for a, b in zip(fused.conv, plain.conv):
                 assert torch.equal(a, b), "convolution cache"
