@@ -16,7 +16,7 @@
 //   decode_backbone grid (N*H, V/32): each workgroup owns 32 columns of S, reads the cleaned query;
 //                  an in-place step (device-held position) also moves the new key sum over the
 //                  cached one and advances the position here.
-// Thread (column j = tid % 32, row group tid / 32) holds K/8 consecutive rows of its column.
+// Thread (columns 4 (tid % 8) .. + 3 of the block, row group tid / 8) holds K/32 consecutive rows of them.
 #include <mutex>
 
 #include "ccq_tile.h"
@@ -44,26 +44,6 @@ __device__ __forceinline__ float block_sum256(float x, float* red) {
 // moves in K / 32 wide instructions per thread (one 4-byte access per instruction moved only a
 // quarter of that per issue slot).  Column sums over the rows go through LDS in two levels.
 constexpr int DC = 32, NQ = DC / 4, RG = kThreads / NQ;
-
-// Sum over the RG row groups of each of the DC columns (every thread holds four columns of one row
-// group, x): within a wave over its eight row groups (lanes l, l ^ 8, l ^ 16, ...: DPP, then two
-// lane swaps), then across the four waves through LDS; on return tot[c] (c < DC) holds the totals.
-// Two barriers.
-__device__ __forceinline__ void colsum(float (*mid)[DC], float* tot, const f32x4& x) {
-  f32x4 y;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    float v = x[c] + dppf<0x128>(x[c]);  // row_ror:8 (lane l ^ 8 of the 16-lane row)
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    y[c] = v;
-  }
-  const int l = lane_id();
-  if (l < NQ) *(f32x4*)&mid[wave_id()][4 * l] = y;
-  __syncthreads();
-  if (threadIdx.x < DC) tot[threadIdx.x] = (mid[0][threadIdx.x] + mid[1][threadIdx.x]) + (mid[2][threadIdx.x] + mid[3][threadIdx.x]);
-  __syncthreads();
-}
 
 // A thread's RPT rows x 4 columns of a state slice to HBM (row stride ld).
 template <int K>
@@ -262,12 +242,25 @@ __global__ __launch_bounds__(kThreads) void decode_clean_kernel(const DecodeArgs
   if (a.m_out && tid < DC) a.m_out[(long)unit * K + j0 + tid] = m_col;
 }
 
+// One token's operands, as loaded: the cleaned query, the key and the key decay's exponent of row
+// tid, this thread's four value columns (bf16 bits) and their decay exponents, the token's g and
+// beta.  Optional inputs come through buffer resources of no records (zeros: e^0 = 1 exactly).
+struct BbOps {
+  float q, k, gk, g, beta;
+  u32x2 v;
+  f32x4 gv;
+};
+
+// Per token: the decayed state's column sums against k and the output's against the cleaned query,
+// each in one LDS exchange with one barrier (every thread adds the four waves' parts of the columns
+// it needs).  The token's operands are loaded ahead of the state slice, and the new key sum's copy
+// over the cached one runs last: a load issued after the slice is waited for with the slice.
 template <int K>
 __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeArgs a) {
   constexpr int RPT = K / RG;
   static_assert(RPT >= 1, "K >= 32");
   __shared__ __attribute__((aligned(16))) float sq[K], sk[K], sgk[K];
-  __shared__ __attribute__((aligned(16))) float sp[4][DC], spt[DC];
+  __shared__ __attribute__((aligned(16))) float mp[4][DC], mo[4][DC];
   const int tid = threadIdx.x, cq = tid % NQ, rg = tid / NQ;
   const int unit = blockIdx.x, n = unit / a.H, h = unit % a.H;
   const int V = a.V, v0 = blockIdx.y * DC, v4 = v0 + 4 * cq;
@@ -275,11 +268,108 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
   int len;
   seq_bounds(a.cu, n, a.T, bos, len);
 
+  // (every load through a buffer resource, of no records for an absent input or when `on` is false:
+  // no branch, whose join would make the waits after it cover the state slice's loads)
+  auto bb_load = [&](long tok, bool on) {
+    BbOps o;
+    const long row = tok * a.H + h;
+    auto ld1 = [&](const float* p, int bytes, int off) {
+      return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(on ? p : nullptr, on && p ? bytes : 0), off, 0, 0));
+    };
+    o.q = ld1(a.qc + row * K, K * 4, tid * 4);
+    o.k = ld1(a.kn + row * K, K * 4, tid * 4);
+    o.gk = ld1(a.gk ? a.gk + row * K : nullptr, K * 4, tid * 4);
+    o.g = ld1(a.g ? a.g + row : nullptr, 4, 0);
+    o.beta = ld1(a.beta ? a.beta + row : nullptr, 4, 0);
+    const bf16* vr = (const bf16*)a.v + (a.vld ? tok * a.vld + (long)h * V : row * V);
+    o.v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(on ? vr : nullptr, on ? V * 2 : 0), v4 * 2, 0, 0));
+    o.gv = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         buf_rsrc(on && a.gv ? a.gv + row * V : nullptr, on && a.gv ? V * 4 : 0), v4 * 4, 0, 0));
+    return o;
+  };
+  // (the cleaned queries of every token are ready: the backbone may run backwards in time)
+  auto tok_of = [&](int tt) { return bos + (a.reverse ? len - 1 - tt : tt); };
+  // the slice's byte offset of this thread's first row, formed before the operand loads (address
+  // arithmetic placed after them can land on a register a pending load writes and wait for it);
+  // row r adds r V 4 bytes as the scalar offset
+  int soff = (rg * RPT * V + v4) * 4;
+  asm volatile("" : "+v"(soff));
+  const BbOps first = bb_load(tok_of(0), len > 0);
+  __builtin_amdgcn_sched_barrier(0);
   f32x4 sreg[RPT];
-  const float* Sin = a.S_in ? a.S_in + (long)unit * K * V : nullptr;
+  {
+    const auto rs = buf_rsrc(a.S_in ? a.S_in + (long)unit * K * V : nullptr, a.S_in ? K * V * 4 : 0);
 #pragma unroll
-  for (int r = 0; r < RPT; ++r)
-    sreg[r] = Sin ? *(const f32x4*)(Sin + (long)(rg * RPT + r) * V + v4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < RPT; ++r)
+      sreg[r] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, soff, r * V * 4, 0));
+  }
+
+  // the column sums of x over the RG row groups: within each wave (its eight row groups: DPP, then
+  // two lane swaps) to mid, then (after the caller's barrier) the four waves' parts
+  auto colpart = [&](float (*mid)[DC], const f32x4& x) {
+    f32x4 y;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float v = x[c] + dppf<0x128>(x[c]);  // row_ror:8 (lane l ^ 8 of the 16-lane row)
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      y[c] = v;
+    }
+    if (lane_id() < NQ) *(f32x4*)&mid[wave_id()][4 * lane_id()] = y;
+  };
+  auto token = [&](int tt, const BbOps& op) {
+    const long tok = tok_of(tt);
+    if (tid < K) {
+      sq[tid] = op.q;
+      sk[tid] = op.k;
+      sgk[tid] = __expf(op.gk);
+    }
+    __syncthreads();
+    f32x4 vt, dv;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const unsigned w = op.v[c >> 1];
+      vt[c] = __uint_as_float((c & 1) ? (w & 0xffff0000u) : (w << 16));
+      dv[c] = __expf(op.gv[c]);
+    }
+    if (a.gla) {
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const int i = rg * RPT + r;
+        sreg[r] = sgk[i] * sreg[r] * dv + sk[i] * vt;
+      }
+    } else {
+      const f32x4 dec = __expf(op.g) * dv;
+      f32x4 p = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        sreg[r] *= dec * sgk[rg * RPT + r];
+        p += sreg[r] * sk[rg * RPT + r];
+      }
+      colpart(mp, p);
+      __syncthreads();
+      const f32x4 ks = (*(const f32x4*)&mp[0][4 * cq] + *(const f32x4*)&mp[1][4 * cq]) +
+                       (*(const f32x4*)&mp[2][4 * cq] + *(const f32x4*)&mp[3][4 * cq]);
+      const f32x4 u = op.beta * (vt - ks);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) sreg[r] += sk[rg * RPT + r] * u;
+    }
+    if (tt == len - 1 && a.S_out) store_cols<K>(a.S_out + (long)unit * K * V, V, rg, v4, sreg);
+    f32x4 po = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) po += sreg[r] * sq[rg * RPT + r];
+    colpart(mo, po);
+    __syncthreads();
+    if (tid < DC) {
+      const float x = (mo[0][tid] + mo[1][tid]) + (mo[2][tid] + mo[3][tid]);
+      ((bf16*)a.o)[(tok * a.H + h) * V + v0 + tid] = (bf16)(a.scale * x);
+    }
+  };
+  // the first token apart from the others (a path shared with their operand loads would wait for
+  // those at its join, which on the first token's path covers the slice's loads)
+  if (len > 0) token(0, first);
+  for (int tt = 1; tt < len; ++tt) token(tt, bb_load(tok_of(tt), true));
+  if (a.S_out && len == 0) store_cols<K>(a.S_out + (long)unit * K * V, V, rg, v4, sreg);
 
   // end of an in-place step (the clean kernel, launched before in the same stream, has read the
   // cached key sum and the position): the new key sum replaces the cached one, the position
@@ -290,57 +380,6 @@ __global__ __launch_bounds__(kThreads) void decode_backbone_kernel(const DecodeA
     for (long i = gid; i < a.m_count; i += nthreads) a.m_dst[i] = a.m_src[i];
   }
   if (a.pos_adv && blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *a.pos_adv += a.T;
-
-  for (int tt = 0; tt < len; ++tt) {
-    // (the cleaned queries of every token are ready: the backbone may run backwards in time)
-    const int t = a.reverse ? len - 1 - tt : tt;
-    const long tok = bos + t;
-    if (tid < K) {
-      sq[tid] = a.qc[(tok * a.H + h) * K + tid];
-      sk[tid] = a.kn[(tok * a.H + h) * K + tid];
-      sgk[tid] = a.gk ? __expf(a.gk[(tok * a.H + h) * K + tid]) : 1.f;
-    }
-    __syncthreads();
-    const long vo = (tok * a.H + h) * V + v4;
-    f32x4 vt, dv = f32x4{1.f, 1.f, 1.f, 1.f};
-    {
-      const bf16x4 vb = *(const bf16x4*)((const bf16*)a.v + (a.vld ? tok * a.vld + (long)h * V + v4 : vo));
-#pragma unroll
-      for (int c = 0; c < 4; ++c) vt[c] = (float)vb[c];
-      if (a.gv) {
-        const f32x4 gv = *(const f32x4*)(a.gv + vo);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) dv[c] = __expf(gv[c]);
-      }
-    }
-    if (a.gla) {
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        const int i = rg * RPT + r;
-        sreg[r] = sgk[i] * sreg[r] * dv + sk[i] * vt;
-      }
-    } else {
-      const f32x4 dec = (a.g ? __expf(a.g[tok * a.H + h]) : 1.f) * dv;
-      f32x4 p = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        sreg[r] *= dec * sgk[rg * RPT + r];
-        p += sreg[r] * sk[rg * RPT + r];
-      }
-      colsum(sp, spt, p);
-      const f32x4 ks = *(const f32x4*)(spt + 4 * cq);
-      const f32x4 u = a.beta[tok * a.H + h] * (vt - ks);
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) sreg[r] += sk[rg * RPT + r] * u;
-    }
-    if (tt == len - 1 && a.S_out) store_cols<K>(a.S_out + (long)unit * K * V, V, rg, v4, sreg);
-    f32x4 po = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) po += sreg[r] * sq[rg * RPT + r];
-    colsum(sp, spt, po);
-    if (tid < DC) ((bf16*)a.o)[(tok * a.H + h) * V + v0 + tid] = (bf16)(a.scale * spt[tid]);
-  }
-  if (a.S_out && len == 0) store_cols<K>(a.S_out + (long)unit * K * V, V, rg, v4, sreg);
 }
 
 template <int K>
