@@ -492,34 +492,40 @@ struct DlGate {
 };
 
 // SPW: 32-wide steps per wave (every wave takes SPW; steps past its range read the range's last
-// step's address and contribute a zero x fragment, so the code has no branch around a load or an MFMA)
-template <int SPW, bool GLU, bool NORM, bool CONV = false, bool GN = false>
+// step's address and contribute a zero x fragment, so the code has no branch around a load or an MFMA).
+// NT: 16-column tiles per workgroup (plain and normed forms, unsplit): a wide output (an LM head's)
+// then has all of its weight loads in flight in one round of workgroups instead of several; wave t
+// finishes tile t.
+template <int SPW, bool GLU, bool NORM, bool CONV = false, bool GN = false, int NT = 1>
 __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void* x_, long ldx, const void* w_,
                                                                        const void* r_, long ldr, void* y_, long ldy,
                                                                        int M, int K, int N, const void* nw_,
                                                                        float eps, const DlSplit sp, const DlConv cv,
                                                                        const DlGate gt) {
-  __shared__ f32x4 sAcc[GLU ? 2 : 1][kDlWaves][64];
+  static_assert(NT == 1 || (!GLU && !CONV && !GN), "column tiles: plain and normed forms");
+  __shared__ f32x4 sAcc[GLU ? 2 : NT][kDlWaves][64];
   __shared__ float sSS[NORM || GN ? kDlWaves : 1][16];
   const bf16* x = (const bf16*)x_;
   const bf16* w = (const bf16*)w_;
   const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * NT;
   const int s0 = blockIdx.y * sp.sps, steps = min(K / 32, s0 + sp.sps);  // this workgroup's steps [s0, steps)
   const int nw = min(n0 + (l & 15), N - 1);            // weight row of this lane (rows past N repeat the last)
   const int mx = min(l & 15, M - 1);                    // token row of this lane (rows past M repeat the last)
   const bf16* wr = w + (long)nw * K + 8 * (l >> 4);
+  auto wrow = [&](int t) { return t == 0 ? wr : w + (long)min(n0 + 16 * t + (l & 15), N - 1) * K + 8 * (l >> 4); };
   const bf16* wu = w + (long)(GLU ? N + nw : nw) * K + 8 * (l >> 4);  // the up half's row (gated form)
   const bf16* xr = x + (long)mx * ldx + 8 * (l >> 4);
   // every load of the wave is issued before the first use
-  bf16x8 wa[SPW], wb[GLU ? SPW : 1], xb[SPW], gw[NORM || GN ? SPW : 1];
+  bf16x8 wa[NT][SPW], wb[GLU ? SPW : 1], xb[SPW], gw[NORM || GN ? SPW : 1];
   f32x4 gn0[GN ? SPW : 1], gn1[GN ? SPW : 1];  // gated-norm form: the norm weight of the step's columns
   const bf16* nr = (const bf16*)(NORM ? nw_ : w_) + 8 * (l >> 4);
   const bf16* gr = GN ? (const bf16*)gt.g + (long)mx * gt.ldg + 8 * (l >> 4) : x;
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
     const int st = min(s0 + wv + kDlWaves * j, steps - 1);
-    wa[j] = *gmem((const bf16x8*)(wr + 32 * st));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) wa[t][j] = *gmem((const bf16x8*)(wrow(t) + 32 * st));
     if constexpr (GLU) wb[j] = *gmem((const bf16x8*)(wu + 32 * st));
     xb[j] = *gmem((const bf16x8*)(xr + 32 * st));
     if constexpr (NORM) gw[j] = *gmem((const bf16x8*)(nr + 32 * st));
@@ -555,7 +561,9 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
     for (int q = 0; q < kDlWaves; ++q) tot += sSS[q][l & 15];
     rs = rsqrtf(tot / (float)(GN ? gt.dv : K) + eps);
   }
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, acu = acc;
+  f32x4 acc[NT], acu = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = acu;
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
     const bool live = s0 + wv + kDlWaves * j < steps;
@@ -570,7 +578,8 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
       }
       xf[i] = live ? v : (bf16)0.f;
     }
-    acc = mfma16(wa[j], xf, acc);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = mfma16(wa[t][j], xf, acc[t]);
     if constexpr (GLU) acu = mfma16(wb[j], xf, acu);
   }
   // convolution epilogue: thread (row tid / 16, column tid % 16) of the first four waves takes one
@@ -605,7 +614,8 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
       cd = (float)((const bf16*)cv.dtb)[ech];
     }
   }
-  sAcc[0][wv][l] = acc;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) sAcc[t][wv][l] = acc[t];
   if constexpr (GLU) sAcc[GLU ? 1 : 0][wv][l] = acu;
   __syncthreads();
   if constexpr (CONV) {
@@ -666,11 +676,12 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
     ((bf16*)y_)[(long)m * ldy + n] = (bf16)out;
     return;
   }
-  if (wv != 0) return;
-  f32x4 sum = sAcc[0][0][l];
+  if (wv >= NT) return;
+  const int tt = NT > 1 ? wv : 0;  // this wave's tile
+  f32x4 sum = sAcc[tt][0][l];
 #pragma unroll
   for (int q = 1; q < kDlWaves; ++q) {
-    const f32x4 v = sAcc[0][q][l];
+    const f32x4 v = sAcc[tt][q][l];
     sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
   }
   if (sp.S > 1) {
@@ -705,8 +716,8 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
       sum[i] = (float)(bf16)(g / (1.f + expf(-g))) * (float)(bf16)su[i];  // rounded once more at the store
     }
   }
-  // sum[i] = y[m = l & 15][n = n0 + 4 (l >> 4) + i]
-  const int m = l & 15, nb = n0 + 4 * (l >> 4);
+  // sum[i] = y[m = l & 15][n = n0 + 16 tt + 4 (l >> 4) + i]
+  const int m = l & 15, nb = n0 + 16 * tt + 4 * (l >> 4);
   if (m >= M) return;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -719,12 +730,32 @@ __global__ __launch_bounds__(kDlWaves * 64) void decode_linear_kernel(const void
   }
 }
 
+// Column tiles per workgroup of a wide plain or normed projection: four when that still leaves 200
+// workgroups or more (an LM head's 32,000 columns: 500 workgroups, 21.6 us for 65.5 MB at 16 tokens
+// against 26.1 us with one tile; eight tiles measured the same as four).
+constexpr int kDlWideTiles = 4;
+inline bool dl_wide(bool glu, int blocks, const DlSplit& sp, const DlConv* conv, const DlGate* gate) {
+  return !glu && !conv && !gate && sp.S == 1 && blocks >= 200 * kDlWideTiles;
+}
+
 template <int SPW>
 static void launch_dl(bool glu, dim3 grid, dim3 block, hipStream_t st, const void* x, long ldx, const void* w,
                       const void* r, long ldr, void* y, long ldy, int M, int K, int N, const void* nw, float eps,
                       const DlSplit& sp, const DlConv* conv, const DlGate* gate) {
   const DlConv cv = conv ? *conv : DlConv{};
   const DlGate gt = gate ? *gate : DlGate{};
+  // (contractions up to 1024: the tiles of longer ones would spill)
+  if (SPW <= 2 && dl_wide(glu, (int)grid.x, sp, conv, gate)) {
+    constexpr int S2 = SPW <= 2 ? SPW : 1;  // (no instances for longer contractions)
+    const dim3 g4((grid.x + kDlWideTiles - 1) / kDlWideTiles, 1);
+    if (nw)
+      hipLaunchKernelGGL((decode_linear_kernel<S2, false, true, false, false, kDlWideTiles>), g4, block, 0, st, x, ldx,
+                         w, r, ldr, y, ldy, M, K, N, nw, eps, sp, cv, gt);
+    else
+      hipLaunchKernelGGL((decode_linear_kernel<S2, false, false, false, false, kDlWideTiles>), g4, block, 0, st, x,
+                         ldx, w, r, ldr, y, ldy, M, K, N, nw, eps, sp, cv, gt);
+    return;
+  }
 #define CCQ_DL(G, NM)                                                                                        \
   hipLaunchKernelGGL((decode_linear_kernel<SPW, G, NM>), grid, block, 0, st, x, ldx, w, r, ldr, y, ldy, M, K, N, \
                      nw, eps, sp, cv, gt)

@@ -40,6 +40,8 @@ CASES = [
     (16, 2048, 1024, True),    # C4: o_proj with the residual
     (3, 1024, 5632, False),    # three tokens
     (1, 4096, 100, True),      # one token, the widest K, N not a multiple of 16
+    (16, 1024, 32000, False),  # C4's LM head: four column tiles per workgroup
+    (5, 512, 17000, True),     # wide, the last workgroup's tiles partly past N
 ]
 
 
@@ -81,15 +83,16 @@ def test_decode_linear_glu(M, K, N):
     assert y.shape == (M, N) and e <= 5e-4
 
 
-@pytest.mark.parametrize("glu", [False, True])
-def test_decode_linear_folded_rmsnorm(glu):
+@pytest.mark.parametrize("glu,N", [(False, 1024), (True, 1024), (False, 32000)])
+def test_decode_linear_folded_rmsnorm(glu, N):
     """The RMSNorm folded into the projection equals torch's bf16 nn.RMSNorm followed by the same
     projection kernel (the norm's output is rounded once; the row's sum of squares runs in another
-    order, which can move a rare element of the normalised row by one ulp)."""
+    order, which can move a rare element of the normalised row by one ulp); N = 32000 is the LM head
+    with the final norm folded in (four column tiles per workgroup)."""
     dev = _cuda()
     import torch.nn as nn
     from ccq_amd.graph import decode_linear, decode_linear_glu
-    M, K, N = 16, 1024, 1024
+    M, K = 16, 1024
     gen = torch.Generator().manual_seed(5)
     norm = nn.RMSNorm(K, eps=1e-5)
     with torch.no_grad():
