@@ -438,8 +438,8 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
     checked against the eager layers' before it is timed."""
     import torch.nn as nn
     import torch.nn.functional as F
-    from ccq_amd.graph import (GDNLayerDecode, decode_linear, decode_linear_glu, decode_linear_split, split_plan,
-                               split_workspace)
+    from ccq_amd.graph import (GDNLayerDecode, decode_linear, decode_linear_glu, decode_linear_split, greedy_embed,
+                               split_plan, split_workspace)
     from ccq_amd.layers import CCQGDN, LayerCache
 
     inter = 256 * ((int(d * 4 * 2 / 3) + 255) // 256)  # fla GatedMLP's intermediate size (hidden_ratio 4)
@@ -496,21 +496,28 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
             out.append(((S.clone(), C.clone(), m.clone(), pos), tuple(c.clone() for c in st["conv_state"])))
         return out
 
-    # the captured step: static token ids and one GDNLayerDecode (static buffers) per layer
+    # the captured step: static token ids and input rows, one GDNLayerDecode (static buffers) per layer
     ids = torch.zeros(b, 1, dtype=torch.long, device=dev)
+    xin = torch.zeros(b, 1, d, dtype=torch.bfloat16, device=dev)
     lds = [GDNLayerDecode(blk.attn, b) for blk in blocks]
+
+    def feed(tok):
+        """The step's input: token ids [b] and their embedding rows."""
+        ids.copy_(tok[:, None])
+        xin.copy_(embed(ids))
 
     def load(snap):
         for ld, (state, convs) in zip(lds, snap):
             ld.load({"recurrent_state": state, "conv_state": convs})
 
     def graph_step():
-        x = embed(ids)
+        x = xin
         for blk, ld in zip(blocks, lds):
             x = blk.mlp_step(ld(x, x, norm=blk.attn_norm))
         # the final RMSNorm folded into the LM head's projection (one launch, the same kernel)
         logits = decode_linear(x[:, -1], head.weight, norm_weight=norm.weight, norm_eps=norm.eps)
-        ids.copy_(logits.argmax(-1, keepdim=True))
+        # the greedy pick and its embedding row, the next step's input, in one launch
+        greedy_embed(logits, embed.weight, ids, xin)
         return logits
 
     with torch.no_grad():
@@ -543,7 +550,7 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
         # captured decode: warm up the step eagerly (libraries pick their kernels), restore the
         # prefill state, capture, then replay on the eager tokens and compare every replay
         load(snap)
-        ids.copy_(tok0[:, None])
+        feed(tok0)
         graph_step()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
@@ -552,14 +559,14 @@ def run_c4(args, dev, layers=24, b=16, t=16384, d=1024, vocab=32000, decode_step
         load(snap)
         errs = []
         for i in range(check_steps):
-            ids.copy_(ref_in[i][:, None])
+            feed(ref_in[i])
             graph.replay()
             torch.cuda.synchronize()
             errs.append(((logits_g.float() - ref_logits[i]).norm() / ref_logits[i].norm()).item())
         if max(errs) > 2e-2:
             raise RuntimeError(f"captured decode step disagrees with the eager layers: rel-L2 {errs}")
         load(snap)
-        ids.copy_(tok0[:, None])
+        feed(tok0)
         for _ in range(warm):
             graph.replay()
         torch.cuda.synchronize()

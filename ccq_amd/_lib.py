@@ -68,6 +68,7 @@ SIGNATURES = {
     "ccq_decode_linear_split": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _I, _P, _P]),
     "ccq_decode_linear_split_workspace_bytes": (_SZ, [_I, _I]),
     "ccq_decode_linear_gnorm": (_I, [_P, _I64, _P, _I64, _P, _I, _F, _P, _P, _I64, _P, _I64, _I, _I, _I, _P, _P]),
+    "ccq_greedy_embed": (_I, [_P, _I64, _I, _I, _P, _I64, _I, _P, _I64, _P, _I64, _P]),
     "ccq_timing_enable": (_I, [_I]),
     "ccq_timing_reset": (_I, []),
     "ccq_timing_select": (_I, [ctypes.c_char_p]),

@@ -39,6 +39,8 @@ hipError_t launch_decode_linear(bool glu, const void* x, long ldx, const void* w
 hipError_t launch_decode_linear_gnorm(const void* x, long ldx, const void* g, long ldg, const float* gw, int dv,
                                       float geps, const void* w, const void* r, long ldr, void* y, long ldy, int M,
                                       int K, int N, void* ws, hipStream_t st);
+hipError_t launch_greedy_embed(const void* logits, long ldl, int M, int N, const void* table, long rows, int D,
+                               int64_t* ids, long ldi, void* x, long ldx, hipStream_t st);
 hipError_t launch_decode_in_proj(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N,
                                  const void* nw, float eps, int oq, int ok, int ov, int oa, int ob, int Dq, int Dv,
                                  int H, int T, int neg_eig, const void* wq, const void* wk, const void* wv,
@@ -872,6 +874,19 @@ int ccq_decode_linear_gnorm(const void* x, int64_t ldx, const void* gate, int64_
   return hip_status(launch_decode_linear_gnorm(x, ldx, gate, ldg, norm_weight, dv, norm_eps, weight, residual, ldr, y,
                                                ldy, M, K, N, workspace, (hipStream_t)stream),
                     who);
+}
+
+int ccq_greedy_embed(const void* logits, int64_t ldl, int M, int N, const void* table, int64_t rows, int D,
+                     int64_t* ids, int64_t ldi, void* x, int64_t ldx, void* stream) {
+  const char* who = "ccq_greedy_embed";
+  if (M < 0 || N < 1 || D < 1 || rows < 1 || ldl < N || ldi < 1 || ldx < D)
+    return fail(CCQ_ERR_SHAPE, "%s: M=%d N=%d D=%d rows=%lld ldl=%lld ldi=%lld ldx=%lld (need N, D, rows >= 1, "
+                "ldl >= N, ldi >= 1, ldx >= D)", who, M, N, D, (long long)rows, (long long)ldl, (long long)ldi,
+                (long long)ldx);
+  if (!logits || !table || !ids || !x) return fail(CCQ_ERR_NULL, "%s: logits, table, ids and x are required", who);
+  if (((uintptr_t)logits & 1) || ((uintptr_t)table & 1) || ((uintptr_t)x & 1) || ((uintptr_t)ids & 7))
+    return fail(CCQ_ERR_ALIGN, "%s: logits, table and x must be 2-byte aligned, ids 8-byte aligned", who);
+  return hip_status(launch_greedy_embed(logits, ldl, M, N, table, rows, D, ids, ldi, x, ldx, (hipStream_t)stream), who);
 }
 
 int ccq_gdn_decode_in_proj(const void* x, int64_t ldx, const void* weight, void* y, int64_t ldy, int M, int K, int N,

@@ -829,6 +829,100 @@ hipError_t launch_decode_linear_gnorm(const void* x, long ldx, const void* g, lo
   return launch_decode_linear(false, x, ldx, w, r, ldr, y, ldy, M, K, N, nullptr, geps, K / dv, ws, nullptr, st, &gt);
 }
 
+// ===========================================================================
+// Greedy step of a generate loop: ids[m] = argmax_n logits[m][n] (the first index of the maximum; a
+// NaN counts as larger than any number, the first NaN winning, as torch.argmax), then the embedding
+// row of that token into x[m] (zeros for an id past the table's rows) -- the next decode step's input,
+// gathered here so that the step needs no launch of its own for it.  One workgroup per row: each
+// thread scans 8-element pieces (16-byte loads, for aligned rows) strided across the row, the wave's
+// best by lane exchanges, the workgroup's through LDS.
+// ===========================================================================
+constexpr int kGreedyThreads = 1024;
+
+__device__ __forceinline__ bool greedy_better(float v, int i, float u, int j) {
+  const bool nv = v != v, nu = u != u;
+  if (nv != nu) return nv;
+  if (!nv && v != u) return v > u;
+  return i < j;
+}
+
+// vec: rows 16-byte aligned (pieces of 8 elements; else every element by itself)
+__global__ __launch_bounds__(kGreedyThreads) void greedy_embed_kernel(const bf16* logits, long ldl, int N, bool vec,
+                                                                      const bf16* table, long rows, int D,
+                                                                      int64_t* ids, long ldi, bf16* x, long ldx) {
+  __shared__ float sv[kGreedyThreads / 64];
+  __shared__ int si[kGreedyThreads / 64];
+  __shared__ int sbest;
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const bf16* row = logits + (long)m * ldl;
+  float bv = -__builtin_inff();
+  int bi = N;  // (no element yet: loses to any element)
+  // PB pieces per thread in flight at once (unconditional loads from clamped addresses; a loop of
+  // one load per pass would wait for each)
+  constexpr int PB = 4;
+  const int n8 = vec ? N / 8 : 0;
+  for (int p0 = 0; p0 < n8; p0 += PB * kGreedyThreads) {
+    bf16x8 v[PB];
+#pragma unroll
+    for (int b = 0; b < PB; ++b) v[b] = *(const bf16x8*)(row + 8 * min(p0 + b * kGreedyThreads + tid, n8 - 1));
+#pragma unroll
+    for (int b = 0; b < PB; ++b) {
+      const int p = p0 + b * kGreedyThreads + tid;
+      if (p < n8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (greedy_better((float)v[b][e], 8 * p + e, bv, bi)) {
+            bv = (float)v[b][e];
+            bi = 8 * p + e;
+          }
+      }
+    }
+  }
+  for (int n = 8 * n8 + tid; n < N; n += kGreedyThreads)
+    if (greedy_better((float)row[n], n, bv, bi)) {
+      bv = (float)row[n];
+      bi = n;
+    }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float u = __shfl_xor(bv, o);
+    const int j = __shfl_xor(bi, o);
+    if (greedy_better(u, j, bv, bi)) {
+      bv = u;
+      bi = j;
+    }
+  }
+  if ((tid & 63) == 0) {
+    sv[tid >> 6] = bv;
+    si[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kGreedyThreads / 64; ++w)
+      if (greedy_better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    ids[(long)m * ldi] = bi;
+    sbest = bi;
+  }
+  __syncthreads();
+  const long id = sbest;
+  const bf16* src = table + id * D;
+  bf16* dst = x + (long)m * ldx;
+  const bool ok = id < rows;
+  for (int c = tid; c < D; c += kGreedyThreads) dst[c] = ok ? src[c] : (bf16)0.f;
+}
+
+hipError_t launch_greedy_embed(const void* logits, long ldl, int M, int N, const void* table, long rows, int D,
+                               int64_t* ids, long ldi, void* x, long ldx, hipStream_t st) {
+  if (M <= 0) return hipSuccess;
+  const bool vec = ((uintptr_t)logits & 15) == 0 && ldl % 8 == 0;
+  hipLaunchKernelGGL(greedy_embed_kernel, dim3(M), dim3(kGreedyThreads), 0, st, (const bf16*)logits, ldl, N, vec,
+                     (const bf16*)table, rows, D, ids, ldi, (bf16*)x, ldx);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t st) {
   if (a.N <= 0 || a.H <= 0) return hipSuccess;
   switch (a.K) {

@@ -34,7 +34,7 @@ from . import _lib
 from ._lib import call, ptr
 
 __all__ = ["DecodeStep", "CapturedDecode", "GDNLayerDecode", "decode_linear", "decode_linear_glu",
-           "decode_linear_ok"]
+           "decode_linear_ok", "greedy_embed"]
 
 
 def decode_linear_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
@@ -157,6 +157,22 @@ def decode_linear_gnorm(x: torch.Tensor, gate: torch.Tensor, norm_weight: Option
          float(norm_eps), ptr(weight), ptr(r2), 0 if r2 is None else r2.stride(0), ptr(y), N, M, K, N,
          ptr(workspace), _lib.stream_of(x))
     return y
+
+
+def greedy_embed(logits: torch.Tensor, table: torch.Tensor, ids: torch.Tensor, x: torch.Tensor) -> None:
+    """Greedy step of a generate loop (``ccq_greedy_embed``): ``ids[:, 0] = logits.argmax(-1)`` (int64,
+    torch's tie and NaN rules) and ``x[:, 0] = table[ids[:, 0]]``, the next decode step's input rows,
+    in one launch on logits' stream.  logits bf16 [M, N] (unit column stride); table bf16 [rows, D];
+    ids int64 [M, 1]; x bf16 [M, 1, D]."""
+    M, N = logits.shape
+    D = table.shape[1]
+    if (logits.dtype != torch.bfloat16 or logits.stride(1) != 1 or table.dtype != torch.bfloat16
+            or not table.is_contiguous() or ids.dtype != torch.int64 or ids.shape != (M, 1)
+            or x.dtype != torch.bfloat16 or x.shape != (M, 1, D) or x.stride(2) != 1):
+        raise ValueError(f"greedy_embed: logits {tuple(logits.shape)} {logits.dtype}, table {tuple(table.shape)} "
+                         f"{table.dtype}, ids {tuple(ids.shape)} {ids.dtype}, x {tuple(x.shape)} {x.dtype}")
+    call("ccq_greedy_embed", ptr(logits), logits.stride(0), M, N, ptr(table), table.shape[0], D, ptr(ids),
+         ids.stride(0), ptr(x), x.stride(0), _lib.stream_of(logits))
 
 
 def decode_linear_glu(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,

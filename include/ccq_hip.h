@@ -311,6 +311,17 @@ int ccq_decode_linear_glu(const void* x, int64_t ldx, const void* weight, void* 
 int ccq_decode_linear_gnorm(const void* x, int64_t ldx, const void* gate, int64_t ldg, const float* norm_weight,
                             int dv, float norm_eps, const void* weight, const void* residual, int64_t ldr, void* y,
                             int64_t ldy, int M, int K, int N, void* workspace, void* stream);
+/*
+ * Greedy step of a generate loop (the argmax that HF greedy decoding takes of the last position's
+ * logits, ccq/generation.py:17-50 feeding the token back): ids[m * ldi] = argmax over n of
+ * logits[m * ldl + n] (int64; the first index of the maximum, a NaN larger than any number -- as
+ * torch.argmax), and x[m * ldx + :D] = table[ids[m] * D + :D] (zeros for an id >= rows), the
+ * embedding rows of the picked tokens: the next decode step's input.  logits bf16, ldl >= N (rows
+ * 16-byte aligned are read in 16-byte pieces); table bf16 [rows, D]; x bf16.  One launch, no
+ * allocation.
+ */
+int ccq_greedy_embed(const void* logits, int64_t ldl, int M, int N, const void* table, int64_t rows, int D,
+                     int64_t* ids, int64_t ldi, void* x, int64_t ldx, void* stream);
 size_t ccq_decode_linear_split_workspace_bytes(int N, int splits);
 int ccq_decode_linear_split(const void* x, int64_t ldx, const void* weight, const void* residual, int64_t ldr, void* y,
                             int64_t ldy, int M, int K, int N, int splits, void* workspace, void* stream);

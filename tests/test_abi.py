@@ -13,7 +13,7 @@ from ccq_amd import _lib
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "ccq_hip.h")
 
-CCQ_ERR_SHAPE, CCQ_ERR_NULL = -1, -2
+CCQ_ERR_SHAPE, CCQ_ERR_NULL, CCQ_ERR_ALIGN = -1, -2, -3
 
 
 def declared():
@@ -212,7 +212,6 @@ def test_decode_rejects_unaligned_states_and_gv():
     # on the host, before any device work
     lib = _lib.load()
     p, odd, m_out = _fake(), ctypes.c_void_p(0x1004), ctypes.c_void_p(0x2000)   # m_out may not alias m
-    CCQ_ERR_ALIGN = -3
 
     def call(state=p, cov=p, state_out=p, cov_out=p, gv=None):
         return lib.ccq_gdn_decode(p, p, p, p, None, None, None, p, None, gv, state, cov, p, None, p, state_out,
@@ -236,3 +235,15 @@ def test_decode_linear_split_checks_and_workspace():
     assert lib.ccq_decode_linear_split(p, 64, p, None, 0, p, 40, 1, 64, 40, 3, p, None) == CCQ_ERR_SHAPE
     assert lib.ccq_decode_linear_split(p, 2048, p, None, 0, p, 40, 1, 2048, 40, 9, p, None) == CCQ_ERR_SHAPE
     assert lib.ccq_decode_linear_split(p, 2048, p, None, 0, p, 40, 1, 2048, 40, 4, None, None) == CCQ_ERR_NULL
+
+
+def test_greedy_embed_checks():
+    # shapes, required pointers and the logits' alignment are refused on the host, before any launch
+    lib = _lib.load()
+    p = _fake()
+    ids = _fake()
+    assert lib.ccq_greedy_embed(p, 32, 2, 40, p, 40, 8, ids, 1, p, 8, None) == CCQ_ERR_SHAPE    # ldl < N
+    assert lib.ccq_greedy_embed(p, 32, 2, 32, p, 0, 8, ids, 1, p, 8, None) == CCQ_ERR_SHAPE     # no table rows
+    assert lib.ccq_greedy_embed(p, 32, 2, 32, p, 32, 8, ids, 1, p, 4, None) == CCQ_ERR_SHAPE    # ldx < D
+    assert lib.ccq_greedy_embed(p, 32, 2, 32, None, 32, 8, ids, 1, p, 8, None) == CCQ_ERR_NULL
+    assert lib.ccq_greedy_embed(ctypes.c_void_p(0x1001), 32, 2, 32, p, 32, 8, ids, 1, p, 8, None) == CCQ_ERR_ALIGN

@@ -200,3 +200,35 @@ def test_decode_linear_folded_gated_norm(M, H, V, N, weighted):
         assert y.shape == (M, N) and e <= 5e-4 and e64 <= 5e-4
         if ws is not None:
             assert int(ws[:4 * ((N + 15) // 16)].view(torch.int32).abs().sum()) == 0, "counters"
+
+
+@pytest.mark.parametrize("M,N,rows,D", [(16, 32000, 32000, 1024), (3, 1003, 1003, 200), (2, 64, 40, 24)])
+def test_greedy_embed(M, N, rows, D):
+    """``greedy_embed`` against ``logits.argmax(-1)`` and the embedding lookup: planted ties (the first
+    index wins), NaNs (the first NaN wins, as torch.argmax), a row of -inf (index 0), a width that is
+    not a multiple of 8, and ids past the table's rows (zero rows)."""
+    dev = _cuda()
+    from ccq_amd.graph import greedy_embed
+    print("test_greedy_embed", M, N, rows, D, flush=True)
+    gen = torch.Generator().manual_seed(N + M)
+    logits = torch.randn(M, N, generator=gen).to(BF)
+    if M >= 3:
+        top = logits[0].max()
+        logits[0, N // 3] = top + 1
+        logits[0, N - 1] = top + 1                     # tie: the first index wins
+        logits[1, 7] = float("nan")
+        logits[1, N // 2] = float("nan")               # NaNs: the first wins
+        logits[2] = float("-inf")                      # all -inf: index 0
+    else:
+        logits[0, N - 1] = logits[0].max() + 1         # an id past the table (rows < N)
+    table = torch.randn(rows, D, generator=gen).to(BF)
+    ref_ids = logits.argmax(-1)
+    ref_x = torch.zeros(M, D, dtype=BF)
+    ok = ref_ids < rows
+    ref_x[ok] = table[ref_ids[ok]]
+    ids = torch.full((M, 1), -1, dtype=torch.int64, device=dev)
+    x = torch.full((M, 1, D), 7.0, dtype=BF, device=dev)
+    greedy_embed(logits.to(dev), table.to(dev), ids, x)
+    torch.cuda.synchronize()
+    assert torch.equal(ids[:, 0].cpu(), ref_ids), (ids[:, 0].cpu(), ref_ids)
+    assert torch.equal(x[:, 0].cpu(), ref_x)
