@@ -19,6 +19,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, stream_of
+from ._pad import CHUNK_K, STEP_K, cut_tail, pad_tail, padded_sizes
 from .clean import as_kernel_dtype, in_dtype
 from .clean import (_check_qk, _f32, check_device, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd,
                     norm_cu_seqlens, reduce_dlambda, reshape_lambda_3d, seq_count)
@@ -195,14 +196,24 @@ def fused_chunk_ccq_gdn(q, k, v, lambda_h, g, beta, scale=None, initial_state=No
         raise TypeError(f"fused_chunk_ccq_gdn: unsupported keyword arguments: {unknown}")
     dt = q.dtype
     q, k, v = as_kernel_dtype(q, k, v)
+    K, V = q.shape[-1], v.shape[-1]
+    scale = _default_scale(scale, K)
+    # head sizes between the kernels' run zero-padded (ccq_amd/_pad.py)
+    Kp, Vp = padded_sizes(K, V, CHUNK_K)
+    if (Kp, Vp) != (K, V):
+        q, k, v = pad_tail(q, Kp), pad_tail(k, Kp), pad_tail(v, Vp)
+        initial_state = pad_tail(initial_state, Kp, Vp)
+        initial_cov_state = pad_tail(initial_cov_state, Kp, Kp)
+        initial_mean_state = pad_tail(initial_mean_state, Kp)
+        gate_w = pad_tail(gate_w, Kp)
     o, sfin, hfin, mfin = ChunkCCQGDNFunction.apply(
-        q, k, v, lambda_h, g, beta, _default_scale(scale, q.shape[-1]), initial_state, initial_cov_state,
+        q, k, v, lambda_h, g, beta, scale, initial_state, initial_cov_state,
         initial_mean_state if subtract_mean else None, bool(output_final_state), bool(use_qk_l2norm_in_kernel),
         cu_seqlens, int(position_offset), bool(subtract_mean), bool(enable_ccq), gate_w, gate_b)
-    o = in_dtype(o, dt)
+    o = in_dtype(cut_tail(o, V), dt)
     if not output_final_state:
         return o, None, None, None
-    return o, sfin, hfin, mfin
+    return o, cut_tail(sfin, K, V), cut_tail(hfin, K, K), cut_tail(mfin, K)
 
 
 def chunk_ccq_gdn(q, k, v, lambda_h, g, beta, scale=None, initial_state=None, initial_cov_state=None,
@@ -250,13 +261,20 @@ def fused_recurrent_ccq_gdn(q, k, v, lambda_h, g=None, gk=None, gv=None, beta=No
             s0 = s0.transpose(-1, -2)
         dt = q.dtype
         q, k, v = as_kernel_dtype(q, k, v)
-        o, s, c, m = gdn_decode(q, k, v, lambda_h, g, beta, _default_scale(scale, q.shape[-1]), s0, initial_cov_state,
-                                initial_mean_state if subtract_mean else None, bool(output_final_state),
+        K, V = q.shape[-1], v.shape[-1]
+        scale = _default_scale(scale, K)
+        cov0, m0 = initial_cov_state, initial_mean_state if subtract_mean else None
+        Kp, Vp = padded_sizes(K, V, STEP_K)
+        if (Kp, Vp) != (K, V):
+            q, k, v, gk, gv = pad_tail(q, Kp), pad_tail(k, Kp), pad_tail(v, Vp), pad_tail(gk, Kp), pad_tail(gv, Vp)
+            s0, cov0, m0 = pad_tail(s0, Kp, Vp), pad_tail(cov0, Kp, Kp), pad_tail(m0, Kp)
+        o, s, c, m = gdn_decode(q, k, v, lambda_h, g, beta, scale, s0, cov0, m0, bool(output_final_state),
                                 bool(use_qk_l2norm_in_kernel), cu_seqlens, position_offset, subtract_mean, enable_ccq,
                                 gk=gk, gv=gv)
-        o = in_dtype(o, dt)
+        o = in_dtype(cut_tail(o, V), dt)
         if not output_final_state:
             return o, None, None, None
+        s, c, m = cut_tail(s, K, V), cut_tail(c, K, K), cut_tail(m, K)
         if transpose_state_layout:
             s = s.transpose(-1, -2).contiguous()
         return o, s, c, m

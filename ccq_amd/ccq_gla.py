@@ -18,6 +18,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, stream_of
+from ._pad import CHUNK_K, STEP_K, cut_tail, pad_tail, padded_sizes
 from .ccq_gdn import _Chunks, _default_scale, _stock_mean
 from .clean import as_kernel_dtype, in_dtype
 from .clean import _check_qk, _f32, check_device, clean_backward, clean_forward, l2norm_bwd, l2norm_fwd, \
@@ -152,14 +153,24 @@ def fused_chunk_ccq_gla(q, k, v, lambda_h, g=None, scale=None, initial_state=Non
     """
     dt = q.dtype
     q, k, v = as_kernel_dtype(q, k, v)
+    K, V = q.shape[-1], v.shape[-1]
+    scale = _default_scale(scale, K)
+    # head sizes between the kernels' run zero-padded (ccq_amd/_pad.py)
+    Kp, Vp = padded_sizes(K, V, CHUNK_K)
+    if (Kp, Vp) != (K, V):
+        q, k, v, g = pad_tail(q, Kp), pad_tail(k, Kp), pad_tail(v, Vp), pad_tail(g, Kp)
+        initial_state = pad_tail(initial_state, Kp, Vp)
+        initial_cov_state = pad_tail(initial_cov_state, Kp, Kp)
+        initial_mean_state = pad_tail(initial_mean_state, Kp)
+        gate_w = pad_tail(gate_w, Kp)
     o, sfin, hfin, mfin = ChunkCCQGLAFunction.apply(
-        q, k, v, lambda_h, g, _default_scale(scale, q.shape[-1]), initial_state, initial_cov_state,
+        q, k, v, lambda_h, g, scale, initial_state, initial_cov_state,
         initial_mean_state if subtract_mean else None, bool(output_final_state), True, cu_seqlens,
         int(position_offset), bool(subtract_mean), True, gate_w, gate_b)
-    o = in_dtype(o, dt)
+    o = in_dtype(cut_tail(o, V), dt)
     if not output_final_state:
         return o, None, None, None
-    return o, sfin, hfin, mfin
+    return o, cut_tail(sfin, K, V), cut_tail(hfin, K, K), cut_tail(mfin, K)
 
 
 def chunk_ccq_gla(q, k, v, lambda_h, g=None, scale=None, initial_state=None, initial_cov_state=None,
@@ -189,14 +200,19 @@ def fused_recurrent_ccq_gla(q, k, v, lambda_h, gk=None, gv=None, scale=None, ini
     if not needs_grad(q, k, v, lambda_h, gk, gv, initial_state, initial_cov_state, initial_mean_state):
         dt = q.dtype
         q, k, v = as_kernel_dtype(q, k, v)
-        o, s, c, m = gla_decode(q, k, v, lambda_h, gk, _default_scale(scale, q.shape[-1]), initial_state,
-                                initial_cov_state, initial_mean_state if subtract_mean else None,
-                                bool(output_final_state), cu_seqlens, position_offset, subtract_mean, gv=gv,
-                                reverse=bool(reverse))
-        o = in_dtype(o, dt)
+        K, V = q.shape[-1], v.shape[-1]
+        scale = _default_scale(scale, K)
+        s0, cov0, m0 = initial_state, initial_cov_state, initial_mean_state if subtract_mean else None
+        Kp, Vp = padded_sizes(K, V, STEP_K)
+        if (Kp, Vp) != (K, V):
+            q, k, v, gk, gv = pad_tail(q, Kp), pad_tail(k, Kp), pad_tail(v, Vp), pad_tail(gk, Kp), pad_tail(gv, Vp)
+            s0, cov0, m0 = pad_tail(s0, Kp, Vp), pad_tail(cov0, Kp, Kp), pad_tail(m0, Kp)
+        o, s, c, m = gla_decode(q, k, v, lambda_h, gk, scale, s0, cov0, m0, bool(output_final_state), cu_seqlens,
+                                position_offset, subtract_mean, gv=gv, reverse=bool(reverse))
+        o = in_dtype(cut_tail(o, V), dt)
         if not output_final_state:
             return o, None, None, None
-        return o, s, c, m
+        return o, cut_tail(s, K, V), cut_tail(c, K, K), cut_tail(m, K)
     if gv is not None:
         raise NotImplementedError("fused_recurrent_ccq_gla: gradients through the per-value decay gv are not "
                                   "supported (inference with gv runs on the decode kernels)")
@@ -253,7 +269,13 @@ def chunk_gla(q, k, v, g=None, scale=None, initial_state=None, output_final_stat
         raise TypeError(f"chunk_gla: unsupported keyword arguments: {unknown}")
     dt = q.dtype
     q, k, v = as_kernel_dtype(q, k, v)
+    K, V = q.shape[-1], v.shape[-1]
+    scale = _default_scale(scale, K)
+    Kp, Vp = padded_sizes(K, V, CHUNK_K)
+    if (Kp, Vp) != (K, V):
+        q, k, v, g = pad_tail(q, Kp), pad_tail(k, Kp), pad_tail(v, Vp), pad_tail(g, Kp)
+        initial_state = pad_tail(initial_state, Kp, Vp)
     o, sfin, _, _ = ChunkCCQGLAFunction.apply(
-        q, k, v, None, g, _default_scale(scale, q.shape[-1]), initial_state, None, None, bool(output_final_state),
+        q, k, v, None, g, scale, initial_state, None, None, bool(output_final_state),
         False, cu_seqlens, 0, True, False, None, None)
-    return in_dtype(o, dt), (sfin if output_final_state else None)
+    return in_dtype(cut_tail(o, V), dt), (cut_tail(sfin, K, V) if output_final_state else None)

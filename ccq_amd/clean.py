@@ -246,13 +246,20 @@ def fused_ccq_clean_read(q, k, lambda_h, *, position_offset=0, initial_cov_state
 
     Returns ``(q_clean, final_cov_state, final_mean_state)``; the states are None unless requested.
     """
+    from ._pad import STEP_K, cut_tail, pad_tail, padded_sizes
     dt = q.dtype
     q, k = as_kernel_dtype(q, k)
+    # head sizes between the kernels' run zero-padded (ccq_amd/_pad.py)
+    K = q.shape[-1]
+    Kp, _ = padded_sizes(K, None, STEP_K)
+    if Kp != K:
+        q, k, gate_w = pad_tail(q, Kp), pad_tail(k, Kp), pad_tail(gate_w, Kp)
+        initial_cov_state, initial_mean_state = pad_tail(initial_cov_state, Kp, Kp), pad_tail(initial_mean_state, Kp)
     qc, hf, mf = FusedCCQCleanRead.apply(q, k, lambda_h, int(position_offset), initial_cov_state, initial_mean_state,
                                          bool(output_final_state), bool(subtract_mean), cu_seqlens, gate_w, gate_b)
     if not output_final_state:
         hf, mf = None, None
-    return in_dtype(qc, dt), hf, mf
+    return in_dtype(cut_tail(qc, K), dt), cut_tail(hf, K, K), cut_tail(mf, K)
 
 
 # ---------------------------------------------------------------------------

@@ -43,6 +43,9 @@ DECODE_CASES = [
     (2, 2, 2, 128, 64, 9, False, "gdn"),
     (3, 1, 2, 128, 256, 37, True, "gla"),
     (2, 3, 2, 256, 128, 70, True, "gla"),
+    # head sizes between the kernels' (zero-padded to K = 64 / 128, V = 128, results sliced back)
+    (2, 2, 2, 40, 72, 11, True, "gdn"),
+    (2, 1, 2, 96, 100, 30, True, "gla"),
 ]
 
 

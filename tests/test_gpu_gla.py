@@ -84,6 +84,8 @@ FUSED_GLA_CASES = [
     (2, 130, 2, 64, 128, True, 0, None),
     (1, 300, 2, 128, 256, False, 3, None),
     (1, 180, 2, 128, 64, True, 0, [0, 70, 71, 180]),
+    # head sizes between the kernels' (zero-padded to K = 128, V = 128, results sliced back)
+    (1, 150, 2, 96, 80, True, 2, None),
 ]
 
 

@@ -165,6 +165,45 @@ def test_layer_train_step(kind, mode, oracle_ops):
 
 
 @pytest.mark.parametrize("kind", ["gdn", "gla"])
+def test_layer_odd_head_sizes(kind, oracle_ops):
+    """Layers whose head sizes the kernels do not take directly (the reference layers accept any
+    head_dim): GDN head_dim 96 with expand_v 1.5 (V = 144), GLA K = V = 96; a training step against
+    the layer running the oracle operators."""
+    dev = _cuda()
+    from ccq_amd import CCQGDN, CCQGLA
+    torch.manual_seed(0)
+    if kind == "gdn":
+        ref = CCQGDN(hidden_size=256, head_dim=96, num_heads=2, expand_v=1.5, layer_idx=0, mode="chunk")
+    else:
+        ref = CCQGLA(hidden_size=256, expand_k=0.75, expand_v=0.75, num_heads=2, use_short_conv=True, layer_idx=0,
+                     mode="chunk")
+    with torch.no_grad():
+        ref.erase_lambda_proj.bias.fill_(0.0)
+    ref = ref.double().train()
+    gpu = copy.deepcopy(ref).float().to(dev).train()
+    B, T = 2, 100
+    x = _x(B, T)
+    gen = torch.Generator().manual_seed(2)
+    do = torch.randn(B, T, 256, generator=gen)
+    print(f"test_layer_odd_head_sizes {kind}", flush=True)
+    with oracle_ops:
+        xr = x.to(D).requires_grad_()
+        o_r, _, _ = ref(xr)
+        (o_r * do.to(D)).sum().backward()
+    xg = x.to(dev).requires_grad_()
+    o, _, _ = gpu(xg)
+    (o * do.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    errs = {"o": rel(o, o_r), "dx": rel(xg.grad, xr.grad)}
+    for (n, p_r), (_, p) in zip(ref.named_parameters(), gpu.named_parameters()):
+        if p_r.grad is not None:
+            errs["d" + n] = rel(p.grad, p_r.grad)
+    print(kind, {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    for n, e in errs.items():
+        assert e <= TOL, n
+
+
+@pytest.mark.parametrize("kind", ["gdn", "gla"])
 def test_layer_prefill_then_decode(kind, oracle_ops):
     """eval: chunked prefill of T0 tokens into a cache, then single-token calls (recurrent mode,
     decode kernels) carrying the recurrent and convolution states; checked against the oracle

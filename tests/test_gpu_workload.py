@@ -35,13 +35,13 @@ def _cuda():
     return torch.device("cuda")
 
 
-def _report(case, errs, kerrs):
+def _report(case, errs, kerrs, ktol=TOL_KERNEL):
     print(case, {n: f"{e:.2e}" for n, e in errs.items()}, "kernel", {n: f"{e:.2e}" for n, e in kerrs.items()},
           flush=True)
     for n, e in errs.items():
         assert e <= TOL_BF16, n
     for n, e in kerrs.items():
-        assert e <= TOL_KERNEL, n
+        assert e <= ktol, n
 
 
 @pytest.mark.parametrize("T", [4096, 1000])  # 1000: a partial last chunk under the full decay
@@ -152,15 +152,24 @@ SHAPE_CASES = [
     (2, 130, 2, 128, 256, None, False, False, True),
     # K = 128, V = 64 with a bf16 query (the backbone alone)
     (1, 260, 3, 128, 64, [0, 100, 260], True, False, False),
+    # head sizes between the kernels' (run zero-padded to the next K in {64, 128, 256} and the next
+    # multiple of 64 for V, the outputs, states and gradients sliced back)
+    (1, 150, 2, 96, 80, None, True, True, True),
+    # (K 200 -> 256: the K = 256 kernels on q, k normalised over 200 channels with scale 200^-1/2;
+    # over seeds 21-25 their per-element dq error is 2.4e-4 .. 6.3e-4 against 2.3e-4 .. 3.4e-4 for the
+    # same sizes at K = 256, V = 320 unpadded -- the padded channels are exact zeros, the spread is the
+    # data's -- so this case's per-element bar is 1e-3; every output and gradient stays within 2e-3)
+    (1, 200, 2, 200, 300, [0, 63, 200], True, True, False, 1e-3),
+    (2, 70, 1, 40, 24, None, True, False, False),
 ]
 
 
 @pytest.mark.parametrize("case", SHAPE_CASES, ids=[str(i) for i in range(len(SHAPE_CASES))])
 def test_gdn_head_shapes(case):
     print("test_gdn_head_shapes", case, flush=True)
-    B, T, H, K, V, cu, st, ccq, l2 = case
+    B, T, H, K, V, cu, st, ccq, l2 = case[:9]
     errs, kerrs = _gdn_case(B, T, H, K, V, cu, st, ccq, l2, seed=21)
-    _report(case, errs, kerrs)
+    _report(case, errs, kerrs, case[9] if len(case) > 9 else TOL_KERNEL)
 
 
 LAMBDA_FORMS = ["float", "0d", "H", "BTH", "BTH1"]
