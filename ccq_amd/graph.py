@@ -211,6 +211,10 @@ class DecodeStep:
             raise ValueError(f"mode must be 'gdn' or 'gla' (got {mode!r})")
         if mode == "gla" and not enable_ccq:
             raise ValueError("the GLA step always cleans the query (enable_ccq=True)")
+        if K not in (32, 64, 128, 256) or V < 64 or V % 64 or V > 1024:
+            # (its static buffers are the kernels' own; the operators pad other sizes, ccq_amd/_pad.py)
+            raise ValueError(f"DecodeStep takes K in {{32, 64, 128, 256}} and V a multiple of 64 up to 1024 "
+                             f"(got K={K}, V={V})")
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         if dev.type != "cuda":
             raise ValueError(f"DecodeStep runs on a GPU (got device {dev})")

@@ -89,3 +89,11 @@ def test_zero_channels_change_nothing(kind):
         g2 = l2[n].grad
         g2 = cut_tail(g2, *shapes[n]) if n in shapes else g2
         assert torch.allclose(t.grad, g2, rtol=1e-10, atol=1e-12), n
+
+
+def test_decode_step_refuses_sizes_it_cannot_hold():
+    # the captured decode step's static buffers are the kernels' sizes (checked before any allocation)
+    from ccq_amd.graph import DecodeStep
+    for K, V in ((96, 128), (128, 100), (512, 128)):
+        with pytest.raises(ValueError, match="DecodeStep takes K"):
+            DecodeStep(1, 2, K, V, device="cpu")
