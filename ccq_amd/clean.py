@@ -283,13 +283,20 @@ class _CCQCleanQ(torch.autograd.Function):
         if z.shape != q.shape:
             raise ValueError(f"z must have q's shape {tuple(q.shape)} (got {tuple(z.shape)})")
         check_device(q.device, z=z, lambda_h=lambda_h, initial_state_K=initial_state_K)
+        from ._pad import STEP_K, pad_tail, padded_sizes
         cu_seqlens = norm_cu_seqlens(cu_seqlens, q)
         q, k = q.contiguous(), k.contiguous()
         z16 = z.contiguous().to(torch.bfloat16)
-        B, T, H, K = q.shape
-        ch = _Chunks(B, T, cu_seqlens, q.device)
         lam3 = reshape_lambda_3d(lambda_h, q)
         m0 = _f32(initial_state_K)
+        # head sizes between the kernels' run zero-padded (ccq_amd/_pad.py); results sliced back here
+        # and in the backward
+        ctx.k0 = K0 = q.shape[-1]
+        Kp, _ = padded_sizes(K0, None, STEP_K)
+        if Kp != K0:
+            q, k, z16, m0 = pad_tail(q, Kp), pad_tail(k, Kp), pad_tail(z16, Kp), pad_tail(m0, Kp)
+        B, T, H, K = q.shape
+        ch = _Chunks(B, T, cu_seqlens, q.device)
         saved = torch.empty(_lib.load().ccq_clean_z_saved_bytes(ch.count, H, K), device=q.device, dtype=torch.uint8)
         qc = torch.empty_like(q)
         mfin = torch.empty(ch.N, H, K, device=q.device, dtype=torch.float32) if output_final_state else None
@@ -302,13 +309,18 @@ class _CCQCleanQ(torch.autograd.Function):
         ctx.z_dtype = z.dtype
         ctx.position_offset = int(position_offset)
         ctx.subtract_mean = bool(subtract_mean)
+        if K != K0:
+            qc, mfin = qc[..., :K0].contiguous(), (mfin[..., :K0].contiguous() if mfin is not None else None)
         return qc, mfin
 
     @staticmethod
     def backward(ctx, dqc, dmfin):
+        from ._pad import cut_tail, pad_tail
         q, k, z16, lam3, saved, cu_seqlens = ctx.saved_tensors
         ch = ctx.ch
         B, T, H, K = q.shape
+        K0 = ctx.k0
+        dqc = pad_tail(dqc, K)
         ws = torch.empty(_lib.load().ccq_clean_z_bwd_workspace_bytes(ch.count, H, K), device=q.device,
                          dtype=torch.uint8)
         dqc = dqc.contiguous()
@@ -322,7 +334,8 @@ class _CCQCleanQ(torch.autograd.Function):
              ch.count, ptr(saved), ptr(d16), ptr(d32), None, ptr(dq), ptr(dk), ptr(dz), ptr(dlam), None,
              ptr(ws), B, T, H, K, ch.N, ctx.position_offset, int(ctx.subtract_mean), stream_of(q))
         dl = reduce_dlambda(dlam, ctx.lambda_h) if dlam is not None else None
-        return dq, dk, dz.to(ctx.z_dtype), dl, None, None, None, None, None
+        return (cut_tail(dq, K0), cut_tail(dk, K0), cut_tail(dz, K0).to(ctx.z_dtype), dl, None, None, None, None,
+                None)
 
 
 class _CovarianceRead(torch.autograd.Function):
@@ -362,5 +375,11 @@ def _ccq_compute_z_and_sum_kk(q, k, output_final_state, cu_seqlens, initial_stat
     form for short inputs; both are the same recurrence).  Evaluated by the GLA chunk kernels with
     ``v = k``, no decay and ``scale = 1``; differentiable in q, k and ``initial_state``.
     Returns ``(z, final_state | None)`` with z in q's dtype."""
+    from ._pad import CHUNK_K, cut_tail, pad_tail, padded_sizes
+    # head sizes between the kernels' run zero-padded (ccq_amd/_pad.py)
+    K = q.shape[-1]
+    Kp, _ = padded_sizes(K, None, CHUNK_K)
+    if Kp != K:
+        q, k, initial_state = pad_tail(q, Kp), pad_tail(k, Kp), pad_tail(initial_state, Kp, Kp)
     z, hfin = _CovarianceRead.apply(q, k, initial_state, bool(output_final_state), cu_seqlens)
-    return z, (hfin if output_final_state else None)
+    return cut_tail(z, K), (cut_tail(hfin, K, K) if output_final_state else None)

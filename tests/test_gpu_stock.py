@@ -26,6 +26,7 @@ READ_CASES = [
     (2, 130, 2, 64, True, None),
     (1, 200, 2, 128, False, None),
     (1, 150, 2, 256, True, [0, 40, 41, 150]),
+    (1, 120, 2, 96, True, None),   # K between the kernels' sizes: zero-padded to 128, results sliced back
 ]
 
 
@@ -73,6 +74,7 @@ CLEANQ_CASES = [
     (1, 300, 2, 128, False, 5, True, None),
     (1, 90, 2, 32, True, 0, False, None),
     (1, 200, 2, 256, True, 2, True, [0, 64, 65, 200]),
+    (1, 110, 2, 48, True, 3, True, None),   # K between the kernels' sizes: zero-padded to 64
 ]
 
 
