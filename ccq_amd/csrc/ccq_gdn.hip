@@ -130,30 +130,46 @@ __device__ __forceinline__ float dpp_move(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
 
+// The magnitudes are taken as bit patterns (sign bit cleared): for non-negative floats the unsigned
+// order of the patterns is the numeric order, so the maxima are integer maxima, whose lane moves fold
+// into the max as DPP operands (a float max canonicalises both operands first).  Beyond 16 lanes the
+// permlane swaps leave each lane's own value in one result and its partner's in the other.
+template <int CTRL>
+__device__ __forceinline__ unsigned umax_dpp(unsigned x) {
+  return max(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false));
+}
+
 template <int G>
-__device__ __forceinline__ float group_max(float v) {
-  if constexpr (G >= 2) v = fmaxf(v, dpp_move<0xB1>(v));    // quad_perm [1, 0, 3, 2]
-  if constexpr (G >= 4) v = fmaxf(v, dpp_move<0x4E>(v));    // quad_perm [2, 3, 0, 1]
-  if constexpr (G >= 8) v = fmaxf(v, dpp_move<0x141>(v));   // row_half_mirror
-  if constexpr (G >= 16) v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
-  if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16));
-  if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+__device__ __forceinline__ unsigned group_umax(unsigned v) {
+  if constexpr (G >= 2) v = umax_dpp<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  if constexpr (G >= 4) v = umax_dpp<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  if constexpr (G >= 8) v = umax_dpp<0x141>(v);   // row_half_mirror
+  if constexpr (G >= 16) v = umax_dpp<0x140>(v);  // row_mirror
+  if constexpr (G >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max((unsigned)r[0], (unsigned)r[1]);
+  }
+  if constexpr (G >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = max((unsigned)r[0], (unsigned)r[1]);
+  }
   return v;
 }
 
 template <int K>
 __device__ __forceinline__ void snap16_store(const bf16* hi, const bf16* lo, short* dst, float* dst_scale, int lane) {
   constexpr int G = K / 8;  // lanes per row
-  float x[8], mx = 0.f;
+  float x[8];
+  unsigned mx = 0;  // bit pattern of the largest |x|
   const bf16x8 h8 = *(const bf16x8*)hi, l8 = *(const bf16x8*)lo;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     x[i] = (float)h8[i] + (float)l8[i];
-    mx = fmaxf(mx, fabsf(x[i]));
+    mx = max(mx, __float_as_uint(x[i]) & 0x7fffffffu);
   }
-  mx = group_max<G>(mx);
+  mx = group_umax<G>(mx);
   // floor(log2 mx) from the exponent field (0 and subnormal maxima land on the lower clamp)
-  const int e = min(max((int)((__float_as_uint(mx) >> 23) & 0xff) - 127 - 14, -126), 113);
+  const int e = min(max((int)((mx >> 23) & 0xff) - 127 - 14, -126), 113);
   i16x8 out;
 #pragma unroll
   for (int i = 0; i < 8; ++i) out[i] = (short)__builtin_amdgcn_fmed3f(rintf(ldexpf(x[i], -e)), -32767.f, 32767.f);
@@ -3568,18 +3584,21 @@ __device__ __forceinline__ float rowsum32(const f32x16& ev, int l) {
   return a1 + xlane<1>(a1, l);
 }
 // Largest |x| of each of the lane's 16 rows of a 32 x 32 C tile, over the row's 32 columns (the 32
-// lanes of the half-wave); every lane ends with the maxima of its own rows.
+// lanes of the half-wave); every lane ends with the maxima of its own rows.  Integer maxima of the
+// magnitudes' bit patterns (as group_umax): after the two quad steps every
+// lane of a quad holds the quad's maximum, so rotating the row by 4 and then by 8 brings in the other
+// three quads'.
 __device__ __forceinline__ f32x16 rowmax32_all(const f32x16& v, int l) {
   f32x16 m;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    float x = fabsf(v[i]);
-    x = fmaxf(x, xlane<1>(x, l));
-    x = fmaxf(x, xlane<2>(x, l));
-    x = fmaxf(x, xlane<4>(x, l));
-    x = fmaxf(x, xlane<8>(x, l));
-    x = fmaxf(x, xlane<16>(x, l));
-    m[i] = x;
+    unsigned x = __float_as_uint(v[i]) & 0x7fffffffu;
+    x = umax_dpp<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    x = umax_dpp<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    x = umax_dpp<0x124>(x);  // row_ror:4
+    x = umax_dpp<0x128>(x);  // row_ror:8
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    m[i] = __uint_as_float(max((unsigned)r[0], (unsigned)r[1]));
   }
   return m;
 }
